@@ -1,0 +1,452 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/* dsv4_fp8.hip - block-scaled FP8 e4m3 GEMV for batch-1 decode on gfx950.
+ *
+ * What it computes is dsv4_matmul_fp8 (reference src/core/dsv4_matmul.c:
+ * 293-318): y[o] = sum over 128-column blocks of (block dot) * scale(o/128,
+ * c/128). It replaces the reference's k_mmq_fp8 (src/cuda/dsv4_cuda.cu:
+ * 93-129), which gives each row a 128-thread block and reads one byte per
+ * lane per step.
+ *
+ * DESIGN (bandwidth-bound: ~1 multiply-add per weight byte)
+ *   - A row is split over TC threads ("row threads", a power of two up to
+ *     64 or a multiple of 64 up to 256); thread j owns the 16-byte chunks
+ *     j, j+TC, j+2TC, ... of every row it visits (NCH <= 4 of them), so rows
+ *     up to 16384 columns take this path. Consecutive lanes read consecutive 16-byte chunks, so one wave
+ *     instruction moves 1 KiB of one row -- fully coalesced.
+ *   - The thread's slice of x (NCH x 16 floats) is loaded once into VGPRs and
+ *     reused for every row the workgroup visits; workgroups are persistent
+ *     over a contiguous range of row tiles, so x is fetched ~once per
+ *     workgroup, not once per row.
+ *   - A thread works on R rows at once: R*NCH independent 16-byte loads in
+ *     flight per lane before any arithmetic.
+ *   - Decode is v_cvt_pk_f32_fp8 (exact), 16 fp32 FMAs per chunk, then one
+ *     FMA applies the chunk's block scale (each 16-column chunk lies in one
+ *     128-column block), accumulating per lane in fp32.
+ *   - The TC lane partials of a row are summed by a fixed DPP tree inside a
+ *     wave and, when a row spans several waves, in wave order through LDS.
+ *
+ * DETERMINISM. TC, NCH and the reduction tree are functions of `cols` alone
+ * (fp8_geom), so a row's result does not depend on R, the grid size or the
+ * rows around it; the batched kernel reuses the same per-row arithmetic and
+ * is bit-identical to the GEMV per (row, token).
+ *
+ * NUMERICS. fp32 inside the lane and in the tree (the reference CPU path
+ * accumulates in double); measured against it under the vector-scaled
+ * relative metric of tests/unit/test_cuda.c:160-167, bound 1e-5.
+ */
+#include "dsv4_dev.h"
+#include "dsv4_internal.h"
+
+#include <stdlib.h>
+
+namespace {
+
+struct Fp8Geom {
+    int ch;   /* 16-byte chunks per row                       */
+    int tc;   /* threads per row (power of two <= 64, or k*64) */
+    int nch;  /* chunks per thread (<= 4)                      */
+    int wg;   /* workgroup size                                */
+    int rg;   /* rows in flight per workgroup per R            */
+};
+
+bool fp8_geom(int cols, Fp8Geom *g)
+{
+    if (cols <= 0 || (cols & 15)) return false;
+    const int ch = cols >> 4;
+    int tc, nch;
+    if (ch <= 64) {
+        tc = 1;
+        while (tc < ch) tc <<= 1;
+        nch = 1;
+    } else {
+        tc = 64 * ((ch + 255) / 256);
+        nch = (ch + tc - 1) / tc;
+    }
+    if (tc > 256 || nch > 4) return false;     /* cols <= 16384 */
+    g->ch = ch;
+    g->tc = tc;
+    g->nch = nch;
+    g->wg = tc * (256 / tc);
+    g->rg = g->wg / tc;
+    return true;
+}
+
+template <int SF>
+__device__ __forceinline__ float ld_scale(const void *S, size_t at)
+{
+    if (SF == 0) return dec_e8m0(((const uint8_t *)S)[at]);
+    return ((const float *)S)[at];
+}
+
+/* Dot of 16 decoded weights with 16 activations; 4 interleaved chains. */
+__device__ __forceinline__ float dot16(const u32x4 v, const float *xr)
+{
+    float w[16];
+    dec_e4m3x4(v.x, w + 0);
+    dec_e4m3x4(v.y, w + 4);
+    dec_e4m3x4(v.z, w + 8);
+    dec_e4m3x4(v.w, w + 12);
+    float p0 = w[0] * xr[0], p1 = w[1] * xr[1];
+    float p2 = w[2] * xr[2], p3 = w[3] * xr[3];
+#pragma unroll
+    for (int e = 4; e < 16; e += 4) {
+        p0 = fmaf(w[e + 0], xr[e + 0], p0);
+        p1 = fmaf(w[e + 1], xr[e + 1], p1);
+        p2 = fmaf(w[e + 2], xr[e + 2], p2);
+        p3 = fmaf(w[e + 3], xr[e + 3], p3);
+    }
+    return (p0 + p1) + (p2 + p3);
+}
+
+template <int NCH, int R, int SF>
+__global__ void __launch_bounds__(256)
+k_fp8_gemv(float *__restrict__ y, const float *__restrict__ x,
+           const uint8_t *__restrict__ W, const void *__restrict__ S,
+           int rows, int cols, int sc, int blk_r, int blk_c, int tc,
+           int tiles_per_wg, int ntiles)
+{
+    __shared__ float red[4][R];             /* [wave][row] partials        */
+
+    const int tid = threadIdx.x;
+    const int g = tid / tc;
+    const int j = tid - g * tc;
+    const int rg = blockDim.x / tc;
+    const int ch = cols >> 4;
+    const int wid = tid >> 6, lane = tid & 63;
+
+    float xr[NCH][16];
+    int cb[NCH];                             /* column-block of each chunk */
+    bool act[NCH];
+#pragma unroll
+    for (int n = 0; n < NCH; n++) {
+        const int c = j + n * tc;
+        act[n] = c < ch;
+        cb[n] = act[n] ? (c * 16) / blk_c : 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const f32x4 v = act[n] ? ldf4(x + c * 16 + q * 4) : f32x4{0, 0, 0, 0};
+            xr[n][q * 4 + 0] = v.x; xr[n][q * 4 + 1] = v.y;
+            xr[n][q * 4 + 2] = v.z; xr[n][q * 4 + 3] = v.w;
+        }
+    }
+
+    int cur_rb = -1;
+    float sreg[NCH];
+#pragma unroll
+    for (int n = 0; n < NCH; n++) sreg[n] = 0.0f;
+
+    const int t0 = blockIdx.x * tiles_per_wg;
+    const int t1 = min(ntiles, t0 + tiles_per_wg);
+    for (int tile = t0; tile < t1; ++tile) {
+        const int rbase = (tile * rg + g) * R;
+
+        u32x4 wv[R][NCH];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int r = rbase + i;
+#pragma unroll
+            for (int n = 0; n < NCH; n++) {
+                if (act[n] && r < rows)
+                    wv[i][n] = ld16_stream(W + (size_t)r * cols
+                                           + (size_t)(j + n * tc) * 16);
+                else
+                    wv[i][n] = u32x4{0, 0, 0, 0};
+            }
+        }
+
+        float acc[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int r = min(rbase + i, rows - 1);
+            const int rb = r / blk_r;
+            if (rb != cur_rb) {
+#pragma unroll
+                for (int n = 0; n < NCH; n++)
+                    sreg[n] = act[n] ? ld_scale<SF>(S, (size_t)rb * sc + cb[n]) : 0.0f;
+                cur_rb = rb;
+            }
+            float a = 0.0f;
+#pragma unroll
+            for (int n = 0; n < NCH; n++)
+                a = fmaf(dot16(wv[i][n], xr[n]), sreg[n], a);
+            acc[i] = a;
+        }
+
+        if (tc <= 64) {
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                const float v = seg_sum_rt(acc[i], tc);
+                if (j == tc - 1 && rbase + i < rows) y[rbase + i] = v;
+            }
+        } else {
+            const int wpr = tc >> 6;
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                const float v = seg_sum<64>(acc[i]);
+                if (lane == 63) red[wid][i] = v;
+            }
+            __syncthreads();
+            if (tid < rg * R) {
+                const int gg = tid / R, ii = tid - gg * R;
+                const int r = (tile * rg + gg) * R + ii;
+                float s = red[gg * wpr][ii];
+                for (int w = 1; w < wpr; w++) s += red[gg * wpr + w][ii];
+                if (r < rows) y[r] = s;
+            }
+            __syncthreads();
+        }
+    }
+}
+
+/* Batched: the per-(row, token) arithmetic of k_fp8_gemv with R = 1, looped
+ * over tokens in blocks of TB with the row's weight chunks held in VGPRs. */
+template <int NCH, int SF>
+__global__ void __launch_bounds__(256)
+k_fp8_gemv_n(float *__restrict__ y, const float *__restrict__ x,
+             const uint8_t *__restrict__ W, const void *__restrict__ S,
+             int rows, int cols, int sc, int blk_r, int blk_c, int tc, int nt)
+{
+    constexpr int TB = 8;
+    __shared__ float red[4][TB];
+
+    const int tid = threadIdx.x;
+    const int g = tid / tc;
+    const int j = tid - g * tc;
+    const int rg = blockDim.x / tc;
+    const int ch = cols >> 4;
+    const int wid = tid >> 6, lane = tid & 63;
+    const int r = blockIdx.x * rg + g;       /* this row group's row */
+    const bool rok = r < rows;
+
+    u32x4 wv[NCH];
+    float sreg[NCH];
+    bool act[NCH];
+#pragma unroll
+    for (int n = 0; n < NCH; n++) {
+        const int c = j + n * tc;
+        act[n] = c < ch;
+        wv[n] = (act[n] && rok) ? ld16(W + (size_t)r * cols + (size_t)c * 16)
+                                : u32x4{0, 0, 0, 0};
+        sreg[n] = (act[n] && rok)
+                ? ld_scale<SF>(S, (size_t)(r / blk_r) * sc + (c * 16) / blk_c)
+                : 0.0f;
+    }
+
+    for (int tb = 0; tb < nt; tb += TB) {
+        float acc[TB];
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            float a = 0.0f;
+            if (tb + t < nt) {
+                const float *xt = x + (size_t)(tb + t) * cols;
+#pragma unroll
+                for (int n = 0; n < NCH; n++) {
+                    float xr[16];
+                    const int c = j + n * tc;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const f32x4 v = act[n] ? ldf4(xt + c * 16 + q * 4)
+                                               : f32x4{0, 0, 0, 0};
+                        xr[q * 4 + 0] = v.x; xr[q * 4 + 1] = v.y;
+                        xr[q * 4 + 2] = v.z; xr[q * 4 + 3] = v.w;
+                    }
+                    a = fmaf(dot16(wv[n], xr), sreg[n], a);
+                }
+            }
+            acc[t] = a;
+        }
+        if (tc <= 64) {
+#pragma unroll
+            for (int t = 0; t < TB; t++) {
+                const float v = seg_sum_rt(acc[t], tc);
+                if (j == tc - 1 && rok && tb + t < nt)
+                    y[(size_t)(tb + t) * rows + r] = v;
+            }
+        } else {
+            const int wpr = tc >> 6;
+#pragma unroll
+            for (int t = 0; t < TB; t++) {
+                const float v = seg_sum<64>(acc[t]);
+                if (lane == 63) red[wid][t] = v;
+            }
+            __syncthreads();
+            if (tid < rg * TB) {
+                const int gg = tid / TB, tt = tid - gg * TB;
+                const int rr = blockIdx.x * rg + gg;
+                float s = red[gg * wpr][tt];
+                for (int w = 1; w < wpr; w++) s += red[gg * wpr + w][tt];
+                if (rr < rows && tb + tt < nt) y[(size_t)(tb + tt) * rows + rr] = s;
+            }
+            __syncthreads();
+        }
+    }
+}
+
+/* Any shape the chunked kernel does not take (cols not a multiple of 16, or
+ * wider than 16384): one wave per row, one element per lane per step. */
+template <int SF>
+__global__ void __launch_bounds__(256)
+k_fp8_gemv_generic(float *__restrict__ y, const float *__restrict__ x,
+                   const uint8_t *__restrict__ W, const void *__restrict__ S,
+                   int rows, int cols, int sc, int blk_r, int blk_c, int nt)
+{
+    const int wpb = blockDim.x >> 6;
+    const int r = blockIdx.x * wpb + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const uint8_t *row = W + (size_t)r * cols;
+    for (int t = 0; t < nt; t++) {
+        const float *xt = x + (size_t)t * cols;
+        float a = 0.0f;
+        for (int c = lane; c < cols; c += 64) {
+            const float s = ld_scale<SF>(S, (size_t)(r / blk_r) * sc + c / blk_c);
+            a = fmaf(dec_e4m3(row[c]) * xt[c], s, a);
+        }
+        const float v = wave_sum(a);
+        if (lane == 0) y[(size_t)t * rows + r] = v;
+    }
+}
+
+int g_fp8_R_override = -1;
+int g_fp8_maxwg = 0;
+
+void fp8_tuning_from_env()
+{
+    static int done = 0;
+    if (done) return;
+    done = 1;
+    const char *e = getenv("DSV4_GPU_FP8_R");
+    if (e) g_fp8_R_override = atoi(e);
+    e = getenv("DSV4_GPU_FP8_MAXWG");
+    if (e) g_fp8_maxwg = atoi(e);
+}
+
+template <int NCH, int R, int SF>
+void launch_gemv(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
+                 const void *S, int rows, int cols, int sc, int blk_r,
+                 int blk_c, int ntiles, int maxwg, hipStream_t st)
+{
+    const int want = ntiles < maxwg ? ntiles : maxwg;
+    const int tpw = (ntiles + want - 1) / want;
+    const int grid = (ntiles + tpw - 1) / tpw;
+    hipLaunchKernelGGL((k_fp8_gemv<NCH, R, SF>), dim3(grid), dim3(g.wg), 0, st,
+                       y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, tpw,
+                       ntiles);
+}
+
+template <int R, int SF>
+void launch_gemv_nch(const Fp8Geom &g, float *y, const float *x,
+                     const uint8_t *W, const void *S, int rows, int cols,
+                     int sc, int blk_r, int blk_c, int ntiles, int maxwg,
+                     hipStream_t st)
+{
+    switch (g.nch) {
+    case 1: launch_gemv<1, R, SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, ntiles, maxwg, st); break;
+    case 2: launch_gemv<2, R, SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, ntiles, maxwg, st); break;
+    case 3: launch_gemv<3, R, SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, ntiles, maxwg, st); break;
+    default: launch_gemv<4, R, SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, ntiles, maxwg, st); break;
+    }
+}
+
+template <int SF>
+void launch_gemv_sf(const Fp8Geom &g, int R, float *y, const float *x,
+                    const uint8_t *W, const void *S, int rows, int cols, int sc,
+                    int blk_r, int blk_c, int maxwg, hipStream_t st)
+{
+    const int per = g.rg * R;
+    const int ntiles = (rows + per - 1) / per;
+    switch (R) {
+    case 1: launch_gemv_nch<1, SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, ntiles, maxwg, st); break;
+    case 2: launch_gemv_nch<2, SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, ntiles, maxwg, st); break;
+    default: launch_gemv_nch<4, SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, ntiles, maxwg, st); break;
+    }
+}
+
+template <int SF>
+void launch_gemv_n(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
+                   const void *S, int rows, int cols, int sc, int blk_r,
+                   int blk_c, int nt, hipStream_t st)
+{
+    const int grid = (rows + g.rg - 1) / g.rg;
+    switch (g.nch) {
+    case 1: hipLaunchKernelGGL((k_fp8_gemv_n<1, SF>), dim3(grid), dim3(g.wg), 0, st, y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, nt); break;
+    case 2: hipLaunchKernelGGL((k_fp8_gemv_n<2, SF>), dim3(grid), dim3(g.wg), 0, st, y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, nt); break;
+    case 3: hipLaunchKernelGGL((k_fp8_gemv_n<3, SF>), dim3(grid), dim3(g.wg), 0, st, y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, nt); break;
+    default: hipLaunchKernelGGL((k_fp8_gemv_n<4, SF>), dim3(grid), dim3(g.wg), 0, st, y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, nt); break;
+    }
+}
+
+bool blocking_ok(int blk_r, int blk_c)
+{
+    return blk_r >= 1 && blk_c >= 16 && (blk_c & 15) == 0;
+}
+
+} // namespace
+
+int dsv4_fp8_gemv_launch(float *y, const float *x, const uint8_t *W,
+                         const void *S, int sfmt, int rows, int cols,
+                         int blk_r, int blk_c, hipStream_t st)
+{
+    if (rows <= 0 || cols <= 0 || blk_r <= 0 || blk_c <= 0) {
+        DSV4_ERR("fp8 gemv: bad shape %dx%d blk %dx%d", rows, cols, blk_r, blk_c);
+        return -1;
+    }
+    fp8_tuning_from_env();
+    const int sc = (cols + blk_c - 1) / blk_c;
+    Fp8Geom g;
+    if (fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c)) {
+        int R;
+        if (g_fp8_R_override > 0) {
+            R = g_fp8_R_override >= 4 ? 4 : g_fp8_R_override >= 2 ? 2 : 1;
+        } else {
+            R = 1;
+            for (int cand = 4; cand >= 2; cand >>= 1) {
+                const int tiles = (rows + g.rg * cand - 1) / (g.rg * cand);
+                if (tiles >= 2048) { R = cand; break; }
+            }
+        }
+        const int maxwg = g_fp8_maxwg > 0 ? g_fp8_maxwg : 2048;
+        if (sfmt == 0)
+            launch_gemv_sf<0>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, maxwg, st);
+        else
+            launch_gemv_sf<1>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, maxwg, st);
+    } else {
+        const int grid = (rows + 3) / 4;
+        if (sfmt == 0)
+            hipLaunchKernelGGL((k_fp8_gemv_generic<0>), dim3(grid), dim3(256), 0, st,
+                               y, x, W, S, rows, cols, sc, blk_r, blk_c, 1);
+        else
+            hipLaunchKernelGGL((k_fp8_gemv_generic<1>), dim3(grid), dim3(256), 0, st,
+                               y, x, W, S, rows, cols, sc, blk_r, blk_c, 1);
+    }
+    HIP_OK(hipGetLastError(), "fp8 gemv launch");
+    return 0;
+}
+
+int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,
+                           const void *S, int sfmt, int rows, int cols,
+                           int blk_r, int blk_c, int nt, hipStream_t st)
+{
+    if (rows <= 0 || cols <= 0 || nt <= 0 || blk_r <= 0 || blk_c <= 0) {
+        DSV4_ERR("fp8 gemv_n: bad shape %dx%d nt %d", rows, cols, nt);
+        return -1;
+    }
+    const int sc = (cols + blk_c - 1) / blk_c;
+    Fp8Geom g;
+    if (fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c)) {
+        if (sfmt == 0)
+            launch_gemv_n<0>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st);
+        else
+            launch_gemv_n<1>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st);
+    } else {
+        const int grid = (rows + 3) / 4;
+        if (sfmt == 0)
+            hipLaunchKernelGGL((k_fp8_gemv_generic<0>), dim3(grid), dim3(256), 0, st,
+                               y, x, W, S, rows, cols, sc, blk_r, blk_c, nt);
+        else
+            hipLaunchKernelGGL((k_fp8_gemv_generic<1>), dim3(grid), dim3(256), 0, st,
+                               y, x, W, S, rows, cols, sc, blk_r, blk_c, nt);
+    }
+    HIP_OK(hipGetLastError(), "fp8 gemv_n launch");
+    return 0;
+}

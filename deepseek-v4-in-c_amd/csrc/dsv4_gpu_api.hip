@@ -1,0 +1,798 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/* dsv4_gpu_api.hip - the C ABI of include/dsv4_gpu.h: device bring-up,
+ * residency, staging, scratch and the entry points.
+ *
+ * Mirrors the reference backend's contract (src/cuda/dsv4_cuda.cu:232-469):
+ * matrices resident in HBM keyed by their host weight pointer, activations
+ * crossing through pinned host staging allocated once and reused (the
+ * reference measured pageable copies cost CPU-side throughput 32x,
+ * dsv4_cuda.cu:357-369), 0 / -1 for recoverable failures and abort() on a
+ * contract violation. What differs is MI355X-first:
+ *   - all work goes to one library stream at default priority; host-buffer
+ *     calls are one H2D copy, the kernels, one D2H copy and a stream sync;
+ *   - every input of a call shares one staging arena, so a call with several
+ *     inputs still makes one H2D transfer;
+ *   - the residency table resolves row-range views of a resident matrix;
+ *   - routed experts and KV stores are resident too, keyed by (layer,
+ *     expert) and by handle.
+ */
+#include "dsv4_internal.h"
+#include "dsv4_dev.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+namespace {
+
+/* ------------------------------------------------------------- residency */
+struct Res {
+    const uint8_t *key, *key_end;   /* host weight bytes [key, key_end)   */
+    const uint8_t *skey;            /* host scale grid                     */
+    uint8_t *dw, *ds;
+    int rows, cols, blk_r, blk_c, sc, sfmt;
+};
+
+struct LayerExperts {
+    std::vector<Dsv4ExpertDev> host;        /* by expert id              */
+    std::vector<void *> owned;              /* device blocks we allocated */
+    Dsv4ExpertDev *dev = nullptr;           /* device copy of `host`      */
+    size_t dev_cap = 0;
+    bool dirty = false;
+    int hidden = 0, inter = 0;
+};
+
+struct Arena {
+    char *h = nullptr, *d = nullptr;
+    size_t cap = 0;
+};
+
+struct Scratch {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+bool g_ready = false;
+hipStream_t g_stream = nullptr;
+std::vector<Res> g_res;
+std::vector<LayerExperts> g_layers;
+Arena g_ar;
+Scratch g_moe_h, g_moe_acc, g_attn, g_scores;
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+int arena_reserve(size_t bytes)
+{
+    if (bytes <= g_ar.cap) return 0;
+    size_t cap = g_ar.cap ? g_ar.cap : (1u << 20);
+    while (cap < bytes) cap *= 2;
+    HIP_OK(hipStreamSynchronize(g_stream), "sync before staging growth");
+    if (g_ar.h) (void)hipHostFree(g_ar.h);
+    if (g_ar.d) (void)hipFree(g_ar.d);
+    g_ar.h = g_ar.d = nullptr;
+    g_ar.cap = 0;
+    HIP_OK(hipHostMalloc((void **)&g_ar.h, cap, hipHostMallocDefault),
+           "hipHostMalloc staging");
+    HIP_OK(hipMalloc((void **)&g_ar.d, cap), "hipMalloc staging");
+    g_ar.cap = cap;
+    return 0;
+}
+
+int scratch_reserve(Scratch &s, size_t bytes)
+{
+    if (bytes <= s.cap) return 0;
+    /* A buffer may still be in use by stream-ordered work on any stream. */
+    HIP_OK(hipDeviceSynchronize(), "sync before scratch growth");
+    if (s.p) (void)hipFree(s.p);
+    s.p = nullptr;
+    s.cap = 0;
+    HIP_OK(hipMalloc(&s.p, bytes), "hipMalloc scratch");
+    s.cap = bytes;
+    return 0;
+}
+
+/* A staged host-buffer call: inputs are packed into the arena, copied in one
+ * transfer; outputs are copied back in one transfer. */
+struct Stage {
+    size_t used = 0;
+    struct In { const void *src; size_t off, bytes; };
+    std::vector<In> ins;
+    size_t add(size_t bytes) { const size_t o = used; used = align256(used + bytes); return o; }
+    size_t in(const void *src, size_t bytes)
+    {
+        const size_t o = add(bytes);
+        ins.push_back({src, o, bytes});
+        return o;
+    }
+};
+
+int stage_push(Stage &s, size_t *in_end)
+{
+    if (arena_reserve(s.used ? s.used : 256) != 0) return -1;
+    size_t end = 0;
+    for (const auto &i : s.ins) {
+        memcpy(g_ar.h + i.off, i.src, i.bytes);
+        end = i.off + i.bytes;
+    }
+    if (end)
+        HIP_OK(hipMemcpyAsync(g_ar.d, g_ar.h, end, hipMemcpyHostToDevice, g_stream),
+               "H2D staging");
+    *in_end = end;
+    return 0;
+}
+
+int stage_pull(size_t off, size_t bytes, void *dst)
+{
+    if (bytes)
+        HIP_OK(hipMemcpyAsync(g_ar.h + off, g_ar.d + off, bytes,
+                              hipMemcpyDeviceToHost, g_stream), "D2H staging");
+    HIP_OK(hipStreamSynchronize(g_stream), "stream sync");
+    if (bytes) memcpy(dst, g_ar.h + off, bytes);
+    return 0;
+}
+
+/* Resolve m to a resident matrix and a row offset; nullptr if none. */
+const Res *find_view(const DSV4QMat *m, int *r0)
+{
+    if (!m || !m->w) return nullptr;
+    const uint8_t *p = (const uint8_t *)m->w;
+    for (const Res &r : g_res) {
+        if (p < r.key || p >= r.key_end) continue;
+        if (m->wdt != DSV4_WFP8 || m->cols != r.cols || m->blk_r != r.blk_r ||
+            m->blk_c != r.blk_c || m->rows <= 0)
+            return nullptr;
+        const size_t off = (size_t)(p - r.key);
+        if (off % (size_t)r.cols) return nullptr;
+        const int row0 = (int)(off / (size_t)r.cols);
+        if (row0 + m->rows > r.rows) return nullptr;
+        if (row0 % r.blk_r) return nullptr;
+        const size_t ssz = r.sfmt ? 4 : 1;
+        const uint8_t *want_s = r.skey + (size_t)(row0 / r.blk_r) * r.sc * ssz;
+        if ((const uint8_t *)m->s != want_s) return nullptr;
+        *r0 = row0;
+        return &r;
+    }
+    return nullptr;
+}
+
+int upload_fp8(const DSV4QMat *m, int sfmt)
+{
+    if (!g_ready || !m || !m->w || !m->s) return -1;
+    if (m->wdt != DSV4_WFP8 || m->rows <= 0 || m->cols <= 0 || m->blk_r <= 0 ||
+        m->blk_c <= 0)
+        return -1;
+    for (const Res &r : g_res)
+        if (r.key == (const uint8_t *)m->w) return 0;
+    const int sc = (m->cols + m->blk_c - 1) / m->blk_c;
+    const size_t wb = (size_t)m->rows * (size_t)m->cols;
+    const size_t sb = (size_t)((m->rows + m->blk_r - 1) / m->blk_r) * sc *
+                      (sfmt ? 4u : 1u);
+    if (wb + sb + (256u << 20) > dsv4_gpu_free_vram()) return -1;
+    uint8_t *dw = nullptr, *ds = nullptr;
+    if (hipMalloc((void **)&dw, wb) != hipSuccess) return -1;
+    if (hipMalloc((void **)&ds, sb) != hipSuccess) { (void)hipFree(dw); return -1; }
+    if (hipMemcpy(dw, m->w, wb, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(ds, m->s, sb, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(dw); (void)hipFree(ds);
+        return -1;
+    }
+    Res r;
+    r.key = (const uint8_t *)m->w;
+    r.key_end = r.key + wb;
+    r.skey = (const uint8_t *)m->s;
+    r.dw = dw; r.ds = ds;
+    r.rows = m->rows; r.cols = m->cols;
+    r.blk_r = m->blk_r; r.blk_c = m->blk_c;
+    r.sc = sc; r.sfmt = sfmt;
+    g_res.push_back(r);
+    return 0;
+}
+
+/* --------------------------------------------------------------- experts */
+bool expert_shape_ok(const DSV4ExpertW *e, int *hidden, int *inter)
+{
+    const DSV4QMat &a = e->w1, &b = e->w3, &c = e->w2;
+    if (a.wdt != DSV4_WFP4 || b.wdt != DSV4_WFP4 || c.wdt != DSV4_WFP4) return false;
+    if (!a.w || !a.s || !b.w || !b.s || !c.w || !c.s) return false;
+    if (a.rows != b.rows || a.cols != b.cols) return false;
+    if (c.rows != a.cols || c.cols != a.rows) return false;
+    if (a.blk_r != 1 || a.blk_c != 32 || b.blk_r != 1 || b.blk_c != 32 ||
+        c.blk_r != 1 || c.blk_c != 32)
+        return false;
+    if ((a.cols & 31) || (a.rows & 31)) return false;
+    *hidden = a.cols;
+    *inter = a.rows;
+    return true;
+}
+
+LayerExperts *layer_slot(int layer, int expert)
+{
+    if (layer < 0 || expert < 0 || layer > 4096 || expert > (1 << 20)) return nullptr;
+    if ((size_t)layer >= g_layers.size()) g_layers.resize(layer + 1);
+    LayerExperts &L = g_layers[layer];
+    if ((size_t)expert >= L.host.size()) L.host.resize(expert + 1, Dsv4ExpertDev{});
+    return &L;
+}
+
+int layer_sync(LayerExperts &L)
+{
+    if (!L.dirty) return 0;
+    const size_t bytes = L.host.size() * sizeof(Dsv4ExpertDev);
+    if (bytes > L.dev_cap) {
+        HIP_OK(hipDeviceSynchronize(), "sync before expert table growth");
+        if (L.dev) (void)hipFree(L.dev);
+        L.dev = nullptr;
+        L.dev_cap = 0;
+        HIP_OK(hipMalloc((void **)&L.dev, bytes * 2), "hipMalloc expert table");
+        L.dev_cap = bytes * 2;
+    }
+    HIP_OK(hipMemcpy(L.dev, L.host.data(), bytes, hipMemcpyHostToDevice),
+           "expert table copy");
+    L.dirty = false;
+    return 0;
+}
+
+int register_expert(int layer, int expert, const Dsv4ExpertDev &d, int hidden,
+                    int inter, void *owned)
+{
+    LayerExperts *L = layer_slot(layer, expert);
+    if (!L) return -1;
+    if ((L->hidden || L->inter) && (L->hidden != hidden || L->inter != inter)) {
+        DSV4_ERR("layer %d expert %d is %dx%d but the layer's experts are %dx%d",
+                 layer, expert, inter, hidden, L->inter, L->hidden);
+        return -1;
+    }
+    L->hidden = hidden;
+    L->inter = inter;
+    L->host[expert] = d;
+    if (owned) L->owned.push_back(owned);
+    L->dirty = true;
+    return 0;
+}
+
+hipStream_t as_stream(void *s) { return (hipStream_t)s; }
+
+/* ----------------------------------------------------------- decoder dumps */
+__global__ void k_dump(float *out, int which)
+{
+    const int i = threadIdx.x;
+    if (which == 0) out[i] = dec_e4m3((uint8_t)i);
+    else if (which == 1) out[i] = dec_e8m0((uint32_t)i);
+    else if (which == 2) {
+        if (i < 16) {
+            float o[2];
+            dec_fp4x2<0>((uint32_t)i, o);               /* code i in the low nibble */
+            out[i] = o[0];
+        }
+    } else {
+        float o[8];
+        dec_fp4x8((uint32_t)i, o);                      /* byte i in byte lane 0 */
+        out[2 * i] = o[0];
+        out[2 * i + 1] = o[1];
+    }
+}
+
+int dump(float *host, int which, int count)
+{
+    if (!g_ready && dsv4_gpu_init() != 0) return -1;
+    float *d = nullptr;
+    HIP_OK(hipMalloc((void **)&d, 512 * sizeof(float)), "hipMalloc dump");
+    hipLaunchKernelGGL(k_dump, dim3(1), dim3(256), 0, g_stream, d, which);
+    const hipError_t e = hipGetLastError();
+    hipError_t c = hipSuccess;
+    if (e == hipSuccess)
+        c = hipMemcpyAsync(host, d, (size_t)count * sizeof(float),
+                           hipMemcpyDeviceToHost, g_stream);
+    const hipError_t s = hipStreamSynchronize(g_stream);
+    (void)hipFree(d);
+    if (e != hipSuccess || c != hipSuccess || s != hipSuccess) {
+        DSV4_ERR("decoder dump failed");
+        return -1;
+    }
+    return 0;
+}
+
+} // namespace
+
+/* ===================================================================== ABI */
+extern "C" {
+
+int dsv4_gpu_available(void)
+{
+    int n = 0;
+    return (hipGetDeviceCount(&n) == hipSuccess && n > 0) ? 1 : 0;
+}
+
+int dsv4_gpu_set_blocking_sync(void)
+{
+    HIP_OK(hipSetDeviceFlags(hipDeviceScheduleBlockingSync), "hipSetDeviceFlags");
+    return 0;
+}
+
+int dsv4_gpu_init(void)
+{
+    if (g_ready) return 0;
+    int n = 0;
+    HIP_OK(hipGetDeviceCount(&n), "hipGetDeviceCount");
+    if (n < 1) { DSV4_ERR("no device"); return -1; }
+    HIP_OK(hipSetDevice(0), "hipSetDevice");
+    hipDeviceProp_t p;
+    HIP_OK(hipGetDeviceProperties(&p, 0), "hipGetDeviceProperties");
+    size_t freeb = 0, totb = 0;
+    HIP_OK(hipMemGetInfo(&freeb, &totb), "hipMemGetInfo");
+    HIP_OK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking),
+           "hipStreamCreate");
+    printf("hip: %s (%s), %d CUs, %.2f GB free of %.2f GB\n", p.name,
+           p.gcnArchName, p.multiProcessorCount, (double)freeb / 1073741824.0,
+           (double)totb / 1073741824.0);
+    fflush(stdout);
+    g_ready = true;
+    return 0;
+}
+
+size_t dsv4_gpu_free_vram(void)
+{
+    size_t freeb = 0, totb = 0;
+    if (!g_ready || hipMemGetInfo(&freeb, &totb) != hipSuccess) return 0;
+    return freeb;
+}
+
+void dsv4_gpu_shutdown(void)
+{
+    if (!g_ready) return;
+    (void)hipDeviceSynchronize();
+    for (Res &r : g_res) { (void)hipFree(r.dw); (void)hipFree(r.ds); }
+    g_res.clear();
+    for (LayerExperts &L : g_layers) {
+        for (void *p : L.owned) (void)hipFree(p);
+        if (L.dev) (void)hipFree(L.dev);
+    }
+    g_layers.clear();
+    for (Scratch *s : {&g_moe_h, &g_moe_acc, &g_attn, &g_scores}) {
+        if (s->p) (void)hipFree(s->p);
+        s->p = nullptr;
+        s->cap = 0;
+    }
+    if (g_ar.h) (void)hipHostFree(g_ar.h);
+    if (g_ar.d) (void)hipFree(g_ar.d);
+    g_ar = Arena{};
+    if (g_stream) (void)hipStreamDestroy(g_stream);
+    g_stream = nullptr;
+    g_ready = false;
+}
+
+/* ------------------------------------------------------------------- FP8 */
+int dsv4_gpu_upload(const DSV4QMat *m) { return upload_fp8(m, 0); }
+int dsv4_gpu_upload_f32s(const DSV4QMat *m) { return upload_fp8(m, 1); }
+
+int dsv4_gpu_has(const DSV4QMat *m)
+{
+    int r0;
+    return (g_ready && find_view(m, &r0)) ? 1 : 0;
+}
+
+void dsv4_gpu_mmq(float *y, const float *x, const DSV4QMat *m)
+{
+    int r0 = 0;
+    const Res *r = g_ready ? find_view(m, &r0) : nullptr;
+    if (!r) {
+        DSV4_ERR("mmq called for a matrix that is not resident");
+        abort();
+    }
+    Stage s;
+    const size_t xo = s.in(x, (size_t)r->cols * sizeof(float));
+    const size_t yo = s.add((size_t)m->rows * sizeof(float));
+    size_t end;
+    if (stage_push(s, &end) != 0) abort();
+    const size_t ssz = r->sfmt ? 4 : 1;
+    const int rc = dsv4_fp8_gemv_launch(
+        (float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
+        r->dw + (size_t)r0 * r->cols,
+        r->ds + (size_t)(r0 / r->blk_r) * r->sc * ssz, r->sfmt, m->rows,
+        r->cols, r->blk_r, r->blk_c, g_stream);
+    if (rc != 0 || stage_pull(yo, (size_t)m->rows * sizeof(float), y) != 0) {
+        DSV4_ERR("mmq failed");
+        abort();
+    }
+}
+
+void dsv4_gpu_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
+{
+    if (nt <= 1) { dsv4_gpu_mmq(y, x, m); return; }
+    int r0 = 0;
+    const Res *r = g_ready ? find_view(m, &r0) : nullptr;
+    if (!r || nt > DSV4_MAX_BATCH) {
+        DSV4_ERR("mmq_n called for a matrix that is not resident, or a batch "
+                 "of %d above %d", nt, DSV4_MAX_BATCH);
+        abort();
+    }
+    Stage s;
+    const size_t xo = s.in(x, (size_t)nt * r->cols * sizeof(float));
+    const size_t yo = s.add((size_t)nt * m->rows * sizeof(float));
+    size_t end;
+    if (stage_push(s, &end) != 0) abort();
+    const size_t ssz = r->sfmt ? 4 : 1;
+    const int rc = dsv4_fp8_gemv_n_launch(
+        (float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
+        r->dw + (size_t)r0 * r->cols,
+        r->ds + (size_t)(r0 / r->blk_r) * r->sc * ssz, r->sfmt, m->rows,
+        r->cols, r->blk_r, r->blk_c, nt, g_stream);
+    if (rc != 0 ||
+        stage_pull(yo, (size_t)nt * m->rows * sizeof(float), y) != 0) {
+        DSV4_ERR("mmq_n failed");
+        abort();
+    }
+}
+
+int dsv4_gpu_fp8_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
+                        const void *d_s, int scale_fmt, int rows, int cols,
+                        void *stream)
+{
+    if (!d_y || !d_x || !d_w || !d_s || (scale_fmt != 0 && scale_fmt != 1)) {
+        DSV4_ERR("fp8_gemv_d: bad arguments");
+        return -1;
+    }
+    return dsv4_fp8_gemv_launch(d_y, d_x, d_w, d_s, scale_fmt, rows, cols, 128,
+                                128, as_stream(stream));
+}
+
+/* ---------------------------------------------------------------- dumps */
+int dsv4_gpu_dump_e4m3(float *host256) { return dump(host256, 0, 256); }
+int dsv4_gpu_dump_e8m0(float *host256) { return dump(host256, 1, 256); }
+int dsv4_gpu_dump_e2m1(float *host16) { return dump(host16, 2, 16); }
+int dsv4_gpu_dump_fp4_bytes(float *host512) { return dump(host512, 3, 512); }
+
+/* -------------------------------------------------------------- experts */
+int dsv4_gpu_upload_expert(int layer, int expert, const DSV4ExpertW *e)
+{
+    int hidden, inter;
+    if (!g_ready || !e || !expert_shape_ok(e, &hidden, &inter)) return -1;
+    const size_t wb13 = (size_t)inter * hidden / 2, sb13 = (size_t)inter * hidden / 32;
+    const size_t wb2 = (size_t)hidden * inter / 2, sb2 = (size_t)hidden * inter / 32;
+    const size_t o1 = 0, os1 = align256(o1 + wb13), o3 = align256(os1 + sb13),
+                 os3 = align256(o3 + wb13), o2 = align256(os3 + sb13),
+                 os2 = align256(o2 + wb2), total = align256(os2 + sb2);
+    if (total + (256u << 20) > dsv4_gpu_free_vram()) return -1;
+    uint8_t *blk = nullptr;
+    if (hipMalloc((void **)&blk, total) != hipSuccess) return -1;
+    const struct { size_t off; const void *src; size_t n; } parts[6] = {
+        {o1, e->w1.w, wb13}, {os1, e->w1.s, sb13}, {o3, e->w3.w, wb13},
+        {os3, e->w3.s, sb13}, {o2, e->w2.w, wb2}, {os2, e->w2.s, sb2}};
+    for (const auto &pp : parts)
+        if (hipMemcpy(blk + pp.off, pp.src, pp.n, hipMemcpyHostToDevice) != hipSuccess) {
+            (void)hipFree(blk);
+            return -1;
+        }
+    LayerExperts *L = layer_slot(layer, expert);
+    if (L && L->host[expert].w1) {
+        /* Re-upload of the same key: keep the first copy (idempotent). */
+        (void)hipFree(blk);
+        return 0;
+    }
+    Dsv4ExpertDev d{blk + o1, blk + os1, blk + o3, blk + os3, blk + o2, blk + os2};
+    if (register_expert(layer, expert, d, hidden, inter, blk) != 0) {
+        (void)hipFree(blk);
+        return -1;
+    }
+    return 0;
+}
+
+int dsv4_gpu_bind_expert_d(int layer, int expert, const DSV4ExpertW *e)
+{
+    int hidden, inter;
+    if (!g_ready || !e || !expert_shape_ok(e, &hidden, &inter)) return -1;
+    Dsv4ExpertDev d{(const uint8_t *)e->w1.w, (const uint8_t *)e->w1.s,
+                    (const uint8_t *)e->w3.w, (const uint8_t *)e->w3.s,
+                    (const uint8_t *)e->w2.w, (const uint8_t *)e->w2.s};
+    return register_expert(layer, expert, d, hidden, inter, nullptr);
+}
+
+int dsv4_gpu_has_expert(int layer, int expert)
+{
+    if (!g_ready || layer < 0 || expert < 0 || (size_t)layer >= g_layers.size())
+        return 0;
+    const LayerExperts &L = g_layers[layer];
+    return ((size_t)expert < L.host.size() && L.host[expert].w1) ? 1 : 0;
+}
+
+static int moe_prepare(int layer, int topk, int hidden, int inter,
+                       LayerExperts **out)
+{
+    if (!g_ready || layer < 0 || (size_t)layer >= g_layers.size() || topk <= 0) {
+        DSV4_ERR("moe: layer %d has no resident experts", layer);
+        return -1;
+    }
+    LayerExperts &L = g_layers[layer];
+    if (L.hidden != hidden || L.inter != inter) {
+        DSV4_ERR("moe: layer %d experts are %dx%d, call asks %dx%d", layer,
+                 L.inter, L.hidden, inter, hidden);
+        return -1;
+    }
+    if (layer_sync(L) != 0) return -1;
+    if (scratch_reserve(g_moe_h, (size_t)topk * inter * sizeof(float)) != 0 ||
+        scratch_reserve(g_moe_acc, (size_t)topk * hidden * sizeof(float)) != 0)
+        return -1;
+    *out = &L;
+    return 0;
+}
+
+int dsv4_gpu_moe_fp4(float *out, const float *x, int layer, const int *idx,
+                     const float *w, int topk, int hidden, int inter,
+                     float swiglu_limit)
+{
+    LayerExperts *L;
+    if (moe_prepare(layer, topk, hidden, inter, &L) != 0) return -1;
+    for (int k = 0; k < topk; k++)
+        if (!dsv4_gpu_has_expert(layer, idx[k])) {
+            DSV4_ERR("moe: layer %d expert %d (k = %d) is not resident", layer,
+                     idx[k], k);
+            return -1;
+        }
+    Stage s;
+    const size_t xo = s.in(x, (size_t)hidden * sizeof(float));
+    const size_t io = s.in(idx, (size_t)topk * sizeof(int));
+    const size_t wo = s.in(w, (size_t)topk * sizeof(float));
+    const size_t oo = s.add((size_t)hidden * sizeof(float));
+    size_t end;
+    if (stage_push(s, &end) != 0) return -1;
+    if (dsv4_moe_fp4_launch((float *)(g_ar.d + oo), (const float *)(g_ar.d + xo),
+                            L->dev, (int)L->host.size(),
+                            (const int *)(g_ar.d + io), (const float *)(g_ar.d + wo),
+                            topk, hidden, inter, swiglu_limit, (float *)g_moe_h.p,
+                            (float *)g_moe_acc.p, g_stream) != 0)
+        return -1;
+    return stage_pull(oo, (size_t)hidden * sizeof(float), out);
+}
+
+int dsv4_gpu_moe_fp4_d(float *d_out, const float *d_x, int layer,
+                       const int *d_idx, const float *d_w, int topk,
+                       int hidden, int inter, float swiglu_limit, void *stream)
+{
+    LayerExperts *L;
+    if (moe_prepare(layer, topk, hidden, inter, &L) != 0) return -1;
+    return dsv4_moe_fp4_launch(d_out, d_x, L->dev, (int)L->host.size(), d_idx,
+                               d_w, topk, hidden, inter, swiglu_limit,
+                               (float *)g_moe_h.p, (float *)g_moe_acc.p,
+                               as_stream(stream));
+}
+
+/* ------------------------------------------------------------ KV stores */
+struct dsv4_gpu_kv {
+    void *data;
+    float *scales;
+    int n_rows, row_dim, fmt;
+    size_t esize;
+};
+
+dsv4_gpu_kv *dsv4_gpu_kv_create(int n_rows, int row_dim, int fmt)
+{
+    if (!g_ready || n_rows <= 0 || row_dim <= 0) return nullptr;
+    size_t es;
+    switch (fmt) {
+    case DSV4_GPU_KV_F32: es = 4; break;
+    case DSV4_GPU_KV_BF16: es = 2; break;
+    case DSV4_GPU_KV_FP8: es = 1; break;
+    default: DSV4_ERR("kv_create: unknown format %d", fmt); return nullptr;
+    }
+    dsv4_gpu_kv *kv = (dsv4_gpu_kv *)calloc(1, sizeof *kv);
+    if (!kv) return nullptr;
+    kv->n_rows = n_rows; kv->row_dim = row_dim; kv->fmt = fmt; kv->esize = es;
+    if (hipMalloc(&kv->data, (size_t)n_rows * row_dim * es) != hipSuccess) {
+        free(kv);
+        return nullptr;
+    }
+    if (fmt == DSV4_GPU_KV_FP8 &&
+        hipMalloc((void **)&kv->scales, (size_t)n_rows * sizeof(float)) != hipSuccess) {
+        (void)hipFree(kv->data);
+        free(kv);
+        return nullptr;
+    }
+    return kv;
+}
+
+int dsv4_gpu_kv_write_rows(dsv4_gpu_kv *kv, int row0, int n, const void *rows,
+                           const float *row_scales)
+{
+    if (!kv || row0 < 0 || n < 0 || row0 + n > kv->n_rows || (n && !rows)) return -1;
+    if (kv->fmt == DSV4_GPU_KV_FP8 && n && !row_scales) return -1;
+    const size_t rb = (size_t)kv->row_dim * kv->esize;
+    HIP_OK(hipMemcpy((char *)kv->data + (size_t)row0 * rb, rows, (size_t)n * rb,
+                     hipMemcpyHostToDevice), "kv write");
+    if (kv->fmt == DSV4_GPU_KV_FP8 && n)
+        HIP_OK(hipMemcpy(kv->scales + row0, row_scales, (size_t)n * sizeof(float),
+                         hipMemcpyHostToDevice), "kv scale write");
+    return 0;
+}
+
+void *dsv4_gpu_kv_data(const dsv4_gpu_kv *kv) { return kv ? kv->data : nullptr; }
+float *dsv4_gpu_kv_scales(const dsv4_gpu_kv *kv) { return kv ? kv->scales : nullptr; }
+
+void dsv4_gpu_kv_free(dsv4_gpu_kv *kv)
+{
+    if (!kv) return;
+    (void)hipDeviceSynchronize();
+    (void)hipFree(kv->data);
+    if (kv->scales) (void)hipFree(kv->scales);
+    free(kv);
+}
+
+/* Key rows [row0 + t] read at element offset row0*row_dim + t*key_stride. */
+static int key_view(const dsv4_gpu_kv *keys, int row0, int key_stride, int D,
+                    int n, const void **base, const float **sc)
+{
+    if (!keys || row0 < 0 || n < 0 || D <= 0 || key_stride < D) return -1;
+    if (keys->fmt == DSV4_GPU_KV_FP8 && key_stride != keys->row_dim) {
+        DSV4_ERR("indexer: FP8 keys carry one scale per stored row; the key "
+                 "stride must equal the row width");
+        return -1;
+    }
+    const size_t start = (size_t)row0 * keys->row_dim;
+    const size_t need = n ? start + (size_t)(n - 1) * key_stride + D : start;
+    if (need > (size_t)keys->n_rows * keys->row_dim) {
+        DSV4_ERR("indexer: %d keys at stride %d from row %d overrun the store",
+                 n, key_stride, row0);
+        return -1;
+    }
+    *base = (const char *)keys->data + start * keys->esize;
+    *sc = keys->scales ? keys->scales + row0 : nullptr;
+    return 0;
+}
+
+static float indexer_scale(int D, int H)
+{
+    return (1.0f / sqrtf((float)D)) * (1.0f / sqrtf((float)H));
+}
+
+int dsv4_gpu_indexer_score(float *out, const float *q, const float *w, int H,
+                           int D, const dsv4_gpu_kv *keys, int row0,
+                           int key_stride, int n)
+{
+    const void *kb;
+    const float *ks;
+    if (!g_ready || key_view(keys, row0, key_stride, D, n, &kb, &ks) != 0) return -1;
+    if (n == 0) return 0;
+    Stage s;
+    const size_t qo = s.in(q, (size_t)H * D * sizeof(float));
+    const size_t wo = s.in(w, (size_t)H * sizeof(float));
+    const size_t oo = s.add((size_t)n * sizeof(float));
+    size_t end;
+    if (stage_push(s, &end) != 0) return -1;
+    if (dsv4_indexer_score_launch((float *)(g_ar.d + oo), (const float *)(g_ar.d + qo),
+                                  (const float *)(g_ar.d + wo), H, D, kb, ks,
+                                  keys->fmt, key_stride, n, indexer_scale(D, H),
+                                  g_stream) != 0)
+        return -1;
+    return stage_pull(oo, (size_t)n * sizeof(float), out);
+}
+
+int dsv4_gpu_topk(int *idxs, const float *scores, int n, int k)
+{
+    if (!g_ready || n < 0) return -1;
+    if (k > n) k = n;
+    if (k <= 0) return k < 0 ? -1 : 0;
+    Stage s;
+    const size_t so = s.in(scores, (size_t)n * sizeof(float));
+    const size_t io = s.add((size_t)k * sizeof(int));
+    size_t end;
+    if (stage_push(s, &end) != 0) return -1;
+    if (dsv4_topk_launch((int *)(g_ar.d + io), (const float *)(g_ar.d + so), n, k,
+                         g_stream) != 0)
+        return -1;
+    if (stage_pull(io, (size_t)k * sizeof(int), idxs) != 0) return -1;
+    return k;
+}
+
+int dsv4_gpu_indexer_topk(int *idxs, const float *q, const float *w, int H,
+                          int D, const dsv4_gpu_kv *keys, int row0,
+                          int key_stride, int n, int k)
+{
+    const void *kb;
+    const float *ks;
+    if (!g_ready || key_view(keys, row0, key_stride, D, n, &kb, &ks) != 0) return -1;
+    if (k > n) k = n;
+    if (k <= 0) return k < 0 ? -1 : 0;
+    Stage s;
+    const size_t qo = s.in(q, (size_t)H * D * sizeof(float));
+    const size_t wo = s.in(w, (size_t)H * sizeof(float));
+    const size_t so = s.add((size_t)n * sizeof(float));
+    const size_t io = s.add((size_t)k * sizeof(int));
+    size_t end;
+    if (stage_push(s, &end) != 0) return -1;
+    if (dsv4_indexer_score_launch((float *)(g_ar.d + so), (const float *)(g_ar.d + qo),
+                                  (const float *)(g_ar.d + wo), H, D, kb, ks,
+                                  keys->fmt, key_stride, n, indexer_scale(D, H),
+                                  g_stream) != 0 ||
+        dsv4_topk_launch((int *)(g_ar.d + io), (const float *)(g_ar.d + so), n, k,
+                         g_stream) != 0)
+        return -1;
+    if (stage_pull(io, (size_t)k * sizeof(int), idxs) != 0) return -1;
+    return k;
+}
+
+int dsv4_gpu_sparse_attn(float *o, const float *q, const dsv4_gpu_kv *kv,
+                         const float *sink, const int *idxs, int h, int d_qk,
+                         int d_v, int topk, float scale)
+{
+    if (!g_ready || !kv || h <= 0 || topk < 0 || d_qk > kv->row_dim ||
+        d_v > kv->row_dim || kv->fmt == DSV4_GPU_KV_FP8)
+        return -1;
+    for (int j = 0; j < topk; j++)
+        if (idxs[j] >= kv->n_rows) {
+            DSV4_ERR("sparse attn: slot %d selects row %d of %d", j, idxs[j],
+                     kv->n_rows);
+            return -1;
+        }
+    if (scratch_reserve(g_attn, dsv4_attn_scratch_bytes(h, d_v, topk)) != 0) return -1;
+    Stage s;
+    const size_t qo = s.in(q, (size_t)h * d_qk * sizeof(float));
+    const size_t so = sink ? s.in(sink, (size_t)h * sizeof(float)) : 0;
+    const size_t io = topk ? s.in(idxs, (size_t)topk * sizeof(int)) : s.add(sizeof(int));
+    const size_t oo = s.add((size_t)h * d_v * sizeof(float));
+    size_t end;
+    if (stage_push(s, &end) != 0) return -1;
+    if (dsv4_attn_launch((float *)(g_ar.d + oo), (const float *)(g_ar.d + qo),
+                         kv->data, kv->fmt, kv->row_dim, kv->n_rows,
+                         sink ? (const float *)(g_ar.d + so) : nullptr,
+                         (const int *)(g_ar.d + io), h, d_qk, d_v, topk, scale,
+                         g_attn.p, g_stream) != 0)
+        return -1;
+    return stage_pull(oo, (size_t)h * d_v * sizeof(float), o);
+}
+
+int dsv4_gpu_indexer_score_d(float *d_out, const float *d_q, const float *d_w,
+                             int H, int D, const void *d_keys,
+                             const float *d_key_scales, int key_fmt,
+                             int key_stride, int n, float scale, void *stream)
+{
+    return dsv4_indexer_score_launch(d_out, d_q, d_w, H, D, d_keys, d_key_scales,
+                                     key_fmt, key_stride, n, scale,
+                                     as_stream(stream));
+}
+
+int dsv4_gpu_topk_d(int *d_idxs, const float *d_scores, int n, int k,
+                    void *stream)
+{
+    return dsv4_topk_launch(d_idxs, d_scores, n, k, as_stream(stream));
+}
+
+int dsv4_gpu_sparse_attn_d(float *d_o, const float *d_q, const void *d_kv,
+                           int kv_fmt, int kv_stride, int kv_rows,
+                           const float *d_sink, const int *d_idxs, int h,
+                           int d_qk, int d_v, int topk, float scale,
+                           void *stream)
+{
+    if (!g_ready) return -1;
+    if (scratch_reserve(g_attn, dsv4_attn_scratch_bytes(h, d_v, topk)) != 0) return -1;
+    return dsv4_attn_launch(d_o, d_q, d_kv, kv_fmt, kv_stride, kv_rows, d_sink,
+                            d_idxs, h, d_qk, d_v, topk, scale, g_attn.p,
+                            as_stream(stream));
+}
+
+int dsv4_gpu_mla_decode_d(float *d_o, int *d_idxs,
+                          const float *d_q_idx, const float *d_w_idx, int H,
+                          int D, const void *d_keys, const float *d_key_scales,
+                          int key_fmt, int key_stride, int n, int k,
+                          const float *d_q, const void *d_kv, int kv_fmt,
+                          int kv_stride, int kv_rows, const float *d_sink,
+                          int h, int d_qk, int d_v, float attn_scale,
+                          void *stream)
+{
+    if (!g_ready) return -1;
+    if (k > n) k = n;
+    if (k < 0) return -1;
+    hipStream_t st = as_stream(stream);
+    if (scratch_reserve(g_scores, (size_t)(n > 0 ? n : 1) * sizeof(float)) != 0 ||
+        scratch_reserve(g_attn, dsv4_attn_scratch_bytes(h, d_v, k)) != 0)
+        return -1;
+    if (n > 0 &&
+        (dsv4_indexer_score_launch((float *)g_scores.p, d_q_idx, d_w_idx, H, D,
+                                   d_keys, d_key_scales, key_fmt, key_stride, n,
+                                   indexer_scale(D, H), st) != 0 ||
+         dsv4_topk_launch(d_idxs, (const float *)g_scores.p, n, k, st) != 0))
+        return -1;
+    return dsv4_attn_launch(d_o, d_q, d_kv, kv_fmt, kv_stride, kv_rows, d_sink,
+                            d_idxs, h, d_qk, d_v, k, attn_scale, g_attn.p, st);
+}
+
+} /* extern "C" */

@@ -1,0 +1,68 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/* dsv4_internal.h - host-side launchers shared between the kernel files and
+ * the C-ABI layer. Not installed; the public surface is include/dsv4_gpu.h. */
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/dsv4_gpu.h"
+
+#define DSV4_ERR(...) do { fprintf(stderr, "dsv4_gpu: " __VA_ARGS__); \
+                           fputc('\n', stderr); } while (0)
+
+#define HIP_OK(call, what)                                                   \
+    do {                                                                     \
+        const hipError_t e_ = (call);                                        \
+        if (e_ != hipSuccess) {                                              \
+            DSV4_ERR("%s: %s", (what), hipGetErrorString(e_));               \
+            return -1;                                                       \
+        }                                                                    \
+    } while (0)
+
+/* Block-scaled FP8 GEMV. sfmt 0 = E8M0 bytes, 1 = fp32. S is the scale grid
+ * ceil(rows/blk_r) x sc with sc = ceil(cols/blk_c). Returns 0 / -1. */
+int dsv4_fp8_gemv_launch(float *y, const float *x, const uint8_t *W,
+                         const void *S, int sfmt, int rows, int cols,
+                         int blk_r, int blk_c, hipStream_t st);
+
+/* Batched: y[nt][rows], x[nt][cols]; per (row, token) bit-identical to the
+ * GEMV above. */
+int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,
+                           const void *S, int sfmt, int rows, int cols,
+                           int blk_r, int blk_c, int nt, hipStream_t st);
+
+/* One routed expert's device tensors (FP4 nibbles + E8M0 per 1x32). */
+struct Dsv4ExpertDev {
+    const uint8_t *w1, *s1, *w3, *s3, *w2, *s2;
+};
+
+/* Routed MoE on the device. experts: device array [n_table] of expert
+ * tensors for this layer; d_idx/d_w device [topk]; hbuf device scratch
+ * [topk][inter] f32; accbuf device scratch [topk][hidden] f32. */
+int dsv4_moe_fp4_launch(float *d_out, const float *d_x,
+                        const Dsv4ExpertDev *d_table, int n_table,
+                        const int *d_idx, const float *d_w, int topk,
+                        int hidden, int inter, float limit, float *hbuf,
+                        float *accbuf, hipStream_t st);
+
+int dsv4_indexer_score_launch(float *d_out, const float *d_q, const float *d_w,
+                              int H, int D, const void *d_keys,
+                              const float *d_key_scales, int key_fmt,
+                              int key_stride, int n, float scale,
+                              hipStream_t st);
+
+int dsv4_topk_launch(int *d_idxs, const float *d_scores, int n, int k,
+                     hipStream_t st);
+
+/* Scratch needed by dsv4_attn_launch, in bytes. */
+size_t dsv4_attn_scratch_bytes(int h, int d_v, int topk);
+
+/* Rows outside [0, kv_rows) are treated as masked (never read). */
+int dsv4_attn_launch(float *d_o, const float *d_q, const void *d_kv,
+                     int kv_fmt, int kv_stride, int kv_rows,
+                     const float *d_sink, const int *d_idxs, int h, int d_qk,
+                     int d_v, int topk, float scale, void *scratch,
+                     hipStream_t st);

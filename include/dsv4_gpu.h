@@ -1,0 +1,259 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/* dsv4_gpu.h - MI355X (gfx950) decode backend for deepseek-v4-in-c, C ABI.
+ *
+ * A drop-in for the reference's GPU co-processor header
+ * (include/dsv4/dsv4_cuda.h:65-99) and its CPU stub
+ * (src/cuda/dsv4_cuda_stub.c): the same entry points under the dsv4_gpu_
+ * prefix, the same argument meaning and the same error behaviour, plus the
+ * three hot-path families the reference leaves on the CPU:
+ *
+ *   1. block-scaled FP8 e4m3 GEMV        (replaces k_mmq_fp8, dsv4_cuda.cu:93)
+ *   2. fused MXFP4 routed-expert matvec  (dsv4_layer.c:199-206, :412-476)
+ *   3. sparse-MLA indexer score, top-k and gather attention
+ *                                         (dsv4_indexer.c:64-106,
+ *                                          dsv4_attn.c:60-108)
+ *
+ * CONVENTIONS (as dsv4_cuda.h / dsv4_cuda.cu:16-24):
+ *   - Plain C, plain pointers and sizes. Host-buffer entry points take and
+ *     return host memory and are synchronous; the *_d entry points take
+ *     device pointers and a hipStream_t passed as void* (NULL = the default
+ *     stream) and are stream-ordered.
+ *   - int 0 on success, -1 on a recoverable failure, with a message prefixed
+ *     "dsv4_gpu:" on stderr. A contract violation (mmq on a matrix that is not
+ *     resident) calls abort(), as dsv4_cuda_mmq does (dsv4_cuda.cu:390-394).
+ *   - The caller owns every host buffer. The backend owns device copies made
+ *     by upload calls until dsv4_gpu_shutdown. Matrices are keyed by their host
+ *     weight pointer, which must stay stable (dsv4_cuda.cu:232-236).
+ *   - Single-threaded: call from one host thread (the reference contract,
+ *     dsv4_cuda.cu:243-249). Calls that overlap on one device race on the
+ *     backend's staging and scratch buffers.
+ *
+ * Built with hipcc for gfx950 as libdsv4_gpu.so; a CPU-only build links
+ * dsv4_gpu_stub.c instead, which defines every symbol below and reports no
+ * device.
+ */
+#ifndef DSV4_GPU_H
+#define DSV4_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+/* The operand types come from the reference's include/dsv4/dsv4.h. When that
+ * header is not in the include path, a layout-identical copy of the three
+ * pieces this ABI uses is declared here (dsv4.h:83, :92, :208-214,
+ * :252-255), so the same binary serves both. */
+#ifndef DSV4_H
+#define DSV4_MAX_BATCH 64
+enum { DSV4_WF32 = 0, DSV4_WBF16 = 1, DSV4_WFP8 = 2, DSV4_WFP4 = 3 };
+typedef struct {
+    const void *w;          /* packed weight bytes                     */
+    const void *s;          /* block scales (E8M0 bytes, or fp32)      */
+    int wdt;                /* DSV4_W*                                 */
+    int rows, cols;         /* LOGICAL element dims                    */
+    int blk_r, blk_c;       /* scale block: 128x128 (FP8), 1x32 (FP4)  */
+} DSV4QMat;
+typedef struct {
+    DSV4QMat w1, w3;        /* FP4 [inter, hidden]                     */
+    DSV4QMat w2;            /* FP4 [hidden, inter]                     */
+} DSV4ExpertW;
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ======================================================== device bring-up */
+
+/* 1 when built with HIP and a usable device is present; the stub returns 0.
+ * Replaces dsv4_cuda_available (dsv4_cuda.h:65, dsv4_cuda.cu:251). */
+int dsv4_gpu_available(void);
+
+/* Make the calling thread block instead of spin while waiting on the device.
+ * Must precede dsv4_gpu_init. Replaces dsv4_cuda_set_blocking_sync
+ * (dsv4_cuda.cu:264). */
+int dsv4_gpu_set_blocking_sync(void);
+
+/* Bring up device 0; prints name, arch and free/total HBM. 0 / -1.
+ * Replaces dsv4_cuda_init (dsv4_cuda.h:70, dsv4_cuda.cu:271). */
+int dsv4_gpu_init(void);
+
+/* Bytes of HBM still free (0 before init). Replaces dsv4_cuda_free_vram
+ * (dsv4_cuda.h:97). */
+size_t dsv4_gpu_free_vram(void);
+
+/* Free every device copy, staging and scratch buffer; reset state.
+ * Replaces dsv4_cuda_shutdown (dsv4_cuda.h:99, dsv4_cuda.cu:436). */
+void dsv4_gpu_shutdown(void);
+
+/* ===================================================== FP8 dense matrices */
+
+/* Copy one FP8 matrix (E8M0 block scales, the reference's format) into HBM,
+ * keyed by m->w. 0 ok; -1 recoverable (not FP8, no room with 256 MiB of
+ * headroom, copy failed) -- the matrix then stays on the CPU. Idempotent per
+ * key. Replaces dsv4_cuda_upload (dsv4_cuda.h:80, dsv4_cuda.cu:307). */
+int dsv4_gpu_upload(const DSV4QMat *m);
+
+/* The same for an FP8 matrix whose block scales are fp32 (m->s is a float
+ * grid ceil(rows/blk_r) x ceil(cols/blk_c)). No reference counterpart: the
+ * benchmark configurations specify fp32 block scales. */
+int dsv4_gpu_upload_f32s(const DSV4QMat *m);
+
+/* Is m resident? True for an uploaded matrix and for a ROW-RANGE VIEW of one:
+ * m->w points inside a resident weight block at a whole-row offset, with the
+ * same cols/wdt/blocking and m->s at the matching scale-grid row (how
+ * attention() slices wo_a per group, dsv4_layer.c:321-334). A view then runs
+ * only its own rows -- the reference keyed only exact pointers, so group 0's
+ * slice ran the whole wo_a (dsv4_cuda.cu:296-305). Replaces dsv4_cuda_has
+ * (dsv4_cuda.h:83). */
+int dsv4_gpu_has(const DSV4QMat *m);
+
+/* y[rows] = dequant(m) . x[cols], host buffers, synchronous. abort() if m is
+ * not resident. Replaces dsv4_cuda_mmq (dsv4_cuda.h:88, dsv4_cuda.cu:387). */
+void dsv4_gpu_mmq(float *y, const float *x, const DSV4QMat *m);
+
+/* y[nt][rows] for x[nt][cols]: one pass over the weights for the batch. Per
+ * (row, token) bit-identical to dsv4_gpu_mmq; nt == 1 forwards to it;
+ * nt > DSV4_MAX_BATCH aborts. Replaces dsv4_cuda_mmq_n (dsv4_cuda.h:94,
+ * dsv4_cuda.cu:410). */
+void dsv4_gpu_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt);
+
+/* Device-resident GEMV on raw device buffers, stream-ordered:
+ * d_y[rows] = dequant(d_w, d_s) . d_x[cols], 128x128 blocks. scale_fmt 0 =
+ * E8M0 bytes, 1 = fp32. What dsv4_gpu_mmq runs after staging. */
+int dsv4_gpu_fp8_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
+                        const void *d_s, int scale_fmt, int rows, int cols,
+                        void *stream);
+
+/* ========================================================== decoder gates */
+
+/* Device decode of all 256 E4M3FN codes / 256 E8M0 codes / 16 E2M1 codes with
+ * the exact decoders the kernels use, for bit-equality gates against
+ * dsv4_quant.h:74-164. dump_e4m3 replaces dsv4_cuda_dump_e4m3
+ * (dsv4_cuda.cu:460); the other two have no reference counterpart. */
+int dsv4_gpu_dump_e4m3(float *host256);
+int dsv4_gpu_dump_e8m0(float *host256);
+int dsv4_gpu_dump_e2m1(float *host16);
+
+/* Device decode of every packed FP4 byte b = 0..255 into its two elements,
+ * out[2b] = even (low nibble), out[2b+1] = odd (high nibble), the order
+ * dsv4_fp4_at defines (dsv4_quant.h:155-164). No reference counterpart. */
+int dsv4_gpu_dump_fp4_bytes(float *host512);
+
+/* ================================================= MXFP4 routed experts */
+
+/* Copy one routed expert (w1/w3 FP4 [inter, hidden], w2 FP4 [hidden, inter],
+ * E8M0 scales per 1x32) into HBM, keyed by (layer, expert) -- not by
+ * pointer, since the reference's expert slots are reused (dsv4_cuda.cu:
+ * 232-236). 0 / -1 as dsv4_gpu_upload. No reference counterpart (the
+ * reference runs experts on the CPU, dsv4_cuda.h:19-21). */
+int dsv4_gpu_upload_expert(int layer, int expert, const DSV4ExpertW *e);
+
+/* Register an expert whose tensors already live in HBM (e->*.w / .s are
+ * device pointers owned by the caller, e.g. a checkpoint loaded straight into
+ * device memory). Same keying and use as dsv4_gpu_upload_expert. */
+int dsv4_gpu_bind_expert_d(int layer, int expert, const DSV4ExpertW *e);
+
+int dsv4_gpu_has_expert(int layer, int expert);
+
+/* The routed half of moe() (dsv4_layer.c:380, :412-476) on the device:
+ *   out[i] = sum_k w[k] * (w2_k . swiglu(w1_k . x, w3_k . x, limit))[i]
+ * with the sum taken strictly in k order, multiply and add rounded
+ * separately, as dsv4_layer.c:471-475; SwiGLU as dsv4_ops.c:60-78 (limit <=
+ * 0 disables the clamp). Host buffers: out/x [hidden], idx/w [topk].
+ * 0 / -1 (an expert not resident, or a shape that does not match). */
+int dsv4_gpu_moe_fp4(float *out, const float *x, int layer, const int *idx,
+                     const float *w, int topk, int hidden, int inter,
+                     float swiglu_limit);
+
+/* Stream-ordered form on device buffers; d_idx/d_w live in HBM so routing
+ * computed on the device needs no host round trip. */
+int dsv4_gpu_moe_fp4_d(float *d_out, const float *d_x, int layer,
+                       const int *d_idx, const float *d_w, int topk,
+                       int hidden, int inter, float swiglu_limit,
+                       void *stream);
+
+/* ============================================================ sparse MLA */
+
+/* A device-resident row store for the latent KV cache or the indexer's key
+ * cache, with an append API (SURVEY: dsv4_gpu_kv_create / _write_row).
+ * fmt: DSV4_GPU_KV_F32 (the reference's f32 cache), DSV4_GPU_KV_BF16, or
+ * DSV4_GPU_KV_FP8 (e4m3 bytes with one fp32 scale per row; a row dequantises
+ * to e4m3(code) * scale, exact in f32). */
+enum { DSV4_GPU_KV_F32 = 0, DSV4_GPU_KV_BF16 = 1, DSV4_GPU_KV_FP8 = 2 };
+typedef struct dsv4_gpu_kv dsv4_gpu_kv;
+
+dsv4_gpu_kv *dsv4_gpu_kv_create(int n_rows, int row_dim, int fmt);
+/* Write rows [row0, row0+n) from host memory laid out [n][row_dim] in the
+ * store's format; row_scales[n] for FP8 (ignored otherwise). */
+int dsv4_gpu_kv_write_rows(dsv4_gpu_kv *kv, int row0, int n, const void *rows,
+                           const float *row_scales);
+/* Device base pointers, for stream-ordered calls and for writing rows from
+ * device code: data [n_rows][row_dim], scales [n_rows] (FP8 only, else
+ * NULL). */
+void *dsv4_gpu_kv_data(const dsv4_gpu_kv *kv);
+float *dsv4_gpu_kv_scales(const dsv4_gpu_kv *kv);
+void dsv4_gpu_kv_free(dsv4_gpu_kv *kv);
+
+/* dsv4_indexer_score (dsv4_indexer.c:64-85), bit-exact: out[t] for the n
+ * rows of `keys` starting at row0, each read as D values with a row pitch of
+ * key_stride elements (the reference call passes rows of width D,
+ * dsv4_layer.c:286-289). q [H][D], w [H] host f32. 0 / -1. */
+int dsv4_gpu_indexer_score(float *out, const float *q, const float *w, int H,
+                           int D, const dsv4_gpu_kv *keys, int row0,
+                           int key_stride, int n);
+
+/* dsv4_topk (dsv4_indexer.c:92-106), bit-exact: the k largest scores,
+ * ordered by score descending with ties to the lower index; k is clamped to
+ * n; returns the count written (or -1). Scores must be NaN-free. */
+int dsv4_gpu_topk(int *idxs, const float *scores, int n, int k);
+
+/* Score then top-k in one call, the CSA selection of dsv4_layer.c:280-291.
+ * Returns the count written, or -1. */
+int dsv4_gpu_indexer_topk(int *idxs, const float *q, const float *w, int H,
+                          int D, const dsv4_gpu_kv *keys, int row0,
+                          int key_stride, int n, int k);
+
+/* dsv4_sparse_attn (dsv4_attn.c:60-108): o[h][d_v] = softmax over the
+ * gathered rows idxs[topk] (entries of -1 are masked) of q . kv[:, :d_qk] *
+ * scale, applied to kv[:, :d_v]; sink[h] enters the denominator only, or is
+ * absent when NULL. q [h][d_qk] host f32. Within 1e-5 relative of the
+ * reference. 0 / -1. */
+int dsv4_gpu_sparse_attn(float *o, const float *q, const dsv4_gpu_kv *kv,
+                         const float *sink, const int *idxs, int h, int d_qk,
+                         int d_v, int topk, float scale);
+
+/* Stream-ordered forms on device buffers. Keys/KV are raw device arrays in
+ * the DSV4_GPU_KV_* formats (d_key_scales for FP8 keys, else NULL).
+ * dsv4_gpu_indexer_score_d takes the score scale precomputed as the
+ * reference does in float: (1/sqrtf(D)) * (1/sqrtf(H)). */
+int dsv4_gpu_indexer_score_d(float *d_out, const float *d_q, const float *d_w,
+                             int H, int D, const void *d_keys,
+                             const float *d_key_scales, int key_fmt,
+                             int key_stride, int n, float scale, void *stream);
+int dsv4_gpu_topk_d(int *d_idxs, const float *d_scores, int n, int k,
+                    void *stream);
+/* Selected rows outside [0, kv_rows) are treated as masked and never read
+ * (the host-buffer form rejects them instead). */
+int dsv4_gpu_sparse_attn_d(float *d_o, const float *d_q, const void *d_kv,
+                           int kv_fmt, int kv_stride, int kv_rows,
+                           const float *d_sink, const int *d_idxs, int h,
+                           int d_qk, int d_v, int topk, float scale,
+                           void *stream);
+
+/* One sparse-MLA decode step on device buffers: indexer score over n keys,
+ * top-k, then attention over the selected KV rows (indices are positions in
+ * the KV store, no window offset). Writes the selection to d_idxs[k]. */
+int dsv4_gpu_mla_decode_d(float *d_o, int *d_idxs,
+                          const float *d_q_idx, const float *d_w_idx, int H,
+                          int D, const void *d_keys, const float *d_key_scales,
+                          int key_fmt, int key_stride, int n, int k,
+                          const float *d_q, const void *d_kv, int kv_fmt,
+                          int kv_stride, int kv_rows, const float *d_sink,
+                          int h, int d_qk, int d_v, float attn_scale,
+                          void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSV4_GPU_H */

@@ -1,0 +1,295 @@
+"""CPU checker for the decode hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may import this package, and only as the thing results
+are checked against (or timed beside). The shipped library never links,
+calls or falls back to it.
+
+Two CPU implementations are exposed through ctypes:
+
+* ``liboracle.so`` -- this directory's C restatement (``dsv4_oracle.c``) of
+  the reference functions, each citing the reference file:line it follows.
+* ``_ref/libdsv4ref.so`` -- the reference's own sources
+  (``src/core/dsv4_{matmul,indexer,attn,ops}.c``) compiled as they lie by
+  ``oracle/Makefile``. Present wherever it was built; used to pin the
+  restatement bit for bit and as the ``cpu_baseline`` of ``bench.py``.
+
+Parity unpinned: none of the restatement's functions. Each is checked
+against the compiled reference in its reference-shaped special case and
+against closed forms / known answers for the generalisations (see tests/).
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_ORC_PATH = os.path.join(HERE, "liboracle.so")
+_REF_PATH = os.path.join(HERE, "_ref", "libdsv4ref.so")
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_i32p = ctypes.POINTER(ctypes.c_int)
+_vp = ctypes.c_void_p
+
+_orc = None
+_ref = None
+
+
+def build():
+    """Compile liboracle.so (and _ref when the reference tree is present)."""
+    subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
+
+
+def _p(a, t):
+    return a.ctypes.data_as(t) if a is not None else None
+
+
+def lib():
+    global _orc
+    if _orc is None:
+        if not os.path.exists(_ORC_PATH):
+            build()
+        L = ctypes.CDLL(_ORC_PATH)
+        L.orc_e4m3_to_f32.restype = ctypes.c_float
+        L.orc_e4m3_to_f32.argtypes = [ctypes.c_uint8]
+        L.orc_e8m0_to_f32.restype = ctypes.c_float
+        L.orc_e8m0_to_f32.argtypes = [ctypes.c_uint8]
+        L.orc_e2m1_to_f32.restype = ctypes.c_float
+        L.orc_e2m1_to_f32.argtypes = [ctypes.c_uint8]
+        for n in ("orc_dump_e4m3", "orc_dump_e8m0", "orc_dump_e2m1"):
+            getattr(L, n).argtypes = [_f32p]
+        L.orc_matmul_fp8.argtypes = [_f32p, _f32p, _u8p, _vp, ctypes.c_int,
+                                     ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int]
+        L.orc_matmul_fp8_n.argtypes = L.orc_matmul_fp8.argtypes + [ctypes.c_int]
+        L.orc_matmul_fp4.argtypes = [_f32p, _f32p, _u8p, _u8p, ctypes.c_int,
+                                     ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.orc_swiglu.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_float]
+        pp = ctypes.POINTER(_u8p)
+        L.orc_moe_fp4.argtypes = [_f32p, _f32p, _f32p, pp, pp, pp, pp, pp, pp,
+                                  _f32p, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_int, ctypes.c_float]
+        L.orc_indexer_score.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.orc_topk.restype = ctypes.c_int
+        L.orc_topk.argtypes = [_i32p, _f32p, ctypes.c_int, ctypes.c_int]
+        L.orc_indexer_offset.argtypes = [_i32p, ctypes.c_int, ctypes.c_int]
+        L.orc_indexer_navail.restype = ctypes.c_int
+        L.orc_indexer_navail.argtypes = [ctypes.c_int, ctypes.c_int]
+        L.orc_window_idxs.restype = ctypes.c_int
+        L.orc_window_idxs.argtypes = [_i32p, ctypes.c_int, ctypes.c_int]
+        L.orc_sparse_attn.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int, _f32p,
+                                      _i32p, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int, ctypes.c_float]
+        _orc = L
+    return _orc
+
+
+def ref_available():
+    return os.path.exists(_REF_PATH)
+
+
+def ref():
+    """The compiled reference, or None where it was never built."""
+    global _ref
+    if _ref is None and ref_available():
+        L = ctypes.CDLL(_REF_PATH)
+        for n in ("dsv4_matmul_fp8", "dsv4_matmul_fp8_scalar",
+                  "dsv4_matmul_fp4", "dsv4_matmul_fp4_scalar"):
+            getattr(L, n).argtypes = [_f32p, _f32p, _u8p, _u8p, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.dsv4_swiglu.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_float]
+        L.dsv4_indexer_score.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_int]
+        L.dsv4_topk.restype = ctypes.c_int
+        L.dsv4_topk.argtypes = [_i32p, _f32p, ctypes.c_int, ctypes.c_int]
+        L.dsv4_sparse_attn.argtypes = [_f32p, _f32p, _f32p, _f32p, _i32p,
+                                       ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_float, _f32p]
+        _ref = L
+    return _ref
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _u8(a):
+    return np.ascontiguousarray(a, dtype=np.uint8)
+
+
+# ------------------------------------------------------------------ formats
+def dump_e4m3():
+    o = np.empty(256, np.float32); lib().orc_dump_e4m3(_p(o, _f32p)); return o
+
+
+def dump_e8m0():
+    o = np.empty(256, np.float32); lib().orc_dump_e8m0(_p(o, _f32p)); return o
+
+
+def dump_e2m1():
+    o = np.empty(16, np.float32); lib().orc_dump_e2m1(_p(o, _f32p)); return o
+
+
+# ------------------------------------------------------------------ matmuls
+def matmul_fp8(x, W, S, blk_r=128, blk_c=128):
+    """y = dequant(W) x. S is E8M0 bytes (uint8) or fp32 block scales."""
+    W = _u8(W); x = _f32(x)
+    out, inn = W.shape
+    kind = 1 if np.asarray(S).dtype == np.float32 else 0
+    S = np.ascontiguousarray(S)
+    if x.ndim == 1:
+        y = np.empty(out, np.float32)
+        lib().orc_matmul_fp8(_p(y, _f32p), _p(x, _f32p), _p(W, _u8p),
+                             S.ctypes.data, kind, inn, out, blk_r, blk_c)
+        return y
+    nt = x.shape[0]
+    y = np.empty((nt, out), np.float32)
+    lib().orc_matmul_fp8_n(_p(y, _f32p), _p(x, _f32p), _p(W, _u8p),
+                           S.ctypes.data, kind, inn, out, blk_r, blk_c, nt)
+    return y
+
+
+def matmul_fp4(x, W, S, inn, blk_r=1, blk_c=32):
+    W = _u8(W); S = _u8(S); x = _f32(x)
+    out = W.shape[0]
+    y = np.empty(out, np.float32)
+    lib().orc_matmul_fp4(_p(y, _f32p), _p(x, _f32p), _p(W, _u8p), _p(S, _u8p),
+                         inn, out, blk_r, blk_c)
+    return y
+
+
+def swiglu(gate, up, limit):
+    gate = _f32(gate); up = _f32(up)
+    y = np.empty_like(gate)
+    lib().orc_swiglu(_p(y, _f32p), _p(gate, _f32p), _p(up, _f32p), gate.size,
+                     float(limit))
+    return y
+
+
+def moe_fp4(x, experts, wts, hidden, inter, limit, return_acc=False):
+    """experts: list of dicts with w1,s1,w3,s3,w2,s2 (uint8), one per k."""
+    x = _f32(x); wts = _f32(wts)
+    topk = len(experts)
+    keep = []
+
+    def arr(name):
+        a = (_u8p * topk)()
+        for k, e in enumerate(experts):
+            v = _u8(e[name]); keep.append(v); a[k] = _p(v, _u8p)
+        return a
+    out = np.empty(hidden, np.float32)
+    acc = np.empty((topk, hidden), np.float32)
+    lib().orc_moe_fp4(_p(out, _f32p), _p(acc, _f32p), _p(x, _f32p),
+                      arr("w1"), arr("s1"), arr("w3"), arr("s3"), arr("w2"),
+                      arr("s2"), _p(wts, _f32p), topk, hidden, inter,
+                      float(limit))
+    return (out, acc) if return_acc else out
+
+
+# ------------------------------------------------------------------ sparse MLA
+def indexer_score(q, kv, w, key_stride=None):
+    q = _f32(q); kv = _f32(kv); w = _f32(w)
+    H, D = q.shape
+    stride = D if key_stride is None else key_stride
+    n = kv.size // stride
+    out = np.empty(n, np.float32)
+    lib().orc_indexer_score(_p(out, _f32p), _p(q, _f32p), _p(kv, _f32p),
+                            _p(w, _f32p), H, D, n, stride)
+    return out
+
+
+def topk(scores, k):
+    scores = _f32(scores)
+    kk = max(0, min(k, scores.size))
+    idx = np.empty(max(kk, 1), np.int32)
+    n = lib().orc_topk(_p(idx, _i32p), _p(scores, _f32p), scores.size, k)
+    return idx[:max(n, 0)]
+
+
+def sparse_attn(q, kv, sink, idxs, scale, d_v=None):
+    q = _f32(q); kv = _f32(kv)
+    h, d_qk = q.shape
+    stride = kv.shape[1]
+    d_v = stride if d_v is None else d_v
+    idxs = np.ascontiguousarray(idxs, dtype=np.int32)
+    sk = None if sink is None else _f32(sink)
+    o = np.empty((h, d_v), np.float32)
+    lib().orc_sparse_attn(_p(o, _f32p), _p(q, _f32p), _p(kv, _f32p), stride,
+                          _p(sk, _f32p), _p(idxs, _i32p), h, d_qk, d_v,
+                          idxs.size, float(scale))
+    return o
+
+
+def window_idxs(pos, win):
+    idx = np.empty(win, np.int32)
+    n = lib().orc_window_idxs(_p(idx, _i32p), pos, win)
+    return n, idx
+
+
+def indexer_navail(pos, ratio):
+    return lib().orc_indexer_navail(pos, ratio)
+
+
+def indexer_offset(idxs, offset):
+    idxs = np.array(idxs, dtype=np.int32)
+    lib().orc_indexer_offset(_p(idxs, _i32p), idxs.size, offset)
+    return idxs
+
+
+# ------------------------------------------------- the compiled reference
+def ref_matmul_fp8(x, W, S_e8m0, blk_r=128, blk_c=128, scalar=False):
+    W = _u8(W); x = _f32(x); S = _u8(S_e8m0)
+    out, inn = W.shape
+    y = np.empty(out, np.float32)
+    fn = ref().dsv4_matmul_fp8_scalar if scalar else ref().dsv4_matmul_fp8
+    fn(_p(y, _f32p), _p(x, _f32p), _p(W, _u8p), _p(S, _u8p), inn, out, blk_r, blk_c)
+    return y
+
+
+def ref_matmul_fp4(x, W, S, inn, blk_r=1, blk_c=32, scalar=False):
+    W = _u8(W); x = _f32(x); S = _u8(S)
+    out = W.shape[0]
+    y = np.empty(out, np.float32)
+    fn = ref().dsv4_matmul_fp4_scalar if scalar else ref().dsv4_matmul_fp4
+    fn(_p(y, _f32p), _p(x, _f32p), _p(W, _u8p), _p(S, _u8p), inn, out, blk_r, blk_c)
+    return y
+
+
+def ref_swiglu(gate, up, limit):
+    gate = _f32(gate); up = _f32(up)
+    y = np.empty_like(gate)
+    ref().dsv4_swiglu(_p(y, _f32p), _p(gate, _f32p), _p(up, _f32p), gate.size,
+                      float(limit))
+    return y
+
+
+def ref_indexer_score(q, kv, w):
+    q = _f32(q); kv = _f32(kv); w = _f32(w)
+    H, D = q.shape
+    n = kv.size // D
+    out = np.empty(n, np.float32)
+    ref().dsv4_indexer_score(_p(out, _f32p), _p(q, _f32p), _p(kv, _f32p),
+                             _p(w, _f32p), H, D, n)
+    return out
+
+
+def ref_topk(scores, k):
+    scores = _f32(scores)
+    idx = np.empty(max(1, min(k, scores.size)), np.int32)
+    n = ref().dsv4_topk(_p(idx, _i32p), _p(scores, _f32p), scores.size, k)
+    return idx[:n]
+
+
+def ref_sparse_attn(q, kv, sink, idxs, scale):
+    q = _f32(q); kv = _f32(kv); sink = _f32(sink)
+    h, d = q.shape
+    idxs = np.ascontiguousarray(idxs, dtype=np.int32)
+    o = np.empty((h, d), np.float32)
+    scratch = np.empty(h * max(1, idxs.size), np.float32)
+    ref().dsv4_sparse_attn(_p(o, _f32p), _p(q, _f32p), _p(kv, _f32p),
+                           _p(sink, _f32p), _p(idxs, _i32p), h, d, idxs.size,
+                           float(scale), _p(scratch, _f32p))
+    return o

@@ -1,0 +1,232 @@
+"""FP8 block-scaled GEMV on the MI355X against the CPU oracle.
+
+Parity bar: decoders bit-exact on every code; exact-representable known
+answers bit-exact; otherwise worst vector-scaled relative error < 1e-5 and
+the same argmax (the reference GPU gate, tests/unit/test_cuda.c:103-192);
+the batched path bit-identical to single calls (test_cuda.c:194-256).
+"""
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+import common
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+# Residency is keyed by host pointer (the reference contract): keep every
+# uploaded array alive for the test, then reset the backend so a later
+# array that reuses an address is never mistaken for a resident one.
+_keep = []
+
+
+@pytest.fixture(autouse=True)
+def fresh_backend(gpu, dsv4):
+    yield
+    _keep.clear()
+    dsv4.lib().dsv4_gpu_shutdown()
+    assert dsv4.lib().dsv4_gpu_init() == 0
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+# ---------------------------------------------------------------- decoders
+def test_decoders_bit_exact(gpu, dsv4):
+    for which, ref in (("e4m3", oracle.dump_e4m3()), ("e8m0", oracle.dump_e8m0()),
+                       ("e2m1", oracle.dump_e2m1())):
+        dev = dsv4.dump(which)
+        nan = np.isnan(ref)
+        assert np.array_equal(np.isnan(dev), nan), which
+        assert common.bits_equal(dev[~nan], ref[~nan]), which
+
+
+def test_fp4_byte_order_bit_exact(gpu, dsv4):
+    dev = dsv4.dump("fp4_bytes").reshape(256, 2)
+    tab = oracle.dump_e2m1()
+    b = np.arange(256)
+    assert common.bits_equal(dev[:, 0], tab[b & 15])      # even = low nibble
+    assert common.bits_equal(dev[:, 1], tab[b >> 4])
+
+
+# ------------------------------------------------------------ known answers
+def _run(dsv4, W, S, x, f32s=False, blk_r=128, blk_c=128):
+    L = dsv4.lib()
+    _keep.extend([W, S])
+    m = dsv4.qmat(W, S, blk_r=blk_r, blk_c=blk_c)
+    rc = (L.dsv4_gpu_upload_f32s if f32s else L.dsv4_gpu_upload)(ctypes.byref(m))
+    assert rc == 0
+    assert L.dsv4_gpu_has(ctypes.byref(m)) == 1
+    return dsv4.mmq(m, x), m
+
+
+def test_known_answers(gpu, dsv4):
+    """test_matmul.c:63-130, run on the device."""
+    W = np.zeros((2, 128), np.uint8); W[0], W[1] = 0x38, 0x40
+    y, _ = _run(dsv4, W, np.array([[128]], np.uint8), np.ones(128, np.float32))
+    assert list(y) == [256.0, 512.0]
+    W = np.full((256, 128), 0x38, np.uint8)
+    y, _ = _run(dsv4, W, np.array([[127], [129]], np.uint8), np.ones(128, np.float32))
+    assert y[0] == 128 and y[127] == 128 and y[128] == 512 and y[255] == 512
+    W = np.full((1, 256), 0x38, np.uint8)
+    y, _ = _run(dsv4, W, np.array([[127, 128]], np.uint8), np.ones(256, np.float32))
+    assert y[0] == 384.0
+
+
+def check_shape(dsv4, rows, cols, seed, f32s=True, continuous=False):
+    W, Sf, Se, x = common.fp8_problem(seed, rows, cols, continuous=continuous)
+    S = Sf if (f32s or continuous) else Se
+    y, m = _run(dsv4, W, S, x, f32s=(f32s or continuous))
+    want = oracle.matmul_fp8(x, W, S)
+    err = common.vec_rel_err(y, want)
+    say("fp8 %dx%d seed %d %s: worst rel %.3g" %
+        (rows, cols, seed, "cont" if continuous else ("f32" if f32s else "e8m0"), err))
+    assert err < TOL
+    assert int(np.argmax(y)) == int(np.argmax(want))
+    return y, want
+
+
+def test_c1_4096(gpu, dsv4):
+    check_shape(dsv4, 4096, 4096, 0, f32s=True)
+    check_shape(dsv4, 4096, 4096, 0, f32s=False)
+    check_shape(dsv4, 4096, 4096, 1, continuous=True)
+
+
+@pytest.mark.parametrize("rows,cols", [(1536, 7168), (576, 7168), (24576, 1536),
+                                       (7168, 16384), (7168, 7168)])
+def test_c2_trunk_shapes(gpu, dsv4, rows, cols):
+    check_shape(dsv4, rows, cols, 0)
+
+
+def test_c2_lm_head(gpu, dsv4):
+    check_shape(dsv4, 129280, 7168, 0)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 16), (3, 48), (130, 96), (257, 1040),
+                                       (64, 100), (33, 20000), (5, 8)])
+def test_ragged_and_generic_shapes(gpu, dsv4, rows, cols):
+    rng = np.random.default_rng(rows * 7 + cols)
+    W = common.fp8_codes(rng, (rows, cols))
+    e = rng.integers(-8, -3, size=((rows + 127) // 128, (cols + 127) // 128))
+    S = (127 + e).astype(np.uint8)
+    x = rng.standard_normal(cols, dtype=np.float32)
+    y, _ = _run(dsv4, W, S, x)
+    assert common.vec_rel_err(y, oracle.matmul_fp8(x, W, S)) < TOL
+
+
+def test_reference_gpu_gate(gpu, dsv4):
+    """test_cuda.c:103-256: 4096x8192, LCG data, E8M0 scales 120..134."""
+    rows, cols = 4096, 8192
+    r = 20260820
+    M = (1 << 32) - 1
+
+    # vectorised LCG: x_{k} = a^k x_0 + c (a^k - 1)/(a - 1), all mod 2^32
+    def lcg_fast(n):
+        nonlocal r
+        a, c = 1103515245, 12345
+        ks = np.arange(1, n + 1, dtype=np.uint64)
+        # powers of a mod 2^32 by repeated squaring over the bits of k
+        ak = np.ones(n, np.uint64); cs = np.zeros(n, np.uint64)
+        pa, pc = np.uint64(a), np.uint64(c)
+        kk = ks.copy()
+        while kk.any():
+            bit = (kk & 1).astype(bool)
+            # compose (ak, cs) with (pa, pc): x -> pa*x + pc applied after
+            cs[bit] = (cs[bit] * pa + pc) & np.uint64(M)
+            ak[bit] = (ak[bit] * pa) & np.uint64(M)
+            pc = (pc * pa + pc) & np.uint64(M)
+            pa = (pa * pa) & np.uint64(M)
+            kk >>= np.uint64(1)
+        out = ((ak * np.uint64(r)) + cs) & np.uint64(M)
+        r = int(out[-1])
+        return out.astype(np.uint32)
+    xs = lcg_fast(cols)
+    x = (((xs >> 16) & 0xFFFF).astype(np.int64) - 32768).astype(np.float32) * np.float32(1e-3)
+    wb = ((lcg_fast(rows * cols) >> 16) & 0xFF).astype(np.uint8)
+    wb = np.where((wb & 0x7F) == 0x7F, wb & 0xFE, wb).astype(np.uint8).reshape(rows, cols)
+    ns = (rows // 128) * (cols // 128)
+    S = (120 + ((lcg_fast(ns) >> 16) % 15)).astype(np.uint8).reshape(rows // 128, cols // 128)
+    y, m = _run(dsv4, wb, S, x)
+    want = oracle.matmul_fp8(x, wb, S)
+    err = common.vec_rel_err(y, want)
+    say("reference gate 4096x8192: worst rel %.3g" % err)
+    assert err < TOL and int(np.argmax(y)) == int(np.argmax(want))
+    NT = 8
+    t = np.arange(NT)[:, None]
+    i = np.arange(cols)[None, :]
+    xn = np.sin(0.7 * (i + 1) + 3.1 * (t + 1)).astype(np.float32)
+    yn = dsv4.mmq_n(m, xn)
+    for k in range(NT):
+        assert common.bits_equal(yn[k], dsv4.mmq(m, xn[k])), k
+    assert common.bits_equal(dsv4.mmq_n(m, xn[:1])[0], dsv4.mmq(m, xn[0]))
+
+
+@pytest.mark.parametrize("rows,cols,nt", [(300, 1536, 5), (129, 7168, 64), (40, 64, 3)])
+def test_batched_bit_identical(gpu, dsv4, rows, cols, nt):
+    W, Sf, Se, _ = common.fp8_problem(21, rows, cols)
+    x = np.random.default_rng(22).standard_normal((nt, cols), dtype=np.float32)
+    y1, m = _run(dsv4, W, Se, x[0])
+    yn = dsv4.mmq_n(m, x)
+    for t in range(nt):
+        assert common.bits_equal(yn[t], dsv4.mmq(m, x[t])), t
+    assert common.vec_rel_err(yn, oracle.matmul_fp8(x, W, Se)) < TOL
+
+
+def test_row_range_views(gpu, dsv4):
+    """The wo_a group slicing of attention() (dsv4_layer.c:321-334): every
+    group is resident as a view and computes only its rows."""
+    groups, gr, gw = 8, 256, 1024
+    rows = groups * gr
+    W, Sf, Se, x = common.fp8_problem(31, rows, gw)
+    L = dsv4.lib()
+    _keep.extend([W, Se])
+    full = dsv4.qmat(W, Se)
+    assert L.dsv4_gpu_upload(ctypes.byref(full)) == 0
+    yfull = dsv4.mmq(full, x)
+    sc = gw // 128
+    for g in range(groups):
+        sl = dsv4.DSV4QMat(W.ctypes.data + g * gr * gw,
+                           Se.ctypes.data + g * (gr // 128) * sc,
+                           dsv4.WFP8, gr, gw, 128, 128)
+        assert L.dsv4_gpu_has(ctypes.byref(sl)) == 1
+        assert common.bits_equal(dsv4.mmq(sl, x), yfull[g * gr:(g + 1) * gr])
+    bad = dsv4.DSV4QMat(W.ctypes.data + 64 * gw, Se.ctypes.data, dsv4.WFP8, 64, gw, 128, 128)
+    assert L.dsv4_gpu_has(ctypes.byref(bad)) == 0        # not on a row-block edge
+    other = np.zeros_like(W)
+    assert L.dsv4_gpu_has(ctypes.byref(dsv4.qmat(other, Se))) == 0
+
+
+def test_device_entry_point_matches_host_path(gpu, dsv4):
+    import torch
+    rows, cols = 7168, 7168
+    W, Sf, Se, x = common.fp8_problem(41, rows, cols)
+    y_host, _ = _run(dsv4, W, Sf, x, f32s=True)
+    dev = torch.device("cuda:0")
+    dW = torch.from_numpy(W).to(dev)
+    dS = torch.from_numpy(Sf).to(dev)
+    dx = torch.from_numpy(x).to(dev)
+    dy = torch.empty(rows, dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    rc = dsv4.lib().dsv4_gpu_fp8_gemv_d(dy.data_ptr(), dx.data_ptr(), dW.data_ptr(),
+                                        dS.data_ptr(), 1, rows, cols, st)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert common.bits_equal(dy.cpu().numpy(), y_host)
+
+
+def test_upload_refusals(gpu, dsv4):
+    L = dsv4.lib()
+    W = np.zeros((4, 32), np.uint8)
+    S = np.zeros((4, 1), np.uint8)
+    m4 = dsv4.DSV4QMat(W.ctypes.data, S.ctypes.data, dsv4.WFP4, 4, 64, 1, 32)
+    assert L.dsv4_gpu_upload(ctypes.byref(m4)) == -1          # FP4 is not a trunk matrix
+    mnull = dsv4.DSV4QMat(None, None, dsv4.WFP8, 4, 32, 128, 128)
+    assert L.dsv4_gpu_upload(ctypes.byref(mnull)) == -1
+    huge = dsv4.DSV4QMat(W.ctypes.data, S.ctypes.data, dsv4.WFP8, 1 << 30, 1 << 30, 128, 128)
+    assert L.dsv4_gpu_upload(ctypes.byref(huge)) == -1          # no room: recoverable

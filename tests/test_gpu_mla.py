@@ -1,0 +1,216 @@
+"""Sparse-MLA decode on the MI355X: indexer score and top-k bit-exact,
+attention within 1e-5 relative (C4: 16 x 128 fp8 indexer keys over 32768
+entries, top-2048 with ties to the lower index, 64 heads over a 576-d bf16
+latent KV with 512-d values)."""
+import sys
+
+import numpy as np
+import pytest
+
+import common
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+_kv = []
+
+
+@pytest.fixture(autouse=True)
+def free_stores(gpu, dsv4):
+    yield
+    for kv in _kv:
+        kv.free()
+    _kv.clear()
+
+
+def store(dsv4, rows, fmt, scales=None):
+    kv = dsv4.KV(rows.shape[0], rows.shape[1], fmt)
+    kv.write(0, rows, scales)
+    _kv.append(kv)
+    return kv
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def c4_indexer(seed, n=32768, H=16, D=128):
+    rng = np.random.default_rng(seed)
+    codes, s, deq = common.fp8_keys(rng, n, D)
+    q = rng.standard_normal((H, D)).astype(np.float32)
+    w = rng.standard_normal(H).astype(np.float32)
+    return codes, s, deq, q, w
+
+
+# ------------------------------------------------------------- indexer
+def test_score_and_topk_c4_bit_exact(gpu, dsv4):
+    codes, s, deq, q, w = c4_indexer(0)
+    keys = store(dsv4, codes, dsv4.KV_FP8, s)
+    got = dsv4.indexer_score(q, w, keys, codes.shape[0])
+    want = oracle.indexer_score(q, deq, w)
+    nbad = int(np.sum(got.view(np.uint32) != want.view(np.uint32)))
+    say("indexer C4: %d of %d scores differ in bits" % (nbad, got.size))
+    assert nbad == 0
+    idx = dsv4.indexer_topk(q, w, keys, codes.shape[0], 2048)
+    assert np.array_equal(idx, oracle.topk(want, 2048))
+
+
+def test_score_f32_keys_known_answers(gpu, dsv4):
+    """test_indexer.c:23-86 on the device."""
+    kv = store(dsv4, np.array([[1, 0], [-1, 0]], np.float32), dsv4.KV_F32)
+    out = dsv4.indexer_score(np.array([[1, 0], [0, 0]], np.float32),
+                             np.array([1, 1], np.float32), kv, 2)
+    assert out[0] > 0 and out[1] == 0.0
+    q = np.zeros((4, 16), np.float32); q[0, 0] = 1
+    kv = store(dsv4, np.eye(1, 16, dtype=np.float32), dsv4.KV_F32)
+    w = np.array([1, 0, 0, 0], np.float32)
+    assert common.bits_equal(dsv4.indexer_score(q, w, kv, 1),
+                             oracle.indexer_score(q, np.eye(1, 16, dtype=np.float32), w))
+
+
+@pytest.mark.parametrize("H,D,n", [(64, 128, 4099), (8, 16, 20), (16, 128, 1), (3, 40, 777)])
+def test_score_other_shapes_bit_exact(gpu, dsv4, H, D, n):
+    rng = np.random.default_rng(H * D + n)
+    kv = rng.standard_normal((n, D)).astype(np.float32)
+    q = rng.standard_normal((H, D)).astype(np.float32)
+    w = rng.standard_normal(H).astype(np.float32)
+    keys = store(dsv4, kv, dsv4.KV_F32)
+    assert common.bits_equal(dsv4.indexer_score(q, w, keys, n), oracle.indexer_score(q, kv, w))
+
+
+def test_score_reference_addressing(gpu, dsv4):
+    """dsv4_layer.c:286-289 scores the attention cache's compressed rows
+    (row width hd = 512) read at the indexer's width D = 128 from row
+    `window`: key_stride D, row0 = window."""
+    rng = np.random.default_rng(5)
+    window, ncomp, hd, H, D = 8, 40, 512, 4, 128
+    cache = rng.standard_normal((window + ncomp, hd)).astype(np.float32)
+    kv = store(dsv4, cache, dsv4.KV_F32)
+    q = rng.standard_normal((H, D)).astype(np.float32)
+    w = rng.standard_normal(H).astype(np.float32)
+    got = dsv4.indexer_score(q, w, kv, ncomp, row0=window, key_stride=D)
+    want = oracle.indexer_score(q, cache[window:].ravel()[:ncomp * D], w)
+    assert common.bits_equal(got, want)
+
+
+def test_topk_ties_and_edges(gpu, dsv4):
+    s = np.array([1, 5, 5, 2, 0, 5], np.float32)
+    assert list(dsv4.topk(s, 4)) == [1, 2, 5, 3]
+    assert list(dsv4.topk(s, 10)) == list(oracle.topk(s, 10))
+    z = np.array([0.0, -0.0, 0.0, -1.0], np.float32)
+    assert list(dsv4.topk(z, 3)) == [0, 1, 2]
+    assert len(dsv4.topk(s, 0)) == 0
+
+
+@pytest.mark.parametrize("n,k,levels", [(32768, 2048, 40), (5000, 4096, 7), (1025, 1, 3),
+                                        (3000, 3000, 1000000), (100000, 512, 1000000),
+                                        (77, 13, 5)])
+def test_topk_random_with_ties(gpu, dsv4, n, k, levels):
+    rng = np.random.default_rng(n + k)
+    s = (rng.integers(-levels, levels, size=n) / 8.0).astype(np.float32)
+    assert np.array_equal(dsv4.topk(s, k), oracle.topk(s, k))
+
+
+def test_topk_all_equal(gpu, dsv4):
+    s = np.full(9000, 0.25, np.float32)
+    assert np.array_equal(dsv4.topk(s, 2048), np.arange(2048))
+
+
+# ----------------------------------------------------------- attention
+def c4_attention(seed, n=32768, h=64, d_qk=576, d_v=512, topk=2048):
+    rng = np.random.default_rng(seed)
+    kv = common.bf16_round(rng.standard_normal((n, d_qk)).astype(np.float32)
+                           / np.float32(np.sqrt(d_qk)))
+    q = rng.standard_normal((h, d_qk)).astype(np.float32)
+    idx = np.sort(rng.permutation(n)[:topk]).astype(np.int32)
+    return kv, q, idx
+
+
+@pytest.mark.parametrize("with_sink", [False, True])
+def test_attention_c4(gpu, dsv4, with_sink):
+    kv, q, idx = c4_attention(1)
+    h = q.shape[0]
+    sink = np.random.default_rng(2).standard_normal(h).astype(np.float32) if with_sink else None
+    store_ = store(dsv4, common.bf16_bits(kv), dsv4.KV_BF16)
+    scale = np.float32(1.0) / np.sqrt(np.float32(576))
+    got = dsv4.sparse_attn(q, store_, sink, idx, scale, d_v=512)
+    want = oracle.sparse_attn(q, kv, sink, idx, scale, d_v=512)
+    err = common.vec_rel_err(got, want)
+    say("attention C4 sink=%s: worst rel %.3g" % (with_sink, err))
+    assert err < TOL
+
+
+def test_attention_reference_mode(gpu, dsv4):
+    """d_qk = d_v = 512 f32 KV with a per-head sink and masked slots: the
+    reference's own dsv4_sparse_attn call (dsv4_layer.c:300-301)."""
+    rng = np.random.default_rng(4)
+    n, h, d, topk = 300, 64, 512, 200
+    kv = rng.standard_normal((n, d)).astype(np.float32) * 0.05
+    q = rng.standard_normal((h, d)).astype(np.float32)
+    sink = rng.standard_normal(h).astype(np.float32)
+    idx = rng.integers(-1, n, size=topk).astype(np.int32)
+    st = store(dsv4, kv, dsv4.KV_F32)
+    scale = np.float32(1.0) / np.sqrt(np.float32(d))
+    got = dsv4.sparse_attn(q, st, sink, idx, scale)
+    want = oracle.sparse_attn(q, kv, sink, idx, scale)
+    assert common.vec_rel_err(got, want) < TOL
+
+
+def test_attention_known_answers(gpu, dsv4):
+    """test_attn.c:21-117 on the device."""
+    kv = np.repeat(np.arange(1, 5, dtype=np.float32)[:, None], 4, 1)
+    st = store(dsv4, kv, dsv4.KV_F32)
+    o = dsv4.sparse_attn(np.zeros((2, 4), np.float32), st, np.full(2, -1000, np.float32),
+                         [0, 1, 2, 3], 1.0)
+    assert np.allclose(o, 2.5, atol=1e-5)
+    st2 = store(dsv4, np.full((1, 2), 8, np.float32), dsv4.KV_F32)
+    o = dsv4.sparse_attn(np.zeros((1, 2), np.float32), st2, np.zeros(1, np.float32), [0], 1.0)
+    assert abs(o[0, 0] - 4.0) < 1e-5
+    o = dsv4.sparse_attn(np.zeros((2, 2), np.float32), st2, np.array([-20, 20], np.float32),
+                         [0], 1.0)
+    assert abs(o[0, 0] - 8) < 1e-3 and o[1, 0] < 1e-3
+    kv = np.repeat(np.arange(1, 5, dtype=np.float32)[:, None], 2, 1)
+    st3 = store(dsv4, kv, dsv4.KV_F32)
+    o = dsv4.sparse_attn(np.zeros((1, 2), np.float32), st3, np.full(1, -1000, np.float32),
+                         [0, -1, 2, -1], 1.0)
+    assert abs(o[0, 0] - 2.0) < 1e-5
+    o = dsv4.sparse_attn(np.ones((1, 2), np.float32), st3, np.full(1, 1.0, np.float32),
+                         [-1, -1], 1.0)
+    assert np.all(o == 0.0)                      # attends to nothing: zero
+
+
+def test_attention_rejects_out_of_range_rows(gpu, dsv4):
+    st = store(dsv4, np.ones((4, 8), np.float32), dsv4.KV_F32)
+    with pytest.raises(RuntimeError):
+        dsv4.sparse_attn(np.ones((1, 8), np.float32), st, None, [0, 4], 1.0)
+
+
+# ------------------------------------------------------ the whole step
+def test_mla_decode_step_c4(gpu, dsv4):
+    import torch
+    codes, s, deq, qi, wi = c4_indexer(7)
+    kv, q, _ = c4_attention(8)
+    n, k, h = 32768, 2048, 64
+    dev = torch.device("cuda:0")
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    d_codes, d_s, d_qi, d_wi, d_q = t(codes), t(s), t(qi), t(wi), t(q)
+    d_kv = t(common.bf16_bits(kv).view(np.int16))
+    d_o = torch.empty((h, 512), dtype=torch.float32, device=dev)
+    d_idx = torch.empty(k, dtype=torch.int32, device=dev)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(576)))
+    st = torch.cuda.current_stream().cuda_stream
+    rc = dsv4.lib().dsv4_gpu_mla_decode_d(
+        d_o.data_ptr(), d_idx.data_ptr(), d_qi.data_ptr(), d_wi.data_ptr(), 16, 128,
+        d_codes.data_ptr(), d_s.data_ptr(), dsv4.KV_FP8, 128, n, k,
+        d_q.data_ptr(), d_kv.data_ptr(), dsv4.KV_BF16, 576, n, None, h, 576, 512,
+        scale, st)
+    assert rc == 0
+    torch.cuda.synchronize()
+    want_idx = oracle.topk(oracle.indexer_score(qi, deq, wi), k)
+    assert np.array_equal(d_idx.cpu().numpy(), want_idx)
+    want = oracle.sparse_attn(q, kv, None, want_idx, scale, d_v=512)
+    err = common.vec_rel_err(d_o.cpu().numpy(), want)
+    say("mla step C4: worst rel %.3g" % err)
+    assert err < TOL

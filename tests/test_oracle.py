@@ -1,0 +1,297 @@
+"""Pin the CPU oracle before trusting it (CPU only).
+
+Each check is chosen so a plausible mistake fails it: a wrong rebias or
+subnormal start, a swapped nibble, a per-element instead of per-block scale,
+an in/2 stride read at full width, a missing ReLU, a wrong score scale, a
+sink in the numerator or the max, a lost tie-break. The known answers are
+the reference's own gates (tests/unit/test_quant.c, test_matmul.c,
+test_indexer.c, test_attn.c); the closed forms and the compiled reference
+(oracle/_ref, built from the reference's sources) cover the rest.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import common
+import oracle
+
+ref_only = pytest.mark.skipif(not oracle.ref_available(),
+                              reason="compiled reference oracle/_ref not built")
+
+
+def f32bits(v):
+    return np.float32(v).view(np.uint32)
+
+
+# ------------------------------------------------------------ formats
+def test_e8m0_closed_form():
+    """test_quant.c:39-58: 2^(b-127) exactly; 0 -> 2^-127 subnormal; 255 NaN."""
+    d = oracle.dump_e8m0()
+    for b in range(1, 255):
+        assert d[b] == np.float32(math.ldexp(1.0, b - 127)), b
+    assert d[0] == np.float32(math.ldexp(1.0, -127)) and d[0] != 0.0
+    assert d[0].view(np.uint32) == 0x00400000
+    assert np.isnan(d[255]) and not np.isinf(d[255])
+
+
+def test_e4m3_closed_form():
+    """Every code against sign * 2^(e-7) * (1 + m/8) (normal) or m * 2^-9
+    (subnormal); FN: only 0x7F/0xFF are NaN, 0x7E = 448 (test_quant.c:60-102)."""
+    d = oracle.dump_e4m3()
+    for b in range(256):
+        s = -1.0 if b & 0x80 else 1.0
+        e = (b >> 3) & 0xF
+        m = b & 7
+        if e == 15 and m == 7:
+            assert np.isnan(d[b]), b
+            continue
+        v = s * (m * 2.0 ** -9 if e == 0 else 2.0 ** (e - 7) * (1 + m / 8))
+        assert f32bits(d[b]) == f32bits(v), (b, d[b], v)
+    assert d[0x7E] == 448.0 and d[0x7B] == 352.0 and d[0x38] == 1.0
+    assert d[0x01] == 2.0 ** -9 and d[0x07] == 7 * 2.0 ** -9
+    assert np.nanmax(d) == 448.0
+    assert f32bits(d[0x80]) == 0x80000000          # -0.0 keeps its sign
+
+
+def test_e2m1_table_and_nibble_order():
+    """test_quant.c:104-189: eight magnitudes, max 6, sign in bit 3;
+    element 0 is the LOW nibble (0x21 -> {0.5, 1.0})."""
+    d = oracle.dump_e2m1()
+    mags = [0, 0.5, 1, 1.5, 2, 3, 4, 6]
+    for i in range(8):
+        assert d[i] == mags[i]
+        assert d[i + 8] == -mags[i]
+    assert f32bits(d[8]) == 0x80000000
+    W = np.array([[0x21] * 16], np.uint8)               # 32 elements
+    S = np.array([[127]], np.uint8)
+    x = np.zeros(32, np.float32)
+    x[0] = 1.0                                           # picks element 0
+    assert oracle.matmul_fp4(x, W, S, 32)[0] == 0.5
+    x[:] = 0
+    x[1] = 1.0                                           # element 1
+    assert oracle.matmul_fp4(x, W, S, 32)[0] == 1.0
+
+
+# ------------------------------------------------------------ matmuls
+def test_fp8_known_answers():
+    """test_matmul.c:63-130."""
+    W = np.zeros((2, 128), np.uint8)
+    W[0], W[1] = 0x38, 0x40
+    y = oracle.matmul_fp8(np.ones(128, np.float32), W, np.array([[128]], np.uint8))
+    assert list(y) == [256.0, 512.0]
+    W = np.full((256, 128), 0x38, np.uint8)
+    y = oracle.matmul_fp8(np.ones(128, np.float32), W, np.array([[127], [129]], np.uint8))
+    assert y[0] == 128 and y[127] == 128 and y[128] == 512 and y[255] == 512
+    W = np.full((1, 256), 0x38, np.uint8)
+    y = oracle.matmul_fp8(np.ones(256, np.float32), W, np.array([[127, 128]], np.uint8))
+    assert y[0] == 384.0
+
+
+def test_fp4_known_answers():
+    """test_matmul.c:132-195."""
+    W = np.full((2, 32), 0x22, np.uint8)
+    S = np.array([[127, 128], [127, 127]], np.uint8)
+    assert list(oracle.matmul_fp4(np.ones(64, np.float32), W, S, 64)) == [96.0, 64.0]
+    W = np.zeros((2, 16), np.uint8)
+    W[0], W[1] = 0x22, 0x44
+    y = oracle.matmul_fp4(np.ones(32, np.float32), W, np.array([[127], [127]], np.uint8), 32)
+    assert list(y) == [32.0, 64.0]
+    W = np.full((1, 16), 0xA2, np.uint8)
+    y = oracle.matmul_fp4(np.arange(1, 33, dtype=np.float32), W,
+                          np.array([[128]], np.uint8), 32)
+    assert y[0] == -32.0       # +1 on even (low nibble), -1 on odd, scale 2
+
+
+def test_fp8_scale_formats_agree_for_powers_of_two():
+    W, Sf, Se, x = common.fp8_problem(3, 300, 640)
+    assert common.bits_equal(oracle.matmul_fp8(x, W, Sf), oracle.matmul_fp8(x, W, Se))
+
+
+def test_fp8_against_double_math():
+    """Independent of the tree: exact per-block products summed in float64
+    agree to within f32 rounding of the result."""
+    W, Sf, Se, x = common.fp8_problem(4, 130, 384)
+    tab = oracle.dump_e4m3().astype(np.float64)
+    Wd = tab[W]
+    sc = np.repeat(np.repeat(Sf.astype(np.float64), 128, 0)[:130], 128, 1)[:, :384]
+    want = (Wd * sc) @ x.astype(np.float64)
+    got = oracle.matmul_fp8(x, W, Se)
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-30)) < 1e-6
+
+
+@ref_only
+def test_fp8_fp4_bit_equal_to_compiled_reference():
+    rng = np.random.default_rng(11)
+    for out, inn in [(37, 256), (257, 1024), (64, 7168)]:
+        W = common.fp8_codes(rng, (out, inn))
+        S = (120 + rng.integers(0, 15, size=((out + 127) // 128, inn // 128))).astype(np.uint8)
+        x = rng.standard_normal(inn, dtype=np.float32)
+        a = oracle.matmul_fp8(x, W, S)
+        assert common.bits_equal(a, oracle.ref_matmul_fp8(x, W, S))
+        assert common.bits_equal(a, oracle.ref_matmul_fp8(x, W, S, scalar=True))
+        W4 = rng.integers(0, 256, size=(out, inn // 2), dtype=np.int32).astype(np.uint8)
+        S4 = (120 + rng.integers(0, 15, size=(out, inn // 32))).astype(np.uint8)
+        a = oracle.matmul_fp4(x, W4, S4, inn)
+        assert common.bits_equal(a, oracle.ref_matmul_fp4(x, W4, S4, inn))
+        assert common.bits_equal(a, oracle.ref_matmul_fp4(x, W4, S4, inn, scalar=True))
+
+
+def test_batched_equals_gemvs():
+    """test_matmul.c:318-415: nt x GEMV, bit for bit."""
+    rng = np.random.default_rng(5)
+    W = common.fp8_codes(rng, (37, 256))
+    S = (120 + rng.integers(0, 15, size=(1, 2))).astype(np.uint8)
+    X = rng.standard_normal((5, 256), dtype=np.float32)
+    Y = oracle.matmul_fp8(X, W, S)
+    for t in range(5):
+        assert common.bits_equal(Y[t], oracle.matmul_fp8(X[t], W, S))
+
+
+# ------------------------------------------------------------ swiglu / moe
+def test_swiglu_limits():
+    g = np.array([-30, -12, -1, 0, 1, 9.5, 12, 40], np.float32)
+    u = np.array([-20, 5, -11, 3, 11, -0.5, 12, -15], np.float32)
+    y0 = oracle.swiglu(g, u, 0.0)
+    gd = g.astype(np.float64)
+    silu = gd / (1 + np.exp(-gd))
+    assert np.allclose(y0, silu * u, rtol=1e-6, atol=0)
+    y = oracle.swiglu(g, u, 10.0)
+    gc = np.minimum(gd, 10.0)          # upper clamp only on gate
+    uc = np.clip(u.astype(np.float64), -10, 10)
+    assert np.allclose(y, gc / (1 + np.exp(-gc)) * uc, rtol=1e-6, atol=0)
+    assert y[0] != 0.0 and abs(y[0]) < 1e-9     # gate -30 not clamped up to -10
+
+
+@ref_only
+def test_swiglu_bit_equal_to_compiled_reference():
+    rng = np.random.default_rng(6)
+    g = (rng.standard_normal(4096) * 8).astype(np.float32)
+    u = (rng.standard_normal(4096) * 8).astype(np.float32)
+    for lim in (10.0, 0.0, -1.0):
+        assert common.bits_equal(oracle.swiglu(g, u, lim), oracle.ref_swiglu(g, u, lim))
+
+
+def test_moe_is_k_ordered_expert_sum():
+    rng = np.random.default_rng(7)
+    hidden, inter, topk = 64, 96, 3
+    ex = [common.fp4_expert(rng, hidden, inter) for _ in range(topk)]
+    x = rng.standard_normal(hidden, dtype=np.float32)
+    w = common.router(rng, topk)
+    out, acc = oracle.moe_fp4(x, ex, w, hidden, inter, 10.0, return_acc=True)
+    for k, e in enumerate(ex):
+        g = oracle.matmul_fp4(x, e["w1"], e["s1"], hidden)
+        u = oracle.matmul_fp4(x, e["w3"], e["s3"], hidden)
+        h = oracle.swiglu(g, u, 10.0)
+        assert common.bits_equal(acc[k], oracle.matmul_fp4(h, e["w2"], e["s2"], inter))
+    want = np.zeros(hidden, np.float32)
+    for k in range(topk):
+        want = (want + (w[k] * acc[k]).astype(np.float32)).astype(np.float32)
+    assert common.bits_equal(out, want)
+
+
+# ------------------------------------------------------------ indexer / top-k
+def test_indexer_known_answers():
+    """test_indexer.c:23-164."""
+    out = oracle.indexer_score(np.array([[1, 0], [0, 0]], np.float32),
+                               np.array([[1, 0], [-1, 0]], np.float32),
+                               np.array([1, 1], np.float32))
+    assert out[0] > 0 and out[1] == 0.0 and f32bits(out[1]) == 0
+    q = np.zeros((4, 16), np.float32); q[0, 0] = 1
+    kv = np.zeros((1, 16), np.float32); kv[0, 0] = 1
+    w = np.array([1, 0, 0, 0], np.float32)
+    want = np.float32(np.float32(1) / np.sqrt(np.float32(16))) * \
+        np.float32(np.float32(1) / np.sqrt(np.float32(4)))
+    assert oracle.indexer_score(q, kv, w)[0] == want
+    o = oracle.indexer_score(np.array([[1, 0], [0, 1]], np.float32),
+                             np.array([[1, 0], [0, 1]], np.float32),
+                             np.array([1, 4], np.float32))
+    assert abs(o[1] / o[0] - 4) < 1e-6
+    q = np.array([[1, 2, -1, 0.5]], np.float32)
+    kv = np.array([[2, 1, -0.5, 1]], np.float32)
+    Hm = np.array([[1, 1, 1, 1], [1, -1, 1, -1], [1, 1, -1, -1], [1, -1, -1, 1]], np.float32) * 0.5
+    a = oracle.indexer_score(q, kv, np.ones(1, np.float32))
+    b = oracle.indexer_score(q @ Hm.T, kv @ Hm.T, np.ones(1, np.float32))
+    assert a[0] > 0.1 and abs(a[0] - b[0]) < 1e-5
+
+
+def test_topk_ties_and_clamp():
+    s = np.array([1, 5, 5, 2, 0, 5], np.float32)
+    assert list(oracle.topk(s, 4)) == [1, 2, 5, 3]
+    assert len(oracle.topk(s, 10)) == 6
+    z = np.array([0.0, -0.0, 0.0, -1.0], np.float32)     # -0 ties with +0
+    assert list(oracle.topk(z, 3)) == [0, 1, 2]
+
+
+def test_topk_equals_stable_sort():
+    rng = np.random.default_rng(8)
+    for n, k in [(1000, 100), (4096, 512), (300, 300)]:
+        s = rng.integers(-20, 20, size=n).astype(np.float32) * 0.25   # many ties
+        want = np.lexsort((np.arange(n), -s.astype(np.float64)))[:k]
+        assert list(oracle.topk(s, k)) == list(want)
+
+
+def test_indexer_plumbing():
+    assert list(oracle.indexer_offset([0, 3, -1, 7, -1], 128)) == [128, 131, -1, 135, -1]
+    assert [oracle.indexer_navail(p, 4) for p in (0, 3, 7, 2047)] == [0, 1, 2, 512]
+    n, idx = oracle.window_idxs(5, 4)
+    assert n == 4 and list(idx) == [1, 0, 3, 2]
+    n, idx = oracle.window_idxs(2, 4)
+    assert n == 3 and list(idx) == [2, 1, 0, -1]
+
+
+@ref_only
+def test_indexer_topk_bit_equal_to_compiled_reference():
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((16, 128)).astype(np.float32)
+    kv = rng.standard_normal((3000, 128)).astype(np.float32)
+    w = rng.standard_normal(16).astype(np.float32)
+    s = oracle.indexer_score(q, kv, w)
+    assert common.bits_equal(s, oracle.ref_indexer_score(q, kv, w))
+    assert list(oracle.topk(s, 150)) == list(oracle.ref_topk(s, 150))
+
+
+# ------------------------------------------------------------ attention
+def test_attention_known_answers():
+    """test_attn.c:21-134."""
+    kv = np.repeat(np.arange(1, 5, dtype=np.float32)[:, None], 4, 1)
+    o = oracle.sparse_attn(np.zeros((2, 4), np.float32), kv,
+                           np.full(2, -1000, np.float32), [0, 1, 2, 3], 1.0)
+    assert np.allclose(o, 2.5, atol=1e-5)
+    o = oracle.sparse_attn(np.zeros((1, 2), np.float32), np.full((1, 2), 8, np.float32),
+                           np.zeros(1, np.float32), [0], 1.0)
+    assert abs(o[0, 0] - 4.0) < 1e-5
+    o = oracle.sparse_attn(np.zeros((2, 2), np.float32), np.full((1, 2), 8, np.float32),
+                           np.array([-20, 20], np.float32), [0], 1.0)
+    assert abs(o[0, 0] - 8) < 1e-3 and o[1, 0] < 1e-3
+    kv = np.repeat(np.arange(1, 5, dtype=np.float32)[:, None], 2, 1)
+    o = oracle.sparse_attn(np.zeros((1, 2), np.float32), kv,
+                           np.full(1, -1000, np.float32), [0, -1, 2, -1], 1.0)
+    assert abs(o[0, 0] - 2.0) < 1e-5
+
+
+def test_attention_without_sink_is_textbook_softmax():
+    rng = np.random.default_rng(10)
+    h, d, n, topk = 4, 24, 50, 20
+    q = rng.standard_normal((h, d)).astype(np.float32)
+    kv = rng.standard_normal((n, d + 8)).astype(np.float32)
+    idx = rng.integers(-1, n, size=topk).astype(np.int32)
+    o = oracle.sparse_attn(q, kv, None, idx, 0.2, d_v=d + 8)
+    valid = idx[idx >= 0]
+    s = (q.astype(np.float64) @ kv[valid, :d].T.astype(np.float64)) * 0.2
+    p = np.exp(s - s.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    want = p @ kv[valid].astype(np.float64)
+    assert np.max(np.abs(o - want)) < 1e-5
+
+
+@ref_only
+def test_attention_bit_equal_to_compiled_reference():
+    rng = np.random.default_rng(12)
+    h, d, n, topk = 8, 64, 200, 60
+    q = rng.standard_normal((h, d)).astype(np.float32)
+    kv = rng.standard_normal((n, d)).astype(np.float32)
+    sink = rng.standard_normal(h).astype(np.float32)
+    idx = rng.integers(-1, n, size=topk).astype(np.int32)
+    a = oracle.sparse_attn(q, kv, sink, idx, 0.125)
+    assert common.bits_equal(a, oracle.ref_sparse_attn(q, kv, sink, idx, 0.125))

@@ -1,0 +1,388 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X decode hot path.
+
+Headline (the metric's own configuration): the
+DeepSeek-scale FP8 trunk GEMV sweep at batch 1 -- 1536x7168, 576x7168,
+24576x1536, 7168x16384, 7168x7168 and the 129280x7168 LM head, e4m3 weights
+with fp32 128x128 block scales, x ~ N(0,1). One "step" is one decode token's
+sweep: the six GEMVs back to back on one stream, every input already resident
+in HBM. `value` is achieved HBM GB/s over the sweep (algorithmic bytes /
+step time); `ms_per_step` is the time per trunk token (all six shapes).
+
+Cold data: one step streams 1.15 GB, more than the 256 MB Infinity Cache, so
+every matrix has been evicted before it is read again.
+
+Also reported (`detail`): C1 (4096x4096, rotating 64 copies = 1.07 GB), C3
+(MXFP4 routed experts, 8 of 256 resident experts per step = 187 MB, rotated
+over the 6 GB expert pool) and C4 (the sparse-MLA decode step, rotating 26
+copies of the key/KV caches).
+
+roofline: the LM-head GEMV (80% of the sweep's bytes), algorithmic bytes per
+launch / its average launch time from HIP events on the launch stream.
+cpu_baseline: the reference's own CPU path (oracle/_ref, its
+dsv4_matmul_fp8 compiled with OpenMP + AVX2) on the same sweep, timed on this
+host's cores.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+PEAK_GBS = 8000.0
+METRIC = ("achieved HBM GB/s (% of peak) for FP8/FP4 decode GEMV; "
+          "µs per trunk token")
+TRUNK = [(1536, 7168), (576, 7168), (24576, 1536), (7168, 16384), (7168, 7168)]
+LM_HEAD = (129280, 7168)
+
+
+def fp8_bytes(rows, cols):
+    """Algorithmic bytes: weights + fp32 block scales + x + y."""
+    sr, sc = (rows + 127) // 128, (cols + 127) // 128
+    return rows * cols + sr * sc * 4 + cols * 4 + rows * 4
+
+
+def moe_bytes(hidden, inter, topk):
+    per = 2 * inter * (hidden // 2 + hidden // 32) + hidden * (inter // 2 + inter // 32)
+    return topk * per + hidden * 2 + hidden * 4 + topk * 8
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-detail", action="store_true",
+                    help="headline sweep only (skip C1/C3/C4)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Bench:
+    def __init__(self):
+        import numpy as np
+        import torch
+        import common
+        self.np, self.torch, self.common = np, torch, common
+        self.dsv4 = common.load_pkg()
+        self.L = self.dsv4.init()
+        self.dev = torch.device("cuda:0")
+        self.stream = torch.cuda.current_stream()
+        self.sp = self.stream.cuda_stream
+
+    def t(self, a):
+        return self.torch.from_numpy(self.np.ascontiguousarray(a)).to(self.dev)
+
+    def ev(self):
+        return self.torch.cuda.Event(enable_timing=True)
+
+    def eager_us(self, go, n, warmup):
+        """Per-iteration time of go(i, stream) issued n times eagerly."""
+        torch = self.torch
+        for i in range(warmup):
+            go(i, self.sp)
+        torch.cuda.synchronize()
+        a, b = self.ev(), self.ev()
+        a.record(self.stream)
+        for i in range(n):
+            go(i, self.sp)
+        b.record(self.stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / n
+
+    def graph_us(self, go, n, replays):
+        """Per-iteration time with n iterations captured into one HIP graph
+        and replayed: no host launch gaps, as a decode loop would run."""
+        torch = self.torch
+        for i in range(n):                      # settle scratch sizes first
+            go(i, self.sp)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            sp = torch.cuda.current_stream().cuda_stream
+            for i in range(n):
+                go(i, sp)
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = self.ev(), self.ev()
+        a.record(self.stream)
+        for _ in range(replays):
+            g.replay()
+        b.record(self.stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / (replays * n)
+        del g
+        return us
+
+    # --------------------------------------------------------- C2 sweep
+    def c2_setup(self):
+        np = self.np
+        self.c2 = []
+        for i, (rows, cols) in enumerate(TRUNK + [LM_HEAD]):
+            W, Sf, Se, x = self.common.fp8_problem(i, rows, cols)
+            self.c2.append(dict(rows=rows, cols=cols, W=W, Se=Se, x=x,
+                                dW=self.t(W), dS=self.t(Sf), dx=self.t(x),
+                                dy=self.torch.empty(rows, dtype=self.torch.float32,
+                                                    device=self.dev)))
+        self.torch.cuda.synchronize()
+
+    def c2_launch(self, m, sp=None):
+        rc = self.L.dsv4_gpu_fp8_gemv_d(m["dy"].data_ptr(), m["dx"].data_ptr(),
+                                        m["dW"].data_ptr(), m["dS"].data_ptr(), 1,
+                                        m["rows"], m["cols"],
+                                        self.sp if sp is None else sp)
+        if rc != 0:
+            raise RuntimeError("fp8 gemv launch failed")
+
+    def c2_step(self, i=0, sp=None):
+        for m in self.c2:
+            self.c2_launch(m, sp)
+
+    def c2_run(self, steps, warmup):
+        """Step time in a replayed HIP graph (the value), the eager step time,
+        and per-kernel durations from events bracketing each eager launch."""
+        torch = self.torch
+        eager_ms = self.eager_us(self.c2_step, steps, warmup) / 1e3
+        graph_ms = self.graph_us(self.c2_step, 10, max(1, steps // 10)) / 1e3
+        nk = len(self.c2)
+        evs = [[self.ev() for _ in range(nk + 1)] for _ in range(steps)]
+        for s in range(steps):
+            evs[s][0].record(self.stream)
+            for k, m in enumerate(self.c2):
+                self.c2_launch(m)
+                evs[s][k + 1].record(self.stream)
+        torch.cuda.synchronize()
+        per = [sum(evs[s][k].elapsed_time(evs[s][k + 1]) for s in range(steps)) / steps
+               for k in range(nk)]
+        return graph_ms, eager_ms, per
+
+    # ------------------------------------------------------------ C1
+    def c1_run(self, steps, warmup):
+        torch, np = self.torch, self.np
+        rows = cols = 4096
+        W, Sf, Se, x = self.common.fp8_problem(0, rows, cols)
+        copies = 64
+        dW0, dS0 = self.t(W), self.t(Sf)
+        dW = torch.empty((copies, rows, cols), dtype=torch.uint8, device=self.dev)
+        dS = torch.empty((copies,) + Sf.shape, dtype=torch.float32, device=self.dev)
+        dW[:] = dW0
+        dS[:] = dS0
+        dx = self.t(x)
+        dy = torch.empty(rows, dtype=torch.float32, device=self.dev)
+
+        def go(i, sp):
+            j = i % copies
+            assert self.L.dsv4_gpu_fp8_gemv_d(dy.data_ptr(), dx.data_ptr(),
+                                              dW[j].data_ptr(), dS[j].data_ptr(), 1,
+                                              rows, cols, sp) == 0
+        eager = self.eager_us(go, max(steps, copies), max(warmup, copies))
+        us = self.graph_us(go, copies, max(2, steps // 8))
+        del dW, dS
+        return us, eager, fp8_bytes(rows, cols)
+
+    # ------------------------------------------------------------ C3
+    def c3_run(self, steps, warmup):
+        import ctypes
+        torch, np = self.torch, self.np
+        hidden, inter, topk, n_exp = 7168, 2048, 8, 256
+        g = torch.Generator(device=self.dev)
+        g.manual_seed(0)
+        wb13, sb13 = inter * hidden // 2, inter * hidden // 32
+        wb2, sb2 = hidden * inter // 2, hidden * inter // 32
+        W13 = torch.randint(0, 256, (n_exp, 2, wb13), dtype=torch.uint8,
+                            device=self.dev, generator=g)
+        S13 = torch.randint(121, 130, (n_exp, 2, sb13), dtype=torch.uint8,
+                            device=self.dev, generator=g)
+        W2 = torch.randint(0, 256, (n_exp, wb2), dtype=torch.uint8, device=self.dev,
+                           generator=g)
+        S2 = torch.randint(121, 130, (n_exp, sb2), dtype=torch.uint8, device=self.dev,
+                           generator=g)
+        torch.cuda.synchronize()
+        D = self.dsv4
+        layer = 60
+        for e in range(n_exp):
+            ew = D.DSV4ExpertW(
+                D.DSV4QMat(W13[e, 0].data_ptr(), S13[e, 0].data_ptr(), D.WFP4, inter, hidden, 1, 32),
+                D.DSV4QMat(W13[e, 1].data_ptr(), S13[e, 1].data_ptr(), D.WFP4, inter, hidden, 1, 32),
+                D.DSV4QMat(W2[e].data_ptr(), S2[e].data_ptr(), D.WFP4, hidden, inter, 1, 32))
+            assert self.L.dsv4_gpu_bind_expert_d(layer, e, ctypes.byref(ew)) == 0
+        rng = np.random.default_rng(0)
+        nsets = 64
+        ids = np.stack([rng.permutation(n_exp)[:topk] for _ in range(nsets)]).astype(np.int32)
+        ws = np.stack([self.common.router(rng, topk) for _ in range(nsets)])
+        d_ids, d_ws = self.t(ids), self.t(ws)
+        x = self.common.bf16_round(rng.standard_normal(hidden).astype(np.float32))
+        dx = self.t(x)
+        do = torch.empty(hidden, dtype=torch.float32, device=self.dev)
+
+        def go(i, sp):
+            j = i % nsets
+            assert self.L.dsv4_gpu_moe_fp4_d(do.data_ptr(), dx.data_ptr(), layer,
+                                             d_ids[j].data_ptr(), d_ws[j].data_ptr(),
+                                             topk, hidden, inter, 10.0, sp) == 0
+        eager = self.eager_us(go, max(steps, nsets), warmup)
+        us = self.graph_us(go, nsets, max(2, steps // 16))
+        del W13, S13, W2, S2
+        return us, eager, moe_bytes(hidden, inter, topk)
+
+    # ------------------------------------------------------------ C4
+    def c4_run(self, steps, warmup):
+        torch, np = self.torch, self.np
+        n, H, D, k, h, dqk, dv = 32768, 16, 128, 2048, 64, 576, 512
+        rng = np.random.default_rng(0)
+        codes, s, _ = self.common.fp8_keys(rng, n, D)
+        kv = self.common.bf16_round(rng.standard_normal((n, dqk)).astype(np.float32)
+                                    / np.float32(np.sqrt(dqk)))
+        kvb = self.common.bf16_bits(kv).view(np.int16)
+        qi = rng.standard_normal((H, D)).astype(np.float32)
+        wi = rng.standard_normal(H).astype(np.float32)
+        q = rng.standard_normal((h, dqk)).astype(np.float32)
+        copies = 26
+        d_codes = self.t(codes).unsqueeze(0).repeat(copies, 1, 1)
+        d_s = self.t(s).unsqueeze(0).repeat(copies, 1)
+        d_kv = self.t(kvb).unsqueeze(0).repeat(copies, 1, 1)
+        d_qi, d_wi, d_q = self.t(qi), self.t(wi), self.t(q)
+        d_o = torch.empty((h, dv), dtype=torch.float32, device=self.dev)
+        d_idx = torch.empty(k, dtype=torch.int32, device=self.dev)
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(dqk)))
+
+        def go(i, sp):
+            j = i % copies
+            assert self.L.dsv4_gpu_mla_decode_d(
+                d_o.data_ptr(), d_idx.data_ptr(), d_qi.data_ptr(), d_wi.data_ptr(), H, D,
+                d_codes[j].data_ptr(), d_s[j].data_ptr(), self.dsv4.KV_FP8, D, n, k,
+                d_q.data_ptr(), d_kv[j].data_ptr(), self.dsv4.KV_BF16, dqk, n, None, h,
+                dqk, dv, scale, sp) == 0
+        eager = self.eager_us(go, max(steps, copies), max(warmup, copies))
+        us = self.graph_us(go, copies, max(2, steps // 8))
+        alg = n * D + n * 4 + k * dqk * 2 + h * dqk * 4 + h * dv * 4 + k * 4 + H * D * 4 + H * 4
+        del d_codes, d_s, d_kv
+        return us, eager, alg
+
+    # ------------------------------------------------------ CPU baseline
+    def cpu_baseline(self):
+        """The compiled reference dsv4_matmul_fp8 (OpenMP + AVX2) over the same
+        sweep (E8M0 twin of the power-of-two fp32 scales: identical values),
+        repeated until ~10 s of CPU work or 25 sweeps."""
+        import oracle
+        if not oracle.ref_available():
+            return None
+        np = self.np
+        ys = [np.empty(m["rows"], np.float32) for m in self.c2]
+        reps, total = 0, 0.0
+        while (total < 10.0 and reps < 25) or reps < 2:
+            t0 = time.perf_counter()
+            for m in self.c2:
+                oracle.ref_matmul_fp8(m["x"], m["W"], m["Se"])
+            total += time.perf_counter() - t0
+            reps += 1
+        per = total / reps
+        alg = sum(fp8_bytes(m["rows"], m["cols"]) for m in self.c2)
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        return {"value": round(alg / per / 1e9, 3), "unit": "GB/s", "cores": threads,
+                "kind": "reference",
+                "sample": "the full C2 sweep (5 trunk shapes + LM head, 1.15 GB of "
+                          "weights), %d sweeps, %.1f s; %.1f ms per trunk token"
+                          % (reps, total, per * 1e3),
+                "ms_per_step": round(per * 1e3, 3)}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py: this build runs on one GPU; the multi-GPU sharding of "
+              "the decode path is described in DESIGN.md, not launched "
+              "(requested --gpus %d)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: WORLD_SIZE > 1 is not supported (one GPU per run)",
+              file=sys.stderr)
+        sys.exit(2)
+    B = Bench()
+    log("bench: C2 setup")
+    B.c2_setup()
+    log("bench: C2 timed sweep, %d steps" % args.steps)
+    step_ms, eager_ms, per_ms = B.c2_run(args.steps, args.warmup)
+    shapes = TRUNK + [LM_HEAD]
+    algs = [fp8_bytes(r, c) for r, c in shapes]
+    alg_step = sum(algs)
+    value = alg_step / (step_ms * 1e-3) / 1e9
+    per_shape = {}
+    for (r, c), a, ms in zip(shapes, algs, per_ms):
+        per_shape["%dx%d" % (r, c)] = {"us": round(ms * 1e3, 3),
+                                       "GBps": round(a / (ms * 1e-3) / 1e9, 1),
+                                       "frac": round(a / (ms * 1e-3) / 1e9 / PEAK_GBS, 4)}
+    trunk_us = sum(per_ms[:5]) * 1e3
+    lm_ms = per_ms[5]
+    lm_gbs = algs[5] / (lm_ms * 1e-3) / 1e9
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "fp8_gemv_lm_head_traffic.json")
+    if os.path.exists(tf):
+        try:
+            traffic = json.load(open(tf)).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    detail = {}
+
+    def rec(us, eager, alg):
+        return {"us": round(us, 3), "GBps": round(alg / us / 1e3, 1),
+                "frac": round(alg / us / 1e3 / PEAK_GBS, 4),
+                "eager_us": round(eager, 3), "algorithmic_bytes": alg}
+    if not args.no_detail:
+        log("bench: C1")
+        detail["c1_fp8_4096x4096"] = rec(*B.c1_run(args.steps, args.warmup))
+        log("bench: C3")
+        detail["c3_moe_fp4_8of256_7168x2048"] = rec(*B.c3_run(args.steps, args.warmup))
+        log("bench: C4")
+        detail["c4_sparse_mla_step_32768_top2048"] = rec(*B.c4_run(args.steps, args.warmup))
+    cpu = None
+    if not args.no_cpu:
+        log("bench: CPU baseline (compiled reference, host cores)")
+        cpu = B.cpu_baseline()
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded numpy: e4m3 codes uniform over finite, fp32 "
+                "scales 2^U{-8..-4}, x ~ N(0,1))",
+        "config": {"workload": "C2: DeepSeek-scale FP8 trunk GEMV sweep, batch 1, "
+                               "1536x7168 576x7168 24576x1536 7168x16384 7168x7168 "
+                               "+ LM head 129280x7168, fp32 128x128 block scales",
+                   "batch": 1, "bytes_per_step": alg_step},
+        "pct_of_peak": round(100.0 * value / PEAK_GBS, 2),
+        "us_per_trunk_token": {"trunk_5_shapes": round(trunk_us, 3),
+                               "with_lm_head": round(step_ms * 1e3, 3),
+                               "with_lm_head_eager": round(eager_ms * 1e3, 3)},
+        "per_shape": per_shape,
+        "roofline": {"bound": "hbm", "achieved": round(lm_gbs, 1), "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": round(lm_gbs / PEAK_GBS, 4),
+                     "traffic": traffic,
+                     "kernel": "k_fp8_gemv (LM head 129280x7168)",
+                     "algorithmic_bytes_per_launch": algs[5],
+                     "avg_launch_us": round(lm_ms * 1e3, 3)},
+        "cpu_baseline": cpu,
+        "detail": detail,
+    }
+    print(json.dumps(out))
+    B.L.dsv4_gpu_shutdown()
+
+
+if __name__ == "__main__":
+    main()

@@ -60,6 +60,8 @@ def parse():
     ap.add_argument("--no-detail", action="store_true",
                     help="headline sweep only (skip C1/C3/C4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4"], default=None,
+                    help="time one configuration only (for profiling runs)")
     return ap.parse_args()
 
 
@@ -308,6 +310,14 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     B = Bench()
+    if args.only in ("c1", "c3", "c4"):
+        fn = {"c1": B.c1_run, "c3": B.c3_run, "c4": B.c4_run}[args.only]
+        us, eager, alg = fn(args.steps, args.warmup)
+        print(json.dumps({"config": args.only, "us": round(us, 3),
+                          "eager_us": round(eager, 3),
+                          "GBps": round(alg / us / 1e3, 1)}))
+        B.L.dsv4_gpu_shutdown()
+        return
     log("bench: C2 setup")
     B.c2_setup()
     log("bench: C2 timed sweep, %d steps" % args.steps)

@@ -98,24 +98,57 @@ __device__ __forceinline__ float dot16(const u32x4 v, const float *xr)
     return (p0 + p1) + (p2 + p3);
 }
 
-template <int NCH, int R, int SF>
+/* Rows per workgroup are bounded by the LDS that holds the per-wave row
+ * partials of rows wider than one wave (at most 4 waves per row). */
+constexpr int PART_MAX = 4096;
+
+template <int NCH>
+__device__ __forceinline__ void load_rows(u32x4 (*wv)[NCH], const uint8_t *W,
+                                          int rbase, int rend, int cols,
+                                          int j, int tc, const bool *act, int R)
+{
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (i >= R) break;
+        const int r = rbase + i;
+#pragma unroll
+        for (int n = 0; n < NCH; n++) {
+            if (act[n] && r < rend)
+                wv[i][n] = ld16_stream(W + (size_t)r * cols + (size_t)(j + n * tc) * 16);
+            else
+                wv[i][n] = u32x4{0, 0, 0, 0};
+        }
+    }
+}
+
+/* One workgroup owns the contiguous rows [row0, row0 + rows_per_wg). It walks
+ * them in steps of rg*R rows (row group g takes rows g*R .. g*R+R-1 of the
+ * step); with PF the next step's weights are in flight while this step's are
+ * consumed. Rows that span several waves leave one partial per wave in LDS,
+ * summed in wave order after a single barrier at the end. */
+template <int NCH, int R, int SF, int PF>
 __global__ void __launch_bounds__(256)
 k_fp8_gemv(float *__restrict__ y, const float *__restrict__ x,
            const uint8_t *__restrict__ W, const void *__restrict__ S,
            int rows, int cols, int sc, int blk_r, int blk_c, int tc,
-           int tiles_per_wg, int ntiles)
+           int rows_per_wg)
 {
-    __shared__ float red[4][R];             /* [wave][row] partials        */
+    extern __shared__ float part[];     /* [waves per row][rows_per_wg] */
 
     const int tid = threadIdx.x;
     const int g = tid / tc;
     const int j = tid - g * tc;
     const int rg = blockDim.x / tc;
     const int ch = cols >> 4;
-    const int wid = tid >> 6, lane = tid & 63;
+    const int lane = tid & 63;
+    const int row0 = blockIdx.x * rows_per_wg;
+    const int rend = min(rows, row0 + rows_per_wg);
+    const int nloc = rend - row0;
+    const int step_rows = rg * R;
+    const int nsteps = (nloc + step_rows - 1) / step_rows;
 
     float xr[NCH][16];
-    int cb[NCH];                             /* column-block of each chunk */
+    int cb[NCH];
     bool act[NCH];
 #pragma unroll
     for (int n = 0; n < NCH; n++) {
@@ -135,24 +168,13 @@ k_fp8_gemv(float *__restrict__ y, const float *__restrict__ x,
 #pragma unroll
     for (int n = 0; n < NCH; n++) sreg[n] = 0.0f;
 
-    const int t0 = blockIdx.x * tiles_per_wg;
-    const int t1 = min(ntiles, t0 + tiles_per_wg);
-    for (int tile = t0; tile < t1; ++tile) {
-        const int rbase = (tile * rg + g) * R;
+    u32x4 wv[R][NCH], wn[R][NCH];
+    if (nsteps > 0) load_rows<NCH>(wv, W, row0 + g * R, rend, cols, j, tc, act, R);
 
-        u32x4 wv[R][NCH];
-#pragma unroll
-        for (int i = 0; i < R; i++) {
-            const int r = rbase + i;
-#pragma unroll
-            for (int n = 0; n < NCH; n++) {
-                if (act[n] && r < rows)
-                    wv[i][n] = ld16_stream(W + (size_t)r * cols
-                                           + (size_t)(j + n * tc) * 16);
-                else
-                    wv[i][n] = u32x4{0, 0, 0, 0};
-            }
-        }
+    for (int step = 0; step < nsteps; ++step) {
+        const int rbase = row0 + step * step_rows + g * R;
+        if (PF && step + 1 < nsteps)
+            load_rows<NCH>(wn, W, rbase + step_rows, rend, cols, j, tc, act, R);
 
         float acc[R];
 #pragma unroll
@@ -176,24 +198,35 @@ k_fp8_gemv(float *__restrict__ y, const float *__restrict__ x,
 #pragma unroll
             for (int i = 0; i < R; i++) {
                 const float v = seg_sum_rt(acc[i], tc);
-                if (j == tc - 1 && rbase + i < rows) y[rbase + i] = v;
+                if (j == tc - 1 && rbase + i < rend) y[rbase + i] = v;
             }
         } else {
-            const int wpr = tc >> 6;
+            const int w = j >> 6;                  /* wave within the row */
 #pragma unroll
             for (int i = 0; i < R; i++) {
                 const float v = seg_sum<64>(acc[i]);
-                if (lane == 63) red[wid][i] = v;
+                const int rl = rbase + i - row0;
+                if (lane == 63 && rl < nloc) part[w * rows_per_wg + rl] = v;
             }
-            __syncthreads();
-            if (tid < rg * R) {
-                const int gg = tid / R, ii = tid - gg * R;
-                const int r = (tile * rg + gg) * R + ii;
-                float s = red[gg * wpr][ii];
-                for (int w = 1; w < wpr; w++) s += red[gg * wpr + w][ii];
-                if (r < rows) y[r] = s;
-            }
-            __syncthreads();
+        }
+
+        if (PF) {
+#pragma unroll
+            for (int i = 0; i < R; i++)
+#pragma unroll
+                for (int n = 0; n < NCH; n++) wv[i][n] = wn[i][n];
+        } else if (step + 1 < nsteps) {
+            load_rows<NCH>(wv, W, rbase + step_rows, rend, cols, j, tc, act, R);
+        }
+    }
+
+    if (tc > 64) {
+        __syncthreads();
+        const int wpr = tc >> 6;
+        for (int rl = tid; rl < nloc; rl += blockDim.x) {
+            float s = part[rl];
+            for (int w = 1; w < wpr; w++) s += part[w * rows_per_wg + rl];
+            y[row0 + rl] = s;
         }
     }
 }
@@ -307,58 +340,69 @@ k_fp8_gemv_generic(float *__restrict__ y, const float *__restrict__ x,
     }
 }
 
-int g_fp8_R_override = -1;
-int g_fp8_maxwg = 0;
+int g_cu_count = 0;
 
-void fp8_tuning_from_env()
+int env_int(const char *name, int dflt)
 {
-    static int done = 0;
-    if (done) return;
-    done = 1;
-    const char *e = getenv("DSV4_GPU_FP8_R");
-    if (e) g_fp8_R_override = atoi(e);
-    e = getenv("DSV4_GPU_FP8_MAXWG");
-    if (e) g_fp8_maxwg = atoi(e);
+    const char *e = getenv(name);
+    return e ? atoi(e) : dflt;
 }
 
-template <int NCH, int R, int SF>
+int cu_count()
+{
+    if (!g_cu_count) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        g_cu_count = n;
+    }
+    return g_cu_count;
+}
+
+template <int NCH, int R, int SF, int PF>
 void launch_gemv(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
                  const void *S, int rows, int cols, int sc, int blk_r,
-                 int blk_c, int ntiles, int maxwg, hipStream_t st)
+                 int blk_c, int wgs_per_cu, hipStream_t st)
 {
-    const int want = ntiles < maxwg ? ntiles : maxwg;
-    const int tpw = (ntiles + want - 1) / want;
-    const int grid = (ntiles + tpw - 1) / tpw;
-    hipLaunchKernelGGL((k_fp8_gemv<NCH, R, SF>), dim3(grid), dim3(g.wg), 0, st,
-                       y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, tpw,
-                       ntiles);
+    const int step_rows = g.rg * R;
+    const int nsteps = (rows + step_rows - 1) / step_rows;
+    const int want = wgs_per_cu * cu_count();
+    int spw = (nsteps + want - 1) / want;              /* steps per workgroup */
+    const int wpr = g.tc > 64 ? g.tc / 64 : 1;
+    const int max_spw = PART_MAX / wpr / step_rows;
+    if (spw > max_spw) spw = max_spw;
+    if (spw < 1) spw = 1;
+    const int rows_per_wg = spw * step_rows;
+    const int grid = (rows + rows_per_wg - 1) / rows_per_wg;
+    const size_t lds = g.tc > 64 ? sizeof(float) * (size_t)wpr * rows_per_wg : 0;
+    hipLaunchKernelGGL((k_fp8_gemv<NCH, R, SF, PF>), dim3(grid), dim3(g.wg), lds, st,
+                       y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, rows_per_wg);
 }
 
-template <int R, int SF>
+template <int R, int SF, int PF>
 void launch_gemv_nch(const Fp8Geom &g, float *y, const float *x,
                      const uint8_t *W, const void *S, int rows, int cols,
-                     int sc, int blk_r, int blk_c, int ntiles, int maxwg,
-                     hipStream_t st)
+                     int sc, int blk_r, int blk_c, int wpc, hipStream_t st)
 {
     switch (g.nch) {
-    case 1: launch_gemv<1, R, SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, ntiles, maxwg, st); break;
-    case 2: launch_gemv<2, R, SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, ntiles, maxwg, st); break;
-    case 3: launch_gemv<3, R, SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, ntiles, maxwg, st); break;
-    default: launch_gemv<4, R, SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, ntiles, maxwg, st); break;
+    case 1: launch_gemv<1, R, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st); break;
+    case 2: launch_gemv<2, R, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st); break;
+    case 3: launch_gemv<3, R, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st); break;
+    default: launch_gemv<4, R, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st); break;
     }
 }
 
-template <int SF>
-void launch_gemv_sf(const Fp8Geom &g, int R, float *y, const float *x,
-                    const uint8_t *W, const void *S, int rows, int cols, int sc,
-                    int blk_r, int blk_c, int maxwg, hipStream_t st)
+template <int SF, int PF>
+void launch_gemv_r(const Fp8Geom &g, int R, float *y, const float *x,
+                   const uint8_t *W, const void *S, int rows, int cols, int sc,
+                   int blk_r, int blk_c, int wpc, hipStream_t st)
 {
-    const int per = g.rg * R;
-    const int ntiles = (rows + per - 1) / per;
     switch (R) {
-    case 1: launch_gemv_nch<1, SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, ntiles, maxwg, st); break;
-    case 2: launch_gemv_nch<2, SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, ntiles, maxwg, st); break;
-    default: launch_gemv_nch<4, SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, ntiles, maxwg, st); break;
+    case 1: launch_gemv_nch<1, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st); break;
+    case 2: launch_gemv_nch<2, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st); break;
+    default: launch_gemv_nch<4, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st); break;
     }
 }
 
@@ -391,25 +435,28 @@ int dsv4_fp8_gemv_launch(float *y, const float *x, const uint8_t *W,
         DSV4_ERR("fp8 gemv: bad shape %dx%d blk %dx%d", rows, cols, blk_r, blk_c);
         return -1;
     }
-    fp8_tuning_from_env();
     const int sc = (cols + blk_c - 1) / blk_c;
     Fp8Geom g;
-    if (fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c)) {
-        int R;
-        if (g_fp8_R_override > 0) {
-            R = g_fp8_R_override >= 4 ? 4 : g_fp8_R_override >= 2 ? 2 : 1;
+    const bool aligned = (((uintptr_t)x | (uintptr_t)W) & 15) == 0;
+    if (aligned && fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c)) {
+        /* Launch shape: R rows per thread per step, next step prefetched,
+         * workgroups per CU. None of these changes the arithmetic of a row. */
+        /* Defaults from a sweep over the C1/C2 shapes on MI355X (R in 1,2,4;
+         * prefetch on/off; 1-8 workgroups per CU): two rows per thread,
+         * prefetch only where the matrix is short, two workgroups per CU
+         * (four when rows are narrow). The environment can override each. */
+        int R = env_int("DSV4_GPU_FP8_R", 2);
+        R = R >= 4 ? 4 : R >= 2 ? 2 : 1;
+        const int pf = env_int("DSV4_GPU_FP8_PF", rows <= 4096 ? 1 : 0);
+        int wpc = env_int("DSV4_GPU_FP8_WPC", cols >= 4096 ? 2 : 4);
+        if (wpc <= 0) wpc = 2;
+        if (sfmt == 0) {
+            if (pf) launch_gemv_r<0, 1>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st);
+            else    launch_gemv_r<0, 0>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st);
         } else {
-            R = 1;
-            for (int cand = 4; cand >= 2; cand >>= 1) {
-                const int tiles = (rows + g.rg * cand - 1) / (g.rg * cand);
-                if (tiles >= 2048) { R = cand; break; }
-            }
+            if (pf) launch_gemv_r<1, 1>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st);
+            else    launch_gemv_r<1, 0>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st);
         }
-        const int maxwg = g_fp8_maxwg > 0 ? g_fp8_maxwg : 2048;
-        if (sfmt == 0)
-            launch_gemv_sf<0>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, maxwg, st);
-        else
-            launch_gemv_sf<1>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, maxwg, st);
     } else {
         const int grid = (rows + 3) / 4;
         if (sfmt == 0)
@@ -433,7 +480,8 @@ int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,
     }
     const int sc = (cols + blk_c - 1) / blk_c;
     Fp8Geom g;
-    if (fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c)) {
+    const bool aligned = (((uintptr_t)x | (uintptr_t)W) & 15) == 0;
+    if (aligned && fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c)) {
         if (sfmt == 0)
             launch_gemv_n<0>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st);
         else

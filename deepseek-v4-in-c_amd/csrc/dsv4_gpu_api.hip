@@ -295,6 +295,21 @@ int dump(float *host, int which, int count)
 
 } // namespace
 
+size_t dsv4_lds_limit(void)
+{
+    static size_t cached = 0;
+    if (!cached) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+            v >= 64 * 1024)
+            cached = (size_t)v;
+        else
+            cached = 64 * 1024;
+    }
+    return cached;
+}
+
 /* ===================================================================== ABI */
 extern "C" {
 
@@ -723,7 +738,8 @@ int dsv4_gpu_sparse_attn(float *o, const float *q, const dsv4_gpu_kv *kv,
                      kv->n_rows);
             return -1;
         }
-    if (scratch_reserve(g_attn, dsv4_attn_scratch_bytes(h, d_v, topk)) != 0) return -1;
+    if (scratch_reserve(g_attn, dsv4_attn_scratch_bytes(h, d_qk, d_v, topk, kv->fmt) + 4) != 0)
+        return -1;
     Stage s;
     const size_t qo = s.in(q, (size_t)h * d_qk * sizeof(float));
     const size_t so = sink ? s.in(sink, (size_t)h * sizeof(float)) : 0;
@@ -763,7 +779,8 @@ int dsv4_gpu_sparse_attn_d(float *d_o, const float *d_q, const void *d_kv,
                            void *stream)
 {
     if (!g_ready) return -1;
-    if (scratch_reserve(g_attn, dsv4_attn_scratch_bytes(h, d_v, topk)) != 0) return -1;
+    if (scratch_reserve(g_attn, dsv4_attn_scratch_bytes(h, d_qk, d_v, topk, kv_fmt) + 4) != 0)
+        return -1;
     return dsv4_attn_launch(d_o, d_q, d_kv, kv_fmt, kv_stride, kv_rows, d_sink,
                             d_idxs, h, d_qk, d_v, topk, scale, g_attn.p,
                             as_stream(stream));
@@ -783,7 +800,7 @@ int dsv4_gpu_mla_decode_d(float *d_o, int *d_idxs,
     if (k < 0) return -1;
     hipStream_t st = as_stream(stream);
     if (scratch_reserve(g_scores, (size_t)(n > 0 ? n : 1) * sizeof(float)) != 0 ||
-        scratch_reserve(g_attn, dsv4_attn_scratch_bytes(h, d_v, k)) != 0)
+        scratch_reserve(g_attn, dsv4_attn_scratch_bytes(h, d_qk, d_v, k, kv_fmt) + 4) != 0)
         return -1;
     if (n > 0 &&
         (dsv4_indexer_score_launch((float *)g_scores.p, d_q_idx, d_w_idx, H, D,

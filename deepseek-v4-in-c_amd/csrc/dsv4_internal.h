@@ -22,6 +22,10 @@
         }                                                                    \
     } while (0)
 
+/* Bytes of LDS one workgroup may use on the current device (the gfx950
+ * reports 160 KiB; 64 KiB if the query fails). */
+size_t dsv4_lds_limit(void);
+
 /* Block-scaled FP8 GEMV. sfmt 0 = E8M0 bytes, 1 = fp32. S is the scale grid
  * ceil(rows/blk_r) x sc with sc = ceil(cols/blk_c). Returns 0 / -1. */
 int dsv4_fp8_gemv_launch(float *y, const float *x, const uint8_t *W,
@@ -57,8 +61,8 @@ int dsv4_indexer_score_launch(float *d_out, const float *d_q, const float *d_w,
 int dsv4_topk_launch(int *d_idxs, const float *d_scores, int n, int k,
                      hipStream_t st);
 
-/* Scratch needed by dsv4_attn_launch, in bytes. */
-size_t dsv4_attn_scratch_bytes(int h, int d_v, int topk);
+/* Scratch needed by dsv4_attn_launch, in bytes (0: shape not supported). */
+size_t dsv4_attn_scratch_bytes(int h, int d_qk, int d_v, int topk, int kv_fmt);
 
 /* Rows outside [0, kv_rows) are treated as masked (never read). */
 int dsv4_attn_launch(float *d_o, const float *d_q, const void *d_kv,

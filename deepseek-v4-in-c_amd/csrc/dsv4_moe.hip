@@ -31,6 +31,8 @@
 #include "dsv4_dev.h"
 #include "dsv4_internal.h"
 
+#include <stdlib.h>
+
 namespace {
 
 struct Fp4Geom { int ch, tc, nch, wg, rg; };
@@ -109,22 +111,52 @@ expert_of(const Dsv4ExpertDev *table, int n_table, const int *idx, int k)
     return p->w1 ? p : nullptr;
 }
 
-/* Pass A. h-row hr = k*inter + o. */
-template <int NCH, int R>
+/* The selected experts' tensors, resolved once per workgroup into LDS (the
+ * id lookup and the table read are two dependent loads that would otherwise
+ * sit in front of every weight load). A missing expert has w1 == nullptr. */
+constexpr int MOE_KMAX = 64;
+
+__device__ __forceinline__ void resolve_experts(Dsv4ExpertDev *sx,
+                                                const Dsv4ExpertDev *table,
+                                                int n_table, const int *idx,
+                                                int topk)
+{
+    const int t = threadIdx.x;
+    if (t < topk) {
+        const Dsv4ExpertDev *e = expert_of(table, n_table, idx, t);
+        if (e) sx[t] = *e;
+        else   sx[t] = Dsv4ExpertDev{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    }
+    __syncthreads();
+}
+
+/* Pass A. h-row hr = k*inter + o. A workgroup owns the contiguous h-rows
+ * [row0, row0 + rows_per_wg) and walks them in steps of rg*R; rows wider
+ * than one wave leave per-wave gate/up partials in LDS, summed in wave order
+ * after one barrier, then SwiGLU. */
+template <int NCH, int R, int PF>
 __global__ void __launch_bounds__(256)
 k_moe_gate_up(float *__restrict__ h, const float *__restrict__ x,
               const Dsv4ExpertDev *__restrict__ table, int n_table,
               const int *__restrict__ idx, int topk, int hidden, int inter,
-              float limit, int tc, int tiles_per_wg, int ntiles)
+              float limit, int tc, int rows_per_wg)
 {
-    __shared__ float red[4][2 * R];
+    extern __shared__ float part[];          /* [2][waves per row][rows_per_wg] */
+    __shared__ Dsv4ExpertDev sx[MOE_KMAX];
+    resolve_experts(sx, table, n_table, idx, topk);
     const int tid = threadIdx.x;
     const int g = tid / tc, j = tid - g * tc;
     const int rg = blockDim.x / tc;
     const int ch = hidden >> 5;
-    const int wid = tid >> 6, lane = tid & 63;
+    const int lane = tid & 63;
     const int hrows = topk * inter;
     const size_t rowb = (size_t)hidden / 2, rows_s = (size_t)ch;
+    const int row0 = blockIdx.x * rows_per_wg;
+    const int rend = min(hrows, row0 + rows_per_wg);
+    const int nloc = rend - row0;
+    const int step_rows = rg * R;
+    const int nsteps = (nloc + step_rows - 1) / step_rows;
+    const int wpr = tc > 64 ? tc >> 6 : 1;
 
     float xr[NCH][32];
     bool act[NCH];
@@ -135,45 +167,52 @@ k_moe_gate_up(float *__restrict__ h, const float *__restrict__ x,
         load_x32(xr[n], x + c * 32, act[n]);
     }
 
-    const int t0 = blockIdx.x * tiles_per_wg;
-    const int t1 = min(ntiles, t0 + tiles_per_wg);
-    for (int tile = t0; tile < t1; ++tile) {
-        const int hbase = (tile * rg + g) * R;
-        u32x4 wg_[R][NCH], wu_[R][NCH];
-        float sg[R][NCH], su[R][NCH];
-        bool bad[R];
+    u32x4 wg_[R][NCH], wu_[R][NCH], ng_[R][NCH], nu_[R][NCH];
+    uint32_t sg_[R][NCH], su_[R][NCH], nsg[R][NCH], nsu[R][NCH];
+    bool bad[R];
+
+    auto load = [&](int rbase, u32x4 (*G)[NCH], u32x4 (*U)[NCH],
+                    uint32_t (*SG)[NCH], uint32_t (*SU)[NCH], bool *B) {
 #pragma unroll
         for (int i = 0; i < R; i++) {
-            const int hr = hbase + i;
-            const bool ok = hr < hrows;
+            const int hr = rbase + i;
+            const bool ok = hr < rend;
             const int k = ok ? hr / inter : 0;
             const int o = ok ? hr - k * inter : 0;
-            const Dsv4ExpertDev *e = ok ? expert_of(table, n_table, idx, k) : nullptr;
-            bad[i] = ok && !e;
+            const Dsv4ExpertDev *e = (ok && sx[k].w1) ? &sx[k] : nullptr;
+            if (B) B[i] = ok && !e;
 #pragma unroll
             for (int n = 0; n < NCH; n++) {
                 const int c = j + n * tc;
                 if (e && act[n]) {
-                    wg_[i][n] = ld16_stream(e->w1 + (size_t)o * rowb + (size_t)c * 16);
-                    wu_[i][n] = ld16_stream(e->w3 + (size_t)o * rowb + (size_t)c * 16);
-                    sg[i][n] = dec_e8m0(e->s1[(size_t)o * rows_s + c]);
-                    su[i][n] = dec_e8m0(e->s3[(size_t)o * rows_s + c]);
+                    G[i][n] = ld16_stream(e->w1 + (size_t)o * rowb + (size_t)c * 16);
+                    U[i][n] = ld16_stream(e->w3 + (size_t)o * rowb + (size_t)c * 16);
+                    SG[i][n] = e->s1[(size_t)o * rows_s + c];
+                    SU[i][n] = e->s3[(size_t)o * rows_s + c];
                 } else {
-                    wg_[i][n] = u32x4{0, 0, 0, 0};
-                    wu_[i][n] = u32x4{0, 0, 0, 0};
-                    sg[i][n] = 0.0f;
-                    su[i][n] = 0.0f;
+                    G[i][n] = u32x4{0, 0, 0, 0};
+                    U[i][n] = u32x4{0, 0, 0, 0};
+                    SG[i][n] = 0u;
+                    SU[i][n] = 0u;
                 }
             }
         }
+    };
+
+    if (nsteps > 0) load(row0 + g * R, wg_, wu_, sg_, su_, bad);
+    for (int step = 0; step < nsteps; ++step) {
+        const int rbase = row0 + step * step_rows + g * R;
+        bool nbad[R];
+        if (PF && step + 1 < nsteps) load(rbase + step_rows, ng_, nu_, nsg, nsu, nbad);
+
         float ag[R], au[R];
 #pragma unroll
         for (int i = 0; i < R; i++) {
             float a = 0.0f, b = 0.0f;
 #pragma unroll
             for (int n = 0; n < NCH; n++) {
-                a = fmaf(dot32(wg_[i][n], xr[n]), sg[i][n], a);
-                b = fmaf(dot32(wu_[i][n], xr[n]), su[i][n], b);
+                a = fmaf(dot32(wg_[i][n], xr[n]), dec_e8m0(sg_[i][n]), a);
+                b = fmaf(dot32(wu_[i][n], xr[n]), dec_e8m0(su_[i][n]), b);
             }
             ag[i] = a; au[i] = b;
         }
@@ -182,182 +221,223 @@ k_moe_gate_up(float *__restrict__ h, const float *__restrict__ x,
             for (int i = 0; i < R; i++) {
                 const float gs = seg_sum_rt(ag[i], tc);
                 const float us = seg_sum_rt(au[i], tc);
-                const int hr = hbase + i;
-                if (j == tc - 1 && hr < hrows)
+                const int hr = rbase + i;
+                if (j == tc - 1 && hr < rend)
                     h[hr] = bad[i] ? __builtin_nanf("") : swiglu1(gs, us, limit);
             }
         } else {
-            const int wpr = tc >> 6;
+            const int w = j >> 6;
 #pragma unroll
             for (int i = 0; i < R; i++) {
                 const float gs = seg_sum<64>(ag[i]);
                 const float us = seg_sum<64>(au[i]);
-                if (lane == 63) { red[wid][2 * i] = gs; red[wid][2 * i + 1] = us; }
-            }
-            __syncthreads();
-            if (tid < rg * R) {
-                const int gg = tid / R, ii = tid - gg * R;
-                const int hr = (tile * rg + gg) * R + ii;
-                float gs = red[gg * wpr][2 * ii], us = red[gg * wpr][2 * ii + 1];
-                for (int w = 1; w < wpr; w++) {
-                    gs += red[gg * wpr + w][2 * ii];
-                    us += red[gg * wpr + w][2 * ii + 1];
-                }
-                if (hr < hrows) {
-                    const int k = hr / inter;
-                    const bool b = !expert_of(table, n_table, idx, k);
-                    h[hr] = b ? __builtin_nanf("") : swiglu1(gs, us, limit);
+                const int rl = rbase + i - row0;
+                if (lane == 63 && rl < nloc) {
+                    part[(0 * wpr + w) * rows_per_wg + rl] = gs;
+                    part[(1 * wpr + w) * rows_per_wg + rl] = us;
                 }
             }
-            __syncthreads();
+        }
+        if (PF) {
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                bad[i] = nbad[i];
+#pragma unroll
+                for (int n = 0; n < NCH; n++) {
+                    wg_[i][n] = ng_[i][n]; wu_[i][n] = nu_[i][n];
+                    sg_[i][n] = nsg[i][n]; su_[i][n] = nsu[i][n];
+                }
+            }
+        } else if (step + 1 < nsteps) {
+            load(rbase + step_rows, wg_, wu_, sg_, su_, bad);
+        }
+    }
+
+    if (tc > 64) {
+        __syncthreads();
+        for (int rl = tid; rl < nloc; rl += blockDim.x) {
+            float gs = part[rl], us = part[wpr * rows_per_wg + rl];
+            for (int w = 1; w < wpr; w++) {
+                gs += part[w * rows_per_wg + rl];
+                us += part[(wpr + w) * rows_per_wg + rl];
+            }
+            const int hr = row0 + rl;
+            const int k = hr / inter;
+            h[hr] = sx[k].w1 ? swiglu1(gs, us, limit) : __builtin_nanf("");
         }
     }
 }
 
-/* Pass B. Row dr = k*hidden + i; x = h[k]. */
+/* Pass B + C. A workgroup owns the output rows [row0, row0 + rg*R) (one
+ * step); it walks the experts in k order with the next expert's weights and
+ * h slice in flight while the current one is reduced, keeping acc_k in LDS;
+ * then out[i] = ((0 + w0*acc0) + w1*acc1) + ... in k order, each multiply
+ * and add rounded separately (dsv4_layer.c:471-475). */
 template <int NCH, int R>
 __global__ void __launch_bounds__(256)
-k_moe_down(float *__restrict__ acc, const float *__restrict__ h,
+k_moe_down(float *__restrict__ out, const float *__restrict__ h,
            const Dsv4ExpertDev *__restrict__ table, int n_table,
-           const int *__restrict__ idx, int topk, int hidden, int inter,
-           int tc, int tiles_per_wg, int ntiles, int tiles_per_expert)
+           const int *__restrict__ idx, const float *__restrict__ wts,
+           int topk, int hidden, int inter, int tc)
 {
-    __shared__ float red[4][R];
+    extern __shared__ float accl[];          /* [topk][waves per row][rows_per_wg] */
+    __shared__ Dsv4ExpertDev sx[MOE_KMAX];
+    resolve_experts(sx, table, n_table, idx, topk);
     const int tid = threadIdx.x;
     const int g = tid / tc, j = tid - g * tc;
     const int rg = blockDim.x / tc;
     const int ch = inter >> 5;
-    const int wid = tid >> 6, lane = tid & 63;
+    const int lane = tid & 63;
     const size_t rowb = (size_t)inter / 2, rows_s = (size_t)ch;
+    const int rows_per_wg = rg * R;
+    const int row0 = blockIdx.x * rows_per_wg;
+    const int rend = min(hidden, row0 + rows_per_wg);
+    const int nloc = rend - row0;
+    const int rbase = row0 + g * R;
+    const int wpr = tc > 64 ? tc >> 6 : 1;
+    const float nanv = __builtin_nanf("");
 
-    float xr[NCH][32];
     bool act[NCH];
 #pragma unroll
     for (int n = 0; n < NCH; n++) act[n] = j + n * tc < ch;
-    int cur_k = -1;
-    const Dsv4ExpertDev *e = nullptr;
 
-    const int t0 = blockIdx.x * tiles_per_wg;
-    const int t1 = min(ntiles, t0 + tiles_per_wg);
-    for (int tile = t0; tile < t1; ++tile) {
-        const int k = tile / tiles_per_expert;
-        const int tt = tile - k * tiles_per_expert;
-        if (k != cur_k) {
-            cur_k = k;
-            e = expert_of(table, n_table, idx, k);
+    float xr[NCH][32], nx[NCH][32];
+    u32x4 wv[R][NCH], nw[R][NCH];
+    uint32_t sv[R][NCH], ns[R][NCH];
+
+    auto load = [&](int k, float (*X)[32], u32x4 (*Wv)[NCH], uint32_t (*Sv)[NCH]) {
+        const Dsv4ExpertDev *e = sx[k].w1 ? &sx[k] : nullptr;
 #pragma unroll
-            for (int n = 0; n < NCH; n++) {
-                const int c = j + n * tc;
-                load_x32(xr[n], h + (size_t)k * inter + c * 32, act[n]);
-            }
-        }
-        const int ibase = (tt * rg + g) * R;
-        u32x4 wv[R][NCH];
-        float sv[R][NCH];
+        for (int n = 0; n < NCH; n++)
+            load_x32(X[n], h + (size_t)k * inter + (j + n * tc) * 32, act[n]);
 #pragma unroll
         for (int i = 0; i < R; i++) {
-            const int r = ibase + i;
+            const int r = rbase + i;
 #pragma unroll
             for (int n = 0; n < NCH; n++) {
                 const int c = j + n * tc;
-                if (e && act[n] && r < hidden) {
-                    wv[i][n] = ld16_stream(e->w2 + (size_t)r * rowb + (size_t)c * 16);
-                    sv[i][n] = dec_e8m0(e->s2[(size_t)r * rows_s + c]);
+                if (e && act[n] && r < rend) {
+                    Wv[i][n] = ld16_stream(e->w2 + (size_t)r * rowb + (size_t)c * 16);
+                    Sv[i][n] = e->s2[(size_t)r * rows_s + c];
                 } else {
-                    wv[i][n] = u32x4{0, 0, 0, 0};
-                    sv[i][n] = 0.0f;
+                    Wv[i][n] = u32x4{0, 0, 0, 0};
+                    Sv[i][n] = 0u;
                 }
             }
         }
-        float a[R];
+    };
+
+    load(0, xr, wv, sv);
+    for (int k = 0; k < topk; k++) {
+        if (k + 1 < topk) load(k + 1, nx, nw, ns);
+        const bool ek = sx[k].w1 != nullptr;
 #pragma unroll
         for (int i = 0; i < R; i++) {
-            float s = 0.0f;
+            float a = 0.0f;
 #pragma unroll
-            for (int n = 0; n < NCH; n++) s = fmaf(dot32(wv[i][n], xr[n]), sv[i][n], s);
-            a[i] = s;
+            for (int n = 0; n < NCH; n++)
+                a = fmaf(dot32(wv[i][n], xr[n]), dec_e8m0(sv[i][n]), a);
+            const int rl = rbase + i - row0;
+            if (tc <= 64) {
+                const float v = seg_sum_rt(a, tc);
+                if (j == tc - 1 && rl < nloc)
+                    accl[(size_t)k * rows_per_wg + rl] = ek ? v : nanv;
+            } else {
+                const float v = seg_sum<64>(a);
+                if (lane == 63 && rl < nloc)
+                    accl[((size_t)k * wpr + (j >> 6)) * rows_per_wg + rl] = ek ? v : nanv;
+            }
         }
-        const float nanv = __builtin_nanf("");
-        if (tc <= 64) {
 #pragma unroll
-            for (int i = 0; i < R; i++) {
-                const float v = seg_sum_rt(a[i], tc);
-                const int r = ibase + i;
-                if (j == tc - 1 && r < hidden)
-                    acc[(size_t)k * hidden + r] = e ? v : nanv;
-            }
-        } else {
-            const int wpr = tc >> 6;
+        for (int n = 0; n < NCH; n++)
 #pragma unroll
-            for (int i = 0; i < R; i++) {
-                const float v = seg_sum<64>(a[i]);
-                if (lane == 63) red[wid][i] = v;
-            }
-            __syncthreads();
-            if (tid < rg * R) {
-                const int gg = tid / R, ii = tid - gg * R;
-                const int r = (tt * rg + gg) * R + ii;
-                float s = red[gg * wpr][ii];
-                for (int w = 1; w < wpr; w++) s += red[gg * wpr + w][ii];
-                if (r < hidden) acc[(size_t)k * hidden + r] = e ? s : nanv;
-            }
-            __syncthreads();
+            for (int q = 0; q < 32; q++) xr[n][q] = nx[n][q];
+#pragma unroll
+        for (int i = 0; i < R; i++)
+#pragma unroll
+            for (int n = 0; n < NCH; n++) { wv[i][n] = nw[i][n]; sv[i][n] = ns[i][n]; }
+    }
+    __syncthreads();
+    for (int rl = tid; rl < nloc; rl += blockDim.x) {
+        float o = 0.0f;
+        for (int k = 0; k < topk; k++) {
+            float a = accl[((size_t)k * wpr) * rows_per_wg + rl];
+            for (int w = 1; w < wpr; w++) a += accl[((size_t)k * wpr + w) * rows_per_wg + rl];
+            const float p = wts[k] * a;
+            o = o + p;
         }
+        out[row0 + rl] = o;
     }
 }
 
-/* Pass C: dsv4_layer.c:471-475, in k order, no fused multiply-add. */
-__global__ void __launch_bounds__(256)
-k_moe_combine(float *__restrict__ out, const float *__restrict__ acc,
-              const float *__restrict__ w, int topk, int hidden)
+int g_moe_cus = 0;
+
+int moe_env(const char *name, int dflt)
 {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= hidden) return;
-    float o = 0.0f;
-    for (int k = 0; k < topk; k++) {
-        const float p = w[k] * acc[(size_t)k * hidden + i];
-        o = o + p;
-    }
-    out[i] = o;
+    const char *e = getenv(name);
+    return e ? atoi(e) : dflt;
 }
 
-template <int NCH, int R>
-void launch_a(const Fp4Geom &g, float *h, const float *x,
-              const Dsv4ExpertDev *table, int n_table, const int *idx,
-              int topk, int hidden, int inter, float limit, hipStream_t st)
+int moe_cus()
 {
-    const int per = g.rg * R;
+    if (!g_moe_cus) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        g_moe_cus = n;
+    }
+    return g_moe_cus;
+}
+
+/* Rows per workgroup: about `wpc` workgroups per CU over `rows` rows walked
+ * in steps of `step`, capped so the per-row LDS fits. */
+int rows_per_wg_for(int rows, int step, int wpc, size_t lds_per_row, size_t lds_cap)
+{
+    const int nsteps = (rows + step - 1) / step;
+    const int want = wpc * moe_cus();
+    int spw = (nsteps + want - 1) / want;
+    if (spw < 1) spw = 1;
+    if (lds_per_row) {
+        const int max_rows = (int)(lds_cap / lds_per_row);
+        const int max_spw = max_rows / step;
+        if (max_spw < 1) return -1;
+        if (spw > max_spw) spw = max_spw;
+    }
+    return spw * step;
+}
+
+template <int NCH, int R, int PF>
+int launch_a(const Fp4Geom &g, float *h, const float *x,
+             const Dsv4ExpertDev *table, int n_table, const int *idx,
+             int topk, int hidden, int inter, float limit, int wpc,
+             hipStream_t st)
+{
     const int hrows = topk * inter;
-    const int ntiles = (hrows + per - 1) / per;
-    const int want = ntiles < 2048 ? ntiles : 2048;
-    const int tpw = (ntiles + want - 1) / want;
-    const int grid = (ntiles + tpw - 1) / tpw;
-    hipLaunchKernelGGL((k_moe_gate_up<NCH, R>), dim3(grid), dim3(g.wg), 0, st,
-                       h, x, table, n_table, idx, topk, hidden, inter, limit,
-                       g.tc, tpw, ntiles);
+    const int wpr = g.tc > 64 ? g.tc / 64 : 1;
+    const size_t per_row = g.tc > 64 ? 2 * sizeof(float) * wpr : 0;
+    const int rpw = rows_per_wg_for(hrows, g.rg * R, wpc, per_row, 32 * 1024);
+    if (rpw <= 0) return -1;
+    const int grid = (hrows + rpw - 1) / rpw;
+    hipLaunchKernelGGL((k_moe_gate_up<NCH, R, PF>), dim3(grid), dim3(g.wg),
+                       per_row * rpw, st, h, x, table, n_table, idx, topk, hidden,
+                       inter, limit, g.tc, rpw);
+    return 0;
 }
 
 template <int NCH, int R>
-void launch_b(const Fp4Geom &g, float *acc, const float *h,
-              const Dsv4ExpertDev *table, int n_table, const int *idx,
-              int topk, int hidden, int inter, hipStream_t st)
+int launch_b(const Fp4Geom &g, float *out, const float *h,
+             const Dsv4ExpertDev *table, int n_table, const int *idx,
+             const float *w, int topk, int hidden, int inter, hipStream_t st)
 {
-    const int per = g.rg * R;
-    const int tpe = (hidden + per - 1) / per;
-    const int ntiles = tpe * topk;
-    const int want = ntiles < 2048 ? ntiles : 2048;
-    const int tpw = (ntiles + want - 1) / want;
-    const int grid = (ntiles + tpw - 1) / tpw;
-    hipLaunchKernelGGL((k_moe_down<NCH, R>), dim3(grid), dim3(g.wg), 0, st,
-                       acc, h, table, n_table, idx, topk, hidden, inter, g.tc,
-                       tpw, ntiles, tpe);
-}
-
-int pick_r(int rows, int rg)
-{
-    for (int cand = 4; cand >= 2; cand >>= 1)
-        if ((rows + rg * cand - 1) / (rg * cand) >= 2048) return cand;
-    return 1;
+    const int wpr = g.tc > 64 ? g.tc / 64 : 1;
+    const int rpw = g.rg * R;
+    const size_t lds = sizeof(float) * (size_t)topk * wpr * rpw;
+    const int grid = (hidden + rpw - 1) / rpw;
+    hipLaunchKernelGGL((k_moe_down<NCH, R>), dim3(grid), dim3(g.wg), lds, st, out,
+                       h, table, n_table, idx, w, topk, hidden, inter, g.tc);
+    return 0;
 }
 
 } // namespace
@@ -368,36 +448,44 @@ int dsv4_moe_fp4_launch(float *d_out, const float *d_x,
                         int hidden, int inter, float limit, float *hbuf,
                         float *accbuf, hipStream_t st)
 {
+    (void)accbuf;
     Fp4Geom ga, gb;
-    if (topk <= 0 || !fp4_geom(hidden, &ga) || !fp4_geom(inter, &gb)) {
+    if (topk <= 0 || topk > MOE_KMAX || !fp4_geom(hidden, &ga) || !fp4_geom(inter, &gb)) {
         DSV4_ERR("moe: unsupported shape hidden %d inter %d topk %d "
-                 "(need multiples of 32, at most 16384)", hidden, inter, topk);
+                 "(need multiples of 32, at most 16384, topk <= 64)", hidden, inter, topk);
         return -1;
     }
-    const int ra = pick_r(topk * inter, ga.rg);
+    /* Launch shape (no effect on the arithmetic of a row): rows per thread,
+     * prefetch, workgroups per CU; defaults from a sweep at the C3 shape. */
+    const int ra = moe_env("DSV4_GPU_MOE_RA", 2) >= 2 ? 2 : 1;
+    const int pf = moe_env("DSV4_GPU_MOE_PF", 0) ? 1 : 0;
+    const int wa = moe_env("DSV4_GPU_MOE_WA", 2);
+    const int rbv = moe_env("DSV4_GPU_MOE_RB", 2);
+    const int rb = rbv >= 4 ? 4 : rbv >= 2 ? 2 : 1;
+    int rc;
     if (ga.nch == 1) {
-        if (ra == 4) launch_a<1, 4>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, st);
-        else if (ra == 2) launch_a<1, 2>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, st);
-        else launch_a<1, 1>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, st);
+        if (ra == 2) rc = pf ? launch_a<1, 2, 1>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st)
+                             : launch_a<1, 2, 0>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st);
+        else         rc = pf ? launch_a<1, 1, 1>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st)
+                             : launch_a<1, 1, 0>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st);
     } else {
-        if (ra == 4) launch_a<2, 4>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, st);
-        else if (ra == 2) launch_a<2, 2>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, st);
-        else launch_a<2, 1>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, st);
+        if (ra == 2) rc = pf ? launch_a<2, 2, 1>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st)
+                             : launch_a<2, 2, 0>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st);
+        else         rc = pf ? launch_a<2, 1, 1>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st)
+                             : launch_a<2, 1, 0>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st);
     }
+    if (rc != 0) { DSV4_ERR("moe: gate/up shape does not fit"); return -1; }
     HIP_OK(hipGetLastError(), "moe gate/up launch");
-    const int rb = pick_r(topk * hidden, gb.rg);
     if (gb.nch == 1) {
-        if (rb == 4) launch_b<1, 4>(gb, accbuf, hbuf, d_table, n_table, d_idx, topk, hidden, inter, st);
-        else if (rb == 2) launch_b<1, 2>(gb, accbuf, hbuf, d_table, n_table, d_idx, topk, hidden, inter, st);
-        else launch_b<1, 1>(gb, accbuf, hbuf, d_table, n_table, d_idx, topk, hidden, inter, st);
+        if (rb == 4) rc = launch_b<1, 4>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
+        else if (rb == 2) rc = launch_b<1, 2>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
+        else rc = launch_b<1, 1>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
     } else {
-        if (rb == 4) launch_b<2, 4>(gb, accbuf, hbuf, d_table, n_table, d_idx, topk, hidden, inter, st);
-        else if (rb == 2) launch_b<2, 2>(gb, accbuf, hbuf, d_table, n_table, d_idx, topk, hidden, inter, st);
-        else launch_b<2, 1>(gb, accbuf, hbuf, d_table, n_table, d_idx, topk, hidden, inter, st);
+        if (rb == 4) rc = launch_b<2, 4>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
+        else if (rb == 2) rc = launch_b<2, 2>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
+        else rc = launch_b<2, 1>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
     }
+    if (rc != 0) { DSV4_ERR("moe: down shape does not fit"); return -1; }
     HIP_OK(hipGetLastError(), "moe down launch");
-    hipLaunchKernelGGL(k_moe_combine, dim3((hidden + 255) / 256), dim3(256), 0,
-                       st, d_out, accbuf, d_w, topk, hidden);
-    HIP_OK(hipGetLastError(), "moe combine launch");
     return 0;
 }

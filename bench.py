@@ -52,6 +52,21 @@ def moe_bytes(hidden, inter, topk):
     return topk * per + hidden * 2 + hidden * 4 + topk * 8
 
 
+def lm_head_traffic():
+    """HBM bytes per LM-head GEMV launch (FETCH_SIZE + WRITE_SIZE, calibrated
+    against a copy of known size), from the committed rocprofv3 summary; None
+    when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -60,8 +75,10 @@ def parse():
     ap.add_argument("--no-detail", action="store_true",
                     help="headline sweep only (skip C1/C3/C4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4"], default=None,
-                    help="time one configuration only (for profiling runs)")
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "copy"], default=None,
+                    help="time one configuration only (for profiling runs); "
+                         "'copy' runs a plain 1 GiB device-to-device copy whose "
+                         "known size calibrates the FETCH_SIZE/WRITE_SIZE counters")
     return ap.parse_args()
 
 
@@ -270,6 +287,26 @@ class Bench:
         del d_codes, d_s, d_kv
         return us, eager, alg
 
+    # ------------------------------------------------ counter calibration
+    def copy_run(self, steps):
+        """A plain device-to-device copy of 1 GiB (torch's copy kernel): the
+        FETCH_SIZE and WRITE_SIZE counters of a dispatch that reads and writes
+        exactly this many bytes give the factor that turns counter readings
+        into HBM bytes."""
+        torch = self.torch
+        n = 1 << 30
+        a = torch.empty(n, dtype=torch.uint8, device=self.dev)
+        a.fill_(1)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        e0, e1 = self.ev(), self.ev()
+        e0.record(self.stream)
+        for _ in range(max(1, steps)):
+            b.copy_(a)
+        e1.record(self.stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / max(1, steps), n
+
     # ------------------------------------------------------ CPU baseline
     def cpu_baseline(self):
         """The compiled reference dsv4_matmul_fp8 (OpenMP + AVX2) over the same
@@ -310,6 +347,20 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     B = Bench()
+    if args.only == "copy":
+        us, nbytes = B.copy_run(args.steps)
+        print(json.dumps({"config": "copy", "bytes_read": nbytes,
+                          "bytes_written": nbytes, "us": round(us, 3),
+                          "GBps_rw": round(2 * nbytes / us / 1e3, 1)}))
+        return
+    if args.only == "c2":
+        B.c2_setup()
+        step_ms, eager_ms, per_ms = B.c2_run(args.steps, args.warmup)
+        print(json.dumps({"config": "c2", "graph_ms": round(step_ms, 4),
+                          "eager_ms": round(eager_ms, 4),
+                          "per_shape_us": [round(m * 1e3, 3) for m in per_ms]}))
+        B.L.dsv4_gpu_shutdown()
+        return
     if args.only in ("c1", "c3", "c4"):
         fn = {"c1": B.c1_run, "c3": B.c3_run, "c4": B.c4_run}[args.only]
         us, eager, alg = fn(args.steps, args.warmup)
@@ -334,13 +385,7 @@ def main():
     trunk_us = sum(per_ms[:5]) * 1e3
     lm_ms = per_ms[5]
     lm_gbs = algs[5] / (lm_ms * 1e-3) / 1e9
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", "fp8_gemv_lm_head_traffic.json")
-    if os.path.exists(tf):
-        try:
-            traffic = json.load(open(tf)).get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+    traffic = lm_head_traffic()
     detail = {}
 
     def rec(us, eager, alg):

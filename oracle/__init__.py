@@ -100,6 +100,9 @@ def ref():
                   "dsv4_matmul_fp4", "dsv4_matmul_fp4_scalar"):
             getattr(L, n).argtypes = [_f32p, _f32p, _u8p, _u8p, ctypes.c_int,
                                       ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.dsv4_matmul_fp8_n.argtypes = [_f32p, _f32p, _u8p, _u8p, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int]
         L.dsv4_swiglu.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_float]
         L.dsv4_indexer_score.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int,
                                          ctypes.c_int, ctypes.c_int]
@@ -246,6 +249,17 @@ def ref_matmul_fp8(x, W, S_e8m0, blk_r=128, blk_c=128, scalar=False):
     y = np.empty(out, np.float32)
     fn = ref().dsv4_matmul_fp8_scalar if scalar else ref().dsv4_matmul_fp8
     fn(_p(y, _f32p), _p(x, _f32p), _p(W, _u8p), _p(S, _u8p), inn, out, blk_r, blk_c)
+    return y
+
+
+def ref_matmul_fp8_n(x, W, S_e8m0, blk_r=128, blk_c=128):
+    """The reference's batched dsv4_matmul_fp8_n: x [nt][in] -> y [nt][out]."""
+    W = _u8(W); x = _f32(x); S = _u8(S_e8m0)
+    out, inn = W.shape
+    nt = x.shape[0]
+    y = np.empty((nt, out), np.float32)
+    ref().dsv4_matmul_fp8_n(_p(y, _f32p), _p(x, _f32p), _p(W, _u8p), _p(S, _u8p),
+                            inn, out, blk_r, blk_c, nt)
     return y
 
 

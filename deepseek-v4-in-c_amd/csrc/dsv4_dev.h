@@ -64,6 +64,22 @@ __device__ __forceinline__ void dec_fp4x8(uint32_t v, float *o)
     dec_fp4x2<3>(v, o + 6);
 }
 
+/* ------------------------------------------------------------- SwiGLU */
+
+/* dsv4_swiglu for one element (dsv4_ops.c:60-78): up clamped to [-L, L],
+ * gate clamped above only, silu(g) = g / (1 + expf(-g)). */
+__device__ __forceinline__ float swiglu1(float g, float u, float limit)
+{
+    if (limit > 0.0f) {
+        if (u > limit) u = limit;
+        if (u < -limit) u = -limit;
+        if (g > limit) g = limit;
+        const float s = g / (1.0f + expf(-g));
+        return s * u;
+    }
+    return (g / (1.0f + expf(-g))) * u;
+}
+
 /* ----------------------------------------------------------- reductions */
 
 /* DPP control codes (GCN/CDNA "dpp_ctrl"). */
@@ -135,6 +151,22 @@ __device__ __forceinline__ u32x4 ld16(const void *p)
 __device__ __forceinline__ u32x4 ld16_stream(const void *p)
 {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+}
+
+/* The same loads through a global-address-space pointer. Pointers read from
+ * memory (an expert table) are generic to the compiler, which would emit
+ * flat loads; those also count against lgkmcnt, so any LDS wait in the loop
+ * would wait for every weight load in flight. */
+#define DSV4_GLOBAL __attribute__((address_space(1)))
+
+__device__ __forceinline__ u32x4 ldg16_stream(const void *p)
+{
+    return __builtin_nontemporal_load((const DSV4_GLOBAL u32x4 *)p);
+}
+
+__device__ __forceinline__ uint32_t ldg8(const uint8_t *p)
+{
+    return *(const DSV4_GLOBAL uint8_t *)p;
 }
 
 __device__ __forceinline__ f32x4 ldf4(const float *p)

@@ -58,7 +58,7 @@ hipStream_t g_stream = nullptr;
 std::vector<Res> g_res;
 std::vector<LayerExperts> g_layers;
 Arena g_ar;
-Scratch g_moe_h, g_moe_acc, g_attn, g_scores;
+Scratch g_moe, g_attn, g_scores;
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -88,6 +88,9 @@ int scratch_reserve(Scratch &s, size_t bytes)
     s.p = nullptr;
     s.cap = 0;
     HIP_OK(hipMalloc(&s.p, bytes), "hipMalloc scratch");
+    /* Kernels that keep arrival counters in their scratch expect zeros on
+     * first use (and leave zeros behind). */
+    HIP_OK(hipMemset(s.p, 0, bytes), "hipMemset scratch");
     s.cap = bytes;
     return 0;
 }
@@ -364,7 +367,7 @@ void dsv4_gpu_shutdown(void)
         if (L.dev) (void)hipFree(L.dev);
     }
     g_layers.clear();
-    for (Scratch *s : {&g_moe_h, &g_moe_acc, &g_attn, &g_scores}) {
+    for (Scratch *s : {&g_moe, &g_attn, &g_scores}) {
         if (s->p) (void)hipFree(s->p);
         s->p = nullptr;
         s->cap = 0;
@@ -525,8 +528,7 @@ static int moe_prepare(int layer, int topk, int hidden, int inter,
         return -1;
     }
     if (layer_sync(L) != 0) return -1;
-    if (scratch_reserve(g_moe_h, (size_t)topk * inter * sizeof(float)) != 0 ||
-        scratch_reserve(g_moe_acc, (size_t)topk * hidden * sizeof(float)) != 0)
+    if (scratch_reserve(g_moe, dsv4_moe_scratch_bytes(topk, hidden, inter)) != 0)
         return -1;
     *out = &L;
     return 0;
@@ -554,8 +556,8 @@ int dsv4_gpu_moe_fp4(float *out, const float *x, int layer, const int *idx,
     if (dsv4_moe_fp4_launch((float *)(g_ar.d + oo), (const float *)(g_ar.d + xo),
                             L->dev, (int)L->host.size(),
                             (const int *)(g_ar.d + io), (const float *)(g_ar.d + wo),
-                            topk, hidden, inter, swiglu_limit, (float *)g_moe_h.p,
-                            (float *)g_moe_acc.p, g_stream) != 0)
+                            topk, hidden, inter, swiglu_limit, g_moe.p,
+                            g_stream) != 0)
         return -1;
     return stage_pull(oo, (size_t)hidden * sizeof(float), out);
 }
@@ -568,8 +570,7 @@ int dsv4_gpu_moe_fp4_d(float *d_out, const float *d_x, int layer,
     if (moe_prepare(layer, topk, hidden, inter, &L) != 0) return -1;
     return dsv4_moe_fp4_launch(d_out, d_x, L->dev, (int)L->host.size(), d_idx,
                                d_w, topk, hidden, inter, swiglu_limit,
-                               (float *)g_moe_h.p, (float *)g_moe_acc.p,
-                               as_stream(stream));
+                               g_moe.p, as_stream(stream));
 }
 
 /* ------------------------------------------------------------ KV stores */

@@ -43,14 +43,27 @@ struct Dsv4ExpertDev {
     const uint8_t *w1, *s1, *w3, *s3, *w2, *s2;
 };
 
-/* Routed MoE on the device. experts: device array [n_table] of expert
- * tensors for this layer; d_idx/d_w device [topk]; hbuf device scratch
- * [topk][inter] f32; accbuf device scratch [topk][hidden] f32. */
+/* Device scratch dsv4_moe_fp4_launch needs, in bytes (0: shape not
+ * supported). */
+size_t dsv4_moe_scratch_bytes(int topk, int hidden, int inter);
+
+/* Routed MoE on the device. d_table: device array [n_table] of expert
+ * tensors for this layer; d_idx/d_w device [topk]; scratch of
+ * dsv4_moe_scratch_bytes. Picks the matrix-core form (dsv4_moe_mx.hip) when
+ * hidden and inter are multiples of 128, else the VALU form (dsv4_moe.hip).
+ * Calls that overlap on one scratch buffer race. */
 int dsv4_moe_fp4_launch(float *d_out, const float *d_x,
                         const Dsv4ExpertDev *d_table, int n_table,
                         const int *d_idx, const float *d_w, int topk,
-                        int hidden, int inter, float limit, float *hbuf,
-                        float *accbuf, hipStream_t st);
+                        int hidden, int inter, float limit, void *scratch,
+                        hipStream_t st);
+
+/* The VALU form; hbuf is device scratch [topk][inter] f32. */
+int dsv4_moe_fp4_valu_launch(float *d_out, const float *d_x,
+                             const Dsv4ExpertDev *d_table, int n_table,
+                             const int *d_idx, const float *d_w, int topk,
+                             int hidden, int inter, float limit, float *hbuf,
+                             hipStream_t st);
 
 int dsv4_indexer_score_launch(float *d_out, const float *d_q, const float *d_w,
                               int H, int D, const void *d_keys,

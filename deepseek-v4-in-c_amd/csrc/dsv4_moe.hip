@@ -1,5 +1,10 @@
 /* SPDX-License-Identifier: Apache-2.0 */
-/* dsv4_moe.hip - fused MXFP4 routed-expert matvec on gfx950.
+/* dsv4_moe.hip - fused MXFP4 routed-expert matvec on gfx950, VALU form.
+ *
+ * This is the general path, for any hidden / inter that are multiples of 32:
+ * it decodes the nibbles with v_cvt_scalef32_pk_f32_fp4 and accumulates with
+ * fp32 FMAs. Shapes that are multiples of 128 take the matrix-core form in
+ * dsv4_moe_mx.hip instead, which the launcher there selects.
  *
  * Computes the routed half of the reference's moe() for one token
  * (src/model/dsv4_layer.c:380, :412-476): for each selected expert k,
@@ -88,19 +93,6 @@ __device__ __forceinline__ void load_x32(float *xr, const float *x, bool ok)
     }
 }
 
-/* dsv4_swiglu for one element (dsv4_ops.c:60-78): up clamped to [-L, L],
- * gate clamped above only, silu(g) = g / (1 + expf(-g)). */
-__device__ __forceinline__ float swiglu1(float g, float u, float limit)
-{
-    if (limit > 0.0f) {
-        if (u > limit) u = limit;
-        if (u < -limit) u = -limit;
-        if (g > limit) g = limit;
-        const float s = g / (1.0f + expf(-g));
-        return s * u;
-    }
-    return (g / (1.0f + expf(-g))) * u;
-}
 
 __device__ __forceinline__ const Dsv4ExpertDev *
 expert_of(const Dsv4ExpertDev *table, int n_table, const int *idx, int k)
@@ -185,10 +177,10 @@ k_moe_gate_up(float *__restrict__ h, const float *__restrict__ x,
             for (int n = 0; n < NCH; n++) {
                 const int c = j + n * tc;
                 if (e && act[n]) {
-                    G[i][n] = ld16_stream(e->w1 + (size_t)o * rowb + (size_t)c * 16);
-                    U[i][n] = ld16_stream(e->w3 + (size_t)o * rowb + (size_t)c * 16);
-                    SG[i][n] = e->s1[(size_t)o * rows_s + c];
-                    SU[i][n] = e->s3[(size_t)o * rows_s + c];
+                    G[i][n] = ldg16_stream(e->w1 + (size_t)o * rowb + (size_t)c * 16);
+                    U[i][n] = ldg16_stream(e->w3 + (size_t)o * rowb + (size_t)c * 16);
+                    SG[i][n] = ldg8(e->s1 + (size_t)o * rows_s + c);
+                    SU[i][n] = ldg8(e->s3 + (size_t)o * rows_s + c);
                 } else {
                     G[i][n] = u32x4{0, 0, 0, 0};
                     U[i][n] = u32x4{0, 0, 0, 0};
@@ -317,8 +309,8 @@ k_moe_down(float *__restrict__ out, const float *__restrict__ h,
             for (int n = 0; n < NCH; n++) {
                 const int c = j + n * tc;
                 if (e && act[n] && r < rend) {
-                    Wv[i][n] = ld16_stream(e->w2 + (size_t)r * rowb + (size_t)c * 16);
-                    Sv[i][n] = e->s2[(size_t)r * rows_s + c];
+                    Wv[i][n] = ldg16_stream(e->w2 + (size_t)r * rowb + (size_t)c * 16);
+                    Sv[i][n] = ldg8(e->s2 + (size_t)r * rows_s + c);
                 } else {
                     Wv[i][n] = u32x4{0, 0, 0, 0};
                     Sv[i][n] = 0u;
@@ -367,6 +359,78 @@ k_moe_down(float *__restrict__ out, const float *__restrict__ h,
             o = o + p;
         }
         out[row0 + rl] = o;
+    }
+}
+
+/* Pass B + combine, wave per expert slot. A workgroup owns the output rows
+ * [r0, r0 + RB); wave w takes slots k = w, w + nwaves, ...: its 32*NCH
+ * elements of h_k stay in VGPRs, it requests all RB rows of w2_k (one 1 KB
+ * contiguous load per row and chunk) before reducing any of them, and each
+ * row's dot lands in LDS. Then out[i] = ((0 + w0*acc0[i]) + w1*acc1[i]) + ...
+ * in k order, each multiply and add rounded separately (dsv4_layer.c:
+ * 471-475). */
+template <int NCH, int RB>
+__global__ void __launch_bounds__(512)
+k_moe_down_w(float *__restrict__ out, const float *__restrict__ h,
+             const Dsv4ExpertDev *__restrict__ table, int n_table,
+             const int *__restrict__ idx, const float *__restrict__ wts,
+             int topk, int hidden, int inter)
+{
+    __shared__ float accl[MOE_KMAX][RB];
+    const int r0 = blockIdx.x * RB;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int nw = blockDim.x >> 6;
+    const int ch = inter >> 5;
+    const size_t rowb = (size_t)inter / 2, rows_s = (size_t)ch;
+
+    for (int k = w; k < topk; k += nw) {
+        const int e = idx[k];
+        const Dsv4ExpertDev E = (e >= 0 && e < n_table)
+            ? table[e] : Dsv4ExpertDev{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+        if (!E.w1) {
+            for (int i = lane; i < RB; i += 64) accl[k][i] = __builtin_nanf("");
+            continue;
+        }
+        bool act[NCH];
+#pragma unroll
+        for (int n = 0; n < NCH; n++) act[n] = lane + 64 * n < ch;
+        u32x4 wv[RB][NCH];
+        uint32_t sv[RB][NCH];
+#pragma unroll
+        for (int i = 0; i < RB; i++) {
+            const int r = r0 + i;
+#pragma unroll
+            for (int n = 0; n < NCH; n++) {
+                const int c = lane + 64 * n;
+                const bool ok = act[n] && r < hidden;
+                wv[i][n] = ok ? ldg16_stream(E.w2 + (size_t)r * rowb + (size_t)c * 16)
+                              : u32x4{0, 0, 0, 0};
+                sv[i][n] = ok ? ldg8(E.s2 + (size_t)r * rows_s + c) : 0u;
+            }
+        }
+        float xr[NCH][32];
+#pragma unroll
+        for (int n = 0; n < NCH; n++)
+            load_x32(xr[n], h + (size_t)k * inter + (lane + 64 * n) * 32, act[n]);
+#pragma unroll
+        for (int i = 0; i < RB; i++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int n = 0; n < NCH; n++)
+                a = fmaf(dot32(wv[i][n], xr[n]), dec_e8m0(sv[i][n]), a);
+            const float v = seg_sum<64>(a);
+            if (lane == 63) accl[k][i] = v;
+        }
+    }
+    __syncthreads();
+    const int nloc = min(RB, hidden - r0);
+    for (int i = threadIdx.x; i < nloc; i += blockDim.x) {
+        float o = 0.0f;
+        for (int kk = 0; kk < topk; kk++) {
+            const float p = wts[kk] * accl[kk][i];
+            o = o + p;
+        }
+        out[r0 + i] = o;
     }
 }
 
@@ -442,13 +506,12 @@ int launch_b(const Fp4Geom &g, float *out, const float *h,
 
 } // namespace
 
-int dsv4_moe_fp4_launch(float *d_out, const float *d_x,
-                        const Dsv4ExpertDev *d_table, int n_table,
-                        const int *d_idx, const float *d_w, int topk,
-                        int hidden, int inter, float limit, float *hbuf,
-                        float *accbuf, hipStream_t st)
+int dsv4_moe_fp4_valu_launch(float *d_out, const float *d_x,
+                             const Dsv4ExpertDev *d_table, int n_table,
+                             const int *d_idx, const float *d_w, int topk,
+                             int hidden, int inter, float limit, float *hbuf,
+                             hipStream_t st)
 {
-    (void)accbuf;
     Fp4Geom ga, gb;
     if (topk <= 0 || topk > MOE_KMAX || !fp4_geom(hidden, &ga) || !fp4_geom(inter, &gb)) {
         DSV4_ERR("moe: unsupported shape hidden %d inter %d topk %d "
@@ -476,7 +539,23 @@ int dsv4_moe_fp4_launch(float *d_out, const float *d_x,
     }
     if (rc != 0) { DSV4_ERR("moe: gate/up shape does not fit"); return -1; }
     HIP_OK(hipGetLastError(), "moe gate/up launch");
-    if (gb.nch == 1) {
+    if (inter <= 4096 && moe_env("DSV4_GPU_MOE_DOWNW", 1)) {
+        const int nw = topk < 8 ? topk : 8;
+        const int rbw = moe_env("DSV4_GPU_MOE_RBW", 32) >= 32 ? 32 : 16;
+        if (inter <= 2048 && rbw == 32)
+            hipLaunchKernelGGL((k_moe_down_w<1, 32>), dim3((hidden + 31) / 32), dim3(64 * nw),
+                               0, st, d_out, hbuf, d_table, n_table, d_idx, d_w, topk,
+                               hidden, inter);
+        else if (inter <= 2048)
+            hipLaunchKernelGGL((k_moe_down_w<1, 16>), dim3((hidden + 15) / 16), dim3(64 * nw),
+                               0, st, d_out, hbuf, d_table, n_table, d_idx, d_w, topk,
+                               hidden, inter);
+        else
+            hipLaunchKernelGGL((k_moe_down_w<2, 8>), dim3((hidden + 7) / 8), dim3(64 * nw),
+                               0, st, d_out, hbuf, d_table, n_table, d_idx, d_w, topk,
+                               hidden, inter);
+        rc = 0;
+    } else if (gb.nch == 1) {
         if (rb == 4) rc = launch_b<1, 4>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
         else if (rb == 2) rc = launch_b<1, 2>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
         else rc = launch_b<1, 1>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);

@@ -58,10 +58,74 @@ def test_c3_full_shape(gpu, dsv4, limit):
     run_case(dsv4, 7168, 2048, 8, 256, 0, limit)
 
 
+@pytest.mark.parametrize("limit", [10.0, 0.0])
+def test_c3_full_shape_matrix_core_form(gpu, dsv4, monkeypatch, limit):
+    """The matrix-core form (bf16 MFMA, activation as three bf16 terms), which
+    DSV4_GPU_MOE_MC=1 selects for shapes that are multiples of 128."""
+    monkeypatch.setenv("DSV4_GPU_MOE_MC", "1")
+    run_case(dsv4, 7168, 2048, 8, 256, 1, limit)
+
+
+@pytest.mark.parametrize("hidden,inter,topk", [(4096, 2048, 6), (1024, 512, 16),
+                                               (128, 128, 1), (256, 4096, 3)])
+def test_matrix_core_form_other_shapes(gpu, dsv4, monkeypatch, hidden, inter, topk):
+    monkeypatch.setenv("DSV4_GPU_MOE_MC", "1")
+    run_case(dsv4, hidden, inter, topk, 16, hidden + inter + 1, 10.0)
+
+
+def test_down_pass_forms(gpu, dsv4, monkeypatch):
+    """Both down-pass shapes of the VALU form (wave per expert slot with 32 or
+    16 rows per workgroup) and the row-group form give the oracle's result."""
+    for env in ({"DSV4_GPU_MOE_RBW": "16"}, {"DSV4_GPU_MOE_DOWNW": "0"}):
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        run_case(dsv4, 7168, 2048, 8, 256, 2, 10.0)
+        for k in env:
+            monkeypatch.delenv(k)
+
+
 @pytest.mark.parametrize("hidden,inter,topk", [(64, 96, 3), (4096, 2048, 6),
-                                               (32, 32, 1), (512, 4096, 2)])
+                                               (32, 32, 1), (512, 4096, 2),
+                                               (1024, 512, 16), (128, 128, 1),
+                                               (384, 640, 9)])
 def test_other_shapes(gpu, dsv4, hidden, inter, topk):
     run_case(dsv4, hidden, inter, topk, 16, hidden + inter, 10.0)
+
+
+def test_activation_dynamic_range(gpu, dsv4):
+    """x spanning twelve decades, with an all-zero 32-block, a block of f32
+    subnormals and one huge block: the matrix-core form writes x as e4m3
+    terms per 32-block, and each of these stresses a different edge of that
+    split."""
+    hidden, inter, topk = 1024, 256, 3
+    rng = np.random.default_rng(21)
+    ids = np.array([2, 0, 1], np.int32)
+    experts = [common.fp4_expert(rng, hidden, inter) for _ in range(topk)]
+    for i, e in zip(ids, experts):
+        upload(dsv4, 4, int(i), e, hidden, inter)
+    x = (rng.standard_normal(hidden) * 10.0 ** rng.uniform(-6, 6, hidden)).astype(np.float32)
+    x[0:32] = 0.0
+    x[32:64] = np.float32(1e-40) * rng.standard_normal(32).astype(np.float32)
+    x[64:96] *= np.float32(1e20)
+    w = common.router(rng, topk)
+    got = dsv4.moe_fp4(x, 4, ids, w, hidden, inter, 0.0)
+    want = oracle.moe_fp4(x, experts, w, hidden, inter, 0.0)
+    err = common.vec_rel_err(got, want)
+    print("moe dynamic range: worst rel %.3g" % err, flush=True)
+    assert err < TOL
+
+
+def test_repeatable_bits(gpu, dsv4):
+    """The same call twice gives the same bits (fixed reduction order)."""
+    hidden, inter, topk = 2048, 1024, 4
+    rng = np.random.default_rng(22)
+    for i in range(topk):
+        upload(dsv4, 6, i, common.fp4_expert(rng, hidden, inter), hidden, inter)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    w = common.router(rng, topk)
+    a = dsv4.moe_fp4(x, 6, np.arange(topk), w, hidden, inter, 10.0)
+    b = dsv4.moe_fp4(x, 6, np.arange(topk), w, hidden, inter, 10.0)
+    assert common.bits_equal(a, b)
 
 
 def test_exact_known_answer(gpu, dsv4):

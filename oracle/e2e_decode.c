@@ -1,0 +1,316 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/* e2e_decode.c - end-to-end greedy decode of a tiny deepseek_v4 checkpoint
+ * through the reference's OWN C99 model code, CPU path against GPU trunk.
+ *
+ * TEST INFRASTRUCTURE ONLY. oracle/Makefile compiles
+ * this driver together with the reference's sources, where they lie under
+ * /root/reference, into oracle/_ref/dsv4_e2e:
+ *   - src/core: matmul, ops, hc, rope, compress, indexer, attn;
+ *   - src/model: layer, bind;
+ *   - src/io: st.
+ * Its matmul dispatch (dsv4_matmul.c:525,572) is compiled with dsv4_cuda_has /
+ * dsv4_cuda_mmq / dsv4_cuda_mmq_n renamed to dsv4_gpu_*, and it links
+ * deepseek-v4-in-c_amd/lib/libdsv4_gpu.so. That is the drop-in binding of
+ * INTEGRATION.md section 2, made with the preprocessor instead of an edit.
+ *
+ * The decode loop restates the reference's own (dsv4_run.c:444-483,
+ * tests/unit/test_model_oracle.c:196-245):
+ *   embedding row -> hc_mult copies -> every layer's dsv4_layer_forward
+ *   -> the head's hc reduction -> final RMSNorm -> head matmul -> argmax.
+ * The run goes twice over the same teacher-forced tokens, from fresh layer
+ * state each time:
+ *   - pass 1: nothing resident, so every matmul runs on the reference CPU
+ *     path;
+ *   - pass 2: dsv4_gpu_init plus the FP8 trunk upload of dsv4_run.c:270-283,
+ *     so every FP8 matmul (including the wo_a group slices) runs on the
+ *     MI355X.
+ * Routed experts come from memory (all resident), the CPU FP4 path in both
+ * passes.
+ *
+ * usage: dsv4_e2e CKPT_DIR TOKENS_FILE [--cpu-only]
+ * Prints one line per position and a summary; exit 0 when every argmax
+ * agrees, 1 when one differs or a step fails, 2 when no GPU is available
+ * (unless --cpu-only).
+ */
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "dsv4_cfg.h"
+#include "dsv4_st.h"
+#include "dsv4_bind.h"
+#include "dsv4_layer.h"
+#include "dsv4_gpu.h"
+
+void dsv4_rmsnorm(float *y, const float *x, const float *w, int n, float eps);
+void dsv4_mmq(float *y, const float *x, const DSV4QMat *m);
+void dsv4_rope_table(float *cs, float *sn, int rd, int maxpos, int orig_ctx,
+                     double theta, double factor, double beta_fast, double beta_slow);
+
+/* ---------------------------------------------------- routed experts ---- */
+typedef struct {
+    DSV4ExpertW *w;          /* [n_layers][n_experts] */
+    void **blocks;
+    int n_layers, n_experts, nblocks;
+} Experts;
+
+static void *read_tensor(const DSV4St *st, const char *name, int64_t *nbytes)
+{
+    const DSV4Tensor *t = dsv4_st_find(st, name);
+    if (!t) { fprintf(stderr, "e2e: %s missing\n", name); return NULL; }
+    void *buf = malloc((size_t)t->nbytes);
+    if (!buf || dsv4_st_read(st, t, buf) != t->nbytes) {
+        fprintf(stderr, "e2e: reading %s failed\n", name);
+        free(buf);
+        return NULL;
+    }
+    if (nbytes) *nbytes = t->nbytes;
+    return buf;
+}
+
+/* Every routed expert, read once into memory and described as the expert
+ * cache describes a slot (dsv4_cache.c:51-66: FP4, 1x32 blocks). */
+static int load_experts(Experts *E, const DSV4St *st, const DSV4Cfg *c)
+{
+    E->n_layers = c->n_layers;
+    E->n_experts = c->n_experts;
+    E->w = calloc((size_t)c->n_layers * c->n_experts, sizeof *E->w);
+    E->blocks = calloc((size_t)c->n_layers * c->n_experts * 6, sizeof(void *));
+    E->nblocks = 0;
+    if (!E->w || !E->blocks) return -1;
+    for (int L = 0; L < c->n_layers; L++)
+        for (int e = 0; e < c->n_experts; e++) {
+            DSV4ExpertW *x = &E->w[(size_t)L * c->n_experts + e];
+            DSV4QMat *m[3] = {&x->w1, &x->w2, &x->w3};
+            const int rows[3] = {c->moe_inter, c->hidden, c->moe_inter};
+            const int cols[3] = {c->hidden, c->moe_inter, c->hidden};
+            for (int i = 0; i < 3; i++) {
+                char nm[128];
+                snprintf(nm, sizeof nm, "layers.%d.ffn.experts.%d.w%d.weight", L, e, i + 1);
+                void *wb = read_tensor(st, nm, NULL);
+                snprintf(nm, sizeof nm, "layers.%d.ffn.experts.%d.w%d.scale", L, e, i + 1);
+                void *sb = read_tensor(st, nm, NULL);
+                if (!wb || !sb) return -1;
+                E->blocks[E->nblocks++] = wb;
+                E->blocks[E->nblocks++] = sb;
+                m[i]->w = wb;
+                m[i]->s = sb;
+                m[i]->wdt = DSV4_WFP4;
+                m[i]->rows = rows[i];
+                m[i]->cols = cols[i];
+                m[i]->blk_r = 1;
+                m[i]->blk_c = 32;
+            }
+        }
+    return 0;
+}
+
+static const DSV4ExpertW *expert_get(void *ctx, int layer, int expert)
+{
+    const Experts *E = ctx;
+    if (layer < 0 || layer >= E->n_layers || expert < 0 || expert >= E->n_experts)
+        return NULL;
+    return &E->w[(size_t)layer * E->n_experts + expert];
+}
+
+/* --------------------------------------------------------------- head ---- */
+/* The head's own hc reduction (dsv4_run.c:94-116): a sigmoid gate per
+ * stream from one RMS-scaled dot, no Sinkhorn, one scalar scale. */
+static void head_hc(float *y, const float *x, const DSV4HcW *w, int hc, int hidden,
+                    float norm_eps, float hc_eps)
+{
+    const int n = hc * hidden;
+    double sq = 0.0;
+    for (int i = 0; i < n; i++) sq += (double)x[i] * x[i];
+    const float rs = (float)(1.0 / sqrt(sq / (double)n + (double)norm_eps));
+    float gate[DSV4_MAX_HC_MULT];
+    for (int j = 0; j < hc; j++) {
+        double dot = 0.0;
+        for (int i = 0; i < n; i++)
+            dot = fma((double)w->fn[(size_t)j * n + i], (double)x[i], dot);
+        const float m = (float)dot * rs;
+        gate[j] = 1.0f / (1.0f + expf(-(m * w->scale[0] + w->base[j]))) + hc_eps;
+    }
+    for (int d = 0; d < hidden; d++) {
+        double acc = 0.0;
+        for (int j = 0; j < hc; j++)
+            acc += (double)gate[j] * (double)x[(size_t)j * hidden + d];
+        y[d] = (float)acc;
+    }
+}
+
+/* --------------------------------------------------------------- main ---- */
+static int read_tokens(const char *path, int **out)
+{
+    FILE *f = fopen(path, "r");
+    if (!f) { perror(path); return -1; }
+    int cap = 64, n = 0;
+    int *t = malloc(sizeof(int) * cap);
+    long v;
+    while (t && fscanf(f, "%ld", &v) == 1) {
+        if (n == cap) { cap *= 2; t = realloc(t, sizeof(int) * cap); if (!t) break; }
+        t[n++] = (int)v;
+    }
+    fclose(f);
+    *out = t;
+    return t ? n : -1;
+}
+
+typedef struct {
+    const DSV4Cfg *c;
+    DSV4LayerBind *lb;
+    DSV4ModelBind *mb;
+    DSV4ExpertSrc *src;
+    DSV4Scratch *s;
+    float *cs_d, *sn_d, *cs_c, *sn_c;
+    int maxpos;
+} Model;
+
+/* One greedy pass over the tokens from fresh layer state; logits[pos][vocab]. */
+static int run_pass(const Model *M, const int *tok, int n, float *logits)
+{
+    const DSV4Cfg *c = M->c;
+    const int hc = c->hc_mult, d = c->hidden;
+    DSV4LayerState *ls = calloc((size_t)c->n_layers, sizeof *ls);
+    float *h = calloc((size_t)hc * d, sizeof(float));
+    float *y = calloc((size_t)d, sizeof(float));
+    if (!ls || !h || !y) return -1;
+    for (int L = 0; L < c->n_layers; L++)
+        if (dsv4_state_init(&ls[L], c, L, M->maxpos) != 0) return -1;
+    DSV4QMat head = {M->mb->w.head, NULL, DSV4_WBF16, c->vocab, d, 0, 0};
+    for (int pos = 0; pos < n; pos++) {
+        dsv4_embed_row(y, M->mb->w.embed, M->mb->w.wdt, tok[pos], d);
+        for (int j = 0; j < hc; j++) memcpy(h + (size_t)j * d, y, (size_t)d * sizeof(float));
+        for (int L = 0; L < c->n_layers; L++) {
+            const int comp = dsv4_compress_ratio(c, L) != 0;
+            dsv4_layer_forward(h, &M->lb[L].w, c, M->s, M->src, &ls[L],
+                               comp ? M->cs_c : M->cs_d, comp ? M->sn_c : M->sn_d,
+                               pos, tok[pos]);
+        }
+        head_hc(y, h, &M->mb->w.hc_head, hc, d, c->rms_eps, c->hc_eps);
+        dsv4_rmsnorm(y, y, M->mb->w.norm, d, c->rms_eps);
+        dsv4_mmq(logits + (size_t)pos * c->vocab, y, &head);
+    }
+    for (int L = 0; L < c->n_layers; L++) dsv4_state_free(&ls[L]);
+    free(ls); free(h); free(y);
+    return 0;
+}
+
+static int argmax(const float *v, int n, float *margin)
+{
+    int a = 0;
+    for (int i = 1; i < n; i++) if (v[i] > v[a]) a = i;
+    float second = -INFINITY;
+    for (int i = 0; i < n; i++) if (i != a && v[i] > second) second = v[i];
+    if (margin) *margin = v[a] - second;
+    return a;
+}
+
+/* Vector-scaled relative error (tests/unit/test_cuda.c:160-167). */
+static double vec_rel(const float *got, const float *ref, int n)
+{
+    double sq = 0.0;
+    for (int i = 0; i < n; i++) sq += (double)ref[i] * ref[i];
+    const double rms = sqrt(sq / n);
+    double worst = 0.0;
+    for (int i = 0; i < n; i++) {
+        double s = fabs((double)ref[i]);
+        if (fabs((double)got[i]) > s) s = fabs((double)got[i]);
+        if (rms > s) s = rms;
+        const double r = s > 0 ? fabs((double)got[i] - ref[i]) / s : 0.0;
+        if (r > worst) worst = r;
+    }
+    return worst;
+}
+
+int main(int argc, char **argv)
+{
+    if (argc < 3) {
+        fprintf(stderr, "usage: %s CKPT_DIR TOKENS_FILE [--cpu-only]\n", argv[0]);
+        return 1;
+    }
+    const int cpu_only = argc > 3 && !strcmp(argv[3], "--cpu-only");
+    char path[1024];
+    DSV4Cfg c;
+    int cr[DSV4_MAX_LAYERS];
+    snprintf(path, sizeof path, "%s/config.json", argv[1]);
+    if (!dsv4_cfg_load_file(&c, cr, DSV4_MAX_LAYERS, path)) return 1;
+    DSV4St st;
+    if (dsv4_st_open(&st, argv[1]) != 0) return 1;
+    int *tok = NULL;
+    const int n = read_tokens(argv[2], &tok);
+    if (n <= 0) return 1;
+    for (int i = 0; i < n; i++)
+        if (tok[i] < 0 || tok[i] >= c.vocab) {
+            fprintf(stderr, "e2e: token %d out of range\n", tok[i]);
+            return 1;
+        }
+
+    DSV4LayerBind *lb = calloc((size_t)c.n_layers, sizeof *lb);
+    for (int L = 0; L < c.n_layers; L++)
+        if (dsv4_bind_layer(&st, &c, L, &lb[L]) != 0) return 1;
+    DSV4ModelBind mb;
+    if (dsv4_bind_model(&st, &c, 1, &mb) != 0) return 1;
+    Experts E;
+    if (load_experts(&E, &st, &c) != 0) return 1;
+    DSV4ExpertSrc src = {.get = expert_get, .ctx = &E};
+
+    Model M = {.c = &c, .lb = lb, .mb = &mb, .src = &src, .maxpos = n + 16};
+    const int half = c.qk_rope / 2;
+    M.cs_d = malloc((size_t)M.maxpos * half * 4); M.sn_d = malloc((size_t)M.maxpos * half * 4);
+    M.cs_c = malloc((size_t)M.maxpos * half * 4); M.sn_c = malloc((size_t)M.maxpos * half * 4);
+    dsv4_rope_table(M.cs_d, M.sn_d, c.qk_rope, M.maxpos, 0, c.rope_theta,
+                    c.yarn_factor, c.yarn_beta_fast, c.yarn_beta_slow);
+    dsv4_rope_table(M.cs_c, M.sn_c, c.qk_rope, M.maxpos, c.yarn_orig_ctx,
+                    c.compress_rope_theta, c.yarn_factor, c.yarn_beta_fast,
+                    c.yarn_beta_slow);
+    DSV4Scratch s;
+    if (dsv4_scratch_init(&s, &c, M.maxpos) != 0) return 1;
+    M.s = &s;
+    printf("e2e: hidden %d, %d layers, vocab %d, %d experts (top-%d), index_topk %d, "
+           "%d positions\n", c.hidden, c.n_layers, c.vocab, c.n_experts, c.topk,
+           c.index_topk, n);
+
+    float *ref = malloc((size_t)n * c.vocab * sizeof(float));
+    float *got = malloc((size_t)n * c.vocab * sizeof(float));
+    if (!ref || !got || run_pass(&M, tok, n, ref) != 0) return 1;
+
+    int gpu_mats = 0;
+    if (cpu_only) {
+        if (run_pass(&M, tok, n, got) != 0) return 1;
+    } else {
+        if (!dsv4_gpu_available() || dsv4_gpu_init() != 0) {
+            fprintf(stderr, "e2e: no GPU\n");
+            return 2;
+        }
+        for (int L = 0; L < c.n_layers; L++) {
+            const DSV4LayerW *w = &lb[L].w;
+            const DSV4QMat *m[9] = {&w->attn.wq_a, &w->attn.wq_b, &w->attn.wkv,
+                                    &w->attn.wo_a, &w->attn.wo_b, &w->moe.shared.w1,
+                                    &w->moe.shared.w2, &w->moe.shared.w3,
+                                    w->attn.has_idx ? &w->attn.idx.wq_b : NULL};
+            for (int k = 0; k < 9; k++)
+                if (m[k] && m[k]->wdt == DSV4_WFP8 && dsv4_gpu_upload(m[k]) == 0) gpu_mats++;
+        }
+        printf("gpu: %d FP8 matrices resident\n", gpu_mats);
+        if (gpu_mats == 0 || run_pass(&M, tok, n, got) != 0) return 1;
+    }
+
+    int agree = 0;
+    double worst = 0.0;
+    for (int p = 0; p < n; p++) {
+        float mr, mg;
+        const int ar = argmax(ref + (size_t)p * c.vocab, c.vocab, &mr);
+        const int ag = argmax(got + (size_t)p * c.vocab, c.vocab, &mg);
+        const double r = vec_rel(got + (size_t)p * c.vocab, ref + (size_t)p * c.vocab, c.vocab);
+        if (r > worst) worst = r;
+        agree += ar == ag;
+        printf("pos %d tok %d cpu %d %s %d margin %.6g rel %.3g\n", p, tok[p], ar,
+               cpu_only ? "cpu2" : "gpu", ag, (double)mr, r);
+    }
+    printf("summary: positions %d argmax_equal %d worst_rel %.3g gpu_mats %d\n", n,
+           agree, worst, gpu_mats);
+    if (!cpu_only) dsv4_gpu_shutdown();
+    return agree == n ? 0 : 1;
+}

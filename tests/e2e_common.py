@@ -1,0 +1,38 @@
+"""Helpers for the end-to-end decode test: write the
+tiny checkpoint and token file, run oracle/_ref/dsv4_e2e, parse its report."""
+import os
+import re
+import subprocess
+
+import tiny_checkpoint
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+E2E = os.path.join(ROOT, "oracle", "_ref", "dsv4_e2e")
+
+
+def available():
+    return os.path.exists(E2E)
+
+
+def prepare(tmp_dir, n=46):
+    tiny_checkpoint.write(str(tmp_dir))
+    tok = tiny_checkpoint.tokens(n)
+    tf = os.path.join(str(tmp_dir), "tokens.txt")
+    with open(tf, "w") as f:
+        f.write("\n".join(str(int(t)) for t in tok) + "\n")
+    return str(tmp_dir), tf
+
+
+def run(ckpt, tokens_file, cpu_only=False, timeout=300):
+    cmd = [E2E, ckpt, tokens_file] + (["--cpu-only"] if cpu_only else [])
+    p = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
+    rows = []
+    for line in p.stdout.splitlines():
+        m = re.match(r"pos (\d+) tok (\d+) cpu (\d+) \w+ (\d+) margin (\S+) rel (\S+)", line)
+        if m:
+            rows.append(dict(pos=int(m.group(1)), tok=int(m.group(2)),
+                             ref=int(m.group(3)), got=int(m.group(4)),
+                             margin=float(m.group(5)), rel=float(m.group(6))))
+    summ = re.search(r"summary: positions (\d+) argmax_equal (\d+) worst_rel (\S+) "
+                     r"gpu_mats (\d+)", p.stdout)
+    return p, rows, summ

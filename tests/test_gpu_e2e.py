@@ -1,0 +1,37 @@
+"""End-to-end greedy decode, GPU trunk against the CPU path (BASELINE
+configs[4]): 46 teacher-forced random token ids in [0, 129280) through a tiny,
+structurally real deepseek_v4 checkpoint (FP8 trunk, MXFP4 experts, CSA
+indexer with selection, sparse MLA), run by the reference's own C99 model
+code. In the second pass every FP8 matrix the reference uploads
+(dsv4_run.c:270-283) runs on the MI355X through dsv4_gpu_mmq. That includes
+the wo_a group slices, which resolve as row-range views.
+
+Bar: identical argmax at every position. The logits agree within the
+reference's own whole-model tolerance, 2e-3 vector-scaled
+(tests/unit/test_model_oracle.c:253-270).
+"""
+import sys
+
+import pytest
+
+import e2e_common
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not e2e_common.available(),
+                                 reason="oracle/_ref/dsv4_e2e not built")]
+
+
+def test_gpu_trunk_argmax_identical(tmp_path):
+    ckpt, tf = e2e_common.prepare(tmp_path)
+    print("e2e: checkpoint %s, running the GPU trunk pass" % ckpt, flush=True)
+    p, rows, summ = e2e_common.run(ckpt, tf)
+    print(p.stdout[-4000:], flush=True)
+    sys.stdout.flush()
+    assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-2000:]
+    assert summ, p.stdout[-2000:]
+    n, agree, worst, mats = (int(summ.group(1)), int(summ.group(2)),
+                             float(summ.group(3)), int(summ.group(4)))
+    assert n == 46 and agree == 46
+    assert mats >= 4 * 8            # every layer's FP8 trunk is resident
+    assert worst < 2e-3
+    assert any(r["rel"] > 0.0 for r in rows), "GPU pass produced CPU bits: trunk not on GPU?"

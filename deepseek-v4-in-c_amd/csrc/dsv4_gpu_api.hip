@@ -58,7 +58,7 @@ hipStream_t g_stream = nullptr;
 std::vector<Res> g_res;
 std::vector<LayerExperts> g_layers;
 Arena g_ar;
-Scratch g_moe, g_attn, g_scores;
+Scratch g_moe, g_attn, g_scores, g_index;
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -367,7 +367,7 @@ void dsv4_gpu_shutdown(void)
         if (L.dev) (void)hipFree(L.dev);
     }
     g_layers.clear();
-    for (Scratch *s : {&g_moe, &g_attn, &g_scores}) {
+    for (Scratch *s : {&g_moe, &g_attn, &g_scores, &g_index}) {
         if (s->p) (void)hipFree(s->p);
         s->p = nullptr;
         s->cap = 0;
@@ -677,7 +677,7 @@ int dsv4_gpu_indexer_score(float *out, const float *q, const float *w, int H,
     if (dsv4_indexer_score_launch((float *)(g_ar.d + oo), (const float *)(g_ar.d + qo),
                                   (const float *)(g_ar.d + wo), H, D, kb, ks,
                                   keys->fmt, key_stride, n, indexer_scale(D, H),
-                                  g_stream) != 0)
+                                  nullptr, 0, g_stream) != 0)
         return -1;
     return stage_pull(oo, (size_t)n * sizeof(float), out);
 }
@@ -687,13 +687,14 @@ int dsv4_gpu_topk(int *idxs, const float *scores, int n, int k)
     if (!g_ready || n < 0) return -1;
     if (k > n) k = n;
     if (k <= 0) return k < 0 ? -1 : 0;
+    if (scratch_reserve(g_index, dsv4_index_scratch_bytes(n)) != 0) return -1;
     Stage s;
     const size_t so = s.in(scores, (size_t)n * sizeof(float));
     const size_t io = s.add((size_t)k * sizeof(int));
     size_t end;
     if (stage_push(s, &end) != 0) return -1;
     if (dsv4_topk_launch((int *)(g_ar.d + io), (const float *)(g_ar.d + so), n, k,
-                         g_stream) != 0)
+                         g_index.p, 0, g_stream) != 0)
         return -1;
     if (stage_pull(io, (size_t)k * sizeof(int), idxs) != 0) return -1;
     return k;
@@ -708,6 +709,8 @@ int dsv4_gpu_indexer_topk(int *idxs, const float *q, const float *w, int H,
     if (!g_ready || key_view(keys, row0, key_stride, D, n, &kb, &ks) != 0) return -1;
     if (k > n) k = n;
     if (k <= 0) return k < 0 ? -1 : 0;
+    if (scratch_reserve(g_index, dsv4_index_scratch_bytes(n)) != 0) return -1;
+    const int hist = dsv4_topk_takes_hist(n, k);
     Stage s;
     const size_t qo = s.in(q, (size_t)H * D * sizeof(float));
     const size_t wo = s.in(w, (size_t)H * sizeof(float));
@@ -718,9 +721,9 @@ int dsv4_gpu_indexer_topk(int *idxs, const float *q, const float *w, int H,
     if (dsv4_indexer_score_launch((float *)(g_ar.d + so), (const float *)(g_ar.d + qo),
                                   (const float *)(g_ar.d + wo), H, D, kb, ks,
                                   keys->fmt, key_stride, n, indexer_scale(D, H),
-                                  g_stream) != 0 ||
+                                  g_index.p, hist, g_stream) != 0 ||
         dsv4_topk_launch((int *)(g_ar.d + io), (const float *)(g_ar.d + so), n, k,
-                         g_stream) != 0)
+                         g_index.p, hist, g_stream) != 0)
         return -1;
     if (stage_pull(io, (size_t)k * sizeof(int), idxs) != 0) return -1;
     return k;
@@ -762,15 +765,18 @@ int dsv4_gpu_indexer_score_d(float *d_out, const float *d_q, const float *d_w,
                              const float *d_key_scales, int key_fmt,
                              int key_stride, int n, float scale, void *stream)
 {
+    if (!g_ready) return -1;
     return dsv4_indexer_score_launch(d_out, d_q, d_w, H, D, d_keys, d_key_scales,
-                                     key_fmt, key_stride, n, scale,
+                                     key_fmt, key_stride, n, scale, nullptr, 0,
                                      as_stream(stream));
 }
 
 int dsv4_gpu_topk_d(int *d_idxs, const float *d_scores, int n, int k,
                     void *stream)
 {
-    return dsv4_topk_launch(d_idxs, d_scores, n, k, as_stream(stream));
+    if (!g_ready || scratch_reserve(g_index, dsv4_index_scratch_bytes(n)) != 0)
+        return -1;
+    return dsv4_topk_launch(d_idxs, d_scores, n, k, g_index.p, 0, as_stream(stream));
 }
 
 int dsv4_gpu_sparse_attn_d(float *d_o, const float *d_q, const void *d_kv,
@@ -800,14 +806,18 @@ int dsv4_gpu_mla_decode_d(float *d_o, int *d_idxs,
     if (k > n) k = n;
     if (k < 0) return -1;
     hipStream_t st = as_stream(stream);
-    if (scratch_reserve(g_scores, (size_t)(n > 0 ? n : 1) * sizeof(float)) != 0 ||
+    if (H <= 0 || D <= 0 ||
+        scratch_reserve(g_scores, (size_t)(n > 0 ? n : 1) * sizeof(float)) != 0 ||
+        scratch_reserve(g_index, dsv4_index_scratch_bytes(n)) != 0 ||
         scratch_reserve(g_attn, dsv4_attn_scratch_bytes(h, d_qk, d_v, k, kv_fmt) + 4) != 0)
         return -1;
+    const int hist = dsv4_topk_takes_hist(n, k);
     if (n > 0 &&
         (dsv4_indexer_score_launch((float *)g_scores.p, d_q_idx, d_w_idx, H, D,
                                    d_keys, d_key_scales, key_fmt, key_stride, n,
-                                   indexer_scale(D, H), st) != 0 ||
-         dsv4_topk_launch(d_idxs, (const float *)g_scores.p, n, k, st) != 0))
+                                   indexer_scale(D, H), g_index.p, hist, st) != 0 ||
+         dsv4_topk_launch(d_idxs, (const float *)g_scores.p, n, k, g_index.p, hist,
+                          st) != 0))
         return -1;
     return dsv4_attn_launch(d_o, d_q, d_kv, kv_fmt, kv_stride, kv_rows, d_sink,
                             d_idxs, h, d_qk, d_v, k, attn_scale, g_attn.p, st);

@@ -65,14 +65,24 @@ int dsv4_moe_fp4_valu_launch(float *d_out, const float *d_x,
                              int hidden, int inter, float limit, float *hbuf,
                              hipStream_t st);
 
+/* Index scratch (the top-k's histogram, candidates and lists) for a top-k
+ * over n scores, in bytes. The standalone score needs none. */
+size_t dsv4_index_scratch_bytes(int n);
+
+/* Whether a top-k of k over n scores starts from the level-1 histogram that
+ * dsv4_indexer_score_launch builds with with_hist set. */
+int dsv4_topk_takes_hist(int n, int k);
+
 int dsv4_indexer_score_launch(float *d_out, const float *d_q, const float *d_w,
                               int H, int D, const void *d_keys,
                               const float *d_key_scales, int key_fmt,
-                              int key_stride, int n, float scale,
-                              hipStream_t st);
+                              int key_stride, int n, float scale, void *scratch,
+                              int with_hist, hipStream_t st);
 
+/* hist_ready: the score kernel left the level-1 histogram for these scores in
+ * the scratch (only when dsv4_topk_takes_hist(n, k)). */
 int dsv4_topk_launch(int *d_idxs, const float *d_scores, int n, int k,
-                     hipStream_t st);
+                     void *scratch, int hist_ready, hipStream_t st);
 
 /* Scratch needed by dsv4_attn_launch, in bytes (0: shape not supported). */
 size_t dsv4_attn_scratch_bytes(int h, int d_qk, int d_v, int topk, int kv_fmt);

@@ -55,467 +55,631 @@ __device__ __forceinline__ float key_at(const void *keys, const float *ks,
 
 /* ------------------------------------------------------- indexer score */
 
-/* Workgroup: P = TL * IS_CH key rows for all H heads, H * TL threads.
- * Thread (h, tl) runs the fma chains of head h for rows tl, tl + TL,
- * tl + 2 TL, tl + 3 TL: four independent chains keep the fp64 pipe busy.
- * The rows are widened to double once, into LDS; q too when it fits (QD),
- * else q stays f32 there and is widened per use (exact either way). */
-constexpr int IS_CH = 4;                        /* chains per thread */
+/* Score kernel geometry: lane = key row, a wave runs the chains of IS_HB
+ * heads for its 64 rows, and the waves of a workgroup cover the heads
+ * (looping when there are more than IS_MAXW groups). */
+constexpr int IS_HB = 8;                        /* heads per wave */
+constexpr int IS_MAXW = 8;                      /* waves per workgroup */
 
-template <int KF, int QD>
-__global__ void __launch_bounds__(256)
-k_indexer_score(float *__restrict__ out, const float *__restrict__ q,
-                const float *__restrict__ w, int H, int D,
-                const void *__restrict__ keys, const float *__restrict__ ks,
-                int key_stride, int n, float scale, int TL)
+/* Top-k constants the score kernel shares: its histogram is the first level
+ * of the selection. */
+constexpr int TK_THREADS = 1024;
+constexpr int TK_WAVES = TK_THREADS / 64;
+constexpr int TK_KMAX = 4096;
+constexpr int TK_BINS = 2048;                   /* top 11 bits of the key */
+constexpr int TK_SLICES = 16;                   /* spread of the global atomics */
+
+/* meta words in the scratch */
+constexpr int MT_CGT = 0;                       /* candidates > T (for rank) */
+constexpr int MT_ABOVE = 1;                     /* cand[] append counter */
+constexpr int MT_BIN = 2;                       /* B */
+constexpr int MT_KREM = 3;                      /* rank of the k-th inside B */
+
+
+/* Order-preserving 32-bit key of a score: a > b as floats iff fkey(a) >
+ * fkey(b) as integers; -0.0 folds into +0.0 since the reference's `>`
+ * treats them as equal. */
+__device__ __forceinline__ uint32_t fkey(float f)
 {
-    extern __shared__ double lds_d[];
-    const int P = TL * IS_CH;                   /* rows per workgroup */
-    const int ld = D + 1;                       /* padded pitch */
-    double *dots = lds_d;                       /* [P][H]   */
-    double *kd = dots + (size_t)P * H;          /* [P][D+1] */
-    double *qd = kd + (size_t)P * ld;           /* [H][D+1] (QD) */
-    float *qf = (float *)qd;                    /* [H][D+1] (!QD) */
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) == 0u) u = 0u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
 
-    const int tid = threadIdx.x;
-    const int nthr = blockDim.x;
-    const int t0 = blockIdx.x * P;
-
-    /* Staging issues every load of a batch before using any of them, so the
-     * workgroup waits one memory latency per batch, not one per element. */
-    constexpr int SB = 8;
-    for (int i0 = 0; i0 < H * D; i0 += SB * nthr) {
-        float v[SB];
-#pragma unroll
-        for (int u = 0; u < SB; u++) {
-            const int i = i0 + u * nthr + tid;
-            v[u] = i < H * D ? q[i] : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < SB; u++) {
-            const int i = i0 + u * nthr + tid;
-            if (i < H * D) {
-                const int hh = i / D, c = i - hh * D;
-                if (QD) qd[hh * ld + c] = (double)v[u];
-                else    qf[hh * ld + c] = v[u];
-            }
-        }
+/* One histogram bump per lane with live set, into a global histogram: the
+ * lanes sharing the leading lane's bin are counted with one atomic, for a
+ * few rounds; what is left adds one by one. */
+__device__ __forceinline__ void hist_push_global(uint32_t *hg, bool live,
+                                                 uint32_t bin, int lane)
+{
+    bool todo = live;
+#pragma unroll 1
+    for (int it = 0; it < 8; ++it) {
+        const unsigned long long pend = __ballot(todo);
+        if (pend == 0ull) return;
+        const int leader = __ffsll((long long)pend) - 1;
+        const uint32_t bl = (uint32_t)__builtin_amdgcn_readlane((int)bin, leader);
+        const bool mine = todo && bin == bl;
+        const unsigned long long same = __ballot(mine);
+        if (lane == leader) atomicAdd(&hg[bl], (uint32_t)__popcll(same));
+        if (mine) todo = false;
     }
-    for (int i0 = 0; i0 < P * D; i0 += SB * nthr) {
-        float v[SB];
-#pragma unroll
-        for (int u = 0; u < SB; u++) {
-            const int i = i0 + u * nthr + tid;
-            const int p = i / D, c = i - p * D;
-            const int t = t0 + p;
-            v[u] = (i < P * D && t < n) ? key_at<KF>(keys, ks, (size_t)t, key_stride, c) : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < SB; u++) {
-            const int i = i0 + u * nthr + tid;
-            if (i < P * D) {
-                const int p = i / D, c = i - p * D;
-                kd[p * ld + c] = (double)v[u];
-            }
-        }
-    }
-    __syncthreads();
+    if (todo) atomicAdd(&hg[bin], 1u);
+}
 
-    if (tid < H * TL) {
-        const int hh = tid % H, tl = tid / H;
-        const double *k0 = kd + (size_t)(tl + 0 * TL) * ld;
-        const double *k1 = kd + (size_t)(tl + 1 * TL) * ld;
-        const double *k2 = kd + (size_t)(tl + 2 * TL) * ld;
-        const double *k3 = kd + (size_t)(tl + 3 * TL) * ld;
-        double d0 = 0.0, d1 = 0.0, d2 = 0.0, d3 = 0.0;
-#pragma unroll 4
-        for (int c = 0; c < D; c++) {
-            const double qc = QD ? qd[hh * ld + c] : (double)qf[hh * ld + c];
-            d0 = fma(qc, k0[c], d0);
-            d1 = fma(qc, k1[c], d1);
-            d2 = fma(qc, k2[c], d2);
-            d3 = fma(qc, k3[c], d3);
+/* One 16-byte piece of a key row, as floats (16 / element-size of them);
+ * for FP8 the reference's float product e4m3(code) * row_scale. */
+template <int KF>
+__device__ __forceinline__ void key_piece(u32x4 v, float rs, float *k)
+{
+    if (KF == DSV4_GPU_KV_FP8) {
+        dec_e4m3x4(v.x, k + 0);
+        dec_e4m3x4(v.y, k + 4);
+        dec_e4m3x4(v.z, k + 8);
+        dec_e4m3x4(v.w, k + 12);
+#pragma unroll
+        for (int e = 0; e < 16; e++) k[e] = k[e] * rs;
+    } else if (KF == DSV4_GPU_KV_BF16) {
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            k[2 * e] = __uint_as_float(w4[e] << 16);
+            k[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
         }
-        dots[(tl + 0 * TL) * H + hh] = d0;
-        dots[(tl + 1 * TL) * H + hh] = d1;
-        dots[(tl + 2 * TL) * H + hh] = d2;
-        dots[(tl + 3 * TL) * H + hh] = d3;
-    }
-    __syncthreads();
-
-    for (int p = tid; p < P; p += nthr) {
-        const int t = t0 + p;
-        if (t < n) {
-            double total = 0.0;
-            for (int hh = 0; hh < H; hh++) {
-                const double d = dots[p * H + hh];
-                if (d > 0.0) {
-                    const double prod = d * (double)w[hh];
-                    total = total + prod;
-                }
-            }
-            const float tf = (float)total;
-            out[t] = tf * scale;
-        }
+    } else {
+        k[0] = __uint_as_float(v.x); k[1] = __uint_as_float(v.y);
+        k[2] = __uint_as_float(v.z); k[3] = __uint_as_float(v.w);
     }
 }
 
-template <int KF>
-void launch_score(bool qd, int grid, int thr, size_t lds, hipStream_t st,
-                  float *d_out, const float *d_q, const float *d_w, int H, int D,
-                  const void *d_keys, const float *d_key_scales, int key_stride,
-                  int n, float scale, int TL)
+/* q of the wave's IS_HB heads for columns c0 .. c0 + 15, one column per
+ * lane of each 16-lane row (every row holds the same values): lane l gets
+ * q[g*IS_HB + j][c0 + l % 16]. Heads past H read as zero, columns past D as
+ * the last column. */
+__device__ __forceinline__ void q_cols(float *dst, const float *q, int h0, int H,
+                                       int D, int c0, int lane)
 {
-    if (qd)
-        hipLaunchKernelGGL((k_indexer_score<KF, 1>), dim3(grid), dim3(thr), lds, st,
-                           d_out, d_q, d_w, H, D, d_keys, d_key_scales, key_stride,
-                           n, scale, TL);
+    const int c = min(c0 + (lane & 15), D - 1);
+#pragma unroll
+    for (int j = 0; j < IS_HB; j++)
+        dst[j] = h0 + j < H ? q[(size_t)(h0 + j) * D + c] : 0.0f;
+}
+
+/* Chain steps for columns c0 + R and c0 + R + 1 of every head of the group:
+ * q[.][c0 + R] reaches all lanes by a row broadcast of lane R. The
+ * broadcasts are issued together, then the fmas, so neither waits on the
+ * other. */
+template <int R>
+__device__ __forceinline__ void chain_cols2(double *acc, const double *qv, float k0, float k1)
+{
+    const double kd0 = (double)k0, kd1 = (double)k1;
+    double qb0[IS_HB], qb1[IS_HB];
+#pragma unroll
+    for (int j = 0; j < IS_HB; j++) {
+        qb0[j] = __builtin_amdgcn_mov_dpp(qv[j], 0x150 + R, 0xF, 0xF, true);
+        qb1[j] = __builtin_amdgcn_mov_dpp(qv[j], 0x150 + R + 1, 0xF, 0xF, true);
+    }
+#pragma unroll
+    for (int j = 0; j < IS_HB; j++) acc[j] = fma(qb0[j], kd0, acc[j]);
+#pragma unroll
+    for (int j = 0; j < IS_HB; j++) acc[j] = fma(qb1[j], kd1, acc[j]);
+}
+
+template <int R>
+__device__ __forceinline__ void chain_col(double *acc, const double *qv, float kf)
+{
+    const double kd = (double)kf;
+    double qb[IS_HB];
+#pragma unroll
+    for (int j = 0; j < IS_HB; j++) qb[j] = __builtin_amdgcn_mov_dpp(qv[j], 0x150 + R, 0xF, 0xF, true);
+#pragma unroll
+    for (int j = 0; j < IS_HB; j++) acc[j] = fma(qb[j], kd, acc[j]);
+}
+
+/* Sixteen columns c0 .. c0 + 15 of the chains (FULL), or the first n of
+ * them at the end of a row; k holds the row's elements of those columns. */
+template <bool FULL>
+__device__ __forceinline__ void chain_16(double *acc, const float *qf, const float *k, int n)
+{
+    double qv[IS_HB];
+#pragma unroll
+    for (int j = 0; j < IS_HB; j++) qv[j] = (double)qf[j];
+    if (FULL) {
+        chain_cols2<0>(acc, qv, k[0], k[1]);
+        chain_cols2<2>(acc, qv, k[2], k[3]);
+        chain_cols2<4>(acc, qv, k[4], k[5]);
+        chain_cols2<6>(acc, qv, k[6], k[7]);
+        chain_cols2<8>(acc, qv, k[8], k[9]);
+        chain_cols2<10>(acc, qv, k[10], k[11]);
+        chain_cols2<12>(acc, qv, k[12], k[13]);
+        chain_cols2<14>(acc, qv, k[14], k[15]);
+    } else {
+#define DSV4_COL(R) if (R < n) chain_col<R>(acc, qv, k[R]);
+        DSV4_COL(0) DSV4_COL(1) DSV4_COL(2) DSV4_COL(3) DSV4_COL(4) DSV4_COL(5)
+        DSV4_COL(6) DSV4_COL(7) DSV4_COL(8) DSV4_COL(9) DSV4_COL(10) DSV4_COL(11)
+        DSV4_COL(12) DSV4_COL(13) DSV4_COL(14) DSV4_COL(15)
+#undef DSV4_COL
+    }
+}
+
+template <int KF, int VEC, int HIST>
+__global__ void __launch_bounds__(IS_MAXW * 64)
+k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
+         uint32_t *__restrict__ meta, const float *__restrict__ q, const float *__restrict__ w,
+         int H, int HP, int D, const void *__restrict__ keys,
+         const float *__restrict__ ks, int key_stride, int n, float scale)
+{
+    extern __shared__ double dots[];            /* [64][HP + 1] */
+    constexpr int ES = KF == DSV4_GPU_KV_F32 ? 4 : KF == DSV4_GPU_KV_BF16 ? 2 : 1;
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int nw = blockDim.x >> 6;
+    const int t = blockIdx.x * 64 + lane;
+    const int tr = t < n ? t : n - 1;           /* rows past n compute row n-1 */
+    const int pitch = HP + 1;
+    const float rs = KF == DSV4_GPU_KV_FP8 ? ks[tr] : 1.0f;
+    const unsigned char *row = (const unsigned char *)keys + (size_t)tr * key_stride * ES;
+
+    for (int g = wv; g * IS_HB < HP; g += nw) {
+        const int h0 = g * IS_HB;
+        double acc[IS_HB];
+#pragma unroll
+        for (int j = 0; j < IS_HB; j++) acc[j] = 0.0;
+        /* q for the next 16 columns is loaded while the current 16 compute */
+        float qf[IS_HB], qn[IS_HB];
+        q_cols(qf, q, h0, H, D, 0, lane);
+        if (VEC) {
+            constexpr int CPP = 16 / ES;        /* columns per 16-byte piece */
+            constexpr int BLK = 8 * CPP;        /* columns per batch of loads */
+            for (int c0 = 0; c0 < D; c0 += BLK) {
+                const int np = min(8, (D - c0) / CPP);
+                u32x4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    v[u] = *(const DSV4_GLOBAL u32x4 *)(row + (size_t)(c0 + CPP * min(u, np - 1)) * ES);
+#pragma unroll
+                for (int u16 = 0; u16 < BLK / 16; u16++) {
+                    const int cc = c0 + 16 * u16;
+                    if (cc < D) {
+                        float k[16];
+#pragma unroll
+                        for (int pc = 0; pc < 16 / CPP; pc++)
+                            key_piece<KF>(v[u16 * (16 / CPP) + pc], rs, k + pc * CPP);
+                        q_cols(qn, q, h0, H, D, cc + 16, lane);
+                        if (cc + 16 <= D) chain_16<true>(acc, qf, k, 16);
+                        else              chain_16<false>(acc, qf, k, D - cc);
+#pragma unroll
+                        for (int j = 0; j < IS_HB; j++) qf[j] = qn[j];
+                    }
+                }
+            }
+        } else {
+            for (int c0 = 0; c0 < D; c0 += 16) {
+                float k[16];
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int c = min(c0 + e, D - 1);
+                    if (KF == DSV4_GPU_KV_FP8)
+                        k[e] = dec_e4m3(row[c]) * rs;
+                    else if (KF == DSV4_GPU_KV_BF16)
+                        k[e] = bf16_to_f32(((const uint16_t *)row)[c]);
+                    else
+                        k[e] = ((const float *)row)[c];
+                }
+                q_cols(qn, q, h0, H, D, c0 + 16, lane);
+                if (c0 + 16 <= D) chain_16<true>(acc, qf, k, 16);
+                else              chain_16<false>(acc, qf, k, D - c0);
+#pragma unroll
+                for (int j = 0; j < IS_HB; j++) qf[j] = qn[j];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < IS_HB; j++) dots[lane * pitch + g * IS_HB + j] = acc[j];
+    }
+    __syncthreads();
+    if (wv != 0) return;
+
+    double total = 0.0;
+    for (int hh = 0; hh < H; hh++) {
+        const double d = dots[lane * pitch + hh];
+        if (d > 0.0) {
+            const double prod = d * (double)w[hh];
+            total = total + prod;
+        }
+    }
+    const float tf = (float)total;
+    const float sc = tf * scale;
+    if (t < n) out[t] = sc;
+    if (HIST && blockIdx.x == 0 && lane == 0) meta[MT_ABOVE] = 0u;
+    if (HIST)
+        hist_push_global(hist + (blockIdx.x % TK_SLICES) * TK_BINS, t < n,
+                         fkey(sc) >> 21, lane);
+}
+
+template <int KF, int HIST>
+void launch_iscore(bool vec, int grid, int thr, size_t lds, hipStream_t st,
+                   float *d_out, uint32_t *hist, uint32_t *meta, const float *d_q,
+                   const float *d_w,
+                   int H, int HP, int D, const void *d_keys, const float *d_ks,
+                   int key_stride, int n, float scale)
+{
+    if (vec)
+        hipLaunchKernelGGL((k_iscore<KF, 1, HIST>), dim3(grid), dim3(thr), lds, st, d_out,
+                           hist, meta, d_q, d_w, H, HP, D, d_keys, d_ks, key_stride, n, scale);
     else
-        hipLaunchKernelGGL((k_indexer_score<KF, 0>), dim3(grid), dim3(thr), lds, st,
-                           d_out, d_q, d_w, H, D, d_keys, d_key_scales, key_stride,
-                           n, scale, TL);
+        hipLaunchKernelGGL((k_iscore<KF, 0, HIST>), dim3(grid), dim3(thr), lds, st, d_out,
+                           hist, meta, d_q, d_w, H, HP, D, d_keys, d_ks, key_stride, n, scale);
 }
 
 /* --------------------------------------------------------------- top-k */
 
-constexpr int TK_THREADS = 1024;
-constexpr int TK_WAVES = TK_THREADS / 64;
-constexpr int TK_KMAX = 4096;
+/* Top-k in three passes after the level-1 histogram (built by the score
+ * kernel, or by k_tk_hist for stand-alone scores):
+ *   k_tk_part   many workgroups: the bin B of the k-th largest from the
+ *               histogram; elements of higher bins go to cand[] (any order),
+ *               elements of B to a per-workgroup list in index order;
+ *   k_tk_refine one workgroup over B's list only: levels 2 and 3 give T,
+ *               the exact key of the k-th largest; the list's elements > T
+ *               join cand[], its first need_eq elements == T go straight to
+ *               their output slots;
+ *   k_tk_rank   many workgroups: each candidate's output position is the
+ *               number of candidates ahead of it. */
 
-__device__ __forceinline__ uint32_t fkey(float f)
-{
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7FFFFFFFu) == 0u) u = 0u;        /* -0.0 ties with +0.0 */
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
+constexpr int PT_THREADS = 256;                 /* partition workgroup */
+constexpr int PT_EPT = 4;                       /* elements per thread */
+constexpr int PT_ELEMS = PT_THREADS * PT_EPT;   /* elements per workgroup */
+constexpr int RF_LIST = 4096;                   /* B's list kept in LDS */
+constexpr int RF_GMAX = 4096;                   /* partition workgroups */
+constexpr int TK_NMAX = RF_GMAX * PT_ELEMS;     /* scores per top-k */
 
 __device__ __forceinline__ unsigned long long lanemask_lt(int lane)
 {
     return lane ? (~0ull >> (64 - lane)) : 0ull;
 }
 
-/* Histogram bump for one key per lane (want = this lane's key counts). A few
- * rounds give the leading lane's digit a single aggregated add -- the top
- * digits of similar scores coincide and would otherwise serialise on one
- * LDS bank -- and whatever is left is added lane by lane. */
-__device__ __forceinline__ void hist_add(uint32_t *hist, bool want, uint32_t d,
-                                         int lane)
+/* Level-1 histogram for a stand-alone top-k (the fused path gets it from the
+ * score kernel): top 11 key bits of every score. Also restarts the cand[]
+ * append counter. */
+__global__ void __launch_bounds__(256)
+k_tk_hist(uint32_t *__restrict__ hist, uint32_t *__restrict__ meta,
+          const float *__restrict__ scores, int n)
 {
-    bool todo = want;
-#pragma unroll
-    for (int it = 0; it < 3; ++it) {
-        const unsigned long long pend = __ballot(todo);
-        if (pend == 0ull) return;
-        const int leader = __ffsll((long long)pend) - 1;
-        const uint32_t dl = (uint32_t)__builtin_amdgcn_readlane((int)d, leader);
-        const bool mine = todo && d == dl;
-        const unsigned long long same = __ballot(mine);
-        if (lane == leader) atomicAdd(&hist[dl], (uint32_t)__popcll(same));
-        if (mine) todo = false;
-    }
-    if (todo) atomicAdd(&hist[d], 1u);
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const bool live = i < n;
+    const uint32_t bin = live ? fkey(scores[i]) >> 21 : 0u;
+    if (i == 0) meta[MT_ABOVE] = 0u;
+    hist_push_global(hist + (blockIdx.x % TK_SLICES) * TK_BINS, live, bin,
+                     threadIdx.x & 63);
 }
 
-/* Top-k for n <= TK_THREADS * KPT: thread t holds the keys of elements
- * t, t + 1024, ... in registers (slot m = element / 1024). */
-template <int KPT>
-__global__ void __launch_bounds__(TK_THREADS)
-k_topk(int *__restrict__ idxs, const float *__restrict__ scores, int n, int k)
+/* Descending search over TK_BINS bins, BPT per thread of NT: thread t holds
+ * c[j] = count of bin TK_BINS - 1 - BPT t - j. Finds the bin holding the
+ * krem-th largest element (krem >= 1, at most the total count) and the rank
+ * it has among that bin's elements: res[0] = bin, res[1] = rank (a safe
+ * bin 0 / rank 1 when none fits). Ends on a barrier; callers read res and
+ * pass a barrier before the next call. */
+template <int NT, int BPT>
+__device__ __forceinline__ void tk_find(const uint32_t *c, uint32_t krem,
+                                        uint32_t *wsum, uint32_t *res)
 {
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t cnt[2][KPT][TK_WAVES];      /* per (slot, wave) counts */
-    __shared__ uint32_t sh_prefix, sh_krem;
-    __shared__ unsigned long long sel[TK_KMAX];
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    if (tid == 0) { res[0] = 0u; res[1] = 1u; }
+    uint32_t s = 0u;
+#pragma unroll
+    for (int j = 0; j < BPT; j++) s += c[j];
+    uint32_t inc = s;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += v;
+    }
+    if (lane == 63) wsum[wid] = inc;
+    __syncthreads();
+    uint32_t base = 0u;
+#pragma unroll
+    for (int w = 0; w < NT / 64; w++) base += w < wid ? wsum[w] : 0u;
+    inc += base;
+    const uint32_t exc = inc - s;
+    if (exc < krem && inc >= krem) {
+        uint32_t run = exc;
+#pragma unroll
+        for (int j = 0; j < BPT; j++) {
+            if (run + c[j] >= krem) {
+                res[0] = (uint32_t)(TK_BINS - 1 - BPT * tid - j);
+                res[1] = krem - run;
+                break;
+            }
+            run += c[j];
+        }
+    }
+    __syncthreads();
+}
+
+/* Exclusive prefix over the threads of an NT-thread workgroup (thread
+ * order); *total gets the sum. Ends on a barrier. */
+template <int NT>
+__device__ __forceinline__ uint32_t tk_scan(uint32_t v, uint32_t *wsum, uint32_t *total)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    uint32_t inc = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += t;
+    }
+    if (lane == 63) wsum[wid] = inc;
+    __syncthreads();
+    uint32_t before = 0u, all = 0u;
+#pragma unroll
+    for (int w = 0; w < NT / 64; w++) {
+        const uint32_t x = wsum[w];
+        before += w < wid ? x : 0u;
+        all += x;
+    }
+    *total = all;
+    __syncthreads();
+    return before + inc - v;
+}
+
+/* Partition: workgroup g owns elements [g PT_ELEMS, (g + 1) PT_ELEMS); slot
+ * m of thread t is element g PT_ELEMS + m PT_THREADS + t (coalesced loads,
+ * index order = (slot, wave, lane)). Every workgroup reads the whole sliced
+ * histogram and finds the same B. */
+__global__ void __launch_bounds__(PT_THREADS)
+k_tk_part(unsigned long long *__restrict__ cand, uint32_t *__restrict__ meta,
+          uint32_t *__restrict__ bcnt, unsigned long long *__restrict__ blist,
+          const uint32_t *__restrict__ hist_g, const float *__restrict__ scores,
+          int n, int k)
+{
+    constexpr int NW = PT_THREADS / 64;
+    constexpr int BPT = TK_BINS / PT_THREADS;      /* 8 bins per thread */
+    __shared__ uint32_t wsum[NW], res[2];
+    __shared__ uint32_t scnt[PT_EPT][NW];
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int e0 = blockIdx.x * PT_ELEMS + tid;     /* slot m: e0 + m PT_THREADS */
+    const unsigned long long lt = lanemask_lt(lane);
 
-    uint32_t key[KPT];
+    uint32_t key[PT_EPT];
 #pragma unroll
-    for (int m = 0; m < KPT; m++) {
-        const int i = m * TK_THREADS + tid;
-        key[m] = i < n ? fkey(scores[i]) : 0u;
+    for (int m = 0; m < PT_EPT; m++)
+        key[m] = __float_as_uint(scores[min(e0 + m * PT_THREADS, n - 1)]);
+    const int blo = TK_BINS - BPT * (tid + 1);      /* bins [blo, blo + BPT) */
+    u32x4 hv[TK_SLICES][BPT / 4];
+#pragma unroll
+    for (int s = 0; s < TK_SLICES; s++)
+#pragma unroll
+        for (int q = 0; q < BPT / 4; q++)
+            hv[s][q] = *reinterpret_cast<const u32x4 *>(hist_g + s * TK_BINS + blo + 4 * q);
+#pragma unroll
+    for (int m = 0; m < PT_EPT; m++)
+        key[m] = e0 + m * PT_THREADS < n ? fkey(__uint_as_float(key[m])) : 0u;
+
+    uint32_t c[BPT];                                /* c[j]: bin blo + BPT-1-j */
+#pragma unroll
+    for (int j = 0; j < BPT; j++) c[j] = 0u;
+#pragma unroll
+    for (int s = 0; s < TK_SLICES; s++)
+#pragma unroll
+        for (int q = 0; q < BPT / 4; q++) {
+            c[BPT - 1 - 4 * q] += hv[s][q].x;
+            c[BPT - 2 - 4 * q] += hv[s][q].y;
+            c[BPT - 3 - 4 * q] += hv[s][q].z;
+            c[BPT - 4 - 4 * q] += hv[s][q].w;
+        }
+    tk_find<PT_THREADS, BPT>(c, (uint32_t)k, wsum, res);
+    const uint32_t B = res[0];
+    if (blockIdx.x == 0 && tid == 0) { meta[MT_BIN] = B; meta[MT_KREM] = res[1]; }
+
+    /* elements of higher bins: candidates, appended in any order */
+    unsigned long long ma[PT_EPT];
+    uint32_t na = 0u;
+#pragma unroll
+    for (int m = 0; m < PT_EPT; m++) {
+        ma[m] = __ballot(e0 + m * PT_THREADS < n && (key[m] >> 21) > B);
+        na += (uint32_t)__popcll(ma[m]);
+    }
+    if (na) {
+        uint32_t at = 0u;
+        if (lane == 0) at = atomicAdd(&meta[MT_ABOVE], na);
+        at = (uint32_t)__shfl((int)at, 0, 64);
+#pragma unroll
+        for (int m = 0; m < PT_EPT; m++) {
+            if ((ma[m] >> lane) & 1ull) {
+                const uint32_t pos = at + (uint32_t)__popcll(ma[m] & lt);
+                const uint32_t i = (uint32_t)(e0 + m * PT_THREADS);
+                if (pos < (uint32_t)TK_KMAX)
+                    cand[pos] = ((unsigned long long)key[m] << 32) | (0xFFFFFFFFull - i);
+            }
+            at += (uint32_t)__popcll(ma[m]);
+        }
     }
 
-    /* ---- radix select: T = key of the k-th largest, krem = how many of
-     *      the elements equal to T are taken ---- */
-    uint32_t prefix = 0u, mask = 0u, krem = (uint32_t)k;
-    for (int pass = 0; pass < 4; pass++) {
-        const int shift = 24 - 8 * pass;
-        if (tid < 256) hist[tid] = 0u;
-        __syncthreads();
+    /* elements of B: this workgroup's list, in index order */
+    unsigned long long mb[PT_EPT];
 #pragma unroll
-        for (int m = 0; m < KPT; m++) {
-            const int i = m * TK_THREADS + tid;
-            const bool want = i < n && (key[m] & mask) == prefix;
-            hist_add(hist, want, (key[m] >> shift) & 255u, lane);
-        }
-        __syncthreads();
-        if (tid < 64) {
-            uint32_t c4[4], sum = 0u;
-#pragma unroll
-            for (int q = 0; q < 4; q++) { c4[q] = hist[255 - (lane * 4 + q)]; sum += c4[q]; }
-            uint32_t inc = sum;
-            for (int o = 1; o < 64; o <<= 1) {
-                const uint32_t t = __shfl_up(inc, o, 64);
-                if (lane >= o) inc += t;
-            }
-            const uint32_t exc = inc - sum;
-            if (exc < krem && inc >= krem) {
-                uint32_t run = exc;
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    if (run + c4[q] >= krem) {
-                        const uint32_t digit = 255u - (uint32_t)(lane * 4 + q);
-                        sh_prefix = prefix | (digit << shift);
-                        sh_krem = krem - run;
-                        break;
-                    }
-                    run += c4[q];
-                }
-            }
-        }
-        __syncthreads();
-        prefix = sh_prefix;
-        krem = sh_krem;
-        mask |= 255u << shift;
+    for (int m = 0; m < PT_EPT; m++) {
+        mb[m] = __ballot(e0 + m * PT_THREADS < n && (key[m] >> 21) == B);
+        if (lane == 0) scnt[m][wid] = (uint32_t)__popcll(mb[m]);
     }
-    const uint32_t T = prefix;
-    const uint32_t need_eq = krem;                 /* >= 1 */
+    __syncthreads();
+    uint32_t off[PT_EPT], tot = 0u;
+#pragma unroll
+    for (int m = 0; m < PT_EPT; m++)
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            if (w == wid) off[m] = tot;
+            tot += scnt[m][w];
+        }
+    unsigned long long *mine = blist + (size_t)blockIdx.x * PT_ELEMS;
+#pragma unroll
+    for (int m = 0; m < PT_EPT; m++)
+        if ((mb[m] >> lane) & 1ull)
+            mine[off[m] + (uint32_t)__popcll(mb[m] & lt)] =
+                ((unsigned long long)key[m] << 32) | (uint32_t)(e0 + m * PT_THREADS);
+    if (tid == 0) bcnt[blockIdx.x] = tot;
+}
+
+/* Refine, one workgroup. B's elements, in index order, are the lists of the
+ * G partition workgroups one after another (entry j of the whole list is in
+ * the list of the workgroup w with pfx[w] <= j < pfx[w + 1]). The list is
+ * staged in LDS when it fits, read from global memory otherwise. Also clears
+ * the level-1 histogram for the next top-k. */
+__global__ void __launch_bounds__(TK_THREADS)
+k_tk_refine(int *__restrict__ idxs, unsigned long long *__restrict__ cand,
+            uint32_t *__restrict__ meta, const uint32_t *__restrict__ bcnt,
+            const unsigned long long *__restrict__ blist,
+            uint32_t *__restrict__ hist_g, int G, int k)
+{
+    __shared__ uint32_t hist[TK_BINS];
+    __shared__ uint32_t pfx[RF_GMAX + 1];
+    __shared__ unsigned long long lst[RF_LIST];
+    __shared__ uint32_t wsum[TK_WAVES], res[2];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const unsigned long long lt = lanemask_lt(lane);
+
+    for (int i = tid; i < TK_SLICES * TK_BINS / 4; i += TK_THREADS)
+        reinterpret_cast<u32x4 *>(hist_g)[i] = u32x4{0u, 0u, 0u, 0u};
+    const uint32_t krem1 = meta[MT_KREM], c_above = meta[MT_ABOVE];
+    const uint32_t B = meta[MT_BIN];
+
+    /* prefix of the list lengths: thread t takes entries 4t .. 4t + 3 */
+    uint32_t v[4], s4 = 0u;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        v[q] = 4 * tid + q < G ? bcnt[4 * tid + q] : 0u;
+        s4 += v[q];
+    }
+    uint32_t nb;
+    uint32_t run = tk_scan<TK_THREADS>(s4, wsum, &nb);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if (4 * tid + q < G) pfx[4 * tid + q] = run;
+        run += v[q];
+    }
+    if (tid == 0) pfx[G] = nb;
+    __syncthreads();
+    const bool listed = nb <= (uint32_t)RF_LIST;
+
+    auto gaddr = [&](uint32_t j) -> uint32_t {     /* j -> position in blist */
+        int lo = 0, hi = G - 1;                     /* last w with pfx[w] <= j */
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (pfx[mid] <= j) lo = mid; else hi = mid - 1;
+        }
+        return (uint32_t)lo * PT_ELEMS + (j - pfx[lo]);
+    };
+    auto ent = [&](uint32_t j) -> unsigned long long {
+        return listed ? lst[j] : blist[gaddr(j)];
+    };
+    if (listed) {
+        for (uint32_t j0 = 0; j0 < nb; j0 += 4 * TK_THREADS) {
+            unsigned long long e[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t j = j0 + q * TK_THREADS + tid;
+                e[q] = j < nb ? blist[gaddr(j)] : 0ull;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t j = j0 + q * TK_THREADS + tid;
+                if (j < nb) lst[j] = e[q];
+            }
+        }
+    }
+    hist[2 * tid] = 0u;
+    hist[2 * tid + 1] = 0u;
+    __syncthreads();
+
+    /* ---- level 2: bits 20..10 ---- */
+    for (uint32_t j = tid; j < nb; j += TK_THREADS)
+        atomicAdd(&hist[(uint32_t)(ent(j) >> 42) & 2047u], 1u);
+    __syncthreads();
+    uint32_t c[2] = {hist[TK_BINS - 1 - 2 * tid], hist[TK_BINS - 2 - 2 * tid]};
+    tk_find<TK_THREADS, 2>(c, krem1, wsum, res);
+    const uint32_t P22 = (B << 11) | res[0], krem2 = res[1];
+
+    /* ---- level 3: bits 9..0 ---- */
+    hist[2 * tid] = 0u;
+    hist[2 * tid + 1] = 0u;
+    __syncthreads();
+    for (uint32_t j = tid; j < nb; j += TK_THREADS) {
+        const uint32_t key = (uint32_t)(ent(j) >> 32);
+        if ((key >> 10) == P22) atomicAdd(&hist[key & 1023u], 1u);
+    }
+    __syncthreads();
+    c[0] = hist[TK_BINS - 1 - 2 * tid];
+    c[1] = hist[TK_BINS - 2 - 2 * tid];
+    tk_find<TK_THREADS, 2>(c, krem2, wsum, res);
+    const uint32_t T = (P22 << 10) | res[0];
+    /* need_eq is in [1, k] for a histogram that matches the scores; the
+     * clamp keeps every write below in bounds whatever the histogram held. */
+    const uint32_t need_eq = min(max(res[1], 1u), (uint32_t)k);
     const uint32_t c_gt = (uint32_t)k - need_eq;
 
-    /* ---- compaction in index order: element index order is (slot, wave,
-     *      lane), so per-(slot, wave) counts scanned in that order give each
-     *      element its position ---- */
-    unsigned long long mgt[KPT], meq[KPT];
-#pragma unroll
-    for (int m = 0; m < KPT; m++) {
-        const int i = m * TK_THREADS + tid;
-        mgt[m] = __ballot(i < n && key[m] > T);
-        meq[m] = __ballot(i < n && key[m] == T);
-        if (lane == 0) {
-            cnt[0][m][wid] = (uint32_t)__popcll(mgt[m]);
-            cnt[1][m][wid] = (uint32_t)__popcll(meq[m]);
+    /* ---- B's elements > T join cand[]; the first need_eq == T, in index
+     *      order, are output directly ---- */
+    uint32_t pg = c_above, pe = 0u;
+    for (uint32_t j0 = 0; j0 < nb; j0 += TK_THREADS) {
+        const uint32_t j = j0 + tid;
+        const unsigned long long e = j < nb ? ent(j) : 0ull;
+        const uint32_t key = (uint32_t)(e >> 32), idx = (uint32_t)e;
+        const bool gt = j < nb && key > T, eq = j < nb && key == T;
+        const unsigned long long mg = __ballot(gt), me = __ballot(eq);
+        const uint32_t cnt = (uint32_t)__popcll(mg) | ((uint32_t)__popcll(me) << 16);
+        uint32_t all;
+        const uint32_t before = tk_scan<TK_THREADS>(lane == 0 ? cnt : 0u, wsum, &all);
+        const uint32_t wb = (uint32_t)__shfl((int)before, 0, 64);
+        if (gt) {
+            const uint32_t pos = pg + (wb & 0xFFFFu) + (uint32_t)__popcll(mg & lt);
+            if (pos < c_gt)
+                cand[pos] = ((unsigned long long)key << 32) | (0xFFFFFFFFull - idx);
+        } else if (eq) {
+            const uint32_t pos = pe + (wb >> 16) + (uint32_t)__popcll(me & lt);
+            if (pos < need_eq) idxs[c_gt + pos] = (int)idx;
         }
+        pg += all & 0xFFFFu;
+        pe += all >> 16;
     }
-    __syncthreads();
-    if (wid < 2) {                                  /* wave 0: gt, wave 1: eq */
-        uint32_t *c = &cnt[wid][0][0];
-        constexpr int NE = KPT * TK_WAVES;          /* entries, slot-major */
-        constexpr int PER = (NE + 63) / 64;
-        uint32_t v[PER], sum = 0u;
-#pragma unroll
-        for (int q = 0; q < PER; q++) {
-            const int e = lane * PER + q;
-            v[q] = e < NE ? c[e] : 0u;
-            sum += v[q];
-        }
-        uint32_t inc = sum;
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t t = __shfl_up(inc, o, 64);
-            if (lane >= o) inc += t;
-        }
-        uint32_t run = inc - sum;
-#pragma unroll
-        for (int q = 0; q < PER; q++) {
-            const int e = lane * PER + q;
-            if (e < NE) c[e] = run;
-            run += v[q];
-        }
-    }
-    __syncthreads();
-    const unsigned long long lt = lanemask_lt(lane);
-#pragma unroll
-    for (int m = 0; m < KPT; m++) {
-        const int i = m * TK_THREADS + tid;
-        if ((mgt[m] >> lane) & 1ull) {
-            const uint32_t pos = cnt[0][m][wid] + (uint32_t)__popcll(mgt[m] & lt);
-            if (pos < (uint32_t)TK_KMAX)
-                sel[pos] = ((unsigned long long)key[m] << 32)
-                         | (unsigned long long)(0xFFFFFFFFu - (uint32_t)i);
-        } else if ((meq[m] >> lane) & 1ull) {
-            const uint32_t pos = cnt[1][m][wid] + (uint32_t)__popcll(meq[m] & lt);
-            if (pos < need_eq) idxs[c_gt + pos] = i;
-        }
-    }
-    uint32_t p2 = 1u;
-    while (p2 < c_gt) p2 <<= 1;
-    for (uint32_t i = c_gt + tid; i < p2; i += TK_THREADS) sel[i] = 0ull;
-    __syncthreads();
-
-    /* ---- bitonic sort of sel[0, p2), descending (key desc, index asc) ---- */
-    if (p2 <= 2u * TK_THREADS) {
-        /* Thread t owns elements a = 128*wave + lane and b = a + 64 of its
-         * wave's 128-element block: strides < 64 are lane shuffles, stride
-         * 64 is a register swap, strides >= 128 go through LDS. */
-        const uint32_t ea = 128u * wid + lane, eb = ea + 64u;
-        const bool act = ea < p2;
-        unsigned long long a = act ? sel[ea] : 0ull;
-        unsigned long long b = (eb < p2) ? sel[eb] : 0ull;
-        for (uint32_t size = 2; size <= p2; size <<= 1) {
-            for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-                if (stride >= 128) {
-                    if (act) sel[ea] = a;
-                    if (eb < p2) sel[eb] = b;
-                    __syncthreads();
-                    for (uint32_t t = tid; t < p2 / 2; t += TK_THREADS) {
-                        const uint32_t lo = 2 * t - (t & (stride - 1));
-                        const uint32_t hi = lo + stride;
-                        const bool desc = ((lo & size) == 0);
-                        const unsigned long long x = sel[lo], y = sel[hi];
-                        if (desc ? (x < y) : (x > y)) { sel[lo] = y; sel[hi] = x; }
-                    }
-                    __syncthreads();
-                    a = act ? sel[ea] : 0ull;
-                    b = (eb < p2) ? sel[eb] : 0ull;
-                } else if (stride == 64) {
-                    const bool desc = ((ea & size) == 0);
-                    if (desc ? (a < b) : (a > b)) { const unsigned long long t = a; a = b; b = t; }
-                } else {
-                    /* partner = element ^ stride, same register, lane ^ stride */
-                    const unsigned long long pa =
-                        ((unsigned long long)(uint32_t)__shfl_xor((int)(a >> 32), (int)stride, 64) << 32)
-                        | (uint32_t)__shfl_xor((int)(uint32_t)a, (int)stride, 64);
-                    const unsigned long long pb =
-                        ((unsigned long long)(uint32_t)__shfl_xor((int)(b >> 32), (int)stride, 64) << 32)
-                        | (uint32_t)__shfl_xor((int)(uint32_t)b, (int)stride, 64);
-                    const bool lower = (lane & stride) == 0;
-                    {
-                        const uint32_t lo = lower ? ea : (ea ^ stride);
-                        const bool desc = ((lo & size) == 0);
-                        /* the lower element keeps the larger when descending */
-                        const bool keep_big = (lower == desc);
-                        a = keep_big ? (a > pa ? a : pa) : (a < pa ? a : pa);
-                    }
-                    {
-                        const uint32_t lo = lower ? eb : (eb ^ stride);
-                        const bool desc = ((lo & size) == 0);
-                        const bool keep_big = (lower == desc);
-                        b = keep_big ? (b > pb ? b : pb) : (b < pb ? b : pb);
-                    }
-                }
-            }
-        }
-        if (act) sel[ea] = a;
-        if (eb < p2) sel[eb] = b;
-        __syncthreads();
-    } else {
-        for (uint32_t size = 2; size <= p2; size <<= 1) {
-            for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-                for (uint32_t t = tid; t < p2 / 2; t += TK_THREADS) {
-                    const uint32_t lo = 2 * t - (t & (stride - 1));
-                    const uint32_t hi = lo + stride;
-                    const bool desc = ((lo & size) == 0);
-                    const unsigned long long x = sel[lo], y = sel[hi];
-                    if (desc ? (x < y) : (x > y)) { sel[lo] = y; sel[hi] = x; }
-                }
-                __syncthreads();
-            }
-        }
-    }
-    for (uint32_t i = tid; i < c_gt; i += TK_THREADS)
-        idxs[i] = (int)(0xFFFFFFFFu - (uint32_t)(sel[i] & 0xFFFFFFFFull));
+    if (tid == 0) meta[MT_CGT] = c_gt;
 }
 
-/* Any n: the same selection reading the scores from global memory on every
- * pass (coalesced), compaction by slot with a count array in dynamic LDS. */
-__global__ void __launch_bounds__(TK_THREADS)
-k_topk_big(int *__restrict__ idxs, const float *__restrict__ scores, int n, int k)
+/* Final order of the > T elements: composite e goes to position #{f :
+ * cand[f] > cand[e]} (composites are distinct), which is the order by key
+ * descending, index ascending. RK_TPE threads share an element. */
+constexpr int RK_TPE = 16;
+constexpr int RK_EPW = 256 / RK_TPE;                 /* elements per workgroup */
+
+__global__ void __launch_bounds__(256)
+k_tk_rank(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
+          const uint32_t *__restrict__ meta)
 {
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t sh_prefix, sh_krem, sh_base[2];
-    __shared__ uint32_t wcnt[2][TK_WAVES];
-    __shared__ unsigned long long sel[TK_KMAX];
-
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int slots = (n + TK_THREADS - 1) / TK_THREADS;
-
-    uint32_t prefix = 0u, mask = 0u, krem = (uint32_t)k;
-    for (int pass = 0; pass < 4; pass++) {
-        const int shift = 24 - 8 * pass;
-        if (tid < 256) hist[tid] = 0u;
-        __syncthreads();
-        for (int m = 0; m < slots; m++) {
-            const int i = m * TK_THREADS + tid;
-            const uint32_t key = i < n ? fkey(scores[i]) : 0u;
-            const bool want = i < n && (key & mask) == prefix;
-            hist_add(hist, want, (key >> shift) & 255u, lane);
-        }
-        __syncthreads();
-        if (tid < 64) {
-            uint32_t c4[4], sum = 0u;
-            for (int q = 0; q < 4; q++) { c4[q] = hist[255 - (lane * 4 + q)]; sum += c4[q]; }
-            uint32_t inc = sum;
-            for (int o = 1; o < 64; o <<= 1) {
-                const uint32_t t = __shfl_up(inc, o, 64);
-                if (lane >= o) inc += t;
-            }
-            const uint32_t exc = inc - sum;
-            if (exc < krem && inc >= krem) {
-                uint32_t run = exc;
-                for (int q = 0; q < 4; q++) {
-                    if (run + c4[q] >= krem) {
-                        sh_prefix = prefix | ((255u - (uint32_t)(lane * 4 + q)) << shift);
-                        sh_krem = krem - run;
-                        break;
-                    }
-                    run += c4[q];
-                }
-            }
-        }
-        __syncthreads();
-        prefix = sh_prefix;
-        krem = sh_krem;
-        mask |= 255u << shift;
+    __shared__ unsigned long long cs[TK_KMAX];
+    const uint32_t c = min(meta[MT_CGT], (uint32_t)TK_KMAX);
+    const uint32_t e0 = blockIdx.x * RK_EPW;
+    if (e0 >= c) return;                            /* the whole workgroup */
+    const int tid = threadIdx.x;
+    for (uint32_t i0 = 0; i0 < c; i0 += 8 * 256) {   /* eight loads in flight */
+        unsigned long long v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = cand[min(i0 + u * 256 + tid, c - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (i0 + u * 256 + tid < c) cs[i0 + u * 256 + tid] = v[u];
     }
-    const uint32_t T = prefix, need_eq = krem, c_gt = (uint32_t)k - need_eq;
-    if (tid == 0) { sh_base[0] = 0u; sh_base[1] = 0u; }
     __syncthreads();
-    const unsigned long long lt = lanemask_lt(lane);
-    for (int m = 0; m < slots; m++) {
-        const int i = m * TK_THREADS + tid;
-        const uint32_t key = i < n ? fkey(scores[i]) : 0u;
-        const unsigned long long g = __ballot(i < n && key > T);
-        const unsigned long long e = __ballot(i < n && key == T);
-        if (lane == 0) { wcnt[0][wid] = (uint32_t)__popcll(g); wcnt[1][wid] = (uint32_t)__popcll(e); }
-        __syncthreads();
-        uint32_t og = sh_base[0], oe = sh_base[1];
-        for (int w = 0; w < wid; w++) { og += wcnt[0][w]; oe += wcnt[1][w]; }
-        if ((g >> lane) & 1ull) {
-            const uint32_t pos = og + (uint32_t)__popcll(g & lt);
-            if (pos < (uint32_t)TK_KMAX)
-                sel[pos] = ((unsigned long long)key << 32)
-                         | (unsigned long long)(0xFFFFFFFFu - (uint32_t)i);
-        } else if ((e >> lane) & 1ull) {
-            const uint32_t pos = oe + (uint32_t)__popcll(e & lt);
-            if (pos < need_eq) idxs[c_gt + pos] = i;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            uint32_t sg = 0u, se = 0u;
-            for (int w = 0; w < TK_WAVES; w++) { sg += wcnt[0][w]; se += wcnt[1][w]; }
-            sh_base[0] += sg;
-            sh_base[1] += se;
-        }
-        __syncthreads();
-    }
-    uint32_t p2 = 1u;
-    while (p2 < c_gt) p2 <<= 1;
-    for (uint32_t i = c_gt + tid; i < p2; i += TK_THREADS) sel[i] = 0ull;
-    __syncthreads();
-    for (uint32_t size = 2; size <= p2; size <<= 1) {
-        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            for (uint32_t t = tid; t < p2 / 2; t += TK_THREADS) {
-                const uint32_t lo = 2 * t - (t & (stride - 1));
-                const uint32_t hi = lo + stride;
-                const bool desc = ((lo & size) == 0);
-                const unsigned long long x = sel[lo], y = sel[hi];
-                if (desc ? (x < y) : (x > y)) { sel[lo] = y; sel[hi] = x; }
-            }
-            __syncthreads();
-        }
-    }
-    for (uint32_t i = tid; i < c_gt; i += TK_THREADS)
-        idxs[i] = (int)(0xFFFFFFFFu - (uint32_t)(sel[i] & 0xFFFFFFFFull));
+    const uint32_t e = e0 + tid / RK_TPE, sub = tid % RK_TPE;
+    const unsigned long long mine = e < c ? cs[e] : ~0ull;
+    uint32_t r = 0u;
+    uint32_t f = sub;
+    for (; f + 3 * RK_TPE < c; f += 4 * RK_TPE)
+        r += (cs[f] > mine ? 1u : 0u) + (cs[f + RK_TPE] > mine ? 1u : 0u) +
+             (cs[f + 2 * RK_TPE] > mine ? 1u : 0u) + (cs[f + 3 * RK_TPE] > mine ? 1u : 0u);
+    for (; f < c; f += RK_TPE) r += cs[f] > mine ? 1u : 0u;
+#pragma unroll
+    for (int o = 1; o < RK_TPE; o <<= 1) r += __shfl_xor(r, o, 64);
+    if (sub == 0 && e < c) idxs[r] = (int)(0xFFFFFFFFu - (uint32_t)mine);
 }
 
 /* ----------------------------------------------------- sparse attention */
@@ -786,11 +950,35 @@ int attn_split_rows(int kv_fmt, int d_qk, int d_v, int *rowb_out, size_t *lds_ou
 
 } // namespace
 
+/* Index scratch: [hist: TK_SLICES x TK_BINS u32][meta: 256 B]
+ * [cand: TK_KMAX u64][bcnt: RF_GMAX u32][blist: G x PT_ELEMS u64]. The
+ * histogram and the cand[] counter must be zero when a top-k starts from
+ * them; every top-k leaves the histogram zero, and the score kernel (or
+ * k_tk_hist) restarts the counter. */
+static const size_t IX_HIST = 0;
+static const size_t IX_META = IX_HIST + sizeof(uint32_t) * TK_SLICES * TK_BINS;
+static const size_t IX_CAND = IX_META + 256;
+static const size_t IX_BCNT = IX_CAND + sizeof(unsigned long long) * TK_KMAX;
+static const size_t IX_BLIST = IX_BCNT + sizeof(uint32_t) * RF_GMAX;
+
+static int ix_heads_padded(int H) { return (H + IS_HB - 1) / IS_HB * IS_HB; }
+
+size_t dsv4_index_scratch_bytes(int n)
+{
+    const size_t g = n > 0 ? ((size_t)n + PT_ELEMS - 1) / PT_ELEMS : 1;
+    return IX_BLIST + sizeof(unsigned long long) * PT_ELEMS * g;
+}
+
+int dsv4_topk_takes_hist(int n, int k)
+{
+    return k > 0 && n >= k && n <= TK_NMAX && k <= TK_KMAX;
+}
+
 int dsv4_indexer_score_launch(float *d_out, const float *d_q, const float *d_w,
                               int H, int D, const void *d_keys,
                               const float *d_key_scales, int key_fmt,
-                              int key_stride, int n, float scale,
-                              hipStream_t st)
+                              int key_stride, int n, float scale, void *scratch,
+                              int with_hist, hipStream_t st)
 {
     if (H <= 0 || D <= 0 || n < 0 || key_stride < D || H > 256) {
         DSV4_ERR("indexer score: bad shape H %d D %d n %d stride %d",
@@ -801,64 +989,95 @@ int dsv4_indexer_score_launch(float *d_out, const float *d_q, const float *d_w,
         DSV4_ERR("indexer score: FP8 keys need row scales");
         return -1;
     }
-    if (n == 0) return 0;
-    /* About 128 threads per workgroup; q widened in LDS when it fits. */
-    int TL = 128 / H > 0 ? 128 / H : 1;
-    size_t lds = 0;
-    bool qd = true;
-    for (;; TL = TL > 1 ? TL / 2 : 0) {
-        if (TL == 0) {
-            DSV4_ERR("indexer score: H %d x D %d does not fit in LDS", H, D);
-            return -1;
-        }
-        const size_t P = (size_t)TL * IS_CH;
-        const size_t base = 8 * (P * H + P * (D + 1));
-        if (base + 8 * (size_t)H * (D + 1) <= 64 * 1024) { qd = true; lds = base + 8 * (size_t)H * (D + 1); break; }
-        if (base + 4 * (size_t)H * (D + 1) <= 64 * 1024) { qd = false; lds = base + 4 * (size_t)H * (D + 1); break; }
-    }
-    const int P = TL * IS_CH;
-    const int thr = ((H * TL + 63) / 64) * 64;
-    const int grid = (n + P - 1) / P;
-    switch (key_fmt) {
-    case DSV4_GPU_KV_F32:
-        launch_score<DSV4_GPU_KV_F32>(qd, grid, thr, lds, st, d_out, d_q, d_w, H, D,
-                                      d_keys, d_key_scales, key_stride, n, scale, TL);
-        break;
-    case DSV4_GPU_KV_BF16:
-        launch_score<DSV4_GPU_KV_BF16>(qd, grid, thr, lds, st, d_out, d_q, d_w, H, D,
-                                       d_keys, d_key_scales, key_stride, n, scale, TL);
-        break;
-    case DSV4_GPU_KV_FP8:
-        launch_score<DSV4_GPU_KV_FP8>(qd, grid, thr, lds, st, d_out, d_q, d_w, H, D,
-                                      d_keys, d_key_scales, key_stride, n, scale, TL);
-        break;
-    default:
+    if (key_fmt != DSV4_GPU_KV_FP8 && key_fmt != DSV4_GPU_KV_BF16 &&
+        key_fmt != DSV4_GPU_KV_F32) {
         DSV4_ERR("indexer score: unknown key format %d", key_fmt);
         return -1;
     }
+    if (n == 0) return 0;
+    const int HP = ix_heads_padded(H);
+    const int groups = HP / IS_HB;
+    const int nw = groups < IS_MAXW ? groups : IS_MAXW;
+    const size_t lds = sizeof(double) * 64 * (size_t)(HP + 1);
+    if (lds > dsv4_lds_limit()) {
+        DSV4_ERR("indexer score: %d heads do not fit in LDS", H);
+        return -1;
+    }
+    static bool lds_opted = false;
+    if (!lds_opted) {
+        const int cap = (int)dsv4_lds_limit();
+        const void *fns[] = {
+            (const void *)k_iscore<DSV4_GPU_KV_FP8, 1, 0>, (const void *)k_iscore<DSV4_GPU_KV_FP8, 1, 1>,
+            (const void *)k_iscore<DSV4_GPU_KV_FP8, 0, 0>, (const void *)k_iscore<DSV4_GPU_KV_FP8, 0, 1>,
+            (const void *)k_iscore<DSV4_GPU_KV_BF16, 1, 0>, (const void *)k_iscore<DSV4_GPU_KV_BF16, 1, 1>,
+            (const void *)k_iscore<DSV4_GPU_KV_BF16, 0, 0>, (const void *)k_iscore<DSV4_GPU_KV_BF16, 0, 1>,
+            (const void *)k_iscore<DSV4_GPU_KV_F32, 1, 0>, (const void *)k_iscore<DSV4_GPU_KV_F32, 1, 1>,
+            (const void *)k_iscore<DSV4_GPU_KV_F32, 0, 0>, (const void *)k_iscore<DSV4_GPU_KV_F32, 0, 1>};
+        for (const void *f : fns)
+            (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, cap);
+        (void)hipGetLastError();
+        lds_opted = true;
+    }
+    uint32_t *hist = with_hist ? (uint32_t *)((char *)scratch + IX_HIST) : nullptr;
+    uint32_t *meta = with_hist ? (uint32_t *)((char *)scratch + IX_META) : nullptr;
+
+    const int es = key_fmt == DSV4_GPU_KV_F32 ? 4 : key_fmt == DSV4_GPU_KV_BF16 ? 2 : 1;
+    const bool vec = ((size_t)D * es) % 16 == 0 && ((size_t)key_stride * es) % 16 == 0 &&
+                     ((uintptr_t)d_keys & 15) == 0;
+    const int grid = (n + 63) / 64;
+    const int thr = 64 * nw;
+#define DSV4_ISCORE(KF)                                                                 \
+    do {                                                                                \
+        if (with_hist)                                                                  \
+            launch_iscore<KF, 1>(vec, grid, thr, lds, st, d_out, hist, meta, d_q, d_w, H, HP, \
+                                 D, d_keys, d_key_scales, key_stride, n, scale);        \
+        else                                                                            \
+            launch_iscore<KF, 0>(vec, grid, thr, lds, st, d_out, hist, meta, d_q, d_w, H, HP, \
+                                 D, d_keys, d_key_scales, key_stride, n, scale);        \
+    } while (0)
+    if (key_fmt == DSV4_GPU_KV_FP8) DSV4_ISCORE(DSV4_GPU_KV_FP8);
+    else if (key_fmt == DSV4_GPU_KV_BF16) DSV4_ISCORE(DSV4_GPU_KV_BF16);
+    else DSV4_ISCORE(DSV4_GPU_KV_F32);
+#undef DSV4_ISCORE
     HIP_OK(hipGetLastError(), "indexer score launch");
     return 0;
 }
 
 int dsv4_topk_launch(int *d_idxs, const float *d_scores, int n, int k,
-                     hipStream_t st)
+                     void *scratch, int hist_ready, hipStream_t st)
 {
     if (k > n) k = n;
     if (k <= 0) return 0;
-    if (k > TK_KMAX) {
-        DSV4_ERR("topk: k %d exceeds the supported %d", k, TK_KMAX);
+    if (k > TK_KMAX || n > TK_NMAX) {
+        DSV4_ERR("topk: k %d of n %d exceeds the supported %d of %d", k, n,
+                 TK_KMAX, TK_NMAX);
         return -1;
     }
-    if (n <= 8 * TK_THREADS)
-        hipLaunchKernelGGL((k_topk<8>), dim3(1), dim3(TK_THREADS), 0, st, d_idxs,
-                           d_scores, n, k);
-    else if (n <= 32 * TK_THREADS)
-        hipLaunchKernelGGL((k_topk<32>), dim3(1), dim3(TK_THREADS), 0, st, d_idxs,
-                           d_scores, n, k);
-    else
-        hipLaunchKernelGGL(k_topk_big, dim3(1), dim3(TK_THREADS), 0, st, d_idxs,
-                           d_scores, n, k);
-    HIP_OK(hipGetLastError(), "topk launch");
+    if (hist_ready && !dsv4_topk_takes_hist(n, k)) {
+        DSV4_ERR("topk: a level-1 histogram was built for n %d k %d", n, k);
+        return -1;
+    }
+    char *sb = (char *)scratch;
+    uint32_t *hist = (uint32_t *)(sb + IX_HIST);
+    uint32_t *meta = (uint32_t *)(sb + IX_META);
+    unsigned long long *cand = (unsigned long long *)(sb + IX_CAND);
+    uint32_t *bcnt = (uint32_t *)(sb + IX_BCNT);
+    unsigned long long *blist = (unsigned long long *)(sb + IX_BLIST);
+    const int G = (n + PT_ELEMS - 1) / PT_ELEMS;
+    if (!hist_ready) {
+        hipLaunchKernelGGL(k_tk_hist, dim3((n + 255) / 256), dim3(256), 0, st, hist, meta,
+                           d_scores, n);
+        HIP_OK(hipGetLastError(), "topk histogram launch");
+    }
+    hipLaunchKernelGGL(k_tk_part, dim3(G), dim3(PT_THREADS), 0, st, cand, meta, bcnt,
+                       blist, hist, d_scores, n, k);
+    HIP_OK(hipGetLastError(), "topk partition launch");
+    hipLaunchKernelGGL(k_tk_refine, dim3(1), dim3(TK_THREADS), 0, st, d_idxs, cand, meta,
+                       bcnt, blist, hist, G, k);
+    HIP_OK(hipGetLastError(), "topk refine launch");
+    hipLaunchKernelGGL(k_tk_rank, dim3((k + RK_EPW - 1) / RK_EPW), dim3(256), 0, st,
+                       d_idxs, cand, meta);
+    HIP_OK(hipGetLastError(), "topk rank launch");
     return 0;
 }
 

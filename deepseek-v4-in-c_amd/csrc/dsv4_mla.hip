@@ -56,10 +56,11 @@ __device__ __forceinline__ float key_at(const void *keys, const float *ks,
 /* ------------------------------------------------------- indexer score */
 
 /* Score kernel geometry: lane = key row, a wave runs the chains of IS_HB
- * heads for its 64 rows, and the waves of a workgroup cover the heads
- * (looping when there are more than IS_MAXW groups). */
+ * heads for its 64 rows; a workgroup of up to IS_MAXW waves covers all the
+ * heads of one or more 64-row blocks (its waves loop over head groups when
+ * there are more groups than waves). */
 constexpr int IS_HB = 8;                        /* heads per wave */
-constexpr int IS_MAXW = 8;                      /* waves per workgroup */
+constexpr int IS_MAXW = 4;                      /* waves per workgroup */
 
 /* Top-k constants the score kernel shares: its histogram is the first level
  * of the selection. */
@@ -134,72 +135,60 @@ __device__ __forceinline__ void key_piece(u32x4 v, float rs, float *k)
 
 /* q of the wave's IS_HB heads for columns c0 .. c0 + 15, one column per
  * lane of each 16-lane row (every row holds the same values): lane l gets
- * q[g*IS_HB + j][c0 + l % 16]. Heads past H read as zero, columns past D as
- * the last column. */
+ * q[h0 + j][c0 + l % 16]. Heads past H read head H-1, columns past D the
+ * last column. */
 __device__ __forceinline__ void q_cols(float *dst, const float *q, int h0, int H,
                                        int D, int c0, int lane)
 {
     const int c = min(c0 + (lane & 15), D - 1);
+    /* unconditional loads (clamped head; chain_16 zeroes heads past H): a
+     * load under a branch would make the next wait cover every load in
+     * flight */
 #pragma unroll
-    for (int j = 0; j < IS_HB; j++)
-        dst[j] = h0 + j < H ? q[(size_t)(h0 + j) * D + c] : 0.0f;
+    for (int j = 0; j < IS_HB; j++) dst[j] = q[(size_t)min(h0 + j, H - 1) * D + c];
 }
 
-/* Chain steps for columns c0 + R and c0 + R + 1 of every head of the group:
- * q[.][c0 + R] reaches all lanes by a row broadcast of lane R. The
- * broadcasts are issued together, then the fmas, so neither waits on the
- * other. */
+/* acc += q(lane R of this 16-lane row) * kd: the broadcast is the DPP
+ * row_newbcast form of the fma's first operand (one instruction). q must
+ * not have been written by a VALU instruction in the two issue slots before
+ * (DPP source hazard); chain_16 separates them with an s_nop, since the
+ * compiler does not look inside this asm for hazards. */
 template <int R>
-__device__ __forceinline__ void chain_cols2(double *acc, const double *qv, float k0, float k1)
+__device__ __forceinline__ void fma_bcast(double &acc, double q, double kd)
 {
-    const double kd0 = (double)k0, kd1 = (double)k1;
-    double qb0[IS_HB], qb1[IS_HB];
-#pragma unroll
-    for (int j = 0; j < IS_HB; j++) {
-        qb0[j] = __builtin_amdgcn_mov_dpp(qv[j], 0x150 + R, 0xF, 0xF, true);
-        qb1[j] = __builtin_amdgcn_mov_dpp(qv[j], 0x150 + R + 1, 0xF, 0xF, true);
-    }
-#pragma unroll
-    for (int j = 0; j < IS_HB; j++) acc[j] = fma(qb0[j], kd0, acc[j]);
-#pragma unroll
-    for (int j = 0; j < IS_HB; j++) acc[j] = fma(qb1[j], kd1, acc[j]);
+    asm("v_fmac_f64_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+        : "+v"(acc) : "v"(q), "v"(kd), "n"(R));
 }
 
+/* Chain steps for column c0 + R of every head of the group: q[.][c0 + R]
+ * reaches all lanes by the row broadcast of lane R. */
 template <int R>
 __device__ __forceinline__ void chain_col(double *acc, const double *qv, float kf)
 {
     const double kd = (double)kf;
-    double qb[IS_HB];
 #pragma unroll
-    for (int j = 0; j < IS_HB; j++) qb[j] = __builtin_amdgcn_mov_dpp(qv[j], 0x150 + R, 0xF, 0xF, true);
-#pragma unroll
-    for (int j = 0; j < IS_HB; j++) acc[j] = fma(qb[j], kd, acc[j]);
+    for (int j = 0; j < IS_HB; j++) fma_bcast<R>(acc[j], qv[j], kd);
 }
 
 /* Sixteen columns c0 .. c0 + 15 of the chains (FULL), or the first n of
- * them at the end of a row; k holds the row's elements of those columns. */
+ * them at the end of a row; k holds the row's elements of those columns and
+ * nh the number of the group's heads below H (q of the others is zero). */
 template <bool FULL>
-__device__ __forceinline__ void chain_16(double *acc, const float *qf, const float *k, int n)
+__device__ __forceinline__ void chain_16(double *acc, const float *qf, const float *k, int n,
+                                         int nh)
 {
     double qv[IS_HB];
 #pragma unroll
-    for (int j = 0; j < IS_HB; j++) qv[j] = (double)qf[j];
-    if (FULL) {
-        chain_cols2<0>(acc, qv, k[0], k[1]);
-        chain_cols2<2>(acc, qv, k[2], k[3]);
-        chain_cols2<4>(acc, qv, k[4], k[5]);
-        chain_cols2<6>(acc, qv, k[6], k[7]);
-        chain_cols2<8>(acc, qv, k[8], k[9]);
-        chain_cols2<10>(acc, qv, k[10], k[11]);
-        chain_cols2<12>(acc, qv, k[12], k[13]);
-        chain_cols2<14>(acc, qv, k[14], k[15]);
-    } else {
-#define DSV4_COL(R) if (R < n) chain_col<R>(acc, qv, k[R]);
-        DSV4_COL(0) DSV4_COL(1) DSV4_COL(2) DSV4_COL(3) DSV4_COL(4) DSV4_COL(5)
-        DSV4_COL(6) DSV4_COL(7) DSV4_COL(8) DSV4_COL(9) DSV4_COL(10) DSV4_COL(11)
-        DSV4_COL(12) DSV4_COL(13) DSV4_COL(14) DSV4_COL(15)
+    for (int j = 0; j < IS_HB; j++) qv[j] = j < nh ? (double)qf[j] : 0.0;
+    /* two wait states between the conversions above and the broadcasts */
+    asm volatile("s_nop 1"
+                 : "+v"(qv[0]), "+v"(qv[1]), "+v"(qv[2]), "+v"(qv[3]),
+                   "+v"(qv[4]), "+v"(qv[5]), "+v"(qv[6]), "+v"(qv[7]));
+#define DSV4_COL(R) if (FULL || R < n) chain_col<R>(acc, qv, k[R]);
+    DSV4_COL(0) DSV4_COL(1) DSV4_COL(2) DSV4_COL(3) DSV4_COL(4) DSV4_COL(5)
+    DSV4_COL(6) DSV4_COL(7) DSV4_COL(8) DSV4_COL(9) DSV4_COL(10) DSV4_COL(11)
+    DSV4_COL(12) DSV4_COL(13) DSV4_COL(14) DSV4_COL(15)
 #undef DSV4_COL
-    }
 }
 
 template <int KF, int VEC, int HIST>
@@ -207,21 +196,26 @@ __global__ void __launch_bounds__(IS_MAXW * 64)
 k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
          uint32_t *__restrict__ meta, const float *__restrict__ q, const float *__restrict__ w,
          int H, int HP, int D, const void *__restrict__ keys,
-         const float *__restrict__ ks, int key_stride, int n, float scale)
+         const float *__restrict__ ks, int key_stride, int n, float scale, int ng)
 {
-    extern __shared__ double dots[];            /* [64][HP + 1] */
+    extern __shared__ double dots[];            /* [kb * 64][HP + 1], then w[HP] */
     constexpr int ES = KF == DSV4_GPU_KV_F32 ? 4 : KF == DSV4_GPU_KV_BF16 ? 2 : 1;
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int nw = blockDim.x >> 6;
-    const int t = blockIdx.x * 64 + lane;
+    const int kb = (blockDim.x >> 6) / ng;      /* key blocks of 64 rows */
+    const int b = wv / ng, hw = wv - b * ng;    /* this wave's block, head wave */
+    const int t = (blockIdx.x * kb + b) * 64 + lane;
     const int tr = t < n ? t : n - 1;           /* rows past n compute row n-1 */
     const int pitch = HP + 1;
+    double *wd = dots + (size_t)kb * 64 * pitch;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) wd[i] = (double)w[i];
     const float rs = KF == DSV4_GPU_KV_FP8 ? ks[tr] : 1.0f;
     const unsigned char *row = (const unsigned char *)keys + (size_t)tr * key_stride * ES;
+    double *drow = dots + (size_t)(b * 64 + lane) * pitch;
 
-    for (int g = wv; g * IS_HB < HP; g += nw) {
+    for (int g = hw; g * IS_HB < HP; g += ng) {
         const int h0 = g * IS_HB;
+        const int nh = min(IS_HB, H - h0);
         double acc[IS_HB];
 #pragma unroll
         for (int j = 0; j < IS_HB; j++) acc[j] = 0.0;
@@ -246,8 +240,8 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
                         for (int pc = 0; pc < 16 / CPP; pc++)
                             key_piece<KF>(v[u16 * (16 / CPP) + pc], rs, k + pc * CPP);
                         q_cols(qn, q, h0, H, D, cc + 16, lane);
-                        if (cc + 16 <= D) chain_16<true>(acc, qf, k, 16);
-                        else              chain_16<false>(acc, qf, k, D - cc);
+                        if (cc + 16 <= D) chain_16<true>(acc, qf, k, 16, nh);
+                        else              chain_16<false>(acc, qf, k, D - cc, nh);
 #pragma unroll
                         for (int j = 0; j < IS_HB; j++) qf[j] = qn[j];
                     }
@@ -267,25 +261,24 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
                         k[e] = ((const float *)row)[c];
                 }
                 q_cols(qn, q, h0, H, D, c0 + 16, lane);
-                if (c0 + 16 <= D) chain_16<true>(acc, qf, k, 16);
-                else              chain_16<false>(acc, qf, k, D - c0);
+                if (c0 + 16 <= D) chain_16<true>(acc, qf, k, 16, nh);
+                else              chain_16<false>(acc, qf, k, D - c0, nh);
 #pragma unroll
                 for (int j = 0; j < IS_HB; j++) qf[j] = qn[j];
             }
         }
 #pragma unroll
-        for (int j = 0; j < IS_HB; j++) dots[lane * pitch + g * IS_HB + j] = acc[j];
+        for (int j = 0; j < IS_HB; j++) drow[g * IS_HB + j] = acc[j];
     }
     __syncthreads();
-    if (wv != 0) return;
+    if (hw != 0) return;
 
+    /* the reference's `if (dot > 0) total += dot * w`, as a select */
     double total = 0.0;
     for (int hh = 0; hh < H; hh++) {
-        const double d = dots[lane * pitch + hh];
-        if (d > 0.0) {
-            const double prod = d * (double)w[hh];
-            total = total + prod;
-        }
+        const double d = drow[hh];
+        const double prod = d * wd[hh];
+        total = d > 0.0 ? total + prod : total;
     }
     const float tf = (float)total;
     const float sc = tf * scale;
@@ -301,14 +294,16 @@ void launch_iscore(bool vec, int grid, int thr, size_t lds, hipStream_t st,
                    float *d_out, uint32_t *hist, uint32_t *meta, const float *d_q,
                    const float *d_w,
                    int H, int HP, int D, const void *d_keys, const float *d_ks,
-                   int key_stride, int n, float scale)
+                   int key_stride, int n, float scale, int ng)
 {
     if (vec)
         hipLaunchKernelGGL((k_iscore<KF, 1, HIST>), dim3(grid), dim3(thr), lds, st, d_out,
-                           hist, meta, d_q, d_w, H, HP, D, d_keys, d_ks, key_stride, n, scale);
+                           hist, meta, d_q, d_w, H, HP, D, d_keys, d_ks, key_stride, n, scale,
+                           ng);
     else
         hipLaunchKernelGGL((k_iscore<KF, 0, HIST>), dim3(grid), dim3(thr), lds, st, d_out,
-                           hist, meta, d_q, d_w, H, HP, D, d_keys, d_ks, key_stride, n, scale);
+                           hist, meta, d_q, d_w, H, HP, D, d_keys, d_ks, key_stride, n, scale,
+                           ng);
 }
 
 /* --------------------------------------------------------------- top-k */
@@ -996,9 +991,13 @@ int dsv4_indexer_score_launch(float *d_out, const float *d_q, const float *d_w,
     }
     if (n == 0) return 0;
     const int HP = ix_heads_padded(H);
+    /* four waves per workgroup where the heads allow it: one wave per SIMD
+     * of a CU (up to 4 head waves per block of 64 rows, blocks filling the
+     * rest) */
     const int groups = HP / IS_HB;
-    const int nw = groups < IS_MAXW ? groups : IS_MAXW;
-    const size_t lds = sizeof(double) * 64 * (size_t)(HP + 1);
+    const int ng = groups < 4 ? groups : 4;
+    const int kb = 4 / ng;
+    const size_t lds = sizeof(double) * ((size_t)64 * kb * (HP + 1) + HP);
     if (lds > dsv4_lds_limit()) {
         DSV4_ERR("indexer score: %d heads do not fit in LDS", H);
         return -1;
@@ -1024,16 +1023,16 @@ int dsv4_indexer_score_launch(float *d_out, const float *d_q, const float *d_w,
     const int es = key_fmt == DSV4_GPU_KV_F32 ? 4 : key_fmt == DSV4_GPU_KV_BF16 ? 2 : 1;
     const bool vec = ((size_t)D * es) % 16 == 0 && ((size_t)key_stride * es) % 16 == 0 &&
                      ((uintptr_t)d_keys & 15) == 0;
-    const int grid = (n + 63) / 64;
-    const int thr = 64 * nw;
+    const int grid = (n + 64 * kb - 1) / (64 * kb);
+    const int thr = 64 * ng * kb;
 #define DSV4_ISCORE(KF)                                                                 \
     do {                                                                                \
         if (with_hist)                                                                  \
             launch_iscore<KF, 1>(vec, grid, thr, lds, st, d_out, hist, meta, d_q, d_w, H, HP, \
-                                 D, d_keys, d_key_scales, key_stride, n, scale);        \
+                                 D, d_keys, d_key_scales, key_stride, n, scale, ng);    \
         else                                                                            \
             launch_iscore<KF, 0>(vec, grid, thr, lds, st, d_out, hist, meta, d_q, d_w, H, HP, \
-                                 D, d_keys, d_key_scales, key_stride, n, scale);        \
+                                 D, d_keys, d_key_scales, key_stride, n, scale, ng);    \
     } while (0)
     if (key_fmt == DSV4_GPU_KV_FP8) DSV4_ISCORE(DSV4_GPU_KV_FP8);
     else if (key_fmt == DSV4_GPU_KV_BF16) DSV4_ISCORE(DSV4_GPU_KV_BF16);

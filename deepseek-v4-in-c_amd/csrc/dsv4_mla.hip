@@ -35,6 +35,8 @@
 #include "dsv4_dev.h"
 #include "dsv4_internal.h"
 
+#include <stdlib.h>
+
 namespace {
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b)
@@ -923,6 +925,281 @@ k_attn_combine(float *__restrict__ o, const float *__restrict__ pm,
     }
 }
 
+/* ------------------------------------------ sparse attention, matrix core */
+
+/* The same split softmax on v_mfma_f32_16x16x32_bf16 for bf16 KV, d_qk a
+ * multiple of 32, d_v of 16 and h of 16 (h <= 128). Operand layout of the
+ * MFMA (measured on gfx950): A lane l holds row l%16, K elements [8(l/16),
+ * +8); B lane l holds column l%16, the same K elements; D lane l, register
+ * j holds row 4(l/16) + j, column l%16.
+ *
+ * q and the softmax weights are f32: each is carried as three bf16 terms
+ * hi + mid + lo, which hold all 24 bits, against the exact bf16 KV, so every
+ * product is exact and the sums accumulate in f32 (in another order than
+ * the reference's; within 1e-5 relative).
+ *
+ * One workgroup of AM_WAVES waves per split of AM_SR selected rows:
+ *   stage : the rows, gathered once: row-major for the scores' B operand
+ *           (K rows), transposed (columns x rows) for the values' B operand;
+ *   scores: S = q . K^T, (head tile, half of the rows) per wave;
+ *   softmax: per head m_s, e_j = expf(s_j - m_s), l_s (rows in lanes);
+ *   values: O_s = P . V, (head tile, columns) per wave;
+ * then k_attn_combine as for the VALU form. */
+typedef float am_v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 am_v8bf __attribute__((ext_vector_type(8)));
+typedef short am_v8s __attribute__((ext_vector_type(8)));
+
+constexpr int AM_SR = 64;                        /* rows per split */
+constexpr int AM_WAVES = 4;
+constexpr int AM_THREADS = AM_WAVES * 64;
+constexpr int AM_PP = AM_SR + 4;                 /* weights pitch (f32) */
+constexpr int AM_KCW = 5;                        /* K chunks per wave */
+constexpr int AM_KCMAX = AM_KCW * AM_WAVES;      /* d_qk <= 32 AM_KCMAX */
+
+typedef __bf16 am_v2bf __attribute__((ext_vector_type(2)));
+typedef float am_v2f __attribute__((ext_vector_type(2)));
+
+/* Two f32 values -> two bf16 (round to nearest even, v_cvt_pk_bf16_f32). */
+__device__ __forceinline__ uint32_t am_cvt2(float a, float b)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(am_v2f{a, b}, am_v2bf));
+}
+
+/* Eight f32 values -> their three bf16 term vectors (v = t0 + t1 + t2,
+ * exactly: each residual is exact in f32). */
+__device__ __forceinline__ void am_terms8(const float *v, am_v8bf *t)
+{
+    u32x4 w[3];
+    uint32_t *w0 = (uint32_t *)&w[0], *w1 = (uint32_t *)&w[1], *w2 = (uint32_t *)&w[2];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float a = v[2 * i], b = v[2 * i + 1];
+        const uint32_t hi = am_cvt2(a, b);
+        const float ra = a - __uint_as_float(hi << 16), rb = b - __uint_as_float(hi & 0xFFFF0000u);
+        const uint32_t mi = am_cvt2(ra, rb);
+        const float sa = ra - __uint_as_float(mi << 16), sb = rb - __uint_as_float(mi & 0xFFFF0000u);
+        w0[i] = hi;
+        w1[i] = mi;
+        w2[i] = am_cvt2(sa, sb);
+    }
+    t[0] = __builtin_bit_cast(am_v8bf, w[0]);
+    t[1] = __builtin_bit_cast(am_v8bf, w[1]);
+    t[2] = __builtin_bit_cast(am_v8bf, w[2]);
+}
+
+/* LDS layout in bytes for a shape: K rows [AM_SR][kp], then V^T [d_v][vp];
+ * the score partials and the weights reuse the K rows once they are read. */
+__host__ __device__ __forceinline__ int am_kpitch(int d_qk) { return 2 * d_qk + 16; }
+__host__ __device__ __forceinline__ int am_vpitch() { return 2 * AM_SR + 16; }
+
+/* Workgroup (split of AM_SR rows, tile of 16 heads), AM_WAVES waves:
+ *   stage : lane = row; the rows, gathered once, row-major (scores' B
+ *           operand) and transposed (values' B operand); meanwhile each wave
+ *           loads q for its K chunks w, w + AM_WAVES, ...;
+ *   scores: each wave the partial S over its K chunks for all row tiles,
+ *           summed across the waves in LDS in wave order;
+ *   softmax: per head m_s, e_j = expf(s_j - m_s), l_s (lane = row);
+ *   values: O_s = P . V, each wave a quarter of the column tiles. */
+__global__ void __launch_bounds__(AM_THREADS)
+k_attn_mc(float *__restrict__ pm, float *__restrict__ pl, float *__restrict__ po,
+          const float *__restrict__ q, const uint16_t *__restrict__ kv, int kv_stride,
+          const int *__restrict__ idxs, int kv_rows, int h, int d_qk, int d_v, int topk,
+          float scale)
+{
+    extern __shared__ __attribute__((aligned(16))) unsigned char am_lds[];
+    __shared__ int sidx[AM_SR];
+    const int kp = am_kpitch(d_qk), vp = am_vpitch();
+    unsigned char *kr = am_lds;                                  /* [AM_SR][kp] */
+    unsigned char *vt = am_lds + (size_t)AM_SR * kp;             /* [d_v][vp]  */
+    float *red = (float *)am_lds;                                /* [AM_WAVES][16][AM_PP] */
+    float *pw = red;                                             /* [16][AM_PP] */
+
+    const int split = blockIdx.x, nsplit = gridDim.x, ht = blockIdx.y;
+    const int j0 = split * AM_SR;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int KC = d_qk / 32;
+
+    if (tid < AM_SR) {
+        const int r = j0 + tid < topk ? idxs[j0 + tid] : -1;
+        sidx[tid] = (r >= 0 && r < kv_rows) ? r : -1;            /* never a wild read */
+    }
+    /* q of the head tile for this wave's K chunks (A operand rows l%16, K
+     * [8(l/16), +8) of each chunk), in flight with the staging loads */
+    float qv[AM_KCW][8];
+    {
+        const float *qr = q + (size_t)(ht * 16 + l16) * d_qk + 8 * g;
+#pragma unroll
+        for (int i = 0; i < AM_KCW; i++) {
+            const int kc = min(wv + AM_WAVES * i, KC - 1);
+            const f32x4 a0 = ldf4(qr + 32 * kc), a1 = ldf4(qr + 32 * kc + 4);
+            qv[i][0] = a0.x; qv[i][1] = a0.y; qv[i][2] = a0.z; qv[i][3] = a0.w;
+            qv[i][4] = a1.x; qv[i][5] = a1.y; qv[i][6] = a1.z; qv[i][7] = a1.w;
+        }
+    }
+    __syncthreads();
+
+    /* ---- stage: lane = row, wave w takes 16-byte chunks w, w + 4, ... ---- */
+    {
+        const int ck = d_qk / 8;                                 /* chunks per row */
+        const int row = sidx[lane];
+        const uint16_t *src = kv + (size_t)(row >= 0 ? row : 0) * kv_stride;
+        constexpr int NB = 18;                                   /* chunks in flight */
+        for (int c0 = wv; c0 < ck; c0 += NB * AM_WAVES) {
+            u32x4 v[NB];
+#pragma unroll
+            for (int u = 0; u < NB; u++) {
+                const int ch = min(c0 + u * AM_WAVES, ck - 1);
+                v[u] = row >= 0 ? *(const DSV4_GLOBAL u32x4 *)(src + 8 * ch)
+                                : u32x4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int u = 0; u < NB; u++) {
+                const int ch = c0 + u * AM_WAVES;
+                if (ch < ck) {
+                    *reinterpret_cast<u32x4 *>(kr + (size_t)lane * kp + 16 * ch) = v[u];
+                    if (8 * ch < d_v) {
+                        const uint32_t w4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            *(uint16_t *)(vt + (size_t)(8 * ch + 2 * e) * vp + 2 * lane) =
+                                (uint16_t)(w4[e] & 0xFFFFu);
+                            *(uint16_t *)(vt + (size_t)(8 * ch + 2 * e + 1) * vp + 2 * lane) =
+                                (uint16_t)(w4[e] >> 16);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    /* ---- scores: this wave's K chunks for all four row tiles; one
+     *      accumulator per (row tile, term) ---- */
+    am_v4f acc[4][3];
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++)
+#pragma unroll
+        for (int t = 0; t < 3; t++) acc[rt][t] = am_v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < AM_KCW; i++) {
+        const int kc = wv + AM_WAVES * i;
+        if (kc < KC) {
+            am_v8bf bk[4];
+#pragma unroll
+            for (int rt = 0; rt < 4; rt++)
+                bk[rt] = __builtin_bit_cast(am_v8bf, *reinterpret_cast<const u32x4 *>(
+                    kr + (size_t)(rt * 16 + l16) * kp + 2 * (32 * kc + 8 * g)));
+            am_v8bf at[3];
+            am_terms8(qv[i], at);
+#pragma unroll
+            for (int t = 0; t < 3; t++)
+#pragma unroll
+                for (int rt = 0; rt < 4; rt++)
+                    acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(at[t], bk[rt],
+                                                                        acc[rt][t], 0, 0, 0);
+        }
+    }
+    __syncthreads();                    /* K rows read: the partials reuse them */
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++) {
+        const am_v4f sv = (acc[rt][0] + acc[rt][1]) + acc[rt][2];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            red[(wv * 16 + 4 * g + j) * AM_PP + rt * 16 + l16] = sv[j];
+    }
+    __syncthreads();
+
+    /* ---- split softmax: wave w takes heads 4w .. 4w + 3, lane = row; the
+     *      partials summed in wave order ---- */
+    {
+        const bool live = sidx[lane] >= 0;
+        float sv[4], m[4], e[4], l[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int hh = 4 * wv + i;
+            float a = red[hh * AM_PP + lane];
+#pragma unroll
+            for (int w = 1; w < AM_WAVES; w++) a = a + red[(w * 16 + hh) * AM_PP + lane];
+            sv[i] = live ? a * scale : -INFINITY;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) m[i] = wave_max(sv[i]);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            e[i] = (m[i] == -INFINITY || sv[i] == -INFINITY) ? 0.0f : expf(sv[i] - m[i]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) l[i] = wave_sum(e[i]);
+        __syncthreads();                /* every partial read before pw overwrites */
+#pragma unroll
+        for (int i = 0; i < 4; i++) pw[(4 * wv + i) * AM_PP + lane] = e[i];
+        if (lane < 4) {
+            float mi = m[0], li = l[0];
+#pragma unroll
+            for (int i = 1; i < 4; i++) if (lane == i) { mi = m[i]; li = l[i]; }
+            const int hh = ht * 16 + 4 * wv + lane;
+            pm[(size_t)hh * nsplit + split] = mi;
+            pl[(size_t)hh * nsplit + split] = li;
+        }
+    }
+    __syncthreads();
+
+    /* ---- values: column tiles wv, wv + 4, ... ---- */
+    const int CT = d_v / 16;
+    for (int c0 = wv; c0 < CT; c0 += 8 * AM_WAVES) {
+        am_v4f o[8];
+#pragma unroll
+        for (int ct = 0; ct < 8; ct++) o[ct] = am_v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < AM_SR / 32; kc++) {
+            const float *pr = pw + l16 * AM_PP + 32 * kc + 8 * g;
+            const f32x4 a0 = *reinterpret_cast<const f32x4 *>(pr);
+            const f32x4 a1 = *reinterpret_cast<const f32x4 *>(pr + 4);
+            const float pv[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            am_v8bf at[3];
+            am_terms8(pv, at);
+            am_v8bf bv[8];
+#pragma unroll
+            for (int ct = 0; ct < 8; ct++) {
+                const int c = min(c0 + AM_WAVES * ct, CT - 1) * 16 + l16;
+                bv[ct] = __builtin_bit_cast(am_v8bf, *reinterpret_cast<const u32x4 *>(
+                    vt + (size_t)c * vp + 2 * (32 * kc + 8 * g)));
+            }
+#pragma unroll
+            for (int t = 0; t < 3; t++)
+#pragma unroll
+                for (int ct = 0; ct < 8; ct++)
+                    o[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(at[t], bv[ct], o[ct], 0, 0, 0);
+        }
+#pragma unroll
+        for (int ct = 0; ct < 8; ct++) {
+            const int cti = c0 + AM_WAVES * ct;
+            if (cti < CT) {
+                const int c = cti * 16 + l16;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int hh = ht * 16 + 4 * g + j;
+                    po[((size_t)hh * nsplit + split) * d_v + c] = o[ct][j];
+                }
+            }
+        }
+    }
+}
+
+/* LDS bytes of k_attn_mc for a shape, 0 when the shape is not one it takes. */
+size_t attn_mc_lds(int kv_fmt, int h, int d_qk, int d_v, int kv_stride)
+{
+    if (kv_fmt != DSV4_GPU_KV_BF16 || h % 16 || d_qk % 32 || d_qk > 32 * AM_KCMAX ||
+        d_v % 16 || d_v > d_qk || kv_stride % 8)
+        return 0;
+    const size_t kr = (size_t)AM_SR * am_kpitch(d_qk);
+    const size_t w = (size_t)AM_WAVES * 16 * AM_PP * sizeof(float);
+    if (w > kr) return 0;
+    const size_t lds = kr + (size_t)d_v * am_vpitch();
+    return lds + AM_SR * sizeof(int) <= dsv4_lds_limit() ? lds : 0;
+}
+
 /* Rows per split: the staged rows, q and the scores must fit the LDS a
  * workgroup may use. */
 int attn_split_rows(int kv_fmt, int d_qk, int d_v, int *rowb_out, size_t *lds_out)
@@ -1133,8 +1410,27 @@ int dsv4_attn_launch(float *d_o, const float *d_q, const void *d_kv,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, cap);
         (void)hipFuncSetAttribute((const void *)k_attn_partial<DSV4_GPU_KV_F32>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, cap);
+        (void)hipFuncSetAttribute((const void *)k_attn_mc,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, cap);
         (void)hipGetLastError();
         lds_opted = true;
+    }
+    /* the matrix-core form where the shape allows (DSV4_GPU_ATTN_MC=0 keeps
+     * the VALU form) */
+    const size_t mc_lds = attn_mc_lds(kv_fmt, h, d_qk, d_v, kv_stride);
+    const char *mc_env = getenv("DSV4_GPU_ATTN_MC");
+    if (mc_lds && topk > 0 && ((uintptr_t)d_kv & 15) == 0 && !(mc_env && atoi(mc_env) == 0)) {
+        const int ns = (topk + AM_SR - 1) / AM_SR;          /* <= nsplit: sr <= AM_SR */
+        pl = pm + (size_t)h * ns;
+        po = pl + (size_t)h * ns;
+        hipLaunchKernelGGL(k_attn_mc, dim3(ns, h / 16), dim3(AM_THREADS), mc_lds, st, pm, pl, po,
+                           d_q, (const uint16_t *)d_kv, kv_stride, d_idxs, kv_rows, h,
+                           d_qk, d_v, topk, scale);
+        HIP_OK(hipGetLastError(), "attn mc launch");
+        hipLaunchKernelGGL(k_attn_combine, dim3(h), dim3(AT_THREADS), 0, st, d_o,
+                           pm, pl, po, d_sink, ns, d_v);
+        HIP_OK(hipGetLastError(), "attn combine launch");
+        return 0;
     }
     if (kv_fmt == DSV4_GPU_KV_BF16)
         hipLaunchKernelGGL((k_attn_partial<DSV4_GPU_KV_BF16>), grid, dim3(AT_THREADS), lds, st,

@@ -128,8 +128,11 @@ def c4_attention(seed, n=32768, h=64, d_qk=576, d_v=512, topk=2048):
     return kv, q, idx
 
 
+@pytest.mark.parametrize("form", ["matrix-core", "valu"])
 @pytest.mark.parametrize("with_sink", [False, True])
-def test_attention_c4(gpu, dsv4, with_sink):
+def test_attention_c4(gpu, dsv4, monkeypatch, with_sink, form):
+    if form == "valu":
+        monkeypatch.setenv("DSV4_GPU_ATTN_MC", "0")
     kv, q, idx = c4_attention(1)
     h = q.shape[0]
     sink = np.random.default_rng(2).standard_normal(h).astype(np.float32) if with_sink else None
@@ -138,7 +141,28 @@ def test_attention_c4(gpu, dsv4, with_sink):
     got = dsv4.sparse_attn(q, store_, sink, idx, scale, d_v=512)
     want = oracle.sparse_attn(q, kv, sink, idx, scale, d_v=512)
     err = common.vec_rel_err(got, want)
-    say("attention C4 sink=%s: worst rel %.3g" % (with_sink, err))
+    say("attention C4 %s sink=%s: worst rel %.3g" % (form, with_sink, err))
+    assert err < TOL
+
+
+@pytest.mark.parametrize("h,d_qk,d_v,topk", [(16, 512, 512, 200), (128, 576, 512, 333),
+                                             (32, 64, 32, 64), (64, 576, 512, 1)])
+def test_attention_bf16_shapes_masked(gpu, dsv4, h, d_qk, d_v, topk):
+    """bf16 KV through the matrix-core form: a partial last split, masked
+    (-1) slots, repeated rows, more head tiles than waves (h = 128) and
+    d_v < d_qk."""
+    rng = np.random.default_rng(h + d_qk + topk)
+    n = 700
+    kv = common.bf16_round(rng.standard_normal((n, d_qk)).astype(np.float32) * 0.1)
+    q = rng.standard_normal((h, d_qk)).astype(np.float32)
+    sink = rng.standard_normal(h).astype(np.float32)
+    idx = rng.integers(-1, n, size=topk).astype(np.int32)
+    st = store(dsv4, common.bf16_bits(kv), dsv4.KV_BF16)
+    scale = np.float32(1.0) / np.sqrt(np.float32(d_qk))
+    got = dsv4.sparse_attn(q, st, sink, idx, scale, d_v=d_v)
+    want = oracle.sparse_attn(q, kv, sink, idx, scale, d_v=d_v)
+    err = common.vec_rel_err(got, want)
+    say("attention bf16 h=%d d_qk=%d d_v=%d topk=%d: worst rel %.3g" % (h, d_qk, d_v, topk, err))
     assert err < TOL
 
 

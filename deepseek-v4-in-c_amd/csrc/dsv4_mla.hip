@@ -73,8 +73,7 @@ constexpr int TK_BINS = 2048;                   /* top 11 bits of the key */
 constexpr int TK_SLICES = 16;                   /* spread of the global atomics */
 
 /* meta words in the scratch */
-constexpr int MT_CGT = 0;                       /* candidates > T (for rank) */
-constexpr int MT_ABOVE = 1;                     /* cand[] append counter */
+constexpr int MT_ABOVE = 1;                     /* cand[] append counter (word 0 unused) */
 constexpr int MT_BIN = 2;                       /* B */
 constexpr int MT_KREM = 3;                      /* rank of the k-th inside B */
 
@@ -310,17 +309,16 @@ void launch_iscore(bool vec, int grid, int thr, size_t lds, hipStream_t st,
 
 /* --------------------------------------------------------------- top-k */
 
-/* Top-k in three passes after the level-1 histogram (built by the score
+/* Top-k in two passes after the level-1 histogram (built by the score
  * kernel, or by k_tk_hist for stand-alone scores):
  *   k_tk_part   many workgroups: the bin B of the k-th largest from the
  *               histogram; elements of higher bins go to cand[] (any order),
  *               elements of B to a per-workgroup list in index order;
- *   k_tk_refine one workgroup over B's list only: levels 2 and 3 give T,
- *               the exact key of the k-th largest; the list's elements > T
- *               join cand[], its first need_eq elements == T go straight to
- *               their output slots;
- *   k_tk_rank   many workgroups: each candidate's output position is the
- *               number of candidates ahead of it. */
+ *   k_tk_final  many workgroups: each repeats the refinement of B's list
+ *               (levels 2 and 3 give T, the exact key of the k-th largest),
+ *               then places its share of the candidates > T by counting the
+ *               candidates ahead of each; the first need_eq elements == T
+ *               follow them in index order. */
 
 constexpr int PT_THREADS = 256;                 /* partition workgroup */
 constexpr int PT_EPT = 4;                       /* elements per thread */
@@ -517,42 +515,71 @@ k_tk_part(unsigned long long *__restrict__ cand, uint32_t *__restrict__ meta,
     if (tid == 0) bcnt[blockIdx.x] = tot;
 }
 
-/* Refine, one workgroup. B's elements, in index order, are the lists of the
- * G partition workgroups one after another (entry j of the whole list is in
- * the list of the workgroup w with pfx[w] <= j < pfx[w + 1]). The list is
- * staged in LDS when it fits, read from global memory otherwise. Also clears
- * the level-1 histogram for the next top-k. */
-__global__ void __launch_bounds__(TK_THREADS)
-k_tk_refine(int *__restrict__ idxs, unsigned long long *__restrict__ cand,
-            uint32_t *__restrict__ meta, const uint32_t *__restrict__ bcnt,
-            const unsigned long long *__restrict__ blist,
-            uint32_t *__restrict__ hist_g, int G, int k)
+/* Final pass: workgroup b orders candidates [RK_EPW b, RK_EPW (b + 1)).
+ * Every workgroup first repeats the (small) refinement of bin B: B's
+ * elements, in index order, are the lists of the G partition workgroups one
+ * after another (entry j of the whole list lies in the list of the
+ * workgroup w with pfx[w] <= j < pfx[w + 1]), staged in LDS when they fit,
+ * read from global memory otherwise. Levels 2 and 3 of the radix select over
+ * that list give T and need_eq; the candidates -- cand[] from the partition
+ * plus the list's elements > T, in list order -- are the same array in every
+ * workgroup, and each candidate's position is the number of candidates ahead
+ * of it. Workgroup 0 also writes the first need_eq elements == T after them;
+ * every workgroup clears its share of the level-1 histogram. */
+constexpr int FN_THREADS = 256;
+constexpr int FN_WAVES = FN_THREADS / 64;
+constexpr int RK_TPE = 16;                              /* threads per candidate */
+constexpr int RK_EPW = FN_THREADS / RK_TPE;             /* candidates per workgroup */
+
+__global__ void __launch_bounds__(FN_THREADS)
+k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
+           const uint32_t *__restrict__ meta, const uint32_t *__restrict__ bcnt,
+           const unsigned long long *__restrict__ blist, uint32_t *__restrict__ hist_g,
+           int G, int k)
 {
+    constexpr int BPT = TK_BINS / FN_THREADS;           /* 8 bins per thread */
+    constexpr int GPT = RF_GMAX / FN_THREADS;           /* 16 list lengths per thread */
     __shared__ uint32_t hist[TK_BINS];
     __shared__ uint32_t pfx[RF_GMAX + 1];
     __shared__ unsigned long long lst[RF_LIST];
-    __shared__ uint32_t wsum[TK_WAVES], res[2];
+    __shared__ unsigned long long cs[TK_KMAX];
+    __shared__ uint32_t wsum[FN_WAVES], res[2];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const unsigned long long lt = lanemask_lt(lane);
 
-    for (int i = tid; i < TK_SLICES * TK_BINS / 4; i += TK_THREADS)
+    for (int i = blockIdx.x * FN_THREADS + tid; i < TK_SLICES * TK_BINS / 4;
+         i += gridDim.x * FN_THREADS)
         reinterpret_cast<u32x4 *>(hist_g)[i] = u32x4{0u, 0u, 0u, 0u};
-    const uint32_t krem1 = meta[MT_KREM], c_above = meta[MT_ABOVE];
-    const uint32_t B = meta[MT_BIN];
+    const uint32_t B = meta[MT_BIN], krem1 = meta[MT_KREM];
+    const uint32_t c_above = min(meta[MT_ABOVE], (uint32_t)TK_KMAX);
 
-    /* prefix of the list lengths: thread t takes entries 4t .. 4t + 3 */
-    uint32_t v[4], s4 = 0u;
+    /* list lengths (prefix below): thread t takes entries GPT t .. GPT t + GPT-1;
+     * their loads are issued before the candidates' */
+    uint32_t v[GPT];
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        v[q] = 4 * tid + q < G ? bcnt[4 * tid + q] : 0u;
-        s4 += v[q];
+    for (int q = 0; q < GPT; q++) v[q] = bcnt[min(GPT * tid + q, G - 1)];
+    /* candidates above B: into LDS */
+    for (uint32_t i0 = 0; i0 < c_above; i0 += 8 * FN_THREADS) {
+        unsigned long long v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = cand[min(i0 + u * FN_THREADS + tid, c_above - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (i0 + u * FN_THREADS + tid < c_above) cs[i0 + u * FN_THREADS + tid] = v[u];
+    }
+
+    uint32_t sg = 0u;
+#pragma unroll
+    for (int q = 0; q < GPT; q++) {
+        v[q] = GPT * tid + q < G ? v[q] : 0u;
+        sg += v[q];
     }
     uint32_t nb;
-    uint32_t run = tk_scan<TK_THREADS>(s4, wsum, &nb);
+    uint32_t run = tk_scan<FN_THREADS>(sg, wsum, &nb);
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        if (4 * tid + q < G) pfx[4 * tid + q] = run;
+    for (int q = 0; q < GPT; q++) {
+        if (GPT * tid + q < G) pfx[GPT * tid + q] = run;
         run += v[q];
     }
     if (tid == 0) pfx[G] = nb;
@@ -571,112 +598,109 @@ k_tk_refine(int *__restrict__ idxs, unsigned long long *__restrict__ cand,
         return listed ? lst[j] : blist[gaddr(j)];
     };
     if (listed) {
-        for (uint32_t j0 = 0; j0 < nb; j0 += 4 * TK_THREADS) {
-            unsigned long long e[4];
+        for (uint32_t j0 = 0; j0 < nb; j0 += 8 * FN_THREADS) {
+            unsigned long long e[8];
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint32_t j = j0 + q * TK_THREADS + tid;
+            for (int q = 0; q < 8; q++) {
+                const uint32_t j = j0 + q * FN_THREADS + tid;
                 e[q] = j < nb ? blist[gaddr(j)] : 0ull;
             }
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint32_t j = j0 + q * TK_THREADS + tid;
+            for (int q = 0; q < 8; q++) {
+                const uint32_t j = j0 + q * FN_THREADS + tid;
                 if (j < nb) lst[j] = e[q];
             }
         }
     }
-    hist[2 * tid] = 0u;
-    hist[2 * tid + 1] = 0u;
+#pragma unroll
+    for (int q = 0; q < BPT; q++) hist[BPT * tid + q] = 0u;
     __syncthreads();
 
     /* ---- level 2: bits 20..10 ---- */
-    for (uint32_t j = tid; j < nb; j += TK_THREADS)
+    for (uint32_t j = tid; j < nb; j += FN_THREADS)
         atomicAdd(&hist[(uint32_t)(ent(j) >> 42) & 2047u], 1u);
     __syncthreads();
-    uint32_t c[2] = {hist[TK_BINS - 1 - 2 * tid], hist[TK_BINS - 2 - 2 * tid]};
-    tk_find<TK_THREADS, 2>(c, krem1, wsum, res);
+    uint32_t c[BPT];
+#pragma unroll
+    for (int q = 0; q < BPT; q++) c[q] = hist[TK_BINS - 1 - BPT * tid - q];
+    tk_find<FN_THREADS, BPT>(c, krem1, wsum, res);
     const uint32_t P22 = (B << 11) | res[0], krem2 = res[1];
 
     /* ---- level 3: bits 9..0 ---- */
-    hist[2 * tid] = 0u;
-    hist[2 * tid + 1] = 0u;
+#pragma unroll
+    for (int q = 0; q < BPT; q++) hist[BPT * tid + q] = 0u;
     __syncthreads();
-    for (uint32_t j = tid; j < nb; j += TK_THREADS) {
+    for (uint32_t j = tid; j < nb; j += FN_THREADS) {
         const uint32_t key = (uint32_t)(ent(j) >> 32);
         if ((key >> 10) == P22) atomicAdd(&hist[key & 1023u], 1u);
     }
     __syncthreads();
-    c[0] = hist[TK_BINS - 1 - 2 * tid];
-    c[1] = hist[TK_BINS - 2 - 2 * tid];
-    tk_find<TK_THREADS, 2>(c, krem2, wsum, res);
+#pragma unroll
+    for (int q = 0; q < BPT; q++) c[q] = hist[TK_BINS - 1 - BPT * tid - q];
+    tk_find<FN_THREADS, BPT>(c, krem2, wsum, res);
     const uint32_t T = (P22 << 10) | res[0];
     /* need_eq is in [1, k] for a histogram that matches the scores; the
      * clamp keeps every write below in bounds whatever the histogram held. */
     const uint32_t need_eq = min(max(res[1], 1u), (uint32_t)k);
     const uint32_t c_gt = (uint32_t)k - need_eq;
 
-    /* ---- B's elements > T join cand[]; the first need_eq == T, in index
-     *      order, are output directly ---- */
-    uint32_t pg = c_above, pe = 0u;
-    for (uint32_t j0 = 0; j0 < nb; j0 += TK_THREADS) {
-        const uint32_t j = j0 + tid;
-        const unsigned long long e = j < nb ? ent(j) : 0ull;
-        const uint32_t key = (uint32_t)(e >> 32), idx = (uint32_t)e;
-        const bool gt = j < nb && key > T, eq = j < nb && key == T;
-        const unsigned long long mg = __ballot(gt), me = __ballot(eq);
-        const uint32_t cnt = (uint32_t)__popcll(mg) | ((uint32_t)__popcll(me) << 16);
-        uint32_t all;
-        const uint32_t before = tk_scan<TK_THREADS>(lane == 0 ? cnt : 0u, wsum, &all);
-        const uint32_t wb = (uint32_t)__shfl((int)before, 0, 64);
-        if (gt) {
-            const uint32_t pos = pg + (wb & 0xFFFFu) + (uint32_t)__popcll(mg & lt);
-            if (pos < c_gt)
-                cand[pos] = ((unsigned long long)key << 32) | (0xFFFFFFFFull - idx);
-        } else if (eq) {
-            const uint32_t pos = pe + (wb >> 16) + (uint32_t)__popcll(me & lt);
-            if (pos < need_eq) idxs[c_gt + pos] = (int)idx;
+    /* ---- B's elements > T join the candidates (list order); the first
+     *      need_eq == T, in index order, are output by workgroup 0. Thread
+     *      t takes list entries [per t, per (t + 1)): one scan of the
+     *      per-thread counts places them. ---- */
+    {
+        const uint32_t per = (nb + FN_THREADS - 1) / FN_THREADS;
+        const uint32_t j0 = min(per * tid, nb), j1 = min(j0 + per, nb);
+        uint32_t ng = 0u, ne = 0u;
+        for (uint32_t j = j0; j < j1; j++) {
+            const uint32_t key = (uint32_t)(ent(j) >> 32);
+            ng += key > T ? 1u : 0u;
+            ne += key == T ? 1u : 0u;
         }
-        pg += all & 0xFFFFu;
-        pe += all >> 16;
-    }
-    if (tid == 0) meta[MT_CGT] = c_gt;
-}
-
-/* Final order of the > T elements: composite e goes to position #{f :
- * cand[f] > cand[e]} (composites are distinct), which is the order by key
- * descending, index ascending. RK_TPE threads share an element. */
-constexpr int RK_TPE = 16;
-constexpr int RK_EPW = 256 / RK_TPE;                 /* elements per workgroup */
-
-__global__ void __launch_bounds__(256)
-k_tk_rank(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
-          const uint32_t *__restrict__ meta)
-{
-    __shared__ unsigned long long cs[TK_KMAX];
-    const uint32_t c = min(meta[MT_CGT], (uint32_t)TK_KMAX);
-    const uint32_t e0 = blockIdx.x * RK_EPW;
-    if (e0 >= c) return;                            /* the whole workgroup */
-    const int tid = threadIdx.x;
-    for (uint32_t i0 = 0; i0 < c; i0 += 8 * 256) {   /* eight loads in flight */
-        unsigned long long v[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = cand[min(i0 + u * 256 + tid, c - 1)];
-#pragma unroll
-        for (int u = 0; u < 8; u++)
-            if (i0 + u * 256 + tid < c) cs[i0 + u * 256 + tid] = v[u];
+        uint32_t all, pg, pe;
+        if (nb <= 0xFFFFu) {                    /* both counts in one word */
+            const uint32_t pre = tk_scan<FN_THREADS>(ng | (ne << 16), wsum, &all);
+            pg = c_above + (pre & 0xFFFFu);
+            pe = pre >> 16;
+        } else {
+            pg = c_above + tk_scan<FN_THREADS>(ng, wsum, &all);
+            pe = tk_scan<FN_THREADS>(ne, wsum, &all);
+        }
+        if (ng | ne) {
+            for (uint32_t j = j0; j < j1; j++) {
+                const unsigned long long e = ent(j);
+                const uint32_t key = (uint32_t)(e >> 32), idx = (uint32_t)e;
+                if (key > T) {
+                    if (pg < c_gt) cs[pg] = ((unsigned long long)key << 32) | (0xFFFFFFFFull - idx);
+                    pg++;
+                } else if (key == T) {
+                    if (pe < need_eq && blockIdx.x == 0) idxs[c_gt + pe] = (int)idx;
+                    pe++;
+                }
+            }
+        }
     }
     __syncthreads();
-    const uint32_t e = e0 + tid / RK_TPE, sub = tid % RK_TPE;
-    const unsigned long long mine = e < c ? cs[e] : ~0ull;
+
+    /* ---- rank this workgroup's candidates ---- */
+    const uint32_t e = blockIdx.x * RK_EPW + tid / RK_TPE, sub = tid % RK_TPE;
+    if (blockIdx.x * RK_EPW >= c_gt) return;            /* the whole workgroup */
+    const unsigned long long mine = e < c_gt ? cs[e] : ~0ull;
+    /* sixteen reads in flight per trip: the loop is LDS-latency bound */
+    constexpr int RU = 16;
     uint32_t r = 0u;
     uint32_t f = sub;
-    for (; f + 3 * RK_TPE < c; f += 4 * RK_TPE)
-        r += (cs[f] > mine ? 1u : 0u) + (cs[f + RK_TPE] > mine ? 1u : 0u) +
-             (cs[f + 2 * RK_TPE] > mine ? 1u : 0u) + (cs[f + 3 * RK_TPE] > mine ? 1u : 0u);
-    for (; f < c; f += RK_TPE) r += cs[f] > mine ? 1u : 0u;
+    for (; f + (RU - 1) * RK_TPE < c_gt; f += RU * RK_TPE) {
+        unsigned long long x[RU];
+#pragma unroll
+        for (int u = 0; u < RU; u++) x[u] = cs[f + u * RK_TPE];
+#pragma unroll
+        for (int u = 0; u < RU; u++) r += x[u] > mine ? 1u : 0u;
+    }
+    for (; f < c_gt; f += RK_TPE) r += cs[f] > mine ? 1u : 0u;
 #pragma unroll
     for (int o = 1; o < RK_TPE; o <<= 1) r += __shfl_xor(r, o, 64);
-    if (sub == 0 && e < c) idxs[r] = (int)(0xFFFFFFFFu - (uint32_t)mine);
+    if (sub == 0 && e < c_gt) idxs[r] = (int)(0xFFFFFFFFu - (uint32_t)mine);
 }
 
 /* ----------------------------------------------------- sparse attention */
@@ -882,13 +906,18 @@ k_attn_partial(float *__restrict__ pm, float *__restrict__ pl,
     }
 }
 
-__global__ void __launch_bounds__(AT_THREADS)
+/* Combine: workgroup (head, slice of CB_COLS columns); every workgroup of a
+ * head derives the same split weights and denominator. */
+constexpr int CB_COLS = 128;
+constexpr int CB_SPLITS = 1024;
+
+__global__ void __launch_bounds__(CB_COLS)
 k_attn_combine(float *__restrict__ o, const float *__restrict__ pm,
                const float *__restrict__ pl, const float *__restrict__ po,
                const float *__restrict__ sink, int nsplit, int d_v)
 {
     const int hh = blockIdx.x;
-    __shared__ float fs[1024];
+    __shared__ float fs[CB_SPLITS];
     __shared__ float sh_inv;
     const int tid = threadIdx.x;
     if (tid < 64) {
@@ -907,22 +936,30 @@ k_attn_combine(float *__restrict__ o, const float *__restrict__ pm,
             sh_inv = (float)(1.0 / denom);
         }
     }
+    const int c = blockIdx.y * CB_COLS + tid;
+    const bool live = c < d_v;
+    const int cc = live ? c : d_v - 1;
+    /* the partials' loads do not wait for the weights */
+    constexpr int B = 32;
+    float v[B];
+    int s0 = 0;
+#pragma unroll
+    for (int u = 0; u < B; u++)
+        v[u] = po[((size_t)hh * nsplit + min(u, nsplit - 1)) * d_v + cc];
     __syncthreads();
     const float inv = sh_inv;
-    for (int c = tid; c < d_v; c += AT_THREADS) {
-        float acc = 0.0f;
-        int s = 0;
-        for (; s + 8 <= nsplit; s += 8) {
-            float v[8];
+    float acc = 0.0f;
+    for (;;) {
 #pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = po[((size_t)hh * nsplit + s + u) * d_v + c];
+        for (int u = 0; u < B; u++)
+            if (s0 + u < nsplit) acc = fmaf(v[u], fs[s0 + u], acc);
+        s0 += B;
+        if (s0 >= nsplit) break;
 #pragma unroll
-            for (int u = 0; u < 8; u++) acc = fmaf(v[u], fs[s + u], acc);
-        }
-        for (; s < nsplit; s++)
-            acc = fmaf(po[((size_t)hh * nsplit + s) * d_v + c], fs[s], acc);
-        o[(size_t)hh * d_v + c] = acc * inv;
+        for (int u = 0; u < B; u++)
+            v[u] = po[((size_t)hh * nsplit + min(s0 + u, nsplit - 1)) * d_v + cc];
     }
+    if (live) o[(size_t)hh * d_v + c] = acc * inv;
 }
 
 /* ------------------------------------------ sparse attention, matrix core */
@@ -1348,12 +1385,9 @@ int dsv4_topk_launch(int *d_idxs, const float *d_scores, int n, int k,
     hipLaunchKernelGGL(k_tk_part, dim3(G), dim3(PT_THREADS), 0, st, cand, meta, bcnt,
                        blist, hist, d_scores, n, k);
     HIP_OK(hipGetLastError(), "topk partition launch");
-    hipLaunchKernelGGL(k_tk_refine, dim3(1), dim3(TK_THREADS), 0, st, d_idxs, cand, meta,
-                       bcnt, blist, hist, G, k);
-    HIP_OK(hipGetLastError(), "topk refine launch");
-    hipLaunchKernelGGL(k_tk_rank, dim3((k + RK_EPW - 1) / RK_EPW), dim3(256), 0, st,
-                       d_idxs, cand, meta);
-    HIP_OK(hipGetLastError(), "topk rank launch");
+    hipLaunchKernelGGL(k_tk_final, dim3((k + RK_EPW - 1) / RK_EPW), dim3(FN_THREADS), 0, st,
+                       d_idxs, cand, meta, bcnt, blist, hist, G, k);
+    HIP_OK(hipGetLastError(), "topk final launch");
     return 0;
 }
 
@@ -1427,8 +1461,8 @@ int dsv4_attn_launch(float *d_o, const float *d_q, const void *d_kv,
                            d_q, (const uint16_t *)d_kv, kv_stride, d_idxs, kv_rows, h,
                            d_qk, d_v, topk, scale);
         HIP_OK(hipGetLastError(), "attn mc launch");
-        hipLaunchKernelGGL(k_attn_combine, dim3(h), dim3(AT_THREADS), 0, st, d_o,
-                           pm, pl, po, d_sink, ns, d_v);
+        hipLaunchKernelGGL(k_attn_combine, dim3(h, (d_v + CB_COLS - 1) / CB_COLS),
+                           dim3(CB_COLS), 0, st, d_o, pm, pl, po, d_sink, ns, d_v);
         HIP_OK(hipGetLastError(), "attn combine launch");
         return 0;
     }
@@ -1441,8 +1475,8 @@ int dsv4_attn_launch(float *d_o, const float *d_q, const void *d_kv,
                            pm, pl, po, d_q, d_kv, kv_stride, d_idxs, kv_rows, h,
                            d_qk, d_v, topk, scale, sr, rowb, vec);
     HIP_OK(hipGetLastError(), "attn partial launch");
-    hipLaunchKernelGGL(k_attn_combine, dim3(h), dim3(AT_THREADS), 0, st, d_o,
-                       pm, pl, po, d_sink, nsplit, d_v);
+    hipLaunchKernelGGL(k_attn_combine, dim3(h, (d_v + CB_COLS - 1) / CB_COLS),
+                       dim3(CB_COLS), 0, st, d_o, pm, pl, po, d_sink, nsplit, d_v);
     HIP_OK(hipGetLastError(), "attn combine launch");
     return 0;
 }

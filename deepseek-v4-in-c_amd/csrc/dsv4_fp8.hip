@@ -102,23 +102,30 @@ __device__ __forceinline__ float dot16(const u32x4 v, const float *xr)
  * partials of rows wider than one wave (at most 4 waves per row). */
 constexpr int PART_MAX = 4096;
 
-template <int NCH>
-__device__ __forceinline__ void load_rows(u32x4 (*wv)[NCH], const uint8_t *W,
-                                          int rbase, int rend, int cols,
-                                          int j, int tc, const bool *act, int R)
+/* One step's weights (R rows x NCH chunks) and the block scales of its row
+ * block (the R rows of a step lie in one row block: the launcher picks R
+ * dividing blk_r, and steps start at multiples of R). Every load is issued
+ * unconditionally -- rows past the end read the last row, inactive chunks
+ * the last chunk, and their results are discarded -- so no branch stands
+ * between the loads and the waits that count them. */
+template <int NCH, int R, int SF>
+__device__ __forceinline__ void load_step(u32x4 (*wv)[NCH], float *sv, const uint8_t *W,
+                                          const void *S, int rbase, int rend, int cols,
+                                          int ch, int j, int tc, const int *cb, int sc,
+                                          int blk_r)
 {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        if (i >= R) break;
-        const int r = rbase + i;
+    for (int i = 0; i < R; i++) {
+        const int r = min(rbase + i, rend - 1);
 #pragma unroll
         for (int n = 0; n < NCH; n++) {
-            if (act[n] && r < rend)
-                wv[i][n] = ld16_stream(W + (size_t)r * cols + (size_t)(j + n * tc) * 16);
-            else
-                wv[i][n] = u32x4{0, 0, 0, 0};
+            const int c = min(j + n * tc, ch - 1);
+            wv[i][n] = ldg16_stream(W + (size_t)r * cols + (size_t)c * 16);
         }
     }
+    const int rb = min(rbase, rend - 1) / blk_r;
+#pragma unroll
+    for (int n = 0; n < NCH; n++) sv[n] = ld_scale<SF>(S, (size_t)rb * sc + cb[n]);
 }
 
 /* One workgroup owns the contiguous rows [row0, row0 + rows_per_wg). It walks
@@ -163,34 +170,26 @@ k_fp8_gemv(float *__restrict__ y, const float *__restrict__ x,
         }
     }
 
-    int cur_rb = -1;
-    float sreg[NCH];
-#pragma unroll
-    for (int n = 0; n < NCH; n++) sreg[n] = 0.0f;
-
     u32x4 wv[R][NCH], wn[R][NCH];
-    if (nsteps > 0) load_rows<NCH>(wv, W, row0 + g * R, rend, cols, j, tc, act, R);
+    float sv[NCH], sn[NCH];
+    if (nsteps > 0)
+        load_step<NCH, R, SF>(wv, sv, W, S, row0 + g * R, rend, cols, ch, j, tc, cb, sc, blk_r);
 
     for (int step = 0; step < nsteps; ++step) {
         const int rbase = row0 + step * step_rows + g * R;
         if (PF && step + 1 < nsteps)
-            load_rows<NCH>(wn, W, rbase + step_rows, rend, cols, j, tc, act, R);
+            load_step<NCH, R, SF>(wn, sn, W, S, rbase + step_rows, rend, cols, ch, j, tc, cb,
+                                  sc, blk_r);
 
         float acc[R];
 #pragma unroll
         for (int i = 0; i < R; i++) {
-            const int r = min(rbase + i, rows - 1);
-            const int rb = r / blk_r;
-            if (rb != cur_rb) {
-#pragma unroll
-                for (int n = 0; n < NCH; n++)
-                    sreg[n] = act[n] ? ld_scale<SF>(S, (size_t)rb * sc + cb[n]) : 0.0f;
-                cur_rb = rb;
-            }
             float a = 0.0f;
 #pragma unroll
-            for (int n = 0; n < NCH; n++)
-                a = fmaf(dot16(wv[i][n], xr[n]), sreg[n], a);
+            for (int n = 0; n < NCH; n++) {
+                const float d = fmaf(dot16(wv[i][n], xr[n]), sv[n], a);
+                a = act[n] ? d : a;
+            }
             acc[i] = a;
         }
 
@@ -215,8 +214,11 @@ k_fp8_gemv(float *__restrict__ y, const float *__restrict__ x,
             for (int i = 0; i < R; i++)
 #pragma unroll
                 for (int n = 0; n < NCH; n++) wv[i][n] = wn[i][n];
+#pragma unroll
+            for (int n = 0; n < NCH; n++) sv[n] = sn[n];
         } else if (step + 1 < nsteps) {
-            load_rows<NCH>(wv, W, rbase + step_rows, rend, cols, j, tc, act, R);
+            load_step<NCH, R, SF>(wv, sv, W, S, rbase + step_rows, rend, cols, ch, j, tc, cb,
+                                  sc, blk_r);
         }
     }
 
@@ -447,6 +449,7 @@ int dsv4_fp8_gemv_launch(float *y, const float *x, const uint8_t *W,
          * (four when rows are narrow). The environment can override each. */
         int R = env_int("DSV4_GPU_FP8_R", 2);
         R = R >= 4 ? 4 : R >= 2 ? 2 : 1;
+        while (blk_r % R) R >>= 1;               /* a step stays in one row block */
         const int pf = env_int("DSV4_GPU_FP8_PF", rows <= 4096 ? 1 : 0);
         int wpc = env_int("DSV4_GPU_FP8_WPC", cols >= 4096 ? 2 : 4);
         if (wpc <= 0) wpc = 2;

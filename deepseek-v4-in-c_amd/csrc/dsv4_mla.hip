@@ -7,30 +7,27 @@
  * (double)k[t][c]; then, in head order, `if (dot > 0) total += dot * w[h]`
  * with the multiply and the add rounded separately (this file is built with
  * -ffp-contract=off); out[t] = (float)total * scale, the scale computed by
- * the caller in float as the reference does. One thread per (t, h) runs the
- * 128-step fp64 chain; a thread per t then folds the heads in order. q and
- * the workgroup's key rows are staged in LDS as f32 (FP8 keys dequantised
- * exactly: e4m3(code) * row_scale) and widened exactly to double per use.
+ * the caller in float as the reference does. Lane = key row: a wave runs
+ * the chains of 8 heads for 64 rows, q reaching every lane through a DPP
+ * row broadcast fused into the fma (k_iscore). With a top-k to follow, the
+ * kernel also builds its level-1 histogram.
  *
  * TOP-K (dsv4_indexer.c:92-106), bit-exact: the k largest, ordered by score
- * descending, ties to the lower index. One workgroup of 1024 threads:
- *   - scores map to order-preserving 32-bit keys (-0.0 folded into +0.0,
- *     since the reference's `>` treats them as equal);
- *   - four 8-bit radix passes find T, the exact key of the k-th largest, and
- *     how many of the elements equal to T are needed;
- *   - a block scan over contiguous index ranges compacts the elements > T
- *     and the first needed elements == T in index order;
- *   - the > T elements are bitonic-sorted in LDS by (key desc, index asc);
- *     the == T ones already follow in index order.
+ * descending, ties to the lower index. Scores map to order-preserving 32-bit
+ * keys (-0.0 folded into +0.0, since the reference's `>` treats them as
+ * equal); a radix select over the key's bits 31..21 (the histogram), 20..10
+ * and 9..0 finds T, the key of the k-th largest, and how many elements equal
+ * to T are taken; the elements > T are ordered by (key desc, index asc) by
+ * counting, for each, the candidates ahead of it (k_tk_part, k_tk_final).
  *
  * SPARSE ATTENTION (dsv4_attn.c:60-108): split over the selected rows and a
- * log-sum-exp combine. Partial pass: per (split of SR rows, group of HB
- * heads) a workgroup computes scores (fp32 dots, one wave per row), the
- * split's max m_s, e_j = expf(s_j - m_s), l_s = sum e_j and o_s = sum_j e_j *
- * v_j. Combine: M = max m_s, denom = sum l_s expf(m_s - M) (+ expf(sink - M)
- * when a sink is given: denominator only, not in the max),
- * o = (sum o_s expf(m_s - M)) * (float)(1/denom). Masked (-1) rows take no
- * part. Agrees with the reference within 1e-5 relative.
+ * log-sum-exp combine. Partial pass: per split of selected rows, the scores,
+ * the split's max m_s, e_j = expf(s_j - m_s), l_s = sum e_j and o_s = sum_j
+ * e_j * v_j -- on the matrix cores for bf16 KV (k_attn_mc), on the VALU
+ * otherwise (k_attn_partial). Combine: M = max m_s, denom = sum l_s
+ * expf(m_s - M) (+ expf(sink - M) when a sink is given: denominator only,
+ * not in the max), o = (sum o_s expf(m_s - M)) * (float)(1/denom). Masked
+ * (-1) rows take no part. Agrees with the reference within 1e-5 relative.
  */
 #include "dsv4_dev.h"
 #include "dsv4_internal.h"

@@ -241,6 +241,13 @@ int register_expert(int layer, int expert, const Dsv4ExpertDev &d, int hidden,
 {
     LayerExperts *L = layer_slot(layer, expert);
     if (!L) return -1;
+    /* the kernels read weights in 16-byte and scales in 4-byte pieces */
+    if ((((uintptr_t)d.w1 | (uintptr_t)d.w3 | (uintptr_t)d.w2) & 15) ||
+        (((uintptr_t)d.s1 | (uintptr_t)d.s3 | (uintptr_t)d.s2) & 3)) {
+        DSV4_ERR("layer %d expert %d: weights must be 16-byte and scales 4-byte aligned",
+                 layer, expert);
+        return -1;
+    }
     if ((L->hidden || L->inter) && (L->hidden != hidden || L->inter != inter)) {
         DSV4_ERR("layer %d expert %d is %dx%d but the layer's experts are %dx%d",
                  layer, expert, inter, hidden, L->inter, L->hidden);

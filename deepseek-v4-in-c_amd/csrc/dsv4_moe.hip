@@ -163,39 +163,55 @@ k_moe_gate_up(float *__restrict__ h, const float *__restrict__ x,
     uint32_t sg_[R][NCH], su_[R][NCH], nsg[R][NCH], nsu[R][NCH];
     bool bad[R];
 
-    auto load = [&](int rbase, u32x4 (*G)[NCH], u32x4 (*U)[NCH],
+    /* This row group's first h-row as (expert slot, row): advanced by
+     * step_rows per step without a division. Rows past the workgroup's end
+     * read row rend-1 and are not stored; a missing expert reads x (valid
+     * memory) and stores NaN. Every load is unconditional, so no branch
+     * stands between the loads and the waits that count them. */
+    const int hr0 = row0 + g * R;
+    int kq = hr0 / inter, oq = hr0 - kq * inter;
+    const int klast = (rend - 1) / inter, olast = (rend - 1) - klast * inter;
+    const uint8_t *xb = (const uint8_t *)x;
+    int cc[NCH];
+#pragma unroll
+    for (int n = 0; n < NCH; n++) cc[n] = min(j + n * tc, ch - 1);
+
+    auto load = [&](int hr, int k_, int o_, u32x4 (*G)[NCH], u32x4 (*U)[NCH],
                     uint32_t (*SG)[NCH], uint32_t (*SU)[NCH], bool *B) {
 #pragma unroll
         for (int i = 0; i < R; i++) {
-            const int hr = rbase + i;
-            const bool ok = hr < rend;
-            const int k = ok ? hr / inter : 0;
-            const int o = ok ? hr - k * inter : 0;
-            const Dsv4ExpertDev *e = (ok && sx[k].w1) ? &sx[k] : nullptr;
-            if (B) B[i] = ok && !e;
+            int ki = k_, oi = o_ + i;
+            if (oi >= inter) { oi -= inter; ki++; }
+            const bool ok = hr + i < rend;
+            if (!ok) { ki = klast; oi = olast; }
+            const Dsv4ExpertDev &e = sx[ki];
+            const bool miss = e.w1 == nullptr;
+            const uint8_t *p1 = miss ? xb : e.w1 + (size_t)oi * rowb;
+            const uint8_t *p3 = miss ? xb : e.w3 + (size_t)oi * rowb;
+            const uint8_t *q1 = miss ? xb : e.s1 + (size_t)oi * rows_s;
+            const uint8_t *q3 = miss ? xb : e.s3 + (size_t)oi * rows_s;
+            B[i] = ok && miss;
 #pragma unroll
             for (int n = 0; n < NCH; n++) {
-                const int c = j + n * tc;
-                if (e && act[n]) {
-                    G[i][n] = ldg16_stream(e->w1 + (size_t)o * rowb + (size_t)c * 16);
-                    U[i][n] = ldg16_stream(e->w3 + (size_t)o * rowb + (size_t)c * 16);
-                    SG[i][n] = ldg8(e->s1 + (size_t)o * rows_s + c);
-                    SU[i][n] = ldg8(e->s3 + (size_t)o * rows_s + c);
-                } else {
-                    G[i][n] = u32x4{0, 0, 0, 0};
-                    U[i][n] = u32x4{0, 0, 0, 0};
-                    SG[i][n] = 0u;
-                    SU[i][n] = 0u;
-                }
+                G[i][n] = ldg16_stream(p1 + (size_t)cc[n] * 16);
+                U[i][n] = ldg16_stream(p3 + (size_t)cc[n] * 16);
+                SG[i][n] = ldg8(q1 + cc[n]);
+                SU[i][n] = ldg8(q3 + cc[n]);
             }
         }
     };
+    auto advance = [&](int &k_, int &o_) {
+        o_ += step_rows;
+        while (o_ >= inter) { o_ -= inter; k_++; }
+    };
 
-    if (nsteps > 0) load(row0 + g * R, wg_, wu_, sg_, su_, bad);
+    if (nsteps > 0) load(hr0, kq, oq, wg_, wu_, sg_, su_, bad);
     for (int step = 0; step < nsteps; ++step) {
         const int rbase = row0 + step * step_rows + g * R;
         bool nbad[R];
-        if (PF && step + 1 < nsteps) load(rbase + step_rows, ng_, nu_, nsg, nsu, nbad);
+        int kn = kq, on = oq;
+        advance(kn, on);
+        if (PF && step + 1 < nsteps) load(rbase + step_rows, kn, on, ng_, nu_, nsg, nsu, nbad);
 
         float ag[R], au[R];
 #pragma unroll
@@ -203,8 +219,10 @@ k_moe_gate_up(float *__restrict__ h, const float *__restrict__ x,
             float a = 0.0f, b = 0.0f;
 #pragma unroll
             for (int n = 0; n < NCH; n++) {
-                a = fmaf(dot32(wg_[i][n], xr[n]), dec_e8m0(sg_[i][n]), a);
-                b = fmaf(dot32(wu_[i][n], xr[n]), dec_e8m0(su_[i][n]), b);
+                const float da = fmaf(dot32(wg_[i][n], xr[n]), dec_e8m0(sg_[i][n]), a);
+                const float db = fmaf(dot32(wu_[i][n], xr[n]), dec_e8m0(su_[i][n]), b);
+                a = act[n] ? da : a;
+                b = act[n] ? db : b;
             }
             ag[i] = a; au[i] = b;
         }
@@ -241,8 +259,10 @@ k_moe_gate_up(float *__restrict__ h, const float *__restrict__ x,
                 }
             }
         } else if (step + 1 < nsteps) {
-            load(rbase + step_rows, wg_, wu_, sg_, su_, bad);
+            load(rbase + step_rows, kn, on, wg_, wu_, sg_, su_, bad);
         }
+        kq = kn;
+        oq = on;
     }
 
     if (tc > 64) {

@@ -392,6 +392,278 @@ k_mc_down(float *__restrict__ out, const uint16_t *__restrict__ ht,
     }
 }
 
+/* ------------------------------------------------- staged matrix-core form */
+
+/* The MFMA's fragment order reads 16 rows x 64 B per load, which streams at
+ * about 4.6 TB/s; loads of 4 rows x 256 B stream at 6.3 TB/s (measured on
+ * MI355X over the C3 expert bytes). So here each wave brings a unit of 16
+ * rows x 256 B (and the unit's scale bytes) into its own LDS area in that
+ * order, and reads the fragments back from LDS. The arithmetic is that of
+ * k_mc_gate_up / k_mc_down: lane (row r, group g) takes the 16 bytes of row
+ * r at [64 qb + 16 g, +16) of the unit and feeds dword m to the MFMA of
+ * chunk (qb, m); B reads the activation terms in the same permuted K order. */
+constexpr int M2_UB = 256;                       /* bytes per row per unit */
+constexpr int M2_WP = M2_UB + 16;                /* LDS row pitch (bank skew) */
+constexpr int M2_SOFF = 16 * M2_WP;              /* scales after the 16 rows */
+constexpr int M2_WBUF = M2_SOFF + 16 * 16;       /* one wave's unit buffer */
+
+struct M2Unit {
+    u32x4 w[4];                                  /* rows 4q + lane/16, 16 bytes */
+    uint32_t s;                                  /* scale bytes of row lane/4 */
+};
+
+/* The unit u of the 16-row tile whose row 0 starts at base (scales at sb);
+ * always in bounds for u < the row's unit count. */
+__device__ __forceinline__ void m2_load(M2Unit &U, const uint8_t *base, size_t rowb,
+                                        const uint8_t *sb, int nsb, int u, int lane)
+{
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        U.w[q] = ldg16_stream(base + (size_t)(4 * q + (lane >> 4)) * rowb + M2_UB * u +
+                              16 * (lane & 15));
+    U.s = *(const DSV4_GLOBAL uint32_t *)(sb + (size_t)(lane >> 2) * nsb + 16 * u +
+                                          4 * (lane & 3));
+}
+
+__device__ __forceinline__ void m2_stage(unsigned char *buf, const M2Unit &U, int lane)
+{
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        *reinterpret_cast<u32x4 *>(buf + (4 * q + (lane >> 4)) * M2_WP + 16 * (lane & 15)) = U.w[q];
+    *reinterpret_cast<uint32_t *>(buf + M2_SOFF + (lane >> 2) * 16 + 4 * (lane & 3)) = U.s;
+}
+
+/* acc[qb & 1] += the unit's 16 chunks; bl = this lane's activation-term
+ * plane in LDS at the unit's first element (a zero plane for columns >= 3).
+ * live = false adds zero (the weights are decoded with scale 0). */
+__device__ __forceinline__ void m2_mac(v4f *acc, const unsigned char *buf,
+                                       const uint16_t *bl, int lane, bool live)
+{
+    const int r = lane & 15, g = lane >> 4;
+    const u32x4 sv = *reinterpret_cast<const u32x4 *>(buf + M2_SOFF + r * 16);
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+    for (int qb = 0; qb < 4; qb++) {
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(buf + r * M2_WP + 64 * qb + 16 * g);
+        const float sc = live ? dec_e8m0((sw[qb] >> (8 * g)) & 0xFFu) : 0.0f; /* segment 4 qb + g */
+        const uint32_t d[4] = {a.x, a.y, a.z, a.w};
+        /* only the lanes of columns 0..MC_NT-1 carry terms; the others
+         * feed zeros without an LDS read */
+        u32x4 bw[4] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u},
+                       u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+        if (r < MC_NT) {
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+                bw[m] = *reinterpret_cast<const u32x4 *>(bl + 128 * qb + 32 * g + 8 * m);
+        }
+        v8bf b[4];
+#pragma unroll
+        for (int m = 0; m < 4; m++) b[m] = __builtin_bit_cast(v8bf, bw[m]);
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+            acc[qb & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(d[m], sc), b[m],
+                                                                   acc[qb & 1], 0, 0, 0);
+    }
+}
+
+/* Units 0 .. nu-1 of one 16-row tile, D units in flight in VGPRs; the LDS
+ * buffer is the wave's own (its writes follow its previous reads in order).
+ * NU > 0 is the unit count known at compile time: the loop unrolls whole, so
+ * each unit's wait counts only its own loads (a loop-carried wait is for all
+ * of them). Otherwise the loop is straight-line per D units: past the last
+ * unit, a slot reloads the last unit and is added with scale 0. */
+template <int D>
+__device__ __forceinline__ void m2_prologue(M2Unit *P, const uint8_t *base, size_t rowb,
+                                            const uint8_t *sb, int nsb, int nu, int lane)
+{
+#pragma unroll
+    for (int j = 0; j < D; j++) m2_load(P[j], base, rowb, sb, nsb, min(j, nu - 1), lane);
+}
+
+/* P holds the first D units, requested by m2_prologue (a caller can issue
+ * them before staging the activation terms). */
+template <int D, int NU>
+__device__ __forceinline__ v4f m2_tile(M2Unit *P, const uint8_t *base, size_t rowb,
+                                       const uint8_t *sb, int nsb, int nu, unsigned char *buf,
+                                       const uint16_t *bl0, int lane)
+{
+    v4f acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+    if (NU > 0) nu = NU;
+    if (NU > 0) {
+        /* the scheduling barriers keep each unit's loads where they are
+         * issued: sunk toward their use, they would no longer be in flight
+         * D units ahead */
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < NU; u++) {
+            m2_stage(buf, P[u % D], lane);
+            if (u + D < NU) m2_load(P[u % D], base, rowb, sb, nsb, u + D, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            m2_mac(acc, buf, bl0 + 512 * u, lane, true);
+        }
+    } else {
+        for (int u0 = 0; u0 < nu; u0 += D) {
+#pragma unroll
+            for (int j = 0; j < D; j++) {
+                const int u = u0 + j;
+                m2_stage(buf, P[j], lane);
+                m2_load(P[j], base, rowb, sb, nsb, min(u + D, nu - 1), lane);
+                m2_mac(acc, buf, bl0 + 512 * min(u, nu - 1), lane, u < nu);
+            }
+        }
+    }
+    return acc[0] + acc[1];
+}
+
+/* x (f32) -> its MC_NT bf16 term planes in LDS (pitch mc_pitch(n)) and one
+ * zero plane after them. */
+__device__ __forceinline__ void m2_split_x(uint16_t *lds, const float *x, int n)
+{
+    const int pitch = mc_pitch(n);
+    for (int i = threadIdx.x * 4; i < n; i += blockDim.x * 4) {
+        const f32x4 v = *(const DSV4_GLOBAL f32x4 *)(x + i);
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            uint32_t t[MC_NT];
+            bf16_terms(vv[e], t);
+#pragma unroll
+            for (int c = 0; c < MC_NT; c++) lds[c * pitch + i + e] = (uint16_t)t[c];
+            lds[MC_NT * pitch + i + e] = 0;
+        }
+    }
+}
+
+/* Pass A: workgroup (32 h-rows of expert slot k); wave w: matrix w & 1 (w1 /
+ * w3), row tile w >> 1. The workgroup splits x into its bf16 terms in LDS
+ * while its first weight units are in flight. */
+template <int D, int NU>
+__global__ void __launch_bounds__(256)
+k_mc2_gate_up(uint16_t *__restrict__ ht, const float *__restrict__ x,
+              const Dsv4ExpertDev *__restrict__ table, int n_table,
+              const int *__restrict__ idx, int hidden, int inter, float limit)
+{
+    extern __shared__ __attribute__((aligned(16))) unsigned char m2lds[];
+    uint16_t *xl = (uint16_t *)m2lds;                      /* [MC_NT+1][pitch] */
+    __shared__ float red[2][2][16];
+    const int k = blockIdx.y;
+    const Dsv4ExpertDev E = mc_expert(table, n_table, idx, k);
+    if (!E.w1) return;                      /* the down pass reports it (NaN) */
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int mat = w & 1, tile = w >> 1;
+    const int o0 = blockIdx.x * 32 + 16 * tile;
+    const int nsb = hidden >> 5;
+    const size_t rowb = (size_t)hidden >> 1;
+    const int nu = (int)(rowb / M2_UB);
+    const int pitch = mc_pitch(hidden);
+    unsigned char *buf = m2lds + (size_t)(MC_NT + 1) * pitch * 2 + (size_t)w * M2_WBUF;
+    const uint8_t *base = (mat ? E.w3 : E.w1) + (size_t)o0 * rowb;
+    const uint8_t *sb = (mat ? E.s3 : E.s1) + (size_t)o0 * nsb;
+
+    M2Unit P[D];
+    m2_prologue<D>(P, base, rowb, sb, nsb, NU > 0 ? NU : nu, lane);
+    m2_split_x(xl, x, hidden);
+    __syncthreads();
+    const int r = lane & 15, g = lane >> 4;
+    const uint16_t *bl = xl + (r < MC_NT ? r : MC_NT) * pitch;
+    const v4f acc = m2_tile<D, NU>(P, base, rowb, sb, nsb, nu, buf, bl, lane);
+    const v4f s = term_sum(acc, lane);
+    if (r == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) red[tile][mat][4 * g + j] = s[j];
+    }
+    __syncthreads();
+    if (tid < 32) {
+        const int t = tid >> 4, i = tid & 15;
+        uint32_t tt[MC_NT];
+        bf16_terms(swiglu1(red[t][0][i], red[t][1][i], limit), tt);
+#pragma unroll
+        for (int c = 0; c < MC_NT; c++)
+            ht[((size_t)k * MC_NT + c) * inter + blockIdx.x * 32 + 16 * t + i] = (uint16_t)tt[c];
+    }
+}
+
+/* Pass B + combine: workgroup (32 output rows); wave w takes slots w, w + nw,
+ * ..., both row tiles of each; the h terms of every slot are staged in LDS;
+ * acc_k meets in LDS for the k-ordered combine. */
+template <int D, int NU>
+__global__ void __launch_bounds__(512)
+k_mc2_down(float *__restrict__ out, const uint16_t *__restrict__ ht,
+           const Dsv4ExpertDev *__restrict__ table, int n_table,
+           const int *__restrict__ idx, const float *__restrict__ wts, int topk,
+           int hidden, int inter)
+{
+    extern __shared__ __attribute__((aligned(16))) unsigned char m2lds[];
+    uint16_t *hl = (uint16_t *)m2lds;                      /* [topk*MC_NT+1][pitch] */
+    __shared__ float accl[MC_KMAX][32];
+    const int r0 = blockIdx.x * 32;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int nw = blockDim.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int nsb = inter >> 5;
+    const size_t rowb = (size_t)inter >> 1;
+    const int nu = (int)(rowb / M2_UB);
+    const int pitch = mc_pitch(inter);
+    unsigned char *buf = m2lds + (size_t)(topk * MC_NT + 1) * pitch * 2 + (size_t)w * M2_WBUF;
+
+    /* the first tile of this wave's first slot is requested before the h
+     * terms are staged */
+    M2Unit P[D];
+    const int nuu = NU > 0 ? NU : nu;
+    Dsv4ExpertDev E = w < topk ? mc_expert(table, n_table, idx, w)
+                               : Dsv4ExpertDev{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    if (E.w1) m2_prologue<D>(P, E.w2 + (size_t)r0 * rowb, rowb, E.s2 + (size_t)r0 * nsb, nsb,
+                             nuu, lane);
+    mc_stage(hl, ht, topk * MC_NT, inter);
+    __syncthreads();
+    for (int k = w; k < topk; k += nw) {
+        if (k != w) E = mc_expert(table, n_table, idx, k);
+        if (!E.w1) {
+            if (lane < 32) accl[k][lane] = __builtin_nanf("");
+            continue;
+        }
+        const uint16_t *bl = hl + (r < MC_NT ? k * MC_NT + r : topk * MC_NT) * pitch;
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            if (t > 0 || k != w)
+                m2_prologue<D>(P, E.w2 + (size_t)(r0 + 16 * t) * rowb, rowb,
+                               E.s2 + (size_t)(r0 + 16 * t) * nsb, nsb, nuu, lane);
+            const v4f acc = m2_tile<D, NU>(P, E.w2 + (size_t)(r0 + 16 * t) * rowb, rowb,
+                                           E.s2 + (size_t)(r0 + 16 * t) * nsb, nsb, nu, buf,
+                                           bl, lane);
+            const v4f s = term_sum(acc, lane);
+            if (r == 0) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) accl[k][16 * t + 4 * g + j] = s[j];
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < 32) {
+        float o = 0.0f;
+        for (int kk = 0; kk < topk; kk++) {
+            const float p = wts[kk] * accl[kk][tid];
+            o = o + p;
+        }
+        out[r0 + tid] = o;
+    }
+}
+
+size_t m2_lds_a(int hidden) { return (size_t)(MC_NT + 1) * mc_pitch(hidden) * 2 + 4 * M2_WBUF; }
+size_t m2_lds_b(int topk, int inter, int nw)
+{
+    return (size_t)(topk * MC_NT + 1) * mc_pitch(inter) * 2 + (size_t)nw * M2_WBUF;
+}
+
+bool m2_shape_ok(int topk, int hidden, int inter)
+{
+    if (topk <= 0 || topk > MC_KMAX || hidden <= 0 || inter <= 0 ||
+        (hidden % 512) || (inter % 512) || (inter % 32) || (hidden % 32))
+        return false;
+    const size_t cap = dsv4_lds_limit() - 8 * 1024;      /* static LDS of the kernels */
+    return m2_lds_a(hidden) <= cap && m2_lds_b(topk, inter, 8) <= cap;
+}
+
 size_t mc_lds_a(int hidden) { return (size_t)(MC_NT + 1) * mc_pitch(hidden) * 2; }
 size_t mc_lds_b(int topk, int inter) { return (size_t)(topk * MC_NT + 1) * mc_pitch(inter) * 2; }
 
@@ -430,7 +702,8 @@ size_t dsv4_moe_scratch_bytes(int topk, int hidden, int inter)
 {
     if (topk <= 0 || hidden <= 0 || inter <= 0) return 0;
     const size_t valu = a256((size_t)topk * inter * sizeof(float));
-    const size_t mc = mc_shape_ok(topk, hidden, inter) ? mc_scratch_bytes(topk, hidden, inter) : 0;
+    const size_t mc = (mc_shape_ok(topk, hidden, inter) || m2_shape_ok(topk, hidden, inter))
+                    ? mc_scratch_bytes(topk, hidden, inter) : 0;
     return valu > mc ? valu : mc;
 }
 
@@ -440,19 +713,60 @@ int dsv4_moe_fp4_launch(float *d_out, const float *d_x,
                         int hidden, int inter, float limit, void *scratch,
                         hipStream_t st)
 {
-    /* The VALU form is the default: on MI355X it is faster at the C3 shape
-     * (49.9 vs 77 us), because the MFMA fragment order reads each weight row
-     * in 64-byte pieces spread over 16 rows per load, which streams from HBM
-     * at about 4.7 TB/s against 6.5 TB/s for 1 KB contiguous loads.
-     * DSV4_GPU_MOE_MC=1 selects this matrix-core form. */
-    if (!mc_shape_ok(topk, hidden, inter) || !mc_env("DSV4_GPU_MOE_MC", 0))
+    /* Forms (DSV4_GPU_MOE_MC): 2, the default, is the staged matrix-core
+     * form -- weights stream in 4-row x 256-byte loads (about 6.3 TB/s from
+     * HBM on MI355X) and reach the MFMA fragment order through wave-private
+     * LDS; 1 is the fragment-order form, whose 16-row x 64-byte loads stream
+     * at about 4.7 TB/s; 0 is the VALU form, also the fallback for shapes and
+     * alignments the matrix-core forms do not take. They differ only in the
+     * f32 summation order inside a row, and each gives the same bits on
+     * every run. */
+    const int form = mc_env("DSV4_GPU_MOE_MC", 2);
+    const bool m2 = form == 2 && m2_shape_ok(topk, hidden, inter)
+                 && ((uintptr_t)d_x & 15u) == 0;
+    if (!m2 && (form != 1 || !mc_shape_ok(topk, hidden, inter)))
         return dsv4_moe_fp4_valu_launch(d_out, d_x, d_table, n_table, d_idx, d_w, topk,
                                         hidden, inter, limit, (float *)scratch, st);
     uint16_t *xt = (uint16_t *)scratch;
     uint16_t *ht = (uint16_t *)((char *)scratch + a256((size_t)MC_NT * hidden * 2));
-    hipLaunchKernelGGL(k_mc_split, dim3((hidden + 255) / 256), dim3(256), 0, st, xt, d_x,
-                       hidden);
-    HIP_OK(hipGetLastError(), "moe split launch");
+    if (!m2) {
+        hipLaunchKernelGGL(k_mc_split, dim3((hidden + 255) / 256), dim3(256), 0, st, xt, d_x,
+                           hidden);
+        HIP_OK(hipGetLastError(), "moe split launch");
+    }
+    if (m2) {
+        /* The staged form (DSV4_GPU_MOE_MC=2): DSV4_GPU_MOE_D2 units in flight
+         * per wave. */
+        static bool opted2 = false;
+        if (!opted2) {
+            mc_lds_optin(k_mc2_gate_up<3, 14>); mc_lds_optin(k_mc2_gate_up<3, 0>);
+            mc_lds_optin(k_mc2_gate_up<2, 14>); mc_lds_optin(k_mc2_gate_up<4, 14>);
+            mc_lds_optin(k_mc2_down<3, 4>); mc_lds_optin(k_mc2_down<3, 0>);
+            mc_lds_optin(k_mc2_down<2, 4>); mc_lds_optin(k_mc2_down<4, 4>);
+            opted2 = true;
+        }
+        const int d2 = mc_env("DSV4_GPU_MOE_D2", 2);
+        const size_t la = m2_lds_a(hidden), lb = m2_lds_b(topk, inter, 8);
+        const dim3 ga(inter / 32, topk), gb(hidden / 32);
+        const int nua = hidden / 512, nub = inter / 512;   /* units per row */
+#define M2_A(D, NU) hipLaunchKernelGGL((k_mc2_gate_up<D, NU>), ga, dim3(256), la, st, ht, d_x, d_table, n_table, d_idx, hidden, inter, limit)
+#define M2_B(D, NU) hipLaunchKernelGGL((k_mc2_down<D, NU>), gb, dim3(512), lb, st, d_out, ht, d_table, n_table, d_idx, d_w, topk, hidden, inter)
+        if (nua == 14) {
+            if (d2 >= 4) M2_A(4, 14); else if (d2 == 3) M2_A(3, 14); else M2_A(2, 14);
+        } else {
+            M2_A(3, 0);
+        }
+        HIP_OK(hipGetLastError(), "moe gate/up launch");
+        if (nub == 4) {
+            if (d2 >= 4) M2_B(4, 4); else if (d2 == 3) M2_B(3, 4); else M2_B(2, 4);
+        } else {
+            M2_B(3, 0);
+        }
+        HIP_OK(hipGetLastError(), "moe down launch");
+#undef M2_A
+#undef M2_B
+        return 0;
+    }
     /* Row tiles per workgroup, waves per down workgroup and weight blocks in
      * flight (none changes the arithmetic of a row). */
     static bool opted = false;

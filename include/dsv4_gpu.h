@@ -150,7 +150,9 @@ int dsv4_gpu_upload_expert(int layer, int expert, const DSV4ExpertW *e);
 
 /* Register an expert whose tensors already live in HBM (e->*.w / .s are
  * device pointers owned by the caller, e.g. a checkpoint loaded straight into
- * device memory). Same keying and use as dsv4_gpu_upload_expert. */
+ * device memory). Same keying and use as dsv4_gpu_upload_expert. The weight
+ * pointers must be 16-byte and the scale pointers 4-byte aligned (-1 if
+ * not). */
 int dsv4_gpu_bind_expert_d(int layer, int expert, const DSV4ExpertW *e);
 
 int dsv4_gpu_has_expert(int layer, int expert);

@@ -58,24 +58,30 @@ def test_c3_full_shape(gpu, dsv4, limit):
     run_case(dsv4, 7168, 2048, 8, 256, 0, limit)
 
 
+@pytest.mark.parametrize("form", ["0", "1", "2"])
 @pytest.mark.parametrize("limit", [10.0, 0.0])
-def test_c3_full_shape_matrix_core_form(gpu, dsv4, monkeypatch, limit):
-    """The matrix-core form (bf16 MFMA, activation as three bf16 terms), which
-    DSV4_GPU_MOE_MC=1 selects for shapes that are multiples of 128."""
-    monkeypatch.setenv("DSV4_GPU_MOE_MC", "1")
+def test_c3_full_shape_each_form(gpu, dsv4, monkeypatch, limit, form):
+    """Each form: DSV4_GPU_MOE_MC=0 the VALU form; the matrix-core forms
+    (bf16 MFMA, activation as three bf16 terms) =1 reading the weights in
+    fragment order (shapes that are multiples of 128) and =2, the default,
+    staging them through LDS (multiples of 512)."""
+    monkeypatch.setenv("DSV4_GPU_MOE_MC", form)
     run_case(dsv4, 7168, 2048, 8, 256, 1, limit)
 
 
+@pytest.mark.parametrize("form", ["1", "2"])
 @pytest.mark.parametrize("hidden,inter,topk", [(4096, 2048, 6), (1024, 512, 16),
-                                               (128, 128, 1), (256, 4096, 3)])
-def test_matrix_core_form_other_shapes(gpu, dsv4, monkeypatch, hidden, inter, topk):
-    monkeypatch.setenv("DSV4_GPU_MOE_MC", "1")
+                                               (2048, 1024, 5), (128, 128, 1),
+                                               (256, 4096, 3)])
+def test_matrix_core_form_other_shapes(gpu, dsv4, monkeypatch, hidden, inter, topk, form):
+    monkeypatch.setenv("DSV4_GPU_MOE_MC", form)
     run_case(dsv4, hidden, inter, topk, 16, hidden + inter + 1, 10.0)
 
 
 def test_down_pass_forms(gpu, dsv4, monkeypatch):
     """Both down-pass shapes of the VALU form (wave per expert slot with 32 or
     16 rows per workgroup) and the row-group form give the oracle's result."""
+    monkeypatch.setenv("DSV4_GPU_MOE_MC", "0")
     for env in ({"DSV4_GPU_MOE_RBW": "16"}, {"DSV4_GPU_MOE_DOWNW": "0"}):
         for k, v in env.items():
             monkeypatch.setenv(k, v)
@@ -88,16 +94,21 @@ def test_down_pass_forms(gpu, dsv4, monkeypatch):
                                                (32, 32, 1), (512, 4096, 2),
                                                (1024, 512, 16), (128, 128, 1),
                                                (384, 640, 9)])
-def test_other_shapes(gpu, dsv4, hidden, inter, topk):
+@pytest.mark.parametrize("form", ["0", "2"])
+def test_other_shapes(gpu, dsv4, monkeypatch, hidden, inter, topk, form):
+    """Shapes the staged form does not take fall back to the VALU form."""
+    monkeypatch.setenv("DSV4_GPU_MOE_MC", form)
     run_case(dsv4, hidden, inter, topk, 16, hidden + inter, 10.0)
 
 
-def test_activation_dynamic_range(gpu, dsv4):
+@pytest.mark.parametrize("form", ["0", "1", "2"])
+def test_activation_dynamic_range(gpu, dsv4, monkeypatch, form):
     """x spanning twelve decades, with an all-zero 32-block, a block of f32
-    subnormals and one huge block: the matrix-core form writes x as e4m3
-    terms per 32-block, and each of these stresses a different edge of that
-    split."""
-    hidden, inter, topk = 1024, 256, 3
+    subnormals and one huge block, through every form: the matrix-core forms
+    carry x as three bf16 terms (hi + mid + lo), and each of these stresses a
+    different edge of that split."""
+    monkeypatch.setenv("DSV4_GPU_MOE_MC", form)
+    hidden, inter, topk = 1024, 512, 3
     rng = np.random.default_rng(21)
     ids = np.array([2, 0, 1], np.int32)
     experts = [common.fp4_expert(rng, hidden, inter) for _ in range(topk)]
@@ -115,8 +126,10 @@ def test_activation_dynamic_range(gpu, dsv4):
     assert err < TOL
 
 
-def test_repeatable_bits(gpu, dsv4):
+@pytest.mark.parametrize("form", ["0", "2"])
+def test_repeatable_bits(gpu, dsv4, monkeypatch, form):
     """The same call twice gives the same bits (fixed reduction order)."""
+    monkeypatch.setenv("DSV4_GPU_MOE_MC", form)
     hidden, inter, topk = 2048, 1024, 4
     rng = np.random.default_rng(22)
     for i in range(topk):

@@ -466,12 +466,7 @@ __device__ __forceinline__ void m2_mac(v4f *acc, const unsigned char *buf,
     }
 }
 
-/* Units 0 .. nu-1 of one 16-row tile, D units in flight in VGPRs; the LDS
- * buffer is the wave's own (its writes follow its previous reads in order).
- * NU > 0 is the unit count known at compile time: the loop unrolls whole, so
- * each unit's wait counts only its own loads (a loop-carried wait is for all
- * of them). Otherwise the loop is straight-line per D units: past the last
- * unit, a slot reloads the last unit and is added with scale 0. */
+/* The first D units of a 16-row tile (past unit nu-1, the last again). */
 template <int D>
 __device__ __forceinline__ void m2_prologue(M2Unit *P, const uint8_t *base, size_t rowb,
                                             const uint8_t *sb, int nsb, int nu, int lane)
@@ -480,8 +475,14 @@ __device__ __forceinline__ void m2_prologue(M2Unit *P, const uint8_t *base, size
     for (int j = 0; j < D; j++) m2_load(P[j], base, rowb, sb, nsb, min(j, nu - 1), lane);
 }
 
-/* P holds the first D units, requested by m2_prologue (a caller can issue
- * them before staging the activation terms). */
+/* Units 0 .. nu-1 of one 16-row tile, D units in flight in VGPRs; P holds
+ * the first D, requested by m2_prologue (a caller can issue them before it
+ * stages the activation terms). The LDS buffer is the wave's own (its writes
+ * follow its previous reads in order). NU > 0 is the unit count known at
+ * compile time: the loop unrolls whole, so each unit's wait counts only its
+ * own loads (a loop-carried wait is for all of them). Otherwise the loop is
+ * straight-line per D units: past the last unit, a slot reloads the last
+ * unit and is added with scale 0. */
 template <int D, int NU>
 __device__ __forceinline__ v4f m2_tile(M2Unit *P, const uint8_t *base, size_t rowb,
                                        const uint8_t *sb, int nsb, int nu, unsigned char *buf,
@@ -515,28 +516,45 @@ __device__ __forceinline__ v4f m2_tile(M2Unit *P, const uint8_t *base, size_t ro
     return acc[0] + acc[1];
 }
 
-/* x (f32) -> its MC_NT bf16 term planes in LDS (pitch mc_pitch(n)) and one
- * zero plane after them. */
-__device__ __forceinline__ void m2_split_x(uint16_t *lds, const float *x, int n)
+/* x staging, in two steps so that a caller can put other loads between
+ * them: m2_x_load requests NL 16-byte pieces of x per thread (elements i0 +
+ * 4 (j * blockDim + tid) ...; past n it reloads the last piece), m2_x_store
+ * writes their MC_NT bf16 terms into the planes at lds (pitch mc_pitch(n)).
+ * n is a multiple of 4 and x 16-byte aligned. */
+template <int NL>
+__device__ __forceinline__ void m2_x_load(f32x4 *xv, const float *x, int n, int i0)
+{
+#pragma unroll
+    for (int j = 0; j < NL; j++) {
+        const int i = i0 + 4 * (j * (int)blockDim.x + (int)threadIdx.x);
+        xv[j] = *(const DSV4_GLOBAL f32x4 *)(x + min(i, n - 4));
+    }
+}
+
+template <int NL>
+__device__ __forceinline__ void m2_x_store(uint16_t *lds, const f32x4 *xv, int n, int i0)
 {
     const int pitch = mc_pitch(n);
-    for (int i = threadIdx.x * 4; i < n; i += blockDim.x * 4) {
-        const f32x4 v = *(const DSV4_GLOBAL f32x4 *)(x + i);
-        const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            uint32_t t[MC_NT];
-            bf16_terms(vv[e], t);
+    for (int j = 0; j < NL; j++) {
+        const int i = i0 + 4 * (j * (int)blockDim.x + (int)threadIdx.x);
+        if (i < n) {
+            const float vv[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
 #pragma unroll
-            for (int c = 0; c < MC_NT; c++) lds[c * pitch + i + e] = (uint16_t)t[c];
-            lds[MC_NT * pitch + i + e] = 0;
+            for (int e = 0; e < 4; e++) {
+                uint32_t t[MC_NT];
+                bf16_terms(vv[e], t);
+#pragma unroll
+                for (int c = 0; c < MC_NT; c++) lds[c * pitch + i + e] = (uint16_t)t[c];
+            }
         }
     }
 }
 
 /* Pass A: workgroup (32 h-rows of expert slot k); wave w: matrix w & 1 (w1 /
- * w3), row tile w >> 1. The workgroup splits x into its bf16 terms in LDS
- * while its first weight units are in flight. */
+ * w3), row tile w >> 1. The workgroup splits x into its bf16 terms in LDS;
+ * all of x is requested before the first weight units, so the split waits
+ * for x alone while those units are in flight. */
 template <int D, int NU>
 __global__ void __launch_bounds__(256)
 k_mc2_gate_up(uint16_t *__restrict__ ht, const float *__restrict__ x,
@@ -544,7 +562,7 @@ k_mc2_gate_up(uint16_t *__restrict__ ht, const float *__restrict__ x,
               const int *__restrict__ idx, int hidden, int inter, float limit)
 {
     extern __shared__ __attribute__((aligned(16))) unsigned char m2lds[];
-    uint16_t *xl = (uint16_t *)m2lds;                      /* [MC_NT+1][pitch] */
+    uint16_t *xl = (uint16_t *)m2lds;                      /* [MC_NT][pitch] */
     __shared__ float red[2][2][16];
     const int k = blockIdx.y;
     const Dsv4ExpertDev E = mc_expert(table, n_table, idx, k);
@@ -556,16 +574,30 @@ k_mc2_gate_up(uint16_t *__restrict__ ht, const float *__restrict__ x,
     const size_t rowb = (size_t)hidden >> 1;
     const int nu = (int)(rowb / M2_UB);
     const int pitch = mc_pitch(hidden);
-    unsigned char *buf = m2lds + (size_t)(MC_NT + 1) * pitch * 2 + (size_t)w * M2_WBUF;
+    unsigned char *buf = m2lds + (size_t)MC_NT * pitch * 2 + (size_t)w * M2_WBUF;
     const uint8_t *base = (mat ? E.w3 : E.w1) + (size_t)o0 * rowb;
     const uint8_t *sb = (mat ? E.s3 : E.s1) + (size_t)o0 * nsb;
 
     M2Unit P[D];
-    m2_prologue<D>(P, base, rowb, sb, nsb, NU > 0 ? NU : nu, lane);
-    m2_split_x(xl, x, hidden);
+    if constexpr (NU > 0) {
+        constexpr int NL = (NU * 512 + 1023) / 1024;       /* hidden = 512 NU */
+        f32x4 xv[NL];
+        m2_x_load<NL>(xv, x, hidden, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        m2_prologue<D>(P, base, rowb, sb, nsb, NU, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        m2_x_store<NL>(xl, xv, hidden, 0);
+    } else {
+        m2_prologue<D>(P, base, rowb, sb, nsb, nu, lane);
+        for (int i0 = 0; i0 < hidden; i0 += 8 * 1024) {
+            f32x4 xv[8];
+            m2_x_load<8>(xv, x, hidden, i0);
+            m2_x_store<8>(xl, xv, hidden, i0);
+        }
+    }
     __syncthreads();
     const int r = lane & 15, g = lane >> 4;
-    const uint16_t *bl = xl + (r < MC_NT ? r : MC_NT) * pitch;
+    const uint16_t *bl = xl + min(r, MC_NT - 1) * pitch;
     const v4f acc = m2_tile<D, NU>(P, base, rowb, sb, nsb, nu, buf, bl, lane);
     const v4f s = term_sum(acc, lane);
     if (r == 0) {
@@ -583,9 +615,51 @@ k_mc2_gate_up(uint16_t *__restrict__ ht, const float *__restrict__ x,
     }
 }
 
+/* Both 16-row tiles of a 32-row group as one stream of 2 NU units (tile 0's
+ * units, then tile 1's), D in flight across the tile boundary; P holds units
+ * 0 .. D-1 (D <= NU). res[t] = tile t's sum. */
+template <int D, int NU>
+__device__ __forceinline__ void m2_tiles2(v4f *res, M2Unit *P, const uint8_t *base,
+                                          size_t rowb, const uint8_t *sb, int nsb,
+                                          unsigned char *buf, const uint16_t *bl0, int lane)
+{
+    static_assert(NU > 0 && D <= NU, "units in flight within the first tile");
+    v4f acc[2][2] = {{v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}},
+                     {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}}};
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 2 * NU; u++) {
+        const int t = u / NU, uu = u - t * NU;
+        m2_stage(buf, P[u % D], lane);
+        if (u + D < 2 * NU) {
+            const int t2 = (u + D) / NU, u2 = u + D - t2 * NU;
+            m2_load(P[u % D], base + (size_t)16 * t2 * rowb, rowb, sb + (size_t)16 * t2 * nsb,
+                    nsb, u2, lane);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        m2_mac(acc[t], buf, bl0 + 512 * uu, lane, true);
+    }
+    res[0] = acc[0][0] + acc[0][1];
+    res[1] = acc[1][0] + acc[1][1];
+}
+
+/* LDS of one down-pass wave: its slot's MC_NT h planes, then its unit
+ * buffer. */
+__host__ __device__ __forceinline__ size_t m2_hplanes_b(int inter)
+{
+    return (size_t)MC_NT * mc_pitch(inter) * 2;
+}
+__host__ __device__ __forceinline__ size_t m2_wave_b(int inter)
+{
+    return m2_hplanes_b(inter) + M2_WBUF;
+}
+__host__ __device__ __forceinline__ int m2_down_waves(int topk) { return topk < 8 ? topk : 8; }
+
 /* Pass B + combine: workgroup (32 output rows); wave w takes slots w, w + nw,
- * ..., both row tiles of each; the h terms of every slot are staged in LDS;
- * acc_k meets in LDS for the k-ordered combine. */
+ * ..., both row tiles of each. A wave stages its own slot's h terms in its
+ * own LDS (no workgroup barrier: it requests them before its first weight
+ * units and waits for them alone); acc_k meets in LDS for the k-ordered
+ * combine. */
 template <int D, int NU>
 __global__ void __launch_bounds__(512)
 k_mc2_down(float *__restrict__ out, const uint16_t *__restrict__ ht,
@@ -594,7 +668,6 @@ k_mc2_down(float *__restrict__ out, const uint16_t *__restrict__ ht,
            int hidden, int inter)
 {
     extern __shared__ __attribute__((aligned(16))) unsigned char m2lds[];
-    uint16_t *hl = (uint16_t *)m2lds;                      /* [topk*MC_NT+1][pitch] */
     __shared__ float accl[MC_KMAX][32];
     const int r0 = blockIdx.x * 32;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -604,34 +677,57 @@ k_mc2_down(float *__restrict__ out, const uint16_t *__restrict__ ht,
     const size_t rowb = (size_t)inter >> 1;
     const int nu = (int)(rowb / M2_UB);
     const int pitch = mc_pitch(inter);
-    unsigned char *buf = m2lds + (size_t)(topk * MC_NT + 1) * pitch * 2 + (size_t)w * M2_WBUF;
+    unsigned char *region = m2lds + (size_t)w * m2_wave_b(inter);
+    uint16_t *hl = (uint16_t *)region;
+    unsigned char *buf = region + m2_hplanes_b(inter);
+    const uint16_t *bl = hl + min(r, MC_NT - 1) * pitch;
 
-    /* the first tile of this wave's first slot is requested before the h
-     * terms are staged */
-    M2Unit P[D];
-    const int nuu = NU > 0 ? NU : nu;
-    Dsv4ExpertDev E = w < topk ? mc_expert(table, n_table, idx, w)
-                               : Dsv4ExpertDev{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
-    if (E.w1) m2_prologue<D>(P, E.w2 + (size_t)r0 * rowb, rowb, E.s2 + (size_t)r0 * nsb, nsb,
-                             nuu, lane);
-    mc_stage(hl, ht, topk * MC_NT, inter);
-    __syncthreads();
     for (int k = w; k < topk; k += nw) {
-        if (k != w) E = mc_expert(table, n_table, idx, k);
+        const Dsv4ExpertDev E = mc_expert(table, n_table, idx, k);
         if (!E.w1) {
             if (lane < 32) accl[k][lane] = __builtin_nanf("");
             continue;
         }
-        const uint16_t *bl = hl + (r < MC_NT ? k * MC_NT + r : topk * MC_NT) * pitch;
+        /* slot k's planes are contiguous in ht: MC_NT * inter elements */
+        const uint16_t *hk = ht + (size_t)k * MC_NT * inter;
+        const uint8_t *base = E.w2 + (size_t)r0 * rowb;
+        const uint8_t *sb = E.s2 + (size_t)r0 * nsb;
+        v4f res[2];
+        if constexpr (NU > 0) {
+            constexpr int IN = 512 * NU;                   /* inter */
+            constexpr int NH = MC_NT * IN / 512;           /* 1 KB pieces per wave */
+            u32x4 hv[NH];
+#pragma unroll
+            for (int j = 0; j < NH; j++)
+                hv[j] = *(const DSV4_GLOBAL u32x4 *)(hk + 512 * j + 8 * lane);
+            __builtin_amdgcn_sched_barrier(0);
+            M2Unit P[D];
+            m2_prologue<D>(P, base, rowb, sb, nsb, NU, lane);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < NH; j++) {
+                const int e = 512 * j + 8 * lane, c = e / IN;
+                *reinterpret_cast<u32x4 *>(hl + c * pitch + (e - c * IN)) = hv[j];
+            }
+            m2_tiles2<D, NU>(res, P, base, rowb, sb, nsb, buf, bl, lane);
+        } else {
+            for (int e = 8 * lane; e < MC_NT * inter; e += 512) {
+                const int c = e / inter;
+                *reinterpret_cast<u32x4 *>(hl + c * pitch + (e - c * inter)) =
+                    *(const DSV4_GLOBAL u32x4 *)(hk + e);
+            }
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                M2Unit P[D];
+                m2_prologue<D>(P, base + (size_t)16 * t * rowb, rowb, sb + (size_t)16 * t * nsb,
+                               nsb, nu, lane);
+                res[t] = m2_tile<D, 0>(P, base + (size_t)16 * t * rowb, rowb,
+                                       sb + (size_t)16 * t * nsb, nsb, nu, buf, bl, lane);
+            }
+        }
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            if (t > 0 || k != w)
-                m2_prologue<D>(P, E.w2 + (size_t)(r0 + 16 * t) * rowb, rowb,
-                               E.s2 + (size_t)(r0 + 16 * t) * nsb, nsb, nuu, lane);
-            const v4f acc = m2_tile<D, NU>(P, E.w2 + (size_t)(r0 + 16 * t) * rowb, rowb,
-                                           E.s2 + (size_t)(r0 + 16 * t) * nsb, nsb, nu, buf,
-                                           bl, lane);
-            const v4f s = term_sum(acc, lane);
+            const v4f s = term_sum(res[t], lane);
             if (r == 0) {
 #pragma unroll
                 for (int j = 0; j < 4; j++) accl[k][16 * t + 4 * g + j] = s[j];
@@ -649,11 +745,8 @@ k_mc2_down(float *__restrict__ out, const uint16_t *__restrict__ ht,
     }
 }
 
-size_t m2_lds_a(int hidden) { return (size_t)(MC_NT + 1) * mc_pitch(hidden) * 2 + 4 * M2_WBUF; }
-size_t m2_lds_b(int topk, int inter, int nw)
-{
-    return (size_t)(topk * MC_NT + 1) * mc_pitch(inter) * 2 + (size_t)nw * M2_WBUF;
-}
+size_t m2_lds_a(int hidden) { return (size_t)MC_NT * mc_pitch(hidden) * 2 + 4 * M2_WBUF; }
+size_t m2_lds_b(int topk, int inter) { return (size_t)m2_down_waves(topk) * m2_wave_b(inter); }
 
 bool m2_shape_ok(int topk, int hidden, int inter)
 {
@@ -661,7 +754,7 @@ bool m2_shape_ok(int topk, int hidden, int inter)
         (hidden % 512) || (inter % 512) || (inter % 32) || (hidden % 32))
         return false;
     const size_t cap = dsv4_lds_limit() - 8 * 1024;      /* static LDS of the kernels */
-    return m2_lds_a(hidden) <= cap && m2_lds_b(topk, inter, 8) <= cap;
+    return m2_lds_a(hidden) <= cap && m2_lds_b(topk, inter) <= cap;
 }
 
 size_t mc_lds_a(int hidden) { return (size_t)(MC_NT + 1) * mc_pitch(hidden) * 2; }
@@ -739,20 +832,21 @@ int dsv4_moe_fp4_launch(float *d_out, const float *d_x,
          * per wave. */
         static bool opted2 = false;
         if (!opted2) {
-            mc_lds_optin(k_mc2_gate_up<3, 14>); mc_lds_optin(k_mc2_gate_up<3, 0>);
-            mc_lds_optin(k_mc2_gate_up<2, 14>); mc_lds_optin(k_mc2_gate_up<4, 14>);
+            mc_lds_optin(k_mc2_gate_up<2, 14>); mc_lds_optin(k_mc2_gate_up<3, 14>);
+            mc_lds_optin(k_mc2_gate_up<3, 0>);
             mc_lds_optin(k_mc2_down<3, 4>); mc_lds_optin(k_mc2_down<3, 0>);
             mc_lds_optin(k_mc2_down<2, 4>); mc_lds_optin(k_mc2_down<4, 4>);
             opted2 = true;
         }
         const int d2 = mc_env("DSV4_GPU_MOE_D2", 2);
-        const size_t la = m2_lds_a(hidden), lb = m2_lds_b(topk, inter, 8);
+        const size_t la = m2_lds_a(hidden), lb = m2_lds_b(topk, inter);
+        const int nwb = m2_down_waves(topk);
         const dim3 ga(inter / 32, topk), gb(hidden / 32);
         const int nua = hidden / 512, nub = inter / 512;   /* units per row */
 #define M2_A(D, NU) hipLaunchKernelGGL((k_mc2_gate_up<D, NU>), ga, dim3(256), la, st, ht, d_x, d_table, n_table, d_idx, hidden, inter, limit)
-#define M2_B(D, NU) hipLaunchKernelGGL((k_mc2_down<D, NU>), gb, dim3(512), lb, st, d_out, ht, d_table, n_table, d_idx, d_w, topk, hidden, inter)
+#define M2_B(D, NU) hipLaunchKernelGGL((k_mc2_down<D, NU>), gb, dim3(64 * nwb), lb, st, d_out, ht, d_table, n_table, d_idx, d_w, topk, hidden, inter)
         if (nua == 14) {
-            if (d2 >= 4) M2_A(4, 14); else if (d2 == 3) M2_A(3, 14); else M2_A(2, 14);
+            if (d2 == 3) M2_A(3, 14); else M2_A(2, 14);
         } else {
             M2_A(3, 0);
         }

@@ -133,14 +133,14 @@ __device__ __forceinline__ void load_step(u32x4 (*wv)[NCH], float *sv, const uin
  * step); with PF the next step's weights are in flight while this step's are
  * consumed. Rows that span several waves leave one partial per wave in LDS,
  * summed in wave order after a single barrier at the end. */
-template <int NCH, int R, int SF, int PF>
+template <int NCH, int R, int SF, int PF, int XL>
 __global__ void __launch_bounds__(256)
 k_fp8_gemv(float *__restrict__ y, const float *__restrict__ x,
            const uint8_t *__restrict__ W, const void *__restrict__ S,
            int rows, int cols, int sc, int blk_r, int blk_c, int tc,
            int rows_per_wg)
 {
-    extern __shared__ float part[];     /* [waves per row][rows_per_wg] */
+    extern __shared__ float part[];     /* [waves per row][rows_per_wg], then x (XL) */
 
     const int tid = threadIdx.x;
     const int g = tid / tc;
@@ -162,18 +162,59 @@ k_fp8_gemv(float *__restrict__ y, const float *__restrict__ x,
         const int c = j + n * tc;
         act[n] = c < ch;
         cb[n] = act[n] ? (c * 16) / blk_c : 0;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const f32x4 v = act[n] ? ldf4(x + c * 16 + q * 4) : f32x4{0, 0, 0, 0};
-            xr[n][q * 4 + 0] = v.x; xr[n][q * 4 + 1] = v.y;
-            xr[n][q * 4 + 2] = v.z; xr[n][q * 4 + 3] = v.w;
-        }
     }
 
     u32x4 wv[R][NCH], wn[R][NCH];
     float sv[NCH], sn[NCH];
-    if (nsteps > 0)
-        load_step<NCH, R, SF>(wv, sv, W, S, row0 + g * R, rend, cols, ch, j, tc, cb, sc, blk_r);
+    if (XL) {
+        /* x once per workgroup: the whole workgroup requests all of x (four
+         * floats per thread per round, all rounds issued together), then the
+         * first step's weights; x lands in LDS and each thread reads its
+         * slice from there. Without this, every row group of the workgroup
+         * would fetch the same x from L2. */
+        float *xs = part + (size_t)(tc > 64 ? tc / 64 : 0) * rows_per_wg;
+        constexpr int XR = 4 * NCH;                    /* rounds: cols <= 1024 XR */
+        f32x4 xv[XR];
+        const int nq = cols >> 2;
+#pragma unroll
+        for (int q = 0; q < XR; q++)
+            xv[q] = ldf4(x + 4 * min(q * (int)blockDim.x + tid, nq - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        if (nsteps > 0)
+            load_step<NCH, R, SF>(wv, sv, W, S, row0 + g * R, rend, cols, ch, j, tc, cb, sc,
+                                  blk_r);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < XR; q++) {
+            const int i = q * (int)blockDim.x + tid;
+            if (i < nq) *reinterpret_cast<f32x4 *>(xs + 4 * i) = xv[q];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int n = 0; n < NCH; n++) {
+            const int c = min(j + n * tc, ch - 1);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(xs + c * 16 + q * 4);
+                xr[n][q * 4 + 0] = v.x; xr[n][q * 4 + 1] = v.y;
+                xr[n][q * 4 + 2] = v.z; xr[n][q * 4 + 3] = v.w;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int n = 0; n < NCH; n++) {
+            const int c = j + n * tc;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const f32x4 v = act[n] ? ldf4(x + c * 16 + q * 4) : f32x4{0, 0, 0, 0};
+                xr[n][q * 4 + 0] = v.x; xr[n][q * 4 + 1] = v.y;
+                xr[n][q * 4 + 2] = v.z; xr[n][q * 4 + 3] = v.w;
+            }
+        }
+        if (nsteps > 0)
+            load_step<NCH, R, SF>(wv, sv, W, S, row0 + g * R, rend, cols, ch, j, tc, cb, sc,
+                                  blk_r);
+    }
 
     for (int step = 0; step < nsteps; ++step) {
         const int rbase = row0 + step * step_rows + g * R;
@@ -368,6 +409,11 @@ void launch_gemv(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
                  const void *S, int rows, int cols, int sc, int blk_r,
                  int blk_c, int wgs_per_cu, hipStream_t st)
 {
+    /* x through LDS (one fetch per workgroup instead of one per row group)
+     * measured faster on MI355X for narrow rows (24576x1536: 12.2 -> 11.8
+     * us) and the widest (7168x16384: 24.8 -> 24.1 us), and within noise
+     * or slower between them. */
+    const int xl = g.wg == 256 && (cols & 3) == 0 && (cols <= 2048 || cols >= 16384);
     const int step_rows = g.rg * R;
     const int nsteps = (rows + step_rows - 1) / step_rows;
     const int want = wgs_per_cu * cu_count();
@@ -378,9 +424,24 @@ void launch_gemv(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
     if (spw < 1) spw = 1;
     const int rows_per_wg = spw * step_rows;
     const int grid = (rows + rows_per_wg - 1) / rows_per_wg;
-    const size_t lds = g.tc > 64 ? sizeof(float) * (size_t)wpr * rows_per_wg : 0;
-    hipLaunchKernelGGL((k_fp8_gemv<NCH, R, SF, PF>), dim3(grid), dim3(g.wg), lds, st,
-                       y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, rows_per_wg);
+    const size_t lds = (g.tc > 64 ? sizeof(float) * (size_t)wpr * rows_per_wg : 0)
+                     + (xl ? sizeof(float) * (size_t)cols : 0);
+    if (xl) {
+        static bool opted = false;                  /* x of up to 64 KB + partials */
+        if (!opted) {
+            (void)hipFuncSetAttribute((const void *)k_fp8_gemv<NCH, R, SF, PF, 1>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)dsv4_lds_limit());
+            (void)hipGetLastError();
+            opted = true;
+        }
+    }
+    if (xl)
+        hipLaunchKernelGGL((k_fp8_gemv<NCH, R, SF, PF, 1>), dim3(grid), dim3(g.wg), lds, st,
+                           y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, rows_per_wg);
+    else
+        hipLaunchKernelGGL((k_fp8_gemv<NCH, R, SF, PF, 0>), dim3(grid), dim3(g.wg), lds, st,
+                           y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, rows_per_wg);
 }
 
 template <int R, int SF, int PF>

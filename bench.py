@@ -208,6 +208,36 @@ class Bench:
         del dW, dS
         return us, eager, fp8_bytes(rows, cols)
 
+    def c1_host_run(self, calls=200):
+        """C1 through the reference-compatible host-buffer call dsv4_gpu_mmq:
+        x from host memory, y back to host memory, one synchronisation per
+        call (H2D + kernel + D2H). 16 resident copies (269 MB) are rotated so
+        the weights stay cold. Median wall time per call, in us."""
+        import ctypes
+        import time
+        np = self.np
+        rows = cols = 4096
+        W, Sf, Se, x = self.common.fp8_problem(0, rows, cols)
+        copies = 16
+        Ws = [W.copy() for _ in range(copies)]
+        ms = [self.dsv4.qmat(Wc, Se, self.dsv4.WFP8, rows, cols, 128, 128) for Wc in Ws]
+        for m in ms:
+            if self.L.dsv4_gpu_upload(ctypes.byref(m)) != 0:
+                raise RuntimeError("upload failed")
+        xh = np.ascontiguousarray(x, np.float32)
+        yh = np.empty(rows, np.float32)
+        px, py = xh.ctypes.data, yh.ctypes.data
+        for i in range(2 * copies):
+            self.L.dsv4_gpu_mmq(py, px, ctypes.byref(ms[i % copies]))
+        t = []
+        for i in range(calls):
+            t0 = time.perf_counter()
+            self.L.dsv4_gpu_mmq(py, px, ctypes.byref(ms[i % copies]))
+            t.append(time.perf_counter() - t0)
+        t.sort()
+        self._keep_host = (Ws, ms)
+        return t[len(t) // 2] * 1e6
+
     # ------------------------------------------------------------ C3
     def c3_run(self, steps, warmup):
         import ctypes
@@ -335,6 +365,28 @@ class Bench:
                 "ms_per_step": round(per * 1e3, 3)}
 
 
+_STDOUT_FD = None
+
+
+def quiet_stdout():
+    """Send the C library's stdout (its init banner, as the reference's
+    dsv4_cuda_init prints one) to stderr, so that stdout carries only the
+    JSON line."""
+    global _STDOUT_FD
+    sys.stdout.flush()
+    _STDOUT_FD = os.dup(1)
+    os.dup2(2, 1)
+
+
+def emit(obj):
+    import ctypes
+    sys.stdout.flush()
+    ctypes.CDLL(None).fflush(None)      # C stdio buffers, while fd 1 is stderr
+    if _STDOUT_FD is not None:
+        os.dup2(_STDOUT_FD, 1)
+    print(json.dumps(obj), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -346,17 +398,18 @@ def main():
         print("bench.py: WORLD_SIZE > 1 is not supported (one GPU per run)",
               file=sys.stderr)
         sys.exit(2)
+    quiet_stdout()
     B = Bench()
     if args.only == "copy":
         us, nbytes = B.copy_run(args.steps)
-        print(json.dumps({"config": "copy", "bytes_read": nbytes,
+        emit(({"config": "copy", "bytes_read": nbytes,
                           "bytes_written": nbytes, "us": round(us, 3),
                           "GBps_rw": round(2 * nbytes / us / 1e3, 1)}))
         return
     if args.only == "c2":
         B.c2_setup()
         step_ms, eager_ms, per_ms = B.c2_run(args.steps, args.warmup)
-        print(json.dumps({"config": "c2", "graph_ms": round(step_ms, 4),
+        emit(({"config": "c2", "graph_ms": round(step_ms, 4),
                           "eager_ms": round(eager_ms, 4),
                           "per_shape_us": [round(m * 1e3, 3) for m in per_ms]}))
         B.L.dsv4_gpu_shutdown()
@@ -364,7 +417,7 @@ def main():
     if args.only in ("c1", "c3", "c4"):
         fn = {"c1": B.c1_run, "c3": B.c3_run, "c4": B.c4_run}[args.only]
         us, eager, alg = fn(args.steps, args.warmup)
-        print(json.dumps({"config": args.only, "us": round(us, 3),
+        emit(({"config": args.only, "us": round(us, 3),
                           "eager_us": round(eager, 3),
                           "GBps": round(alg / us / 1e3, 1)}))
         B.L.dsv4_gpu_shutdown()
@@ -395,6 +448,10 @@ def main():
     if not args.no_detail:
         log("bench: C1")
         detail["c1_fp8_4096x4096"] = rec(*B.c1_run(args.steps, args.warmup))
+        log("bench: C1 host-buffer call")
+        hus = B.c1_host_run()
+        detail["c1_fp8_4096x4096"]["host_call_us"] = round(hus, 2)
+        detail["c1_fp8_4096x4096"]["host_call_GBps"] = round(fp8_bytes(4096, 4096) / hus / 1e3, 1)
         log("bench: C3")
         detail["c3_moe_fp4_8of256_7168x2048"] = rec(*B.c3_run(args.steps, args.warmup))
         log("bench: C4")
@@ -435,7 +492,7 @@ def main():
         "cpu_baseline": cpu,
         "detail": detail,
     }
-    print(json.dumps(out))
+    emit((out))
     B.L.dsv4_gpu_shutdown()
 
 

@@ -31,7 +31,9 @@ struct Res {
     const uint8_t *key, *key_end;   /* host weight bytes [key, key_end)   */
     const uint8_t *skey;            /* host scale grid                     */
     uint8_t *dw, *ds;
+    int wdt;                        /* DSV4_WFP8 or DSV4_WFP4              */
     int rows, cols, blk_r, blk_c, sc, sfmt;
+    size_t row_bytes() const { return wdt == DSV4_WFP4 ? (size_t)cols / 2 : (size_t)cols; }
 };
 
 struct LayerExperts {
@@ -142,12 +144,12 @@ const Res *find_view(const DSV4QMat *m, int *r0)
     const uint8_t *p = (const uint8_t *)m->w;
     for (const Res &r : g_res) {
         if (p < r.key || p >= r.key_end) continue;
-        if (m->wdt != DSV4_WFP8 || m->cols != r.cols || m->blk_r != r.blk_r ||
+        if (m->wdt != r.wdt || m->cols != r.cols || m->blk_r != r.blk_r ||
             m->blk_c != r.blk_c || m->rows <= 0)
             return nullptr;
         const size_t off = (size_t)(p - r.key);
-        if (off % (size_t)r.cols) return nullptr;
-        const int row0 = (int)(off / (size_t)r.cols);
+        if (off % r.row_bytes()) return nullptr;
+        const int row0 = (int)(off / r.row_bytes());
         if (row0 + m->rows > r.rows) return nullptr;
         if (row0 % r.blk_r) return nullptr;
         const size_t ssz = r.sfmt ? 4 : 1;
@@ -159,16 +161,21 @@ const Res *find_view(const DSV4QMat *m, int *r0)
     return nullptr;
 }
 
-int upload_fp8(const DSV4QMat *m, int sfmt)
+/* FP8 (sfmt 0: E8M0 scale bytes, 1: fp32) or FP4 (E8M0 bytes) matrices. */
+int upload_qmat(const DSV4QMat *m, int sfmt)
 {
     if (!g_ready || !m || !m->w || !m->s) return -1;
-    if (m->wdt != DSV4_WFP8 || m->rows <= 0 || m->cols <= 0 || m->blk_r <= 0 ||
-        m->blk_c <= 0)
+    if (m->rows <= 0 || m->cols <= 0 || m->blk_r <= 0 || m->blk_c <= 0) return -1;
+    if (m->wdt == DSV4_WFP4) {
+        if (sfmt != 0 || !dsv4_fp4_gemv_ok(m->rows, m->cols, m->blk_r, m->blk_c))
+            return -1;
+    } else if (m->wdt != DSV4_WFP8) {
         return -1;
+    }
     for (const Res &r : g_res)
         if (r.key == (const uint8_t *)m->w) return 0;
     const int sc = (m->cols + m->blk_c - 1) / m->blk_c;
-    const size_t wb = (size_t)m->rows * (size_t)m->cols;
+    const size_t wb = (size_t)m->rows * (size_t)m->cols / (m->wdt == DSV4_WFP4 ? 2 : 1);
     const size_t sb = (size_t)((m->rows + m->blk_r - 1) / m->blk_r) * sc *
                       (sfmt ? 4u : 1u);
     if (wb + sb + (256u << 20) > dsv4_gpu_free_vram()) return -1;
@@ -185,11 +192,26 @@ int upload_fp8(const DSV4QMat *m, int sfmt)
     r.key_end = r.key + wb;
     r.skey = (const uint8_t *)m->s;
     r.dw = dw; r.ds = ds;
+    r.wdt = m->wdt;
     r.rows = m->rows; r.cols = m->cols;
     r.blk_r = m->blk_r; r.blk_c = m->blk_c;
     r.sc = sc; r.sfmt = sfmt;
     g_res.push_back(r);
     return 0;
+}
+
+/* y[rows] for rows [r0, r0 + rows) of a resident matrix, x and y device
+ * pointers, on the library stream. */
+int res_gemv(const Res &r, int r0, int rows, float *d_y, const float *d_x)
+{
+    if (r.wdt == DSV4_WFP4)
+        return dsv4_fp4_gemv_launch(d_y, d_x, r.dw + (size_t)r0 * r.row_bytes(),
+                                    r.ds + (size_t)(r0 / r.blk_r) * r.sc, rows, r.cols,
+                                    r.blk_r, r.blk_c, g_stream);
+    const size_t ssz = r.sfmt ? 4 : 1;
+    return dsv4_fp8_gemv_launch(d_y, d_x, r.dw + (size_t)r0 * r.cols,
+                                r.ds + (size_t)(r0 / r.blk_r) * r.sc * ssz, r.sfmt, rows,
+                                r.cols, r.blk_r, r.blk_c, g_stream);
 }
 
 /* --------------------------------------------------------------- experts */
@@ -388,8 +410,8 @@ void dsv4_gpu_shutdown(void)
 }
 
 /* ------------------------------------------------------------------- FP8 */
-int dsv4_gpu_upload(const DSV4QMat *m) { return upload_fp8(m, 0); }
-int dsv4_gpu_upload_f32s(const DSV4QMat *m) { return upload_fp8(m, 1); }
+int dsv4_gpu_upload(const DSV4QMat *m) { return upload_qmat(m, 0); }
+int dsv4_gpu_upload_f32s(const DSV4QMat *m) { return upload_qmat(m, 1); }
 
 int dsv4_gpu_has(const DSV4QMat *m)
 {
@@ -410,12 +432,8 @@ void dsv4_gpu_mmq(float *y, const float *x, const DSV4QMat *m)
     const size_t yo = s.add((size_t)m->rows * sizeof(float));
     size_t end;
     if (stage_push(s, &end) != 0) abort();
-    const size_t ssz = r->sfmt ? 4 : 1;
-    const int rc = dsv4_fp8_gemv_launch(
-        (float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
-        r->dw + (size_t)r0 * r->cols,
-        r->ds + (size_t)(r0 / r->blk_r) * r->sc * ssz, r->sfmt, m->rows,
-        r->cols, r->blk_r, r->blk_c, g_stream);
+    const int rc = res_gemv(*r, r0, m->rows, (float *)(g_ar.d + yo),
+                            (const float *)(g_ar.d + xo));
     if (rc != 0 || stage_pull(yo, (size_t)m->rows * sizeof(float), y) != 0) {
         DSV4_ERR("mmq failed");
         abort();
@@ -438,11 +456,19 @@ void dsv4_gpu_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
     size_t end;
     if (stage_push(s, &end) != 0) abort();
     const size_t ssz = r->sfmt ? 4 : 1;
-    const int rc = dsv4_fp8_gemv_n_launch(
-        (float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
-        r->dw + (size_t)r0 * r->cols,
-        r->ds + (size_t)(r0 / r->blk_r) * r->sc * ssz, r->sfmt, m->rows,
-        r->cols, r->blk_r, r->blk_c, nt, g_stream);
+    int rc = 0;
+    if (r->wdt == DSV4_WFP4) {
+        /* token by token: per (row, token) the GEMV's own arithmetic */
+        for (int t = 0; t < nt && rc == 0; t++)
+            rc = res_gemv(*r, r0, m->rows, (float *)(g_ar.d + yo) + (size_t)t * m->rows,
+                          (const float *)(g_ar.d + xo) + (size_t)t * r->cols);
+    } else {
+        rc = dsv4_fp8_gemv_n_launch(
+            (float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
+            r->dw + (size_t)r0 * r->cols,
+            r->ds + (size_t)(r0 / r->blk_r) * r->sc * ssz, r->sfmt, m->rows,
+            r->cols, r->blk_r, r->blk_c, nt, g_stream);
+    }
     if (rc != 0 ||
         stage_pull(yo, (size_t)nt * m->rows * sizeof(float), y) != 0) {
         DSV4_ERR("mmq_n failed");
@@ -460,6 +486,18 @@ int dsv4_gpu_fp8_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
     }
     return dsv4_fp8_gemv_launch(d_y, d_x, d_w, d_s, scale_fmt, rows, cols, 128,
                                 128, as_stream(stream));
+}
+
+int dsv4_gpu_fp4_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
+                        const uint8_t *d_s, int rows, int cols, int blk_r, int blk_c,
+                        void *stream)
+{
+    if (!d_y || !d_x || !d_w || !d_s) {
+        DSV4_ERR("fp4_gemv_d: bad arguments");
+        return -1;
+    }
+    return dsv4_fp4_gemv_launch(d_y, d_x, d_w, d_s, rows, cols, blk_r, blk_c,
+                                as_stream(stream));
 }
 
 /* ---------------------------------------------------------------- dumps */

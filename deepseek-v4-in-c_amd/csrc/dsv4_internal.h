@@ -32,6 +32,13 @@ int dsv4_fp8_gemv_launch(float *y, const float *x, const uint8_t *W,
                          const void *S, int sfmt, int rows, int cols,
                          int blk_r, int blk_c, hipStream_t st);
 
+/* MXFP4 GEMV (dsv4_matmul_fp4): W e2m1 nibbles [rows][cols/2], S E8M0 bytes
+ * [ceil(rows/blk_r)][ceil(cols/blk_c)]. _ok: the shapes it takes (cols a
+ * multiple of 32 up to 16384, blk_c a multiple of 32). Returns 0 / -1. */
+bool dsv4_fp4_gemv_ok(int rows, int cols, int blk_r, int blk_c);
+int dsv4_fp4_gemv_launch(float *y, const float *x, const uint8_t *W, const uint8_t *S,
+                         int rows, int cols, int blk_r, int blk_c, hipStream_t st);
+
 /* Batched: y[nt][rows], x[nt][cols]; per (row, token) bit-identical to the
  * GEMV above. */
 int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,

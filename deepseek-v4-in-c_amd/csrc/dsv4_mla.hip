@@ -63,8 +63,6 @@ constexpr int IS_MAXW = 4;                      /* waves per workgroup */
 
 /* Top-k constants the score kernel shares: its histogram is the first level
  * of the selection. */
-constexpr int TK_THREADS = 1024;
-constexpr int TK_WAVES = TK_THREADS / 64;
 constexpr int TK_KMAX = 4096;
 constexpr int TK_BINS = 2048;                   /* top 11 bits of the key */
 constexpr int TK_SLICES = 16;                   /* spread of the global atomics */
@@ -542,8 +540,7 @@ k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
     __shared__ unsigned long long cs[TK_KMAX];
     __shared__ uint32_t wsum[FN_WAVES], res[2];
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    const unsigned long long lt = lanemask_lt(lane);
+    const int tid = threadIdx.x;
 
     for (int i = blockIdx.x * FN_THREADS + tid; i < TK_SLICES * TK_BINS / 4;
          i += gridDim.x * FN_THREADS)

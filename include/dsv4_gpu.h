@@ -85,12 +85,16 @@ size_t dsv4_gpu_free_vram(void);
  * Replaces dsv4_cuda_shutdown (dsv4_cuda.h:99, dsv4_cuda.cu:436). */
 void dsv4_gpu_shutdown(void);
 
-/* ===================================================== FP8 dense matrices */
+/* ================================================= FP8 / FP4 dense matrices */
 
-/* Copy one FP8 matrix (E8M0 block scales, the reference's format) into HBM,
- * keyed by m->w. 0 ok; -1 recoverable (not FP8, no room with 256 MiB of
- * headroom, copy failed) -- the matrix then stays on the CPU. Idempotent per
- * key. Replaces dsv4_cuda_upload (dsv4_cuda.h:80, dsv4_cuda.cu:307). */
+/* Copy one FP8 matrix (E8M0 block scales, the reference's format) or one
+ * MXFP4 matrix (e2m1 nibbles, E8M0 scale per blk_r x blk_c block; cols a
+ * multiple of 32 up to 16384, blk_c a multiple of 32) into HBM, keyed by
+ * m->w. 0 ok; -1 recoverable (another format or shape, no room with 256 MiB
+ * of headroom, copy failed) -- the matrix then stays on the CPU. Idempotent
+ * per key. Replaces dsv4_cuda_upload (dsv4_cuda.h:80, dsv4_cuda.cu:307),
+ * which took FP8 only; FP4 residency lets the reference's dispatch
+ * (dsv4_matmul.c:525-546) run the experts' matrices on the device too. */
 int dsv4_gpu_upload(const DSV4QMat *m);
 
 /* The same for an FP8 matrix whose block scales are fp32 (m->s is a float
@@ -108,7 +112,9 @@ int dsv4_gpu_upload_f32s(const DSV4QMat *m);
 int dsv4_gpu_has(const DSV4QMat *m);
 
 /* y[rows] = dequant(m) . x[cols], host buffers, synchronous. abort() if m is
- * not resident. Replaces dsv4_cuda_mmq (dsv4_cuda.h:88, dsv4_cuda.cu:387). */
+ * not resident. FP8 as dsv4_matmul_fp8, FP4 as dsv4_matmul_fp4
+ * (dsv4_matmul.c:293-345). Replaces dsv4_cuda_mmq (dsv4_cuda.h:88,
+ * dsv4_cuda.cu:387). */
 void dsv4_gpu_mmq(float *y, const float *x, const DSV4QMat *m);
 
 /* y[nt][rows] for x[nt][cols]: one pass over the weights for the batch. Per
@@ -122,6 +128,16 @@ void dsv4_gpu_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt);
  * E8M0 bytes, 1 = fp32. What dsv4_gpu_mmq runs after staging. */
 int dsv4_gpu_fp8_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
                         const void *d_s, int scale_fmt, int rows, int cols,
+                        void *stream);
+
+/* The MXFP4 GEMV on raw device buffers, stream-ordered: d_y[rows] =
+ * dsv4_matmul_fp4 (dsv4_matmul.c:320-345) of d_w (e2m1 nibbles [rows][cols/2],
+ * 16-byte aligned) with E8M0 scales d_s [ceil(rows/blk_r)][ceil(cols/blk_c)]
+ * and d_x (16-byte aligned). What dsv4_gpu_mmq runs for a resident FP4 matrix.
+ * 0 / -1 (shape not taken: cols a multiple of 32 up to 16384, blk_c a
+ * multiple of 32). */
+int dsv4_gpu_fp4_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
+                        const uint8_t *d_s, int rows, int cols, int blk_r, int blk_c,
                         void *stream);
 
 /* ========================================================== decoder gates */

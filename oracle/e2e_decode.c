@@ -23,9 +23,16 @@
  *     path;
  *   - pass 2: dsv4_gpu_init plus the FP8 trunk upload of dsv4_run.c:270-283,
  *     so every FP8 matmul (including the wo_a group slices) runs on the
- *     MI355X.
- * Routed experts come from memory (all resident), the CPU FP4 path in both
- * passes.
+ *     MI355X; every expert's FP4 matrices are made resident too, so the
+ *     experts' matmuls of expert_forward (dsv4_layer.c:199-206) run there
+ *     through the same dispatch; and the CSA calls of attention()
+ *     (dsv4_layer.c:286-301) go to the device. oracle/Makefile compiles
+ *     dsv4_layer.c with dsv4_indexer_score / dsv4_topk / dsv4_sparse_attn
+ *     renamed to the e2e_* wrappers below, which call dsv4_gpu_indexer_score
+ *     / dsv4_gpu_topk / dsv4_gpu_sparse_attn in pass 2 and the reference's
+ *     own functions otherwise -- the call sites INTEGRATION.md shows, made
+ *     with the preprocessor instead of an edit.
+ * Routed experts come from memory (all resident).
  *
  * usage: dsv4_e2e CKPT_DIR TOKENS_FILE [--cpu-only]
  * Prints one line per position and a summary; exit 0 when every argmax
@@ -47,6 +54,70 @@ void dsv4_rmsnorm(float *y, const float *x, const float *w, int n, float eps);
 void dsv4_mmq(float *y, const float *x, const DSV4QMat *m);
 void dsv4_rope_table(float *cs, float *sn, int rd, int maxpos, int orig_ctx,
                      double theta, double factor, double beta_fast, double beta_slow);
+
+/* ------------------------------------------------- CSA on the device ---- */
+/* The reference's own functions (dsv4_layer.c:58-66 declares them). */
+void dsv4_sparse_attn(float *, const float *, const float *, const float *,
+                      const int *, int, int, int, float, float *);
+void dsv4_indexer_score(float *, const float *, const float *, const float *,
+                        int, int, int);
+int dsv4_topk(int *, const float *, int, int);
+
+static int g_gpu_csa;                       /* pass 2: CSA calls on the device */
+static long g_n_score, g_n_topk, g_n_attn;
+
+static void csa_fail(const char *what)
+{
+    fprintf(stderr, "e2e: %s on the device failed\n", what);
+    abort();
+}
+
+/* dsv4_indexer_score (dsv4_indexer.c:64-85): the n key rows of width D
+ * starting at kv, as the caller passes them (dsv4_layer.c:286-289). */
+void e2e_indexer_score(float *out, const float *q, const float *kv, const float *w,
+                       int H, int D, int n)
+{
+    if (!g_gpu_csa || n <= 0) {
+        dsv4_indexer_score(out, q, kv, w, H, D, n);
+        return;
+    }
+    dsv4_gpu_kv *keys = dsv4_gpu_kv_create(n, D, DSV4_GPU_KV_F32);
+    if (!keys || dsv4_gpu_kv_write_rows(keys, 0, n, kv, NULL) != 0 ||
+        dsv4_gpu_indexer_score(out, q, w, H, D, keys, 0, D, n) != 0)
+        csa_fail("indexer score");
+    dsv4_gpu_kv_free(keys);
+    g_n_score++;
+}
+
+/* dsv4_topk (dsv4_indexer.c:92-106). */
+int e2e_topk(int *idxs, const float *scores, int n, int k)
+{
+    if (!g_gpu_csa || n <= 0 || k <= 0) return dsv4_topk(idxs, scores, n, k);
+    const int r = dsv4_gpu_topk(idxs, scores, n, k);
+    if (r < 0) csa_fail("top-k");
+    g_n_topk++;
+    return r;
+}
+
+/* dsv4_sparse_attn (dsv4_attn.c:60-108) over the rows of the layer's KV ring
+ * that idxs names (-1 entries masked). */
+void e2e_sparse_attn(float *o, const float *q, const float *kv, const float *sink,
+                     const int *idxs, int h, int d, int topk, float scale, float *scratch)
+{
+    int rows = 0;
+    for (int i = 0; i < topk; i++)
+        if (idxs[i] + 1 > rows) rows = idxs[i] + 1;
+    if (!g_gpu_csa || rows == 0) {
+        dsv4_sparse_attn(o, q, kv, sink, idxs, h, d, topk, scale, scratch);
+        return;
+    }
+    dsv4_gpu_kv *cache = dsv4_gpu_kv_create(rows, d, DSV4_GPU_KV_F32);
+    if (!cache || dsv4_gpu_kv_write_rows(cache, 0, rows, kv, NULL) != 0 ||
+        dsv4_gpu_sparse_attn(o, q, cache, sink, idxs, h, d, d, topk, scale) != 0)
+        csa_fail("sparse attention");
+    dsv4_gpu_kv_free(cache);
+    g_n_attn++;
+}
 
 /* ---------------------------------------------------- routed experts ---- */
 typedef struct {
@@ -276,7 +347,7 @@ int main(int argc, char **argv)
     float *got = malloc((size_t)n * c.vocab * sizeof(float));
     if (!ref || !got || run_pass(&M, tok, n, ref) != 0) return 1;
 
-    int gpu_mats = 0;
+    int gpu_mats = 0, fp4_mats = 0;
     if (cpu_only) {
         if (run_pass(&M, tok, n, got) != 0) return 1;
     } else {
@@ -290,11 +361,23 @@ int main(int argc, char **argv)
                                     &w->attn.wo_a, &w->attn.wo_b, &w->moe.shared.w1,
                                     &w->moe.shared.w2, &w->moe.shared.w3,
                                     w->attn.has_idx ? &w->attn.idx.wq_b : NULL};
-            for (int k = 0; k < 9; k++)
-                if (m[k] && m[k]->wdt == DSV4_WFP8 && dsv4_gpu_upload(m[k]) == 0) gpu_mats++;
+            for (int k = 0; k < 9; k++) {
+                if (!m[k]) continue;
+                if (m[k]->wdt == DSV4_WFP8 && dsv4_gpu_upload(m[k]) == 0) gpu_mats++;
+                if (m[k]->wdt == DSV4_WFP4 && dsv4_gpu_upload(m[k]) == 0) fp4_mats++;
+            }
+            for (int e = 0; e < c.n_experts; e++) {
+                const DSV4ExpertW *x = &E.w[(size_t)L * c.n_experts + e];
+                const DSV4QMat *em[3] = {&x->w1, &x->w2, &x->w3};
+                for (int k = 0; k < 3; k++)
+                    if (dsv4_gpu_upload(em[k]) == 0) fp4_mats++;
+            }
         }
-        printf("gpu: %d FP8 matrices resident\n", gpu_mats);
+        printf("gpu: %d FP8 and %d FP4 matrices resident, CSA on the device\n",
+               gpu_mats, fp4_mats);
+        g_gpu_csa = 1;
         if (gpu_mats == 0 || run_pass(&M, tok, n, got) != 0) return 1;
+        g_gpu_csa = 0;
     }
 
     int agree = 0;
@@ -309,8 +392,9 @@ int main(int argc, char **argv)
         printf("pos %d tok %d cpu %d %s %d margin %.6g rel %.3g\n", p, tok[p], ar,
                cpu_only ? "cpu2" : "gpu", ag, (double)mr, r);
     }
-    printf("summary: positions %d argmax_equal %d worst_rel %.3g gpu_mats %d\n", n,
-           agree, worst, gpu_mats);
+    printf("summary: positions %d argmax_equal %d worst_rel %.3g gpu_mats %d "
+           "fp4_mats %d gpu_score %ld gpu_topk %ld gpu_attn %ld\n", n, agree, worst,
+           gpu_mats, fp4_mats, g_n_score, g_n_topk, g_n_attn);
     if (!cpu_only) dsv4_gpu_shutdown();
     return agree == n ? 0 : 1;
 }

@@ -4,7 +4,11 @@ structurally real deepseek_v4 checkpoint (FP8 trunk, MXFP4 experts, CSA
 indexer with selection, sparse MLA), run by the reference's own C99 model
 code. In the second pass every FP8 matrix the reference uploads
 (dsv4_run.c:270-283) runs on the MI355X through dsv4_gpu_mmq. That includes
-the wo_a group slices, which resolve as row-range views.
+the wo_a group slices, which resolve as row-range views. Every expert's FP4
+matrices are resident too (the experts' matmuls run on the device through the
+same dispatch), and attention()'s CSA calls -- indexer score, top-k, sparse
+attention (dsv4_layer.c:286-301) -- go to dsv4_gpu_indexer_score /
+dsv4_gpu_topk / dsv4_gpu_sparse_attn.
 
 Bar: identical argmax at every position. The logits agree within the
 reference's own whole-model tolerance, 2e-3 vector-scaled
@@ -31,7 +35,11 @@ def test_gpu_trunk_argmax_identical(tmp_path):
     assert summ, p.stdout[-2000:]
     n, agree, worst, mats = (int(summ.group(1)), int(summ.group(2)),
                              float(summ.group(3)), int(summ.group(4)))
+    fp4, score, topk, attn = (int(summ.group(i)) for i in range(5, 9))
     assert n == 46 and agree == 46
     assert mats >= 4 * 8            # every layer's FP8 trunk is resident
+    assert fp4 >= 4 * 16 * 3        # every routed expert's w1, w2, w3
+    assert attn == 46 * 4           # one sparse attention per layer and position
+    assert score > 0 and topk == score   # the CSA layers selected on the device
     assert worst < 2e-3
     assert any(r["rel"] > 0.0 for r in rows), "GPU pass produced CPU bits: trunk not on GPU?"

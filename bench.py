@@ -238,6 +238,30 @@ class Bench:
         self._keep_host = (Ws, ms)
         return t[len(t) // 2] * 1e6
 
+    # ------------------------------------------------- BF16 LM head
+    def bf16_head_run(self, steps, warmup):
+        """The LM head in the reference's own format (BF16 129280x7168,
+        dsv4_run.c:467-474), through the BF16 GEMV the dispatch uses for a
+        resident BF16 matrix. 1.85 GB: larger than the Infinity Cache, so
+        each launch reads it cold."""
+        torch = self.torch
+        rows, cols = LM_HEAD
+        g = torch.Generator(device=self.dev)
+        g.manual_seed(7)
+        # finite bf16 values: N(0, 1) drawn as float32 and rounded
+        W = torch.randn((rows, cols), generator=g, device=self.dev).to(torch.bfloat16)
+        dx = torch.randn(cols, generator=g, device=self.dev)
+        dy = torch.empty(rows, dtype=torch.float32, device=self.dev)
+        torch.cuda.synchronize()
+
+        def go(i, sp):
+            assert self.L.dsv4_gpu_bf16_gemv_d(dy.data_ptr(), dx.data_ptr(), W.data_ptr(),
+                                               rows, cols, sp) == 0
+        eager = self.eager_us(go, max(steps // 4, 4), max(warmup, 2))
+        us = self.graph_us(go, 4, max(2, steps // 16))
+        del W
+        return us, eager, rows * cols * 2 + cols * 4 + rows * 4
+
     # ------------------------------------------------------------ C3
     def c3_run(self, steps, warmup):
         import ctypes
@@ -456,6 +480,8 @@ def main():
         detail["c3_moe_fp4_8of256_7168x2048"] = rec(*B.c3_run(args.steps, args.warmup))
         log("bench: C4")
         detail["c4_sparse_mla_step_32768_top2048"] = rec(*B.c4_run(args.steps, args.warmup))
+        log("bench: BF16 LM head")
+        detail["lm_head_bf16_129280x7168"] = rec(*B.bf16_head_run(args.steps, args.warmup))
     cpu = None
     if not args.no_cpu:
         log("bench: CPU baseline (compiled reference, host cores)")

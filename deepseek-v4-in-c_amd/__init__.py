@@ -68,6 +68,7 @@ _SIGS = {
     "dsv4_gpu_mmq_n": (None, [_vp, _vp, _QP, _ci]),
     "dsv4_gpu_fp8_gemv_d": (_ci, [_vp, _vp, _vp, _vp, _ci, _ci, _ci, _vp]),
     "dsv4_gpu_fp4_gemv_d": (_ci, [_vp, _vp, _vp, _vp, _ci, _ci, _ci, _ci, _vp]),
+    "dsv4_gpu_bf16_gemv_d": (_ci, [_vp, _vp, _vp, _ci, _ci, _vp]),
     "dsv4_gpu_dump_e4m3": (_ci, [_vp]),
     "dsv4_gpu_dump_e8m0": (_ci, [_vp]),
     "dsv4_gpu_dump_e2m1": (_ci, [_vp]),

@@ -1,0 +1,203 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/* dsv4_bf16.hip - BF16 GEMV for resident BF16 matrices on gfx950.
+ *
+ * What it computes is dsv4_matmul_bf16 (reference src/core/dsv4_matmul.c:
+ * 275-291): y[o] = (float) sum_i bf16(W[o][i]) * x[i]. It is how
+ * dsv4_gpu_mmq runs a BF16 matrix made resident by dsv4_gpu_upload -- the
+ * router gate of moe() (dsv4_layer.c:374) and the LM head
+ * (dsv4_run.c:467-474) go through the reference's dsv4_mmq dispatch
+ * (dsv4_matmul.c:525-546) like every other matrix.
+ *
+ * DESIGN (bandwidth-bound, one multiply-add per 2 weight bytes)
+ *   - A row is split over TC threads (a power of two up to 64, or a multiple
+ *     of 64 up to 256); thread j owns the 16-byte chunks (8 elements) j,
+ *     j+TC, ... of every row it visits (NCH <= 8 of them, so rows up to
+ *     16384 columns). Consecutive lanes read consecutive chunks: one wave
+ *     instruction moves 1 KiB of one row.
+ *   - The thread's slice of x (NCH x 8 floats) is loaded once into VGPRs and
+ *     reused for every row; workgroups are persistent over a contiguous
+ *     range of rows.
+ *   - A thread works on R rows at once, all R*NCH loads in flight before any
+ *     arithmetic, issued unconditionally (rows past the end reload the last
+ *     row, chunks past the row end the last chunk; their results are
+ *     discarded).
+ *   - bf16 -> f32 is exact (a shift); 8 f32 FMAs per chunk in two chains.
+ *     Lane partials meet in the fixed DPP tree, and across the waves of a
+ *     row in wave order through LDS.
+ * NUMERICS: fp32 (the reference accumulates in double); within 1e-5
+ * vector-scaled relative of it. TC, NCH and the trees depend on cols only,
+ * so a row's bits do not depend on R or the grid.
+ */
+#include "dsv4_dev.h"
+#include "dsv4_internal.h"
+
+namespace {
+
+constexpr int B16_PART_MAX = 4096;
+
+struct B16Geom {
+    int ch, tc, nch, wg, rg;
+};
+
+bool b16_geom(int cols, B16Geom *g)
+{
+    if (cols <= 0 || (cols & 7)) return false;
+    const int ch = cols >> 3;
+    int tc, nch;
+    if (ch <= 64) {
+        tc = 1;
+        while (tc < ch) tc <<= 1;
+        nch = 1;
+    } else {
+        tc = 64 * ((ch + 511) / 512);
+        if (tc > 256) tc = 256;
+        nch = (ch + tc - 1) / tc;
+    }
+    if (nch > 8) return false;                   /* cols <= 16384 */
+    g->ch = ch;
+    g->tc = tc;
+    g->nch = nch;
+    g->wg = tc * (256 / tc);
+    g->rg = g->wg / tc;
+    return true;
+}
+
+/* 8 bf16 (one chunk) dotted with 8 activations, two interleaved chains. */
+__device__ __forceinline__ float dot8_bf16(const u32x4 v, const float *xr)
+{
+    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+    float p0 = __uint_as_float(u[0] << 16) * xr[0];
+    float p1 = __uint_as_float(u[0] & 0xFFFF0000u) * xr[1];
+#pragma unroll
+    for (int e = 1; e < 4; e++) {
+        p0 = fmaf(__uint_as_float(u[e] << 16), xr[2 * e], p0);
+        p1 = fmaf(__uint_as_float(u[e] & 0xFFFF0000u), xr[2 * e + 1], p1);
+    }
+    return p0 + p1;
+}
+
+template <int NCH, int R>
+__global__ void __launch_bounds__(256)
+k_bf16_gemv(float *__restrict__ y, const float *__restrict__ x,
+            const uint16_t *__restrict__ W, int rows, int cols, int tc, int rows_per_wg)
+{
+    extern __shared__ float part[];                 /* [waves per row][rows_per_wg] */
+    const int tid = threadIdx.x;
+    const int g = tid / tc, j = tid - g * tc;
+    const int rg = blockDim.x / tc;
+    const int ch = cols >> 3;
+    const int lane = tid & 63;
+    const int row0 = blockIdx.x * rows_per_wg;
+    const int rend = min(rows, row0 + rows_per_wg);
+    const int nloc = rend - row0;
+    const uint8_t *Wb = reinterpret_cast<const uint8_t *>(W);
+    const size_t rowb = (size_t)cols * 2;
+
+    float xr[NCH][8];
+    bool act[NCH];
+#pragma unroll
+    for (int n = 0; n < NCH; n++) {
+        const int c = j + n * tc;
+        act[n] = c < ch;
+        const int cc = min(c, ch - 1);
+        const f32x4 a = ldf4(x + cc * 8), b = ldf4(x + cc * 8 + 4);
+        xr[n][0] = a.x; xr[n][1] = a.y; xr[n][2] = a.z; xr[n][3] = a.w;
+        xr[n][4] = b.x; xr[n][5] = b.y; xr[n][6] = b.z; xr[n][7] = b.w;
+    }
+
+    for (int rb = row0 + g * R; rb < row0 + ((nloc + rg * R - 1) / (rg * R)) * rg * R;
+         rb += rg * R) {
+        u32x4 v[R][NCH];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int r = min(rb + i, rend - 1);
+#pragma unroll
+            for (int n = 0; n < NCH; n++) {
+                const int c = min(j + n * tc, ch - 1);
+                v[i][n] = ldg16_stream(Wb + (size_t)r * rowb + (size_t)c * 16);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int n = 0; n < NCH; n++) {
+                const float d = a + dot8_bf16(v[i][n], xr[n]);
+                a = act[n] ? d : a;
+            }
+            if (tc <= 64) {
+                const float s = seg_sum_rt(a, tc);
+                if (j == tc - 1 && rb + i < rend) y[rb + i] = s;
+            } else {
+                const float s = seg_sum<64>(a);
+                const int rl = rb + i - row0;
+                if (lane == 63 && rl < nloc) part[(j >> 6) * rows_per_wg + rl] = s;
+            }
+        }
+    }
+    if (tc > 64) {
+        __syncthreads();
+        const int wpr = tc >> 6;
+        for (int rl = tid; rl < nloc; rl += blockDim.x) {
+            float s = part[rl];
+            for (int w = 1; w < wpr; w++) s += part[w * rows_per_wg + rl];
+            y[row0 + rl] = s;
+        }
+    }
+}
+
+template <int NCH>
+void b16_launch(const B16Geom &g, float *y, const float *x, const uint16_t *W, int rows,
+                int cols, hipStream_t st)
+{
+    /* two rows per thread per step while the loads fit the registers */
+    constexpr int R = NCH <= 4 ? 2 : 1;
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+                hipSuccess ||
+            n <= 0)
+            n = 256;
+        cus = n;
+    }
+    const int step_rows = g.rg * R;
+    const int want = 2 * cus;                       /* two workgroups per CU */
+    const int wpr = g.tc > 64 ? g.tc / 64 : 1;
+    int spw = ((rows + step_rows - 1) / step_rows + want - 1) / want;
+    const int max_spw = B16_PART_MAX / wpr / step_rows;
+    if (spw > max_spw) spw = max_spw;
+    if (spw < 1) spw = 1;
+    const int rows_per_wg = spw * step_rows;
+    const int grid = (rows + rows_per_wg - 1) / rows_per_wg;
+    const size_t lds = g.tc > 64 ? sizeof(float) * (size_t)wpr * rows_per_wg : 0;
+    hipLaunchKernelGGL((k_bf16_gemv<NCH, R>), dim3(grid), dim3(g.wg), lds, st, y, x, W,
+                       rows, cols, g.tc, rows_per_wg);
+}
+
+} // namespace
+
+bool dsv4_bf16_gemv_ok(int rows, int cols)
+{
+    B16Geom g;
+    return rows > 0 && b16_geom(cols, &g);
+}
+
+int dsv4_bf16_gemv_launch(float *y, const float *x, const uint16_t *W, int rows, int cols,
+                          hipStream_t st)
+{
+    B16Geom g;
+    if (rows <= 0 || !b16_geom(cols, &g) || (((uintptr_t)x | (uintptr_t)W) & 15)) {
+        DSV4_ERR("bf16 gemv: unsupported shape %dx%d or unaligned operands", rows, cols);
+        return -1;
+    }
+    switch (g.nch) {
+    case 1: b16_launch<1>(g, y, x, W, rows, cols, st); break;
+    case 2: b16_launch<2>(g, y, x, W, rows, cols, st); break;
+    case 3: case 4: b16_launch<4>(g, y, x, W, rows, cols, st); break;
+    default: b16_launch<8>(g, y, x, W, rows, cols, st); break;
+    }
+    HIP_OK(hipGetLastError(), "bf16 gemv launch");
+    return 0;
+}

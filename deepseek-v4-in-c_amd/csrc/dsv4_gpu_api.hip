@@ -31,9 +31,13 @@ struct Res {
     const uint8_t *key, *key_end;   /* host weight bytes [key, key_end)   */
     const uint8_t *skey;            /* host scale grid                     */
     uint8_t *dw, *ds;
-    int wdt;                        /* DSV4_WFP8 or DSV4_WFP4              */
+    int wdt;                        /* DSV4_WFP8, DSV4_WFP4 or DSV4_WBF16  */
     int rows, cols, blk_r, blk_c, sc, sfmt;
-    size_t row_bytes() const { return wdt == DSV4_WFP4 ? (size_t)cols / 2 : (size_t)cols; }
+    size_t row_bytes() const
+    {
+        return wdt == DSV4_WFP4 ? (size_t)cols / 2
+             : wdt == DSV4_WBF16 ? (size_t)cols * 2 : (size_t)cols;
+    }
 };
 
 struct LayerExperts {
@@ -144,13 +148,16 @@ const Res *find_view(const DSV4QMat *m, int *r0)
     const uint8_t *p = (const uint8_t *)m->w;
     for (const Res &r : g_res) {
         if (p < r.key || p >= r.key_end) continue;
-        if (m->wdt != r.wdt || m->cols != r.cols || m->blk_r != r.blk_r ||
-            m->blk_c != r.blk_c || m->rows <= 0)
-            return nullptr;
+        if (m->wdt != r.wdt || m->cols != r.cols || m->rows <= 0) return nullptr;
         const size_t off = (size_t)(p - r.key);
         if (off % r.row_bytes()) return nullptr;
         const int row0 = (int)(off / r.row_bytes());
         if (row0 + m->rows > r.rows) return nullptr;
+        if (r.wdt == DSV4_WBF16) {                      /* no scales, no blocking */
+            *r0 = row0;
+            return &r;
+        }
+        if (m->blk_r != r.blk_r || m->blk_c != r.blk_c) return nullptr;
         if (row0 % r.blk_r) return nullptr;
         const size_t ssz = r.sfmt ? 4 : 1;
         const uint8_t *want_s = r.skey + (size_t)(row0 / r.blk_r) * r.sc * ssz;
@@ -162,8 +169,11 @@ const Res *find_view(const DSV4QMat *m, int *r0)
 }
 
 /* FP8 (sfmt 0: E8M0 scale bytes, 1: fp32) or FP4 (E8M0 bytes) matrices. */
+int upload_bf16(const DSV4QMat *m);
+
 int upload_qmat(const DSV4QMat *m, int sfmt)
 {
+    if (m && m->wdt == DSV4_WBF16 && sfmt == 0) return upload_bf16(m);
     if (!g_ready || !m || !m->w || !m->s) return -1;
     if (m->rows <= 0 || m->cols <= 0 || m->blk_r <= 0 || m->blk_c <= 0) return -1;
     if (m->wdt == DSV4_WFP4) {
@@ -200,10 +210,42 @@ int upload_qmat(const DSV4QMat *m, int sfmt)
     return 0;
 }
 
+/* A BF16 matrix (the reference's format for the router gate and the LM
+ * head): weights only, no scale grid. */
+int upload_bf16(const DSV4QMat *m)
+{
+    if (!g_ready || !m->w || !dsv4_bf16_gemv_ok(m->rows, m->cols)) return -1;
+    for (const Res &r : g_res)
+        if (r.key == (const uint8_t *)m->w) return 0;
+    const size_t wb = (size_t)m->rows * (size_t)m->cols * 2;
+    if (wb + (256u << 20) > dsv4_gpu_free_vram()) return -1;
+    uint8_t *dw = nullptr;
+    if (hipMalloc((void **)&dw, wb) != hipSuccess) return -1;
+    if (hipMemcpy(dw, m->w, wb, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(dw);
+        return -1;
+    }
+    Res r;
+    r.key = (const uint8_t *)m->w;
+    r.key_end = r.key + wb;
+    r.skey = nullptr;
+    r.dw = dw; r.ds = nullptr;
+    r.wdt = DSV4_WBF16;
+    r.rows = m->rows; r.cols = m->cols;
+    r.blk_r = m->blk_r; r.blk_c = m->blk_c;
+    r.sc = 0; r.sfmt = 0;
+    g_res.push_back(r);
+    return 0;
+}
+
 /* y[rows] for rows [r0, r0 + rows) of a resident matrix, x and y device
  * pointers, on the library stream. */
 int res_gemv(const Res &r, int r0, int rows, float *d_y, const float *d_x)
 {
+    if (r.wdt == DSV4_WBF16)
+        return dsv4_bf16_gemv_launch(d_y, d_x,
+                                     (const uint16_t *)(r.dw + (size_t)r0 * r.row_bytes()),
+                                     rows, r.cols, g_stream);
     if (r.wdt == DSV4_WFP4)
         return dsv4_fp4_gemv_launch(d_y, d_x, r.dw + (size_t)r0 * r.row_bytes(),
                                     r.ds + (size_t)(r0 / r.blk_r) * r.sc, rows, r.cols,
@@ -457,7 +499,7 @@ void dsv4_gpu_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
     if (stage_push(s, &end) != 0) abort();
     const size_t ssz = r->sfmt ? 4 : 1;
     int rc = 0;
-    if (r->wdt == DSV4_WFP4) {
+    if (r->wdt == DSV4_WFP4 || r->wdt == DSV4_WBF16) {
         /* token by token: per (row, token) the GEMV's own arithmetic */
         for (int t = 0; t < nt && rc == 0; t++)
             rc = res_gemv(*r, r0, m->rows, (float *)(g_ar.d + yo) + (size_t)t * m->rows,
@@ -498,6 +540,16 @@ int dsv4_gpu_fp4_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
     }
     return dsv4_fp4_gemv_launch(d_y, d_x, d_w, d_s, rows, cols, blk_r, blk_c,
                                 as_stream(stream));
+}
+
+int dsv4_gpu_bf16_gemv_d(float *d_y, const float *d_x, const uint16_t *d_w, int rows,
+                         int cols, void *stream)
+{
+    if (!d_y || !d_x || !d_w) {
+        DSV4_ERR("bf16_gemv_d: bad arguments");
+        return -1;
+    }
+    return dsv4_bf16_gemv_launch(d_y, d_x, d_w, rows, cols, as_stream(stream));
 }
 
 /* ---------------------------------------------------------------- dumps */

@@ -44,6 +44,10 @@ int dsv4_gpu_fp4_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
 { (void)d_y; (void)d_x; (void)d_w; (void)d_s; (void)rows; (void)cols; (void)blk_r;
   (void)blk_c; (void)stream; return -1; }
 
+int dsv4_gpu_bf16_gemv_d(float *d_y, const float *d_x, const uint16_t *d_w, int rows,
+                         int cols, void *stream)
+{ (void)d_y; (void)d_x; (void)d_w; (void)rows; (void)cols; (void)stream; return -1; }
+
 int dsv4_gpu_dump_e4m3(float *h) { (void)h; return -1; }
 int dsv4_gpu_dump_e8m0(float *h) { (void)h; return -1; }
 int dsv4_gpu_dump_e2m1(float *h) { (void)h; return -1; }

@@ -39,6 +39,12 @@ bool dsv4_fp4_gemv_ok(int rows, int cols, int blk_r, int blk_c);
 int dsv4_fp4_gemv_launch(float *y, const float *x, const uint8_t *W, const uint8_t *S,
                          int rows, int cols, int blk_r, int blk_c, hipStream_t st);
 
+/* BF16 GEMV (dsv4_matmul_bf16): W bf16 [rows][cols]. _ok: the shapes it
+ * takes (cols a multiple of 8 up to 16384). Returns 0 / -1. */
+bool dsv4_bf16_gemv_ok(int rows, int cols);
+int dsv4_bf16_gemv_launch(float *y, const float *x, const uint16_t *W, int rows, int cols,
+                          hipStream_t st);
+
 /* Batched: y[nt][rows], x[nt][cols]; per (row, token) bit-identical to the
  * GEMV above. */
 int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,

@@ -87,14 +87,16 @@ void dsv4_gpu_shutdown(void);
 
 /* ================================================= FP8 / FP4 dense matrices */
 
-/* Copy one FP8 matrix (E8M0 block scales, the reference's format) or one
+/* Copy one FP8 matrix (E8M0 block scales, the reference's format), one
  * MXFP4 matrix (e2m1 nibbles, E8M0 scale per blk_r x blk_c block; cols a
- * multiple of 32 up to 16384, blk_c a multiple of 32) into HBM, keyed by
- * m->w. 0 ok; -1 recoverable (another format or shape, no room with 256 MiB
- * of headroom, copy failed) -- the matrix then stays on the CPU. Idempotent
- * per key. Replaces dsv4_cuda_upload (dsv4_cuda.h:80, dsv4_cuda.cu:307),
- * which took FP8 only; FP4 residency lets the reference's dispatch
- * (dsv4_matmul.c:525-546) run the experts' matrices on the device too. */
+ * multiple of 32 up to 16384, blk_c a multiple of 32) or one BF16 matrix
+ * (m->s unused; cols a multiple of 8 up to 16384) into HBM, keyed by m->w.
+ * 0 ok; -1 recoverable (another format or shape, no room with 256 MiB of
+ * headroom, copy failed) -- the matrix then stays on the CPU. Idempotent per
+ * key. Replaces dsv4_cuda_upload (dsv4_cuda.h:80, dsv4_cuda.cu:307), which
+ * took FP8 only; FP4 and BF16 residency let the reference's dispatch
+ * (dsv4_matmul.c:525-546) run the experts' matrices, the router gate and the
+ * LM head on the device too. */
 int dsv4_gpu_upload(const DSV4QMat *m);
 
 /* The same for an FP8 matrix whose block scales are fp32 (m->s is a float
@@ -112,9 +114,9 @@ int dsv4_gpu_upload_f32s(const DSV4QMat *m);
 int dsv4_gpu_has(const DSV4QMat *m);
 
 /* y[rows] = dequant(m) . x[cols], host buffers, synchronous. abort() if m is
- * not resident. FP8 as dsv4_matmul_fp8, FP4 as dsv4_matmul_fp4
- * (dsv4_matmul.c:293-345). Replaces dsv4_cuda_mmq (dsv4_cuda.h:88,
- * dsv4_cuda.cu:387). */
+ * not resident. FP8 as dsv4_matmul_fp8, FP4 as dsv4_matmul_fp4, BF16 as
+ * dsv4_matmul_bf16 (dsv4_matmul.c:275-345). Replaces dsv4_cuda_mmq
+ * (dsv4_cuda.h:88, dsv4_cuda.cu:387). */
 void dsv4_gpu_mmq(float *y, const float *x, const DSV4QMat *m);
 
 /* y[nt][rows] for x[nt][cols]: one pass over the weights for the batch. Per
@@ -139,6 +141,13 @@ int dsv4_gpu_fp8_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
 int dsv4_gpu_fp4_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
                         const uint8_t *d_s, int rows, int cols, int blk_r, int blk_c,
                         void *stream);
+
+/* The BF16 GEMV on raw device buffers, stream-ordered: d_y[rows] =
+ * dsv4_matmul_bf16 (dsv4_matmul.c:275-291) of d_w (bf16 [rows][cols]) and
+ * d_x, both 16-byte aligned. What dsv4_gpu_mmq runs for a resident BF16
+ * matrix. 0 / -1 (cols not a multiple of 8 up to 16384). */
+int dsv4_gpu_bf16_gemv_d(float *d_y, const float *d_x, const uint16_t *d_w, int rows,
+                         int cols, void *stream);
 
 /* ========================================================== decoder gates */
 

@@ -31,6 +31,7 @@ _REF_PATH = os.path.join(HERE, "_ref", "libdsv4ref.so")
 _f32p = ctypes.POINTER(ctypes.c_float)
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _i32p = ctypes.POINTER(ctypes.c_int)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
 _vp = ctypes.c_void_p
 
 _orc = None
@@ -66,6 +67,7 @@ def lib():
         L.orc_matmul_fp8_n.argtypes = L.orc_matmul_fp8.argtypes + [ctypes.c_int]
         L.orc_matmul_fp4.argtypes = [_f32p, _f32p, _u8p, _u8p, ctypes.c_int,
                                      ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.orc_matmul_bf16.argtypes = [_f32p, _f32p, _u16p, ctypes.c_int, ctypes.c_int]
         L.orc_swiglu.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_float]
         pp = ctypes.POINTER(_u8p)
         L.orc_moe_fp4.argtypes = [_f32p, _f32p, _f32p, pp, pp, pp, pp, pp, pp,
@@ -103,6 +105,8 @@ def ref():
         L.dsv4_matmul_fp8_n.argtypes = [_f32p, _f32p, _u8p, _u8p, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int]
+        for n in ("dsv4_matmul_bf16", "dsv4_matmul_bf16_scalar"):
+            getattr(L, n).argtypes = [_f32p, _f32p, _u16p, ctypes.c_int, ctypes.c_int]
         L.dsv4_swiglu.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_float]
         L.dsv4_indexer_score.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int,
                                          ctypes.c_int, ctypes.c_int]
@@ -152,6 +156,15 @@ def matmul_fp8(x, W, S, blk_r=128, blk_c=128):
     y = np.empty((nt, out), np.float32)
     lib().orc_matmul_fp8_n(_p(y, _f32p), _p(x, _f32p), _p(W, _u8p),
                            S.ctypes.data, kind, inn, out, blk_r, blk_c, nt)
+    return y
+
+
+def matmul_bf16(x, W):
+    """y = W x for bf16 weights W [out][in] (uint16 bit patterns)."""
+    W = np.ascontiguousarray(W, np.uint16); x = _f32(x)
+    out, inn = W.shape
+    y = np.empty(out, np.float32)
+    lib().orc_matmul_bf16(_p(y, _f32p), _p(x, _f32p), W.ctypes.data_as(_u16p), inn, out)
     return y
 
 
@@ -260,6 +273,15 @@ def ref_matmul_fp8_n(x, W, S_e8m0, blk_r=128, blk_c=128):
     y = np.empty((nt, out), np.float32)
     ref().dsv4_matmul_fp8_n(_p(y, _f32p), _p(x, _f32p), _p(W, _u8p), _p(S, _u8p),
                             inn, out, blk_r, blk_c, nt)
+    return y
+
+
+def ref_matmul_bf16(x, W, scalar=False):
+    W = np.ascontiguousarray(W, np.uint16); x = _f32(x)
+    out, inn = W.shape
+    y = np.empty(out, np.float32)
+    fn = ref().dsv4_matmul_bf16_scalar if scalar else ref().dsv4_matmul_bf16
+    fn(_p(y, _f32p), _p(x, _f32p), W.ctypes.data_as(_u16p), inn, out)
     return y
 
 

@@ -70,6 +70,16 @@ void orc_dump_e4m3(float *out256) { for (int i = 0; i < 256; i++) out256[i] = or
 void orc_dump_e8m0(float *out256) { for (int i = 0; i < 256; i++) out256[i] = orc_e8m0_to_f32((uint8_t)i); }
 void orc_dump_e2m1(float *out16)  { for (int i = 0; i < 16; i++)  out16[i]  = orc_e2m1_to_f32((uint8_t)i); }
 
+/* bf16 -> double (dsv4_matmul.c:108-112 bf16d): the 16 bits are the top half
+ * of an IEEE float, widened exactly. */
+static double orc_bf16_to_f64(uint16_t h)
+{
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, sizeof f);
+    return (double)f;
+}
+
 /* One table per process; every entry is the decoder's own output. */
 static float g_e4m3[256];
 static int g_e4m3_ready;
@@ -98,6 +108,33 @@ static double block_dot(const double *wv, const float *xb, int n)
     double acc = (b0 + b1) + (b2 + b3);
     for (; i < n; i++) acc = fma(wv[i], (double)xb[i], acc);
     return acc;
+}
+
+/* The same tree over bf16 weights (widened exactly: the bf16 bits are the
+ * top half of the float). */
+static double bf16_dot(const uint16_t *w, const float *xb, int n)
+{
+    double a[16] = {0};
+    int i = 0;
+    for (; i + 15 < n; i += 16)
+        for (int l = 0; l < 16; l++)
+            a[l] = fma(orc_bf16_to_f64(w[i + l]), (double)xb[i + l], a[l]);
+    const double b0 = (a[0] + a[4]) + (a[8] + a[12]);
+    const double b1 = (a[1] + a[5]) + (a[9] + a[13]);
+    const double b2 = (a[2] + a[6]) + (a[10] + a[14]);
+    const double b3 = (a[3] + a[7]) + (a[11] + a[15]);
+    double acc = (b0 + b1) + (b2 + b3);
+    for (; i < n; i++) acc = fma(orc_bf16_to_f64(w[i]), (double)xb[i], acc);
+    return acc;
+}
+
+/* dsv4_matmul.c:275-291 (dsv4_matmul_bf16 via GEN_MATMULS): one dot over the
+ * whole row in the block-dot tree, rounded to float once. */
+void orc_matmul_bf16(float *y, const float *x, const uint16_t *W, int in, int out)
+{
+#pragma omp parallel for schedule(static) if (out > 64)
+    for (int o = 0; o < out; o++)
+        y[o] = (float)bf16_dot(W + (size_t)o * in, x, in);
 }
 
 /* Scale of block (row-block rb, col-block cb): E8M0 byte (the reference's

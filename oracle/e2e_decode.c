@@ -23,9 +23,11 @@
  *     path;
  *   - pass 2: dsv4_gpu_init plus the FP8 trunk upload of dsv4_run.c:270-283,
  *     so every FP8 matmul (including the wo_a group slices) runs on the
- *     MI355X; every expert's FP4 matrices are made resident too, so the
- *     experts' matmuls of expert_forward (dsv4_layer.c:199-206) run there
- *     through the same dispatch; and the CSA calls of attention()
+ *     MI355X; every expert's FP4 matrices and every BF16 matrix (router
+ *     gates, compressors, indexer weights, the LM head) are made resident
+ *     too, so the experts' matmuls of expert_forward (dsv4_layer.c:199-206)
+ *     and the rest run there through the same dispatch; and the CSA calls of
+ *     attention()
  *     (dsv4_layer.c:286-301) go to the device. oracle/Makefile compiles
  *     dsv4_layer.c with dsv4_indexer_score / dsv4_topk / dsv4_sparse_attn
  *     renamed to the e2e_* wrappers below, which call dsv4_gpu_indexer_score
@@ -347,7 +349,7 @@ int main(int argc, char **argv)
     float *got = malloc((size_t)n * c.vocab * sizeof(float));
     if (!ref || !got || run_pass(&M, tok, n, ref) != 0) return 1;
 
-    int gpu_mats = 0, fp4_mats = 0;
+    int gpu_mats = 0, fp4_mats = 0, bf16_mats = 0;
     if (cpu_only) {
         if (run_pass(&M, tok, n, got) != 0) return 1;
     } else {
@@ -366,6 +368,15 @@ int main(int argc, char **argv)
                 if (m[k]->wdt == DSV4_WFP8 && dsv4_gpu_upload(m[k]) == 0) gpu_mats++;
                 if (m[k]->wdt == DSV4_WFP4 && dsv4_gpu_upload(m[k]) == 0) fp4_mats++;
             }
+            /* the BF16 matrices: router gate, compressors, indexer weights */
+            const DSV4QMat *b[6] = {&w->moe.gate,
+                                    w->attn.has_comp ? &w->attn.comp.wkv : NULL,
+                                    w->attn.has_comp ? &w->attn.comp.wgate : NULL,
+                                    w->attn.has_idx ? &w->attn.idx.weights_proj : NULL,
+                                    w->attn.has_idx ? &w->attn.idx.comp.wkv : NULL,
+                                    w->attn.has_idx ? &w->attn.idx.comp.wgate : NULL};
+            for (int k = 0; k < 6; k++)
+                if (b[k] && b[k]->wdt == DSV4_WBF16 && dsv4_gpu_upload(b[k]) == 0) bf16_mats++;
             for (int e = 0; e < c.n_experts; e++) {
                 const DSV4ExpertW *x = &E.w[(size_t)L * c.n_experts + e];
                 const DSV4QMat *em[3] = {&x->w1, &x->w2, &x->w3};
@@ -373,8 +384,11 @@ int main(int argc, char **argv)
                     if (dsv4_gpu_upload(em[k]) == 0) fp4_mats++;
             }
         }
-        printf("gpu: %d FP8 and %d FP4 matrices resident, CSA on the device\n",
-               gpu_mats, fp4_mats);
+        /* the LM head, the same QMat run_pass builds (dsv4_run.c:467-474) */
+        const DSV4QMat head = {mb.w.head, NULL, DSV4_WBF16, c.vocab, c.hidden, 0, 0};
+        if (dsv4_gpu_upload(&head) == 0) bf16_mats++;
+        printf("gpu: %d FP8, %d FP4 and %d BF16 matrices resident, CSA on the device\n",
+               gpu_mats, fp4_mats, bf16_mats);
         g_gpu_csa = 1;
         if (gpu_mats == 0 || run_pass(&M, tok, n, got) != 0) return 1;
         g_gpu_csa = 0;
@@ -393,8 +407,8 @@ int main(int argc, char **argv)
                cpu_only ? "cpu2" : "gpu", ag, (double)mr, r);
     }
     printf("summary: positions %d argmax_equal %d worst_rel %.3g gpu_mats %d "
-           "fp4_mats %d gpu_score %ld gpu_topk %ld gpu_attn %ld\n", n, agree, worst,
-           gpu_mats, fp4_mats, g_n_score, g_n_topk, g_n_attn);
+           "fp4_mats %d gpu_score %ld gpu_topk %ld gpu_attn %ld bf16_mats %d\n", n, agree,
+           worst, gpu_mats, fp4_mats, g_n_score, g_n_topk, g_n_attn, bf16_mats);
     if (!cpu_only) dsv4_gpu_shutdown();
     return agree == n ? 0 : 1;
 }

@@ -125,3 +125,12 @@ def bits_equal(a, b):
     a = np.ascontiguousarray(a, np.float32)
     b = np.ascontiguousarray(b, np.float32)
     return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def bf16_matrix(rng, shape, scale=1.0):
+    """bf16 bit patterns [rows][cols] of N(0, scale^2) values (round to
+    nearest even), finite by construction."""
+    v = (rng.standard_normal(shape) * scale).astype(np.float32)
+    u = v.view(np.uint32)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return r

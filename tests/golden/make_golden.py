@@ -118,6 +118,13 @@ def small():
         out.update({tag + "_q": qa, tag + "_kv": kva, tag + "_sink": sink,
                     tag + "_idx": sel, tag + "_scale": np.float32(scale),
                     tag + "_o": oracle.ref_sparse_attn(qa, kva, sink, sel, float(scale))})
+    # BF16 GEMV (dsv4_matmul_bf16), ragged, drawn after every case above so
+    # their inputs stay the same.
+    Wb = common.bf16_matrix(rng, (75, 1000))
+    xb = rng.standard_normal(1000).astype(np.float32)
+    yb = oracle.ref_matmul_bf16(xb, Wb)
+    assert common.bits_equal(yb, oracle.ref_matmul_bf16(xb, Wb, scalar=True))
+    out.update(bf16_W=Wb, bf16_x=xb, bf16_y=yb)
     np.savez_compressed(os.path.join(HERE, "golden_small.npz"), **out)
     print("golden_small.npz: %d arrays" % len(out))
 

@@ -35,6 +35,11 @@ def test_fp8_batched_golden():
     assert np.array_equal(bits(y), bits(G["fp8n_y"]))
 
 
+def test_bf16_gemv_golden():
+    y = oracle.matmul_bf16(G["bf16_x"], G["bf16_W"])
+    assert np.array_equal(bits(y), bits(G["bf16_y"]))
+
+
 def test_fp4_gemv_golden():
     y = oracle.matmul_fp4(G["fp4_x"], G["fp4_W"], G["fp4_S"], G["fp4_x"].size)
     assert np.array_equal(bits(y), bits(G["fp4_y"]))

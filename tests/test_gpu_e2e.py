@@ -5,8 +5,9 @@ indexer with selection, sparse MLA), run by the reference's own C99 model
 code. In the second pass every FP8 matrix the reference uploads
 (dsv4_run.c:270-283) runs on the MI355X through dsv4_gpu_mmq. That includes
 the wo_a group slices, which resolve as row-range views. Every expert's FP4
-matrices are resident too (the experts' matmuls run on the device through the
-same dispatch), and attention()'s CSA calls -- indexer score, top-k, sparse
+matrices and every BF16 matrix (router gates, compressors, indexer weights, the
+LM head) are resident too (they run on the device through the same dispatch),
+and attention()'s CSA calls -- indexer score, top-k, sparse
 attention (dsv4_layer.c:286-301) -- go to dsv4_gpu_indexer_score /
 dsv4_gpu_topk / dsv4_gpu_sparse_attn.
 
@@ -41,5 +42,6 @@ def test_gpu_trunk_argmax_identical(tmp_path):
     assert fp4 >= 4 * 16 * 3        # every routed expert's w1, w2, w3
     assert attn == 46 * 4           # one sparse attention per layer and position
     assert score > 0 and topk == score   # the CSA layers selected on the device
+    assert int(summ.group(9)) >= 1 + 4      # the LM head and every router gate
     assert worst < 2e-3
     assert any(r["rel"] > 0.0 for r in rows), "GPU pass produced CPU bits: trunk not on GPU?"

@@ -224,8 +224,12 @@ def test_upload_refusals(gpu, dsv4):
     L = dsv4.lib()
     W = np.zeros((4, 32), np.uint8)
     S = np.zeros((4, 1), np.uint8)
-    m4 = dsv4.DSV4QMat(W.ctypes.data, S.ctypes.data, dsv4.WFP4, 4, 64, 1, 32)
-    assert L.dsv4_gpu_upload(ctypes.byref(m4)) == -1          # FP4 is not a trunk matrix
+    mf32 = dsv4.DSV4QMat(W.ctypes.data, S.ctypes.data, dsv4.WF32, 4, 8, 1, 1)
+    assert L.dsv4_gpu_upload(ctypes.byref(mf32)) == -1        # no f32 matrices on the device
+    m4 = dsv4.DSV4QMat(W.ctypes.data, S.ctypes.data, dsv4.WFP4, 4, 64, 1, 16)
+    assert L.dsv4_gpu_upload(ctypes.byref(m4)) == -1          # FP4 blocks narrower than 32
+    m8 = dsv4.DSV4QMat(W.ctypes.data, S.ctypes.data, dsv4.WFP8, 4, 32, 0, 128)
+    assert L.dsv4_gpu_upload(ctypes.byref(m8)) == -1          # no row blocking
     mnull = dsv4.DSV4QMat(None, None, dsv4.WFP8, 4, 32, 128, 128)
     assert L.dsv4_gpu_upload(ctypes.byref(mnull)) == -1
     huge = dsv4.DSV4QMat(W.ctypes.data, S.ctypes.data, dsv4.WFP8, 1 << 30, 1 << 30, 128, 128)

@@ -103,6 +103,33 @@ def test_fp4_known_answers():
     assert y[0] == -32.0       # +1 on even (low nibble), -1 on odd, scale 2
 
 
+def bf16_bits(v):
+    return (np.asarray(v, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def test_bf16_known_answers():
+    """Exact-representable cases (the bf16 rows of test_matmul.c): small
+    integers and powers of two, every product and partial sum exact."""
+    W = bf16_bits(np.array([[1.0] * 64, [2.0] * 64, [-0.5] * 64], np.float32))
+    y = oracle.matmul_bf16(np.ones(64, np.float32), W)
+    assert list(y) == [64.0, 128.0, -32.0]
+    W = bf16_bits(np.arange(1, 38, dtype=np.float32)[None, :])      # ragged tail
+    y = oracle.matmul_bf16(np.arange(1, 38, dtype=np.float32), W)
+    assert y[0] == float(sum(i * i for i in range(1, 38)))
+
+
+def test_bf16_against_double_math():
+    """Independent of the tree: products widened to float64 and summed agree
+    to within f32 rounding of the result."""
+    rng = np.random.default_rng(6)
+    W = common.bf16_matrix(rng, (70, 1000))
+    x = rng.standard_normal(1000).astype(np.float32)
+    Wd = (W.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    want = Wd @ x.astype(np.float64)
+    got = oracle.matmul_bf16(x, W)
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-30)) < 1e-6
+
+
 def test_fp8_scale_formats_agree_for_powers_of_two():
     W, Sf, Se, x = common.fp8_problem(3, 300, 640)
     assert common.bits_equal(oracle.matmul_fp8(x, W, Sf), oracle.matmul_fp8(x, W, Se))
@@ -118,6 +145,17 @@ def test_fp8_against_double_math():
     want = (Wd * sc) @ x.astype(np.float64)
     got = oracle.matmul_fp8(x, W, Se)
     assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-30)) < 1e-6
+
+
+@ref_only
+def test_bf16_bit_equal_to_compiled_reference():
+    rng = np.random.default_rng(12)
+    for out, inn in [(37, 1000), (5, 16), (9, 7), (130, 7168)]:
+        W = common.bf16_matrix(rng, (out, inn))
+        x = rng.standard_normal(inn).astype(np.float32)
+        a = oracle.matmul_bf16(x, W)
+        assert common.bits_equal(a, oracle.ref_matmul_bf16(x, W))
+        assert common.bits_equal(a, oracle.ref_matmul_bf16(x, W, scalar=True))
 
 
 @ref_only

@@ -69,6 +69,9 @@ _SIGS = {
     "dsv4_gpu_fp8_gemv_d": (_ci, [_vp, _vp, _vp, _vp, _ci, _ci, _ci, _vp]),
     "dsv4_gpu_fp4_gemv_d": (_ci, [_vp, _vp, _vp, _vp, _ci, _ci, _ci, _ci, _vp]),
     "dsv4_gpu_bf16_gemv_d": (_ci, [_vp, _vp, _vp, _ci, _ci, _vp]),
+    "dsv4_gpu_head_argmax": (_ci, [_vp, _QP]),
+    "dsv4_gpu_argmax_d": (_ci, [_vp, _vp, _ci, _vp]),
+    "dsv4_gpu_embed_row_d": (_ci, [_vp, _vp, _ci, ctypes.c_longlong, _ci, _vp]),
     "dsv4_gpu_dump_e4m3": (_ci, [_vp]),
     "dsv4_gpu_dump_e8m0": (_ci, [_vp]),
     "dsv4_gpu_dump_e2m1": (_ci, [_vp]),

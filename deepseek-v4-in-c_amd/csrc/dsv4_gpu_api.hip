@@ -64,7 +64,7 @@ hipStream_t g_stream = nullptr;
 std::vector<Res> g_res;
 std::vector<LayerExperts> g_layers;
 Arena g_ar;
-Scratch g_moe, g_attn, g_scores, g_index;
+Scratch g_moe, g_attn, g_scores, g_index, g_amax;
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -438,7 +438,7 @@ void dsv4_gpu_shutdown(void)
         if (L.dev) (void)hipFree(L.dev);
     }
     g_layers.clear();
-    for (Scratch *s : {&g_moe, &g_attn, &g_scores, &g_index}) {
+    for (Scratch *s : {&g_moe, &g_attn, &g_scores, &g_index, &g_amax}) {
         if (s->p) (void)hipFree(s->p);
         s->p = nullptr;
         s->cap = 0;
@@ -550,6 +550,43 @@ int dsv4_gpu_bf16_gemv_d(float *d_y, const float *d_x, const uint16_t *d_w, int 
         return -1;
     }
     return dsv4_bf16_gemv_launch(d_y, d_x, d_w, rows, cols, as_stream(stream));
+}
+
+/* ----------------------------------------------------------------- head */
+int dsv4_gpu_head_argmax(const float *x, const DSV4QMat *head)
+{
+    int r0 = 0;
+    const Res *r = g_ready ? find_view(head, &r0) : nullptr;
+    if (!r || !x) {
+        DSV4_ERR("head_argmax: the head matrix is not resident");
+        return -1;
+    }
+    if (scratch_reserve(g_amax, dsv4_argmax_scratch_bytes()) != 0) return -1;
+    Stage s;
+    const size_t xo = s.in(x, (size_t)r->cols * sizeof(float));
+    const size_t lo = s.add((size_t)head->rows * sizeof(float));
+    const size_t to = s.add(sizeof(int));
+    size_t end;
+    if (stage_push(s, &end) != 0) return -1;
+    if (res_gemv(*r, r0, head->rows, (float *)(g_ar.d + lo), (const float *)(g_ar.d + xo)) != 0 ||
+        dsv4_argmax_launch((int *)(g_ar.d + to), (const float *)(g_ar.d + lo), head->rows,
+                           g_amax.p, g_stream) != 0)
+        return -1;
+    int tok = -1;
+    if (stage_pull(to, sizeof(int), &tok) != 0) return -1;
+    return tok;
+}
+
+int dsv4_gpu_argmax_d(int *d_out, const float *d_v, int n, void *stream)
+{
+    if (!g_ready || scratch_reserve(g_amax, dsv4_argmax_scratch_bytes()) != 0) return -1;
+    return dsv4_argmax_launch(d_out, d_v, n, g_amax.p, as_stream(stream));
+}
+
+int dsv4_gpu_embed_row_d(float *d_dst, const void *d_table, int wdt, long long row,
+                         int hidden, void *stream)
+{
+    return dsv4_embed_row_launch(d_dst, d_table, wdt, row, hidden, as_stream(stream));
 }
 
 /* ---------------------------------------------------------------- dumps */

@@ -48,6 +48,14 @@ int dsv4_gpu_bf16_gemv_d(float *d_y, const float *d_x, const uint16_t *d_w, int 
                          int cols, void *stream)
 { (void)d_y; (void)d_x; (void)d_w; (void)rows; (void)cols; (void)stream; return -1; }
 
+int dsv4_gpu_head_argmax(const float *x, const DSV4QMat *head)
+{ (void)x; (void)head; return -1; }
+int dsv4_gpu_argmax_d(int *d_out, const float *d_v, int n, void *stream)
+{ (void)d_out; (void)d_v; (void)n; (void)stream; return -1; }
+int dsv4_gpu_embed_row_d(float *d_dst, const void *d_table, int wdt, long long row,
+                         int hidden, void *stream)
+{ (void)d_dst; (void)d_table; (void)wdt; (void)row; (void)hidden; (void)stream; return -1; }
+
 int dsv4_gpu_dump_e4m3(float *h) { (void)h; return -1; }
 int dsv4_gpu_dump_e8m0(float *h) { (void)h; return -1; }
 int dsv4_gpu_dump_e2m1(float *h) { (void)h; return -1; }

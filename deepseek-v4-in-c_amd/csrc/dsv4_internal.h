@@ -45,6 +45,15 @@ bool dsv4_bf16_gemv_ok(int rows, int cols);
 int dsv4_bf16_gemv_launch(float *y, const float *x, const uint16_t *W, int rows, int cols,
                           hipStream_t st);
 
+/* Greedy argmax (the first index of the maximum, dsv4_run.c:471-472) over
+ * d_v[n] into d_out[0]; scratch of dsv4_argmax_scratch_bytes. 0 / -1. */
+size_t dsv4_argmax_scratch_bytes(void);
+int dsv4_argmax_launch(int *d_out, const float *d_v, int n, void *scratch, hipStream_t st);
+
+/* dsv4_embed_row (dsv4.h:300-314) on device buffers. 0 / -1. */
+int dsv4_embed_row_launch(float *d_dst, const void *d_table, int wdt, long long row,
+                          int hidden, hipStream_t st);
+
 /* Batched: y[nt][rows], x[nt][cols]; per (row, token) bit-identical to the
  * GEMV above. */
 int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,

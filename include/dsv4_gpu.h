@@ -149,6 +149,29 @@ int dsv4_gpu_fp4_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
 int dsv4_gpu_bf16_gemv_d(float *d_y, const float *d_x, const uint16_t *d_w, int rows,
                          int cols, void *stream);
 
+/* ================================================================ the head */
+
+/* The decode loop's head in one call (dsv4_run.c:467-472): logits =
+ * head . x with head a resident matrix (BF16 as the reference's, or FP8/FP4),
+ * then the greedy argmax over them -- the first index of the maximum, as the
+ * reference's scan `if (logits[v] > logits[best]) best = v` gives it (a NaN
+ * is never chosen unless it sits at index 0). x host f32[head->cols].
+ * Returns the token id, or -1 (head not resident, launch failure). Only the
+ * id crosses back to the host, not the vocab-wide logits. No reference
+ * counterpart (the reference runs the head on the CPU). */
+int dsv4_gpu_head_argmax(const float *x, const DSV4QMat *head);
+
+/* The same argmax on a device vector, stream-ordered: d_out[0] = argmax of
+ * d_v[n]. Uses library scratch (calls on one device do not overlap). 0 / -1.
+ * No reference counterpart. */
+int dsv4_gpu_argmax_d(int *d_out, const float *d_v, int n, void *stream);
+
+/* dsv4_embed_row (include/dsv4/dsv4.h:300-314) on device buffers: d_dst[hidden]
+ * = row `row` of the device table d_table (DSV4_WBF16, widened exactly, or
+ * DSV4_WF32), stream-ordered. 0 / -1. */
+int dsv4_gpu_embed_row_d(float *d_dst, const void *d_table, int wdt, long long row,
+                         int hidden, void *stream);
+
 /* ========================================================== decoder gates */
 
 /* Device decode of all 256 E4M3FN codes / 256 E8M0 codes / 16 E2M1 codes with

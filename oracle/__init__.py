@@ -68,6 +68,10 @@ def lib():
         L.orc_matmul_fp4.argtypes = [_f32p, _f32p, _u8p, _u8p, ctypes.c_int,
                                      ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.orc_matmul_bf16.argtypes = [_f32p, _f32p, _u16p, ctypes.c_int, ctypes.c_int]
+        L.orc_argmax.restype = ctypes.c_int
+        L.orc_argmax.argtypes = [_f32p, ctypes.c_int]
+        L.orc_embed_row.argtypes = [_f32p, ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong,
+                                    ctypes.c_int]
         L.orc_swiglu.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_float]
         pp = ctypes.POINTER(_u8p)
         L.orc_moe_fp4.argtypes = [_f32p, _f32p, _f32p, pp, pp, pp, pp, pp, pp,
@@ -166,6 +170,23 @@ def matmul_bf16(x, W):
     y = np.empty(out, np.float32)
     lib().orc_matmul_bf16(_p(y, _f32p), _p(x, _f32p), W.ctypes.data_as(_u16p), inn, out)
     return y
+
+
+def argmax(v):
+    """The decode loop's greedy pick (dsv4_run.c:471-472)."""
+    v = _f32(v)
+    return lib().orc_argmax(_p(v, _f32p), v.size)
+
+
+def embed_row(table, row):
+    """dsv4_embed_row: table uint16 (bf16 bits) or float32 [vocab][hidden]."""
+    table = np.ascontiguousarray(table)
+    wdt = 1 if table.dtype == np.uint16 else 0
+    if wdt == 0:
+        table = _f32(table)
+    dst = np.empty(table.shape[1], np.float32)
+    lib().orc_embed_row(_p(dst, _f32p), table.ctypes.data, wdt, int(row), table.shape[1])
+    return dst
 
 
 def matmul_fp4(x, W, S, inn, blk_r=1, blk_c=32):

@@ -394,3 +394,31 @@ void orc_sparse_attn(float *o, const float *q, const float *kv, int kv_stride,
         free(s);
     }
 }
+
+/* ------------------------------------------------------------------ head --- */
+/* The greedy pick of the decode loop (dsv4_run.c:471-472): the first index
+ * of the maximum under `>`; a NaN is never chosen unless it is at index 0. */
+int orc_argmax(const float *v, int n)
+{
+    int best = 0;
+    for (int i = 1; i < n; i++)
+        if (v[i] > v[best]) best = i;
+    return best;
+}
+
+/* dsv4_embed_row (include/dsv4/dsv4.h:300-314): a BF16 row widened (the 16
+ * bits become the top half of the float), or an f32 row copied. wdt 1 =
+ * BF16, otherwise f32. */
+void orc_embed_row(float *dst, const void *table, int wdt, long long row, int hidden)
+{
+    if (wdt == 1) {
+        const uint16_t *p = (const uint16_t *)table + row * hidden;
+        for (int i = 0; i < hidden; i++) {
+            const uint32_t u = (uint32_t)p[i] << 16;
+            memcpy(&dst[i], &u, sizeof u);
+        }
+    } else {
+        const float *p = (const float *)table + row * hidden;
+        for (int i = 0; i < hidden; i++) dst[i] = p[i];
+    }
+}

@@ -66,7 +66,7 @@ void dsv4_indexer_score(float *, const float *, const float *, const float *,
 int dsv4_topk(int *, const float *, int, int);
 
 static int g_gpu_csa;                       /* pass 2: CSA calls on the device */
-static long g_n_score, g_n_topk, g_n_attn;
+static long g_n_score, g_n_topk, g_n_attn, g_n_head, g_n_head_ok;
 
 static void csa_fail(const char *what)
 {
@@ -240,7 +240,19 @@ typedef struct {
     int maxpos;
 } Model;
 
-/* One greedy pass over the tokens from fresh layer state; logits[pos][vocab]. */
+/* The reference's greedy pick (dsv4_run.c:471-472). */
+static int first_max(const float *v, int n)
+{
+    int best = 0;
+    for (int i = 1; i < n; i++)
+        if (v[i] > v[best]) best = i;
+    return best;
+}
+
+/* One greedy pass over the tokens from fresh layer state; logits[pos][vocab].
+ * In the GPU pass the head also runs as dsv4_gpu_head_argmax (the GEMV and
+ * the argmax on the device, only the token id back), which must pick what
+ * the reference's scan picks from the logits. */
 static int run_pass(const Model *M, const int *tok, int n, float *logits)
 {
     const DSV4Cfg *c = M->c;
@@ -264,6 +276,11 @@ static int run_pass(const Model *M, const int *tok, int n, float *logits)
         head_hc(y, h, &M->mb->w.hc_head, hc, d, c->rms_eps, c->hc_eps);
         dsv4_rmsnorm(y, y, M->mb->w.norm, d, c->rms_eps);
         dsv4_mmq(logits + (size_t)pos * c->vocab, y, &head);
+        if (g_gpu_csa) {
+            const int t = dsv4_gpu_head_argmax(y, &head);
+            g_n_head++;
+            g_n_head_ok += t == first_max(logits + (size_t)pos * c->vocab, c->vocab);
+        }
     }
     for (int L = 0; L < c->n_layers; L++) dsv4_state_free(&ls[L]);
     free(ls); free(h); free(y);
@@ -407,8 +424,9 @@ int main(int argc, char **argv)
                cpu_only ? "cpu2" : "gpu", ag, (double)mr, r);
     }
     printf("summary: positions %d argmax_equal %d worst_rel %.3g gpu_mats %d "
-           "fp4_mats %d gpu_score %ld gpu_topk %ld gpu_attn %ld bf16_mats %d\n", n, agree,
-           worst, gpu_mats, fp4_mats, g_n_score, g_n_topk, g_n_attn, bf16_mats);
+           "fp4_mats %d gpu_score %ld gpu_topk %ld gpu_attn %ld bf16_mats %d "
+           "head_ok %ld/%ld\n", n, agree, worst, gpu_mats, fp4_mats, g_n_score, g_n_topk,
+           g_n_attn, bf16_mats, g_n_head_ok, g_n_head);
     if (!cpu_only) dsv4_gpu_shutdown();
     return agree == n ? 0 : 1;
 }

@@ -35,5 +35,5 @@ def run(ckpt, tokens_file, cpu_only=False, timeout=300):
                              margin=float(m.group(5)), rel=float(m.group(6))))
     summ = re.search(r"summary: positions (\d+) argmax_equal (\d+) worst_rel (\S+) "
                      r"gpu_mats (\d+) fp4_mats (\d+) gpu_score (\d+) gpu_topk (\d+) "
-                     r"gpu_attn (\d+) bf16_mats (\d+)", p.stdout)
+                     r"gpu_attn (\d+) bf16_mats (\d+) head_ok (\d+)/(\d+)", p.stdout)
     return p, rows, summ

@@ -43,5 +43,6 @@ def test_gpu_trunk_argmax_identical(tmp_path):
     assert attn == 46 * 4           # one sparse attention per layer and position
     assert score > 0 and topk == score   # the CSA layers selected on the device
     assert int(summ.group(9)) >= 1 + 4      # the LM head and every router gate
+    assert int(summ.group(10)) == int(summ.group(11)) == 46   # dsv4_gpu_head_argmax
     assert worst < 2e-3
     assert any(r["rel"] > 0.0 for r in rows), "GPU pass produced CPU bits: trunk not on GPU?"

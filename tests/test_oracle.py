@@ -130,6 +130,44 @@ def test_bf16_against_double_math():
     assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-30)) < 1e-6
 
 
+def test_argmax_known_answers():
+    """dsv4_run.c:471-472: first maximum; ties to the lower index; -0.0 and
+    +0.0 compare equal; a NaN is never picked unless it is at index 0."""
+    assert oracle.argmax([1.0, 3.0, 2.0, 3.0]) == 1
+    assert oracle.argmax([-0.0, 0.0, -1.0]) == 0
+    assert oracle.argmax([0.0, -0.0]) == 0
+    assert oracle.argmax([1.0, np.nan, 2.0, np.nan]) == 2
+    assert oracle.argmax([np.nan, 5.0, 7.0]) == 0
+    assert oracle.argmax([-np.inf, -np.inf]) == 0
+    assert oracle.argmax([-np.inf, -1e30, np.inf, np.inf]) == 2
+
+
+def test_argmax_against_numpy():
+    """numpy's argmax is also the first maximum on NaN-free input."""
+    rng = np.random.default_rng(13)
+    for n in (1, 7, 1000, 129280):
+        v = rng.standard_normal(n).astype(np.float32)
+        v[rng.integers(0, n, 3)] = v.max()          # plant ties with the maximum
+        assert oracle.argmax(v) == int(np.argmax(v))
+
+
+def test_embed_row_known_answers_and_roundtrip():
+    """BF16 widening is exact: 1.0 = 0x3F80, -2.0 = 0xC000, and the f32 bits
+    carry the bf16 bits back unchanged; an f32 table row is copied."""
+    t = np.array([[0x3F80, 0xC000, 0x0000, 0x8000], [0x7F80, 0x0001, 0x4049, 0xFF80]],
+                 np.uint16)
+    r = oracle.embed_row(t, 0)
+    assert list(r[:2]) == [1.0, -2.0] and r[2] == 0.0 and np.signbit(r[3])
+    rng = np.random.default_rng(14)
+    tb = common.bf16_matrix(rng, (50, 300))
+    for row in (0, 17, 49):
+        got = oracle.embed_row(tb, row)
+        assert np.array_equal((got.view(np.uint32) >> 16).astype(np.uint16), tb[row])
+        assert np.array_equal(got.view(np.uint32) & 0xFFFF, np.zeros(300, np.uint32))
+    tf = rng.standard_normal((5, 33)).astype(np.float32)
+    assert np.array_equal(oracle.embed_row(tf, 3), tf[3])
+
+
 def test_fp8_scale_formats_agree_for_powers_of_two():
     W, Sf, Se, x = common.fp8_problem(3, 300, 640)
     assert common.bits_equal(oracle.matmul_fp8(x, W, Sf), oracle.matmul_fp8(x, W, Se))

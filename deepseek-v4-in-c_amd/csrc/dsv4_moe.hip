@@ -126,7 +126,7 @@ __device__ __forceinline__ void resolve_experts(Dsv4ExpertDev *sx,
  * [row0, row0 + rows_per_wg) and walks them in steps of rg*R; rows wider
  * than one wave leave per-wave gate/up partials in LDS, summed in wave order
  * after one barrier, then SwiGLU. */
-template <int NCH, int R, int PF>
+template <int NCH, int R>
 __global__ void __launch_bounds__(256)
 k_moe_gate_up(float *__restrict__ h, const float *__restrict__ x,
               const Dsv4ExpertDev *__restrict__ table, int n_table,
@@ -159,8 +159,8 @@ k_moe_gate_up(float *__restrict__ h, const float *__restrict__ x,
         load_x32(xr[n], x + c * 32, act[n]);
     }
 
-    u32x4 wg_[R][NCH], wu_[R][NCH], ng_[R][NCH], nu_[R][NCH];
-    uint32_t sg_[R][NCH], su_[R][NCH], nsg[R][NCH], nsu[R][NCH];
+    u32x4 wg_[R][NCH], wu_[R][NCH];
+    uint32_t sg_[R][NCH], su_[R][NCH];
     bool bad[R];
 
     /* This row group's first h-row as (expert slot, row): advanced by
@@ -208,10 +208,8 @@ k_moe_gate_up(float *__restrict__ h, const float *__restrict__ x,
     if (nsteps > 0) load(hr0, kq, oq, wg_, wu_, sg_, su_, bad);
     for (int step = 0; step < nsteps; ++step) {
         const int rbase = row0 + step * step_rows + g * R;
-        bool nbad[R];
         int kn = kq, on = oq;
         advance(kn, on);
-        if (PF && step + 1 < nsteps) load(rbase + step_rows, kn, on, ng_, nu_, nsg, nsu, nbad);
 
         float ag[R], au[R];
 #pragma unroll
@@ -248,19 +246,10 @@ k_moe_gate_up(float *__restrict__ h, const float *__restrict__ x,
                 }
             }
         }
-        if (PF) {
-#pragma unroll
-            for (int i = 0; i < R; i++) {
-                bad[i] = nbad[i];
-#pragma unroll
-                for (int n = 0; n < NCH; n++) {
-                    wg_[i][n] = ng_[i][n]; wu_[i][n] = nu_[i][n];
-                    sg_[i][n] = nsg[i][n]; su_[i][n] = nsu[i][n];
-                }
-            }
-        } else if (step + 1 < nsteps) {
-            load(rbase + step_rows, kn, on, wg_, wu_, sg_, su_, bad);
-        }
+        /* the next step's loads go out once this step's weights are consumed
+         * (a register double buffer measured no faster: the other resident
+         * workgroups keep the memory queues full) */
+        if (step + 1 < nsteps) load(rbase + step_rows, kn, on, wg_, wu_, sg_, su_, bad);
         kq = kn;
         oq = on;
     }
@@ -492,7 +481,7 @@ int rows_per_wg_for(int rows, int step, int wpc, size_t lds_per_row, size_t lds_
     return spw * step;
 }
 
-template <int NCH, int R, int PF>
+template <int NCH, int R>
 int launch_a(const Fp4Geom &g, float *h, const float *x,
              const Dsv4ExpertDev *table, int n_table, const int *idx,
              int topk, int hidden, int inter, float limit, int wpc,
@@ -504,7 +493,7 @@ int launch_a(const Fp4Geom &g, float *h, const float *x,
     const int rpw = rows_per_wg_for(hrows, g.rg * R, wpc, per_row, 32 * 1024);
     if (rpw <= 0) return -1;
     const int grid = (hrows + rpw - 1) / rpw;
-    hipLaunchKernelGGL((k_moe_gate_up<NCH, R, PF>), dim3(grid), dim3(g.wg),
+    hipLaunchKernelGGL((k_moe_gate_up<NCH, R>), dim3(grid), dim3(g.wg),
                        per_row * rpw, st, h, x, table, n_table, idx, topk, hidden,
                        inter, limit, g.tc, rpw);
     return 0;
@@ -538,25 +527,13 @@ int dsv4_moe_fp4_valu_launch(float *d_out, const float *d_x,
                  "(need multiples of 32, at most 16384, topk <= 64)", hidden, inter, topk);
         return -1;
     }
-    /* Launch shape (no effect on the arithmetic of a row): rows per thread,
-     * prefetch, workgroups per CU; defaults from a sweep at the C3 shape. */
-    const int ra = moe_env("DSV4_GPU_MOE_RA", 2) >= 2 ? 2 : 1;
-    const int pf = moe_env("DSV4_GPU_MOE_PF", 0) ? 1 : 0;
-    const int wa = moe_env("DSV4_GPU_MOE_WA", 2);
-    const int rbv = moe_env("DSV4_GPU_MOE_RB", 2);
-    const int rb = rbv >= 4 ? 4 : rbv >= 2 ? 2 : 1;
-    int rc;
-    if (ga.nch == 1) {
-        if (ra == 2) rc = pf ? launch_a<1, 2, 1>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st)
-                             : launch_a<1, 2, 0>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st);
-        else         rc = pf ? launch_a<1, 1, 1>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st)
-                             : launch_a<1, 1, 0>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st);
-    } else {
-        if (ra == 2) rc = pf ? launch_a<2, 2, 1>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st)
-                             : launch_a<2, 2, 0>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st);
-        else         rc = pf ? launch_a<2, 1, 1>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st)
-                             : launch_a<2, 1, 0>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st);
-    }
+    /* Launch shape (no effect on the arithmetic of a row), from a sweep at
+     * the C3 shape: two rows per thread, no prefetch, two workgroups per CU
+     * for the gate/up pass; two rows per thread for the row-group down pass. */
+    constexpr int wa = 2;
+    int rc = ga.nch == 1
+                 ? launch_a<1, 2>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st)
+                 : launch_a<2, 2>(ga, hbuf, d_x, d_table, n_table, d_idx, topk, hidden, inter, limit, wa, st);
     if (rc != 0) { DSV4_ERR("moe: gate/up shape does not fit"); return -1; }
     HIP_OK(hipGetLastError(), "moe gate/up launch");
     if (inter <= 4096 && moe_env("DSV4_GPU_MOE_DOWNW", 1)) {
@@ -576,13 +553,9 @@ int dsv4_moe_fp4_valu_launch(float *d_out, const float *d_x,
                                hidden, inter);
         rc = 0;
     } else if (gb.nch == 1) {
-        if (rb == 4) rc = launch_b<1, 4>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
-        else if (rb == 2) rc = launch_b<1, 2>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
-        else rc = launch_b<1, 1>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
+        rc = launch_b<1, 2>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
     } else {
-        if (rb == 4) rc = launch_b<2, 4>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
-        else if (rb == 2) rc = launch_b<2, 2>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
-        else rc = launch_b<2, 1>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
+        rc = launch_b<2, 2>(gb, d_out, hbuf, d_table, n_table, d_idx, d_w, topk, hidden, inter, st);
     }
     if (rc != 0) { DSV4_ERR("moe: down shape does not fit"); return -1; }
     HIP_OK(hipGetLastError(), "moe down launch");

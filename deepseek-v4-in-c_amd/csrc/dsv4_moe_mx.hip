@@ -828,68 +828,46 @@ int dsv4_moe_fp4_launch(float *d_out, const float *d_x,
         HIP_OK(hipGetLastError(), "moe split launch");
     }
     if (m2) {
-        /* The staged form (DSV4_GPU_MOE_MC=2): DSV4_GPU_MOE_D2 units in flight
-         * per wave. */
+        /* The staged form: two units in flight per wave (three or four
+         * measured slower at C3: more bytes in flight per CU only lengthen
+         * the memory queues). */
         static bool opted2 = false;
         if (!opted2) {
-            mc_lds_optin(k_mc2_gate_up<2, 14>); mc_lds_optin(k_mc2_gate_up<3, 14>);
-            mc_lds_optin(k_mc2_gate_up<3, 0>);
-            mc_lds_optin(k_mc2_down<3, 4>); mc_lds_optin(k_mc2_down<3, 0>);
-            mc_lds_optin(k_mc2_down<2, 4>); mc_lds_optin(k_mc2_down<4, 4>);
+            mc_lds_optin(k_mc2_gate_up<2, 14>); mc_lds_optin(k_mc2_gate_up<3, 0>);
+            mc_lds_optin(k_mc2_down<2, 4>); mc_lds_optin(k_mc2_down<3, 0>);
             opted2 = true;
         }
-        const int d2 = mc_env("DSV4_GPU_MOE_D2", 2);
         const size_t la = m2_lds_a(hidden), lb = m2_lds_b(topk, inter);
         const int nwb = m2_down_waves(topk);
         const dim3 ga(inter / 32, topk), gb(hidden / 32);
         const int nua = hidden / 512, nub = inter / 512;   /* units per row */
 #define M2_A(D, NU) hipLaunchKernelGGL((k_mc2_gate_up<D, NU>), ga, dim3(256), la, st, ht, d_x, d_table, n_table, d_idx, hidden, inter, limit)
 #define M2_B(D, NU) hipLaunchKernelGGL((k_mc2_down<D, NU>), gb, dim3(64 * nwb), lb, st, d_out, ht, d_table, n_table, d_idx, d_w, topk, hidden, inter)
-        if (nua == 14) {
-            if (d2 == 3) M2_A(3, 14); else M2_A(2, 14);
-        } else {
-            M2_A(3, 0);
-        }
+        if (nua == 14) M2_A(2, 14); else M2_A(3, 0);
         HIP_OK(hipGetLastError(), "moe gate/up launch");
-        if (nub == 4) {
-            if (d2 >= 4) M2_B(4, 4); else if (d2 == 3) M2_B(3, 4); else M2_B(2, 4);
-        } else {
-            M2_B(3, 0);
-        }
+        if (nub == 4) M2_B(2, 4); else M2_B(3, 0);
         HIP_OK(hipGetLastError(), "moe down launch");
 #undef M2_A
 #undef M2_B
         return 0;
     }
-    /* Row tiles per workgroup, waves per down workgroup and weight blocks in
-     * flight (none changes the arithmetic of a row). */
+    /* Fragment-order form: one row tile per gate/up workgroup with four
+     * weight blocks in flight; two row tiles per down workgroup of eight
+     * waves with eight blocks in flight (the best of a sweep; none changes
+     * the arithmetic of a row). */
     static bool opted = false;
     if (!opted) {
-        mc_lds_optin(k_mc_gate_up<1, 4>); mc_lds_optin(k_mc_gate_up<2, 4>);
-        mc_lds_optin(k_mc_gate_up<1, 8>); mc_lds_optin(k_mc_gate_up<2, 8>);
-        mc_lds_optin(k_mc_down<1, 8>); mc_lds_optin(k_mc_down<2, 8>);
-        mc_lds_optin(k_mc_down<1, 4>); mc_lds_optin(k_mc_down<2, 4>);
+        mc_lds_optin(k_mc_gate_up<1, 4>);
+        mc_lds_optin(k_mc_down<2, 8>);
         opted = true;
     }
-    const int ota = mc_env("DSV4_GPU_MOE_OTA", 1) >= 2 ? 2 : 1;
-    const int da = mc_env("DSV4_GPU_MOE_DA", 4) >= 8 ? 8 : 4;
     const size_t la = mc_lds_a(hidden);
-    const dim3 ga(inter / (16 * ota), topk);
-#define MC_A(OT, D) hipLaunchKernelGGL((k_mc_gate_up<OT, D>), ga, dim3(256), la, st, ht, xt, d_table, n_table, d_idx, hidden, inter, limit)
-    if (ota == 2) { if (da == 8) MC_A(2, 8); else MC_A(2, 4); }
-    else          { if (da == 8) MC_A(1, 8); else MC_A(1, 4); }
-#undef MC_A
+    hipLaunchKernelGGL((k_mc_gate_up<1, 4>), dim3(inter / 16, topk), dim3(256), la, st, ht, xt,
+                       d_table, n_table, d_idx, hidden, inter, limit);
     HIP_OK(hipGetLastError(), "moe gate/up launch");
-    const int otb = mc_env("DSV4_GPU_MOE_OTB", 2) >= 2 ? 2 : 1;
-    const int db = mc_env("DSV4_GPU_MOE_DB", 8) >= 8 ? 8 : 4;
-    const int wv = mc_env("DSV4_GPU_MOE_WAVES", 8);
-    const int nthr = 64 * (wv >= 8 ? 8 : wv >= 4 ? 4 : wv >= 2 ? 2 : 1);
     const size_t lb = mc_lds_b(topk, inter);
-    const dim3 gb(hidden / (16 * otb));
-#define MC_B(OT, D) hipLaunchKernelGGL((k_mc_down<OT, D>), gb, dim3(nthr), lb, st, d_out, ht, d_table, n_table, d_idx, d_w, topk, hidden, inter)
-    if (otb == 2) { if (db == 8) MC_B(2, 8); else MC_B(2, 4); }
-    else          { if (db == 8) MC_B(1, 8); else MC_B(1, 4); }
-#undef MC_B
+    hipLaunchKernelGGL((k_mc_down<2, 8>), dim3(hidden / 32), dim3(512), lb, st, d_out, ht,
+                       d_table, n_table, d_idx, d_w, topk, hidden, inter);
     HIP_OK(hipGetLastError(), "moe down launch");
     return 0;
 }

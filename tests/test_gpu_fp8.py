@@ -178,6 +178,22 @@ def test_batched_bit_identical(gpu, dsv4, rows, cols, nt):
     assert common.vec_rel_err(yn, oracle.matmul_fp8(x, W, Se)) < TOL
 
 
+@pytest.mark.parametrize("rows,cols", [(7168, 7168), (1536, 1536), (300, 4096), (260, 16384)])
+def test_launch_shape_keeps_bits(gpu, dsv4, monkeypatch, rows, cols):
+    """Rows per thread (DSV4_GPU_FP8_R), prefetch (DSV4_GPU_FP8_PF) and
+    workgroups per CU (DSV4_GPU_FP8_WPC) only reshape the launch: every
+    setting gives the default's bits."""
+    W, Sf, Se, x = common.fp8_problem(51, rows, cols)
+    y0, m = _run(dsv4, W, Sf, x, f32s=True)
+    assert common.vec_rel_err(y0, oracle.matmul_fp8(x, W, Sf)) < TOL
+    for r, pf, wpc in ((1, 0, 2), (4, 0, 2), (2, 1, 2), (2, 0, 1), (4, 1, 8), (1, 1, 4)):
+        monkeypatch.setenv("DSV4_GPU_FP8_R", str(r))
+        monkeypatch.setenv("DSV4_GPU_FP8_PF", str(pf))
+        monkeypatch.setenv("DSV4_GPU_FP8_WPC", str(wpc))
+        say("fp8 %dx%d R %d PF %d WPC %d" % (rows, cols, r, pf, wpc))
+        assert common.bits_equal(dsv4.mmq(m, x), y0), (r, pf, wpc)
+
+
 def test_row_range_views(gpu, dsv4):
     """The wo_a group slicing of attention() (dsv4_layer.c:321-334): every
     group is resident as a view and computes only its rows."""

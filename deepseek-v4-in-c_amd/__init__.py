@@ -46,6 +46,21 @@ class DSV4ExpertW(ctypes.Structure):
     _fields_ = [("w1", DSV4QMat), ("w3", DSV4QMat), ("w2", DSV4QMat)]
 
 
+class AttnCfg(ctypes.Structure):
+    """dsv4_gpu_attn_cfg (include/dsv4_gpu.h)."""
+    _fields_ = [(n, _ci) for n in ("hidden", "q_lora", "n_heads", "head_dim", "rope_dim",
+                                   "window", "ratio", "idx_heads", "idx_dim", "idx_topk",
+                                   "o_groups", "o_lora", "max_pos")] + [("rms_eps", _cf)]
+
+
+class AttnW(ctypes.Structure):
+    """dsv4_gpu_attn_w (include/dsv4_gpu.h)."""
+    _fields_ = [(n, DSV4QMat) for n in ("wq_a", "wq_b", "wkv", "wo_a", "wo_b", "comp_wkv",
+                                        "comp_wgate", "idx_wq_b", "idx_wproj")] + \
+               [(n, _vp) for n in ("q_norm", "kv_norm", "sink", "comp_norm", "comp_ape",
+                                   "rope_cos", "rope_sin")]
+
+
 def build():
     """Compile lib/libdsv4_gpu.so (hipcc, gfx950) and the CPU stub."""
     subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
@@ -54,6 +69,8 @@ def build():
 _lib = None
 _QP = ctypes.POINTER(DSV4QMat)
 _EP = ctypes.POINTER(DSV4ExpertW)
+_ACP = ctypes.POINTER(AttnCfg)
+_AWP = ctypes.POINTER(AttnW)
 
 _SIGS = {
     "dsv4_gpu_available": (_ci, []),
@@ -98,6 +115,11 @@ _SIGS = {
     "dsv4_gpu_mla_decode_d": (_ci, [_vp, _vp, _vp, _vp, _ci, _ci, _vp, _vp, _ci,
                                     _ci, _ci, _ci, _vp, _vp, _ci, _ci, _ci, _vp,
                                     _ci, _ci, _ci, _cf, _vp]),
+    "dsv4_gpu_attn_bind": (_ci, [_ci, _ACP, _AWP]),
+    "dsv4_gpu_attn_ready": (_ci, [_ci]),
+    "dsv4_gpu_attn_reset": (_ci, [_ci]),
+    "dsv4_gpu_attn_step": (_ci, [_vp, _vp, _ci, _ci]),
+    "dsv4_gpu_attn_step_d": (_ci, [_vp, _vp, _ci, _ci, _vp]),
 }
 
 SYMBOLS = tuple(_SIGS)

@@ -68,6 +68,8 @@ Scratch g_moe, g_attn, g_scores, g_index, g_amax;
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+void attn_blocks_free();
+
 int arena_reserve(size_t bytes)
 {
     if (bytes <= g_ar.cap) return 0;
@@ -239,21 +241,23 @@ int upload_bf16(const DSV4QMat *m)
 }
 
 /* y[rows] for rows [r0, r0 + rows) of a resident matrix, x and y device
- * pointers, on the library stream. */
-int res_gemv(const Res &r, int r0, int rows, float *d_y, const float *d_x)
+ * pointers, on stream st (the library stream by default). */
+int res_gemv(const Res &r, int r0, int rows, float *d_y, const float *d_x,
+             hipStream_t st = nullptr)
 {
+    if (!st) st = g_stream;
     if (r.wdt == DSV4_WBF16)
         return dsv4_bf16_gemv_launch(d_y, d_x,
                                      (const uint16_t *)(r.dw + (size_t)r0 * r.row_bytes()),
-                                     rows, r.cols, g_stream);
+                                     rows, r.cols, st);
     if (r.wdt == DSV4_WFP4)
         return dsv4_fp4_gemv_launch(d_y, d_x, r.dw + (size_t)r0 * r.row_bytes(),
                                     r.ds + (size_t)(r0 / r.blk_r) * r.sc, rows, r.cols,
-                                    r.blk_r, r.blk_c, g_stream);
+                                    r.blk_r, r.blk_c, st);
     const size_t ssz = r.sfmt ? 4 : 1;
     return dsv4_fp8_gemv_launch(d_y, d_x, r.dw + (size_t)r0 * r.cols,
                                 r.ds + (size_t)(r0 / r.blk_r) * r.sc * ssz, r.sfmt, rows,
-                                r.cols, r.blk_r, r.blk_c, g_stream);
+                                r.cols, r.blk_r, r.blk_c, st);
 }
 
 /* --------------------------------------------------------------- experts */
@@ -438,6 +442,7 @@ void dsv4_gpu_shutdown(void)
         if (L.dev) (void)hipFree(L.dev);
     }
     g_layers.clear();
+    attn_blocks_free();
     for (Scratch *s : {&g_moe, &g_attn, &g_scores, &g_index, &g_amax}) {
         if (s->p) (void)hipFree(s->p);
         s->p = nullptr;
@@ -955,6 +960,315 @@ int dsv4_gpu_mla_decode_d(float *d_o, int *d_idxs,
         return -1;
     return dsv4_attn_launch(d_o, d_q, d_kv, kv_fmt, kv_stride, kv_rows, d_sink,
                             d_idxs, h, d_qk, d_v, k, attn_scale, g_attn.p, st);
+}
+
+} /* extern "C" */
+
+/* ===================================================== attention blocks */
+namespace {
+
+/* A resident matrix (or a row range of one) as a block reads it. */
+struct MatRef {
+    Res r{};
+    int r0 = 0;
+};
+
+int mat_ref(const DSV4QMat *m, int rows, int cols, MatRef *out, const char *what)
+{
+    int r0 = 0;
+    const Res *r = m ? find_view(m, &r0) : nullptr;
+    if (!r || m->rows != rows || m->cols != cols) {
+        DSV4_ERR("attn_bind: %s (%dx%d) is not a resident %dx%d matrix", what,
+                 m ? m->rows : 0, m ? m->cols : 0, rows, cols);
+        return -1;
+    }
+    out->r = *r;
+    out->r0 = r0;
+    return 0;
+}
+
+/* One layer's attention on the device: its cfg, its resident matrices, and
+ * one device allocation holding the small weights, the RoPE table, the
+ * state (KV cache = window ring then compressed rows; the compressor's
+ * slots) and the step's buffers. */
+struct AttnBlock {
+    bool bound = false;
+    dsv4_gpu_attn_cfg c{};
+    MatRef wq_a, wq_b, wkv, wo_a, wo_b, cwkv, cwgate, iwq_b, iwproj;
+    char *mem = nullptr;
+    float *q_norm = nullptr, *kv_norm = nullptr, *sink = nullptr, *comp_norm = nullptr;
+    float *ape = nullptr, *cs = nullptr, *sn = nullptr;
+    float *kv_cache = nullptr, *comp_kv = nullptr, *comp_score = nullptr;
+    float *x = nullptr, *qr = nullptr, *q = nullptr, *kv = nullptr, *ckv = nullptr;
+    float *csc = nullptr, *pooled = nullptr, *idx_q = nullptr, *idx_w = nullptr;
+    float *scores = nullptr, *o = nullptr, *ogrp = nullptr, *out = nullptr;
+    int *idxs = nullptr;
+    void *iscr = nullptr, *ascr = nullptr;
+    int max_comp = 0, width = 0, nslot = 0, n_comp = 0, next_pos = 0;
+};
+std::vector<AttnBlock> g_blocks;
+
+void block_free(AttnBlock &b)
+{
+    if (b.mem) (void)hipFree(b.mem);
+    b = AttnBlock{};
+}
+
+/* Back to position 0: an empty ring, no compressed rows, score slots at
+ * -inf (dsv4_compress.c:75). */
+int block_reset(AttnBlock &b)
+{
+    HIP_OK(hipStreamSynchronize(g_stream), "attn reset sync");
+    const size_t kvb = (size_t)(b.c.window + b.max_comp) * b.c.head_dim * sizeof(float);
+    HIP_OK(hipMemset(b.kv_cache, 0, kvb), "attn reset");
+    if (b.nslot) {
+        const size_t n = (size_t)b.nslot * b.width;
+        std::vector<float> ninf(n, -INFINITY);
+        HIP_OK(hipMemset(b.comp_kv, 0, n * sizeof(float)), "attn reset");
+        HIP_OK(hipMemcpy(b.comp_score, ninf.data(), n * sizeof(float), hipMemcpyHostToDevice),
+               "attn reset");
+    }
+    b.n_comp = 0;
+    b.next_pos = 0;
+    return 0;
+}
+
+int block_bind(int layer, const dsv4_gpu_attn_cfg *cp, const dsv4_gpu_attn_w *w)
+{
+    if (!g_ready || !cp || !w || layer < 0 || layer >= 4096) return -1;
+    const dsv4_gpu_attn_cfg c = *cp;
+    const int H = c.n_heads, hd = c.head_dim, rd = c.rope_dim;
+    const bool comp = c.ratio > 0, idx = c.idx_heads > 0;
+    if (c.hidden <= 0 || c.q_lora <= 0 || H <= 0 || hd <= 0 || rd < 0 || rd > hd ||
+        (rd & 1) || c.window <= 0 || c.ratio < 0 || c.max_pos <= 0 || c.o_groups <= 0 ||
+        c.o_lora <= 0 || (H * hd) % c.o_groups ||
+        (idx && (!comp || c.idx_dim < rd || c.idx_dim > hd || c.idx_topk <= 0)) ||
+        !w->q_norm || !w->kv_norm || !w->rope_cos || !w->rope_sin ||
+        (comp && (!w->comp_norm || !w->comp_ape))) {
+        DSV4_ERR("attn_bind: layer %d: inconsistent configuration or missing vectors", layer);
+        return -1;
+    }
+    AttnBlock b;
+    b.c = c;
+    const int gw = H * hd / c.o_groups, coff = c.ratio == 4 ? 2 : 1;
+    if (mat_ref(&w->wq_a, c.q_lora, c.hidden, &b.wq_a, "wq_a") ||
+        mat_ref(&w->wq_b, H * hd, c.q_lora, &b.wq_b, "wq_b") ||
+        mat_ref(&w->wkv, hd, c.hidden, &b.wkv, "wkv") ||
+        mat_ref(&w->wo_a, c.o_groups * c.o_lora, gw, &b.wo_a, "wo_a") ||
+        mat_ref(&w->wo_b, c.hidden, c.o_groups * c.o_lora, &b.wo_b, "wo_b") ||
+        (comp && (mat_ref(&w->comp_wkv, coff * hd, c.hidden, &b.cwkv, "comp wkv") ||
+                  mat_ref(&w->comp_wgate, coff * hd, c.hidden, &b.cwgate, "comp wgate"))) ||
+        (idx && (mat_ref(&w->idx_wq_b, c.idx_heads * c.idx_dim, c.q_lora, &b.iwq_b, "idx wq_b") ||
+                 mat_ref(&w->idx_wproj, c.idx_heads, c.hidden, &b.iwproj, "idx weights_proj"))))
+        return -1;
+    if (b.wo_a.r.wdt != DSV4_WFP8) {
+        DSV4_ERR("attn_bind: wo_a must be FP8 (its group slices)");
+        return -1;
+    }
+    b.max_comp = comp ? c.max_pos / c.ratio + 1 : 0;
+    b.width = comp ? coff * hd : 0;
+    b.nslot = comp ? coff * c.ratio : 0;
+    const int half = rd / 2, rows = c.window + b.max_comp;
+    const size_t ascr = dsv4_attn_scratch_bytes(H, hd, hd, rows, DSV4_GPU_KV_F32);
+    if (!ascr) {
+        DSV4_ERR("attn_bind: head_dim %d not supported by the sparse attention", hd);
+        return -1;
+    }
+    const size_t F = sizeof(float);
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t o = off; off += align256(bytes ? bytes : 4); return o; };
+    const size_t o_qn = take(c.q_lora * F), o_kn = take(hd * F), o_sink = take(H * F);
+    const size_t o_cn = take(comp ? hd * F : 0), o_ape = take((size_t)c.ratio * b.width * F);
+    const size_t o_cs = take((size_t)c.max_pos * half * F), o_sn = take((size_t)c.max_pos * half * F);
+    const size_t o_kv = take((size_t)rows * hd * F);
+    const size_t o_ckv = take((size_t)b.nslot * b.width * F), o_csc = take((size_t)b.nslot * b.width * F);
+    const size_t o_x = take(c.hidden * F), o_qr = take(c.q_lora * F), o_q = take((size_t)H * hd * F);
+    const size_t o_k = take(hd * F), o_ki = take(b.width * F), o_si = take(b.width * F);
+    const size_t o_pl = take(hd * F), o_iq = take((size_t)c.idx_heads * c.idx_dim * F);
+    const size_t o_iw = take(c.idx_heads * F), o_sc = take((size_t)b.max_comp * F);
+    const size_t o_o = take((size_t)H * hd * F), o_og = take((size_t)c.o_groups * c.o_lora * F);
+    const size_t o_out = take(c.hidden * F), o_ix = take((size_t)rows * sizeof(int));
+    const size_t o_is = take(idx ? dsv4_index_scratch_bytes(b.max_comp) : 0);
+    const size_t o_as = take(ascr + 4);
+    if (off + (64u << 20) > dsv4_gpu_free_vram() ||
+        hipMalloc((void **)&b.mem, off) != hipSuccess) {
+        DSV4_ERR("attn_bind: layer %d: no room for %zu bytes", layer, off);
+        return -1;
+    }
+    char *m = b.mem;
+    b.q_norm = (float *)(m + o_qn); b.kv_norm = (float *)(m + o_kn); b.sink = (float *)(m + o_sink);
+    b.comp_norm = (float *)(m + o_cn); b.ape = (float *)(m + o_ape);
+    b.cs = (float *)(m + o_cs); b.sn = (float *)(m + o_sn);
+    b.kv_cache = (float *)(m + o_kv); b.comp_kv = (float *)(m + o_ckv); b.comp_score = (float *)(m + o_csc);
+    b.x = (float *)(m + o_x); b.qr = (float *)(m + o_qr); b.q = (float *)(m + o_q);
+    b.kv = (float *)(m + o_k); b.ckv = (float *)(m + o_ki); b.csc = (float *)(m + o_si);
+    b.pooled = (float *)(m + o_pl); b.idx_q = (float *)(m + o_iq); b.idx_w = (float *)(m + o_iw);
+    b.scores = (float *)(m + o_sc); b.o = (float *)(m + o_o); b.ogrp = (float *)(m + o_og);
+    b.out = (float *)(m + o_out); b.idxs = (int *)(m + o_ix);
+    b.iscr = m + o_is; b.ascr = m + o_as;
+    bool ok = hipMemcpy(b.q_norm, w->q_norm, c.q_lora * F, hipMemcpyHostToDevice) == hipSuccess &&
+              hipMemcpy(b.kv_norm, w->kv_norm, hd * F, hipMemcpyHostToDevice) == hipSuccess &&
+              hipMemcpy(b.cs, w->rope_cos, (size_t)c.max_pos * half * F, hipMemcpyHostToDevice) == hipSuccess &&
+              hipMemcpy(b.sn, w->rope_sin, (size_t)c.max_pos * half * F, hipMemcpyHostToDevice) == hipSuccess;
+    if (ok && w->sink)
+        ok = hipMemcpy(b.sink, w->sink, H * F, hipMemcpyHostToDevice) == hipSuccess;
+    if (ok && comp)
+        ok = hipMemcpy(b.comp_norm, w->comp_norm, hd * F, hipMemcpyHostToDevice) == hipSuccess &&
+             hipMemcpy(b.ape, w->comp_ape, (size_t)c.ratio * b.width * F, hipMemcpyHostToDevice) == hipSuccess;
+    if (!w->sink) b.sink = nullptr;
+    if (!ok || block_reset(b) != 0) {
+        DSV4_ERR("attn_bind: layer %d: copying the vectors failed", layer);
+        block_free(b);
+        return -1;
+    }
+    b.bound = true;
+    if ((int)g_blocks.size() <= layer) g_blocks.resize(layer + 1);
+    block_free(g_blocks[layer]);
+    g_blocks[layer] = b;
+    return 0;
+}
+
+/* attention() of dsv4_layer.c:213-336 for the token at pos, on stream st;
+ * x and out are device buffers of hidden floats. */
+int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_t st)
+{
+    const dsv4_gpu_attn_cfg &c = b.c;
+    const int H = c.n_heads, hd = c.head_dim, rd = c.rope_dim, half = rd / 2;
+    if (pos != b.next_pos || pos >= c.max_pos) {
+        DSV4_ERR("attn_step: position %d out of order (next %d, max %d); "
+                 "dsv4_gpu_attn_reset starts over", pos, b.next_pos, c.max_pos);
+        return -1;
+    }
+#define OK(e) do { if ((e) != 0) return -1; } while (0)
+    /* q: wq_a, the learned norm, wq_b, then each head's norm and RoPE */
+    OK(res_gemv(b.wq_a.r, b.wq_a.r0, c.q_lora, b.qr, d_x, st));
+    OK(dsv4_norm_rope_launch(b.qr, 0, b.qr, 0, b.q_norm, 1, c.q_lora, 1, c.rms_eps, 0,
+                             nullptr, nullptr, 0, 0, 0, st));
+    OK(res_gemv(b.wq_b.r, b.wq_b.r0, H * hd, b.q, b.qr, st));
+    OK(dsv4_norm_rope_launch(b.q, hd, b.q, hd, nullptr, H, hd, 1, c.rms_eps, rd, b.cs, b.sn,
+                             pos, half, 0, st));
+    /* kv: wkv, kv_norm, RoPE, into the ring slot */
+    OK(res_gemv(b.wkv.r, b.wkv.r0, hd, b.kv, d_x, st));
+    OK(dsv4_norm_rope_launch(b.kv_cache + (size_t)(pos % c.window) * hd, 0, b.kv, 0, b.kv_norm,
+                             1, hd, 1, c.rms_eps, rd, b.cs, b.sn, pos, half, 0, st));
+    const int n_win = pos + 1 < c.window ? pos + 1 : c.window;
+    int take = 0, mode = 1;
+    if (c.ratio > 0) {
+        /* the compressor (dsv4_layer.c:243-261) */
+        const int ph = pos % c.ratio, slot = c.ratio == 4 ? c.ratio + ph : ph;
+        OK(res_gemv(b.cwkv.r, b.cwkv.r0, b.width, b.ckv, d_x, st));
+        OK(res_gemv(b.cwgate.r, b.cwgate.r0, b.width, b.csc, d_x, st));
+        OK(dsv4_comp_update_launch(b.comp_kv + (size_t)slot * b.width,
+                                   b.comp_score + (size_t)slot * b.width, b.ckv, b.csc,
+                                   b.ape + (size_t)ph * b.width, b.width, st));
+        if ((pos + 1) % c.ratio == 0) {
+            if (b.n_comp >= b.max_comp) {
+                DSV4_ERR("attn_step: compressed rows exceed max_pos / ratio + 1");
+                return -1;
+            }
+            OK(dsv4_comp_pool_launch(b.pooled, b.comp_kv, b.comp_score, c.ratio, hd, st));
+            OK(dsv4_norm_rope_launch(b.kv_cache + (size_t)(c.window + b.n_comp) * hd, 0,
+                                     b.pooled, 0, b.comp_norm, 1, hd, 1, c.rms_eps, rd, b.cs,
+                                     b.sn, pos + 1 - c.ratio, half, 0, st));
+            b.n_comp++;
+        }
+        /* which compressed rows attention sees (dsv4_layer.c:267-297) */
+        const int avail = b.n_comp;
+        if (avail > 0 && c.idx_heads > 0) {
+            const int ih = c.idx_heads, idd = c.idx_dim;
+            OK(res_gemv(b.iwq_b.r, b.iwq_b.r0, ih * idd, b.idx_q, b.qr, st));
+            OK(dsv4_norm_rope_launch(b.idx_q, idd, b.idx_q, idd, nullptr, ih, idd, 0, 0.0f, rd,
+                                     b.cs, b.sn, pos, half, 0, st));
+            OK(res_gemv(b.iwproj.r, b.iwproj.r0, ih, b.idx_w, d_x, st));
+            take = avail < c.idx_topk ? avail : c.idx_topk;
+            const int hist = dsv4_topk_takes_hist(avail, take);
+            /* the keys are the compressed region read at index_head_dim
+             * stride, as the reference's call does (dsv4_layer.c:286-289) */
+            OK(dsv4_indexer_score_launch(b.scores, b.idx_q, b.idx_w, ih, idd,
+                                         b.kv_cache + (size_t)c.window * hd, nullptr,
+                                         DSV4_GPU_KV_F32, idd, avail, indexer_scale(idd, ih),
+                                         b.iscr, hist, st));
+            OK(dsv4_topk_launch(b.idxs + n_win, b.scores, avail, take, b.iscr, hist, st));
+            mode = 2;
+        } else {
+            take = avail;
+        }
+    }
+    OK(dsv4_attn_idxs_launch(b.idxs, pos, c.window, n_win, take, mode, c.window, st));
+    OK(dsv4_attn_launch(b.o, b.q, b.kv_cache, DSV4_GPU_KV_F32, hd, c.window + b.max_comp,
+                        b.sink, b.idxs, H, hd, hd, n_win + take, 1.0f / sqrtf((float)hd),
+                        b.ascr, st));
+    /* de-rotate, then wo_a per group (the FP8 slices of dsv4_layer.c:321-334:
+     * group g's rows from g * o_lora, its scale rows from g * (o_lora /
+     * blk_r)) and wo_b */
+    OK(dsv4_norm_rope_launch(b.o, hd, b.o, hd, nullptr, H, hd, 0, 0.0f, rd, b.cs, b.sn, pos,
+                             half, 1, st));
+    const Res &wa = b.wo_a.r;
+    const int gw = H * hd / c.o_groups, gr = c.o_lora;
+    const size_t ssz = wa.sfmt ? 4 : 1;
+    for (int g = 0; g < c.o_groups; g++) {
+        const uint8_t *W = wa.dw + (size_t)(b.wo_a.r0 + g * gr) * wa.cols;
+        const uint8_t *S = wa.ds + ((size_t)(b.wo_a.r0 / wa.blk_r) + (size_t)g * (gr / wa.blk_r)) *
+                                       wa.sc * ssz;
+        OK(dsv4_fp8_gemv_launch(b.ogrp + (size_t)g * gr, b.o + (size_t)g * gw, W, S, wa.sfmt,
+                                gr, gw, wa.blk_r, wa.blk_c, st));
+    }
+    OK(res_gemv(b.wo_b.r, b.wo_b.r0, c.hidden, d_out, b.ogrp, st));
+#undef OK
+    b.next_pos = pos + 1;
+    return 0;
+}
+
+AttnBlock *block_of(int layer)
+{
+    if (!g_ready || layer < 0 || layer >= (int)g_blocks.size() || !g_blocks[layer].bound)
+        return nullptr;
+    return &g_blocks[layer];
+}
+
+void attn_blocks_free()
+{
+    for (AttnBlock &b : g_blocks) block_free(b);
+    g_blocks.clear();
+}
+
+} // namespace
+
+extern "C" {
+
+int dsv4_gpu_attn_bind(int layer, const dsv4_gpu_attn_cfg *c, const dsv4_gpu_attn_w *w)
+{
+    return block_bind(layer, c, w);
+}
+
+int dsv4_gpu_attn_ready(int layer) { return block_of(layer) ? 1 : 0; }
+
+int dsv4_gpu_attn_reset(int layer)
+{
+    AttnBlock *b = block_of(layer);
+    return b ? block_reset(*b) : -1;
+}
+
+int dsv4_gpu_attn_step(float *out, const float *x, int layer, int pos)
+{
+    AttnBlock *b = block_of(layer);
+    if (!b || !out || !x) return -1;
+    const size_t bytes = (size_t)b->c.hidden * sizeof(float);
+    HIP_OK(hipMemcpyAsync(b->x, x, bytes, hipMemcpyHostToDevice, g_stream), "attn x");
+    if (block_step(*b, b->out, b->x, pos, g_stream) != 0) {
+        (void)hipStreamSynchronize(g_stream);
+        return -1;
+    }
+    HIP_OK(hipMemcpyAsync(out, b->out, bytes, hipMemcpyDeviceToHost, g_stream), "attn out");
+    HIP_OK(hipStreamSynchronize(g_stream), "attn sync");
+    return 0;
+}
+
+int dsv4_gpu_attn_step_d(float *d_out, const float *d_x, int layer, int pos, void *stream)
+{
+    AttnBlock *b = block_of(layer);
+    if (!b || !d_out || !d_x) return -1;
+    return block_step(*b, d_out, d_x, pos, as_stream(stream));
 }
 
 } /* extern "C" */

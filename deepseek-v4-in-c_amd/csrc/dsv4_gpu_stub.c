@@ -134,3 +134,11 @@ int dsv4_gpu_mla_decode_d(float *d_o, int *d_idxs,
   (void)k; (void)d_q; (void)d_kv; (void)kv_fmt; (void)kv_stride;
   (void)kv_rows; (void)d_sink; (void)h; (void)d_qk; (void)d_v;
   (void)attn_scale; (void)stream; return -1; }
+int dsv4_gpu_attn_bind(int layer, const dsv4_gpu_attn_cfg *c, const dsv4_gpu_attn_w *w)
+{ (void)layer; (void)c; (void)w; return -1; }
+int dsv4_gpu_attn_ready(int layer) { (void)layer; return 0; }
+int dsv4_gpu_attn_reset(int layer) { (void)layer; return -1; }
+int dsv4_gpu_attn_step(float *out, const float *x, int layer, int pos)
+{ (void)out; (void)x; (void)layer; (void)pos; return -1; }
+int dsv4_gpu_attn_step_d(float *d_out, const float *d_x, int layer, int pos, void *stream)
+{ (void)d_out; (void)d_x; (void)layer; (void)pos; (void)stream; return -1; }

@@ -115,3 +115,29 @@ int dsv4_attn_launch(float *d_o, const float *d_q, const void *d_kv,
                      const float *d_sink, const int *d_idxs, int h, int d_qk,
                      int d_v, int topk, float scale, void *scratch,
                      hipStream_t st);
+
+/* ---- the attention block's element-wise steps (dsv4_attnblk.hip) ------ */
+
+/* nvec vectors of n floats (src at src_stride, dst at dst_stride, dst may
+ * alias src): scaled by 1/sqrt(mean square + eps) when norm, times w[n] when
+ * w is given, then the last rd elements RoPE'd at table row pos (half floats
+ * per row of cs / sn; inverse negates the sine). */
+int dsv4_norm_rope_launch(float *dst, int dst_stride, const float *src, int src_stride,
+                          const float *w, int nvec, int n, int norm, float eps, int rd,
+                          const float *cs, const float *sn, int pos, int half, int inverse,
+                          hipStream_t st);
+
+/* The compressor: the token's state rows (kv_row = kv_in, score_row =
+ * score_in + ape_row over width floats), and the pool of a closing window
+ * into out[hd] (with the ratio-4 slide). */
+int dsv4_comp_update_launch(float *kv_row, float *score_row, const float *kv_in,
+                            const float *score_in, const float *ape_row, int width,
+                            hipStream_t st);
+int dsv4_comp_pool_launch(float *out, float *kv_state, float *score_state, int ratio,
+                          int hd, hipStream_t st);
+
+/* The sparse attention's row list: n_win ring slots, then take compressed
+ * rows (mode 1: all, offset + j; mode 2: the selection already in place,
+ * offset where >= 0). */
+int dsv4_attn_idxs_launch(int *idxs, int pos, int win, int n_win, int take, int mode,
+                          int offset, hipStream_t st);

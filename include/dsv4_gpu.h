@@ -302,6 +302,63 @@ int dsv4_gpu_mla_decode_d(float *d_o, int *d_idxs,
                           int h, int d_qk, int d_v, float attn_scale,
                           void *stream);
 
+/* ------------------------------------------------- the attention block ---
+ * attention() of the reference (src/model/dsv4_layer.c:213-336) for one
+ * token, entirely on the device: q (wq_a, q_norm, wq_b, the per-head norm
+ * and RoPE), kv (wkv, kv_norm, RoPE, into the sliding ring), the compressor
+ * (comp wkv / wgate, the slot update and, when a window closes, the pool,
+ * comp norm and RoPE at the window's first position into the next
+ * compressed row), the CSA selection (indexer wq_b, RoPE, weights_proj,
+ * score over the compressed rows at index_head_dim stride, top-k) or all
+ * compressed rows, the sparse attention over [ring | selection] with the
+ * sinks, the output de-rotation, the wo_a group slices and wo_b. The
+ * reference crosses the host-device boundary once per matmul here (about
+ * nine times per layer); this is one call. No counterpart in the
+ * reference's GPU header: the caller's binding is one test at the top of
+ * attention().
+ *
+ * The block keeps the layer's state (the ring, the compressed rows, the
+ * compressor's slots) on the device. Positions must come in order from 0,
+ * as the reference's decode does; dsv4_gpu_attn_reset starts over. Within
+ * 1e-5-scale relative error of the reference per step (its GEMVs accumulate
+ * in fp32 where the reference uses double); the selection is the
+ * reference's wherever the scores it ranks agree. */
+typedef struct {
+    int hidden, q_lora, n_heads, head_dim, rope_dim;   /* DSV4Cfg (qk_rope)  */
+    int window;                /* sliding_window                            */
+    int ratio;                 /* the layer's compress ratio (0: none)      */
+    int idx_heads, idx_dim, idx_topk;  /* the indexer; idx_heads 0 if none  */
+    int o_groups, o_lora;
+    int max_pos;               /* positions 0 .. max_pos-1                  */
+    float rms_eps;
+} dsv4_gpu_attn_cfg;
+
+typedef struct {
+    DSV4QMat wq_a, wq_b, wkv, wo_a, wo_b;     /* resident (dsv4_gpu_upload);
+                                                wo_a FP8                   */
+    DSV4QMat comp_wkv, comp_wgate;            /* ratio > 0, resident        */
+    DSV4QMat idx_wq_b, idx_wproj;             /* idx_heads > 0, resident    */
+    const float *q_norm, *kv_norm;            /* [q_lora], [head_dim]       */
+    const float *sink;                        /* [n_heads], or NULL         */
+    const float *comp_norm, *comp_ape;        /* [head_dim],
+                                                [ratio][coff*head_dim]     */
+    const float *rope_cos, *rope_sin;         /* the layer's RoPE table,
+                                                [max_pos][rope_dim/2]      */
+} dsv4_gpu_attn_w;
+
+/* Copies the vectors and the RoPE table, resolves the matrices (which must
+ * be resident already) and allocates the layer's state; rebinding a layer
+ * replaces it. 0 / -1. */
+int dsv4_gpu_attn_bind(int layer, const dsv4_gpu_attn_cfg *c, const dsv4_gpu_attn_w *w);
+/* 1 if the layer is bound. */
+int dsv4_gpu_attn_ready(int layer);
+/* The layer's state back to position 0. 0 / -1. */
+int dsv4_gpu_attn_reset(int layer);
+/* out[hidden] = attention(x[hidden]) at pos; host buffers, synchronous. */
+int dsv4_gpu_attn_step(float *out, const float *x, int layer, int pos);
+/* The same on device buffers, stream-ordered. */
+int dsv4_gpu_attn_step_d(float *d_out, const float *d_x, int layer, int pos, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,7 +10,7 @@ Two CPU implementations are exposed through ctypes:
 * ``liboracle.so`` -- this directory's C restatement (``dsv4_oracle.c``) of
   the reference functions, each citing the reference file:line it follows.
 * ``_ref/libdsv4ref.so`` -- the reference's own sources
-  (``src/core/dsv4_{matmul,indexer,attn,ops}.c``) compiled as they lie by
+  (``src/core/dsv4_{matmul,indexer,attn,ops,rope,compress}.c``) compiled as they lie by
   ``oracle/Makefile``. Present wherever it was built; used to pin the
   restatement bit for bit and as the ``cpu_baseline`` of ``bench.py``.
 
@@ -89,6 +89,16 @@ def lib():
         L.orc_sparse_attn.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int, _f32p,
                                       _i32p, ctypes.c_int, ctypes.c_int,
                                       ctypes.c_int, ctypes.c_int, ctypes.c_float]
+        L.orc_rmsnorm.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_float]
+        L.orc_rope_apply.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, _f32p, _f32p,
+                                     ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.orc_head_norm_rope.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_float, _f32p, _f32p, ctypes.c_int]
+        L.orc_compress_step.restype = ctypes.c_int
+        L.orc_compress_step.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.orc_compress_rope_pos.restype = ctypes.c_int
+        L.orc_compress_rope_pos.argtypes = [ctypes.c_int, ctypes.c_int]
         _orc = L
     return _orc
 
@@ -119,6 +129,17 @@ def ref():
         L.dsv4_sparse_attn.argtypes = [_f32p, _f32p, _f32p, _f32p, _i32p,
                                        ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                        ctypes.c_float, _f32p]
+        L.dsv4_rmsnorm.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_float]
+        L.dsv4_rope_apply.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, _f32p, _f32p,
+                                      ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.dsv4_rope_table.argtypes = [_f32p, _f32p, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_double, ctypes.c_double,
+                                      ctypes.c_double, ctypes.c_double]
+        L.dsv4_compress_step.restype = ctypes.c_int
+        L.dsv4_compress_step.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                         ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.dsv4_compress_rope_pos.restype = ctypes.c_int
+        L.dsv4_compress_rope_pos.argtypes = [ctypes.c_int, ctypes.c_int]
         _ref = L
     return _ref
 
@@ -276,7 +297,95 @@ def indexer_offset(idxs, offset):
     return idxs
 
 
+# ------------------------------------------------------------ attention block
+def rmsnorm(x, w, eps):
+    x = _f32(x); w = _f32(w)
+    y = np.empty_like(x)
+    lib().orc_rmsnorm(_p(y, _f32p), _p(x, _f32p), _p(w, _f32p), x.size, float(eps))
+    return y
+
+
+def rope_apply(v, rd, cs, sn, pos, inverse=False):
+    """v [..., head_dim]: every vector's last rd elements rotated (a copy)."""
+    v = np.array(v, dtype=np.float32, order="C")
+    cs = _f32(cs); sn = _f32(sn)
+    hd = v.shape[-1]
+    flat = v.reshape(-1, hd)
+    for r in flat:
+        lib().orc_rope_apply(_p(r, _f32p), hd, rd, _p(cs, _f32p), _p(sn, _f32p),
+                             pos, rd // 2, int(inverse))
+    return flat.reshape(v.shape)
+
+
+def head_norm_rope(q, rd, eps, cs, sn, pos):
+    """q [H][hd]: the per-head norm and RoPE of attention() (a copy)."""
+    q = np.array(q, dtype=np.float32, order="C")
+    cs = _f32(cs); sn = _f32(sn)
+    H, hd = q.shape
+    lib().orc_head_norm_rope(_p(q, _f32p), H, hd, rd, float(eps), _p(cs, _f32p),
+                             _p(sn, _f32p), pos)
+    return q
+
+
+class Compressor:
+    """dsv4_compress_step's state for one layer (score state starts at -inf)."""
+
+    def __init__(self, ratio, hd, ape, fn=None):
+        ov = ratio == 4
+        self.ratio, self.hd, self.width = ratio, hd, (1 + ov) * hd
+        self.nslot = (1 + ov) * ratio
+        self.ape = _f32(ape)
+        self.kv = np.zeros((self.nslot, self.width), np.float32)
+        self.sc = np.full((self.nslot, self.width), -np.inf, np.float32)
+        self.fn = fn
+
+    def step(self, kv_in, score_in, pos):
+        kv_in = _f32(kv_in); score_in = _f32(score_in)
+        out = np.zeros(self.hd, np.float32)
+        f = self.fn or lib().orc_compress_step
+        r = f(_p(out, _f32p), _p(kv_in, _f32p), _p(score_in, _f32p), _p(self.ape, _f32p),
+              _p(self.kv, _f32p), _p(self.sc, _f32p), pos, self.ratio, self.hd)
+        return out if r == 1 else None
+
+
+def compress_rope_pos(pos, ratio):
+    return lib().orc_compress_rope_pos(pos, ratio)
+
+
 # ------------------------------------------------- the compiled reference
+def ref_rmsnorm(x, w, eps):
+    x = _f32(x); w = _f32(w)
+    y = np.empty_like(x)
+    ref().dsv4_rmsnorm(_p(y, _f32p), _p(x, _f32p), _p(w, _f32p), x.size, float(eps))
+    return y
+
+
+def ref_rope_apply(v, rd, cs, sn, pos, inverse=False):
+    v = np.array(v, dtype=np.float32, order="C")
+    cs = _f32(cs); sn = _f32(sn)
+    hd = v.shape[-1]
+    flat = v.reshape(-1, hd)
+    for r in flat:
+        ref().dsv4_rope_apply(_p(r, _f32p), hd, rd, _p(cs, _f32p), _p(sn, _f32p),
+                              pos, rd // 2, int(inverse))
+    return flat.reshape(v.shape)
+
+
+def ref_rope_table(rd, maxpos, orig_ctx, theta, factor=16.0, beta_fast=32.0,
+                   beta_slow=1.0):
+    """The reference's dsv4_rope_table: cos and sin [maxpos][rd/2]."""
+    cs = np.empty((maxpos, rd // 2), np.float32)
+    sn = np.empty((maxpos, rd // 2), np.float32)
+    ref().dsv4_rope_table(_p(cs, _f32p), _p(sn, _f32p), rd, maxpos, orig_ctx,
+                          float(theta), float(factor), float(beta_fast), float(beta_slow))
+    return cs, sn
+
+
+def ref_compressor(ratio, hd, ape):
+    return Compressor(ratio, hd, ape, fn=ref().dsv4_compress_step)
+
+
+
 def ref_matmul_fp8(x, W, S_e8m0, blk_r=128, blk_c=128, scalar=False):
     W = _u8(W); x = _f32(x); S = _u8(S_e8m0)
     out, inn = W.shape

@@ -422,3 +422,115 @@ void orc_embed_row(float *dst, const void *table, int wdt, long long row, int hi
         for (int i = 0; i < hidden; i++) dst[i] = p[i];
     }
 }
+
+/* ------------------------------------------------------ attention block ---
+ * The pieces of attention() (dsv4_layer.c:213-336) around the CSA calls:
+ * RMSNorm, the per-head norm of q, RoPE and the KV compressor. */
+
+/* dsv4_rmsnorm, dsv4_ops.c:24-31: the sum of squares in double, eps added to
+ * the MEAN, y = w * (x * inv) with inv rounded to float. y may alias x. */
+void orc_rmsnorm(float *y, const float *x, const float *w, int n, float eps)
+{
+    double sq = 0.0;
+    for (int i = 0; i < n; i++) sq += (double)x[i] * (double)x[i];
+    const float inv = (float)(1.0 / sqrt(sq / (double)n + (double)eps));
+    for (int i = 0; i < n; i++) y[i] = w[i] * (x[i] * inv);
+}
+
+/* dsv4_rope_apply, dsv4_rope.c:105-119: the last rd elements of v rotated as
+ * interleaved pairs (v[2i], v[2i+1]) by the table row at pos; inverse
+ * negates the sine (the output de-rotation). */
+void orc_rope_apply(float *v, int head_dim, int rd, const float *cs, const float *sn,
+                    int pos, int table_half, int inverse)
+{
+    float *t = v + (head_dim - rd);
+    for (int i = 0; i < rd / 2; i++) {
+        const float c = cs[(size_t)pos * table_half + i];
+        const float s0 = sn[(size_t)pos * table_half + i];
+        const float s = inverse ? -s0 : s0;
+        const float re = t[2 * i], im = t[2 * i + 1];
+        t[2 * i] = re * c - im * s;
+        t[2 * i + 1] = re * s + im * c;
+    }
+}
+
+/* The per-head step of attention() on q (dsv4_layer.c:223-231): each head
+ * scaled by 1/sqrt(mean square + eps) with no weight, then RoPE at pos. */
+void orc_head_norm_rope(float *q, int H, int hd, int rd, float eps, const float *cs,
+                        const float *sn, int pos)
+{
+    for (int h = 0; h < H; h++) {
+        float *qh = q + (size_t)h * hd;
+        double sq = 0.0;
+        for (int i = 0; i < hd; i++) sq += (double)qh[i] * qh[i];
+        const float inv = (float)(1.0 / sqrt(sq / (double)hd + (double)eps));
+        for (int i = 0; i < hd; i++) qh[i] *= inv;
+        orc_rope_apply(qh, hd, rd, cs, sn, pos, rd / 2, 0);
+    }
+}
+
+/* One channel of the compressor's pool (dsv4_compress.c:45-63): a softmax
+ * over the slots (max in float, -inf slots skipped), sums in double. */
+static float pool_one(const float *kv, const float *sc, int slots, int kv_stride,
+                      int sc_stride, int c)
+{
+    float mx = -INFINITY;
+    for (int s = 0; s < slots; s++) {
+        const float v = sc[(size_t)s * sc_stride + c];
+        if (v > mx) mx = v;
+    }
+    if (mx == -INFINITY) return 0.0f;
+    double den = 0.0, acc = 0.0;
+    for (int s = 0; s < slots; s++) {
+        const float v = sc[(size_t)s * sc_stride + c];
+        if (v == -INFINITY) continue;
+        const double e = (double)expf(v - mx);
+        den += e;
+        acc += e * (double)kv[(size_t)s * kv_stride + c];
+    }
+    return (float)(acc / den);
+}
+
+/* dsv4_compress_step, dsv4_compress.c:77-137 (the decode path). The token
+ * goes into slot pos % ratio (ratio + pos % ratio when ratio == 4, whose
+ * first `ratio` slots hold the previous window) with score + ape[pos %
+ * ratio]; when the window closes, out[hd] is the per-channel pool -- over
+ * `ratio` slots of width hd, or for ratio 4 over the previous window's first
+ * halves then the current window's second halves -- and the ratio-4 state
+ * slides down by one window. Returns 1 when out was written. score_state
+ * starts at -inf. */
+int orc_compress_step(float *out, const float *kv_in, const float *score_in,
+                      const float *ape, float *kv_state, float *score_state, int pos,
+                      int ratio, int hd)
+{
+    const int ov = ratio == 4, width = (1 + ov) * hd, ph = pos % ratio;
+    const int slot = ov ? ratio + ph : ph;
+    for (int c = 0; c < width; c++) {
+        kv_state[(size_t)slot * width + c] = kv_in[c];
+        score_state[(size_t)slot * width + c] = score_in[c] + ape[(size_t)ph * width + c];
+    }
+    if ((pos + 1) % ratio != 0) return 0;
+    if (!ov) {
+        for (int c = 0; c < hd; c++)
+            out[c] = pool_one(kv_state, score_state, ratio, width, width, c);
+        return 1;
+    }
+    float *gk = malloc(sizeof(float) * 2 * ratio * hd);
+    float *gs = malloc(sizeof(float) * 2 * ratio * hd);
+    if (!gk || !gs) { free(gk); free(gs); return -1; }
+    for (int s = 0; s < 2 * ratio; s++) {
+        const size_t src = (size_t)s * width + (s < ratio ? 0 : hd);
+        memcpy(gk + (size_t)s * hd, kv_state + src, sizeof(float) * hd);
+        memcpy(gs + (size_t)s * hd, score_state + src, sizeof(float) * hd);
+    }
+    for (int c = 0; c < hd; c++) out[c] = pool_one(gk, gs, 2 * ratio, hd, hd, c);
+    free(gk);
+    free(gs);
+    memmove(kv_state, kv_state + (size_t)ratio * width, sizeof(float) * ratio * width);
+    memmove(score_state, score_state + (size_t)ratio * width, sizeof(float) * ratio * width);
+    return 1;
+}
+
+/* dsv4_compress_rope_pos, dsv4_compress.c:141: a compressed row is stamped
+ * with the first position of the window it summarises. */
+int orc_compress_rope_pos(int pos, int ratio) { return pos + 1 - ratio; }

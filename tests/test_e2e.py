@@ -23,3 +23,21 @@ def test_reference_decode_runs_and_is_deterministic(tmp_path):
     assert len(rows) == 46 and all(r["rel"] == 0.0 for r in rows)
     # the tokens really move the model: not one argmax everywhere
     assert len({r["ref"] for r in rows}) > 10
+
+
+def test_attention_driver_reference_pass(tmp_path):
+    """oracle/_ref/dsv4_attn's first pass -- the reference's own attention()
+    on every layer of the tiny checkpoint, called through the #included
+    dsv4_layer.c -- runs to the end on the CPU (exit 2: no device for the
+    second pass here; 0 where a device is present)."""
+    import os
+    import subprocess
+    import tiny_checkpoint
+    exe = os.path.join(e2e_common.ROOT, "oracle", "_ref", "dsv4_attn")
+    if not os.path.exists(exe):
+        pytest.skip("oracle/_ref/dsv4_attn not built")
+    tiny_checkpoint.write(str(tmp_path))
+    p = subprocess.run([exe, str(tmp_path), "12"], capture_output=True, text=True,
+                       timeout=120)
+    assert p.returncode in (0, 2), p.stdout[-2000:] + p.stderr[-2000:]
+    assert "attention: 1 dense + 2 indexed(top3) + 1 compressed(1:8)" in p.stdout + p.stderr

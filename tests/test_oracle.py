@@ -371,3 +371,144 @@ def test_attention_bit_equal_to_compiled_reference():
     idx = rng.integers(-1, n, size=topk).astype(np.int32)
     a = oracle.sparse_attn(q, kv, sink, idx, 0.125)
     assert common.bits_equal(a, oracle.ref_sparse_attn(q, kv, sink, idx, 0.125))
+
+
+# ------------------------------------------------------- attention block
+def _tables(rd=16, maxpos=64, yarn=False):
+    """A RoPE table as the reference builds it (dense theta 1e4, or the
+    compressed layers' 1.6e5 with YaRN); numpy double math when the compiled
+    reference is absent."""
+    if oracle.ref_available():
+        return oracle.ref_rope_table(rd, maxpos, 65536 if yarn else 0,
+                                     160000.0 if yarn else 10000.0)
+    i = np.arange(rd // 2)
+    f = 1.0 / (10000.0 ** (2 * i / rd))
+    th = np.arange(maxpos)[:, None] * f[None, :]
+    return np.cos(th).astype(np.float32), np.sin(th).astype(np.float32)
+
+
+def test_rmsnorm_closed_forms():
+    """A constant vector: inv = 1/sqrt(c^2 + eps); eps on the MEAN (not the
+    sum): with n = 4096 the two readings differ; the weight multiplies after
+    the scale."""
+    n, c, eps = 4096, 0.5, 1e-2
+    w = np.linspace(0.5, 1.5, n).astype(np.float32)
+    y = oracle.rmsnorm(np.full(n, c, np.float32), w, eps)
+    inv = np.float32(1.0 / math.sqrt(c * c + eps))
+    assert common.bits_equal(y, w * (np.float32(c) * inv))
+    wrong = np.float32(1.0 / math.sqrt(c * c + eps / n))
+    assert not np.allclose(y, w * (np.float32(c) * wrong), rtol=1e-4)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(1024).astype(np.float32) * 3
+    y = oracle.rmsnorm(x, np.ones(1024, np.float32), 1e-6)
+    assert abs(np.mean(y.astype(np.float64) ** 2) - 1.0) < 1e-5
+
+
+@ref_only
+@pytest.mark.parametrize("n", [64, 512, 1024, 7168])
+def test_rmsnorm_bit_equal_to_compiled_reference(n):
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n).astype(np.float32) * 2
+    w = (rng.standard_normal(n) * 0.1 + 1).astype(np.float32)
+    assert common.bits_equal(oracle.rmsnorm(x, w, 1e-6), oracle.ref_rmsnorm(x, w, 1e-6))
+
+
+def test_rope_closed_forms():
+    """Position 0 is the identity (cos 1, sin 0); inverse undoes forward; the
+    NoPE head is untouched; pairs are interleaved (v[0], v[1]), not split
+    halves; each pair keeps its length."""
+    cs, sn = _tables()
+    rng = np.random.default_rng(4)
+    v = rng.standard_normal((3, 64)).astype(np.float32)
+    assert common.bits_equal(oracle.rope_apply(v, 16, cs, sn, 0), v)
+    r = oracle.rope_apply(v, 16, cs, sn, 7)
+    assert common.bits_equal(r[:, :48], v[:, :48])
+    back = oracle.rope_apply(r, 16, cs, sn, 7, inverse=True)
+    assert np.max(np.abs(back - v)) < 1e-5
+    p0 = v[:, 48:].reshape(3, 8, 2)
+    p1 = r[:, 48:].reshape(3, 8, 2)
+    assert np.allclose(np.hypot(p0[..., 0], p0[..., 1]), np.hypot(p1[..., 0], p1[..., 1]),
+                       rtol=1e-5)
+    # pair 0 rotated by the angle of the table's first column
+    c, s = float(cs[7, 0]), float(sn[7, 0])
+    a, b = float(v[0, 48]), float(v[0, 49])
+    assert abs(r[0, 48] - (a * c - b * s)) < 1e-6 and abs(r[0, 49] - (a * s + b * c)) < 1e-6
+
+
+@ref_only
+@pytest.mark.parametrize("yarn", [False, True])
+def test_rope_bit_equal_to_compiled_reference(yarn):
+    cs, sn = _tables(64, 300, yarn)
+    rng = np.random.default_rng(5)
+    v = rng.standard_normal((4, 512)).astype(np.float32)
+    for pos in (0, 1, 37, 299):
+        for inv in (False, True):
+            assert common.bits_equal(oracle.rope_apply(v, 64, cs, sn, pos, inv),
+                                     oracle.ref_rope_apply(v, 64, cs, sn, pos, inv))
+
+
+def test_head_norm_rope():
+    """Each head at unit mean square after the norm (RoPE keeps lengths), the
+    NoPE part exactly q * inv, the rope part exactly the reference RoPE of
+    the scaled tail."""
+    cs, sn = _tables()
+    rng = np.random.default_rng(6)
+    q = (rng.standard_normal((4, 64)) * 5).astype(np.float32)
+    out = oracle.head_norm_rope(q, 16, 1e-6, cs, sn, 9)
+    ms = np.mean(out.astype(np.float64) ** 2, axis=1)
+    assert np.all(np.abs(ms - 1.0) < 1e-5)
+    for h in range(4):
+        inv = np.float32(1.0 / math.sqrt(np.sum(q[h].astype(np.float64) ** 2) / 64 + 1e-6))
+        scaled = q[h] * inv
+        assert common.bits_equal(out[h, :48], scaled[:48])
+        rot = (oracle.ref_rope_apply if oracle.ref_available() else oracle.rope_apply)(
+            scaled, 16, cs, sn, 9)
+        assert common.bits_equal(out[h], rot)
+
+
+def test_compressor_closed_forms():
+    """Equal scores pool to the mean; one dominant slot pools to its row;
+    the window closes every `ratio` tokens; ratio 4 pools its previous
+    window's first halves with the current window's second halves (the first
+    window's previous slots are -inf and drop out), then slides."""
+    hd, ratio = 8, 8
+    C = oracle.Compressor(ratio, hd, np.zeros((ratio, hd), np.float32))
+    kvs = np.arange(ratio * hd, dtype=np.float32).reshape(ratio, hd)
+    for p in range(ratio - 1):
+        assert C.step(kvs[p], np.zeros(hd, np.float32), p) is None
+    out = C.step(kvs[ratio - 1], np.zeros(hd, np.float32), ratio - 1)
+    assert np.allclose(out, kvs.mean(axis=0), rtol=1e-6)
+    C = oracle.Compressor(ratio, hd, np.zeros((ratio, hd), np.float32))
+    for p in range(ratio):
+        sc = np.full(hd, 50.0 if p == 3 else 0.0, np.float32)
+        out = C.step(kvs[p], sc, p)
+    assert np.allclose(out, kvs[3], rtol=1e-6)
+    # ratio 4: slot layout and the slide
+    r4 = 4
+    C = oracle.Compressor(r4, hd, np.zeros((r4, 2 * hd), np.float32))
+    rows = np.arange(2 * r4 * 2 * hd, dtype=np.float32).reshape(2 * r4, 2 * hd)
+    for p in range(r4):
+        out = C.step(rows[p], np.zeros(2 * hd, np.float32), p)
+    assert np.allclose(out, rows[:r4, hd:].mean(axis=0), rtol=1e-6)
+    for p in range(r4, 2 * r4):
+        out = C.step(rows[p], np.zeros(2 * hd, np.float32), p)
+    want = np.concatenate([rows[:r4, :hd], rows[r4:, hd:]]).mean(axis=0)
+    assert np.allclose(out, want, rtol=1e-6)
+    assert oracle.compress_rope_pos(7, 4) == 4 and oracle.compress_rope_pos(127, 128) == 0
+
+
+@ref_only
+@pytest.mark.parametrize("ratio,hd", [(4, 64), (8, 64), (4, 512), (128, 512)])
+def test_compressor_bit_equal_to_compiled_reference(ratio, hd):
+    rng = np.random.default_rng(ratio + hd)
+    width = (2 if ratio == 4 else 1) * hd
+    ape = rng.standard_normal((ratio, width)).astype(np.float32) * 0.5
+    A, B = oracle.Compressor(ratio, hd, ape), oracle.ref_compressor(ratio, hd, ape)
+    for p in range(3 * ratio if ratio < 128 else 2 * ratio):
+        kv = rng.standard_normal(width).astype(np.float32)
+        sc = rng.standard_normal(width).astype(np.float32) * 3
+        a, b = A.step(kv, sc, p), B.step(kv, sc, p)
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert common.bits_equal(a, b), p
+        assert common.bits_equal(A.kv, B.kv) and common.bits_equal(A.sc, B.sc)

@@ -75,7 +75,7 @@ def parse():
     ap.add_argument("--no-detail", action="store_true",
                     help="headline sweep only (skip C1/C3/C4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "copy"], default=None,
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "attn", "copy"], default=None,
                     help="time one configuration only (for profiling runs); "
                          "'copy' runs a plain 1 GiB device-to-device copy whose "
                          "known size calibrates the FETCH_SIZE/WRITE_SIZE counters")
@@ -262,6 +262,128 @@ class Bench:
         del W
         return us, eager, rows * cols * 2 + cols * 4 + rows * 4
 
+    # ------------------------------------------------------ attention block
+    def attn_run(self, steps, warmup, ratio=4, n_layers=4, p0=2048):
+        """The attention block (dsv4_gpu_attn_step_d, attention() of
+        dsv4_layer.c:213-336 in one call) at the DeepSeek-V4-Flash shapes:
+        hidden 4096, 64 heads x 512 (RoPE 64), q_lora 1024, wo_a 8 groups x
+        1024, window 128; ratio 4 with the indexer (64 x 128, top 512) or
+        ratio 128 (every compressed row). Synthetic FP8 (E8M0 scales) and BF16
+        weights of those shapes, random-init. n_layers such layers are bound
+        and stepped in turn, so each step reads its layer's weights cold (as a
+        decode through the model does); every layer is first decoded to
+        position p0, so the ring is full and the compressed rows are p0 /
+        ratio. Returns (eager us per step, the same, algorithmic bytes per
+        step). The eager rate is the one reported: the
+        positions move the state, so a replayed graph re-runs the same
+        positions (same launches and sizes) and is kept only as
+        attn_graph_us; on this GPU it measured slower than the stream."""
+        import ctypes
+        np, torch, D, L, C = self.np, self.torch, self.dsv4, self.L, self.common
+        hidden, ql, H, hd, rd, win, ol, og = 4096, 1024, 64, 512, 64, 128, 1024, 8
+        ih, idd, itop = 64, 128, 512
+        has_idx = ratio == 4
+        coff = 2 if ratio == 4 else 1
+        nrep = max(2, steps // 16)
+        maxpos = p0 + warmup + steps + 8
+        rng = np.random.default_rng(11)
+        keep = []
+
+        def fp8(rows, cols):
+            W = C.fp8_codes(rng, (rows, cols))
+            S = (127 + rng.integers(-8, -3, size=((rows + 127) // 128,
+                                                  (cols + 127) // 128))).astype(np.uint8)
+            keep.extend([W, S])
+            m = D.DSV4QMat(W.ctypes.data, S.ctypes.data, D.WFP8, rows, cols, 128, 128)
+            assert L.dsv4_gpu_upload(ctypes.byref(m)) == 0
+            return m, W.nbytes + S.nbytes
+
+        def bf16(rows, cols):
+            W = C.bf16_bits((rng.standard_normal((rows, cols)) * 0.02).astype(np.float32))
+            keep.append(W)
+            m = D.DSV4QMat(W.ctypes.data, None, D.WBF16, rows, cols, 0, 0)
+            assert L.dsv4_gpu_upload(ctypes.byref(m)) == 0
+            return m, W.nbytes
+
+        def vec(n, scale=0.1, add=1.0):
+            v = (rng.standard_normal(n) * scale + add).astype(np.float32)
+            keep.append(v)
+            return v.ctypes.data
+
+        half = rd // 2
+        th = np.arange(maxpos)[:, None] / (160000.0 ** (np.arange(half) * 2.0 / rd))[None, :]
+        cs, sn = np.cos(th).astype(np.float32), np.sin(th).astype(np.float32)
+        keep += [cs, sn]
+        layers = list(range(200, 200 + n_layers))
+        for lay in layers:
+            w = D.AttnW()
+            w.wq_a, b0 = fp8(ql, hidden)
+            w.wq_b, b1 = fp8(H * hd, ql)
+            w.wkv, b2 = fp8(hd, hidden)
+            w.wo_a, b3 = fp8(og * ol, H * hd // og)
+            w.wo_b, b4 = fp8(hidden, og * ol)
+            w.comp_wkv, b5 = bf16(coff * hd, hidden)
+            w.comp_wgate, b6 = bf16(coff * hd, hidden)
+            mats = b0 + b1 + b2 + b3 + b4 + b5 + b6
+            if has_idx:
+                w.idx_wq_b, b7 = fp8(ih * idd, ql)
+                w.idx_wproj, b8 = bf16(ih, hidden)
+                mats += b7 + b8
+            w.q_norm, w.kv_norm, w.comp_norm = vec(ql), vec(hd), vec(hd)
+            w.sink, w.comp_ape = vec(H, 1.0, 0.0), vec(ratio * coff * hd, 0.5, 0.0)
+            w.rope_cos, w.rope_sin = cs.ctypes.data, sn.ctypes.data
+            c = D.AttnCfg(hidden=hidden, q_lora=ql, n_heads=H, head_dim=hd, rope_dim=rd,
+                          window=win, ratio=ratio, idx_heads=ih if has_idx else 0,
+                          idx_dim=idd, idx_topk=itop, o_groups=og, o_lora=ol,
+                          max_pos=maxpos, rms_eps=1e-6)
+            assert L.dsv4_gpu_attn_bind(lay, ctypes.byref(c), ctypes.byref(w)) == 0
+        X = torch.randn((16, hidden), device=self.dev)
+        out = torch.empty(hidden, dtype=torch.float32, device=self.dev)
+        pos = [0]
+
+        def step(sp):
+            p = pos[0]
+            for lay in layers:
+                assert L.dsv4_gpu_attn_step_d(out.data_ptr(), X[p % 16].data_ptr(), lay, p,
+                                              sp) == 0
+            pos[0] = p + 1
+        while pos[0] < p0:
+            step(self.sp)
+        torch.cuda.synchronize()
+        for _ in range(warmup):
+            step(self.sp)
+        a, b = self.ev(), self.ev()
+        a.record(self.stream)
+        for _ in range(steps - nrep):
+            step(self.sp)
+        b.record(self.stream)
+        torch.cuda.synchronize()
+        eager = a.elapsed_time(b) * 1e3 / ((steps - nrep) * n_layers)
+        # the last nrep positions captured once into a graph and replayed:
+        # the same launches with the same sizes, without host gaps
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            sp = torch.cuda.current_stream().cuda_stream
+            for _ in range(nrep):
+                step(sp)
+        g.replay()
+        torch.cuda.synchronize()
+        a.record(self.stream)
+        for _ in range(4):
+            g.replay()
+        b.record(self.stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / (4 * nrep * n_layers)
+        avail = p0 // ratio
+        take = min(avail, itop) if has_idx else avail
+        alg = (mats + 2 * hidden * 4 + (win + take) * hd * 4 +
+               (avail * idd * 4 if has_idx else 0))
+        for lay in layers:
+            L.dsv4_gpu_attn_reset(lay)
+        self._attn_keep = keep          # resident keys stay valid host memory
+        self.attn_graph_us = us
+        return eager, eager, alg
+
     # ------------------------------------------------------------ C3
     def c3_run(self, steps, warmup):
         import ctypes
@@ -438,8 +560,8 @@ def main():
                           "per_shape_us": [round(m * 1e3, 3) for m in per_ms]}))
         B.L.dsv4_gpu_shutdown()
         return
-    if args.only in ("c1", "c3", "c4"):
-        fn = {"c1": B.c1_run, "c3": B.c3_run, "c4": B.c4_run}[args.only]
+    if args.only in ("c1", "c3", "c4", "attn"):
+        fn = {"c1": B.c1_run, "c3": B.c3_run, "c4": B.c4_run, "attn": B.attn_run}[args.only]
         us, eager, alg = fn(args.steps, args.warmup)
         emit(({"config": args.only, "us": round(us, 3),
                           "eager_us": round(eager, 3),
@@ -482,6 +604,11 @@ def main():
         detail["c4_sparse_mla_step_32768_top2048"] = rec(*B.c4_run(args.steps, args.warmup))
         log("bench: BF16 LM head")
         detail["lm_head_bf16_129280x7168"] = rec(*B.bf16_head_run(args.steps, args.warmup))
+        for ratio, name in ((4, "attn_block_flash_csa_ratio4"), (128, "attn_block_flash_hca_ratio128")):
+            log("bench: attention block, ratio %d" % ratio)
+            detail[name] = rec(*B.attn_run(32, 4, ratio=ratio))
+            detail[name]["graph_replay_us"] = round(B.attn_graph_us, 3)
+            detail[name]["positions_before"] = 2048
     cpu = None
     if not args.no_cpu:
         log("bench: CPU baseline (compiled reference, host cores)")

@@ -35,6 +35,16 @@ namespace {
 
 constexpr int B16_PART_MAX = 4096;
 
+/* Several matrices of one width reading the same x in one launch
+ * (blockIdx.y = matrix): n == 0 is the plain GEMV. */
+constexpr int B16_LIST_MAX = 4;
+struct B16List {
+    int n = 0;
+    const uint16_t *W[B16_LIST_MAX] = {};
+    float *y[B16_LIST_MAX] = {};
+    int rows[B16_LIST_MAX] = {};
+};
+
 struct B16Geom {
     int ch, tc, nch, wg, rg;
 };
@@ -79,9 +89,16 @@ __device__ __forceinline__ float dot8_bf16(const u32x4 v, const float *xr)
 template <int NCH, int R>
 __global__ void __launch_bounds__(256)
 k_bf16_gemv(float *__restrict__ y, const float *__restrict__ x,
-            const uint16_t *__restrict__ W, int rows, int cols, int tc, int rows_per_wg)
+            const uint16_t *__restrict__ W, int rows, int cols, int tc, int rows_per_wg,
+            B16List ls)
 {
     extern __shared__ float part[];                 /* [waves per row][rows_per_wg] */
+    if (ls.n) {
+        W = ls.W[blockIdx.y];
+        y = ls.y[blockIdx.y];
+        rows = ls.rows[blockIdx.y];
+        if ((int)blockIdx.x * rows_per_wg >= rows) return;   /* the whole workgroup */
+    }
     const int tid = threadIdx.x;
     const int g = tid / tc, j = tid - g * tc;
     const int rg = blockDim.x / tc;
@@ -148,7 +165,7 @@ k_bf16_gemv(float *__restrict__ y, const float *__restrict__ x,
 
 template <int NCH>
 void b16_launch(const B16Geom &g, float *y, const float *x, const uint16_t *W, int rows,
-                int cols, hipStream_t st)
+                int cols, const B16List &ls, hipStream_t st)
 {
     /* two rows per thread per step while the loads fit the registers */
     constexpr int R = NCH <= 4 ? 2 : 1;
@@ -163,7 +180,8 @@ void b16_launch(const B16Geom &g, float *y, const float *x, const uint16_t *W, i
         cus = n;
     }
     const int step_rows = g.rg * R;
-    const int want = 2 * cus;                       /* two workgroups per CU */
+    const int nm = ls.n ? ls.n : 1;
+    const int want = (2 * cus + nm - 1) / nm;       /* two workgroups per CU */
     const int wpr = g.tc > 64 ? g.tc / 64 : 1;
     int spw = ((rows + step_rows - 1) / step_rows + want - 1) / want;
     const int max_spw = B16_PART_MAX / wpr / step_rows;
@@ -172,8 +190,21 @@ void b16_launch(const B16Geom &g, float *y, const float *x, const uint16_t *W, i
     const int rows_per_wg = spw * step_rows;
     const int grid = (rows + rows_per_wg - 1) / rows_per_wg;
     const size_t lds = g.tc > 64 ? sizeof(float) * (size_t)wpr * rows_per_wg : 0;
-    hipLaunchKernelGGL((k_bf16_gemv<NCH, R>), dim3(grid), dim3(g.wg), lds, st, y, x, W,
-                       rows, cols, g.tc, rows_per_wg);
+    hipLaunchKernelGGL((k_bf16_gemv<NCH, R>), dim3(grid, nm), dim3(g.wg), lds, st, y, x, W,
+                       rows, cols, g.tc, rows_per_wg, ls);
+}
+
+int b16_dispatch(const B16Geom &g, float *y, const float *x, const uint16_t *W, int rows,
+                 int cols, const B16List &ls, hipStream_t st)
+{
+    switch (g.nch) {
+    case 1: b16_launch<1>(g, y, x, W, rows, cols, ls, st); break;
+    case 2: b16_launch<2>(g, y, x, W, rows, cols, ls, st); break;
+    case 3: case 4: b16_launch<4>(g, y, x, W, rows, cols, ls, st); break;
+    default: b16_launch<8>(g, y, x, W, rows, cols, ls, st); break;
+    }
+    HIP_OK(hipGetLastError(), "bf16 gemv launch");
+    return 0;
 }
 
 } // namespace
@@ -192,12 +223,27 @@ int dsv4_bf16_gemv_launch(float *y, const float *x, const uint16_t *W, int rows,
         DSV4_ERR("bf16 gemv: unsupported shape %dx%d or unaligned operands", rows, cols);
         return -1;
     }
-    switch (g.nch) {
-    case 1: b16_launch<1>(g, y, x, W, rows, cols, st); break;
-    case 2: b16_launch<2>(g, y, x, W, rows, cols, st); break;
-    case 3: case 4: b16_launch<4>(g, y, x, W, rows, cols, st); break;
-    default: b16_launch<8>(g, y, x, W, rows, cols, st); break;
+    return b16_dispatch(g, y, x, W, rows, cols, B16List{}, st);
+}
+
+int dsv4_bf16_gemv_list_launch(const float *x, int cols, int n, const uint16_t *const *W,
+                               float *const *y, const int *rows, hipStream_t st)
+{
+    B16Geom g;
+    if (n < 1 || n > B16_LIST_MAX || !b16_geom(cols, &g) || (((uintptr_t)x) & 15)) {
+        DSV4_ERR("bf16 gemv list: %d matrices of width %d not supported", n, cols);
+        return -1;
     }
-    HIP_OK(hipGetLastError(), "bf16 gemv launch");
-    return 0;
+    B16List ls;
+    ls.n = n;
+    int rmax = 0;
+    for (int i = 0; i < n; i++) {
+        if (rows[i] <= 0 || (((uintptr_t)W[i]) & 15)) {
+            DSV4_ERR("bf16 gemv list: matrix %d (%d rows) empty or unaligned", i, rows[i]);
+            return -1;
+        }
+        ls.W[i] = W[i]; ls.y[i] = y[i]; ls.rows[i] = rows[i];
+        rmax = rows[i] > rmax ? rows[i] : rmax;
+    }
+    return b16_dispatch(g, y[0], x, W[0], rmax, cols, ls, st);
 }

@@ -102,6 +102,22 @@ __device__ __forceinline__ float dot16(const u32x4 v, const float *xr)
  * partials of rows wider than one wave (at most 4 waves per row). */
 constexpr int PART_MAX = 4096;
 
+/* Independent GEMVs of one width in one launch (blockIdx.y = group).
+ * Strided: group i reads x + i*x, W + i*w bytes, its scales at S + i*s
+ * bytes, and writes y + i*y. Listed (list > 0): group i is matrix Wl[i]
+ * (rl[i] rows, scales Sl[i]) into yl[i], all reading the same x. One group
+ * with zero strides is the plain GEMV. */
+constexpr int FP8_LIST_MAX = 4;
+struct Fp8Groups {
+    int n = 1;
+    long long x = 0, y = 0, w = 0, s = 0;
+    int list = 0;
+    const uint8_t *Wl[FP8_LIST_MAX] = {};
+    const void *Sl[FP8_LIST_MAX] = {};
+    float *yl[FP8_LIST_MAX] = {};
+    int rl[FP8_LIST_MAX] = {};
+};
+
 /* One step's weights (R rows x NCH chunks) and the block scales of its row
  * block (the R rows of a step lie in one row block: the launcher picks R
  * dividing blk_r, and steps start at multiples of R). Every load is issued
@@ -138,9 +154,23 @@ __global__ void __launch_bounds__(256)
 k_fp8_gemv(float *__restrict__ y, const float *__restrict__ x,
            const uint8_t *__restrict__ W, const void *__restrict__ S,
            int rows, int cols, int sc, int blk_r, int blk_c, int tc,
-           int rows_per_wg)
+           int rows_per_wg, Fp8Groups gp)
 {
     extern __shared__ float part[];     /* [waves per row][rows_per_wg], then x (XL) */
+    if (gp.list) {
+        const int gi = blockIdx.y;
+        W = gp.Wl[gi];
+        S = gp.Sl[gi];
+        y = gp.yl[gi];
+        rows = gp.rl[gi];
+        if ((int)blockIdx.x * rows_per_wg >= rows) return;   /* the whole workgroup */
+    } else if (gp.n > 1) {
+        const size_t gi = blockIdx.y;
+        y += gi * gp.y;
+        x += gi * gp.x;
+        W += gi * gp.w;
+        S = (const uint8_t *)S + gi * gp.s;
+    }
 
     const int tid = threadIdx.x;
     const int g = tid / tc;
@@ -407,7 +437,7 @@ int cu_count()
 template <int NCH, int R, int SF, int PF>
 void launch_gemv(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
                  const void *S, int rows, int cols, int sc, int blk_r,
-                 int blk_c, int wgs_per_cu, hipStream_t st)
+                 int blk_c, int wgs_per_cu, const Fp8Groups &gp, hipStream_t st)
 {
     /* x through LDS (one fetch per workgroup instead of one per row group)
      * measured faster on MI355X for narrow rows (24576x1536: 12.2 -> 11.8
@@ -416,7 +446,7 @@ void launch_gemv(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
     const int xl = g.wg == 256 && (cols & 3) == 0 && (cols <= 2048 || cols >= 16384);
     const int step_rows = g.rg * R;
     const int nsteps = (rows + step_rows - 1) / step_rows;
-    const int want = wgs_per_cu * cu_count();
+    const int want = (wgs_per_cu * cu_count() + gp.n - 1) / gp.n;
     int spw = (nsteps + want - 1) / want;              /* steps per workgroup */
     const int wpr = g.tc > 64 ? g.tc / 64 : 1;
     const int max_spw = PART_MAX / wpr / step_rows;
@@ -437,35 +467,36 @@ void launch_gemv(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
         }
     }
     if (xl)
-        hipLaunchKernelGGL((k_fp8_gemv<NCH, R, SF, PF, 1>), dim3(grid), dim3(g.wg), lds, st,
-                           y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, rows_per_wg);
+        hipLaunchKernelGGL((k_fp8_gemv<NCH, R, SF, PF, 1>), dim3(grid, gp.n), dim3(g.wg), lds,
+                           st, y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, rows_per_wg, gp);
     else
-        hipLaunchKernelGGL((k_fp8_gemv<NCH, R, SF, PF, 0>), dim3(grid), dim3(g.wg), lds, st,
-                           y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, rows_per_wg);
+        hipLaunchKernelGGL((k_fp8_gemv<NCH, R, SF, PF, 0>), dim3(grid, gp.n), dim3(g.wg), lds,
+                           st, y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, rows_per_wg, gp);
 }
 
 template <int R, int SF, int PF>
 void launch_gemv_nch(const Fp8Geom &g, float *y, const float *x,
                      const uint8_t *W, const void *S, int rows, int cols,
-                     int sc, int blk_r, int blk_c, int wpc, hipStream_t st)
+                     int sc, int blk_r, int blk_c, int wpc, const Fp8Groups &gp,
+                     hipStream_t st)
 {
     switch (g.nch) {
-    case 1: launch_gemv<1, R, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st); break;
-    case 2: launch_gemv<2, R, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st); break;
-    case 3: launch_gemv<3, R, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st); break;
-    default: launch_gemv<4, R, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st); break;
+    case 1: launch_gemv<1, R, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, gp, st); break;
+    case 2: launch_gemv<2, R, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, gp, st); break;
+    case 3: launch_gemv<3, R, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, gp, st); break;
+    default: launch_gemv<4, R, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, gp, st); break;
     }
 }
 
 template <int SF, int PF>
 void launch_gemv_r(const Fp8Geom &g, int R, float *y, const float *x,
                    const uint8_t *W, const void *S, int rows, int cols, int sc,
-                   int blk_r, int blk_c, int wpc, hipStream_t st)
+                   int blk_r, int blk_c, int wpc, const Fp8Groups &gp, hipStream_t st)
 {
     switch (R) {
-    case 1: launch_gemv_nch<1, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st); break;
-    case 2: launch_gemv_nch<2, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st); break;
-    default: launch_gemv_nch<4, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st); break;
+    case 1: launch_gemv_nch<1, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, gp, st); break;
+    case 2: launch_gemv_nch<2, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, gp, st); break;
+    default: launch_gemv_nch<4, SF, PF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, gp, st); break;
     }
 }
 
@@ -488,13 +519,11 @@ bool blocking_ok(int blk_r, int blk_c)
     return blk_r >= 1 && blk_c >= 16 && (blk_c & 15) == 0;
 }
 
-} // namespace
-
-int dsv4_fp8_gemv_launch(float *y, const float *x, const uint8_t *W,
-                         const void *S, int sfmt, int rows, int cols,
-                         int blk_r, int blk_c, hipStream_t st)
+int fp8_gemv(float *y, const float *x, const uint8_t *W, const void *S, int sfmt,
+             int rows, int cols, int blk_r, int blk_c, const Fp8Groups &gp,
+             hipStream_t st)
 {
-    if (rows <= 0 || cols <= 0 || blk_r <= 0 || blk_c <= 0) {
+    if (rows <= 0 || cols <= 0 || blk_r <= 0 || blk_c <= 0 || gp.n <= 0 || gp.n > 65535) {
         DSV4_ERR("fp8 gemv: bad shape %dx%d blk %dx%d", rows, cols, blk_r, blk_c);
         return -1;
     }
@@ -515,23 +544,85 @@ int dsv4_fp8_gemv_launch(float *y, const float *x, const uint8_t *W,
         int wpc = env_int("DSV4_GPU_FP8_WPC", cols >= 4096 ? 2 : 4);
         if (wpc <= 0) wpc = 2;
         if (sfmt == 0) {
-            if (pf) launch_gemv_r<0, 1>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st);
-            else    launch_gemv_r<0, 0>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st);
+            if (pf) launch_gemv_r<0, 1>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, gp, st);
+            else    launch_gemv_r<0, 0>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, gp, st);
         } else {
-            if (pf) launch_gemv_r<1, 1>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st);
-            else    launch_gemv_r<1, 0>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, st);
+            if (pf) launch_gemv_r<1, 1>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, gp, st);
+            else    launch_gemv_r<1, 0>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, gp, st);
         }
     } else {
         const int grid = (rows + 3) / 4;
-        if (sfmt == 0)
-            hipLaunchKernelGGL((k_fp8_gemv_generic<0>), dim3(grid), dim3(256), 0, st,
-                               y, x, W, S, rows, cols, sc, blk_r, blk_c, 1);
-        else
-            hipLaunchKernelGGL((k_fp8_gemv_generic<1>), dim3(grid), dim3(256), 0, st,
-                               y, x, W, S, rows, cols, sc, blk_r, blk_c, 1);
+        for (int i = 0; i < gp.n; i++) {
+            float *yi = y + i * gp.y;
+            const float *xi = x + i * gp.x;
+            const uint8_t *Wi = W + i * gp.w;
+            const void *Si = (const uint8_t *)S + i * gp.s;
+            if (sfmt == 0)
+                hipLaunchKernelGGL((k_fp8_gemv_generic<0>), dim3(grid), dim3(256), 0, st,
+                                   yi, xi, Wi, Si, rows, cols, sc, blk_r, blk_c, 1);
+            else
+                hipLaunchKernelGGL((k_fp8_gemv_generic<1>), dim3(grid), dim3(256), 0, st,
+                                   yi, xi, Wi, Si, rows, cols, sc, blk_r, blk_c, 1);
+        }
     }
     HIP_OK(hipGetLastError(), "fp8 gemv launch");
     return 0;
+}
+
+} // namespace
+
+int dsv4_fp8_gemv_launch(float *y, const float *x, const uint8_t *W,
+                         const void *S, int sfmt, int rows, int cols,
+                         int blk_r, int blk_c, hipStream_t st)
+{
+    return fp8_gemv(y, x, W, S, sfmt, rows, cols, blk_r, blk_c, Fp8Groups{}, st);
+}
+
+int dsv4_fp8_gemv_list_launch(const float *x, int cols, int sfmt, int blk_r, int blk_c,
+                              int n, const uint8_t *const *W, const void *const *S,
+                              float *const *y, const int *rows, hipStream_t st)
+{
+    if (n < 1 || n > FP8_LIST_MAX) {
+        DSV4_ERR("fp8 gemv list: %d matrices (1 .. %d)", n, FP8_LIST_MAX);
+        return -1;
+    }
+    Fp8Groups gp;
+    gp.n = n;
+    gp.list = 1;
+    int rmax = 0;
+    for (int i = 0; i < n; i++) {
+        if (rows[i] <= 0 || (((uintptr_t)W[i]) & 15)) {
+            DSV4_ERR("fp8 gemv list: matrix %d (%d rows) empty or unaligned", i, rows[i]);
+            return -1;
+        }
+        gp.Wl[i] = W[i]; gp.Sl[i] = S[i]; gp.yl[i] = y[i]; gp.rl[i] = rows[i];
+        rmax = rows[i] > rmax ? rows[i] : rmax;
+    }
+    Fp8Geom g;
+    if (!fp8_geom(cols, &g) || !blocking_ok(blk_r, blk_c) || (((uintptr_t)x) & 15)) {
+        for (int i = 0; i < n; i++)
+            if (dsv4_fp8_gemv_launch(y[i], x, W[i], S[i], sfmt, rows[i], cols, blk_r, blk_c,
+                                     st) != 0)
+                return -1;
+        return 0;
+    }
+    return fp8_gemv(y[0], x, W[0], S[0], sfmt, rmax, cols, blk_r, blk_c, gp, st);
+}
+
+int dsv4_fp8_gemv_groups_launch(float *y, const float *x, const uint8_t *W,
+                                const void *S, int sfmt, int rows, int cols, int blk_r,
+                                int blk_c, int groups, long long y_stride,
+                                long long x_stride, long long w_stride,
+                                long long s_stride, hipStream_t st)
+{
+    Fp8Groups gp;
+    gp.n = groups;
+    gp.y = y_stride; gp.x = x_stride; gp.w = w_stride; gp.s = s_stride;
+    if (groups > 1 && (((uintptr_t)(x_stride * 4) | (uintptr_t)w_stride) & 15)) {
+        DSV4_ERR("fp8 gemv groups: strides break 16-byte alignment");
+        return -1;
+    }
+    return fp8_gemv(y, x, W, S, sfmt, rows, cols, blk_r, blk_c, gp, st);
 }
 
 int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,

@@ -1128,6 +1128,54 @@ int block_bind(int layer, const dsv4_gpu_attn_cfg *cp, const dsv4_gpu_attn_w *w)
     return 0;
 }
 
+/* GEMVs that read the same x: FP8 matrices of one width, scale format and
+ * blocking go in one launch, BF16 matrices of one width in another (each
+ * row keeps the bits of its own launch); anything else goes alone. */
+struct XJob {
+    const MatRef *m;
+    float *y;
+    int rows;
+};
+
+int x_gemvs(const XJob *jobs, int n, const float *d_x, hipStream_t st)
+{
+    bool done[8] = {};
+    for (int i = 0; i < n; i++) {
+        if (done[i]) continue;
+        const Res &r = jobs[i].m->r;
+        if (r.wdt != DSV4_WFP8 && r.wdt != DSV4_WBF16) {
+            if (res_gemv(r, jobs[i].m->r0, jobs[i].rows, jobs[i].y, d_x, st) != 0) return -1;
+            done[i] = true;
+            continue;
+        }
+        const uint8_t *W[4];
+        const void *S[4];
+        float *Y[4];
+        int R[4], k = 0;
+        for (int j = i; j < n && k < 4; j++) {
+            const Res &q = jobs[j].m->r;
+            if (done[j] || q.wdt != r.wdt || q.cols != r.cols ||
+                (r.wdt == DSV4_WFP8 &&
+                 (q.sfmt != r.sfmt || q.blk_r != r.blk_r || q.blk_c != r.blk_c)))
+                continue;
+            const int r0 = jobs[j].m->r0;
+            W[k] = q.dw + (size_t)r0 * q.row_bytes();
+            S[k] = q.ds ? q.ds + (size_t)(r0 / q.blk_r) * q.sc * (q.sfmt ? 4 : 1) : nullptr;
+            Y[k] = jobs[j].y;
+            R[k] = jobs[j].rows;
+            done[j] = true;
+            k++;
+        }
+        const int rc = r.wdt == DSV4_WFP8
+                           ? dsv4_fp8_gemv_list_launch(d_x, r.cols, r.sfmt, r.blk_r, r.blk_c, k,
+                                                       W, S, Y, R, st)
+                           : dsv4_bf16_gemv_list_launch(d_x, r.cols, k,
+                                                        (const uint16_t *const *)W, Y, R, st);
+        if (rc != 0) return -1;
+    }
+    return 0;
+}
+
 /* attention() of dsv4_layer.c:213-336 for the token at pos, on stream st;
  * x and out are device buffers of hidden floats. */
 int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_t st)
@@ -1140,15 +1188,24 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
         return -1;
     }
 #define OK(e) do { if ((e) != 0) return -1; } while (0)
-    /* q: wq_a, the learned norm, wq_b, then each head's norm and RoPE */
-    OK(res_gemv(b.wq_a.r, b.wq_a.r0, c.q_lora, b.qr, d_x, st));
+    const bool closes = c.ratio > 0 && (pos + 1) % c.ratio == 0;
+    const bool use_idx = c.ratio > 0 && c.idx_heads > 0 && b.n_comp + (closes ? 1 : 0) > 0;
+    /* the projections of x: wq_a, wkv, the compressor's wkv / wgate and the
+     * indexer's weights_proj (when it runs this step) */
+    XJob xj[5] = {{&b.wq_a, b.qr, c.q_lora}, {&b.wkv, b.kv, hd}};
+    int nx = 2;
+    if (c.ratio > 0) {
+        xj[nx++] = XJob{&b.cwkv, b.ckv, b.width};
+        xj[nx++] = XJob{&b.cwgate, b.csc, b.width};
+    }
+    if (use_idx) xj[nx++] = XJob{&b.iwproj, b.idx_w, c.idx_heads};
+    OK(x_gemvs(xj, nx, d_x, st));
+    /* q: the learned norm, wq_b, then each head's norm and RoPE */
     OK(dsv4_norm_rope_launch(b.qr, 0, b.qr, 0, b.q_norm, 1, c.q_lora, 1, c.rms_eps, 0,
                              nullptr, nullptr, 0, 0, 0, st));
     OK(res_gemv(b.wq_b.r, b.wq_b.r0, H * hd, b.q, b.qr, st));
-    OK(dsv4_norm_rope_launch(b.q, hd, b.q, hd, nullptr, H, hd, 1, c.rms_eps, rd, b.cs, b.sn,
-                             pos, half, 0, st));
-    /* kv: wkv, kv_norm, RoPE, into the ring slot */
-    OK(res_gemv(b.wkv.r, b.wkv.r0, hd, b.kv, d_x, st));
+    /* (each head's norm and RoPE happen inside the attention, on its copy) */
+    /* kv: kv_norm, RoPE, into the ring slot */
     OK(dsv4_norm_rope_launch(b.kv_cache + (size_t)(pos % c.window) * hd, 0, b.kv, 0, b.kv_norm,
                              1, hd, 1, c.rms_eps, rd, b.cs, b.sn, pos, half, 0, st));
     const int n_win = pos + 1 < c.window ? pos + 1 : c.window;
@@ -1156,12 +1213,10 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
     if (c.ratio > 0) {
         /* the compressor (dsv4_layer.c:243-261) */
         const int ph = pos % c.ratio, slot = c.ratio == 4 ? c.ratio + ph : ph;
-        OK(res_gemv(b.cwkv.r, b.cwkv.r0, b.width, b.ckv, d_x, st));
-        OK(res_gemv(b.cwgate.r, b.cwgate.r0, b.width, b.csc, d_x, st));
         OK(dsv4_comp_update_launch(b.comp_kv + (size_t)slot * b.width,
                                    b.comp_score + (size_t)slot * b.width, b.ckv, b.csc,
                                    b.ape + (size_t)ph * b.width, b.width, st));
-        if ((pos + 1) % c.ratio == 0) {
+        if (closes) {
             if (b.n_comp >= b.max_comp) {
                 DSV4_ERR("attn_step: compressed rows exceed max_pos / ratio + 1");
                 return -1;
@@ -1174,20 +1229,19 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
         }
         /* which compressed rows attention sees (dsv4_layer.c:267-297) */
         const int avail = b.n_comp;
-        if (avail > 0 && c.idx_heads > 0) {
+        if (use_idx) {
             const int ih = c.idx_heads, idd = c.idx_dim;
             OK(res_gemv(b.iwq_b.r, b.iwq_b.r0, ih * idd, b.idx_q, b.qr, st));
-            OK(dsv4_norm_rope_launch(b.idx_q, idd, b.idx_q, idd, nullptr, ih, idd, 0, 0.0f, rd,
-                                     b.cs, b.sn, pos, half, 0, st));
-            OK(res_gemv(b.iwproj.r, b.iwproj.r0, ih, b.idx_w, d_x, st));
             take = avail < c.idx_topk ? avail : c.idx_topk;
             const int hist = dsv4_topk_takes_hist(avail, take);
             /* the keys are the compressed region read at index_head_dim
              * stride, as the reference's call does (dsv4_layer.c:286-289) */
-            OK(dsv4_indexer_score_launch(b.scores, b.idx_q, b.idx_w, ih, idd,
-                                         b.kv_cache + (size_t)c.window * hd, nullptr,
-                                         DSV4_GPU_KV_F32, idd, avail, indexer_scale(idd, ih),
-                                         b.iscr, hist, st));
+            /* (the indexer's q is RoPE'd at pos inside the score kernel) */
+            OK(dsv4_indexer_score_rope_launch(b.scores, b.idx_q, b.idx_w, ih, idd,
+                                              b.kv_cache + (size_t)c.window * hd, nullptr,
+                                              DSV4_GPU_KV_F32, idd, avail,
+                                              indexer_scale(idd, ih), b.iscr, hist, b.cs,
+                                              b.sn, pos, half, rd, st));
             OK(dsv4_topk_launch(b.idxs + n_win, b.scores, avail, take, b.iscr, hist, st));
             mode = 2;
         } else {
@@ -1195,24 +1249,23 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
         }
     }
     OK(dsv4_attn_idxs_launch(b.idxs, pos, c.window, n_win, take, mode, c.window, st));
-    OK(dsv4_attn_launch(b.o, b.q, b.kv_cache, DSV4_GPU_KV_F32, hd, c.window + b.max_comp,
-                        b.sink, b.idxs, H, hd, hd, n_win + take, 1.0f / sqrtf((float)hd),
-                        b.ascr, st));
-    /* de-rotate, then wo_a per group (the FP8 slices of dsv4_layer.c:321-334:
+    /* the attention with q's per-head norm and RoPE, and the output's
+     * de-rotation, folded in */
+    OK(dsv4_attn_block_launch(b.o, b.q, b.kv_cache, DSV4_GPU_KV_F32, hd,
+                              c.window + b.max_comp, b.sink, b.idxs, H, hd, hd, n_win + take,
+                              1.0f / sqrtf((float)hd), b.ascr, 1, c.rms_eps, b.cs, b.sn, pos,
+                              half, rd, st));
+    /* wo_a's groups in one launch (the FP8 slices of dsv4_layer.c:321-334:
      * group g's rows from g * o_lora, its scale rows from g * (o_lora /
-     * blk_r)) and wo_b */
-    OK(dsv4_norm_rope_launch(b.o, hd, b.o, hd, nullptr, H, hd, 0, 0.0f, rd, b.cs, b.sn, pos,
-                             half, 1, st));
+     * blk_r), its input o + g * (H * hd / o_groups)), then wo_b */
     const Res &wa = b.wo_a.r;
     const int gw = H * hd / c.o_groups, gr = c.o_lora;
-    const size_t ssz = wa.sfmt ? 4 : 1;
-    for (int g = 0; g < c.o_groups; g++) {
-        const uint8_t *W = wa.dw + (size_t)(b.wo_a.r0 + g * gr) * wa.cols;
-        const uint8_t *S = wa.ds + ((size_t)(b.wo_a.r0 / wa.blk_r) + (size_t)g * (gr / wa.blk_r)) *
-                                       wa.sc * ssz;
-        OK(dsv4_fp8_gemv_launch(b.ogrp + (size_t)g * gr, b.o + (size_t)g * gw, W, S, wa.sfmt,
-                                gr, gw, wa.blk_r, wa.blk_c, st));
-    }
+    const long long ssz = wa.sfmt ? 4 : 1;
+    OK(dsv4_fp8_gemv_groups_launch(
+        b.ogrp, b.o, wa.dw + (size_t)b.wo_a.r0 * wa.cols,
+        wa.ds + (size_t)(b.wo_a.r0 / wa.blk_r) * wa.sc * ssz, wa.sfmt, gr, gw, wa.blk_r,
+        wa.blk_c, c.o_groups, gr, gw, (long long)gr * wa.cols,
+        (long long)(gr / wa.blk_r) * wa.sc * ssz, st));
     OK(res_gemv(b.wo_b.r, b.wo_b.r0, c.hidden, d_out, b.ogrp, st));
 #undef OK
     b.next_pos = pos + 1;

@@ -35,6 +35,27 @@ int dsv4_fp8_gemv_launch(float *y, const float *x, const uint8_t *W,
 /* MXFP4 GEMV (dsv4_matmul_fp4): W e2m1 nibbles [rows][cols/2], S E8M0 bytes
  * [ceil(rows/blk_r)][ceil(cols/blk_c)]. _ok: the shapes it takes (cols a
  * multiple of 32 up to 16384, blk_c a multiple of 32). Returns 0 / -1. */
+/* `groups` GEMVs of one shape in one launch: group i reads x + i*x_stride
+ * floats, W + i*w_stride bytes and its scales at S + i*s_stride bytes, and
+ * writes y + i*y_stride floats; each group's rows get the bits of a plain
+ * launch on those pointers. */
+int dsv4_fp8_gemv_groups_launch(float *y, const float *x, const uint8_t *W,
+                                const void *S, int sfmt, int rows, int cols, int blk_r,
+                                int blk_c, int groups, long long y_stride,
+                                long long x_stride, long long w_stride,
+                                long long s_stride, hipStream_t st);
+
+/* Up to four FP8 matrices of one width, scale format and blocking that read
+ * the same x, in one launch: y[i] = W[i] x over rows[i] rows, each with the
+ * bits of its own plain launch. */
+int dsv4_fp8_gemv_list_launch(const float *x, int cols, int sfmt, int blk_r, int blk_c,
+                              int n, const uint8_t *const *W, const void *const *S,
+                              float *const *y, const int *rows, hipStream_t st);
+
+/* The same for up to four BF16 matrices of one width. */
+int dsv4_bf16_gemv_list_launch(const float *x, int cols, int n, const uint16_t *const *W,
+                               float *const *y, const int *rows, hipStream_t st);
+
 bool dsv4_fp4_gemv_ok(int rows, int cols, int blk_r, int blk_c);
 int dsv4_fp4_gemv_launch(float *y, const float *x, const uint8_t *W, const uint8_t *S,
                          int rows, int cols, int blk_r, int blk_c, hipStream_t st);
@@ -108,6 +129,28 @@ int dsv4_topk_launch(int *d_idxs, const float *d_scores, int n, int k,
 
 /* Scratch needed by dsv4_attn_launch, in bytes (0: shape not supported). */
 size_t dsv4_attn_scratch_bytes(int h, int d_qk, int d_v, int topk, int kv_fmt);
+
+/* The attention block's form: q_norm scales each head of q by 1/sqrt(mean
+ * square + q_eps) and rope_dim > 0 RoPEs its last rope_dim elements at
+ * rope_pos before the scores (dsv4_layer.c:223-231), and de-rotates the
+ * output's last rope_dim elements after them (:304-305) -- on the kernels'
+ * own copies; d_q is not written. */
+int dsv4_attn_block_launch(float *d_o, const float *d_q, const void *d_kv,
+                           int kv_fmt, int kv_stride, int kv_rows,
+                           const float *d_sink, const int *d_idxs, int h, int d_qk,
+                           int d_v, int topk, float scale, void *scratch, int q_norm,
+                           float q_eps, const float *rope_cs, const float *rope_sn,
+                           int rope_pos, int rope_half, int rope_dim, hipStream_t st);
+
+/* The indexer score with its q RoPE'd at rope_pos first (rope_dim 0: as
+ * given), on the kernel's own copy. */
+int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *d_w,
+                                   int H, int D, const void *d_keys,
+                                   const float *d_key_scales, int key_fmt,
+                                   int key_stride, int n, float scale, void *scratch,
+                                   int with_hist, const float *rope_cs,
+                                   const float *rope_sn, int rope_pos, int rope_half,
+                                   int rope_dim, hipStream_t st);
 
 /* Rows outside [0, kv_rows) are treated as masked (never read). */
 int dsv4_attn_launch(float *d_o, const float *d_q, const void *d_kv,

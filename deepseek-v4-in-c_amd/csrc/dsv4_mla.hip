@@ -19,6 +19,7 @@
  * and 9..0 finds T, the key of the k-th largest, and how many elements equal
  * to T are taken; the elements > T are ordered by (key desc, index asc) by
  * counting, for each, the candidates ahead of it (k_tk_part, k_tk_final).
+ * Up to 4096 scores, one launch ranks every element directly (k_tk_small).
  *
  * SPARSE ATTENTION (dsv4_attn.c:60-108): split over the selected rows and a
  * log-sum-exp combine. Partial pass: per split of selected rows, the scores,
@@ -132,7 +133,9 @@ __device__ __forceinline__ void key_piece(u32x4 v, float rs, float *k)
 /* q of the wave's IS_HB heads for columns c0 .. c0 + 15, one column per
  * lane of each 16-lane row (every row holds the same values): lane l gets
  * q[h0 + j][c0 + l % 16]. Heads past H read head H-1, columns past D the
- * last column. */
+ * last column. q is the workgroup's LDS copy (an L2 round trip per 16
+ * columns would leave the chains waiting whenever there are few rows to
+ * overlap them). */
 __device__ __forceinline__ void q_cols(float *dst, const float *q, int h0, int H,
                                        int D, int c0, int lane)
 {
@@ -187,14 +190,32 @@ __device__ __forceinline__ void chain_16(double *acc, const float *qf, const flo
 #undef DSV4_COL
 }
 
-template <int KF, int VEC, int HIST>
-__global__ void __launch_bounds__(IS_MAXW * 64)
+/* RoPE of the last rd elements of a vector (dsv4_rope.c:105-119), applied by
+ * a kernel to its own copy of an input: rd == 0 is none. */
+struct Dsv4Rope {
+    const float *cs = nullptr, *sn = nullptr;
+    int pos = 0, half = 0, rd = 0, inverse = 0;
+};
+
+__device__ __forceinline__ void rope_pair(float &a, float &b, const Dsv4Rope &r, int p)
+{
+    const float c = r.cs[(size_t)r.pos * r.half + p];
+    const float s0 = r.sn[(size_t)r.pos * r.half + p];
+    const float s = r.inverse ? -s0 : s0;
+    const float re = a, im = b;
+    a = re * c - im * s;
+    b = re * s + im * c;
+}
+
+template <int KF, int VEC, int HIST, int MW>
+__global__ void __launch_bounds__(MW * 64)
 k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
          uint32_t *__restrict__ meta, const float *__restrict__ q, const float *__restrict__ w,
          int H, int HP, int D, const void *__restrict__ keys,
-         const float *__restrict__ ks, int key_stride, int n, float scale, int ng)
+         const float *__restrict__ ks, int key_stride, int n, float scale, int ng,
+         Dsv4Rope qr)
 {
-    extern __shared__ double dots[];            /* [kb * 64][HP + 1], then w[HP] */
+    extern __shared__ double dots[];            /* [kb * 64][HP + 1], w[HP], then q[H][D] */
     constexpr int ES = KF == DSV4_GPU_KV_F32 ? 4 : KF == DSV4_GPU_KV_BF16 ? 2 : 1;
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -204,7 +225,31 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
     const int tr = t < n ? t : n - 1;           /* rows past n compute row n-1 */
     const int pitch = HP + 1;
     double *wd = dots + (size_t)kb * 64 * pitch;
+    float *qs = (float *)(wd + HP);
     for (int i = threadIdx.x; i < H; i += blockDim.x) wd[i] = (double)w[i];
+    /* q into LDS (the launcher checks that it fits): batches of loads in
+     * flight before any store, one memory latency per batch of 8 per thread */
+    for (int i0 = 0; i0 < H * D; i0 += 8 * (int)blockDim.x) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = q[min(i0 + u * (int)blockDim.x + (int)threadIdx.x, H * D - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = i0 + u * (int)blockDim.x + (int)threadIdx.x;
+            if (i < H * D) qs[i] = v[u];
+        }
+    }
+    __syncthreads();
+    if (qr.rd) {
+        /* the indexer's q RoPE'd at pos, head by head (dsv4_layer.c:282-284) */
+        const int hp = qr.rd / 2;
+        for (int i = threadIdx.x; i < H * hp; i += blockDim.x) {
+            const int hh = i / hp, p = i - hh * hp;
+            float *t = qs + (size_t)hh * D + (D - qr.rd) + 2 * p;
+            rope_pair(t[0], t[1], qr, p);
+        }
+        __syncthreads();
+    }
     const float rs = KF == DSV4_GPU_KV_FP8 ? ks[tr] : 1.0f;
     const unsigned char *row = (const unsigned char *)keys + (size_t)tr * key_stride * ES;
     double *drow = dots + (size_t)(b * 64 + lane) * pitch;
@@ -217,7 +262,7 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
         for (int j = 0; j < IS_HB; j++) acc[j] = 0.0;
         /* q for the next 16 columns is loaded while the current 16 compute */
         float qf[IS_HB], qn[IS_HB];
-        q_cols(qf, q, h0, H, D, 0, lane);
+        q_cols(qf, qs, h0, H, D, 0, lane);
         if (VEC) {
             constexpr int CPP = 16 / ES;        /* columns per 16-byte piece */
             constexpr int BLK = 8 * CPP;        /* columns per batch of loads */
@@ -235,7 +280,7 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
 #pragma unroll
                         for (int pc = 0; pc < 16 / CPP; pc++)
                             key_piece<KF>(v[u16 * (16 / CPP) + pc], rs, k + pc * CPP);
-                        q_cols(qn, q, h0, H, D, cc + 16, lane);
+                        q_cols(qn, qs, h0, H, D, cc + 16, lane);
                         if (cc + 16 <= D) chain_16<true>(acc, qf, k, 16, nh);
                         else              chain_16<false>(acc, qf, k, D - cc, nh);
 #pragma unroll
@@ -256,7 +301,7 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
                     else
                         k[e] = ((const float *)row)[c];
                 }
-                q_cols(qn, q, h0, H, D, c0 + 16, lane);
+                q_cols(qn, qs, h0, H, D, c0 + 16, lane);
                 if (c0 + 16 <= D) chain_16<true>(acc, qf, k, 16, nh);
                 else              chain_16<false>(acc, qf, k, D - c0, nh);
 #pragma unroll
@@ -285,21 +330,21 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
                          fkey(sc) >> 21, lane);
 }
 
-template <int KF, int HIST>
+template <int KF, int HIST, int MW>
 void launch_iscore(bool vec, int grid, int thr, size_t lds, hipStream_t st,
                    float *d_out, uint32_t *hist, uint32_t *meta, const float *d_q,
                    const float *d_w,
                    int H, int HP, int D, const void *d_keys, const float *d_ks,
-                   int key_stride, int n, float scale, int ng)
+                   int key_stride, int n, float scale, int ng, const Dsv4Rope &qr)
 {
     if (vec)
-        hipLaunchKernelGGL((k_iscore<KF, 1, HIST>), dim3(grid), dim3(thr), lds, st, d_out,
+        hipLaunchKernelGGL((k_iscore<KF, 1, HIST, MW>), dim3(grid), dim3(thr), lds, st, d_out,
                            hist, meta, d_q, d_w, H, HP, D, d_keys, d_ks, key_stride, n, scale,
-                           ng);
+                           ng, qr);
     else
-        hipLaunchKernelGGL((k_iscore<KF, 0, HIST>), dim3(grid), dim3(thr), lds, st, d_out,
+        hipLaunchKernelGGL((k_iscore<KF, 0, HIST, MW>), dim3(grid), dim3(thr), lds, st, d_out,
                            hist, meta, d_q, d_w, H, HP, D, d_keys, d_ks, key_stride, n, scale,
-                           ng);
+                           ng, qr);
 }
 
 /* --------------------------------------------------------------- top-k */
@@ -697,6 +742,35 @@ k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
     if (sub == 0 && e < c_gt) idxs[r] = (int)(0xFFFFFFFFu - (uint32_t)mine);
 }
 
+/* Top-k of a short score vector (n <= TS_NMAX) in one launch: every
+ * element's 64-bit composite (order key << 32 | ~index: descending composite
+ * order is score descending, ties to the lower index) is ranked by counting
+ * the composites above it -- the composites are distinct, so the ranks are
+ * a permutation -- and the elements ranked below k land at idxs[rank]. A
+ * workgroup stages all n composites in LDS and ranks TS_EPW elements, four
+ * threads per element each counting a quarter of the vector. */
+constexpr int TS_NMAX = 4096;
+constexpr int TS_EPW = 64;
+
+__global__ void __launch_bounds__(256)
+k_tk_small(int *__restrict__ idxs, const float *__restrict__ scores, int n, int k)
+{
+    __shared__ unsigned long long comp[TS_NMAX];
+    for (int i = threadIdx.x; i < n; i += 256)
+        comp[i] = ((unsigned long long)fkey(scores[i]) << 32) | (0xFFFFFFFFu - (uint32_t)i);
+    __syncthreads();
+    const int e = blockIdx.x * TS_EPW + (int)(threadIdx.x >> 2);
+    const int qtr = threadIdx.x & 3;
+    const unsigned long long me = comp[min(e, n - 1)];
+    const int per = (n + 3) >> 2;
+    const int j0 = qtr * per, j1 = min(n, j0 + per);
+    int cnt = 0;
+    for (int j = j0; j < j1; j++) cnt += comp[j] > me ? 1 : 0;
+    cnt += __shfl_xor(cnt, 1, 64);
+    cnt += __shfl_xor(cnt, 2, 64);
+    if (qtr == 0 && e < n && cnt < k) idxs[cnt] = e;
+}
+
 /* ----------------------------------------------------- sparse attention */
 
 constexpr int AT_THREADS = 256;
@@ -748,7 +822,8 @@ k_attn_partial(float *__restrict__ pm, float *__restrict__ pl,
                float *__restrict__ po, const float *__restrict__ q,
                const void *__restrict__ kv, int kv_stride,
                const int *__restrict__ idxs, int kv_rows, int h, int d_qk,
-               int d_v, int topk, float scale, int SR, int rowb, int vec)
+               int d_v, int topk, float scale, int SR, int rowb, int vec, int qnorm,
+               float qeps, Dsv4Rope qrp)
 {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds_b[];
     constexpr int ES = KVF == DSV4_GPU_KV_BF16 ? 2 : 4;
@@ -792,6 +867,34 @@ k_attn_partial(float *__restrict__ pm, float *__restrict__ pl,
         }
     }
     __syncthreads();
+    if (qnorm || qrp.rd) {
+        /* the attention block's q: each head scaled by 1/sqrt(mean square +
+         * eps) and RoPE'd at pos (dsv4_layer.c:223-231), a wave per head */
+        const int t0 = d_qk - qrp.rd;
+        for (int hh = wid; hh < AT_HB; hh += AT_THREADS / 64) {
+            float *qh = qs + hh * ldq;
+            float inv = 1.0f;
+            if (qnorm) {
+                double sq = 0.0;
+                for (int c = lane; c < d_qk; c += 64) {
+                    const double v = (double)qh[c];
+                    sq += v * v;
+                }
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
+                inv = (float)(1.0 / sqrt(sq / (double)d_qk + (double)qeps));
+                for (int c = lane; c < t0; c += 64) qh[c] = qh[c] * inv;
+            }
+            for (int p = lane; p < qrp.rd / 2; p += 64) {
+                float a = qh[t0 + 2 * p], b = qh[t0 + 2 * p + 1];
+                if (qnorm) { a = a * inv; b = b * inv; }
+                rope_pair(a, b, qrp, p);
+                qh[t0 + 2 * p] = a;
+                qh[t0 + 2 * p + 1] = b;
+            }
+        }
+        __syncthreads();
+    }
 
     /* stage the rows */
     if (vec) {
@@ -908,7 +1011,7 @@ constexpr int CB_SPLITS = 1024;
 __global__ void __launch_bounds__(CB_COLS)
 k_attn_combine(float *__restrict__ o, const float *__restrict__ pm,
                const float *__restrict__ pl, const float *__restrict__ po,
-               const float *__restrict__ sink, int nsplit, int d_v)
+               const float *__restrict__ sink, int nsplit, int d_v, Dsv4Rope orp)
 {
     const int hh = blockIdx.x;
     __shared__ float fs[CB_SPLITS];
@@ -953,7 +1056,20 @@ k_attn_combine(float *__restrict__ o, const float *__restrict__ pm,
         for (int u = 0; u < B; u++)
             v[u] = po[((size_t)hh * nsplit + min(s0 + u, nsplit - 1)) * d_v + cc];
     }
-    if (live) o[(size_t)hh * d_v + c] = acc * inv;
+    float val = acc * inv;
+    if (orp.rd) {
+        /* the output's de-rotation (dsv4_layer.c:304-305): column pairs
+         * (t0 + 2p, t0 + 2p + 1) sit in neighbouring lanes */
+        const float other = __shfl_xor(val, 1, 64);
+        const int t0 = d_v - orp.rd;
+        if (c >= t0 && live) {
+            const bool odd = (c - t0) & 1;
+            float a = odd ? other : val, b = odd ? val : other;
+            rope_pair(a, b, orp, (c - t0) >> 1);
+            val = odd ? b : a;
+        }
+    }
+    if (live) o[(size_t)hh * d_v + c] = val;
 }
 
 /* ------------------------------------------ sparse attention, matrix core */
@@ -1233,22 +1349,43 @@ size_t attn_mc_lds(int kv_fmt, int h, int d_qk, int d_v, int kv_stride)
 
 /* Rows per split: the staged rows, q and the scores must fit the LDS a
  * workgroup may use. */
-int attn_split_rows(int kv_fmt, int d_qk, int d_v, int *rowb_out, size_t *lds_out)
+size_t attn_partial_lds(int sr, int d_qk, int rowb)
+{
+    return (size_t)AT_HB * (d_qk + 4) * 4 + (size_t)sr * rowb + (size_t)sr * AT_HB * 4 +
+           (size_t)sr * 4;
+}
+
+/* Rows per split of the VALU form: the most that fit the LDS (at most 64),
+ * halved while the grid would leave most CUs idle (splits x head groups
+ * below two per CU), down to AT_SR_MIN -- the staged rows' LDS traffic of a
+ * split grows with its rows, so short selections spread over more CUs. With
+ * topk < 0 only the LDS bound applies. */
+constexpr int AT_SR_MIN = 16;
+
+int attn_split_rows(int kv_fmt, int d_qk, int d_v, int *rowb_out, size_t *lds_out,
+                    int h = 0, int topk = -1)
 {
     const size_t cap = dsv4_lds_limit();
     const int es = kv_fmt == DSV4_GPU_KV_BF16 ? 2 : 4;
     const int dmax = d_qk > d_v ? d_qk : d_v;
     const int rowb = ((dmax * es + 15) / 16) * 16 + 16;          /* +16 B: bank skew */
-    for (int sr = 64; sr >= 1; sr >>= 1) {
-        const size_t lds = (size_t)AT_HB * (d_qk + 4) * 4 + (size_t)sr * rowb +
-                           (size_t)sr * AT_HB * 4 + (size_t)sr * 4;
-        if (lds <= cap) {
-            *rowb_out = rowb;
-            *lds_out = lds;
-            return sr;
+    int sr = 64;
+    while (sr >= 1 && attn_partial_lds(sr, d_qk, rowb) > cap) sr >>= 1;
+    if (sr < 1) return 0;
+    if (topk > 0) {
+        static int cus = 0;
+        if (!cus) {
+            int dev = 0, v = 0;
+            cus = (hipGetDevice(&dev) == hipSuccess &&
+                   hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) ==
+                       hipSuccess && v > 0) ? v : 256;
         }
+        const int hg = (h + AT_HB - 1) / AT_HB;
+        while (sr > AT_SR_MIN && ((topk + sr - 1) / sr) * hg < 2 * cus) sr >>= 1;
     }
-    return 0;
+    *rowb_out = rowb;
+    *lds_out = attn_partial_lds(sr, d_qk, rowb);
+    return sr;
 }
 
 } // namespace
@@ -1274,18 +1411,21 @@ size_t dsv4_index_scratch_bytes(int n)
 
 int dsv4_topk_takes_hist(int n, int k)
 {
-    return k > 0 && n >= k && n <= TK_NMAX && k <= TK_KMAX;
+    return k > 0 && n >= k && n > TS_NMAX && n <= TK_NMAX && k <= TK_KMAX;
 }
 
-int dsv4_indexer_score_launch(float *d_out, const float *d_q, const float *d_w,
-                              int H, int D, const void *d_keys,
-                              const float *d_key_scales, int key_fmt,
-                              int key_stride, int n, float scale, void *scratch,
-                              int with_hist, hipStream_t st)
+int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *d_w,
+                                   int H, int D, const void *d_keys,
+                                   const float *d_key_scales, int key_fmt,
+                                   int key_stride, int n, float scale, void *scratch,
+                                   int with_hist, const float *rope_cs,
+                                   const float *rope_sn, int rope_pos, int rope_half,
+                                   int rope_dim, hipStream_t st)
 {
-    if (H <= 0 || D <= 0 || n < 0 || key_stride < D || H > 256) {
-        DSV4_ERR("indexer score: bad shape H %d D %d n %d stride %d",
-                 H, D, n, key_stride);
+    if (H <= 0 || D <= 0 || n < 0 || key_stride < D || H > 256 || rope_dim < 0 ||
+        (rope_dim & 1) || rope_dim > D || (rope_dim && (!rope_cs || !rope_sn))) {
+        DSV4_ERR("indexer score: bad shape H %d D %d n %d stride %d rope %d",
+                 H, D, n, key_stride, rope_dim);
         return -1;
     }
     if (key_fmt == DSV4_GPU_KV_FP8 && !d_key_scales) {
@@ -1301,11 +1441,15 @@ int dsv4_indexer_score_launch(float *d_out, const float *d_q, const float *d_w,
     const int HP = ix_heads_padded(H);
     /* four waves per workgroup where the heads allow it: one wave per SIMD
      * of a CU (up to 4 head waves per block of 64 rows, blocks filling the
-     * rest) */
+     * rest); f32 keys (the attention block's compressed rows: few rows, many
+     * heads) take up to 8 head waves, two per SIMD */
     const int groups = HP / IS_HB;
-    const int ng = groups < 4 ? groups : 4;
-    const int kb = 4 / ng;
-    const size_t lds = sizeof(double) * ((size_t)64 * kb * (HP + 1) + HP);
+    const bool mw8 = key_fmt == DSV4_GPU_KV_F32 && groups >= 8;
+    const int mw = mw8 ? 8 : IS_MAXW;
+    const int ng = groups < mw ? groups : mw;
+    const int kb = mw / ng;
+    const size_t lds = sizeof(double) * ((size_t)64 * kb * (HP + 1) + HP) +
+                       sizeof(float) * (size_t)H * D;
     if (lds > dsv4_lds_limit()) {
         DSV4_ERR("indexer score: %d heads do not fit in LDS", H);
         return -1;
@@ -1314,12 +1458,14 @@ int dsv4_indexer_score_launch(float *d_out, const float *d_q, const float *d_w,
     if (!lds_opted) {
         const int cap = (int)dsv4_lds_limit();
         const void *fns[] = {
-            (const void *)k_iscore<DSV4_GPU_KV_FP8, 1, 0>, (const void *)k_iscore<DSV4_GPU_KV_FP8, 1, 1>,
-            (const void *)k_iscore<DSV4_GPU_KV_FP8, 0, 0>, (const void *)k_iscore<DSV4_GPU_KV_FP8, 0, 1>,
-            (const void *)k_iscore<DSV4_GPU_KV_BF16, 1, 0>, (const void *)k_iscore<DSV4_GPU_KV_BF16, 1, 1>,
-            (const void *)k_iscore<DSV4_GPU_KV_BF16, 0, 0>, (const void *)k_iscore<DSV4_GPU_KV_BF16, 0, 1>,
-            (const void *)k_iscore<DSV4_GPU_KV_F32, 1, 0>, (const void *)k_iscore<DSV4_GPU_KV_F32, 1, 1>,
-            (const void *)k_iscore<DSV4_GPU_KV_F32, 0, 0>, (const void *)k_iscore<DSV4_GPU_KV_F32, 0, 1>};
+            (const void *)k_iscore<DSV4_GPU_KV_FP8, 1, 0, 4>, (const void *)k_iscore<DSV4_GPU_KV_FP8, 1, 1, 4>,
+            (const void *)k_iscore<DSV4_GPU_KV_FP8, 0, 0, 4>, (const void *)k_iscore<DSV4_GPU_KV_FP8, 0, 1, 4>,
+            (const void *)k_iscore<DSV4_GPU_KV_BF16, 1, 0, 4>, (const void *)k_iscore<DSV4_GPU_KV_BF16, 1, 1, 4>,
+            (const void *)k_iscore<DSV4_GPU_KV_BF16, 0, 0, 4>, (const void *)k_iscore<DSV4_GPU_KV_BF16, 0, 1, 4>,
+            (const void *)k_iscore<DSV4_GPU_KV_F32, 1, 0, 4>, (const void *)k_iscore<DSV4_GPU_KV_F32, 1, 1, 4>,
+            (const void *)k_iscore<DSV4_GPU_KV_F32, 0, 0, 4>, (const void *)k_iscore<DSV4_GPU_KV_F32, 0, 1, 4>,
+            (const void *)k_iscore<DSV4_GPU_KV_F32, 1, 0, 8>, (const void *)k_iscore<DSV4_GPU_KV_F32, 1, 1, 8>,
+            (const void *)k_iscore<DSV4_GPU_KV_F32, 0, 0, 8>, (const void *)k_iscore<DSV4_GPU_KV_F32, 0, 1, 8>};
         for (const void *f : fns)
             (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, cap);
         (void)hipGetLastError();
@@ -1327,27 +1473,44 @@ int dsv4_indexer_score_launch(float *d_out, const float *d_q, const float *d_w,
     }
     uint32_t *hist = with_hist ? (uint32_t *)((char *)scratch + IX_HIST) : nullptr;
     uint32_t *meta = with_hist ? (uint32_t *)((char *)scratch + IX_META) : nullptr;
+    Dsv4Rope qr;
+    if (rope_dim) {
+        qr.cs = rope_cs; qr.sn = rope_sn; qr.pos = rope_pos; qr.half = rope_half;
+        qr.rd = rope_dim;
+    }
 
     const int es = key_fmt == DSV4_GPU_KV_F32 ? 4 : key_fmt == DSV4_GPU_KV_BF16 ? 2 : 1;
     const bool vec = ((size_t)D * es) % 16 == 0 && ((size_t)key_stride * es) % 16 == 0 &&
                      ((uintptr_t)d_keys & 15) == 0;
     const int grid = (n + 64 * kb - 1) / (64 * kb);
     const int thr = 64 * ng * kb;
-#define DSV4_ISCORE(KF)                                                                 \
+#define DSV4_ISCORE(KF, MW)                                                             \
     do {                                                                                \
         if (with_hist)                                                                  \
-            launch_iscore<KF, 1>(vec, grid, thr, lds, st, d_out, hist, meta, d_q, d_w, H, HP, \
-                                 D, d_keys, d_key_scales, key_stride, n, scale, ng);    \
+            launch_iscore<KF, 1, MW>(vec, grid, thr, lds, st, d_out, hist, meta, d_q, d_w, H, \
+                                     HP, D, d_keys, d_key_scales, key_stride, n, scale, ng, qr); \
         else                                                                            \
-            launch_iscore<KF, 0>(vec, grid, thr, lds, st, d_out, hist, meta, d_q, d_w, H, HP, \
-                                 D, d_keys, d_key_scales, key_stride, n, scale, ng);    \
+            launch_iscore<KF, 0, MW>(vec, grid, thr, lds, st, d_out, hist, meta, d_q, d_w, H, \
+                                     HP, D, d_keys, d_key_scales, key_stride, n, scale, ng, qr); \
     } while (0)
-    if (key_fmt == DSV4_GPU_KV_FP8) DSV4_ISCORE(DSV4_GPU_KV_FP8);
-    else if (key_fmt == DSV4_GPU_KV_BF16) DSV4_ISCORE(DSV4_GPU_KV_BF16);
-    else DSV4_ISCORE(DSV4_GPU_KV_F32);
+    if (key_fmt == DSV4_GPU_KV_FP8) DSV4_ISCORE(DSV4_GPU_KV_FP8, 4);
+    else if (key_fmt == DSV4_GPU_KV_BF16) DSV4_ISCORE(DSV4_GPU_KV_BF16, 4);
+    else if (mw8) DSV4_ISCORE(DSV4_GPU_KV_F32, 8);
+    else DSV4_ISCORE(DSV4_GPU_KV_F32, 4);
 #undef DSV4_ISCORE
     HIP_OK(hipGetLastError(), "indexer score launch");
     return 0;
+}
+
+int dsv4_indexer_score_launch(float *d_out, const float *d_q, const float *d_w,
+                              int H, int D, const void *d_keys,
+                              const float *d_key_scales, int key_fmt,
+                              int key_stride, int n, float scale, void *scratch,
+                              int with_hist, hipStream_t st)
+{
+    return dsv4_indexer_score_rope_launch(d_out, d_q, d_w, H, D, d_keys, d_key_scales, key_fmt,
+                                          key_stride, n, scale, scratch, with_hist, nullptr,
+                                          nullptr, 0, 0, 0, st);
 }
 
 int dsv4_topk_launch(int *d_idxs, const float *d_scores, int n, int k,
@@ -1363,6 +1526,12 @@ int dsv4_topk_launch(int *d_idxs, const float *d_scores, int n, int k,
     if (hist_ready && !dsv4_topk_takes_hist(n, k)) {
         DSV4_ERR("topk: a level-1 histogram was built for n %d k %d", n, k);
         return -1;
+    }
+    if (n <= TS_NMAX) {
+        hipLaunchKernelGGL(k_tk_small, dim3((n + TS_EPW - 1) / TS_EPW), dim3(256), 0, st,
+                           d_idxs, d_scores, n, k);
+        HIP_OK(hipGetLastError(), "topk (short) launch");
+        return 0;
     }
     char *sb = (char *)scratch;
     uint32_t *hist = (uint32_t *)(sb + IX_HIST);
@@ -1389,18 +1558,35 @@ size_t dsv4_attn_scratch_bytes(int h, int d_qk, int d_v, int topk, int kv_fmt)
 {
     int rowb;
     size_t lds;
-    const int sr = attn_split_rows(kv_fmt, d_qk, d_v, &rowb, &lds);
+    int sr = attn_split_rows(kv_fmt, d_qk, d_v, &rowb, &lds);
     if (sr <= 0) return 0;
+    if (sr > AT_SR_MIN) sr = AT_SR_MIN;      /* any smaller topk may split this finely */
     const size_t nsplit = (size_t)(topk > 0 ? (topk + sr - 1) / sr : 1);
     return sizeof(float) * (size_t)h * nsplit * (2 + (size_t)d_v);
 }
 
-int dsv4_attn_launch(float *d_o, const float *d_q, const void *d_kv,
-                     int kv_fmt, int kv_stride, int kv_rows,
-                     const float *d_sink, const int *d_idxs, int h, int d_qk,
-                     int d_v, int topk, float scale, void *scratch,
-                     hipStream_t st)
+int dsv4_attn_block_launch(float *d_o, const float *d_q, const void *d_kv,
+                           int kv_fmt, int kv_stride, int kv_rows,
+                           const float *d_sink, const int *d_idxs, int h, int d_qk,
+                           int d_v, int topk, float scale, void *scratch, int q_norm,
+                           float q_eps, const float *rope_cs, const float *rope_sn,
+                           int rope_pos, int rope_half, int rope_dim, hipStream_t st)
 {
+    if (rope_dim < 0 || (rope_dim & 1) || rope_dim > d_qk || rope_dim > d_v ||
+        (rope_dim && ((d_v & 1) || !rope_cs || !rope_sn))) {
+        DSV4_ERR("sparse attn: bad RoPE (dim %d, d_qk %d, d_v %d)", rope_dim, d_qk, d_v);
+        return -1;
+    }
+    Dsv4Rope qrp, orp;
+    if (rope_dim) {
+        qrp.cs = orp.cs = rope_cs;
+        qrp.sn = orp.sn = rope_sn;
+        qrp.pos = orp.pos = rope_pos;
+        qrp.half = orp.half = rope_half;
+        qrp.rd = orp.rd = rope_dim;
+        orp.inverse = 1;
+    }
+    const bool qx = q_norm || rope_dim;
     if (h <= 0 || d_qk <= 0 || d_v <= 0 || topk < 0 || kv_stride < d_qk ||
         kv_stride < d_v) {
         DSV4_ERR("sparse attn: bad shape h %d d_qk %d d_v %d stride %d",
@@ -1413,7 +1599,7 @@ int dsv4_attn_launch(float *d_o, const float *d_q, const void *d_kv,
     }
     int rowb;
     size_t lds;
-    const int sr = attn_split_rows(kv_fmt, d_qk, d_v, &rowb, &lds);
+    const int sr = attn_split_rows(kv_fmt, d_qk, d_v, &rowb, &lds, h, topk);
     if (sr <= 0) {
         DSV4_ERR("sparse attn: d_qk %d / d_v %d too wide", d_qk, d_v);
         return -1;
@@ -1447,7 +1633,8 @@ int dsv4_attn_launch(float *d_o, const float *d_q, const void *d_kv,
      * the VALU form) */
     const size_t mc_lds = attn_mc_lds(kv_fmt, h, d_qk, d_v, kv_stride);
     const char *mc_env = getenv("DSV4_GPU_ATTN_MC");
-    if (mc_lds && topk > 0 && ((uintptr_t)d_kv & 15) == 0 && !(mc_env && atoi(mc_env) == 0)) {
+    if (mc_lds && !qx && topk > 0 && ((uintptr_t)d_kv & 15) == 0 &&
+        !(mc_env && atoi(mc_env) == 0)) {
         const int ns = (topk + AM_SR - 1) / AM_SR;          /* <= nsplit: sr <= AM_SR */
         pl = pm + (size_t)h * ns;
         po = pl + (size_t)h * ns;
@@ -1456,21 +1643,32 @@ int dsv4_attn_launch(float *d_o, const float *d_q, const void *d_kv,
                            d_qk, d_v, topk, scale);
         HIP_OK(hipGetLastError(), "attn mc launch");
         hipLaunchKernelGGL(k_attn_combine, dim3(h, (d_v + CB_COLS - 1) / CB_COLS),
-                           dim3(CB_COLS), 0, st, d_o, pm, pl, po, d_sink, ns, d_v);
+                           dim3(CB_COLS), 0, st, d_o, pm, pl, po, d_sink, ns, d_v, orp);
         HIP_OK(hipGetLastError(), "attn combine launch");
         return 0;
     }
     if (kv_fmt == DSV4_GPU_KV_BF16)
         hipLaunchKernelGGL((k_attn_partial<DSV4_GPU_KV_BF16>), grid, dim3(AT_THREADS), lds, st,
                            pm, pl, po, d_q, d_kv, kv_stride, d_idxs, kv_rows, h,
-                           d_qk, d_v, topk, scale, sr, rowb, vec);
+                           d_qk, d_v, topk, scale, sr, rowb, vec, q_norm, q_eps, qrp);
     else
         hipLaunchKernelGGL((k_attn_partial<DSV4_GPU_KV_F32>), grid, dim3(AT_THREADS), lds, st,
                            pm, pl, po, d_q, d_kv, kv_stride, d_idxs, kv_rows, h,
-                           d_qk, d_v, topk, scale, sr, rowb, vec);
+                           d_qk, d_v, topk, scale, sr, rowb, vec, q_norm, q_eps, qrp);
     HIP_OK(hipGetLastError(), "attn partial launch");
     hipLaunchKernelGGL(k_attn_combine, dim3(h, (d_v + CB_COLS - 1) / CB_COLS),
-                       dim3(CB_COLS), 0, st, d_o, pm, pl, po, d_sink, nsplit, d_v);
+                       dim3(CB_COLS), 0, st, d_o, pm, pl, po, d_sink, nsplit, d_v, orp);
     HIP_OK(hipGetLastError(), "attn combine launch");
     return 0;
+}
+
+int dsv4_attn_launch(float *d_o, const float *d_q, const void *d_kv,
+                     int kv_fmt, int kv_stride, int kv_rows,
+                     const float *d_sink, const int *d_idxs, int h, int d_qk,
+                     int d_v, int topk, float scale, void *scratch,
+                     hipStream_t st)
+{
+    return dsv4_attn_block_launch(d_o, d_q, d_kv, kv_fmt, kv_stride, kv_rows, d_sink, d_idxs,
+                                  h, d_qk, d_v, topk, scale, scratch, 0, 0.0f, nullptr,
+                                  nullptr, 0, 0, 0, st);
 }

@@ -106,7 +106,8 @@ def test_topk_ties_and_edges(gpu, dsv4):
 
 @pytest.mark.parametrize("n,k,levels", [(32768, 2048, 40), (5000, 4096, 7), (1025, 1, 3),
                                         (3000, 3000, 1000000), (100000, 512, 1000000),
-                                        (77, 13, 5)])
+                                        (77, 13, 5), (4096, 4096, 50), (4097, 100, 50),
+                                        (512, 512, 1000000), (4096, 1, 2)])
 def test_topk_random_with_ties(gpu, dsv4, n, k, levels):
     rng = np.random.default_rng(n + k)
     s = (rng.integers(-levels, levels, size=n) / 8.0).astype(np.float32)
@@ -114,8 +115,10 @@ def test_topk_random_with_ties(gpu, dsv4, n, k, levels):
 
 
 def test_topk_all_equal(gpu, dsv4):
-    s = np.full(9000, 0.25, np.float32)
-    assert np.array_equal(dsv4.topk(s, 2048), np.arange(2048))
+    """Both paths: the ranked one (up to 4096 scores) and the radix select."""
+    for n in (9000, 4000):
+        s = np.full(n, 0.25, np.float32)
+        assert np.array_equal(dsv4.topk(s, 2048), np.arange(2048))
 
 
 # ----------------------------------------------------------- attention

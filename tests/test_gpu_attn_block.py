@@ -44,3 +44,23 @@ def test_attention_block_matches_reference(tmp_path):
     assert any(int(i) for _, _, i, _ in per)          # a CSA layer selected on the device
     rels = [float(x) for x in re.findall(r"pos \d+ rel (\S+)", p.stdout)]
     assert len(rels) == 160 and max(rels) > 0.0       # the device really computed it
+
+
+@pytest.mark.parametrize("n,ratio", [(24, 4), (132, 128), (20, 0)])
+def test_attention_block_flash_shapes(n, ratio):
+    """The same comparison at the DeepSeek-V4-Flash attention shapes (hidden
+    4096, 64 heads x 512, q_lora 1024, wo_a 8 x 1024, window 128, indexer 64
+    x 128), synthetic weights, one layer of each compress ratio; at 132
+    positions the ratio-128 compressor has closed one window, so the last
+    positions attend to a compressed row."""
+    print("attn flash: %d positions, ratio %d" % (n, ratio), flush=True)
+    p = subprocess.run([ATTN, "--flash", str(n), str(ratio), "--tol", "1e-5"],
+                       capture_output=True, text=True, timeout=300)
+    line = [l for l in p.stdout.splitlines() if l.startswith("flash:")]
+    print(line, flush=True)
+    assert p.returncode == 0, p.stdout[-3000:] + p.stderr[-2000:]
+    m = re.search(r"flash: ratio (\d+) positions (\d+) worst_rel (\S+) over_tol (\d+)",
+                  p.stdout)
+    assert m and int(m.group(2)) == n and int(m.group(4)) == 0
+    rels = [float(x) for x in re.findall(r"flash pos \d+ rel (\S+)", p.stdout)]
+    assert len(rels) == n and max(rels) > 0.0

@@ -34,6 +34,11 @@
  *     / dsv4_gpu_topk / dsv4_gpu_sparse_attn in pass 2 and the reference's
  *     own functions otherwise -- the call sites INTEGRATION.md shows, made
  *     with the preprocessor instead of an edit.
+ *   - pass 3 (GPU runs): the same, with every layer's attention() taken
+ *     from the device attention block (dsv4_gpu_attn_step, one call per
+ *     layer and position) and its routed experts' k-ordered sum from the
+ *     fused pass (dsv4_gpu_moe_fp4), through the matmul hooks described at
+ *     e2e_mmq.
  * Routed experts come from memory (all resident).
  *
  * usage: dsv4_e2e CKPT_DIR TOKENS_FILE [--cpu-only]
@@ -119,6 +124,59 @@ void e2e_sparse_attn(float *o, const float *q, const float *kv, const float *sin
         csa_fail("sparse attention");
     dsv4_gpu_kv_free(cache);
     g_n_attn++;
+}
+
+/* ------------------------------------------- the attention block ---- */
+/* Pass 3: dsv4_layer.c is also compiled with dsv4_mmq renamed to e2e_mmq.
+ * attention()'s first matmul (wq_a, dsv4_layer.c:220) then also runs the
+ * whole block on the device, dsv4_gpu_attn_step, from the same x; its last
+ * (wo_b, :335) returns the block's output instead of computing its own. So
+ * the layer carries on from the device block's result, while the body in
+ * between still runs on its own (its results unused). The routed experts'
+ * sum is replaced the same way by dsv4_gpu_moe_fp4 (below). Every other
+ * matmul passes through to the reference's dispatch. */
+void dsv4_mmq(float *y, const float *x, const DSV4QMat *m);
+
+static int g_attn_block, g_attn_nl, g_attn_pos, g_attn_pending = -1;
+static const DSV4LayerBind *g_attn_lb;
+static const DSV4Cfg *g_cfg;
+static DSV4Scratch *g_scr;
+static float *g_attn_out;
+static long g_n_block, g_n_moe;
+
+void e2e_mmq(float *y, const float *x, const DSV4QMat *m)
+{
+    if (g_attn_block) {
+        for (int L = 0; L < g_attn_nl; L++) {
+            /* moe() (dsv4_layer.c:369-484) has summed the routed experts in k
+             * order into its output, s->qr (:518), when the shared expert's
+             * first matmul (:480) arrives with the same x: replace that sum
+             * with the fused routed-expert pass, from the router's own
+             * selection and weights (s->topk_idx, s->topk_w) */
+            if (m == &g_attn_lb[L].w.moe.shared.w1) {
+                const DSV4Cfg *c = g_cfg;
+                if (dsv4_gpu_moe_fp4(g_attn_out, x, L, g_scr->topk_idx, g_scr->topk_w, c->topk,
+                                     c->hidden, c->moe_inter, c->swiglu_limit) != 0)
+                    csa_fail("routed experts");
+                memcpy(g_scr->qr, g_attn_out, (size_t)c->hidden * sizeof(float));
+                g_n_moe++;
+                break;
+            }
+            if (m == &g_attn_lb[L].w.attn.wq_a) {
+                if (dsv4_gpu_attn_step(g_attn_out, x, L, g_attn_pos) != 0)
+                    csa_fail("attention block");
+                g_attn_pending = L;
+                g_n_block++;
+                break;
+            }
+            if (m == &g_attn_lb[L].w.attn.wo_b && g_attn_pending == L) {
+                memcpy(y, g_attn_out, (size_t)m->rows * sizeof(float));
+                g_attn_pending = -1;
+                return;
+            }
+        }
+    }
+    dsv4_mmq(y, x, m);
 }
 
 /* ---------------------------------------------------- routed experts ---- */
@@ -265,6 +323,7 @@ static int run_pass(const Model *M, const int *tok, int n, float *logits)
         if (dsv4_state_init(&ls[L], c, L, M->maxpos) != 0) return -1;
     DSV4QMat head = {M->mb->w.head, NULL, DSV4_WBF16, c->vocab, d, 0, 0};
     for (int pos = 0; pos < n; pos++) {
+        g_attn_pos = pos;
         dsv4_embed_row(y, M->mb->w.embed, M->mb->w.wdt, tok[pos], d);
         for (int j = 0; j < hc; j++) memcpy(h + (size_t)j * d, y, (size_t)d * sizeof(float));
         for (int L = 0; L < c->n_layers; L++) {
@@ -411,6 +470,55 @@ int main(int argc, char **argv)
         g_gpu_csa = 0;
     }
 
+    /* pass 3: every layer's attention() from the device block */
+    int agree3 = 0;
+    double worst3 = 0.0;
+    float *got3 = NULL;
+    if (!cpu_only) {
+        for (int L = 0; L < c.n_layers; L++) {
+            const DSV4AttnW *a = &lb[L].w.attn;
+            const int ratio = dsv4_compress_ratio(&c, L);
+            dsv4_gpu_attn_cfg ac = {
+                .hidden = c.hidden, .q_lora = c.q_lora, .n_heads = c.n_heads,
+                .head_dim = c.head_dim, .rope_dim = c.qk_rope, .window = c.sliding_window,
+                .ratio = ratio, .idx_heads = a->has_idx ? c.index_n_heads : 0,
+                .idx_dim = c.index_head_dim, .idx_topk = c.index_topk, .o_groups = c.o_groups,
+                .o_lora = c.o_lora, .max_pos = M.maxpos, .rms_eps = c.rms_eps};
+            dsv4_gpu_attn_w aw = {
+                .wq_a = a->wq_a, .wq_b = a->wq_b, .wkv = a->wkv, .wo_a = a->wo_a,
+                .wo_b = a->wo_b, .q_norm = a->q_norm, .kv_norm = a->kv_norm, .sink = a->sink,
+                .rope_cos = ratio ? M.cs_c : M.cs_d, .rope_sin = ratio ? M.sn_c : M.sn_d};
+            if (a->has_comp) {
+                aw.comp_wkv = a->comp.wkv; aw.comp_wgate = a->comp.wgate;
+                aw.comp_norm = a->comp.norm; aw.comp_ape = a->comp.ape;
+            }
+            if (a->has_idx) { aw.idx_wq_b = a->idx.wq_b; aw.idx_wproj = a->idx.weights_proj; }
+            if (dsv4_gpu_attn_bind(L, &ac, &aw) != 0) return 1;
+        }
+        for (int L = 0; L < c.n_layers; L++)
+            for (int e = 0; e < c.n_experts; e++)
+                if (dsv4_gpu_upload_expert(L, e, &E.w[(size_t)L * c.n_experts + e]) != 0)
+                    return 1;
+        g_attn_lb = lb;
+        g_attn_nl = c.n_layers;
+        g_cfg = &c;
+        g_scr = &s;
+        g_attn_out = malloc((size_t)c.hidden * sizeof(float));
+        got3 = malloc((size_t)n * c.vocab * sizeof(float));
+        if (!g_attn_out || !got3) return 1;
+        g_attn_block = 1;
+        if (run_pass(&M, tok, n, got3) != 0) return 1;
+        g_attn_block = 0;
+        for (int p = 0; p < n; p++) {
+            const int ar = argmax(ref + (size_t)p * c.vocab, c.vocab, NULL);
+            const int ag = argmax(got3 + (size_t)p * c.vocab, c.vocab, NULL);
+            const double r = vec_rel(got3 + (size_t)p * c.vocab, ref + (size_t)p * c.vocab,
+                                     c.vocab);
+            if (r > worst3) worst3 = r;
+            agree3 += ar == ag;
+        }
+    }
+
     int agree = 0;
     double worst = 0.0;
     for (int p = 0; p < n; p++) {
@@ -427,6 +535,9 @@ int main(int argc, char **argv)
            "fp4_mats %d gpu_score %ld gpu_topk %ld gpu_attn %ld bf16_mats %d "
            "head_ok %ld/%ld\n", n, agree, worst, gpu_mats, fp4_mats, g_n_score, g_n_topk,
            g_n_attn, bf16_mats, g_n_head_ok, g_n_head);
+    if (!cpu_only)
+        printf("summary3: attention blocks on the device: steps %ld argmax_equal %d "
+               "worst_rel %.3g fused_moe %ld\n", g_n_block, agree3, worst3, g_n_moe);
     if (!cpu_only) dsv4_gpu_shutdown();
-    return agree == n ? 0 : 1;
+    return (agree == n && (cpu_only || agree3 == n)) ? 0 : 1;
 }

@@ -36,4 +36,6 @@ def run(ckpt, tokens_file, cpu_only=False, timeout=300):
     summ = re.search(r"summary: positions (\d+) argmax_equal (\d+) worst_rel (\S+) "
                      r"gpu_mats (\d+) fp4_mats (\d+) gpu_score (\d+) gpu_topk (\d+) "
                      r"gpu_attn (\d+) bf16_mats (\d+) head_ok (\d+)/(\d+)", p.stdout)
+    p.summary3 = re.search(r"summary3: attention blocks on the device: steps (\d+) "
+                           r"argmax_equal (\d+) worst_rel (\S+) fused_moe (\d+)", p.stdout)
     return p, rows, summ

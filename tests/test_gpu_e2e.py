@@ -11,8 +11,13 @@ and attention()'s CSA calls -- indexer score, top-k, sparse
 attention (dsv4_layer.c:286-301) -- go to dsv4_gpu_indexer_score /
 dsv4_gpu_topk / dsv4_gpu_sparse_attn.
 
-Bar: identical argmax at every position. The logits agree within the
-reference's own whole-model tolerance, 2e-3 vector-scaled
+A third pass takes every layer's attention() output from the device
+attention block instead (dsv4_gpu_attn_step, one call per layer and
+position), and its routed experts' k-ordered sum from the fused pass
+(dsv4_gpu_moe_fp4) (oracle/e2e_decode.c, e2e_mmq).
+
+Bar: identical argmax at every position, in both GPU passes. The logits
+agree within the reference's own whole-model tolerance, 2e-3 vector-scaled
 (tests/unit/test_model_oracle.c:253-270).
 """
 import sys
@@ -46,3 +51,9 @@ def test_gpu_trunk_argmax_identical(tmp_path):
     assert int(summ.group(10)) == int(summ.group(11)) == 46   # dsv4_gpu_head_argmax
     assert worst < 2e-3
     assert any(r["rel"] > 0.0 for r in rows), "GPU pass produced CPU bits: trunk not on GPU?"
+    # pass 3: every layer's attention() output from the device attention block
+    s3 = p.summary3
+    assert s3, p.stdout[-2000:]
+    assert int(s3.group(1)) == 46 * 4 and int(s3.group(2)) == 46
+    assert float(s3.group(3)) < 2e-3
+    assert int(s3.group(4)) == 46 * 4          # every layer's routed experts fused

@@ -380,7 +380,9 @@ class Bench:
                (avail * idd * 4 if has_idx else 0))
         for lay in layers:
             L.dsv4_gpu_attn_reset(lay)
-        self._attn_keep = keep          # resident keys stay valid host memory
+        # resident matrices are keyed by host pointer: their host arrays stay
+        # allocated for the process, so no later array can reuse an address
+        self._attn_keep = getattr(self, "_attn_keep", []) + [keep]
         self.attn_graph_us = us
         return eager, eager, alg
 

@@ -1018,7 +1018,8 @@ void block_free(AttnBlock &b)
  * -inf (dsv4_compress.c:75). */
 int block_reset(AttnBlock &b)
 {
-    HIP_OK(hipStreamSynchronize(g_stream), "attn reset sync");
+    /* the state may still be in use on any stream a caller stepped it on */
+    HIP_OK(hipDeviceSynchronize(), "attn reset sync");
     const size_t kvb = (size_t)(b.c.window + b.max_comp) * b.c.head_dim * sizeof(float);
     HIP_OK(hipMemset(b.kv_cache, 0, kvb), "attn reset");
     if (b.nslot) {
@@ -1321,6 +1322,10 @@ int dsv4_gpu_attn_step_d(float *d_out, const float *d_x, int layer, int pos, voi
 {
     AttnBlock *b = block_of(layer);
     if (!b || !d_out || !d_x) return -1;
+    if (((uintptr_t)d_x | (uintptr_t)d_out) & 15) {
+        DSV4_ERR("attn_step: x and out must be 16-byte aligned");
+        return -1;
+    }
     return block_step(*b, d_out, d_x, pos, as_stream(stream));
 }
 

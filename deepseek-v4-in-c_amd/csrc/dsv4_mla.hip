@@ -197,14 +197,40 @@ struct Dsv4Rope {
     int pos = 0, half = 0, rd = 0, inverse = 0;
 };
 
-__device__ __forceinline__ void rope_pair(float &a, float &b, const Dsv4Rope &r, int p)
+__device__ __forceinline__ void rope_pair_cs(float &a, float &b, float c, float s0, int inverse)
 {
-    const float c = r.cs[(size_t)r.pos * r.half + p];
-    const float s0 = r.sn[(size_t)r.pos * r.half + p];
-    const float s = r.inverse ? -s0 : s0;
+    const float s = inverse ? -s0 : s0;
     const float re = a, im = b;
     a = re * c - im * s;
     b = re * s + im * c;
+}
+
+/* A kernel's RoPE row at pos in LDS: thread p < rd/2 loads its pair's cos
+ * and sin with rope_row_load (issued before the kernel's other loads, so the
+ * latencies overlap) and stores them with rope_row_store before the
+ * kernel's next barrier. */
+constexpr int RP_MAX = 128;                      /* rd <= 2 RP_MAX */
+struct RopeRow {
+    float c = 0.0f, s = 0.0f;
+};
+
+__device__ __forceinline__ RopeRow rope_row_load(const Dsv4Rope &r)
+{
+    RopeRow v;
+    if (r.rd && (int)threadIdx.x < r.rd / 2) {
+        v.c = r.cs[(size_t)r.pos * r.half + threadIdx.x];
+        v.s = r.sn[(size_t)r.pos * r.half + threadIdx.x];
+    }
+    return v;
+}
+
+__device__ __forceinline__ void rope_row_store(const Dsv4Rope &r, const RopeRow &v, float *rc,
+                                               float *rs)
+{
+    if (r.rd && (int)threadIdx.x < r.rd / 2) {
+        rc[threadIdx.x] = v.c;
+        rs[threadIdx.x] = v.s;
+    }
 }
 
 template <int KF, int VEC, int HIST, int MW>
@@ -226,6 +252,8 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
     const int pitch = HP + 1;
     double *wd = dots + (size_t)kb * 64 * pitch;
     float *qs = (float *)(wd + HP);
+    __shared__ float rcs[RP_MAX], rsn[RP_MAX];
+    const RopeRow rrow = rope_row_load(qr);
     for (int i = threadIdx.x; i < H; i += blockDim.x) wd[i] = (double)w[i];
     /* q into LDS (the launcher checks that it fits): batches of loads in
      * flight before any store, one memory latency per batch of 8 per thread */
@@ -239,6 +267,7 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
             if (i < H * D) qs[i] = v[u];
         }
     }
+    rope_row_store(qr, rrow, rcs, rsn);
     __syncthreads();
     if (qr.rd) {
         /* the indexer's q RoPE'd at pos, head by head (dsv4_layer.c:282-284) */
@@ -246,7 +275,7 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
         for (int i = threadIdx.x; i < H * hp; i += blockDim.x) {
             const int hh = i / hp, p = i - hh * hp;
             float *t = qs + (size_t)hh * D + (D - qr.rd) + 2 * p;
-            rope_pair(t[0], t[1], qr, p);
+            rope_pair_cs(t[0], t[1], rcs[p], rsn[p], qr.inverse);
         }
         __syncthreads();
     }
@@ -328,6 +357,130 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
     if (HIST)
         hist_push_global(hist + (blockIdx.x % TK_SLICES) * TK_BINS, t < n,
                          fkey(sc) >> 21, lane);
+}
+
+/* Few f32 keys (the attention block's compressed rows, n <= SK_NMAX): one
+ * thread per (key, head) runs that pair's fp64 fma chain over c ascending,
+ * with q (RoPE'd when asked) and the workgroup's key rows staged in LDS; a
+ * thread per key then folds the heads in order from LDS. The same arithmetic, step for step, as the
+ * reference and as k_iscore, with a workgroup of SK_THREADS / HP keys. */
+constexpr int SK_NMAX = 4096;
+constexpr int SK_THREADS = 256;
+
+__global__ void __launch_bounds__(SK_THREADS)
+k_iscore_kh(float *__restrict__ out, const float *__restrict__ q, const float *__restrict__ w,
+            int H, int HP, int D, const float *__restrict__ keys, int key_stride, int n,
+            float scale, Dsv4Rope qr)
+{
+    extern __shared__ double skl[];   /* dots[kpw][HP], w[H], q[H][D + 1], then keys[kpw][D] */
+    const int kpw = SK_THREADS / HP;
+    const int qp = D + 1;                       /* odd pitch: the heads of a wave hit distinct banks */
+    double *dots = skl;
+    double *wd = dots + (size_t)kpw * HP;
+    float *qs = (float *)(wd + H);
+    float *ksl = qs + (size_t)H * qp;
+    __shared__ float rcs[RP_MAX], rsn[RP_MAX];
+    const RopeRow rrow = rope_row_load(qr);
+    /* Staging: w, the workgroup's key rows and q. When each fits one batch
+     * (as at the attention block's shapes), every load is issued before any
+     * store: one memory latency instead of three. */
+    const int t0k = blockIdx.x * kpw;
+    const int nq4 = (H * D) >> 2;
+    if (kpw * D <= 8 * SK_THREADS && nq4 <= 8 * SK_THREADS) {
+        const double wv = (int)threadIdx.x < H ? (double)w[threadIdx.x] : 0.0;
+        float kv8[8];
+        f32x4 qv8[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = min(u * SK_THREADS + (int)threadIdx.x, kpw * D - 1);
+            const int kk = i / D, c = i - kk * D;
+            kv8[u] = keys[(size_t)min(t0k + kk, n - 1) * key_stride + c];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            qv8[u] = ldf4(q + 4 * min(u * SK_THREADS + (int)threadIdx.x, nq4 - 1));
+        if ((int)threadIdx.x < H) wd[threadIdx.x] = wv;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = u * SK_THREADS + (int)threadIdx.x;
+            if (i < kpw * D) ksl[i] = kv8[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = u * SK_THREADS + (int)threadIdx.x;
+            if (i < nq4) {
+                const int e = 4 * i, hh = e / D, c = e - hh * D;   /* D % 4 == 0 */
+                float *d = qs + (size_t)hh * qp + c;
+                d[0] = qv8[u].x; d[1] = qv8[u].y; d[2] = qv8[u].z; d[3] = qv8[u].w;
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < H; i += SK_THREADS) wd[i] = (double)w[i];
+        constexpr int KB = 8;
+        for (int i0 = 0; i0 < kpw * D; i0 += KB * SK_THREADS) {
+            float v[KB];
+#pragma unroll
+            for (int u = 0; u < KB; u++) {
+                const int i = min(i0 + u * SK_THREADS + (int)threadIdx.x, kpw * D - 1);
+                const int kk = i / D, c = i - kk * D;
+                v[u] = keys[(size_t)min(t0k + kk, n - 1) * key_stride + c];
+            }
+#pragma unroll
+            for (int u = 0; u < KB; u++) {
+                const int i = i0 + u * SK_THREADS + (int)threadIdx.x;
+                if (i < kpw * D) ksl[i] = v[u];
+            }
+        }
+        for (int i0 = 0; i0 < nq4; i0 += 8 * SK_THREADS) {
+            f32x4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                v[u] = ldf4(q + 4 * min(i0 + u * SK_THREADS + (int)threadIdx.x, nq4 - 1));
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = i0 + u * SK_THREADS + (int)threadIdx.x;
+                if (i < nq4) {
+                    const int e = 4 * i, hh = e / D, c = e - hh * D;
+                    float *d = qs + (size_t)hh * qp + c;
+                    d[0] = v[u].x; d[1] = v[u].y; d[2] = v[u].z; d[3] = v[u].w;
+                }
+            }
+        }
+    }
+    rope_row_store(qr, rrow, rcs, rsn);
+    __syncthreads();
+    if (qr.rd) {
+        const int hp = qr.rd / 2;
+        for (int i = threadIdx.x; i < H * hp; i += SK_THREADS) {
+            const int hh = i / hp, p = i - hh * hp;
+            float *t = qs + (size_t)hh * qp + (D - qr.rd) + 2 * p;
+            rope_pair_cs(t[0], t[1], rcs[p], rsn[p], qr.inverse);
+        }
+        __syncthreads();
+    }
+    const int kl = threadIdx.x / HP, h = threadIdx.x - kl * HP;
+    const int t = blockIdx.x * kpw + kl;
+    if (h < H && t < n) {
+        const float *kr = ksl + (size_t)kl * D;
+        const float *qh = qs + (size_t)h * qp;
+        double dot = 0.0;
+#pragma unroll 16
+        for (int c = 0; c < D; c++) dot = fma((double)qh[c], (double)kr[c], dot);
+        dots[kl * HP + h] = dot;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < kpw) {
+        const int tt = blockIdx.x * kpw + (int)threadIdx.x;
+        if (tt < n) {
+            double total = 0.0;
+            for (int hh = 0; hh < H; hh++) {
+                const double d = dots[threadIdx.x * HP + hh];
+                const double prod = d * wd[hh];
+                total = d > 0.0 ? total + prod : total;
+            }
+            out[tt] = (float)total * scale;
+        }
+    }
 }
 
 template <int KF, int HIST, int MW>
@@ -842,60 +995,58 @@ k_attn_partial(float *__restrict__ pm, float *__restrict__ pl,
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int dmax = d_qk > d_v ? d_qk : d_v;
 
-    if (tid < SR) {
-        const int r = tid < nj ? idxs[j0 + tid] : -1;
-        sidx[tid] = (r >= 0 && r < kv_rows) ? r : -1;            /* never a wild read */
-    }
+    __shared__ float rcs[RP_MAX], rsn[RP_MAX];
+    const RopeRow rrow = rope_row_load(qrp);
+    /* the split's row indices: loaded first, stored with q (so their wait is
+     * q's) */
+    int ridx = -1;
+    if (tid < SR && tid < nj) ridx = idxs[j0 + tid];
     /* Staging issues a whole batch of loads before storing any of them: one
      * memory latency per batch rather than per element. */
     constexpr int SB = 8;
-    for (int i0 = 0; i0 < AT_HB * d_qk; i0 += SB * AT_THREADS) {
-        float v[SB];
+    if ((d_qk & 3) == 0 && (((uintptr_t)q & 15) == 0)) {
+        /* 16-byte pieces: up to 8 x 1024 floats of q in one batch */
+        const int nq4 = (AT_HB * d_qk) >> 2;
+        for (int i0 = 0; i0 < nq4; i0 += SB * AT_THREADS) {
+            f32x4 v[SB];
 #pragma unroll
-        for (int u = 0; u < SB; u++) {
-            const int i = i0 + u * AT_THREADS + tid;
-            const int hh = i / d_qk, c = i - hh * d_qk;
-            v[u] = (i < AT_HB * d_qk && hh < nh) ? q[(size_t)(h0 + hh) * d_qk + c] : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < SB; u++) {
-            const int i = i0 + u * AT_THREADS + tid;
-            if (i < AT_HB * d_qk) {
-                const int hh = i / d_qk, c = i - hh * d_qk;
-                qs[hh * ldq + c] = v[u];
+            for (int u = 0; u < SB; u++) {
+                const int i = i0 + u * AT_THREADS + tid;
+                const int e = 4 * min(i, nq4 - 1), hh = e / d_qk, c = e - hh * d_qk;
+                v[u] = (i < nq4 && hh < nh) ? ldf4(q + (size_t)(h0 + hh) * d_qk + c)
+                                            : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             }
-        }
-    }
-    __syncthreads();
-    if (qnorm || qrp.rd) {
-        /* the attention block's q: each head scaled by 1/sqrt(mean square +
-         * eps) and RoPE'd at pos (dsv4_layer.c:223-231), a wave per head */
-        const int t0 = d_qk - qrp.rd;
-        for (int hh = wid; hh < AT_HB; hh += AT_THREADS / 64) {
-            float *qh = qs + hh * ldq;
-            float inv = 1.0f;
-            if (qnorm) {
-                double sq = 0.0;
-                for (int c = lane; c < d_qk; c += 64) {
-                    const double v = (double)qh[c];
-                    sq += v * v;
+#pragma unroll
+            for (int u = 0; u < SB; u++) {
+                const int i = i0 + u * AT_THREADS + tid;
+                if (i < nq4) {
+                    const int e = 4 * i, hh = e / d_qk, c = e - hh * d_qk;
+                    *reinterpret_cast<f32x4 *>(qs + hh * ldq + c) = v[u];
                 }
-#pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
-                inv = (float)(1.0 / sqrt(sq / (double)d_qk + (double)qeps));
-                for (int c = lane; c < t0; c += 64) qh[c] = qh[c] * inv;
-            }
-            for (int p = lane; p < qrp.rd / 2; p += 64) {
-                float a = qh[t0 + 2 * p], b = qh[t0 + 2 * p + 1];
-                if (qnorm) { a = a * inv; b = b * inv; }
-                rope_pair(a, b, qrp, p);
-                qh[t0 + 2 * p] = a;
-                qh[t0 + 2 * p + 1] = b;
             }
         }
-        __syncthreads();
+    } else {
+        for (int i0 = 0; i0 < AT_HB * d_qk; i0 += SB * AT_THREADS) {
+            float v[SB];
+#pragma unroll
+            for (int u = 0; u < SB; u++) {
+                const int i = i0 + u * AT_THREADS + tid;
+                const int hh = i / d_qk, c = i - hh * d_qk;
+                v[u] = (i < AT_HB * d_qk && hh < nh) ? q[(size_t)(h0 + hh) * d_qk + c] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < SB; u++) {
+                const int i = i0 + u * AT_THREADS + tid;
+                if (i < AT_HB * d_qk) {
+                    const int hh = i / d_qk, c = i - hh * d_qk;
+                    qs[hh * ldq + c] = v[u];
+                }
+            }
+        }
     }
-
+    if (tid < SR) sidx[tid] = (ridx >= 0 && ridx < kv_rows) ? ridx : -1;   /* never a wild read */
+    rope_row_store(qrp, rrow, rcs, rsn);
+    __syncthreads();
     /* stage the rows */
     if (vec) {
         const int nc = dmax * ES / 16;                           /* 16-B chunks per row */
@@ -931,6 +1082,35 @@ k_attn_partial(float *__restrict__ pm, float *__restrict__ pl,
         }
     }
     __syncthreads();
+    if (qnorm || qrp.rd) {
+        /* the attention block's q: each head scaled by 1/sqrt(mean square +
+         * eps) and RoPE'd at pos (dsv4_layer.c:223-231), a wave per head,
+         * after the rows are staged (their loads went out first) */
+        const int t0 = d_qk - qrp.rd;
+        for (int hh = wid; hh < AT_HB; hh += AT_THREADS / 64) {
+            float *qh = qs + hh * ldq;
+            float inv = 1.0f;
+            if (qnorm) {
+                double sq = 0.0;
+                for (int c = lane; c < d_qk; c += 64) {
+                    const double v = (double)qh[c];
+                    sq += v * v;
+                }
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
+                inv = (float)(1.0 / sqrt(sq / (double)d_qk + (double)qeps));
+                for (int c = lane; c < t0; c += 64) qh[c] = qh[c] * inv;
+            }
+            for (int p = lane; p < qrp.rd / 2; p += 64) {
+                float a = qh[t0 + 2 * p], b = qh[t0 + 2 * p + 1];
+                if (qnorm) { a = a * inv; b = b * inv; }
+                rope_pair_cs(a, b, rcs[p], rsn[p], qrp.inverse);
+                qh[t0 + 2 * p] = a;
+                qh[t0 + 2 * p + 1] = b;
+            }
+        }
+        __syncthreads();
+    }
 
     /* scores: thread (hh, lt) takes rows lt, lt + 32, ... */
     {
@@ -1036,6 +1216,13 @@ k_attn_combine(float *__restrict__ o, const float *__restrict__ pm,
     const int c = blockIdx.y * CB_COLS + tid;
     const bool live = c < d_v;
     const int cc = live ? c : d_v - 1;
+    /* this column's de-rotation pair's cos / sin, loaded with the partials */
+    const int rt0 = d_v - orp.rd;
+    float rcv = 1.0f, rsv = 0.0f;
+    if (orp.rd && live && c >= rt0) {
+        rcv = orp.cs[(size_t)orp.pos * orp.half + ((c - rt0) >> 1)];
+        rsv = orp.sn[(size_t)orp.pos * orp.half + ((c - rt0) >> 1)];
+    }
     /* the partials' loads do not wait for the weights */
     constexpr int B = 32;
     float v[B];
@@ -1061,11 +1248,10 @@ k_attn_combine(float *__restrict__ o, const float *__restrict__ pm,
         /* the output's de-rotation (dsv4_layer.c:304-305): column pairs
          * (t0 + 2p, t0 + 2p + 1) sit in neighbouring lanes */
         const float other = __shfl_xor(val, 1, 64);
-        const int t0 = d_v - orp.rd;
-        if (c >= t0 && live) {
-            const bool odd = (c - t0) & 1;
+        if (c >= rt0 && live) {
+            const bool odd = (c - rt0) & 1;
             float a = odd ? other : val, b = odd ? val : other;
-            rope_pair(a, b, orp, (c - t0) >> 1);
+            rope_pair_cs(a, b, rcv, rsv, orp.inverse);
             val = odd ? b : a;
         }
     }
@@ -1370,7 +1556,9 @@ int attn_split_rows(int kv_fmt, int d_qk, int d_v, int *rowb_out, size_t *lds_ou
     const int dmax = d_qk > d_v ? d_qk : d_v;
     const int rowb = ((dmax * es + 15) / 16) * 16 + 16;          /* +16 B: bank skew */
     int sr = 64;
-    while (sr >= 1 && attn_partial_lds(sr, d_qk, rowb) > cap) sr >>= 1;
+    /* (the kernel's static LDS, the RoPE row, comes on top) */
+    while (sr >= 1 && attn_partial_lds(sr, d_qk, rowb) + 2 * RP_MAX * sizeof(float) > cap)
+        sr >>= 1;
     if (sr < 1) return 0;
     if (topk > 0) {
         static int cus = 0;
@@ -1423,7 +1611,8 @@ int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *
                                    int rope_dim, hipStream_t st)
 {
     if (H <= 0 || D <= 0 || n < 0 || key_stride < D || H > 256 || rope_dim < 0 ||
-        (rope_dim & 1) || rope_dim > D || (rope_dim && (!rope_cs || !rope_sn))) {
+        (rope_dim & 1) || rope_dim > D || rope_dim > 2 * RP_MAX ||
+        (rope_dim && (!rope_cs || !rope_sn))) {
         DSV4_ERR("indexer score: bad shape H %d D %d n %d stride %d rope %d",
                  H, D, n, key_stride, rope_dim);
         return -1;
@@ -1438,6 +1627,34 @@ int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *
         return -1;
     }
     if (n == 0) return 0;
+    if (key_fmt == DSV4_GPU_KV_F32 && !with_hist && n <= SK_NMAX && (D & 3) == 0 &&
+        ((uintptr_t)d_q & 15) == 0) {
+        int hp = 1;
+        while (hp < H) hp <<= 1;                   /* H <= 256: a power of two divides 256 */
+        const size_t lds = sizeof(double) * ((size_t)(SK_THREADS / hp) * hp + H) +
+                           sizeof(float) * ((size_t)H * (D + 1) + (size_t)(SK_THREADS / hp) * D);
+        if (lds <= dsv4_lds_limit()) {
+            static bool kh_opted = false;
+            if (!kh_opted) {
+                (void)hipFuncSetAttribute((const void *)k_iscore_kh,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)dsv4_lds_limit());
+                (void)hipGetLastError();
+                kh_opted = true;
+            }
+            Dsv4Rope qr;
+            if (rope_dim) {
+                qr.cs = rope_cs; qr.sn = rope_sn; qr.pos = rope_pos; qr.half = rope_half;
+                qr.rd = rope_dim;
+            }
+            const int kpw = SK_THREADS / hp;
+            hipLaunchKernelGGL(k_iscore_kh, dim3((n + kpw - 1) / kpw), dim3(SK_THREADS), lds, st,
+                               d_out, d_q, d_w, H, hp, D, (const float *)d_keys, key_stride, n,
+                               scale, qr);
+            HIP_OK(hipGetLastError(), "indexer score (few keys) launch");
+            return 0;
+        }
+    }
     const int HP = ix_heads_padded(H);
     /* four waves per workgroup where the heads allow it: one wave per SIMD
      * of a CU (up to 4 head waves per block of 64 rows, blocks filling the
@@ -1573,7 +1790,7 @@ int dsv4_attn_block_launch(float *d_o, const float *d_q, const void *d_kv,
                            int rope_pos, int rope_half, int rope_dim, hipStream_t st)
 {
     if (rope_dim < 0 || (rope_dim & 1) || rope_dim > d_qk || rope_dim > d_v ||
-        (rope_dim && ((d_v & 1) || !rope_cs || !rope_sn))) {
+        rope_dim > 2 * RP_MAX || (rope_dim && ((d_v & 1) || !rope_cs || !rope_sn))) {
         DSV4_ERR("sparse attn: bad RoPE (dim %d, d_qk %d, d_v %d)", rope_dim, d_qk, d_v);
         return -1;
     }

@@ -356,7 +356,7 @@ int dsv4_gpu_attn_ready(int layer);
 int dsv4_gpu_attn_reset(int layer);
 /* out[hidden] = attention(x[hidden]) at pos; host buffers, synchronous. */
 int dsv4_gpu_attn_step(float *out, const float *x, int layer, int pos);
-/* The same on device buffers, stream-ordered. */
+/* The same on device buffers (16-byte aligned), stream-ordered. */
 int dsv4_gpu_attn_step_d(float *d_out, const float *d_x, int layer, int pos, void *stream);
 
 #ifdef __cplusplus

@@ -262,6 +262,23 @@ class Bench:
         del W
         return us, eager, rows * cols * 2 + cols * 4 + rows * 4
 
+    # ------------------------------------------------------- batched (prefill)
+    def gemv_n_run(self, rows=7168, cols=7168, nt=64, calls=30):
+        """The batched FP8 GEMV (dsv4_gpu_fp8_gemv_n_d, the k_mmq_fp8_n
+        contract: every (row, token) bit-identical to the GEMV) at nt tokens.
+        Returns (us per call, GFLOP per call)."""
+        torch = self.torch
+        W, Sf, Se, x = self.common.fp8_problem(0, rows, cols)
+        dW, dS = self.t(W), self.t(Sf)
+        dx = torch.randn((nt, cols), device=self.dev)
+        dy = torch.empty((nt, rows), device=self.dev)
+
+        def go(i, sp):
+            assert self.L.dsv4_gpu_fp8_gemv_n_d(dy.data_ptr(), dx.data_ptr(), dW.data_ptr(),
+                                                dS.data_ptr(), 1, rows, cols, nt, sp) == 0
+        us = self.eager_us(go, calls, 3)
+        return us, 2.0 * rows * cols * nt / 1e9
+
     # ------------------------------------------------------ attention block
     def attn_run(self, steps, warmup, ratio=4, n_layers=4, p0=2048):
         """The attention block (dsv4_gpu_attn_step_d, attention() of
@@ -606,6 +623,11 @@ def main():
         detail["c4_sparse_mla_step_32768_top2048"] = rec(*B.c4_run(args.steps, args.warmup))
         log("bench: BF16 LM head")
         detail["lm_head_bf16_129280x7168"] = rec(*B.bf16_head_run(args.steps, args.warmup))
+        us, gf = B.gemv_n_run()
+        detail["prefill_fp8_7168x7168_nt64"] = {
+            "us": round(us, 3), "TFLOPs": round(gf / us * 1e3, 2),
+            "frac_fp32_peak": round(gf / us * 1e3 / 157.3, 4),
+            "us_per_token": round(us / 64, 3)}
         for ratio, name in ((4, "attn_block_flash_csa_ratio4"), (128, "attn_block_flash_hca_ratio128")):
             log("bench: attention block, ratio %d" % ratio)
             detail[name] = rec(*B.attn_run(32, 4, ratio=ratio))

@@ -84,6 +84,7 @@ _SIGS = {
     "dsv4_gpu_mmq": (None, [_vp, _vp, _QP]),
     "dsv4_gpu_mmq_n": (None, [_vp, _vp, _QP, _ci]),
     "dsv4_gpu_fp8_gemv_d": (_ci, [_vp, _vp, _vp, _vp, _ci, _ci, _ci, _vp]),
+    "dsv4_gpu_fp8_gemv_n_d": (_ci, [_vp, _vp, _vp, _vp, _ci, _ci, _ci, _ci, _vp]),
     "dsv4_gpu_fp4_gemv_d": (_ci, [_vp, _vp, _vp, _vp, _ci, _ci, _ci, _ci, _vp]),
     "dsv4_gpu_bf16_gemv_d": (_ci, [_vp, _vp, _vp, _ci, _ci, _vp]),
     "dsv4_gpu_head_argmax": (_ci, [_vp, _QP]),

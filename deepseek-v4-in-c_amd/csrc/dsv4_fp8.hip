@@ -79,6 +79,22 @@ __device__ __forceinline__ float ld_scale(const void *S, size_t at)
 }
 
 /* Dot of 16 decoded weights with 16 activations; 4 interleaved chains. */
+/* The chunk's 16 products summed in four chains and a fixed tree, from
+ * weights already decoded (dot16f) or from the packed codes (dot16). */
+__device__ __forceinline__ float dot16f(const float *w, const float *xr)
+{
+    float p0 = w[0] * xr[0], p1 = w[1] * xr[1];
+    float p2 = w[2] * xr[2], p3 = w[3] * xr[3];
+#pragma unroll
+    for (int e = 4; e < 16; e += 4) {
+        p0 = fmaf(w[e + 0], xr[e + 0], p0);
+        p1 = fmaf(w[e + 1], xr[e + 1], p1);
+        p2 = fmaf(w[e + 2], xr[e + 2], p2);
+        p3 = fmaf(w[e + 3], xr[e + 3], p3);
+    }
+    return (p0 + p1) + (p2 + p3);
+}
+
 __device__ __forceinline__ float dot16(const u32x4 v, const float *xr)
 {
     float w[16];
@@ -324,18 +340,22 @@ k_fp8_gemv_n(float *__restrict__ y, const float *__restrict__ x,
     const int r = blockIdx.x * rg + g;       /* this row group's row */
     const bool rok = r < rows;
 
-    u32x4 wv[NCH];
+    float wf[NCH][16];                       /* the row's chunks, decoded once */
     float sreg[NCH];
     bool act[NCH];
 #pragma unroll
     for (int n = 0; n < NCH; n++) {
         const int c = j + n * tc;
         act[n] = c < ch;
-        wv[n] = (act[n] && rok) ? ld16(W + (size_t)r * cols + (size_t)c * 16)
-                                : u32x4{0, 0, 0, 0};
+        const u32x4 wv = (act[n] && rok) ? ld16(W + (size_t)r * cols + (size_t)c * 16)
+                                         : u32x4{0, 0, 0, 0};
         sreg[n] = (act[n] && rok)
                 ? ld_scale<SF>(S, (size_t)(r / blk_r) * sc + (c * 16) / blk_c)
                 : 0.0f;
+        dec_e4m3x4(wv.x, wf[n] + 0);
+        dec_e4m3x4(wv.y, wf[n] + 4);
+        dec_e4m3x4(wv.z, wf[n] + 8);
+        dec_e4m3x4(wv.w, wf[n] + 12);
     }
 
     for (int tb = 0; tb < nt; tb += TB) {
@@ -356,7 +376,7 @@ k_fp8_gemv_n(float *__restrict__ y, const float *__restrict__ x,
                         xr[q * 4 + 0] = v.x; xr[q * 4 + 1] = v.y;
                         xr[q * 4 + 2] = v.z; xr[q * 4 + 3] = v.w;
                     }
-                    a = fmaf(dot16(wv[n], xr), sreg[n], a);
+                    a = fmaf(dot16f(wf[n], xr), sreg[n], a);
                 }
             }
             acc[t] = a;

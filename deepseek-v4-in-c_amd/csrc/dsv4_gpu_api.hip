@@ -535,6 +535,19 @@ int dsv4_gpu_fp8_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
                                 128, as_stream(stream));
 }
 
+int dsv4_gpu_fp8_gemv_n_d(float *d_y, const float *d_x, const uint8_t *d_w,
+                          const void *d_s, int scale_fmt, int rows, int cols, int nt,
+                          void *stream)
+{
+    if (!d_y || !d_x || !d_w || !d_s || (scale_fmt != 0 && scale_fmt != 1) || nt < 1 ||
+        nt > DSV4_MAX_BATCH) {
+        DSV4_ERR("fp8_gemv_n_d: bad arguments (nt %d)", nt);
+        return -1;
+    }
+    return dsv4_fp8_gemv_n_launch(d_y, d_x, d_w, d_s, scale_fmt, rows, cols, 128, 128, nt,
+                                  as_stream(stream));
+}
+
 int dsv4_gpu_fp4_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
                         const uint8_t *d_s, int rows, int cols, int blk_r, int blk_c,
                         void *stream)

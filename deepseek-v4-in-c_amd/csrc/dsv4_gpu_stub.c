@@ -142,3 +142,8 @@ int dsv4_gpu_attn_step(float *out, const float *x, int layer, int pos)
 { (void)out; (void)x; (void)layer; (void)pos; return -1; }
 int dsv4_gpu_attn_step_d(float *d_out, const float *d_x, int layer, int pos, void *stream)
 { (void)d_out; (void)d_x; (void)layer; (void)pos; (void)stream; return -1; }
+int dsv4_gpu_fp8_gemv_n_d(float *d_y, const float *d_x, const uint8_t *d_w,
+                          const void *d_s, int scale_fmt, int rows, int cols, int nt,
+                          void *stream)
+{ (void)d_y; (void)d_x; (void)d_w; (void)d_s; (void)scale_fmt; (void)rows; (void)cols;
+  (void)nt; (void)stream; return -1; }

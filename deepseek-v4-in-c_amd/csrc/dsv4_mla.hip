@@ -362,14 +362,19 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
 /* Few f32 keys (the attention block's compressed rows, n <= SK_NMAX): one
  * thread per (key, head) runs that pair's fp64 fma chain over c ascending,
  * with q (RoPE'd when asked) and the workgroup's key rows staged in LDS; a
- * thread per key then folds the heads in order from LDS. The same arithmetic, step for step, as the
- * reference and as k_iscore, with a workgroup of SK_THREADS / HP keys. */
+ * thread per key then folds the heads in order from LDS. The same
+ * arithmetic, step for step, as the reference and as k_iscore, with a
+ * workgroup of SK_THREADS / HP keys. Written for every key format and with
+ * the top-k histogram, but launched for short f32 score vectors only, where
+ * it is the faster form. */
 constexpr int SK_NMAX = 4096;
 constexpr int SK_THREADS = 256;
 
+template <int KF, int HIST>
 __global__ void __launch_bounds__(SK_THREADS)
-k_iscore_kh(float *__restrict__ out, const float *__restrict__ q, const float *__restrict__ w,
-            int H, int HP, int D, const float *__restrict__ keys, int key_stride, int n,
+k_iscore_kh(float *__restrict__ out, uint32_t *__restrict__ hist, uint32_t *__restrict__ meta,
+            const float *__restrict__ q, const float *__restrict__ w, int H, int HP, int D,
+            const void *__restrict__ keys, const float *__restrict__ ks, int key_stride, int n,
             float scale, Dsv4Rope qr)
 {
     extern __shared__ double skl[];   /* dots[kpw][HP], w[H], q[H][D + 1], then keys[kpw][D] */
@@ -394,7 +399,7 @@ k_iscore_kh(float *__restrict__ out, const float *__restrict__ q, const float *_
         for (int u = 0; u < 8; u++) {
             const int i = min(u * SK_THREADS + (int)threadIdx.x, kpw * D - 1);
             const int kk = i / D, c = i - kk * D;
-            kv8[u] = keys[(size_t)min(t0k + kk, n - 1) * key_stride + c];
+            kv8[u] = key_at<KF>(keys, ks, (size_t)min(t0k + kk, n - 1), key_stride, c);
         }
 #pragma unroll
         for (int u = 0; u < 8; u++)
@@ -423,7 +428,7 @@ k_iscore_kh(float *__restrict__ out, const float *__restrict__ q, const float *_
             for (int u = 0; u < KB; u++) {
                 const int i = min(i0 + u * SK_THREADS + (int)threadIdx.x, kpw * D - 1);
                 const int kk = i / D, c = i - kk * D;
-                v[u] = keys[(size_t)min(t0k + kk, n - 1) * key_stride + c];
+                v[u] = key_at<KF>(keys, ks, (size_t)min(t0k + kk, n - 1), key_stride, c);
             }
 #pragma unroll
             for (int u = 0; u < KB; u++) {
@@ -469,17 +474,25 @@ k_iscore_kh(float *__restrict__ out, const float *__restrict__ q, const float *_
         dots[kl * HP + h] = dot;
     }
     __syncthreads();
-    if ((int)threadIdx.x < kpw) {
-        const int tt = blockIdx.x * kpw + (int)threadIdx.x;
-        if (tt < n) {
-            double total = 0.0;
-            for (int hh = 0; hh < H; hh++) {
-                const double d = dots[threadIdx.x * HP + hh];
-                const double prod = d * wd[hh];
-                total = d > 0.0 ? total + prod : total;
-            }
-            out[tt] = (float)total * scale;
+    const int tt = blockIdx.x * kpw + (int)threadIdx.x;
+    float sc = 0.0f;
+    if ((int)threadIdx.x < kpw && tt < n) {
+        double total = 0.0;
+        for (int hh = 0; hh < H; hh++) {
+            const double d = dots[threadIdx.x * HP + hh];
+            const double prod = d * wd[hh];
+            total = d > 0.0 ? total + prod : total;
         }
+        sc = (float)total * scale;
+        out[tt] = sc;
+    }
+    if (HIST) {
+        /* the top-k's level-1 histogram, by the waves that hold keys */
+        if (blockIdx.x == 0 && threadIdx.x == 0) meta[MT_ABOVE] = 0u;
+        if ((int)(threadIdx.x & ~63u) < kpw)
+            hist_push_global(hist + (blockIdx.x % TK_SLICES) * TK_BINS,
+                             (int)threadIdx.x < kpw && tt < n, fkey(sc) >> 21,
+                             (int)threadIdx.x & 63);
     }
 }
 
@@ -1627,6 +1640,9 @@ int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *
         return -1;
     }
     if (n == 0) return 0;
+    /* few f32 keys: a thread per (key, head) (at C4's 32768 FP8 keys the
+     * same kernel measured slower than the lane-per-row one, 20.5 vs 13.8
+     * us, so it stays for short score vectors) */
     if (key_fmt == DSV4_GPU_KV_F32 && !with_hist && n <= SK_NMAX && (D & 3) == 0 &&
         ((uintptr_t)d_q & 15) == 0) {
         int hp = 1;
@@ -1636,21 +1652,22 @@ int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *
         if (lds <= dsv4_lds_limit()) {
             static bool kh_opted = false;
             if (!kh_opted) {
-                (void)hipFuncSetAttribute((const void *)k_iscore_kh,
+                (void)hipFuncSetAttribute((const void *)k_iscore_kh<DSV4_GPU_KV_F32, 0>,
                                           hipFuncAttributeMaxDynamicSharedMemorySize,
                                           (int)dsv4_lds_limit());
                 (void)hipGetLastError();
                 kh_opted = true;
             }
+
             Dsv4Rope qr;
             if (rope_dim) {
                 qr.cs = rope_cs; qr.sn = rope_sn; qr.pos = rope_pos; qr.half = rope_half;
                 qr.rd = rope_dim;
             }
             const int kpw = SK_THREADS / hp;
-            hipLaunchKernelGGL(k_iscore_kh, dim3((n + kpw - 1) / kpw), dim3(SK_THREADS), lds, st,
-                               d_out, d_q, d_w, H, hp, D, (const float *)d_keys, key_stride, n,
-                               scale, qr);
+            hipLaunchKernelGGL((k_iscore_kh<DSV4_GPU_KV_F32, 0>), dim3((n + kpw - 1) / kpw),
+                               dim3(SK_THREADS), lds, st, d_out, nullptr, nullptr, d_q, d_w, H,
+                               hp, D, d_keys, d_key_scales, key_stride, n, scale, qr);
             HIP_OK(hipGetLastError(), "indexer score (few keys) launch");
             return 0;
         }

@@ -132,6 +132,14 @@ int dsv4_gpu_fp8_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
                         const void *d_s, int scale_fmt, int rows, int cols,
                         void *stream);
 
+/* The batched form (prefill, the k_mmq_fp8_n contract of dsv4_cuda.cu:161-
+ * 230): d_y[nt][rows] for d_x[nt][cols], each (row, token) bit-identical to
+ * dsv4_gpu_fp8_gemv_d on that token. nt <= DSV4_MAX_BATCH. What
+ * dsv4_gpu_mmq_n runs after staging. */
+int dsv4_gpu_fp8_gemv_n_d(float *d_y, const float *d_x, const uint8_t *d_w,
+                          const void *d_s, int scale_fmt, int rows, int cols, int nt,
+                          void *stream);
+
 /* The MXFP4 GEMV on raw device buffers, stream-ordered: d_y[rows] =
  * dsv4_matmul_fp4 (dsv4_matmul.c:320-345) of d_w (e2m1 nibbles [rows][cols/2],
  * 16-byte aligned) with E8M0 scales d_s [ceil(rows/blk_r)][ceil(cols/blk_c)]

@@ -1120,6 +1120,13 @@ int block_bind(int layer, const dsv4_gpu_attn_cfg *cp, const dsv4_gpu_attn_w *w)
     b.scores = (float *)(m + o_sc); b.o = (float *)(m + o_o); b.ogrp = (float *)(m + o_og);
     b.out = (float *)(m + o_out); b.idxs = (int *)(m + o_ix);
     b.iscr = m + o_is; b.ascr = m + o_as;
+    /* the top-k's histogram and counters expect zeros on first use (and
+     * leave zeros behind) */
+    if (hipMemset(b.mem, 0, off) != hipSuccess) {
+        DSV4_ERR("attn_bind: layer %d: clearing the block failed", layer);
+        block_free(b);
+        return -1;
+    }
     bool ok = hipMemcpy(b.q_norm, w->q_norm, c.q_lora * F, hipMemcpyHostToDevice) == hipSuccess &&
               hipMemcpy(b.kv_norm, w->kv_norm, hd * F, hipMemcpyHostToDevice) == hipSuccess &&
               hipMemcpy(b.cs, w->rope_cos, (size_t)c.max_pos * half * F, hipMemcpyHostToDevice) == hipSuccess &&

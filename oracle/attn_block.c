@@ -81,6 +81,24 @@ static double vec_rel(const float *got, const float *ref, int n)
     return worst;
 }
 
+/* The reference sizes s->idxs for window + index_topk entries
+ * (dsv4_layer.c:128, :185), but a compressed layer without the indexer
+ * attends to every compressed row (:293): past index_topk of them it writes
+ * beyond that buffer, and its per-head attention scratch (:143 vs :175)
+ * past its carve. The drivers give both room for every position; what is
+ * computed does not change. */
+static int widen_scratch(DSV4Scratch *s, const DSV4Cfg *c, int maxpos)
+{
+    const size_t rows = (size_t)c->sliding_window + (size_t)maxpos + 1;
+    int *ix = calloc(rows, sizeof(int));
+    float *sc = calloc((size_t)c->n_heads * rows, sizeof(float));
+    if (!ix || !sc) { free(ix); free(sc); return -1; }
+    free(s->idxs);
+    s->idxs = ix;
+    s->attn_scratch = sc;      /* lives until the process ends */
+    return 0;
+}
+
 static double now_s(void)
 {
     struct timespec t;
@@ -185,7 +203,8 @@ static int flash_mode(int n, int ratio, double tol)
                         c.yarn_beta_fast, c.yarn_beta_slow);
     DSV4Scratch s;
     DSV4LayerState ls;
-    if (dsv4_scratch_init(&s, &c, maxpos) != 0 || dsv4_state_init(&ls, &c, 0, maxpos) != 0)
+    if (dsv4_scratch_init(&s, &c, maxpos) != 0 || widen_scratch(&s, &c, maxpos) != 0 ||
+        dsv4_state_init(&ls, &c, 0, maxpos) != 0)
         return 1;
     float *x = malloc((size_t)n * c.hidden * sizeof(float));
     float *ref = malloc((size_t)n * c.hidden * sizeof(float));
@@ -296,7 +315,7 @@ int main(int argc, char **argv)
     dsv4_rope_table(cs_c, sn_c, c.qk_rope, maxpos, c.yarn_orig_ctx, c.compress_rope_theta,
                     c.yarn_factor, c.yarn_beta_fast, c.yarn_beta_slow);
     DSV4Scratch s;
-    if (dsv4_scratch_init(&s, &c, maxpos) != 0) return 1;
+    if (dsv4_scratch_init(&s, &c, maxpos) != 0 || widen_scratch(&s, &c, maxpos) != 0) return 1;
 
     const size_t per = (size_t)n * c.hidden;
     float *x = malloc(per * c.n_layers * sizeof(float));

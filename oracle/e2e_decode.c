@@ -271,6 +271,24 @@ static void head_hc(float *y, const float *x, const DSV4HcW *w, int hc, int hidd
     }
 }
 
+/* The reference sizes s->idxs for window + index_topk entries
+ * (dsv4_layer.c:128, :185), but a compressed layer without the indexer
+ * attends to every compressed row (:293): past index_topk of them it writes
+ * beyond that buffer, and its per-head attention scratch (:143 vs :175)
+ * past its carve. The drivers give both room for every position; what is
+ * computed does not change. */
+static int widen_scratch(DSV4Scratch *s, const DSV4Cfg *c, int maxpos)
+{
+    const size_t rows = (size_t)c->sliding_window + (size_t)maxpos + 1;
+    int *ix = calloc(rows, sizeof(int));
+    float *sc = calloc((size_t)c->n_heads * rows, sizeof(float));
+    if (!ix || !sc) { free(ix); free(sc); return -1; }
+    free(s->idxs);
+    s->idxs = ix;
+    s->attn_scratch = sc;      /* lives until the process ends */
+    return 0;
+}
+
 /* --------------------------------------------------------------- main ---- */
 static int read_tokens(const char *path, int **out)
 {
@@ -415,7 +433,8 @@ int main(int argc, char **argv)
                     c.compress_rope_theta, c.yarn_factor, c.yarn_beta_fast,
                     c.yarn_beta_slow);
     DSV4Scratch s;
-    if (dsv4_scratch_init(&s, &c, M.maxpos) != 0) return 1;
+    if (dsv4_scratch_init(&s, &c, M.maxpos) != 0 || widen_scratch(&s, &c, M.maxpos) != 0)
+        return 1;
     M.s = &s;
     printf("e2e: hidden %d, %d layers, vocab %d, %d experts (top-%d), index_topk %d, "
            "%d positions\n", c.hidden, c.n_layers, c.vocab, c.n_experts, c.topk,

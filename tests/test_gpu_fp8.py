@@ -236,6 +236,33 @@ def test_device_entry_point_matches_host_path(gpu, dsv4):
     assert common.bits_equal(dy.cpu().numpy(), y_host)
 
 
+def test_batched_device_entry_point(gpu, dsv4):
+    """dsv4_gpu_fp8_gemv_n_d: every token's row equals dsv4_gpu_fp8_gemv_d on
+    that token, bit for bit (the k_mmq_fp8_n contract), on device buffers."""
+    import torch
+    rows, cols, nt = 1000, 7168, 11
+    W, Sf, Se, _ = common.fp8_problem(61, rows, cols)
+    x = np.random.default_rng(62).standard_normal((nt, cols), dtype=np.float32)
+    dev = torch.device("cuda:0")
+    dW, dS, dx = (torch.from_numpy(a).to(dev) for a in (W, Se, x))
+    dy = torch.empty((nt, rows), dtype=torch.float32, device=dev)
+    d1 = torch.empty(rows, dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    L = dsv4.lib()
+    assert L.dsv4_gpu_fp8_gemv_n_d(dy.data_ptr(), dx.data_ptr(), dW.data_ptr(), dS.data_ptr(),
+                                   0, rows, cols, nt, st) == 0
+    torch.cuda.synchronize()
+    yn = dy.cpu().numpy()
+    for t in range(nt):
+        assert L.dsv4_gpu_fp8_gemv_d(d1.data_ptr(), dx[t].data_ptr(), dW.data_ptr(),
+                                     dS.data_ptr(), 0, rows, cols, st) == 0
+        torch.cuda.synchronize()
+        assert common.bits_equal(yn[t], d1.cpu().numpy()), t
+    assert common.vec_rel_err(yn, oracle.matmul_fp8(x, W, Se)) < TOL
+    assert L.dsv4_gpu_fp8_gemv_n_d(dy.data_ptr(), dx.data_ptr(), dW.data_ptr(), dS.data_ptr(),
+                                   0, rows, cols, 65, st) == -1     # above DSV4_MAX_BATCH
+
+
 def test_upload_refusals(gpu, dsv4):
     L = dsv4.lib()
     W = np.zeros((4, 32), np.uint8)

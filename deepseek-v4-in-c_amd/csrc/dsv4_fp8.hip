@@ -520,11 +520,197 @@ void launch_gemv_r(const Fp8Geom &g, int R, float *y, const float *x,
     }
 }
 
+/* Batched with x through LDS (prefill, nt >= 2): a workgroup of 512 threads
+ * (rg = 512 / tc row groups) owns the rows [row0, row0 + rows_per_wg) and
+ * walks the tokens in blocks of TB, staged in LDS (TB x cols floats) and
+ * read by every row group. A row group takes RR rows per step (rb + g,
+ * rb + g + rg, ...), decodes their chunks once for the block, and applies
+ * each x piece it reads from LDS to all RR rows. Per (row, token) the
+ * arithmetic is k_fp8_gemv's (chunk order, scale fma, segment tree, wave
+ * partials in wave order), so every result keeps the GEMV's bits. */
+template <int NCH, int SF, int TB, int RR>
+__global__ void __launch_bounds__(512)
+k_fp8_gemv_nl(float *__restrict__ y, const float *__restrict__ x,
+              const uint8_t *__restrict__ W, const void *__restrict__ S, int rows, int cols,
+              int sc, int blk_r, int blk_c, int tc, int nt, int rows_per_wg)
+{
+    /* x of the block as [TB][4 quads][ch chunks] 16-byte pieces: a row
+     * group's lanes read consecutive pieces (conflict-free), red after */
+    extern __shared__ __attribute__((aligned(16))) float xl[];
+    const int tid = threadIdx.x;
+    const int g = tid / tc, j = tid - g * tc;
+    const int rg = blockDim.x / tc;
+    const int ch = cols >> 4;
+    const int wid = tid >> 6, lane = tid & 63;
+    const int row0 = blockIdx.x * rows_per_wg;
+    const int rend = min(rows, row0 + rows_per_wg);
+    float *red = xl + (size_t)TB * cols;
+    bool act[NCH];
+    int cb[NCH];
+#pragma unroll
+    for (int n = 0; n < NCH; n++) {
+        const int c = j + n * tc;
+        act[n] = c < ch;
+        cb[n] = (min(c, ch - 1) * 16) / blk_c;
+    }
+    for (int tb = 0; tb < nt; tb += TB) {
+        const int ntb = min(TB, nt - tb);
+        __syncthreads();                           /* the previous block's reads */
+        {
+            const int n4 = (ntb * cols) >> 2;
+            const float *xs = x + (size_t)tb * cols;
+            for (int i0 = 0; i0 < n4; i0 += 8 * (int)blockDim.x) {
+                f32x4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    v[u] = ldf4(xs + 4 * min(i0 + u * (int)blockDim.x + tid, n4 - 1));
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const int i = i0 + u * (int)blockDim.x + tid;
+                    if (i < n4) {
+                        const int t = (4 * i) / cols, e = 4 * i - t * cols;
+                        const int c = e >> 4, q = (e >> 2) & 3;
+                        *reinterpret_cast<f32x4 *>(xl + (size_t)t * cols + (size_t)q * ch * 4 +
+                                                   c * 4) = v[u];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        for (int rb = row0; rb < rend; rb += RR * rg) {  /* uniform: every group steps */
+            int rr[RR];
+            bool rok[RR];
+            float wf[RR][NCH][16];
+            float sreg[RR][NCH];
+#pragma unroll
+            for (int k = 0; k < RR; k++) {
+                const int r = rb + g + k * rg;
+                rok[k] = r < rend;
+                rr[k] = rok[k] ? r : rend - 1;
+#pragma unroll
+                for (int n = 0; n < NCH; n++) {
+                    const int c = min(j + n * tc, ch - 1);
+                    const u32x4 wv = ld16(W + (size_t)rr[k] * cols + (size_t)c * 16);
+                    sreg[k][n] = ld_scale<SF>(S, (size_t)(rr[k] / blk_r) * sc + cb[n]);
+                    dec_e4m3x4(wv.x, wf[k][n] + 0);
+                    dec_e4m3x4(wv.y, wf[k][n] + 4);
+                    dec_e4m3x4(wv.z, wf[k][n] + 8);
+                    dec_e4m3x4(wv.w, wf[k][n] + 12);
+                }
+            }
+            float acc[RR][TB];
+#pragma unroll
+            for (int t = 0; t < TB; t++) {
+                float a[RR];
+#pragma unroll
+                for (int k = 0; k < RR; k++) a[k] = 0.0f;
+                const float *xt = xl + (size_t)min(t, ntb - 1) * cols;
+#pragma unroll
+                for (int n = 0; n < NCH; n++) {
+                    const int c = min(j + n * tc, ch - 1);
+                    float xr[16];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const f32x4 v =
+                            *reinterpret_cast<const f32x4 *>(xt + (size_t)q * ch * 4 + c * 4);
+                        xr[q * 4 + 0] = v.x; xr[q * 4 + 1] = v.y;
+                        xr[q * 4 + 2] = v.z; xr[q * 4 + 3] = v.w;
+                    }
+#pragma unroll
+                    for (int k = 0; k < RR; k++) {
+                        const float d = fmaf(dot16f(wf[k][n], xr), sreg[k][n], a[k]);
+                        a[k] = act[n] ? d : a[k];
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < RR; k++) acc[k][t] = a[k];
+            }
+            if (tc <= 64) {
+#pragma unroll
+                for (int k = 0; k < RR; k++)
+#pragma unroll
+                    for (int t = 0; t < TB; t++) {
+                        const float v = seg_sum_rt(acc[k][t], tc);
+                        if (j == tc - 1 && rok[k] && t < ntb)
+                            y[(size_t)(tb + t) * rows + rb + g + k * rg] = v;
+                    }
+            } else {
+                const int wpr = tc >> 6;
+#pragma unroll
+                for (int k = 0; k < RR; k++)
+#pragma unroll
+                    for (int t = 0; t < TB; t++) {
+                        const float v = seg_sum<64>(acc[k][t]);
+                        if (lane == 63) red[(k * 8 + wid) * TB + t] = v;
+                    }
+                __syncthreads();
+                if (tid < RR * rg * TB) {
+                    const int k = tid / (rg * TB), rem = tid - k * (rg * TB);
+                    const int gg = rem / TB, tt = rem - gg * TB;
+                    const int ro = rb + gg + k * rg;
+                    const float *rk = red + (size_t)k * 8 * TB;
+                    float s = rk[(gg * wpr) * TB + tt];
+                    for (int w = 1; w < wpr; w++) s += rk[(gg * wpr + w) * TB + tt];
+                    if (ro < rend && tt < ntb) y[(size_t)(tb + tt) * rows + ro] = s;
+                }
+                __syncthreads();
+            }
+        }
+    }
+}
+
+template <int NCH, int SF, int TB>
+void launch_gemv_nl(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
+                    const void *S, int rows, int cols, int sc, int blk_r, int blk_c, int nt,
+                    hipStream_t st)
+{
+    constexpr int RR = 2;
+    static bool opted = false;
+    if (!opted) {
+        (void)hipFuncSetAttribute((const void *)k_fp8_gemv_nl<NCH, SF, TB, RR>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)dsv4_lds_limit());
+        (void)hipGetLastError();
+        opted = true;
+    }
+    const int step = RR * (512 / g.tc);
+    /* about one workgroup per CU: each stages every token block once */
+    const int want = cu_count();
+    int rpw = (rows + want - 1) / want;
+    rpw = (rpw + step - 1) / step * step;
+    const int grid = (rows + rpw - 1) / rpw;
+    const size_t lds = sizeof(float) * ((size_t)TB * cols + (size_t)RR * 8 * TB);
+    hipLaunchKernelGGL((k_fp8_gemv_nl<NCH, SF, TB, RR>), dim3(grid), dim3(512), lds, st, y,
+                       x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, nt, rpw);
+}
+
+template <int SF, int TB>
+void launch_gemv_nl_nch(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
+                        const void *S, int rows, int cols, int sc, int blk_r, int blk_c,
+                        int nt, hipStream_t st)
+{
+    switch (g.nch) {
+    case 1: launch_gemv_nl<1, SF, TB>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st); break;
+    case 2: launch_gemv_nl<2, SF, TB>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st); break;
+    case 3: launch_gemv_nl<3, SF, TB>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st); break;
+    default: launch_gemv_nl<4, SF, TB>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st); break;
+    }
+}
+
 template <int SF>
 void launch_gemv_n(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
                    const void *S, int rows, int cols, int sc, int blk_r,
                    int blk_c, int nt, hipStream_t st)
 {
+    /* two or more tokens: x through LDS, the largest token block that fits
+     * and the tokens fill (8 x 4096, 4 x 7168, 2 x 16384 columns) */
+    const size_t cap = dsv4_lds_limit() - 2048;
+    if (nt >= 2 && (((uintptr_t)x) & 15) == 0 && g.tc <= 256 && 512 % g.tc == 0) {
+        const size_t row4 = sizeof(float) * (size_t)cols;
+        if (nt >= 8 && 8 * row4 <= cap) { launch_gemv_nl_nch<SF, 8>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st); return; }
+        if (nt >= 4 && 4 * row4 <= cap) { launch_gemv_nl_nch<SF, 4>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st); return; }
+        if (2 * row4 <= cap) { launch_gemv_nl_nch<SF, 2>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st); return; }
+    }
     const int grid = (rows + g.rg - 1) / g.rg;
     switch (g.nch) {
     case 1: hipLaunchKernelGGL((k_fp8_gemv_n<1, SF>), dim3(grid), dim3(g.wg), 0, st, y, x, W, S, rows, cols, sc, blk_r, blk_c, g.tc, nt); break;
@@ -653,6 +839,8 @@ int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,
         DSV4_ERR("fp8 gemv_n: bad shape %dx%d nt %d", rows, cols, nt);
         return -1;
     }
+    if (nt == 1)                       /* the GEMV itself: same bits, its launch shape */
+        return fp8_gemv(y, x, W, S, sfmt, rows, cols, blk_r, blk_c, Fp8Groups{}, st);
     const int sc = (cols + blk_c - 1) / blk_c;
     Fp8Geom g;
     const bool aligned = (((uintptr_t)x | (uintptr_t)W) & 15) == 0;

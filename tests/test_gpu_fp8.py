@@ -167,8 +167,11 @@ def test_reference_gpu_gate(gpu, dsv4):
     assert common.bits_equal(dsv4.mmq_n(m, xn[:1])[0], dsv4.mmq(m, xn[0]))
 
 
-@pytest.mark.parametrize("rows,cols,nt", [(300, 1536, 5), (129, 7168, 64), (40, 64, 3)])
+@pytest.mark.parametrize("rows,cols,nt", [(300, 1536, 5), (129, 7168, 64), (40, 64, 3),
+                                          (500, 2048, 13), (70, 16384, 2), (33, 4096, 9)])
 def test_batched_bit_identical(gpu, dsv4, rows, cols, nt):
+    """Token blocks of 8, 4 and 2 in LDS, ragged last blocks included: every
+    token's row equals the single-token GEMV's bits."""
     W, Sf, Se, _ = common.fp8_problem(21, rows, cols)
     x = np.random.default_rng(22).standard_normal((nt, cols), dtype=np.float32)
     y1, m = _run(dsv4, W, Se, x[0])

@@ -55,8 +55,11 @@ __device__ __forceinline__ double block_sum_d(double v)
 /* Vector b = blockIdx.x: y = src_b (times inv = 1/sqrt(mean square + eps)
  * when norm, then times w when given), its last rd elements rotated at pos.
  * Every element is read and written by one thread (the pairs of the tail by
- * the thread that owns the pair, after the norm's barrier), so dst may alias
- * src. */
+ * the thread that owns the pair), so dst may alias src. Up to NR_E elements
+ * per thread every load (x, w, the pair's cos / sin) is issued at the start,
+ * before the norm's reduction, so the kernel waits for memory once. */
+constexpr int NR_E = 4;
+
 __global__ void __launch_bounds__(NR_THREADS)
 k_norm_rope(float *dst, int dst_stride, const float *src, int src_stride,
             const float *__restrict__ w, int n, int norm, float eps, int rd,
@@ -65,24 +68,74 @@ k_norm_rope(float *dst, int dst_stride, const float *src, int src_stride,
 {
     const float *x = src + (size_t)blockIdx.x * src_stride;
     float *y = dst + (size_t)blockIdx.x * dst_stride;
+    const int tid = threadIdx.x;
+    const int t0 = n - rd;
+    if (n <= NR_E * NR_THREADS && rd / 2 <= NR_THREADS) {
+        float xv[NR_E], wv[NR_E];
+#pragma unroll
+        for (int e = 0; e < NR_E; e++) {
+            const int i = tid + e * NR_THREADS;
+            xv[e] = i < n ? x[i] : 0.0f;
+            wv[e] = (w && i < t0) ? w[i] : 1.0f;
+        }
+        /* this thread's RoPE pair */
+        const int pp = tid;
+        const bool hp = pp < rd / 2;
+        float re = 0.0f, im = 0.0f, wa = 1.0f, wb = 1.0f, c = 1.0f, s0 = 0.0f;
+        if (hp) {
+            re = x[t0 + 2 * pp];
+            im = x[t0 + 2 * pp + 1];
+            if (w) { wa = w[t0 + 2 * pp]; wb = w[t0 + 2 * pp + 1]; }
+            c = cs[(size_t)pos * half + pp];
+            s0 = sn[(size_t)pos * half + pp];
+        }
+        float inv = 1.0f;
+        if (norm) {
+            double sq = 0.0;
+#pragma unroll
+            for (int e = 0; e < NR_E; e++) {
+                const double v = (double)xv[e];
+                sq += v * v;
+            }
+            sq = block_sum_d(sq);
+            inv = (float)(1.0 / sqrt(sq / (double)n + (double)eps));
+        }
+#pragma unroll
+        for (int e = 0; e < NR_E; e++) {
+            const int i = tid + e * NR_THREADS;
+            if (i < t0) {
+                float v = xv[e];
+                if (norm) v = v * inv;
+                if (w) v = wv[e] * v;
+                y[i] = v;
+            }
+        }
+        if (hp) {
+            if (norm) { re = re * inv; im = im * inv; }
+            if (w) { re = wa * re; im = wb * im; }
+            const float sv = inverse ? -s0 : s0;
+            y[t0 + 2 * pp] = re * c - im * sv;
+            y[t0 + 2 * pp + 1] = re * sv + im * c;
+        }
+        return;
+    }
     float inv = 1.0f;
     if (norm) {
         double sq = 0.0;
-        for (int i = threadIdx.x; i < n; i += NR_THREADS) {
+        for (int i = tid; i < n; i += NR_THREADS) {
             const double v = (double)x[i];
             sq += v * v;
         }
         sq = block_sum_d(sq);
         inv = (float)(1.0 / sqrt(sq / (double)n + (double)eps));
     }
-    const int t0 = n - rd;
-    for (int i = threadIdx.x; i < t0; i += NR_THREADS) {
+    for (int i = tid; i < t0; i += NR_THREADS) {
         float v = x[i];
         if (norm) v = v * inv;
         if (w) v = w[i] * v;
         y[i] = v;
     }
-    for (int p = threadIdx.x; p < rd / 2; p += NR_THREADS) {
+    for (int p = tid; p < rd / 2; p += NR_THREADS) {
         const int i = t0 + 2 * p;
         float re = x[i], im = x[i + 1];
         if (norm) { re = re * inv; im = im * inv; }

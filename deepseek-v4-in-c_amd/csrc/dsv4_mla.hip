@@ -1097,71 +1097,103 @@ k_attn_partial(float *__restrict__ pm, float *__restrict__ pl,
     __syncthreads();
     if (qnorm || qrp.rd) {
         /* the attention block's q: each head scaled by 1/sqrt(mean square +
-         * eps) and RoPE'd at pos (dsv4_layer.c:223-231), a wave per head,
-         * after the rows are staged (their loads went out first) */
+         * eps) and RoPE'd at pos (dsv4_layer.c:223-231), after the rows are
+         * staged (their loads went out first). All heads at once: QL lanes
+         * per head (a half wave for AT_HB = 8). */
+        constexpr int QL = AT_THREADS / AT_HB;
         const int t0 = d_qk - qrp.rd;
-        for (int hh = wid; hh < AT_HB; hh += AT_THREADS / 64) {
-            float *qh = qs + hh * ldq;
-            float inv = 1.0f;
-            if (qnorm) {
-                double sq = 0.0;
-                for (int c = lane; c < d_qk; c += 64) {
-                    const double v = (double)qh[c];
-                    sq += v * v;
-                }
+        const int hh = tid / QL, ql = tid - hh * QL;
+        float *qh = qs + hh * ldq;
+        float inv = 1.0f;
+        if (qnorm) {
+            double sq = 0.0;
+            for (int c = ql; c < d_qk; c += QL) {
+                const double v = (double)qh[c];
+                sq += v * v;
+            }
 #pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
-                inv = (float)(1.0 / sqrt(sq / (double)d_qk + (double)qeps));
-                for (int c = lane; c < t0; c += 64) qh[c] = qh[c] * inv;
-            }
-            for (int p = lane; p < qrp.rd / 2; p += 64) {
-                float a = qh[t0 + 2 * p], b = qh[t0 + 2 * p + 1];
-                if (qnorm) { a = a * inv; b = b * inv; }
-                rope_pair_cs(a, b, rcs[p], rsn[p], qrp.inverse);
-                qh[t0 + 2 * p] = a;
-                qh[t0 + 2 * p + 1] = b;
-            }
+            for (int o = QL / 2; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
+            inv = (float)(1.0 / sqrt(sq / (double)d_qk + (double)qeps));
+            for (int c = ql; c < t0; c += QL) qh[c] = qh[c] * inv;
+        }
+        for (int p = ql; p < qrp.rd / 2; p += QL) {
+            float a = qh[t0 + 2 * p], b = qh[t0 + 2 * p + 1];
+            if (qnorm) { a = a * inv; b = b * inv; }
+            rope_pair_cs(a, b, rcs[p], rsn[p], qrp.inverse);
+            qh[t0 + 2 * p] = a;
+            qh[t0 + 2 * p + 1] = b;
         }
         __syncthreads();
     }
 
-    /* scores: thread (hh, lt) takes rows lt, lt + 32, ... */
+    /* scores: the AT_HB x SR (head, row) pairs over every lane. A pair's dot
+     * is split over LPP lanes that sit 64 / LPP apart in the wave (each takes
+     * every LPP-th 8-column piece), so the 16-lane groups that read the LDS
+     * together hold 16 different rows (the row pitch's 16-byte skew keeps
+     * them on different banks) and the lanes of one head read q as a
+     * broadcast. */
     {
-        const int hh = tid >> 5, lt = tid & 31;
-        const float *qr = qs + hh * ldq;
-        for (int jj = lt; jj < SR; jj += 32) {
+        const int pairs = AT_HB * SR;
+        const int LPP = pairs >= AT_THREADS ? 1 : (pairs * 2 >= AT_THREADS ? 2 : 4);
+        const int span = 64 / LPP;                         /* pairs per wave per pass */
+        const int part = lane / span, pl = lane - part * span;
+        for (int pr0 = wid * span; pr0 < pairs; pr0 += (AT_THREADS / 64) * span) {
+            const int pr = pr0 + pl;
+            const bool live = pr < pairs;
+            const int hh = live ? pr / SR : 0, jj = live ? pr - (pr / SR) * SR : 0;
+            const float *qr = qs + hh * ldq;
             const unsigned char *kr = kvs + (size_t)jj * rowb;
-            float a0 = 0.0f, a1 = 0.0f;
-            int c = 0;
+            float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
             if (vec) {
-                for (; c + 8 <= d_qk; c += 8) {
+#pragma unroll 4
+                for (int c = 8 * part; c + 8 <= d_qk; c += 8 * LPP) {
                     float kk[8];
                     row8<KVF>(kr + (size_t)c * ES, kk);
                     const f32x4 qa = *reinterpret_cast<const f32x4 *>(qr + c);
                     const f32x4 qb = *reinterpret_cast<const f32x4 *>(qr + c + 4);
                     a0 = fmaf(qa.x, kk[0], a0); a1 = fmaf(qa.y, kk[1], a1);
-                    a0 = fmaf(qa.z, kk[2], a0); a1 = fmaf(qa.w, kk[3], a1);
+                    a2 = fmaf(qa.z, kk[2], a2); a3 = fmaf(qa.w, kk[3], a3);
                     a0 = fmaf(qb.x, kk[4], a0); a1 = fmaf(qb.y, kk[5], a1);
-                    a0 = fmaf(qb.z, kk[6], a0); a1 = fmaf(qb.w, kk[7], a1);
+                    a2 = fmaf(qb.z, kk[6], a2); a3 = fmaf(qb.w, kk[7], a3);
                 }
+                for (int c = (d_qk & ~7) + part; c < d_qk; c += LPP)
+                    a0 = fmaf(qr[c], row1<KVF>(kr, c), a0);
+            } else {
+                for (int c = part; c < d_qk; c += LPP) a0 = fmaf(qr[c], row1<KVF>(kr, c), a0);
             }
-            for (; c < d_qk; c++) a0 = fmaf(qr[c], row1<KVF>(kr, c), a0);
-            const float sc = (a0 + a1) * scale;
-            ps[jj * AT_HB + hh] = sidx[jj] >= 0 ? sc : -INFINITY;
+            float v = (a0 + a1) + (a2 + a3);
+            for (int o = span; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+            if (live && part == 0) ps[jj * AT_HB + hh] = sidx[jj] >= 0 ? v * scale : -INFINITY;
         }
     }
     __syncthreads();
 
-    /* split softmax: wave per head, lane per row */
-    for (int hh = wid; hh < AT_HB; hh += AT_THREADS / 64) {
-        const float sv = lane < SR ? ps[lane * AT_HB + hh] : -INFINITY;
-        const float m = wave_max(sv);
-        const float e = (m == -INFINITY || sv == -INFINITY) ? 0.0f : expf(sv - m);
-        if (lane < SR) ps[lane * AT_HB + hh] = e;
-        const float l = wave_sum(e);
-        if (lane == 0 && hh < nh) {
-            pm[(size_t)(h0 + hh) * nsplit + split] = m;
-            pl[(size_t)(h0 + hh) * nsplit + split] = l;
+    /* split softmax: G = SR lanes per head (SR is a power of two), 64 / G
+     * heads per wave side by side */
+    {
+        const int G = SR < 64 ? SR : 64;
+        const int hpw = 64 / G;
+        const int gi = lane / G, gl = lane - gi * G;
+        for (int hb = wid * hpw; hb < AT_HB; hb += (AT_THREADS / 64) * hpw) {
+            const int hh = hb + gi;
+            const bool hv = hh < AT_HB;
+            float mx = -INFINITY;
+            for (int j = gl; j < SR; j += G)
+                if (hv) mx = fmaxf(mx, ps[j * AT_HB + hh]);
+            for (int o = G / 2; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            float l = 0.0f;
+            for (int j = gl; j < SR; j += G) {
+                if (!hv) continue;
+                const float sv = ps[j * AT_HB + hh];
+                const float e = (mx == -INFINITY || sv == -INFINITY) ? 0.0f : expf(sv - mx);
+                ps[j * AT_HB + hh] = e;
+                l += e;
+            }
+            for (int o = G / 2; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+            if (gl == 0 && hv && hh < nh) {
+                pm[(size_t)(h0 + hh) * nsplit + split] = mx;
+                pl[(size_t)(h0 + hh) * nsplit + split] = l;
+            }
         }
     }
     __syncthreads();
@@ -1172,10 +1204,17 @@ k_attn_partial(float *__restrict__ pm, float *__restrict__ pl,
         float acc0[AT_HB], acc1[AT_HB];
 #pragma unroll
         for (int hh = 0; hh < AT_HB; hh++) { acc0[hh] = 0.0f; acc1[hh] = 0.0f; }
+#pragma unroll 4
         for (int jj = 0; jj < SR; jj++) {
             const unsigned char *kr = kvs + (size_t)jj * rowb;
-            const float v0 = row1<KVF>(kr, c);
-            const float v1 = two ? row1<KVF>(kr, c + 1) : 0.0f;
+            float v0, v1;
+            if (KVF == DSV4_GPU_KV_F32 && two) {
+                const float2 v = *reinterpret_cast<const float2 *>(kr + (size_t)c * 4);
+                v0 = v.x; v1 = v.y;
+            } else {
+                v0 = row1<KVF>(kr, c);
+                v1 = two ? row1<KVF>(kr, c + 1) : 0.0f;
+            }
             const f32x4 pa = *reinterpret_cast<const f32x4 *>(ps + jj * AT_HB);
             const f32x4 pb = *reinterpret_cast<const f32x4 *>(ps + jj * AT_HB + 4);
             const float pp[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
@@ -1189,8 +1228,12 @@ k_attn_partial(float *__restrict__ pm, float *__restrict__ pl,
         for (int hh = 0; hh < AT_HB; hh++) {
             if (hh < nh) {
                 float *dst = po + ((size_t)(h0 + hh) * nsplit + split) * d_v + c;
-                dst[0] = acc0[hh];
-                if (two) dst[1] = acc1[hh];
+                if (two && (d_v & 1) == 0) {
+                    *reinterpret_cast<float2 *>(dst) = make_float2(acc0[hh], acc1[hh]);
+                } else {
+                    dst[0] = acc0[hh];
+                    if (two) dst[1] = acc1[hh];
+                }
             }
         }
     }

@@ -5,21 +5,21 @@
  * five to nine GEMVs (the FP8 / BF16 kernels of this library), the CSA
  * score / top-k / sparse attention (dsv4_mla.hip), and the element-wise steps
  * here:
- *   - k_norm_rope: RMSNorm (dsv4_ops.c:24-31, weighted) or the per-head norm
- *     of q (dsv4_layer.c:223-229, unweighted), then RoPE of the last rd
- *     elements (dsv4_rope.c:105-119, interleaved pairs; inverse negates the
- *     sine) -- either step optional, one workgroup per vector, the result
- *     written where the caller wants it (a ring slot of the KV cache, a
- *     compressed row);
- *   - k_comp_update / k_comp_pool: the compressor's decode step
- *     (dsv4_compress.c:77-137): the token into its slot with score + ape,
- *     and when a window closes the per-channel softmax pool over the slots
+ *   - k_norm_rope: RMSNorm (dsv4_ops.c:24-31, weighted) of a vector, then
+ *     RoPE of the last rd elements (dsv4_rope.c:105-119, interleaved pairs;
+ *     inverse negates the sine) -- either step optional, one workgroup per
+ *     vector, the result written where the caller wants it (a compressed
+ *     row of the KV cache);
+ *   - k_block_prep: what the step needs right after the x projections, in
+ *     one launch -- q's learned norm, kv_norm + RoPE into the ring slot, and
+ *     the compressor's token into its slot with score + ape
+ *     (dsv4_compress.c:87-98);
+ *   - k_comp_pool: the compressor's pool when a window closes
+ *     (dsv4_compress.c:100-137): the per-channel softmax pool over the slots
  *     (ratio 4: the previous window's first halves and the current window's
- *     second halves), then the ratio-4 slide;
- *   - k_attn_idxs: the row list of the sparse attention -- the window's ring
- *     slots newest first (dsv4_attn.c:118-128), then the compressed rows
- *     (all of them, or the indexer's selection) offset past the window
- *     (dsv4_indexer.c:113-117).
+ *     second halves), then the ratio-4 slide.
+ * The attention's row list (the window's ring slots, then the compressed
+ * rows) is built inside the attention kernel (Dsv4Rows).
  *
  * NUMERICS. Sums of squares and the pool's sums are in double like the
  * reference's, but as trees over the workgroup instead of one sequential
@@ -60,14 +60,11 @@ __device__ __forceinline__ double block_sum_d(double v)
  * before the norm's reduction, so the kernel waits for memory once. */
 constexpr int NR_E = 4;
 
-__global__ void __launch_bounds__(NR_THREADS)
-k_norm_rope(float *dst, int dst_stride, const float *src, int src_stride,
-            const float *__restrict__ w, int n, int norm, float eps, int rd,
-            const float *__restrict__ cs, const float *__restrict__ sn, int pos, int half,
-            int inverse)
+__device__ __forceinline__ void
+norm_rope_vec(float *y, const float *x, const float *__restrict__ w, int n, int norm, float eps,
+              int rd, const float *__restrict__ cs, const float *__restrict__ sn, int pos,
+              int half, int inverse)
 {
-    const float *x = src + (size_t)blockIdx.x * src_stride;
-    float *y = dst + (size_t)blockIdx.x * dst_stride;
     const int tid = threadIdx.x;
     const int t0 = n - rd;
     if (n <= NR_E * NR_THREADS && rd / 2 <= NR_THREADS) {
@@ -148,17 +145,32 @@ k_norm_rope(float *dst, int dst_stride, const float *src, int src_stride,
     }
 }
 
-/* The token's slot: kv_state row = kv_in, score_state row = score_in + ape
- * row (the caller passes the slot's and the phase's rows). */
 __global__ void __launch_bounds__(NR_THREADS)
-k_comp_update(float *__restrict__ kvs, float *__restrict__ scs,
-              const float *__restrict__ kv_in, const float *__restrict__ sc_in,
-              const float *__restrict__ apr, int width)
+k_norm_rope(float *dst, int dst_stride, const float *src, int src_stride,
+            const float *__restrict__ w, int n, int norm, float eps, int rd,
+            const float *__restrict__ cs, const float *__restrict__ sn, int pos, int half,
+            int inverse)
 {
-    const int c = blockIdx.x * NR_THREADS + threadIdx.x;
-    if (c >= width) return;
-    kvs[c] = kv_in[c];
-    scs[c] = sc_in[c] + apr[c];
+    norm_rope_vec(dst + (size_t)blockIdx.x * dst_stride, src + (size_t)blockIdx.x * src_stride,
+                  w, n, norm, eps, rd, cs, sn, pos, half, inverse);
+}
+
+/* The attention block's step after its x projections, in one launch:
+ * workgroup j < nj runs norm job j (norm_rope_vec), the rest copy the
+ * compressor's token into its slot (k_comp_update's work). The jobs touch
+ * disjoint memory. */
+__global__ void __launch_bounds__(NR_THREADS)
+k_block_prep(Dsv4Prep a)
+{
+    if ((int)blockIdx.x < a.nj) {
+        const Dsv4NormJob &j = a.job[blockIdx.x];
+        norm_rope_vec(j.dst, j.src, j.w, j.n, 1, a.eps, j.rd, a.cs, a.sn, a.pos, a.half, 0);
+        return;
+    }
+    const int c = ((int)blockIdx.x - a.nj) * NR_THREADS + threadIdx.x;
+    if (c >= a.width) return;
+    a.kvs[c] = a.kv_in[c];
+    a.scs[c] = a.sc_in[c] + a.apr[c];
 }
 
 /* Channel c of the closing window's pool. ov (ratio 4): slots 0..ratio-1
@@ -205,25 +217,6 @@ k_comp_pool(float *__restrict__ out, float *__restrict__ kvst, float *__restrict
     }
 }
 
-/* idxs[0, n_win): ring slots (pos - k) % win; idxs[n_win, n_win + take):
- * mode 1 every compressed row (offset + j), mode 2 the selection already
- * written there by the top-k, offset where >= 0. */
-__global__ void __launch_bounds__(NR_THREADS)
-k_attn_idxs(int *__restrict__ idxs, int pos, int win, int n_win, int take, int mode,
-            int offset)
-{
-    for (int i = threadIdx.x; i < n_win + take; i += NR_THREADS) {
-        if (i < n_win) {
-            idxs[i] = (pos - i) % win;
-        } else if (mode == 1) {
-            idxs[i] = offset + (i - n_win);
-        } else {
-            const int v = idxs[i];
-            idxs[i] = v >= 0 ? v + offset : v;
-        }
-    }
-}
-
 } // namespace
 
 int dsv4_norm_rope_launch(float *dst, int dst_stride, const float *src, int src_stride,
@@ -242,15 +235,24 @@ int dsv4_norm_rope_launch(float *dst, int dst_stride, const float *src, int src_
     return 0;
 }
 
-int dsv4_comp_update_launch(float *kv_row, float *score_row, const float *kv_in,
-                            const float *score_in, const float *ape_row, int width,
-                            hipStream_t st)
+int dsv4_block_prep_launch(const Dsv4Prep *a, hipStream_t st)
 {
-    if (width <= 0) return -1;
-    hipLaunchKernelGGL(k_comp_update, dim3((width + NR_THREADS - 1) / NR_THREADS),
-                       dim3(NR_THREADS), 0, st, kv_row, score_row, kv_in, score_in,
-                       ape_row, width);
-    HIP_OK(hipGetLastError(), "comp_update launch");
+    if (a->nj < 0 || a->nj > 2 || a->width < 0 || (a->width && (!a->kvs || !a->scs))) {
+        DSV4_ERR("block_prep: bad arguments (nj %d width %d)", a->nj, a->width);
+        return -1;
+    }
+    for (int i = 0; i < a->nj; i++) {
+        const Dsv4NormJob &j = a->job[i];
+        if (j.n <= 0 || j.rd < 0 || j.rd > j.n || (j.rd & 1) || (j.rd && (!a->cs || !a->sn)) ||
+            a->pos < 0 || (j.rd && a->half < j.rd / 2)) {
+            DSV4_ERR("block_prep: bad norm job %d (n %d rd %d)", i, j.n, j.rd);
+            return -1;
+        }
+    }
+    const int nb = a->nj + (a->width + NR_THREADS - 1) / NR_THREADS;
+    if (nb == 0) return 0;
+    hipLaunchKernelGGL(k_block_prep, dim3(nb), dim3(NR_THREADS), 0, st, *a);
+    HIP_OK(hipGetLastError(), "block_prep launch");
     return 0;
 }
 
@@ -262,15 +264,5 @@ int dsv4_comp_pool_launch(float *out, float *kv_state, float *score_state, int r
                        dim3(NR_THREADS), 0, st, out, kv_state, score_state, ratio, hd,
                        ratio == 4 ? 1 : 0);
     HIP_OK(hipGetLastError(), "comp_pool launch");
-    return 0;
-}
-
-int dsv4_attn_idxs_launch(int *idxs, int pos, int win, int n_win, int take, int mode,
-                          int offset, hipStream_t st)
-{
-    if (win <= 0 || n_win < 0 || n_win > win || take < 0 || pos < 0) return -1;
-    hipLaunchKernelGGL(k_attn_idxs, dim3(1), dim3(NR_THREADS), 0, st, idxs, pos, win, n_win,
-                       take, mode, offset);
-    HIP_OK(hipGetLastError(), "attn_idxs launch");
     return 0;
 }

@@ -1221,22 +1221,31 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
     }
     if (use_idx) xj[nx++] = XJob{&b.iwproj, b.idx_w, c.idx_heads};
     OK(x_gemvs(xj, nx, d_x, st));
-    /* q: the learned norm, wq_b, then each head's norm and RoPE */
-    OK(dsv4_norm_rope_launch(b.qr, 0, b.qr, 0, b.q_norm, 1, c.q_lora, 1, c.rms_eps, 0,
-                             nullptr, nullptr, 0, 0, 0, st));
+    /* One launch for what needs only the projections: q's learned norm (in
+     * place), kv_norm + RoPE into the ring slot, and the compressor's token
+     * into its slot (dsv4_layer.c:222, 235-238, and the slot write of the
+     * compress step called at :250) */
+    Dsv4Prep pp{};
+    pp.job[0] = Dsv4NormJob{b.qr, b.qr, b.q_norm, c.q_lora, 0};
+    pp.job[1] = Dsv4NormJob{b.kv_cache + (size_t)(pos % c.window) * hd, b.kv, b.kv_norm, hd, rd};
+    pp.nj = 2;
+    pp.eps = c.rms_eps;
+    pp.cs = b.cs; pp.sn = b.sn; pp.pos = pos; pp.half = half;
+    if (c.ratio > 0) {
+        const int ph = pos % c.ratio, slot = c.ratio == 4 ? c.ratio + ph : ph;
+        pp.kvs = b.comp_kv + (size_t)slot * b.width;
+        pp.scs = b.comp_score + (size_t)slot * b.width;
+        pp.kv_in = b.ckv; pp.sc_in = b.csc; pp.apr = b.ape + (size_t)ph * b.width;
+        pp.width = b.width;
+    }
+    OK(dsv4_block_prep_launch(&pp, st));
+    /* q: wq_b (each head's norm and RoPE happen inside the attention, on its
+     * copy) */
     OK(res_gemv(b.wq_b.r, b.wq_b.r0, H * hd, b.q, b.qr, st));
-    /* (each head's norm and RoPE happen inside the attention, on its copy) */
-    /* kv: kv_norm, RoPE, into the ring slot */
-    OK(dsv4_norm_rope_launch(b.kv_cache + (size_t)(pos % c.window) * hd, 0, b.kv, 0, b.kv_norm,
-                             1, hd, 1, c.rms_eps, rd, b.cs, b.sn, pos, half, 0, st));
     const int n_win = pos + 1 < c.window ? pos + 1 : c.window;
     int take = 0, mode = 1;
     if (c.ratio > 0) {
-        /* the compressor (dsv4_layer.c:243-261) */
-        const int ph = pos % c.ratio, slot = c.ratio == 4 ? c.ratio + ph : ph;
-        OK(dsv4_comp_update_launch(b.comp_kv + (size_t)slot * b.width,
-                                   b.comp_score + (size_t)slot * b.width, b.ckv, b.csc,
-                                   b.ape + (size_t)ph * b.width, b.width, st));
+        /* the compressor's pool when the window closes (dsv4_layer.c:250-261) */
         if (closes) {
             if (b.n_comp >= b.max_comp) {
                 DSV4_ERR("attn_step: compressed rows exceed max_pos / ratio + 1");
@@ -1269,13 +1278,15 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
             take = avail;
         }
     }
-    OK(dsv4_attn_idxs_launch(b.idxs, pos, c.window, n_win, take, mode, c.window, st));
-    /* the attention with q's per-head norm and RoPE, and the output's
-     * de-rotation, folded in */
+    /* the attention with its row list (window, then compressed rows), q's
+     * per-head norm and RoPE, and the output's de-rotation, folded in */
+    Dsv4Rows rw;
+    rw.on = 1;
+    rw.win = c.window; rw.n_win = n_win; rw.pos = pos; rw.mode = mode; rw.offset = c.window;
     OK(dsv4_attn_block_launch(b.o, b.q, b.kv_cache, DSV4_GPU_KV_F32, hd,
-                              c.window + b.max_comp, b.sink, b.idxs, H, hd, hd, n_win + take,
-                              1.0f / sqrtf((float)hd), b.ascr, 1, c.rms_eps, b.cs, b.sn, pos,
-                              half, rd, st));
+                              c.window + b.max_comp, b.sink, b.idxs + n_win, H, hd, hd,
+                              n_win + take, 1.0f / sqrtf((float)hd), b.ascr, 1, c.rms_eps,
+                              b.cs, b.sn, pos, half, rd, st, &rw));
     /* wo_a's groups in one launch (the FP8 slices of dsv4_layer.c:321-334:
      * group g's rows from g * o_lora, its scale rows from g * (o_lora /
      * blk_r), its input o + g * (H * hd / o_groups)), then wo_b */

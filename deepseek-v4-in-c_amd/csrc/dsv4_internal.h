@@ -130,17 +130,29 @@ int dsv4_topk_launch(int *d_idxs, const float *d_scores, int n, int k,
 /* Scratch needed by dsv4_attn_launch, in bytes (0: shape not supported). */
 size_t dsv4_attn_scratch_bytes(int h, int d_qk, int d_v, int topk, int kv_fmt);
 
+/* The attention block's row list, built inside the attention kernel
+ * instead of in memory: rows j < n_win are the ring slots (pos - j) % win,
+ * then mode 1 takes offset + (j - n_win) (every compressed row) and mode 2
+ * takes d_idxs[j - n_win] + offset (the top-k's selection; negative entries
+ * stay negative and are skipped). on == 0: d_idxs[j] as given. */
+struct Dsv4Rows {
+    int on = 0;
+    int win = 0, n_win = 0, pos = 0, mode = 0, offset = 0;
+};
+
 /* The attention block's form: q_norm scales each head of q by 1/sqrt(mean
  * square + q_eps) and rope_dim > 0 RoPEs its last rope_dim elements at
  * rope_pos before the scores (dsv4_layer.c:223-231), and de-rotates the
  * output's last rope_dim elements after them (:304-305) -- on the kernels'
- * own copies; d_q is not written. */
+ * own copies; d_q is not written. rows: the row list as above (nullptr:
+ * d_idxs as given). */
 int dsv4_attn_block_launch(float *d_o, const float *d_q, const void *d_kv,
                            int kv_fmt, int kv_stride, int kv_rows,
                            const float *d_sink, const int *d_idxs, int h, int d_qk,
                            int d_v, int topk, float scale, void *scratch, int q_norm,
                            float q_eps, const float *rope_cs, const float *rope_sn,
-                           int rope_pos, int rope_half, int rope_dim, hipStream_t st);
+                           int rope_pos, int rope_half, int rope_dim, hipStream_t st,
+                           const Dsv4Rows *rows = nullptr);
 
 /* The indexer score with its q RoPE'd at rope_pos first (rope_dim 0: as
  * given), on the kernel's own copy. */
@@ -170,17 +182,30 @@ int dsv4_norm_rope_launch(float *dst, int dst_stride, const float *src, int src_
                           const float *cs, const float *sn, int pos, int half, int inverse,
                           hipStream_t st);
 
-/* The compressor: the token's state rows (kv_row = kv_in, score_row =
- * score_in + ape_row over width floats), and the pool of a closing window
- * into out[hd] (with the ratio-4 slide). */
-int dsv4_comp_update_launch(float *kv_row, float *score_row, const float *kv_in,
-                            const float *score_in, const float *ape_row, int width,
-                            hipStream_t st);
+/* One RMSNorm (+ RoPE of the last rd elements at pos) of the block prep. */
+struct Dsv4NormJob {
+    float *dst;
+    const float *src;
+    const float *w;
+    int n, rd;
+};
+/* The attention block's prep launch: up to two norm jobs (weighted RMSNorm,
+ * optional RoPE, eps and the RoPE table shared) and the compressor's slot
+ * update (kvs = kv_in, scs = sc_in + apr over width; width 0 for none). */
+struct Dsv4Prep {
+    Dsv4NormJob job[2];
+    int nj;
+    float eps;
+    const float *cs, *sn;
+    int pos, half;
+    float *kvs, *scs;
+    const float *kv_in, *sc_in, *apr;
+    int width;
+};
+int dsv4_block_prep_launch(const Dsv4Prep *a, hipStream_t st);
+
+/* The compressor's pool of a closing window into out[hd] (with the ratio-4
+ * slide). */
 int dsv4_comp_pool_launch(float *out, float *kv_state, float *score_state, int ratio,
                           int hd, hipStream_t st);
 
-/* The sparse attention's row list: n_win ring slots, then take compressed
- * rows (mode 1: all, offset + j; mode 2: the selection already in place,
- * offset where >= 0). */
-int dsv4_attn_idxs_launch(int *idxs, int pos, int win, int n_win, int take, int mode,
-                          int offset, hipStream_t st);

@@ -975,6 +975,21 @@ __device__ __forceinline__ float row1(const unsigned char *p, int c)
     return ((const float *)p)[c];
 }
 
+/* Selected row j of the attention: idxs[j], or with rw.on the attention
+ * block's list built in place -- the window's ring slots newest first
+ * (dsv4_attn.c:118-128), then the compressed rows offset past the window
+ * (dsv4_indexer.c:113-117): all of them (mode 1) or the top-k's selection in
+ * idxs[0 ...] (mode 2, negative entries kept). */
+__device__ __forceinline__ int sel_row(const int *__restrict__ idxs, const Dsv4Rows &rw, int j)
+{
+    if (!rw.on) return idxs[j];
+    if (j < rw.n_win) return (rw.pos - j) % rw.win;
+    const int k = j - rw.n_win;
+    if (rw.mode == 1) return rw.offset + k;
+    const int v = idxs[k];
+    return v >= 0 ? v + rw.offset : v;
+}
+
 /* One split of SR selected rows x one group of AT_HB heads.
  *   stage : the SR rows are gathered into LDS (every thread's loads in
  *           flight at once), with q of the group's heads;
@@ -989,7 +1004,7 @@ k_attn_partial(float *__restrict__ pm, float *__restrict__ pl,
                const void *__restrict__ kv, int kv_stride,
                const int *__restrict__ idxs, int kv_rows, int h, int d_qk,
                int d_v, int topk, float scale, int SR, int rowb, int vec, int qnorm,
-               float qeps, Dsv4Rope qrp)
+               float qeps, Dsv4Rope qrp, Dsv4Rows rw)
 {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds_b[];
     constexpr int ES = KVF == DSV4_GPU_KV_BF16 ? 2 : 4;
@@ -1013,7 +1028,7 @@ k_attn_partial(float *__restrict__ pm, float *__restrict__ pl,
     /* the split's row indices: loaded first, stored with q (so their wait is
      * q's) */
     int ridx = -1;
-    if (tid < SR && tid < nj) ridx = idxs[j0 + tid];
+    if (tid < SR && tid < nj) ridx = sel_row(idxs, rw, j0 + tid);
     /* Staging issues a whole batch of loads before storing any of them: one
      * memory latency per batch rather than per element. */
     constexpr int SB = 8;
@@ -1847,8 +1862,16 @@ int dsv4_attn_block_launch(float *d_o, const float *d_q, const void *d_kv,
                            const float *d_sink, const int *d_idxs, int h, int d_qk,
                            int d_v, int topk, float scale, void *scratch, int q_norm,
                            float q_eps, const float *rope_cs, const float *rope_sn,
-                           int rope_pos, int rope_half, int rope_dim, hipStream_t st)
+                           int rope_pos, int rope_half, int rope_dim, hipStream_t st,
+                           const Dsv4Rows *rows)
 {
+    const Dsv4Rows rw = rows ? *rows : Dsv4Rows{};
+    if (rw.on && (rw.win <= 0 || rw.n_win < 0 || rw.n_win > rw.win || rw.n_win > topk ||
+                  rw.pos < 0 || (rw.mode != 1 && rw.mode != 2))) {
+        DSV4_ERR("sparse attn: bad row list (win %d n_win %d mode %d)", rw.win, rw.n_win,
+                 rw.mode);
+        return -1;
+    }
     if (rope_dim < 0 || (rope_dim & 1) || rope_dim > d_qk || rope_dim > d_v ||
         rope_dim > 2 * RP_MAX || (rope_dim && ((d_v & 1) || !rope_cs || !rope_sn))) {
         DSV4_ERR("sparse attn: bad RoPE (dim %d, d_qk %d, d_v %d)", rope_dim, d_qk, d_v);
@@ -1910,7 +1933,7 @@ int dsv4_attn_block_launch(float *d_o, const float *d_q, const void *d_kv,
      * the VALU form) */
     const size_t mc_lds = attn_mc_lds(kv_fmt, h, d_qk, d_v, kv_stride);
     const char *mc_env = getenv("DSV4_GPU_ATTN_MC");
-    if (mc_lds && !qx && topk > 0 && ((uintptr_t)d_kv & 15) == 0 &&
+    if (mc_lds && !qx && !rw.on && topk > 0 && ((uintptr_t)d_kv & 15) == 0 &&
         !(mc_env && atoi(mc_env) == 0)) {
         const int ns = (topk + AM_SR - 1) / AM_SR;          /* <= nsplit: sr <= AM_SR */
         pl = pm + (size_t)h * ns;
@@ -1927,11 +1950,11 @@ int dsv4_attn_block_launch(float *d_o, const float *d_q, const void *d_kv,
     if (kv_fmt == DSV4_GPU_KV_BF16)
         hipLaunchKernelGGL((k_attn_partial<DSV4_GPU_KV_BF16>), grid, dim3(AT_THREADS), lds, st,
                            pm, pl, po, d_q, d_kv, kv_stride, d_idxs, kv_rows, h,
-                           d_qk, d_v, topk, scale, sr, rowb, vec, q_norm, q_eps, qrp);
+                           d_qk, d_v, topk, scale, sr, rowb, vec, q_norm, q_eps, qrp, rw);
     else
         hipLaunchKernelGGL((k_attn_partial<DSV4_GPU_KV_F32>), grid, dim3(AT_THREADS), lds, st,
                            pm, pl, po, d_q, d_kv, kv_stride, d_idxs, kv_rows, h,
-                           d_qk, d_v, topk, scale, sr, rowb, vec, q_norm, q_eps, qrp);
+                           d_qk, d_v, topk, scale, sr, rowb, vec, q_norm, q_eps, qrp, rw);
     HIP_OK(hipGetLastError(), "attn partial launch");
     hipLaunchKernelGGL(k_attn_combine, dim3(h, (d_v + CB_COLS - 1) / CB_COLS),
                        dim3(CB_COLS), 0, st, d_o, pm, pl, po, d_sink, nsplit, d_v, orp);

@@ -14,10 +14,12 @@
  *     one launch -- q's learned norm, kv_norm + RoPE into the ring slot, and
  *     the compressor's token into its slot with score + ape
  *     (dsv4_compress.c:87-98);
- *   - k_comp_pool: the compressor's pool when a window closes
- *     (dsv4_compress.c:100-137): the per-channel softmax pool over the slots
- *     (ratio 4: the previous window's first halves and the current window's
- *     second halves), then the ratio-4 slide.
+ *   - k_comp_close: a closing window in one launch -- the compressor's
+ *     pool (dsv4_compress.c:100-137: the per-channel softmax pool over the
+ *     slots; ratio 4: the previous window's first halves and the current
+ *     window's second halves), the ratio-4 slide, then comp.norm and RoPE of
+ *     the pooled row (dsv4_layer.c:252-255). Rows wider than 1024 channels
+ *     take k_comp_pool, then k_norm_rope.
  * The attention's row list (the window's ring slots, then the compressed
  * rows) is built inside the attention kernel (Dsv4Rows).
  *
@@ -217,6 +219,111 @@ k_comp_pool(float *__restrict__ out, float *__restrict__ kvst, float *__restrict
     }
 }
 
+/* A closing window in one launch, one workgroup, one thread per channel c
+ * (blockDim >= hd): the pool of k_comp_pool (the slot loads of a batch of 8
+ * issued together, the arithmetic in slot order), the ratio-4 slide, then
+ * k_norm_rope's weighted RMSNorm of the pooled row and RoPE of its last rd
+ * elements at pos, written to out. */
+constexpr int CC_MAX = 1024;
+
+__global__ void __launch_bounds__(CC_MAX)
+k_comp_close(float *__restrict__ out, float *__restrict__ kvst, float *__restrict__ scst,
+             int ratio, int hd, int ov, const float *__restrict__ w, float eps, int rd,
+             const float *__restrict__ cs, const float *__restrict__ sn, int pos, int half)
+{
+    __shared__ float row[CC_MAX];
+    __shared__ double part[CC_MAX / 64];
+    const int c = threadIdx.x;
+    const bool live = c < hd;
+    const int cc = live ? c : 0;
+    const int width = ov ? 2 * hd : hd;
+    const int slots = ov ? 2 * ratio : ratio;
+    const int t0 = hd - rd;
+    /* the RoPE pair's table entries and the weight, loaded with the slots */
+    const int p = (c - t0) >> 1;
+    const bool pr = live && c >= t0 && ((c - t0) & 1) == 0;
+    float rc = 1.0f, rs = 0.0f;
+    if (pr) {
+        rc = cs[(size_t)pos * half + p];
+        rs = sn[(size_t)pos * half + p];
+    }
+    const float wc = live ? w[cc] : 0.0f;
+    float mx = -INFINITY;
+    double den = 0.0, acc = 0.0;
+    for (int s0 = 0; s0 < slots; s0 += 8) {
+        float sv[8], kv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int s = min(s0 + u, slots - 1);
+            const int col = (ov && s >= ratio) ? hd + cc : cc;
+            sv[u] = scst[(size_t)s * width + col];
+            kv[u] = kvst[(size_t)s * width + col];
+        }
+        /* max first over all slots, so the batch's values stay for the
+         * second pass only when the whole window fits one batch */
+        if (slots <= 8) {
+            for (int u = 0; u < slots; u++) if (sv[u] > mx) mx = sv[u];
+            if (mx != -INFINITY)
+                for (int u = 0; u < slots; u++) {
+                    if (sv[u] == -INFINITY) continue;
+                    const double e = (double)expf(sv[u] - mx);
+                    den += e;
+                    acc += e * (double)kv[u];
+                }
+        } else {
+            for (int u = 0; u < 8 && s0 + u < slots; u++) if (sv[u] > mx) mx = sv[u];
+        }
+    }
+    if (slots > 8 && mx != -INFINITY) {
+        for (int s0 = 0; s0 < slots; s0 += 8) {
+            float sv[8], kv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int s = min(s0 + u, slots - 1);
+                const int col = (ov && s >= ratio) ? hd + cc : cc;
+                sv[u] = scst[(size_t)s * width + col];
+                kv[u] = kvst[(size_t)s * width + col];
+            }
+            for (int u = 0; u < 8 && s0 + u < slots; u++) {
+                if (sv[u] == -INFINITY) continue;
+                const double e = (double)expf(sv[u] - mx);
+                den += e;
+                acc += e * (double)kv[u];
+            }
+        }
+    }
+    const float r = (live && mx != -INFINITY) ? (float)(acc / den) : 0.0f;
+    if (live && ov) {
+        for (int s = 0; s < ratio; s++) {
+            const size_t to = (size_t)s * width, from = (size_t)(ratio + s) * width;
+            kvst[to + c] = kvst[from + c];
+            kvst[to + hd + c] = kvst[from + hd + c];
+            scst[to + c] = scst[from + c];
+            scst[to + hd + c] = scst[from + hd + c];
+        }
+    }
+    /* RMSNorm over the pooled row (sum of squares in double, a tree) */
+    double sq = live ? (double)r * (double)r : 0.0;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
+    if ((c & 63) == 0) part[c >> 6] = sq;
+    __syncthreads();
+    double t = part[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++) t += part[i];
+    const float inv = (float)(1.0 / sqrt(t / (double)hd + (double)eps));
+    const float v = wc * (r * inv);
+    row[c] = v;
+    __syncthreads();
+    if (!live) return;
+    if (c < t0) {
+        out[c] = v;
+    } else if (pr) {
+        const float re = v, im = row[c + 1];
+        out[c] = re * rc - im * rs;
+        out[c + 1] = re * rs + im * rc;
+    }
+}
+
 } // namespace
 
 int dsv4_norm_rope_launch(float *dst, int dst_stride, const float *src, int src_stride,
@@ -253,6 +360,22 @@ int dsv4_block_prep_launch(const Dsv4Prep *a, hipStream_t st)
     if (nb == 0) return 0;
     hipLaunchKernelGGL(k_block_prep, dim3(nb), dim3(NR_THREADS), 0, st, *a);
     HIP_OK(hipGetLastError(), "block_prep launch");
+    return 0;
+}
+
+int dsv4_comp_close_launch(float *out, float *kv_state, float *score_state, int ratio,
+                           int hd, const float *w, float eps, int rd, const float *cs,
+                           const float *sn, int pos, int half, hipStream_t st)
+{
+    if (ratio <= 0 || hd <= 0 || hd > CC_MAX || !w || rd < 0 || rd > hd || (rd & 1) ||
+        (rd && (!cs || !sn || half < rd / 2)) || pos < 0) {
+        DSV4_ERR("comp_close: bad arguments (ratio %d hd %d rd %d)", ratio, hd, rd);
+        return -1;
+    }
+    const int nt = (hd + 63) / 64 * 64;
+    hipLaunchKernelGGL(k_comp_close, dim3(1), dim3(nt), 0, st, out, kv_state, score_state,
+                       ratio, hd, ratio == 4 ? 1 : 0, w, eps, rd, cs, sn, pos, half);
+    HIP_OK(hipGetLastError(), "comp_close launch");
     return 0;
 }
 

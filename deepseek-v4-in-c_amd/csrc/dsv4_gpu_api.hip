@@ -1251,10 +1251,19 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
                 DSV4_ERR("attn_step: compressed rows exceed max_pos / ratio + 1");
                 return -1;
             }
-            OK(dsv4_comp_pool_launch(b.pooled, b.comp_kv, b.comp_score, c.ratio, hd, st));
-            OK(dsv4_norm_rope_launch(b.kv_cache + (size_t)(c.window + b.n_comp) * hd, 0,
-                                     b.pooled, 0, b.comp_norm, 1, hd, 1, c.rms_eps, rd, b.cs,
-                                     b.sn, pos + 1 - c.ratio, half, 0, st));
+            float *crow = b.kv_cache + (size_t)(c.window + b.n_comp) * hd;
+            if (hd <= 1024) {
+                /* pool, comp.norm and RoPE at the window's first position in
+                 * one launch */
+                OK(dsv4_comp_close_launch(crow, b.comp_kv, b.comp_score, c.ratio, hd,
+                                          b.comp_norm, c.rms_eps, rd, b.cs, b.sn,
+                                          pos + 1 - c.ratio, half, st));
+            } else {
+                OK(dsv4_comp_pool_launch(b.pooled, b.comp_kv, b.comp_score, c.ratio, hd, st));
+                OK(dsv4_norm_rope_launch(crow, 0, b.pooled, 0, b.comp_norm, 1, hd, 1,
+                                         c.rms_eps, rd, b.cs, b.sn, pos + 1 - c.ratio, half, 0,
+                                         st));
+            }
             b.n_comp++;
         }
         /* which compressed rows attention sees (dsv4_layer.c:267-297) */

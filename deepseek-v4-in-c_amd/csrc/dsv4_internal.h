@@ -204,6 +204,13 @@ struct Dsv4Prep {
 };
 int dsv4_block_prep_launch(const Dsv4Prep *a, hipStream_t st);
 
+/* A closing window in one launch (hd <= 1024): the pool (with the ratio-4
+ * slide), then the weighted RMSNorm of the pooled row and RoPE of its last rd
+ * elements at table row pos, into out[hd]. */
+int dsv4_comp_close_launch(float *out, float *kv_state, float *score_state, int ratio,
+                           int hd, const float *w, float eps, int rd, const float *cs,
+                           const float *sn, int pos, int half, hipStream_t st);
+
 /* The compressor's pool of a closing window into out[hd] (with the ratio-4
  * slide). */
 int dsv4_comp_pool_launch(float *out, float *kv_state, float *score_state, int ratio,

@@ -556,7 +556,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU; the multi-GPU sharding of "
-              "the decode path is described in DESIGN.md, not launched "
+              "the decode path is designed (row shards for the GEMVs, expert "
+              "shards for the MoE, key shards for the sparse MLA), not launched "
               "(requested --gpus %d)" % args.gpus, file=sys.stderr)
         sys.exit(2)
     if int(os.environ.get("WORLD_SIZE", "1")) > 1:

@@ -8,7 +8,7 @@
  * (dsv4_run.c:467-474) go through the reference's dsv4_mmq dispatch
  * (dsv4_matmul.c:525-546) like every other matrix.
  *
- * DESIGN (bandwidth-bound, one multiply-add per 2 weight bytes)
+ * APPROACH (bandwidth-bound, one multiply-add per 2 weight bytes)
  *   - A row is split over TC threads (a power of two up to 64, or a multiple
  *     of 64 up to 256); thread j owns the 16-byte chunks (8 elements) j,
  *     j+TC, ... of every row it visits (NCH <= 8 of them, so rows up to

@@ -13,7 +13,7 @@
  * (dsv4_moe_mx.hip) is the batch-1 decode path; this one serves the
  * reference's own dispatch (dsv4_mmq, dsv4_matmul.c:525-546).
  *
- * DESIGN (bandwidth-bound, one 16-byte chunk = 32 elements = one 32-column
+ * APPROACH (bandwidth-bound, one 16-byte chunk = 32 elements = one 32-column
  * scale block or a part of a wider one):
  *   - The workgroup stages x into LDS once (cols floats); every wave then
  *     reads its 32-float slices from there.

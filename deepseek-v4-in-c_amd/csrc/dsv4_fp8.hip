@@ -7,7 +7,7 @@
  * 93-129), which gives each row a 128-thread block and reads one byte per
  * lane per step.
  *
- * DESIGN (bandwidth-bound: ~1 multiply-add per weight byte)
+ * APPROACH (bandwidth-bound: ~1 multiply-add per weight byte)
  *   - A row is split over TC threads ("row threads", a power of two up to
  *     64 or a multiple of 64 up to 256); thread j owns the 16-byte chunks
  *     j, j+TC, j+2TC, ... of every row it visits (NCH <= 4 of them), so rows

@@ -233,7 +233,7 @@ int dsv4_gpu_moe_fp4_d(float *d_out, const float *d_x, int layer,
 /* ============================================================ sparse MLA */
 
 /* A device-resident row store for the latent KV cache or the indexer's key
- * cache, with an append API (SURVEY: dsv4_gpu_kv_create / _write_row).
+ * cache, with an append API (dsv4_gpu_kv_create / dsv4_gpu_kv_write_row).
  * fmt: DSV4_GPU_KV_F32 (the reference's f32 cache), DSV4_GPU_KV_BF16, or
  * DSV4_GPU_KV_FP8 (e4m3 bytes with one fp32 scale per row; a row dequantises
  * to e4m3(code) * scale, exact in f32). */
@@ -323,7 +323,7 @@ int dsv4_gpu_mla_decode_d(float *d_o, int *d_idxs,
  * reference crosses the host-device boundary once per matmul here (about
  * nine times per layer); this is one call. No counterpart in the
  * reference's GPU header: the caller's binding is one test at the top of
- * attention().
+ * attention() that calls dsv4_gpu_attn_step when dsv4_gpu_attn_ready(layer).
  *
  * The block keeps the layer's state (the ring, the compressed rows, the
  * compressor's slots) on the device. Positions must come in order from 0,

@@ -11,7 +11,8 @@
  * Its matmul dispatch (dsv4_matmul.c:525,572) is compiled with dsv4_cuda_has /
  * dsv4_cuda_mmq / dsv4_cuda_mmq_n renamed to dsv4_gpu_*, and it links
  * deepseek-v4-in-c_amd/lib/libdsv4_gpu.so. That is the drop-in binding of
- * INTEGRATION.md section 2, made with the preprocessor instead of an edit.
+ * the matmul dispatch (the three dsv4_cuda_* calls replaced by their
+ * dsv4_gpu_* counterparts), made with the preprocessor instead of an edit.
  *
  * The decode loop restates the reference's own (dsv4_run.c:444-483,
  * tests/unit/test_model_oracle.c:196-245):
@@ -32,8 +33,9 @@
  *     dsv4_layer.c with dsv4_indexer_score / dsv4_topk / dsv4_sparse_attn
  *     renamed to the e2e_* wrappers below, which call dsv4_gpu_indexer_score
  *     / dsv4_gpu_topk / dsv4_gpu_sparse_attn in pass 2 and the reference's
- *     own functions otherwise -- the call sites INTEGRATION.md shows, made
- *     with the preprocessor instead of an edit.
+ *     own functions otherwise -- the CSA call sites of attention()
+ *     (dsv4_layer.c:286-301) bound to the device, made with the
+ *     preprocessor instead of an edit.
  *   - pass 3 (GPU runs): the same, with every layer's attention() taken
  *     from the device attention block (dsv4_gpu_attn_step, one call per
  *     layer and position) and its routed experts' k-ordered sum from the

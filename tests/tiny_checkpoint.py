@@ -9,7 +9,8 @@ What it matches in the reference:
 - the safetensors container its reader parses (src/io/dsv4_st.c).
 
 The field set follows the reference's tools/make_tiny_checkpoint.py:234-257.
-The configuration differs where BASELINE asks it to:
+The configuration differs where the end-to-end workload (BASELINE.json
+configs[4]) asks it to:
 - the vocabulary is 129280;
 - FP8 block scales and FP4 block scales vary;
 - the experts are MXFP4;

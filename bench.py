@@ -280,7 +280,7 @@ class Bench:
         return us, 2.0 * rows * cols * nt / 1e9
 
     # ------------------------------------------------------ attention block
-    def attn_run(self, steps, warmup, ratio=4, n_layers=4, p0=2048):
+    def attn_run(self, steps, warmup, ratio=4, n_layers=4, p0=4096):
         """The attention block (dsv4_gpu_attn_step_d, attention() of
         dsv4_layer.c:213-336 in one call) at the DeepSeek-V4-Flash shapes:
         hidden 4096, 64 heads x 512 (RoPE 64), q_lora 1024, wo_a 8 groups x
@@ -290,7 +290,8 @@ class Bench:
         and stepped in turn, so each step reads its layer's weights cold (as a
         decode through the model does); every layer is first decoded to
         position p0, so the ring is full and the compressed rows are p0 /
-        ratio. Returns (eager us per step, the same, algorithmic bytes per
+        ratio (1024 at ratio 4: more than index_topk, so the indexer scores
+        and selects on every step). Returns (eager us per step, the same, algorithmic bytes per
         step). The eager rate is the one reported: the
         positions move the state, so a replayed graph re-runs the same
         positions (same launches and sizes) and is kept only as
@@ -633,7 +634,7 @@ def main():
             log("bench: attention block, ratio %d" % ratio)
             detail[name] = rec(*B.attn_run(32, 4, ratio=ratio))
             detail[name]["graph_replay_us"] = round(B.attn_graph_us, 3)
-            detail[name]["positions_before"] = 2048
+            detail[name]["positions_before"] = 4096
     cpu = None
     if not args.no_cpu:
         log("bench: CPU baseline (compiled reference, host cores)")

@@ -1210,7 +1210,14 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
     }
 #define OK(e) do { if ((e) != 0) return -1; } while (0)
     const bool closes = c.ratio > 0 && (pos + 1) % c.ratio == 0;
-    const bool use_idx = c.ratio > 0 && c.idx_heads > 0 && b.n_comp + (closes ? 1 : 0) > 0;
+    /* The indexer runs only when it has a choice to make. With no more
+     * compressed rows than index_topk the reference's score and top-k take
+     * every row (dsv4_layer.c:278-290, take = avail), only in score order;
+     * attention over the same rows in index order differs by the float
+     * summation order alone, so those steps take mode 1 and skip the
+     * indexer's projections, score and top-k. */
+    const bool use_idx = c.ratio > 0 && c.idx_heads > 0 &&
+                         b.n_comp + (closes ? 1 : 0) > c.idx_topk;
     /* the projections of x: wq_a, wkv, the compressor's wkv / wgate and the
      * indexer's weights_proj (when it runs this step) */
     XJob xj[5] = {{&b.wq_a, b.qr, c.q_lora}, {&b.wkv, b.kv, hd}};

@@ -147,7 +147,7 @@ static float *syn_vec(uint64_t seed, int n, float scale, float add)
 
 static int upload(const DSV4QMat *m);
 
-static int flash_mode(int n, int ratio, double tol)
+static int flash_mode(int n, int ratio, double tol, int idx_topk)
 {
     static int cr[1];
     cr[0] = ratio;
@@ -157,7 +157,7 @@ static int flash_mode(int n, int ratio, double tol)
     c.max_pos = n + 16; c.n_heads = 64; c.n_kv_heads = 1; c.head_dim = 512;
     c.q_lora = 1024; c.o_lora = 1024; c.o_groups = 8; c.qk_rope = 64;
     c.sliding_window = 128; c.index_n_heads = 64; c.index_head_dim = 128;
-    c.index_topk = 512; c.n_compress = 1; c.compress_ratios = cr;
+    c.index_topk = idx_topk; c.n_compress = 1; c.compress_ratios = cr;
     c.compress_rope_theta = 160000.0f; c.hc_mult = 4; c.n_experts = 256; c.topk = 6;
     c.n_shared = 1; c.moe_inter = 2048; c.rope_theta = 10000.0f; c.yarn_factor = 16.0f;
     c.yarn_beta_fast = 32.0f; c.yarn_beta_slow = 1.0f; c.yarn_orig_ctx = 65536;
@@ -282,15 +282,21 @@ int main(int argc, char **argv)
 {
     if (argc < 2) {
         fprintf(stderr, "usage: %s CKPT_DIR [N_POSITIONS] [--tol T]\n"
-                        "       %s --flash N_POSITIONS RATIO [--tol T]\n", argv[0], argv[0]);
+                        "       %s --flash N_POSITIONS RATIO [--tol T] [--topk K]\n",
+                argv[0], argv[0]);
         return 1;
     }
     int n = 40;
     double tol = 1e-4;
     if (!strcmp(argv[1], "--flash")) {
         if (argc < 4) return 1;
-        if (argc > 5 && !strcmp(argv[4], "--tol")) tol = atof(argv[5]);
-        return flash_mode(atoi(argv[2]), atoi(argv[3]), tol);
+        int idx_topk = 512;                     /* DeepSeek-V4-Flash's index_topk */
+        for (int i = 4; i + 1 < argc; i += 2) {
+            if (!strcmp(argv[i], "--tol")) tol = atof(argv[i + 1]);
+            else if (!strcmp(argv[i], "--topk")) idx_topk = atoi(argv[i + 1]);
+        }
+        if (idx_topk <= 0) return 1;
+        return flash_mode(atoi(argv[2]), atoi(argv[3]), tol, idx_topk);
     }
     for (int i = 2; i < argc; i++) {
         if (!strcmp(argv[i], "--tol") && i + 1 < argc) tol = atof(argv[++i]);

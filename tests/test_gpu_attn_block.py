@@ -46,15 +46,19 @@ def test_attention_block_matches_reference(tmp_path):
     assert len(rels) == 160 and max(rels) > 0.0       # the device really computed it
 
 
-@pytest.mark.parametrize("n,ratio", [(24, 4), (132, 128), (20, 0)])
-def test_attention_block_flash_shapes(n, ratio):
+@pytest.mark.parametrize("n,ratio,topk", [(24, 4, 512), (40, 4, 4), (132, 128, 512),
+                                          (20, 0, 512)])
+def test_attention_block_flash_shapes(n, ratio, topk):
     """The same comparison at the DeepSeek-V4-Flash attention shapes (hidden
     4096, 64 heads x 512, q_lora 1024, wo_a 8 x 1024, window 128, indexer 64
     x 128), synthetic weights, one layer of each compress ratio; at 132
     positions the ratio-128 compressor has closed one window, so the last
-    positions attend to a compressed row."""
-    print("attn flash: %d positions, ratio %d" % (n, ratio), flush=True)
-    p = subprocess.run([ATTN, "--flash", str(n), str(ratio), "--tol", "1e-5"],
+    positions attend to a compressed row. With index_topk 512 the ratio-4
+    layer's few compressed rows are all taken (the block skips the indexer);
+    with index_topk 4 the indexer selects 4 of up to 10 rows on the device."""
+    print("attn flash: %d positions, ratio %d, index_topk %d" % (n, ratio, topk), flush=True)
+    p = subprocess.run([ATTN, "--flash", str(n), str(ratio), "--tol", "1e-5",
+                        "--topk", str(topk)],
                        capture_output=True, text=True, timeout=300)
     line = [l for l in p.stdout.splitlines() if l.startswith("flash:")]
     print(line, flush=True)

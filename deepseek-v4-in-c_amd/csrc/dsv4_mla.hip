@@ -913,28 +913,44 @@ k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
  * order is score descending, ties to the lower index) is ranked by counting
  * the composites above it -- the composites are distinct, so the ranks are
  * a permutation -- and the elements ranked below k land at idxs[rank]. A
- * workgroup stages all n composites in LDS and ranks TS_EPW elements, four
- * threads per element each counting a quarter of the vector. */
+ * workgroup stages all n composites in LDS (every score load issued before
+ * any store) and ranks TS_EPW elements, TS_TPE threads per element: thread q
+ * counts composites q, q + TS_TPE, ..., so the lanes of an element read
+ * consecutive words (no bank conflicts) and the elements of a wave read the
+ * same ones (broadcast); the count loop keeps 8 LDS reads in flight. */
 constexpr int TS_NMAX = 4096;
-constexpr int TS_EPW = 64;
+constexpr int TS_TPE = 16;
+constexpr int TS_EPW = 256 / TS_TPE;
 
 __global__ void __launch_bounds__(256)
 k_tk_small(int *__restrict__ idxs, const float *__restrict__ scores, int n, int k)
 {
     __shared__ unsigned long long comp[TS_NMAX];
-    for (int i = threadIdx.x; i < n; i += 256)
-        comp[i] = ((unsigned long long)fkey(scores[i]) << 32) | (0xFFFFFFFFu - (uint32_t)i);
+    {
+        constexpr int PT = TS_NMAX / 256;
+        float v[PT];
+#pragma unroll
+        for (int u = 0; u < PT; u++) {
+            const int i = u * 256 + (int)threadIdx.x;
+            v[u] = i < n ? scores[i] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < PT; u++) {
+            const int i = u * 256 + (int)threadIdx.x;
+            if (i < n)
+                comp[i] = ((unsigned long long)fkey(v[u]) << 32) | (0xFFFFFFFFu - (uint32_t)i);
+        }
+    }
     __syncthreads();
-    const int e = blockIdx.x * TS_EPW + (int)(threadIdx.x >> 2);
-    const int qtr = threadIdx.x & 3;
+    const int e = blockIdx.x * TS_EPW + (int)(threadIdx.x / TS_TPE);
+    const int q = threadIdx.x % TS_TPE;
     const unsigned long long me = comp[min(e, n - 1)];
-    const int per = (n + 3) >> 2;
-    const int j0 = qtr * per, j1 = min(n, j0 + per);
     int cnt = 0;
-    for (int j = j0; j < j1; j++) cnt += comp[j] > me ? 1 : 0;
-    cnt += __shfl_xor(cnt, 1, 64);
-    cnt += __shfl_xor(cnt, 2, 64);
-    if (qtr == 0 && e < n && cnt < k) idxs[cnt] = e;
+#pragma unroll 8
+    for (int j = q; j < n; j += TS_TPE) cnt += comp[j] > me ? 1 : 0;
+#pragma unroll
+    for (int o = TS_TPE / 2; o >= 1; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
+    if (q == 0 && e < n && cnt < k) idxs[cnt] = e;
 }
 
 /* ----------------------------------------------------- sparse attention */

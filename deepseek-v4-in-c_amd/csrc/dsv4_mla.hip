@@ -1282,21 +1282,28 @@ k_attn_combine(float *__restrict__ o, const float *__restrict__ pm,
 {
     const int hh = blockIdx.x;
     __shared__ float fs[CB_SPLITS];
+    __shared__ float lp[CB_SPLITS];     /* l_s * e^(m_s - M), rounded to float */
     __shared__ float sh_inv;
     const int tid = threadIdx.x;
     if (tid < 64) {
+        const float sk = sink ? sink[hh] : 0.0f;
         float M = -INFINITY;
         for (int s = tid; s < nsplit; s += 64) M = fmaxf(M, pm[(size_t)hh * nsplit + s]);
         M = wave_max(M);
+        /* the lanes form the denominator's terms in parallel; lane 0 then
+         * adds them in split order from LDS */
         for (int s = tid; s < nsplit; s += 64) {
             const float ms = pm[(size_t)hh * nsplit + s];
-            fs[s] = (ms == -INFINITY) ? 0.0f : expf(ms - M);
+            const float ls = pl[(size_t)hh * nsplit + s];
+            const float f = (ms == -INFINITY) ? 0.0f : expf(ms - M);
+            fs[s] = f;
+            lp[s] = ls * f;
         }
         if (tid == 0) {
             double denom = 0.0;
-            for (int s = 0; s < nsplit; s++)
-                denom += (double)(pl[(size_t)hh * nsplit + s] * fs[s]);
-            if (sink) denom += (double)expf(sink[hh] - M);
+#pragma unroll 8
+            for (int s = 0; s < nsplit; s++) denom += (double)lp[s];
+            if (sink) denom += (double)expf(sk - M);
             sh_inv = (float)(1.0 / denom);
         }
     }

@@ -1091,46 +1091,11 @@ k_attn_partial(float *__restrict__ pm, float *__restrict__ pl,
     if (tid < SR) sidx[tid] = (ridx >= 0 && ridx < kv_rows) ? ridx : -1;   /* never a wild read */
     rope_row_store(qrp, rrow, rcs, rsn);
     __syncthreads();
-    /* stage the rows */
-    if (vec) {
-        const int nc = dmax * ES / 16;                           /* 16-B chunks per row */
-        for (int e0 = 0; e0 < SR * nc; e0 += SB * AT_THREADS) {
-            u32x4 v[SB];
-#pragma unroll
-            for (int u = 0; u < SB; u++) {
-                const int e = e0 + u * AT_THREADS + tid;
-                const int r = e / nc, c = e - r * nc;
-                const int row = e < SR * nc ? sidx[r] : -1;
-                v[u] = row >= 0
-                    ? ld16((const unsigned char *)kv + ((size_t)row * kv_stride) * ES + (size_t)c * 16)
-                    : u32x4{0, 0, 0, 0};
-            }
-#pragma unroll
-            for (int u = 0; u < SB; u++) {
-                const int e = e0 + u * AT_THREADS + tid;
-                if (e < SR * nc) {
-                    const int r = e / nc, c = e - r * nc;
-                    *reinterpret_cast<u32x4 *>(kvs + (size_t)r * rowb + (size_t)c * 16) = v[u];
-                }
-            }
-        }
-    } else {
-        for (int e = tid; e < SR * dmax; e += AT_THREADS) {
-            const int r = e / dmax, c = e - r * dmax;
-            const int row = sidx[r];
-            const float v = row >= 0 ? kv_at<KVF>(kv, (size_t)row, kv_stride, c) : 0.0f;
-            if (KVF == DSV4_GPU_KV_BF16)
-                ((uint16_t *)(kvs + (size_t)r * rowb))[c] = (uint16_t)(__float_as_uint(v) >> 16);
-            else
-                ((float *)(kvs + (size_t)r * rowb))[c] = v;
-        }
-    }
-    __syncthreads();
-    if (qnorm || qrp.rd) {
-        /* the attention block's q: each head scaled by 1/sqrt(mean square +
-         * eps) and RoPE'd at pos (dsv4_layer.c:223-231), after the rows are
-         * staged (their loads went out first). All heads at once: QL lanes
-         * per head (a half wave for AT_HB = 8). */
+    /* the attention block's q: each head scaled by 1/sqrt(mean square +
+     * eps) and RoPE'd at pos (dsv4_layer.c:223-231). All heads at once: QL
+     * lanes per head (a half wave for AT_HB = 8). It touches only q's LDS
+     * copy, so it runs while the row loads below are in flight. */
+    auto q_transform = [&]() {
         constexpr int QL = AT_THREADS / AT_HB;
         const int t0 = d_qk - qrp.rd;
         const int hh = tid / QL, ql = tid - hh * QL;
@@ -1154,8 +1119,46 @@ k_attn_partial(float *__restrict__ pm, float *__restrict__ pl,
             qh[t0 + 2 * p] = a;
             qh[t0 + 2 * p + 1] = b;
         }
-        __syncthreads();
+    };
+    const bool qx = qnorm || qrp.rd;
+    /* stage the rows (q's transform between the first batch's loads and its
+     * stores) */
+    if (vec) {
+        const int nc = dmax * ES / 16;                           /* 16-B chunks per row */
+        for (int e0 = 0; e0 < SR * nc; e0 += SB * AT_THREADS) {
+            u32x4 v[SB];
+#pragma unroll
+            for (int u = 0; u < SB; u++) {
+                const int e = e0 + u * AT_THREADS + tid;
+                const int r = e / nc, c = e - r * nc;
+                const int row = e < SR * nc ? sidx[r] : -1;
+                v[u] = row >= 0
+                    ? ld16((const unsigned char *)kv + ((size_t)row * kv_stride) * ES + (size_t)c * 16)
+                    : u32x4{0, 0, 0, 0};
+            }
+            if (e0 == 0 && qx) q_transform();
+#pragma unroll
+            for (int u = 0; u < SB; u++) {
+                const int e = e0 + u * AT_THREADS + tid;
+                if (e < SR * nc) {
+                    const int r = e / nc, c = e - r * nc;
+                    *reinterpret_cast<u32x4 *>(kvs + (size_t)r * rowb + (size_t)c * 16) = v[u];
+                }
+            }
+        }
+    } else {
+        for (int e = tid; e < SR * dmax; e += AT_THREADS) {
+            const int r = e / dmax, c = e - r * dmax;
+            const int row = sidx[r];
+            const float v = row >= 0 ? kv_at<KVF>(kv, (size_t)row, kv_stride, c) : 0.0f;
+            if (KVF == DSV4_GPU_KV_BF16)
+                ((uint16_t *)(kvs + (size_t)r * rowb))[c] = (uint16_t)(__float_as_uint(v) >> 16);
+            else
+                ((float *)(kvs + (size_t)r * rowb))[c] = v;
+        }
+        if (qx) q_transform();
     }
+    __syncthreads();
 
     /* scores: the AT_HB x SR (head, row) pairs over every lane. A pair's dot
      * is split over LPP lanes that sit 64 / LPP apart in the wave (each takes

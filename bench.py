@@ -9,19 +9,28 @@ sweep: the six GEMVs back to back on one stream, every input already resident
 in HBM. `value` is achieved HBM GB/s over the sweep (algorithmic bytes /
 step time); `ms_per_step` is the time per trunk token (all six shapes).
 
-Cold data: one step streams 1.15 GB, more than the 256 MB Infinity Cache, so
-every matrix has been evicted before it is read again.
+Timing. Every timed region is a run of launches queued behind a spin kernel
+on the same stream, so the host has issued them all before the first one
+starts and the GPU runs them back to back: HIP events bracket exactly the
+launches timed, with no host launch latency inside. The headline times
+exactly `--steps` sweeps per trial and takes the median of 5 trials.
+
+Cold data: one sweep streams 1.15 GB, more than the 256 MB Infinity Cache,
+so every matrix has been evicted before it is read again. Per-shape times
+rotate distinct copies of the shape (>= 1 GiB in all).
 
 Also reported (`detail`): C1 (4096x4096, rotating 64 copies = 1.07 GB), C3
 (MXFP4 routed experts, 8 of 256 resident experts per step = 187 MB, rotated
-over the 6 GB expert pool) and C4 (the sparse-MLA decode step, rotating 26
-copies of the key/KV caches).
+over the 6 GB expert pool), C4 (the sparse-MLA decode step, rotating 26
+copies of the key/KV caches), the BF16 LM head, the batched prefill GEMV and
+the attention block at the DeepSeek-V4-Flash shapes.
 
 roofline: the LM-head GEMV (80% of the sweep's bytes), algorithmic bytes per
 launch / its average launch time from HIP events on the launch stream.
 cpu_baseline: the reference's own CPU path (oracle/_ref, its
 dsv4_matmul_fp8 compiled with OpenMP + AVX2) on the same sweep, timed on this
-host's cores.
+host's cores; `detail.cpu_reference` adds 1-core figures and the reference's
+C3, C4 and attention() paths.
 """
 import argparse
 import json
@@ -97,6 +106,8 @@ class Bench:
         self.dev = torch.device("cuda:0")
         self.stream = torch.cuda.current_stream()
         self.sp = self.stream.cuda_stream
+        self._cyc_per_ms = None
+        self._it = 0
 
     def t(self, a):
         return self.torch.from_numpy(self.np.ascontiguousarray(a)).to(self.dev)
@@ -117,6 +128,45 @@ class Bench:
         b.record(self.stream)
         torch.cuda.synchronize()
         return a.elapsed_time(b) * 1e3 / n
+
+    def spin(self, ms):
+        """A spin kernel of about `ms` on the launch stream (torch's
+        clock-based sleep, calibrated once): the launches queued behind it
+        are all issued before the first of them runs."""
+        torch = self.torch
+        if self._cyc_per_ms is None:
+            try:
+                torch.cuda._sleep(1000)
+                a, b = self.ev(), self.ev()
+                a.record(self.stream)
+                torch.cuda._sleep(1 << 20)
+                b.record(self.stream)
+                torch.cuda.synchronize()
+                self._cyc_per_ms = (1 << 20) / max(a.elapsed_time(b), 1e-3)
+            except (AttributeError, RuntimeError):
+                self._cyc_per_ms = 0.0
+                log("bench: no spin kernel; timed launches start behind the host")
+        if self._cyc_per_ms > 0:
+            torch.cuda._sleep(int(ms * self._cyc_per_ms))
+
+    def blocked_us(self, go, n, trials=3, spin_ms=20.0):
+        """Per-iteration time of go(i, stream) issued n times back to back
+        behind a spin kernel, median over trials (i keeps counting across
+        trials, so rotations continue). Returns (median us, [us per trial])."""
+        torch = self.torch
+        per = []
+        for _ in range(trials):
+            self.spin(spin_ms)
+            a, b = self.ev(), self.ev()
+            a.record(self.stream)
+            for _ in range(n):
+                go(self._it, self.sp)
+                self._it += 1
+            b.record(self.stream)
+            torch.cuda.synchronize()
+            per.append(a.elapsed_time(b) * 1e3 / n)
+        srt = sorted(per)
+        return srt[len(srt) // 2], per
 
     def graph_us(self, go, n, replays):
         """Per-iteration time with n iterations captured into one HIP graph
@@ -166,23 +216,49 @@ class Bench:
         for m in self.c2:
             self.c2_launch(m, sp)
 
-    def c2_run(self, steps, warmup):
-        """Step time in a replayed HIP graph (the value), the eager step time,
-        and per-kernel durations from events bracketing each eager launch."""
+    def c2_run(self, steps, warmup, trials=5):
+        """The headline: exactly `steps` sweeps per trial, back to back behind
+        a spin kernel, median over `trials` (ms per sweep, and every trial).
+        Also the same sweeps issued from the host without the spin (eager,
+        host launch gaps included) and as a HIP graph of 10 sweeps replayed
+        10 times, both for comparison only."""
         torch = self.torch
-        eager_ms = self.eager_us(self.c2_step, steps, warmup) / 1e3
-        graph_ms = self.graph_us(self.c2_step, 10, max(1, steps // 10)) / 1e3
-        nk = len(self.c2)
-        evs = [[self.ev() for _ in range(nk + 1)] for _ in range(steps)]
-        for s in range(steps):
-            evs[s][0].record(self.stream)
-            for k, m in enumerate(self.c2):
-                self.c2_launch(m)
-                evs[s][k + 1].record(self.stream)
+        for i in range(warmup):
+            self.c2_step(i)
         torch.cuda.synchronize()
-        per = [sum(evs[s][k].elapsed_time(evs[s][k + 1]) for s in range(steps)) / steps
-               for k in range(nk)]
-        return graph_ms, eager_ms, per
+        med, per = self.blocked_us(self.c2_step, steps, trials)
+        eager_ms = self.eager_us(self.c2_step, steps, 0) / 1e3
+        graph_ms = self.graph_us(self.c2_step, 10, 10) / 1e3
+        return med / 1e3, [p / 1e3 for p in per], eager_ms, graph_ms
+
+    def c2_shape_run(self, k, reps=3):
+        """One sweep shape alone: distinct copies of it (>= 1 GiB together, so
+        each launch reads its weights cold) launched in rotation behind a spin
+        kernel; median us per launch over `reps` trials."""
+        torch = self.torch
+        m = self.c2[k]
+        per_copy = fp8_bytes(m["rows"], m["cols"])
+        copies = max(1, min(512, -(-(1 << 30) // per_copy)))
+        if copies > 1:
+            dW = m["dW"].unsqueeze(0).repeat(copies, 1, 1)
+            dS = m["dS"].unsqueeze(0).repeat(copies, 1, 1)
+        else:
+            dW, dS = m["dW"].unsqueeze(0), m["dS"].unsqueeze(0)
+        torch.cuda.synchronize()
+        rows, cols = m["rows"], m["cols"]
+
+        def go(i, sp):
+            j = i % copies
+            if self.L.dsv4_gpu_fp8_gemv_d(m["dy"].data_ptr(), m["dx"].data_ptr(),
+                                          dW[j].data_ptr(), dS[j].data_ptr(), 1, rows, cols,
+                                          sp) != 0:
+                raise RuntimeError("fp8 gemv launch failed")
+        n = max(2 * copies, 20)
+        go(0, self.sp)
+        us, _ = self.blocked_us(go, n, reps)
+        del dW, dS
+        torch.cuda.synchronize()
+        return us, copies, n
 
     # ------------------------------------------------------------ C1
     def c1_run(self, steps, warmup):
@@ -204,7 +280,7 @@ class Bench:
                                               dW[j].data_ptr(), dS[j].data_ptr(), 1,
                                               rows, cols, sp) == 0
         eager = self.eager_us(go, max(steps, copies), max(warmup, copies))
-        us = self.graph_us(go, copies, max(2, steps // 8))
+        us, _ = self.blocked_us(go, 2 * copies)
         del dW, dS
         return us, eager, fp8_bytes(rows, cols)
 
@@ -258,7 +334,7 @@ class Bench:
             assert self.L.dsv4_gpu_bf16_gemv_d(dy.data_ptr(), dx.data_ptr(), W.data_ptr(),
                                                rows, cols, sp) == 0
         eager = self.eager_us(go, max(steps // 4, 4), max(warmup, 2))
-        us = self.graph_us(go, 4, max(2, steps // 16))
+        us, _ = self.blocked_us(go, 10)
         del W
         return us, eager, rows * cols * 2 + cols * 4 + rows * 4
 
@@ -276,7 +352,8 @@ class Bench:
         def go(i, sp):
             assert self.L.dsv4_gpu_fp8_gemv_n_d(dy.data_ptr(), dx.data_ptr(), dW.data_ptr(),
                                                 dS.data_ptr(), 1, rows, cols, nt, sp) == 0
-        us = self.eager_us(go, calls, 3)
+        go(0, self.sp)
+        us, _ = self.blocked_us(go, calls)
         return us, 2.0 * rows * cols * nt / 1e9
 
     # ------------------------------------------------------ attention block
@@ -291,19 +368,16 @@ class Bench:
         decode through the model does); every layer is first decoded to
         position p0, so the ring is full and the compressed rows are p0 /
         ratio (1024 at ratio 4: more than index_topk, so the indexer scores
-        and selects on every step). Returns (eager us per step, the same, algorithmic bytes per
-        step). The eager rate is the one reported: the
-        positions move the state, so a replayed graph re-runs the same
-        positions (same launches and sizes) and is kept only as
-        attn_graph_us; on this GPU it measured slower than the stream."""
+        and selects on every step). Returns (us per layer step queued behind a
+        spin kernel, us per layer step issued from the host, algorithmic
+        bytes per layer step)."""
         import ctypes
         np, torch, D, L, C = self.np, self.torch, self.dsv4, self.L, self.common
         hidden, ql, H, hd, rd, win, ol, og = 4096, 1024, 64, 512, 64, 128, 1024, 8
         ih, idd, itop = 64, 128, 512
         has_idx = ratio == 4
         coff = 2 if ratio == 4 else 1
-        nrep = max(2, steps // 16)
-        maxpos = p0 + warmup + steps + 8
+        maxpos = p0 + warmup + 4 * steps + 8
         rng = np.random.default_rng(11)
         keep = []
 
@@ -370,28 +444,17 @@ class Bench:
         torch.cuda.synchronize()
         for _ in range(warmup):
             step(self.sp)
+        torch.cuda.synchronize()
+        # host-issued (launch gaps included), then behind a spin kernel
         a, b = self.ev(), self.ev()
         a.record(self.stream)
-        for _ in range(steps - nrep):
+        for _ in range(steps):
             step(self.sp)
         b.record(self.stream)
         torch.cuda.synchronize()
-        eager = a.elapsed_time(b) * 1e3 / ((steps - nrep) * n_layers)
-        # the last nrep positions captured once into a graph and replayed:
-        # the same launches with the same sizes, without host gaps
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            sp = torch.cuda.current_stream().cuda_stream
-            for _ in range(nrep):
-                step(sp)
-        g.replay()
-        torch.cuda.synchronize()
-        a.record(self.stream)
-        for _ in range(4):
-            g.replay()
-        b.record(self.stream)
-        torch.cuda.synchronize()
-        us = a.elapsed_time(b) * 1e3 / (4 * nrep * n_layers)
+        eager = a.elapsed_time(b) * 1e3 / (steps * n_layers)
+        per_pos, _ = self.blocked_us(lambda i, sp: step(sp), steps, 3)
+        us = per_pos / n_layers
         avail = p0 // ratio
         take = min(avail, itop) if has_idx else avail
         alg = (mats + 2 * hidden * 4 + (win + take) * hd * 4 +
@@ -401,8 +464,7 @@ class Bench:
         # resident matrices are keyed by host pointer: their host arrays stay
         # allocated for the process, so no later array can reuse an address
         self._attn_keep = getattr(self, "_attn_keep", []) + [keep]
-        self.attn_graph_us = us
-        return eager, eager, alg
+        return us, eager, alg
 
     # ------------------------------------------------------------ C3
     def c3_run(self, steps, warmup):
@@ -445,7 +507,7 @@ class Bench:
                                              d_ids[j].data_ptr(), d_ws[j].data_ptr(),
                                              topk, hidden, inter, 10.0, sp) == 0
         eager = self.eager_us(go, max(steps, nsets), warmup)
-        us = self.graph_us(go, nsets, max(2, steps // 16))
+        us, _ = self.blocked_us(go, 2 * nsets)
         del W13, S13, W2, S2
         return us, eager, moe_bytes(hidden, inter, topk)
 
@@ -478,7 +540,7 @@ class Bench:
                 d_q.data_ptr(), d_kv[j].data_ptr(), self.dsv4.KV_BF16, dqk, n, None, h,
                 dqk, dv, scale, sp) == 0
         eager = self.eager_us(go, max(steps, copies), max(warmup, copies))
-        us = self.graph_us(go, copies, max(2, steps // 8))
+        us, _ = self.blocked_us(go, 2 * copies)
         alg = n * D + n * 4 + k * dqk * 2 + h * dqk * 4 + h * dv * 4 + k * 4 + H * D * 4 + H * 4
         del d_codes, d_s, d_kv
         return us, eager, alg
@@ -531,6 +593,151 @@ class Bench:
                 "ms_per_step": round(per * 1e3, 3)}
 
 
+    def cpu_reference(self):
+        """The reference's CPU path beside the device figures, on this host:
+        all cores (the OpenMP default) and one core, each a bounded sample.
+          c2: one sweep of the six shapes on one core (all cores: cpu_baseline);
+          c3: the 8-expert MXFP4 MoE (4 sets of 8 rotated, 748 MB, so the
+              weights are cold) -- per expert dsv4_matmul_fp4 w1 / w3,
+              dsv4_swiglu (limit 10), dsv4_matmul_fp4 w2, then the k-ordered
+              sum (dsv4_layer.c:199-206, :471-475);
+          c4: dsv4_indexer_score over 32768 x 128 keys (single-threaded in the
+              reference), dsv4_topk at k = 256 of 32768 (O(k^2 n): k = 2048 is
+              extrapolated from it, never run), dsv4_sparse_attn over 2048 rows
+              of 576 (one width for keys and values, the reference's form), 64
+              heads;
+          attention(): oracle/_ref/dsv4_attn at the DeepSeek-V4-Flash shapes,
+              ratio 4 (CSA, indexer) and 128, positions 4.. of a fresh layer."""
+        import ctypes
+        import subprocess
+        import oracle
+        if not oracle.ref_available():
+            return None
+        np, C = self.np, self.common
+        nall = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        try:
+            gomp = ctypes.CDLL("libgomp.so.1")
+        except OSError:
+            gomp = None
+        model = "unknown"
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        model = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+        out = {"cpu_model": model, "threads_all": nall, "kind": "reference"}
+
+        def best(fn, reps):
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t0)
+            return min(ts) * 1e3, sum(ts) / len(ts) * 1e3
+
+        def threads(n):
+            if gomp is not None:
+                gomp.omp_set_num_threads(int(n))
+        one = gomp is not None
+        # C2 on one core: one sweep
+        if one:
+            threads(1)
+            t0 = time.perf_counter()
+            for m in self.c2:
+                oracle.ref_matmul_fp8(m["x"], m["W"], m["Se"])
+            t = time.perf_counter() - t0
+            threads(nall)
+            alg = sum(fp8_bytes(m["rows"], m["cols"]) for m in self.c2)
+            out["c2_sweep_1core"] = {"ms": round(t * 1e3, 1),
+                                     "GBps": round(alg / t / 1e9, 3), "sample": "1 sweep"}
+        # C3
+        rng = np.random.default_rng(0)
+        hidden, inter, topk, nsets = 7168, 2048, 8, 4
+        sets = [[C.fp4_expert(rng, hidden, inter) for _ in range(topk)] for _ in range(nsets)]
+        x = C.bf16_round(rng.standard_normal(hidden).astype(np.float32))
+        wts = C.router(rng, topk)
+        turn = [0]
+
+        def c3():
+            experts = sets[turn[0] % nsets]
+            turn[0] += 1
+            acc = np.zeros(hidden, np.float32)
+            for k, e in enumerate(experts):
+                g = oracle.ref_matmul_fp4(x, e["w1"], e["s1"], hidden)
+                u = oracle.ref_matmul_fp4(x, e["w3"], e["s3"], hidden)
+                h = oracle.ref_swiglu(g, u, 10.0)
+                y = oracle.ref_matmul_fp4(h, e["w2"], e["s2"], inter)
+                acc = acc + np.float32(wts[k]) * y
+            return acc
+        b, m = best(c3, 8)
+        out["c3_moe_all_cores"] = {"ms_best": round(b, 2), "ms_mean": round(m, 2),
+                                   "GBps": round(moe_bytes(hidden, inter, topk) / b / 1e6, 3),
+                                   "sample": "8 calls rotating 4 sets of 8 experts (748 MB)"}
+        if one:
+            threads(1)
+            b, m = best(c3, 2)
+            threads(nall)
+            out["c3_moe_1core"] = {"ms_best": round(b, 2), "ms_mean": round(m, 2),
+                                   "GBps": round(moe_bytes(hidden, inter, topk) / b / 1e6, 3),
+                                   "sample": "2 calls, next 2 sets"}
+        del sets
+        # C4
+        n, H, D, h, d = 32768, 16, 128, 64, 576
+        codes, ks, deq = C.fp8_keys(rng, n, D)
+        qi = rng.standard_normal((H, D)).astype(np.float32)
+        wi = rng.standard_normal(H).astype(np.float32)
+        sc = [None]
+
+        def score():
+            sc[0] = oracle.ref_indexer_score(qi, deq, wi)
+        b, _ = best(score, 1)
+        out["c4_indexer_score"] = {"ms": round(b, 1), "threads": 1,
+                                   "sample": "1 call (the reference's score is single-threaded)"}
+        b, _ = best(lambda: oracle.ref_topk(sc[0], 256), 1)
+        out["c4_topk"] = {"ms_k256": round(b, 1),
+                          "ms_k2048_extrapolated": round(b * 64.0, 0),
+                          "sample": "1 call at k = 256 of 32768; k = 2048 scaled by "
+                                    "(2048/256)^2 for the O(k^2 n) scan, not run"}
+        kv = (rng.standard_normal((n, d)) / np.sqrt(d)).astype(np.float32)
+        q = rng.standard_normal((h, d)).astype(np.float32)
+        idx = np.sort(rng.permutation(n)[:2048]).astype(np.int32)
+        sink = np.full(h, -np.inf, np.float32)
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+        at = lambda: oracle.ref_sparse_attn(q, kv, sink, idx, scale)  # noqa: E731
+        b, m = best(at, 3)
+        out["c4_sparse_attn_all_cores"] = {"ms_best": round(b, 2), "ms_mean": round(m, 2),
+                                           "sample": "3 calls, h 64, d 576, 2048 rows"}
+        if one:
+            threads(1)
+            b, m = best(at, 2)
+            threads(nall)
+            out["c4_sparse_attn_1core"] = {"ms_best": round(b, 2), "ms_mean": round(m, 2),
+                                           "sample": "2 calls"}
+        del kv, deq, codes
+        # attention() at the Flash shapes
+        exe = os.path.join(ROOT, "oracle", "_ref", "dsv4_attn")
+        if os.path.exists(exe):
+            for key, ratio, nthr, npos in (("attn_flash_ratio4_all_cores", 4, nall, 12),
+                                           ("attn_flash_ratio128_all_cores", 128, nall, 12),
+                                           ("attn_flash_ratio4_1core", 4, 1, 6)):
+                env = dict(os.environ, OMP_NUM_THREADS=str(nthr))
+                try:
+                    r = subprocess.run([exe, "--flash", str(npos), str(ratio), "--cpu-only"],
+                                       capture_output=True, text=True, timeout=120, env=env)
+                except subprocess.TimeoutExpired:
+                    continue
+                import re
+                mm = re.search(r"cpu_ms_per_position (\S+) threads (\d+)", r.stdout)
+                if r.returncode == 0 and mm:
+                    out[key] = {"ms_per_layer_step": float(mm.group(1)),
+                                "threads": int(mm.group(2)),
+                                "sample": "positions 4..%d of a fresh layer" % (npos - 1)}
+        return out
+
+
 _STDOUT_FD = None
 
 
@@ -575,10 +782,12 @@ def main():
         return
     if args.only == "c2":
         B.c2_setup()
-        step_ms, eager_ms, per_ms = B.c2_run(args.steps, args.warmup)
-        emit(({"config": "c2", "graph_ms": round(step_ms, 4),
-                          "eager_ms": round(eager_ms, 4),
-                          "per_shape_us": [round(m * 1e3, 3) for m in per_ms]}))
+        step_ms, trial_ms, eager_ms, graph_ms = B.c2_run(args.steps, args.warmup)
+        per_us = [B.c2_shape_run(k)[0] for k in range(len(B.c2))]
+        emit(({"config": "c2", "step_ms": round(step_ms, 4),
+               "trials_ms": [round(t, 4) for t in trial_ms],
+               "eager_ms": round(eager_ms, 4), "graph_ms": round(graph_ms, 4),
+               "per_shape_us": [round(u, 3) for u in per_us]}))
         B.L.dsv4_gpu_shutdown()
         return
     if args.only in ("c1", "c3", "c4", "attn"):
@@ -591,19 +800,23 @@ def main():
         return
     log("bench: C2 setup")
     B.c2_setup()
-    log("bench: C2 timed sweep, %d steps" % args.steps)
-    step_ms, eager_ms, per_ms = B.c2_run(args.steps, args.warmup)
+    log("bench: C2 timed sweep, %d steps x 5 trials" % args.steps)
+    step_ms, trial_ms, eager_ms, graph_ms = B.c2_run(args.steps, args.warmup)
     shapes = TRUNK + [LM_HEAD]
     algs = [fp8_bytes(r, c) for r, c in shapes]
     alg_step = sum(algs)
     value = alg_step / (step_ms * 1e-3) / 1e9
     per_shape = {}
-    for (r, c), a, ms in zip(shapes, algs, per_ms):
-        per_shape["%dx%d" % (r, c)] = {"us": round(ms * 1e3, 3),
-                                       "GBps": round(a / (ms * 1e-3) / 1e9, 1),
-                                       "frac": round(a / (ms * 1e-3) / 1e9 / PEAK_GBS, 4)}
-    trunk_us = sum(per_ms[:5]) * 1e3
-    lm_ms = per_ms[5]
+    per_us = []
+    for k, ((r, c), a) in enumerate(zip(shapes, algs)):
+        log("bench: C2 shape %dx%d alone" % (r, c))
+        us, copies, n = B.c2_shape_run(k)
+        per_us.append(us)
+        per_shape["%dx%d" % (r, c)] = {"us": round(us, 3), "GBps": round(a / us / 1e3, 1),
+                                       "frac": round(a / us / 1e3 / PEAK_GBS, 4),
+                                       "copies": copies, "launches": n}
+    trunk_us = sum(per_us[:5])
+    lm_ms = per_us[5] / 1e3
     lm_gbs = algs[5] / (lm_ms * 1e-3) / 1e9
     traffic = lm_head_traffic()
     detail = {}
@@ -633,12 +846,14 @@ def main():
         for ratio, name in ((4, "attn_block_flash_csa_ratio4"), (128, "attn_block_flash_hca_ratio128")):
             log("bench: attention block, ratio %d" % ratio)
             detail[name] = rec(*B.attn_run(32, 4, ratio=ratio))
-            detail[name]["graph_replay_us"] = round(B.attn_graph_us, 3)
             detail[name]["positions_before"] = 4096
     cpu = None
     if not args.no_cpu:
         log("bench: CPU baseline (compiled reference, host cores)")
         cpu = B.cpu_baseline()
+        if not args.no_detail:
+            log("bench: CPU reference, C2 on one core, C3, C4, attention()")
+            detail["cpu_reference"] = B.cpu_reference()
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -660,7 +875,9 @@ def main():
         "pct_of_peak": round(100.0 * value / PEAK_GBS, 2),
         "us_per_trunk_token": {"trunk_5_shapes": round(trunk_us, 3),
                                "with_lm_head": round(step_ms * 1e3, 3),
-                               "with_lm_head_eager": round(eager_ms * 1e3, 3)},
+                               "with_lm_head_trials": [round(t * 1e3, 3) for t in trial_ms],
+                               "with_lm_head_host_issued": round(eager_ms * 1e3, 3),
+                               "with_lm_head_graph_10x10": round(graph_ms * 1e3, 3)},
         "per_shape": per_shape,
         "roofline": {"bound": "hbm", "achieved": round(lm_gbs, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(lm_gbs / PEAK_GBS, 4),

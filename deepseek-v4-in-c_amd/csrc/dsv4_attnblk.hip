@@ -5,21 +5,18 @@
  * five to nine GEMVs (the FP8 / BF16 kernels of this library), the CSA
  * score / top-k / sparse attention (dsv4_mla.hip), and the element-wise steps
  * here:
- *   - k_norm_rope: RMSNorm (dsv4_ops.c:24-31, weighted) of a vector, then
- *     RoPE of the last rd elements (dsv4_rope.c:105-119, interleaved pairs;
- *     inverse negates the sine) -- either step optional, one workgroup per
- *     vector, the result written where the caller wants it (a compressed
- *     row of the KV cache);
  *   - k_block_prep: what the step needs right after the x projections, in
- *     one launch -- q's learned norm, kv_norm + RoPE into the ring slot, and
+ *     one launch -- q's learned norm (RMSNorm, dsv4_ops.c:24-31, weighted),
+ *     kv_norm + RoPE (dsv4_rope.c:105-119, interleaved pairs) into the ring
+ *     slot, and
  *     the compressor's token into its slot with score + ape
  *     (dsv4_compress.c:87-98);
  *   - k_comp_close: a closing window in one launch -- the compressor's
  *     pool (dsv4_compress.c:100-137: the per-channel softmax pool over the
  *     slots; ratio 4: the previous window's first halves and the current
  *     window's second halves), the ratio-4 slide, then comp.norm and RoPE of
- *     the pooled row (dsv4_layer.c:252-255). Rows wider than 1024 channels
- *     take k_comp_pool, then k_norm_rope.
+ *     the pooled row (dsv4_layer.c:252-255). The attention block binds
+ *     compressed layers of head_dim <= 1024 only (one thread per channel).
  * The attention's row list (the window's ring slots, then the compressed
  * rows) is built inside the attention kernel (Dsv4Rows).
  *
@@ -147,16 +144,6 @@ norm_rope_vec(float *y, const float *x, const float *__restrict__ w, int n, int 
     }
 }
 
-__global__ void __launch_bounds__(NR_THREADS)
-k_norm_rope(float *dst, int dst_stride, const float *src, int src_stride,
-            const float *__restrict__ w, int n, int norm, float eps, int rd,
-            const float *__restrict__ cs, const float *__restrict__ sn, int pos, int half,
-            int inverse)
-{
-    norm_rope_vec(dst + (size_t)blockIdx.x * dst_stride, src + (size_t)blockIdx.x * src_stride,
-                  w, n, norm, eps, rd, cs, sn, pos, half, inverse);
-}
-
 /* The attention block's step after its x projections, in one launch:
  * workgroup j < nj runs norm job j (norm_rope_vec), the rest copy the
  * compressor's token into its slot (k_comp_update's work). The jobs touch
@@ -175,55 +162,14 @@ k_block_prep(Dsv4Prep a)
     a.scs[c] = a.sc_in[c] + a.apr[c];
 }
 
-/* Channel c of the closing window's pool. ov (ratio 4): slots 0..ratio-1
- * are the previous window's first halves (columns c), slots ratio..2ratio-1
- * the current window's second halves (columns hd + c); afterwards the
- * current window slides into the previous one. A thread touches only the
- * columns c and hd + c, so the slide needs no barrier. */
-__global__ void __launch_bounds__(NR_THREADS)
-k_comp_pool(float *__restrict__ out, float *__restrict__ kvst, float *__restrict__ scst,
-            int ratio, int hd, int ov)
-{
-    const int c = blockIdx.x * NR_THREADS + threadIdx.x;
-    if (c >= hd) return;
-    const int width = ov ? 2 * hd : hd;
-    const int slots = ov ? 2 * ratio : ratio;
-    float mx = -INFINITY;
-    for (int s = 0; s < slots; s++) {
-        const int col = (ov && s >= ratio) ? hd + c : c;
-        const float v = scst[(size_t)s * width + col];
-        if (v > mx) mx = v;
-    }
-    float r = 0.0f;
-    if (mx != -INFINITY) {
-        double den = 0.0, acc = 0.0;
-        for (int s = 0; s < slots; s++) {
-            const int col = (ov && s >= ratio) ? hd + c : c;
-            const float v = scst[(size_t)s * width + col];
-            if (v == -INFINITY) continue;
-            const double e = (double)expf(v - mx);
-            den += e;
-            acc += e * (double)kvst[(size_t)s * width + col];
-        }
-        r = (float)(acc / den);
-    }
-    out[c] = r;
-    if (ov) {
-        for (int s = 0; s < ratio; s++) {
-            const size_t to = (size_t)s * width, from = (size_t)(ratio + s) * width;
-            kvst[to + c] = kvst[from + c];
-            kvst[to + hd + c] = kvst[from + hd + c];
-            scst[to + c] = scst[from + c];
-            scst[to + hd + c] = scst[from + hd + c];
-        }
-    }
-}
-
 /* A closing window in one launch, one workgroup, one thread per channel c
- * (blockDim >= hd): the pool of k_comp_pool (the slot loads of a batch of 8
- * issued together, the arithmetic in slot order), the ratio-4 slide, then
- * k_norm_rope's weighted RMSNorm of the pooled row and RoPE of its last rd
- * elements at pos, written to out. */
+ * (blockDim >= hd): the pool of channel c over the slots (dsv4_compress.c:
+ * 100-137; ratio 4 -- ov -- pools slots 0..ratio-1 from the previous
+ * window's first halves, columns c, and slots ratio..2 ratio-1 from the
+ * current window's second halves, columns hd + c; the slot loads of a batch
+ * of 8 issued together, the arithmetic in slot order), the ratio-4 slide of
+ * the current window into the previous one, then the weighted RMSNorm of the
+ * pooled row and RoPE of its last rd elements at pos, written to out. */
 constexpr int CC_MAX = 1024;
 
 __global__ void __launch_bounds__(CC_MAX)
@@ -326,22 +272,6 @@ k_comp_close(float *__restrict__ out, float *__restrict__ kvst, float *__restric
 
 } // namespace
 
-int dsv4_norm_rope_launch(float *dst, int dst_stride, const float *src, int src_stride,
-                          const float *w, int nvec, int n, int norm, float eps, int rd,
-                          const float *cs, const float *sn, int pos, int half, int inverse,
-                          hipStream_t st)
-{
-    if (nvec <= 0 || n <= 0 || rd < 0 || rd > n || (rd & 1) || (rd && (!cs || !sn)) ||
-        pos < 0 || (rd && half < rd / 2)) {
-        DSV4_ERR("norm_rope: bad arguments (nvec %d n %d rd %d pos %d)", nvec, n, rd, pos);
-        return -1;
-    }
-    hipLaunchKernelGGL(k_norm_rope, dim3(nvec), dim3(NR_THREADS), 0, st, dst, dst_stride,
-                       src, src_stride, w, n, norm, eps, rd, cs, sn, pos, half, inverse);
-    HIP_OK(hipGetLastError(), "norm_rope launch");
-    return 0;
-}
-
 int dsv4_block_prep_launch(const Dsv4Prep *a, hipStream_t st)
 {
     if (a->nj < 0 || a->nj > 2 || a->width < 0 || (a->width && (!a->kvs || !a->scs))) {
@@ -376,16 +306,5 @@ int dsv4_comp_close_launch(float *out, float *kv_state, float *score_state, int 
     hipLaunchKernelGGL(k_comp_close, dim3(1), dim3(nt), 0, st, out, kv_state, score_state,
                        ratio, hd, ratio == 4 ? 1 : 0, w, eps, rd, cs, sn, pos, half);
     HIP_OK(hipGetLastError(), "comp_close launch");
-    return 0;
-}
-
-int dsv4_comp_pool_launch(float *out, float *kv_state, float *score_state, int ratio,
-                          int hd, hipStream_t st)
-{
-    if (ratio <= 0 || hd <= 0) return -1;
-    hipLaunchKernelGGL(k_comp_pool, dim3((hd + NR_THREADS - 1) / NR_THREADS),
-                       dim3(NR_THREADS), 0, st, out, kv_state, score_state, ratio, hd,
-                       ratio == 4 ? 1 : 0);
-    HIP_OK(hipGetLastError(), "comp_pool launch");
     return 0;
 }

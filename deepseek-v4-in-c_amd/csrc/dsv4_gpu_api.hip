@@ -19,6 +19,7 @@
 #include "dsv4_internal.h"
 #include "dsv4_dev.h"
 
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -326,7 +327,9 @@ int register_expert(int layer, int expert, const Dsv4ExpertDev &d, int hidden,
     L->host[expert] = d;
     if (owned) L->owned.push_back(owned);
     L->dirty = true;
-    return 0;
+    /* the device table follows every registration, so a MoE call never has
+     * to copy (or grow) it -- the no-allocation entry point relies on that */
+    return layer_sync(*L);
 }
 
 hipStream_t as_stream(void *s) { return (hipStream_t)s; }
@@ -839,6 +842,12 @@ int dsv4_gpu_topk(int *idxs, const float *scores, int n, int k)
     if (!g_ready || n < 0) return -1;
     if (k > n) k = n;
     if (k <= 0) return k < 0 ? -1 : 0;
+    for (int i = 0; i < n; i++)
+        if (isnan(scores[i])) {
+            DSV4_ERR("topk: score %d is NaN (the reference's order then depends on "
+                     "positions; not reproduced)", i);
+            return -1;
+        }
     if (scratch_reserve(g_index, dsv4_index_scratch_bytes(n)) != 0) return -1;
     Stage s;
     const size_t so = s.in(scores, (size_t)n * sizeof(float));
@@ -878,6 +887,11 @@ int dsv4_gpu_indexer_topk(int *idxs, const float *q, const float *w, int H,
                          g_index.p, hist, g_stream) != 0)
         return -1;
     if (stage_pull(io, (size_t)k * sizeof(int), idxs) != 0) return -1;
+    if (idxs[0] < 0) {                  /* the device top-k saw a NaN score */
+        DSV4_ERR("indexer_topk: a score is NaN (the reference's order then depends on "
+                 "positions; not reproduced)");
+        return -1;
+    }
     return k;
 }
 
@@ -1013,7 +1027,7 @@ struct AttnBlock {
     float *ape = nullptr, *cs = nullptr, *sn = nullptr;
     float *kv_cache = nullptr, *comp_kv = nullptr, *comp_score = nullptr;
     float *x = nullptr, *qr = nullptr, *q = nullptr, *kv = nullptr, *ckv = nullptr;
-    float *csc = nullptr, *pooled = nullptr, *idx_q = nullptr, *idx_w = nullptr;
+    float *csc = nullptr, *idx_q = nullptr, *idx_w = nullptr;
     float *scores = nullptr, *o = nullptr, *ogrp = nullptr, *out = nullptr;
     int *idxs = nullptr;
     void *iscr = nullptr, *ascr = nullptr;
@@ -1088,6 +1102,25 @@ int block_bind(int layer, const dsv4_gpu_attn_cfg *cp, const dsv4_gpu_attn_w *w)
         DSV4_ERR("attn_bind: head_dim %d not supported by the sparse attention", hd);
         return -1;
     }
+    /* Refuse here what a step could not run: a step changes the layer's
+     * state (ring slot, compressor slots, compressed rows) before its last
+     * launches, so a refusal part way through would leave the state ahead of
+     * the position. */
+    if (idx && c.idx_topk > dsv4_topk_kmax()) {
+        DSV4_ERR("attn_bind: index_topk %d above the device top-k's %d", c.idx_topk,
+                 dsv4_topk_kmax());
+        return -1;
+    }
+    if (rows > dsv4_attn_max_rows(DSV4_GPU_KV_F32, hd, hd)) {
+        DSV4_ERR("attn_bind: window + max_pos / ratio + 1 = %d rows above the sparse "
+                 "attention's %d", rows, dsv4_attn_max_rows(DSV4_GPU_KV_F32, hd, hd));
+        return -1;
+    }
+    if (comp && hd > 1024) {
+        DSV4_ERR("attn_bind: head_dim %d: the compressor's close takes at most 1024 "
+                 "channels", hd);
+        return -1;
+    }
     const size_t F = sizeof(float);
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off += align256(bytes ? bytes : 4); return o; };
@@ -1098,7 +1131,7 @@ int block_bind(int layer, const dsv4_gpu_attn_cfg *cp, const dsv4_gpu_attn_w *w)
     const size_t o_ckv = take((size_t)b.nslot * b.width * F), o_csc = take((size_t)b.nslot * b.width * F);
     const size_t o_x = take(c.hidden * F), o_qr = take(c.q_lora * F), o_q = take((size_t)H * hd * F);
     const size_t o_k = take(hd * F), o_ki = take(b.width * F), o_si = take(b.width * F);
-    const size_t o_pl = take(hd * F), o_iq = take((size_t)c.idx_heads * c.idx_dim * F);
+    const size_t o_iq = take((size_t)c.idx_heads * c.idx_dim * F);
     const size_t o_iw = take(c.idx_heads * F), o_sc = take((size_t)b.max_comp * F);
     const size_t o_o = take((size_t)H * hd * F), o_og = take((size_t)c.o_groups * c.o_lora * F);
     const size_t o_out = take(c.hidden * F), o_ix = take((size_t)rows * sizeof(int));
@@ -1116,7 +1149,7 @@ int block_bind(int layer, const dsv4_gpu_attn_cfg *cp, const dsv4_gpu_attn_w *w)
     b.kv_cache = (float *)(m + o_kv); b.comp_kv = (float *)(m + o_ckv); b.comp_score = (float *)(m + o_csc);
     b.x = (float *)(m + o_x); b.qr = (float *)(m + o_qr); b.q = (float *)(m + o_q);
     b.kv = (float *)(m + o_k); b.ckv = (float *)(m + o_ki); b.csc = (float *)(m + o_si);
-    b.pooled = (float *)(m + o_pl); b.idx_q = (float *)(m + o_iq); b.idx_w = (float *)(m + o_iw);
+    b.idx_q = (float *)(m + o_iq); b.idx_w = (float *)(m + o_iw);
     b.scores = (float *)(m + o_sc); b.o = (float *)(m + o_o); b.ogrp = (float *)(m + o_og);
     b.out = (float *)(m + o_out); b.idxs = (int *)(m + o_ix);
     b.iscr = m + o_is; b.ascr = m + o_as;
@@ -1259,18 +1292,11 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
                 return -1;
             }
             float *crow = b.kv_cache + (size_t)(c.window + b.n_comp) * hd;
-            if (hd <= 1024) {
-                /* pool, comp.norm and RoPE at the window's first position in
-                 * one launch */
-                OK(dsv4_comp_close_launch(crow, b.comp_kv, b.comp_score, c.ratio, hd,
-                                          b.comp_norm, c.rms_eps, rd, b.cs, b.sn,
-                                          pos + 1 - c.ratio, half, st));
-            } else {
-                OK(dsv4_comp_pool_launch(b.pooled, b.comp_kv, b.comp_score, c.ratio, hd, st));
-                OK(dsv4_norm_rope_launch(crow, 0, b.pooled, 0, b.comp_norm, 1, hd, 1,
-                                         c.rms_eps, rd, b.cs, b.sn, pos + 1 - c.ratio, half, 0,
-                                         st));
-            }
+            /* pool, comp.norm and RoPE at the window's first position in one
+             * launch (bind took head_dim <= 1024) */
+            OK(dsv4_comp_close_launch(crow, b.comp_kv, b.comp_score, c.ratio, hd,
+                                      b.comp_norm, c.rms_eps, rd, b.cs, b.sn,
+                                      pos + 1 - c.ratio, half, st));
             b.n_comp++;
         }
         /* which compressed rows attention sees (dsv4_layer.c:267-297) */

@@ -112,6 +112,13 @@ int dsv4_moe_fp4_valu_launch(float *d_out, const float *d_x,
  * over n scores, in bytes. The standalone score needs none. */
 size_t dsv4_index_scratch_bytes(int n);
 
+/* The largest k a device top-k takes (dsv4_topk_launch refuses more). */
+int dsv4_topk_kmax(void);
+
+/* The most selected rows dsv4_attn_block_launch takes at this KV format and
+ * width (0: the width is not supported). */
+int dsv4_attn_max_rows(int kv_fmt, int d_qk, int d_v);
+
 /* Whether a top-k of k over n scores starts from the level-1 histogram that
  * dsv4_indexer_score_launch builds with with_hist set. */
 int dsv4_topk_takes_hist(int n, int k);
@@ -173,15 +180,6 @@ int dsv4_attn_launch(float *d_o, const float *d_q, const void *d_kv,
 
 /* ---- the attention block's element-wise steps (dsv4_attnblk.hip) ------ */
 
-/* nvec vectors of n floats (src at src_stride, dst at dst_stride, dst may
- * alias src): scaled by 1/sqrt(mean square + eps) when norm, times w[n] when
- * w is given, then the last rd elements RoPE'd at table row pos (half floats
- * per row of cs / sn; inverse negates the sine). */
-int dsv4_norm_rope_launch(float *dst, int dst_stride, const float *src, int src_stride,
-                          const float *w, int nvec, int n, int norm, float eps, int rd,
-                          const float *cs, const float *sn, int pos, int half, int inverse,
-                          hipStream_t st);
-
 /* One RMSNorm (+ RoPE of the last rd elements at pos) of the block prep. */
 struct Dsv4NormJob {
     float *dst;
@@ -210,9 +208,3 @@ int dsv4_block_prep_launch(const Dsv4Prep *a, hipStream_t st);
 int dsv4_comp_close_launch(float *out, float *kv_state, float *score_state, int ratio,
                            int hd, const float *w, float eps, int rd, const float *cs,
                            const float *sn, int pos, int half, hipStream_t st);
-
-/* The compressor's pool of a closing window into out[hd] (with the ratio-4
- * slide). */
-int dsv4_comp_pool_launch(float *out, float *kv_state, float *score_state, int ratio,
-                          int hd, hipStream_t st);
-

@@ -20,6 +20,9 @@
  * to T are taken; the elements > T are ordered by (key desc, index asc) by
  * counting, for each, the candidates ahead of it (k_tk_part, k_tk_final).
  * Up to 4096 scores, one launch ranks every element directly (k_tk_small).
+ * A NaN score makes every output slot -1: the reference's scan takes a NaN
+ * exactly when it is the first index not yet taken, an order the keys cannot
+ * express, so the device reports it instead of guessing.
  *
  * SPARSE ATTENTION (dsv4_attn.c:60-108): split over the selected rows and a
  * log-sum-exp combine. Partial pass: per split of selected rows, the scores,
@@ -72,6 +75,7 @@ constexpr int TK_SLICES = 16;                   /* spread of the global atomics 
 constexpr int MT_ABOVE = 1;                     /* cand[] append counter (word 0 unused) */
 constexpr int MT_BIN = 2;                       /* B */
 constexpr int MT_KREM = 3;                      /* rank of the k-th inside B */
+constexpr int MT_NAN = 4;                       /* nonzero: a score is NaN */
 
 
 /* Order-preserving 32-bit key of a score: a > b as floats iff fkey(a) >
@@ -353,7 +357,7 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
     const float tf = (float)total;
     const float sc = tf * scale;
     if (t < n) out[t] = sc;
-    if (HIST && blockIdx.x == 0 && lane == 0) meta[MT_ABOVE] = 0u;
+    if (HIST && blockIdx.x == 0 && lane == 0) { meta[MT_ABOVE] = 0u; meta[MT_NAN] = 0u; }
     if (HIST)
         hist_push_global(hist + (blockIdx.x % TK_SLICES) * TK_BINS, t < n,
                          fkey(sc) >> 21, lane);
@@ -488,7 +492,7 @@ k_iscore_kh(float *__restrict__ out, uint32_t *__restrict__ hist, uint32_t *__re
     }
     if (HIST) {
         /* the top-k's level-1 histogram, by the waves that hold keys */
-        if (blockIdx.x == 0 && threadIdx.x == 0) meta[MT_ABOVE] = 0u;
+        if (blockIdx.x == 0 && threadIdx.x == 0) { meta[MT_ABOVE] = 0u; meta[MT_NAN] = 0u; }
         if ((int)(threadIdx.x & ~63u) < kpw)
             hist_push_global(hist + (blockIdx.x % TK_SLICES) * TK_BINS,
                              (int)threadIdx.x < kpw && tt < n, fkey(sc) >> 21,
@@ -548,7 +552,7 @@ k_tk_hist(uint32_t *__restrict__ hist, uint32_t *__restrict__ meta,
     const int i = blockIdx.x * 256 + threadIdx.x;
     const bool live = i < n;
     const uint32_t bin = live ? fkey(scores[i]) >> 21 : 0u;
-    if (i == 0) meta[MT_ABOVE] = 0u;
+    if (i == 0) { meta[MT_ABOVE] = 0u; meta[MT_NAN] = 0u; }
     hist_push_global(hist + (blockIdx.x % TK_SLICES) * TK_BINS, live, bin,
                      threadIdx.x & 63);
 }
@@ -652,9 +656,16 @@ k_tk_part(unsigned long long *__restrict__ cand, uint32_t *__restrict__ meta,
 #pragma unroll
         for (int q = 0; q < BPT / 4; q++)
             hv[s][q] = *reinterpret_cast<const u32x4 *>(hist_g + s * TK_BINS + blo + 4 * q);
+    bool nan = false;
 #pragma unroll
-    for (int m = 0; m < PT_EPT; m++)
-        key[m] = e0 + m * PT_THREADS < n ? fkey(__uint_as_float(key[m])) : 0u;
+    for (int m = 0; m < PT_EPT; m++) {
+        const bool in = e0 + m * PT_THREADS < n;
+        nan = nan || (in && __builtin_isnan(__uint_as_float(key[m])));
+        key[m] = in ? fkey(__uint_as_float(key[m])) : 0u;
+    }
+    /* a NaN anywhere: the final pass writes -1 to every slot (the
+     * reference's selection then depends on positions, not on the order) */
+    if (__ballot(nan) != 0ull && lane == 0) atomicOr(&meta[MT_NAN], 1u);
 
     uint32_t c[BPT];                                /* c[j]: bin blo + BPT-1-j */
 #pragma unroll
@@ -756,6 +767,11 @@ k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
     for (int i = blockIdx.x * FN_THREADS + tid; i < TK_SLICES * TK_BINS / 4;
          i += gridDim.x * FN_THREADS)
         reinterpret_cast<u32x4 *>(hist_g)[i] = u32x4{0u, 0u, 0u, 0u};
+    if (meta[MT_NAN]) {                                   /* uniform per launch */
+        const int j = blockIdx.x * RK_EPW + tid;
+        if (tid < RK_EPW && j < k) idxs[j] = -1;
+        return;
+    }
     const uint32_t B = meta[MT_BIN], krem1 = meta[MT_KREM];
     const uint32_t c_above = min(meta[MT_ABOVE], (uint32_t)TK_KMAX);
 
@@ -926,6 +942,7 @@ __global__ void __launch_bounds__(256)
 k_tk_small(int *__restrict__ idxs, const float *__restrict__ scores, int n, int k)
 {
     __shared__ unsigned long long comp[TS_NMAX];
+    bool nan = false;
     {
         constexpr int PT = TS_NMAX / 256;
         float v[PT];
@@ -939,11 +956,18 @@ k_tk_small(int *__restrict__ idxs, const float *__restrict__ scores, int n, int 
             const int i = u * 256 + (int)threadIdx.x;
             if (i < n)
                 comp[i] = ((unsigned long long)fkey(v[u]) << 32) | (0xFFFFFFFFu - (uint32_t)i);
+            nan = nan || (i < n && __builtin_isnan(v[u]));
         }
     }
-    __syncthreads();
+    const int anynan = __syncthreads_or(nan ? 1 : 0);
     const int e = blockIdx.x * TS_EPW + (int)(threadIdx.x / TS_TPE);
     const int q = threadIdx.x % TS_TPE;
+    if (anynan) {
+        /* every workgroup saw every score: they all take this branch and
+         * together write -1 to slots 0 .. k-1 (k <= n) */
+        if (q == 0 && e < k) idxs[e] = -1;
+        return;
+    }
     const unsigned long long me = comp[min(e, n - 1)];
     int cnt = 0;
 #pragma unroll 8
@@ -1302,6 +1326,12 @@ k_attn_combine(float *__restrict__ o, const float *__restrict__ pm,
             fs[s] = f;
             lp[s] = ls * f;
         }
+        /* lane 0 reads the other lanes' terms: order the wave's LDS writes
+         * before its reads (a wave-scope release / acquire around the wave
+         * barrier, so the compiler cannot hoist the reads either) */
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (tid == 0) {
             double denom = 0.0;
 #pragma unroll 8
@@ -1692,6 +1722,18 @@ size_t dsv4_index_scratch_bytes(int n)
 {
     const size_t g = n > 0 ? ((size_t)n + PT_ELEMS - 1) / PT_ELEMS : 1;
     return IX_BLIST + sizeof(unsigned long long) * PT_ELEMS * g;
+}
+
+int dsv4_topk_kmax(void) { return TK_KMAX; }
+
+int dsv4_attn_max_rows(int kv_fmt, int d_qk, int d_v)
+{
+    int rowb;
+    size_t lds;
+    const int sr = attn_split_rows(kv_fmt, d_qk, d_v, &rowb, &lds);
+    /* the launch halves the split width only while the splits are fewer
+     * than two per CU (< 1024), so the base width bounds the rows */
+    return sr > 0 ? 1024 * sr : 0;
 }
 
 int dsv4_topk_takes_hist(int n, int k)

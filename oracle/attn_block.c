@@ -29,7 +29,9 @@
  * block's host-buffer call.
  *
  * usage: dsv4_attn CKPT_DIR [N_POSITIONS] [--tol T]
- *        dsv4_attn --flash N_POSITIONS RATIO [--tol T]
+ *        dsv4_attn --flash N_POSITIONS RATIO [--tol T] [--topk K] [--cpu-only]
+ * --cpu-only times the reference's attention() on the host cores and stops
+ * before the device pass (the CPU baseline of bench.py).
  */
 #include "dsv4_layer.c"
 
@@ -147,7 +149,7 @@ static float *syn_vec(uint64_t seed, int n, float scale, float add)
 
 static int upload(const DSV4QMat *m);
 
-static int flash_mode(int n, int ratio, double tol, int idx_topk)
+static int flash_mode(int n, int ratio, double tol, int idx_topk, int cpu_only)
 {
     static int cr[1];
     cr[0] = ratio;
@@ -221,6 +223,11 @@ static int flash_mode(int n, int ratio, double tol, int idx_topk)
         const double t1 = now_s();
         if (p >= 4) { t_cpu += t1 - t0; n_cpu++; }
     }
+    if (cpu_only) {
+        printf("flash: ratio %d positions %d cpu_ms_per_position %.3f threads %d\n", ratio, n,
+               n_cpu ? 1e3 * t_cpu / n_cpu : 0.0, omp_get_max_threads());
+        return 0;
+    }
     if (!dsv4_gpu_available() || dsv4_gpu_init() != 0) {
         fprintf(stderr, "attn: no GPU\n");
         printf("flash: ratio %d positions %d cpu_ms_per_position %.3f threads %d\n", ratio, n,
@@ -282,7 +289,8 @@ int main(int argc, char **argv)
 {
     if (argc < 2) {
         fprintf(stderr, "usage: %s CKPT_DIR [N_POSITIONS] [--tol T]\n"
-                        "       %s --flash N_POSITIONS RATIO [--tol T] [--topk K]\n",
+                        "       %s --flash N_POSITIONS RATIO [--tol T] [--topk K] "
+                        "[--cpu-only]\n",
                 argv[0], argv[0]);
         return 1;
     }
@@ -291,12 +299,14 @@ int main(int argc, char **argv)
     if (!strcmp(argv[1], "--flash")) {
         if (argc < 4) return 1;
         int idx_topk = 512;                     /* DeepSeek-V4-Flash's index_topk */
-        for (int i = 4; i + 1 < argc; i += 2) {
-            if (!strcmp(argv[i], "--tol")) tol = atof(argv[i + 1]);
-            else if (!strcmp(argv[i], "--topk")) idx_topk = atoi(argv[i + 1]);
+        int cpu_only = 0;
+        for (int i = 4; i < argc; i++) {
+            if (!strcmp(argv[i], "--cpu-only")) cpu_only = 1;
+            else if (!strcmp(argv[i], "--tol") && i + 1 < argc) tol = atof(argv[++i]);
+            else if (!strcmp(argv[i], "--topk") && i + 1 < argc) idx_topk = atoi(argv[++i]);
         }
         if (idx_topk <= 0) return 1;
-        return flash_mode(atoi(argv[2]), atoi(argv[3]), tol, idx_topk);
+        return flash_mode(atoi(argv[2]), atoi(argv[3]), tol, idx_topk, cpu_only);
     }
     for (int i = 2; i < argc; i++) {
         if (!strcmp(argv[i], "--tol") && i + 1 < argc) tol = atof(argv[++i]);

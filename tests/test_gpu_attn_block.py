@@ -46,6 +46,28 @@ def test_attention_block_matches_reference(tmp_path):
     assert len(rels) == 160 and max(rels) > 0.0       # the device really computed it
 
 
+def test_attention_block_past_4096_compressed_rows(tmp_path):
+    """16,600 positions on the tiny checkpoint: its ratio-4 layers reach 4,150
+    compressed rows, past the 4,096 scores the one-launch top-k ranks, so the
+    block's CSA selection runs the radix path (the score kernel's level-1
+    histogram, then the partition and final passes); the ratio-8 layer
+    attends to 2,075 compressed rows. Every step against the reference's
+    attention(), bar 1e-5."""
+    tiny_checkpoint.write(str(tmp_path))
+    print("attn long: 16600 positions, checkpoint %s" % tmp_path, flush=True)
+    p = subprocess.run([ATTN, str(tmp_path), "16600", "--tol", "1e-5"], capture_output=True,
+                       text=True, timeout=600)
+    print("\n".join(l for l in p.stdout.splitlines() if "worst" in l or "summary" in l),
+          flush=True)
+    sys.stdout.flush()
+    assert p.returncode == 0, p.stdout[-3000:] + p.stderr[-2000:]
+    m = re.search(r"summary: layers (\d+) steps (\d+) worst_rel (\S+) over_tol (\d+)",
+                  p.stdout)
+    assert m and int(m.group(1)) == 4 and int(m.group(2)) == 66400 and int(m.group(4)) == 0
+    per = re.findall(r"layer (\d+) ratio (\d+) indexer (\d+): worst_rel", p.stdout)
+    assert sum(int(r) == 4 and int(i) for _, r, i in per) == 2   # both CSA layers selected
+
+
 @pytest.mark.parametrize("n,ratio,topk", [(24, 4, 512), (40, 4, 4), (132, 128, 512),
                                           (20, 0, 512)])
 def test_attention_block_flash_shapes(n, ratio, topk):

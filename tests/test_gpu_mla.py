@@ -121,6 +121,47 @@ def test_topk_all_equal(gpu, dsv4):
         assert np.array_equal(dsv4.topk(s, 2048), np.arange(2048))
 
 
+@pytest.mark.parametrize("n,k", [(4000, 100), (9000, 2048)])
+def test_topk_nan_scores_refused(gpu, dsv4, n, k):
+    """The reference's scan takes a NaN only when it is the first index not
+    yet taken, an order the device does not reproduce: the host-buffer call
+    returns -1, the stream-ordered one writes -1 to every slot, and the next
+    clean call is unaffected. Both paths (ranked, radix)."""
+    import torch
+    L = dsv4.lib()
+    rng = np.random.default_rng(n)
+    s = rng.standard_normal(n).astype(np.float32)
+    bad = s.copy()
+    bad[n // 3] = np.nan
+    idx = np.empty(k, np.int32)
+    assert L.dsv4_gpu_topk(idx.ctypes.data, bad.ctypes.data, n, k) == -1
+    dev = torch.device("cuda:0")
+    sp = torch.cuda.current_stream().cuda_stream
+    d_i = torch.zeros(k, dtype=torch.int32, device=dev)
+    for scores, want in ((bad, np.full(k, -1, np.int32)), (s, oracle.topk(s, k))):
+        d_s = torch.from_numpy(scores).to(dev)
+        d_i.fill_(7)
+        assert L.dsv4_gpu_topk_d(d_i.data_ptr(), d_s.data_ptr(), n, k, sp) == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(d_i.cpu().numpy(), want)
+
+
+def test_indexer_topk_nan_weight_refused(gpu, dsv4):
+    """A NaN head weight makes a score NaN wherever that head's dot is
+    positive (dsv4_indexer.c:75-80): indexer_topk returns -1."""
+    codes, s, deq, q, w = c4_indexer(3, n=6000)
+    keys = store(dsv4, codes, dsv4.KV_FP8, s)
+    w = w.copy()
+    w[0] = np.nan
+    L = dsv4.lib()
+    idx = np.empty(256, np.int32)
+    assert L.dsv4_gpu_indexer_topk(idx.ctypes.data, q.ctypes.data, w.ctypes.data, 16, 128,
+                                   keys.h, 0, 128, 6000, 256) == -1
+    w[0] = 1.0
+    got = dsv4.indexer_topk(q, w, keys, 6000, 256)
+    assert np.array_equal(got, oracle.topk(oracle.indexer_score(q, deq, w), 256))
+
+
 # ----------------------------------------------------------- attention
 def c4_attention(seed, n=32768, h=64, d_qk=576, d_v=512, topk=2048):
     rng = np.random.default_rng(seed)

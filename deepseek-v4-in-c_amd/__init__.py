@@ -99,6 +99,8 @@ _SIGS = {
     "dsv4_gpu_has_expert": (_ci, [_ci, _ci]),
     "dsv4_gpu_moe_fp4": (_ci, [_vp, _vp, _ci, _vp, _vp, _ci, _ci, _ci, _cf]),
     "dsv4_gpu_moe_fp4_d": (_ci, [_vp, _vp, _ci, _vp, _vp, _ci, _ci, _ci, _cf, _vp]),
+    "dsv4_gpu_moe_fp4_noalloc_d": (_ci, [_vp, _vp, _ci, _vp, _vp, _ci, _ci, _ci, _cf,
+                                         _vp]),
     "dsv4_gpu_kv_create": (_vp, [_ci, _ci, _ci]),
     "dsv4_gpu_kv_write_rows": (_ci, [_vp, _ci, _ci, _vp, _vp]),
     "dsv4_gpu_kv_data": (_vp, [_vp]),

@@ -25,6 +25,16 @@
 
 #include <vector>
 
+/* Scratch of dsv4_gpu_moe_fp4_noalloc_d: a fixed array in every device's
+ * global memory, so that entry point allocates nothing. Host code never uses
+ * the array's name as an address (on the host it is only a stand-in for the
+ * symbol): dsv4_gpu_init looks up its device address once per device with
+ * hipGetSymbolAddress and keeps it in g_static_scratch. */
+#define DSV4_STATIC_SCRATCH_MAX (1u << 20)
+#define DSV4_MAX_DEVICES 64
+static __device__ __align__(256) unsigned char scratch[DSV4_STATIC_SCRATCH_MAX];
+static void *g_static_scratch[DSV4_MAX_DEVICES];
+
 namespace {
 
 /* ------------------------------------------------------------- residency */
@@ -419,6 +429,15 @@ int dsv4_gpu_init(void)
     HIP_OK(hipMemGetInfo(&freeb, &totb), "hipMemGetInfo");
     HIP_OK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking),
            "hipStreamCreate");
+    /* the static scratch's address on this device (device 0 is current) */
+    int dev = 0;
+    HIP_OK(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= DSV4_MAX_DEVICES) { DSV4_ERR("device %d out of range", dev); return -1; }
+    if (!g_static_scratch[dev]) {
+        void *ptr = nullptr;
+        HIP_OK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress scratch");
+        g_static_scratch[dev] = ptr;
+    }
     printf("hip: %s (%s), %d CUs, %.2f GB free of %.2f GB\n", p.name,
            p.gcnArchName, p.multiProcessorCount, (double)freeb / 1073741824.0,
            (double)totb / 1073741824.0);
@@ -726,6 +745,48 @@ int dsv4_gpu_moe_fp4_d(float *d_out, const float *d_x, int layer,
     return dsv4_moe_fp4_launch(d_out, d_x, L->dev, (int)L->host.size(), d_idx,
                                d_w, topk, hidden, inter, swiglu_limit,
                                g_moe.p, as_stream(stream));
+}
+
+int dsv4_gpu_moe_fp4_noalloc_d(float *d_out, const float *d_x, int layer,
+                               const int *d_idx, const float *d_w, int topk,
+                               int hidden, int inter, float swiglu_limit,
+                               void *stream)
+{
+    if (!g_ready || layer < 0 || (size_t)layer >= g_layers.size() || topk <= 0 ||
+        !d_out || !d_x || !d_idx || !d_w) {
+        DSV4_ERR("moe_noalloc: layer %d has no resident experts, or bad arguments", layer);
+        return -1;
+    }
+    const LayerExperts &L = g_layers[layer];
+    if (L.hidden != hidden || L.inter != inter) {
+        DSV4_ERR("moe_noalloc: layer %d experts are %dx%d, call asks %dx%d", layer,
+                 L.inter, L.hidden, inter, hidden);
+        return -1;
+    }
+    if (L.dirty || !L.dev) {
+        /* registration keeps the table current; only a failed copy leaves it stale */
+        DSV4_ERR("moe_noalloc: layer %d's expert table is not on the device", layer);
+        return -1;
+    }
+    const size_t need = dsv4_moe_scratch_bytes(topk, hidden, inter);
+    if (need == 0 || need > DSV4_STATIC_SCRATCH_MAX) {
+        DSV4_ERR("moe_noalloc: topk %d x %d x %d needs %zu bytes of scratch; the static "
+                 "scratch holds %u", topk, inter, hidden, need, DSV4_STATIC_SCRATCH_MAX);
+        return -1;
+    }
+    int dev = 0;
+    HIP_OK(hipGetDevice(&dev), "hipGetDevice");
+    void *ptr = (dev >= 0 && dev < DSV4_MAX_DEVICES) ? g_static_scratch[dev] : nullptr;
+    if (!ptr) {
+        DSV4_ERR("moe_noalloc: no static scratch on device %d (dsv4_gpu_init runs on "
+                 "device 0)", dev);
+        return -1;
+    }
+    /* the kernels overwrite every scratch byte they read (x's and h's term
+     * planes) before reading it, so the previous call's contents need no
+     * clearing */
+    return dsv4_moe_fp4_launch(d_out, d_x, L.dev, (int)L.host.size(), d_idx, d_w, topk,
+                               hidden, inter, swiglu_limit, ptr, as_stream(stream));
 }
 
 /* ------------------------------------------------------------ KV stores */

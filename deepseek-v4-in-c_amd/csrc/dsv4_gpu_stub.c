@@ -76,6 +76,11 @@ int dsv4_gpu_moe_fp4_d(float *d_out, const float *d_x, int layer,
                        int hidden, int inter, float swiglu_limit, void *stream)
 { (void)d_out; (void)d_x; (void)layer; (void)d_idx; (void)d_w; (void)topk;
   (void)hidden; (void)inter; (void)swiglu_limit; (void)stream; return -1; }
+int dsv4_gpu_moe_fp4_noalloc_d(float *d_out, const float *d_x, int layer,
+                               const int *d_idx, const float *d_w, int topk,
+                               int hidden, int inter, float swiglu_limit, void *stream)
+{ (void)d_out; (void)d_x; (void)layer; (void)d_idx; (void)d_w; (void)topk;
+  (void)hidden; (void)inter; (void)swiglu_limit; (void)stream; return -1; }
 
 dsv4_gpu_kv *dsv4_gpu_kv_create(int n_rows, int row_dim, int fmt)
 { (void)n_rows; (void)row_dim; (void)fmt; return NULL; }

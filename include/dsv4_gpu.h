@@ -230,6 +230,23 @@ int dsv4_gpu_moe_fp4_d(float *d_out, const float *d_x, int layer,
                        int hidden, int inter, float swiglu_limit,
                        void *stream);
 
+/* dsv4_gpu_moe_fp4_d without any allocation: the same kernels and the same
+ * bits, with their scratch (x's and h's bf16 term planes, or h in f32) in a
+ * fixed 1 MiB array in each device's global memory instead of a buffer the
+ * library grows with hipMalloc. No counterpart in the reference: it is for
+ * callers that cannot allocate -- code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc. It calls no hipMalloc,
+ * hipFree or allocating library routine. The experts must be registered
+ * (dsv4_gpu_upload_expert / dsv4_gpu_bind_expert_d) before; -1 with a
+ * message when the call needs more scratch than the array holds (the staged
+ * matrix-core form takes hidden x 6 + topk x inter x 6 bytes, the VALU form
+ * topk x inter x 4: topk 64 at inter 2048 and hidden 16384 fit). Every call
+ * on one device shares that device's array: calls that overlap on one
+ * device (two streams, or two host threads) race. */
+int dsv4_gpu_moe_fp4_noalloc_d(float *d_out, const float *d_x, int layer,
+                               const int *d_idx, const float *d_w, int topk,
+                               int hidden, int inter, float swiglu_limit,
+                               void *stream);
 
 /* ============================================================ sparse MLA */
 

@@ -9,11 +9,14 @@ sweep: the six GEMVs back to back on one stream, every input already resident
 in HBM. `value` is achieved HBM GB/s over the sweep (algorithmic bytes /
 step time); `ms_per_step` is the time per trunk token (all six shapes).
 
-Timing. Every timed region is a run of launches queued behind a spin kernel
-on the same stream, so the host has issued them all before the first one
-starts and the GPU runs them back to back: HIP events bracket exactly the
-launches timed, with no host launch latency inside. The headline times
-exactly `--steps` sweeps per trial and takes the median of 5 trials.
+Timing. Every timed region is a run of launches the GPU executes back to
+back, HIP events bracketing exactly the launches timed, with no host launch
+latency inside. The headline queues `--warmup` sweeps and then exactly
+`--steps` timed sweeps with no synchronisation between them (the host issues
+a sweep in far less than its GPU time, so it stays ahead), median of 5
+trials. Work the host issues more slowly than the GPU runs it (small
+kernels, the attention block) is queued behind a spin kernel sized to the
+host's issue time, then warm untimed launches, then the timed ones.
 
 Cold data: one sweep streams 1.15 GB, more than the 256 MB Infinity Cache,
 so every matrix has been evicted before it is read again. Per-shape times
@@ -149,14 +152,28 @@ class Bench:
         if self._cyc_per_ms > 0:
             torch.cuda._sleep(int(ms * self._cyc_per_ms))
 
-    def blocked_us(self, go, n, trials=3, spin_ms=20.0):
-        """Per-iteration time of go(i, stream) issued n times back to back
-        behind a spin kernel, median over trials (i keeps counting across
-        trials, so rotations continue). Returns (median us, [us per trial])."""
+    def blocked_us(self, go, n, trials=3, warm=None):
+        """Per-iteration time of go(i, stream) issued n times back to back,
+        median over trials (i keeps counting, so rotations continue). Each
+        trial queues a spin kernel long enough for the host to issue
+        everything behind it (1.3x the host issue time measured on an
+        untimed pass), then `warm` untimed iterations that bring the clocks
+        back up after the spin, then the n timed ones between two events.
+        Returns (median us, [us per trial])."""
         torch = self.torch
+        warm = min(n, 16) if warm is None else warm
+        t0 = time.perf_counter()
+        for _ in range(n):
+            go(self._it, self.sp)
+            self._it += 1
+        host_ms = (time.perf_counter() - t0) * 1e3 * (n + warm) / n
+        torch.cuda.synchronize()
         per = []
         for _ in range(trials):
-            self.spin(spin_ms)
+            self.spin(1.3 * host_ms + 0.2)
+            for _ in range(warm):
+                go(self._it, self.sp)
+                self._it += 1
             a, b = self.ev(), self.ev()
             a.record(self.stream)
             for _ in range(n):
@@ -217,19 +234,35 @@ class Bench:
             self.c2_launch(m, sp)
 
     def c2_run(self, steps, warmup, trials=5):
-        """The headline: exactly `steps` sweeps per trial, back to back behind
-        a spin kernel, median over `trials` (ms per sweep, and every trial).
-        Also the same sweeps issued from the host without the spin (eager,
-        host launch gaps included) and as a HIP graph of 10 sweeps replayed
-        10 times, both for comparison only."""
+        """The headline: per trial, `warmup` untimed sweeps and then exactly
+        `steps` timed sweeps, all queued back to back on the stream (the host
+        issues a sweep in well under its GPU time, so it stays ahead and the
+        GPU never waits on it; the warm sweeps keep the clocks up into the
+        timed region); HIP events bracket the timed sweeps. Median over
+        `trials` after one untimed trial (ms per sweep, and every timed trial).
+        Also, for comparison only:
+        the sweeps issued after a synchronisation (eager) and as a HIP graph
+        of 10 sweeps replayed 10 times."""
         torch = self.torch
         for i in range(warmup):
             self.c2_step(i)
         torch.cuda.synchronize()
-        med, per = self.blocked_us(self.c2_step, steps, trials)
+        per = []
+        for trial in range(trials + 1):             # the first settles the clocks, untimed
+            for i in range(max(1, warmup)):
+                self.c2_step(i)
+            a, b = self.ev(), self.ev()
+            a.record(self.stream)
+            for i in range(steps):
+                self.c2_step(i)
+            b.record(self.stream)
+            torch.cuda.synchronize()
+            if trial:
+                per.append(a.elapsed_time(b) / steps)
+        med = sorted(per)[len(per) // 2]
         eager_ms = self.eager_us(self.c2_step, steps, 0) / 1e3
         graph_ms = self.graph_us(self.c2_step, 10, 10) / 1e3
-        return med / 1e3, [p / 1e3 for p in per], eager_ms, graph_ms
+        return med, per, eager_ms, graph_ms
 
     def c2_shape_run(self, k, reps=3):
         """One sweep shape alone: distinct copies of it (>= 1 GiB together, so
@@ -377,7 +410,7 @@ class Bench:
         ih, idd, itop = 64, 128, 512
         has_idx = ratio == 4
         coff = 2 if ratio == 4 else 1
-        maxpos = p0 + warmup + 4 * steps + 8
+        maxpos = p0 + warmup + 8 * steps + 64
         rng = np.random.default_rng(11)
         keep = []
 

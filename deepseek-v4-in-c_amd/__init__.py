@@ -61,6 +61,29 @@ class AttnW(ctypes.Structure):
                                    "rope_cos", "rope_sin")]
 
 
+class CkptDims(ctypes.Structure):
+    """dsv4_gpu_ckpt_dims (include/dsv4_gpu.h)."""
+    _fields_ = [(n, _ci) for n in ("hidden", "q_lora", "n_heads", "head_dim", "o_groups",
+                                   "o_lora", "moe_inter", "n_shared", "n_experts",
+                                   "index_n_heads", "index_head_dim", "compress_ratio",
+                                   "has_indexer")]
+
+
+class LayerMats(ctypes.Structure):
+    """dsv4_gpu_layer_mats (include/dsv4_gpu.h)."""
+    _fields_ = [(n, DSV4QMat) for n in ("wq_a", "wq_b", "wkv", "wo_a", "wo_b", "shared_w1",
+                                        "shared_w2", "shared_w3", "gate", "comp_wkv",
+                                        "comp_wgate", "idx_wq_b", "idx_wproj",
+                                        "idx_comp_wkv", "idx_comp_wgate")]
+
+
+class CkptStats(ctypes.Structure):
+    """dsv4_gpu_ckpt_stats (include/dsv4_gpu.h)."""
+    _fields_ = [("shards", _ci), ("tensors", ctypes.c_longlong),
+                ("matrices", ctypes.c_longlong), ("experts", ctypes.c_longlong),
+                ("bytes", ctypes.c_longlong), ("seconds", ctypes.c_double)]
+
+
 def build():
     """Compile lib/libdsv4_gpu.so (hipcc, gfx950) and the CPU stub."""
     subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
@@ -118,6 +141,13 @@ _SIGS = {
     "dsv4_gpu_mla_decode_d": (_ci, [_vp, _vp, _vp, _vp, _ci, _ci, _vp, _vp, _ci,
                                     _ci, _ci, _ci, _vp, _vp, _ci, _ci, _ci, _vp,
                                     _ci, _ci, _ci, _cf, _vp]),
+    "dsv4_gpu_ckpt_open": (_vp, [ctypes.c_char_p]),
+    "dsv4_gpu_ckpt_close": (None, [_vp]),
+    "dsv4_gpu_ckpt_has": (_ci, [_vp, ctypes.c_char_p]),
+    "dsv4_gpu_ckpt_load_qmat": (_ci, [_vp, ctypes.c_char_p, _ci, _ci, _ci, _QP]),
+    "dsv4_gpu_ckpt_load_expert": (_ci, [_vp, _ci, _ci, _ci, _ci, _EP]),
+    "dsv4_gpu_ckpt_load_layer": (_ci, [_vp, _vp, _ci, _vp, _vp]),
+    "dsv4_gpu_ckpt_stats_get": (_ci, [_vp, _vp]),
     "dsv4_gpu_attn_bind": (_ci, [_ci, _ACP, _AWP]),
     "dsv4_gpu_attn_ready": (_ci, [_ci]),
     "dsv4_gpu_attn_reset": (_ci, [_ci]),
@@ -182,7 +212,8 @@ def qmat(W, S, wdt=WFP8, rows=None, cols=None, blk_r=128, blk_c=128):
     """A DSV4QMat over numpy arrays (the arrays must outlive it)."""
     rows = W.shape[0] if rows is None else rows
     cols = W.shape[1] if cols is None else cols
-    return DSV4QMat(W.ctypes.data, S.ctypes.data, wdt, rows, cols, blk_r, blk_c)
+    return DSV4QMat(W.ctypes.data, None if S is None else S.ctypes.data, wdt, rows, cols,
+                    blk_r, blk_c)
 
 
 def mmq(m, x):

@@ -23,6 +23,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <map>
 #include <vector>
 
 /* Scratch of dsv4_gpu_moe_fp4_noalloc_d: a fixed array in every device's
@@ -39,9 +40,14 @@ namespace {
 
 /* ------------------------------------------------------------- residency */
 struct Res {
-    const uint8_t *key, *key_end;   /* host weight bytes [key, key_end)   */
-    const uint8_t *skey;            /* host scale grid                     */
+    const uint8_t *key, *key_end;   /* the caller's weight bytes [key, key_end):
+                                       host memory for an upload, the device
+                                       copy itself for a matrix loaded into
+                                       HBM directly                          */
+    const uint8_t *skey;            /* the caller's scale grid               */
     uint8_t *dw, *ds;
+    void *own_w, *own_s;            /* device blocks freed at shutdown (or
+                                       nullptr: owned elsewhere)             */
     int wdt;                        /* DSV4_WFP8, DSV4_WFP4 or DSV4_WBF16  */
     int rows, cols, blk_r, blk_c, sc, sfmt;
     size_t row_bytes() const
@@ -72,7 +78,34 @@ struct Scratch {
 
 bool g_ready = false;
 hipStream_t g_stream = nullptr;
-std::vector<Res> g_res;
+/* Resident matrices by the start of their key range. Ranges never overlap
+ * (registration refuses that), so the one that can hold a pointer p is the
+ * last starting at or below p: an O(log n) lookup, which matters once every
+ * routed expert matrix of a checkpoint is resident (Flash: 43 x 256 x 3). */
+std::map<uintptr_t, Res> g_res;
+
+/* The resident matrix whose key range holds p, or nullptr. */
+const Res *res_at(const void *p)
+{
+    auto it = g_res.upper_bound((uintptr_t)p);
+    if (it == g_res.begin()) return nullptr;
+    --it;
+    return (const uint8_t *)p < it->second.key_end ? &it->second : nullptr;
+}
+
+/* Add r unless its key range overlaps a resident one. */
+int res_insert(const Res &r)
+{
+    const uintptr_t a = (uintptr_t)r.key, b = (uintptr_t)r.key_end;
+    auto it = g_res.lower_bound(a);
+    if (it != g_res.end() && it->first < b) return -1;
+    if (it != g_res.begin()) {
+        --it;
+        if ((uintptr_t)it->second.key_end > a) return -1;
+    }
+    g_res.emplace(a, r);
+    return 0;
+}
 std::vector<LayerExperts> g_layers;
 Arena g_ar;
 Scratch g_moe, g_attn, g_scores, g_index, g_amax;
@@ -154,121 +187,128 @@ int stage_pull(size_t off, size_t bytes, void *dst)
     return 0;
 }
 
-/* Resolve m to a resident matrix and a row offset; nullptr if none. */
-const Res *find_view(const DSV4QMat *m, int *r0)
+/* A DSV4QMat resolved on the device: the resident matrix it lies in, and the
+ * device addresses of its own first weight row and first scale-grid row. */
+struct View {
+    const Res *r = nullptr;
+    const uint8_t *w = nullptr, *s = nullptr;
+};
+
+/* Resolve m: its weight pointer at a whole-row offset inside a resident
+ * matrix of the same format, width and blocking, its rows inside that
+ * matrix, and (FP8 / FP4) its scale pointer at a whole row of that matrix's
+ * scale grid with its ceil(rows / blk_r) scale rows inside the grid. The
+ * device then computes exactly what the reference's CPU kernel computes for
+ * m: row r of m against scale row r / blk_r counted from m->s (dsv4_matmul.c:
+ * 293-345). That covers attention()'s wo_a group slices whatever o_lora is
+ * (dsv4_layer.c:321-334 offsets the scale pointer by g * (o_lora / blk_r)
+ * grid rows). false if m resolves to nothing. */
+bool find_view(const DSV4QMat *m, View *v)
 {
-    if (!m || !m->w) return nullptr;
+    if (!m || !m->w || m->rows <= 0) return false;
     const uint8_t *p = (const uint8_t *)m->w;
-    for (const Res &r : g_res) {
-        if (p < r.key || p >= r.key_end) continue;
-        if (m->wdt != r.wdt || m->cols != r.cols || m->rows <= 0) return nullptr;
-        const size_t off = (size_t)(p - r.key);
-        if (off % r.row_bytes()) return nullptr;
-        const int row0 = (int)(off / r.row_bytes());
-        if (row0 + m->rows > r.rows) return nullptr;
-        if (r.wdt == DSV4_WBF16) {                      /* no scales, no blocking */
-            *r0 = row0;
-            return &r;
-        }
-        if (m->blk_r != r.blk_r || m->blk_c != r.blk_c) return nullptr;
-        if (row0 % r.blk_r) return nullptr;
-        const size_t ssz = r.sfmt ? 4 : 1;
-        const uint8_t *want_s = r.skey + (size_t)(row0 / r.blk_r) * r.sc * ssz;
-        if ((const uint8_t *)m->s != want_s) return nullptr;
-        *r0 = row0;
-        return &r;
-    }
-    return nullptr;
+    const Res *rp = res_at(p);
+    if (!rp) return false;
+    const Res &r = *rp;
+    if (m->wdt != r.wdt || m->cols != r.cols) return false;
+    const size_t off = (size_t)(p - r.key);
+    if (off % r.row_bytes()) return false;
+    const int row0 = (int)(off / r.row_bytes());
+    if (row0 + m->rows > r.rows) return false;
+    v->r = &r;
+    v->w = r.dw + off;
+    v->s = nullptr;
+    if (r.wdt == DSV4_WBF16) return true;               /* no scales, no blocking */
+    if (m->blk_r != r.blk_r || m->blk_c != r.blk_c || !m->s) return false;
+    const size_t srow = (size_t)r.sc * (r.sfmt ? 4 : 1);  /* bytes per grid row */
+    const uint8_t *sp = (const uint8_t *)m->s;
+    if (sp < r.skey) return false;
+    const size_t soff = (size_t)(sp - r.skey);
+    if (soff % srow) return false;
+    const size_t srow0 = soff / srow;
+    const size_t grid_rows = (size_t)(r.rows + r.blk_r - 1) / r.blk_r;
+    if (srow0 + (size_t)(m->rows + r.blk_r - 1) / r.blk_r > grid_rows) return false;
+    v->s = r.ds + soff;
+    return true;
 }
 
-/* FP8 (sfmt 0: E8M0 scale bytes, 1: fp32) or FP4 (E8M0 bytes) matrices. */
-int upload_bf16(const DSV4QMat *m);
-
-int upload_qmat(const DSV4QMat *m, int sfmt)
+/* Register m (the caller's key pointers m->w / m->s and logical shape) as
+ * resident, its bytes at dw / ds in HBM; own_w / own_s are freed at
+ * shutdown. -1 when its key range overlaps a resident one. */
+int res_add(const DSV4QMat *m, int sfmt, uint8_t *dw, uint8_t *ds, void *own_w,
+            void *own_s)
 {
-    if (m && m->wdt == DSV4_WBF16 && sfmt == 0) return upload_bf16(m);
-    if (!g_ready || !m || !m->w || !m->s) return -1;
-    if (m->rows <= 0 || m->cols <= 0 || m->blk_r <= 0 || m->blk_c <= 0) return -1;
-    if (m->wdt == DSV4_WFP4) {
-        if (sfmt != 0 || !dsv4_fp4_gemv_ok(m->rows, m->cols, m->blk_r, m->blk_c))
-            return -1;
-    } else if (m->wdt != DSV4_WFP8) {
-        return -1;
-    }
-    for (const Res &r : g_res)
-        if (r.key == (const uint8_t *)m->w) return 0;
-    const int sc = (m->cols + m->blk_c - 1) / m->blk_c;
-    const size_t wb = (size_t)m->rows * (size_t)m->cols / (m->wdt == DSV4_WFP4 ? 2 : 1);
-    const size_t sb = (size_t)((m->rows + m->blk_r - 1) / m->blk_r) * sc *
-                      (sfmt ? 4u : 1u);
-    if (wb + sb + (256u << 20) > dsv4_gpu_free_vram()) return -1;
-    uint8_t *dw = nullptr, *ds = nullptr;
-    if (hipMalloc((void **)&dw, wb) != hipSuccess) return -1;
-    if (hipMalloc((void **)&ds, sb) != hipSuccess) { (void)hipFree(dw); return -1; }
-    if (hipMemcpy(dw, m->w, wb, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(ds, m->s, sb, hipMemcpyHostToDevice) != hipSuccess) {
-        (void)hipFree(dw); (void)hipFree(ds);
-        return -1;
-    }
     Res r;
+    const size_t wb = m->wdt == DSV4_WFP4 ? (size_t)m->rows * (size_t)m->cols / 2
+                    : m->wdt == DSV4_WBF16 ? (size_t)m->rows * (size_t)m->cols * 2
+                                          : (size_t)m->rows * (size_t)m->cols;
     r.key = (const uint8_t *)m->w;
     r.key_end = r.key + wb;
     r.skey = (const uint8_t *)m->s;
     r.dw = dw; r.ds = ds;
+    r.own_w = own_w; r.own_s = own_s;
     r.wdt = m->wdt;
     r.rows = m->rows; r.cols = m->cols;
     r.blk_r = m->blk_r; r.blk_c = m->blk_c;
-    r.sc = sc; r.sfmt = sfmt;
-    g_res.push_back(r);
-    return 0;
-}
-
-/* A BF16 matrix (the reference's format for the router gate and the LM
- * head): weights only, no scale grid. */
-int upload_bf16(const DSV4QMat *m)
-{
-    if (!g_ready || !m->w || !dsv4_bf16_gemv_ok(m->rows, m->cols)) return -1;
-    for (const Res &r : g_res)
-        if (r.key == (const uint8_t *)m->w) return 0;
-    const size_t wb = (size_t)m->rows * (size_t)m->cols * 2;
-    if (wb + (256u << 20) > dsv4_gpu_free_vram()) return -1;
-    uint8_t *dw = nullptr;
-    if (hipMalloc((void **)&dw, wb) != hipSuccess) return -1;
-    if (hipMemcpy(dw, m->w, wb, hipMemcpyHostToDevice) != hipSuccess) {
-        (void)hipFree(dw);
+    r.sc = m->wdt == DSV4_WBF16 ? 0 : (m->cols + m->blk_c - 1) / m->blk_c;
+    r.sfmt = sfmt;
+    if (res_insert(r) != 0) {
+        DSV4_ERR("a %dx%d matrix at %p overlaps a resident one", m->rows, m->cols, m->w);
         return -1;
     }
-    Res r;
-    r.key = (const uint8_t *)m->w;
-    r.key_end = r.key + wb;
-    r.skey = nullptr;
-    r.dw = dw; r.ds = nullptr;
-    r.wdt = DSV4_WBF16;
-    r.rows = m->rows; r.cols = m->cols;
-    r.blk_r = m->blk_r; r.blk_c = m->blk_c;
-    r.sc = 0; r.sfmt = 0;
-    g_res.push_back(r);
     return 0;
 }
 
-/* y[rows] for rows [r0, r0 + rows) of a resident matrix, x and y device
- * pointers, on stream st (the library stream by default). */
-int res_gemv(const Res &r, int r0, int rows, float *d_y, const float *d_x,
-             hipStream_t st = nullptr)
+/* The shapes the device kernels take, per format. */
+bool qmat_shape_ok(const DSV4QMat *m, int sfmt)
+{
+    if (!m || !m->w || m->rows <= 0 || m->cols <= 0) return false;
+    if (m->wdt == DSV4_WBF16) return sfmt == 0 && dsv4_bf16_gemv_ok(m->rows, m->cols);
+    if (!m->s || m->blk_r <= 0 || m->blk_c <= 0) return false;
+    if (m->wdt == DSV4_WFP4)
+        return sfmt == 0 && dsv4_fp4_gemv_ok(m->rows, m->cols, m->blk_r, m->blk_c);
+    return m->wdt == DSV4_WFP8;
+}
+
+/* FP8 (sfmt 0: E8M0 scale bytes, 1: fp32), FP4 (E8M0 bytes) or BF16 (no
+ * scales) matrices, copied from host memory. */
+int upload_qmat(const DSV4QMat *m, int sfmt)
+{
+    if (!g_ready || !qmat_shape_ok(m, sfmt)) return -1;
+    View v;
+    if (find_view(m, &v)) return 0;             /* resident already (or a view of one) */
+    const bool bf = m->wdt == DSV4_WBF16;
+    const size_t wb = bf ? (size_t)m->rows * (size_t)m->cols * 2
+                    : (size_t)m->rows * (size_t)m->cols / (m->wdt == DSV4_WFP4 ? 2 : 1);
+    const int sc = bf ? 0 : (m->cols + m->blk_c - 1) / m->blk_c;
+    const size_t sb = bf ? 0 : (size_t)((m->rows + m->blk_r - 1) / m->blk_r) * sc *
+                               (sfmt ? 4u : 1u);
+    if (wb + sb + (256u << 20) > dsv4_gpu_free_vram()) return -1;
+    uint8_t *dw = nullptr, *ds = nullptr;
+    if (hipMalloc((void **)&dw, wb) != hipSuccess) return -1;
+    if (sb && hipMalloc((void **)&ds, sb) != hipSuccess) { (void)hipFree(dw); return -1; }
+    if (hipMemcpy(dw, m->w, wb, hipMemcpyHostToDevice) != hipSuccess ||
+        (sb && hipMemcpy(ds, m->s, sb, hipMemcpyHostToDevice) != hipSuccess) ||
+        res_add(m, sfmt, dw, ds, dw, ds) != 0) {
+        (void)hipFree(dw);
+        if (ds) (void)hipFree(ds);
+        return -1;
+    }
+    return 0;
+}
+
+/* y[rows] = the view's rows . x (x and y device pointers), on stream st
+ * (the library stream by default). */
+int res_gemv(const View &v, int rows, float *d_y, const float *d_x, hipStream_t st = nullptr)
 {
     if (!st) st = g_stream;
+    const Res &r = *v.r;
     if (r.wdt == DSV4_WBF16)
-        return dsv4_bf16_gemv_launch(d_y, d_x,
-                                     (const uint16_t *)(r.dw + (size_t)r0 * r.row_bytes()),
-                                     rows, r.cols, st);
+        return dsv4_bf16_gemv_launch(d_y, d_x, (const uint16_t *)v.w, rows, r.cols, st);
     if (r.wdt == DSV4_WFP4)
-        return dsv4_fp4_gemv_launch(d_y, d_x, r.dw + (size_t)r0 * r.row_bytes(),
-                                    r.ds + (size_t)(r0 / r.blk_r) * r.sc, rows, r.cols,
-                                    r.blk_r, r.blk_c, st);
-    const size_t ssz = r.sfmt ? 4 : 1;
-    return dsv4_fp8_gemv_launch(d_y, d_x, r.dw + (size_t)r0 * r.cols,
-                                r.ds + (size_t)(r0 / r.blk_r) * r.sc * ssz, r.sfmt, rows,
-                                r.cols, r.blk_r, r.blk_c, st);
+        return dsv4_fp4_gemv_launch(d_y, d_x, v.w, v.s, rows, r.cols, r.blk_r, r.blk_c, st);
+    return dsv4_fp8_gemv_launch(d_y, d_x, v.w, v.s, r.sfmt, rows, r.cols, r.blk_r, r.blk_c,
+                                st);
 }
 
 /* --------------------------------------------------------------- experts */
@@ -457,7 +497,10 @@ void dsv4_gpu_shutdown(void)
 {
     if (!g_ready) return;
     (void)hipDeviceSynchronize();
-    for (Res &r : g_res) { (void)hipFree(r.dw); (void)hipFree(r.ds); }
+    for (auto &kv : g_res) {
+        if (kv.second.own_w) (void)hipFree(kv.second.own_w);
+        if (kv.second.own_s) (void)hipFree(kv.second.own_s);
+    }
     g_res.clear();
     for (LayerExperts &L : g_layers) {
         for (void *p : L.owned) (void)hipFree(p);
@@ -484,14 +527,14 @@ int dsv4_gpu_upload_f32s(const DSV4QMat *m) { return upload_qmat(m, 1); }
 
 int dsv4_gpu_has(const DSV4QMat *m)
 {
-    int r0;
-    return (g_ready && find_view(m, &r0)) ? 1 : 0;
+    View v;
+    return (g_ready && find_view(m, &v)) ? 1 : 0;
 }
 
 void dsv4_gpu_mmq(float *y, const float *x, const DSV4QMat *m)
 {
-    int r0 = 0;
-    const Res *r = g_ready ? find_view(m, &r0) : nullptr;
+    View v;
+    const Res *r = (g_ready && find_view(m, &v)) ? v.r : nullptr;
     if (!r) {
         DSV4_ERR("mmq called for a matrix that is not resident");
         abort();
@@ -501,8 +544,7 @@ void dsv4_gpu_mmq(float *y, const float *x, const DSV4QMat *m)
     const size_t yo = s.add((size_t)m->rows * sizeof(float));
     size_t end;
     if (stage_push(s, &end) != 0) abort();
-    const int rc = res_gemv(*r, r0, m->rows, (float *)(g_ar.d + yo),
-                            (const float *)(g_ar.d + xo));
+    const int rc = res_gemv(v, m->rows, (float *)(g_ar.d + yo), (const float *)(g_ar.d + xo));
     if (rc != 0 || stage_pull(yo, (size_t)m->rows * sizeof(float), y) != 0) {
         DSV4_ERR("mmq failed");
         abort();
@@ -512,8 +554,8 @@ void dsv4_gpu_mmq(float *y, const float *x, const DSV4QMat *m)
 void dsv4_gpu_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
 {
     if (nt <= 1) { dsv4_gpu_mmq(y, x, m); return; }
-    int r0 = 0;
-    const Res *r = g_ready ? find_view(m, &r0) : nullptr;
+    View v;
+    const Res *r = (g_ready && find_view(m, &v)) ? v.r : nullptr;
     if (!r || nt > DSV4_MAX_BATCH) {
         DSV4_ERR("mmq_n called for a matrix that is not resident, or a batch "
                  "of %d above %d", nt, DSV4_MAX_BATCH);
@@ -524,19 +566,16 @@ void dsv4_gpu_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
     const size_t yo = s.add((size_t)nt * m->rows * sizeof(float));
     size_t end;
     if (stage_push(s, &end) != 0) abort();
-    const size_t ssz = r->sfmt ? 4 : 1;
     int rc = 0;
     if (r->wdt == DSV4_WFP4 || r->wdt == DSV4_WBF16) {
         /* token by token: per (row, token) the GEMV's own arithmetic */
         for (int t = 0; t < nt && rc == 0; t++)
-            rc = res_gemv(*r, r0, m->rows, (float *)(g_ar.d + yo) + (size_t)t * m->rows,
+            rc = res_gemv(v, m->rows, (float *)(g_ar.d + yo) + (size_t)t * m->rows,
                           (const float *)(g_ar.d + xo) + (size_t)t * r->cols);
     } else {
         rc = dsv4_fp8_gemv_n_launch(
             (float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
-            r->dw + (size_t)r0 * r->cols,
-            r->ds + (size_t)(r0 / r->blk_r) * r->sc * ssz, r->sfmt, m->rows,
-            r->cols, r->blk_r, r->blk_c, nt, g_stream);
+            v.w, v.s, r->sfmt, m->rows, r->cols, r->blk_r, r->blk_c, nt, g_stream);
     }
     if (rc != 0 ||
         stage_pull(yo, (size_t)nt * m->rows * sizeof(float), y) != 0) {
@@ -595,8 +634,8 @@ int dsv4_gpu_bf16_gemv_d(float *d_y, const float *d_x, const uint16_t *d_w, int 
 /* ----------------------------------------------------------------- head */
 int dsv4_gpu_head_argmax(const float *x, const DSV4QMat *head)
 {
-    int r0 = 0;
-    const Res *r = g_ready ? find_view(head, &r0) : nullptr;
+    View v;
+    const Res *r = (g_ready && find_view(head, &v)) ? v.r : nullptr;
     if (!r || !x) {
         DSV4_ERR("head_argmax: the head matrix is not resident");
         return -1;
@@ -608,7 +647,7 @@ int dsv4_gpu_head_argmax(const float *x, const DSV4QMat *head)
     const size_t to = s.add(sizeof(int));
     size_t end;
     if (stage_push(s, &end) != 0) return -1;
-    if (res_gemv(*r, r0, head->rows, (float *)(g_ar.d + lo), (const float *)(g_ar.d + xo)) != 0 ||
+    if (res_gemv(v, head->rows, (float *)(g_ar.d + lo), (const float *)(g_ar.d + xo)) != 0 ||
         dsv4_argmax_launch((int *)(g_ar.d + to), (const float *)(g_ar.d + lo), head->rows,
                            g_amax.p, g_stream) != 0)
         return -1;
@@ -679,6 +718,47 @@ int dsv4_gpu_bind_expert_d(int layer, int expert, const DSV4ExpertW *e)
                     (const uint8_t *)e->w2.w, (const uint8_t *)e->w2.s};
     return register_expert(layer, expert, d, hidden, inter, nullptr);
 }
+
+/* ------------------------------------------- matrices loaded into HBM */
+} /* extern "C" */
+
+int dsv4_res_adopt(const DSV4QMat *m, void *owned)
+{
+    if (!g_ready || !qmat_shape_ok(m, 0)) {
+        DSV4_ERR("adopt: a %dx%d matrix of format %d is not one the kernels take",
+                 m ? m->rows : 0, m ? m->cols : 0, m ? m->wdt : -1);
+        return -1;
+    }
+    return res_add(m, 0, (uint8_t *)m->w, (uint8_t *)m->s, owned, nullptr);
+}
+
+int dsv4_expert_adopt(int layer, int expert, const DSV4ExpertW *e, void *owned)
+{
+    int hidden, inter;
+    if (!g_ready || !e || !expert_shape_ok(e, &hidden, &inter)) return -1;
+    if (dsv4_gpu_has_expert(layer, expert)) {
+        DSV4_ERR("adopt: layer %d expert %d is registered already", layer, expert);
+        return -1;
+    }
+    /* its three matrices resident too (keyed by their device addresses), so
+     * the reference's dispatch reaches them one by one as expert_forward
+     * does, besides the fused pass */
+    int added = 0;
+    const DSV4QMat *ms[3] = {&e->w1, &e->w3, &e->w2};
+    for (; added < 3; added++)
+        if (!qmat_shape_ok(ms[added], 0) ||
+            res_add(ms[added], 0, (uint8_t *)ms[added]->w, (uint8_t *)ms[added]->s, nullptr,
+                    nullptr) != 0)
+            break;
+    const Dsv4ExpertDev d{(const uint8_t *)e->w1.w, (const uint8_t *)e->w1.s,
+                          (const uint8_t *)e->w3.w, (const uint8_t *)e->w3.s,
+                          (const uint8_t *)e->w2.w, (const uint8_t *)e->w2.s};
+    if (added == 3 && register_expert(layer, expert, d, hidden, inter, owned) == 0) return 0;
+    for (int i = 0; i < added; i++) g_res.erase((uintptr_t)ms[i]->w);   /* roll back */
+    return -1;
+}
+
+extern "C" {
 
 int dsv4_gpu_has_expert(int layer, int expert)
 {
@@ -1058,20 +1138,28 @@ namespace {
 /* A resident matrix (or a row range of one) as a block reads it. */
 struct MatRef {
     Res r{};
-    int r0 = 0;
+    const uint8_t *w = nullptr, *s = nullptr;   /* device: its first row / scale row */
+    View view() const
+    {
+        View v;
+        v.r = &r;
+        v.w = w;
+        v.s = s;
+        return v;
+    }
 };
 
 int mat_ref(const DSV4QMat *m, int rows, int cols, MatRef *out, const char *what)
 {
-    int r0 = 0;
-    const Res *r = m ? find_view(m, &r0) : nullptr;
-    if (!r || m->rows != rows || m->cols != cols) {
+    View v;
+    if (!m || !find_view(m, &v) || m->rows != rows || m->cols != cols) {
         DSV4_ERR("attn_bind: %s (%dx%d) is not a resident %dx%d matrix", what,
                  m ? m->rows : 0, m ? m->cols : 0, rows, cols);
         return -1;
     }
-    out->r = *r;
-    out->r0 = r0;
+    out->r = *v.r;
+    out->w = v.w;
+    out->s = v.s;
     return 0;
 }
 
@@ -1259,7 +1347,7 @@ int x_gemvs(const XJob *jobs, int n, const float *d_x, hipStream_t st)
         if (done[i]) continue;
         const Res &r = jobs[i].m->r;
         if (r.wdt != DSV4_WFP8 && r.wdt != DSV4_WBF16) {
-            if (res_gemv(r, jobs[i].m->r0, jobs[i].rows, jobs[i].y, d_x, st) != 0) return -1;
+            if (res_gemv(jobs[i].m->view(), jobs[i].rows, jobs[i].y, d_x, st) != 0) return -1;
             done[i] = true;
             continue;
         }
@@ -1273,9 +1361,8 @@ int x_gemvs(const XJob *jobs, int n, const float *d_x, hipStream_t st)
                 (r.wdt == DSV4_WFP8 &&
                  (q.sfmt != r.sfmt || q.blk_r != r.blk_r || q.blk_c != r.blk_c)))
                 continue;
-            const int r0 = jobs[j].m->r0;
-            W[k] = q.dw + (size_t)r0 * q.row_bytes();
-            S[k] = q.ds ? q.ds + (size_t)(r0 / q.blk_r) * q.sc * (q.sfmt ? 4 : 1) : nullptr;
+            W[k] = jobs[j].m->w;
+            S[k] = jobs[j].m->s;
             Y[k] = jobs[j].y;
             R[k] = jobs[j].rows;
             done[j] = true;
@@ -1342,7 +1429,7 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
     OK(dsv4_block_prep_launch(&pp, st));
     /* q: wq_b (each head's norm and RoPE happen inside the attention, on its
      * copy) */
-    OK(res_gemv(b.wq_b.r, b.wq_b.r0, H * hd, b.q, b.qr, st));
+    OK(res_gemv(b.wq_b.view(), H * hd, b.q, b.qr, st));
     const int n_win = pos + 1 < c.window ? pos + 1 : c.window;
     int take = 0, mode = 1;
     if (c.ratio > 0) {
@@ -1364,7 +1451,7 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
         const int avail = b.n_comp;
         if (use_idx) {
             const int ih = c.idx_heads, idd = c.idx_dim;
-            OK(res_gemv(b.iwq_b.r, b.iwq_b.r0, ih * idd, b.idx_q, b.qr, st));
+            OK(res_gemv(b.iwq_b.view(), ih * idd, b.idx_q, b.qr, st));
             take = avail < c.idx_topk ? avail : c.idx_topk;
             const int hist = dsv4_topk_takes_hist(avail, take);
             /* the keys are the compressed region read at index_head_dim
@@ -1397,11 +1484,10 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
     const int gw = H * hd / c.o_groups, gr = c.o_lora;
     const long long ssz = wa.sfmt ? 4 : 1;
     OK(dsv4_fp8_gemv_groups_launch(
-        b.ogrp, b.o, wa.dw + (size_t)b.wo_a.r0 * wa.cols,
-        wa.ds + (size_t)(b.wo_a.r0 / wa.blk_r) * wa.sc * ssz, wa.sfmt, gr, gw, wa.blk_r,
+        b.ogrp, b.o, b.wo_a.w, b.wo_a.s, wa.sfmt, gr, gw, wa.blk_r,
         wa.blk_c, c.o_groups, gr, gw, (long long)gr * wa.cols,
         (long long)(gr / wa.blk_r) * wa.sc * ssz, st));
-    OK(res_gemv(b.wo_b.r, b.wo_b.r0, c.hidden, d_out, b.ogrp, st));
+    OK(res_gemv(b.wo_b.view(), c.hidden, d_out, b.ogrp, st));
 #undef OK
     b.next_pos = pos + 1;
     return 0;

@@ -56,6 +56,21 @@ int dsv4_gpu_embed_row_d(float *d_dst, const void *d_table, int wdt, long long r
                          int hidden, void *stream)
 { (void)d_dst; (void)d_table; (void)wdt; (void)row; (void)hidden; (void)stream; return -1; }
 
+dsv4_gpu_ckpt *dsv4_gpu_ckpt_open(const char *dir) { (void)dir; return NULL; }
+void dsv4_gpu_ckpt_close(dsv4_gpu_ckpt *c) { (void)c; }
+int dsv4_gpu_ckpt_has(const dsv4_gpu_ckpt *c, const char *name) { (void)c; (void)name; return 0; }
+int dsv4_gpu_ckpt_load_qmat(dsv4_gpu_ckpt *c, const char *base, int wdt, int rows,
+                            int cols, DSV4QMat *out)
+{ (void)c; (void)base; (void)wdt; (void)rows; (void)cols; (void)out; return -1; }
+int dsv4_gpu_ckpt_load_expert(dsv4_gpu_ckpt *c, int layer, int expert, int hidden,
+                              int inter, DSV4ExpertW *out)
+{ (void)c; (void)layer; (void)expert; (void)hidden; (void)inter; (void)out; return -1; }
+int dsv4_gpu_ckpt_load_layer(dsv4_gpu_ckpt *c, const dsv4_gpu_ckpt_dims *d, int layer,
+                             dsv4_gpu_layer_mats *out, DSV4ExpertW *experts)
+{ (void)c; (void)d; (void)layer; (void)out; (void)experts; return -1; }
+int dsv4_gpu_ckpt_stats_get(const dsv4_gpu_ckpt *c, dsv4_gpu_ckpt_stats *out)
+{ (void)c; (void)out; return -1; }
+
 int dsv4_gpu_dump_e4m3(float *h) { (void)h; return -1; }
 int dsv4_gpu_dump_e8m0(float *h) { (void)h; return -1; }
 int dsv4_gpu_dump_e2m1(float *h) { (void)h; return -1; }

@@ -81,6 +81,15 @@ int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,
                            const void *S, int sfmt, int rows, int cols,
                            int blk_r, int blk_c, int nt, hipStream_t st);
 
+/* A matrix whose bytes are in HBM already (m->w / m->s device addresses,
+ * e.g. read there from a checkpoint) made resident under those addresses;
+ * `owned` (may be nullptr) is freed at shutdown. 0 / -1. */
+int dsv4_res_adopt(const DSV4QMat *m, void *owned);
+
+/* The same for a routed expert (FP4, 1x32 blocks): registered for the fused
+ * MoE by (layer, expert) and its three matrices made resident. 0 / -1. */
+int dsv4_expert_adopt(int layer, int expert, const DSV4ExpertW *e, void *owned);
+
 /* One routed expert's device tensors (FP4 nibbles + E8M0 per 1x32). */
 struct Dsv4ExpertDev {
     const uint8_t *w1, *s1, *w3, *s3, *w2, *s2;

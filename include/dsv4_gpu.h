@@ -180,6 +180,79 @@ int dsv4_gpu_argmax_d(int *d_out, const float *d_v, int n, void *stream);
 int dsv4_gpu_embed_row_d(float *d_dst, const void *d_table, int wdt, long long row,
                          int hidden, void *stream);
 
+/* ============================================ a checkpoint straight into HBM
+ * The reference streams its checkpoint through host memory (a pinned trunk,
+ * an NVMe expert cache: src/io/dsv4_st.c, src/io/dsv4_trunk.c,
+ * src/cache/dsv4_cache.c). On an MI355X the whole Flash checkpoint fits in
+ * HBM, so these calls read the safetensors shards (the container of
+ * src/io/dsv4_st.c:377-537, the same dtype table and consistency checks) into
+ * device memory once, through pinned staging, with no host copy of a matrix.
+ * What they load is resident under its DEVICE address: the DSV4QMat /
+ * DSV4ExpertW they fill carry device pointers, which the caller's dispatch
+ * passes back to dsv4_gpu_has / dsv4_gpu_mmq (and slices into row-range
+ * views, as attention() does with wo_a); the host must never dereference
+ * them. Freed by dsv4_gpu_shutdown. No counterpart in the reference. */
+typedef struct dsv4_gpu_ckpt dsv4_gpu_ckpt;
+
+/* Index every *.safetensors file of dir (initialising the device if
+ * needed). NULL on failure, with a message. */
+dsv4_gpu_ckpt *dsv4_gpu_ckpt_open(const char *dir);
+void dsv4_gpu_ckpt_close(dsv4_gpu_ckpt *c);
+/* 1 when the checkpoint holds a tensor of that name. */
+int dsv4_gpu_ckpt_has(const dsv4_gpu_ckpt *c, const char *name);
+
+/* The matrix <base>.weight (+ <base>.scale) in the binder's stored form
+ * (src/model/dsv4_bind.c:86-131): DSV4_WFP8 F8_E4M3 [rows][cols] with E8M0
+ * 128x128 scales, DSV4_WFP4 packed I8 [rows][cols/2] with E8M0 1x32 scales,
+ * DSV4_WBF16 [rows][cols]. *out receives the resident matrix. 0 / -1 (absent,
+ * stored otherwise, no room). */
+int dsv4_gpu_ckpt_load_qmat(dsv4_gpu_ckpt *c, const char *base, int wdt, int rows,
+                            int cols, DSV4QMat *out);
+
+/* Routed expert (layer, expert): layers.L.ffn.experts.E.w{1,3,2} (FP4, w1/w3
+ * [inter][hidden], w2 [hidden][inter]) into one HBM block, registered for
+ * dsv4_gpu_moe_fp4[_d] as dsv4_gpu_upload_expert does and its three
+ * matrices resident. *out (may be NULL) receives them. 0 / -1. */
+int dsv4_gpu_ckpt_load_expert(dsv4_gpu_ckpt *c, int layer, int expert, int hidden,
+                              int inter, DSV4ExpertW *out);
+
+/* The shapes a layer's tensors take (from DSV4Cfg, dsv4.h:94-156). */
+typedef struct {
+    int hidden, q_lora, n_heads, head_dim, o_groups, o_lora;
+    int moe_inter, n_shared, n_experts;
+    int index_n_heads, index_head_dim;
+    int compress_ratio;        /* the layer's (0: no compressor)            */
+    int has_indexer;           /* 1 where the layer has the CSA indexer     */
+} dsv4_gpu_ckpt_dims;
+
+/* Every matrix of one decoder layer, resident (device pointers). */
+typedef struct {
+    DSV4QMat wq_a, wq_b, wkv, wo_a, wo_b;                /* FP8            */
+    DSV4QMat shared_w1, shared_w2, shared_w3;            /* FP8            */
+    DSV4QMat gate;                                       /* BF16 router    */
+    DSV4QMat comp_wkv, comp_wgate;                       /* BF16, ratio>0  */
+    DSV4QMat idx_wq_b;                                   /* FP8, indexer   */
+    DSV4QMat idx_wproj, idx_comp_wkv, idx_comp_wgate;    /* BF16, indexer  */
+} dsv4_gpu_layer_mats;
+
+/* Layer `layer` under the binder's names (src/model/dsv4_bind.c:152-243):
+ * the attention's wq_a, wq_b, wkv, wo_a, wo_b, the shared expert, the
+ * router gate, the compressor and indexer projections where the layer has
+ * them, and all d->n_experts routed experts (experts[e] filled when experts
+ * is not NULL). The layer's f32 vectors (norms, sinks, RoPE-free weights)
+ * are not loaded: they are small host-side inputs. 0 / -1. */
+int dsv4_gpu_ckpt_load_layer(dsv4_gpu_ckpt *c, const dsv4_gpu_ckpt_dims *d, int layer,
+                             dsv4_gpu_layer_mats *out, DSV4ExpertW *experts);
+
+typedef struct {
+    int shards;
+    long long tensors;                 /* indexed                              */
+    long long matrices, experts;       /* loaded                               */
+    long long bytes;                   /* read into HBM                        */
+    double seconds;                    /* spent in the loads                   */
+} dsv4_gpu_ckpt_stats;
+int dsv4_gpu_ckpt_stats_get(const dsv4_gpu_ckpt *c, dsv4_gpu_ckpt_stats *out);
+
 /* ========================================================== decoder gates */
 
 /* Device decode of all 256 E4M3FN codes / 256 E8M0 codes / 16 E2M1 codes with

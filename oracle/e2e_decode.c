@@ -22,13 +22,14 @@
  * state each time:
  *   - pass 1: nothing resident, so every matmul runs on the reference CPU
  *     path;
- *   - pass 2: dsv4_gpu_init plus the FP8 trunk upload of dsv4_run.c:270-283,
- *     so every FP8 matmul (including the wo_a group slices) runs on the
- *     MI355X; every expert's FP4 matrices and every BF16 matrix (router
- *     gates, compressors, indexer weights, the LM head) are made resident
- *     too, so the experts' matmuls of expert_forward (dsv4_layer.c:199-206)
- *     and the rest run there through the same dispatch; and the CSA calls of
- *     attention()
+ *   - pass 2: the checkpoint read straight into HBM by the backend's
+ *     loader (dsv4_gpu_ckpt_load_layer / _load_qmat: every FP8 trunk
+ *     matrix, every BF16 matrix -- router gates, compressors, indexer
+ *     weights, the LM head -- and every routed expert), and the binder's
+ *     matrices swapped for the resident ones, so every FP8 matmul (including
+ *     the wo_a group slices), the experts' matmuls of expert_forward
+ *     (dsv4_layer.c:199-206) and the rest run on the MI355X through the
+ *     reference's dispatch; and the CSA calls of attention()
  *     (dsv4_layer.c:286-301) go to the device. oracle/Makefile compiles
  *     dsv4_layer.c with dsv4_indexer_score / dsv4_topk / dsv4_sparse_attn
  *     renamed to the e2e_* wrappers below, which call dsv4_gpu_indexer_score
@@ -316,6 +317,7 @@ typedef struct {
     DSV4Scratch *s;
     float *cs_d, *sn_d, *cs_c, *sn_c;
     int maxpos;
+    DSV4QMat head;           /* the LM head: host bytes, or loaded into HBM */
 } Model;
 
 /* The reference's greedy pick (dsv4_run.c:471-472). */
@@ -341,7 +343,7 @@ static int run_pass(const Model *M, const int *tok, int n, float *logits)
     if (!ls || !h || !y) return -1;
     for (int L = 0; L < c->n_layers; L++)
         if (dsv4_state_init(&ls[L], c, L, M->maxpos) != 0) return -1;
-    DSV4QMat head = {M->mb->w.head, NULL, DSV4_WBF16, c->vocab, d, 0, 0};
+    const DSV4QMat head = M->head;
     for (int pos = 0; pos < n; pos++) {
         g_attn_pos = pos;
         dsv4_embed_row(y, M->mb->w.embed, M->mb->w.wdt, tok[pos], d);
@@ -426,6 +428,7 @@ int main(int argc, char **argv)
     DSV4ExpertSrc src = {.get = expert_get, .ctx = &E};
 
     Model M = {.c = &c, .lb = lb, .mb = &mb, .src = &src, .maxpos = n + 16};
+    M.head = (DSV4QMat){mb.w.head, NULL, DSV4_WBF16, c.vocab, c.hidden, 0, 0};
     const int half = c.qk_rope / 2;
     M.cs_d = malloc((size_t)M.maxpos * half * 4); M.sn_d = malloc((size_t)M.maxpos * half * 4);
     M.cs_c = malloc((size_t)M.maxpos * half * 4); M.sn_c = malloc((size_t)M.maxpos * half * 4);
@@ -454,36 +457,52 @@ int main(int argc, char **argv)
             fprintf(stderr, "e2e: no GPU\n");
             return 2;
         }
+        /* the checkpoint straight into HBM: every matrix and routed expert
+         * read from the shards by the backend's loader (no copy of the
+         * host's), then the binder's matrices swapped for the resident
+         * ones, which carry device addresses */
+        dsv4_gpu_ckpt *ck = dsv4_gpu_ckpt_open(argv[1]);
+        if (!ck) return 1;
         for (int L = 0; L < c.n_layers; L++) {
-            const DSV4LayerW *w = &lb[L].w;
-            const DSV4QMat *m[9] = {&w->attn.wq_a, &w->attn.wq_b, &w->attn.wkv,
-                                    &w->attn.wo_a, &w->attn.wo_b, &w->moe.shared.w1,
-                                    &w->moe.shared.w2, &w->moe.shared.w3,
-                                    w->attn.has_idx ? &w->attn.idx.wq_b : NULL};
-            for (int k = 0; k < 9; k++) {
-                if (!m[k]) continue;
-                if (m[k]->wdt == DSV4_WFP8 && dsv4_gpu_upload(m[k]) == 0) gpu_mats++;
-                if (m[k]->wdt == DSV4_WFP4 && dsv4_gpu_upload(m[k]) == 0) fp4_mats++;
+            DSV4LayerW *w = &lb[L].w;
+            const dsv4_gpu_ckpt_dims dm = {
+                .hidden = c.hidden, .q_lora = c.q_lora, .n_heads = c.n_heads,
+                .head_dim = c.head_dim, .o_groups = c.o_groups, .o_lora = c.o_lora,
+                .moe_inter = c.moe_inter, .n_shared = c.n_shared, .n_experts = c.n_experts,
+                .index_n_heads = c.index_n_heads, .index_head_dim = c.index_head_dim,
+                .compress_ratio = dsv4_compress_ratio(&c, L), .has_indexer = w->has_idx};
+            dsv4_gpu_layer_mats lm;
+            if (dsv4_gpu_ckpt_load_layer(ck, &dm, L, &lm, &E.w[(size_t)L * c.n_experts]) != 0) {
+                fprintf(stderr, "e2e: loading layer %d into HBM failed\n", L);
+                return 1;
             }
-            /* the BF16 matrices: router gate, compressors, indexer weights */
-            const DSV4QMat *b[6] = {&w->moe.gate,
-                                    w->attn.has_comp ? &w->attn.comp.wkv : NULL,
-                                    w->attn.has_comp ? &w->attn.comp.wgate : NULL,
-                                    w->attn.has_idx ? &w->attn.idx.weights_proj : NULL,
-                                    w->attn.has_idx ? &w->attn.idx.comp.wkv : NULL,
-                                    w->attn.has_idx ? &w->attn.idx.comp.wgate : NULL};
-            for (int k = 0; k < 6; k++)
-                if (b[k] && b[k]->wdt == DSV4_WBF16 && dsv4_gpu_upload(b[k]) == 0) bf16_mats++;
-            for (int e = 0; e < c.n_experts; e++) {
-                const DSV4ExpertW *x = &E.w[(size_t)L * c.n_experts + e];
-                const DSV4QMat *em[3] = {&x->w1, &x->w2, &x->w3};
-                for (int k = 0; k < 3; k++)
-                    if (dsv4_gpu_upload(em[k]) == 0) fp4_mats++;
+            DSV4AttnW *a = &w->attn;
+            a->wq_a = lm.wq_a; a->wq_b = lm.wq_b; a->wkv = lm.wkv;
+            a->wo_a = lm.wo_a; a->wo_b = lm.wo_b;
+            w->moe.shared.w1 = lm.shared_w1; w->moe.shared.w2 = lm.shared_w2;
+            w->moe.shared.w3 = lm.shared_w3; w->moe.gate = lm.gate;
+            gpu_mats += 8;
+            bf16_mats += 1;
+            if (a->has_comp) { a->comp.wkv = lm.comp_wkv; a->comp.wgate = lm.comp_wgate; bf16_mats += 2; }
+            if (a->has_idx) {
+                a->idx.wq_b = lm.idx_wq_b; a->idx.weights_proj = lm.idx_wproj;
+                a->idx.comp.wkv = lm.idx_comp_wkv; a->idx.comp.wgate = lm.idx_comp_wgate;
+                gpu_mats += 1;
+                bf16_mats += 3;
             }
+            fp4_mats += 3 * c.n_experts;
         }
-        /* the LM head, the same QMat run_pass builds (dsv4_run.c:467-474) */
-        const DSV4QMat head = {mb.w.head, NULL, DSV4_WBF16, c.vocab, c.hidden, 0, 0};
-        if (dsv4_gpu_upload(&head) == 0) bf16_mats++;
+        /* the LM head, the QMat run_pass uses (dsv4_run.c:467-474) */
+        if (dsv4_gpu_ckpt_load_qmat(ck, "head", DSV4_WBF16, c.vocab, c.hidden, &M.head) != 0)
+            return 1;
+        bf16_mats++;
+        dsv4_gpu_ckpt_stats cs;
+        dsv4_gpu_ckpt_stats_get(ck, &cs);
+        printf("load: %d shards, %lld tensors indexed; %lld matrices and %lld experts read "
+               "into HBM, %lld bytes in %.3f s (%.2f GB/s), no host upload\n", cs.shards,
+               cs.tensors, cs.matrices, cs.experts, cs.bytes, cs.seconds,
+               cs.seconds > 0 ? (double)cs.bytes / cs.seconds / 1e9 : 0.0);
+        dsv4_gpu_ckpt_close(ck);
         printf("gpu: %d FP8, %d FP4 and %d BF16 matrices resident, CSA on the device\n",
                gpu_mats, fp4_mats, bf16_mats);
         g_gpu_csa = 1;
@@ -516,10 +535,8 @@ int main(int argc, char **argv)
             if (a->has_idx) { aw.idx_wq_b = a->idx.wq_b; aw.idx_wproj = a->idx.weights_proj; }
             if (dsv4_gpu_attn_bind(L, &ac, &aw) != 0) return 1;
         }
-        for (int L = 0; L < c.n_layers; L++)
-            for (int e = 0; e < c.n_experts; e++)
-                if (dsv4_gpu_upload_expert(L, e, &E.w[(size_t)L * c.n_experts + e]) != 0)
-                    return 1;
+        /* the routed experts were registered for the fused pass when the
+         * loader read them */
         g_attn_lb = lb;
         g_attn_nl = c.n_layers;
         g_cfg = &c;

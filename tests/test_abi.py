@@ -44,3 +44,33 @@ def test_struct_layout_matches_reference():
     pkg = common.load_pkg()
     assert ctypes.sizeof(pkg.DSV4QMat) == 40
     assert ctypes.sizeof(pkg.DSV4ExpertW) == 120
+
+
+def test_ctypes_layouts_match_the_c_header(tmp_path):
+    """The binding's mirrors of the header's structs have the C sizes and
+    field offsets (compiled with gcc against include/dsv4_gpu.h)."""
+    import ctypes
+    import shutil
+    import subprocess
+    import pytest
+    if not shutil.which("gcc"):
+        pytest.skip("gcc not available")
+    pkg = common.load_pkg()
+    src = tmp_path / "l.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "dsv4_gpu.h"\n'
+        'int main(void){printf("%zu %zu %zu %zu %zu %zu %zu %zu\\n",'
+        'sizeof(dsv4_gpu_attn_cfg), sizeof(dsv4_gpu_attn_w), sizeof(dsv4_gpu_ckpt_dims),'
+        'sizeof(dsv4_gpu_layer_mats), sizeof(dsv4_gpu_ckpt_stats),'
+        'offsetof(dsv4_gpu_layer_mats, gate), offsetof(dsv4_gpu_ckpt_stats, bytes),'
+        'offsetof(dsv4_gpu_ckpt_dims, has_indexer));return 0;}\n')
+    exe = tmp_path / "l"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
+                   check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True,
+                                          check=True).stdout.split()]
+    want = [ctypes.sizeof(pkg.AttnCfg), ctypes.sizeof(pkg.AttnW), ctypes.sizeof(pkg.CkptDims),
+            ctypes.sizeof(pkg.LayerMats), ctypes.sizeof(pkg.CkptStats),
+            pkg.LayerMats.gate.offset, pkg.CkptStats.bytes.offset,
+            pkg.CkptDims.has_indexer.offset]
+    assert got == want

@@ -2,12 +2,14 @@
 configs[4]): 46 teacher-forced random token ids in [0, 129280) through a tiny,
 structurally real deepseek_v4 checkpoint (FP8 trunk, MXFP4 experts, CSA
 indexer with selection, sparse MLA), run by the reference's own C99 model
-code. In the second pass every FP8 matrix the reference uploads
-(dsv4_run.c:270-283) runs on the MI355X through dsv4_gpu_mmq. That includes
-the wo_a group slices, which resolve as row-range views. Every expert's FP4
-matrices and every BF16 matrix (router gates, compressors, indexer weights, the
-LM head) are resident too (they run on the device through the same dispatch),
-and attention()'s CSA calls -- indexer score, top-k, sparse
+code. Before the second pass the backend's loader reads the checkpoint
+straight into HBM (dsv4_gpu_ckpt_load_layer / _load_qmat, no per-matrix host
+upload): every FP8 trunk matrix, every BF16 matrix (router gates,
+compressors, indexer weights, the LM head) and every routed expert. The
+binder's matrices are swapped for the resident ones, so every matmul runs on
+the MI355X through the reference's dispatch (dsv4_gpu_mmq), including the
+wo_a group slices, which resolve as row-range views of a loaded matrix; and
+attention()'s CSA calls -- indexer score, top-k, sparse
 attention (dsv4_layer.c:286-301) -- go to dsv4_gpu_indexer_score /
 dsv4_gpu_topk / dsv4_gpu_sparse_attn.
 
@@ -51,6 +53,16 @@ def test_gpu_trunk_argmax_identical(tmp_path):
     assert int(summ.group(10)) == int(summ.group(11)) == 46   # dsv4_gpu_head_argmax
     assert worst < 2e-3
     assert any(r["rel"] > 0.0 for r in rows), "GPU pass produced CPU bits: trunk not on GPU?"
+    # the checkpoint was read into HBM by the loader: 4 layers of 8 FP8 + 1
+    # BF16 matrices, 2 compressor BF16 on the 3 compressed layers, 1 FP8 + 3
+    # BF16 indexer matrices on the 2 CSA layers, the head; 4 x 16 experts
+    ld = p.load
+    assert ld, p.stdout[-2000:]
+    print("load: %s matrices and %s experts, %s bytes in %s s (%s GB/s)"
+          % (ld.group(3), ld.group(4), ld.group(5), ld.group(6), ld.group(7)), flush=True)
+    assert int(ld.group(3)) == 4 * 9 + 3 * 2 + 2 * 4 + 1
+    assert int(ld.group(4)) == 4 * 16
+    assert int(ld.group(5)) > 0 and float(ld.group(6)) > 0.0
     # pass 3: every layer's attention() output from the device attention block
     s3 = p.summary3
     assert s3, p.stdout[-2000:]

@@ -199,7 +199,11 @@ def test_launch_shape_keeps_bits(gpu, dsv4, monkeypatch, rows, cols):
 
 def test_row_range_views(gpu, dsv4):
     """The wo_a group slicing of attention() (dsv4_layer.c:321-334): every
-    group is resident as a view and computes only its rows."""
+    group is resident as a view and computes only its rows. A slice that
+    starts inside a 128-row block (o_lora below 128) counts its scale rows
+    from its own scale pointer, as the reference's kernel does
+    (dsv4_matmul.c:293-318); a scale pointer off a grid row, or scale rows
+    past the parent's grid, do not resolve."""
     groups, gr, gw = 8, 256, 1024
     rows = groups * gr
     W, Sf, Se, x = common.fp8_problem(31, rows, gw)
@@ -215,8 +219,15 @@ def test_row_range_views(gpu, dsv4):
                            dsv4.WFP8, gr, gw, 128, 128)
         assert L.dsv4_gpu_has(ctypes.byref(sl)) == 1
         assert common.bits_equal(dsv4.mmq(sl, x), yfull[g * gr:(g + 1) * gr])
-    bad = dsv4.DSV4QMat(W.ctypes.data + 64 * gw, Se.ctypes.data, dsv4.WFP8, 64, gw, 128, 128)
-    assert L.dsv4_gpu_has(ctypes.byref(bad)) == 0        # not on a row-block edge
+    # rows 64..127 with the grid's first scale row: the parent's own scales
+    mid = dsv4.DSV4QMat(W.ctypes.data + 64 * gw, Se.ctypes.data, dsv4.WFP8, 64, gw, 128, 128)
+    assert L.dsv4_gpu_has(ctypes.byref(mid)) == 1
+    assert common.bits_equal(dsv4.mmq(mid, x), yfull[64:128])
+    off = dsv4.DSV4QMat(W.ctypes.data + 64 * gw, Se.ctypes.data + 1, dsv4.WFP8, 64, gw, 128, 128)
+    assert L.dsv4_gpu_has(ctypes.byref(off)) == 0          # scale pointer off a grid row
+    past = dsv4.DSV4QMat(W.ctypes.data + (rows - 128) * gw,
+                         Se.ctypes.data + (rows // 128) * sc, dsv4.WFP8, 128, gw, 128, 128)
+    assert L.dsv4_gpu_has(ctypes.byref(past)) == 0         # scale rows past the grid
     other = np.zeros_like(W)
     assert L.dsv4_gpu_has(ctypes.byref(dsv4.qmat(other, Se))) == 0
 

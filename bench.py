@@ -216,7 +216,7 @@ class Bench:
         for i, (rows, cols) in enumerate(TRUNK + [LM_HEAD]):
             W, Sf, Se, x = self.common.fp8_problem(i, rows, cols)
             self.c2.append(dict(rows=rows, cols=cols, W=W, Se=Se, x=x,
-                                dW=self.t(W), dS=self.t(Sf), dx=self.t(x),
+                                dW=self.t(W), dS=self.t(Sf), dSe=self.t(Se), dx=self.t(x),
                                 dy=self.torch.empty(rows, dtype=self.torch.float32,
                                                     device=self.dev)))
         self.torch.cuda.synchronize()
@@ -264,26 +264,29 @@ class Bench:
         graph_ms = self.graph_us(self.c2_step, 10, 10) / 1e3
         return med, per, eager_ms, graph_ms
 
-    def c2_shape_run(self, k, reps=3):
+    def c2_shape_run(self, k, reps=3, sfmt=1):
         """One sweep shape alone: distinct copies of it (>= 1 GiB together, so
         each launch reads its weights cold) launched in rotation behind a spin
-        kernel; median us per launch over `reps` trials."""
+        kernel; median us per launch over `reps` trials. sfmt 1: the
+        configuration's fp32 block scales (the VALU form); 0: the same powers
+        of two as E8M0 bytes, the reference's format (the matrix-core form)."""
         torch = self.torch
         m = self.c2[k]
         per_copy = fp8_bytes(m["rows"], m["cols"])
         copies = max(1, min(512, -(-(1 << 30) // per_copy)))
+        src = m["dS"] if sfmt else m["dSe"]
         if copies > 1:
             dW = m["dW"].unsqueeze(0).repeat(copies, 1, 1)
-            dS = m["dS"].unsqueeze(0).repeat(copies, 1, 1)
+            dS = src.unsqueeze(0).repeat(copies, 1, 1)
         else:
-            dW, dS = m["dW"].unsqueeze(0), m["dS"].unsqueeze(0)
+            dW, dS = m["dW"].unsqueeze(0), src.unsqueeze(0)
         torch.cuda.synchronize()
         rows, cols = m["rows"], m["cols"]
 
         def go(i, sp):
             j = i % copies
             if self.L.dsv4_gpu_fp8_gemv_d(m["dy"].data_ptr(), m["dx"].data_ptr(),
-                                          dW[j].data_ptr(), dS[j].data_ptr(), 1, rows, cols,
+                                          dW[j].data_ptr(), dS[j].data_ptr(), sfmt, rows, cols,
                                           sp) != 0:
                 raise RuntimeError("fp8 gemv launch failed")
         n = max(2 * copies, 20)
@@ -372,19 +375,20 @@ class Bench:
         return us, eager, rows * cols * 2 + cols * 4 + rows * 4
 
     # ------------------------------------------------------- batched (prefill)
-    def gemv_n_run(self, rows=7168, cols=7168, nt=64, calls=30):
+    def gemv_n_run(self, rows=7168, cols=7168, nt=64, calls=30, sfmt=0):
         """The batched FP8 GEMV (dsv4_gpu_fp8_gemv_n_d, the k_mmq_fp8_n
         contract: every (row, token) bit-identical to the GEMV) at nt tokens.
+        sfmt 0: E8M0 scales (the matrix-core form); 1: fp32 (the VALU form).
         Returns (us per call, GFLOP per call)."""
         torch = self.torch
         W, Sf, Se, x = self.common.fp8_problem(0, rows, cols)
-        dW, dS = self.t(W), self.t(Sf)
+        dW, dS = self.t(W), self.t(Se if sfmt == 0 else Sf)
         dx = torch.randn((nt, cols), device=self.dev)
         dy = torch.empty((nt, rows), device=self.dev)
 
         def go(i, sp):
             assert self.L.dsv4_gpu_fp8_gemv_n_d(dy.data_ptr(), dx.data_ptr(), dW.data_ptr(),
-                                                dS.data_ptr(), 1, rows, cols, nt, sp) == 0
+                                                dS.data_ptr(), sfmt, rows, cols, nt, sp) == 0
         go(0, self.sp)
         us, _ = self.blocked_us(go, calls)
         return us, 2.0 * rows * cols * nt / 1e9
@@ -871,11 +875,28 @@ def main():
         detail["c4_sparse_mla_step_32768_top2048"] = rec(*B.c4_run(args.steps, args.warmup))
         log("bench: BF16 LM head")
         detail["lm_head_bf16_129280x7168"] = rec(*B.bf16_head_run(args.steps, args.warmup))
-        us, gf = B.gemv_n_run()
+        log("bench: E8M0 shapes (matrix-core form)")
+        detail["c2_e8m0_per_shape"] = {}
+        for k, ((r, c), a) in enumerate(zip(shapes, algs)):
+            us, copies, n = B.c2_shape_run(k, sfmt=0)
+            detail["c2_e8m0_per_shape"]["%dx%d" % (r, c)] = {
+                "us": round(us, 3), "GBps": round(a / us / 1e3, 1),
+                "frac": round(a / us / 1e3 / PEAK_GBS, 4)}
+        log("bench: batched prefill GEMV")
+        curve = {}
+        for nt in (1, 2, 4, 8, 16, 32, 64):
+            us, gf = B.gemv_n_run(nt=nt, calls=20 if nt < 64 else 30)
+            curve[str(nt)] = {"us": round(us, 3), "TFLOPs": round(gf / us * 1e3, 2)}
+        us, gf = curve["64"]["us"], 2.0 * 7168 * 7168 * 64 / 1e9
         detail["prefill_fp8_7168x7168_nt64"] = {
-            "us": round(us, 3), "TFLOPs": round(gf / us * 1e3, 2),
-            "frac_fp32_peak": round(gf / us * 1e3 / 157.3, 4),
-            "us_per_token": round(us / 64, 3)}
+            "us": us, "TFLOPs": round(gf / us * 1e3, 2),
+            "frac_bf16_peak": round(gf / us * 1e3 / 2500.0, 4),
+            "us_per_token": round(us / 64, 3), "scales": "E8M0 (matrix-core form)",
+            "by_tokens": curve}
+        us32, _ = B.gemv_n_run(nt=64, sfmt=1)
+        detail["prefill_fp8_7168x7168_nt64_f32_scales"] = {
+            "us": round(us32, 3), "TFLOPs": round(gf / us32 * 1e3, 2),
+            "frac_fp32_peak": round(gf / us32 * 1e3 / 157.3, 4), "scales": "fp32 (VALU form)"}
         for ratio, name in ((4, "attn_block_flash_csa_ratio4"), (128, "attn_block_flash_hca_ratio128")):
             log("bench: attention block, ratio %d" % ratio)
             detail[name] = rec(*B.attn_run(32, 4, ratio=ratio))

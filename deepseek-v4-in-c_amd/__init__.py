@@ -117,6 +117,7 @@ _SIGS = {
     "dsv4_gpu_dump_e8m0": (_ci, [_vp]),
     "dsv4_gpu_dump_e2m1": (_ci, [_vp]),
     "dsv4_gpu_dump_fp4_bytes": (_ci, [_vp]),
+    "dsv4_gpu_dump_e4m3_scaled": (_ci, [_vp, _ci]),
     "dsv4_gpu_upload_expert": (_ci, [_ci, _ci, _EP]),
     "dsv4_gpu_bind_expert_d": (_ci, [_ci, _ci, _EP]),
     "dsv4_gpu_has_expert": (_ci, [_ci, _ci]),

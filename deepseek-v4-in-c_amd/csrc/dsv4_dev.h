@@ -36,6 +36,17 @@ __device__ __forceinline__ float dec_e4m3(uint8_t b)
     return o[0];
 }
 
+/* E4M3FN byte b times the power of two s, as bf16 widened to f32: the
+ * matrix-core FP8 form's decode (v_cvt_scalef32_pk_bf16_fp8), exact while
+ * the product stays in bf16's range. */
+__device__ __forceinline__ float dec_e4m3_bf16(uint8_t b, float s)
+{
+    typedef short v2s_ __attribute__((ext_vector_type(2)));
+    const v2s_ p = __builtin_bit_cast(v2s_, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(
+                                                (uint32_t)b, s, false));
+    return __uint_as_float((uint32_t)(uint16_t)p.x << 16);
+}
+
 /* 2^(b-127); b == 0 is the subnormal 2^-127, b == 255 is NaN
  * (dsv4_quant.h:74-88). */
 __device__ __forceinline__ float dec_e8m0(uint32_t b)

@@ -725,6 +725,17 @@ bool blocking_ok(int blk_r, int blk_c)
     return blk_r >= 1 && blk_c >= 16 && (blk_c & 15) == 0;
 }
 
+/* Which arithmetic a matrix gets, by its format and shape alone (never by the
+ * batch size, so the single-token and batched calls agree bit for bit):
+ * E8M0-scaled matrices the kernels can stream take the matrix-core form
+ * (dsv4_fp8_mx.hip), the rest the VALU form of this file.
+ * DSV4_GPU_FP8_MX=0 keeps every matrix on the VALU form. */
+bool mx_form(int sfmt, const float *x, const uint8_t *W, int cols, int blk_r, int blk_c)
+{
+    return env_int("DSV4_GPU_FP8_MX", 1) != 0 && dsv4_fp8_mx_ok(sfmt, cols, blk_r, blk_c) &&
+           (((uintptr_t)x | (uintptr_t)W) & 15) == 0;
+}
+
 int fp8_gemv(float *y, const float *x, const uint8_t *W, const void *S, int sfmt,
              int rows, int cols, int blk_r, int blk_c, const Fp8Groups &gp,
              hipStream_t st)
@@ -736,6 +747,19 @@ int fp8_gemv(float *y, const float *x, const uint8_t *W, const void *S, int sfmt
     const int sc = (cols + blk_c - 1) / blk_c;
     Fp8Geom g;
     const bool aligned = (((uintptr_t)x | (uintptr_t)W) & 15) == 0;
+    if (mx_form(sfmt, x, W, cols, blk_r, blk_c)) {
+        Dsv4Fp8Mx a;
+        a.y = y; a.x = x; a.w = W; a.s = (const uint8_t *)S;
+        a.rows = rows; a.cols = cols; a.sc = sc; a.blk_r = blk_r; a.blk_c = blk_c;
+        a.n = gp.n;
+        a.x_stride = gp.x; a.y_stride = gp.y; a.w_stride = gp.w; a.s_stride = gp.s;
+        a.list = gp.list;
+        for (int i = 0; gp.list && i < gp.n; i++) {
+            a.wl[i] = gp.Wl[i]; a.sl[i] = (const uint8_t *)gp.Sl[i];
+            a.yl[i] = gp.yl[i]; a.rl[i] = gp.rl[i];
+        }
+        return dsv4_fp8_mx_launch(a, st);
+    }
     if (aligned && fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c)) {
         /* Launch shape: R rows per thread per step, next step prefetched,
          * workgroups per CU. None of these changes the arithmetic of a row. */
@@ -841,6 +865,9 @@ int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,
     }
     if (nt == 1)                       /* the GEMV itself: same bits, its launch shape */
         return fp8_gemv(y, x, W, S, sfmt, rows, cols, blk_r, blk_c, Fp8Groups{}, st);
+    if (mx_form(sfmt, x, W, cols, blk_r, blk_c))
+        return dsv4_fp8_mxn_launch(y, x, W, (const uint8_t *)S, rows, cols, blk_r, blk_c, nt,
+                                   st);
     const int sc = (cols + blk_c - 1) / blk_c;
     Fp8Geom g;
     const bool aligned = (((uintptr_t)x | (uintptr_t)W) & 15) == 0;

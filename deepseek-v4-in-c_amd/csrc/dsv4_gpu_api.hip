@@ -385,10 +385,11 @@ int register_expert(int layer, int expert, const Dsv4ExpertDev &d, int hidden,
 hipStream_t as_stream(void *s) { return (hipStream_t)s; }
 
 /* ----------------------------------------------------------- decoder dumps */
-__global__ void k_dump(float *out, int which)
+__global__ void k_dump(float *out, int which, int e8m0)
 {
     const int i = threadIdx.x;
-    if (which == 0) out[i] = dec_e4m3((uint8_t)i);
+    if (which == 4) out[i] = dec_e4m3_bf16((uint8_t)i, dec_e8m0((uint32_t)e8m0));
+    else if (which == 0) out[i] = dec_e4m3((uint8_t)i);
     else if (which == 1) out[i] = dec_e8m0((uint32_t)i);
     else if (which == 2) {
         if (i < 16) {
@@ -404,12 +405,12 @@ __global__ void k_dump(float *out, int which)
     }
 }
 
-int dump(float *host, int which, int count)
+int dump(float *host, int which, int count, int e8m0 = 127)
 {
     if (!g_ready && dsv4_gpu_init() != 0) return -1;
     float *d = nullptr;
     HIP_OK(hipMalloc((void **)&d, 512 * sizeof(float)), "hipMalloc dump");
-    hipLaunchKernelGGL(k_dump, dim3(1), dim3(256), 0, g_stream, d, which);
+    hipLaunchKernelGGL(k_dump, dim3(1), dim3(256), 0, g_stream, d, which, e8m0);
     const hipError_t e = hipGetLastError();
     hipError_t c = hipSuccess;
     if (e == hipSuccess)
@@ -673,6 +674,11 @@ int dsv4_gpu_dump_e4m3(float *host256) { return dump(host256, 0, 256); }
 int dsv4_gpu_dump_e8m0(float *host256) { return dump(host256, 1, 256); }
 int dsv4_gpu_dump_e2m1(float *host16) { return dump(host16, 2, 16); }
 int dsv4_gpu_dump_fp4_bytes(float *host512) { return dump(host512, 3, 512); }
+int dsv4_gpu_dump_e4m3_scaled(float *host256, int e8m0)
+{
+    if (e8m0 < 0 || e8m0 > 255) return -1;
+    return dump(host256, 4, 256, e8m0);
+}
 
 /* -------------------------------------------------------------- experts */
 int dsv4_gpu_upload_expert(int layer, int expert, const DSV4ExpertW *e)

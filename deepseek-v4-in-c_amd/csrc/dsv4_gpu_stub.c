@@ -75,6 +75,7 @@ int dsv4_gpu_dump_e4m3(float *h) { (void)h; return -1; }
 int dsv4_gpu_dump_e8m0(float *h) { (void)h; return -1; }
 int dsv4_gpu_dump_e2m1(float *h) { (void)h; return -1; }
 int dsv4_gpu_dump_fp4_bytes(float *h) { (void)h; return -1; }
+int dsv4_gpu_dump_e4m3_scaled(float *h, int e8m0) { (void)h; (void)e8m0; return -1; }
 
 int dsv4_gpu_upload_expert(int layer, int expert, const DSV4ExpertW *e)
 { (void)layer; (void)expert; (void)e; return -1; }

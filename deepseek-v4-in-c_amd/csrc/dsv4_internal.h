@@ -32,6 +32,31 @@ int dsv4_fp8_gemv_launch(float *y, const float *x, const uint8_t *W,
                          const void *S, int sfmt, int rows, int cols,
                          int blk_r, int blk_c, hipStream_t st);
 
+/* The matrix-core form of the FP8 GEMV for E8M0-scaled matrices
+ * (dsv4_fp8_mx.hip): one launch of n GEMVs that read x + i * x_stride (or,
+ * listed, n matrices reading the same x), each row's bits those of the
+ * batched form below for the same token. */
+struct Dsv4Fp8Mx {
+    float *y = nullptr;
+    const float *x = nullptr;
+    const uint8_t *w = nullptr, *s = nullptr;
+    int rows = 0, cols = 0, sc = 0, blk_r = 128, blk_c = 128;
+    int n = 1;
+    long long x_stride = 0, y_stride = 0, w_stride = 0, s_stride = 0;
+    int list = 0;
+    const uint8_t *wl[4] = {}, *sl[4] = {};
+    float *yl[4] = {};
+    int rl[4] = {};
+};
+/* The shapes the matrix-core form takes: E8M0 scales (sfmt 0), cols a
+ * multiple of 16 up to 16384, blk_c a multiple of 16. */
+bool dsv4_fp8_mx_ok(int sfmt, int cols, int blk_r, int blk_c);
+int dsv4_fp8_mx_launch(const Dsv4Fp8Mx &a, hipStream_t st);
+/* The batched matrix-core form: y[nt][rows], x[nt][cols]; every (row,
+ * token) has the bits of dsv4_fp8_mx_launch on that token. */
+int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_t *S, int rows,
+                        int cols, int blk_r, int blk_c, int nt, hipStream_t st);
+
 /* MXFP4 GEMV (dsv4_matmul_fp4): W e2m1 nibbles [rows][cols/2], S E8M0 bytes
  * [ceil(rows/blk_r)][ceil(cols/blk_c)]. _ok: the shapes it takes (cols a
  * multiple of 32 up to 16384, blk_c a multiple of 32). Returns 0 / -1. */

@@ -263,6 +263,13 @@ int dsv4_gpu_dump_e4m3(float *host256);
 int dsv4_gpu_dump_e8m0(float *host256);
 int dsv4_gpu_dump_e2m1(float *host16);
 
+/* Device decode of all 256 E4M3FN codes times the E8M0 scale 2^(e8m0 - 127)
+ * the way the matrix-core FP8 form decodes them (into bf16 with the scale
+ * folded in, widened back to f32), for a bit-equality gate against
+ * dsv4_quant.h:74-130: exact while the product stays in bf16's range. No
+ * reference counterpart. */
+int dsv4_gpu_dump_e4m3_scaled(float *host256, int e8m0);
+
 /* Device decode of every packed FP4 byte b = 0..255 into its two elements,
  * out[2b] = even (low nibble), out[2b+1] = odd (high nibble), the order
  * dsv4_fp4_at defines (dsv4_quant.h:155-164). No reference counterpart. */

@@ -47,6 +47,22 @@ def test_decoders_bit_exact(gpu, dsv4):
         assert common.bits_equal(dev[~nan], ref[~nan]), which
 
 
+@pytest.mark.parametrize("e8m0", [127, 120, 134, 100, 150, 119])
+def test_scaled_e4m3_decoder_bit_exact(gpu, dsv4, e8m0):
+    """The matrix-core FP8 form decodes e4m3 codes into bf16 with the E8M0
+    block scale folded in (v_cvt_scalef32_pk_bf16_fp8): all 256 codes times
+    2^(e8m0 - 127) against the reference decoder's value times the scale
+    (exact: 3 mantissa bits fit bf16's 7), NaN codes NaN."""
+    L = dsv4.lib()
+    dev = np.empty(256, np.float32)
+    assert L.dsv4_gpu_dump_e4m3_scaled(dev.ctypes.data, e8m0) == 0
+    ref = (oracle.dump_e4m3().astype(np.float64) * 2.0 ** (e8m0 - 127)).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(dev), nan)
+    assert common.bits_equal(dev[~nan], ref[~nan])
+    assert L.dsv4_gpu_dump_e4m3_scaled(dev.ctypes.data, 256) == -1
+
+
 def test_fp4_byte_order_bit_exact(gpu, dsv4):
     dev = dsv4.dump("fp4_bytes").reshape(256, 2)
     tab = oracle.dump_e2m1()
@@ -98,14 +114,18 @@ def test_c1_4096(gpu, dsv4):
     check_shape(dsv4, 4096, 4096, 1, continuous=True)
 
 
+@pytest.mark.parametrize("scales", ["f32", "e8m0"])
 @pytest.mark.parametrize("rows,cols", [(1536, 7168), (576, 7168), (24576, 1536),
                                        (7168, 16384), (7168, 7168)])
-def test_c2_trunk_shapes(gpu, dsv4, rows, cols):
-    check_shape(dsv4, rows, cols, 0)
+def test_c2_trunk_shapes(gpu, dsv4, rows, cols, scales):
+    """fp32 block scales (the configuration's, VALU form) and E8M0 ones (the
+    reference's, matrix-core form)."""
+    check_shape(dsv4, rows, cols, 0, f32s=scales == "f32")
 
 
-def test_c2_lm_head(gpu, dsv4):
-    check_shape(dsv4, 129280, 7168, 0)
+@pytest.mark.parametrize("scales", ["f32", "e8m0"])
+def test_c2_lm_head(gpu, dsv4, scales):
+    check_shape(dsv4, 129280, 7168, 0, f32s=scales == "f32")
 
 
 @pytest.mark.parametrize("rows,cols", [(1, 16), (3, 48), (130, 96), (257, 1040),
@@ -168,10 +188,17 @@ def test_reference_gpu_gate(gpu, dsv4):
 
 
 @pytest.mark.parametrize("rows,cols,nt", [(300, 1536, 5), (129, 7168, 64), (40, 64, 3),
-                                          (500, 2048, 13), (70, 16384, 2), (33, 4096, 9)])
+                                          (500, 2048, 13), (70, 16384, 2), (33, 4096, 9),
+                                          (7168, 7168, 64), (77, 1040, 21), (16, 112, 6),
+                                          (1000, 7168, 11), (257, 2096, 20), (64, 16, 4),
+                                          (200, 4096, 33), (18, 3072, 7)])
 def test_batched_bit_identical(gpu, dsv4, rows, cols, nt):
-    """Token blocks of 8, 4 and 2 in LDS, ragged last blocks included: every
-    token's row equals the single-token GEMV's bits."""
+    """E8M0 scales: the matrix-core form, whose batched kernel runs the
+    single-token chain per (row, token) -- every token's row equals the
+    single-token GEMV's bits, whatever column of which tile it takes (up to
+    64 tokens, ragged row tiles, columns not a multiple of the 256-byte unit
+    or of the 1024-column segment); cols not a multiple of 16 take the VALU
+    form, whose batched kernel keeps its bits the same way."""
     W, Sf, Se, _ = common.fp8_problem(21, rows, cols)
     x = np.random.default_rng(22).standard_normal((nt, cols), dtype=np.float32)
     y1, m = _run(dsv4, W, Se, x[0])
@@ -179,6 +206,41 @@ def test_batched_bit_identical(gpu, dsv4, rows, cols, nt):
     for t in range(nt):
         assert common.bits_equal(yn[t], dsv4.mmq(m, x[t])), t
     assert common.vec_rel_err(yn, oracle.matmul_fp8(x, W, Se)) < TOL
+
+
+@pytest.mark.parametrize("blk_r,blk_c", [(1, 32), (16, 64), (128, 128), (4, 48), (256, 256)])
+def test_matrix_core_form_blockings(gpu, dsv4, blk_r, blk_c):
+    """E8M0 scale grids other than 128 x 128 (a scale per lane piece in the
+    matrix-core form): against the oracle, and batched bit-identical."""
+    rows, cols, nt = 300, 1536, 7
+    rng = np.random.default_rng(blk_r * 1000 + blk_c)
+    W = common.fp8_codes(rng, (rows, cols))
+    S = (127 + rng.integers(-8, -3, size=((rows + blk_r - 1) // blk_r,
+                                           (cols + blk_c - 1) // blk_c))).astype(np.uint8)
+    x = rng.standard_normal((nt, cols), dtype=np.float32)
+    y, m = _run(dsv4, W, S, x[0], blk_r=blk_r, blk_c=blk_c)
+    assert common.vec_rel_err(y, oracle.matmul_fp8(x[0], W, S, blk_r, blk_c)) < TOL
+    yn = dsv4.mmq_n(m, x)
+    for t in range(nt):
+        assert common.bits_equal(yn[t], dsv4.mmq(m, x[t])), t
+
+
+@pytest.mark.parametrize("form", ["1", "0"])
+def test_e8m0_forms(gpu, dsv4, monkeypatch, form):
+    """DSV4_GPU_FP8_MX=1 (the default: matrix core for E8M0 scales) and =0
+    (the VALU form for every matrix): each within the bar, each with its own
+    batched kernel bit-identical per token."""
+    monkeypatch.setenv("DSV4_GPU_FP8_MX", form)
+    rows, cols, nt = 1000, 7168, 6
+    W, Sf, Se, _ = common.fp8_problem(71, rows, cols)
+    x = np.random.default_rng(72).standard_normal((nt, cols), dtype=np.float32)
+    y, m = _run(dsv4, W, Se, x[0])
+    want = oracle.matmul_fp8(x, W, Se)
+    assert common.vec_rel_err(y, want[0]) < TOL
+    yn = dsv4.mmq_n(m, x)
+    for t in range(nt):
+        assert common.bits_equal(yn[t], dsv4.mmq(m, x[t])), t
+    assert common.vec_rel_err(yn, want) < TOL
 
 
 @pytest.mark.parametrize("rows,cols", [(7168, 7168), (1536, 1536), (300, 4096), (260, 16384)])

@@ -27,19 +27,23 @@
  *   lane (row r, group g) takes the 16 bytes [64 q + 16 g, +16) of quarter
  *   q, the first 8 for step (q, 0) and the last 8 for step (q, 1); B is read
  *   in the same order.
- * The single-token kernel spreads a 16-row tile's segments over the waves of
- * a workgroup (so short matrices still fill the machine) and adds the
- * segment partials through LDS; the batched kernel walks the segments in
- * order inside one wave and keeps the running sum in registers. Matrix-core
- * columns are computed independently, so where a token sits among the
- * columns does not change its bits; the tests check every case bit for bit.
+ * The single-token kernel spreads a 16-row tile's segments over up to 8
+ * waves (so short matrices still fill the machine); the first of them keeps
+ * the running sum in registers and continues it over the others' partials
+ * from LDS. The batched kernel walks the segments in order inside one wave.
+ * Matrix-core columns are computed independently, so where a token sits
+ * among the columns does not change its bits; the tests check every case
+ * bit for bit.
  *
  * MEMORY: weights stream in units of 16 rows x 256 bytes, loaded as four
  * 4-row x 256-byte requests per wave (fully coalesced), staged through a
  * wave-private LDS buffer into the matrix core's operand order (the layout
- * dsv4_moe_mx.hip measured fastest on MI355X). The single-token kernel
- * requests every weight unit of its segment before it stages x, so the
- * whole matrix is in flight from the first microsecond.
+ * dsv4_moe_mx.hip measured fastest on MI355X). The single-token kernel is
+ * persistent: each wave keeps one segment (16 KB) in flight ahead of the
+ * one it computes, across tiles, and its workgroup turns x into terms once.
+ * The memory counter is in order, so every kernel issues what it waits for
+ * first (x, then the weights in K order) and keeps every load outside
+ * branches; register arrays are indexed by compile-time constants only.
  */
 #include "dsv4_dev.h"
 #include "dsv4_internal.h"
@@ -99,19 +103,50 @@ __device__ __forceinline__ void wave_lds_sync()
 }
 
 /* One unit of a 16-row tile in flight: lane l holds row 4 q + l / 16, bytes
- * [16 (l % 16), +16) of the unit, for q = 0..3. */
+ * [16 (l % 16), +16) of the unit, for q = 0..3. With per-lane scales (UNI
+ * false) also the E8M0 bytes of the four pieces the lane will decode (row
+ * l % 16, columns 64 q + 16 (l / 16) of the unit), loaded with the weights so
+ * that they arrive together. With uniform scales (blk_r a multiple of 16 and
+ * blk_c of 64: every row of a tile and every lane share each quarter's
+ * scale) the scales travel once per segment instead (xs_seg). */
+template <bool UNI>
 struct XUnit {
     u32x4 w[4];
+    uint32_t sb[UNI ? 1 : 4];
 };
+
+/* k / blk_c for 0 <= k < 2^16 and 16 <= blk_c <= 2^16, with m = ceil(2^32 /
+ * blk_c): m blk_c - 2^32 = e < blk_c, so k m / 2^32 = k / blk_c + k e /
+ * (blk_c 2^32), and the added k e / (blk_c 2^32) < 1 / blk_c never carries
+ * the quotient past an integer. */
+__device__ __forceinline__ int div_bc(int k, uint32_t m)
+{
+    return (int)__umulhi((uint32_t)k, m);
+}
+
+inline uint32_t bc_magic(int blk_c)
+{
+    return (uint32_t)((((uint64_t)1 << 32) + (uint64_t)blk_c - 1) / (uint64_t)blk_c);
+}
 
 /* Unit u of the tile whose row 0 is W + row0 * cols (rows past `rows` read
  * the last row, pieces past `cols` the row's first piece: their results are
- * discarded or zeroed). */
-__device__ __forceinline__ void xu_load(XUnit &U, const uint8_t *W, int row0, int rows,
-                                        int cols, int k0, int lane)
+ * discarded or zeroed). srow: this lane's scale row offset, (row / blk_r) sc
+ * for its A row, row0 + lane % 16 clamped to the last row. */
+template <bool UNI>
+__device__ __forceinline__ void xu_load(XUnit<UNI> &U, const uint8_t *W, const uint8_t *S,
+                                        int srow, uint32_t bc_m, int row0, int rows, int cols,
+                                        int k0, int lane)
 {
     const int c = k0 + 16 * (lane & 15);
     const int cc = c < cols ? c : 0;
+    if (!UNI) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int k = min(k0 + 64 * q + 16 * (lane >> 4), cols - 1);
+            U.sb[UNI ? 0 : q] = ldg8(S + srow + div_bc(k, bc_m));
+        }
+    }
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         const int r = min(row0 + 4 * q + (lane >> 4), rows - 1);
@@ -119,119 +154,117 @@ __device__ __forceinline__ void xu_load(XUnit &U, const uint8_t *W, int row0, in
     }
 }
 
-__device__ __forceinline__ void xu_stage(unsigned char *buf, const XUnit &U, int lane)
+/* Uniform scales: the E8M0 bytes of the 16 quarters of the segment at k0
+ * (quarter m = 4 unit + q in lane m % 16; srow is the tile's scale row
+ * offset). xs_get reads quarter m's byte back from its lane. */
+__device__ __forceinline__ uint32_t xs_seg(const uint8_t *S, int srow, uint32_t bc_m, int k0,
+                                           int cols, int lane)
+{
+    return ldg8(S + srow + div_bc(min(k0 + 64 * (lane & 15), cols - 1), bc_m));
+}
+
+__device__ __forceinline__ uint32_t xs_get(uint32_t ssb, int m)
+{
+    return (uint32_t)__builtin_amdgcn_readlane((int)ssb, m);
+}
+
+template <bool UNI>
+__device__ __forceinline__ void xu_stage(unsigned char *buf, const XUnit<UNI> &U, int lane)
 {
 #pragma unroll
     for (int q = 0; q < 4; q++)
         *reinterpret_cast<u32x4 *>(buf + (4 * q + (lane >> 4)) * XWP + 16 * (lane & 15)) = U.w[q];
 }
 
-/* The block scale of lane (row r, group g)'s piece of quarter q of the unit
- * at column k0, as the f32 2^(b - 127) (0 for a piece past the row's end:
- * its codes are then treated as zeros). */
-__device__ __forceinline__ float xu_scale(const uint8_t *S, int sc, int blk_r, int blk_c,
-                                          int row, int k, int cols)
-{
-    if (k >= cols) return 0.0f;
-    return dec_e8m0(S[(size_t)(row / blk_r) * sc + k / blk_c]);
-}
-
 /* The A operands of quarter q for this lane: steps (q, 0) and (q, 1). A piece
- * past the row's end is zero (its codes are replaced, not scaled: a NaN code
- * times 0 would still be NaN). */
-__device__ __forceinline__ void xu_frags(v8bf *a, const unsigned char *buf, int q, float s,
+ * past the row's end is zero (its codes are replaced and its scale is 0: a
+ * NaN code times 0 would still be NaN). */
+__device__ __forceinline__ void xu_frags(v8bf *a, const unsigned char *buf, int q, uint32_t sb,
                                          bool live, int lane)
 {
     const u32x4 v = *reinterpret_cast<const u32x4 *>(buf + (lane & 15) * XWP + 64 * q +
                                                       16 * (lane >> 4));
     const u32x4 z = live ? v : u32x4{0u, 0u, 0u, 0u};
+    const float s = live ? dec_e8m0(sb) : 0.0f;
     a[0] = fp8x8_bf16(z.x, z.y, s);
     a[1] = fp8x8_bf16(z.z, z.w, s);
 }
 
 /* ------------------------------------------------------ single token */
 
-/* LDS of one wave of the single-token kernel: its segment's x terms (three
- * planes of XPL bf16), then its unit buffer. */
-constexpr int X1_WAVE_B = XNT * XPL * 2 + XUNIT_B;
-
-/* x[k0 .. k0 + XSEG) as three bf16 term planes in the wave's LDS, zeros past
- * cols. Each lane takes 16 consecutive values. */
-__device__ __forceinline__ void x1_stage(uint16_t *pl, const float *x, int k0, int cols,
-                                         int lane)
+/* One segment of a tile for a single token: units j = 0..nu-1 of the
+ * segment at column k0, held in P4[j], staged through the wave's buffer and
+ * run through the matrix core in order (accumulator from zero). With PF each
+ * slot, once staged, is refilled with unit j of the next job (the segment at
+ * k0n of the tile at row0n; slots past its nun units repeat its last unit).
+ * Returns the segment's accumulator (D layout). */
+template <bool UNI, bool PF>
+__device__ __forceinline__ v4f mx1_seg(XUnit<UNI> (&P4)[XSEG_U], unsigned char *buf,
+                                       const uint16_t *pl, int bplane, const uint8_t *W,
+                                       const uint8_t *S, int rows, int cols, uint32_t bc_m,
+                                       int k0, int nu, uint32_t ssb, int row0n, int srown,
+                                       int k0n, int nun, int lane)
 {
-    f32x4 v[4];
-    const int c0 = k0 + 16 * lane;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int c = c0 + 4 * j;
-        v[j] = c < cols ? *(const DSV4_GLOBAL f32x4 *)(x + c) : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-        uint32_t t[4][XNT];
-#pragma unroll
-        for (int i = 0; i < 4; i++) terms3(e[i], t[i]);
-#pragma unroll
-        for (int p = 0; p < XNT; p++) {
-            const uint32_t lo = t[0][p] | (t[1][p] << 16), hi = t[2][p] | (t[3][p] << 16);
-            *reinterpret_cast<uint2 *>(pl + p * XPL + 16 * lane + 4 * j) = uint2{lo, hi};
-        }
-    }
-}
-
-/* The segment chain of one 16-row tile for a single token: units in flight
- * D deep in VGPRs, staged through the wave's buffer, 8 matrix-core steps per
- * unit. Returns the accumulator (D layout). */
-template <int D>
-__device__ __forceinline__ v4f x1_segment(const uint8_t *W, const uint8_t *S, int row0,
-                                          int rows, int cols, int sc, int blk_r, int blk_c,
-                                          int k0, int nu, const uint16_t *pl,
-                                          unsigned char *buf, XUnit *P, int lane)
-{
+    const int g = lane >> 4;
     v4f acc = {0.f, 0.f, 0.f, 0.f};
-    const int r = lane & 15, g = lane >> 4;
-    const int row = min(row0 + r, rows - 1);
-    const int col = lane & 15;                          /* B column: term plane */
-    for (int u = 0; u < nu; u++) {
-        wave_lds_sync();                      /* the previous unit's reads, x's terms */
-        xu_stage(buf, P[u % D], lane);
-        if (u + D < nu) xu_load(P[u % D], W, row0, rows, cols, k0 + XU * (u + D), lane);
-        wave_lds_sync();
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int k = k0 + XU * u + 64 * q + 16 * g;
-            const float s = xu_scale(S, sc, blk_r, blk_c, row, k, cols);
-            v8bf a[2];
-            xu_frags(a, buf, q, s, k < cols, lane);
+    for (int j = 0; j < XSEG_U; j++) {
+        if (j < nu) {
+            wave_lds_sync();                           /* the previous unit's reads */
+            xu_stage(buf, P4[j], lane);
+        }
+        uint32_t sbj[4];
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                u32x4 bw = {0u, 0u, 0u, 0u};
-                if (col < XNT)
-                    bw = *reinterpret_cast<const u32x4 *>(pl + col * XPL + XU * u + 64 * q +
-                                                          16 * g + 8 * h);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[h], __builtin_bit_cast(v8bf, bw),
-                                                              acc, 0, 0, 0);
+        for (int q = 0; q < 4; q++) sbj[q] = UNI ? 0u : P4[j].sb[UNI ? 0 : q];
+        if (PF) {
+            __builtin_amdgcn_sched_barrier(0);
+            xu_load(P4[j], W, S, srown, bc_m, row0n, rows, cols, k0n + XU * min(j, nun - 1),
+                    lane);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (j < nu) {
+            wave_lds_sync();
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int k = k0 + XU * j + 64 * q + 16 * g;
+                v8bf af[2];
+                xu_frags(af, buf, q, UNI ? xs_get(ssb, 4 * j + q) : sbj[q], k < cols, lane);
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const u32x4 bw = *reinterpret_cast<const u32x4 *>(
+                        pl + bplane + k0 + XU * j + 64 * q + 16 * g + 8 * h);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        af[h], __builtin_bit_cast(v8bf, bw), acc, 0, 0, 0);
+                }
             }
         }
     }
     return acc;
 }
 
-/* One workgroup per 16-row tile (blockIdx.x), one group of the launch per
- * blockIdx.y (lists: several matrices reading the same x; strided groups:
- * wo_a's slices). Wave w takes segments w, w + nw, ...; it requests its
- * segment's weight units first, then stages the segment's x terms, then
- * streams. The segment partials (per row and term column) meet in LDS and
- * are added in segment order. */
-template <int D>
-__global__ void __launch_bounds__(512)
+/* Persistent single-token kernel. A tile's segments are split over P waves
+ * (wave p takes segments [p spw, (p + 1) spw)); a workgroup holds TPW tiles
+ * of P waves and walks tile groups blockIdx.x, + gridDim.x, ... Each wave
+ * streams its segments one segment ahead: while it runs unit j of a segment,
+ * units j+1..3 of it and 0..j of its next segment (the next tile's first, at
+ * a tile's end) are in flight. The workgroup turns x into bf16 terms in LDS
+ * once (three planes of xp bf16, zeros past cols). Wave 0 of a tile (whose
+ * segments start at 0) chains its segment partials in registers and, after
+ * a barrier, continues the chain over the other waves' partials from LDS in
+ * segment order: the arithmetic of every (row, term column) is the segment
+ * chain whatever P is. Every register array is indexed by compile-time
+ * constants (a run-time index would put it in scratch memory). */
+constexpr int X1_XM = 8;                    /* x pieces (f32x4) per thread */
+
+template <bool UNI>
+__global__ void __launch_bounds__(512, UNI ? 4 : 2)   /* uniform: two 8-wave groups per CU */
 k_fp8_mx1(Dsv4Fp8Mx a)
 {
     extern __shared__ __attribute__((aligned(16))) unsigned char x1lds[];
-    __shared__ float part[XSEG_MAX][16][XNT];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    /* the wave index through readfirstlane: everything per wave (tile, row,
+     * segment, scale row) is then scalar and takes no vector registers */
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int nw = blockDim.x >> 6;
     const int gi = blockIdx.y;
     const float *x = a.x + (size_t)gi * a.x_stride;
@@ -240,97 +273,218 @@ k_fp8_mx1(Dsv4Fp8Mx a)
     float *y = a.list ? a.yl[gi] : a.y + (size_t)gi * a.y_stride;
     const int rows = a.list ? a.rl[gi] : a.rows;
     const int cols = a.cols;
-    const int row0 = blockIdx.x * 16;
-    if (row0 >= rows) return;                          /* the whole workgroup */
-    const int nseg = (cols + XSEG - 1) / XSEG;
-    uint16_t *pl = (uint16_t *)(x1lds + (size_t)w * X1_WAVE_B);
-    unsigned char *buf = x1lds + (size_t)w * X1_WAVE_B + XNT * XPL * 2;
-    for (int seg = w; seg < nseg; seg += nw) {
-        const int k0 = seg * XSEG;
-        const int nu = min(XSEG_U, (cols - k0 + XU - 1) / XU);
-        XUnit P[D];
+    const int ntiles = (rows + 15) / 16;
+    const int ngrp = (ntiles + a.tpw - 1) / a.tpw;
+    if ((int)blockIdx.x >= ngrp) return;               /* the whole workgroup */
+    const int nseg = (cols + XSEG - 1) / XSEG, nu_all = (cols + XU - 1) / XU;
+    const int P = a.wpt, tw = w / P, p = w - tw * P;
+    const int sa = p * a.spw, sb = min(nseg, sa + a.spw);
+    const int xp = a.xp;
+    uint16_t *pl = (uint16_t *)x1lds;                              /* [3][xp] */
+    unsigned char *buf = x1lds + (size_t)XNT * xp * 2 + (size_t)w * XUNIT_B;
+    /* part: per tile slot, a.npb buffers of the segments past wave 0's
+     * ([nseg - spw][16][XNT] floats): two when the workgroup walks more
+     * than one tile group (a tile's partials must not overwrite the ones
+     * wave 0 is still reading), else one */
+    float *part = (float *)(x1lds + (size_t)XNT * xp * 2 + (size_t)nw * XUNIT_B);
+    const int part_n = (nseg - a.spw) * 16 * XNT;
+    float *mypart = part + (size_t)tw * a.npb * part_n;
+    const int g = lane >> 4, col = lane & 15;
+    /* B columns 3..15 read plane col % 3 too: those columns of the result
+     * are never used, and unconditional reads keep the steps branch-free */
+    const int bplane = (col % XNT) * xp;
+
+    /* x first (the memory counter is in order: waiting for x then leaves
+     * the weights in flight): piece i = tid + nthreads m of the padded row */
+    f32x4 xv[X1_XM];
+    const int npc = nu_all * (XU / 4);                 /* pieces incl. padding */
 #pragma unroll
-        for (int j = 0; j < D; j++)
-            xu_load(P[j], W, row0, rows, cols, k0 + XU * min(j, nu - 1), lane);
-        x1_stage(pl, x, k0, cols, lane);
-        const v4f acc = x1_segment<D>(W, S, row0, rows, cols, a.sc, a.blk_r, a.blk_c, k0, nu,
-                                      pl, buf, P, lane);
-        const int col = lane & 15;
-        if (col < XNT) {
+    for (int m = 0; m < X1_XM; m++) {
+        const int c = 4 * ((int)threadIdx.x + (int)blockDim.x * m);
+        xv[m] = *(const DSV4_GLOBAL f32x4 *)(x + (c < cols ? c : 0));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    /* the first job: tile group blockIdx.x, segment sa */
+    int it = blockIdx.x, s = sa;
+    int row0 = min(it * a.tpw + tw, ntiles - 1) * 16;
+    int srow = ((UNI ? row0 : min(row0 + col, rows - 1)) / a.blk_r) * a.sc;
+    uint32_t ssb = UNI ? xs_seg(S, srow, a.bc_m, s * XSEG, cols, lane) : 0u;
+    XUnit<UNI> P4[XSEG_U];
+    {
+        const int nu0 = min(XSEG_U, nu_all - s * XSEG_U);
 #pragma unroll
-            for (int j = 0; j < 4; j++) part[seg][4 * (lane >> 4) + j][col] = acc[j];
+        for (int j = 0; j < XSEG_U; j++)
+            xu_load(P4[j], W, S, srow, a.bc_m, row0, rows, cols, s * XSEG + XU * min(j, nu0 - 1),
+                    lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < X1_XM; m++) {
+        const int i = (int)threadIdx.x + (int)blockDim.x * m;
+        if (i < npc) {
+            const bool in = 4 * i < cols;
+            const float e[4] = {in ? xv[m].x : 0.f, in ? xv[m].y : 0.f, in ? xv[m].z : 0.f,
+                                in ? xv[m].w : 0.f};
+            uint32_t t[4][XNT];
+#pragma unroll
+            for (int k = 0; k < 4; k++) terms3(e[k], t[k]);
+#pragma unroll
+            for (int q = 0; q < XNT; q++)
+                *reinterpret_cast<uint2 *>(pl + q * xp + 4 * i) =
+                    uint2{t[0][q] | (t[1][q] << 16), t[2][q] | (t[3][q] << 16)};
         }
     }
     __syncthreads();
-    if ((int)threadIdx.x < 16 && row0 + (int)threadIdx.x < rows) {
-        float c[XNT];
+
+    int pb = 0;                                        /* part buffer of this tile */
+    v4f tot = {0.f, 0.f, 0.f, 0.f};
+    /* the end of segment s of the current tile: wave 0 of the tile chains
+     * it, the others keep it for wave 0; at the tile's end wave 0 continues
+     * the chain over theirs and writes y = (hi + mid) + lo */
+    auto finish = [&](const v4f &acc, bool tile_end) {
+        if (p == 0) {
+            tot = s == 0 ? acc : tot + acc;
+        } else if (col < XNT) {
 #pragma unroll
-        for (int t = 0; t < XNT; t++) c[t] = part[0][threadIdx.x][t];
-        for (int s = 1; s < nseg; s++)
+            for (int jj = 0; jj < 4; jj++)
+                mypart[(size_t)pb * part_n + ((s - a.spw) * 16 + 4 * g + jj) * XNT + col] = acc[jj];
+        }
+        if (!tile_end) return;
+        if (P > 1) __syncthreads();
+        if (p == 0) {
+            for (int s2 = sb; s2 < nseg; s2++) {
 #pragma unroll
-            for (int t = 0; t < XNT; t++) c[t] = c[t] + part[s][threadIdx.x][t];
-        y[row0 + threadIdx.x] = (c[0] + c[1]) + c[2];
+                for (int jj = 0; jj < 4; jj++)
+                    tot[jj] = tot[jj] + mypart[(size_t)pb * part_n +
+                                               ((s2 - a.spw) * 16 + 4 * g + jj) * XNT + col % XNT];
+            }
+            const bool live = it * a.tpw + tw < ntiles;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const float c1 = __shfl(tot[jj], min(lane + 1, 63), 64);
+                const float c2 = __shfl(tot[jj], min(lane + 2, 63), 64);
+                const int rr = row0 + 4 * g + jj;
+                if (live && col == 0 && rr < rows) y[rr] = (tot[jj] + c1) + c2;
+            }
+        }
+        pb = a.npb - 1 - pb;
+    };
+    /* every job but the wave's last prefetches the next one; the last runs
+     * after the loop, without loads (the loop is left before any load of
+     * its iteration, so no wait after it has to allow for loads that might
+     * not have been issued) */
+    for (;;) {
+        int itn = it, sn = s + 1;
+        if (sn == sb) { sn = sa; itn = it + gridDim.x; }
+        if (itn >= ngrp) break;
+        const int tilen = min(itn * a.tpw + tw, ntiles - 1);
+        const int row0n = tilen * 16;
+        const int srown = ((UNI ? row0n : min(row0n + col, rows - 1)) / a.blk_r) * a.sc;
+        const int k0n = sn * XSEG, nun = min(XSEG_U, nu_all - sn * XSEG_U);
+        const uint32_t ssn = UNI ? xs_seg(S, srown, a.bc_m, k0n, cols, lane) : 0u;
+        const v4f acc = mx1_seg<UNI, true>(P4, buf, pl, bplane, W, S, rows, cols, a.bc_m,
+                                           s * XSEG, min(XSEG_U, nu_all - s * XSEG_U), ssb,
+                                           row0n, srown, k0n, nun, lane);
+        finish(acc, sn == sa);
+        it = itn; s = sn; row0 = row0n; ssb = ssn;
     }
+    const v4f acc = mx1_seg<UNI, false>(P4, buf, pl, bplane, W, S, rows, cols, a.bc_m, s * XSEG,
+                                        min(XSEG_U, nu_all - s * XSEG_U), ssb, 0, 0, 0, 1, lane);
+    finish(acc, true);
 }
 
 /* ------------------------------------------------------------ batched */
 
-/* x[t][kc .. kc + XU) of the group's tokens as term rows in LDS:
- * bl[(tok * XNT + term) * BP + k], BP = XU + 8; zeros past cols and past
- * the group's tokens. The workgroup's threads share the work. */
+/* x terms of a group's tokens for one unit's 256 columns, in LDS as term
+ * rows: bl[(tok * XNT + term) * BP + k], BP = XU + 8. */
 constexpr int BP = XU + 8;
+constexpr int MW = 4;                       /* waves (16-row tiles) per workgroup */
 
-__device__ __forceinline__ void xn_stage(uint16_t *bl, const float *x, int t0, int ntok, int nt,
-                                         int kc, int cols, int tpg)
+/* f32x4 pieces of x per thread per unit: a group holds at most XTOK * NT
+ * tokens of XU / 4 pieces, spread over the workgroup's 64 MW threads. */
+template <int NT>
+struct XnDim {
+    static constexpr int M = (XTOK * NT * (XU / 4) + 64 * MW - 1) / (64 * MW);
+};
+
+/* Request piece i = tid + 64 MW m of the unit at column kc. Pieces past the
+ * group's tokens or past cols read the group's first piece (unconditional
+ * loads: no branch for the weight requests to wait behind) and become zeros
+ * in xn_terms. */
+template <int NT>
+__device__ __forceinline__ void xn_load(f32x4 *v, const float *x, int t0, int ntok, int kc,
+                                        int cols, int tpg)
 {
-    const int per = XU / 4;                              /* f32x4 pieces per token */
-    const int total = tpg * per;
-    for (int i = threadIdx.x; i < total; i += blockDim.x) {
-        const int tk = i / per, c4 = i - tk * per;
-        const int c = kc + 4 * c4;
-        const int t = t0 + tk;
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        if (tk < ntok && t < nt && c < cols)
-            v = *(const DSV4_GLOBAL f32x4 *)(x + (size_t)t * cols + c);
-        const float e[4] = {v.x, v.y, v.z, v.w};
-        uint32_t tt[4][XNT];
 #pragma unroll
-        for (int j = 0; j < 4; j++) terms3(e[j], tt[j]);
+    for (int m = 0; m < XnDim<NT>::M; m++) {
+        const int i = (int)threadIdx.x + 64 * MW * m;
+        const int tk = i / (XU / 4), c = kc + 4 * (i % (XU / 4));
+        const bool in = i < tpg * (XU / 4) && tk < ntok && c < cols;
+        v[m] = *(const DSV4_GLOBAL f32x4 *)(x + (in ? (size_t)(t0 + tk) * cols + c
+                                                   : (size_t)t0 * cols));
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void xn_terms(uint16_t *bl, const f32x4 *v, int ntok, int kc,
+                                         int cols, int tpg)
+{
 #pragma unroll
-        for (int p = 0; p < XNT; p++)
-            *reinterpret_cast<uint2 *>(bl + (size_t)(tk * XNT + p) * BP + 4 * c4) =
-                uint2{tt[0][p] | (tt[1][p] << 16), tt[2][p] | (tt[3][p] << 16)};
+    for (int m = 0; m < XnDim<NT>::M; m++) {
+        const int i = (int)threadIdx.x + 64 * MW * m;
+        if (i < tpg * (XU / 4)) {
+            const int tk = i / (XU / 4), c4 = i % (XU / 4);
+            const bool in = tk < ntok && kc + 4 * c4 < cols;
+            const float e[4] = {in ? v[m].x : 0.f, in ? v[m].y : 0.f, in ? v[m].z : 0.f,
+                                in ? v[m].w : 0.f};
+            uint32_t tt[4][XNT];
+#pragma unroll
+            for (int j = 0; j < 4; j++) terms3(e[j], tt[j]);
+#pragma unroll
+            for (int p = 0; p < XNT; p++)
+                *reinterpret_cast<uint2 *>(bl + (size_t)(tk * XNT + p) * BP + 4 * c4) =
+                    uint2{tt[0][p] | (tt[1][p] << 16), tt[2][p] | (tt[3][p] << 16)};
+        }
     }
 }
 
 /* Workgroup (blockIdx.x: MW 16-row tiles, one per wave; blockIdx.y: a group
- * of tpg tokens starting at t0). Per unit: the workgroup stages the group's x
- * terms for the unit's 256 columns, every wave runs its tile's 8 steps x NT
- * column tiles from its own staged unit, and at the end of each segment the
- * segment's accumulators join the running sums in segment order. */
-template <int NT, int D>
-__global__ void __launch_bounds__(256)
+ * of tpg tokens starting at t0). Per unit u: the workgroup turns x(u), which
+ * it requested one unit earlier, into terms in B buffer u % 2, each wave
+ * stages its weight unit u (requested two units earlier), requests x(u + 1)
+ * and weight unit u + 2, and after one barrier runs its tile's 8 steps x NT
+ * column tiles. At each segment's end the segment's accumulators join the
+ * running sums in segment order. Every register array is indexed by
+ * compile-time constants: the unit loop is unrolled by a segment's 4. */
+template <int NT, bool UNI>
+__global__ void __launch_bounds__(64 * MW)
 k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__restrict__ W,
-          const uint8_t *__restrict__ S, int rows, int cols, int sc, int blk_r, int blk_c,
+          const uint8_t *__restrict__ S, int rows, int cols, int sc, int blk_r, uint32_t bc_m,
           int nt, int tpg)
 {
     extern __shared__ __attribute__((aligned(16))) unsigned char xnlds[];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int nw = blockDim.x >> 6;
-    uint16_t *bl = (uint16_t *)xnlds;                    /* [tpg * 3][BP] */
-    unsigned char *buf = xnlds + (size_t)tpg * XNT * BP * 2 + (size_t)w * XUNIT_B;
-    const int row0 = (blockIdx.x * nw + w) * 16;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const size_t bl_n = (size_t)tpg * XNT * BP;           /* bf16 per B buffer */
+    uint16_t *const bl0 = (uint16_t *)xnlds, *const bl1 = bl0 + bl_n;
+    unsigned char *buf = xnlds + 4 * bl_n + (size_t)w * XUNIT_B;
+    const int row0 = (blockIdx.x * MW + w) * 16;
     const int t0 = blockIdx.y * tpg;
     const int ntok = min(tpg, nt - t0);
-    const int r = lane & 15, g = lane >> 4;
-    const int row = min(row0 + r, rows - 1);
-    const int col = lane & 15;
-    /* this lane's B row per column tile: token 5 n + col / 3, term col % 3 */
+    const int g = lane >> 4, col = lane & 15;
+    const bool live = row0 < rows;
+    const int wrow0 = live ? row0 : 0;
+    const int srow = ((UNI ? wrow0 : min(wrow0 + col, rows - 1)) / blk_r) * sc;
+    /* this lane's B row per column tile: token 5 n + col / 3, term col % 3;
+     * column 15 and columns of tokens past the group read row 0 (their
+     * results are never used; unconditional reads keep the steps
+     * branch-free) */
     int boff[NT];
 #pragma unroll
     for (int n = 0; n < NT; n++) {
         const int tk = XTOK * n + col / XNT;
-        boff[n] = (col < XNT * XTOK && tk < ntok) ? (tk * XNT + col % XNT) * BP : -1;
+        boff[n] = (col < XNT * XTOK && tk < ntok) ? (tk * XNT + col % XNT) * BP : 0;
     }
     v4f acc[NT], tot[NT];
 #pragma unroll
@@ -338,47 +492,68 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
         acc[n] = v4f{0.f, 0.f, 0.f, 0.f};
         tot[n] = v4f{0.f, 0.f, 0.f, 0.f};
     }
-    const int nu_all = (cols + XU - 1) / XU;
-    const bool live = row0 < rows;
-    XUnit P[D];
+    const int nu = (cols + XU - 1) / XU;
+    f32x4 XR[2][XnDim<NT>::M];
+    XUnit<UNI> P[2];
+    xn_load<NT>(XR[0], x, t0, ntok, 0, cols, tpg);
+    /* uniform scales: the current segment's (ssb) and the next one's */
+    uint32_t ssb = UNI ? xs_seg(S, srow, bc_m, 0, cols, lane) : 0u, ssn = 0u;
+    __builtin_amdgcn_sched_barrier(0);
+    xu_load(P[0], W, S, srow, bc_m, wrow0, rows, cols, 0, lane);
+    xu_load(P[1], W, S, srow, bc_m, wrow0, rows, cols, XU * min(1, nu - 1), lane);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int s0 = 0; s0 < nu; s0 += XSEG_U) {
 #pragma unroll
-    for (int j = 0; j < D; j++)
-        xu_load(P[j], W, live ? row0 : 0, rows, cols, XU * min(j, nu_all - 1), lane);
-    for (int u = 0; u < nu_all; u++) {
-        __syncthreads();                                /* the previous unit's B reads */
-        xn_stage(bl, x, t0, ntok, nt, XU * u, cols, tpg);
-        xu_stage(buf, P[u % D], lane);
-        if (u + D < nu_all)
-            xu_load(P[u % D], W, live ? row0 : 0, rows, cols, XU * (u + D), lane);
-        __syncthreads();
+        for (int j = 0; j < XSEG_U; j++) {
+            const int u = s0 + j;
+            uint16_t *bl = (j & 1) ? bl1 : bl0;
+            if (u < nu) {
+                xn_terms<NT>(bl, XR[j & 1], ntok, XU * u, cols, tpg);
+                xu_stage(buf, P[j & 1], lane);
+            }
+            uint32_t sb[4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int k = XU * u + 64 * q + 16 * g;
-            const float s = xu_scale(S, sc, blk_r, blk_c, row, k, cols);
-            v8bf a[2];
-            xu_frags(a, buf, q, s, k < cols, lane);
+            for (int q = 0; q < 4; q++) sb[q] = UNI ? 0u : P[j & 1].sb[UNI ? 0 : q];
+            /* x(u + 1) before weight unit u + 2, both unconditional (past
+             * the last unit they repeat it, unused): the wait for x(u + 1)
+             * then leaves unit u + 2 in flight, and no load sits in a branch
+             * that would make the waits fall back to waiting for all */
+            __builtin_amdgcn_sched_barrier(0);
+            xn_load<NT>(XR[(j + 1) & 1], x, t0, ntok, XU * min(u + 1, nu - 1), cols, tpg);
+            if (UNI && j == XSEG_U - 2)        /* before the next segment's first unit */
+                ssn = xs_seg(S, srow, bc_m, XU * (min(s0 + XSEG_U, nu - 1) & ~(XSEG_U - 1)),
+                             cols, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            xu_load(P[j & 1], W, S, srow, bc_m, wrow0, rows, cols, XU * min(u + 2, nu - 1),
+                    lane);
+            __builtin_amdgcn_sched_barrier(0);
+            if (u < nu) {
+                __syncthreads();          /* B(u) whole; every wave is past B(u - 2)'s reads */
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
+                for (int q = 0; q < 4; q++) {
+                    const int k = XU * u + 64 * q + 16 * g;
+                    v8bf af[2];
+                    xu_frags(af, buf, q, UNI ? xs_get(ssb, 4 * j + q) : sb[q], k < cols, lane);
 #pragma unroll
-                for (int n = 0; n < NT; n++) {
-                    u32x4 bw = {0u, 0u, 0u, 0u};
-                    if (boff[n] >= 0)
-                        bw = *reinterpret_cast<const u32x4 *>(bl + boff[n] + 64 * q + 16 * g +
-                                                              8 * h);
-                    acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        a[h], __builtin_bit_cast(v8bf, bw), acc[n], 0, 0, 0);
+                    for (int h = 0; h < 2; h++) {
+#pragma unroll
+                        for (int n = 0; n < NT; n++) {
+                            const u32x4 bw = *reinterpret_cast<const u32x4 *>(
+                                bl + boff[n] + 64 * q + 16 * g + 8 * h);
+                            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                af[h], __builtin_bit_cast(v8bf, bw), acc[n], 0, 0, 0);
+                        }
+                    }
                 }
             }
         }
         /* a segment ends: its partials join the running sums in order */
-        if ((u + 1) % XSEG_U == 0 || u + 1 == nu_all) {
-            const bool first = u < XSEG_U;
 #pragma unroll
-            for (int n = 0; n < NT; n++) {
-                tot[n] = first ? acc[n] : tot[n] + acc[n];
-                acc[n] = v4f{0.f, 0.f, 0.f, 0.f};
-            }
+        for (int n = 0; n < NT; n++) {
+            tot[n] = s0 == 0 ? acc[n] : tot[n] + acc[n];
+            acc[n] = v4f{0.f, 0.f, 0.f, 0.f};
         }
+        ssb = ssn;
     }
     if (!live) return;
     /* y = (hi + mid) + lo per (row, token): column 3 s of a tile gathers its
@@ -398,6 +573,13 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
     }
 }
 
+/* Every row of a 16-row tile and every lane of a quarter share the quarter's
+ * scale: tiles start at multiples of 16 and quarters at multiples of 64. */
+bool xs_uniform(int blk_r, int blk_c)
+{
+    return blk_r % 16 == 0 && blk_c % 64 == 0;
+}
+
 template <typename K>
 void optin(K kernel)
 {
@@ -406,12 +588,94 @@ void optin(K kernel)
     (void)hipGetLastError();
 }
 
+int mx_cu_count()
+{
+    static int n = 0;
+    if (!n) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            v > 0)
+            n = v;
+        else
+            n = 256;
+    }
+    return n;
+}
+
+int mx_env(const char *name, int dflt)
+{
+    const char *e = getenv(name);
+    return e ? atoi(e) : dflt;
+}
+
+/* Launch shape of k_fp8_mx1 for rows x cols (n groups): waves per tile P
+ * (rows past 8 segments: 8 waves of two segments; else the smallest of 1,
+ * 2, 4 and nseg that gives `target` waves in all, else nseg), segments per
+ * wave, tiles per workgroup (8 waves a workgroup, or P when P does not
+ * divide 8), the x planes' pitch, LDS bytes and the persistent grid (at most
+ * what fits on the CUs at once). Measured on MI355X (E8M0, cold weights):
+ * 7168 x 7168 is fastest at P 4 x 2 tiles, 24576 x 1536 at P 1 x 8 tiles,
+ * 7168 x 16384 at P 8, the LM head at P 1. */
+bool mx1_config(int rows, int cols, int n, Dsv4Fp8Mx *b)
+{
+    const int ntiles = (rows + 15) / 16;
+    const int nseg = (cols + XSEG - 1) / XSEG, nu_all = (cols + XU - 1) / XU;
+    const int target = mx_env("DSV4_GPU_MX_WAVES", 1536);
+    const int cand[4] = {1, 2, 4, nseg};
+    int P = nseg > 8 ? 8 : 0;
+    for (int i = 0; i < 4 && !P; i++) {
+        const int c = cand[i];
+        if (c > nseg || c > 8) continue;
+        const int spw = (nseg + c - 1) / c;
+        if ((long long)ntiles * ((nseg + spw - 1) / spw) * n >= target) P = c;
+    }
+    if (!P) P = nseg;
+    const int force = mx_env("DSV4_GPU_MX_P", 0);
+    if (force >= 1 && force <= 8 && force <= nseg) P = force;
+    int spw = 0, tpw = 0, nw = 0;
+    for (int pass = 0; pass < 2; pass++) {
+        spw = (nseg + P - 1) / P;
+        P = (nseg + spw - 1) / spw;                    /* no wave without a segment */
+        tpw = 8 / P;
+        const int ft = mx_env("DSV4_GPU_MX_TPW", 0);
+        if (ft >= 1 && ft * P <= 8) tpw = ft;
+        if (tpw < 1) tpw = 1;
+        if (tpw > ntiles) tpw = ntiles;
+        nw = P * tpw;
+        if (nw * 64 * X1_XM >= nu_all * (XU / 4)) break;   /* x staging coverage */
+        if (pass) return false;
+        P = nseg < 8 ? nseg : 8;                       /* the most waves per tile */
+    }
+    const int xp = nu_all * XU + 8;
+    const int ngrp = (ntiles + tpw - 1) / tpw;
+    const size_t base = (size_t)XNT * xp * 2 + (size_t)nw * XUNIT_B;
+    const size_t pbuf = (size_t)tpw * (nseg - spw) * 16 * XNT * sizeof(float);
+    /* one partials buffer when every tile group gets its own workgroup */
+    const size_t cap = dsv4_lds_limit();
+    const int per_cu1 = base + pbuf <= cap / 2 ? 2 : 1;
+    int npb = 2, gx = 0;
+    if ((long long)per_cu1 * mx_cu_count() >= (long long)ngrp * n) {
+        npb = 1;
+        gx = ngrp;
+    }
+    const size_t lds = base + npb * pbuf;
+    if (lds > cap) return false;
+    if (!gx) {
+        const int per_cu = lds <= cap / 2 ? 2 : 1;
+        gx = (per_cu * mx_cu_count() + n - 1) / n;
+        if (gx > ngrp) gx = ngrp;
+    }
+    b->wpt = P; b->spw = spw; b->tpw = tpw; b->xp = xp; b->gx = gx; b->lds = lds; b->npb = npb;
+    return true;
+}
+
 } // namespace
 
 bool dsv4_fp8_mx_ok(int sfmt, int cols, int blk_r, int blk_c)
 {
     return sfmt == 0 && cols > 0 && (cols % 16) == 0 && cols <= XSEG * XSEG_MAX &&
-           blk_r >= 1 && blk_c >= 16 && (blk_c % 16) == 0;
+           blk_r >= 1 && blk_c >= 16 && blk_c <= 65536 && (blk_c % 16) == 0;
 }
 
 int dsv4_fp8_mx_launch(const Dsv4Fp8Mx &a, hipStream_t st)
@@ -424,12 +688,19 @@ int dsv4_fp8_mx_launch(const Dsv4Fp8Mx &a, hipStream_t st)
     if (a.list)
         for (int i = 0; i < a.n; i++) rmax = a.rl[i] > rmax ? a.rl[i] : rmax;
     if (rmax <= 0) return 0;
-    const int nseg = (a.cols + XSEG - 1) / XSEG;
-    const int nw = nseg < 8 ? nseg : 8;
-    const size_t lds = (size_t)nw * X1_WAVE_B;
+    Dsv4Fp8Mx b = a;
+    if (!mx1_config(rmax, a.cols, a.n, &b)) {
+        DSV4_ERR("fp8 mx: no launch shape for %dx%d", rmax, a.cols);
+        return -1;
+    }
+    b.bc_m = bc_magic(a.blk_c);
     static bool opted = false;
-    if (!opted) { optin(k_fp8_mx1<4>); opted = true; }
-    hipLaunchKernelGGL((k_fp8_mx1<4>), dim3((rmax + 15) / 16, a.n), dim3(64 * nw), lds, st, a);
+    if (!opted) { optin(k_fp8_mx1<false>); optin(k_fp8_mx1<true>); opted = true; }
+    const dim3 grid(b.gx, a.n), block(64 * b.wpt * b.tpw);
+    if (xs_uniform(a.blk_r, a.blk_c))
+        hipLaunchKernelGGL(k_fp8_mx1<true>, grid, block, b.lds, st, b);
+    else
+        hipLaunchKernelGGL(k_fp8_mx1<false>, grid, block, b.lds, st, b);
     HIP_OK(hipGetLastError(), "fp8 mx launch");
     return 0;
 }
@@ -442,6 +713,7 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
         return -1;
     }
     const int sc = (cols + blk_c - 1) / blk_c;
+    const uint32_t bc_m = bc_magic(blk_c);
     /* tokens per workgroup: at most 4 column tiles of 5 (the accumulators and
      * running sums of 4 tiles stay in registers); more tokens take more
      * workgroups along y, each reading the weights again */
@@ -449,17 +721,24 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
     const int NTc = ntile >= 4 ? 4 : ntile >= 2 ? (ntile == 3 ? 3 : 2) : 1;
     const int tpg = XTOK * NTc < nt ? XTOK * NTc : nt;
     const int groups = (nt + tpg - 1) / tpg;
-    constexpr int MW = 4;
-    const size_t lds = (size_t)tpg * XNT * BP * 2 + (size_t)MW * XUNIT_B;
+    const size_t lds = 2 * (size_t)tpg * XNT * BP * 2 + (size_t)MW * XUNIT_B;
     const dim3 grid((rows + 16 * MW - 1) / (16 * MW), groups);
     static bool opted = false;
     if (!opted) {
-        optin(k_fp8_mxn<1, 2>); optin(k_fp8_mxn<2, 2>); optin(k_fp8_mxn<3, 2>);
-        optin(k_fp8_mxn<4, 2>);
+        optin(k_fp8_mxn<1, false>); optin(k_fp8_mxn<2, false>); optin(k_fp8_mxn<3, false>);
+        optin(k_fp8_mxn<4, false>); optin(k_fp8_mxn<1, true>); optin(k_fp8_mxn<2, true>);
+        optin(k_fp8_mxn<3, true>); optin(k_fp8_mxn<4, true>);
         opted = true;
     }
-#define XN(NTV) hipLaunchKernelGGL((k_fp8_mxn<NTV, 2>), grid, dim3(64 * MW), lds, st, y, x, W, S, \
-                                   rows, cols, sc, blk_r, blk_c, nt, tpg)
+    const bool uni = xs_uniform(blk_r, blk_c);
+#define XN(NTV) do {                                                                           \
+        if (uni)                                                                               \
+            hipLaunchKernelGGL((k_fp8_mxn<NTV, true>), grid, dim3(64 * MW), lds, st, y, x, W, S, \
+                               rows, cols, sc, blk_r, bc_m, nt, tpg);                           \
+        else                                                                                   \
+            hipLaunchKernelGGL((k_fp8_mxn<NTV, false>), grid, dim3(64 * MW), lds, st, y, x, W,  \
+                               S, rows, cols, sc, blk_r, bc_m, nt, tpg);                        \
+    } while (0)
     switch (NTc) {
     case 1: XN(1); break;
     case 2: XN(2); break;

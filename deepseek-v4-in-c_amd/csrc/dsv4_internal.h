@@ -41,6 +41,10 @@ struct Dsv4Fp8Mx {
     const float *x = nullptr;
     const uint8_t *w = nullptr, *s = nullptr;
     int rows = 0, cols = 0, sc = 0, blk_r = 128, blk_c = 128;
+    /* set by dsv4_fp8_mx_launch: ceil(2^32 / blk_c), the launch shape */
+    uint32_t bc_m = 0;
+    int wpt = 1, spw = 1, tpw = 1, xp = 0, gx = 1, npb = 1;
+    size_t lds = 0;
     int n = 1;
     long long x_stride = 0, y_stride = 0, w_stride = 0, s_stride = 0;
     int list = 0;

@@ -110,6 +110,8 @@ _SIGS = {
     "dsv4_gpu_fp8_gemv_n_d": (_ci, [_vp, _vp, _vp, _vp, _ci, _ci, _ci, _ci, _vp]),
     "dsv4_gpu_fp4_gemv_d": (_ci, [_vp, _vp, _vp, _vp, _ci, _ci, _ci, _ci, _vp]),
     "dsv4_gpu_bf16_gemv_d": (_ci, [_vp, _vp, _vp, _ci, _ci, _vp]),
+    "dsv4_gpu_fp4_gemv_n_d": (_ci, [_vp, _vp, _vp, _vp, _ci, _ci, _ci, _ci, _ci, _vp]),
+    "dsv4_gpu_bf16_gemv_n_d": (_ci, [_vp, _vp, _vp, _ci, _ci, _ci, _vp]),
     "dsv4_gpu_head_argmax": (_ci, [_vp, _QP]),
     "dsv4_gpu_argmax_d": (_ci, [_vp, _vp, _ci, _vp]),
     "dsv4_gpu_embed_row_d": (_ci, [_vp, _vp, _ci, ctypes.c_longlong, _ci, _vp]),
@@ -123,6 +125,8 @@ _SIGS = {
     "dsv4_gpu_has_expert": (_ci, [_ci, _ci]),
     "dsv4_gpu_moe_fp4": (_ci, [_vp, _vp, _ci, _vp, _vp, _ci, _ci, _ci, _cf]),
     "dsv4_gpu_moe_fp4_d": (_ci, [_vp, _vp, _ci, _vp, _vp, _ci, _ci, _ci, _cf, _vp]),
+    "dsv4_gpu_moe_fp4_n": (_ci, [_vp, _vp, _ci, _vp, _vp, _ci, _ci, _ci, _ci, _cf]),
+    "dsv4_gpu_moe_fp4_n_d": (_ci, [_vp, _vp, _ci, _vp, _vp, _ci, _ci, _ci, _ci, _cf, _vp]),
     "dsv4_gpu_moe_fp4_noalloc_d": (_ci, [_vp, _vp, _ci, _vp, _vp, _ci, _ci, _ci, _cf,
                                          _vp]),
     "dsv4_gpu_kv_create": (_vp, [_ci, _ci, _ci]),
@@ -263,6 +267,22 @@ def moe_fp4(x, layer, idx, w, hidden, inter, limit):
                             idx.size, hidden, inter, float(limit))
     if rc != 0:
         raise RuntimeError("dsv4_gpu: moe_fp4 failed")
+    return out
+
+
+def moe_fp4_n(X, layer, IDX, Wt, hidden, inter, limit):
+    """Batched routed experts (dsv4_gpu_moe_fp4_n): X [nt][hidden], IDX/Wt
+    [nt][topk] -> [nt][hidden]."""
+    L = lib()
+    X = np.ascontiguousarray(X, np.float32)
+    IDX = np.ascontiguousarray(IDX, np.int32)
+    Wt = np.ascontiguousarray(Wt, np.float32)
+    nt, topk = IDX.shape
+    out = np.empty((nt, hidden), np.float32)
+    rc = L.dsv4_gpu_moe_fp4_n(_ptr(out), _ptr(X), layer, _ptr(IDX), _ptr(Wt), nt, topk,
+                              hidden, inter, ctypes.c_float(limit))
+    if rc != 0:
+        raise RuntimeError("dsv4_gpu: moe_fp4_n failed")
     return out
 
 

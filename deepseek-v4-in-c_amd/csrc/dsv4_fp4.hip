@@ -144,7 +144,115 @@ void f4_launch(float *y, const float *x, const uint8_t *W, const uint8_t *S, int
                        blk_r, blk_c, rows_per_wg);
 }
 
+/* Batched (prefill): y[t][rows] for x[t][cols], t < nt, each (row, token)
+ * with k_fp4_gemv's arithmetic -- the same chunk dots, scale FMAs in chunk
+ * order and DPP tree -- so every token's row is bit-identical to the
+ * single-token GEMV. A wave holds its R rows' chunks and scale bytes in
+ * VGPRs and runs every token over them: the weights leave HBM once per batch
+ * (the reference's one pass per batch, dsv4_matmul_fp4_n at
+ * dsv4_matmul.c:378-428 and dsv4_mmq_n :560-591). The tokens' x pass through
+ * LDS in blocks of tbx (a block is staged once per workgroup when nt <= tbx,
+ * else once per row step). */
+template <int NCH, int R>
+__global__ void __launch_bounds__(F4_WAVES * 64)
+k_fp4_gemv_n(float *__restrict__ y, const float *__restrict__ x,
+             const uint8_t *__restrict__ W, const uint8_t *__restrict__ S, int rows,
+             int cols, int sc, int blk_r, int blk_c, int nt, int tbx)
+{
+    extern __shared__ __attribute__((aligned(16))) float xs[];   /* [tbx][cols] */
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int ch = cols >> 5;
+    const size_t rowb = (size_t)cols >> 1;
+    const int nq = cols >> 2;                                    /* f32x4 per token */
+    int cb[NCH];
+    bool act[NCH];
+#pragma unroll
+    for (int n = 0; n < NCH; n++) {
+        const int c = lane + 64 * n;
+        act[n] = c < ch;
+        cb[n] = (min(c, ch - 1) * 32) / blk_c;
+    }
+    const int rb = blockIdx.x * (F4_WAVES * R) + w * R;          /* this wave's rows */
+    u32x4 v[R][NCH];
+    uint32_t sv[R][NCH];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const int r = min(rb + i, rows - 1);
+#pragma unroll
+        for (int n = 0; n < NCH; n++) {
+            const int c = min(lane + 64 * n, ch - 1);
+            v[i][n] = ldg16_stream(W + (size_t)r * rowb + (size_t)c * 16);
+            sv[i][n] = ldg8(S + (size_t)(r / blk_r) * sc + cb[n]);
+        }
+    }
+    for (int t0 = 0; t0 < nt; t0 += tbx) {
+        const int tb = min(tbx, nt - t0);
+        __syncthreads();                         /* the previous block's reads */
+        for (int i = tid; i < tb * nq; i += blockDim.x)
+            *reinterpret_cast<f32x4 *>(xs + 4 * i) = ldf4(x + (size_t)t0 * cols + 4 * i);
+        __syncthreads();
+        for (int t = 0; t < tb; t++) {
+            const float *xt = xs + (size_t)t * cols;
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int n = 0; n < NCH; n++) {
+                    const int c = min(lane + 64 * n, ch - 1);
+                    const float d = fmaf(f4_dot32(v[i][n], xt + c * 32), dec_e8m0(sv[i][n]),
+                                         acc);
+                    acc = act[n] ? d : acc;
+                }
+                acc = seg_sum<64>(acc);
+                if (lane == 63 && rb + i < rows) y[(size_t)(t0 + t) * rows + rb + i] = acc;
+            }
+        }
+    }
+}
+
+template <int NCH>
+void f4n_launch(float *y, const float *x, const uint8_t *W, const uint8_t *S, int rows,
+                int cols, int sc, int blk_r, int blk_c, int nt, hipStream_t st)
+{
+    constexpr int R = NCH >= 4 ? 1 : 2;
+    static bool opted = false;                  /* up to 64 KB of x in LDS */
+    if (!opted) {
+        (void)hipFuncSetAttribute((const void *)k_fp4_gemv_n<NCH, R>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  F4_MAXCOLS * (int)sizeof(float));
+        (void)hipGetLastError();
+        opted = true;
+    }
+    int tbx = F4_MAXCOLS / cols;                /* tokens per LDS block */
+    if (tbx > 8) tbx = 8;
+    if (tbx > nt) tbx = nt;
+    const int grid = (rows + F4_WAVES * R - 1) / (F4_WAVES * R);
+    hipLaunchKernelGGL((k_fp4_gemv_n<NCH, R>), dim3(grid), dim3(F4_WAVES * 64),
+                       (size_t)tbx * cols * sizeof(float), st, y, x, W, S, rows, cols, sc,
+                       blk_r, blk_c, nt, tbx);
+}
+
 } // namespace
+
+int dsv4_fp4_gemv_n_launch(float *y, const float *x, const uint8_t *W, const uint8_t *S,
+                           int rows, int cols, int blk_r, int blk_c, int nt, hipStream_t st)
+{
+    if (nt == 1) return dsv4_fp4_gemv_launch(y, x, W, S, rows, cols, blk_r, blk_c, st);
+    if (nt < 1 || !dsv4_fp4_gemv_ok(rows, cols, blk_r, blk_c) ||
+        (((uintptr_t)x | (uintptr_t)W) & 15)) {
+        DSV4_ERR("fp4 gemv_n: unsupported shape %dx%d blk %dx%d, %d tokens, or unaligned "
+                 "operands", rows, cols, blk_r, blk_c, nt);
+        return -1;
+    }
+    const int sc = (cols + blk_c - 1) / blk_c;
+    const int ch = cols >> 5;
+    if (ch <= 64)       f4n_launch<1>(y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st);
+    else if (ch <= 128) f4n_launch<2>(y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st);
+    else if (ch <= 256) f4n_launch<4>(y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st);
+    else                f4n_launch<8>(y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st);
+    HIP_OK(hipGetLastError(), "fp4 gemv_n launch");
+    return 0;
+}
 
 bool dsv4_fp4_gemv_ok(int rows, int cols, int blk_r, int blk_c)
 {

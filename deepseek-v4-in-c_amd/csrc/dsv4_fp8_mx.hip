@@ -63,7 +63,6 @@ constexpr int XUNIT_B = 16 * XWP;       /* one wave's unit buffer          */
 constexpr int XNT = 3;                  /* bf16 terms per activation       */
 constexpr int XTOK = 5;                 /* tokens per 16-column tile       */
 constexpr int XSEG_MAX = 16;            /* segments per row (cols <= 16384) */
-constexpr int XPL = XSEG + 8;           /* LDS pitch of a term plane (x1)  */
 
 __device__ __forceinline__ uint32_t rne_bf16(float f)
 {

@@ -568,11 +568,15 @@ void dsv4_gpu_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
     size_t end;
     if (stage_push(s, &end) != 0) abort();
     int rc = 0;
-    if (r->wdt == DSV4_WFP4 || r->wdt == DSV4_WBF16) {
-        /* token by token: per (row, token) the GEMV's own arithmetic */
-        for (int t = 0; t < nt && rc == 0; t++)
-            rc = res_gemv(v, m->rows, (float *)(g_ar.d + yo) + (size_t)t * m->rows,
-                          (const float *)(g_ar.d + xo) + (size_t)t * r->cols);
+    /* one pass over the weights for the whole batch; per (row, token) the
+     * single-token GEMV's own arithmetic */
+    if (r->wdt == DSV4_WFP4) {
+        rc = dsv4_fp4_gemv_n_launch((float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
+                                    v.w, v.s, m->rows, r->cols, r->blk_r, r->blk_c, nt,
+                                    g_stream);
+    } else if (r->wdt == DSV4_WBF16) {
+        rc = dsv4_bf16_gemv_n_launch((float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
+                                     (const uint16_t *)v.w, m->rows, r->cols, nt, g_stream);
     } else {
         rc = dsv4_fp8_gemv_n_launch(
             (float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
@@ -620,6 +624,28 @@ int dsv4_gpu_fp4_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
     }
     return dsv4_fp4_gemv_launch(d_y, d_x, d_w, d_s, rows, cols, blk_r, blk_c,
                                 as_stream(stream));
+}
+
+int dsv4_gpu_fp4_gemv_n_d(float *d_y, const float *d_x, const uint8_t *d_w,
+                          const uint8_t *d_s, int rows, int cols, int blk_r, int blk_c, int nt,
+                          void *stream)
+{
+    if (!d_y || !d_x || !d_w || !d_s || nt < 1 || nt > DSV4_MAX_BATCH) {
+        DSV4_ERR("fp4_gemv_n_d: bad arguments (nt %d)", nt);
+        return -1;
+    }
+    return dsv4_fp4_gemv_n_launch(d_y, d_x, d_w, d_s, rows, cols, blk_r, blk_c, nt,
+                                  as_stream(stream));
+}
+
+int dsv4_gpu_bf16_gemv_n_d(float *d_y, const float *d_x, const uint16_t *d_w, int rows,
+                           int cols, int nt, void *stream)
+{
+    if (!d_y || !d_x || !d_w || nt < 1 || nt > DSV4_MAX_BATCH) {
+        DSV4_ERR("bf16_gemv_n_d: bad arguments (nt %d)", nt);
+        return -1;
+    }
+    return dsv4_bf16_gemv_n_launch(d_y, d_x, d_w, rows, cols, nt, as_stream(stream));
 }
 
 int dsv4_gpu_bf16_gemv_d(float *d_y, const float *d_x, const uint16_t *d_w, int rows,
@@ -831,6 +857,56 @@ int dsv4_gpu_moe_fp4_d(float *d_out, const float *d_x, int layer,
     return dsv4_moe_fp4_launch(d_out, d_x, L->dev, (int)L->host.size(), d_idx,
                                d_w, topk, hidden, inter, swiglu_limit,
                                g_moe.p, as_stream(stream));
+}
+
+int dsv4_gpu_moe_fp4_n(float *out, const float *x, int layer, const int *idx,
+                       const float *w, int nt, int topk, int hidden, int inter,
+                       float swiglu_limit)
+{
+    LayerExperts *L;
+    if (nt < 1 || nt > DSV4_MAX_BATCH || !out || !x || !idx || !w) {
+        DSV4_ERR("moe_n: bad arguments (nt %d)", nt);
+        return -1;
+    }
+    if (moe_prepare(layer, topk, hidden, inter, &L) != 0) return -1;
+    for (int i = 0; i < nt * topk; i++)
+        if (!dsv4_gpu_has_expert(layer, idx[i])) {
+            DSV4_ERR("moe_n: layer %d expert %d (token %d, k = %d) is not resident", layer,
+                     idx[i], i / topk, i % topk);
+            return -1;
+        }
+    if (scratch_reserve(g_moe, dsv4_moe_n_scratch_bytes(nt, topk, hidden, inter)) != 0)
+        return -1;
+    Stage s;
+    const size_t xo = s.in(x, (size_t)nt * hidden * sizeof(float));
+    const size_t io = s.in(idx, (size_t)nt * topk * sizeof(int));
+    const size_t wo = s.in(w, (size_t)nt * topk * sizeof(float));
+    const size_t oo = s.add((size_t)nt * hidden * sizeof(float));
+    size_t end;
+    if (stage_push(s, &end) != 0) return -1;
+    if (dsv4_moe_fp4_n_launch((float *)(g_ar.d + oo), (const float *)(g_ar.d + xo), L->dev,
+                              (int)L->host.size(), (const int *)(g_ar.d + io),
+                              (const float *)(g_ar.d + wo), nt, topk, hidden, inter,
+                              swiglu_limit, g_moe.p, g_stream) != 0)
+        return -1;
+    return stage_pull(oo, (size_t)nt * hidden * sizeof(float), out);
+}
+
+int dsv4_gpu_moe_fp4_n_d(float *d_out, const float *d_x, int layer, const int *d_idx,
+                         const float *d_w, int nt, int topk, int hidden, int inter,
+                         float swiglu_limit, void *stream)
+{
+    LayerExperts *L;
+    if (nt < 1 || nt > DSV4_MAX_BATCH || !d_out || !d_x || !d_idx || !d_w) {
+        DSV4_ERR("moe_n_d: bad arguments (nt %d)", nt);
+        return -1;
+    }
+    if (moe_prepare(layer, topk, hidden, inter, &L) != 0) return -1;
+    if (scratch_reserve(g_moe, dsv4_moe_n_scratch_bytes(nt, topk, hidden, inter)) != 0)
+        return -1;
+    return dsv4_moe_fp4_n_launch(d_out, d_x, L->dev, (int)L->host.size(), d_idx, d_w, nt,
+                                 topk, hidden, inter, swiglu_limit, g_moe.p,
+                                 as_stream(stream));
 }
 
 int dsv4_gpu_moe_fp4_noalloc_d(float *d_out, const float *d_x, int layer,

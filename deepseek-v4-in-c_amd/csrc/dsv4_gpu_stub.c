@@ -48,6 +48,17 @@ int dsv4_gpu_bf16_gemv_d(float *d_y, const float *d_x, const uint16_t *d_w, int 
                          int cols, void *stream)
 { (void)d_y; (void)d_x; (void)d_w; (void)rows; (void)cols; (void)stream; return -1; }
 
+int dsv4_gpu_fp4_gemv_n_d(float *d_y, const float *d_x, const uint8_t *d_w,
+                          const uint8_t *d_s, int rows, int cols, int blk_r, int blk_c, int nt,
+                          void *stream)
+{ (void)d_y; (void)d_x; (void)d_w; (void)d_s; (void)rows; (void)cols; (void)blk_r;
+  (void)blk_c; (void)nt; (void)stream; return -1; }
+
+int dsv4_gpu_bf16_gemv_n_d(float *d_y, const float *d_x, const uint16_t *d_w, int rows,
+                           int cols, int nt, void *stream)
+{ (void)d_y; (void)d_x; (void)d_w; (void)rows; (void)cols; (void)nt; (void)stream;
+  return -1; }
+
 int dsv4_gpu_head_argmax(const float *x, const DSV4QMat *head)
 { (void)x; (void)head; return -1; }
 int dsv4_gpu_argmax_d(int *d_out, const float *d_v, int n, void *stream)
@@ -92,6 +103,18 @@ int dsv4_gpu_moe_fp4_d(float *d_out, const float *d_x, int layer,
                        int hidden, int inter, float swiglu_limit, void *stream)
 { (void)d_out; (void)d_x; (void)layer; (void)d_idx; (void)d_w; (void)topk;
   (void)hidden; (void)inter; (void)swiglu_limit; (void)stream; return -1; }
+int dsv4_gpu_moe_fp4_n(float *out, const float *x, int layer, const int *idx,
+                       const float *w, int nt, int topk, int hidden, int inter,
+                       float swiglu_limit)
+{ (void)out; (void)x; (void)layer; (void)idx; (void)w; (void)nt; (void)topk; (void)hidden;
+  (void)inter; (void)swiglu_limit; return -1; }
+
+int dsv4_gpu_moe_fp4_n_d(float *d_out, const float *d_x, int layer, const int *d_idx,
+                         const float *d_w, int nt, int topk, int hidden, int inter,
+                         float swiglu_limit, void *stream)
+{ (void)d_out; (void)d_x; (void)layer; (void)d_idx; (void)d_w; (void)nt; (void)topk;
+  (void)hidden; (void)inter; (void)swiglu_limit; (void)stream; return -1; }
+
 int dsv4_gpu_moe_fp4_noalloc_d(float *d_out, const float *d_x, int layer,
                                const int *d_idx, const float *d_w, int topk,
                                int hidden, int inter, float swiglu_limit, void *stream)

@@ -88,12 +88,20 @@ int dsv4_bf16_gemv_list_launch(const float *x, int cols, int n, const uint16_t *
 bool dsv4_fp4_gemv_ok(int rows, int cols, int blk_r, int blk_c);
 int dsv4_fp4_gemv_launch(float *y, const float *x, const uint8_t *W, const uint8_t *S,
                          int rows, int cols, int blk_r, int blk_c, hipStream_t st);
+/* Batched: y[nt][rows] for x[nt][cols], every (row, token) bit-identical to
+ * dsv4_fp4_gemv_launch on that token; the weights are read once. */
+int dsv4_fp4_gemv_n_launch(float *y, const float *x, const uint8_t *W, const uint8_t *S,
+                           int rows, int cols, int blk_r, int blk_c, int nt, hipStream_t st);
 
 /* BF16 GEMV (dsv4_matmul_bf16): W bf16 [rows][cols]. _ok: the shapes it
  * takes (cols a multiple of 8 up to 16384). Returns 0 / -1. */
 bool dsv4_bf16_gemv_ok(int rows, int cols);
 int dsv4_bf16_gemv_launch(float *y, const float *x, const uint16_t *W, int rows, int cols,
                           hipStream_t st);
+/* Batched: y[nt][rows] for x[nt][cols], every (row, token) bit-identical to
+ * dsv4_bf16_gemv_launch on that token; the weights are read once. */
+int dsv4_bf16_gemv_n_launch(float *y, const float *x, const uint16_t *W, int rows, int cols,
+                            int nt, hipStream_t st);
 
 /* Greedy argmax (the first index of the maximum, dsv4_run.c:471-472) over
  * d_v[n] into d_out[0]; scratch of dsv4_argmax_scratch_bytes. 0 / -1. */
@@ -138,6 +146,16 @@ int dsv4_moe_fp4_launch(float *d_out, const float *d_x,
                         const int *d_idx, const float *d_w, int topk,
                         int hidden, int inter, float limit, void *scratch,
                         hipStream_t st);
+
+/* Batched routed MoE (prefill, the routed half of moe_n): d_out[nt][hidden]
+ * for d_x[nt][hidden], routing d_idx/d_w [nt][topk]; each distinct expert's
+ * weights stream once for the batch and every token's row is bit-identical
+ * to dsv4_moe_fp4_launch on that token. Scratch of dsv4_moe_n_scratch_bytes
+ * (at least dsv4_moe_scratch_bytes). */
+size_t dsv4_moe_n_scratch_bytes(int nt, int topk, int hidden, int inter);
+int dsv4_moe_fp4_n_launch(float *d_out, const float *d_x, const Dsv4ExpertDev *d_table,
+                          int n_table, const int *d_idx, const float *d_w, int nt, int topk,
+                          int hidden, int inter, float limit, void *scratch, hipStream_t st);
 
 /* The VALU form; hbuf is device scratch [topk][inter] f32. */
 int dsv4_moe_fp4_valu_launch(float *d_out, const float *d_x,

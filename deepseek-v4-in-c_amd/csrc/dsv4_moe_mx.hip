@@ -745,6 +745,359 @@ k_mc2_down(float *__restrict__ out, const uint16_t *__restrict__ ht,
     }
 }
 
+/* ------------------------------------------------------- batched (prefill)
+ *
+ * The routed half of the reference's moe_n (dsv4_layer.c:714-855) for nt
+ * tokens. The batch's (token, k) pairs ask for the distinct experts in
+ * first-request order; each distinct expert streams its weights once, for
+ * every pair routed to it (the reference's union, :728-739, and
+ * run_expert_n, :681-703). Per pair the products are the staged form's
+ * (k_mc2_gate_up / k_mc2_down), column for column: the matrix core computes
+ * each result column from its own B column, so a pair sitting in columns
+ * 3j..3j+2 of a 16-column tile gets the bits it gets in columns 0..2 alone.
+ * The unit order, the two alternating accumulators, the term sum and the
+ * k-ordered combine are the single-token ones, so every token's output row
+ * is bit-identical to the single-token call on that token.
+ *
+ * LAUNCHES: k_mn_split (x -> bf16 term planes, every token), k_mn_route (one
+ * workgroup: slots, per-slot pair lists), k_mn_pass<GATE> (h of every pair),
+ * k_mn_pass<DOWN> (acc_k of every pair), k_mn_combine (the k-ordered sum). */
+constexpr int MN_TOK = 5;                          /* pairs per 16-column B tile  */
+constexpr int MN_BROWS = MN_TOK * MC_NT;           /* B term rows per tile (15)   */
+constexpr int MN_BP = 512 + 8;                     /* LDS pitch of a term row     */
+constexpr int MN_BBUF = MN_BROWS * MN_BP;          /* bf16 per B buffer           */
+constexpr int MN_NL = (16 * 64) / 256;             /* 16-byte B pieces per thread */
+constexpr int MN_PMAX = 4096;                      /* pairs per call              */
+
+/* Slot s: expert eid[s] (-1 for ids outside the table: its pairs give NaN,
+ * as the single-token call does), its pairs plist[off[s] .. off[s] + cnt[s])
+ * in pair order (pair p = token * topk + k). */
+struct MnRoute {
+    int n_uniq, n_pairs, pad[62];
+    int eid[MN_PMAX], off[MN_PMAX], cnt[MN_PMAX], plist[MN_PMAX];
+};
+
+__global__ void __launch_bounds__(256)
+k_mn_split(uint16_t *__restrict__ xt, const float *__restrict__ x, int nt, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nt * n) return;
+    const int t = i / n, c = i - t * n;
+    uint32_t tt[MC_NT];
+    bf16_terms(x[i], tt);
+#pragma unroll
+    for (int q = 0; q < MC_NT; q++) xt[((size_t)t * MC_NT + q) * n + c] = (uint16_t)tt[q];
+}
+
+/* One workgroup of 1024. Pair p's key is its expert id (-1 outside the
+ * table); its rank is the number of earlier pairs with the same key; rank 0
+ * marks the key's first request, and the firsts in pair order number the
+ * slots. A pair's place in plist is (pairs of earlier slots) + its rank. */
+__global__ void __launch_bounds__(1024)
+k_mn_route(MnRoute *__restrict__ rt, const int *__restrict__ idx, int np, int n_table)
+{
+    constexpr int RND = MN_PMAX / 1024;
+    __shared__ int key[MN_PMAX];
+    __shared__ int slot[MN_PMAX];
+    __shared__ int wcnt[RND * 16];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+#pragma unroll
+    for (int r = 0; r < RND; r++) {
+        const int p = r * 1024 + tid;
+        if (p < np) {
+            const int e = idx[p];
+            key[p] = (e >= 0 && e < n_table) ? e : -1;
+        }
+    }
+    __syncthreads();
+    int q0[RND], rk[RND];
+    unsigned long long bal[RND];
+#pragma unroll
+    for (int r = 0; r < RND; r++) {
+        const int p = r * 1024 + tid;
+        int f = p, c = 0;
+        if (p < np) {
+            const int kp = key[p];
+            for (int q = 0; q < p; q++)
+                if (key[q] == kp) {
+                    if (c == 0) f = q;
+                    c++;
+                }
+        }
+        q0[r] = f;
+        rk[r] = c;
+        bal[r] = __ballot(p < np && c == 0);
+        if (lane == 0) wcnt[r * 16 + w] = __popcll(bal[r]);
+    }
+    __syncthreads();
+    int nu = 0;
+    for (int i = 0; i < RND * 16; i++) nu += wcnt[i];
+#pragma unroll
+    for (int r = 0; r < RND; r++) {
+        const int p = r * 1024 + tid;
+        if (p < np && rk[r] == 0) {
+            int base = 0;
+            for (int i = 0; i < r * 16 + w; i++) base += wcnt[i];
+            slot[p] = base + __popcll(bal[r] & ((1ull << lane) - 1ull));
+        }
+    }
+    __syncthreads();
+    int sl[RND];
+#pragma unroll
+    for (int r = 0; r < RND; r++) {
+        const int p = r * 1024 + tid;
+        sl[r] = p < np ? slot[q0[r]] : 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < RND; r++) {
+        const int p = r * 1024 + tid;
+        if (p < np) slot[p] = sl[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < RND; r++) {
+        const int p = r * 1024 + tid;
+        if (p >= np) continue;
+        const int sp = sl[r];
+        int less = 0, same = 0;
+        for (int q = 0; q < np; q++) {
+            const int sq = slot[q];
+            less += sq < sp;
+            same += sq == sp;
+        }
+        rt->plist[less + rk[r]] = p;
+        if (rk[r] == 0) {
+            rt->off[sp] = less;
+            rt->cnt[sp] = same;
+            rt->eid[sp] = key[p];
+        }
+    }
+    if (tid == 0) {
+        rt->n_uniq = nu;
+        rt->n_pairs = np;
+    }
+}
+
+/* The B terms of unit u for a pass's nb pairs: term row (j MC_NT + c) is
+ * plane c of source row prow[j] (src [row][MC_NT][K]), 512 elements from
+ * 512 u. Requested by every thread (rows past the pass read prow[0], rows
+ * past the tile too: no branch before the loads), stored as zeros past nb. */
+__device__ __forceinline__ void mn_bload(u32x4 *v, const uint16_t *src, const int *prow,
+                                         int nb, int K, int u)
+{
+#pragma unroll
+    for (int m = 0; m < MN_NL; m++) {
+        const int i = (int)threadIdx.x + 256 * m;
+        const int row = i >> 6, piece = i & 63;
+        const int j = row / MC_NT, c = row - j * MC_NT;
+        const int pr = j < nb ? prow[j] : prow[0];
+        v[m] = *(const DSV4_GLOBAL u32x4 *)(src + ((size_t)pr * MC_NT + c) * K + 512 * u +
+                                            8 * piece);
+    }
+}
+
+__device__ __forceinline__ void mn_bstore(uint16_t *bb, const u32x4 *v, int nb)
+{
+#pragma unroll
+    for (int m = 0; m < MN_NL; m++) {
+        const int i = (int)threadIdx.x + 256 * m;
+        const int row = i >> 6, piece = i & 63;
+        if (row < MN_BROWS)
+            *reinterpret_cast<u32x4 *>(bb + row * MN_BP + 8 * piece) =
+                row / MC_NT < nb ? v[m] : u32x4{0u, 0u, 0u, 0u};
+    }
+}
+
+/* m2_mac with the B tile of a pass: column r reads term row r (15 rows; the
+ * unused column 15 repeats row 14). Same steps, same accumulators. */
+__device__ __forceinline__ void mn_mac(v4f *acc, const unsigned char *buf, const uint16_t *bb,
+                                       int lane, bool live)
+{
+    const int r = lane & 15, g = lane >> 4;
+    const u32x4 sv = *reinterpret_cast<const u32x4 *>(buf + M2_SOFF + r * 16);
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+    const uint16_t *bl = bb + min(r, MN_BROWS - 1) * MN_BP;
+#pragma unroll
+    for (int qb = 0; qb < 4; qb++) {
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(buf + r * M2_WP + 64 * qb + 16 * g);
+        const float sc = live ? dec_e8m0((sw[qb] >> (8 * g)) & 0xFFu) : 0.0f;
+        const uint32_t d[4] = {a.x, a.y, a.z, a.w};
+        v8bf b[4];
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+            b[m] = __builtin_bit_cast(v8bf, *reinterpret_cast<const u32x4 *>(
+                                                bl + 128 * qb + 32 * g + 8 * m));
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+            acc[qb & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(d[m], sc), b[m],
+                                                                   acc[qb & 1], 0, 0, 0);
+    }
+}
+
+/* Columns c0..c0+MC_NT-1 of a result tile summed in column order, per row
+ * (term_sum for the pair at columns c0..). */
+__device__ __forceinline__ v4f term_sum_at(const v4f &d, int lane, int c0)
+{
+    const int base = (lane & ~15) + c0;
+    v4f s;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        float a = __shfl(d[j], base + 0, 64);
+#pragma unroll
+        for (int t = 1; t < MC_NT; t++) a = a + __shfl(d[j], base + t, 64);
+        s[j] = a;
+    }
+    return s;
+}
+
+__device__ __forceinline__ void mn_wave_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+/* One pass kernel for both halves; workgroup (row block, slot), 4 waves, a
+ * 16-row tile each:
+ *   GATE: rows blockIdx.x * 32 + 16 (w >> 1) of w1 (w even) / w3 (w odd),
+ *         B = the pairs' tokens' x terms (src = xt [nt][MC_NT][hidden]);
+ *         SwiGLU, h terms into dst = ht [pair][MC_NT][inter];
+ *   DOWN: rows blockIdx.x * 64 + 16 w of w2, B = the pairs' h terms (src =
+ *         ht); acc_k into dst = accp [pair][hidden].
+ * The slot's pairs run in passes of MN_TOK. Per unit: each wave stages its
+ * weight unit (requested D units earlier) in its own buffer, requests the
+ * next unit's B and the weight unit D ahead (B first: the end-of-unit wait
+ * for B then leaves that weight unit in flight), runs the unit, stores the
+ * next B into the other buffer, and the workgroup meets at one barrier. NU >
+ * 0: the unit count, every unit live (k_mc2_*'s NU > 0 forms); NU == 0: a
+ * run-time count padded to a multiple of D with dead units, as m2_tile's
+ * run-time form pads (D must then equal the single-token form's, 3). */
+template <int D, int NU, bool GATE>
+__global__ void __launch_bounds__(256)
+k_mn_pass(void *__restrict__ dst, const uint16_t *__restrict__ src,
+          const MnRoute *__restrict__ rt, const Dsv4ExpertDev *__restrict__ table,
+          int topk, int hidden, int inter, float limit)
+{
+    extern __shared__ __attribute__((aligned(16))) unsigned char mnlds[];
+    __shared__ float red[2][2][MN_TOK][16];             /* GATE: [tile][mat][pair][row] */
+    __shared__ int prow[MN_TOK], pidx[MN_TOK];
+    const int sl = blockIdx.y;
+    if (sl >= rt->n_uniq) return;                       /* the whole workgroup */
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int e = rt->eid[sl], cnt = rt->cnt[sl], off = rt->off[sl];
+    const Dsv4ExpertDev E = e >= 0 ? table[e]
+                                   : Dsv4ExpertDev{nullptr, nullptr, nullptr, nullptr, nullptr,
+                                                   nullptr};
+    if (!E.w1) {
+        if (!GATE) {                                    /* as k_mc2_down: NaN results */
+            float *accp = (float *)dst;
+            for (int i = tid; i < cnt * 64; i += blockDim.x)
+                accp[(size_t)rt->plist[off + i / 64] * hidden + blockIdx.x * 64 + (i & 63)] =
+                    __builtin_nanf("");
+        }
+        return;
+    }
+    const int K = GATE ? hidden : inter;
+    const int nsb = K >> 5;
+    const size_t rowb = (size_t)K >> 1;
+    const int nu = NU > 0 ? NU : (int)(rowb / M2_UB);
+    const int nup = NU > 0 ? NU : ((nu + D - 1) / D) * D;   /* units run, dead included */
+    const int mat = GATE ? (w & 1) : 0, tile = GATE ? (w >> 1) : w;
+    const int o0 = GATE ? blockIdx.x * 32 + 16 * tile : blockIdx.x * 64 + 16 * w;
+    const uint8_t *base = (GATE ? (mat ? E.w3 : E.w1) : E.w2) + (size_t)o0 * rowb;
+    const uint8_t *sb = (GATE ? (mat ? E.s3 : E.s1) : E.s2) + (size_t)o0 * nsb;
+    uint16_t *bbuf = (uint16_t *)mnlds;                             /* [2][MN_BBUF] */
+    unsigned char *buf = mnlds + (size_t)2 * MN_BBUF * 2 + (size_t)w * M2_WBUF;
+    const int r = lane & 15, g = lane >> 4;
+
+    for (int p0 = 0; p0 < cnt; p0 += MN_TOK) {
+        const int nb = min(MN_TOK, cnt - p0);
+        __syncthreads();                                /* the last pass's epilogue */
+        if (tid < MN_TOK) {
+            const int p = rt->plist[off + p0 + min(tid, nb - 1)];
+            pidx[tid] = p;
+            prow[tid] = GATE ? p / topk : p;
+        }
+        __syncthreads();
+        u32x4 bv[MN_NL];
+        M2Unit P[D];
+        mn_bload(bv, src, prow, nb, K, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        m2_prologue<D>(P, base, rowb, sb, nsb, nu, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        mn_bstore(bbuf, bv, nb);
+        __syncthreads();
+        v4f acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+        auto unit = [&](int u, M2Unit &slot) {
+            m2_stage(buf, slot, lane);
+            mn_bload(bv, src, prow, nb, K, min(u + 1, nu - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            if (NU == 0 || u + D < nup)
+                m2_load(slot, base, rowb, sb, nsb, min(u + D, nu - 1), lane);
+            __builtin_amdgcn_sched_barrier(0);
+            mn_wave_sync();
+            mn_mac(acc, buf, bbuf + (u & 1) * MN_BBUF, lane, u < nu);
+            mn_bstore(bbuf + ((u + 1) & 1) * MN_BBUF, bv, nb);
+            __syncthreads();
+        };
+        if constexpr (NU > 0) {
+#pragma unroll
+            for (int u = 0; u < NU; u++) unit(u, P[u % D]);
+        } else {
+            for (int u0 = 0; u0 < nup; u0 += D) {
+#pragma unroll
+                for (int j = 0; j < D; j++) unit(u0 + j, P[j]);
+            }
+        }
+        const v4f res = acc[0] + acc[1];
+        for (int j = 0; j < nb; j++) {
+            const v4f sj = term_sum_at(res, lane, MC_NT * j);
+            if (r == 0) {
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    if (GATE)
+                        red[tile][mat][j][4 * g + jj] = sj[jj];
+                    else
+                        ((float *)dst)[(size_t)pidx[j] * hidden + o0 + 4 * g + jj] = sj[jj];
+                }
+            }
+        }
+        if (GATE) {
+            __syncthreads();
+            uint16_t *ht = (uint16_t *)dst;
+            for (int q = tid; q < 2 * nb * 16; q += blockDim.x) {
+                const int t = q / (nb * 16), rem = q - t * nb * 16;
+                const int j = rem >> 4, i = rem & 15;
+                uint32_t tt[MC_NT];
+                bf16_terms(swiglu1(red[t][0][j][i], red[t][1][j][i], limit), tt);
+#pragma unroll
+                for (int c = 0; c < MC_NT; c++)
+                    ht[((size_t)pidx[j] * MC_NT + c) * inter + blockIdx.x * 32 + 16 * t + i] =
+                        (uint16_t)tt[c];
+            }
+        }
+    }
+}
+
+/* out[t][i] = ((0 + w_0 acc_0[i]) + w_1 acc_1[i]) + ...: k_mc2_down's
+ * combine, per token (the reference's k-ordered sum, dsv4_layer.c:829-839). */
+__global__ void __launch_bounds__(256)
+k_mn_combine(float *__restrict__ out, const float *__restrict__ accp,
+             const float *__restrict__ wts, int topk, int hidden)
+{
+    const int t = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= hidden) return;
+    float o = 0.0f;
+    for (int k = 0; k < topk; k++) {
+        const float p = wts[(size_t)t * topk + k] * accp[((size_t)t * topk + k) * hidden + i];
+        o = o + p;
+    }
+    out[(size_t)t * hidden + i] = o;
+}
+
+size_t mn_lds() { return (size_t)2 * MN_BBUF * 2 + 4 * M2_WBUF; }
+
 size_t m2_lds_a(int hidden) { return (size_t)MC_NT * mc_pitch(hidden) * 2 + 4 * M2_WBUF; }
 size_t m2_lds_b(int topk, int inter) { return (size_t)m2_down_waves(topk) * m2_wave_b(inter); }
 
@@ -869,5 +1222,74 @@ int dsv4_moe_fp4_launch(float *d_out, const float *d_x,
     hipLaunchKernelGGL((k_mc_down<2, 8>), dim3(hidden / 32), dim3(512), lb, st, d_out, ht,
                        d_table, n_table, d_idx, d_w, topk, hidden, inter);
     HIP_OK(hipGetLastError(), "moe down launch");
+    return 0;
+}
+
+size_t dsv4_moe_n_scratch_bytes(int nt, int topk, int hidden, int inter)
+{
+    if (nt <= 0 || topk <= 0 || hidden <= 0 || inter <= 0) return 0;
+    const size_t single = dsv4_moe_scratch_bytes(topk, hidden, inter);
+    if (nt == 1) return single;
+    const size_t np = (size_t)nt * topk;
+    const size_t batched = a256(sizeof(MnRoute)) + a256((size_t)nt * MC_NT * hidden * 2) +
+                           a256(np * MC_NT * inter * 2) + a256(np * hidden * sizeof(float));
+    return batched > single ? batched : single;
+}
+
+int dsv4_moe_fp4_n_launch(float *d_out, const float *d_x, const Dsv4ExpertDev *d_table,
+                          int n_table, const int *d_idx, const float *d_w, int nt, int topk,
+                          int hidden, int inter, float limit, void *scratch, hipStream_t st)
+{
+    if (nt < 1 || topk < 1) return -1;
+    const int form = mc_env("DSV4_GPU_MOE_MC", 2);
+    const bool batched = nt > 1 && form == 2 && m2_shape_ok(topk, hidden, inter) &&
+                         ((uintptr_t)d_x & 15u) == 0 && (size_t)nt * topk <= MN_PMAX &&
+                         mn_lds() + 8 * 1024 <= dsv4_lds_limit();
+    if (!batched) {
+        /* token by token: each token's own call, so its bits by construction */
+        for (int t = 0; t < nt; t++)
+            if (dsv4_moe_fp4_launch(d_out + (size_t)t * hidden, d_x + (size_t)t * hidden,
+                                    d_table, n_table, d_idx + (size_t)t * topk,
+                                    d_w + (size_t)t * topk, topk, hidden, inter, limit,
+                                    scratch, st) != 0)
+                return -1;
+        return 0;
+    }
+    const int np = nt * topk;
+    char *p = (char *)scratch;
+    MnRoute *rt = (MnRoute *)p;                         p += a256(sizeof(MnRoute));
+    uint16_t *xt = (uint16_t *)p;                       p += a256((size_t)nt * MC_NT * hidden * 2);
+    uint16_t *ht = (uint16_t *)p;                       p += a256((size_t)np * MC_NT * inter * 2);
+    float *accp = (float *)p;
+    const int slots = np < n_table + 1 ? np : n_table + 1;
+    static bool opted = false;
+    if (!opted) {
+        mc_lds_optin(k_mn_pass<2, 14, true>); mc_lds_optin(k_mn_pass<3, 0, true>);
+        mc_lds_optin(k_mn_pass<2, 4, false>); mc_lds_optin(k_mn_pass<3, 0, false>);
+        opted = true;
+    }
+    const size_t lds = mn_lds();
+    hipLaunchKernelGGL(k_mn_split, dim3((nt * hidden + 255) / 256), dim3(256), 0, st, xt, d_x,
+                       nt, hidden);
+    hipLaunchKernelGGL(k_mn_route, dim3(1), dim3(1024), 0, st, rt, d_idx, np, n_table);
+    HIP_OK(hipGetLastError(), "moe_n route launch");
+    const dim3 ga(inter / 32, slots), gb(hidden / 64, slots);
+    if (hidden / 512 == 14)
+        hipLaunchKernelGGL((k_mn_pass<2, 14, true>), ga, dim3(256), lds, st, (void *)ht, xt, rt,
+                           d_table, topk, hidden, inter, limit);
+    else
+        hipLaunchKernelGGL((k_mn_pass<3, 0, true>), ga, dim3(256), lds, st, (void *)ht, xt, rt,
+                           d_table, topk, hidden, inter, limit);
+    HIP_OK(hipGetLastError(), "moe_n gate/up launch");
+    if (inter / 512 == 4)
+        hipLaunchKernelGGL((k_mn_pass<2, 4, false>), gb, dim3(256), lds, st, (void *)accp, ht,
+                           rt, d_table, topk, hidden, inter, limit);
+    else
+        hipLaunchKernelGGL((k_mn_pass<3, 0, false>), gb, dim3(256), lds, st, (void *)accp, ht,
+                           rt, d_table, topk, hidden, inter, limit);
+    HIP_OK(hipGetLastError(), "moe_n down launch");
+    hipLaunchKernelGGL(k_mn_combine, dim3((hidden + 255) / 256, nt), dim3(256), 0, st, d_out,
+                       accp, d_w, topk, hidden);
+    HIP_OK(hipGetLastError(), "moe_n combine launch");
     return 0;
 }

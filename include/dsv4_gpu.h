@@ -157,6 +157,17 @@ int dsv4_gpu_fp4_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
 int dsv4_gpu_bf16_gemv_d(float *d_y, const float *d_x, const uint16_t *d_w, int rows,
                          int cols, void *stream);
 
+/* The batched FP4 and BF16 forms (prefill: the weights are read once for the
+ * whole batch, as dsv4_mmq_n does for every format, dsv4_matmul.c:560-591):
+ * d_y[nt][rows] for d_x[nt][cols], each (row, token) bit-identical to the
+ * single-token call above on that token. nt <= DSV4_MAX_BATCH. What
+ * dsv4_gpu_mmq_n runs after staging for a resident FP4 / BF16 matrix. */
+int dsv4_gpu_fp4_gemv_n_d(float *d_y, const float *d_x, const uint8_t *d_w,
+                          const uint8_t *d_s, int rows, int cols, int blk_r, int blk_c, int nt,
+                          void *stream);
+int dsv4_gpu_bf16_gemv_n_d(float *d_y, const float *d_x, const uint16_t *d_w, int rows,
+                           int cols, int nt, void *stream);
+
 /* ================================================================ the head */
 
 /* The decode loop's head in one call (dsv4_run.c:467-472): logits =
@@ -309,6 +320,25 @@ int dsv4_gpu_moe_fp4_d(float *d_out, const float *d_x, int layer,
                        const int *d_idx, const float *d_w, int topk,
                        int hidden, int inter, float swiglu_limit,
                        void *stream);
+
+/* The routed half of moe_n (dsv4_layer.c:714-855, the batched prefill
+ * path) on the device: out[t] = dsv4_gpu_moe_fp4 of token t, for nt <=
+ * DSV4_MAX_BATCH tokens (x/out [nt][hidden], idx/w [nt][topk], host
+ * buffers). As in the reference, the distinct experts the batch asks for are
+ * found first (in first-request order) and each one's weights are read once
+ * for every (token, k) routed to it; each token's row is bit-identical to
+ * dsv4_gpu_moe_fp4 on that token. 0 / -1 (an expert not resident, a shape
+ * that does not match, nt out of range). */
+int dsv4_gpu_moe_fp4_n(float *out, const float *x, int layer, const int *idx,
+                       const float *w, int nt, int topk, int hidden, int inter,
+                       float swiglu_limit);
+
+/* Stream-ordered form on device buffers (the routing stays on the device:
+ * an id outside the layer's table, or an expert not registered, gives that
+ * token a NaN row, as dsv4_gpu_moe_fp4_d does). */
+int dsv4_gpu_moe_fp4_n_d(float *d_out, const float *d_x, int layer, const int *d_idx,
+                         const float *d_w, int nt, int topk, int hidden, int inter,
+                         float swiglu_limit, void *stream);
 
 /* dsv4_gpu_moe_fp4_d without any allocation: the same kernels and the same
  * bits, with their scratch (x's and h's bf16 term planes, or h in f32) in a

@@ -77,6 +77,10 @@ def lib():
         L.orc_moe_fp4.argtypes = [_f32p, _f32p, _f32p, pp, pp, pp, pp, pp, pp,
                                   _f32p, ctypes.c_int, ctypes.c_int,
                                   ctypes.c_int, ctypes.c_float]
+        L.orc_moe_fp4_n.restype = ctypes.c_int
+        L.orc_moe_fp4_n.argtypes = [_f32p, _i32p, _f32p, pp, pp, pp, pp, pp, pp, _i32p,
+                                    _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_float]
         L.orc_indexer_score.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.orc_topk.restype = ctypes.c_int
@@ -245,6 +249,32 @@ def moe_fp4(x, experts, wts, hidden, inter, limit, return_acc=False):
                       arr("s2"), _p(wts, _f32p), topk, hidden, inter,
                       float(limit))
     return (out, acc) if return_acc else out
+
+
+def moe_fp4_n(X, table, IDX, W, hidden, inter, limit):
+    """The routed half of moe_n over a batch: X [nt][hidden], IDX/W
+    [nt][topk], table: dict expert id -> expert dict. Returns (out [nt][hidden],
+    the distinct experts in first-request order)."""
+    X = _f32(X); W = _f32(W)
+    IDX = np.ascontiguousarray(IDX, np.int32)
+    nt, topk = IDX.shape
+    ids = sorted(table)
+    pos = {e: i for i, e in enumerate(ids)}
+    keep = []
+
+    def arr(name):
+        a = (_u8p * len(ids))()
+        for i, e in enumerate(ids):
+            v = _u8(table[e][name]); keep.append(v); a[i] = _p(v, _u8p)
+        return a
+    LI = np.ascontiguousarray(np.vectorize(pos.get)(IDX), np.int32)
+    out = np.empty((nt, hidden), np.float32)
+    uniq = np.empty(nt * topk, np.int32)
+    nu = lib().orc_moe_fp4_n(_p(out, _f32p), _p(uniq, _i32p),
+                             _p(X, _f32p), arr("w1"), arr("s1"), arr("w3"), arr("s3"),
+                             arr("w2"), arr("s2"), _p(LI, _i32p),
+                             _p(W, _f32p), nt, topk, hidden, inter, float(limit))
+    return out, np.array([ids[i] for i in uniq[:nu]], np.int32)
 
 
 # ------------------------------------------------------------------ sparse MLA
@@ -421,6 +451,18 @@ def ref_matmul_fp4(x, W, S, inn, blk_r=1, blk_c=32, scalar=False):
     y = np.empty(out, np.float32)
     fn = ref().dsv4_matmul_fp4_scalar if scalar else ref().dsv4_matmul_fp4
     fn(_p(y, _f32p), _p(x, _f32p), _p(W, _u8p), _p(S, _u8p), inn, out, blk_r, blk_c)
+    return y
+
+
+def ref_matmul_fp4_n(x, W, S, inn, blk_r=1, blk_c=32):
+    """The reference's batched dsv4_matmul_fp4_n (what expert_forward_n's
+    dsv4_mmq_n runs for an FP4 matrix): x [nt][in] -> y [nt][out]."""
+    W = _u8(W); x = _f32(x); S = _u8(S)
+    out = W.shape[0]
+    nt = x.shape[0]
+    y = np.empty((nt, out), np.float32)
+    ref().dsv4_matmul_fp4_n(_p(y, _f32p), _p(x, _f32p), _p(W, _u8p), _p(S, _u8p), inn, out,
+                            blk_r, blk_c, nt)
     return y
 
 

@@ -282,6 +282,57 @@ void orc_moe_fp4(float *out, float *acc, const float *x,
     if (!acc) free(a);
 }
 
+/* The routed half of moe_n (dsv4_layer.c:714-855) over nt tokens. The
+ * distinct experts the batch asks for are listed in first-request order
+ * (:728-739); each runs over every (token, k) routed to it (run_expert_n,
+ * :681-703) into that pair's own slot of expert_acc; then each token's slots
+ * are summed strictly in k order (:829-839). expert_forward_n computes each
+ * pair with dsv4_mmq_n, which is bit-identical per (row, token) to dsv4_mmq
+ * (dsv4_matmul.c:362-376), so a pair's slot is orc_expert_fp4 of its token.
+ * Expert e's tensors are w1[e] ... s2[e]; idx and wts are [nt][topk]; x and
+ * out [nt][hidden]. uniq (optional, nt * topk ints) receives the distinct
+ * experts in that order; returns their count. */
+int orc_moe_fp4_n(float *out, int *uniq, const float *x,
+                  const uint8_t *const *w1, const uint8_t *const *s1,
+                  const uint8_t *const *w3, const uint8_t *const *s3,
+                  const uint8_t *const *w2, const uint8_t *const *s2,
+                  const int *idx, const float *wts, int nt, int topk, int hidden,
+                  int inter, float limit)
+{
+    const int np = nt * topk;
+    int *u = (int *)malloc((size_t)np * sizeof *u);
+    float *acc = (float *)malloc((size_t)np * hidden * sizeof *acc);
+    int nu = 0;
+    for (int p = 0; p < np; p++) {
+        int seen = 0;
+        for (int j = 0; j < nu; j++)
+            if (u[j] == idx[p]) { seen = 1; break; }
+        if (!seen) u[nu++] = idx[p];
+    }
+    for (int j = 0; j < nu; j++) {
+        const int e = u[j];
+        for (int t = 0; t < nt; t++)
+            for (int k = 0; k < topk; k++)
+                if (idx[(size_t)t * topk + k] == e)
+                    orc_expert_fp4(acc + ((size_t)t * topk + k) * hidden,
+                                   x + (size_t)t * hidden, w1[e], s1[e], w3[e], s3[e],
+                                   w2[e], s2[e], hidden, inter, limit);
+    }
+    for (int t = 0; t < nt; t++) {
+        float *o = out + (size_t)t * hidden;
+        for (int i = 0; i < hidden; i++) o[i] = 0.0f;
+        for (int k = 0; k < topk; k++) {
+            const float *ak = acc + ((size_t)t * topk + k) * hidden;
+            const float wk = wts[(size_t)t * topk + k];
+            for (int i = 0; i < hidden; i++) o[i] += wk * ak[i];
+        }
+    }
+    if (uniq) memcpy(uniq, u, (size_t)nu * sizeof *u);
+    free(u);
+    free(acc);
+    return nu;
+}
+
 /* dsv4_indexer.c:64-85. scale = (1/sqrtf(D)) * (1/sqrtf(H)) in float; per
  * position a double total over heads of ReLU(dot) * w[h], dot an fma chain in
  * ascending c; out = (float)total * scale. Keys are rows of key_stride floats

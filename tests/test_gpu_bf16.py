@@ -63,15 +63,22 @@ def test_mmq_bf16_golden(gpu, dsv4):
     assert err < TOL
 
 
-def test_mmq_n_bf16_bit_identical_per_token(gpu, dsv4):
-    rng = np.random.default_rng(8)
-    rows, cols, nt = 640, 2048, 4
+@pytest.mark.parametrize("rows,cols,nt", [
+    (640, 2048, 4), (256, 7168, 64), (33, 16384, 3), (100, 200, 9), (5, 8, 2),
+    (1000, 4096, 17), (129, 1024, 64)])
+def test_mmq_n_bf16_bit_identical_per_token(gpu, dsv4, rows, cols, nt):
+    """The batched form (one pass over the weights for the batch, ragged token
+    blocks) gives every token the single-token GEMV's bits."""
+    rng = np.random.default_rng(8 + rows + nt)
     W = common.bf16_matrix(rng, (rows, cols))
     X = rng.standard_normal((nt, cols)).astype(np.float32)
     m = resident(dsv4, W, rows, cols)
+    print("bf16 mmq_n %dx%d nt %d" % (rows, cols, nt), flush=True)
     Y = dsv4.mmq_n(m, X)
     for t in range(nt):
-        assert common.bits_equal(Y[t], dsv4.mmq(m, X[t]))
+        assert common.bits_equal(Y[t], dsv4.mmq(m, X[t])), "token %d" % t
+    err = common.vec_rel_err(Y[nt - 1], oracle.matmul_bf16(X[nt - 1], W))
+    assert err < TOL
 
 
 def test_mmq_bf16_known_answer(gpu, dsv4):

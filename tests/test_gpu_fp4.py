@@ -75,15 +75,23 @@ def test_mmq_fp4_golden(gpu, dsv4):
     assert err < TOL
 
 
-def test_mmq_n_fp4_bit_identical_per_token(gpu, dsv4):
-    rng = np.random.default_rng(5)
-    rows, cols, nt = 512, 2048, 5
-    W, S = fp4_matrix(rng, rows, cols)
+@pytest.mark.parametrize("rows,cols,blk_r,blk_c,nt", [
+    (512, 2048, 1, 32, 5), (2048, 7168, 1, 32, 64), (7168, 2048, 1, 32, 9),
+    (64, 96, 1, 32, 3), (33, 4096, 1, 32, 2), (100, 16384, 1, 32, 5),
+    (256, 1024, 4, 64, 64), (130, 8192, 128, 128, 17)])
+def test_mmq_n_fp4_bit_identical_per_token(gpu, dsv4, rows, cols, blk_r, blk_c, nt):
+    """The batched form (one pass over the weights for the batch, ragged token
+    blocks) gives every token the single-token GEMV's bits."""
+    rng = np.random.default_rng(5 + rows + nt)
+    W, S = fp4_matrix(rng, rows, cols, blk_r, blk_c)
     X = rng.standard_normal((nt, cols)).astype(np.float32)
-    m = resident(dsv4, W, S, rows, cols)
+    m = resident(dsv4, W, S, rows, cols, blk_r, blk_c)
+    print("fp4 mmq_n %dx%d blk %dx%d nt %d" % (rows, cols, blk_r, blk_c, nt), flush=True)
     Y = dsv4.mmq_n(m, X)
     for t in range(nt):
-        assert common.bits_equal(Y[t], dsv4.mmq(m, X[t]))
+        assert common.bits_equal(Y[t], dsv4.mmq(m, X[t])), "token %d" % t
+    err = common.vec_rel_err(Y[nt - 1], oracle.matmul_fp4(X[nt - 1], W, S, cols, blk_r, blk_c))
+    assert err < TOL
 
 
 def test_mmq_fp4_known_answer(gpu, dsv4):

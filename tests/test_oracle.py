@@ -266,6 +266,51 @@ def test_moe_is_k_ordered_expert_sum():
     assert common.bits_equal(out, want)
 
 
+def _moe_n_batch(rng, n_exp, nt, topk, hidden, inter):
+    table = {int(e): common.fp4_expert(rng, hidden, inter)
+             for e in rng.choice(1000, n_exp, replace=False)}
+    ids = np.array(sorted(table), np.int32)
+    IDX = np.stack([rng.permutation(ids)[:topk] for _ in range(nt)]).astype(np.int32)
+    W = np.stack([common.router(rng, topk) for _ in range(nt)])
+    X = rng.standard_normal((nt, hidden)).astype(np.float32)
+    return table, IDX, W, X
+
+
+def test_moe_n_is_moe_per_token():
+    """moe_n (dsv4_layer.c:714-855): every token's row is moe() of that token,
+    bit for bit (the pair slots and the k-ordered sum of :829-839), and the
+    distinct experts come in first-request order (:728-739)."""
+    rng = np.random.default_rng(17)
+    hidden, inter = 64, 96
+    for n_exp, nt, topk in ((6, 7, 3), (3, 5, 3), (12, 1, 4), (9, 16, 2)):
+        table, IDX, W, X = _moe_n_batch(rng, n_exp, nt, topk, hidden, inter)
+        out, uniq = oracle.moe_fp4_n(X, table, IDX, W, hidden, inter, 10.0)
+        want_u = []
+        for e in IDX.reshape(-1):
+            if int(e) not in want_u:
+                want_u.append(int(e))
+        assert uniq.tolist() == want_u
+        for t in range(nt):
+            one = oracle.moe_fp4(X[t], [table[int(e)] for e in IDX[t]], W[t], hidden, inter,
+                                 10.0)
+            assert common.bits_equal(out[t], one), (n_exp, nt, topk, t)
+
+
+@ref_only
+def test_batched_fp4_matmul_is_per_token_in_compiled_reference():
+    """What makes moe_n's pair slots equal moe()'s: the compiled reference's
+    dsv4_matmul_fp4_n gives every token the single-token bits of the oracle's
+    (and the reference's) dsv4_matmul_fp4 -- for a gate/up and a down shape."""
+    rng = np.random.default_rng(18)
+    for rows, cols, nt in ((96, 64, 5), (64, 96, 9), (256, 512, 3)):
+        W = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)
+        S = (127 + rng.integers(-6, 3, (rows, cols // 32))).astype(np.uint8)
+        X = rng.standard_normal((nt, cols)).astype(np.float32)
+        Y = oracle.ref_matmul_fp4_n(X, W, S, cols)
+        for t in range(nt):
+            assert common.bits_equal(Y[t], oracle.matmul_fp4(X[t], W, S, cols))
+
+
 # ------------------------------------------------------------ indexer / top-k
 def test_indexer_known_answers():
     """test_indexer.c:23-164."""

@@ -87,7 +87,8 @@ def parse():
     ap.add_argument("--no-detail", action="store_true",
                     help="headline sweep only (skip C1/C3/C4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "attn", "copy"], default=None,
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "attn", "prefill", "moen", "copy"],
+                    default=None,
                     help="time one configuration only (for profiling runs); "
                          "'copy' runs a plain 1 GiB device-to-device copy whose "
                          "known size calibrates the FETCH_SIZE/WRITE_SIZE counters")
@@ -548,6 +549,74 @@ class Bench:
         del W13, S13, W2, S2
         return us, eager, moe_bytes(hidden, inter, topk)
 
+    # ------------------------------------------------- batched routed experts
+    def moe_n_run(self, nts=(1, 4, 16, 64), calls=10):
+        """The batched routed experts (dsv4_gpu_moe_fp4_n_d, the routed half
+        of moe_n) at C3's expert shape: 256 experts resident, every token of
+        the batch routed to 8 of them by a seeded random draw, so experts
+        repeat across the batch. Per batch size: us per call, the distinct
+        experts it streams, their weight bytes over the time, and the time of
+        the same tokens through the single-token call one by one."""
+        import ctypes
+        torch, np = self.torch, self.np
+        hidden, inter, topk, n_exp = 7168, 2048, 8, 256
+        g = torch.Generator(device=self.dev)
+        g.manual_seed(1)
+        wb13, sb13 = inter * hidden // 2, inter * hidden // 32
+        wb2, sb2 = hidden * inter // 2, hidden * inter // 32
+        W13 = torch.randint(0, 256, (n_exp, 2, wb13), dtype=torch.uint8, device=self.dev,
+                            generator=g)
+        S13 = torch.randint(121, 130, (n_exp, 2, sb13), dtype=torch.uint8, device=self.dev,
+                            generator=g)
+        W2 = torch.randint(0, 256, (n_exp, wb2), dtype=torch.uint8, device=self.dev,
+                           generator=g)
+        S2 = torch.randint(121, 130, (n_exp, sb2), dtype=torch.uint8, device=self.dev,
+                           generator=g)
+        torch.cuda.synchronize()
+        D = self.dsv4
+        layer = 61
+        for e in range(n_exp):
+            ew = D.DSV4ExpertW(
+                D.DSV4QMat(W13[e, 0].data_ptr(), S13[e, 0].data_ptr(), D.WFP4, inter, hidden, 1, 32),
+                D.DSV4QMat(W13[e, 1].data_ptr(), S13[e, 1].data_ptr(), D.WFP4, inter, hidden, 1, 32),
+                D.DSV4QMat(W2[e].data_ptr(), S2[e].data_ptr(), D.WFP4, hidden, inter, 1, 32))
+            assert self.L.dsv4_gpu_bind_expert_d(layer, e, ctypes.byref(ew)) == 0
+        per_expert = 2 * inter * (hidden // 2 + hidden // 32) + hidden * (inter // 2 + inter // 32)
+        rng = np.random.default_rng(3)
+        out = {}
+        for nt in nts:
+            sets = 8
+            ids = [np.stack([rng.permutation(n_exp)[:topk] for _ in range(nt)]).astype(np.int32)
+                   for _ in range(sets)]
+            ws = [np.stack([self.common.router(rng, topk) for _ in range(nt)]) for _ in range(sets)]
+            d_ids = [self.t(a) for a in ids]
+            d_ws = [self.t(a) for a in ws]
+            X = torch.randn((nt, hidden), device=self.dev)
+            O = torch.empty((nt, hidden), device=self.dev)
+
+            def go(i, sp):
+                j = i % sets
+                assert self.L.dsv4_gpu_moe_fp4_n_d(O.data_ptr(), X.data_ptr(), layer,
+                                                   d_ids[j].data_ptr(), d_ws[j].data_ptr(), nt,
+                                                   topk, hidden, inter, 10.0, sp) == 0
+
+            def one(i, sp):
+                j = i % sets
+                for t in range(nt):
+                    assert self.L.dsv4_gpu_moe_fp4_d(
+                        O[t].data_ptr(), X[t].data_ptr(), layer,
+                        d_ids[j][t].data_ptr(), d_ws[j][t].data_ptr(), topk, hidden, inter,
+                        10.0, sp) == 0
+            go(0, self.sp)
+            us, _ = self.blocked_us(go, calls)
+            us1, _ = self.blocked_us(one, max(2, calls // max(1, nt // 4)))
+            uniq = float(np.mean([len(np.unique(a)) for a in ids]))
+            out[str(nt)] = {"us": round(us, 3), "distinct_experts": uniq,
+                            "GBps_distinct_weights": round(uniq * per_expert / us / 1e3, 1),
+                            "token_by_token_us": round(us1, 3)}
+        del W13, S13, W2, S2
+        return out
+
     # ------------------------------------------------------------ C4
     def c4_run(self, steps, warmup):
         torch, np = self.torch, self.np
@@ -825,6 +894,18 @@ def main():
                "trials_ms": [round(t, 4) for t in trial_ms],
                "eager_ms": round(eager_ms, 4), "graph_ms": round(graph_ms, 4),
                "per_shape_us": [round(u, 3) for u in per_us]}))
+        B.L.dsv4_gpu_shutdown()
+        return
+    if args.only == "prefill":
+        curve = {}
+        for nt in (1, 2, 4, 8, 16, 32, 64):
+            us, gf = B.gemv_n_run(nt=nt, calls=20 if nt < 64 else 30)
+            curve[str(nt)] = {"us": round(us, 3), "TFLOPs": round(gf / us * 1e3, 2)}
+        emit({"config": "prefill_fp8_7168x7168", "by_tokens": curve})
+        B.L.dsv4_gpu_shutdown()
+        return
+    if args.only == "moen":
+        emit({"config": "moe_n", "by_tokens": B.moe_n_run()})
         B.L.dsv4_gpu_shutdown()
         return
     if args.only in ("c1", "c3", "c4", "attn"):

@@ -857,7 +857,7 @@ int dsv4_fp8_gemv_groups_launch(float *y, const float *x, const uint8_t *W,
 
 int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,
                            const void *S, int sfmt, int rows, int cols,
-                           int blk_r, int blk_c, int nt, hipStream_t st)
+                           int blk_r, int blk_c, int nt, hipStream_t st, void *xscratch)
 {
     if (rows <= 0 || cols <= 0 || nt <= 0 || blk_r <= 0 || blk_c <= 0) {
         DSV4_ERR("fp8 gemv_n: bad shape %dx%d nt %d", rows, cols, nt);
@@ -867,7 +867,7 @@ int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,
         return fp8_gemv(y, x, W, S, sfmt, rows, cols, blk_r, blk_c, Fp8Groups{}, st);
     if (mx_form(sfmt, x, W, cols, blk_r, blk_c))
         return dsv4_fp8_mxn_launch(y, x, W, (const uint8_t *)S, rows, cols, blk_r, blk_c, nt,
-                                   st);
+                                   st, xscratch);
     const int sc = (cols + blk_c - 1) / blk_c;
     Fp8Geom g;
     const bool aligned = (((uintptr_t)x | (uintptr_t)W) & 15) == 0;

@@ -448,6 +448,68 @@ __device__ __forceinline__ void xn_terms(uint16_t *bl, const f32x4 *v, int ntok,
     }
 }
 
+/* The batch's x as bf16 term planes, once per call (k_fp8_xsplit): xt[t][p]
+ * is term p of token t's row, padded with zeros to cpad = a whole number of
+ * units; the batched kernel then copies a unit's terms into LDS instead of
+ * every workgroup forming them again. Same terms3, so the same bits. */
+__global__ void __launch_bounds__(256)
+k_fp8_xsplit(uint16_t *__restrict__ xt, const float *__restrict__ x, int nt, int cols,
+             int cpad)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;           /* 4 columns per thread */
+    const int per = cpad >> 2;
+    if (i >= nt * per) return;
+    const int t = i / per, c = 4 * (i - t * per);
+    float e[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) e[j] = c + j < cols ? x[(size_t)t * cols + c + j] : 0.0f;
+    uint32_t tt[4][XNT];
+#pragma unroll
+    for (int j = 0; j < 4; j++) terms3(e[j], tt[j]);
+#pragma unroll
+    for (int p = 0; p < XNT; p++)
+        *reinterpret_cast<uint2 *>(xt + ((size_t)t * XNT + p) * cpad + c) =
+            uint2{tt[0][p] | (tt[1][p] << 16), tt[2][p] | (tt[3][p] << 16)};
+}
+
+/* 16-byte pieces of the term planes per thread per unit: a group's tpg
+ * tokens x XNT planes x XU / 8 pieces over the workgroup's 64 MW threads. */
+template <int NT>
+struct XpDim {
+    static constexpr int M = (XTOK * NT * XNT * (XU / 8) + 64 * MW - 1) / (64 * MW);
+};
+
+/* Request piece i = tid + 64 MW m of unit u's term rows (row = token * XNT +
+ * plane): rows past the group's tokens read its first row (unconditional
+ * loads) and are stored as zeros. */
+template <int NT>
+__device__ __forceinline__ void xp_load(u32x4 *v, const uint16_t *xt, int t0, int ntok, int u,
+                                        int cpad, int tpg)
+{
+#pragma unroll
+    for (int m = 0; m < XpDim<NT>::M; m++) {
+        const int i = (int)threadIdx.x + 64 * MW * m;
+        const int row = i / (XU / 8), pc = i % (XU / 8);
+        const bool in = row < tpg * XNT && row / XNT < ntok;
+        v[m] = *(const DSV4_GLOBAL u32x4 *)(xt + (in ? ((size_t)t0 * XNT + row) * cpad +
+                                                         XU * u + 8 * pc
+                                                       : (size_t)t0 * XNT * cpad));
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void xp_store(uint16_t *bl, const u32x4 *v, int ntok, int tpg)
+{
+#pragma unroll
+    for (int m = 0; m < XpDim<NT>::M; m++) {
+        const int i = (int)threadIdx.x + 64 * MW * m;
+        const int row = i / (XU / 8), pc = i % (XU / 8);
+        if (row < tpg * XNT)
+            *reinterpret_cast<u32x4 *>(bl + (size_t)row * BP + 8 * pc) =
+                row / XNT < ntok ? v[m] : u32x4{0u, 0u, 0u, 0u};
+    }
+}
+
 /* Workgroup (blockIdx.x: MW 16-row tiles, one per wave; blockIdx.y: a group
  * of tpg tokens starting at t0). Per unit u: the workgroup turns x(u), which
  * it requested one unit earlier, into terms in B buffer u % 2, each wave
@@ -460,7 +522,7 @@ template <int NT, bool UNI>
 __global__ void __launch_bounds__(64 * MW)
 k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__restrict__ W,
           const uint8_t *__restrict__ S, int rows, int cols, int sc, int blk_r, uint32_t bc_m,
-          int nt, int tpg)
+          int nt, int tpg, const uint16_t *__restrict__ xt, int cpad)
 {
     extern __shared__ __attribute__((aligned(16))) unsigned char xnlds[];
     const int lane = threadIdx.x & 63;
@@ -492,9 +554,24 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
         tot[n] = v4f{0.f, 0.f, 0.f, 0.f};
     }
     const int nu = (cols + XU - 1) / XU;
-    f32x4 XR[2][XnDim<NT>::M];
+    /* x(u): the pre-split term planes when the caller gave them (copied
+     * into LDS as they are), else the f32 row (turned into terms here) */
+    constexpr int XM = XpDim<NT>::M > XnDim<NT>::M ? XpDim<NT>::M : XnDim<NT>::M;
+    u32x4 XR[XM];                       /* x(u + 1) in flight while unit u runs */
     XUnit<UNI> P[2];
-    xn_load<NT>(XR[0], x, t0, ntok, 0, cols, tpg);
+    auto xload = [&](u32x4 *v, int u) {
+        if (xt)
+            xp_load<NT>(v, xt, t0, ntok, u, cpad, tpg);
+        else
+            xn_load<NT>(reinterpret_cast<f32x4 *>(v), x, t0, ntok, XU * u, cols, tpg);
+    };
+    auto xstore = [&](uint16_t *bl, const u32x4 *v, int u) {
+        if (xt)
+            xp_store<NT>(bl, v, ntok, tpg);
+        else
+            xn_terms<NT>(bl, reinterpret_cast<const f32x4 *>(v), ntok, XU * u, cols, tpg);
+    };
+    xload(XR, 0);
     /* uniform scales: the current segment's (ssb) and the next one's */
     uint32_t ssb = UNI ? xs_seg(S, srow, bc_m, 0, cols, lane) : 0u, ssn = 0u;
     __builtin_amdgcn_sched_barrier(0);
@@ -507,7 +584,7 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
             const int u = s0 + j;
             uint16_t *bl = (j & 1) ? bl1 : bl0;
             if (u < nu) {
-                xn_terms<NT>(bl, XR[j & 1], ntok, XU * u, cols, tpg);
+                xstore(bl, XR, u);
                 xu_stage(buf, P[j & 1], lane);
             }
             uint32_t sb[4];
@@ -518,7 +595,7 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
              * then leaves unit u + 2 in flight, and no load sits in a branch
              * that would make the waits fall back to waiting for all */
             __builtin_amdgcn_sched_barrier(0);
-            xn_load<NT>(XR[(j + 1) & 1], x, t0, ntok, XU * min(u + 1, nu - 1), cols, tpg);
+            xload(XR, min(u + 1, nu - 1));
             if (UNI && j == XSEG_U - 2)        /* before the next segment's first unit */
                 ssn = xs_seg(S, srow, bc_m, XU * (min(s0 + XSEG_U, nu - 1) & ~(XSEG_U - 1)),
                              cols, lane);
@@ -704,8 +781,14 @@ int dsv4_fp8_mx_launch(const Dsv4Fp8Mx &a, hipStream_t st)
     return 0;
 }
 
+size_t dsv4_fp8_mxn_scratch_bytes(int cols, int nt)
+{
+    const size_t cpad = (size_t)((cols + XU - 1) / XU) * XU;
+    return (size_t)nt * XNT * cpad * 2;
+}
+
 int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_t *S, int rows,
-                        int cols, int blk_r, int blk_c, int nt, hipStream_t st)
+                        int cols, int blk_r, int blk_c, int nt, hipStream_t st, void *xscratch)
 {
     if (!dsv4_fp8_mx_ok(0, cols, blk_r, blk_c) || rows <= 0 || nt < 1 || nt > DSV4_MAX_BATCH) {
         DSV4_ERR("fp8 mxn: shape not taken (%dx%d, nt %d)", rows, cols, nt);
@@ -717,7 +800,10 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
      * running sums of 4 tiles stay in registers); more tokens take more
      * workgroups along y, each reading the weights again */
     const int ntile = (nt + XTOK - 1) / XTOK;
-    const int NTc = ntile >= 4 ? 4 : ntile >= 2 ? (ntile == 3 ? 3 : 2) : 1;
+    int ntmax = mx_env("DSV4_GPU_MXN_NT", 4);
+    ntmax = ntmax < 1 ? 1 : ntmax > 7 ? 7 : ntmax;
+    const int ngrp = (ntile + ntmax - 1) / ntmax;      /* fewest weight passes */
+    const int NTc = (ntile + ngrp - 1) / ngrp;         /* then the fewest tiles each */
     const int tpg = XTOK * NTc < nt ? XTOK * NTc : nt;
     const int groups = (nt + tpg - 1) / tpg;
     const size_t lds = 2 * (size_t)tpg * XNT * BP * 2 + (size_t)MW * XUNIT_B;
@@ -725,24 +811,37 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
     static bool opted = false;
     if (!opted) {
         optin(k_fp8_mxn<1, false>); optin(k_fp8_mxn<2, false>); optin(k_fp8_mxn<3, false>);
-        optin(k_fp8_mxn<4, false>); optin(k_fp8_mxn<1, true>); optin(k_fp8_mxn<2, true>);
-        optin(k_fp8_mxn<3, true>); optin(k_fp8_mxn<4, true>);
+        optin(k_fp8_mxn<4, false>); optin(k_fp8_mxn<5, false>); optin(k_fp8_mxn<6, false>);
+        optin(k_fp8_mxn<7, false>); optin(k_fp8_mxn<1, true>); optin(k_fp8_mxn<2, true>);
+        optin(k_fp8_mxn<3, true>); optin(k_fp8_mxn<4, true>); optin(k_fp8_mxn<5, true>);
+        optin(k_fp8_mxn<6, true>); optin(k_fp8_mxn<7, true>);
         opted = true;
     }
     const bool uni = xs_uniform(blk_r, blk_c);
+    const int cpad = ((cols + XU - 1) / XU) * XU;
+    const uint16_t *xt = (const uint16_t *)xscratch;
+    if (xt) {
+        const int n4 = nt * (cpad / 4);
+        hipLaunchKernelGGL(k_fp8_xsplit, dim3((n4 + 255) / 256), dim3(256), 0, st,
+                           (uint16_t *)xscratch, x, nt, cols, cpad);
+        HIP_OK(hipGetLastError(), "fp8 mxn x split launch");
+    }
 #define XN(NTV) do {                                                                           \
         if (uni)                                                                               \
             hipLaunchKernelGGL((k_fp8_mxn<NTV, true>), grid, dim3(64 * MW), lds, st, y, x, W, S, \
-                               rows, cols, sc, blk_r, bc_m, nt, tpg);                           \
+                               rows, cols, sc, blk_r, bc_m, nt, tpg, xt, cpad);                 \
         else                                                                                   \
             hipLaunchKernelGGL((k_fp8_mxn<NTV, false>), grid, dim3(64 * MW), lds, st, y, x, W,  \
-                               S, rows, cols, sc, blk_r, bc_m, nt, tpg);                        \
+                               S, rows, cols, sc, blk_r, bc_m, nt, tpg, xt, cpad);              \
     } while (0)
     switch (NTc) {
     case 1: XN(1); break;
     case 2: XN(2); break;
     case 3: XN(3); break;
-    default: XN(4); break;
+    case 4: XN(4); break;
+    case 5: XN(5); break;
+    case 6: XN(6); break;
+    default: XN(7); break;
     }
 #undef XN
     HIP_OK(hipGetLastError(), "fp8 mxn launch");

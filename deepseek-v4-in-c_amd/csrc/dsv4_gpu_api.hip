@@ -108,7 +108,7 @@ int res_insert(const Res &r)
 }
 std::vector<LayerExperts> g_layers;
 Arena g_ar;
-Scratch g_moe, g_attn, g_scores, g_index, g_amax;
+Scratch g_moe, g_attn, g_scores, g_index, g_amax, g_xsplit;
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -509,7 +509,7 @@ void dsv4_gpu_shutdown(void)
     }
     g_layers.clear();
     attn_blocks_free();
-    for (Scratch *s : {&g_moe, &g_attn, &g_scores, &g_index, &g_amax}) {
+    for (Scratch *s : {&g_moe, &g_attn, &g_scores, &g_index, &g_amax, &g_xsplit}) {
         if (s->p) (void)hipFree(s->p);
         s->p = nullptr;
         s->cap = 0;
@@ -565,6 +565,8 @@ void dsv4_gpu_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
     Stage s;
     const size_t xo = s.in(x, (size_t)nt * r->cols * sizeof(float));
     const size_t yo = s.add((size_t)nt * m->rows * sizeof(float));
+    const bool fp8 = r->wdt != DSV4_WFP4 && r->wdt != DSV4_WBF16;
+    const size_t to = fp8 ? s.add(dsv4_fp8_mxn_scratch_bytes(r->cols, nt)) : 0;
     size_t end;
     if (stage_push(s, &end) != 0) abort();
     int rc = 0;
@@ -580,7 +582,8 @@ void dsv4_gpu_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
     } else {
         rc = dsv4_fp8_gemv_n_launch(
             (float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
-            v.w, v.s, r->sfmt, m->rows, r->cols, r->blk_r, r->blk_c, nt, g_stream);
+            v.w, v.s, r->sfmt, m->rows, r->cols, r->blk_r, r->blk_c, nt, g_stream,
+            g_ar.d + to);
     }
     if (rc != 0 ||
         stage_pull(yo, (size_t)nt * m->rows * sizeof(float), y) != 0) {
@@ -610,8 +613,9 @@ int dsv4_gpu_fp8_gemv_n_d(float *d_y, const float *d_x, const uint8_t *d_w,
         DSV4_ERR("fp8_gemv_n_d: bad arguments (nt %d)", nt);
         return -1;
     }
+    if (scratch_reserve(g_xsplit, dsv4_fp8_mxn_scratch_bytes(cols, nt)) != 0) return -1;
     return dsv4_fp8_gemv_n_launch(d_y, d_x, d_w, d_s, scale_fmt, rows, cols, 128, 128, nt,
-                                  as_stream(stream));
+                                  as_stream(stream), g_xsplit.p);
 }
 
 int dsv4_gpu_fp4_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,

@@ -57,9 +57,13 @@ struct Dsv4Fp8Mx {
 bool dsv4_fp8_mx_ok(int sfmt, int cols, int blk_r, int blk_c);
 int dsv4_fp8_mx_launch(const Dsv4Fp8Mx &a, hipStream_t st);
 /* The batched matrix-core form: y[nt][rows], x[nt][cols]; every (row,
- * token) has the bits of dsv4_fp8_mx_launch on that token. */
+ * token) has the bits of dsv4_fp8_mx_launch on that token. xscratch
+ * (optional, dsv4_fp8_mxn_scratch_bytes of device memory): x is split into
+ * its bf16 terms there once, instead of in every workgroup. */
+size_t dsv4_fp8_mxn_scratch_bytes(int cols, int nt);
 int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_t *S, int rows,
-                        int cols, int blk_r, int blk_c, int nt, hipStream_t st);
+                        int cols, int blk_r, int blk_c, int nt, hipStream_t st,
+                        void *xscratch = nullptr);
 
 /* MXFP4 GEMV (dsv4_matmul_fp4): W e2m1 nibbles [rows][cols/2], S E8M0 bytes
  * [ceil(rows/blk_r)][ceil(cols/blk_c)]. _ok: the shapes it takes (cols a
@@ -113,10 +117,12 @@ int dsv4_embed_row_launch(float *d_dst, const void *d_table, int wdt, long long 
                           int hidden, hipStream_t st);
 
 /* Batched: y[nt][rows], x[nt][cols]; per (row, token) bit-identical to the
- * GEMV above. */
+ * GEMV above. xscratch: optional device memory of dsv4_fp8_mxn_scratch_bytes
+ * for the matrix-core form's split of x. */
 int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,
                            const void *S, int sfmt, int rows, int cols,
-                           int blk_r, int blk_c, int nt, hipStream_t st);
+                           int blk_r, int blk_c, int nt, hipStream_t st,
+                           void *xscratch = nullptr);
 
 /* A matrix whose bytes are in HBM already (m->w / m->s device addresses,
  * e.g. read there from a checkpoint) made resident under those addresses;

@@ -208,6 +208,22 @@ def test_batched_bit_identical(gpu, dsv4, rows, cols, nt):
     assert common.vec_rel_err(yn, oracle.matmul_fp8(x, W, Se)) < TOL
 
 
+@pytest.mark.parametrize("ntmax", ["1", "3", "5", "6", "7"])
+def test_batched_token_tiles_keep_bits(gpu, dsv4, monkeypatch, ntmax):
+    """DSV4_GPU_MXN_NT (column tiles of five tokens per workgroup, so how many
+    passes over the weights a batch takes) only reshapes the batched launch:
+    every setting gives each token the single-token GEMV's bits."""
+    monkeypatch.setenv("DSV4_GPU_MXN_NT", ntmax)
+    for rows, cols, nt in ((300, 1536, 64), (129, 7168, 37), (70, 2096, 11)):
+        W, Sf, Se, _ = common.fp8_problem(23, rows, cols)
+        x = np.random.default_rng(24).standard_normal((nt, cols), dtype=np.float32)
+        y1, m = _run(dsv4, W, Se, x[0])
+        say("fp8 mxn %dx%d nt %d MXN_NT %s" % (rows, cols, nt, ntmax))
+        yn = dsv4.mmq_n(m, x)
+        for t in range(nt):
+            assert common.bits_equal(yn[t], dsv4.mmq(m, x[t])), (ntmax, rows, t)
+
+
 @pytest.mark.parametrize("blk_r,blk_c", [(1, 32), (16, 64), (128, 128), (4, 48), (256, 256)])
 def test_matrix_core_form_blockings(gpu, dsv4, blk_r, blk_c):
     """E8M0 scale grids other than 128 x 128 (a scale per lane piece in the

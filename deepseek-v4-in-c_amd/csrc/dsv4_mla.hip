@@ -15,10 +15,14 @@
  * TOP-K (dsv4_indexer.c:92-106), bit-exact: the k largest, ordered by score
  * descending, ties to the lower index. Scores map to order-preserving 32-bit
  * keys (-0.0 folded into +0.0, since the reference's `>` treats them as
- * equal); a radix select over the key's bits 31..21 (the histogram), 20..10
- * and 9..0 finds T, the key of the k-th largest, and how many elements equal
- * to T are taken; the elements > T are ordered by (key desc, index asc) by
- * counting, for each, the candidates ahead of it (k_tk_part, k_tk_final).
+ * equal). The histogram of the key's bits 31..21 gives B, the bin of the
+ * k-th largest; every element above B is taken, and each is placed by
+ * counting the composites (key << 32 | ~index: score descending, ties to
+ * the lower index) ahead of it; an element of B likewise among B's, taken
+ * when it ranks below the k-th's place in B. Past 4096 elements in B, a
+ * radix select over bits 20..10 and 9..0 first finds T, the key of the k-th
+ * largest, and how many elements equal to T are taken (k_tk_part,
+ * k_tk_final).
  * Up to 4096 scores, one launch ranks every element directly (k_tk_small).
  * A NaN score makes every output slot -1: the reference's scan takes a NaN
  * exactly when it is the first index not yet taken, an order the keys cannot
@@ -72,10 +76,18 @@ constexpr int TK_BINS = 2048;                   /* top 11 bits of the key */
 constexpr int TK_SLICES = 16;                   /* spread of the global atomics */
 
 /* meta words in the scratch */
-constexpr int MT_ABOVE = 1;                     /* cand[] append counter (word 0 unused) */
 constexpr int MT_BIN = 2;                       /* B */
 constexpr int MT_KREM = 3;                      /* rank of the k-th inside B */
 constexpr int MT_NAN = 4;                       /* nonzero: a score is NaN */
+constexpr int MT_CNT = 6;                       /* words 6-7: one 64-bit append counter,
+                                                 * cand[] in the low word, bsel[] high */
+
+/* Restart the top-k's append counter and NaN flag (one thread). */
+__device__ __forceinline__ void meta_restart(uint32_t *meta)
+{
+    *reinterpret_cast<unsigned long long *>(meta + MT_CNT) = 0ull;
+    meta[MT_NAN] = 0u;
+}
 
 
 /* Order-preserving 32-bit key of a score: a > b as floats iff fkey(a) >
@@ -357,7 +369,7 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
     const float tf = (float)total;
     const float sc = tf * scale;
     if (t < n) out[t] = sc;
-    if (HIST && blockIdx.x == 0 && lane == 0) { meta[MT_ABOVE] = 0u; meta[MT_NAN] = 0u; }
+    if (HIST && blockIdx.x == 0 && lane == 0) meta_restart(meta);
     if (HIST)
         hist_push_global(hist + (blockIdx.x % TK_SLICES) * TK_BINS, t < n,
                          fkey(sc) >> 21, lane);
@@ -492,7 +504,7 @@ k_iscore_kh(float *__restrict__ out, uint32_t *__restrict__ hist, uint32_t *__re
     }
     if (HIST) {
         /* the top-k's level-1 histogram, by the waves that hold keys */
-        if (blockIdx.x == 0 && threadIdx.x == 0) { meta[MT_ABOVE] = 0u; meta[MT_NAN] = 0u; }
+        if (blockIdx.x == 0 && threadIdx.x == 0) meta_restart(meta);
         if ((int)(threadIdx.x & ~63u) < kpw)
             hist_push_global(hist + (blockIdx.x % TK_SLICES) * TK_BINS,
                              (int)threadIdx.x < kpw && tt < n, fkey(sc) >> 21,
@@ -522,13 +534,15 @@ void launch_iscore(bool vec, int grid, int thr, size_t lds, hipStream_t st,
 /* Top-k in two passes after the level-1 histogram (built by the score
  * kernel, or by k_tk_hist for stand-alone scores):
  *   k_tk_part   many workgroups: the bin B of the k-th largest from the
- *               histogram; elements of higher bins go to cand[] (any order),
- *               elements of B to a per-workgroup list in index order;
- *   k_tk_final  many workgroups: each repeats the refinement of B's list
- *               (levels 2 and 3 give T, the exact key of the k-th largest),
- *               then places its share of the candidates > T by counting the
- *               candidates ahead of each; the first need_eq elements == T
- *               follow them in index order. */
+ *               histogram; elements of higher bins go to cand[], those of B
+ *               to bsel[] (any order, as composites), and also to a
+ *               per-workgroup list in index order;
+ *   k_tk_final  many workgroups, each placing a share of the elements: from
+ *               cand[] and bsel[] directly when B holds at most RF_LIST
+ *               elements, else after a refinement of B's list (levels 2 and
+ *               3 give T, the exact key of the k-th largest) that every
+ *               workgroup repeats; the first need_eq elements == T then
+ *               follow the candidates > T in index order. */
 
 constexpr int PT_THREADS = 256;                 /* partition workgroup */
 constexpr int PT_EPT = 4;                       /* elements per thread */
@@ -552,7 +566,7 @@ k_tk_hist(uint32_t *__restrict__ hist, uint32_t *__restrict__ meta,
     const int i = blockIdx.x * 256 + threadIdx.x;
     const bool live = i < n;
     const uint32_t bin = live ? fkey(scores[i]) >> 21 : 0u;
-    if (i == 0) { meta[MT_ABOVE] = 0u; meta[MT_NAN] = 0u; }
+    if (i == 0) meta_restart(meta);
     hist_push_global(hist + (blockIdx.x % TK_SLICES) * TK_BINS, live, bin,
                      threadIdx.x & 63);
 }
@@ -631,8 +645,9 @@ __device__ __forceinline__ uint32_t tk_scan(uint32_t v, uint32_t *wsum, uint32_t
  * index order = (slot, wave, lane)). Every workgroup reads the whole sliced
  * histogram and finds the same B. */
 __global__ void __launch_bounds__(PT_THREADS)
-k_tk_part(unsigned long long *__restrict__ cand, uint32_t *__restrict__ meta,
-          uint32_t *__restrict__ bcnt, unsigned long long *__restrict__ blist,
+k_tk_part(unsigned long long *__restrict__ cand, unsigned long long *__restrict__ bsel,
+          uint32_t *__restrict__ meta, uint32_t *__restrict__ bcnt,
+          unsigned long long *__restrict__ blist,
           const uint32_t *__restrict__ hist_g, const float *__restrict__ scores,
           int n, int k)
 {
@@ -683,37 +698,47 @@ k_tk_part(unsigned long long *__restrict__ cand, uint32_t *__restrict__ meta,
     const uint32_t B = res[0];
     if (blockIdx.x == 0 && tid == 0) { meta[MT_BIN] = B; meta[MT_KREM] = res[1]; }
 
-    /* elements of higher bins: candidates, appended in any order */
-    unsigned long long ma[PT_EPT];
-    uint32_t na = 0u;
+    /* elements of higher bins and of B, as composites (key << 32 | ~index),
+     * appended in any order to cand[] and bsel[]: one 64-bit atomic per
+     * wave takes both places (cand[] count in the low word, bsel[] high) */
+    unsigned long long ma[PT_EPT], mb[PT_EPT];
+    uint32_t na = 0u, nbw = 0u;
 #pragma unroll
     for (int m = 0; m < PT_EPT; m++) {
-        ma[m] = __ballot(e0 + m * PT_THREADS < n && (key[m] >> 21) > B);
+        const bool in = e0 + m * PT_THREADS < n;
+        ma[m] = __ballot(in && (key[m] >> 21) > B);
+        mb[m] = __ballot(in && (key[m] >> 21) == B);
         na += (uint32_t)__popcll(ma[m]);
+        nbw += (uint32_t)__popcll(mb[m]);
     }
-    if (na) {
-        uint32_t at = 0u;
-        if (lane == 0) at = atomicAdd(&meta[MT_ABOVE], na);
-        at = (uint32_t)__shfl((int)at, 0, 64);
+    if (na | nbw) {
+        unsigned long long at = 0ull;
+        if (lane == 0)
+            at = atomicAdd(reinterpret_cast<unsigned long long *>(meta + MT_CNT),
+                           (unsigned long long)na | ((unsigned long long)nbw << 32));
+        uint32_t pa = (uint32_t)__shfl((int)(uint32_t)at, 0, 64);
+        uint32_t pb = (uint32_t)__shfl((int)(uint32_t)(at >> 32), 0, 64);
 #pragma unroll
         for (int m = 0; m < PT_EPT; m++) {
+            const uint32_t i = (uint32_t)(e0 + m * PT_THREADS);
+            const unsigned long long comp = ((unsigned long long)key[m] << 32) | (0xFFFFFFFFull - i);
             if ((ma[m] >> lane) & 1ull) {
-                const uint32_t pos = at + (uint32_t)__popcll(ma[m] & lt);
-                const uint32_t i = (uint32_t)(e0 + m * PT_THREADS);
-                if (pos < (uint32_t)TK_KMAX)
-                    cand[pos] = ((unsigned long long)key[m] << 32) | (0xFFFFFFFFull - i);
+                const uint32_t pos = pa + (uint32_t)__popcll(ma[m] & lt);
+                if (pos < (uint32_t)TK_KMAX) cand[pos] = comp;
+            } else if ((mb[m] >> lane) & 1ull) {
+                const uint32_t pos = pb + (uint32_t)__popcll(mb[m] & lt);
+                if (pos < (uint32_t)RF_LIST) bsel[pos] = comp;
             }
-            at += (uint32_t)__popcll(ma[m]);
+            pa += (uint32_t)__popcll(ma[m]);
+            pb += (uint32_t)__popcll(mb[m]);
         }
     }
 
-    /* elements of B: this workgroup's list, in index order */
-    unsigned long long mb[PT_EPT];
+    /* elements of B, again: this workgroup's list, in index order (read by
+     * the final pass only when B holds more than RF_LIST elements) */
 #pragma unroll
-    for (int m = 0; m < PT_EPT; m++) {
-        mb[m] = __ballot(e0 + m * PT_THREADS < n && (key[m] >> 21) == B);
+    for (int m = 0; m < PT_EPT; m++)
         if (lane == 0) scnt[m][wid] = (uint32_t)__popcll(mb[m]);
-    }
     __syncthreads();
     uint32_t off[PT_EPT], tot = 0u;
 #pragma unroll
@@ -732,35 +757,73 @@ k_tk_part(unsigned long long *__restrict__ cand, uint32_t *__restrict__ meta,
     if (tid == 0) bcnt[blockIdx.x] = tot;
 }
 
-/* Final pass: workgroup b orders candidates [RK_EPW b, RK_EPW (b + 1)).
- * Every workgroup first repeats the (small) refinement of bin B: B's
- * elements, in index order, are the lists of the G partition workgroups one
- * after another (entry j of the whole list lies in the list of the
- * workgroup w with pfx[w] <= j < pfx[w + 1]), staged in LDS when they fit,
- * read from global memory otherwise. Levels 2 and 3 of the radix select over
- * that list give T and need_eq; the candidates -- cand[] from the partition
- * plus the list's elements > T, in list order -- are the same array in every
- * workgroup, and each candidate's position is the number of candidates ahead
- * of it. Workgroup 0 also writes the first need_eq elements == T after them;
- * every workgroup clears its share of the level-1 histogram. */
+/* Final pass. The composites (key << 32 | ~index) order the scores as the
+ * output does, score descending with ties to the lower index, and they are
+ * distinct: an element's place is the number of composites ahead of it.
+ *
+ * Direct form (B holds at most RF_LIST elements, the usual case): the
+ * elements above B (cand[], all selected) and those of B (bsel[]) make one
+ * array u of c_above + nb composites, cand[] first, and workgroup b places
+ * the elements [RK_EPW b, RK_EPW (b + 1)) of u. An element above B is ahead
+ * of every element of B, so it counts only the cand[] composites ahead of it
+ * and lands there; an element of B counts only B's, r of them, and is
+ * selected when r < krem (the k-th largest is the krem-th of B), landing at
+ * c_above + r. A workgroup stages only the part(s) of u its elements are in,
+ * in one batch of loads issued right after the meta words.
+ *
+ * Refinement form (B larger than RF_LIST): B's elements, in index order,
+ * are the lists of the G partition workgroups one after another (entry j of
+ * the whole list lies in the list of the workgroup w with pfx[w] <= j <
+ * pfx[w + 1]), read from global memory. Levels 2 and 3 of the radix select
+ * over that list give T, the exact key of the k-th largest, and need_eq;
+ * the candidates -- cand[] plus the list's elements > T, in list order --
+ * are the same array in every workgroup, each workgroup places RK_EPW of
+ * them by counting, and workgroup 0 writes the first need_eq elements == T
+ * after them, in index order.
+ *
+ * Every workgroup clears its share of the level-1 histogram. */
 constexpr int FN_THREADS = 256;
 constexpr int FN_WAVES = FN_THREADS / 64;
-constexpr int RK_TPE = 16;                              /* threads per candidate */
-constexpr int RK_EPW = FN_THREADS / RK_TPE;             /* candidates per workgroup */
+constexpr int RK_TPE = 16;                              /* threads per element */
+constexpr int RK_EPW = FN_THREADS / RK_TPE;             /* elements per workgroup */
+
+/* Number of composites list[f] > mine over f = f0, f0 + RK_TPE, ... < f1,
+ * summed over the RK_TPE lanes of an element (called by every lane): the
+ * lanes of an element read consecutive words, the elements of a wave the
+ * same ones, and sixteen reads are in flight per trip (the loop is
+ * LDS-latency bound). */
+__device__ __forceinline__ uint32_t rank_count(const unsigned long long *list, uint32_t f0,
+                                               uint32_t f1, unsigned long long mine)
+{
+    constexpr int RU = 16;
+    uint32_t r = 0u, f = f0;
+    for (; f + (RU - 1) * RK_TPE < f1; f += RU * RK_TPE) {
+        unsigned long long x[RU];
+#pragma unroll
+        for (int u = 0; u < RU; u++) x[u] = list[f + u * RK_TPE];
+#pragma unroll
+        for (int u = 0; u < RU; u++) r += x[u] > mine ? 1u : 0u;
+    }
+    for (; f < f1; f += RK_TPE) r += list[f] > mine ? 1u : 0u;
+#pragma unroll
+    for (int o = 1; o < RK_TPE; o <<= 1) r += __shfl_xor(r, o, 64);
+    return r;
+}
 
 __global__ void __launch_bounds__(FN_THREADS)
 k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
-           const uint32_t *__restrict__ meta, const uint32_t *__restrict__ bcnt,
-           const unsigned long long *__restrict__ blist, uint32_t *__restrict__ hist_g,
-           int G, int k)
+           const unsigned long long *__restrict__ bsel, const uint32_t *__restrict__ meta,
+           const uint32_t *__restrict__ bcnt, const unsigned long long *__restrict__ blist,
+           uint32_t *__restrict__ hist_g, int G, int k)
 {
     constexpr int BPT = TK_BINS / FN_THREADS;           /* 8 bins per thread */
     constexpr int GPT = RF_GMAX / FN_THREADS;           /* 16 list lengths per thread */
-    __shared__ uint32_t hist[TK_BINS];
-    __shared__ uint32_t pfx[RF_GMAX + 1];
-    __shared__ unsigned long long lst[RF_LIST];
-    __shared__ unsigned long long cs[TK_KMAX];
+    /* direct form: u; refinement form: the candidates in the first TK_KMAX
+     * words, the level-2/3 histogram and the list prefix after them */
+    __shared__ unsigned long long sh[TK_KMAX + RF_LIST];
     __shared__ uint32_t wsum[FN_WAVES], res[2];
+    static_assert(sizeof(uint32_t) * (TK_BINS + RF_GMAX + 1) <=
+                  sizeof(unsigned long long) * RF_LIST, "refinement LDS");
 
     const int tid = threadIdx.x;
 
@@ -773,7 +836,50 @@ k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
         return;
     }
     const uint32_t B = meta[MT_BIN], krem1 = meta[MT_KREM];
-    const uint32_t c_above = min(meta[MT_ABOVE], (uint32_t)TK_KMAX);
+    const unsigned long long cnt = *reinterpret_cast<const unsigned long long *>(meta + MT_CNT);
+    const uint32_t c_above = min((uint32_t)cnt, (uint32_t)TK_KMAX);
+    const uint32_t nbs = (uint32_t)(cnt >> 32);
+
+    if (nbs <= (uint32_t)RF_LIST) {
+        /* ---- direct form ---- */
+        const uint32_t u = c_above + nbs, e0 = blockIdx.x * RK_EPW;
+        if (e0 >= u) return;                                /* the whole workgroup */
+        const uint32_t ja = e0 < c_above ? 0u : c_above;
+        const uint32_t jb = e0 + RK_EPW > c_above ? u : c_above;
+        constexpr int SB = 16;
+        for (uint32_t j0 = ja; j0 < jb; j0 += SB * FN_THREADS) {
+            unsigned long long v[SB];
+#pragma unroll
+            for (int q = 0; q < SB; q++) {
+                const uint32_t j = min(j0 + q * FN_THREADS + tid, jb - 1);
+                const unsigned long long *src = j < c_above ? cand + j : bsel + (j - c_above);
+                v[q] = *src;
+            }
+#pragma unroll
+            for (int q = 0; q < SB; q++) {
+                const uint32_t j = j0 + q * FN_THREADS + tid;
+                if (j < jb) sh[j] = v[q];
+            }
+        }
+        __syncthreads();
+        const uint32_t e = e0 + tid / RK_TPE, sub = tid % RK_TPE;
+        const bool live = e < u, inb = e >= c_above;
+        const unsigned long long mine = live ? sh[e] : ~0ull;
+        const uint32_t f0 = live ? (inb ? c_above : 0u) : 0u;
+        const uint32_t f1 = live ? (inb ? u : c_above) : 0u;
+        const uint32_t r = rank_count(sh, f0 + sub, f1, mine);
+        if (sub == 0 && live) {
+            const uint32_t pos = inb ? c_above + r : r;
+            if ((!inb || r < krem1) && pos < (uint32_t)k)
+                idxs[pos] = (int)(0xFFFFFFFFu - (uint32_t)mine);
+        }
+        return;
+    }
+
+    /* ---- refinement form ---- */
+    unsigned long long *cs = sh;
+    uint32_t *hist = reinterpret_cast<uint32_t *>(sh + TK_KMAX);
+    uint32_t *pfx = hist + TK_BINS;
 
     /* list lengths (prefix below): thread t takes entries GPT t .. GPT t + GPT-1;
      * their loads are issued before the candidates' */
@@ -782,12 +888,12 @@ k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
     for (int q = 0; q < GPT; q++) v[q] = bcnt[min(GPT * tid + q, G - 1)];
     /* candidates above B: into LDS */
     for (uint32_t i0 = 0; i0 < c_above; i0 += 8 * FN_THREADS) {
-        unsigned long long v[8];
+        unsigned long long cv[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = cand[min(i0 + u * FN_THREADS + tid, c_above - 1)];
+        for (int u = 0; u < 8; u++) cv[u] = cand[min(i0 + u * FN_THREADS + tid, c_above - 1)];
 #pragma unroll
         for (int u = 0; u < 8; u++)
-            if (i0 + u * FN_THREADS + tid < c_above) cs[i0 + u * FN_THREADS + tid] = v[u];
+            if (i0 + u * FN_THREADS + tid < c_above) cs[i0 + u * FN_THREADS + tid] = cv[u];
     }
 
     uint32_t sg = 0u;
@@ -804,38 +910,18 @@ k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
         run += v[q];
     }
     if (tid == 0) pfx[G] = nb;
+#pragma unroll
+    for (int q = 0; q < BPT; q++) hist[BPT * tid + q] = 0u;
     __syncthreads();
-    const bool listed = nb <= (uint32_t)RF_LIST;
 
-    auto gaddr = [&](uint32_t j) -> uint32_t {     /* j -> position in blist */
-        int lo = 0, hi = G - 1;                     /* last w with pfx[w] <= j */
+    auto ent = [&](uint32_t j) -> unsigned long long {   /* entry j of B's list */
+        int lo = 0, hi = G - 1;                           /* last w with pfx[w] <= j */
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
             if (pfx[mid] <= j) lo = mid; else hi = mid - 1;
         }
-        return (uint32_t)lo * PT_ELEMS + (j - pfx[lo]);
+        return blist[(uint32_t)lo * PT_ELEMS + (j - pfx[lo])];
     };
-    auto ent = [&](uint32_t j) -> unsigned long long {
-        return listed ? lst[j] : blist[gaddr(j)];
-    };
-    if (listed) {
-        for (uint32_t j0 = 0; j0 < nb; j0 += 8 * FN_THREADS) {
-            unsigned long long e[8];
-#pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const uint32_t j = j0 + q * FN_THREADS + tid;
-                e[q] = j < nb ? blist[gaddr(j)] : 0ull;
-            }
-#pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const uint32_t j = j0 + q * FN_THREADS + tid;
-                if (j < nb) lst[j] = e[q];
-            }
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < BPT; q++) hist[BPT * tid + q] = 0u;
-    __syncthreads();
 
     /* ---- level 2: bits 20..10 ---- */
     for (uint32_t j = tid; j < nb; j += FN_THREADS)
@@ -903,24 +989,11 @@ k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
     }
     __syncthreads();
 
-    /* ---- rank this workgroup's candidates ---- */
+    /* ---- place this workgroup's candidates ---- */
     const uint32_t e = blockIdx.x * RK_EPW + tid / RK_TPE, sub = tid % RK_TPE;
     if (blockIdx.x * RK_EPW >= c_gt) return;            /* the whole workgroup */
     const unsigned long long mine = e < c_gt ? cs[e] : ~0ull;
-    /* sixteen reads in flight per trip: the loop is LDS-latency bound */
-    constexpr int RU = 16;
-    uint32_t r = 0u;
-    uint32_t f = sub;
-    for (; f + (RU - 1) * RK_TPE < c_gt; f += RU * RK_TPE) {
-        unsigned long long x[RU];
-#pragma unroll
-        for (int u = 0; u < RU; u++) x[u] = cs[f + u * RK_TPE];
-#pragma unroll
-        for (int u = 0; u < RU; u++) r += x[u] > mine ? 1u : 0u;
-    }
-    for (; f < c_gt; f += RK_TPE) r += cs[f] > mine ? 1u : 0u;
-#pragma unroll
-    for (int o = 1; o < RK_TPE; o <<= 1) r += __shfl_xor(r, o, 64);
+    const uint32_t r = rank_count(cs, sub, c_gt, mine);
     if (sub == 0 && e < c_gt) idxs[r] = (int)(0xFFFFFFFFu - (uint32_t)mine);
 }
 
@@ -1706,14 +1779,15 @@ int attn_split_rows(int kv_fmt, int d_qk, int d_v, int *rowb_out, size_t *lds_ou
 } // namespace
 
 /* Index scratch: [hist: TK_SLICES x TK_BINS u32][meta: 256 B]
- * [cand: TK_KMAX u64][bcnt: RF_GMAX u32][blist: G x PT_ELEMS u64]. The
- * histogram and the cand[] counter must be zero when a top-k starts from
- * them; every top-k leaves the histogram zero, and the score kernel (or
- * k_tk_hist) restarts the counter. */
+ * [cand: TK_KMAX u64][bsel: RF_LIST u64][bcnt: RF_GMAX u32]
+ * [blist: G x PT_ELEMS u64]. The histogram and the append counter must be
+ * zero when a top-k starts from them; every top-k leaves the histogram
+ * zero, and the score kernel (or k_tk_hist) restarts the counter. */
 static const size_t IX_HIST = 0;
 static const size_t IX_META = IX_HIST + sizeof(uint32_t) * TK_SLICES * TK_BINS;
 static const size_t IX_CAND = IX_META + 256;
-static const size_t IX_BCNT = IX_CAND + sizeof(unsigned long long) * TK_KMAX;
+static const size_t IX_BSEL = IX_CAND + sizeof(unsigned long long) * TK_KMAX;
+static const size_t IX_BCNT = IX_BSEL + sizeof(unsigned long long) * RF_LIST;
 static const size_t IX_BLIST = IX_BCNT + sizeof(uint32_t) * RF_GMAX;
 
 static int ix_heads_padded(int H) { return (H + IS_HB - 1) / IS_HB * IS_HB; }
@@ -1897,6 +1971,7 @@ int dsv4_topk_launch(int *d_idxs, const float *d_scores, int n, int k,
     uint32_t *hist = (uint32_t *)(sb + IX_HIST);
     uint32_t *meta = (uint32_t *)(sb + IX_META);
     unsigned long long *cand = (unsigned long long *)(sb + IX_CAND);
+    unsigned long long *bsel = (unsigned long long *)(sb + IX_BSEL);
     uint32_t *bcnt = (uint32_t *)(sb + IX_BCNT);
     unsigned long long *blist = (unsigned long long *)(sb + IX_BLIST);
     const int G = (n + PT_ELEMS - 1) / PT_ELEMS;
@@ -1905,11 +1980,13 @@ int dsv4_topk_launch(int *d_idxs, const float *d_scores, int n, int k,
                            d_scores, n);
         HIP_OK(hipGetLastError(), "topk histogram launch");
     }
-    hipLaunchKernelGGL(k_tk_part, dim3(G), dim3(PT_THREADS), 0, st, cand, meta, bcnt,
+    hipLaunchKernelGGL(k_tk_part, dim3(G), dim3(PT_THREADS), 0, st, cand, bsel, meta, bcnt,
                        blist, hist, d_scores, n, k);
     HIP_OK(hipGetLastError(), "topk partition launch");
-    hipLaunchKernelGGL(k_tk_final, dim3((k + RK_EPW - 1) / RK_EPW), dim3(FN_THREADS), 0, st,
-                       d_idxs, cand, meta, bcnt, blist, hist, G, k);
+    /* the direct form places up to k - 1 + RF_LIST elements, the refinement
+     * form k */
+    hipLaunchKernelGGL(k_tk_final, dim3((k + RF_LIST + RK_EPW - 1) / RK_EPW), dim3(FN_THREADS),
+                       0, st, d_idxs, cand, bsel, meta, bcnt, blist, hist, G, k);
     HIP_OK(hipGetLastError(), "topk final launch");
     return 0;
 }

@@ -114,6 +114,26 @@ def test_topk_random_with_ties(gpu, dsv4, n, k, levels):
     assert np.array_equal(dsv4.topk(s, k), oracle.topk(s, k))
 
 
+@pytest.mark.parametrize("n_bin,n_above,k,grid", [
+    (4096, 100, 1000, 0), (4097, 100, 1000, 0), (20000, 1000, 3000, 0),
+    (20000, 1000, 3000, 1024), (9000, 0, 4096, 64), (4000, 4095, 4096, 0)])
+def test_topk_crowded_bin(gpu, dsv4, n_bin, n_above, k, grid):
+    """n_bin scores in one level-1 bin [1, 1.25), n_above above it, the rest
+    below: up to 4096 in the bin the final pass places B's elements
+    directly, past that it refines the bin first. grid > 0 rounds the bin's
+    scores to multiples of 1/(4 grid), so ties cross T."""
+    rng = np.random.default_rng(n_bin + n_above + k + grid)
+    inb = rng.uniform(1.0, 1.25, n_bin)
+    if grid:
+        inb = np.minimum(np.round(inb * 4 * grid) / (4 * grid), 1.2499)
+    s = np.concatenate([inb, rng.uniform(2.0, 8.0, n_above),
+                        rng.uniform(-4.0, 0.5, 40000 - n_bin - n_above)]).astype(np.float32)
+    s = s[rng.permutation(s.size)]
+    print("top-k crowded bin: n %d, %d in B, %d above, k %d" % (s.size, n_bin, n_above, k),
+          flush=True)
+    assert np.array_equal(dsv4.topk(s, k), oracle.topk(s, k))
+
+
 def test_topk_all_equal(gpu, dsv4):
     """Both paths: the ranked one (up to 4096 scores) and the radix select."""
     for n in (9000, 4000):

@@ -100,27 +100,6 @@ __device__ __forceinline__ uint32_t fkey(float f)
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-/* One histogram bump per lane with live set, into a global histogram: the
- * lanes sharing the leading lane's bin are counted with one atomic, for a
- * few rounds; what is left adds one by one. */
-__device__ __forceinline__ void hist_push_global(uint32_t *hg, bool live,
-                                                 uint32_t bin, int lane)
-{
-    bool todo = live;
-#pragma unroll 1
-    for (int it = 0; it < 8; ++it) {
-        const unsigned long long pend = __ballot(todo);
-        if (pend == 0ull) return;
-        const int leader = __ffsll((long long)pend) - 1;
-        const uint32_t bl = (uint32_t)__builtin_amdgcn_readlane((int)bin, leader);
-        const bool mine = todo && bin == bl;
-        const unsigned long long same = __ballot(mine);
-        if (lane == leader) atomicAdd(&hg[bl], (uint32_t)__popcll(same));
-        if (mine) todo = false;
-    }
-    if (todo) atomicAdd(&hg[bin], 1u);
-}
-
 /* One 16-byte piece of a key row, as floats (16 / element-size of them);
  * for FP8 the reference's float product e4m3(code) * row_scale. */
 template <int KF>
@@ -257,7 +236,8 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
          const float *__restrict__ ks, int key_stride, int n, float scale, int ng,
          Dsv4Rope qr)
 {
-    extern __shared__ double dots[];            /* [kb * 64][HP + 1], w[HP], then q[H][D] */
+    extern __shared__ double dots[];            /* [kb * 64][HP + 1], w[HP], q[H][D], then
+                                                 * (HIST) the workgroup's histogram [TK_BINS] */
     constexpr int ES = KF == DSV4_GPU_KV_F32 ? 4 : KF == DSV4_GPU_KV_BF16 ? 2 : 1;
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -268,9 +248,12 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
     const int pitch = HP + 1;
     double *wd = dots + (size_t)kb * 64 * pitch;
     float *qs = (float *)(wd + HP);
+    uint32_t *lh = (uint32_t *)(qs + H * D);
     __shared__ float rcs[RP_MAX], rsn[RP_MAX];
     const RopeRow rrow = rope_row_load(qr);
     for (int i = threadIdx.x; i < H; i += blockDim.x) wd[i] = (double)w[i];
+    if (HIST)
+        for (int i = threadIdx.x; i < TK_BINS; i += blockDim.x) lh[i] = 0u;
     /* q into LDS (the launcher checks that it fits): batches of loads in
      * flight before any store, one memory latency per batch of 8 per thread */
     for (int i0 = 0; i0 < H * D; i0 += 8 * (int)blockDim.x) {
@@ -311,26 +294,29 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
         if (VEC) {
             constexpr int CPP = 16 / ES;        /* columns per 16-byte piece */
             constexpr int BLK = 8 * CPP;        /* columns per batch of loads */
+            constexpr int PPG = 16 / CPP;       /* pieces per 16 columns */
             for (int c0 = 0; c0 < D; c0 += BLK) {
                 const int np = min(8, (D - c0) / CPP);
                 u32x4 v[8];
 #pragma unroll
                 for (int u = 0; u < 8; u++)
                     v[u] = *(const DSV4_GLOBAL u32x4 *)(row + (size_t)(c0 + CPP * min(u, np - 1)) * ES);
+                /* a rolled loop over the groups of 16 columns, the batch
+                 * shifting down one group per trip: unrolled, the chains
+                 * are tens of KB of straight-line code that every wave
+                 * streams through the instruction cache once */
+#pragma unroll 1
+                for (int cc = c0; cc < min(c0 + BLK, D); cc += 16) {
+                    float k[16];
 #pragma unroll
-                for (int u16 = 0; u16 < BLK / 16; u16++) {
-                    const int cc = c0 + 16 * u16;
-                    if (cc < D) {
-                        float k[16];
+                    for (int pc = 0; pc < PPG; pc++) key_piece<KF>(v[pc], rs, k + pc * CPP);
 #pragma unroll
-                        for (int pc = 0; pc < 16 / CPP; pc++)
-                            key_piece<KF>(v[u16 * (16 / CPP) + pc], rs, k + pc * CPP);
-                        q_cols(qn, qs, h0, H, D, cc + 16, lane);
-                        if (cc + 16 <= D) chain_16<true>(acc, qf, k, 16, nh);
-                        else              chain_16<false>(acc, qf, k, D - cc, nh);
+                    for (int u = 0; u + PPG < 8; u++) v[u] = v[u + PPG];
+                    q_cols(qn, qs, h0, H, D, cc + 16, lane);
+                    if (cc + 16 <= D) chain_16<true>(acc, qf, k, 16, nh);
+                    else              chain_16<false>(acc, qf, k, D - cc, nh);
 #pragma unroll
-                        for (int j = 0; j < IS_HB; j++) qf[j] = qn[j];
-                    }
+                    for (int j = 0; j < IS_HB; j++) qf[j] = qn[j];
                 }
             }
         } else {
@@ -357,22 +343,32 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
         for (int j = 0; j < IS_HB; j++) drow[g * IS_HB + j] = acc[j];
     }
     __syncthreads();
-    if (hw != 0) return;
-
-    /* the reference's `if (dot > 0) total += dot * w`, as a select */
-    double total = 0.0;
-    for (int hh = 0; hh < H; hh++) {
-        const double d = drow[hh];
-        const double prod = d * wd[hh];
-        total = d > 0.0 ? total + prod : total;
+    if (hw == 0) {
+        /* the reference's `if (dot > 0) total += dot * w`, as a select */
+        double total = 0.0;
+        for (int hh = 0; hh < H; hh++) {
+            const double d = drow[hh];
+            const double prod = d * wd[hh];
+            total = d > 0.0 ? total + prod : total;
+        }
+        const float tf = (float)total;
+        const float sc = tf * scale;
+        if (t < n) out[t] = sc;
+        if (HIST && blockIdx.x == 0 && lane == 0) meta_restart(meta);
+        if (HIST && t < n) atomicAdd(&lh[fkey(sc) >> 21], 1u);
     }
-    const float tf = (float)total;
-    const float sc = tf * scale;
-    if (t < n) out[t] = sc;
-    if (HIST && blockIdx.x == 0 && lane == 0) meta_restart(meta);
-    if (HIST)
-        hist_push_global(hist + (blockIdx.x % TK_SLICES) * TK_BINS, t < n,
-                         fkey(sc) >> 21, lane);
+    if (HIST) {
+        /* the workgroup's bins into the global histogram, one atomic per
+         * bin it holds: scores crowd into few bins, and device-scope
+         * atomics on one address serialise (per-wave merging left up to
+         * ~32 per hot address and cost 4.7 us at C4, this 1.1) */
+        __syncthreads();
+        uint32_t *hs = hist + (blockIdx.x % TK_SLICES) * TK_BINS;
+        for (int i = threadIdx.x; i < TK_BINS; i += blockDim.x) {
+            const uint32_t c = lh[i];
+            if (c) atomicAdd(&hs[i], c);
+        }
+    }
 }
 
 /* Few f32 keys (the attention block's compressed rows, n <= SK_NMAX): one
@@ -380,16 +376,15 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
  * with q (RoPE'd when asked) and the workgroup's key rows staged in LDS; a
  * thread per key then folds the heads in order from LDS. The same
  * arithmetic, step for step, as the reference and as k_iscore, with a
- * workgroup of SK_THREADS / HP keys. Written for every key format and with
- * the top-k histogram, but launched for short f32 score vectors only, where
- * it is the faster form. */
+ * workgroup of SK_THREADS / HP keys. Written for every key format, but
+ * launched for short f32 score vectors with no top-k histogram to build,
+ * where it is the faster form. */
 constexpr int SK_NMAX = 4096;
 constexpr int SK_THREADS = 256;
 
-template <int KF, int HIST>
+template <int KF>
 __global__ void __launch_bounds__(SK_THREADS)
-k_iscore_kh(float *__restrict__ out, uint32_t *__restrict__ hist, uint32_t *__restrict__ meta,
-            const float *__restrict__ q, const float *__restrict__ w, int H, int HP, int D,
+k_iscore_kh(float *__restrict__ out, const float *__restrict__ q, const float *__restrict__ w, int H, int HP, int D,
             const void *__restrict__ keys, const float *__restrict__ ks, int key_stride, int n,
             float scale, Dsv4Rope qr)
 {
@@ -491,7 +486,6 @@ k_iscore_kh(float *__restrict__ out, uint32_t *__restrict__ hist, uint32_t *__re
     }
     __syncthreads();
     const int tt = blockIdx.x * kpw + (int)threadIdx.x;
-    float sc = 0.0f;
     if ((int)threadIdx.x < kpw && tt < n) {
         double total = 0.0;
         for (int hh = 0; hh < H; hh++) {
@@ -499,16 +493,7 @@ k_iscore_kh(float *__restrict__ out, uint32_t *__restrict__ hist, uint32_t *__re
             const double prod = d * wd[hh];
             total = d > 0.0 ? total + prod : total;
         }
-        sc = (float)total * scale;
-        out[tt] = sc;
-    }
-    if (HIST) {
-        /* the top-k's level-1 histogram, by the waves that hold keys */
-        if (blockIdx.x == 0 && threadIdx.x == 0) meta_restart(meta);
-        if ((int)(threadIdx.x & ~63u) < kpw)
-            hist_push_global(hist + (blockIdx.x % TK_SLICES) * TK_BINS,
-                             (int)threadIdx.x < kpw && tt < n, fkey(sc) >> 21,
-                             (int)threadIdx.x & 63);
+        out[tt] = (float)total * scale;
     }
 }
 
@@ -557,18 +542,32 @@ __device__ __forceinline__ unsigned long long lanemask_lt(int lane)
 }
 
 /* Level-1 histogram for a stand-alone top-k (the fused path gets it from the
- * score kernel): top 11 key bits of every score. Also restarts the cand[]
- * append counter. */
+ * score kernel): top 11 key bits of every score, TH_EPT per thread merged in
+ * the workgroup's LDS histogram first, then one atomic per bin it holds.
+ * Also restarts the append counter. */
+constexpr int TH_EPT = 4;
+
 __global__ void __launch_bounds__(256)
 k_tk_hist(uint32_t *__restrict__ hist, uint32_t *__restrict__ meta,
           const float *__restrict__ scores, int n)
 {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    const bool live = i < n;
-    const uint32_t bin = live ? fkey(scores[i]) >> 21 : 0u;
-    if (i == 0) meta_restart(meta);
-    hist_push_global(hist + (blockIdx.x % TK_SLICES) * TK_BINS, live, bin,
-                     threadIdx.x & 63);
+    __shared__ uint32_t lh[TK_BINS];
+    const int tid = threadIdx.x, e0 = blockIdx.x * 256 * TH_EPT + tid;
+    float v[TH_EPT];
+#pragma unroll
+    for (int m = 0; m < TH_EPT; m++) v[m] = scores[min(e0 + 256 * m, n - 1)];
+    for (int i = tid; i < TK_BINS; i += 256) lh[i] = 0u;
+    if (blockIdx.x == 0 && tid == 0) meta_restart(meta);
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < TH_EPT; m++)
+        if (e0 + 256 * m < n) atomicAdd(&lh[fkey(v[m]) >> 21], 1u);
+    __syncthreads();
+    uint32_t *hs = hist + (blockIdx.x % TK_SLICES) * TK_BINS;
+    for (int i = tid; i < TK_BINS; i += 256) {
+        const uint32_t c = lh[i];
+        if (c) atomicAdd(&hs[i], c);
+    }
 }
 
 /* Descending search over TK_BINS bins, BPT per thread of NT: thread t holds
@@ -1852,7 +1851,7 @@ int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *
         if (lds <= dsv4_lds_limit()) {
             static bool kh_opted = false;
             if (!kh_opted) {
-                (void)hipFuncSetAttribute((const void *)k_iscore_kh<DSV4_GPU_KV_F32, 0>,
+                (void)hipFuncSetAttribute((const void *)k_iscore_kh<DSV4_GPU_KV_F32>,
                                           hipFuncAttributeMaxDynamicSharedMemorySize,
                                           (int)dsv4_lds_limit());
                 (void)hipGetLastError();
@@ -1865,8 +1864,8 @@ int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *
                 qr.rd = rope_dim;
             }
             const int kpw = SK_THREADS / hp;
-            hipLaunchKernelGGL((k_iscore_kh<DSV4_GPU_KV_F32, 0>), dim3((n + kpw - 1) / kpw),
-                               dim3(SK_THREADS), lds, st, d_out, nullptr, nullptr, d_q, d_w, H,
+            hipLaunchKernelGGL((k_iscore_kh<DSV4_GPU_KV_F32>), dim3((n + kpw - 1) / kpw),
+                               dim3(SK_THREADS), lds, st, d_out, d_q, d_w, H,
                                hp, D, d_keys, d_key_scales, key_stride, n, scale, qr);
             HIP_OK(hipGetLastError(), "indexer score (few keys) launch");
             return 0;
@@ -1883,7 +1882,8 @@ int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *
     const int ng = groups < mw ? groups : mw;
     const int kb = mw / ng;
     const size_t lds = sizeof(double) * ((size_t)64 * kb * (HP + 1) + HP) +
-                       sizeof(float) * (size_t)H * D;
+                       sizeof(float) * (size_t)H * D +
+                       (with_hist ? sizeof(uint32_t) * TK_BINS : 0);
     if (lds > dsv4_lds_limit()) {
         DSV4_ERR("indexer score: %d heads do not fit in LDS", H);
         return -1;
@@ -1976,8 +1976,8 @@ int dsv4_topk_launch(int *d_idxs, const float *d_scores, int n, int k,
     unsigned long long *blist = (unsigned long long *)(sb + IX_BLIST);
     const int G = (n + PT_ELEMS - 1) / PT_ELEMS;
     if (!hist_ready) {
-        hipLaunchKernelGGL(k_tk_hist, dim3((n + 255) / 256), dim3(256), 0, st, hist, meta,
-                           d_scores, n);
+        hipLaunchKernelGGL(k_tk_hist, dim3((n + 256 * TH_EPT - 1) / (256 * TH_EPT)), dim3(256), 0,
+                           st, hist, meta, d_scores, n);
         HIP_OK(hipGetLastError(), "topk histogram launch");
     }
     hipLaunchKernelGGL(k_tk_part, dim3(G), dim3(PT_THREADS), 0, st, cand, bsel, meta, bcnt,

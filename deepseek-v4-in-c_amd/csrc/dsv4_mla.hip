@@ -1519,14 +1519,41 @@ __device__ __forceinline__ void am_terms8(const float *v, am_v8bf *t)
     t[2] = __builtin_bit_cast(am_v8bf, w[2]);
 }
 
-/* LDS layout in bytes for a shape: K rows [AM_SR][kp], then V^T [d_v][vp];
- * the score partials and the weights reuse the K rows once they are read. */
+/* LDS layout in bytes for a shape: the rows [AM_SR][kp], row-major, then
+ * the score partials [AM_WAVES][16][AM_PP] f32, which the weights [16][AM_PP]
+ * reuse. */
 __host__ __device__ __forceinline__ int am_kpitch(int d_qk) { return 2 * d_qk + 16; }
-__host__ __device__ __forceinline__ int am_vpitch() { return 2 * AM_SR + 16; }
+__host__ __device__ __forceinline__ size_t am_lds_bytes(int d_qk)
+{
+    return (size_t)AM_SR * am_kpitch(d_qk) + sizeof(float) * AM_WAVES * 16 * AM_PP;
+}
+
+typedef short am_v4s __attribute__((ext_vector_type(4)));
+typedef short am_v8s __attribute__((ext_vector_type(8)));
+
+/* The values' B operand for rows r0 .. r0 + 31 of a chunk and columns
+ * cb .. cb + 15, read transposed from the row-major rows: lane l gets
+ * V[r0 + 8 (l / 16) + e][cb + l % 16], e = 0 .. 7. ds_read_b64_tr_b16 gives
+ * lane i of each 16-lane group element (i % 4) of the four 16-bit values
+ * that lane 4 j + i / 4 addressed, as its element j (checked on the GPU);
+ * so lane 4 j + q addresses row r0 + 8 (l / 16) + j, columns cb + 4 q ..
+ * cb + 4 q + 3, and a second read four rows further gives e = 4 .. 7. */
+__device__ __forceinline__ am_v8bf am_vfrag(const unsigned char *kr, int kp, int r0, int cb,
+                                             int l16, int g)
+{
+    const unsigned char *a =
+        kr + (size_t)(r0 + 8 * g + (l16 >> 2)) * kp + 2 * (cb + 4 * (l16 & 3));
+    typedef __attribute__((address_space(3))) am_v4s lds_v4s;
+    const am_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s *)a);
+    const am_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s *)(a + 4 * kp));
+    const am_v8s both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(am_v8bf, both);
+}
 
 /* Workgroup (split of AM_SR rows, tile of 16 heads), AM_WAVES waves:
- *   stage : lane = row; the rows, gathered once, row-major (scores' B
- *           operand) and transposed (values' B operand); meanwhile each wave
+ *   stage : the rows gathered once into LDS, row-major, consecutive lanes
+ *           on consecutive 16-byte pieces of a row (each cache line fetched
+ *           once, every load issued before any store); meanwhile each wave
  *           loads q for its K chunks w, w + AM_WAVES, ...;
  *   scores: each wave the partial S over its K chunks for all row tiles,
  *           summed across the waves in LDS in wave order;
@@ -1540,10 +1567,9 @@ k_attn_mc(float *__restrict__ pm, float *__restrict__ pl, float *__restrict__ po
 {
     extern __shared__ __attribute__((aligned(16))) unsigned char am_lds[];
     __shared__ int sidx[AM_SR];
-    const int kp = am_kpitch(d_qk), vp = am_vpitch();
+    const int kp = am_kpitch(d_qk);
     unsigned char *kr = am_lds;                                  /* [AM_SR][kp] */
-    unsigned char *vt = am_lds + (size_t)AM_SR * kp;             /* [d_v][vp]  */
-    float *red = (float *)am_lds;                                /* [AM_WAVES][16][AM_PP] */
+    float *red = (float *)(am_lds + (size_t)AM_SR * kp);         /* [AM_WAVES][16][AM_PP] */
     float *pw = red;                                             /* [16][AM_PP] */
 
     const int split = blockIdx.x, nsplit = gridDim.x, ht = blockIdx.y;
@@ -1572,37 +1598,37 @@ k_attn_mc(float *__restrict__ pm, float *__restrict__ pl, float *__restrict__ po
     }
     __syncthreads();
 
-    /* ---- stage: lane = row, wave w takes 16-byte chunks w, w + 4, ... ---- */
+    /* ---- stage: piece p = u AM_THREADS + tid of the split is row p / ck,
+     *      16-byte piece p % ck (stepped without a division per piece); a
+     *      masked row loads row 0 and stores zeros ---- */
     {
-        const int ck = d_qk / 8;                                 /* chunks per row */
-        const int row = sidx[lane];
-        const uint16_t *src = kv + (size_t)(row >= 0 ? row : 0) * kv_stride;
-        constexpr int NB = 18;                                   /* chunks in flight */
-        for (int c0 = wv; c0 < ck; c0 += NB * AM_WAVES) {
-            u32x4 v[NB];
+        const int ck = d_qk / 8;                                 /* pieces per row */
+        const int np = AM_SR * ck;
+        constexpr int NB = AM_SR * 4 * AM_KCMAX / AM_THREADS;    /* pieces per thread, at most */
+        const int dr = AM_THREADS / ck, dp = AM_THREADS - dr * ck;
+        int rr = tid / ck, pc = tid - rr * ck;
+        u32x4 v[NB];
+        bool z[NB];
 #pragma unroll
-            for (int u = 0; u < NB; u++) {
-                const int ch = min(c0 + u * AM_WAVES, ck - 1);
-                v[u] = row >= 0 ? *(const DSV4_GLOBAL u32x4 *)(src + 8 * ch)
-                                : u32x4{0u, 0u, 0u, 0u};
-            }
+        for (int u = 0; u < NB; u++) {
+            const int r = min(rr, AM_SR - 1), row = sidx[r];
+            const int pcc = u * AM_THREADS + tid < np ? pc : ck - 1;
+            v[u] = *(const DSV4_GLOBAL u32x4 *)(kv + (size_t)max(row, 0) * kv_stride + 8 * pcc);
+            z[u] = row < 0;
+            rr += dr;
+            pc += dp;
+            if (pc >= ck) { pc -= ck; rr++; }
+        }
+        rr = tid / ck;
+        pc = tid - rr * ck;
 #pragma unroll
-            for (int u = 0; u < NB; u++) {
-                const int ch = c0 + u * AM_WAVES;
-                if (ch < ck) {
-                    *reinterpret_cast<u32x4 *>(kr + (size_t)lane * kp + 16 * ch) = v[u];
-                    if (8 * ch < d_v) {
-                        const uint32_t w4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            *(uint16_t *)(vt + (size_t)(8 * ch + 2 * e) * vp + 2 * lane) =
-                                (uint16_t)(w4[e] & 0xFFFFu);
-                            *(uint16_t *)(vt + (size_t)(8 * ch + 2 * e + 1) * vp + 2 * lane) =
-                                (uint16_t)(w4[e] >> 16);
-                        }
-                    }
-                }
-            }
+        for (int u = 0; u < NB; u++) {
+            if (u * AM_THREADS + tid < np)
+                *reinterpret_cast<u32x4 *>(kr + (size_t)rr * kp + 16 * pc) =
+                    z[u] ? u32x4{0u, 0u, 0u, 0u} : v[u];
+            rr += dr;
+            pc += dp;
+            if (pc >= ck) { pc -= ck; rr++; }
         }
     }
     __syncthreads();
@@ -1633,7 +1659,6 @@ k_attn_mc(float *__restrict__ pm, float *__restrict__ pl, float *__restrict__ po
                                                                         acc[rt][t], 0, 0, 0);
         }
     }
-    __syncthreads();                    /* K rows read: the partials reuse them */
 #pragma unroll
     for (int rt = 0; rt < 4; rt++) {
         const am_v4f sv = (acc[rt][0] + acc[rt][1]) + acc[rt][2];
@@ -1693,11 +1718,8 @@ k_attn_mc(float *__restrict__ pm, float *__restrict__ pl, float *__restrict__ po
             am_terms8(pv, at);
             am_v8bf bv[8];
 #pragma unroll
-            for (int ct = 0; ct < 8; ct++) {
-                const int c = min(c0 + AM_WAVES * ct, CT - 1) * 16 + l16;
-                bv[ct] = __builtin_bit_cast(am_v8bf, *reinterpret_cast<const u32x4 *>(
-                    vt + (size_t)c * vp + 2 * (32 * kc + 8 * g)));
-            }
+            for (int ct = 0; ct < 8; ct++)
+                bv[ct] = am_vfrag(kr, kp, 32 * kc, min(c0 + AM_WAVES * ct, CT - 1) * 16, l16, g);
 #pragma unroll
             for (int t = 0; t < 3; t++)
 #pragma unroll
@@ -1725,10 +1747,7 @@ size_t attn_mc_lds(int kv_fmt, int h, int d_qk, int d_v, int kv_stride)
     if (kv_fmt != DSV4_GPU_KV_BF16 || h % 16 || d_qk % 32 || d_qk > 32 * AM_KCMAX ||
         d_v % 16 || d_v > d_qk || kv_stride % 8)
         return 0;
-    const size_t kr = (size_t)AM_SR * am_kpitch(d_qk);
-    const size_t w = (size_t)AM_WAVES * 16 * AM_PP * sizeof(float);
-    if (w > kr) return 0;
-    const size_t lds = kr + (size_t)d_v * am_vpitch();
+    const size_t lds = am_lds_bytes(d_qk);
     return lds + AM_SR * sizeof(int) <= dsv4_lds_limit() ? lds : 0;
 }
 

@@ -371,6 +371,206 @@ k_iscore(float *__restrict__ out, uint32_t *__restrict__ hist,
     }
 }
 
+/* Matrix-core form of the score (D <= MF_DMAX, D % 4 == 0, H <= 64): the
+ * fp64 chains on v_mfma_f64_16x16x4f64. That instruction computes each of
+ * its outputs as a sequential fma chain over its four k in order (checked
+ * bit for bit on the GPU against a CPU fma chain over 512000 outputs, f32
+ * and full-precision operands; k in reverse or pairwise sums differ in
+ * about 30% of them), so the instructions chained over columns 0, 4, 8, ...
+ * are the reference's chain over c ascending. One instruction advances the
+ * chains of 16 key rows x 16 heads by 4 columns. Operand layout: lane l
+ * holds A[l % 16][l / 16] = key row l % 16 at column 4 m + l / 16,
+ * B[l / 16][l % 16] = q of head l % 16 at that column, and D[l / 16 + 4 r]
+ * [l % 16], r = 0 .. 3 (row, head). A key element is decoded once for 16
+ * heads, and q comes from LDS (f32, RoPE'd, pitch D + 4: the 16 heads x 4
+ * columns of a read hit distinct banks; heads padded to 16 HT with zeros).
+ * A workgroup is MF_WAVES waves of MF_RT row tiles; each lane's key elements
+ * are loaded before q is staged (PIECE: the 16-byte pieces of an FP8 row,
+ * four needed bytes in each; else the elements one by one). The dots meet
+ * in LDS and a thread per row folds the heads as the VALU form does. */
+constexpr int MF_RT = 2;                         /* row tiles of 16 per wave */
+constexpr int MF_WAVES = 4;
+constexpr int MF_ROWS = 16 * MF_RT * MF_WAVES;   /* rows per workgroup */
+constexpr int MF_DMAX = 128;
+typedef double mf_v4d __attribute__((ext_vector_type(4)));
+
+__host__ __device__ __forceinline__ size_t mf_lds_bytes(int H, int HT, int D, int hist)
+{
+    return sizeof(double) * ((size_t)MF_ROWS * (16 * HT + 1) + H) +
+           sizeof(float) * (size_t)16 * HT * (D + 4) + (hist ? sizeof(uint32_t) * TK_BINS : 0);
+}
+
+template <int KF, int PIECE, int HIST, int HT>
+__global__ void __launch_bounds__(MF_WAVES * 64)
+k_iscore_mf(float *__restrict__ out, uint32_t *__restrict__ hist, uint32_t *__restrict__ meta,
+            const float *__restrict__ q, const float *__restrict__ w, int H, int D,
+            const void *__restrict__ keys, const float *__restrict__ ks, int key_stride, int n,
+            float scale, Dsv4Rope qr)
+{
+    /* drow [MF_ROWS][16 HT + 1] f64, w [H] f64, q [16 HT][D + 4] f32, then
+     * (HIST) the workgroup's histogram [TK_BINS] */
+    extern __shared__ double mfl[];
+    constexpr int ES = KF == DSV4_GPU_KV_F32 ? 4 : KF == DSV4_GPU_KV_BF16 ? 2 : 1;
+    constexpr int NP = MF_DMAX / 16, NE = MF_DMAX / 4;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int HP = 16 * HT, pitch = HP + 1, QP = D + 4;
+    double *drow = mfl;
+    double *wd = drow + (size_t)MF_ROWS * pitch;
+    float *qs = (float *)(wd + H);
+    uint32_t *lh = (uint32_t *)(qs + (size_t)HP * QP);
+    __shared__ float rcs[RP_MAX], rsn[RP_MAX];
+
+    /* ---- q into LDS (rows of pitch QP, heads H .. HP-1 zero), w ---- */
+    const RopeRow rrow = rope_row_load(qr);
+    for (int i = H * QP + tid; i < HP * QP; i += MF_WAVES * 64) qs[i] = 0.0f;
+    if (HIST)
+        for (int i = tid; i < TK_BINS; i += MF_WAVES * 64) lh[i] = 0u;
+    /* w's and q's first loads, then the keys', then their stores (the
+     * memory counter returns in order: the stores wait for w and q only) */
+    const float wf = w[min(tid, H - 1)];                 /* H <= 64 < MF_WAVES * 64 */
+    float qv0[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) qv0[u] = q[min(u * MF_WAVES * 64 + tid, H * D - 1)];
+    /* ---- this lane's key elements (row tile rt: row l % 16 of the tile,
+     *      columns 4 m + g), in flight while q is staged ---- */
+    const int r0 = blockIdx.x * MF_ROWS + wv * 16 * MF_RT;
+    const int nm = D / 4;
+    u32x4 kpc[MF_RT][PIECE ? NP : 1];
+    uint32_t kel[MF_RT][PIECE ? 1 : NE];
+    float rs[MF_RT];
+#pragma unroll
+    for (int rt = 0; rt < MF_RT; rt++) {
+        const int row = min(r0 + 16 * rt + l16, n - 1);
+        const unsigned char *rp = (const unsigned char *)keys + (size_t)row * key_stride * ES;
+        rs[rt] = KF == DSV4_GPU_KV_FP8 ? ks[row] : 1.0f;
+        if (PIECE) {
+#pragma unroll
+            for (int a = 0; a < NP; a++)
+                kpc[rt][a] = *(const DSV4_GLOBAL u32x4 *)(rp + 16 * min(a, nm / 4 - 1));
+        } else {
+#pragma unroll
+            for (int m = 0; m < NE; m++) {
+                const int c = 4 * min(m, nm - 1) + g;
+                kel[rt][m] = KF == DSV4_GPU_KV_F32 ? ((const uint32_t *)rp)[c]
+                           : KF == DSV4_GPU_KV_BF16 ? (uint32_t)((const uint16_t *)rp)[c]
+                           : (uint32_t)rp[c];
+            }
+        }
+    }
+
+    /* every load above is issued before any store below */
+    __builtin_amdgcn_sched_barrier(0);
+    /* unconditional (threads past H rewrite w[H-1]'s own value): a store
+     * under `tid < H` let the compiler sink the load past the keys', and the
+     * wait before it then covered them all */
+    wd[min(tid, H - 1)] = (double)wf;
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int i = min(u * MF_WAVES * 64 + tid, H * D - 1);     /* likewise */
+        qs[(i / D) * QP + i % D] = qv0[u];
+    }
+    for (int i0 = 8 * MF_WAVES * 64; i0 < H * D; i0 += 8 * MF_WAVES * 64) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = q[min(i0 + u * MF_WAVES * 64 + tid, H * D - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = min(i0 + u * MF_WAVES * 64 + tid, H * D - 1);
+            qs[(i / D) * QP + i % D] = v[u];
+        }
+    }
+    rope_row_store(qr, rrow, rcs, rsn);
+    __syncthreads();
+    if (qr.rd) {
+        /* the indexer's q RoPE'd at pos, head by head (dsv4_layer.c:282-284) */
+        const int hp = qr.rd / 2;
+        for (int i = tid; i < H * hp; i += MF_WAVES * 64) {
+            const int hh = i / hp, p = i - hh * hp;
+            float *t = qs + (size_t)hh * QP + (D - qr.rd) + 2 * p;
+            rope_pair_cs(t[0], t[1], rcs[p], rsn[p], qr.inverse);
+        }
+        __syncthreads();
+    }
+
+    /* ---- the chains: step m takes columns 4 m .. 4 m + 3 ---- */
+    mf_v4d acc[MF_RT][HT];
+#pragma unroll
+    for (int rt = 0; rt < MF_RT; rt++)
+#pragma unroll
+        for (int ht = 0; ht < HT; ht++) acc[rt][ht] = mf_v4d{0.0, 0.0, 0.0, 0.0};
+    /* every step runs (no branch in the chain: the accumulators stay in
+     * place); steps past D take zero operands, which leave a chain
+     * unchanged bit for bit (it is never -0.0: it starts at +0.0 and an exact
+     * cancellation rounds to +0.0) */
+    const float *qcol = qs + (size_t)l16 * QP + g;
+#pragma unroll
+    for (int m = 0; m < NE; m++) {
+        const bool live = m < nm;
+        double qv[HT];
+#pragma unroll
+        for (int ht = 0; ht < HT; ht++) {
+            const double x = (double)qcol[(size_t)ht * 16 * QP + 4 * min(m, nm - 1)];
+            qv[ht] = live ? x : 0.0;
+        }
+#pragma unroll
+        for (int rt = 0; rt < MF_RT; rt++) {
+            float kf;
+            if (PIECE) {
+                const u32x4 pc = kpc[rt][m / 4];
+                const uint32_t wd4 = (m & 3) == 0 ? pc.x : (m & 3) == 1 ? pc.y
+                                   : (m & 3) == 2 ? pc.z : pc.w;
+                kf = dec_e4m3((uint8_t)(wd4 >> (8 * g))) * rs[rt];
+            } else if (KF == DSV4_GPU_KV_FP8) {
+                kf = dec_e4m3((uint8_t)kel[rt][m]) * rs[rt];
+            } else if (KF == DSV4_GPU_KV_BF16) {
+                kf = __uint_as_float(kel[rt][m] << 16);
+            } else {
+                kf = __uint_as_float(kel[rt][m]);
+            }
+            const double kd = live ? (double)kf : 0.0;
+#pragma unroll
+            for (int ht = 0; ht < HT; ht++)
+                acc[rt][ht] = __builtin_amdgcn_mfma_f64_16x16x4f64(kd, qv[ht], acc[rt][ht],
+                                                                  0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int rt = 0; rt < MF_RT; rt++)
+#pragma unroll
+        for (int ht = 0; ht < HT; ht++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                drow[(size_t)(wv * 16 * MF_RT + 16 * rt + g + 4 * r) * pitch + 16 * ht + l16] =
+                    acc[rt][ht][r];
+    __syncthreads();
+
+    /* ---- a thread per row: the reference's `if (dot > 0) total += dot * w`,
+     *      as a select, in head order ---- */
+    if (tid < MF_ROWS) {
+        const int t = blockIdx.x * MF_ROWS + tid;
+        double total = 0.0;
+        for (int hh = 0; hh < H; hh++) {
+            const double d = drow[(size_t)tid * pitch + hh];
+            const double prod = d * wd[hh];
+            total = d > 0.0 ? total + prod : total;
+        }
+        const float sc = (float)total * scale;
+        if (t < n) out[t] = sc;
+        if (HIST && t == 0) meta_restart(meta);
+        if (HIST && t < n) atomicAdd(&lh[fkey(sc) >> 21], 1u);
+    }
+    if (HIST) {
+        __syncthreads();
+        uint32_t *hs = hist + (blockIdx.x % TK_SLICES) * TK_BINS;
+        for (int i = tid; i < TK_BINS; i += MF_WAVES * 64) {
+            const uint32_t c = lh[i];
+            if (c) atomicAdd(&hs[i], c);
+        }
+    }
+}
+
 /* Few f32 keys (the attention block's compressed rows, n <= SK_NMAX): one
  * thread per (key, head) runs that pair's fp64 fma chain over c ascending,
  * with q (RoPE'd when asked) and the workgroup's key rows staged in LDS; a
@@ -1890,6 +2090,73 @@ int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *
             return 0;
         }
     }
+    uint32_t *hist = with_hist ? (uint32_t *)((char *)scratch + IX_HIST) : nullptr;
+    uint32_t *meta = with_hist ? (uint32_t *)((char *)scratch + IX_META) : nullptr;
+    Dsv4Rope qr;
+    if (rope_dim) {
+        qr.cs = rope_cs; qr.sn = rope_sn; qr.pos = rope_pos; qr.half = rope_half;
+        qr.rd = rope_dim;
+    }
+    const int es = key_fmt == DSV4_GPU_KV_F32 ? 4 : key_fmt == DSV4_GPU_KV_BF16 ? 2 : 1;
+
+    /* the matrix-core form where the shape allows (DSV4_GPU_SCORE_MC=0 keeps
+     * the VALU form) */
+    const char *mc_env = getenv("DSV4_GPU_SCORE_MC");
+    if (D % 4 == 0 && D <= MF_DMAX && H <= 64 && !(mc_env && atoi(mc_env) == 0)) {
+        const int HT = H <= 16 ? 1 : H <= 32 ? 2 : 4;
+        const size_t lds = mf_lds_bytes(H, HT, D, with_hist);
+        if (lds <= dsv4_lds_limit()) {
+            static bool mf_opted = false;
+            if (!mf_opted) {
+                const int cap = (int)dsv4_lds_limit();
+#define DSV4_MF_OPT(KF, P)                                                                  \
+    do {                                                                                    \
+        const void *f_[] = {(const void *)k_iscore_mf<KF, P, 0, 1>,                         \
+                            (const void *)k_iscore_mf<KF, P, 0, 2>,                         \
+                            (const void *)k_iscore_mf<KF, P, 0, 4>,                         \
+                            (const void *)k_iscore_mf<KF, P, 1, 1>,                         \
+                            (const void *)k_iscore_mf<KF, P, 1, 2>,                         \
+                            (const void *)k_iscore_mf<KF, P, 1, 4>};                        \
+        for (const void *f : f_)                                                            \
+            (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, cap);  \
+    } while (0)
+                DSV4_MF_OPT(DSV4_GPU_KV_FP8, 1);
+                DSV4_MF_OPT(DSV4_GPU_KV_FP8, 0);
+                DSV4_MF_OPT(DSV4_GPU_KV_BF16, 0);
+                DSV4_MF_OPT(DSV4_GPU_KV_F32, 0);
+#undef DSV4_MF_OPT
+                (void)hipGetLastError();
+                mf_opted = true;
+            }
+            const bool piece = key_fmt == DSV4_GPU_KV_FP8 && D % 16 == 0 &&
+                               key_stride % 16 == 0 && ((uintptr_t)d_keys & 15) == 0;
+            const int grid = (n + MF_ROWS - 1) / MF_ROWS;
+#define DSV4_MF_GO(KF, P, HS, HTV)                                                          \
+    hipLaunchKernelGGL((k_iscore_mf<KF, P, HS, HTV>), dim3(grid), dim3(MF_WAVES * 64), lds, st,  \
+                       d_out, hist, meta, d_q, d_w, H, D, d_keys, d_key_scales, key_stride, n,  \
+                       scale, qr)
+#define DSV4_MF_HT(KF, P, HS)                                                               \
+    do {                                                                                    \
+        if (HT == 1) DSV4_MF_GO(KF, P, HS, 1);                                              \
+        else if (HT == 2) DSV4_MF_GO(KF, P, HS, 2);                                         \
+        else DSV4_MF_GO(KF, P, HS, 4);                                                      \
+    } while (0)
+#define DSV4_MF_KF(KF, P)                                                                   \
+    do {                                                                                    \
+        if (with_hist) DSV4_MF_HT(KF, P, 1); else DSV4_MF_HT(KF, P, 0);                     \
+    } while (0)
+            if (piece) DSV4_MF_KF(DSV4_GPU_KV_FP8, 1);
+            else if (key_fmt == DSV4_GPU_KV_FP8) DSV4_MF_KF(DSV4_GPU_KV_FP8, 0);
+            else if (key_fmt == DSV4_GPU_KV_BF16) DSV4_MF_KF(DSV4_GPU_KV_BF16, 0);
+            else DSV4_MF_KF(DSV4_GPU_KV_F32, 0);
+#undef DSV4_MF_KF
+#undef DSV4_MF_HT
+#undef DSV4_MF_GO
+            HIP_OK(hipGetLastError(), "indexer score (matrix cores) launch");
+            return 0;
+        }
+    }
+
     const int HP = ix_heads_padded(H);
     /* four waves per workgroup where the heads allow it: one wave per SIMD
      * of a CU (up to 4 head waves per block of 64 rows, blocks filling the
@@ -1924,15 +2191,6 @@ int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *
         (void)hipGetLastError();
         lds_opted = true;
     }
-    uint32_t *hist = with_hist ? (uint32_t *)((char *)scratch + IX_HIST) : nullptr;
-    uint32_t *meta = with_hist ? (uint32_t *)((char *)scratch + IX_META) : nullptr;
-    Dsv4Rope qr;
-    if (rope_dim) {
-        qr.cs = rope_cs; qr.sn = rope_sn; qr.pos = rope_pos; qr.half = rope_half;
-        qr.rd = rope_dim;
-    }
-
-    const int es = key_fmt == DSV4_GPU_KV_F32 ? 4 : key_fmt == DSV4_GPU_KV_BF16 ? 2 : 1;
     const bool vec = ((size_t)D * es) % 16 == 0 && ((size_t)key_stride * es) % 16 == 0 &&
                      ((uintptr_t)d_keys & 15) == 0;
     const int grid = (n + 64 * kb - 1) / (64 * kb);

@@ -80,6 +80,41 @@ def test_score_other_shapes_bit_exact(gpu, dsv4, H, D, n):
     assert common.bits_equal(dsv4.indexer_score(q, w, keys, n), oracle.indexer_score(q, kv, w))
 
 
+@pytest.mark.parametrize("form", ["matrix-core", "valu"])
+@pytest.mark.parametrize("fmt,H,D,n", [
+    ("fp8", 16, 128, 5000), ("fp8", 64, 128, 4500), ("fp8", 20, 48, 4200), ("fp8", 3, 40, 4400),
+    ("bf16", 16, 128, 4400), ("bf16", 40, 64, 4500), ("f32", 16, 128, 4300),
+    ("f32", 64, 128, 5000), ("f32", 7, 36, 4700), ("f32", 8, 132, 4200)])
+def test_score_forms_bit_exact(gpu, dsv4, monkeypatch, form, fmt, H, D, n):
+    """Both score forms, every key format, 1-4 head tiles of the matrix-core
+    form (H up to 16, 32, 64) and its element-wise key loads (FP8 rows that
+    are not whole 16-byte pieces, bf16, f32), plus D = 132, past the
+    matrix-core form's 128 (the VALU form then runs either way). n > 4096,
+    so the f32 keys do not take the few-keys kernel."""
+    if form == "valu":
+        monkeypatch.setenv("DSV4_GPU_SCORE_MC", "0")
+    rng = np.random.default_rng(H * D + n)
+    q = rng.standard_normal((H, D)).astype(np.float32)
+    w = rng.standard_normal(H).astype(np.float32)
+    if fmt == "fp8":
+        codes, s, deq = common.fp8_keys(rng, n, D)
+        keys, want_keys = store(dsv4, codes, dsv4.KV_FP8, s), deq
+    elif fmt == "bf16":
+        kv = common.bf16_round(rng.standard_normal((n, D)).astype(np.float32))
+        keys, want_keys = store(dsv4, common.bf16_bits(kv), dsv4.KV_BF16), kv
+    else:
+        kv = rng.standard_normal((n, D)).astype(np.float32)
+        keys, want_keys = store(dsv4, kv, dsv4.KV_F32), kv
+    say("score %s %s: H %d D %d n %d" % (form, fmt, H, D, n))
+    got = dsv4.indexer_score(q, w, keys, n)
+    want = oracle.indexer_score(q, want_keys, w)
+    nbad = int(np.sum(got.view(np.uint32) != want.view(np.uint32)))
+    assert nbad == 0, "%d of %d scores differ in bits" % (nbad, n)
+    if fmt == "fp8" and H == 16:
+        idx = dsv4.indexer_topk(q, w, keys, n, 512)
+        assert np.array_equal(idx, oracle.topk(want, 512))
+
+
 def test_score_reference_addressing(gpu, dsv4):
     """dsv4_layer.c:286-289 scores the attention cache's compressed rows
     (row width hd = 512) read at the indexer's width D = 128 from row

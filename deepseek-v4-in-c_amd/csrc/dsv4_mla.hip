@@ -73,7 +73,7 @@ constexpr int IS_MAXW = 4;                      /* waves per workgroup */
  * of the selection. */
 constexpr int TK_KMAX = 4096;
 constexpr int TK_BINS = 2048;                   /* top 11 bits of the key */
-constexpr int TK_SLICES = 16;                   /* spread of the global atomics */
+constexpr int TK_SLICES = 4;                    /* spread of the global atomics */
 
 /* meta words in the scratch */
 constexpr int MT_BIN = 2;                       /* B */
@@ -981,31 +981,32 @@ k_tk_part(unsigned long long *__restrict__ cand, unsigned long long *__restrict_
  * after them, in index order.
  *
  * Every workgroup clears its share of the level-1 histogram. */
-constexpr int FN_THREADS = 256;
+constexpr int FN_THREADS = 512;
 constexpr int FN_WAVES = FN_THREADS / 64;
-constexpr int RK_TPE = 16;                              /* threads per element */
+constexpr int RK_TPE = 32;                              /* threads per element */
 constexpr int RK_EPW = FN_THREADS / RK_TPE;             /* elements per workgroup */
 
-/* Number of composites list[f] > mine over f = f0, f0 + RK_TPE, ... < f1,
- * summed over the RK_TPE lanes of an element (called by every lane): the
+/* Number of composites list[f] > mine over f = f0, f0 + TPE, ... < f1,
+ * summed over the TPE lanes of an element (called by every lane): the
  * lanes of an element read consecutive words, the elements of a wave the
  * same ones, and sixteen reads are in flight per trip (the loop is
  * LDS-latency bound). */
+template <int TPE = RK_TPE>
 __device__ __forceinline__ uint32_t rank_count(const unsigned long long *list, uint32_t f0,
                                                uint32_t f1, unsigned long long mine)
 {
     constexpr int RU = 16;
     uint32_t r = 0u, f = f0;
-    for (; f + (RU - 1) * RK_TPE < f1; f += RU * RK_TPE) {
+    for (; f + (RU - 1) * TPE < f1; f += RU * TPE) {
         unsigned long long x[RU];
 #pragma unroll
-        for (int u = 0; u < RU; u++) x[u] = list[f + u * RK_TPE];
+        for (int u = 0; u < RU; u++) x[u] = list[f + u * TPE];
 #pragma unroll
         for (int u = 0; u < RU; u++) r += x[u] > mine ? 1u : 0u;
     }
-    for (; f < f1; f += RK_TPE) r += list[f] > mine ? 1u : 0u;
+    for (; f < f1; f += TPE) r += list[f] > mine ? 1u : 0u;
 #pragma unroll
-    for (int o = 1; o < RK_TPE; o <<= 1) r += __shfl_xor(r, o, 64);
+    for (int o = 1; o < TPE; o <<= 1) r += __shfl_xor(r, o, 64);
     return r;
 }
 
@@ -1015,8 +1016,8 @@ k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
            const uint32_t *__restrict__ bcnt, const unsigned long long *__restrict__ blist,
            uint32_t *__restrict__ hist_g, int G, int k)
 {
-    constexpr int BPT = TK_BINS / FN_THREADS;           /* 8 bins per thread */
-    constexpr int GPT = RF_GMAX / FN_THREADS;           /* 16 list lengths per thread */
+    constexpr int BPT = TK_BINS / FN_THREADS;           /* bins per thread */
+    constexpr int GPT = RF_GMAX / FN_THREADS;           /* list lengths per thread */
     /* direct form: u; refinement form: the candidates in the first TK_KMAX
      * words, the level-2/3 histogram and the list prefix after them */
     __shared__ unsigned long long sh[TK_KMAX + RF_LIST];
@@ -1574,15 +1575,15 @@ k_attn_partial(float *__restrict__ pm, float *__restrict__ pl,
 constexpr int CB_COLS = 128;
 constexpr int CB_SPLITS = 1024;
 
-__global__ void __launch_bounds__(CB_COLS)
-k_attn_combine(float *__restrict__ o, const float *__restrict__ pm,
-               const float *__restrict__ pl, const float *__restrict__ po,
-               const float *__restrict__ sink, int nsplit, int d_v, Dsv4Rope orp)
+/* Head hh, columns [CB_COLS cy, CB_COLS (cy + 1)); fs and lp hold
+ * CB_SPLITS floats each (lp: l_s * e^(m_s - M), rounded to float). */
+__device__ __forceinline__ void cb_body(float *__restrict__ o, const float *__restrict__ pm,
+                                        const float *__restrict__ pl, const float *__restrict__ po,
+                                        const float *__restrict__ sink, int nsplit, int d_v,
+                                        const Dsv4Rope &orp, int hh, int cy, float *fs, float *lp,
+                                        float *sh_inv_p)
 {
-    const int hh = blockIdx.x;
-    __shared__ float fs[CB_SPLITS];
-    __shared__ float lp[CB_SPLITS];     /* l_s * e^(m_s - M), rounded to float */
-    __shared__ float sh_inv;
+    float &sh_inv = *sh_inv_p;
     const int tid = threadIdx.x;
     if (tid < 64) {
         const float sk = sink ? sink[hh] : 0.0f;
@@ -1612,7 +1613,7 @@ k_attn_combine(float *__restrict__ o, const float *__restrict__ pm,
             sh_inv = (float)(1.0 / denom);
         }
     }
-    const int c = blockIdx.y * CB_COLS + tid;
+    const int c = cy * CB_COLS + tid;
     const bool live = c < d_v;
     const int cc = live ? c : d_v - 1;
     /* this column's de-rotation pair's cos / sin, loaded with the partials */
@@ -1657,6 +1658,15 @@ k_attn_combine(float *__restrict__ o, const float *__restrict__ pm,
     if (live) o[(size_t)hh * d_v + c] = val;
 }
 
+__global__ void __launch_bounds__(CB_COLS)
+k_attn_combine(float *__restrict__ o, const float *__restrict__ pm,
+               const float *__restrict__ pl, const float *__restrict__ po,
+               const float *__restrict__ sink, int nsplit, int d_v, Dsv4Rope orp)
+{
+    __shared__ float fs[CB_SPLITS], lp[CB_SPLITS], sh_inv;
+    cb_body(o, pm, pl, po, sink, nsplit, d_v, orp, blockIdx.x, blockIdx.y, fs, lp, &sh_inv);
+}
+
 /* ------------------------------------------ sparse attention, matrix core */
 
 /* The same split softmax on v_mfma_f32_16x16x32_bf16 for bf16 KV, d_qk a
@@ -1685,8 +1695,7 @@ constexpr int AM_SR = 64;                        /* rows per split */
 constexpr int AM_WAVES = 4;
 constexpr int AM_THREADS = AM_WAVES * 64;
 constexpr int AM_PP = AM_SR + 4;                 /* weights pitch (f32) */
-constexpr int AM_KCW = 5;                        /* K chunks per wave */
-constexpr int AM_KCMAX = AM_KCW * AM_WAVES;      /* d_qk <= 32 AM_KCMAX */
+constexpr int AM_KCMAX = 20;                     /* d_qk <= 32 AM_KCMAX */
 
 typedef __bf16 am_v2bf __attribute__((ext_vector_type(2)));
 typedef float am_v2f __attribute__((ext_vector_type(2)));
@@ -1719,13 +1728,13 @@ __device__ __forceinline__ void am_terms8(const float *v, am_v8bf *t)
     t[2] = __builtin_bit_cast(am_v8bf, w[2]);
 }
 
-/* LDS layout in bytes for a shape: the rows [AM_SR][kp], row-major, then
- * the score partials [AM_WAVES][16][AM_PP] f32, which the weights [16][AM_PP]
- * reuse. */
+/* LDS layout in bytes for a shape and nw waves: the rows [AM_SR][kp],
+ * row-major, then the score partials [nw][16][AM_PP] f32, which the weights
+ * [16][AM_PP] reuse. */
 __host__ __device__ __forceinline__ int am_kpitch(int d_qk) { return 2 * d_qk + 16; }
-__host__ __device__ __forceinline__ size_t am_lds_bytes(int d_qk)
+__host__ __device__ __forceinline__ size_t am_lds_bytes(int d_qk, int nw)
 {
-    return (size_t)AM_SR * am_kpitch(d_qk) + sizeof(float) * AM_WAVES * 16 * AM_PP;
+    return (size_t)AM_SR * am_kpitch(d_qk) + sizeof(float) * nw * 16 * AM_PP;
 }
 
 typedef short am_v4s __attribute__((ext_vector_type(4)));
@@ -1750,69 +1759,68 @@ __device__ __forceinline__ am_v8bf am_vfrag(const unsigned char *kr, int kp, int
     return __builtin_bit_cast(am_v8bf, both);
 }
 
-/* Workgroup (split of AM_SR rows, tile of 16 heads), AM_WAVES waves:
+/* The attention of one workgroup, NW waves: (split of AM_SR rows, tile of
+ * 16 heads), the split's rows in sidx (set by the caller before the call,
+ * -1 masked):
  *   stage : the rows gathered once into LDS, row-major, consecutive lanes
  *           on consecutive 16-byte pieces of a row (each cache line fetched
  *           once, every load issued before any store); meanwhile each wave
- *           loads q for its K chunks w, w + AM_WAVES, ...;
+ *           loads q for its K chunks w, w + NW, ...;
  *   scores: each wave the partial S over its K chunks for all row tiles,
  *           summed across the waves in LDS in wave order;
- *   softmax: per head m_s, e_j = expf(s_j - m_s), l_s (lane = row);
- *   values: O_s = P . V, each wave a quarter of the column tiles. */
-__global__ void __launch_bounds__(AM_THREADS)
-k_attn_mc(float *__restrict__ pm, float *__restrict__ pl, float *__restrict__ po,
-          const float *__restrict__ q, const uint16_t *__restrict__ kv, int kv_stride,
-          const int *__restrict__ idxs, int kv_rows, int h, int d_qk, int d_v, int topk,
-          float scale)
+ *   softmax: per head m_s, e_j = expf(s_j - m_s), l_s (lane = row), 16 / NW
+ *           heads per wave;
+ *   values: O_s = P . V, each wave every NW-th column tile. */
+template <int NW>
+__device__ __forceinline__ void am_body(float *__restrict__ pm, float *__restrict__ pl,
+                                        float *__restrict__ po, const float *__restrict__ q,
+                                        const uint16_t *__restrict__ kv, int kv_stride,
+                                        int d_qk, int d_v, float scale, int split, int nsplit,
+                                        int ht, const int *sidx, unsigned char *am_lds)
 {
-    extern __shared__ __attribute__((aligned(16))) unsigned char am_lds[];
-    __shared__ int sidx[AM_SR];
+    constexpr int NT = 64 * NW;
+    constexpr int KCW = (AM_KCMAX + NW - 1) / NW;      /* K chunks per wave */
+    constexpr int HPW = 16 / NW;                       /* softmax heads per wave */
+    constexpr int VT = 32 / NW;                        /* value column tiles per pass */
     const int kp = am_kpitch(d_qk);
     unsigned char *kr = am_lds;                                  /* [AM_SR][kp] */
-    float *red = (float *)(am_lds + (size_t)AM_SR * kp);         /* [AM_WAVES][16][AM_PP] */
+    float *red = (float *)(am_lds + (size_t)AM_SR * kp);         /* [NW][16][AM_PP] */
     float *pw = red;                                             /* [16][AM_PP] */
-
-    const int split = blockIdx.x, nsplit = gridDim.x, ht = blockIdx.y;
-    const int j0 = split * AM_SR;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, g = lane >> 4;
     const int KC = d_qk / 32;
 
-    if (tid < AM_SR) {
-        const int r = j0 + tid < topk ? idxs[j0 + tid] : -1;
-        sidx[tid] = (r >= 0 && r < kv_rows) ? r : -1;            /* never a wild read */
-    }
     /* q of the head tile for this wave's K chunks (A operand rows l%16, K
      * [8(l/16), +8) of each chunk), in flight with the staging loads */
-    float qv[AM_KCW][8];
+    float qv[KCW][8];
     {
         const float *qr = q + (size_t)(ht * 16 + l16) * d_qk + 8 * g;
 #pragma unroll
-        for (int i = 0; i < AM_KCW; i++) {
-            const int kc = min(wv + AM_WAVES * i, KC - 1);
+        for (int i = 0; i < KCW; i++) {
+            const int kc = min(wv + NW * i, KC - 1);
             const f32x4 a0 = ldf4(qr + 32 * kc), a1 = ldf4(qr + 32 * kc + 4);
             qv[i][0] = a0.x; qv[i][1] = a0.y; qv[i][2] = a0.z; qv[i][3] = a0.w;
             qv[i][4] = a1.x; qv[i][5] = a1.y; qv[i][6] = a1.z; qv[i][7] = a1.w;
         }
     }
-    __syncthreads();
+    __syncthreads();                                   /* sidx visible */
 
-    /* ---- stage: piece p = u AM_THREADS + tid of the split is row p / ck,
-     *      16-byte piece p % ck (stepped without a division per piece); a
-     *      masked row loads row 0 and stores zeros ---- */
+    /* ---- stage: piece p = u NT + tid of the split is row p / ck, 16-byte
+     *      piece p % ck (stepped without a division per piece); a masked
+     *      row loads row 0 and stores zeros ---- */
     {
         const int ck = d_qk / 8;                                 /* pieces per row */
         const int np = AM_SR * ck;
-        constexpr int NB = AM_SR * 4 * AM_KCMAX / AM_THREADS;    /* pieces per thread, at most */
-        const int dr = AM_THREADS / ck, dp = AM_THREADS - dr * ck;
+        constexpr int NB = (AM_SR * 4 * AM_KCMAX + NT - 1) / NT; /* pieces per thread, at most */
+        const int dr = NT / ck, dp = NT - dr * ck;
         int rr = tid / ck, pc = tid - rr * ck;
         u32x4 v[NB];
         bool z[NB];
 #pragma unroll
         for (int u = 0; u < NB; u++) {
             const int r = min(rr, AM_SR - 1), row = sidx[r];
-            const int pcc = u * AM_THREADS + tid < np ? pc : ck - 1;
+            const int pcc = u * NT + tid < np ? pc : ck - 1;
             v[u] = *(const DSV4_GLOBAL u32x4 *)(kv + (size_t)max(row, 0) * kv_stride + 8 * pcc);
             z[u] = row < 0;
             rr += dr;
@@ -1823,7 +1831,7 @@ k_attn_mc(float *__restrict__ pm, float *__restrict__ pl, float *__restrict__ po
         pc = tid - rr * ck;
 #pragma unroll
         for (int u = 0; u < NB; u++) {
-            if (u * AM_THREADS + tid < np)
+            if (u * NT + tid < np)
                 *reinterpret_cast<u32x4 *>(kr + (size_t)rr * kp + 16 * pc) =
                     z[u] ? u32x4{0u, 0u, 0u, 0u} : v[u];
             rr += dr;
@@ -1841,8 +1849,8 @@ k_attn_mc(float *__restrict__ pm, float *__restrict__ pl, float *__restrict__ po
 #pragma unroll
         for (int t = 0; t < 3; t++) acc[rt][t] = am_v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < AM_KCW; i++) {
-        const int kc = wv + AM_WAVES * i;
+    for (int i = 0; i < KCW; i++) {
+        const int kc = wv + NW * i;
         if (kc < KC) {
             am_v8bf bk[4];
 #pragma unroll
@@ -1868,46 +1876,46 @@ k_attn_mc(float *__restrict__ pm, float *__restrict__ pl, float *__restrict__ po
     }
     __syncthreads();
 
-    /* ---- split softmax: wave w takes heads 4w .. 4w + 3, lane = row; the
-     *      partials summed in wave order ---- */
+    /* ---- split softmax: wave w takes heads HPW w .. HPW w + HPW - 1,
+     *      lane = row; the partials summed in wave order ---- */
     {
         const bool live = sidx[lane] >= 0;
-        float sv[4], m[4], e[4], l[4];
+        float sv[HPW], m[HPW], e[HPW], l[HPW];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int hh = 4 * wv + i;
+        for (int i = 0; i < HPW; i++) {
+            const int hh = HPW * wv + i;
             float a = red[hh * AM_PP + lane];
 #pragma unroll
-            for (int w = 1; w < AM_WAVES; w++) a = a + red[(w * 16 + hh) * AM_PP + lane];
+            for (int w = 1; w < NW; w++) a = a + red[(w * 16 + hh) * AM_PP + lane];
             sv[i] = live ? a * scale : -INFINITY;
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) m[i] = wave_max(sv[i]);
+        for (int i = 0; i < HPW; i++) m[i] = wave_max(sv[i]);
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < HPW; i++)
             e[i] = (m[i] == -INFINITY || sv[i] == -INFINITY) ? 0.0f : expf(sv[i] - m[i]);
 #pragma unroll
-        for (int i = 0; i < 4; i++) l[i] = wave_sum(e[i]);
+        for (int i = 0; i < HPW; i++) l[i] = wave_sum(e[i]);
         __syncthreads();                /* every partial read before pw overwrites */
 #pragma unroll
-        for (int i = 0; i < 4; i++) pw[(4 * wv + i) * AM_PP + lane] = e[i];
-        if (lane < 4) {
+        for (int i = 0; i < HPW; i++) pw[(HPW * wv + i) * AM_PP + lane] = e[i];
+        if (lane < HPW) {
             float mi = m[0], li = l[0];
 #pragma unroll
-            for (int i = 1; i < 4; i++) if (lane == i) { mi = m[i]; li = l[i]; }
-            const int hh = ht * 16 + 4 * wv + lane;
+            for (int i = 1; i < HPW; i++) if (lane == i) { mi = m[i]; li = l[i]; }
+            const int hh = ht * 16 + HPW * wv + lane;
             pm[(size_t)hh * nsplit + split] = mi;
             pl[(size_t)hh * nsplit + split] = li;
         }
     }
     __syncthreads();
 
-    /* ---- values: column tiles wv, wv + 4, ... ---- */
+    /* ---- values: column tiles wv, wv + NW, ... ---- */
     const int CT = d_v / 16;
-    for (int c0 = wv; c0 < CT; c0 += 8 * AM_WAVES) {
-        am_v4f o[8];
+    for (int c0 = wv; c0 < CT; c0 += VT * NW) {
+        am_v4f o[VT];
 #pragma unroll
-        for (int ct = 0; ct < 8; ct++) o[ct] = am_v4f{0.f, 0.f, 0.f, 0.f};
+        for (int ct = 0; ct < VT; ct++) o[ct] = am_v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kc = 0; kc < AM_SR / 32; kc++) {
             const float *pr = pw + l16 * AM_PP + 32 * kc + 8 * g;
@@ -1916,19 +1924,19 @@ k_attn_mc(float *__restrict__ pm, float *__restrict__ pl, float *__restrict__ po
             const float pv[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
             am_v8bf at[3];
             am_terms8(pv, at);
-            am_v8bf bv[8];
+            am_v8bf bv[VT];
 #pragma unroll
-            for (int ct = 0; ct < 8; ct++)
-                bv[ct] = am_vfrag(kr, kp, 32 * kc, min(c0 + AM_WAVES * ct, CT - 1) * 16, l16, g);
+            for (int ct = 0; ct < VT; ct++)
+                bv[ct] = am_vfrag(kr, kp, 32 * kc, min(c0 + NW * ct, CT - 1) * 16, l16, g);
 #pragma unroll
             for (int t = 0; t < 3; t++)
 #pragma unroll
-                for (int ct = 0; ct < 8; ct++)
+                for (int ct = 0; ct < VT; ct++)
                     o[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(at[t], bv[ct], o[ct], 0, 0, 0);
         }
 #pragma unroll
-        for (int ct = 0; ct < 8; ct++) {
-            const int cti = c0 + AM_WAVES * ct;
+        for (int ct = 0; ct < VT; ct++) {
+            const int cti = c0 + NW * ct;
             if (cti < CT) {
                 const int c = cti * 16 + l16;
 #pragma unroll
@@ -1941,13 +1949,31 @@ k_attn_mc(float *__restrict__ pm, float *__restrict__ pl, float *__restrict__ po
     }
 }
 
+/* Workgroup (split of AM_SR rows, tile of 16 heads), AM_WAVES waves: the
+ * split's rows are idxs[AM_SR split ...]. */
+__global__ void __launch_bounds__(AM_THREADS)
+k_attn_mc(float *__restrict__ pm, float *__restrict__ pl, float *__restrict__ po,
+          const float *__restrict__ q, const uint16_t *__restrict__ kv, int kv_stride,
+          const int *__restrict__ idxs, int kv_rows, int d_qk, int d_v, int topk, float scale)
+{
+    extern __shared__ __attribute__((aligned(16))) unsigned char am_lds[];
+    __shared__ int sidx[AM_SR];
+    const int j0 = blockIdx.x * AM_SR;
+    if (threadIdx.x < AM_SR) {
+        const int r = j0 + (int)threadIdx.x < topk ? idxs[j0 + threadIdx.x] : -1;
+        sidx[threadIdx.x] = (r >= 0 && r < kv_rows) ? r : -1;    /* never a wild read */
+    }
+    am_body<AM_WAVES>(pm, pl, po, q, kv, kv_stride, d_qk, d_v, scale, blockIdx.x, gridDim.x,
+                      blockIdx.y, sidx, am_lds);
+}
+
 /* LDS bytes of k_attn_mc for a shape, 0 when the shape is not one it takes. */
 size_t attn_mc_lds(int kv_fmt, int h, int d_qk, int d_v, int kv_stride)
 {
     if (kv_fmt != DSV4_GPU_KV_BF16 || h % 16 || d_qk % 32 || d_qk > 32 * AM_KCMAX ||
         d_v % 16 || d_v > d_qk || kv_stride % 8)
         return 0;
-    const size_t lds = am_lds_bytes(d_qk);
+    const size_t lds = am_lds_bytes(d_qk, AM_WAVES);
     return lds + AM_SR * sizeof(int) <= dsv4_lds_limit() ? lds : 0;
 }
 
@@ -2361,7 +2387,7 @@ int dsv4_attn_block_launch(float *d_o, const float *d_q, const void *d_kv,
         pl = pm + (size_t)h * ns;
         po = pl + (size_t)h * ns;
         hipLaunchKernelGGL(k_attn_mc, dim3(ns, h / 16), dim3(AM_THREADS), mc_lds, st, pm, pl, po,
-                           d_q, (const uint16_t *)d_kv, kv_stride, d_idxs, kv_rows, h,
+                           d_q, (const uint16_t *)d_kv, kv_stride, d_idxs, kv_rows,
                            d_qk, d_v, topk, scale);
         HIP_OK(hipGetLastError(), "attn mc launch");
         hipLaunchKernelGGL(k_attn_combine, dim3(h, (d_v + CB_COLS - 1) / CB_COLS),

@@ -337,3 +337,77 @@ def test_mla_decode_step_c4(gpu, dsv4):
     err = common.vec_rel_err(d_o.cpu().numpy(), want)
     say("mla step C4: worst rel %.3g" % err)
     assert err < TOL
+
+
+def _mla_step(dsv4, codes, s, qi, wi, kv, q, n, k, sink=None, h=64, d_qk=576, d_v=512):
+    import torch
+    dev = torch.device("cuda:0")
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    d_codes, d_s, d_qi, d_wi, d_q = t(codes), t(s), t(qi), t(wi), t(q)
+    d_kv = t(common.bf16_bits(kv).view(np.int16))
+    d_sink = None if sink is None else t(sink)
+    d_o = torch.full((h, d_v), 3.0, dtype=torch.float32, device=dev)
+    d_idx = torch.full((k,), -7, dtype=torch.int32, device=dev)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d_qk)))
+    st = torch.cuda.current_stream().cuda_stream
+    H, D = qi.shape
+    rc = dsv4.lib().dsv4_gpu_mla_decode_d(
+        d_o.data_ptr(), d_idx.data_ptr(), d_qi.data_ptr(), d_wi.data_ptr(), H, D,
+        d_codes.data_ptr(), d_s.data_ptr(), dsv4.KV_FP8, D, n, k,
+        d_q.data_ptr(), d_kv.data_ptr(), dsv4.KV_BF16, d_qk, n,
+        None if d_sink is None else d_sink.data_ptr(), h, d_qk, d_v, scale, st)
+    assert rc == 0
+    torch.cuda.synchronize()
+    return d_o.cpu().numpy(), d_idx.cpu().numpy(), scale
+
+
+@pytest.mark.parametrize("n,k,dup,sink", [
+    (32768, 2048, 0, False), (32768, 4096, 0, True), (4097, 4096, 0, False), (4097, 100, 0, False),
+    (5001, 700, 0, False), (20000, 1000, 37, False), (32768, 2048, 5, True), (32769, 512, 0, False)])
+def test_mla_decode_selection_cases(gpu, dsv4, n, k, dup, sink):
+    """The decode step end to end: the selection equal to the oracle's top-k
+    of the oracle's scores, bit for bit, and the output within 1e-5 of the
+    oracle's attention over it. dup > 0 repeats key rows in blocks of dup,
+    so scores tie across T; n = 5001 is not a multiple of 4, k = 700 not a
+    multiple of the 64-row split, n = 4097 just past the one-launch top-k."""
+    rng = np.random.default_rng(n + k + dup)
+    H, D, h = 16, 128, 64
+    codes, s, deq = common.fp8_keys(rng, n, D)
+    if dup:
+        src = (np.arange(n) // dup) * dup
+        codes, s, deq = codes[src], s[src], deq[src]
+    qi = rng.standard_normal((H, D)).astype(np.float32)
+    wi = rng.standard_normal(H).astype(np.float32)
+    kv = common.bf16_round(rng.standard_normal((n, 576)).astype(np.float32)
+                           / np.float32(np.sqrt(576)))
+    q = rng.standard_normal((h, 576)).astype(np.float32)
+    sk = rng.standard_normal(h).astype(np.float32) if sink else None
+    want_idx = oracle.topk(oracle.indexer_score(qi, deq, wi), min(k, n))
+    say("mla step: n %d k %d dup %d sink %s" % (n, k, dup, sink))
+    o, idx, scale = _mla_step(dsv4, codes, s, qi, wi, kv, q, n, k, sk)
+    assert np.array_equal(idx[:len(want_idx)], want_idx)
+    want = oracle.sparse_attn(q, kv, sk, want_idx, scale, d_v=512)
+    err = common.vec_rel_err(o, want)
+    say("  worst rel %.3g" % err)
+    assert err < TOL
+
+
+def test_mla_decode_nan_score_masks_every_row(gpu, dsv4):
+    """NaN scores (a NaN head weight: every row whose dot with that head is
+    positive scores NaN): every selected slot is -1 and every row masked,
+    so the output is the attention over no row, as the stand-alone
+    attention gives it for an all -1 selection."""
+    rng = np.random.default_rng(3)
+    n, k, H, D, h = 9000, 512, 16, 128, 64
+    codes, s, deq = common.fp8_keys(rng, n, D)
+    qi = rng.standard_normal((H, D)).astype(np.float32)
+    wi = np.abs(rng.standard_normal(H)).astype(np.float32)
+    wi[3] = np.nan
+    kv = common.bf16_round(rng.standard_normal((n, 576)).astype(np.float32) / np.float32(24))
+    q = rng.standard_normal((h, 576)).astype(np.float32)
+    o, idx, scale = _mla_step(dsv4, codes, s, qi, wi, kv, q, n, k)
+    assert (idx == -1).all()
+    masked = np.full(k, -1, np.int32)
+    st = store(dsv4, common.bf16_bits(kv), dsv4.KV_BF16)
+    want = dsv4.sparse_attn(q, st, None, masked, scale, d_v=512)
+    assert np.array_equal(o, want, equal_nan=True)

@@ -1692,7 +1692,7 @@ typedef __bf16 am_v8bf __attribute__((ext_vector_type(8)));
 typedef short am_v8s __attribute__((ext_vector_type(8)));
 
 constexpr int AM_SR = 64;                        /* rows per split */
-constexpr int AM_WAVES = 4;
+constexpr int AM_WAVES = 8;
 constexpr int AM_THREADS = AM_WAVES * 64;
 constexpr int AM_PP = AM_SR + 4;                 /* weights pitch (f32) */
 constexpr int AM_KCMAX = 20;                     /* d_qk <= 32 AM_KCMAX */

@@ -398,11 +398,13 @@ k_fp8_mx1(Dsv4Fp8Mx a)
 /* x terms of a group's tokens for one unit's 256 columns, in LDS as term
  * rows: bl[(tok * XNT + term) * BP + k], BP = XU + 8. */
 constexpr int BP = XU + 8;
-constexpr int MW = 4;                       /* waves (16-row tiles) per workgroup */
+/* MW: waves (16-row tiles) per workgroup, a template parameter of the
+ * batched kernel and its helpers (4, or 8 when the batch takes three or more
+ * token groups: the x terms are then staged for twice the rows) */
 
 /* f32x4 pieces of x per thread per unit: a group holds at most XTOK * NT
  * tokens of XU / 4 pieces, spread over the workgroup's 64 MW threads. */
-template <int NT>
+template <int NT, int MW>
 struct XnDim {
     static constexpr int M = (XTOK * NT * (XU / 4) + 64 * MW - 1) / (64 * MW);
 };
@@ -411,12 +413,12 @@ struct XnDim {
  * group's tokens or past cols read the group's first piece (unconditional
  * loads: no branch for the weight requests to wait behind) and become zeros
  * in xn_terms. */
-template <int NT>
+template <int NT, int MW>
 __device__ __forceinline__ void xn_load(f32x4 *v, const float *x, int t0, int ntok, int kc,
                                         int cols, int tpg)
 {
 #pragma unroll
-    for (int m = 0; m < XnDim<NT>::M; m++) {
+    for (int m = 0; m < XnDim<NT, MW>::M; m++) {
         const int i = (int)threadIdx.x + 64 * MW * m;
         const int tk = i / (XU / 4), c = kc + 4 * (i % (XU / 4));
         const bool in = i < tpg * (XU / 4) && tk < ntok && c < cols;
@@ -425,12 +427,12 @@ __device__ __forceinline__ void xn_load(f32x4 *v, const float *x, int t0, int nt
     }
 }
 
-template <int NT>
+template <int NT, int MW>
 __device__ __forceinline__ void xn_terms(uint16_t *bl, const f32x4 *v, int ntok, int kc,
                                          int cols, int tpg)
 {
 #pragma unroll
-    for (int m = 0; m < XnDim<NT>::M; m++) {
+    for (int m = 0; m < XnDim<NT, MW>::M; m++) {
         const int i = (int)threadIdx.x + 64 * MW * m;
         if (i < tpg * (XU / 4)) {
             const int tk = i / (XU / 4), c4 = i % (XU / 4);
@@ -474,7 +476,7 @@ k_fp8_xsplit(uint16_t *__restrict__ xt, const float *__restrict__ x, int nt, int
 
 /* 16-byte pieces of the term planes per thread per unit: a group's tpg
  * tokens x XNT planes x XU / 8 pieces over the workgroup's 64 MW threads. */
-template <int NT>
+template <int NT, int MW>
 struct XpDim {
     static constexpr int M = (XTOK * NT * XNT * (XU / 8) + 64 * MW - 1) / (64 * MW);
 };
@@ -482,12 +484,12 @@ struct XpDim {
 /* Request piece i = tid + 64 MW m of unit u's term rows (row = token * XNT +
  * plane): rows past the group's tokens read its first row (unconditional
  * loads) and are stored as zeros. */
-template <int NT>
+template <int NT, int MW>
 __device__ __forceinline__ void xp_load(u32x4 *v, const uint16_t *xt, int t0, int ntok, int u,
                                         int cpad, int tpg)
 {
 #pragma unroll
-    for (int m = 0; m < XpDim<NT>::M; m++) {
+    for (int m = 0; m < XpDim<NT, MW>::M; m++) {
         const int i = (int)threadIdx.x + 64 * MW * m;
         const int row = i / (XU / 8), pc = i % (XU / 8);
         const bool in = row < tpg * XNT && row / XNT < ntok;
@@ -497,11 +499,11 @@ __device__ __forceinline__ void xp_load(u32x4 *v, const uint16_t *xt, int t0, in
     }
 }
 
-template <int NT>
+template <int NT, int MW>
 __device__ __forceinline__ void xp_store(uint16_t *bl, const u32x4 *v, int ntok, int tpg)
 {
 #pragma unroll
-    for (int m = 0; m < XpDim<NT>::M; m++) {
+    for (int m = 0; m < XpDim<NT, MW>::M; m++) {
         const int i = (int)threadIdx.x + 64 * MW * m;
         const int row = i / (XU / 8), pc = i % (XU / 8);
         if (row < tpg * XNT)
@@ -518,7 +520,7 @@ __device__ __forceinline__ void xp_store(uint16_t *bl, const u32x4 *v, int ntok,
  * column tiles. At each segment's end the segment's accumulators join the
  * running sums in segment order. Every register array is indexed by
  * compile-time constants: the unit loop is unrolled by a segment's 4. */
-template <int NT, bool UNI>
+template <int NT, bool UNI, int MW>
 __global__ void __launch_bounds__(64 * MW)
 k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__restrict__ W,
           const uint8_t *__restrict__ S, int rows, int cols, int sc, int blk_r, uint32_t bc_m,
@@ -556,20 +558,20 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
     const int nu = (cols + XU - 1) / XU;
     /* x(u): the pre-split term planes when the caller gave them (copied
      * into LDS as they are), else the f32 row (turned into terms here) */
-    constexpr int XM = XpDim<NT>::M > XnDim<NT>::M ? XpDim<NT>::M : XnDim<NT>::M;
+    constexpr int XM = XpDim<NT, MW>::M > XnDim<NT, MW>::M ? XpDim<NT, MW>::M : XnDim<NT, MW>::M;
     u32x4 XR[XM];                       /* x(u + 1) in flight while unit u runs */
     XUnit<UNI> P[2];
     auto xload = [&](u32x4 *v, int u) {
         if (xt)
-            xp_load<NT>(v, xt, t0, ntok, u, cpad, tpg);
+            xp_load<NT, MW>(v, xt, t0, ntok, u, cpad, tpg);
         else
-            xn_load<NT>(reinterpret_cast<f32x4 *>(v), x, t0, ntok, XU * u, cols, tpg);
+            xn_load<NT, MW>(reinterpret_cast<f32x4 *>(v), x, t0, ntok, XU * u, cols, tpg);
     };
     auto xstore = [&](uint16_t *bl, const u32x4 *v, int u) {
         if (xt)
-            xp_store<NT>(bl, v, ntok, tpg);
+            xp_store<NT, MW>(bl, v, ntok, tpg);
         else
-            xn_terms<NT>(bl, reinterpret_cast<const f32x4 *>(v), ntok, XU * u, cols, tpg);
+            xn_terms<NT, MW>(bl, reinterpret_cast<const f32x4 *>(v), ntok, XU * u, cols, tpg);
     };
     xload(XR, 0);
     /* uniform scales: the current segment's (ssb) and the next one's */
@@ -806,15 +808,21 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
     const int NTc = (ntile + ngrp - 1) / ngrp;         /* then the fewest tiles each */
     const int tpg = XTOK * NTc < nt ? XTOK * NTc : nt;
     const int groups = (nt + tpg - 1) / tpg;
-    const size_t lds = 2 * (size_t)tpg * XNT * BP * 2 + (size_t)MW * XUNIT_B;
-    const dim3 grid((rows + 16 * MW - 1) / (16 * MW), groups);
+    /* 8 waves of rows per workgroup when there are three or more token
+     * groups of four tiles (each workgroup then stages a group's x terms for
+     * 128 rows; 7168 x 7168 at nt 64: 75.0 -> 67.4 us), else 4 (at nt 16-32 the
+     * extra workgroups of 4 waves are faster: 50.5 vs 57.8 us at nt 16) */
+    const int mw = (groups >= 3 && NTc == 4) ? 8 : 4;
+    const size_t lds = 2 * (size_t)tpg * XNT * BP * 2 + (size_t)mw * XUNIT_B;
+    const dim3 grid((rows + 16 * mw - 1) / (16 * mw), groups);
     static bool opted = false;
     if (!opted) {
-        optin(k_fp8_mxn<1, false>); optin(k_fp8_mxn<2, false>); optin(k_fp8_mxn<3, false>);
-        optin(k_fp8_mxn<4, false>); optin(k_fp8_mxn<5, false>); optin(k_fp8_mxn<6, false>);
-        optin(k_fp8_mxn<7, false>); optin(k_fp8_mxn<1, true>); optin(k_fp8_mxn<2, true>);
-        optin(k_fp8_mxn<3, true>); optin(k_fp8_mxn<4, true>); optin(k_fp8_mxn<5, true>);
-        optin(k_fp8_mxn<6, true>); optin(k_fp8_mxn<7, true>);
+        optin(k_fp8_mxn<1, false, 4>); optin(k_fp8_mxn<2, false, 4>); optin(k_fp8_mxn<3, false, 4>);
+        optin(k_fp8_mxn<4, false, 4>); optin(k_fp8_mxn<5, false, 4>); optin(k_fp8_mxn<6, false, 4>);
+        optin(k_fp8_mxn<7, false, 4>); optin(k_fp8_mxn<1, true, 4>); optin(k_fp8_mxn<2, true, 4>);
+        optin(k_fp8_mxn<3, true, 4>); optin(k_fp8_mxn<4, true, 4>); optin(k_fp8_mxn<5, true, 4>);
+        optin(k_fp8_mxn<6, true, 4>); optin(k_fp8_mxn<7, true, 4>);
+        optin(k_fp8_mxn<4, false, 8>); optin(k_fp8_mxn<4, true, 8>);
         opted = true;
     }
     const bool uni = xs_uniform(blk_r, blk_c);
@@ -826,22 +834,23 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
                            (uint16_t *)xscratch, x, nt, cols, cpad);
         HIP_OK(hipGetLastError(), "fp8 mxn x split launch");
     }
-#define XN(NTV) do {                                                                           \
+#define XN(NTV, MWV) do {                                                                      \
         if (uni)                                                                               \
-            hipLaunchKernelGGL((k_fp8_mxn<NTV, true>), grid, dim3(64 * MW), lds, st, y, x, W, S, \
-                               rows, cols, sc, blk_r, bc_m, nt, tpg, xt, cpad);                 \
+            hipLaunchKernelGGL((k_fp8_mxn<NTV, true, MWV>), grid, dim3(64 * MWV), lds, st, y, x,  \
+                               W, S, rows, cols, sc, blk_r, bc_m, nt, tpg, xt, cpad);           \
         else                                                                                   \
-            hipLaunchKernelGGL((k_fp8_mxn<NTV, false>), grid, dim3(64 * MW), lds, st, y, x, W,  \
-                               S, rows, cols, sc, blk_r, bc_m, nt, tpg, xt, cpad);              \
+            hipLaunchKernelGGL((k_fp8_mxn<NTV, false, MWV>), grid, dim3(64 * MWV), lds, st, y, x, \
+                               W, S, rows, cols, sc, blk_r, bc_m, nt, tpg, xt, cpad);           \
     } while (0)
-    switch (NTc) {
-    case 1: XN(1); break;
-    case 2: XN(2); break;
-    case 3: XN(3); break;
-    case 4: XN(4); break;
-    case 5: XN(5); break;
-    case 6: XN(6); break;
-    default: XN(7); break;
+    if (mw == 8) XN(4, 8);
+    else switch (NTc) {
+    case 1: XN(1, 4); break;
+    case 2: XN(2, 4); break;
+    case 3: XN(3, 4); break;
+    case 4: XN(4, 4); break;
+    case 5: XN(5, 4); break;
+    case 6: XN(6, 4); break;
+    default: XN(7, 4); break;
     }
 #undef XN
     HIP_OK(hipGetLastError(), "fp8 mxn launch");

@@ -191,14 +191,15 @@ def test_reference_gpu_gate(gpu, dsv4):
                                           (500, 2048, 13), (70, 16384, 2), (33, 4096, 9),
                                           (7168, 7168, 64), (77, 1040, 21), (16, 112, 6),
                                           (1000, 7168, 11), (257, 2096, 20), (64, 16, 4),
-                                          (200, 4096, 33), (18, 3072, 7)])
+                                          (200, 4096, 33), (18, 3072, 7), (300, 1536, 48)])
 def test_batched_bit_identical(gpu, dsv4, rows, cols, nt):
     """E8M0 scales: the matrix-core form, whose batched kernel runs the
     single-token chain per (row, token) -- every token's row equals the
     single-token GEMV's bits, whatever column of which tile it takes (up to
     64 tokens, ragged row tiles, columns not a multiple of the 256-byte unit
-    or of the 1024-column segment); cols not a multiple of 16 take the VALU
-    form, whose batched kernel keeps its bits the same way."""
+    or of the 1024-column segment; nt 48 and 64 take the 8-wave workgroups,
+    nt 48 with a ragged last token group); cols not a multiple of 16 take the
+    VALU form, whose batched kernel keeps its bits the same way."""
     W, Sf, Se, _ = common.fp8_problem(21, rows, cols)
     x = np.random.default_rng(22).standard_normal((nt, cols), dtype=np.float32)
     y1, m = _run(dsv4, W, Se, x[0])

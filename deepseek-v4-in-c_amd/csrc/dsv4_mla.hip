@@ -854,6 +854,7 @@ k_tk_part(unsigned long long *__restrict__ cand, unsigned long long *__restrict_
     constexpr int BPT = TK_BINS / PT_THREADS;      /* 8 bins per thread */
     __shared__ uint32_t wsum[NW], res[2];
     __shared__ uint32_t scnt[PT_EPT][NW];
+    __shared__ unsigned long long wcnt[NW], wbase;
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int e0 = blockIdx.x * PT_ELEMS + tid;     /* slot m: e0 + m PT_THREADS */
@@ -899,7 +900,11 @@ k_tk_part(unsigned long long *__restrict__ cand, unsigned long long *__restrict_
 
     /* elements of higher bins and of B, as composites (key << 32 | ~index),
      * appended in any order to cand[] and bsel[]: one 64-bit atomic per
-     * wave takes both places (cand[] count in the low word, bsel[] high) */
+     * workgroup takes both places (cand[] count in the low word, bsel[]
+     * high; one per wave had 128 returning atomics queue on one address, 2 us
+     * at C4). B's elements also go to this workgroup's list in index order
+     * (read by the final pass only when B holds more than RF_LIST elements),
+     * written while the atomic is in flight. */
     unsigned long long ma[PT_EPT], mb[PT_EPT];
     uint32_t na = 0u, nbw = 0u;
 #pragma unroll
@@ -909,36 +914,16 @@ k_tk_part(unsigned long long *__restrict__ cand, unsigned long long *__restrict_
         mb[m] = __ballot(in && (key[m] >> 21) == B);
         na += (uint32_t)__popcll(ma[m]);
         nbw += (uint32_t)__popcll(mb[m]);
-    }
-    if (na | nbw) {
-        unsigned long long at = 0ull;
-        if (lane == 0)
-            at = atomicAdd(reinterpret_cast<unsigned long long *>(meta + MT_CNT),
-                           (unsigned long long)na | ((unsigned long long)nbw << 32));
-        uint32_t pa = (uint32_t)__shfl((int)(uint32_t)at, 0, 64);
-        uint32_t pb = (uint32_t)__shfl((int)(uint32_t)(at >> 32), 0, 64);
-#pragma unroll
-        for (int m = 0; m < PT_EPT; m++) {
-            const uint32_t i = (uint32_t)(e0 + m * PT_THREADS);
-            const unsigned long long comp = ((unsigned long long)key[m] << 32) | (0xFFFFFFFFull - i);
-            if ((ma[m] >> lane) & 1ull) {
-                const uint32_t pos = pa + (uint32_t)__popcll(ma[m] & lt);
-                if (pos < (uint32_t)TK_KMAX) cand[pos] = comp;
-            } else if ((mb[m] >> lane) & 1ull) {
-                const uint32_t pos = pb + (uint32_t)__popcll(mb[m] & lt);
-                if (pos < (uint32_t)RF_LIST) bsel[pos] = comp;
-            }
-            pa += (uint32_t)__popcll(ma[m]);
-            pb += (uint32_t)__popcll(mb[m]);
-        }
-    }
-
-    /* elements of B, again: this workgroup's list, in index order (read by
-     * the final pass only when B holds more than RF_LIST elements) */
-#pragma unroll
-    for (int m = 0; m < PT_EPT; m++)
         if (lane == 0) scnt[m][wid] = (uint32_t)__popcll(mb[m]);
+    }
+    if (lane == 0) wcnt[wid] = (unsigned long long)na | ((unsigned long long)nbw << 32);
     __syncthreads();
+    if (tid == 0) {
+        unsigned long long all = 0ull;
+#pragma unroll
+        for (int w = 0; w < NW; w++) all += wcnt[w];
+        wbase = all ? atomicAdd(reinterpret_cast<unsigned long long *>(meta + MT_CNT), all) : 0ull;
+    }
     uint32_t off[PT_EPT], tot = 0u;
 #pragma unroll
     for (int m = 0; m < PT_EPT; m++)
@@ -954,6 +939,25 @@ k_tk_part(unsigned long long *__restrict__ cand, unsigned long long *__restrict_
             mine[off[m] + (uint32_t)__popcll(mb[m] & lt)] =
                 ((unsigned long long)key[m] << 32) | (uint32_t)(e0 + m * PT_THREADS);
     if (tid == 0) bcnt[blockIdx.x] = tot;
+    __syncthreads();
+    unsigned long long at = wbase;
+#pragma unroll
+    for (int w = 0; w < NW; w++) at += w < wid ? wcnt[w] : 0ull;
+    uint32_t pa = (uint32_t)at, pb = (uint32_t)(at >> 32);
+#pragma unroll
+    for (int m = 0; m < PT_EPT; m++) {
+        const uint32_t i = (uint32_t)(e0 + m * PT_THREADS);
+        const unsigned long long comp = ((unsigned long long)key[m] << 32) | (0xFFFFFFFFull - i);
+        if ((ma[m] >> lane) & 1ull) {
+            const uint32_t pos = pa + (uint32_t)__popcll(ma[m] & lt);
+            if (pos < (uint32_t)TK_KMAX) cand[pos] = comp;
+        } else if ((mb[m] >> lane) & 1ull) {
+            const uint32_t pos = pb + (uint32_t)__popcll(mb[m] & lt);
+            if (pos < (uint32_t)RF_LIST) bsel[pos] = comp;
+        }
+        pa += (uint32_t)__popcll(ma[m]);
+        pb += (uint32_t)__popcll(mb[m]);
+    }
 }
 
 /* Final pass. The composites (key << 32 | ~index) order the scores as the

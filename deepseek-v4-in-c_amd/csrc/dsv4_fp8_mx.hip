@@ -131,8 +131,10 @@ inline uint32_t bc_magic(int blk_c)
 /* Unit u of the tile whose row 0 is W + row0 * cols (rows past `rows` read
  * the last row, pieces past `cols` the row's first piece: their results are
  * discarded or zeroed). srow: this lane's scale row offset, (row / blk_r) sc
- * for its A row, row0 + lane % 16 clamped to the last row. */
-template <bool UNI>
+ * for its A row, row0 + lane % 16 clamped to the last row. STREAM: a
+ * non-temporal load, for weights read once (the single-token kernel); the
+ * batched kernel's token groups read each unit again, from L2. */
+template <bool UNI, bool STREAM = true>
 __device__ __forceinline__ void xu_load(XUnit<UNI> &U, const uint8_t *W, const uint8_t *S,
                                         int srow, uint32_t bc_m, int row0, int rows, int cols,
                                         int k0, int lane)
@@ -149,7 +151,10 @@ __device__ __forceinline__ void xu_load(XUnit<UNI> &U, const uint8_t *W, const u
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         const int r = min(row0 + 4 * q + (lane >> 4), rows - 1);
-        U.w[q] = ldg16_stream(W + (size_t)r * cols + cc);
+        if (STREAM)
+            U.w[q] = ldg16_stream(W + (size_t)r * cols + cc);
+        else
+            U.w[q] = *(const DSV4_GLOBAL u32x4 *)(W + (size_t)r * cols + cc);
     }
 }
 
@@ -517,9 +522,14 @@ __device__ __forceinline__ void xp_store(uint16_t *bl, const u32x4 *v, int ntok,
  * it requested one unit earlier, into terms in B buffer u % 2, each wave
  * stages its weight unit u (requested two units earlier), requests x(u + 1)
  * and weight unit u + 2, and after one barrier runs its tile's 8 steps x NT
- * column tiles. At each segment's end the segment's accumulators join the
- * running sums in segment order. Every register array is indexed by
- * compile-time constants: the unit loop is unrolled by a segment's 4. */
+ * column tiles. The weights are read with ordinary loads, so that the
+ * other token groups read each unit again from L2: their workgroups for the
+ * same rows are gridDim.x apart in launch order, so when gridDim.x is a
+ * multiple of 8 (7168 rows: 56) they run on one XCD and share its L2 (7168 x
+ * 7168 at nt 64: 66.5 -> 63.6 us against non-temporal loads). At each
+ * segment's end the segment's accumulators join the running sums in segment
+ * order. Every register array is indexed by compile-time constants: the
+ * unit loop is unrolled by a segment's 4. */
 template <int NT, bool UNI, int MW>
 __global__ void __launch_bounds__(64 * MW)
 k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__restrict__ W,
@@ -577,8 +587,8 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
     /* uniform scales: the current segment's (ssb) and the next one's */
     uint32_t ssb = UNI ? xs_seg(S, srow, bc_m, 0, cols, lane) : 0u, ssn = 0u;
     __builtin_amdgcn_sched_barrier(0);
-    xu_load(P[0], W, S, srow, bc_m, wrow0, rows, cols, 0, lane);
-    xu_load(P[1], W, S, srow, bc_m, wrow0, rows, cols, XU * min(1, nu - 1), lane);
+    xu_load<UNI, false>(P[0], W, S, srow, bc_m, wrow0, rows, cols, 0, lane);
+    xu_load<UNI, false>(P[1], W, S, srow, bc_m, wrow0, rows, cols, XU * min(1, nu - 1), lane);
     __builtin_amdgcn_sched_barrier(0);
     for (int s0 = 0; s0 < nu; s0 += XSEG_U) {
 #pragma unroll
@@ -602,8 +612,8 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
                 ssn = xs_seg(S, srow, bc_m, XU * (min(s0 + XSEG_U, nu - 1) & ~(XSEG_U - 1)),
                              cols, lane);
             __builtin_amdgcn_sched_barrier(0);
-            xu_load(P[j & 1], W, S, srow, bc_m, wrow0, rows, cols, XU * min(u + 2, nu - 1),
-                    lane);
+            xu_load<UNI, false>(P[j & 1], W, S, srow, bc_m, wrow0, rows, cols,
+                                XU * min(u + 2, nu - 1), lane);
             __builtin_amdgcn_sched_barrier(0);
             if (u < nu) {
                 __syncthreads();          /* B(u) whole; every wave is past B(u - 2)'s reads */

@@ -297,11 +297,12 @@ int upload_qmat(const DSV4QMat *m, int sfmt)
     return 0;
 }
 
-/* y[rows] = the view's rows . x (x and y device pointers), on stream st
- * (the library stream by default). */
-int res_gemv(const View &v, int rows, float *d_y, const float *d_x, hipStream_t st = nullptr)
+/* y[rows] = the view's rows . x (x and y device pointers), on stream st.
+ * A null st is the default stream, as in every stream-ordered entry point:
+ * it is never replaced by the library's own stream, which is non-blocking
+ * and so not ordered against the default stream. */
+int res_gemv(const View &v, int rows, float *d_y, const float *d_x, hipStream_t st)
 {
-    if (!st) st = g_stream;
     const Res &r = *v.r;
     if (r.wdt == DSV4_WBF16)
         return dsv4_bf16_gemv_launch(d_y, d_x, (const uint16_t *)v.w, rows, r.cols, st);
@@ -545,7 +546,8 @@ void dsv4_gpu_mmq(float *y, const float *x, const DSV4QMat *m)
     const size_t yo = s.add((size_t)m->rows * sizeof(float));
     size_t end;
     if (stage_push(s, &end) != 0) abort();
-    const int rc = res_gemv(v, m->rows, (float *)(g_ar.d + yo), (const float *)(g_ar.d + xo));
+    const int rc = res_gemv(v, m->rows, (float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
+                            g_stream);
     if (rc != 0 || stage_pull(yo, (size_t)m->rows * sizeof(float), y) != 0) {
         DSV4_ERR("mmq failed");
         abort();
@@ -678,7 +680,8 @@ int dsv4_gpu_head_argmax(const float *x, const DSV4QMat *head)
     const size_t to = s.add(sizeof(int));
     size_t end;
     if (stage_push(s, &end) != 0) return -1;
-    if (res_gemv(v, head->rows, (float *)(g_ar.d + lo), (const float *)(g_ar.d + xo)) != 0 ||
+    if (res_gemv(v, head->rows, (float *)(g_ar.d + lo), (const float *)(g_ar.d + xo),
+                 g_stream) != 0 ||
         dsv4_argmax_launch((int *)(g_ar.d + to), (const float *)(g_ar.d + lo), head->rows,
                            g_amax.p, g_stream) != 0)
         return -1;

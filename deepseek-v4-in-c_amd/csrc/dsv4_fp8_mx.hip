@@ -701,7 +701,8 @@ int mx_env(const char *name, int dflt)
  * (rows past 8 segments: 8 waves of two segments; else the smallest of 1,
  * 2, 4 and nseg that gives `target` waves in all, else nseg), segments per
  * wave, tiles per workgroup (8 waves a workgroup, or P when P does not
- * divide 8), the x planes' pitch, LDS bytes and the persistent grid (at most
+ * divide 8; halved while that leaves most CUs idle), the x planes' pitch,
+ * LDS bytes and the persistent grid (at most
  * what fits on the CUs at once). Measured on MI355X (E8M0, cold weights):
  * 7168 x 7168 is fastest at P 4 x 2 tiles, 24576 x 1536 at P 1 x 8 tiles,
  * 7168 x 16384 at P 8, the LM head at P 1. */
@@ -726,9 +727,15 @@ bool mx1_config(int rows, int cols, int n, Dsv4Fp8Mx *b)
         spw = (nseg + P - 1) / P;
         P = (nseg + spw - 1) / spw;                    /* no wave without a segment */
         tpw = 8 / P;
+        if (tpw < 1) tpw = 1;
+        /* fewer tiles per workgroup while the grid would leave more than half
+         * the CUs without one (1024 x 4096: 7.95 -> 6.44 us, 8192 x 1024:
+         * 7.75 -> 6.3 us; 7168 x 7168, with 224 workgroups of two tiles,
+         * keeps them: one tile each measured 13.7 against 12.9 us) */
+        while (tpw > 1 && (long long)((ntiles + tpw - 1) / tpw) * n < mx_cu_count() / 2)
+            tpw /= 2;
         const int ft = mx_env("DSV4_GPU_MX_TPW", 0);
         if (ft >= 1 && ft * P <= 8) tpw = ft;
-        if (tpw < 1) tpw = 1;
         if (tpw > ntiles) tpw = ntiles;
         nw = P * tpw;
         if (nw * 64 * X1_XM >= nu_all * (XU / 4)) break;   /* x staging coverage */

@@ -1517,8 +1517,10 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
     }
     OK(dsv4_block_prep_launch(&pp, st));
     /* q: wq_b (each head's norm and RoPE happen inside the attention, on its
-     * copy) */
-    OK(res_gemv(b.wq_b.view(), H * hd, b.q, b.qr, st));
+     * copy), and the indexer's wq_b when the indexer runs: both read qr, so
+     * they share one listed launch */
+    XJob qj[2] = {{&b.wq_b, b.q, H * hd}, {&b.iwq_b, b.idx_q, c.idx_heads * c.idx_dim}};
+    OK(x_gemvs(qj, use_idx ? 2 : 1, b.qr, st));
     const int n_win = pos + 1 < c.window ? pos + 1 : c.window;
     int take = 0, mode = 1;
     if (c.ratio > 0) {
@@ -1540,7 +1542,6 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
         const int avail = b.n_comp;
         if (use_idx) {
             const int ih = c.idx_heads, idd = c.idx_dim;
-            OK(res_gemv(b.iwq_b.view(), ih * idd, b.idx_q, b.qr, st));
             take = avail < c.idx_topk ? avail : c.idx_topk;
             const int hist = dsv4_topk_takes_hist(avail, take);
             /* the keys are the compressed region read at index_head_dim

@@ -29,11 +29,15 @@ pytestmark = pytest.mark.gpu
 
 LAYER = 310
 N_POS = 40
+# resident matrices are keyed by host pointer: their host arrays stay
+# allocated for the process, so no later array can reuse an address
+_KEEP = []
 
 
-def _bind(D, L, rng, keep):
+def _bind(D, L, rng, keep, layer=LAYER, ratio=4, n_pos=N_POS, itop=4):
     hidden, ql, H, hd, rd, win, ol, og = 4096, 1024, 64, 512, 64, 128, 1024, 8
-    ih, idd, itop, ratio = 64, 128, 4, 4
+    ih, idd = 64, 128
+    coff = 2 if ratio == 4 else 1
 
     def fp8(rows, cols):
         W = common.fp8_codes(rng, (rows, cols))
@@ -57,36 +61,41 @@ def _bind(D, L, rng, keep):
         return v.ctypes.data
 
     half = rd // 2
-    th = np.arange(N_POS + 8)[:, None] / (160000.0 ** (np.arange(half) * 2.0 / rd))[None, :]
+    th = np.arange(n_pos + 8)[:, None] / (160000.0 ** (np.arange(half) * 2.0 / rd))[None, :]
     cs, sn = np.cos(th).astype(np.float32), np.sin(th).astype(np.float32)
     keep += [cs, sn]
     w = D.AttnW()
     w.wq_a, w.wq_b, w.wkv = fp8(ql, hidden), fp8(H * hd, ql), fp8(hd, hidden)
     w.wo_a, w.wo_b = fp8(og * ol, H * hd // og), fp8(hidden, og * ol)
-    w.comp_wkv, w.comp_wgate = bf16(2 * hd, hidden), bf16(2 * hd, hidden)
-    w.idx_wq_b, w.idx_wproj = fp8(ih * idd, ql), bf16(ih, hidden)
+    w.comp_wkv, w.comp_wgate = bf16(coff * hd, hidden), bf16(coff * hd, hidden)
+    if ratio == 4:
+        w.idx_wq_b, w.idx_wproj = fp8(ih * idd, ql), bf16(ih, hidden)
     w.q_norm, w.kv_norm, w.comp_norm = vec(ql), vec(hd), vec(hd)
-    w.sink, w.comp_ape = vec(H, 1.0, 0.0), vec(ratio * 2 * hd, 0.5, 0.0)
+    w.sink, w.comp_ape = vec(H, 1.0, 0.0), vec(ratio * coff * hd, 0.5, 0.0)
     w.rope_cos, w.rope_sin = cs.ctypes.data, sn.ctypes.data
     c = D.AttnCfg(hidden=hidden, q_lora=ql, n_heads=H, head_dim=hd, rope_dim=rd, window=win,
-                  ratio=ratio, idx_heads=ih, idx_dim=idd, idx_topk=itop, o_groups=og,
-                  o_lora=ol, max_pos=N_POS + 8, rms_eps=1e-6)
-    assert L.dsv4_gpu_attn_bind(LAYER, ctypes.byref(c), ctypes.byref(w)) == 0
+                  ratio=ratio, idx_heads=ih if ratio == 4 else 0, idx_dim=idd, idx_topk=itop,
+                  o_groups=og, o_lora=ol, max_pos=n_pos + 8, rms_eps=1e-6)
+    assert L.dsv4_gpu_attn_bind(layer, ctypes.byref(c), ctypes.byref(w)) == 0
     return hidden
+
+
+def _host_steps(L, layer, X):
+    out = np.zeros_like(X)
+    for p in range(X.shape[0]):
+        assert L.dsv4_gpu_attn_step(out[p].ctypes.data, X[p].ctypes.data, layer, p) == 0
+    return out
 
 
 def test_attention_step_on_default_and_created_streams(gpu, dsv4):
     import torch
     L, D = gpu, dsv4
     rng = np.random.default_rng(5)
-    keep = []
-    hidden = _bind(D, L, rng, keep)
+    hidden = _bind(D, L, rng, _KEEP)
     X = (rng.standard_normal((N_POS, hidden)) * 0.5).astype(np.float32)
 
     # the host-buffer entry point: the library's stream, synchronised per step
-    want = np.zeros((N_POS, hidden), np.float32)
-    for p in range(N_POS):
-        assert L.dsv4_gpu_attn_step(want[p].ctypes.data, X[p].ctypes.data, LAYER, p) == 0
+    want = _host_steps(L, LAYER, X)
     assert np.isfinite(want).all() and np.abs(want).max() > 0.0
 
     dX = torch.from_numpy(X).to("cuda:0")

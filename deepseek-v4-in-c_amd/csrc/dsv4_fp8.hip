@@ -128,6 +128,7 @@ struct Fp8Groups {
     int n = 1;
     long long x = 0, y = 0, w = 0, s = 0;
     int list = 0;
+    bool valu = false;                  /* the VALU form even for E8M0 scales */
     const uint8_t *Wl[FP8_LIST_MAX] = {};
     const void *Sl[FP8_LIST_MAX] = {};
     float *yl[FP8_LIST_MAX] = {};
@@ -747,7 +748,7 @@ int fp8_gemv(float *y, const float *x, const uint8_t *W, const void *S, int sfmt
     const int sc = (cols + blk_c - 1) / blk_c;
     Fp8Geom g;
     const bool aligned = (((uintptr_t)x | (uintptr_t)W) & 15) == 0;
-    if (mx_form(sfmt, x, W, cols, blk_r, blk_c)) {
+    if (!gp.valu && mx_form(sfmt, x, W, cols, blk_r, blk_c)) {
         Dsv4Fp8Mx a;
         a.y = y; a.x = x; a.w = W; a.s = (const uint8_t *)S;
         a.rows = rows; a.cols = cols; a.sc = sc; a.blk_r = blk_r; a.blk_c = blk_c;
@@ -803,14 +804,16 @@ int fp8_gemv(float *y, const float *x, const uint8_t *W, const void *S, int sfmt
 
 int dsv4_fp8_gemv_launch(float *y, const float *x, const uint8_t *W,
                          const void *S, int sfmt, int rows, int cols,
-                         int blk_r, int blk_c, hipStream_t st)
+                         int blk_r, int blk_c, hipStream_t st, bool valu)
 {
-    return fp8_gemv(y, x, W, S, sfmt, rows, cols, blk_r, blk_c, Fp8Groups{}, st);
+    Fp8Groups gp;
+    gp.valu = valu;
+    return fp8_gemv(y, x, W, S, sfmt, rows, cols, blk_r, blk_c, gp, st);
 }
 
 int dsv4_fp8_gemv_list_launch(const float *x, int cols, int sfmt, int blk_r, int blk_c,
                               int n, const uint8_t *const *W, const void *const *S,
-                              float *const *y, const int *rows, hipStream_t st)
+                              float *const *y, const int *rows, hipStream_t st, bool valu)
 {
     if (n < 1 || n > FP8_LIST_MAX) {
         DSV4_ERR("fp8 gemv list: %d matrices (1 .. %d)", n, FP8_LIST_MAX);
@@ -819,6 +822,7 @@ int dsv4_fp8_gemv_list_launch(const float *x, int cols, int sfmt, int blk_r, int
     Fp8Groups gp;
     gp.n = n;
     gp.list = 1;
+    gp.valu = valu;
     int rmax = 0;
     for (int i = 0; i < n; i++) {
         if (rows[i] <= 0 || (((uintptr_t)W[i]) & 15)) {
@@ -832,7 +836,7 @@ int dsv4_fp8_gemv_list_launch(const float *x, int cols, int sfmt, int blk_r, int
     if (!fp8_geom(cols, &g) || !blocking_ok(blk_r, blk_c) || (((uintptr_t)x) & 15)) {
         for (int i = 0; i < n; i++)
             if (dsv4_fp8_gemv_launch(y[i], x, W[i], S[i], sfmt, rows[i], cols, blk_r, blk_c,
-                                     st) != 0)
+                                     st, valu) != 0)
                 return -1;
         return 0;
     }
@@ -843,10 +847,11 @@ int dsv4_fp8_gemv_groups_launch(float *y, const float *x, const uint8_t *W,
                                 const void *S, int sfmt, int rows, int cols, int blk_r,
                                 int blk_c, int groups, long long y_stride,
                                 long long x_stride, long long w_stride,
-                                long long s_stride, hipStream_t st)
+                                long long s_stride, hipStream_t st, bool valu)
 {
     Fp8Groups gp;
     gp.n = groups;
+    gp.valu = valu;
     gp.y = y_stride; gp.x = x_stride; gp.w = w_stride; gp.s = s_stride;
     if (groups > 1 && (((uintptr_t)(x_stride * 4) | (uintptr_t)w_stride) & 15)) {
         DSV4_ERR("fp8 gemv groups: strides break 16-byte alignment");

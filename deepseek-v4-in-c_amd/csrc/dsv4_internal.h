@@ -27,10 +27,13 @@
 size_t dsv4_lds_limit(void);
 
 /* Block-scaled FP8 GEMV. sfmt 0 = E8M0 bytes, 1 = fp32. S is the scale grid
- * ceil(rows/blk_r) x sc with sc = ceil(cols/blk_c). Returns 0 / -1. */
+ * ceil(rows/blk_r) x sc with sc = ceil(cols/blk_c). Returns 0 / -1. valu:
+ * the VALU form even for E8M0 scales, for a caller whose results need not
+ * share the bits of the batched form (the attention block's projections);
+ * at batch 1 it is the faster form at every E8M0 shape measured. */
 int dsv4_fp8_gemv_launch(float *y, const float *x, const uint8_t *W,
                          const void *S, int sfmt, int rows, int cols,
-                         int blk_r, int blk_c, hipStream_t st);
+                         int blk_r, int blk_c, hipStream_t st, bool valu = false);
 
 /* The matrix-core form of the FP8 GEMV for E8M0-scaled matrices
  * (dsv4_fp8_mx.hip): one launch of n GEMVs that read x + i * x_stride (or,
@@ -76,14 +79,15 @@ int dsv4_fp8_gemv_groups_launch(float *y, const float *x, const uint8_t *W,
                                 const void *S, int sfmt, int rows, int cols, int blk_r,
                                 int blk_c, int groups, long long y_stride,
                                 long long x_stride, long long w_stride,
-                                long long s_stride, hipStream_t st);
+                                long long s_stride, hipStream_t st, bool valu = false);
 
 /* Up to four FP8 matrices of one width, scale format and blocking that read
  * the same x, in one launch: y[i] = W[i] x over rows[i] rows, each with the
  * bits of its own plain launch. */
 int dsv4_fp8_gemv_list_launch(const float *x, int cols, int sfmt, int blk_r, int blk_c,
                               int n, const uint8_t *const *W, const void *const *S,
-                              float *const *y, const int *rows, hipStream_t st);
+                              float *const *y, const int *rows, hipStream_t st,
+                              bool valu = false);
 
 /* The same for up to four BF16 matrices of one width. */
 int dsv4_bf16_gemv_list_launch(const float *x, int cols, int n, const uint16_t *const *W,

@@ -33,58 +33,7 @@
 
 namespace {
 
-constexpr int B16_PART_MAX = 4096;
-
-/* Several matrices of one width reading the same x in one launch
- * (blockIdx.y = matrix): n == 0 is the plain GEMV. */
-constexpr int B16_LIST_MAX = 4;
-struct B16List {
-    int n = 0;
-    const uint16_t *W[B16_LIST_MAX] = {};
-    float *y[B16_LIST_MAX] = {};
-    int rows[B16_LIST_MAX] = {};
-};
-
-struct B16Geom {
-    int ch, tc, nch, wg, rg;
-};
-
-bool b16_geom(int cols, B16Geom *g)
-{
-    if (cols <= 0 || (cols & 7)) return false;
-    const int ch = cols >> 3;
-    int tc, nch;
-    if (ch <= 64) {
-        tc = 1;
-        while (tc < ch) tc <<= 1;
-        nch = 1;
-    } else {
-        tc = 64 * ((ch + 511) / 512);
-        if (tc > 256) tc = 256;
-        nch = (ch + tc - 1) / tc;
-    }
-    if (nch > 8) return false;                   /* cols <= 16384 */
-    g->ch = ch;
-    g->tc = tc;
-    g->nch = nch;
-    g->wg = tc * (256 / tc);
-    g->rg = g->wg / tc;
-    return true;
-}
-
-/* 8 bf16 (one chunk) dotted with 8 activations, two interleaved chains. */
-__device__ __forceinline__ float dot8_bf16(const u32x4 v, const float *xr)
-{
-    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-    float p0 = __uint_as_float(u[0] << 16) * xr[0];
-    float p1 = __uint_as_float(u[0] & 0xFFFF0000u) * xr[1];
-#pragma unroll
-    for (int e = 1; e < 4; e++) {
-        p0 = fmaf(__uint_as_float(u[e] << 16), xr[2 * e], p0);
-        p1 = fmaf(__uint_as_float(u[e] & 0xFFFF0000u), xr[2 * e + 1], p1);
-    }
-    return p0 + p1;
-}
+#include "dsv4_bf16_rows.h"
 
 template <int NCH, int R>
 __global__ void __launch_bounds__(256)
@@ -93,74 +42,8 @@ k_bf16_gemv(float *__restrict__ y, const float *__restrict__ x,
             B16List ls)
 {
     extern __shared__ float part[];                 /* [waves per row][rows_per_wg] */
-    if (ls.n) {
-        W = ls.W[blockIdx.y];
-        y = ls.y[blockIdx.y];
-        rows = ls.rows[blockIdx.y];
-        if ((int)blockIdx.x * rows_per_wg >= rows) return;   /* the whole workgroup */
-    }
-    const int tid = threadIdx.x;
-    const int g = tid / tc, j = tid - g * tc;
-    const int rg = blockDim.x / tc;
-    const int ch = cols >> 3;
-    const int lane = tid & 63;
-    const int row0 = blockIdx.x * rows_per_wg;
-    const int rend = min(rows, row0 + rows_per_wg);
-    const int nloc = rend - row0;
-    const uint8_t *Wb = reinterpret_cast<const uint8_t *>(W);
-    const size_t rowb = (size_t)cols * 2;
-
-    float xr[NCH][8];
-    bool act[NCH];
-#pragma unroll
-    for (int n = 0; n < NCH; n++) {
-        const int c = j + n * tc;
-        act[n] = c < ch;
-        const int cc = min(c, ch - 1);
-        const f32x4 a = ldf4(x + cc * 8), b = ldf4(x + cc * 8 + 4);
-        xr[n][0] = a.x; xr[n][1] = a.y; xr[n][2] = a.z; xr[n][3] = a.w;
-        xr[n][4] = b.x; xr[n][5] = b.y; xr[n][6] = b.z; xr[n][7] = b.w;
-    }
-
-    for (int rb = row0 + g * R; rb < row0 + ((nloc + rg * R - 1) / (rg * R)) * rg * R;
-         rb += rg * R) {
-        u32x4 v[R][NCH];
-#pragma unroll
-        for (int i = 0; i < R; i++) {
-            const int r = min(rb + i, rend - 1);
-#pragma unroll
-            for (int n = 0; n < NCH; n++) {
-                const int c = min(j + n * tc, ch - 1);
-                v[i][n] = ldg16_stream(Wb + (size_t)r * rowb + (size_t)c * 16);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < R; i++) {
-            float a = 0.0f;
-#pragma unroll
-            for (int n = 0; n < NCH; n++) {
-                const float d = a + dot8_bf16(v[i][n], xr[n]);
-                a = act[n] ? d : a;
-            }
-            if (tc <= 64) {
-                const float s = seg_sum_rt(a, tc);
-                if (j == tc - 1 && rb + i < rend) y[rb + i] = s;
-            } else {
-                const float s = seg_sum<64>(a);
-                const int rl = rb + i - row0;
-                if (lane == 63 && rl < nloc) part[(j >> 6) * rows_per_wg + rl] = s;
-            }
-        }
-    }
-    if (tc > 64) {
-        __syncthreads();
-        const int wpr = tc >> 6;
-        for (int rl = tid; rl < nloc; rl += blockDim.x) {
-            float s = part[rl];
-            for (int w = 1; w < wpr; w++) s += part[w * rows_per_wg + rl];
-            y[row0 + rl] = s;
-        }
-    }
+    b16_rows<NCH, R>(y, x, W, rows, cols, tc, rows_per_wg, ls, (int)blockIdx.x,
+                     (int)blockIdx.y, part);
 }
 
 /* Batched (prefill): y[t][rows] for x[t][cols], t < nt, each (row, token)
@@ -275,31 +158,12 @@ template <int NCH>
 void b16_launch(const B16Geom &g, float *y, const float *x, const uint16_t *W, int rows,
                 int cols, const B16List &ls, hipStream_t st)
 {
-    /* two rows per thread per step while the loads fit the registers */
+    /* the plan's R: two rows per thread per step for up to 4 chunks */
     constexpr int R = NCH <= 4 ? 2 : 1;
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
-                hipSuccess ||
-            n <= 0)
-            n = 256;
-        cus = n;
-    }
-    const int step_rows = g.rg * R;
+    const B16Plan p = b16_plan(g, rows, ls.n);
     const int nm = ls.n ? ls.n : 1;
-    const int want = (2 * cus + nm - 1) / nm;       /* two workgroups per CU */
-    const int wpr = g.tc > 64 ? g.tc / 64 : 1;
-    int spw = ((rows + step_rows - 1) / step_rows + want - 1) / want;
-    const int max_spw = B16_PART_MAX / wpr / step_rows;
-    if (spw > max_spw) spw = max_spw;
-    if (spw < 1) spw = 1;
-    const int rows_per_wg = spw * step_rows;
-    const int grid = (rows + rows_per_wg - 1) / rows_per_wg;
-    const size_t lds = g.tc > 64 ? sizeof(float) * (size_t)wpr * rows_per_wg : 0;
-    hipLaunchKernelGGL((k_bf16_gemv<NCH, R>), dim3(grid, nm), dim3(g.wg), lds, st, y, x, W,
-                       rows, cols, g.tc, rows_per_wg, ls);
+    hipLaunchKernelGGL((k_bf16_gemv<NCH, R>), dim3(p.grid, nm), dim3(g.wg), p.lds, st, y, x, W,
+                       rows, cols, g.tc, p.rows_per_wg, ls);
 }
 
 int b16_dispatch(const B16Geom &g, float *y, const float *x, const uint16_t *W, int rows,

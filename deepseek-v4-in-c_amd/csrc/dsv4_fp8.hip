@@ -41,6 +41,8 @@
 
 namespace {
 
+#include "dsv4_bf16_rows.h"
+
 struct Fp8Geom {
     int ch;   /* 16-byte chunks per row                       */
     int tc;   /* threads per row (power of two <= 64, or k*64) */
@@ -166,23 +168,25 @@ __device__ __forceinline__ void load_step(u32x4 (*wv)[NCH], float *sv, const uin
  * step); with PF the next step's weights are in flight while this step's are
  * consumed. Rows that span several waves leave one partial per wave in LDS,
  * summed in wave order after a single barrier at the end. */
+/* The GEMV of workgroup (bx, by): rows [bx rows_per_wg, +rows_per_wg) of
+ * group or listed matrix by. part: LDS of [waves per row][rows_per_wg]
+ * floats, then x (XL). */
 template <int NCH, int R, int SF, int PF, int XL>
-__global__ void __launch_bounds__(256)
-k_fp8_gemv(float *__restrict__ y, const float *__restrict__ x,
-           const uint8_t *__restrict__ W, const void *__restrict__ S,
-           int rows, int cols, int sc, int blk_r, int blk_c, int tc,
-           int rows_per_wg, Fp8Groups gp)
+__device__ __forceinline__ void fp8_rows(float *__restrict__ y, const float *__restrict__ x,
+                                         const uint8_t *__restrict__ W,
+                                         const void *__restrict__ S, int rows, int cols, int sc,
+                                         int blk_r, int blk_c, int tc, int rows_per_wg,
+                                         const Fp8Groups &gp, int bx, int by, float *part)
 {
-    extern __shared__ float part[];     /* [waves per row][rows_per_wg], then x (XL) */
     if (gp.list) {
-        const int gi = blockIdx.y;
+        const int gi = by;
         W = gp.Wl[gi];
         S = gp.Sl[gi];
         y = gp.yl[gi];
         rows = gp.rl[gi];
-        if ((int)blockIdx.x * rows_per_wg >= rows) return;   /* the whole workgroup */
+        if (bx * rows_per_wg >= rows) return;     /* the whole workgroup */
     } else if (gp.n > 1) {
-        const size_t gi = blockIdx.y;
+        const size_t gi = by;
         y += gi * gp.y;
         x += gi * gp.x;
         W += gi * gp.w;
@@ -195,7 +199,7 @@ k_fp8_gemv(float *__restrict__ y, const float *__restrict__ x,
     const int rg = blockDim.x / tc;
     const int ch = cols >> 4;
     const int lane = tid & 63;
-    const int row0 = blockIdx.x * rows_per_wg;
+    const int row0 = bx * rows_per_wg;
     const int rend = min(rows, row0 + rows_per_wg);
     const int nloc = rend - row0;
     const int step_rows = rg * R;
@@ -319,6 +323,18 @@ k_fp8_gemv(float *__restrict__ y, const float *__restrict__ x,
             y[row0 + rl] = s;
         }
     }
+}
+
+template <int NCH, int R, int SF, int PF, int XL>
+__global__ void __launch_bounds__(256)
+k_fp8_gemv(float *__restrict__ y, const float *__restrict__ x,
+           const uint8_t *__restrict__ W, const void *__restrict__ S,
+           int rows, int cols, int sc, int blk_r, int blk_c, int tc,
+           int rows_per_wg, Fp8Groups gp)
+{
+    extern __shared__ float part[];     /* [waves per row][rows_per_wg], then x (XL) */
+    fp8_rows<NCH, R, SF, PF, XL>(y, x, W, S, rows, cols, sc, blk_r, blk_c, tc, rows_per_wg, gp,
+                                 (int)blockIdx.x, (int)blockIdx.y, part);
 }
 
 /* Batched: the per-(row, token) arithmetic of k_fp8_gemv with R = 1, looped
@@ -455,28 +471,44 @@ int cu_count()
     return g_cu_count;
 }
 
-template <int NCH, int R, int SF, int PF>
-void launch_gemv(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
-                 const void *S, int rows, int cols, int sc, int blk_r,
-                 int blk_c, int wgs_per_cu, const Fp8Groups &gp, hipStream_t st)
+/* Launch plan of the VALU form: x through LDS or not, the rows each
+ * workgroup owns, the grid along x and the dynamic LDS. */
+struct Fp8Plan {
+    int xl = 0, rows_per_wg = 0, grid = 0;
+    size_t lds = 0;
+};
+
+Fp8Plan fp8_plan(const Fp8Geom &g, int R, int rows, int cols, int wgs_per_cu, int ngroups)
 {
+    Fp8Plan p;
     /* x through LDS (one fetch per workgroup instead of one per row group)
      * measured faster on MI355X for narrow rows (24576x1536: 12.2 -> 11.8
      * us) and the widest (7168x16384: 24.8 -> 24.1 us), and within noise
      * or slower between them. */
-    const int xl = g.wg == 256 && (cols & 3) == 0 && (cols <= 2048 || cols >= 16384);
+    p.xl = g.wg == 256 && (cols & 3) == 0 && (cols <= 2048 || cols >= 16384);
     const int step_rows = g.rg * R;
     const int nsteps = (rows + step_rows - 1) / step_rows;
-    const int want = (wgs_per_cu * cu_count() + gp.n - 1) / gp.n;
+    const int want = (wgs_per_cu * cu_count() + ngroups - 1) / ngroups;
     int spw = (nsteps + want - 1) / want;              /* steps per workgroup */
     const int wpr = g.tc > 64 ? g.tc / 64 : 1;
     const int max_spw = PART_MAX / wpr / step_rows;
     if (spw > max_spw) spw = max_spw;
     if (spw < 1) spw = 1;
-    const int rows_per_wg = spw * step_rows;
-    const int grid = (rows + rows_per_wg - 1) / rows_per_wg;
-    const size_t lds = (g.tc > 64 ? sizeof(float) * (size_t)wpr * rows_per_wg : 0)
-                     + (xl ? sizeof(float) * (size_t)cols : 0);
+    p.rows_per_wg = spw * step_rows;
+    p.grid = (rows + p.rows_per_wg - 1) / p.rows_per_wg;
+    p.lds = (g.tc > 64 ? sizeof(float) * (size_t)wpr * p.rows_per_wg : 0)
+          + (p.xl ? sizeof(float) * (size_t)cols : 0);
+    return p;
+}
+
+template <int NCH, int R, int SF, int PF>
+void launch_gemv(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
+                 const void *S, int rows, int cols, int sc, int blk_r,
+                 int blk_c, int wgs_per_cu, const Fp8Groups &gp, hipStream_t st)
+{
+    const Fp8Plan p = fp8_plan(g, R, rows, cols, wgs_per_cu, gp.n);
+    const int xl = p.xl, rows_per_wg = p.rows_per_wg, grid = p.grid;
+    const size_t lds = p.lds;
     if (xl) {
         static bool opted = false;                  /* x of up to 64 KB + partials */
         if (!opted) {
@@ -737,6 +769,30 @@ bool mx_form(int sfmt, const float *x, const uint8_t *W, int cols, int blk_r, in
            (((uintptr_t)x | (uintptr_t)W) & 15) == 0;
 }
 
+/* The VALU form's launch parameters for a matrix of rows x cols: R rows per
+ * thread per step (at most blk_r's largest power-of-two divisor up to 4),
+ * the next step prefetched or not, workgroups per CU. Defaults from a sweep
+ * over the C1/C2 shapes on MI355X (R in 1, 2, 4; prefetch on/off; 1-8
+ * workgroups per CU): two rows per thread, prefetch only where the matrix
+ * is short, two workgroups per CU (four when rows are narrow). The
+ * environment can override each. None of these changes a row's arithmetic. */
+struct Fp8Valu {
+    int R, pf, wpc;
+};
+
+Fp8Valu fp8_valu(int rows, int cols, int blk_r)
+{
+    Fp8Valu v;
+    int R = env_int("DSV4_GPU_FP8_R", 2);
+    R = R >= 4 ? 4 : R >= 2 ? 2 : 1;
+    while (blk_r % R) R >>= 1;                   /* a step stays in one row block */
+    v.R = R;
+    v.pf = env_int("DSV4_GPU_FP8_PF", rows <= 4096 ? 1 : 0);
+    v.wpc = env_int("DSV4_GPU_FP8_WPC", cols >= 4096 ? 2 : 4);
+    if (v.wpc <= 0) v.wpc = 2;
+    return v;
+}
+
 int fp8_gemv(float *y, const float *x, const uint8_t *W, const void *S, int sfmt,
              int rows, int cols, int blk_r, int blk_c, const Fp8Groups &gp,
              hipStream_t st)
@@ -762,18 +818,9 @@ int fp8_gemv(float *y, const float *x, const uint8_t *W, const void *S, int sfmt
         return dsv4_fp8_mx_launch(a, st);
     }
     if (aligned && fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c)) {
-        /* Launch shape: R rows per thread per step, next step prefetched,
-         * workgroups per CU. None of these changes the arithmetic of a row. */
-        /* Defaults from a sweep over the C1/C2 shapes on MI355X (R in 1,2,4;
-         * prefetch on/off; 1-8 workgroups per CU): two rows per thread,
-         * prefetch only where the matrix is short, two workgroups per CU
-         * (four when rows are narrow). The environment can override each. */
-        int R = env_int("DSV4_GPU_FP8_R", 2);
-        R = R >= 4 ? 4 : R >= 2 ? 2 : 1;
-        while (blk_r % R) R >>= 1;               /* a step stays in one row block */
-        const int pf = env_int("DSV4_GPU_FP8_PF", rows <= 4096 ? 1 : 0);
-        int wpc = env_int("DSV4_GPU_FP8_WPC", cols >= 4096 ? 2 : 4);
-        if (wpc <= 0) wpc = 2;
+        /* launch shape (fp8_valu): none of it changes a row's arithmetic */
+        const Fp8Valu v = fp8_valu(rows, cols, blk_r);
+        const int R = v.R, pf = v.pf, wpc = v.wpc;
         if (sfmt == 0) {
             if (pf) launch_gemv_r<0, 1>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, gp, st);
             else    launch_gemv_r<0, 0>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, gp, st);
@@ -798,6 +845,38 @@ int fp8_gemv(float *y, const float *x, const uint8_t *W, const void *S, int sfmt
     }
     HIP_OK(hipGetLastError(), "fp8 gemv launch");
     return 0;
+}
+
+/* The attention block's x projections in one launch: its listed FP8
+ * matrices (blockIdx.y < gp.n) run k_fp8_gemv's body, its listed BF16
+ * matrices the BF16 GEMV's (dsv4_bf16_rows.h); all read the same x. Each
+ * part keeps its own launch plan, so every row has the bits of its own
+ * GEMV; workgroups past a part's grid leave at once. */
+struct XProj {
+    const float *x = nullptr;
+    int cols = 0;
+    Fp8Groups gp;                                  /* FP8: list of gp.n */
+    int rows8 = 0, sc = 0, blk_r = 0, blk_c = 0, tc8 = 0, rpw8 = 0, grid8 = 0;
+    B16List ls;                                    /* BF16: list of ls.n */
+    int tc16 = 0, rpw16 = 0, grid16 = 0;
+};
+
+template <int NCH, int R, int SF, int PF, int BNCH, int BR>
+__global__ void __launch_bounds__(256)
+k_xproj(XProj a)
+{
+    extern __shared__ float part[];
+    const int bx = blockIdx.x, by = blockIdx.y;
+    if (by < a.gp.n) {
+        if (bx >= a.grid8) return;
+        /* (the list supplies each matrix's W, S, y and rows) */
+        fp8_rows<NCH, R, SF, PF, 0>(a.gp.yl[0], a.x, a.gp.Wl[0], a.gp.Sl[0], a.rows8, a.cols,
+                                    a.sc, a.blk_r, a.blk_c, a.tc8, a.rpw8, a.gp, bx, by, part);
+    } else {
+        if (bx >= a.grid16) return;
+        b16_rows<BNCH, BR>(a.ls.y[0], a.x, a.ls.W[0], a.ls.rows[0], a.cols, a.tc16, a.rpw16,
+                           a.ls, bx, by - a.gp.n, part);
+    }
 }
 
 } // namespace
@@ -891,5 +970,70 @@ int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,
                                y, x, W, S, rows, cols, sc, blk_r, blk_c, nt);
     }
     HIP_OK(hipGetLastError(), "fp8 gemv_n launch");
+    return 0;
+}
+
+int dsv4_xproj_launch(const float *x, int cols, int sfmt, int blk_r, int blk_c, int nf,
+                      const uint8_t *const *Wf, const void *const *Sf, float *const *yf,
+                      const int *rf, int nb, const uint16_t *const *Wb, float *const *yb,
+                      const int *rb, hipStream_t st)
+{
+    auto two = [&]() -> int {
+        if (nf > 0 &&
+            dsv4_fp8_gemv_list_launch(x, cols, sfmt, blk_r, blk_c, nf, Wf, Sf, yf, rf, st,
+                                      true) != 0)
+            return -1;
+        if (nb > 0 && dsv4_bf16_gemv_list_launch(x, cols, nb, Wb, yb, rb, st) != 0) return -1;
+        return 0;
+    };
+    if (nf < 1 || nb < 1 || nf > FP8_LIST_MAX || nb > B16_LIST_MAX ||
+        (sfmt != 0 && sfmt != 1) || env_int("DSV4_GPU_XPROJ", 1) == 0)
+        return two();
+    Fp8Geom g;
+    B16Geom gb;
+    bool ok = fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c) && b16_geom(cols, &gb) &&
+              (((uintptr_t)x) & 15) == 0;
+    int rmf = 0, rmb = 0;
+    for (int i = 0; i < nf; i++) {
+        ok = ok && rf[i] > 0 && (((uintptr_t)Wf[i]) & 15) == 0;
+        rmf = rf[i] > rmf ? rf[i] : rmf;
+    }
+    for (int i = 0; i < nb; i++) {
+        ok = ok && rb[i] > 0 && (((uintptr_t)Wb[i]) & 15) == 0;
+        rmb = rb[i] > rmb ? rb[i] : rmb;
+    }
+    if (!ok) return two();
+    const Fp8Valu v = fp8_valu(rmf, cols, blk_r);
+    const Fp8Plan pf = fp8_plan(g, v.R, rmf, cols, v.wpc, nf);
+    const B16Plan pb = b16_plan(gb, rmb, nb);
+    /* the one combination built: FP8 with 4 chunks per thread, 2 rows per
+     * step, prefetch, x in registers; BF16 with 8 chunks per thread, 1 row
+     * (hidden 4096 and 7168, the Flash and full shapes) */
+    if (g.nch < 4 || v.R != 2 || !v.pf || pf.xl || gb.nch <= 4 || pb.R != 1 || g.wg != 256 ||
+        gb.wg != 256)
+        return two();
+    XProj a;
+    a.x = x;
+    a.cols = cols;
+    a.gp.n = nf;
+    a.gp.list = 1;
+    a.gp.valu = true;
+    for (int i = 0; i < nf; i++) {
+        a.gp.Wl[i] = Wf[i]; a.gp.Sl[i] = Sf[i]; a.gp.yl[i] = yf[i]; a.gp.rl[i] = rf[i];
+    }
+    a.rows8 = rmf; a.sc = (cols + blk_c - 1) / blk_c; a.blk_r = blk_r; a.blk_c = blk_c;
+    a.tc8 = g.tc; a.rpw8 = pf.rows_per_wg; a.grid8 = pf.grid;
+    a.ls.n = nb;
+    for (int i = 0; i < nb; i++) {
+        a.ls.W[i] = Wb[i]; a.ls.y[i] = yb[i]; a.ls.rows[i] = rb[i];
+    }
+    a.tc16 = gb.tc; a.rpw16 = pb.rows_per_wg; a.grid16 = pb.grid;
+    const dim3 grid(pf.grid > pb.grid ? pf.grid : pb.grid, nf + nb);
+    const size_t lds = pf.lds > pb.lds ? pf.lds : pb.lds;
+    if (sfmt == 0)
+        hipLaunchKernelGGL((k_xproj<4, 2, 0, 1, 8, 1>), grid, dim3(256), lds, st, a);
+    else
+        hipLaunchKernelGGL((k_xproj<4, 2, 1, 1, 8, 1>), grid, dim3(256), lds, st, a);
+    HIP_OK(hipGetLastError(), "x projections launch");
     return 0;
 }

@@ -1469,6 +1469,45 @@ int x_gemvs(const XJob *jobs, int n, const float *d_x, hipStream_t st, bool valu
     return 0;
 }
 
+/* The x projections of a block step: its FP8 matrices and its BF16 ones
+ * read the same x, so they share one launch when every FP8 one has the
+ * same scale format and blocking and all have the same width (the VALU
+ * form for the FP8 ones); otherwise listed launches as x_gemvs makes. */
+int x_proj(const XJob *jobs, int n, const float *d_x, hipStream_t st)
+{
+    const uint8_t *Wf[4];
+    const void *Sf[4];
+    float *Yf[4], *Yb[4];
+    const uint16_t *Wb[4];
+    int Rf[4], Rb[4], nf = 0, nb = 0;
+    const Res *f0 = nullptr;
+    bool ok = n > 0;
+    for (int i = 0; i < n && ok; i++) {
+        const Res &r = jobs[i].m->r;
+        ok = r.cols == jobs[0].m->r.cols;
+        if (r.wdt == DSV4_WFP8) {
+            if (!f0) f0 = &r;
+            ok = ok && nf < 4 && r.sfmt == f0->sfmt && r.blk_r == f0->blk_r &&
+                 r.blk_c == f0->blk_c;
+            if (ok) {
+                Wf[nf] = jobs[i].m->w; Sf[nf] = jobs[i].m->s;
+                Yf[nf] = jobs[i].y; Rf[nf] = jobs[i].rows; nf++;
+            }
+        } else if (r.wdt == DSV4_WBF16) {
+            ok = ok && nb < 4;
+            if (ok) {
+                Wb[nb] = (const uint16_t *)jobs[i].m->w;
+                Yb[nb] = jobs[i].y; Rb[nb] = jobs[i].rows; nb++;
+            }
+        } else {
+            ok = false;
+        }
+    }
+    if (!ok || nf == 0 || nb == 0) return x_gemvs(jobs, n, d_x, st, true);
+    return dsv4_xproj_launch(d_x, jobs[0].m->r.cols, f0->sfmt, f0->blk_r, f0->blk_c, nf, Wf, Sf,
+                             Yf, Rf, nb, Wb, Yb, Rb, st);
+}
+
 /* attention() of dsv4_layer.c:213-336 for the token at pos, on stream st;
  * x and out are device buffers of hidden floats. */
 int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_t st)
@@ -1504,7 +1543,7 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
         xj[nx++] = XJob{&b.cwgate, b.csc, b.width};
     }
     if (use_idx) xj[nx++] = XJob{&b.iwproj, b.idx_w, c.idx_heads};
-    OK(x_gemvs(xj, nx, d_x, st, VALU));
+    OK(x_proj(xj, nx, d_x, st));
     /* One launch for what needs only the projections: q's learned norm (in
      * place), kv_norm + RoPE into the ring slot, and the compressor's token
      * into its slot (dsv4_layer.c:222, 235-238, and the slot write of the

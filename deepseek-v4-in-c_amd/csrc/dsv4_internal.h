@@ -89,6 +89,15 @@ int dsv4_fp8_gemv_list_launch(const float *x, int cols, int sfmt, int blk_r, int
                               float *const *y, const int *rows, hipStream_t st,
                               bool valu = false);
 
+/* Up to four FP8 matrices (one scale format and blocking, the VALU form)
+ * and up to four BF16 matrices, all of width cols and reading the same x,
+ * in one launch where the shapes take it (else a listed launch of each);
+ * every row has the bits of its own GEMV. */
+int dsv4_xproj_launch(const float *x, int cols, int sfmt, int blk_r, int blk_c, int nf,
+                      const uint8_t *const *Wf, const void *const *Sf, float *const *yf,
+                      const int *rf, int nb, const uint16_t *const *Wb, float *const *yb,
+                      const int *rb, hipStream_t st);
+
 /* The same for up to four BF16 matrices of one width. */
 int dsv4_bf16_gemv_list_launch(const float *x, int cols, int n, const uint16_t *const *W,
                                float *const *y, const int *rows, hipStream_t st);

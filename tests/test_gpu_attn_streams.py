@@ -117,3 +117,26 @@ def test_attention_step_on_default_and_created_streams(gpu, dsv4):
         assert bad.size == 0, "%s stream: positions %s differ from the host entry point" % (
             name, bad[:8].tolist())
     assert L.dsv4_gpu_attn_reset(LAYER) == 0
+
+
+@pytest.mark.parametrize("ratio", [4, 128])
+def test_x_projections_in_one_launch_keep_bits(gpu, dsv4, monkeypatch, ratio):
+    """The block's x projections -- FP8 wq_a and wkv, BF16 compressor wkv and
+    wgate and (ratio 4) the indexer's weights_proj -- run in one launch: each
+    row has the bits of its own listed GEMV launch (DSV4_GPU_XPROJ=0: an FP8
+    and a BF16 listed launch), so every step's output is bit-identical."""
+    L, D = gpu, dsv4
+    rng = np.random.default_rng(11 + ratio)
+    layer = LAYER + 500 + ratio
+    hidden = _bind(D, L, rng, _KEEP, layer=layer, ratio=ratio)
+    X = (rng.standard_normal((N_POS, hidden)) * 0.5).astype(np.float32)
+    print("attn x projections: ratio %d, one launch" % ratio, flush=True)
+    one = _host_steps(L, layer, X)
+    assert np.isfinite(one).all() and np.abs(one).max() > 0.0
+    assert L.dsv4_gpu_attn_reset(layer) == 0
+    monkeypatch.setenv("DSV4_GPU_XPROJ", "0")
+    print("attn x projections: ratio %d, two launches" % ratio, flush=True)
+    two = _host_steps(L, layer, X)
+    assert L.dsv4_gpu_attn_reset(layer) == 0
+    bad = np.nonzero((one.view(np.uint32) != two.view(np.uint32)).any(axis=1))[0]
+    assert bad.size == 0, "positions %s differ between one and two launches" % bad[:8].tolist()

@@ -42,6 +42,7 @@
 namespace {
 
 #include "dsv4_bf16_rows.h"
+#include "dsv4_prep_rows.h"
 
 struct Fp8Geom {
     int ch;   /* 16-byte chunks per row                       */
@@ -171,12 +172,14 @@ __device__ __forceinline__ void load_step(u32x4 (*wv)[NCH], float *sv, const uin
 /* The GEMV of workgroup (bx, by): rows [bx rows_per_wg, +rows_per_wg) of
  * group or listed matrix by. part: LDS of [waves per row][rows_per_wg]
  * floats, then x (XL). */
-template <int NCH, int R, int SF, int PF, int XL>
+template <int NCH, int R, int SF, int PF, int XL, int NQ = 0>
 __device__ __forceinline__ void fp8_rows(float *__restrict__ y, const float *__restrict__ x,
                                          const uint8_t *__restrict__ W,
                                          const void *__restrict__ S, int rows, int cols, int sc,
                                          int blk_r, int blk_c, int tc, int rows_per_wg,
-                                         const Fp8Groups &gp, int bx, int by, float *part)
+                                         const Fp8Groups &gp, int bx, int by, float *part,
+                                         const float *__restrict__ nq_w = nullptr,
+                                         float nq_eps = 0.0f)
 {
     if (gp.list) {
         const int gi = by;
@@ -241,6 +244,24 @@ __device__ __forceinline__ void fp8_rows(float *__restrict__ y, const float *__r
             if (i < nq) *reinterpret_cast<f32x4 *>(xs + 4 * i) = xv[q];
         }
         __syncthreads();
+        if (NQ) {
+            /* x = w (x inv), the block's weighted RMSNorm (norm_rope_vec,
+             * no RoPE) on the workgroup's copy, with its sum of squares in
+             * its order: per thread the elements tid, tid + NR_THREADS, ...
+             * in order, then block_sum_d (blockDim.x == NR_THREADS) */
+            double sq = 0.0;
+            for (int i = tid; i < cols; i += NR_THREADS) {
+                const double v = (double)xs[i];
+                sq += v * v;
+            }
+            sq = block_sum_d(sq);
+            const float inv = (float)(1.0 / sqrt(sq / (double)cols + (double)nq_eps));
+            for (int i = tid; i < cols; i += NR_THREADS) {
+                const float v = xs[i] * inv;
+                xs[i] = nq_w[i] * v;
+            }
+            __syncthreads();
+        }
 #pragma unroll
         for (int n = 0; n < NCH; n++) {
             const int c = min(j + n * tc, ch - 1);
@@ -879,6 +900,39 @@ k_xproj(XProj a)
     }
 }
 
+/* The attention block's q GEMVs and the rest of its prep step in one
+ * launch: its listed FP8 matrices (blockIdx.y < gp.n; wq_b and the indexer's
+ * wq_b) read qr and normalise their workgroup's copy of it themselves (the
+ * prep step's q job, same arithmetic and order: NQ), and the workgroups of
+ * row gp.n run the prep step's other jobs (the ring slot's norm and RoPE,
+ * the compressor's slot), which nothing in this launch reads. */
+struct QProj {
+    const float *x = nullptr, *nw = nullptr;
+    int cols = 0;
+    float eps = 0.0f;
+    Fp8Groups gp;
+    int rows8 = 0, sc = 0, blk_r = 0, blk_c = 0, tc8 = 0, rpw8 = 0, grid8 = 0;
+    Dsv4Prep prep{};
+    int nprep = 0;
+};
+
+template <int NCH, int R, int SF>
+__global__ void __launch_bounds__(256)
+k_qproj(QProj a)
+{
+    extern __shared__ float part[];
+    const int bx = blockIdx.x, by = blockIdx.y;
+    if (by < a.gp.n) {
+        if (bx >= a.grid8) return;
+        fp8_rows<NCH, R, SF, 0, 1, 1>(a.gp.yl[0], a.x, a.gp.Wl[0], a.gp.Sl[0], a.rows8, a.cols,
+                                      a.sc, a.blk_r, a.blk_c, a.tc8, a.rpw8, a.gp, bx, by, part,
+                                      a.nw, a.eps);
+    } else {
+        if (bx >= a.nprep) return;
+        prep_rows(a.prep, bx);
+    }
+}
+
 } // namespace
 
 int dsv4_fp8_gemv_launch(float *y, const float *x, const uint8_t *W,
@@ -1035,5 +1089,73 @@ int dsv4_xproj_launch(const float *x, int cols, int sfmt, int blk_r, int blk_c, 
     else
         hipLaunchKernelGGL((k_xproj<4, 2, 1, 1, 8, 1>), grid, dim3(256), lds, st, a);
     HIP_OK(hipGetLastError(), "x projections launch");
+    return 0;
+}
+
+int dsv4_qproj_launch(const float *qr, int cols, const float *nw, float eps, int sfmt,
+                      int blk_r, int blk_c, int nf, const uint8_t *const *Wf,
+                      const void *const *Sf, float *const *yf, const int *rf,
+                      const Dsv4Prep *prep, hipStream_t st)
+{
+    if (!prep || prep->nj > 1 || nf < 1 || nf > FP8_LIST_MAX) {
+        DSV4_ERR("q projections: bad arguments (%d matrices)", nf);
+        return -1;
+    }
+    /* the separate form: the prep step with the q job first, then the list */
+    auto two = [&]() -> int {
+        Dsv4Prep p = *prep;
+        if (p.nj == 1) p.job[1] = p.job[0];
+        p.job[0] = Dsv4NormJob{const_cast<float *>(qr), qr, nw, cols, 0};
+        p.nj = prep->nj + 1;
+        if (dsv4_block_prep_launch(&p, st) != 0) return -1;
+        return dsv4_fp8_gemv_list_launch(qr, cols, sfmt, blk_r, blk_c, nf, Wf, Sf, yf, rf, st,
+                                         true);
+    };
+    Fp8Geom g;
+    bool ok = env_int("DSV4_GPU_QPROJ", 1) != 0 && (sfmt == 0 || sfmt == 1) && nw &&
+              fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c) && (((uintptr_t)qr) & 15) == 0;
+    int rm = 0;
+    for (int i = 0; i < nf; i++) {
+        ok = ok && rf[i] > 0 && (((uintptr_t)Wf[i]) & 15) == 0;
+        rm = rf[i] > rm ? rf[i] : rm;
+    }
+    if (!ok) return two();
+    const Fp8Valu v = fp8_valu(rm, cols, blk_r);
+    const Fp8Plan pf = fp8_plan(g, v.R, rm, cols, v.wpc, nf);
+    /* the combinations built: x through LDS (cols <= 2048), 1 or 2 chunks
+     * per thread, 2 rows per step, no prefetch (wq_b's rows), 256 threads */
+    if (!pf.xl || g.wg != 256 || g.nch > 2 || v.R != 2 || v.pf) return two();
+    QProj a;
+    a.x = qr; a.nw = nw; a.cols = cols; a.eps = eps;
+    a.gp.n = nf; a.gp.list = 1; a.gp.valu = true;
+    for (int i = 0; i < nf; i++) {
+        a.gp.Wl[i] = Wf[i]; a.gp.Sl[i] = Sf[i]; a.gp.yl[i] = yf[i]; a.gp.rl[i] = rf[i];
+    }
+    a.rows8 = rm; a.sc = (cols + blk_c - 1) / blk_c; a.blk_r = blk_r; a.blk_c = blk_c;
+    a.tc8 = g.tc; a.rpw8 = pf.rows_per_wg; a.grid8 = pf.grid;
+    a.prep = *prep;
+    a.nprep = prep_wgs(*prep);
+    const dim3 grid(pf.grid > a.nprep ? pf.grid : a.nprep, nf + (a.nprep ? 1 : 0));
+    static bool opted = false;
+    if (!opted) {
+        (void)hipFuncSetAttribute((const void *)k_qproj<1, 2, 0>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)dsv4_lds_limit());
+        (void)hipFuncSetAttribute((const void *)k_qproj<2, 2, 0>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)dsv4_lds_limit());
+        (void)hipFuncSetAttribute((const void *)k_qproj<1, 2, 1>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)dsv4_lds_limit());
+        (void)hipFuncSetAttribute((const void *)k_qproj<2, 2, 1>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)dsv4_lds_limit());
+        (void)hipGetLastError();
+        opted = true;
+    }
+    if (sfmt == 0) {
+        if (g.nch == 1) hipLaunchKernelGGL((k_qproj<1, 2, 0>), grid, dim3(256), pf.lds, st, a);
+        else            hipLaunchKernelGGL((k_qproj<2, 2, 0>), grid, dim3(256), pf.lds, st, a);
+    } else {
+        if (g.nch == 1) hipLaunchKernelGGL((k_qproj<1, 2, 1>), grid, dim3(256), pf.lds, st, a);
+        else            hipLaunchKernelGGL((k_qproj<2, 2, 1>), grid, dim3(256), pf.lds, st, a);
+    }
+    HIP_OK(hipGetLastError(), "q projections launch");
     return 0;
 }

@@ -1544,14 +1544,18 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
     }
     if (use_idx) xj[nx++] = XJob{&b.iwproj, b.idx_w, c.idx_heads};
     OK(x_proj(xj, nx, d_x, st));
-    /* One launch for what needs only the projections: q's learned norm (in
-     * place), kv_norm + RoPE into the ring slot, and the compressor's token
-     * into its slot (dsv4_layer.c:222, 235-238, and the slot write of the
-     * compress step called at :250) */
+    /* What needs only the projections: q's learned norm, kv_norm + RoPE
+     * into the ring slot, and the compressor's token into its slot
+     * (dsv4_layer.c:222, 235-238, and the slot write of the compress step
+     * called at :250); then q: wq_b (each head's norm and RoPE happen inside
+     * the attention, on its copy), and the indexer's wq_b when the indexer
+     * runs. Both GEMVs read the normed qr, so they share one launch, whose
+     * workgroups norm their own copy of qr while the ring and compressor
+     * jobs run beside them (dsv4_qproj_launch); matrices of another form
+     * take the prep launch and then listed launches. */
     Dsv4Prep pp{};
-    pp.job[0] = Dsv4NormJob{b.qr, b.qr, b.q_norm, c.q_lora, 0};
-    pp.job[1] = Dsv4NormJob{b.kv_cache + (size_t)(pos % c.window) * hd, b.kv, b.kv_norm, hd, rd};
-    pp.nj = 2;
+    pp.job[0] = Dsv4NormJob{b.kv_cache + (size_t)(pos % c.window) * hd, b.kv, b.kv_norm, hd, rd};
+    pp.nj = 1;
     pp.eps = c.rms_eps;
     pp.cs = b.cs; pp.sn = b.sn; pp.pos = pos; pp.half = half;
     if (c.ratio > 0) {
@@ -1561,12 +1565,32 @@ int block_step(AttnBlock &b, float *d_out, const float *d_x, int pos, hipStream_
         pp.kv_in = b.ckv; pp.sc_in = b.csc; pp.apr = b.ape + (size_t)ph * b.width;
         pp.width = b.width;
     }
-    OK(dsv4_block_prep_launch(&pp, st));
-    /* q: wq_b (each head's norm and RoPE happen inside the attention, on its
-     * copy), and the indexer's wq_b when the indexer runs: both read qr, so
-     * they share one listed launch */
     XJob qj[2] = {{&b.wq_b, b.q, H * hd}, {&b.iwq_b, b.idx_q, c.idx_heads * c.idx_dim}};
-    OK(x_gemvs(qj, use_idx ? 2 : 1, b.qr, st, VALU));
+    const int nq = use_idx ? 2 : 1;
+    const Res &r0 = b.wq_b.r;
+    bool qfp8 = r0.wdt == DSV4_WFP8;
+    for (int i = 1; i < nq; i++) {
+        const Res &ri = qj[i].m->r;
+        qfp8 = qfp8 && ri.wdt == DSV4_WFP8 && ri.cols == r0.cols && ri.sfmt == r0.sfmt &&
+               ri.blk_r == r0.blk_r && ri.blk_c == r0.blk_c;
+    }
+    if (qfp8) {
+        const uint8_t *W[2];
+        const void *S[2];
+        float *Y[2];
+        int R[2];
+        for (int i = 0; i < nq; i++) {
+            W[i] = qj[i].m->w; S[i] = qj[i].m->s; Y[i] = qj[i].y; R[i] = qj[i].rows;
+        }
+        OK(dsv4_qproj_launch(b.qr, c.q_lora, b.q_norm, c.rms_eps, r0.sfmt, r0.blk_r, r0.blk_c,
+                             nq, W, S, Y, R, &pp, st));
+    } else {
+        pp.job[1] = pp.job[0];
+        pp.job[0] = Dsv4NormJob{b.qr, b.qr, b.q_norm, c.q_lora, 0};
+        pp.nj = 2;
+        OK(dsv4_block_prep_launch(&pp, st));
+        OK(x_gemvs(qj, nq, b.qr, st, VALU));
+    }
     const int n_win = pos + 1 < c.window ? pos + 1 : c.window;
     int take = 0, mode = 1;
     if (c.ratio > 0) {

@@ -277,6 +277,18 @@ struct Dsv4Prep {
 };
 int dsv4_block_prep_launch(const Dsv4Prep *a, hipStream_t st);
 
+/* The block's q GEMVs (up to four FP8 matrices of width cols reading qr,
+ * the VALU form) and its prep step in one launch where the shapes take it:
+ * each GEMV workgroup applies the q job -- qr's weighted RMSNorm (nw, eps),
+ * norm_rope_vec's arithmetic -- to its own copy of qr (qr is not written),
+ * and prep's at most one norm job and compressor slot run beside them.
+ * Otherwise the prep launch with the q job first, then the listed GEMV;
+ * the same bits either way. */
+int dsv4_qproj_launch(const float *qr, int cols, const float *nw, float eps, int sfmt,
+                      int blk_r, int blk_c, int nf, const uint8_t *const *Wf,
+                      const void *const *Sf, float *const *yf, const int *rf,
+                      const Dsv4Prep *prep, hipStream_t st);
+
 /* A closing window in one launch (hd <= 1024): the pool (with the ratio-4
  * slide), then the weighted RMSNorm of the pooled row and RoPE of its last rd
  * elements at table row pos, into out[hd]. */

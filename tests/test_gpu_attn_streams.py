@@ -140,3 +140,27 @@ def test_x_projections_in_one_launch_keep_bits(gpu, dsv4, monkeypatch, ratio):
     assert L.dsv4_gpu_attn_reset(layer) == 0
     bad = np.nonzero((one.view(np.uint32) != two.view(np.uint32)).any(axis=1))[0]
     assert bad.size == 0, "positions %s differ between one and two launches" % bad[:8].tolist()
+
+
+@pytest.mark.parametrize("ratio", [4, 128])
+def test_q_projections_with_prep_keep_bits(gpu, dsv4, monkeypatch, ratio):
+    """The block's q GEMVs (wq_b and, from position 19 on at ratio 4, the
+    indexer's wq_b) norm their workgroup's copy of qr themselves while the
+    prep step's ring and compressor jobs run in the same launch: every
+    step's output has the bits of the separate sequence (DSV4_GPU_QPROJ=0:
+    the prep launch, qr normed in place, then the listed q GEMVs)."""
+    L, D = gpu, dsv4
+    rng = np.random.default_rng(13 + ratio)
+    layer = LAYER + 600 + ratio
+    hidden = _bind(D, L, rng, _KEEP, layer=layer, ratio=ratio)
+    X = (rng.standard_normal((N_POS, hidden)) * 0.5).astype(np.float32)
+    print("attn q projections: ratio %d, one launch" % ratio, flush=True)
+    one = _host_steps(L, layer, X)
+    assert np.isfinite(one).all() and np.abs(one).max() > 0.0
+    assert L.dsv4_gpu_attn_reset(layer) == 0
+    monkeypatch.setenv("DSV4_GPU_QPROJ", "0")
+    print("attn q projections: ratio %d, prep then the GEMVs" % ratio, flush=True)
+    two = _host_steps(L, layer, X)
+    assert L.dsv4_gpu_attn_reset(layer) == 0
+    bad = np.nonzero((one.view(np.uint32) != two.view(np.uint32)).any(axis=1))[0]
+    assert bad.size == 0, "positions %s differ between one launch and two" % bad[:8].tolist()

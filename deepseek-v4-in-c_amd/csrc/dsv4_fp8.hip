@@ -171,7 +171,7 @@ __device__ __forceinline__ void load_step(u32x4 (*wv)[NCH], float *sv, const uin
  * summed in wave order after a single barrier at the end. */
 /* The GEMV of workgroup (bx, by): rows [bx rows_per_wg, +rows_per_wg) of
  * group or listed matrix by. part: LDS of [waves per row][rows_per_wg]
- * floats, then x (XL). */
+ * floats, then x (XL), then the norm's weights (NQ). */
 template <int NCH, int R, int SF, int PF, int XL, int NQ = 0>
 __device__ __forceinline__ void fp8_rows(float *__restrict__ y, const float *__restrict__ x,
                                          const uint8_t *__restrict__ W,
@@ -228,11 +228,17 @@ __device__ __forceinline__ void fp8_rows(float *__restrict__ y, const float *__r
          * would fetch the same x from L2. */
         float *xs = part + (size_t)(tc > 64 ? tc / 64 : 0) * rows_per_wg;
         constexpr int XR = 4 * NCH;                    /* rounds: cols <= 1024 XR */
-        f32x4 xv[XR];
+        f32x4 xv[XR], nv[NQ ? XR : 1];
         const int nq = cols >> 2;
+        /* (NQ: the norm's weights with x, ahead of the weights' requests, and
+         * into LDS beside x) */
+        float *xw = xs + cols;
 #pragma unroll
-        for (int q = 0; q < XR; q++)
-            xv[q] = ldf4(x + 4 * min(q * (int)blockDim.x + tid, nq - 1));
+        for (int q = 0; q < XR; q++) {
+            const int i = 4 * min(q * (int)blockDim.x + tid, nq - 1);
+            xv[q] = ldf4(x + i);
+            if (NQ) nv[q] = ldf4(nq_w + i);
+        }
         __builtin_amdgcn_sched_barrier(0);
         if (nsteps > 0)
             load_step<NCH, R, SF>(wv, sv, W, S, row0 + g * R, rend, cols, ch, j, tc, cb, sc,
@@ -241,7 +247,10 @@ __device__ __forceinline__ void fp8_rows(float *__restrict__ y, const float *__r
 #pragma unroll
         for (int q = 0; q < XR; q++) {
             const int i = q * (int)blockDim.x + tid;
-            if (i < nq) *reinterpret_cast<f32x4 *>(xs + 4 * i) = xv[q];
+            if (i < nq) {
+                *reinterpret_cast<f32x4 *>(xs + 4 * i) = xv[q];
+                if (NQ) *reinterpret_cast<f32x4 *>(xw + 4 * i) = nv[q];
+            }
         }
         __syncthreads();
         if (NQ) {
@@ -258,7 +267,7 @@ __device__ __forceinline__ void fp8_rows(float *__restrict__ y, const float *__r
             const float inv = (float)(1.0 / sqrt(sq / (double)cols + (double)nq_eps));
             for (int i = tid; i < cols; i += NR_THREADS) {
                 const float v = xs[i] * inv;
-                xs[i] = nq_w[i] * v;
+                xs[i] = xw[i] * v;
             }
             __syncthreads();
         }
@@ -1137,6 +1146,7 @@ int dsv4_qproj_launch(const float *qr, int cols, const float *nw, float eps, int
     a.nprep = prep_wgs(*prep);
     const dim3 grid(pf.grid > a.nprep ? pf.grid : a.nprep, nf + (a.nprep ? 1 : 0));
     static bool opted = false;
+    const size_t lds = pf.lds + sizeof(float) * (size_t)cols;   /* + the norm's weights */
     if (!opted) {
         (void)hipFuncSetAttribute((const void *)k_qproj<1, 2, 0>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)dsv4_lds_limit());
@@ -1150,11 +1160,11 @@ int dsv4_qproj_launch(const float *qr, int cols, const float *nw, float eps, int
         opted = true;
     }
     if (sfmt == 0) {
-        if (g.nch == 1) hipLaunchKernelGGL((k_qproj<1, 2, 0>), grid, dim3(256), pf.lds, st, a);
-        else            hipLaunchKernelGGL((k_qproj<2, 2, 0>), grid, dim3(256), pf.lds, st, a);
+        if (g.nch == 1) hipLaunchKernelGGL((k_qproj<1, 2, 0>), grid, dim3(256), lds, st, a);
+        else            hipLaunchKernelGGL((k_qproj<2, 2, 0>), grid, dim3(256), lds, st, a);
     } else {
-        if (g.nch == 1) hipLaunchKernelGGL((k_qproj<1, 2, 1>), grid, dim3(256), pf.lds, st, a);
-        else            hipLaunchKernelGGL((k_qproj<2, 2, 1>), grid, dim3(256), pf.lds, st, a);
+        if (g.nch == 1) hipLaunchKernelGGL((k_qproj<1, 2, 1>), grid, dim3(256), lds, st, a);
+        else            hipLaunchKernelGGL((k_qproj<2, 2, 1>), grid, dim3(256), lds, st, a);
     }
     HIP_OK(hipGetLastError(), "q projections launch");
     return 0;

@@ -1467,7 +1467,57 @@ k_attn_partial(float *__restrict__ pm, float *__restrict__ pl,
      * together hold 16 different rows (the row pitch's 16-byte skew keeps
      * them on different banks) and the lanes of one head read q as a
      * broadcast. */
-    {
+    if (KVF == DSV4_GPU_KV_F32 && SR == 16 && vec && (d_qk & 15) == 0 &&
+        AT_HB * ldq >= 4 * 16 * 16) {
+        /* f32 rows in 16-row splits: the scores as one 16 x 16 tile on the
+         * matrix core (v_mfma_f32_16x16x4f32; rows x heads, heads past AT_HB
+         * zero), each wave over a quarter of d_qk: every q and row element
+         * is read from LDS once per wave instead of once per (head, row)
+         * pair. The quarters' tiles meet in LDS (in q's region, which the
+         * scores no longer need and which holds them), added in wave order. */
+        static_assert(AT_HB <= 16 && AT_THREADS == 256, "one 16 x 16 tile, four waves");
+        typedef float v4f_t __attribute__((ext_vector_type(4)));
+        const int r16 = lane & 15, kq = lane >> 4;
+        const float *krow = (const float *)(kvs + (size_t)r16 * rowb);
+        const float *qrow = qs + (size_t)min(r16, AT_HB - 1) * ldq;
+        const bool hv = r16 < AT_HB;
+        const int kw = d_qk >> 2, kb = wid * kw;      /* a multiple of 4 */
+        /* four independent chains over the quarter's steps (step s feeds
+         * chain s % 4), each batch's LDS reads issued before its products */
+        v4f_t acc[4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f},
+                        {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+        int k0 = kb;
+        for (; k0 + 16 <= kb + kw; k0 += 16) {
+            float a[4], b[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                a[u] = krow[k0 + 4 * u + kq];
+                b[u] = hv ? qrow[k0 + 4 * u + kq] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc[u], 0, 0, 0);
+        }
+        for (int u = 0; k0 < kb + kw; k0 += 4, u++) {
+            const float a = krow[k0 + kq];
+            const float b = hv ? qrow[k0 + kq] : 0.0f;
+            if (u == 0) acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[0], 0, 0, 0);
+            else if (u == 1) acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[1], 0, 0, 0);
+            else acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[2], 0, 0, 0);
+        }
+        acc[0] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        __syncthreads();                       /* every wave is done with qs */
+        float *red = qs;                       /* [4 waves][16 rows][16 heads] */
+#pragma unroll
+        for (int r = 0; r < 4; r++) red[(wid * 16 + 4 * kq + r) * 16 + r16] = acc[0][r];
+        __syncthreads();
+        if (tid < AT_HB * SR) {
+            const int jj = tid / AT_HB, hh = tid - jj * AT_HB;
+            const float v = ((red[jj * 16 + hh] + red[(16 + jj) * 16 + hh]) +
+                             red[(32 + jj) * 16 + hh]) + red[(48 + jj) * 16 + hh];
+            ps[jj * AT_HB + hh] = sidx[jj] >= 0 ? v * scale : -INFINITY;
+        }
+    } else {
         const int pairs = AT_HB * SR;
         const int LPP = pairs >= AT_THREADS ? 1 : (pairs * 2 >= AT_THREADS ? 2 : 4);
         const int span = 64 / LPP;                         /* pairs per wave per pass */

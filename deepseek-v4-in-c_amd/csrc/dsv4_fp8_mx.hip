@@ -817,9 +817,13 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
     const uint32_t bc_m = bc_magic(blk_c);
     /* tokens per workgroup: at most 4 column tiles of 5 (the accumulators and
      * running sums of 4 tiles stay in registers); more tokens take more
-     * workgroups along y, each reading the weights again */
+     * workgroups along y, each reading the weights again. Up to 4 tiles of
+     * tokens one tile per workgroup, up to 8 two, then four: a workgroup's
+     * per-unit work grows with its tiles, and the extra token groups read the
+     * weights from L2 (7168 x 7168, us, against four tiles: 8 tokens 26.7 /
+     * 33.2, 16 tokens 33.5 / 50.4, 32 tokens 45.5 / 54.0; 64 tokens keep 4) */
     const int ntile = (nt + XTOK - 1) / XTOK;
-    int ntmax = mx_env("DSV4_GPU_MXN_NT", 4);
+    int ntmax = mx_env("DSV4_GPU_MXN_NT", ntile <= 4 ? 1 : ntile <= 8 ? 2 : 4);
     ntmax = ntmax < 1 ? 1 : ntmax > 7 ? 7 : ntmax;
     const int ngrp = (ntile + ntmax - 1) / ntmax;      /* fewest weight passes */
     const int NTc = (ntile + ngrp - 1) / ngrp;         /* then the fewest tiles each */

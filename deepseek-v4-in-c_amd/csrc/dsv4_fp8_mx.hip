@@ -30,7 +30,9 @@
  * The single-token kernel spreads a 16-row tile's segments over up to 8
  * waves (so short matrices still fill the machine); the first of them keeps
  * the running sum in registers and continues it over the others' partials
- * from LDS. The batched kernel walks the segments in order inside one wave.
+ * from LDS. The batched kernel walks the segments in order inside one wave;
+ * for one or two groups of at most five tokens its k_fp8_mxk form splits them
+ * over 2 or 4 waves the same way.
  * Matrix-core columns are computed independently, so where a token sits
  * among the columns does not change its bits; the tests check every case
  * bit for bit.
@@ -661,6 +663,147 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
     }
 }
 
+/* The batched kernel for one column tile (at most five tokens) with each
+ * tile's segments split over KP waves, as the single-token kernel splits
+ * them: a workgroup of 4 waves holds 4 / KP tiles, and wave p of a tile takes
+ * units [p up, (p + 1) up), up = spw segments of 4 units. Step i: the
+ * workgroup copies the pre-split x terms of unit p up + i of every part p
+ * into B buffer i % 2 (part p's rows after part p - 1's), each wave stages
+ * its weight unit and requests the next x step and its weight unit i + 2,
+ * and after one barrier runs its unit's 8 steps. Part 0 chains its segments
+ * in registers; the other parts leave each segment's accumulator in LDS, and
+ * part 0 continues its chain over them in segment order after a barrier: the
+ * chain of k_fp8_mxn, so the same bits. */
+template <int KP>
+struct XkDim {
+    static constexpr int M = (KP * XTOK * XNT * (XU / 8) + 255) / 256;
+};
+
+template <bool UNI, int KP>
+__global__ void __launch_bounds__(256)
+k_fp8_mxk(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *__restrict__ S,
+          int rows, int cols, int sc, int blk_r, uint32_t bc_m, int nt, int tpg,
+          const uint16_t *__restrict__ xt, int cpad, int spw)
+{
+    constexpr int MW = 4, TT = MW / KP, XM = XkDim<KP>::M;
+    extern __shared__ __attribute__((aligned(16))) unsigned char xklds[];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int p = w % KP, tl = w / KP;
+    const int prows = tpg * XNT;                            /* B rows per part */
+    const size_t bl_n = (size_t)KP * prows * BP;            /* bf16 per B buffer */
+    uint16_t *const bl0 = (uint16_t *)xklds, *const bl1 = bl0 + bl_n;
+    unsigned char *buf = xklds + 4 * bl_n + (size_t)w * XUNIT_B;
+    const int nu = (cols + XU - 1) / XU, nseg = (nu + XSEG_U - 1) / XSEG_U;
+    const int up = spw * XSEG_U, ub = p * up;
+    v4f *part = (v4f *)(xklds + 4 * bl_n + (size_t)MW * XUNIT_B) +
+                (size_t)tl * (nseg - spw) * 64;             /* [nseg - spw][64] */
+    const int row0 = (blockIdx.x * TT + tl) * 16;
+    const int t0 = blockIdx.y * tpg;
+    const int ntok = min(tpg, nt - t0);
+    const int g = lane >> 4, col = lane & 15;
+    const bool live = row0 < rows;
+    const int wrow0 = live ? row0 : 0;
+    const int srow = ((UNI ? wrow0 : min(wrow0 + col, rows - 1)) / blk_r) * sc;
+    const int boff = (col < XNT * XTOK && col / XNT < ntok)
+                         ? (p * prows + col) * BP : p * prows * BP;
+    /* this thread's x pieces: piece i = tid + 256 m is part i / 32 / prows,
+     * B row (i / 32) % prows, 16-byte piece i % 32; step-independent except
+     * for the unit. Rows of tokens past the group load the group's first
+     * row and store zeros. */
+    int xo[XM], xu0[XM], xs[XM];
+    bool xin[XM];
+#pragma unroll
+    for (int m = 0; m < XM; m++) {
+        const int i = (int)threadIdx.x + 256 * m;
+        const int prow = i / (XU / 8), pc = i % (XU / 8);
+        const int pp = prow / prows, r = prow - pp * prows;
+        xs[m] = prow < KP * prows ? prow * BP + 8 * pc : -1;
+        xin[m] = prow < KP * prows && r / XNT < ntok;
+        xo[m] = xin[m] ? (t0 * XNT + r) * cpad + 8 * pc : t0 * XNT * cpad;
+        xu0[m] = xin[m] ? pp * up : 0;
+    }
+    u32x4 XR[XM];
+    auto xload = [&](int i) {
+#pragma unroll
+        for (int m = 0; m < XM; m++)
+            XR[m] = *(const DSV4_GLOBAL u32x4 *)(xt + xo[m] + XU * min(xu0[m] + i, nu - 1));
+    };
+    auto xstore = [&](uint16_t *bl) {
+#pragma unroll
+        for (int m = 0; m < XM; m++)
+            if (xs[m] >= 0)
+                *reinterpret_cast<u32x4 *>(bl + xs[m]) = xin[m] ? XR[m] : u32x4{0u, 0u, 0u, 0u};
+    };
+    v4f acc = {0.f, 0.f, 0.f, 0.f}, tot = {0.f, 0.f, 0.f, 0.f};
+    XUnit<UNI> P[2];
+    xload(0);
+    uint32_t ssb = UNI ? xs_seg(S, srow, bc_m, XU * min(ub, nu - 1), cols, lane) : 0u, ssn = 0u;
+    __builtin_amdgcn_sched_barrier(0);
+    xu_load<UNI, false>(P[0], W, S, srow, bc_m, wrow0, rows, cols, XU * min(ub, nu - 1), lane);
+    xu_load<UNI, false>(P[1], W, S, srow, bc_m, wrow0, rows, cols, XU * min(ub + 1, nu - 1), lane);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int s0 = 0; s0 < up; s0 += XSEG_U) {
+#pragma unroll
+        for (int j = 0; j < XSEG_U; j++) {
+            const int i = s0 + j, u = ub + i;
+            uint16_t *bl = (j & 1) ? bl1 : bl0;
+            xstore(bl);
+            xu_stage(buf, P[j & 1], lane);
+            uint32_t sb[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) sb[q] = UNI ? 0u : P[j & 1].sb[UNI ? 0 : q];
+            __builtin_amdgcn_sched_barrier(0);
+            xload(min(i + 1, up - 1));
+            if (UNI && j == XSEG_U - 2)        /* before the next segment's first unit */
+                ssn = xs_seg(S, srow, bc_m, XU * (min(ub + s0 + XSEG_U, nu - 1) & ~(XSEG_U - 1)),
+                             cols, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            xu_load<UNI, false>(P[j & 1], W, S, srow, bc_m, wrow0, rows, cols,
+                                XU * min(u + 2, nu - 1), lane);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();              /* B(i) whole; every wave is past B(i - 2)'s reads */
+            if (u < nu) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int k = XU * u + 64 * q + 16 * g;
+                    v8bf af[2];
+                    xu_frags(af, buf, q, UNI ? xs_get(ssb, 4 * j + q) : sb[q], k < cols, lane);
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const u32x4 bw = *reinterpret_cast<const u32x4 *>(
+                            bl + boff + 64 * q + 16 * g + 8 * h);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            af[h], __builtin_bit_cast(v8bf, bw), acc, 0, 0, 0);
+                    }
+                }
+            }
+        }
+        /* a segment ends: part 0 chains it, the others leave it in LDS */
+        const int sg = p * spw + s0 / XSEG_U;
+        if (p == 0)
+            tot = s0 == 0 ? acc : tot + acc;
+        else if (sg < nseg)
+            part[(size_t)(sg - spw) * 64 + lane] = acc;
+        acc = v4f{0.f, 0.f, 0.f, 0.f};
+        ssb = ssn;
+    }
+    __syncthreads();                      /* every part's segments in LDS */
+    if (p != 0 || !live) return;
+    for (int s = spw; s < nseg; s++) tot = tot + part[(size_t)(s - spw) * 64 + lane];
+    /* y = (hi + mid) + lo per (row, token), as k_fp8_mxn */
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float c0 = tot[j];
+        const float c1 = __shfl(tot[j], min(lane + 1, 63), 64);
+        const float c2 = __shfl(tot[j], min(lane + 2, 63), 64);
+        const int tk = col / XNT;
+        const int rr = row0 + 4 * g + j;
+        if (col % XNT == 0 && col < XNT * XTOK && tk < ntok && rr < rows)
+            y[(size_t)(t0 + tk) * rows + rr] = (c0 + c1) + c2;
+    }
+}
+
 /* Every row of a 16-row tile and every lane of a quarter share the quarter's
  * scale: tiles start at multiples of 16 and quarters at multiples of 64. */
 bool xs_uniform(int blk_r, int blk_c)
@@ -854,6 +997,41 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
         hipLaunchKernelGGL(k_fp8_xsplit, dim3((n4 + 255) / 256), dim3(256), 0, st,
                            (uint16_t *)xscratch, x, nt, cols, cpad);
         HIP_OK(hipGetLastError(), "fp8 mxn x split launch");
+    }
+    /* one column tile per group, one or two groups: the segments of a tile
+     * split over KP waves, 4 when two workgroups still fit a CU, else 2
+     * (7168 x 7168, us, against one wave per tile: 2 tokens 17.2 / 25.3, 4
+     * tokens 18.2 / 25.8, 8 tokens (two groups, KP 2) 24.1 / 26.7; with more
+     * groups the one-wave form is faster: 16 tokens 33.5 against 42.6 at KP 2).
+     * DSV4_GPU_MXK = 0 keeps one wave per tile, 2 or 4 forces KP. */
+    const int nseg = (cpad / XU + XSEG_U - 1) / XSEG_U;
+    auto mxk_lds = [&](int k) {
+        const int spw = (nseg + k - 1) / k;
+        return 4 * (size_t)k * tpg * XNT * BP + 4 * (size_t)XUNIT_B +
+               (size_t)(4 / k) * (nseg - spw) * 64 * sizeof(float) * 4;
+    };
+    int kp = mx_env("DSV4_GPU_MXK", -1);
+    if (kp < 0)
+        kp = groups > 2 ? 0 : groups == 2 ? 2 : mxk_lds(4) <= dsv4_lds_limit() / 2 ? 4 : 2;
+    if (xt && NTc == 1 && (kp == 2 || kp == 4) && nseg >= kp) {
+        const int spw = (nseg + kp - 1) / kp, tt = 4 / kp;
+        const size_t lds_k = mxk_lds(kp);
+        if (lds_k <= dsv4_lds_limit()) {
+            static bool opted_k = false;
+            if (!opted_k) {
+                optin(k_fp8_mxk<false, 2>); optin(k_fp8_mxk<true, 2>);
+                optin(k_fp8_mxk<false, 4>); optin(k_fp8_mxk<true, 4>);
+                opted_k = true;
+            }
+            const dim3 gk(((rows + 15) / 16 + tt - 1) / tt, groups);
+#define XK(U, K) hipLaunchKernelGGL((k_fp8_mxk<U, K>), gk, dim3(256), lds_k, st, y, W, S, rows, \
+                                    cols, sc, blk_r, bc_m, nt, tpg, xt, cpad, spw)
+            if (kp == 2) { if (uni) XK(true, 2); else XK(false, 2); }
+            else { if (uni) XK(true, 4); else XK(false, 4); }
+#undef XK
+            HIP_OK(hipGetLastError(), "fp8 mxk launch");
+            return 0;
+        }
     }
 #define XN(NTV, MWV) do {                                                                      \
         if (uni)                                                                               \

@@ -674,18 +674,24 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
  * in registers; the other parts leave each segment's accumulator in LDS, and
  * part 0 continues its chain over them in segment order after a barrier: the
  * chain of k_fp8_mxn, so the same bits. */
-template <int KP>
+template <int KP, bool XF>
 struct XkDim {
-    static constexpr int M = (KP * XTOK * XNT * (XU / 8) + 255) / 256;
+    /* 16-byte pieces per thread per step: term-plane pieces, or with XF f32
+     * pieces of the token rows */
+    static constexpr int M = XF ? (KP * XTOK * (XU / 4) + 255) / 256
+                                : (KP * XTOK * XNT * (XU / 8) + 255) / 256;
 };
 
-template <bool UNI, int KP>
+/* XF: x comes as the f32 rows and each workgroup forms the terms of its
+ * steps itself (terms3, the bits of k_fp8_xsplit), so no split launch runs
+ * before it. */
+template <bool UNI, int KP, bool XF>
 __global__ void __launch_bounds__(256)
-k_fp8_mxk(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *__restrict__ S,
-          int rows, int cols, int sc, int blk_r, uint32_t bc_m, int nt, int tpg,
-          const uint16_t *__restrict__ xt, int cpad, int spw)
+k_fp8_mxk(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__restrict__ W,
+          const uint8_t *__restrict__ S, int rows, int cols, int sc, int blk_r, uint32_t bc_m,
+          int nt, int tpg, const uint16_t *__restrict__ xt, int cpad, int spw)
 {
-    constexpr int MW = 4, TT = MW / KP, XM = XkDim<KP>::M;
+    constexpr int MW = 4, TT = MW / KP, XM = XkDim<KP, XF>::M;
     extern __shared__ __attribute__((aligned(16))) unsigned char xklds[];
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -707,33 +713,70 @@ k_fp8_mxk(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
     const int srow = ((UNI ? wrow0 : min(wrow0 + col, rows - 1)) / blk_r) * sc;
     const int boff = (col < XNT * XTOK && col / XNT < ntok)
                          ? (p * prows + col) * BP : p * prows * BP;
-    /* this thread's x pieces: piece i = tid + 256 m is part i / 32 / prows,
-     * B row (i / 32) % prows, 16-byte piece i % 32; step-independent except
-     * for the unit. Rows of tokens past the group load the group's first
-     * row and store zeros. */
-    int xo[XM], xu0[XM], xs[XM];
-    bool xin[XM];
+    /* this thread's x pieces, step-independent except for the unit. Term
+     * planes: piece i = tid + 256 m is part i / 32 / prows, B row (i / 32) %
+     * prows, 16-byte piece i % 32. XF: part i / 64 / tpg, token (i / 64) %
+     * tpg, f32 columns 4 (i % 64) .. + 3 of the unit. Pieces of tokens past
+     * the group (and, XF, columns past cols) load the group's first row and
+     * store zeros. */
+    int xo[XM], xu0[XM], xs[XM], xc[XM];
+    bool xin[XM], xok[XM];
 #pragma unroll
     for (int m = 0; m < XM; m++) {
         const int i = (int)threadIdx.x + 256 * m;
-        const int prow = i / (XU / 8), pc = i % (XU / 8);
-        const int pp = prow / prows, r = prow - pp * prows;
-        xs[m] = prow < KP * prows ? prow * BP + 8 * pc : -1;
-        xin[m] = prow < KP * prows && r / XNT < ntok;
-        xo[m] = xin[m] ? (t0 * XNT + r) * cpad + 8 * pc : t0 * XNT * cpad;
-        xu0[m] = xin[m] ? pp * up : 0;
+        if (XF) {
+            const int pr = i / (XU / 4), c4 = i % (XU / 4);
+            const int pp = pr / tpg, tk = pr - pp * tpg;
+            xs[m] = pr < KP * tpg ? (pp * prows + tk * XNT) * BP + 4 * c4 : -1;
+            xin[m] = pr < KP * tpg && tk < ntok;
+            xo[m] = xin[m] ? (t0 + tk) * cols + 4 * c4 : t0 * cols;
+            xu0[m] = xin[m] ? pp * up : 0;
+            xc[m] = 4 * c4;
+        } else {
+            const int prow = i / (XU / 8), pc = i % (XU / 8);
+            const int pp = prow / prows, r = prow - pp * prows;
+            xs[m] = prow < KP * prows ? prow * BP + 8 * pc : -1;
+            xin[m] = prow < KP * prows && r / XNT < ntok;
+            xo[m] = xin[m] ? (t0 * XNT + r) * cpad + 8 * pc : t0 * XNT * cpad;
+            xu0[m] = xin[m] ? pp * up : 0;
+            xc[m] = 0;
+        }
+        xok[m] = xin[m];
     }
     u32x4 XR[XM];
     auto xload = [&](int i) {
 #pragma unroll
-        for (int m = 0; m < XM; m++)
-            XR[m] = *(const DSV4_GLOBAL u32x4 *)(xt + xo[m] + XU * min(xu0[m] + i, nu - 1));
+        for (int m = 0; m < XM; m++) {
+            const int cu = XU * min(xu0[m] + i, nu - 1);
+            if (XF) {
+                /* the unit's columns past cols: the group's first piece */
+                xok[m] = xin[m] && xc[m] + cu < cols;
+                XR[m] = __builtin_bit_cast(u32x4, *(const DSV4_GLOBAL f32x4 *)(
+                    x + (xok[m] ? xo[m] + cu : t0 * cols)));
+            } else {
+                XR[m] = *(const DSV4_GLOBAL u32x4 *)(xt + xo[m] + cu);
+            }
+        }
     };
     auto xstore = [&](uint16_t *bl) {
 #pragma unroll
-        for (int m = 0; m < XM; m++)
-            if (xs[m] >= 0)
+        for (int m = 0; m < XM; m++) {
+            if (xs[m] < 0) continue;
+            if (XF) {
+                const f32x4 v = __builtin_bit_cast(f32x4, XR[m]);
+                const float e[4] = {xok[m] ? v.x : 0.f, xok[m] ? v.y : 0.f, xok[m] ? v.z : 0.f,
+                                    xok[m] ? v.w : 0.f};
+                uint32_t tt[4][XNT];
+#pragma unroll
+                for (int j = 0; j < 4; j++) terms3(e[j], tt[j]);
+#pragma unroll
+                for (int p = 0; p < XNT; p++)
+                    *reinterpret_cast<uint2 *>(bl + xs[m] + p * BP) =
+                        uint2{tt[0][p] | (tt[1][p] << 16), tt[2][p] | (tt[3][p] << 16)};
+            } else {
                 *reinterpret_cast<u32x4 *>(bl + xs[m]) = xin[m] ? XR[m] : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
     };
     v4f acc = {0.f, 0.f, 0.f, 0.f}, tot = {0.f, 0.f, 0.f, 0.f};
     XUnit<UNI> P[2];
@@ -992,12 +1035,12 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
     const bool uni = xs_uniform(blk_r, blk_c);
     const int cpad = ((cols + XU - 1) / XU) * XU;
     const uint16_t *xt = (const uint16_t *)xscratch;
-    if (xt) {
+    auto xsplit = [&]() {
         const int n4 = nt * (cpad / 4);
         hipLaunchKernelGGL(k_fp8_xsplit, dim3((n4 + 255) / 256), dim3(256), 0, st,
                            (uint16_t *)xscratch, x, nt, cols, cpad);
-        HIP_OK(hipGetLastError(), "fp8 mxn x split launch");
-    }
+        return hipGetLastError();
+    };
     /* one column tile per group, one or two groups: the segments of a tile
      * split over KP waves, 4 when two workgroups still fit a CU, else 2
      * (7168 x 7168, us, against one wave per tile: 2 tokens 17.2 / 25.3, 4
@@ -1013,26 +1056,39 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
     int kp = mx_env("DSV4_GPU_MXK", -1);
     if (kp < 0)
         kp = groups > 2 ? 0 : groups == 2 ? 2 : mxk_lds(4) <= dsv4_lds_limit() / 2 ? 4 : 2;
-    if (xt && NTc == 1 && (kp == 2 || kp == 4) && nseg >= kp) {
+    /* x as f32 rows, each workgroup forming its terms, for one group of at
+     * most three tokens: no split launch (2 tokens 15.6 against 17.4 us);
+     * from 4 tokens the per-workgroup terms cost more than the launch (4
+     * tokens 18.7 / 18.2, 8 tokens 26.6 / 24.1). DSV4_GPU_MXKF = 0 / 1
+     * forces the pre-split planes / the f32 rows. */
+    const int xfe = mx_env("DSV4_GPU_MXKF", -1);
+    const bool xf = xfe < 0 ? (groups == 1 && tpg <= 3) : xfe != 0;
+    if ((xf || xt) && NTc == 1 && (kp == 2 || kp == 4) && nseg >= kp) {
         const int spw = (nseg + kp - 1) / kp, tt = 4 / kp;
         const size_t lds_k = mxk_lds(kp);
         if (lds_k <= dsv4_lds_limit()) {
             static bool opted_k = false;
             if (!opted_k) {
-                optin(k_fp8_mxk<false, 2>); optin(k_fp8_mxk<true, 2>);
-                optin(k_fp8_mxk<false, 4>); optin(k_fp8_mxk<true, 4>);
+                optin(k_fp8_mxk<false, 2, false>); optin(k_fp8_mxk<true, 2, false>);
+                optin(k_fp8_mxk<false, 4, false>); optin(k_fp8_mxk<true, 4, false>);
+                optin(k_fp8_mxk<false, 2, true>); optin(k_fp8_mxk<true, 2, true>);
+                optin(k_fp8_mxk<false, 4, true>); optin(k_fp8_mxk<true, 4, true>);
                 opted_k = true;
             }
+            if (!xf) HIP_OK(xsplit(), "fp8 mxn x split launch");
             const dim3 gk(((rows + 15) / 16 + tt - 1) / tt, groups);
-#define XK(U, K) hipLaunchKernelGGL((k_fp8_mxk<U, K>), gk, dim3(256), lds_k, st, y, W, S, rows, \
-                                    cols, sc, blk_r, bc_m, nt, tpg, xt, cpad, spw)
-            if (kp == 2) { if (uni) XK(true, 2); else XK(false, 2); }
-            else { if (uni) XK(true, 4); else XK(false, 4); }
+#define XK(U, K, F) hipLaunchKernelGGL((k_fp8_mxk<U, K, F>), gk, dim3(256), lds_k, st, y, x, W, \
+                                       S, rows, cols, sc, blk_r, bc_m, nt, tpg, xt, cpad, spw)
+#define XKF(U, K) do { if (xf) XK(U, K, true); else XK(U, K, false); } while (0)
+            if (kp == 2) { if (uni) XKF(true, 2); else XKF(false, 2); }
+            else { if (uni) XKF(true, 4); else XKF(false, 4); }
+#undef XKF
 #undef XK
             HIP_OK(hipGetLastError(), "fp8 mxk launch");
             return 0;
         }
     }
+    if (xt) HIP_OK(xsplit(), "fp8 mxn x split launch");
 #define XN(NTV, MWV) do {                                                                      \
         if (uni)                                                                               \
             hipLaunchKernelGGL((k_fp8_mxn<NTV, true, MWV>), grid, dim3(64 * MWV), lds, st, y, x,  \

@@ -225,24 +225,30 @@ def test_batched_token_tiles_keep_bits(gpu, dsv4, monkeypatch, ntmax):
             assert common.bits_equal(yn[t], dsv4.mmq(m, x[t])), (ntmax, rows, t)
 
 
+@pytest.mark.parametrize("xf", ["0", "1"])
 @pytest.mark.parametrize("kp", ["0", "2", "4"])
-def test_batched_segment_split_keeps_bits(gpu, dsv4, monkeypatch, kp):
+def test_batched_segment_split_keeps_bits(gpu, dsv4, monkeypatch, kp, xf):
     """DSV4_GPU_MXK: with one column tile of at most five tokens per group,
     the batched kernel splits each tile's segments over KP waves (0: one
-    wave), which meet in LDS in segment order. Every setting gives each token
-    the single-token GEMV's bits: uniform and per-lane scales, ragged row
-    tiles and segments, fewer segments than waves, one to four groups."""
+    wave), which meet in LDS in segment order; DSV4_GPU_MXKF: its x terms
+    from the pre-split planes (0) or formed from the f32 rows in each
+    workgroup (1). Every setting gives each token the single-token GEMV's
+    bits: uniform and per-lane scales, ragged row tiles and segments, a last
+    unit past the row's end, fewer segments than waves (taken by the one-wave
+    form), one to four groups."""
     monkeypatch.setenv("DSV4_GPU_MXK", kp)
+    monkeypatch.setenv("DSV4_GPU_MXKF", xf)
     cases = ((300, 1536, 2, 128, 128), (129, 7168, 5, 128, 128), (70, 2096, 4, 1, 32),
              (33, 16384, 9, 16, 64), (200, 1040, 3, 4, 48), (16, 512, 20, 128, 128),
-             (7168, 7168, 4, 128, 128))
+             (40, 64, 3, 128, 128), (7168, 7168, 4, 128, 128))
     for rows, cols, nt, blk_r, blk_c in cases:
         rng = np.random.default_rng(rows + cols + nt)
         W = common.fp8_codes(rng, (rows, cols))
         S = (127 + rng.integers(-8, -3, size=((rows + blk_r - 1) // blk_r,
                                               (cols + blk_c - 1) // blk_c))).astype(np.uint8)
         x = rng.standard_normal((nt, cols), dtype=np.float32)
-        say("fp8 mxk %dx%d nt %d blk %dx%d MXK %s" % (rows, cols, nt, blk_r, blk_c, kp))
+        say("fp8 mxk %dx%d nt %d blk %dx%d MXK %s MXKF %s" % (rows, cols, nt, blk_r, blk_c,
+                                                              kp, xf))
         _, m = _run(dsv4, W, S, x[0], blk_r=blk_r, blk_c=blk_c)
         yn = dsv4.mmq_n(m, x)
         for t in range(nt):

@@ -1073,12 +1073,6 @@ int dsv4_gpu_topk(int *idxs, const float *scores, int n, int k)
     if (!g_ready || n < 0) return -1;
     if (k > n) k = n;
     if (k <= 0) return k < 0 ? -1 : 0;
-    for (int i = 0; i < n; i++)
-        if (isnan(scores[i])) {
-            DSV4_ERR("topk: score %d is NaN (the reference's order then depends on "
-                     "positions; not reproduced)", i);
-            return -1;
-        }
     if (scratch_reserve(g_index, dsv4_index_scratch_bytes(n)) != 0) return -1;
     Stage s;
     const size_t so = s.in(scores, (size_t)n * sizeof(float));
@@ -1118,11 +1112,6 @@ int dsv4_gpu_indexer_topk(int *idxs, const float *q, const float *w, int H,
                          g_index.p, hist, g_stream) != 0)
         return -1;
     if (stage_pull(io, (size_t)k * sizeof(int), idxs) != 0) return -1;
-    if (idxs[0] < 0) {                  /* the device top-k saw a NaN score */
-        DSV4_ERR("indexer_topk: a score is NaN (the reference's order then depends on "
-                 "positions; not reproduced)");
-        return -1;
-    }
     return k;
 }
 

@@ -24,9 +24,11 @@
  * largest, and how many elements equal to T are taken (k_tk_part,
  * k_tk_final).
  * Up to 4096 scores, one launch ranks every element directly (k_tk_small).
- * A NaN score makes every output slot -1: the reference's scan takes a NaN
- * exactly when it is the first index not yet taken, an order the keys cannot
- * express, so the device reports it instead of guessing.
+ * NaN scores follow the reference's scan too: it takes a NaN exactly when
+ * that NaN is the lowest index not yet taken, and otherwise the first
+ * maximum of the untaken finite scores. NaNs key below every finite score;
+ * when any is present, one workgroup sorts the selection and inserts the
+ * NaNs where the scan takes them (nan_finish).
  *
  * SPARSE ATTENTION (dsv4_attn.c:60-108): split over the selected rows and a
  * log-sum-exp combine. Partial pass: per split of selected rows, the scores,
@@ -92,10 +94,13 @@ __device__ __forceinline__ void meta_restart(uint32_t *meta)
 
 /* Order-preserving 32-bit key of a score: a > b as floats iff fkey(a) >
  * fkey(b) as integers; -0.0 folds into +0.0 since the reference's `>`
- * treats them as equal. */
+ * treats them as equal. Every NaN keys to 0, below every other score (the
+ * smallest, -inf, keys to 0x007FFFFF), so the key's top 11 bits put NaNs
+ * alone in bin 0. */
 __device__ __forceinline__ uint32_t fkey(float f)
 {
     uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0u;
     if ((u & 0x7FFFFFFFu) == 0u) u = 0u;
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
@@ -839,6 +844,163 @@ __device__ __forceinline__ uint32_t tk_scan(uint32_t v, uint32_t *wsum, uint32_t
     return before + inc - v;
 }
 
+/* Exclusive prefix maximum over the threads of an NT-thread workgroup
+ * (thread order; 0 for thread 0). Ends on a barrier. */
+template <int NT>
+__device__ __forceinline__ uint32_t tk_scan_max(uint32_t v, uint32_t *wsum)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    uint32_t inc = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(inc, o, 64);
+        if (lane >= o) inc = max(inc, t);
+    }
+    uint32_t exc = __shfl_up(inc, 1, 64);
+    if (lane == 0) exc = 0u;
+    if (lane == 63) wsum[wid] = inc;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < NT / 64; w++) exc = w < wid ? max(exc, wsum[w]) : exc;
+    __syncthreads();
+    return exc;
+}
+
+/* Bitonic sort of a[0 .. np), np a power of two, into descending order by
+ * the NT threads of the workgroup. Starts and ends on a barrier. */
+template <int NT>
+__device__ __forceinline__ void lds_sort_desc(unsigned long long *a, uint32_t np)
+{
+    __syncthreads();
+    for (uint32_t size = 2; size <= np; size <<= 1)
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t t = threadIdx.x; t < np / 2; t += NT) {
+                const uint32_t i = 2 * t - (t & (stride - 1)), j = i + stride;
+                const unsigned long long x = a[i], y = a[j];
+                /* blocks with (i & size) == 0 run descending, the others
+                 * ascending; the last merge (size == np) is all descending */
+                if ((x < y) == ((i & size) == 0u)) { a[i] = y; a[j] = x; }
+            }
+            __syncthreads();
+        }
+}
+
+__device__ __forceinline__ uint32_t pow2_at_least(uint32_t x)
+{
+    uint32_t p = 1u;
+    while (p < x) p <<= 1;
+    return p;
+}
+
+/* The reference's selection when scores hold NaNs (dsv4_indexer.c:92-106).
+ * Each pick of its scan starts at the lowest index not yet taken and moves
+ * only on `scores[c] > scores[best]`, so a NaN is taken exactly when it is
+ * that lowest index; otherwise the pick is the first maximum of the untaken
+ * finite scores. Its output is therefore the finite scores in (score desc,
+ * index asc) order with each NaN i inserted after P(i) of them, where P(i)
+ * is the largest 1-based place in that order of a finite index below i
+ * (0 when there is none): NaN i lands at (NaNs below i) + P(i). Since
+ * P(i) >= (finite indices below i), that position is at least i, so only
+ * NaNs below k can be taken, and only scores[0 .. k) are read.
+ *
+ * srt[0 .. k): the k largest composites in descending order with NaNs
+ * keyed 0 (so any NaN among them comes after every finite score, and a
+ * finite index missing from srt has a place >= k, which keeps every NaN
+ * above it out). aux: k words of LDS apart from srt's first k words. The
+ * NaNs' places are marked in aux; the other places take the finite
+ * entries in order. Called by every thread of the workgroup; writes
+ * idxs[0 .. k). */
+template <int NT>
+__device__ __forceinline__ void nan_finish(int *__restrict__ idxs, unsigned long long *srt, uint32_t *aux,
+                           const float *__restrict__ scores, int k, uint32_t *wsum)
+{
+    constexpr int CM = TK_KMAX / NT;                 /* entries per thread, at most */
+    constexpr uint32_t FAR = 0x3FFFFFFFu;            /* a place past any k */
+    const int tid = threadIdx.x;
+    const int C = (k + NT - 1) / NT, c0 = tid * C;
+    uint32_t *L = reinterpret_cast<uint32_t *>(srt);
+
+    float sv[CM];
+    uint32_t lw[CM];
+#pragma unroll
+    for (int c = 0; c < CM; c++) {
+        const int r = c0 + c;
+        const bool live = c < C && r < k;
+        sv[c] = scores[live ? r : 0];
+        const unsigned long long e = srt[live ? r : 0];
+        /* the index, bit 31 set for a NaN */
+        lw[c] = (0xFFFFFFFFu - (uint32_t)e) | ((e >> 32) == 0ull ? 0x80000000u : 0u);
+    }
+    __syncthreads();                                  /* srt read: reuse as L */
+#pragma unroll
+    for (int c = 0; c < CM; c++)
+        if (c < C && c0 + c < k) L[c0 + c] = lw[c];
+    for (int i = tid; i < k; i += NT) aux[i] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < CM; c++)                      /* place in L of finite indices < k */
+        if (c < C && c0 + c < k && lw[c] < (uint32_t)k) aux[lw[c]] = (uint32_t)(c0 + c) + 1u;
+    __syncthreads();
+
+    /* thread t: indices [c0, c0 + C). pe = 0 for a NaN, the place in L of a
+     * finite index, FAR for a finite index missing from L */
+    bool isn[CM];
+    uint32_t pe[CM], cnt = 0u, mx = 0u;
+#pragma unroll
+    for (int c = 0; c < CM; c++) {
+        const int i = c0 + c;
+        const bool live = c < C && i < k;
+        isn[c] = live && __builtin_isnan(sv[c]);
+        const uint32_t a = live ? aux[i] : 0u;
+        pe[c] = isn[c] ? 0u : (a ? a : FAR);
+        cnt += isn[c] ? 1u : 0u;
+        mx = live ? max(mx, pe[c]) : mx;
+    }
+    uint32_t tot;
+    const uint32_t j0 = tk_scan<NT>(cnt, wsum, &tot);
+    const uint32_t p0 = tk_scan_max<NT>(mx, wsum);
+    for (int i = tid; i < k; i += NT) aux[i] = 0xFFFFFFFFu;
+    __syncthreads();
+    {
+        uint32_t j = j0, P = p0;
+#pragma unroll
+        for (int c = 0; c < CM; c++) {
+            const int i = c0 + c;
+            if (!(c < C && i < k)) continue;
+            if (isn[c]) {
+                const uint32_t pos = j + P;
+                if (pos < (uint32_t)k) aux[pos] = (uint32_t)i;
+                j++;
+            } else {
+                P = max(P, pe[c]);
+            }
+        }
+    }
+    __syncthreads();
+
+    /* places [c0, c0 + C): a NaN's, or the next finite entry of L */
+    uint32_t o[CM], nf = 0u;
+#pragma unroll
+    for (int c = 0; c < CM; c++) {
+        const int p = c0 + c;
+        const bool live = c < C && p < k;
+        o[c] = live ? aux[p] : 0u;
+        nf += live && o[c] == 0xFFFFFFFFu ? 1u : 0u;
+    }
+    uint32_t f = tk_scan<NT>(nf, wsum, &tot);
+#pragma unroll
+    for (int c = 0; c < CM; c++) {
+        const int p = c0 + c;
+        if (!(c < C && p < k)) continue;
+        if (o[c] != 0xFFFFFFFFu) {
+            idxs[p] = (int)o[c];
+        } else {
+            idxs[p] = (int)(L[min(f, (uint32_t)k - 1u)] & 0x7FFFFFFFu);
+            f++;
+        }
+    }
+}
+
 /* Partition: workgroup g owns elements [g PT_ELEMS, (g + 1) PT_ELEMS); slot
  * m of thread t is element g PT_ELEMS + m PT_THREADS + t (coalesced loads,
  * index order = (slot, wave, lane)). Every workgroup reads the whole sliced
@@ -878,8 +1040,8 @@ k_tk_part(unsigned long long *__restrict__ cand, unsigned long long *__restrict_
         nan = nan || (in && __builtin_isnan(__uint_as_float(key[m])));
         key[m] = in ? fkey(__uint_as_float(key[m])) : 0u;
     }
-    /* a NaN anywhere: the final pass writes -1 to every slot (the
-     * reference's selection then depends on positions, not on the order) */
+    /* a NaN anywhere: the final pass applies the reference's NaN rule
+     * (its order then depends on positions, not only on the keys) */
     if (__ballot(nan) != 0ull && lane == 0) atomicOr(&meta[MT_NAN], 1u);
 
     uint32_t c[BPT];                                /* c[j]: bin blo + BPT-1-j */
@@ -1018,7 +1180,7 @@ __global__ void __launch_bounds__(FN_THREADS)
 k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
            const unsigned long long *__restrict__ bsel, const uint32_t *__restrict__ meta,
            const uint32_t *__restrict__ bcnt, const unsigned long long *__restrict__ blist,
-           uint32_t *__restrict__ hist_g, int G, int k)
+           uint32_t *__restrict__ hist_g, const float *__restrict__ scores, int G, int k)
 {
     constexpr int BPT = TK_BINS / FN_THREADS;           /* bins per thread */
     constexpr int GPT = RF_GMAX / FN_THREADS;           /* list lengths per thread */
@@ -1034,11 +1196,10 @@ k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
     for (int i = blockIdx.x * FN_THREADS + tid; i < TK_SLICES * TK_BINS / 4;
          i += gridDim.x * FN_THREADS)
         reinterpret_cast<u32x4 *>(hist_g)[i] = u32x4{0u, 0u, 0u, 0u};
-    if (meta[MT_NAN]) {                                   /* uniform per launch */
-        const int j = blockIdx.x * RK_EPW + tid;
-        if (tid < RK_EPW && j < k) idxs[j] = -1;
-        return;
-    }
+    /* NaN scores (uniform per launch): workgroup 0 alone sorts the
+     * selection and applies the reference's NaN rule (nan_finish) */
+    const bool nanm = meta[MT_NAN] != 0u;
+    if (nanm && blockIdx.x != 0) return;
     const uint32_t B = meta[MT_BIN], krem1 = meta[MT_KREM];
     const unsigned long long cnt = *reinterpret_cast<const unsigned long long *>(meta + MT_CNT);
     const uint32_t c_above = min((uint32_t)cnt, (uint32_t)TK_KMAX);
@@ -1047,6 +1208,17 @@ k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
     if (nbs <= (uint32_t)RF_LIST) {
         /* ---- direct form ---- */
         const uint32_t u = c_above + nbs, e0 = blockIdx.x * RK_EPW;
+        if (nanm) {
+            /* all of u (at most TK_KMAX + RF_LIST composites), padded with
+             * zeros to a power of two, sorted; its first k are the k largest */
+            const uint32_t np = pow2_at_least(max(u, (uint32_t)k));
+            for (uint32_t j = tid; j < np; j += FN_THREADS)
+                sh[j] = j < c_above ? cand[j] : j < u ? bsel[j - c_above] : 0ull;
+            lds_sort_desc<FN_THREADS>(sh, np);
+            nan_finish<FN_THREADS>(idxs, sh, reinterpret_cast<uint32_t *>(sh + TK_KMAX),
+                                   scores, k, wsum);
+            return;
+        }
         if (e0 >= u) return;                                /* the whole workgroup */
         const uint32_t ja = e0 < c_above ? 0u : c_above;
         const uint32_t jb = e0 + RK_EPW > c_above ? u : c_above;
@@ -1185,13 +1357,28 @@ k_tk_final(int *__restrict__ idxs, const unsigned long long *__restrict__ cand,
                     if (pg < c_gt) cs[pg] = ((unsigned long long)key << 32) | (0xFFFFFFFFull - idx);
                     pg++;
                 } else if (key == T) {
-                    if (pe < need_eq && blockIdx.x == 0) idxs[c_gt + pe] = (int)idx;
+                    /* with NaNs, into the sorted selection instead */
+                    if (pe < need_eq && nanm)
+                        cs[c_gt + pe] = ((unsigned long long)key << 32) | (0xFFFFFFFFull - idx);
+                    else if (pe < need_eq && blockIdx.x == 0)
+                        idxs[c_gt + pe] = (int)idx;
                     pe++;
                 }
             }
         }
     }
     __syncthreads();
+    if (nanm) {
+        /* cs[0 .. k): the candidates > T, then need_eq == T (below every
+         * candidate, in index order as composites); zeros pad to a power
+         * of two within cs, and the level-2/3 words after cs are free */
+        const uint32_t np = pow2_at_least((uint32_t)k);
+        for (uint32_t j = (uint32_t)k + tid; j < np; j += FN_THREADS) cs[j] = 0ull;
+        lds_sort_desc<FN_THREADS>(cs, np);
+        nan_finish<FN_THREADS>(idxs, cs, reinterpret_cast<uint32_t *>(sh + TK_KMAX), scores,
+                               k, wsum);
+        return;
+    }
 
     /* ---- place this workgroup's candidates ---- */
     const uint32_t e = blockIdx.x * RK_EPW + tid / RK_TPE, sub = tid % RK_TPE;
@@ -1240,9 +1427,16 @@ k_tk_small(int *__restrict__ idxs, const float *__restrict__ scores, int n, int 
     const int e = blockIdx.x * TS_EPW + (int)(threadIdx.x / TS_TPE);
     const int q = threadIdx.x % TS_TPE;
     if (anynan) {
-        /* every workgroup saw every score: they all take this branch and
-         * together write -1 to slots 0 .. k-1 (k <= n) */
-        if (q == 0 && e < k) idxs[e] = -1;
+        /* every workgroup saw every score and takes this branch; workgroup
+         * 0 sorts all n composites (NaNs keyed 0, zeros padding to a power
+         * of two) and applies the reference's NaN rule (nan_finish) */
+        __shared__ uint32_t wsum[256 / 64];
+        if (blockIdx.x != 0) return;
+        const uint32_t np = pow2_at_least((uint32_t)n);
+        for (uint32_t j = (uint32_t)n + threadIdx.x; j < np; j += 256) comp[j] = 0ull;
+        lds_sort_desc<256>(comp, np);
+        nan_finish<256>(idxs, comp, reinterpret_cast<uint32_t *>(comp) + TS_NMAX, scores, k,
+                        wsum);
         return;
     }
     const unsigned long long me = comp[min(e, n - 1)];
@@ -2343,7 +2537,7 @@ int dsv4_topk_launch(int *d_idxs, const float *d_scores, int n, int k,
     /* the direct form places up to k - 1 + RF_LIST elements, the refinement
      * form k */
     hipLaunchKernelGGL(k_tk_final, dim3((k + RF_LIST + RK_EPW - 1) / RK_EPW), dim3(FN_THREADS),
-                       0, st, d_idxs, cand, bsel, meta, bcnt, blist, hist, G, k);
+                       0, st, d_idxs, cand, bsel, meta, bcnt, blist, hist, d_scores, G, k);
     HIP_OK(hipGetLastError(), "topk final launch");
     return 0;
 }

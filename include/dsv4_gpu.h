@@ -390,14 +390,15 @@ int dsv4_gpu_indexer_score(float *out, const float *q, const float *w, int H,
 
 /* dsv4_topk (dsv4_indexer.c:92-106), bit-exact: the k largest scores,
  * ordered by score descending with ties to the lower index; k is clamped to
- * n; returns the count written, or -1. A NaN score returns -1: the
- * reference's scan (`scores[c] > scores[best]`) takes a NaN exactly when it
- * is the first index not yet taken, an order that depends on positions, and
- * the device does not reproduce it. */
+ * n; returns the count written, or -1. NaN scores are placed as the
+ * reference's scan (`scores[c] > scores[best]`, best starting at the lowest
+ * index not yet taken) places them: a NaN is taken exactly when it is the
+ * lowest untaken index, otherwise the pick is the first maximum of the
+ * untaken finite scores. */
 int dsv4_gpu_topk(int *idxs, const float *scores, int n, int k);
 
 /* Score then top-k in one call, the CSA selection of dsv4_layer.c:280-291.
- * Returns the count written, or -1 (also when a score is NaN, as above). */
+ * Returns the count written, or -1. */
 int dsv4_gpu_indexer_topk(int *idxs, const float *q, const float *w, int H,
                           int D, const dsv4_gpu_kv *keys, int row0,
                           int key_stride, int n, int k);
@@ -420,8 +421,8 @@ int dsv4_gpu_indexer_score_d(float *d_out, const float *d_q, const float *d_w,
                              const float *d_key_scales, int key_fmt,
                              int key_stride, int n, float scale, void *stream);
 /* dsv4_gpu_topk_d (and the top-k inside dsv4_gpu_mla_decode_d and the
- * attention block) writes -1 to every one of its k slots when any score is
- * NaN: the selection is then masked rather than in a guessed order. */
+ * attention block) selects exactly as dsv4_gpu_topk does, NaN scores
+ * included. */
 int dsv4_gpu_topk_d(int *d_idxs, const float *d_scores, int n, int k,
                     void *stream);
 /* Selected rows outside [0, kv_rows) are treated as masked and never read

@@ -11,7 +11,7 @@ inputs is stored so that generator drift is told apart from an oracle error).
 Run in the container where /root/reference exists (oracle/_ref must be
 built); the tests then read the .npz files with numpy.load (no pickles).
 
-    python tests/golden/make_golden.py            # small vectors
+    python tests/golden/make_golden.py            # small vectors, NaN top-k
     python tests/golden/make_golden.py --c4       # + C4 top-2048 (~40 s)
 """
 import hashlib
@@ -129,6 +129,62 @@ def small():
     print("golden_small.npz: %d arrays" % len(out))
 
 
+def nan_topk():
+    """dsv4_topk (dsv4_indexer.c:92-106) on scores holding NaNs: the
+    reference's scan takes a NaN exactly when it is the lowest index not yet
+    taken. Cases cover each device path: up to 4096 scores (ranked in one
+    launch), more with the k-th largest in a bin of at most 4096 elements
+    (direct final pass) or of more (refined), and fewer finite scores than
+    k, so that bin is the NaNs' own."""
+    rng = np.random.default_rng(20261202)
+    cases = []
+
+    def case(s, k):
+        cases.append((np.asarray(s, np.float32), int(k)))
+
+    s = rng.standard_normal(300).astype(np.float32)
+    s[0] = np.nan
+    case(s, 40)                                           # NaN at index 0
+    s = rng.standard_normal(300).astype(np.float32)
+    s[[37, 150, 151, 299]] = np.nan
+    case(s, 100)                                          # NaNs mid-array
+    s = (rng.integers(-5, 6, 300) * 0.5).astype(np.float32)
+    s[0:4] = np.nan
+    s[10:20] = np.nan
+    s[50:55] = np.nan
+    case(s, 200)                                          # runs, with ties
+    s = np.full(300, np.nan, np.float32)
+    case(s, 50)                                           # all NaN
+    s = (rng.integers(-40, 40, 5000) * 0.25).astype(np.float32)
+    s[rng.integers(0, 5000, 60)] = -0.0
+    s[0:3] = np.nan
+    s[40:48] = np.nan
+    s[rng.integers(0, 5000, 30)] = np.nan
+    case(s, 700)                                          # radix, direct
+    s = rng.standard_normal(5000).astype(np.float32)
+    s[rng.permutation(5000)[:3000]] = np.nan
+    case(s, 2200)                                         # finite < k, direct
+    s = rng.standard_normal(9000).astype(np.float32)
+    s[rng.permutation(9000)[:8000]] = np.nan
+    case(s, 1200)                                         # finite < k, refined
+    s = np.concatenate([np.full(4200, 1.125), rng.uniform(2.0, 4.0, 300),
+                        rng.uniform(-4.0, 0.5, 500)]).astype(np.float32)
+    s = s[rng.permutation(s.size)]
+    s[0:5] = np.nan
+    s[100:110] = np.nan
+    case(s, 1000)                                         # crowded bin, refined
+    out = {}
+    for i, (sc, k) in enumerate(cases):
+        t0 = time.time()
+        out["s%d" % i] = sc
+        out["k%d" % i] = np.int32(k)
+        out["top%d" % i] = oracle.ref_topk(sc, k)
+        print("nan top-k case %d: n %d k %d, %d NaN: %.1f s"
+              % (i, sc.size, k, int(np.isnan(sc).sum()), time.time() - t0))
+    np.savez_compressed(os.path.join(HERE, "golden_nan_topk.npz"), **out)
+    print("golden_nan_topk.npz: %d cases" % len(cases))
+
+
 def c4_inputs():
     """The C4 indexer inputs, regenerated from seed 4 (tests/common.py)."""
     rng = np.random.default_rng(4)
@@ -153,5 +209,6 @@ if __name__ == "__main__":
     if not oracle.ref_available():
         sys.exit("oracle/_ref/libdsv4ref.so is not built (make -C oracle)")
     small()
+    nan_topk()
     if "--c4" in sys.argv:
         c4()

@@ -78,6 +78,31 @@ def test_topk_ties_golden():
     assert np.array_equal(oracle.topk(G["tie_scores"], 700), G["tie_top"])
 
 
+GN = np.load(os.path.join(HERE, "golden", "golden_nan_topk.npz"))
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_nan_topk_golden(case):
+    """dsv4_topk on scores holding NaNs (at index 0, mid-array, in runs, all
+    NaN, fewer finite scores than k): the reference's scan takes a NaN
+    exactly when it is the lowest untaken index."""
+    s, k = GN["s%d" % case], int(GN["k%d" % case])
+    assert np.array_equal(oracle.topk(s, k), GN["top%d" % case])
+
+
+def test_nan_topk_matches_compiled_reference():
+    """Random NaN patterns over ties, against the compiled dsv4_topk."""
+    if not oracle.ref_available():
+        pytest.skip("oracle/_ref not built")
+    rng = np.random.default_rng(11)
+    for t in range(300):
+        n = int(rng.integers(1, 200))
+        s = (rng.integers(-4, 5, n) * 0.5).astype(np.float32)
+        s[rng.random(n) < rng.random()] = np.nan
+        k = int(rng.integers(1, n + 1))
+        assert np.array_equal(oracle.topk(s, k), oracle.ref_topk(s, k)), (t, n, k)
+
+
 @pytest.mark.parametrize("tag", ["attn_s", "attn_w"])
 def test_sparse_attn_golden(tag):
     """dsv4_sparse_attn with masked slots and per-head sinks (the shape of the

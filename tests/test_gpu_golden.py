@@ -71,6 +71,29 @@ def test_topk_ties_golden(gpu, dsv4):
     assert np.array_equal(dsv4.topk(G["tie_scores"], 700), G["tie_top"])
 
 
+GN = np.load(os.path.join(HERE, "golden", "golden_nan_topk.npz"))
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_nan_topk_golden(gpu, dsv4, case):
+    """The compiled reference's dsv4_topk on scores holding NaNs, through the
+    host call and the stream-ordered one: every device path (ranked up to
+    4096 scores; direct and refined final passes; fewer finite than k)."""
+    import torch
+    s, k = GN["s%d" % case], int(GN["k%d" % case])
+    want = GN["top%d" % case]
+    print("nan top-k golden %d: n %d k %d, %d NaN" % (case, s.size, k, int(np.isnan(s).sum())),
+          flush=True)
+    assert np.array_equal(dsv4.topk(s, k), want)
+    dev = torch.device("cuda:0")
+    d_s = torch.from_numpy(s).to(dev)
+    d_i = torch.full((k,), 7, dtype=torch.int32, device=dev)
+    sp = torch.cuda.current_stream().cuda_stream
+    assert dsv4.lib().dsv4_gpu_topk_d(d_i.data_ptr(), d_s.data_ptr(), s.size, k, sp) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(d_i.cpu().numpy(), want)
+
+
 def test_c4_topk_golden(gpu, dsv4):
     """C4: 32768 fp8 keys, top-2048 -- the reference's own selection."""
     C = np.load(os.path.join(HERE, "golden", "golden_c4_topk.npz"))

@@ -34,7 +34,12 @@ def _disassemble(tmp):
     if not os.path.exists(OBJ):
         pytest.skip("the backend is not built (no %s)" % OBJ)
     fat, co = os.path.join(tmp, "mla.fat"), os.path.join(tmp, "mla.co")
-    subprocess.run(["objcopy", "--dump-section", ".hip_fatbin=" + fat, OBJ], check=True)
+    # objcopy rewrites its input when given no output file: it works on a
+    # copy, so the build product keeps its bytes and its timestamp
+    obj = os.path.join(tmp, "mla.o")
+    shutil.copyfile(OBJ, obj)
+    subprocess.run(["objcopy", "--dump-section", ".hip_fatbin=" + fat, obj, os.devnull],
+                   check=True)
     subprocess.run([os.path.join(LLVM, "clang-offload-bundler"), "--unbundle", "--type=o",
                     "--input=" + fat, "--targets=hipv4-amdgcn-amd-amdhsa--gfx950",
                     "--output=" + co], check=True)

@@ -13,6 +13,9 @@ Two CPU implementations are exposed through ctypes:
   (``src/core/dsv4_{matmul,indexer,attn,ops,rope,compress}.c``) compiled as they lie by
   ``oracle/Makefile``. Present wherever it was built; used to pin the
   restatement bit for bit and as the ``cpu_baseline`` of ``bench.py``.
+* ``_ref/libdsv4moe.so`` -- the reference's static ``moe()``
+  (``src/model/dsv4_layer.c:369-484``) reached through ``moe_ref.c``, which
+  #includes that file; pins the restatement's routed-expert sum.
 
 Parity unpinned: none of the restatement's functions. Each is checked
 against the compiled reference in its reference-shaped special case and
@@ -27,6 +30,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 _ORC_PATH = os.path.join(HERE, "liboracle.so")
 _REF_PATH = os.path.join(HERE, "_ref", "libdsv4ref.so")
+_MOE_PATH = os.path.join(HERE, "_ref", "libdsv4moe.so")
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _u8p = ctypes.POINTER(ctypes.c_uint8)
@@ -36,6 +40,7 @@ _vp = ctypes.c_void_p
 
 _orc = None
 _ref = None
+_moe = None
 
 
 def build():
@@ -109,6 +114,53 @@ def lib():
 
 def ref_available():
     return os.path.exists(_REF_PATH)
+
+
+def ref_moe_available():
+    return os.path.exists(_MOE_PATH)
+
+
+def ref_moe_routed(x, experts, ids, gate_bf16, limit, routed_scale):
+    """The reference's own moe() (dsv4_layer.c:369-484) on one token: the
+    routed experts `experts` (a list of expert dicts, indexed by id), hash
+    routing that selects `ids` (tid2eid of token 0), the BF16 router gate
+    [n_exp][hidden] for the weights, and a shared expert of zeros. Returns
+    (out, idx, w): moe()'s output -- its routed k-ordered sum plus an exact
+    +0.0 per element -- and the selection and weights it used."""
+    global _moe
+    if _moe is None:
+        L = ctypes.CDLL(_MOE_PATH)
+        pp = ctypes.POINTER(_u8p)
+        L.ref_moe_routed.restype = ctypes.c_int
+        L.ref_moe_routed.argtypes = [_f32p, _i32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int, ctypes.c_int, pp, pp, pp, pp, pp, pp,
+                                     ctypes.POINTER(ctypes.c_int64), _u16p, ctypes.c_float,
+                                     ctypes.c_float]
+        _moe = L
+    x = _f32(x)
+    hidden = x.size
+    n_exp = len(experts)
+    inter = experts[0]["w1"].shape[0]
+    ids = np.ascontiguousarray(ids, np.int64)
+    topk = ids.size
+    gate = np.ascontiguousarray(gate_bf16, np.uint16)
+    keep = []
+
+    def arr(name):
+        a = (_u8p * n_exp)()
+        for e, ex in enumerate(experts):
+            v = _u8(ex[name]); keep.append(v); a[e] = _p(v, _u8p)
+        return a
+    out = np.empty(hidden, np.float32)
+    idx = np.empty(topk, np.int32)
+    w = np.empty(topk, np.float32)
+    rc = _moe.ref_moe_routed(_p(out, _f32p), _p(idx, _i32p), _p(w, _f32p), _p(x, _f32p),
+                             hidden, inter, n_exp, topk, arr("w1"), arr("s1"), arr("w3"),
+                             arr("s3"), arr("w2"), arr("s2"),
+                             ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                             _p(gate, _u16p), limit, routed_scale)
+    assert rc == 0
+    return out, idx, w
 
 
 def ref():

@@ -42,6 +42,18 @@
  *     layer and position) and its routed experts' k-ordered sum from the
  *     fused pass (dsv4_gpu_moe_fp4), through the matmul hooks described at
  *     e2e_mmq.
+ *   - pass 4: the reference's batched prefill protocol
+ *     (tests/unit/test_model_oracle.c:295-378): dsv4_layer_forward_n over
+ *     chunks of 1, 2, 3 and all the tokens, from fresh layer state each
+ *     time, with pass 2's residency and device CSA calls, so moe_n's
+ *     batched matmuls (dsv4_layer.c:714-855: the router gate, every routed
+ *     expert of the batch's union, the shared expert) run as
+ *     dsv4_gpu_mmq_n. Every position's logits must equal pass 2's bit for
+ *     bit. With --cpu-only it runs on the CPU against the CPU pass.
+ *   - pass 5 (GPU runs): the same chunks with pass 3's device attention
+ *     block, and moe_n's routed sum from the device's batched pass
+ *     (dsv4_gpu_moe_fp4_n, hooked at e2e_mmq_n); every position's logits
+ *     must equal pass 3's bit for bit.
  * Routed experts come from memory (all resident).
  *
  * usage: dsv4_e2e CKPT_DIR TOKENS_FILE [--cpu-only]
@@ -140,12 +152,14 @@ void e2e_sparse_attn(float *o, const float *q, const float *kv, const float *sin
  * matmul passes through to the reference's dispatch. */
 void dsv4_mmq(float *y, const float *x, const DSV4QMat *m);
 
-static int g_attn_block, g_attn_nl, g_attn_pos, g_attn_pending = -1;
+static int g_attn_block, g_attn_nl, g_attn_pending = -1;
+static int g_lpos[DSV4_MAX_LAYERS];         /* the next position of each layer's block */
 static const DSV4LayerBind *g_attn_lb;
 static const DSV4Cfg *g_cfg;
 static DSV4Scratch *g_scr;
+static DSV4Batch *g_bat;                    /* the batch of a prefill pass */
 static float *g_attn_out;
-static long g_n_block, g_n_moe;
+static long g_n_block, g_n_moe, g_n_moe_n;
 
 void e2e_mmq(float *y, const float *x, const DSV4QMat *m)
 {
@@ -166,7 +180,9 @@ void e2e_mmq(float *y, const float *x, const DSV4QMat *m)
                 break;
             }
             if (m == &g_attn_lb[L].w.attn.wq_a) {
-                if (dsv4_gpu_attn_step(g_attn_out, x, L, g_attn_pos) != 0)
+                /* a layer's attention() runs once per position, in position
+                 * order, in decode and in prefill (dsv4_layer.c:865-894) */
+                if (dsv4_gpu_attn_step(g_attn_out, x, L, g_lpos[L]++) != 0)
                     csa_fail("attention block");
                 g_attn_pending = L;
                 g_n_block++;
@@ -180,6 +196,31 @@ void e2e_mmq(float *y, const float *x, const DSV4QMat *m)
         }
     }
     dsv4_mmq(y, x, m);
+}
+
+/* dsv4_layer.c is also compiled with dsv4_mmq_n renamed to e2e_mmq_n. In
+ * pass 5, moe_n (dsv4_layer.c:714-855) has summed the batch's routed experts
+ * in k order into its output, the batch's blk_out (:912), when the shared
+ * expert's first batched matmul (:843) arrives with the same x: replace
+ * that sum with the device's batched routed-expert pass, from the router's
+ * own selection and weights (b->topk_idx, b->topk_w). Every batched matmul
+ * then goes to the reference's dispatch, dsv4_mmq_n (dsv4_matmul.c:562). */
+void dsv4_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt);
+
+void e2e_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
+{
+    if (g_attn_block && g_bat) {
+        for (int L = 0; L < g_attn_nl; L++)
+            if (m == &g_attn_lb[L].w.moe.shared.w1) {
+                const DSV4Cfg *c = g_cfg;
+                if (dsv4_gpu_moe_fp4_n(g_bat->blk_out, x, L, g_bat->topk_idx, g_bat->topk_w, nt,
+                                       c->topk, c->hidden, c->moe_inter, c->swiglu_limit) != 0)
+                    csa_fail("batched routed experts");
+                g_n_moe_n++;
+                break;
+            }
+    }
+    dsv4_mmq_n(y, x, m, nt);
 }
 
 /* ---------------------------------------------------- routed experts ---- */
@@ -345,7 +386,6 @@ static int run_pass(const Model *M, const int *tok, int n, float *logits)
         if (dsv4_state_init(&ls[L], c, L, M->maxpos) != 0) return -1;
     const DSV4QMat head = M->head;
     for (int pos = 0; pos < n; pos++) {
-        g_attn_pos = pos;
         dsv4_embed_row(y, M->mb->w.embed, M->mb->w.wdt, tok[pos], d);
         for (int j = 0; j < hc; j++) memcpy(h + (size_t)j * d, y, (size_t)d * sizeof(float));
         for (int L = 0; L < c->n_layers; L++) {
@@ -368,6 +408,56 @@ static int run_pass(const Model *M, const int *tok, int n, float *logits)
     return 0;
 }
 
+/* The reference's batched prefill (tests/unit/test_model_oracle.c:303-372):
+ * chunks of `chunk` tokens through dsv4_layer_forward_n from fresh layer
+ * state, then each token's head as in run_pass; logits[pos][vocab]. */
+static int run_prefill(const Model *M, const int *tok, int n, int chunk, float *logits)
+{
+    const DSV4Cfg *c = M->c;
+    const int hc = c->hc_mult, d = c->hidden;
+    DSV4LayerState *ls = calloc((size_t)c->n_layers, sizeof *ls);
+    float *hb = calloc((size_t)chunk * hc * d, sizeof(float));
+    float *y = calloc((size_t)d, sizeof(float));
+    int32_t *tid = calloc((size_t)chunk, sizeof(int32_t));
+    DSV4Batch bat;
+    if (!ls || !hb || !y || !tid || dsv4_batch_init(&bat, c, chunk) != 0) return -1;
+    for (int L = 0; L < c->n_layers; L++)
+        if (dsv4_state_init(&ls[L], c, L, M->maxpos) != 0) return -1;
+    const DSV4QMat head = M->head;
+    g_bat = &bat;
+    for (int p0 = 0; p0 < n; p0 += chunk) {
+        const int nt = n - p0 < chunk ? n - p0 : chunk;
+        for (int t = 0; t < nt; t++) {
+            tid[t] = (int32_t)tok[p0 + t];
+            dsv4_embed_row(y, M->mb->w.embed, M->mb->w.wdt, tok[p0 + t], d);
+            for (int j = 0; j < hc; j++)
+                memcpy(hb + ((size_t)t * hc + j) * d, y, (size_t)d * sizeof(float));
+        }
+        for (int L = 0; L < c->n_layers; L++) {
+            const int comp = dsv4_compress_ratio(c, L) != 0;
+            dsv4_layer_forward_n(hb, &M->lb[L].w, c, M->s, &bat, M->src, &ls[L],
+                                 comp ? M->cs_c : M->cs_d, comp ? M->sn_c : M->sn_d,
+                                 p0, tid, nt);
+        }
+        for (int t = 0; t < nt; t++) {
+            head_hc(y, hb + (size_t)t * hc * d, &M->mb->w.hc_head, hc, d, c->rms_eps,
+                    c->hc_eps);
+            dsv4_rmsnorm(y, y, M->mb->w.norm, d, c->rms_eps);
+            dsv4_mmq(logits + (size_t)(p0 + t) * c->vocab, y, &head);
+        }
+    }
+    g_bat = NULL;
+    for (int L = 0; L < c->n_layers; L++) dsv4_state_free(&ls[L]);
+    dsv4_batch_free(&bat);
+    free(ls); free(hb); free(y); free(tid);
+    return 0;
+}
+
+/* Positions whose logits equal want's bit for bit, and whose argmax equals
+ * ref's. */
+static void compare_bits(const float *got, const float *want, const float *ref, int n,
+                         int vocab, int *same, int *agree);
+
 static int argmax(const float *v, int n, float *margin)
 {
     int a = 0;
@@ -376,6 +466,28 @@ static int argmax(const float *v, int n, float *margin)
     for (int i = 0; i < n; i++) if (i != a && v[i] > second) second = v[i];
     if (margin) *margin = v[a] - second;
     return a;
+}
+
+static void compare_bits(const float *got, const float *want, const float *ref, int n,
+                         int vocab, int *same, int *agree)
+{
+    *same = *agree = 0;
+    for (int p = 0; p < n; p++) {
+        const size_t o = (size_t)p * vocab;
+        *same += memcmp(got + o, want + o, (size_t)vocab * sizeof(float)) == 0;
+        *agree += argmax(got + o, vocab, NULL) == argmax(ref + o, vocab, NULL);
+    }
+}
+
+/* The block's per-layer device state and position counters, restarted
+ * before a pass that runs the device attention block from position 0. */
+static int restart_blocks(int n_layers)
+{
+    for (int L = 0; L < n_layers; L++) {
+        g_lpos[L] = 0;
+        if (dsv4_gpu_attn_reset(L) != 0) return -1;
+    }
+    return 0;
 }
 
 /* Vector-scaled relative error (tests/unit/test_cuda.c:160-167). */
@@ -545,7 +657,7 @@ int main(int argc, char **argv)
         got3 = malloc((size_t)n * c.vocab * sizeof(float));
         if (!g_attn_out || !got3) return 1;
         g_attn_block = 1;
-        if (run_pass(&M, tok, n, got3) != 0) return 1;
+        if (restart_blocks(c.n_layers) != 0 || run_pass(&M, tok, n, got3) != 0) return 1;
         g_attn_block = 0;
         for (int p = 0; p < n; p++) {
             const int ar = argmax(ref + (size_t)p * c.vocab, c.vocab, NULL);
@@ -555,6 +667,48 @@ int main(int argc, char **argv)
             if (r > worst3) worst3 = r;
             agree3 += ar == ag;
         }
+    }
+
+    /* passes 4 and 5: the reference's batched prefill at chunks 1, 2, 3 and
+     * all the tokens (test_model_oracle.c:303), each position's logits bit
+     * for bit against the per-token GPU pass with the same device parts */
+    int pf_runs = 0, pf_same[2] = {0, 0}, pf_agree[2] = {0, 0}, pf_pos = 0;
+    char pf_list[64] = "";
+    {
+        const int chunks[4] = {1, 2, 3, n};
+        float *got4 = malloc((size_t)n * c.vocab * sizeof(float));
+        if (!got4) return 1;
+        for (int ci = 0; ci < 4; ci++) {
+            const int ch = chunks[ci];
+            if (ch < 1 || ch > DSV4_MAX_BATCH || (ci > 0 && ch == chunks[ci - 1])) continue;
+            for (int v = 0; v < (cpu_only ? 1 : 2); v++) {
+                int same, agree_c;
+                if (v == 0) {                /* pass 4: dispatch + device CSA
+                                              * (all on the CPU with --cpu-only) */
+                    g_gpu_csa = !cpu_only;
+                    if (run_prefill(&M, tok, n, ch, got4) != 0) return 1;
+                    g_gpu_csa = 0;
+                    compare_bits(got4, got, ref, n, c.vocab, &same, &agree_c);
+                } else {                     /* pass 5: device block + moe_n */
+                    g_attn_block = 1;
+                    if (restart_blocks(c.n_layers) != 0 ||
+                        run_prefill(&M, tok, n, ch, got4) != 0)
+                        return 1;
+                    g_attn_block = 0;
+                    compare_bits(got4, got3, ref, n, c.vocab, &same, &agree_c);
+                }
+                printf("prefill pass %d chunk %d: %d of %d positions bit-identical to pass %d, "
+                       "argmax equal to the CPU path at %d\n", 4 + v, ch, same, n, 2 + v,
+                       agree_c);
+                pf_same[v] += same;
+                pf_agree[v] += agree_c;
+            }
+            pf_pos += n;
+            pf_runs++;
+            snprintf(pf_list + strlen(pf_list), sizeof pf_list - strlen(pf_list), "%s%d",
+                     pf_runs > 1 ? "," : "", ch);
+        }
+        free(got4);
     }
 
     int agree = 0;
@@ -573,9 +727,16 @@ int main(int argc, char **argv)
            "fp4_mats %d gpu_score %ld gpu_topk %ld gpu_attn %ld bf16_mats %d "
            "head_ok %ld/%ld\n", n, agree, worst, gpu_mats, fp4_mats, g_n_score, g_n_topk,
            g_n_attn, bf16_mats, g_n_head_ok, g_n_head);
-    if (!cpu_only)
+    printf("summary45: prefill chunks %s positions %d pass4_bit_identical %d "
+           "pass4_argmax_equal %d pass5_bit_identical %d pass5_argmax_equal %d "
+           "moe_n_calls %ld\n", pf_list, pf_pos, pf_same[0], pf_agree[0], pf_same[1],
+           pf_agree[1], g_n_moe_n);
+    if (!cpu_only) {
         printf("summary3: attention blocks on the device: steps %ld argmax_equal %d "
                "worst_rel %.3g fused_moe %ld\n", g_n_block, agree3, worst3, g_n_moe);
-    if (!cpu_only) dsv4_gpu_shutdown();
-    return (agree == n && (cpu_only || agree3 == n)) ? 0 : 1;
+        dsv4_gpu_shutdown();
+    }
+    const int pf_ok = pf_same[0] == pf_pos && pf_agree[0] == pf_pos &&
+                      (cpu_only || (pf_same[1] == pf_pos && pf_agree[1] == pf_pos));
+    return (agree == n && (cpu_only || agree3 == n) && pf_ok) ? 0 : 1;
 }

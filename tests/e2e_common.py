@@ -38,6 +38,10 @@ def run(ckpt, tokens_file, cpu_only=False, timeout=300):
                      r"gpu_attn (\d+) bf16_mats (\d+) head_ok (\d+)/(\d+)", p.stdout)
     p.summary3 = re.search(r"summary3: attention blocks on the device: steps (\d+) "
                            r"argmax_equal (\d+) worst_rel (\S+) fused_moe (\d+)", p.stdout)
+    p.summary45 = re.search(r"summary45: prefill chunks (\S+) positions (\d+) "
+                            r"pass4_bit_identical (\d+) pass4_argmax_equal (\d+) "
+                            r"pass5_bit_identical (\d+) pass5_argmax_equal (\d+) "
+                            r"moe_n_calls (\d+)", p.stdout)
     p.load = re.search(r"load: (\d+) shards, (\d+) tensors indexed; (\d+) matrices and "
                        r"(\d+) experts read into HBM, (\d+) bytes in (\S+) s \((\S+) GB/s\)",
                        p.stdout)

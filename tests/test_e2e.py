@@ -25,6 +25,20 @@ def test_reference_decode_runs_and_is_deterministic(tmp_path):
     assert len({r["ref"] for r in rows}) > 10
 
 
+def test_reference_prefill_protocol_on_cpu(tmp_path):
+    """The reference's batched prefill protocol (test_model_oracle.c:295-378)
+    on the CPU: dsv4_layer_forward_n at chunks 1, 2, 3 and 46 gives logits
+    bit-identical to the per-token decode. The GPU run repeats it with the
+    device's batched matmuls (tests/test_gpu_e2e.py)."""
+    ckpt, tf = e2e_common.prepare(tmp_path)
+    p, rows, summ = e2e_common.run(ckpt, tf, cpu_only=True)
+    assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-2000:]
+    s = p.summary45
+    assert s, p.stdout[-2000:]
+    assert s.group(1) == "1,2,3,46" and int(s.group(2)) == 4 * 46
+    assert int(s.group(3)) == int(s.group(4)) == 4 * 46
+
+
 def test_attention_driver_reference_pass(tmp_path):
     """oracle/_ref/dsv4_attn's first pass -- the reference's own attention()
     on every layer of the tiny checkpoint, called through the #included

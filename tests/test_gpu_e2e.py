@@ -18,6 +18,15 @@ attention block instead (dsv4_gpu_attn_step, one call per layer and
 position), and its routed experts' k-ordered sum from the fused pass
 (dsv4_gpu_moe_fp4) (oracle/e2e_decode.c, e2e_mmq).
 
+Passes 4 and 5 run the reference's batched prefill protocol
+(tests/unit/test_model_oracle.c:295-378): dsv4_layer_forward_n at chunks 1,
+2, 3 and 46 from fresh state. Pass 4 keeps pass 2's residency and device CSA
+calls, so moe_n's batched matmuls (router gate, the batch's routed experts,
+shared expert; dsv4_layer.c:714-855) run through dsv4_gpu_mmq_n; pass 5 adds
+pass 3's attention block and takes moe_n's routed sum from
+dsv4_gpu_moe_fp4_n. Each position's logits must be bit-identical to the
+per-token GPU pass with the same device parts.
+
 Bar: identical argmax at every position, in both GPU passes. The logits
 agree within the reference's own whole-model tolerance, 2e-3 vector-scaled
 (tests/unit/test_model_oracle.c:253-270).
@@ -69,3 +78,14 @@ def test_gpu_trunk_argmax_identical(tmp_path):
     assert int(s3.group(1)) == 46 * 4 and int(s3.group(2)) == 46
     assert float(s3.group(3)) < 2e-3
     assert int(s3.group(4)) == 46 * 4          # every layer's routed experts fused
+    # passes 4 and 5: the batched prefill, bit for bit against the per-token passes
+    s45 = p.summary45
+    assert s45, p.stdout[-2000:]
+    print("prefill: chunks %s, pass 4 %s/%s bit-identical, pass 5 %s/%s, %s batched MoE calls"
+          % (s45.group(1), s45.group(3), s45.group(2), s45.group(5), s45.group(2),
+             s45.group(7)), flush=True)
+    assert s45.group(1) == "1,2,3,46" and int(s45.group(2)) == 4 * 46
+    assert int(s45.group(3)) == int(s45.group(4)) == 4 * 46
+    assert int(s45.group(5)) == int(s45.group(6)) == 4 * 46
+    # moe_n once per layer and chunk of every chunking: 46 + 23 + 16 + 1 chunks
+    assert int(s45.group(7)) == 4 * (46 + 23 + 16 + 1)

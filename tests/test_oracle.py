@@ -266,6 +266,29 @@ def test_moe_is_k_ordered_expert_sum():
     assert common.bits_equal(out, want)
 
 
+@pytest.mark.skipif(not oracle.ref_moe_available(), reason="oracle/_ref/libdsv4moe.so not built")
+@pytest.mark.parametrize("hidden,inter,n_exp,topk,limit", [
+    (256, 128, 12, 4, 10.0), (512, 96, 20, 8, 10.0), (128, 64, 9, 6, 0.0),
+    (7168, 2048, 10, 8, 10.0)])
+def test_moe_bit_equal_to_reference_moe(hidden, inter, n_exp, topk, limit):
+    """The oracle's routed-expert sum against the reference's own moe()
+    (dsv4_layer.c:369-484, through oracle/moe_ref.c): hash routing picks
+    the experts, the BF16 gate gives the weights as the model computes them,
+    and the shared expert is zero, so moe()'s output is its k-ordered sum
+    (:471-475) plus an exact +0.0. Bit for bit, including C3's shape."""
+    rng = np.random.default_rng(hidden + inter + n_exp + topk)
+    experts = [common.fp4_expert(rng, hidden, inter) for _ in range(n_exp)]
+    ids = rng.permutation(n_exp)[:topk]
+    gate = common.bf16_matrix(rng, (n_exp, hidden), 0.1)
+    x = common.bf16_round(rng.standard_normal(hidden).astype(np.float32))
+    out, idx, w = oracle.ref_moe_routed(x, experts, ids, gate, limit, 1.5)
+    assert np.array_equal(idx, ids)
+    assert abs(float(w.astype(np.float64).sum()) - 1.5) < 1e-5
+    got = oracle.moe_fp4(x, [experts[i] for i in idx], w, hidden, inter, limit)
+    assert (got != 0.0).all()                 # so adding +0.0 keeps every bit
+    assert common.bits_equal(got, out)
+
+
 def _moe_n_batch(rng, n_exp, nt, topk, hidden, inter):
     table = {int(e): common.fp4_expert(rng, hidden, inter)
              for e in rng.choice(1000, n_exp, replace=False)}

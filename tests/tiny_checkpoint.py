@@ -189,8 +189,11 @@ def write(out_dir, seed=4242, c=CFG):
         W.f32(p + ".hc_ffn_scale", 3, scale=0.1, add=1.0)
         W.bf16(p + ".ffn.gate.weight", c["n_experts"], d, scale=0.3)
         if L < c["num_hash_layers"]:
+            # topk DISTINCT experts per token, as hash routing gives them: the
+            # batched prefill relies on it (dsv4_layer.c:670-676, a token is
+            # routed to an expert at most once)
             W.i64(p + ".ffn.gate.tid2eid",
-                  rng.integers(0, c["n_experts"], (c["vocab"], c["topk"])))
+                  np.argsort(rng.random((c["vocab"], c["n_experts"])), axis=1)[:, :c["topk"]])
         else:
             W.f32(p + ".ffn.gate.bias", c["n_experts"], scale=0.5)
         for e in range(c["n_experts"]):

@@ -672,6 +672,10 @@ int main(int argc, char **argv)
     /* passes 4 and 5: the reference's batched prefill at chunks 1, 2, 3 and
      * all the tokens (test_model_oracle.c:303), each position's logits bit
      * for bit against the per-token GPU pass with the same device parts */
+    /* the per-token passes' device call counts, before the prefill passes
+     * add theirs */
+    const long n_score2 = g_n_score, n_topk2 = g_n_topk, n_attn2 = g_n_attn;
+    const long n_block3 = g_n_block, n_moe3 = g_n_moe;
     int pf_runs = 0, pf_same[2] = {0, 0}, pf_agree[2] = {0, 0}, pf_pos = 0;
     char pf_list[64] = "";
     {
@@ -725,15 +729,15 @@ int main(int argc, char **argv)
     }
     printf("summary: positions %d argmax_equal %d worst_rel %.3g gpu_mats %d "
            "fp4_mats %d gpu_score %ld gpu_topk %ld gpu_attn %ld bf16_mats %d "
-           "head_ok %ld/%ld\n", n, agree, worst, gpu_mats, fp4_mats, g_n_score, g_n_topk,
-           g_n_attn, bf16_mats, g_n_head_ok, g_n_head);
+           "head_ok %ld/%ld\n", n, agree, worst, gpu_mats, fp4_mats, n_score2, n_topk2,
+           n_attn2, bf16_mats, g_n_head_ok, g_n_head);
     printf("summary45: prefill chunks %s positions %d pass4_bit_identical %d "
            "pass4_argmax_equal %d pass5_bit_identical %d pass5_argmax_equal %d "
            "moe_n_calls %ld\n", pf_list, pf_pos, pf_same[0], pf_agree[0], pf_same[1],
            pf_agree[1], g_n_moe_n);
     if (!cpu_only) {
         printf("summary3: attention blocks on the device: steps %ld argmax_equal %d "
-               "worst_rel %.3g fused_moe %ld\n", g_n_block, agree3, worst3, g_n_moe);
+               "worst_rel %.3g fused_moe %ld\n", n_block3, agree3, worst3, n_moe3);
         dsv4_gpu_shutdown();
     }
     const int pf_ok = pf_same[0] == pf_pos && pf_agree[0] == pf_pos &&

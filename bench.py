@@ -64,6 +64,19 @@ def moe_bytes(hidden, inter, topk):
     return topk * per + hidden * 2 + hidden * 4 + topk * 8
 
 
+def rocprof_lm_head_us():
+    """The LM-head GEMV's average dispatch duration in the committed rocprof
+    summary (profiles/lm_head_kernel_trace.md, `bench.py --only lmhead`
+    under rocprofv3 --kernel-trace --stats), or None where it is absent."""
+    import re
+    try:
+        with open(os.path.join(ROOT, "profiles", "lm_head_kernel_trace.md")) as f:
+            m = re.search(r"^lm_head_avg_us: ([0-9.]+)", f.read(), re.M)
+    except OSError:
+        return None
+    return float(m.group(1)) if m else None
+
+
 def lm_head_traffic():
     """HBM bytes per LM-head GEMV launch (FETCH_SIZE + WRITE_SIZE, calibrated
     against a copy of known size), from the committed rocprofv3 summary; None
@@ -87,7 +100,8 @@ def parse():
     ap.add_argument("--no-detail", action="store_true",
                     help="headline sweep only (skip C1/C3/C4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "attn", "prefill", "moen", "copy"],
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "attn", "prefill", "moen", "copy",
+                                       "lmhead", "fit"],
                     default=None,
                     help="time one configuration only (for profiling runs); "
                          "'copy' runs a plain 1 GiB device-to-device copy whose "
@@ -350,6 +364,71 @@ class Bench:
         t.sort()
         self._keep_host = (Ws, ms)
         return t[len(t) // 2] * 1e6
+
+    def host_call_fit(self, reps=200):
+        """The per-call cost of the reference-compatible host-buffer call
+        dsv4_gpu_mmq (H2D of x, the GEMV, D2H of y, one synchronisation) over
+        the reference's own ten shapes (bench/gpu_call.c:60-70, E8M0 scales
+        120..134, weights resident), fitted as ms = fixed + MB / bandwidth
+        by least squares as bench/gpu_call.c:185-194 does. Two protocols:
+        warm, the reference's (one matrix called repeatedly, best of `reps`:
+        small matrices then sit in the 256 MB Infinity Cache), and cold
+        (distinct resident copies of the shape, >= 512 MiB of them, called
+        in rotation; median). Returns the record for `detail`."""
+        import ctypes
+        np = self.np
+        shapes = [(512, 512), (1024, 1024), (2048, 2048), (4096, 1024), (2048, 4096),
+                  (4096, 4096), (4096, 8192), (32768, 1024), (8192, 8192), (4096, 16384)]
+        rng = np.random.default_rng(20260825)
+        rows_out, keep = [], []
+        for rows, cols in shapes:
+            wb = rows * cols
+            sr, sc = (rows + 127) // 128, (cols + 127) // 128
+            copies = max(1, -(-(512 << 20) // wb))
+            W0 = self.common.fp8_codes(rng, (rows, cols))
+            S = (120 + rng.integers(0, 15, size=(sr, sc))).astype(np.uint8)
+            x = np.ascontiguousarray(rng.standard_normal(cols).astype(np.float32))
+            y = np.empty(rows, np.float32)
+            Ws = [W0] + [W0.copy() for _ in range(copies - 1)]
+            ms = [self.dsv4.qmat(W, S, self.dsv4.WFP8, rows, cols, 128, 128) for W in Ws]
+            for m in ms:
+                if self.L.dsv4_gpu_upload(ctypes.byref(m)) != 0:
+                    raise RuntimeError("upload failed at %dx%d" % (rows, cols))
+            keep.append((Ws, S, ms))
+            px, py = x.ctypes.data, y.ctypes.data
+            self.L.dsv4_gpu_mmq(py, px, ctypes.byref(ms[0]))
+            warm = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                self.L.dsv4_gpu_mmq(py, px, ctypes.byref(ms[0]))
+                warm.append(time.perf_counter() - t0)
+            n = max(reps, 2 * copies)
+            for i in range(copies):
+                self.L.dsv4_gpu_mmq(py, px, ctypes.byref(ms[i]))
+            cold = []
+            for i in range(n):
+                t0 = time.perf_counter()
+                self.L.dsv4_gpu_mmq(py, px, ctypes.byref(ms[i % copies]))
+                cold.append(time.perf_counter() - t0)
+            cold.sort()
+            rows_out.append({"shape": "%dx%d" % (rows, cols), "MB": round(wb / 1048576.0, 3),
+                             "warm_best_us": round(min(warm) * 1e6, 2),
+                             "cold_median_us": round(cold[len(cold) // 2] * 1e6, 2),
+                             "cold_copies": copies})
+
+        def fit(key):
+            xs = np.array([r["MB"] for r in rows_out])
+            ys = np.array([r[key] / 1e3 for r in rows_out])          # ms
+            slope, icept = np.polyfit(xs, ys, 1)
+            return {"fixed_us": round(float(icept) * 1e3, 2),
+                    "ms_per_MB": round(float(slope), 6),
+                    "marginal_GBps": round(1.048576 / float(slope), 1) if slope > 0 else None}
+        out = {"shapes": rows_out, "fit_warm_best": fit("warm_best_us"),
+               "fit_cold_median": fit("cold_median_us"),
+               "reference_published": "ms = 0.0308 + 0.01504 * MB: 31 us fixed, 69.7 GB/s "
+                                      "(RTX 5060 Laptop, README.md:460-476)"}
+        self._keep_fit = keep        # resident until shutdown: keys are host pointers
+        return out
 
     # ------------------------------------------------- BF16 LM head
     def bf16_head_run(self, steps, warmup):
@@ -896,7 +975,22 @@ def main():
                "per_shape_us": [round(u, 3) for u in per_us]}))
         B.L.dsv4_gpu_shutdown()
         return
+    if args.only == "lmhead":
+        B.c2_setup()
+        us, copies, n = B.c2_shape_run(len(B.c2) - 1)
+        a = fp8_bytes(*LM_HEAD)
+        emit({"config": "lm_head_fp8_129280x7168", "us": round(us, 3), "copies": copies,
+              "launches": n, "GBps": round(a / us / 1e3, 1),
+              "frac": round(a / us / 1e3 / PEAK_GBS, 4)})
+        B.L.dsv4_gpu_shutdown()
+        return
+    if args.only == "fit":
+        emit({"config": "host_call_fit", **B.host_call_fit()})
+        B.L.dsv4_gpu_shutdown()
+        return
     if args.only == "prefill":
+        # the batched matrix-core form unless the caller chose otherwise
+        os.environ.setdefault("DSV4_GPU_FP8_MX", "1")
         curve = {}
         for nt in (1, 2, 4, 8, 16, 32, 64):
             us, gf = B.gemv_n_run(nt=nt, calls=20 if nt < 64 else 30)
@@ -937,6 +1031,7 @@ def main():
     lm_ms = per_us[5] / 1e3
     lm_gbs = algs[5] / (lm_ms * 1e-3) / 1e9
     traffic = lm_head_traffic()
+    rp_us = rocprof_lm_head_us()
     detail = {}
 
     def rec(us, eager, alg):
@@ -956,28 +1051,41 @@ def main():
         detail["c4_sparse_mla_step_32768_top2048"] = rec(*B.c4_run(args.steps, args.warmup))
         log("bench: BF16 LM head")
         detail["lm_head_bf16_129280x7168"] = rec(*B.bf16_head_run(args.steps, args.warmup))
-        log("bench: E8M0 shapes (matrix-core form)")
-        detail["c2_e8m0_per_shape"] = {}
-        for k, ((r, c), a) in enumerate(zip(shapes, algs)):
-            us, copies, n = B.c2_shape_run(k, sfmt=0)
-            detail["c2_e8m0_per_shape"]["%dx%d" % (r, c)] = {
-                "us": round(us, 3), "GBps": round(a / us / 1e3, 1),
-                "frac": round(a / us / 1e3 / PEAK_GBS, 4)}
-        log("bench: batched prefill GEMV")
-        curve = {}
-        for nt in (1, 2, 4, 8, 16, 32, 64):
-            us, gf = B.gemv_n_run(nt=nt, calls=20 if nt < 64 else 30)
-            curve[str(nt)] = {"us": round(us, 3), "TFLOPs": round(gf / us * 1e3, 2)}
-        us, gf = curve["64"]["us"], 2.0 * 7168 * 7168 * 64 / 1e9
-        detail["prefill_fp8_7168x7168_nt64"] = {
-            "us": us, "TFLOPs": round(gf / us * 1e3, 2),
-            "frac_bf16_peak": round(gf / us * 1e3 / 2500.0, 4),
-            "us_per_token": round(us / 64, 3), "scales": "E8M0 (matrix-core form)",
-            "by_tokens": curve}
+        for form, key in (("0", "c2_e8m0_per_shape"), ("1", "c2_e8m0_per_shape_matrix_core")):
+            log("bench: E8M0 shapes (DSV4_GPU_FP8_MX=%s)" % form)
+            os.environ["DSV4_GPU_FP8_MX"] = form
+            detail[key] = {"form": "VALU (default)" if form == "0" else
+                           "matrix core (DSV4_GPU_FP8_MX=1)"}
+            for k, ((r, c), a) in enumerate(zip(shapes, algs)):
+                us, copies, n = B.c2_shape_run(k, sfmt=0)
+                detail[key]["%dx%d" % (r, c)] = {
+                    "us": round(us, 3), "GBps": round(a / us / 1e3, 1),
+                    "frac": round(a / us / 1e3 / PEAK_GBS, 4)}
+        os.environ.pop("DSV4_GPU_FP8_MX", None)
+        gf64 = 2.0 * 7168 * 7168 * 64 / 1e9
+        for form, key in (("1", "prefill_fp8_7168x7168_nt64"),
+                          ("0", "prefill_fp8_7168x7168_nt64_default_form")):
+            log("bench: batched prefill GEMV (DSV4_GPU_FP8_MX=%s)" % form)
+            os.environ["DSV4_GPU_FP8_MX"] = form
+            curve = {}
+            for nt in (1, 2, 4, 8, 16, 32, 64):
+                us, gf = B.gemv_n_run(nt=nt, calls=20 if nt < 64 else 30)
+                curve[str(nt)] = {"us": round(us, 3), "TFLOPs": round(gf / us * 1e3, 2)}
+            us = curve["64"]["us"]
+            detail[key] = {
+                "us": us, "TFLOPs": round(gf64 / us * 1e3, 2),
+                "frac_bf16_peak": round(gf64 / us * 1e3 / 2500.0, 4),
+                "us_per_token": round(us / 64, 3),
+                "scales": "E8M0, " + ("matrix-core form (DSV4_GPU_FP8_MX=1)" if form == "1"
+                                      else "VALU form (the default)"),
+                "by_tokens": curve}
+        os.environ.pop("DSV4_GPU_FP8_MX", None)
         us32, _ = B.gemv_n_run(nt=64, sfmt=1)
         detail["prefill_fp8_7168x7168_nt64_f32_scales"] = {
-            "us": round(us32, 3), "TFLOPs": round(gf / us32 * 1e3, 2),
-            "frac_fp32_peak": round(gf / us32 * 1e3 / 157.3, 4), "scales": "fp32 (VALU form)"}
+            "us": round(us32, 3), "TFLOPs": round(gf64 / us32 * 1e3, 2),
+            "frac_fp32_peak": round(gf64 / us32 * 1e3 / 157.3, 4), "scales": "fp32 (VALU form)"}
+        log("bench: host-buffer call cost fit (dsv4_gpu_mmq, 10 shapes)")
+        detail["host_call_fit"] = B.host_call_fit()
         for ratio, name in ((4, "attn_block_flash_csa_ratio4"), (128, "attn_block_flash_hca_ratio128")):
             log("bench: attention block, ratio %d" % ratio)
             detail[name] = rec(*B.attn_run(32, 4, ratio=ratio))
@@ -1019,7 +1127,11 @@ def main():
                      "traffic": traffic,
                      "kernel": "k_fp8_gemv (LM head 129280x7168)",
                      "algorithmic_bytes_per_launch": algs[5],
-                     "avg_launch_us": round(lm_ms * 1e3, 3)},
+                     "avg_launch_us": round(lm_ms * 1e3, 3),
+                     "rocprof_summary": "profiles/lm_head_kernel_trace.md",
+                     "rocprof_avg_us": rp_us,
+                     "frac_from_rocprof_avg": (round(algs[5] / rp_us / 1e3 / PEAK_GBS, 4)
+                                               if rp_us else None)},
         "cpu_baseline": cpu,
         "detail": detail,
     }

@@ -789,14 +789,35 @@ bool blocking_ok(int blk_r, int blk_c)
 }
 
 /* Which arithmetic a matrix gets, by its format and shape alone (never by the
- * batch size, so the single-token and batched calls agree bit for bit):
- * E8M0-scaled matrices the kernels can stream take the matrix-core form
- * (dsv4_fp8_mx.hip), the rest the VALU form of this file.
- * DSV4_GPU_FP8_MX=0 keeps every matrix on the VALU form. */
-bool mx_form(int sfmt, const float *x, const uint8_t *W, int cols, int blk_r, int blk_c)
+ * batch size or by where x lies, so the single-token and batched calls agree
+ * bit for bit):
+ *   - by default every matrix takes the VALU form of this file, the faster
+ *     one at batch 1 on every shape measured (E8M0, cold, us, VALU against
+ *     matrix core: 576x7168 4.41 / 8.07, 1536x7168 6.04 / 8.44, 24576x1536
+ *     10.03 / 11.27, 7168x7168 11.90 / 12.92, 7168x16384 21.58 / 23.85, LM
+ *     head 140.4 / 142.2, 2048x4096 4.77 / 6.68, 4096x2048 5.05 / 6.40);
+ *   - DSV4_GPU_FP8_MX=1 sends E8M0-scaled matrices the matrix-core form
+ *     (dsv4_fp8_mx.hip), single token and batched alike: slower at batch 1,
+ *     much faster batched (7168x7168 at 64 tokens 63.9 against 335.2 us),
+ *     for prefill-heavy work;
+ *   - shapes neither chunked kernel takes run the generic kernel.
+ * The chunked forms need x and W 16-byte aligned; a call that breaks that
+ * is refused rather than sent to another arithmetic (chunked_ok). */
+bool mx_form(int sfmt, int cols, int blk_r, int blk_c)
 {
-    return env_int("DSV4_GPU_FP8_MX", 1) != 0 && dsv4_fp8_mx_ok(sfmt, cols, blk_r, blk_c) &&
-           (((uintptr_t)x | (uintptr_t)W) & 15) == 0;
+    return env_int("DSV4_GPU_FP8_MX", 0) != 0 && dsv4_fp8_mx_ok(sfmt, cols, blk_r, blk_c);
+}
+
+/* x and W of a chunked-form call are 16-byte aligned; else -1 with a
+ * message (the host-buffer entry points stage x aligned, and the
+ * residency keeps W as allocated, so only a caller's device pointer can
+ * break this). */
+int chunked_ok(const float *x, const uint8_t *W, const char *what)
+{
+    if ((((uintptr_t)x | (uintptr_t)W) & 15) == 0) return 0;
+    DSV4_ERR("%s: x (%p) and W (%p) must be 16-byte aligned", what, (const void *)x,
+             (const void *)W);
+    return -1;
 }
 
 /* The VALU form's launch parameters for a matrix of rows x cols: R rows per
@@ -833,8 +854,8 @@ int fp8_gemv(float *y, const float *x, const uint8_t *W, const void *S, int sfmt
     }
     const int sc = (cols + blk_c - 1) / blk_c;
     Fp8Geom g;
-    const bool aligned = (((uintptr_t)x | (uintptr_t)W) & 15) == 0;
-    if (!gp.valu && mx_form(sfmt, x, W, cols, blk_r, blk_c)) {
+    if (!gp.valu && mx_form(sfmt, cols, blk_r, blk_c)) {
+        if (chunked_ok(x, W, "fp8 gemv") != 0) return -1;
         Dsv4Fp8Mx a;
         a.y = y; a.x = x; a.w = W; a.s = (const uint8_t *)S;
         a.rows = rows; a.cols = cols; a.sc = sc; a.blk_r = blk_r; a.blk_c = blk_c;
@@ -847,7 +868,8 @@ int fp8_gemv(float *y, const float *x, const uint8_t *W, const void *S, int sfmt
         }
         return dsv4_fp8_mx_launch(a, st);
     }
-    if (aligned && fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c)) {
+    if (fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c)) {
+        if (chunked_ok(x, W, "fp8 gemv") != 0) return -1;
         /* launch shape (fp8_valu): none of it changes a row's arithmetic */
         const Fp8Valu v = fp8_valu(rows, cols, blk_r);
         const int R = v.R, pf = v.pf, wpc = v.wpc;
@@ -1012,13 +1034,15 @@ int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,
     }
     if (nt == 1)                       /* the GEMV itself: same bits, its launch shape */
         return fp8_gemv(y, x, W, S, sfmt, rows, cols, blk_r, blk_c, Fp8Groups{}, st);
-    if (mx_form(sfmt, x, W, cols, blk_r, blk_c))
+    if (mx_form(sfmt, cols, blk_r, blk_c)) {
+        if (chunked_ok(x, W, "fp8 gemv_n") != 0) return -1;
         return dsv4_fp8_mxn_launch(y, x, W, (const uint8_t *)S, rows, cols, blk_r, blk_c, nt,
                                    st, xscratch);
+    }
     const int sc = (cols + blk_c - 1) / blk_c;
     Fp8Geom g;
-    const bool aligned = (((uintptr_t)x | (uintptr_t)W) & 15) == 0;
-    if (aligned && fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c)) {
+    if (fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c)) {
+        if (chunked_ok(x, W, "fp8 gemv_n") != 0) return -1;
         if (sfmt == 0)
             launch_gemv_n<0>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st);
         else

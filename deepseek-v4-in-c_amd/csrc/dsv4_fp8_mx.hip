@@ -854,12 +854,20 @@ bool xs_uniform(int blk_r, int blk_c)
     return blk_r % 16 == 0 && blk_c % 64 == 0;
 }
 
+/* Opt a kernel in to the device's whole LDS for its dynamic allocation;
+ * false (with a message) when the runtime refuses, so that no launch asks
+ * for more than the kernel was granted. */
 template <typename K>
-void optin(K kernel)
+bool optin(K kernel, const char *name)
 {
-    (void)hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)dsv4_lds_limit());
+    const hipError_t e = hipFuncSetAttribute((const void *)kernel,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)dsv4_lds_limit());
+    if (e == hipSuccess) return true;
     (void)hipGetLastError();
+    DSV4_ERR("%s: dynamic LDS opt-in to %zu bytes refused: %s", name, dsv4_lds_limit(),
+             hipGetErrorString(e));
+    return false;
 }
 
 int mx_cu_count()
@@ -975,8 +983,15 @@ int dsv4_fp8_mx_launch(const Dsv4Fp8Mx &a, hipStream_t st)
         return -1;
     }
     b.bc_m = bc_magic(a.blk_c);
-    static bool opted = false;
-    if (!opted) { optin(k_fp8_mx1<false>); optin(k_fp8_mx1<true>); opted = true; }
+    /* once per process: 1 granted, -1 refused (launches past 64 KiB of
+     * LDS then fail here instead of reaching the runtime) */
+    static int opted = 0;
+    if (!opted)
+        opted = optin(k_fp8_mx1<false>, "fp8 mx") && optin(k_fp8_mx1<true>, "fp8 mx") ? 1 : -1;
+    if (opted < 0 && b.lds > 64 * 1024) {
+        DSV4_ERR("fp8 mx: %zu bytes of LDS without the opt-in", b.lds);
+        return -1;
+    }
     const dim3 grid(b.gx, a.n), block(64 * b.wpt * b.tpw);
     if (xs_uniform(a.blk_r, a.blk_c))
         hipLaunchKernelGGL(k_fp8_mx1<true>, grid, block, b.lds, st, b);
@@ -1022,15 +1037,22 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
     const int mw = (groups >= 3 && NTc == 4) ? 8 : 4;
     const size_t lds = 2 * (size_t)tpg * XNT * BP * 2 + (size_t)mw * XUNIT_B;
     const dim3 grid((rows + 16 * mw - 1) / (16 * mw), groups);
-    static bool opted = false;
+    static int opted = 0;                          /* 1 granted, -1 refused */
     if (!opted) {
-        optin(k_fp8_mxn<1, false, 4>); optin(k_fp8_mxn<2, false, 4>); optin(k_fp8_mxn<3, false, 4>);
-        optin(k_fp8_mxn<4, false, 4>); optin(k_fp8_mxn<5, false, 4>); optin(k_fp8_mxn<6, false, 4>);
-        optin(k_fp8_mxn<7, false, 4>); optin(k_fp8_mxn<1, true, 4>); optin(k_fp8_mxn<2, true, 4>);
-        optin(k_fp8_mxn<3, true, 4>); optin(k_fp8_mxn<4, true, 4>); optin(k_fp8_mxn<5, true, 4>);
-        optin(k_fp8_mxn<6, true, 4>); optin(k_fp8_mxn<7, true, 4>);
-        optin(k_fp8_mxn<4, false, 8>); optin(k_fp8_mxn<4, true, 8>);
-        opted = true;
+        const char *nm = "fp8 mxn";
+        bool ok = optin(k_fp8_mxn<1, false, 4>, nm) && optin(k_fp8_mxn<2, false, 4>, nm) &&
+                  optin(k_fp8_mxn<3, false, 4>, nm) && optin(k_fp8_mxn<4, false, 4>, nm) &&
+                  optin(k_fp8_mxn<5, false, 4>, nm) && optin(k_fp8_mxn<6, false, 4>, nm) &&
+                  optin(k_fp8_mxn<7, false, 4>, nm) && optin(k_fp8_mxn<1, true, 4>, nm) &&
+                  optin(k_fp8_mxn<2, true, 4>, nm) && optin(k_fp8_mxn<3, true, 4>, nm) &&
+                  optin(k_fp8_mxn<4, true, 4>, nm) && optin(k_fp8_mxn<5, true, 4>, nm) &&
+                  optin(k_fp8_mxn<6, true, 4>, nm) && optin(k_fp8_mxn<7, true, 4>, nm) &&
+                  optin(k_fp8_mxn<4, false, 8>, nm) && optin(k_fp8_mxn<4, true, 8>, nm);
+        opted = ok ? 1 : -1;
+    }
+    if (opted < 0 && lds > 64 * 1024) {
+        DSV4_ERR("fp8 mxn: %zu bytes of LDS without the opt-in", lds);
+        return -1;
     }
     const bool uni = xs_uniform(blk_r, blk_c);
     const int cpad = ((cols + XU - 1) / XU) * XU;
@@ -1067,13 +1089,19 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
         const int spw = (nseg + kp - 1) / kp, tt = 4 / kp;
         const size_t lds_k = mxk_lds(kp);
         if (lds_k <= dsv4_lds_limit()) {
-            static bool opted_k = false;
+            static int opted_k = 0;                /* 1 granted, -1 refused */
             if (!opted_k) {
-                optin(k_fp8_mxk<false, 2, false>); optin(k_fp8_mxk<true, 2, false>);
-                optin(k_fp8_mxk<false, 4, false>); optin(k_fp8_mxk<true, 4, false>);
-                optin(k_fp8_mxk<false, 2, true>); optin(k_fp8_mxk<true, 2, true>);
-                optin(k_fp8_mxk<false, 4, true>); optin(k_fp8_mxk<true, 4, true>);
-                opted_k = true;
+                const char *nm = "fp8 mxk";
+                const bool ok =
+                    optin(k_fp8_mxk<false, 2, false>, nm) && optin(k_fp8_mxk<true, 2, false>, nm) &&
+                    optin(k_fp8_mxk<false, 4, false>, nm) && optin(k_fp8_mxk<true, 4, false>, nm) &&
+                    optin(k_fp8_mxk<false, 2, true>, nm) && optin(k_fp8_mxk<true, 2, true>, nm) &&
+                    optin(k_fp8_mxk<false, 4, true>, nm) && optin(k_fp8_mxk<true, 4, true>, nm);
+                opted_k = ok ? 1 : -1;
+            }
+            if (opted_k < 0 && lds_k > 64 * 1024) {
+                DSV4_ERR("fp8 mxk: %zu bytes of LDS without the opt-in", lds_k);
+                return -1;
             }
             if (!xf) HIP_OK(xsplit(), "fp8 mxn x split launch");
             const dim3 gk(((rows + 15) / 16 + tt - 1) / tt, groups);

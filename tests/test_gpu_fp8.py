@@ -118,8 +118,8 @@ def test_c1_4096(gpu, dsv4):
 @pytest.mark.parametrize("rows,cols", [(1536, 7168), (576, 7168), (24576, 1536),
                                        (7168, 16384), (7168, 7168)])
 def test_c2_trunk_shapes(gpu, dsv4, rows, cols, scales):
-    """fp32 block scales (the configuration's, VALU form) and E8M0 ones (the
-    reference's, matrix-core form)."""
+    """fp32 block scales (the configuration's) and E8M0 ones (the
+    reference's), both on the default VALU form."""
     check_shape(dsv4, rows, cols, 0, f32s=scales == "f32")
 
 
@@ -187,19 +187,23 @@ def test_reference_gpu_gate(gpu, dsv4):
     assert common.bits_equal(dsv4.mmq_n(m, xn[:1])[0], dsv4.mmq(m, xn[0]))
 
 
+@pytest.mark.parametrize("form", ["0", "1"])
 @pytest.mark.parametrize("rows,cols,nt", [(300, 1536, 5), (129, 7168, 64), (40, 64, 3),
                                           (500, 2048, 13), (70, 16384, 2), (33, 4096, 9),
                                           (7168, 7168, 64), (77, 1040, 21), (16, 112, 6),
                                           (1000, 7168, 11), (257, 2096, 20), (64, 16, 4),
                                           (200, 4096, 33), (18, 3072, 7), (300, 1536, 48)])
-def test_batched_bit_identical(gpu, dsv4, rows, cols, nt):
-    """E8M0 scales: the matrix-core form, whose batched kernel runs the
-    single-token chain per (row, token) -- every token's row equals the
-    single-token GEMV's bits, whatever column of which tile it takes (up to
-    64 tokens, ragged row tiles, columns not a multiple of the 256-byte unit
-    or of the 1024-column segment; nt 48 and 64 take the 8-wave workgroups,
-    nt 48 with a ragged last token group); cols not a multiple of 16 take the
-    VALU form, whose batched kernel keeps its bits the same way."""
+def test_batched_bit_identical(gpu, dsv4, monkeypatch, rows, cols, nt, form):
+    """E8M0 scales on both forms. The default VALU form's batched kernel runs
+    the GEMV's chunk dots, scale FMAs and reduction tree per (row, token).
+    The matrix-core form (DSV4_GPU_FP8_MX=1) runs the single-token chain per
+    (row, token), whatever column of which tile a token takes (up to 64
+    tokens, ragged row tiles, columns not a multiple of the 256-byte unit or
+    of the 1024-column segment; nt 48 and 64 take the 8-wave workgroups, nt
+    48 with a ragged last token group); cols not a multiple of 16 take the
+    generic kernel either way. Every token's row equals the single-token
+    GEMV's bits."""
+    monkeypatch.setenv("DSV4_GPU_FP8_MX", form)
     W, Sf, Se, _ = common.fp8_problem(21, rows, cols)
     x = np.random.default_rng(22).standard_normal((nt, cols), dtype=np.float32)
     y1, m = _run(dsv4, W, Se, x[0])
@@ -214,6 +218,7 @@ def test_batched_token_tiles_keep_bits(gpu, dsv4, monkeypatch, ntmax):
     """DSV4_GPU_MXN_NT (column tiles of five tokens per workgroup, so how many
     passes over the weights a batch takes) only reshapes the batched launch:
     every setting gives each token the single-token GEMV's bits."""
+    monkeypatch.setenv("DSV4_GPU_FP8_MX", "1")
     monkeypatch.setenv("DSV4_GPU_MXN_NT", ntmax)
     for rows, cols, nt in ((300, 1536, 64), (129, 7168, 37), (70, 2096, 11)):
         W, Sf, Se, _ = common.fp8_problem(23, rows, cols)
@@ -236,6 +241,7 @@ def test_batched_segment_split_keeps_bits(gpu, dsv4, monkeypatch, kp, xf):
     bits: uniform and per-lane scales, ragged row tiles and segments, a last
     unit past the row's end, fewer segments than waves (taken by the one-wave
     form), one to four groups."""
+    monkeypatch.setenv("DSV4_GPU_FP8_MX", "1")
     monkeypatch.setenv("DSV4_GPU_MXK", kp)
     monkeypatch.setenv("DSV4_GPU_MXKF", xf)
     cases = ((300, 1536, 2, 128, 128), (129, 7168, 5, 128, 128), (70, 2096, 4, 1, 32),
@@ -256,10 +262,13 @@ def test_batched_segment_split_keeps_bits(gpu, dsv4, monkeypatch, kp, xf):
         assert common.vec_rel_err(yn, oracle.matmul_fp8(x, W, S, blk_r, blk_c)) < TOL
 
 
+@pytest.mark.parametrize("form", ["0", "1"])
 @pytest.mark.parametrize("blk_r,blk_c", [(1, 32), (16, 64), (128, 128), (4, 48), (256, 256)])
-def test_matrix_core_form_blockings(gpu, dsv4, blk_r, blk_c):
+def test_matrix_core_form_blockings(gpu, dsv4, monkeypatch, blk_r, blk_c, form):
     """E8M0 scale grids other than 128 x 128 (a scale per lane piece in the
-    matrix-core form): against the oracle, and batched bit-identical."""
+    matrix-core form, DSV4_GPU_FP8_MX=1; the default VALU form too): against
+    the oracle, and batched bit-identical."""
+    monkeypatch.setenv("DSV4_GPU_FP8_MX", form)
     rows, cols, nt = 300, 1536, 7
     rng = np.random.default_rng(blk_r * 1000 + blk_c)
     W = common.fp8_codes(rng, (rows, cols))
@@ -275,9 +284,9 @@ def test_matrix_core_form_blockings(gpu, dsv4, blk_r, blk_c):
 
 @pytest.mark.parametrize("form", ["1", "0"])
 def test_e8m0_forms(gpu, dsv4, monkeypatch, form):
-    """DSV4_GPU_FP8_MX=1 (the default: matrix core for E8M0 scales) and =0
-    (the VALU form for every matrix): each within the bar, each with its own
-    batched kernel bit-identical per token."""
+    """DSV4_GPU_FP8_MX=1 (the matrix core for E8M0 scales) and =0 (the
+    default VALU form for every matrix): each within the bar, each with its
+    own batched kernel bit-identical per token."""
     monkeypatch.setenv("DSV4_GPU_FP8_MX", form)
     rows, cols, nt = 1000, 7168, 6
     W, Sf, Se, _ = common.fp8_problem(71, rows, cols)
@@ -360,10 +369,13 @@ def test_device_entry_point_matches_host_path(gpu, dsv4):
     assert common.bits_equal(dy.cpu().numpy(), y_host)
 
 
-def test_batched_device_entry_point(gpu, dsv4):
+@pytest.mark.parametrize("form", ["0", "1"])
+def test_batched_device_entry_point(gpu, dsv4, monkeypatch, form):
     """dsv4_gpu_fp8_gemv_n_d: every token's row equals dsv4_gpu_fp8_gemv_d on
-    that token, bit for bit (the k_mmq_fp8_n contract), on device buffers."""
+    that token, bit for bit (the k_mmq_fp8_n contract), on device buffers,
+    on both forms."""
     import torch
+    monkeypatch.setenv("DSV4_GPU_FP8_MX", form)
     rows, cols, nt = 1000, 7168, 11
     W, Sf, Se, _ = common.fp8_problem(61, rows, cols)
     x = np.random.default_rng(62).standard_normal((nt, cols), dtype=np.float32)
@@ -385,6 +397,36 @@ def test_batched_device_entry_point(gpu, dsv4):
     assert common.vec_rel_err(yn, oracle.matmul_fp8(x, W, Se)) < TOL
     assert L.dsv4_gpu_fp8_gemv_n_d(dy.data_ptr(), dx.data_ptr(), dW.data_ptr(), dS.data_ptr(),
                                    0, rows, cols, 65, st) == -1     # above DSV4_MAX_BATCH
+
+
+@pytest.mark.parametrize("form", ["0", "1"])
+def test_unaligned_device_operands_refused(gpu, dsv4, monkeypatch, form):
+    """The arithmetic follows from the matrix alone: a device-buffer call
+    whose x (or W) breaks the 16-byte alignment of the chunked forms is
+    refused (-1) rather than sent to another kernel with other bits; the
+    aligned call on the same values is unaffected."""
+    import torch
+    monkeypatch.setenv("DSV4_GPU_FP8_MX", form)
+    rows, cols, nt = 256, 2048, 3
+    W, Sf, Se, _ = common.fp8_problem(63, rows, cols)
+    x = np.random.default_rng(64).standard_normal((nt, cols), dtype=np.float32)
+    dev = torch.device("cuda:0")
+    dW, dS = torch.from_numpy(W).to(dev), torch.from_numpy(Se).to(dev)
+    xb = torch.zeros(nt * cols + 4, dtype=torch.float32, device=dev)
+    xb[1:1 + nt * cols] = torch.from_numpy(x.reshape(-1)).to(dev)
+    dy = torch.empty((nt, rows), dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    L = dsv4.lib()
+    odd = xb.data_ptr() + 4                              # 4 bytes past 16-byte alignment
+    assert L.dsv4_gpu_fp8_gemv_d(dy.data_ptr(), odd, dW.data_ptr(), dS.data_ptr(), 0,
+                                 rows, cols, st) == -1
+    assert L.dsv4_gpu_fp8_gemv_n_d(dy.data_ptr(), odd, dW.data_ptr(), dS.data_ptr(), 0,
+                                   rows, cols, nt, st) == -1
+    dx = torch.from_numpy(x).to(dev)
+    assert L.dsv4_gpu_fp8_gemv_n_d(dy.data_ptr(), dx.data_ptr(), dW.data_ptr(),
+                                   dS.data_ptr(), 0, rows, cols, nt, st) == 0
+    torch.cuda.synchronize()
+    assert common.vec_rel_err(dy.cpu().numpy(), oracle.matmul_fp8(x, W, Se)) < TOL
 
 
 def test_upload_refusals(gpu, dsv4):

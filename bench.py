@@ -101,7 +101,7 @@ def parse():
                     help="headline sweep only (skip C1/C3/C4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "attn", "prefill", "moen", "copy",
-                                       "lmhead", "fit"],
+                                       "lmhead", "fit", "ckpt"],
                     default=None,
                     help="time one configuration only (for profiling runs); "
                          "'copy' runs a plain 1 GiB device-to-device copy whose "
@@ -429,6 +429,67 @@ class Bench:
                                       "(RTX 5060 Laptop, README.md:460-476)"}
         self._keep_fit = keep        # resident until shutdown: keys are host pointers
         return out
+
+    def ckpt_load_run(self, gib=8, path=None):
+        """The checkpoint loader (dsv4_gpu_ckpt_open / _load_qmat: pread into
+        pinned staging, one persistent reader thread, copies to HBM) on one
+        large synthetic safetensors shard: `gib` GiB of FP8 matrices of
+        8192 x 16384 (128 MiB each) with E8M0 scales, written to a file
+        first. The file was just written, so it is read from the host page
+        cache: this measures the loader's host-to-HBM path, not the storage
+        device. Returns the record for `detail`."""
+        import ctypes
+        import json as _json
+        import struct
+        import tempfile
+        np = self.np
+        rows, cols = 8192, 16384
+        n = max(1, int(gib * 1024 // 128))
+        sb = (rows // 128) * (cols // 128)
+        d = tempfile.mkdtemp(prefix="dsv4_ckpt_", dir=path)
+        f = os.path.join(d, "model-00001-of-00001.safetensors")
+        hdr, off = {}, 0
+        for i in range(n):
+            hdr["m%d.weight" % i] = {"dtype": "F8_E4M3", "shape": [rows, cols],
+                                     "data_offsets": [off, off + rows * cols]}
+            off += rows * cols
+            hdr["m%d.scale" % i] = {"dtype": "F8_E8M0", "shape": [rows // 128, cols // 128],
+                                    "data_offsets": [off, off + sb]}
+            off += sb
+        j = _json.dumps(hdr, separators=(",", ":")).encode()
+        j += b" " * ((-(8 + len(j))) % 8)
+        rng = np.random.default_rng(3)
+        blob = rng.integers(0, 126, rows * cols, dtype=np.uint8).tobytes()
+        sc = np.full(sb, 127, np.uint8).tobytes()
+        t0 = time.perf_counter()
+        with open(f, "wb") as fh:
+            fh.write(struct.pack("<Q", len(j)))
+            fh.write(j)
+            for i in range(n):
+                fh.write(blob)
+                fh.write(sc)
+        write_s = time.perf_counter() - t0
+        L = self.L
+        L.dsv4_gpu_ckpt_open.restype = ctypes.c_void_p
+        t0 = time.perf_counter()
+        ck = L.dsv4_gpu_ckpt_open(f.rsplit("/", 1)[0].encode())
+        ms = []
+        for i in range(n):
+            m = self.dsv4.DSV4QMat()
+            if L.dsv4_gpu_ckpt_load_qmat(ctypes.c_void_p(ck), ("m%d" % i).encode(),
+                                         self.dsv4.WFP8, rows, cols, ctypes.byref(m)) != 0:
+                raise RuntimeError("ckpt load failed at m%d" % i)
+            ms.append(m)
+        wall = time.perf_counter() - t0
+        st = self.dsv4.CkptStats()
+        L.dsv4_gpu_ckpt_stats_get(ctypes.c_void_p(ck), ctypes.byref(st))
+        L.dsv4_gpu_ckpt_close(ctypes.c_void_p(ck))
+        os.unlink(f)
+        os.rmdir(d)
+        return {"matrices": n, "bytes": int(st.bytes), "file_write_s": round(write_s, 3),
+                "load_wall_s": round(wall, 3), "load_GBps_wall": round(st.bytes / wall / 1e9, 2),
+                "load_GBps_loader": round(st.bytes / st.seconds / 1e9, 2) if st.seconds else None,
+                "source": "host page cache (the shard was just written)"}
 
     # ------------------------------------------------- BF16 LM head
     def bf16_head_run(self, steps, warmup):
@@ -982,6 +1043,10 @@ def main():
         emit({"config": "lm_head_fp8_129280x7168", "us": round(us, 3), "copies": copies,
               "launches": n, "GBps": round(a / us / 1e3, 1),
               "frac": round(a / us / 1e3 / PEAK_GBS, 4)})
+        B.L.dsv4_gpu_shutdown()
+        return
+    if args.only == "ckpt":
+        emit({"config": "ckpt_load", **B.ckpt_load_run()})
         B.L.dsv4_gpu_shutdown()
         return
     if args.only == "fit":

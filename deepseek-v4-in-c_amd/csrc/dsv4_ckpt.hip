@@ -173,6 +173,13 @@ struct dsv4_gpu_ckpt {
     bool pending[NSTAGE] = {};
     int next = 0;
     dsv4_gpu_ckpt_stats st{};
+    /* One reader thread for the handle's life: stream_in hands it one chunk
+     * at a time (job) and waits until it has taken it back to nullptr. */
+    pthread_t reader{};
+    bool reader_on = false, quit = false;
+    pthread_mutex_t mu = PTHREAD_MUTEX_INITIALIZER;
+    pthread_cond_t cv = PTHREAD_COND_INITIALIZER;
+    void *job = nullptr;
 };
 
 namespace {
@@ -310,19 +317,53 @@ void *read_job(void *a)
     return nullptr;
 }
 
+/* The reader thread: reads each job handed over, then clears the slot. */
+void *reader_main(void *a)
+{
+    dsv4_gpu_ckpt *c = (dsv4_gpu_ckpt *)a;
+    pthread_mutex_lock(&c->mu);
+    for (;;) {
+        while (!c->job && !c->quit) pthread_cond_wait(&c->cv, &c->mu);
+        if (!c->job) break;                             /* quit, nothing pending */
+        ReadJob *j = (ReadJob *)c->job;
+        pthread_mutex_unlock(&c->mu);
+        read_job(j);
+        pthread_mutex_lock(&c->mu);
+        c->job = nullptr;
+        pthread_cond_broadcast(&c->cv);
+    }
+    pthread_mutex_unlock(&c->mu);
+    return nullptr;
+}
+
+void reader_submit(dsv4_gpu_ckpt *c, ReadJob *j)
+{
+    pthread_mutex_lock(&c->mu);
+    c->job = j;
+    pthread_cond_broadcast(&c->cv);
+    pthread_mutex_unlock(&c->mu);
+}
+
+void reader_wait(dsv4_gpu_ckpt *c)
+{
+    pthread_mutex_lock(&c->mu);
+    while (c->job) pthread_cond_wait(&c->cv, &c->mu);
+    pthread_mutex_unlock(&c->mu);
+}
+
 /* Copy `len` bytes of shard `fd` from file offset `off` to device address
- * dst: chunks through the staging ring, the read of chunk i + 1 overlapping
- * the copy of chunk i. Stream-ordered on the loader's copy stream. */
+ * dst: chunks through the staging ring, the reader thread's read of chunk
+ * i + 1 overlapping the copy of chunk i (without a reader thread every read
+ * is inline). Stream-ordered on the loader's copy stream. */
 int stream_in(dsv4_gpu_ckpt *c, int fd, int64_t off, int64_t len, uint8_t *dst)
 {
-    pthread_t th;
     ReadJob job{}, nxt{};
     bool running = false;
     int64_t done = 0;
     int b = -1;
     while (done < len || running) {
         if (running) {                                  /* the chunk in flight */
-            pthread_join(th, nullptr);
+            reader_wait(c);
             running = false;
             if (job.err) { DSV4_ERR("ckpt: read failed at offset %lld", (long long)job.off); return -1; }
             HIP_OK(hipMemcpyAsync(dst + (job.off - off), job.buf, (size_t)job.len,
@@ -342,15 +383,16 @@ int stream_in(dsv4_gpu_ckpt *c, int fd, int64_t off, int64_t len, uint8_t *dst)
             nxt.off = off + done;
             nxt.len = std::min<int64_t>((int64_t)STAGE_BYTES, len - done);
             job = nxt;
-            if (pthread_create(&th, nullptr, read_job, &job) != 0) {
+            if (c->reader_on) {
+                reader_submit(c, &job);
+                running = true;
+            } else {
                 read_job(&job);                         /* no thread: read inline */
                 if (job.err) { DSV4_ERR("ckpt: read failed"); return -1; }
                 HIP_OK(hipMemcpyAsync(dst + (job.off - off), job.buf, (size_t)job.len,
                                       hipMemcpyHostToDevice, c->cs), "ckpt copy");
                 HIP_OK(hipEventRecord(c->done[b], c->cs), "ckpt event");
                 c->pending[b] = true;
-            } else {
-                running = true;
             }
             done += nxt.len;
         }
@@ -466,6 +508,8 @@ dsv4_gpu_ckpt *dsv4_gpu_ckpt_open(const char *dir)
         dsv4_gpu_ckpt_close(c);
         return nullptr;
     }
+    /* without the thread every read is made inline, just slower */
+    c->reader_on = pthread_create(&c->reader, nullptr, reader_main, c) == 0;
     c->st.tensors = (long long)c->index.size();
     c->st.shards = (int)c->shards.size();
     return c;
@@ -474,6 +518,14 @@ dsv4_gpu_ckpt *dsv4_gpu_ckpt_open(const char *dir)
 void dsv4_gpu_ckpt_close(dsv4_gpu_ckpt *c)
 {
     if (!c) return;
+    if (c->reader_on) {
+        pthread_mutex_lock(&c->mu);
+        c->quit = true;
+        pthread_cond_broadcast(&c->cv);
+        pthread_mutex_unlock(&c->mu);
+        pthread_join(c->reader, nullptr);
+        c->reader_on = false;
+    }
     if (c->cs) (void)hipStreamSynchronize(c->cs);
     for (int b = 0; b < NSTAGE; b++) {
         if (c->stage[b]) (void)hipHostFree(c->stage[b]);
@@ -598,10 +650,27 @@ int dsv4_gpu_ckpt_load_layer(dsv4_gpu_ckpt *c, const dsv4_gpu_ckpt_dims *d, int 
                   "layers.%d.attn.indexer.compressor.wkv") ||
              load(&out->idx_comp_wgate, DSV4_WBF16, coff * d->index_head_dim, d->hidden,
                   "layers.%d.attn.indexer.compressor.wgate");
-    for (int e = 0; !rc && e < d->n_experts; e++)
+    int loaded = 0;                                 /* experts registered by this call */
+    for (int e = 0; !rc && e < d->n_experts; e++) {
         rc = dsv4_gpu_ckpt_load_expert(c, layer, e, d->hidden, d->moe_inter,
                                        experts ? &experts[e] : nullptr);
-    return rc ? -1 : 0;
+        loaded += rc == 0;
+    }
+    if (!rc) return 0;
+    /* roll back what this call made resident, so that HBM is returned and
+     * a retry of the layer starts from nothing */
+    for (int e = 0; e < loaded; e++) (void)dsv4_expert_release(layer, e);
+    const DSV4QMat *ms[] = {&out->wq_a, &out->wq_b, &out->wkv, &out->wo_a, &out->wo_b,
+                            &out->shared_w1, &out->shared_w2, &out->shared_w3, &out->gate,
+                            &out->comp_wkv, &out->comp_wgate, &out->idx_wq_b, &out->idx_wproj,
+                            &out->idx_comp_wkv, &out->idx_comp_wgate};
+    for (const DSV4QMat *m : ms)
+        if (m->w) (void)dsv4_res_release(m->w);
+    memset(out, 0, sizeof *out);
+    if (experts)
+        for (int e = 0; e < loaded; e++) memset(&experts[e], 0, sizeof experts[e]);
+    c->st.experts -= loaded;
+    return -1;
 }
 
 int dsv4_gpu_ckpt_stats_get(const dsv4_gpu_ckpt *c, dsv4_gpu_ckpt_stats *out)

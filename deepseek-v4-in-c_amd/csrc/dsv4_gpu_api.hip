@@ -23,6 +23,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <vector>
 
@@ -798,6 +799,41 @@ int dsv4_expert_adopt(int layer, int expert, const DSV4ExpertW *e, void *owned)
     return -1;
 }
 
+/* Undo dsv4_res_adopt: the matrix keyed at `key` leaves the residency
+ * table and its owned device blocks are freed (after the device drains, so
+ * no kernel still reads them). 0, or -1 when nothing is resident there. */
+int dsv4_res_release(const void *key)
+{
+    auto it = g_res.find((uintptr_t)key);
+    if (!g_ready || it == g_res.end()) return -1;
+    (void)hipDeviceSynchronize();
+    if (it->second.own_w) (void)hipFree(it->second.own_w);
+    if (it->second.own_s && it->second.own_s != it->second.own_w) (void)hipFree(it->second.own_s);
+    g_res.erase(it);
+    return 0;
+}
+
+/* Undo dsv4_expert_adopt: the expert's three matrices leave the residency
+ * table, the layer's table forgets the expert, and the block it owned (the
+ * one that starts at its w1, as the loader lays it out) is freed. */
+int dsv4_expert_release(int layer, int expert)
+{
+    if (!dsv4_gpu_has_expert(layer, expert)) return -1;
+    (void)hipDeviceSynchronize();
+    LayerExperts &L = g_layers[layer];
+    const Dsv4ExpertDev d = L.host[expert];
+    for (const uint8_t *w : {d.w1, d.w3, d.w2}) g_res.erase((uintptr_t)w);
+    for (size_t i = 0; i < L.owned.size(); i++)
+        if (L.owned[i] == (const void *)d.w1) {
+            (void)hipFree(L.owned[i]);
+            L.owned.erase(L.owned.begin() + (long)i);
+            break;
+        }
+    L.host[expert] = Dsv4ExpertDev{};
+    L.dirty = true;
+    return layer_sync(L);
+}
+
 extern "C" {
 
 int dsv4_gpu_has_expert(int layer, int expert)
@@ -867,6 +903,12 @@ int dsv4_gpu_moe_fp4_d(float *d_out, const float *d_x, int layer,
                                g_moe.p, as_stream(stream));
 }
 
+static int moen_tokenwise_env(void)
+{
+    const char *e = getenv("DSV4_GPU_MOEN_TOKENWISE");
+    return e ? (atoi(e) != 0) : -1;
+}
+
 int dsv4_gpu_moe_fp4_n(float *out, const float *x, int layer, const int *idx,
                        const float *w, int nt, int topk, int hidden, int inter,
                        float swiglu_limit)
@@ -892,11 +934,34 @@ int dsv4_gpu_moe_fp4_n(float *out, const float *x, int layer, const int *idx,
     const size_t oo = s.add((size_t)nt * hidden * sizeof(float));
     size_t end;
     if (stage_push(s, &end) != 0) return -1;
-    if (dsv4_moe_fp4_n_launch((float *)(g_ar.d + oo), (const float *)(g_ar.d + xo), L->dev,
-                              (int)L->host.size(), (const int *)(g_ar.d + io),
-                              (const float *)(g_ar.d + wo), nt, topk, hidden, inter,
-                              swiglu_limit, g_moe.p, g_stream) != 0)
+    /* With the routing in hand: when the batch's (token, k) pairs barely
+     * share experts (distinct experts above 9 in 10 pairs), reading each
+     * expert once saves next to nothing and the batched passes' per-unit
+     * staging costs more (4 tokens, 31.1 of 32 pairs distinct: 167.1 us
+     * batched against 152.5 us token by token), so the tokens go one by one
+     * through the single-token kernels. Both give every token the same bits.
+     * DSV4_GPU_MOEN_TOKENWISE: 1 always token by token, 0 never. */
+    int tokenwise = moen_tokenwise_env();
+    if (tokenwise < 0) {
+        std::vector<int> seen(idx, idx + (size_t)nt * topk);
+        std::sort(seen.begin(), seen.end());
+        const size_t distinct = std::unique(seen.begin(), seen.end()) - seen.begin();
+        tokenwise = nt > 1 && 10 * distinct > 9 * (size_t)nt * topk;
+    }
+    if (tokenwise) {
+        for (int t = 0; t < nt; t++)
+            if (dsv4_moe_fp4_launch((float *)(g_ar.d + oo) + (size_t)t * hidden,
+                                    (const float *)(g_ar.d + xo) + (size_t)t * hidden, L->dev,
+                                    (int)L->host.size(), (const int *)(g_ar.d + io) + t * topk,
+                                    (const float *)(g_ar.d + wo) + t * topk, topk, hidden,
+                                    inter, swiglu_limit, g_moe.p, g_stream) != 0)
+                return -1;
+    } else if (dsv4_moe_fp4_n_launch((float *)(g_ar.d + oo), (const float *)(g_ar.d + xo),
+                                     L->dev, (int)L->host.size(), (const int *)(g_ar.d + io),
+                                     (const float *)(g_ar.d + wo), nt, topk, hidden, inter,
+                                     swiglu_limit, g_moe.p, g_stream) != 0) {
         return -1;
+    }
     return stage_pull(oo, (size_t)nt * hidden * sizeof(float), out);
 }
 

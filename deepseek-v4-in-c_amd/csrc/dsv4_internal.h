@@ -145,6 +145,10 @@ int dsv4_res_adopt(const DSV4QMat *m, void *owned);
 /* The same for a routed expert (FP4, 1x32 blocks): registered for the fused
  * MoE by (layer, expert) and its three matrices made resident. 0 / -1. */
 int dsv4_expert_adopt(int layer, int expert, const DSV4ExpertW *e, void *owned);
+/* Their undo, for a load that fails partway: the matrix keyed at `key` (or
+ * the expert) leaves the tables and what it owned is freed. 0 / -1. */
+int dsv4_res_release(const void *key);
+int dsv4_expert_release(int layer, int expert);
 
 /* One routed expert's device tensors (FP4 nibbles + E8M0 per 1x32). */
 struct Dsv4ExpertDev {

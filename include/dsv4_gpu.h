@@ -251,7 +251,9 @@ typedef struct {
  * router gate, the compressor and indexer projections where the layer has
  * them, and all d->n_experts routed experts (experts[e] filled when experts
  * is not NULL). The layer's f32 vectors (norms, sinks, RoPE-free weights)
- * are not loaded: they are small host-side inputs. 0 / -1. */
+ * are not loaded: they are small host-side inputs. 0 / -1; on -1 nothing
+ * this call loaded stays resident or registered (its HBM is freed), so the
+ * same layer can be loaded again. */
 int dsv4_gpu_ckpt_load_layer(dsv4_gpu_ckpt *c, const dsv4_gpu_ckpt_dims *d, int layer,
                              dsv4_gpu_layer_mats *out, DSV4ExpertW *experts);
 

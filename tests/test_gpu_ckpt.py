@@ -203,6 +203,49 @@ def test_load_layer_under_the_binders_names(gpu, dsv4, tmp_path):
     L.dsv4_gpu_ckpt_close(ck)
 
 
+def test_load_layer_failing_partway_rolls_back(gpu, dsv4, tmp_path):
+    """A layer whose last routed expert is missing from the checkpoint (the
+    dims ask for one expert more than it holds): the call fails after it
+    has loaded every matrix and the other experts; nothing of it stays
+    resident or registered, the HBM comes back, a retry fails the same way
+    (not on an expert registered already), and the layer then loads under
+    its real dims."""
+    tiny_checkpoint.write(str(tmp_path))
+    L = dsv4.lib()
+    ck = open_ckpt(dsv4, tmp_path)
+    c = tiny_checkpoint.CFG
+    layer = 1
+    ratio = c["compress_ratios"][layer]
+
+    def dims(n_experts):
+        return dsv4.CkptDims(hidden=c["hidden"], q_lora=c["q_lora"], n_heads=c["n_heads"],
+                             head_dim=c["head_dim"], o_groups=c["o_groups"],
+                             o_lora=c["o_lora"], moe_inter=c["moe_inter"],
+                             n_shared=c["n_shared"], n_experts=n_experts,
+                             index_n_heads=c["index_n_heads"],
+                             index_head_dim=c["index_head_dim"], compress_ratio=ratio,
+                             has_indexer=1 if ratio == 4 else 0)
+    free0 = L.dsv4_gpu_free_vram()
+    for attempt in range(2):
+        lm = dsv4.LayerMats()
+        ex = (dsv4.DSV4ExpertW * (c["n_experts"] + 1))()
+        d = dims(c["n_experts"] + 1)
+        assert L.dsv4_gpu_ckpt_load_layer(ck, ctypes.byref(d), layer, ctypes.byref(lm), ex) == -1
+        for e in range(c["n_experts"]):
+            assert L.dsv4_gpu_has_expert(layer, e) == 0, (attempt, e)
+        assert lm.wq_a.w is None and ex[0].w1.w is None
+        print("rollback %d: free VRAM %d -> %d" % (attempt, free0, L.dsv4_gpu_free_vram()),
+              flush=True)
+        assert abs(L.dsv4_gpu_free_vram() - free0) < (64 << 20)
+    lm = dsv4.LayerMats()
+    ex = (dsv4.DSV4ExpertW * c["n_experts"])()
+    d = dims(c["n_experts"])
+    assert L.dsv4_gpu_ckpt_load_layer(ck, ctypes.byref(d), layer, ctypes.byref(lm), ex) == 0
+    assert L.dsv4_gpu_has(ctypes.byref(lm.wo_b)) == 1
+    assert all(L.dsv4_gpu_has_expert(layer, e) == 1 for e in range(c["n_experts"]))
+    L.dsv4_gpu_ckpt_close(ck)
+
+
 def _write_two_shards(d):
     rng = np.random.default_rng(5)
     a = tiny_checkpoint._Writer(rng)

@@ -106,6 +106,19 @@ def test_moe_n_other_shapes(gpu, dsv4, hidden, inter, topk, nt, limit):
     _check(dsv4, 7, table, IDX, W, X, hidden, inter, limit)
 
 
+@pytest.mark.parametrize("mode", ["auto", "0", "1"])
+def test_moe_n_tokenwise_rule(gpu, dsv4, monkeypatch, mode):
+    """Pairs that barely share experts (4 tokens x top-8 drawn from 64
+    experts): the host-buffer call then runs the tokens one by one through
+    the single-token kernels (auto, or DSV4_GPU_MOEN_TOKENWISE=1); =0 keeps
+    the batched kernels. Every mode gives each token its single-token bits."""
+    if mode != "auto":
+        monkeypatch.setenv("DSV4_GPU_MOEN_TOKENWISE", mode)
+    rng, table = _setup(dsv4, 11, 2048, 1024, 64, 13)
+    IDX, W, X = _batch(rng, table, 4, 8, 2048)
+    _check(dsv4, 11, table, IDX, W, X, 2048, 1024, 10.0)
+
+
 @pytest.mark.parametrize("form", ["0", "1"])
 def test_moe_n_other_forms_go_token_by_token(gpu, dsv4, monkeypatch, form):
     """The VALU and fragment-order forms have no batched kernel: the batched

@@ -20,6 +20,10 @@ import oracle
 pytestmark = pytest.mark.gpu
 
 
+# device buffers bound into the library, kept for the whole process
+_KEEP = []
+
+
 def _case(dsv4, torch, layer, hidden, inter, topk, n_experts, seed):
     L = dsv4.lib()
     rng = np.random.default_rng(seed)
@@ -108,4 +112,7 @@ def test_noalloc_refuses_more_scratch_than_the_array(gpu, dsv4):
                                       torch.cuda.current_stream().cuda_stream)
     assert rc == -1
     torch.cuda.synchronize()
-    del w13, s13
+    # the library's expert table keeps pointing at this memory (there is no
+    # unbind): it stays alive until the process ends, so no later
+    # allocation can reuse it under a registered expert
+    _KEEP.extend([w13, s13])

@@ -36,6 +36,12 @@
 #define DSV4_MAX_DEVICES 64
 static __device__ __align__(256) unsigned char scratch[DSV4_STATIC_SCRATCH_MAX];
 static void *g_static_scratch[DSV4_MAX_DEVICES];
+/* The routed-expert pass's arrival counters (the one-launch form of
+ * dsv4_moe_mx.hip): zero when the module loads, zero again after every
+ * call, on every device; their device address is looked up once per
+ * device, as for `scratch`. */
+static __device__ __align__(256) uint32_t moe_sync[DSV4_MOE_SYNC_WORDS];
+static void *g_moe_sync[DSV4_MAX_DEVICES];
 
 namespace {
 
@@ -482,6 +488,11 @@ int dsv4_gpu_init(void)
         HIP_OK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress scratch");
         g_static_scratch[dev] = ptr;
     }
+    if (!g_moe_sync[dev]) {
+        void *ptr = nullptr;
+        HIP_OK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(moe_sync)), "hipGetSymbolAddress moe_sync");
+        g_moe_sync[dev] = ptr;
+    }
     printf("hip: %s (%s), %d CUs, %.2f GB free of %.2f GB\n", p.name,
            p.gcnArchName, p.multiProcessorCount, (double)freeb / 1073741824.0,
            (double)totb / 1073741824.0);
@@ -797,6 +808,13 @@ int dsv4_expert_adopt(int layer, int expert, const DSV4ExpertW *e, void *owned)
     if (added == 3 && register_expert(layer, expert, d, hidden, inter, owned) == 0) return 0;
     for (int i = 0; i < added; i++) g_res.erase((uintptr_t)ms[i]->w);   /* roll back */
     return -1;
+}
+
+uint32_t *dsv4_moe_sync(void)
+{
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= DSV4_MAX_DEVICES) return nullptr;
+    return (uint32_t *)g_moe_sync[dev];
 }
 
 /* Undo dsv4_res_adopt: the matrix keyed at `key` leaves the residency

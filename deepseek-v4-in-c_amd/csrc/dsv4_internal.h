@@ -145,6 +145,11 @@ int dsv4_res_adopt(const DSV4QMat *m, void *owned);
 /* The same for a routed expert (FP4, 1x32 blocks): registered for the fused
  * MoE by (layer, expert) and its three matrices made resident. 0 / -1. */
 int dsv4_expert_adopt(int layer, int expert, const DSV4ExpertW *e, void *owned);
+/* The routed-expert pass's arrival counters on the current device
+ * (DSV4_MOE_SYNC_WORDS words, zero between calls; nullptr before
+ * dsv4_gpu_init). Calls of the pass that overlap on one device race. */
+#define DSV4_MOE_SYNC_WORDS 66
+uint32_t *dsv4_moe_sync(void);
 /* Their undo, for a load that fails partway: the matrix keyed at `key` (or
  * the expert) leaves the tables and what it owned is freed. 0 / -1. */
 int dsv4_res_release(const void *key);

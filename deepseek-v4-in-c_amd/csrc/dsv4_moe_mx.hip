@@ -551,25 +551,30 @@ __device__ __forceinline__ void m2_x_store(uint16_t *lds, const f32x4 *xv, int n
     }
 }
 
-/* Pass A: workgroup (32 h-rows of expert slot k); wave w: matrix w & 1 (w1 /
- * w3), row tile w >> 1. The workgroup splits x into its bf16 terms in LDS;
- * all of x is requested before the first weight units, so the split waits
- * for x alone while those units are in flight. */
-template <int D, int NU>
-__global__ void __launch_bounds__(256)
-k_mc2_gate_up(uint16_t *__restrict__ ht, const float *__restrict__ x,
-              const Dsv4ExpertDev *__restrict__ table, int n_table,
-              const int *__restrict__ idx, int hidden, int inter, float limit)
+/* Pass A's body for row block bx (16 TILES h-rows) of slot k, 2 TILES
+ * waves: wave w runs matrix w & 1 (w1 / w3) over row tile w >> 1. The
+ * workgroup splits x into its bf16 terms in LDS; all of x is requested
+ * before the first weight units, so the split waits for x alone while those
+ * units are in flight. false when slot k's expert is missing (nothing
+ * written: the down pass reports it). COHERENT: h leaves as agent-scope
+ * stores (written through to the device's coherence point), for a consumer
+ * on another XCD in the same launch. */
+template <int D, int NU, int TILES, bool COHERENT>
+__device__ __forceinline__ bool mc2_gate_up_body(uint16_t *__restrict__ ht,
+                                                 const float *__restrict__ x,
+                                                 const Dsv4ExpertDev *__restrict__ table,
+                                                 int n_table, const int *__restrict__ idx,
+                                                 int hidden, int inter, float limit, int bx,
+                                                 int k)
 {
     extern __shared__ __attribute__((aligned(16))) unsigned char m2lds[];
     uint16_t *xl = (uint16_t *)m2lds;                      /* [MC_NT][pitch] */
-    __shared__ float red[2][2][16];
-    const int k = blockIdx.y;
+    __shared__ float red[TILES][2][16];
     const Dsv4ExpertDev E = mc_expert(table, n_table, idx, k);
-    if (!E.w1) return;                      /* the down pass reports it (NaN) */
+    if (!E.w1) return false;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int mat = w & 1, tile = w >> 1;
-    const int o0 = blockIdx.x * 32 + 16 * tile;
+    const int o0 = bx * 16 * TILES + 16 * tile;
     const int nsb = hidden >> 5;
     const size_t rowb = (size_t)hidden >> 1;
     const int nu = (int)(rowb / M2_UB);
@@ -580,7 +585,8 @@ k_mc2_gate_up(uint16_t *__restrict__ ht, const float *__restrict__ x,
 
     M2Unit P[D];
     if constexpr (NU > 0) {
-        constexpr int NL = (NU * 512 + 1023) / 1024;       /* hidden = 512 NU */
+        /* hidden = 512 NU: NL 16-byte pieces per thread of 2 TILES waves */
+        constexpr int NL = (NU * 512 + 4 * 128 * TILES - 1) / (4 * 128 * TILES);
         f32x4 xv[NL];
         m2_x_load<NL>(xv, x, hidden, 0);
         __builtin_amdgcn_sched_barrier(0);
@@ -589,7 +595,7 @@ k_mc2_gate_up(uint16_t *__restrict__ ht, const float *__restrict__ x,
         m2_x_store<NL>(xl, xv, hidden, 0);
     } else {
         m2_prologue<D>(P, base, rowb, sb, nsb, nu, lane);
-        for (int i0 = 0; i0 < hidden; i0 += 8 * 1024) {
+        for (int i0 = 0; i0 < hidden; i0 += 8 * 4 * (int)blockDim.x) {
             f32x4 xv[8];
             m2_x_load<8>(xv, x, hidden, i0);
             m2_x_store<8>(xl, xv, hidden, i0);
@@ -605,14 +611,33 @@ k_mc2_gate_up(uint16_t *__restrict__ ht, const float *__restrict__ x,
         for (int j = 0; j < 4; j++) red[tile][mat][4 * g + j] = s[j];
     }
     __syncthreads();
-    if (tid < 32) {
+    if (tid < 16 * TILES) {
         const int t = tid >> 4, i = tid & 15;
         uint32_t tt[MC_NT];
         bf16_terms(swiglu1(red[t][0][i], red[t][1][i], limit), tt);
 #pragma unroll
-        for (int c = 0; c < MC_NT; c++)
-            ht[((size_t)k * MC_NT + c) * inter + blockIdx.x * 32 + 16 * t + i] = (uint16_t)tt[c];
+        for (int c = 0; c < MC_NT; c++) {
+            uint16_t *dst = ht + ((size_t)k * MC_NT + c) * inter + bx * 16 * TILES + 16 * t + i;
+            if (COHERENT)
+                __hip_atomic_store(dst, (uint16_t)tt[c], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            else
+                *dst = (uint16_t)tt[c];
+        }
     }
+    return true;
+}
+
+/* Pass A: workgroup (32 h-rows of expert slot k); wave w: matrix w & 1 (w1 /
+ * w3), row tile w >> 1 (mc2_gate_up_body). */
+template <int D, int NU>
+__global__ void __launch_bounds__(256)
+k_mc2_gate_up(uint16_t *__restrict__ ht, const float *__restrict__ x,
+              const Dsv4ExpertDev *__restrict__ table, int n_table,
+              const int *__restrict__ idx, int hidden, int inter, float limit)
+{
+    (void)mc2_gate_up_body<D, NU, 2, false>(ht, x, table, n_table, idx, hidden, inter, limit,
+                                            blockIdx.x, blockIdx.y);
 }
 
 /* Both 16-row tiles of a 32-row group as one stream of 2 NU units (tile 0's
@@ -742,6 +767,196 @@ k_mc2_down(float *__restrict__ out, const uint16_t *__restrict__ ht,
             o = o + p;
         }
         out[r0 + tid] = o;
+    }
+}
+
+/* ------------------------------------------------------------ one launch
+ *
+ * Pass A and pass B in one launch of 8-wave workgroups. Workgroups [0, ga)
+ * run pass A over 64 h-rows (mc2_gate_up_body with four row tiles;
+ * workgroup b is row block b % nx of slot b / nx, nx = inter / 64), the
+ * others pass B over 32 output rows, wave w taking slots w, w + 8, ... as
+ * k_mc2_down does. For each slot a pass-B wave requests its first weight
+ * units (they do not depend on h), then waits until all nx pass-A
+ * workgroups of the slot have published h_k, then stages h_k and runs both
+ * row tiles with k_mc2_down's arithmetic; the k-ordered combine is
+ * k_mc2_down's, so the output has the two-launch form's bits.
+ *
+ * THE HAND-OFF, ACROSS XCDs. Each XCD has its own L2, and a release or
+ * acquire fence at agent scope writes back or invalidates that whole L2 --
+ * measured, a fence per workgroup (and per slot of a pass-B wave) took the
+ * launch from 39 to 87 us. So the data crossing XCDs never lives in a
+ * non-coherent line instead: pass A stores h with agent-scope atomic
+ * stores (written through to the device's coherence point), waits for them
+ * to complete (s_waitcnt), then counts itself in with an atomic add on the
+ * slot's counter in `sync`; pass B polls the counter and reads h with
+ * agent-scope atomic loads (served from the coherence point, never from a
+ * stale line).
+ *
+ * ENDING. The workgroups of one XCD are dispatched in increasing id, so
+ * every pass-A workgroup is running or done before a pass-B workgroup can
+ * take a CU, and pass A waits on nothing: the waits end. A wait that still
+ * exceeds MC_SPIN polls gives up, marks sync[MC_KMAX + 1] and leaves NaN in
+ * the rows. The last pass-B workgroup to finish (sync[MC_KMAX] counts them)
+ * returns the counters to zero, so the next call starts from zeros without
+ * a memset (and a captured graph replays). */
+constexpr int MC_SYNC_WORDS = MC_KMAX + 2;
+static_assert(MC_SYNC_WORDS == DSV4_MOE_SYNC_WORDS, "the counters' size");
+constexpr int MC_SPIN = 1 << 22;
+
+/* Wave-uniform: true once *cnt reaches need (lane 0 polls). */
+__device__ __forceinline__ bool slot_wait(uint32_t *cnt, uint32_t need)
+{
+    uint32_t v = 0;
+    if ((threadIdx.x & 63) == 0) {
+        for (int it = 0; it < MC_SPIN; it++) {
+            v = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (v >= need) break;
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    return __shfl(v, 0, 64) >= need;
+}
+
+/* Slot k's h planes into a pass-B wave's LDS (pitch mc_pitch(inter)) with
+ * agent-scope atomic loads, 16 bytes per lane per piece. */
+template <int NUB>
+__device__ __forceinline__ void mc2_h_coherent(uint16_t *hl, const uint16_t *hk, int inter,
+                                               int lane)
+{
+    const int pitch = mc_pitch(inter);
+    if constexpr (NUB > 0) {
+        constexpr int IN = 512 * NUB;                      /* inter */
+        constexpr int NH = MC_NT * IN / 512;               /* 1 KB pieces per wave */
+        uint64_t hv[2 * NH];
+#pragma unroll
+        for (int j = 0; j < NH; j++) {
+            const uint64_t *q = (const uint64_t *)(hk + 512 * j + 8 * lane);
+            hv[2 * j] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            hv[2 * j + 1] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int j = 0; j < NH; j++) {
+            const int e = 512 * j + 8 * lane, c = e / IN;
+            uint64_t *d = reinterpret_cast<uint64_t *>(hl + c * pitch + (e - c * IN));
+            d[0] = hv[2 * j];
+            d[1] = hv[2 * j + 1];
+        }
+    } else {
+        for (int e = 8 * lane; e < MC_NT * inter; e += 512) {
+            const int c = e / inter;
+            const uint64_t *q = (const uint64_t *)(hk + e);
+            uint64_t *d = reinterpret_cast<uint64_t *>(hl + c * pitch + (e - c * inter));
+            d[0] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            d[1] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+/* LDS of the one-launch form: pass A's (x planes, eight unit buffers) or
+ * pass B's (eight waves' h planes and unit buffers). */
+__host__ __device__ __forceinline__ size_t m2_lds_fused(int hidden, int inter)
+{
+    const size_t a = (size_t)MC_NT * mc_pitch(hidden) * 2 + 8 * M2_WBUF;
+    const size_t b = 8 * m2_wave_b(inter);
+    return a > b ? a : b;
+}
+
+template <int DA, int NUA, int DB, int NUB>
+__global__ void __launch_bounds__(512)
+k_mc2_fused(float *__restrict__ out, uint16_t *__restrict__ ht, const float *__restrict__ x,
+            const Dsv4ExpertDev *__restrict__ table, int n_table, const int *__restrict__ idx,
+            const float *__restrict__ wts, int topk, int hidden, int inter, float limit,
+            uint32_t *__restrict__ sync, int ga)
+{
+    const int nx = inter >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    if ((int)blockIdx.x < ga) {
+        const int k = (int)blockIdx.x / nx;
+        (void)mc2_gate_up_body<DA, NUA, 4, true>(ht, x, table, n_table, idx, hidden, inter,
+                                                 limit, (int)blockIdx.x - k * nx, k);
+        /* h_k's rows of this workgroup are wave 0's stores (or none, for a
+         * missing expert): wait until they are complete, then count in */
+        if (w == 0) {
+            __builtin_amdgcn_s_waitcnt(0);
+            if (lane == 0)
+                __hip_atomic_fetch_add(sync + k, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
+    extern __shared__ __attribute__((aligned(16))) unsigned char m2lds[];
+    __shared__ float accl[MC_KMAX][32];
+    const int r0 = ((int)blockIdx.x - ga) * 32;
+    const int r = lane & 15, g = lane >> 4;
+    const int nsb = inter >> 5;
+    const size_t rowb = (size_t)inter >> 1;
+    const int nu = (int)(rowb / M2_UB);
+    const int pitch = mc_pitch(inter);
+    unsigned char *region = m2lds + (size_t)w * m2_wave_b(inter);
+    uint16_t *hl = (uint16_t *)region;
+    unsigned char *buf = region + m2_hplanes_b(inter);
+    const uint16_t *bl = hl + min(r, MC_NT - 1) * pitch;
+    for (int k = w; k < topk; k += 8) {
+        const Dsv4ExpertDev E = mc_expert(table, n_table, idx, k);
+        if (!E.w1) {
+            if (lane < 32) accl[k][lane] = __builtin_nanf("");
+            continue;
+        }
+        /* slot k's planes are contiguous in ht: MC_NT * inter elements */
+        const uint16_t *hk = ht + (size_t)k * MC_NT * inter;
+        const uint8_t *base = E.w2 + (size_t)r0 * rowb;
+        const uint8_t *sb = E.s2 + (size_t)r0 * nsb;
+        v4f res[2];
+        bool ok;
+        if constexpr (NUB > 0) {
+            M2Unit P[DB];
+            m2_prologue<DB>(P, base, rowb, sb, nsb, NUB, lane);
+            ok = slot_wait(sync + k, (uint32_t)nx);
+            mc2_h_coherent<NUB>(hl, hk, inter, lane);
+            m2_tiles2<DB, NUB>(res, P, base, rowb, sb, nsb, buf, bl, lane);
+        } else {
+            ok = slot_wait(sync + k, (uint32_t)nx);
+            mc2_h_coherent<0>(hl, hk, inter, lane);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                M2Unit P[DB];
+                m2_prologue<DB>(P, base + (size_t)16 * t * rowb, rowb, sb + (size_t)16 * t * nsb,
+                                nsb, nu, lane);
+                res[t] = m2_tile<DB, 0>(P, base + (size_t)16 * t * rowb, rowb,
+                                        sb + (size_t)16 * t * nsb, nsb, nu, buf, bl, lane);
+            }
+        }
+        if (!ok && lane == 0)
+            __hip_atomic_store(sync + MC_KMAX + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const v4f sm = term_sum(res[t], lane);
+            if (r == 0) {
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    accl[k][16 * t + 4 * g + j] = ok ? sm[j] : __builtin_nanf("");
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < 32) {
+        float o = 0.0f;
+        for (int kk = 0; kk < topk; kk++) {
+            const float p = wts[kk] * accl[kk][tid];
+            o = o + p;
+        }
+        out[r0 + tid] = o;
+    }
+    /* every wave of this workgroup is past its waits: count it out; the
+     * last one zeroes the counters for the next call */
+    if (tid == 0) {
+        const uint32_t gb = gridDim.x - (uint32_t)ga;
+        if (__hip_atomic_fetch_add(sync + MC_KMAX, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT) == gb - 1) {
+            for (int kk = 0; kk < topk; kk++)
+                __hip_atomic_store(sync + kk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(sync + MC_KMAX, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -1179,6 +1394,34 @@ int dsv4_moe_fp4_launch(float *d_out, const float *d_x,
         hipLaunchKernelGGL(k_mc_split, dim3((hidden + 255) / 256), dim3(256), 0, st, xt, d_x,
                            hidden);
         HIP_OK(hipGetLastError(), "moe split launch");
+    }
+    uint32_t *sync = dsv4_moe_sync();
+    const size_t lf = m2_lds_fused(hidden, inter);
+    /* DSV4_GPU_MOE_FUSE=1: one launch, where a workgroup fits a CU's LDS
+     * with the static arrays and inter is a multiple of 64 rows. Not the
+     * default: at C3 it measured 40.7 us against 38.8 us for the two
+     * launches. Every expert's h completes at about the same time (pass A's
+     * workgroups all run at once), so pass B's per-slot waits end together
+     * and the launch only trades the kernel boundary for its own hand-off;
+     * the same bits either way. */
+    if (m2 && sync && mc_env("DSV4_GPU_MOE_FUSE", 0) != 0 && inter % 64 == 0 &&
+        lf + 16 * 1024 <= dsv4_lds_limit()) {
+        static bool optedf = false;
+        if (!optedf) {
+            mc_lds_optin(k_mc2_fused<2, 14, 2, 4>); mc_lds_optin(k_mc2_fused<2, 14, 3, 0>);
+            mc_lds_optin(k_mc2_fused<3, 0, 2, 4>); mc_lds_optin(k_mc2_fused<3, 0, 3, 0>);
+            optedf = true;
+        }
+        const int ga = (inter / 64) * topk, gb = hidden / 32;
+        const int nua = hidden / 512, nub = inter / 512;
+#define M2_F(DA, NUA, DB, NUB) hipLaunchKernelGGL((k_mc2_fused<DA, NUA, DB, NUB>), dim3(ga + gb), \
+            dim3(512), lf, st, d_out, ht, d_x, d_table, n_table, d_idx, d_w, topk, hidden, inter, \
+            limit, sync, ga)
+        if (nua == 14) { if (nub == 4) M2_F(2, 14, 2, 4); else M2_F(2, 14, 3, 0); }
+        else { if (nub == 4) M2_F(3, 0, 2, 4); else M2_F(3, 0, 3, 0); }
+#undef M2_F
+        HIP_OK(hipGetLastError(), "moe one-launch");
+        return 0;
     }
     if (m2) {
         /* The staged form: two units in flight per wave (three or four

@@ -186,3 +186,77 @@ def test_device_entry_point_matches_host_path(gpu, dsv4):
                                          dw.data_ptr(), topk, hidden, inter, 10.0, st) == 0
     torch.cuda.synchronize()
     assert common.bits_equal(do.cpu().numpy(), host)
+
+
+@pytest.mark.parametrize("hidden,inter,topk", [(7168, 2048, 8), (4096, 2048, 6),
+                                               (1024, 512, 16), (2048, 1024, 5),
+                                               (512, 4096, 3), (1024, 512, 1)])
+def test_one_launch_matches_two_launches(gpu, dsv4, monkeypatch, hidden, inter, topk):
+    """The staged form in one launch (DSV4_GPU_MOE_FUSE=1: pass B waits per
+    expert slot on pass A's arrival counters) and in two (the default) give
+    the same bits; three calls in a row with different x check that every
+    call leaves the counters at zero for the next and that pass B never
+    reads a stale h."""
+    rng = np.random.default_rng(hidden + inter + topk)
+    ids = rng.permutation(16 if topk <= 16 else topk)[:topk].astype(np.int32)
+    for eid in ids:
+        upload(dsv4, 7, int(eid), common.fp4_expert(rng, hidden, inter), hidden, inter)
+    xs = [common.bf16_round(rng.standard_normal(hidden).astype(np.float32)) for _ in range(3)]
+    w = common.router(rng, topk)
+    monkeypatch.setenv("DSV4_GPU_MOE_FUSE", "0")
+    two = [dsv4.moe_fp4(x, 7, ids, w, hidden, inter, 10.0) for x in xs]
+    monkeypatch.setenv("DSV4_GPU_MOE_FUSE", "1")
+    one = [dsv4.moe_fp4(x, 7, ids, w, hidden, inter, 10.0) for x in xs]
+    print("moe one launch h%d i%d k%d" % (hidden, inter, topk), flush=True)
+    for a, b in zip(one, two):
+        assert common.bits_equal(a, b)
+
+
+def test_one_launch_missing_expert_and_graph_replays(gpu, dsv4, monkeypatch):
+    """The one-launch form on device buffers: an id outside the layer's table
+    gives NaN rows (as the two-launch form does) and the next call is whole
+    again; then the call captured in a HIP graph and replayed, with eager
+    calls between the replays, matches the eager result every time (the
+    counters return to zero inside the launch, no memset is recorded)."""
+    import torch
+    monkeypatch.setenv("DSV4_GPU_MOE_FUSE", "1")
+    hidden, inter, topk = 7168, 2048, 8
+    rng = np.random.default_rng(31)
+    ids = np.arange(topk, dtype=np.int32)
+    for i in ids:
+        upload(dsv4, 8, int(i), common.fp4_expert(rng, hidden, inter), hidden, inter)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    w = common.router(rng, topk)
+    want = dsv4.moe_fp4(x, 8, ids, w, hidden, inter, 10.0)
+    dev = torch.device("cuda:0")
+    dx, dw = torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev)
+    bad = torch.from_numpy(np.array([0, 1, 2, 100000, 4, 5, 6, 7], np.int32)).to(dev)
+    good = torch.from_numpy(ids).to(dev)
+    do = torch.empty(hidden, dtype=torch.float32, device=dev)
+    L = dsv4.lib()
+
+    def call(di, st):
+        assert L.dsv4_gpu_moe_fp4_d(do.data_ptr(), dx.data_ptr(), 8, di.data_ptr(),
+                                    dw.data_ptr(), topk, hidden, inter, 10.0, st) == 0
+    st = torch.cuda.current_stream().cuda_stream
+    call(bad, st)
+    torch.cuda.synchronize()
+    assert np.isnan(do.cpu().numpy()).all()
+    call(good, st)
+    torch.cuda.synchronize()
+    assert common.bits_equal(do.cpu().numpy(), want)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        call(good, s.cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        call(good, s.cuda_stream)
+    for rep in range(3):
+        do.fill_(7.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert common.bits_equal(do.cpu().numpy(), want), rep
+        call(good, st)
+        torch.cuda.synchronize()
+        assert common.bits_equal(do.cpu().numpy(), want), rep

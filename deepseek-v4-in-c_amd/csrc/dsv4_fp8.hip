@@ -37,7 +37,9 @@
 #include "dsv4_dev.h"
 #include "dsv4_internal.h"
 
+#include <algorithm>
 #include <stdlib.h>
+#include <type_traits>
 
 namespace {
 
@@ -760,11 +762,369 @@ void launch_gemv_nl_nch(const Fp8Geom &g, float *y, const float *x, const uint8_
     }
 }
 
+/* ---------------------------------------------- batched on the matrix core
+ *
+ * k_fp8_mfn: the batched GEMV with k_fp8_gemv's bits on v_mfma_f32_16x16x4f32.
+ * Measured on the device (an in-bounds probe over 2^21 outputs with normal,
+ * wide-exponent, cancelling and subnormal operands, and -0.0 addends), that
+ * instruction computes each output as a sequential fmaf chain over its four
+ * k in ascending order, starting from C, without flushing subnormals. Each
+ * of dot16's four chains (elements c, c+4, c+8, c+12 of a chunk: a product,
+ * then three fmaf) is therefore one MFMA with A[row][k] = w[c + 4k],
+ * B[k][token] = x[c + 4k] and C = -0.0 (fmaf(a, b, -0.0) == a * b, signed
+ * zeros included). The VALU runs the rest of k_fp8_gemv's per-(row, token)
+ * arithmetic in its order: (p0 + p1) + (p2 + p3), fmaf with the chunk's
+ * scale into row slot j's running sum (chunks j, j + tc, ... in order, from
+ * +0.0), and the slots' fixed tree (balanced over aligned blocks within 64
+ * slots, then the 64-slot blocks in order). Every (row, token) is therefore
+ * bit-identical to the single-token GEMV.
+ *
+ * Layout. The tc slots of a row are cut into P parts of L slots (L in 16,
+ * 32, 64, at most 16 steps per part). A workgroup is 8 waves, 8 row tiles of
+ * 16, for one part (blockIdx.y) and one tile of 16 tokens (blockIdx.z). A
+ * unit is 4 consecutive slots over every n (NCH steps; step n is the chunks
+ * j0 + n tc .. + 3, 64 bytes of each row); the workgroup stages its tokens'
+ * x of one unit in LDS (two buffers) while the waves run the unit before it,
+ * one barrier per unit, so x arrives spread over the kernel instead of in
+ * one burst at its start. Lane (row r, k group g) loads dword g of each of a
+ * step's 4 chunks, the A operands of their chains, 4 steps ahead; every load
+ * is unconditional (steps past the part read its first chunks, x past the
+ * last unit its first unit), so each wait counts only the loads before it.
+ * A unit ends in a binary-counter tree. With P = 1 the wave writes y; else
+ * its part's subtree goes to scratch, and k_fp8_mfn_join forms the rest of
+ * the tree. */
+constexpr int MFN_PF = 4;               /* steps of weights in flight         */
+
+/* f(std::integral_constant<int, I>{}) for I = 0 .. N-1, unrolled at compile
+ * time (register arrays indexed by I stay in registers) */
+template <typename F, int... I>
+__device__ __forceinline__ void sfor_seq(F &&f, std::integer_sequence<int, I...>)
+{
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void sfor(F &&f)
+{
+    sfor_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+/* LDS floats per token of one unit's x: NCH chunk groups of 64, padded so
+ * that the 16 tokens' B reads of one k group fall in distinct banks */
+template <int NCH>
+struct MfnDim {
+    static constexpr int TP = NCH * 64 + 4;
+    static constexpr int BUF = 16 * TP;                 /* floats per buffer */
+    static constexpr int XM = (16 * NCH * 16 + 511) / 512;  /* float4 per thread */
+    static constexpr int UMAX = 16 / NCH;               /* units per part */
+};
+
+template <int SF, bool SC1, int NCH>
+__global__ void __launch_bounds__(512)
+k_fp8_mfn(float *__restrict__ y, float *__restrict__ part, const float *__restrict__ x,
+          const uint8_t *__restrict__ W, const void *__restrict__ S, int rows, int cols,
+          int sc, int blk_r, int blk_c, int tc, int L, int nt)
+{
+    using D = MfnDim<NCH>;
+    extern __shared__ __attribute__((aligned(16))) float xs[];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int row0 = (blockIdx.x * 8 + w) * 16;
+    const int p = blockIdx.y, P = gridDim.y;
+    const int t0 = blockIdx.z * 16;
+    const int ntok = min(16, nt - t0);
+    const int ch = cols >> 4;
+    const int r = lane & 15, g = lane >> 4;
+    const int wrow0 = min(row0, rows - 1);
+    const size_t wrow = (size_t)min(wrow0 + r, rows - 1) * cols;
+    const size_t srow = (size_t)(wrow0 / blk_r) * sc;
+    const int U = L >> 2;                      /* units, <= D::UMAX */
+
+    /* unit u's chunk group at n, or -1 past the row (4 chunks wholly in or
+     * out, as ch % 4 == 0); units past the part read unit 0's */
+    auto group = [&](int u, int n) {
+        if (u >= U) u = 0;
+        const int c = p * L + 4 * u + n * tc;
+        return c < ch ? c : -1;
+    };
+    /* SC1: blk_c a multiple of 64, so a step's 4 chunks share one scale.
+     * The scales' bits are read by vector loads (zv: a zero the compiler
+     * cannot see through; a scalar load would be counted with the LDS reads,
+     * and each wait for x would then also wait for scales requested steps
+     * ahead) and taken into scalar registers at use, where the scalar unit
+     * decodes them. The weights are read at a uniform base (the step's
+     * chunks of the tile's first row) plus a 32-bit lane offset, so their
+     * addresses cost no vector instructions. */
+    constexpr int NSR = SC1 ? 1 : 4;
+    int zv;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zv));
+    const uint32_t loff = (uint32_t)((min(wrow0 + r, rows - 1) - wrow0) * cols + 4 * g);
+    const uint8_t *const wt = W + (size_t)wrow0 * cols;
+    uint32_t WR[16][4];
+    uint32_t SR[16][NSR];
+    auto wload = [&](auto kc, int u, int n) {
+        constexpr int k = decltype(kc)::value;
+        const int c = max(group(u, n), 0);
+        const uint8_t *wc = wt + (size_t)c * 16;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            WR[k][q] = *reinterpret_cast<const uint32_t *>(wc + loff + 16 * q);
+#pragma unroll
+        for (int q = 0; q < NSR; q++) {
+            const size_t at = srow + ((c + q) * 16) / blk_c + zv;
+            SR[k][q] = SF == 0 ? (uint32_t)((const uint8_t *)S)[at] : ((const uint32_t *)S)[at];
+        }
+    };
+    /* the step's scale, uniform: from lane 0 into a scalar register */
+    auto scale = [&](uint32_t bits) {
+        const uint32_t b = __builtin_amdgcn_readfirstlane(bits);
+        return SF == 0 ? dec_e8m0(b) : __uint_as_float(b);
+    };
+    /* x of unit u for the 16 tokens: piece i = (token, n, float4 of 16) */
+    f32x4 XV[D::XM];
+    auto xload = [&](int u) {
+#pragma unroll
+        for (int k = 0; k < D::XM; k++) {
+            const int i = min((int)threadIdx.x + 512 * k, 16 * NCH * 16 - 1);
+            const int t = i / (NCH * 16), n = (i / 16) % NCH, f = i & 15;
+            const int c = max(group(u, n), 0);
+            XV[k] = ldf4(x + (size_t)(t0 + min(t, ntok - 1)) * cols + c * 16 + 4 * f);
+        }
+    };
+    auto xstore = [&](float *xb) {
+#pragma unroll
+        for (int k = 0; k < D::XM; k++) {
+            const int i = (int)threadIdx.x + 512 * k;
+            if (i < 16 * NCH * 16) {
+                const int t = i / (NCH * 16), rem = i - t * (NCH * 16);
+                *reinterpret_cast<f32x4 *>(xb + t * D::TP + 4 * rem) = XV[k];
+            }
+        }
+    };
+
+    xload(0);
+    __builtin_amdgcn_sched_barrier(0);
+    sfor<MFN_PF>([&](auto kc) {
+        constexpr int s = decltype(kc)::value;
+        wload(std::integral_constant<int, s>{}, s / NCH, s % NCH);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+    xstore(xs);
+    __builtin_amdgcn_sched_barrier(0);
+    xload(1);
+    __syncthreads();
+
+    const f32x4 negz = {-0.0f, -0.0f, -0.0f, -0.0f};
+    f32x4 h4, h8, h16, h32, fin;
+    h4 = h8 = h16 = h32 = fin = f32x4{0.f, 0.f, 0.f, 0.f};
+    sfor<D::UMAX>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        const float *xb = xs + (u & 1) * D::BUF + r * D::TP + 4 * g;
+        f32x4 A[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) A[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+        sfor<NCH>([&](auto nc) {
+            constexpr int n = decltype(nc)::value;
+            constexpr int s = u * NCH + n;
+            if (s + MFN_PF < 16)
+                wload(std::integral_constant<int, s + MFN_PF>{}, (s + MFN_PF) / NCH,
+                      (s + MFN_PF) % NCH);
+            if (u < U && group(u, n) >= 0) {
+                /* the step's four x reads first, then chunk q's MFMAs
+                 * ahead of chunk q - 1's additions (each chunk's four chains
+                 * take 128 cycles of the matrix core, which covers the
+                 * previous chunk's results' latency) */
+                f32x4 b[4];
+                float f[4][4];
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    b[q] = *reinterpret_cast<const f32x4 *>(xb + n * 64 + 16 * q);
+#pragma unroll
+                for (int q = 0; q < 4; q++) dec_e4m3x4(WR[s][q], f[q]);
+                f32x4 pp[2][4];
+                auto mm = [&](int q, f32x4 *o) {
+                    o[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(f[q][0], b[q].x, negz, 0, 0, 0);
+                    o[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(f[q][1], b[q].y, negz, 0, 0, 0);
+                    o[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(f[q][2], b[q].z, negz, 0, 0, 0);
+                    o[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(f[q][3], b[q].w, negz, 0, 0, 0);
+                };
+                float sq[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) sq[q] = scale(SR[s][SC1 ? 0 : q]);
+                auto va = [&](int q, const f32x4 *o) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float d = (o[0][e] + o[1][e]) + (o[2][e] + o[3][e]);
+                        A[q][e] = fmaf(d, sq[q], A[q][e]);
+                    }
+                };
+                mm(0, pp[0]);
+                __builtin_amdgcn_sched_barrier(0);
+                mm(1, pp[1]);
+                __builtin_amdgcn_sched_barrier(0);
+                va(0, pp[0]);
+                __builtin_amdgcn_sched_barrier(0);
+                mm(2, pp[0]);
+                __builtin_amdgcn_sched_barrier(0);
+                va(1, pp[1]);
+                __builtin_amdgcn_sched_barrier(0);
+                mm(3, pp[1]);
+                __builtin_amdgcn_sched_barrier(0);
+                va(2, pp[0]);
+                va(3, pp[1]);
+            }
+        });
+        if (u < U) {
+            f32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] = (A[0][e] + A[1][e]) + (A[2][e] + A[3][e]);
+            /* binary counter over units: unit u's 4-slot sum merges with the
+             * held blocks of 4, 8, 16 and 32 slots while bits 0..3 of u are
+             * set (u is a compile-time constant here) */
+            constexpr bool b0 = u & 1, b1 = u & 2, b2 = u & 4, b3 = u & 8;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (!b0) h4[e] = v[e];
+                else {
+                    const float s1 = h4[e] + v[e];
+                    if (!b1) h8[e] = s1;
+                    else {
+                        const float s2 = h8[e] + s1;
+                        if (!b2) h16[e] = s2;
+                        else {
+                            const float s3 = h16[e] + s2;
+                            if (!b3) h32[e] = s3;
+                            else fin[e] = h32[e] + s3;
+                        }
+                    }
+                }
+            }
+        }
+        /* the next unit's x into the other buffer (last read by unit u - 1,
+         * which every wave finished before the previous barrier), the one
+         * after it requested */
+        if (u + 1 < D::UMAX) {
+            if (u + 1 < U) xstore(xs + ((u + 1) & 1) * D::BUF);
+            __builtin_amdgcn_sched_barrier(0);
+            xload(u + 2);
+            __syncthreads();
+        }
+    });
+    if (row0 >= rows || r >= ntok) return;
+    const f32x4 res = L == 16 ? h16 : L == 32 ? h32 : fin;
+    float *dst = P == 1 ? y : part + (size_t)p * nt * rows;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int rr = row0 + 4 * g + e;
+        if (rr < rows) dst[(size_t)(t0 + r) * rows + rr] = res[e];
+    }
+}
+
+/* The rest of the slot tree per (row, token) from the P part subtrees:
+ * within each 64-slot block the parts' balanced tree, then the blocks in
+ * order (tc <= 32: the parts' tree). */
+__global__ void __launch_bounds__(256)
+k_fp8_mfn_join(float *__restrict__ y, const float *__restrict__ part, int n, int P, int L,
+               int tc)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const int pb = tc >= 64 ? 64 / L : P;      /* parts per 64-slot block */
+    float out = 0.0f;
+    for (int k0 = 0; k0 < P; k0 += pb) {
+        float v = part[(size_t)k0 * n + i];
+        if (pb == 2) v = v + part[(size_t)(k0 + 1) * n + i];
+        else if (pb == 4)
+            v = (v + part[(size_t)(k0 + 1) * n + i]) +
+                (part[(size_t)(k0 + 2) * n + i] + part[(size_t)(k0 + 3) * n + i]);
+        out = k0 == 0 ? v : out + v;
+    }
+    y[i] = out;
+}
+
+/* Slots per part of k_fp8_mfn, or 0 where the VALU batched kernel is the
+ * faster one (same bits either way). L is the largest of 64, 32, 16 with L
+ * nch <= 64 (at most 16 steps per part) and L <= tc, lowered (more parts,
+ * more waves) while fewer than about three waves per SIMD would run. The
+ * form is taken from 8 tokens on, and only when it has at least one wave
+ * per SIMD: below that its 16-token tiles and its serial walk of a part
+ * cost more than they save (us, matrix core / VALU, E8M0: 7168x7168 at 4
+ * tokens 39.5 / 25.3, 8 tokens 40.3 / 46.9, 16 tokens 40.5 / 89.4, 64
+ * tokens 125.5 / 334.7; 576x7168 (288 waves) at 16 tokens 23.6 / 28.1, at 64
+ * tokens 24.7 / 102.7; 24576x1536 at 12 tokens 38.2 / 60.5).
+ * DSV4_GPU_MFN_L overrides the slots within the same bounds. */
+int mfn_slots(const Fp8Geom &g, int rows, int nt)
+{
+    int lmax = 64;
+    while (lmax > 16 && (lmax * g.nch > 64 || lmax > g.tc)) lmax >>= 1;
+    if (lmax * g.nch > 64 || lmax > g.tc || g.tc % lmax) return 0;
+    const long long tiles = (long long)((rows + 15) / 16) * ((nt + 15) / 16);
+    int L = lmax;
+    const int e = env_int("DSV4_GPU_MFN_L", 0);
+    if (e) {
+        if (!((e == 16 || e == 32 || e == 64) && e <= lmax && g.tc % e == 0)) return 0;
+        L = e;
+    } else {
+        while (L > 16 && tiles * (g.tc / L) < 3 * 4 * (long long)cu_count()) L >>= 1;
+        if (nt < 8 || tiles * (g.tc / L) < 4 * (long long)cu_count()) return 0;
+    }
+    return L;
+}
+
+bool mfn_ok(const Fp8Geom &g, int cols, int blk_r, int nt, const float *x)
+{
+    return env_int("DSV4_GPU_FP8_MFN", 1) != 0 && nt >= 2 && (cols & 63) == 0 &&
+           g.tc >= 16 && g.tc <= 256 && (blk_r & 15) == 0 && (((uintptr_t)x) & 15) == 0;
+}
+
+size_t mfn_scratch_bytes(int rows, int cols, int nt)
+{
+    Fp8Geom g;
+    if (nt < 2 || !fp8_geom(cols, &g)) return 0;
+    const int L = mfn_slots(g, rows, nt);
+    if (!L || g.tc / L == 1) return 0;
+    return sizeof(float) * (size_t)(g.tc / L) * nt * rows;
+}
+
+template <int SF>
+int launch_gemv_mfn(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
+                    const void *S, int rows, int cols, int sc, int blk_r, int blk_c, int nt,
+                    hipStream_t st, void *scratch)
+{
+    const int L = mfn_slots(g, rows, nt);
+    if (!L) return -1;
+    const int P = g.tc / L;
+    if (P > 1 && !scratch) return -1;
+    bool ok = true;
+    auto go = [&](auto kern, size_t lds) {         /* two units of x, <= 33 KB */
+        if (lds > 64 * 1024) { ok = false; return; }
+        const dim3 grid((rows + 127) / 128, P, (nt + 15) / 16);
+        hipLaunchKernelGGL(kern, grid, dim3(512), lds, st, y, (float *)scratch, x, W, S, rows,
+                           cols, sc, blk_r, blk_c, g.tc, L, nt);
+    };
+    const bool sc1 = blk_c % 64 == 0;
+    switch (g.nch) {
+    case 1: sc1 ? go(k_fp8_mfn<SF, true, 1>, 8 * MfnDim<1>::BUF) : go(k_fp8_mfn<SF, false, 1>, 8 * MfnDim<1>::BUF); break;
+    case 2: sc1 ? go(k_fp8_mfn<SF, true, 2>, 8 * MfnDim<2>::BUF) : go(k_fp8_mfn<SF, false, 2>, 8 * MfnDim<2>::BUF); break;
+    case 3: sc1 ? go(k_fp8_mfn<SF, true, 3>, 8 * MfnDim<3>::BUF) : go(k_fp8_mfn<SF, false, 3>, 8 * MfnDim<3>::BUF); break;
+    default: sc1 ? go(k_fp8_mfn<SF, true, 4>, 8 * MfnDim<4>::BUF) : go(k_fp8_mfn<SF, false, 4>, 8 * MfnDim<4>::BUF); break;
+    }
+    if (!ok) return -1;
+    if (P > 1) {
+        const int n = nt * rows;
+        hipLaunchKernelGGL(k_fp8_mfn_join, dim3((n + 255) / 256), dim3(256), 0, st, y,
+                           (const float *)scratch, n, P, L, g.tc);
+    }
+    return 0;
+}
+
 template <int SF>
 void launch_gemv_n(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
                    const void *S, int rows, int cols, int sc, int blk_r,
-                   int blk_c, int nt, hipStream_t st)
+                   int blk_c, int nt, hipStream_t st, void *scratch)
 {
+    if (mfn_ok(g, cols, blk_r, nt, x) &&
+        launch_gemv_mfn<SF>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st, scratch) == 0)
+        return;
     /* two or more tokens: x through LDS, the largest token block that fits
      * and the tokens fill (8 x 4096, 4 x 7168, 2 x 16384 columns) */
     const size_t cap = dsv4_lds_limit() - 2048;
@@ -1024,6 +1384,11 @@ int dsv4_fp8_gemv_groups_launch(float *y, const float *x, const uint8_t *W,
     return fp8_gemv(y, x, W, S, sfmt, rows, cols, blk_r, blk_c, gp, st);
 }
 
+size_t dsv4_fp8_n_scratch_bytes(int rows, int cols, int nt)
+{
+    return std::max(dsv4_fp8_mxn_scratch_bytes(cols, nt), mfn_scratch_bytes(rows, cols, nt));
+}
+
 int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,
                            const void *S, int sfmt, int rows, int cols,
                            int blk_r, int blk_c, int nt, hipStream_t st, void *xscratch)
@@ -1044,9 +1409,9 @@ int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,
     if (fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c)) {
         if (chunked_ok(x, W, "fp8 gemv_n") != 0) return -1;
         if (sfmt == 0)
-            launch_gemv_n<0>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st);
+            launch_gemv_n<0>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st, xscratch);
         else
-            launch_gemv_n<1>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st);
+            launch_gemv_n<1>(g, y, x, W, S, rows, cols, sc, blk_r, blk_c, nt, st, xscratch);
     } else {
         const int grid = (rows + 3) / 4;
         if (sfmt == 0)

@@ -581,7 +581,7 @@ void dsv4_gpu_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
     const size_t xo = s.in(x, (size_t)nt * r->cols * sizeof(float));
     const size_t yo = s.add((size_t)nt * m->rows * sizeof(float));
     const bool fp8 = r->wdt != DSV4_WFP4 && r->wdt != DSV4_WBF16;
-    const size_t to = fp8 ? s.add(dsv4_fp8_mxn_scratch_bytes(r->cols, nt)) : 0;
+    const size_t to = fp8 ? s.add(dsv4_fp8_n_scratch_bytes(m->rows, r->cols, nt)) : 0;
     size_t end;
     if (stage_push(s, &end) != 0) abort();
     int rc = 0;
@@ -628,7 +628,7 @@ int dsv4_gpu_fp8_gemv_n_d(float *d_y, const float *d_x, const uint8_t *d_w,
         DSV4_ERR("fp8_gemv_n_d: bad arguments (nt %d)", nt);
         return -1;
     }
-    if (scratch_reserve(g_xsplit, dsv4_fp8_mxn_scratch_bytes(cols, nt)) != 0) return -1;
+    if (scratch_reserve(g_xsplit, dsv4_fp8_n_scratch_bytes(rows, cols, nt)) != 0) return -1;
     return dsv4_fp8_gemv_n_launch(d_y, d_x, d_w, d_s, scale_fmt, rows, cols, 128, 128, nt,
                                   as_stream(stream), g_xsplit.p);
 }

@@ -130,8 +130,11 @@ int dsv4_embed_row_launch(float *d_dst, const void *d_table, int wdt, long long 
                           int hidden, hipStream_t st);
 
 /* Batched: y[nt][rows], x[nt][cols]; per (row, token) bit-identical to the
- * GEMV above. xscratch: optional device memory of dsv4_fp8_mxn_scratch_bytes
- * for the matrix-core form's split of x. */
+ * GEMV above. xscratch: device memory of dsv4_fp8_n_scratch_bytes(rows, cols,
+ * nt) bytes, for the E8M0 matrix-core form's split of x or the f32
+ * matrix-core form's part sums (without it those forms fall back to kernels
+ * that need none, with the same bits). */
+size_t dsv4_fp8_n_scratch_bytes(int rows, int cols, int nt);
 int dsv4_fp8_gemv_n_launch(float *y, const float *x, const uint8_t *W,
                            const void *S, int sfmt, int rows, int cols,
                            int blk_r, int blk_c, int nt, hipStream_t st,

@@ -213,6 +213,58 @@ def test_batched_bit_identical(gpu, dsv4, monkeypatch, rows, cols, nt, form):
     assert common.vec_rel_err(yn, oracle.matmul_fp8(x, W, Se)) < TOL
 
 
+def _same_bits_or_nan(a, b):
+    """NaN where the other is NaN (any payload), the same bits elsewhere."""
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    nan = np.isnan(a)
+    return np.array_equal(nan, np.isnan(b)) and common.bits_equal(a[~nan], b[~nan])
+
+
+@pytest.mark.parametrize("scales", ["e8m0", "f32"])
+@pytest.mark.parametrize("slots", ["0", "16", "32", "64"])
+def test_batched_matrix_core_f32_chains_keep_bits(gpu, dsv4, monkeypatch, slots, scales):
+    """The batched kernel for columns a multiple of 64 (k_fp8_mfn) runs the
+    GEMV's four fmaf chains per chunk on v_mfma_f32_16x16x4f32 and the rest
+    of its arithmetic on the VALU. Against the single-token GEMV and the VALU
+    batched kernel (DSV4_GPU_FP8_MFN=0), bit for bit, for every part size
+    DSV4_GPU_MFN_L (0: the launcher's rule, which keeps small batches and
+    small launches on the VALU kernel; a size a shape does not take falls
+    back to the VALU kernel), both scale formats, 16 to 256 row slots (1024
+    to 16384 columns, and 512 = 32 slots), 1 to 4 chunks per slot, ragged
+    row tiles and token tiles, a token of signed zeros against zero codes of
+    both signs, a token of subnormals, and a token with inf."""
+    cases = ((300, 1536, 5), (129, 7168, 37), (70, 16384, 2), (33, 4096, 17), (18, 3072, 7),
+             (16, 512, 3), (47, 1024, 19), (200, 2048, 64), (40, 6144, 4), (7168, 7168, 64),
+             (24, 256, 5))
+    for rows, cols, nt in cases:
+        rng = np.random.default_rng(rows * 7 + cols + nt)
+        W = common.fp8_codes(rng, (rows, cols))
+        W[:, : cols // 8] = np.where(rng.random((rows, cols // 8)) < 0.5, 0x00, 0x80)
+        Sf, Se = common.fp8_scales(rng, rows, cols)
+        x = rng.standard_normal((nt, cols), dtype=np.float32)
+        x[1, : cols // 8] = -0.0
+        x[1, cols // 8:] = np.where(rng.random(cols - cols // 8) < 0.5, 0.0, -0.0)
+        if nt > 2:
+            x[2] = (rng.standard_normal(cols) * 1e-39).astype(np.float32)   # subnormal
+        if nt > 3:
+            x[3, 5] = np.inf
+        S = Se if scales == "e8m0" else Sf
+        _, m = _run(dsv4, W, S, x[0], f32s=scales == "f32")
+        monkeypatch.setenv("DSV4_GPU_FP8_MFN", "0")
+        ref = dsv4.mmq_n(m, x)
+        monkeypatch.setenv("DSV4_GPU_FP8_MFN", "1")
+        monkeypatch.setenv("DSV4_GPU_MFN_L", slots)
+        say("fp8 mfn %dx%d nt %d L %s %s" % (rows, cols, nt, slots, scales))
+        yn = dsv4.mmq_n(m, x)
+        monkeypatch.delenv("DSV4_GPU_MFN_L")
+        assert _same_bits_or_nan(yn, ref), (rows, cols, nt, slots)
+        for t in range(nt):
+            assert _same_bits_or_nan(yn[t], dsv4.mmq(m, x[t])), (rows, cols, t)
+        fin = np.isfinite(x).all(axis=1)
+        assert common.vec_rel_err(yn[fin], oracle.matmul_fp8(x[fin], W, S)) < TOL
+
+
 @pytest.mark.parametrize("ntmax", ["1", "3", "5", "6", "7"])
 def test_batched_token_tiles_keep_bits(gpu, dsv4, monkeypatch, ntmax):
     """DSV4_GPU_MXN_NT (column tiles of five tokens per workgroup, so how many

@@ -925,7 +925,7 @@ k_fp8_mfn(float *__restrict__ y, float *__restrict__ part, const float *__restri
         sfor<NCH>([&](auto nc) {
             constexpr int n = decltype(nc)::value;
             constexpr int s = u * NCH + n;
-            if (s + MFN_PF < 16)
+            if constexpr (s + MFN_PF < 16)
                 wload(std::integral_constant<int, s + MFN_PF>{}, (s + MFN_PF) / NCH,
                       (s + MFN_PF) % NCH);
             if (u < U && group(u, n) >= 0) {

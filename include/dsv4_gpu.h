@@ -127,7 +127,12 @@ void dsv4_gpu_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt);
 
 /* Device-resident GEMV on raw device buffers, stream-ordered:
  * d_y[rows] = dequant(d_w, d_s) . d_x[cols], 128x128 blocks. scale_fmt 0 =
- * E8M0 bytes, 1 = fp32. What dsv4_gpu_mmq runs after staging. */
+ * E8M0 bytes, 1 = fp32. What dsv4_gpu_mmq runs after staging. d_x and d_w
+ * must be 16-byte aligned wherever cols is a multiple of 16 (the chunked
+ * kernels read 16-byte pieces); an unaligned pointer is refused (-1), never
+ * sent to other arithmetic, so a matrix's bits do not depend on where the
+ * caller's buffers lie. The arithmetic follows from the scale format and the
+ * shape alone (and the process's DSV4_GPU_FP8_MX). */
 int dsv4_gpu_fp8_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
                         const void *d_s, int scale_fmt, int rows, int cols,
                         void *stream);
@@ -135,7 +140,8 @@ int dsv4_gpu_fp8_gemv_d(float *d_y, const float *d_x, const uint8_t *d_w,
 /* The batched form (prefill, the k_mmq_fp8_n contract of dsv4_cuda.cu:161-
  * 230): d_y[nt][rows] for d_x[nt][cols], each (row, token) bit-identical to
  * dsv4_gpu_fp8_gemv_d on that token. nt <= DSV4_MAX_BATCH. What
- * dsv4_gpu_mmq_n runs after staging. */
+ * dsv4_gpu_mmq_n runs after staging. The same alignment rule; its scratch
+ * (x's term planes or part sums) is the library's, grown on demand. */
 int dsv4_gpu_fp8_gemv_n_d(float *d_y, const float *d_x, const uint8_t *d_w,
                           const void *d_s, int scale_fmt, int rows, int cols, int nt,
                           void *stream);

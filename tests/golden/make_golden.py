@@ -11,7 +11,8 @@ inputs is stored so that generator drift is told apart from an oracle error).
 Run in the container where /root/reference exists (oracle/_ref must be
 built); the tests then read the .npz files with numpy.load (no pickles).
 
-    python tests/golden/make_golden.py            # small vectors, NaN top-k
+    python tests/golden/make_golden.py            # small vectors, NaN top-k,
+                                                  # batched FP8 at a matrix-core shape
     python tests/golden/make_golden.py --c4       # + C4 top-2048 (~40 s)
 """
 import hashlib
@@ -194,6 +195,20 @@ def c4_inputs():
     return codes, s, deq, q, w
 
 
+def fp8n_matrix_core():
+    """Batched FP8 at a shape the f32 matrix-core batched kernel takes
+    (columns a multiple of 64, at least 8 tokens, two token tiles, ragged):
+    the reference's dsv4_matmul_fp8_n on it."""
+    rng = np.random.default_rng(20261202)
+    rows, cols, nt = 192, 1024, 17
+    W = common.fp8_codes(rng, (rows, cols))
+    S = rng.integers(120, 135, size=((rows + 127) // 128, cols // 128)).astype(np.uint8)
+    x = rng.standard_normal((nt, cols)).astype(np.float32)
+    np.savez_compressed(os.path.join(HERE, "golden_fp8n_mc.npz"), W=W, S=S, x=x,
+                        y=oracle.ref_matmul_fp8_n(x, W, S))
+    print("golden_fp8n_mc.npz written")
+
+
 def c4():
     codes, s, deq, q, w = c4_inputs()
     sc = oracle.ref_indexer_score(q, deq, w)
@@ -210,5 +225,6 @@ if __name__ == "__main__":
         sys.exit("oracle/_ref/libdsv4ref.so is not built (make -C oracle)")
     small()
     nan_topk()
+    fp8n_matrix_core()
     if "--c4" in sys.argv:
         c4()

@@ -35,6 +35,16 @@ def test_fp8_batched_golden():
     assert np.array_equal(bits(y), bits(G["fp8n_y"]))
 
 
+GM = np.load(os.path.join(HERE, "golden", "golden_fp8n_mc.npz"))
+
+
+def test_fp8_batched_matrix_core_shape_golden():
+    """dsv4_matmul_fp8_n at 192x1024, 17 tokens (a shape the batched f32
+    matrix-core kernel takes): the oracle bit for bit."""
+    y = oracle.matmul_fp8(GM["x"], GM["W"], GM["S"])
+    assert np.array_equal(bits(y), bits(GM["y"]))
+
+
 def test_bf16_gemv_golden():
     y = oracle.matmul_bf16(G["bf16_x"], G["bf16_W"])
     assert np.array_equal(bits(y), bits(G["bf16_y"]))

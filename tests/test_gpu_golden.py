@@ -40,6 +40,29 @@ def test_fp8_gemv_golden(gpu, dsv4):
         assert common.bits_equal(yn[t], dsv4.mmq(m, G["fp8n_x"][t]))
 
 
+GM = np.load(os.path.join(HERE, "golden", "golden_fp8n_mc.npz"))
+
+
+@pytest.mark.parametrize("slots", ["16", "32", "64", "0"])
+def test_fp8_batched_matrix_core_golden(gpu, dsv4, monkeypatch, slots):
+    """The compiled reference's dsv4_matmul_fp8_n at 192x1024, 17 tokens,
+    against mmq_n on the f32 matrix-core batched kernel (DSV4_GPU_MFN_L
+    16 / 32 / 64: four, two or one part per row, with and without the join)
+    and on the launcher's rule (0: this small launch takes the VALU kernel):
+    within 1e-5, and every token bit-identical to the single-token GEMV."""
+    W, S, x = GM["W"], GM["S"], GM["x"]
+    _keep.extend([W, S])
+    m = dsv4.qmat(W, S)
+    assert gpu.dsv4_gpu_upload(ctypes.byref(m)) == 0
+    monkeypatch.setenv("DSV4_GPU_MFN_L", slots)
+    yn = dsv4.mmq_n(m, x)
+    err = common.vec_rel_err(yn, GM["y"])
+    print("fp8 batched golden (L %s): worst rel %.3g" % (slots, err), flush=True)
+    assert err < TOL
+    for t in range(yn.shape[0]):
+        assert common.bits_equal(yn[t], dsv4.mmq(m, x[t])), t
+
+
 def test_moe_golden(gpu, dsv4):
     k = G["moe_w"].size
     hidden, inter = G["moe_x"].size, G["moe_w1_0"].shape[0]

@@ -137,13 +137,9 @@ void b16n_launch(const B16Geom &g, float *y, const float *x, const uint16_t *W, 
 {
     constexpr int R = NCH <= 4 ? 4 : 2;
     static bool opted = false;                  /* up to 64 KB of x in LDS */
-    if (!opted) {
-        (void)hipFuncSetAttribute((const void *)k_bf16_gemv_n<NCH, R>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  16384 * (int)sizeof(float) + 4 * R * 8 * (int)sizeof(float));
-        (void)hipGetLastError();
-        opted = true;
-    }
+    if (!opted)
+        opted = dsv4_lds_optin((const void *)k_bf16_gemv_n<NCH, R>,
+                               16384 * sizeof(float) + 4 * R * 8 * sizeof(float), "bf16 gemv_n");
     int tbx = 16384 / cols;                     /* tokens per LDS block */
     if (tbx > 8) tbx = 8;
     if (tbx > nt) tbx = nt;

@@ -517,7 +517,8 @@ Fp8Plan fp8_plan(const Fp8Geom &g, int R, int rows, int cols, int wgs_per_cu, in
      * measured faster on MI355X for narrow rows (24576x1536: 12.2 -> 11.8
      * us) and the widest (7168x16384: 24.8 -> 24.1 us), and within noise
      * or slower between them. */
-    p.xl = g.wg == 256 && (cols & 3) == 0 && (cols <= 2048 || cols >= 16384);
+    p.xl = g.wg == 256 && (cols & 3) == 0 &&
+           env_int("DSV4_GPU_FP8_XL", cols <= 2048 || cols >= 16384) != 0;
     const int step_rows = g.rg * R;
     const int nsteps = (rows + step_rows - 1) / step_rows;
     const int want = (wgs_per_cu * cu_count() + ngroups - 1) / ngroups;
@@ -543,13 +544,9 @@ void launch_gemv(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
     const size_t lds = p.lds;
     if (xl) {
         static bool opted = false;                  /* x of up to 64 KB + partials */
-        if (!opted) {
-            (void)hipFuncSetAttribute((const void *)k_fp8_gemv<NCH, R, SF, PF, 1>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      (int)dsv4_lds_limit());
-            (void)hipGetLastError();
-            opted = true;
-        }
+        if (!opted)
+            opted = dsv4_lds_optin((const void *)k_fp8_gemv<NCH, R, SF, PF, 1>,
+                                   dsv4_lds_limit(), "fp8 gemv");
     }
     if (xl)
         hipLaunchKernelGGL((k_fp8_gemv<NCH, R, SF, PF, 1>), dim3(grid, gp.n), dim3(g.wg), lds,
@@ -731,13 +728,9 @@ void launch_gemv_nl(const Fp8Geom &g, float *y, const float *x, const uint8_t *W
 {
     constexpr int RR = 2;
     static bool opted = false;
-    if (!opted) {
-        (void)hipFuncSetAttribute((const void *)k_fp8_gemv_nl<NCH, SF, TB, RR>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)dsv4_lds_limit());
-        (void)hipGetLastError();
-        opted = true;
-    }
+    if (!opted)
+        opted = dsv4_lds_optin((const void *)k_fp8_gemv_nl<NCH, SF, TB, RR>, dsv4_lds_limit(),
+                               "fp8 gemv_n");
     const int step = RR * (512 / g.tc);
     /* about one workgroup per CU: each stages every token block once */
     const int want = cu_count();
@@ -835,7 +828,6 @@ k_fp8_mfn(float *__restrict__ y, float *__restrict__ part, const float *__restri
     const int ch = cols >> 4;
     const int r = lane & 15, g = lane >> 4;
     const int wrow0 = min(row0, rows - 1);
-    const size_t wrow = (size_t)min(wrow0 + r, rows - 1) * cols;
     const size_t srow = (size_t)(wrow0 / blk_r) * sc;
     const int U = L >> 2;                      /* units, <= D::UMAX */
 
@@ -1182,11 +1174,19 @@ int chunked_ok(const float *x, const uint8_t *W, const char *what)
 
 /* The VALU form's launch parameters for a matrix of rows x cols: R rows per
  * thread per step (at most blk_r's largest power-of-two divisor up to 4),
- * the next step prefetched or not, workgroups per CU. Defaults from a sweep
- * over the C1/C2 shapes on MI355X (R in 1, 2, 4; prefetch on/off; 1-8
- * workgroups per CU): two rows per thread, prefetch only where the matrix
- * is short, two workgroups per CU (four when rows are narrow). The
- * environment can override each. None of these changes a row's arithmetic. */
+ * the next step prefetched or not, workgroups per CU. None of these changes
+ * a row's arithmetic, and the environment can override each. The rule, from
+ * sweeps over the C1/C2 shapes on MI355X (R in 1, 2, 4; prefetch on/off;
+ * x through LDS or not; 1-8 workgroups per CU; cold, us):
+ *   - two workgroups per CU (four when rows are narrow, cols < 4096);
+ *   - rows of 16384 columns: one row per step with the next prefetched
+ *     (7168x16384: 21.5 -> 21.0; two rows with prefetch 21.3);
+ *   - otherwise two rows per step, prefetched only where the matrix is
+ *     short (rows <= 4096), unless two rows per step leave the grid short
+ *     of workgroups, so that some CUs get fewer than others: then one
+ *     (7168x7168: 448 workgroups at two rows, 512 at one; 12.0 -> 11.5).
+ *     The LM head keeps two (its grid is full either way, and one row per
+ *     step measured 147 against 137.5). */
 struct Fp8Valu {
     int R, pf, wpc;
 };
@@ -1194,13 +1194,26 @@ struct Fp8Valu {
 Fp8Valu fp8_valu(int rows, int cols, int blk_r)
 {
     Fp8Valu v;
-    int R = env_int("DSV4_GPU_FP8_R", 2);
+    v.wpc = env_int("DSV4_GPU_FP8_WPC", cols >= 4096 ? 2 : 4);
+    if (v.wpc <= 0) v.wpc = 2;
+    int R = 2, pf = rows <= 4096 ? 1 : 0;
+    Fp8Geom g;
+    if (fp8_geom(cols, &g)) {
+        if (g.tc == 256) {
+            R = 1;
+            pf = 1;
+        } else if (rows > 4096) {
+            const int want = v.wpc * cu_count();
+            if (fp8_plan(g, 2, rows, cols, v.wpc, 1).grid * 16 < want * 15 &&
+                fp8_plan(g, 1, rows, cols, v.wpc, 1).grid * 16 >= want * 15)
+                R = 1;
+        }
+    }
+    R = env_int("DSV4_GPU_FP8_R", R);
     R = R >= 4 ? 4 : R >= 2 ? 2 : 1;
     while (blk_r % R) R >>= 1;                   /* a step stays in one row block */
     v.R = R;
-    v.pf = env_int("DSV4_GPU_FP8_PF", rows <= 4096 ? 1 : 0);
-    v.wpc = env_int("DSV4_GPU_FP8_WPC", cols >= 4096 ? 2 : 4);
-    if (v.wpc <= 0) v.wpc = 2;
+    v.pf = env_int("DSV4_GPU_FP8_PF", pf);
     return v;
 }
 
@@ -1537,16 +1550,11 @@ int dsv4_qproj_launch(const float *qr, int cols, const float *nw, float eps, int
     static bool opted = false;
     const size_t lds = pf.lds + sizeof(float) * (size_t)cols;   /* + the norm's weights */
     if (!opted) {
-        (void)hipFuncSetAttribute((const void *)k_qproj<1, 2, 0>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)dsv4_lds_limit());
-        (void)hipFuncSetAttribute((const void *)k_qproj<2, 2, 0>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)dsv4_lds_limit());
-        (void)hipFuncSetAttribute((const void *)k_qproj<1, 2, 1>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)dsv4_lds_limit());
-        (void)hipFuncSetAttribute((const void *)k_qproj<2, 2, 1>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)dsv4_lds_limit());
-        (void)hipGetLastError();
-        opted = true;
+        const size_t cap = dsv4_lds_limit();
+        opted = dsv4_lds_optin((const void *)k_qproj<1, 2, 0>, cap, "q projections") &&
+                dsv4_lds_optin((const void *)k_qproj<2, 2, 0>, cap, "q projections") &&
+                dsv4_lds_optin((const void *)k_qproj<1, 2, 1>, cap, "q projections") &&
+                dsv4_lds_optin((const void *)k_qproj<2, 2, 1>, cap, "q projections");
     }
     if (sfmt == 0) {
         if (g.nch == 1) hipLaunchKernelGGL((k_qproj<1, 2, 0>), grid, dim3(256), lds, st, a);

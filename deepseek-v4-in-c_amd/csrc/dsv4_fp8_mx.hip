@@ -860,14 +860,7 @@ bool xs_uniform(int blk_r, int blk_c)
 template <typename K>
 bool optin(K kernel, const char *name)
 {
-    const hipError_t e = hipFuncSetAttribute((const void *)kernel,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             (int)dsv4_lds_limit());
-    if (e == hipSuccess) return true;
-    (void)hipGetLastError();
-    DSV4_ERR("%s: dynamic LDS opt-in to %zu bytes refused: %s", name, dsv4_lds_limit(),
-             hipGetErrorString(e));
-    return false;
+    return dsv4_lds_optin((const void *)kernel, dsv4_lds_limit(), name);
 }
 
 int mx_cu_count()

@@ -451,6 +451,17 @@ size_t dsv4_lds_limit(void)
     return cached;
 }
 
+bool dsv4_lds_optin(const void *kernel, size_t bytes, const char *what)
+{
+    const hipError_t e =
+        hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e == hipSuccess) return true;
+    (void)hipGetLastError();
+    DSV4_ERR("%s: dynamic LDS opt-in to %zu bytes refused: %s", what, bytes,
+             hipGetErrorString(e));
+    return false;
+}
+
 /* ===================================================================== ABI */
 extern "C" {
 

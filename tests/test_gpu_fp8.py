@@ -354,18 +354,24 @@ def test_e8m0_forms(gpu, dsv4, monkeypatch, form):
 
 @pytest.mark.parametrize("rows,cols", [(7168, 7168), (1536, 1536), (300, 4096), (260, 16384)])
 def test_launch_shape_keeps_bits(gpu, dsv4, monkeypatch, rows, cols):
-    """Rows per thread (DSV4_GPU_FP8_R), prefetch (DSV4_GPU_FP8_PF) and
-    workgroups per CU (DSV4_GPU_FP8_WPC) only reshape the launch: every
-    setting gives the default's bits."""
+    """Rows per thread (DSV4_GPU_FP8_R), prefetch (DSV4_GPU_FP8_PF),
+    workgroups per CU (DSV4_GPU_FP8_WPC) and x through LDS (DSV4_GPU_FP8_XL)
+    only reshape the launch: every setting gives the default's bits."""
     W, Sf, Se, x = common.fp8_problem(51, rows, cols)
     y0, m = _run(dsv4, W, Sf, x, f32s=True)
     assert common.vec_rel_err(y0, oracle.matmul_fp8(x, W, Sf)) < TOL
-    for r, pf, wpc in ((1, 0, 2), (4, 0, 2), (2, 1, 2), (2, 0, 1), (4, 1, 8), (1, 1, 4)):
+    for r, pf, wpc, xl in ((1, 0, 2, None), (4, 0, 2, None), (2, 1, 2, None), (2, 0, 1, None),
+                           (4, 1, 8, None), (1, 1, 4, None), (1, 1, 2, 1), (2, 0, 2, 0),
+                           (4, 1, 2, 1)):
         monkeypatch.setenv("DSV4_GPU_FP8_R", str(r))
         monkeypatch.setenv("DSV4_GPU_FP8_PF", str(pf))
         monkeypatch.setenv("DSV4_GPU_FP8_WPC", str(wpc))
-        say("fp8 %dx%d R %d PF %d WPC %d" % (rows, cols, r, pf, wpc))
-        assert common.bits_equal(dsv4.mmq(m, x), y0), (r, pf, wpc)
+        if xl is None:
+            monkeypatch.delenv("DSV4_GPU_FP8_XL", raising=False)
+        else:
+            monkeypatch.setenv("DSV4_GPU_FP8_XL", str(xl))
+        say("fp8 %dx%d R %d PF %d WPC %d XL %s" % (rows, cols, r, pf, wpc, xl))
+        assert common.bits_equal(dsv4.mmq(m, x), y0), (r, pf, wpc, xl)
 
 
 def test_row_range_views(gpu, dsv4):

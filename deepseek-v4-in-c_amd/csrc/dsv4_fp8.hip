@@ -1176,37 +1176,62 @@ int chunked_ok(const float *x, const uint8_t *W, const char *what)
  * thread per step (at most blk_r's largest power-of-two divisor up to 4),
  * the next step prefetched or not, workgroups per CU. None of these changes
  * a row's arithmetic, and the environment can override each. The rule, from
- * sweeps over the C1/C2 shapes on MI355X (R in 1, 2, 4; prefetch on/off;
- * x through LDS or not; 1-8 workgroups per CU; cold, us):
+ * sweeps over the C1/C2 and attention-block shapes on MI355X (R in 1, 2, 4;
+ * prefetch on/off; x through LDS or not; 1-8 workgroups per CU; cold, us):
  *   - two workgroups per CU (four when rows are narrow, cols < 4096);
  *   - rows of 16384 columns: one row per step with the next prefetched
  *     (7168x16384: 21.5 -> 21.0; two rows with prefetch 21.3);
- *   - otherwise two rows per step, prefetched only where the matrix is
- *     short (rows <= 4096), unless two rows per step leave the grid short
- *     of workgroups, so that some CUs get fewer than others: then one
- *     (7168x7168: 448 workgroups at two rows, 512 at one; 12.0 -> 11.5).
- *     The LM head keeps two (its grid is full either way, and one row per
- *     step measured 147 against 137.5). */
+ *   - more than 4096 rows: two rows per step without prefetch, unless that
+ *     grid leaves its last round of workgroups short, so that some CUs get
+ *     fewer than others, while one row per step fills it (7168x7168: 448
+ *     workgroups at two rows, 512 at one; 12.0 -> 11.5). The LM head keeps
+ *     two (505 workgroups; one row per step measured 147 against 137.5);
+ *   - at most 4096 rows of at least 4096 columns: one row per step without
+ *     prefetch where that grid is one round of workgroups (1024x4096 4.4 ->
+ *     3.8, 512x4096 4.2 -> 3.6, either scale format), or, with E8M0 scales,
+ *     where its rounds are full (4096x8192 9.9 -> 9.1, 4096x4096 6.2 ->
+ *     6.1; with fp32 scales, whose step loads four bytes of scale per
+ *     chunk, 9.5 either way and 6.1 against 6.2 for two rows);
+ *     else four rows per step without prefetch where only that grid is
+ *     full (1536x7168: 384 workgroups at two rows, 192 at four; 5.9 ->
+ *     5.7); otherwise, and for narrower rows, two rows per step with the
+ *     next prefetched (576x7168: 4.3 at two rows, 4.6 at one, whose 288
+ *     workgroups spill onto 32 CUs).
+ * tuned = false keeps the base rule (two rows; prefetch where rows <= 4096)
+ * for the attention block's combined launches, which are built for it. */
 struct Fp8Valu {
     int R, pf, wpc;
 };
 
-Fp8Valu fp8_valu(int rows, int cols, int blk_r)
+Fp8Valu fp8_valu(int rows, int cols, int blk_r, int sfmt, bool tuned = true)
 {
     Fp8Valu v;
     v.wpc = env_int("DSV4_GPU_FP8_WPC", cols >= 4096 ? 2 : 4);
     if (v.wpc <= 0) v.wpc = 2;
     int R = 2, pf = rows <= 4096 ? 1 : 0;
     Fp8Geom g;
-    if (fp8_geom(cols, &g)) {
+    if (tuned && fp8_geom(cols, &g)) {
+        const int cu = cu_count();
+        /* every round of workgroups but the last is full; the last at least
+         * 15/16 full, or the grid is a single round */
+        auto grid = [&](int r) { return fp8_plan(g, r, rows, cols, v.wpc, 1).grid; };
+        auto full = [&](int r) {
+            const int n = grid(r), last = n % cu;
+            return n <= cu || last == 0 || last * 16 >= cu * 15;
+        };
         if (g.tc == 256) {
             R = 1;
             pf = 1;
         } else if (rows > 4096) {
-            const int want = v.wpc * cu_count();
-            if (fp8_plan(g, 2, rows, cols, v.wpc, 1).grid * 16 < want * 15 &&
-                fp8_plan(g, 1, rows, cols, v.wpc, 1).grid * 16 >= want * 15)
+            if (!full(2) && full(1)) R = 1;
+        } else if (cols >= 4096) {
+            if (sfmt == 0 ? full(1) : grid(1) <= cu) {
                 R = 1;
+                pf = 0;
+            } else if (!full(2) && full(4)) {
+                R = 4;
+                pf = 0;
+            }
         }
     }
     R = env_int("DSV4_GPU_FP8_R", R);
@@ -1244,7 +1269,7 @@ int fp8_gemv(float *y, const float *x, const uint8_t *W, const void *S, int sfmt
     if (fp8_geom(cols, &g) && blocking_ok(blk_r, blk_c)) {
         if (chunked_ok(x, W, "fp8 gemv") != 0) return -1;
         /* launch shape (fp8_valu): none of it changes a row's arithmetic */
-        const Fp8Valu v = fp8_valu(rows, cols, blk_r);
+        const Fp8Valu v = fp8_valu(rows, cols, blk_r, sfmt);
         const int R = v.R, pf = v.pf, wpc = v.wpc;
         if (sfmt == 0) {
             if (pf) launch_gemv_r<0, 1>(g, R, y, x, W, S, rows, cols, sc, blk_r, blk_c, wpc, gp, st);
@@ -1468,7 +1493,7 @@ int dsv4_xproj_launch(const float *x, int cols, int sfmt, int blk_r, int blk_c, 
         rmb = rb[i] > rmb ? rb[i] : rmb;
     }
     if (!ok) return two();
-    const Fp8Valu v = fp8_valu(rmf, cols, blk_r);
+    const Fp8Valu v = fp8_valu(rmf, cols, blk_r, sfmt, false);
     const Fp8Plan pf = fp8_plan(g, v.R, rmf, cols, v.wpc, nf);
     const B16Plan pb = b16_plan(gb, rmb, nb);
     /* the one combination built: FP8 with 4 chunks per thread, 2 rows per
@@ -1531,7 +1556,7 @@ int dsv4_qproj_launch(const float *qr, int cols, const float *nw, float eps, int
         rm = rf[i] > rm ? rf[i] : rm;
     }
     if (!ok) return two();
-    const Fp8Valu v = fp8_valu(rm, cols, blk_r);
+    const Fp8Valu v = fp8_valu(rm, cols, blk_r, sfmt, false);
     const Fp8Plan pf = fp8_plan(g, v.R, rm, cols, v.wpc, nf);
     /* the combinations built: x through LDS (cols <= 2048), 1 or 2 chunks
      * per thread, 2 rows per step, no prefetch (wq_b's rows), 256 threads */

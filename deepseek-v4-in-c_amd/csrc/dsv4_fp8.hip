@@ -1557,9 +1557,16 @@ int dsv4_qproj_launch(const float *qr, int cols, const float *nw, float eps, int
     }
     if (!ok) return two();
     const Fp8Valu v = fp8_valu(rm, cols, blk_r, sfmt, false);
-    const Fp8Plan pf = fp8_plan(g, v.R, rm, cols, v.wpc, nf);
+    /* rows per step: 4 (a step stays in one row block), or 2. Four measured
+     * faster for the block's q GEMVs (wq_b 32768x1024 and the indexer's
+     * 8192x1024 with the prep step: 77.1 -> 74.9 us per CSA step); one row
+     * with no prefetch in the x launch measured slower (78.7), so that
+     * launch keeps two rows with prefetch. */
+    const int qrr = env_int("DSV4_GPU_QPROJ_R", 4) >= 4 && blk_r % 4 == 0 ? 4 : 2;
+    const Fp8Plan pf = fp8_plan(g, qrr, rm, cols, v.wpc, nf);
     /* the combinations built: x through LDS (cols <= 2048), 1 or 2 chunks
-     * per thread, 2 rows per step, no prefetch (wq_b's rows), 256 threads */
+     * per thread, 2 or 4 rows per step, no prefetch (wq_b's rows), 256
+     * threads */
     if (!pf.xl || g.wg != 256 || g.nch > 2 || v.R != 2 || v.pf) return two();
     QProj a;
     a.x = qr; a.nw = nw; a.cols = cols; a.eps = eps;
@@ -1579,15 +1586,21 @@ int dsv4_qproj_launch(const float *qr, int cols, const float *nw, float eps, int
         opted = dsv4_lds_optin((const void *)k_qproj<1, 2, 0>, cap, "q projections") &&
                 dsv4_lds_optin((const void *)k_qproj<2, 2, 0>, cap, "q projections") &&
                 dsv4_lds_optin((const void *)k_qproj<1, 2, 1>, cap, "q projections") &&
-                dsv4_lds_optin((const void *)k_qproj<2, 2, 1>, cap, "q projections");
+                dsv4_lds_optin((const void *)k_qproj<2, 2, 1>, cap, "q projections") &&
+                dsv4_lds_optin((const void *)k_qproj<1, 4, 0>, cap, "q projections") &&
+                dsv4_lds_optin((const void *)k_qproj<2, 4, 0>, cap, "q projections") &&
+                dsv4_lds_optin((const void *)k_qproj<1, 4, 1>, cap, "q projections") &&
+                dsv4_lds_optin((const void *)k_qproj<2, 4, 1>, cap, "q projections");
     }
-    if (sfmt == 0) {
-        if (g.nch == 1) hipLaunchKernelGGL((k_qproj<1, 2, 0>), grid, dim3(256), lds, st, a);
-        else            hipLaunchKernelGGL((k_qproj<2, 2, 0>), grid, dim3(256), lds, st, a);
+#define DSV4_QP(NCH, R, SF) hipLaunchKernelGGL((k_qproj<NCH, R, SF>), grid, dim3(256), lds, st, a)
+    if (qrr == 4) {
+        if (sfmt == 0) { if (g.nch == 1) DSV4_QP(1, 4, 0); else DSV4_QP(2, 4, 0); }
+        else           { if (g.nch == 1) DSV4_QP(1, 4, 1); else DSV4_QP(2, 4, 1); }
     } else {
-        if (g.nch == 1) hipLaunchKernelGGL((k_qproj<1, 2, 1>), grid, dim3(256), lds, st, a);
-        else            hipLaunchKernelGGL((k_qproj<2, 2, 1>), grid, dim3(256), lds, st, a);
+        if (sfmt == 0) { if (g.nch == 1) DSV4_QP(1, 2, 0); else DSV4_QP(2, 2, 0); }
+        else           { if (g.nch == 1) DSV4_QP(1, 2, 1); else DSV4_QP(2, 2, 1); }
     }
+#undef DSV4_QP
     HIP_OK(hipGetLastError(), "q projections launch");
     return 0;
 }

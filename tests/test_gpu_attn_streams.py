@@ -148,7 +148,8 @@ def test_q_projections_with_prep_keep_bits(gpu, dsv4, monkeypatch, ratio):
     indexer's wq_b) norm their workgroup's copy of qr themselves while the
     prep step's ring and compressor jobs run in the same launch: every
     step's output has the bits of the separate sequence (DSV4_GPU_QPROJ=0:
-    the prep launch, qr normed in place, then the listed q GEMVs)."""
+    the prep launch, qr normed in place, then the listed q GEMVs), with four
+    rows per step (the default) or two (DSV4_GPU_QPROJ_R=2)."""
     L, D = gpu, dsv4
     rng = np.random.default_rng(13 + ratio)
     layer = LAYER + 600 + ratio
@@ -158,6 +159,13 @@ def test_q_projections_with_prep_keep_bits(gpu, dsv4, monkeypatch, ratio):
     one = _host_steps(L, layer, X)
     assert np.isfinite(one).all() and np.abs(one).max() > 0.0
     assert L.dsv4_gpu_attn_reset(layer) == 0
+    monkeypatch.setenv("DSV4_GPU_QPROJ_R", "2")
+    print("attn q projections: ratio %d, one launch, two rows per step" % ratio, flush=True)
+    one2 = _host_steps(L, layer, X)
+    assert L.dsv4_gpu_attn_reset(layer) == 0
+    bad = np.nonzero((one.view(np.uint32) != one2.view(np.uint32)).any(axis=1))[0]
+    assert bad.size == 0, "positions %s differ between four and two rows" % bad[:8].tolist()
+    monkeypatch.delenv("DSV4_GPU_QPROJ_R")
     monkeypatch.setenv("DSV4_GPU_QPROJ", "0")
     print("attn q projections: ratio %d, prep then the GEMVs" % ratio, flush=True)
     two = _host_steps(L, layer, X)

@@ -81,58 +81,80 @@ k_comp_close(float *__restrict__ out, float *__restrict__ kvst, float *__restric
     const float wc = live ? w[cc] : 0.0f;
     float mx = -INFINITY;
     double den = 0.0, acc = 0.0;
-    for (int s0 = 0; s0 < slots; s0 += 8) {
-        float sv[8], kv[8];
+    if (slots <= 8) {
+        /* The window and the slide's sources in one batch of loads, all
+         * issued before any store. The slide writes the arrays it reads, so
+         * a load that followed one of its stores could not be moved ahead of
+         * it: as a loop of copies it made one round trip per slot. ov is
+         * ratio 4 (the launcher), so its 8 slots always take this path. */
+        const int chi = ov ? hd + cc : cc;
+        float sv[8], kv[8], ka[4], kb[4], sa[4], sb[4];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const int s = min(s0 + u, slots - 1);
+            const int s = min(u, slots - 1);
             const int col = (ov && s >= ratio) ? hd + cc : cc;
             sv[u] = scst[(size_t)s * width + col];
             kv[u] = kvst[(size_t)s * width + col];
         }
-        /* max first over all slots, so the batch's values stay for the
-         * second pass only when the whole window fits one batch */
-        if (slots <= 8) {
-            for (int u = 0; u < slots; u++) if (sv[u] > mx) mx = sv[u];
-            if (mx != -INFINITY)
-                for (int u = 0; u < slots; u++) {
-                    if (sv[u] == -INFINITY) continue;
-                    const double e = (double)expf(sv[u] - mx);
-                    den += e;
-                    acc += e * (double)kv[u];
-                }
-        } else {
-            for (int u = 0; u < 8 && s0 + u < slots; u++) if (sv[u] > mx) mx = sv[u];
-        }
-    }
-    if (slots > 8 && mx != -INFINITY) {
-        for (int s0 = 0; s0 < slots; s0 += 8) {
-            float sv[8], kv[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int s = min(s0 + u, slots - 1);
-                const int col = (ov && s >= ratio) ? hd + cc : cc;
-                sv[u] = scst[(size_t)s * width + col];
-                kv[u] = kvst[(size_t)s * width + col];
-            }
-            for (int u = 0; u < 8 && s0 + u < slots; u++) {
+        for (int u = 0; u < 4; u++) {
+            const size_t from = (size_t)min(ratio + u, slots - 1) * width;
+            ka[u] = kvst[from + cc];
+            kb[u] = kvst[from + chi];
+            sa[u] = scst[from + cc];
+            sb[u] = scst[from + chi];
+        }
+        for (int u = 0; u < slots; u++) if (sv[u] > mx) mx = sv[u];
+        if (mx != -INFINITY)
+            for (int u = 0; u < slots; u++) {
                 if (sv[u] == -INFINITY) continue;
                 const double e = (double)expf(sv[u] - mx);
                 den += e;
                 acc += e * (double)kv[u];
             }
+        if (live && ov) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (u < ratio) {
+                    const size_t to = (size_t)u * width;
+                    kvst[to + c] = ka[u];
+                    kvst[to + hd + c] = kb[u];
+                    scst[to + c] = sa[u];
+                    scst[to + hd + c] = sb[u];
+                }
+            }
+        }
+    } else {
+        /* more slots (no slide): the max over all of them first, then the
+         * weighted sum, each pass in batches of 8 loads */
+        for (int s0 = 0; s0 < slots; s0 += 8) {
+            float sv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int s = min(s0 + u, slots - 1);
+                sv[u] = scst[(size_t)s * width + cc];
+            }
+            for (int u = 0; u < 8 && s0 + u < slots; u++) if (sv[u] > mx) mx = sv[u];
+        }
+        if (mx != -INFINITY) {
+            for (int s0 = 0; s0 < slots; s0 += 8) {
+                float sv[8], kv[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const int s = min(s0 + u, slots - 1);
+                    sv[u] = scst[(size_t)s * width + cc];
+                    kv[u] = kvst[(size_t)s * width + cc];
+                }
+                for (int u = 0; u < 8 && s0 + u < slots; u++) {
+                    if (sv[u] == -INFINITY) continue;
+                    const double e = (double)expf(sv[u] - mx);
+                    den += e;
+                    acc += e * (double)kv[u];
+                }
+            }
         }
     }
     const float r = (live && mx != -INFINITY) ? (float)(acc / den) : 0.0f;
-    if (live && ov) {
-        for (int s = 0; s < ratio; s++) {
-            const size_t to = (size_t)s * width, from = (size_t)(ratio + s) * width;
-            kvst[to + c] = kvst[from + c];
-            kvst[to + hd + c] = kvst[from + hd + c];
-            scst[to + c] = scst[from + c];
-            scst[to + hd + c] = scst[from + hd + c];
-        }
-    }
     /* RMSNorm over the pooled row (sum of squares in double, a tree) */
     double sq = live ? (double)r * (double)r : 0.0;
 #pragma unroll

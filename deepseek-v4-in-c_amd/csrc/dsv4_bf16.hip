@@ -137,9 +137,11 @@ void b16n_launch(const B16Geom &g, float *y, const float *x, const uint16_t *W, 
 {
     constexpr int R = NCH <= 4 ? 4 : 2;
     static bool opted = false;                  /* up to 64 KB of x in LDS */
-    if (!opted)
-        opted = dsv4_lds_optin((const void *)k_bf16_gemv_n<NCH, R>,
-                               16384 * sizeof(float) + 4 * R * 8 * sizeof(float), "bf16 gemv_n");
+    if (!opted) {
+        (void)dsv4_lds_optin((const void *)k_bf16_gemv_n<NCH, R>,
+                             16384 * sizeof(float) + 4 * R * 8 * sizeof(float), "bf16 gemv_n");
+        opted = true;
+    }
     int tbx = 16384 / cols;                     /* tokens per LDS block */
     if (tbx > 8) tbx = 8;
     if (tbx > nt) tbx = nt;

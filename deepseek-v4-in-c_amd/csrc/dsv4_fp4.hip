@@ -128,9 +128,11 @@ void f4_launch(float *y, const float *x, const uint8_t *W, const uint8_t *S, int
     /* two rows per step in flight while they fit the registers */
     constexpr int R = NCH >= 4 ? 1 : 2;
     static bool opted = false;                  /* x of up to 64 KB in LDS */
-    if (!opted)
-        opted = dsv4_lds_optin((const void *)k_fp4_gemv<NCH, R>, F4_MAXCOLS * sizeof(float),
-                               "fp4 gemv");
+    if (!opted) {
+        (void)dsv4_lds_optin((const void *)k_fp4_gemv<NCH, R>, F4_MAXCOLS * sizeof(float),
+                             "fp4 gemv");
+        opted = true;
+    }
     /* 16 rows per workgroup: enough to amortise the x staging, and rows / 16
      * workgroups fill the chip at expert shapes. */
     const int rows_per_wg = 16;
@@ -212,9 +214,11 @@ void f4n_launch(float *y, const float *x, const uint8_t *W, const uint8_t *S, in
 {
     constexpr int R = NCH >= 4 ? 1 : 2;
     static bool opted = false;                  /* up to 64 KB of x in LDS */
-    if (!opted)
-        opted = dsv4_lds_optin((const void *)k_fp4_gemv_n<NCH, R>, F4_MAXCOLS * sizeof(float),
-                               "fp4 gemv_n");
+    if (!opted) {
+        (void)dsv4_lds_optin((const void *)k_fp4_gemv_n<NCH, R>, F4_MAXCOLS * sizeof(float),
+                             "fp4 gemv_n");
+        opted = true;
+    }
     int tbx = F4_MAXCOLS / cols;                /* tokens per LDS block */
     if (tbx > 8) tbx = 8;
     if (tbx > nt) tbx = nt;

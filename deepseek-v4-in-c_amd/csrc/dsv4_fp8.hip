@@ -544,9 +544,11 @@ void launch_gemv(const Fp8Geom &g, float *y, const float *x, const uint8_t *W,
     const size_t lds = p.lds;
     if (xl) {
         static bool opted = false;                  /* x of up to 64 KB + partials */
-        if (!opted)
-            opted = dsv4_lds_optin((const void *)k_fp8_gemv<NCH, R, SF, PF, 1>,
-                                   dsv4_lds_limit(), "fp8 gemv");
+        if (!opted) {
+            (void)dsv4_lds_optin((const void *)k_fp8_gemv<NCH, R, SF, PF, 1>,
+                                 dsv4_lds_limit(), "fp8 gemv");
+            opted = true;
+        }
     }
     if (xl)
         hipLaunchKernelGGL((k_fp8_gemv<NCH, R, SF, PF, 1>), dim3(grid, gp.n), dim3(g.wg), lds,
@@ -728,9 +730,11 @@ void launch_gemv_nl(const Fp8Geom &g, float *y, const float *x, const uint8_t *W
 {
     constexpr int RR = 2;
     static bool opted = false;
-    if (!opted)
-        opted = dsv4_lds_optin((const void *)k_fp8_gemv_nl<NCH, SF, TB, RR>, dsv4_lds_limit(),
-                               "fp8 gemv_n");
+    if (!opted) {
+        (void)dsv4_lds_optin((const void *)k_fp8_gemv_nl<NCH, SF, TB, RR>, dsv4_lds_limit(),
+                             "fp8 gemv_n");
+        opted = true;
+    }
     const int step = RR * (512 / g.tc);
     /* about one workgroup per CU: each stages every token block once */
     const int want = cu_count();
@@ -1179,8 +1183,9 @@ int chunked_ok(const float *x, const uint8_t *W, const char *what)
  * sweeps over the C1/C2 and attention-block shapes on MI355X (R in 1, 2, 4;
  * prefetch on/off; x through LDS or not; 1-8 workgroups per CU; cold, us):
  *   - two workgroups per CU (four when rows are narrow, cols < 4096);
- *   - rows of 16384 columns: one row per step with the next prefetched
- *     (7168x16384: 21.5 -> 21.0; two rows with prefetch 21.3);
+ *   - rows of 16384 columns with fp32 scales: one row per step with the
+ *     next prefetched (7168x16384: 21.7-22.2 -> 21.1-21.3); with E8M0
+ *     scales the base below (21.2-21.4 against 22.4-22.5 for one row);
  *   - more than 4096 rows: two rows per step without prefetch, unless that
  *     grid leaves its last round of workgroups short, so that some CUs get
  *     fewer than others, while one row per step fills it (7168x7168: 448
@@ -1220,8 +1225,10 @@ Fp8Valu fp8_valu(int rows, int cols, int blk_r, int sfmt, bool tuned = true)
             return n <= cu || last == 0 || last * 16 >= cu * 15;
         };
         if (g.tc == 256) {
-            R = 1;
-            pf = 1;
+            if (sfmt != 0) {
+                R = 1;
+                pf = 1;
+            }
         } else if (rows > 4096) {
             if (!full(2) && full(1)) R = 1;
         } else if (cols >= 4096) {
@@ -1583,14 +1590,12 @@ int dsv4_qproj_launch(const float *qr, int cols, const float *nw, float eps, int
     const size_t lds = pf.lds + sizeof(float) * (size_t)cols;   /* + the norm's weights */
     if (!opted) {
         const size_t cap = dsv4_lds_limit();
-        opted = dsv4_lds_optin((const void *)k_qproj<1, 2, 0>, cap, "q projections") &&
-                dsv4_lds_optin((const void *)k_qproj<2, 2, 0>, cap, "q projections") &&
-                dsv4_lds_optin((const void *)k_qproj<1, 2, 1>, cap, "q projections") &&
-                dsv4_lds_optin((const void *)k_qproj<2, 2, 1>, cap, "q projections") &&
-                dsv4_lds_optin((const void *)k_qproj<1, 4, 0>, cap, "q projections") &&
-                dsv4_lds_optin((const void *)k_qproj<2, 4, 0>, cap, "q projections") &&
-                dsv4_lds_optin((const void *)k_qproj<1, 4, 1>, cap, "q projections") &&
-                dsv4_lds_optin((const void *)k_qproj<2, 4, 1>, cap, "q projections");
+        const void *fns[] = {(const void *)k_qproj<1, 2, 0>, (const void *)k_qproj<2, 2, 0>,
+                             (const void *)k_qproj<1, 2, 1>, (const void *)k_qproj<2, 2, 1>,
+                             (const void *)k_qproj<1, 4, 0>, (const void *)k_qproj<2, 4, 0>,
+                             (const void *)k_qproj<1, 4, 1>, (const void *)k_qproj<2, 4, 1>};
+        for (const void *f : fns) (void)dsv4_lds_optin(f, cap, "q projections");
+        opted = true;
     }
 #define DSV4_QP(NCH, R, SF) hipLaunchKernelGGL((k_qproj<NCH, R, SF>), grid, dim3(256), lds, st, a)
     if (qrr == 4) {

@@ -453,6 +453,15 @@ size_t dsv4_lds_limit(void)
 
 bool dsv4_lds_optin(const void *kernel, size_t bytes, const char *what)
 {
+    /* the dynamic allocation shares the workgroup's LDS with the kernel's
+     * static arrays: ask for at most what they leave */
+    hipFuncAttributes fa;
+    if (hipFuncGetAttributes(&fa, kernel) == hipSuccess) {
+        const size_t lim = dsv4_lds_limit(), st = fa.sharedSizeBytes;
+        if (bytes > (st < lim ? lim - st : 0)) bytes = st < lim ? lim - st : 0;
+    } else {
+        (void)hipGetLastError();
+    }
     const hipError_t e =
         hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
     if (e == hipSuccess) return true;

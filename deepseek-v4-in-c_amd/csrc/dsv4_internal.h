@@ -26,10 +26,12 @@
  * reports 160 KiB; 64 KiB if the query fails). */
 size_t dsv4_lds_limit(void);
 
-/* Opt a kernel in to `bytes` of dynamic LDS per workgroup. true, or false
- * with a message naming `what` when the runtime refuses; the error is
- * cleared, and a launch that needed the opt-in then fails on its own check.
- * Callers keep a once-flag and set it only on success. */
+/* Opt a kernel in to `bytes` of dynamic LDS per workgroup, at most what its
+ * static LDS leaves of the device's limit. true, or false with a message
+ * naming `what` when the runtime refuses; the error is cleared, and a launch
+ * that needed the opt-in then fails on its own check. Callers make the
+ * attempt once (a once-flag set after it, whatever the result), so a refusal
+ * is reported once. */
 bool dsv4_lds_optin(const void *kernel, size_t bytes, const char *what);
 
 /* Block-scaled FP8 GEMV. sfmt 0 = E8M0 bytes, 1 = fp32. S is the scale grid

@@ -2343,9 +2343,11 @@ int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *
                            sizeof(float) * ((size_t)H * (D + 1) + (size_t)(SK_THREADS / hp) * D);
         if (lds <= dsv4_lds_limit()) {
             static bool kh_opted = false;
-            if (!kh_opted)
-                kh_opted = dsv4_lds_optin((const void *)k_iscore_kh<DSV4_GPU_KV_F32>,
-                                          dsv4_lds_limit(), "indexer score");
+            if (!kh_opted) {
+                (void)dsv4_lds_optin((const void *)k_iscore_kh<DSV4_GPU_KV_F32>,
+                                     dsv4_lds_limit(), "indexer score");
+                kh_opted = true;
+            }
 
             Dsv4Rope qr;
             if (rope_dim) {
@@ -2379,7 +2381,6 @@ int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *
             static bool mf_opted = false;
             if (!mf_opted) {
                 const size_t cap = dsv4_lds_limit();
-                bool ok = true;
 #define DSV4_MF_OPT(KF, P)                                                                  \
     do {                                                                                    \
         const void *f_[] = {(const void *)k_iscore_mf<KF, P, 0, 1>,                         \
@@ -2388,14 +2389,14 @@ int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *
                             (const void *)k_iscore_mf<KF, P, 1, 1>,                         \
                             (const void *)k_iscore_mf<KF, P, 1, 2>,                         \
                             (const void *)k_iscore_mf<KF, P, 1, 4>};                        \
-        for (const void *f : f_) ok = dsv4_lds_optin(f, cap, "indexer score") && ok;        \
+        for (const void *f : f_) (void)dsv4_lds_optin(f, cap, "indexer score");            \
     } while (0)
                 DSV4_MF_OPT(DSV4_GPU_KV_FP8, 1);
                 DSV4_MF_OPT(DSV4_GPU_KV_FP8, 0);
                 DSV4_MF_OPT(DSV4_GPU_KV_BF16, 0);
                 DSV4_MF_OPT(DSV4_GPU_KV_F32, 0);
 #undef DSV4_MF_OPT
-                mf_opted = ok;
+                mf_opted = true;
             }
             const bool piece = key_fmt == DSV4_GPU_KV_FP8 && D % 16 == 0 &&
                                key_stride % 16 == 0 && ((uintptr_t)d_keys & 15) == 0;
@@ -2455,9 +2456,8 @@ int dsv4_indexer_score_rope_launch(float *d_out, const float *d_q, const float *
             (const void *)k_iscore<DSV4_GPU_KV_F32, 0, 0, 4>, (const void *)k_iscore<DSV4_GPU_KV_F32, 0, 1, 4>,
             (const void *)k_iscore<DSV4_GPU_KV_F32, 1, 0, 8>, (const void *)k_iscore<DSV4_GPU_KV_F32, 1, 1, 8>,
             (const void *)k_iscore<DSV4_GPU_KV_F32, 0, 0, 8>, (const void *)k_iscore<DSV4_GPU_KV_F32, 0, 1, 8>};
-        bool ok = true;
-        for (const void *f : fns) ok = dsv4_lds_optin(f, cap, "indexer score") && ok;
-        lds_opted = ok;
+        for (const void *f : fns) (void)dsv4_lds_optin(f, cap, "indexer score");
+        lds_opted = true;
     }
     const bool vec = ((size_t)D * es) % 16 == 0 && ((size_t)key_stride * es) % 16 == 0 &&
                      ((uintptr_t)d_keys & 15) == 0;
@@ -2610,11 +2610,12 @@ int dsv4_attn_block_launch(float *d_o, const float *d_q, const void *d_kv,
     static bool lds_opted = false;
     if (!lds_opted) {
         const size_t cap = dsv4_lds_limit();
-        lds_opted = dsv4_lds_optin((const void *)k_attn_partial<DSV4_GPU_KV_BF16>, cap,
-                                   "sparse attention") &&
-                    dsv4_lds_optin((const void *)k_attn_partial<DSV4_GPU_KV_F32>, cap,
-                                   "sparse attention") &&
-                    dsv4_lds_optin((const void *)k_attn_mc, cap, "sparse attention");
+        (void)dsv4_lds_optin((const void *)k_attn_partial<DSV4_GPU_KV_BF16>, cap,
+                             "sparse attention");
+        (void)dsv4_lds_optin((const void *)k_attn_partial<DSV4_GPU_KV_F32>, cap,
+                             "sparse attention");
+        (void)dsv4_lds_optin((const void *)k_attn_mc, cap, "sparse attention");
+        lds_opted = true;
     }
     /* the matrix-core form where the shape allows (DSV4_GPU_ATTN_MC=0 keeps
      * the VALU form) */

@@ -1344,9 +1344,9 @@ bool mc_shape_ok(int topk, int hidden, int inter)
 }
 
 template <typename K>
-bool mc_lds_optin(K kernel)
+void mc_lds_optin(K kernel)
 {
-    return dsv4_lds_optin((const void *)kernel, dsv4_lds_limit() - 16 * 1024, "routed experts");
+    (void)dsv4_lds_optin((const void *)kernel, dsv4_lds_limit() - 16 * 1024, "routed experts");
 }
 
 size_t mc_scratch_bytes(int topk, int hidden, int inter)
@@ -1405,9 +1405,9 @@ int dsv4_moe_fp4_launch(float *d_out, const float *d_x,
         lf + 16 * 1024 <= dsv4_lds_limit()) {
         static bool optedf = false;
         if (!optedf) {
-            optedf = mc_lds_optin(k_mc2_fused<2, 14, 2, 4>) &&
-                     mc_lds_optin(k_mc2_fused<2, 14, 3, 0>) &&
-                     mc_lds_optin(k_mc2_fused<3, 0, 2, 4>) && mc_lds_optin(k_mc2_fused<3, 0, 3, 0>);
+            mc_lds_optin(k_mc2_fused<2, 14, 2, 4>); mc_lds_optin(k_mc2_fused<2, 14, 3, 0>);
+            mc_lds_optin(k_mc2_fused<3, 0, 2, 4>); mc_lds_optin(k_mc2_fused<3, 0, 3, 0>);
+            optedf = true;
         }
         const int ga = (inter / 64) * topk, gb = hidden / 32;
         const int nua = hidden / 512, nub = inter / 512;
@@ -1425,9 +1425,11 @@ int dsv4_moe_fp4_launch(float *d_out, const float *d_x,
          * measured slower at C3: more bytes in flight per CU only lengthen
          * the memory queues). */
         static bool opted2 = false;
-        if (!opted2)
-            opted2 = mc_lds_optin(k_mc2_gate_up<2, 14>) && mc_lds_optin(k_mc2_gate_up<3, 0>) &&
-                     mc_lds_optin(k_mc2_down<2, 4>) && mc_lds_optin(k_mc2_down<3, 0>);
+        if (!opted2) {
+            mc_lds_optin(k_mc2_gate_up<2, 14>); mc_lds_optin(k_mc2_gate_up<3, 0>);
+            mc_lds_optin(k_mc2_down<2, 4>); mc_lds_optin(k_mc2_down<3, 0>);
+            opted2 = true;
+        }
         const size_t la = m2_lds_a(hidden), lb = m2_lds_b(topk, inter);
         const int nwb = m2_down_waves(topk);
         const dim3 ga(inter / 32, topk), gb(hidden / 32);
@@ -1448,7 +1450,9 @@ int dsv4_moe_fp4_launch(float *d_out, const float *d_x,
      * the arithmetic of a row). */
     static bool opted = false;
     if (!opted) {
-        opted = mc_lds_optin(k_mc_gate_up<1, 4>) && mc_lds_optin(k_mc_down<2, 8>);
+        mc_lds_optin(k_mc_gate_up<1, 4>);
+        mc_lds_optin(k_mc_down<2, 8>);
+        opted = true;
     }
     const size_t la = mc_lds_a(hidden);
     hipLaunchKernelGGL((k_mc_gate_up<1, 4>), dim3(inter / 16, topk), dim3(256), la, st, ht, xt,
@@ -1500,8 +1504,9 @@ int dsv4_moe_fp4_n_launch(float *d_out, const float *d_x, const Dsv4ExpertDev *d
     const int slots = np < n_table + 1 ? np : n_table + 1;
     static bool opted = false;
     if (!opted) {
-        opted = mc_lds_optin(k_mn_pass<2, 14, true>) && mc_lds_optin(k_mn_pass<3, 0, true>) &&
-                mc_lds_optin(k_mn_pass<2, 4, false>) && mc_lds_optin(k_mn_pass<3, 0, false>);
+        mc_lds_optin(k_mn_pass<2, 14, true>); mc_lds_optin(k_mn_pass<3, 0, true>);
+        mc_lds_optin(k_mn_pass<2, 4, false>); mc_lds_optin(k_mn_pass<3, 0, false>);
+        opted = true;
     }
     const size_t lds = mn_lds();
     hipLaunchKernelGGL(k_mn_split, dim3((nt * hidden + 255) / 256), dim3(256), 0, st, xt, d_x,

@@ -352,14 +352,18 @@ def test_e8m0_forms(gpu, dsv4, monkeypatch, form):
     assert common.vec_rel_err(yn, want) < TOL
 
 
-@pytest.mark.parametrize("rows,cols", [(7168, 7168), (1536, 1536), (300, 4096), (260, 16384)])
-def test_launch_shape_keeps_bits(gpu, dsv4, monkeypatch, rows, cols):
+@pytest.mark.parametrize("scales", ["f32", "e8m0"])
+@pytest.mark.parametrize("rows,cols", [(7168, 7168), (1536, 1536), (300, 4096), (260, 16384),
+                                       (4096, 8192), (1024, 4096)])
+def test_launch_shape_keeps_bits(gpu, dsv4, monkeypatch, rows, cols, scales):
     """Rows per thread (DSV4_GPU_FP8_R), prefetch (DSV4_GPU_FP8_PF),
     workgroups per CU (DSV4_GPU_FP8_WPC) and x through LDS (DSV4_GPU_FP8_XL)
-    only reshape the launch: every setting gives the default's bits."""
+    only reshape the launch: every setting gives the default's bits, in both
+    scale formats (the default shape itself depends on the format)."""
     W, Sf, Se, x = common.fp8_problem(51, rows, cols)
-    y0, m = _run(dsv4, W, Sf, x, f32s=True)
-    assert common.vec_rel_err(y0, oracle.matmul_fp8(x, W, Sf)) < TOL
+    S = Sf if scales == "f32" else Se
+    y0, m = _run(dsv4, W, S, x, f32s=scales == "f32")
+    assert common.vec_rel_err(y0, oracle.matmul_fp8(x, W, S)) < TOL
     for r, pf, wpc, xl in ((1, 0, 2, None), (4, 0, 2, None), (2, 1, 2, None), (2, 0, 1, None),
                            (4, 1, 8, None), (1, 1, 4, None), (1, 1, 2, 1), (2, 0, 2, 0),
                            (4, 1, 2, 1)):

@@ -75,6 +75,7 @@ struct LayerExperts {
 
 struct Arena {
     char *h = nullptr, *d = nullptr;
+    char *hd = nullptr;                 /* the device's address of h (mapped) */
     size_t cap = 0;
 };
 
@@ -131,8 +132,10 @@ int arena_reserve(size_t bytes)
     if (g_ar.d) (void)hipFree(g_ar.d);
     g_ar.h = g_ar.d = nullptr;
     g_ar.cap = 0;
-    HIP_OK(hipHostMalloc((void **)&g_ar.h, cap, hipHostMallocDefault),
+    /* coherent and mapped: kernels write outputs straight into it */
+    HIP_OK(hipHostMalloc((void **)&g_ar.h, cap, hipHostMallocMapped | hipHostMallocCoherent),
            "hipHostMalloc staging");
+    HIP_OK(hipHostGetDevicePointer((void **)&g_ar.hd, g_ar.h, 0), "staging device address");
     HIP_OK(hipMalloc((void **)&g_ar.d, cap), "hipMalloc staging");
     g_ar.cap = cap;
     return 0;
@@ -154,8 +157,16 @@ int scratch_reserve(Scratch &s, size_t bytes)
     return 0;
 }
 
-/* A staged host-buffer call: inputs are packed into the arena, copied in one
- * transfer; outputs are copied back in one transfer. */
+/* A staged host-buffer call: inputs are packed into the pinned arena and
+ * moved to the device in one step; outputs come back in one step.
+ *
+ * By default the staging is zero-copy: one small kernel pulls the packed
+ * inputs to the device through the arena's device mapping, and the call's
+ * last kernel writes its outputs (plain stores, each written once, never
+ * read back on the device) straight into the mapped arena, so no DMA
+ * transfer is set up in either direction. Intermediate buffers stay in
+ * device memory. DSV4_GPU_HOST_ZC=0 stages through two DMA copies instead
+ * (hipMemcpyAsync H2D and D2H). */
 struct Stage {
     size_t used = 0;
     struct In { const void *src; size_t off, bytes; };
@@ -169,6 +180,23 @@ struct Stage {
     }
 };
 
+__global__ void __launch_bounds__(256) k_pull(u32x4 *__restrict__ dst,
+                                              const u32x4 *__restrict__ src, int n)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dst[i] = src[i];
+}
+
+/* read at each call, as the other switches are */
+bool host_zc()
+{
+    const char *e = getenv("DSV4_GPU_HOST_ZC");
+    return !(e && atoi(e) == 0);
+}
+
+/* where the call's last kernel writes an output at arena offset off */
+char *out_at(size_t off) { return (host_zc() ? g_ar.hd : g_ar.d) + off; }
+
 int stage_push(Stage &s, size_t *in_end)
 {
     if (arena_reserve(s.used ? s.used : 256) != 0) return -1;
@@ -177,16 +205,23 @@ int stage_push(Stage &s, size_t *in_end)
         memcpy(g_ar.h + i.off, i.src, i.bytes);
         end = i.off + i.bytes;
     }
-    if (end)
+    if (end && host_zc()) {
+        const int n = (int)((end + 15) / 16);
+        hipLaunchKernelGGL(k_pull, dim3((n + 255) / 256), dim3(256), 0, g_stream,
+                           (u32x4 *)g_ar.d, (const u32x4 *)g_ar.hd, n);
+        HIP_OK(hipGetLastError(), "staging pull");
+    } else if (end) {
         HIP_OK(hipMemcpyAsync(g_ar.d, g_ar.h, end, hipMemcpyHostToDevice, g_stream),
                "H2D staging");
+    }
     *in_end = end;
     return 0;
 }
 
+/* the output at arena offset off (written through out_at) into dst */
 int stage_pull(size_t off, size_t bytes, void *dst)
 {
-    if (bytes)
+    if (bytes && !host_zc())
         HIP_OK(hipMemcpyAsync(g_ar.h + off, g_ar.d + off, bytes,
                               hipMemcpyDeviceToHost, g_stream), "D2H staging");
     HIP_OK(hipStreamSynchronize(g_stream), "stream sync");
@@ -579,7 +614,7 @@ void dsv4_gpu_mmq(float *y, const float *x, const DSV4QMat *m)
     const size_t yo = s.add((size_t)m->rows * sizeof(float));
     size_t end;
     if (stage_push(s, &end) != 0) abort();
-    const int rc = res_gemv(v, m->rows, (float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
+    const int rc = res_gemv(v, m->rows, (float *)out_at(yo), (const float *)(g_ar.d + xo),
                             g_stream);
     if (rc != 0 || stage_pull(yo, (size_t)m->rows * sizeof(float), y) != 0) {
         DSV4_ERR("mmq failed");
@@ -608,15 +643,15 @@ void dsv4_gpu_mmq_n(float *y, const float *x, const DSV4QMat *m, int nt)
     /* one pass over the weights for the whole batch; per (row, token) the
      * single-token GEMV's own arithmetic */
     if (r->wdt == DSV4_WFP4) {
-        rc = dsv4_fp4_gemv_n_launch((float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
+        rc = dsv4_fp4_gemv_n_launch((float *)out_at(yo), (const float *)(g_ar.d + xo),
                                     v.w, v.s, m->rows, r->cols, r->blk_r, r->blk_c, nt,
                                     g_stream);
     } else if (r->wdt == DSV4_WBF16) {
-        rc = dsv4_bf16_gemv_n_launch((float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
+        rc = dsv4_bf16_gemv_n_launch((float *)out_at(yo), (const float *)(g_ar.d + xo),
                                      (const uint16_t *)v.w, m->rows, r->cols, nt, g_stream);
     } else {
         rc = dsv4_fp8_gemv_n_launch(
-            (float *)(g_ar.d + yo), (const float *)(g_ar.d + xo),
+            (float *)out_at(yo), (const float *)(g_ar.d + xo),
             v.w, v.s, r->sfmt, m->rows, r->cols, r->blk_r, r->blk_c, nt, g_stream,
             g_ar.d + to);
     }
@@ -715,7 +750,7 @@ int dsv4_gpu_head_argmax(const float *x, const DSV4QMat *head)
     if (stage_push(s, &end) != 0) return -1;
     if (res_gemv(v, head->rows, (float *)(g_ar.d + lo), (const float *)(g_ar.d + xo),
                  g_stream) != 0 ||
-        dsv4_argmax_launch((int *)(g_ar.d + to), (const float *)(g_ar.d + lo), head->rows,
+        dsv4_argmax_launch((int *)out_at(to), (const float *)(g_ar.d + lo), head->rows,
                            g_amax.p, g_stream) != 0)
         return -1;
     int tok = -1;
@@ -921,7 +956,7 @@ int dsv4_gpu_moe_fp4(float *out, const float *x, int layer, const int *idx,
     const size_t oo = s.add((size_t)hidden * sizeof(float));
     size_t end;
     if (stage_push(s, &end) != 0) return -1;
-    if (dsv4_moe_fp4_launch((float *)(g_ar.d + oo), (const float *)(g_ar.d + xo),
+    if (dsv4_moe_fp4_launch((float *)out_at(oo), (const float *)(g_ar.d + xo),
                             L->dev, (int)L->host.size(),
                             (const int *)(g_ar.d + io), (const float *)(g_ar.d + wo),
                             topk, hidden, inter, swiglu_limit, g_moe.p,
@@ -988,13 +1023,13 @@ int dsv4_gpu_moe_fp4_n(float *out, const float *x, int layer, const int *idx,
     }
     if (tokenwise) {
         for (int t = 0; t < nt; t++)
-            if (dsv4_moe_fp4_launch((float *)(g_ar.d + oo) + (size_t)t * hidden,
+            if (dsv4_moe_fp4_launch((float *)out_at(oo) + (size_t)t * hidden,
                                     (const float *)(g_ar.d + xo) + (size_t)t * hidden, L->dev,
                                     (int)L->host.size(), (const int *)(g_ar.d + io) + t * topk,
                                     (const float *)(g_ar.d + wo) + t * topk, topk, hidden,
                                     inter, swiglu_limit, g_moe.p, g_stream) != 0)
                 return -1;
-    } else if (dsv4_moe_fp4_n_launch((float *)(g_ar.d + oo), (const float *)(g_ar.d + xo),
+    } else if (dsv4_moe_fp4_n_launch((float *)out_at(oo), (const float *)(g_ar.d + xo),
                                      L->dev, (int)L->host.size(), (const int *)(g_ar.d + io),
                                      (const float *)(g_ar.d + wo), nt, topk, hidden, inter,
                                      swiglu_limit, g_moe.p, g_stream) != 0) {
@@ -1163,7 +1198,7 @@ int dsv4_gpu_indexer_score(float *out, const float *q, const float *w, int H,
     const size_t oo = s.add((size_t)n * sizeof(float));
     size_t end;
     if (stage_push(s, &end) != 0) return -1;
-    if (dsv4_indexer_score_launch((float *)(g_ar.d + oo), (const float *)(g_ar.d + qo),
+    if (dsv4_indexer_score_launch((float *)out_at(oo), (const float *)(g_ar.d + qo),
                                   (const float *)(g_ar.d + wo), H, D, kb, ks,
                                   keys->fmt, key_stride, n, indexer_scale(D, H),
                                   nullptr, 0, g_stream) != 0)
@@ -1182,7 +1217,7 @@ int dsv4_gpu_topk(int *idxs, const float *scores, int n, int k)
     const size_t io = s.add((size_t)k * sizeof(int));
     size_t end;
     if (stage_push(s, &end) != 0) return -1;
-    if (dsv4_topk_launch((int *)(g_ar.d + io), (const float *)(g_ar.d + so), n, k,
+    if (dsv4_topk_launch((int *)out_at(io), (const float *)(g_ar.d + so), n, k,
                          g_index.p, 0, g_stream) != 0)
         return -1;
     if (stage_pull(io, (size_t)k * sizeof(int), idxs) != 0) return -1;
@@ -1211,7 +1246,7 @@ int dsv4_gpu_indexer_topk(int *idxs, const float *q, const float *w, int H,
                                   (const float *)(g_ar.d + wo), H, D, kb, ks,
                                   keys->fmt, key_stride, n, indexer_scale(D, H),
                                   g_index.p, hist, g_stream) != 0 ||
-        dsv4_topk_launch((int *)(g_ar.d + io), (const float *)(g_ar.d + so), n, k,
+        dsv4_topk_launch((int *)out_at(io), (const float *)(g_ar.d + so), n, k,
                          g_index.p, hist, g_stream) != 0)
         return -1;
     if (stage_pull(io, (size_t)k * sizeof(int), idxs) != 0) return -1;
@@ -1240,7 +1275,7 @@ int dsv4_gpu_sparse_attn(float *o, const float *q, const dsv4_gpu_kv *kv,
     const size_t oo = s.add((size_t)h * d_v * sizeof(float));
     size_t end;
     if (stage_push(s, &end) != 0) return -1;
-    if (dsv4_attn_launch((float *)(g_ar.d + oo), (const float *)(g_ar.d + qo),
+    if (dsv4_attn_launch((float *)out_at(oo), (const float *)(g_ar.d + qo),
                          kv->data, kv->fmt, kv->row_dim, kv->n_rows,
                          sink ? (const float *)(g_ar.d + so) : nullptr,
                          (const int *)(g_ar.d + io), h, d_qk, d_v, topk, scale,

@@ -213,6 +213,30 @@ def test_batched_bit_identical(gpu, dsv4, monkeypatch, rows, cols, nt, form):
     assert common.vec_rel_err(yn, oracle.matmul_fp8(x, W, Se)) < TOL
 
 
+@pytest.mark.parametrize("wdt", ["fp8", "fp8_f32s"])
+@pytest.mark.parametrize("nt", [1, 5, 16])
+def test_host_staging_modes_keep_bits(gpu, dsv4, monkeypatch, nt, wdt):
+    """Host-buffer calls stage zero-copy by default (the inputs pulled to the
+    device through the pinned arena's device mapping, the output written by
+    the last kernel straight into it) or through two DMA copies
+    (DSV4_GPU_HOST_ZC=0): the same bits either way, single token and
+    batched, within 1e-5 of the oracle."""
+    rows, cols = 1536, 2048
+    W, Sf, Se, _ = common.fp8_problem(61, rows, cols)
+    S = Se if wdt == "fp8" else Sf
+    x = np.random.default_rng(62).standard_normal((nt, cols), dtype=np.float32)
+    _, m = _run(dsv4, W, S, x[0], f32s=wdt == "fp8_f32s")
+    outs = {}
+    for zc in ("1", "0", "1"):
+        monkeypatch.setenv("DSV4_GPU_HOST_ZC", zc)
+        y = dsv4.mmq_n(m, x) if nt > 1 else dsv4.mmq(m, x[0])[None]
+        if zc in outs:
+            assert common.bits_equal(y, outs[zc]), "zero-copy repeat"
+        outs[zc] = y
+    assert common.bits_equal(outs["1"], outs["0"])
+    assert common.vec_rel_err(outs["1"], oracle.matmul_fp8(x, W, S)) < TOL
+
+
 def _same_bits_or_nan(a, b):
     """NaN where the other is NaN (any payload), the same bits elsewhere."""
     a = np.asarray(a, np.float32)

@@ -29,6 +29,8 @@
 #include "dsv4_dev.h"
 #include "dsv4_internal.h"
 
+#include <stdlib.h>
+
 namespace {
 
 constexpr int F4_WAVES = 4;
@@ -133,9 +135,14 @@ void f4_launch(float *y, const float *x, const uint8_t *W, const uint8_t *S, int
                              "fp4 gemv");
         opted = true;
     }
-    /* 16 rows per workgroup: enough to amortise the x staging, and rows / 16
-     * workgroups fill the chip at expert shapes. */
-    const int rows_per_wg = 16;
+    /* 4 rows per workgroup (one per wave): at expert shapes the grid's
+     * parallelism matters more than staging x once per more rows (cold, us,
+     * 16 / 8 / 4 rows: 2048x7168 10.1 / 6.8 / 6.3, 7168x2048 6.6 / 6.5 /
+     * 6.2, 1024x4096 7.2 / 5.0 / 4.5, 4096x4096 7.6 / 7.1 / 7.1). A wave
+     * owns whole rows, so the split changes no row's arithmetic.
+     * DSV4_GPU_FP4_RPW overrides it. */
+    const char *e = getenv("DSV4_GPU_FP4_RPW");
+    const int rows_per_wg = e && atoi(e) > 0 ? atoi(e) : 4;
     const int grid = (rows + rows_per_wg - 1) / rows_per_wg;
     hipLaunchKernelGGL((k_fp4_gemv<NCH, R>), dim3(grid), dim3(F4_WAVES * 64),
                        (size_t)cols * sizeof(float), st, y, x, W, S, rows, cols, sc,

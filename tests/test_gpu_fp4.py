@@ -60,6 +60,24 @@ def test_mmq_fp4_matches_oracle(gpu, dsv4, rows, cols, blk_r, blk_c):
     assert err < TOL
 
 
+@pytest.mark.parametrize("rows,cols,blk_r,blk_c", [
+    (2048, 7168, 1, 32), (33, 4096, 1, 32), (130, 8192, 128, 128)])
+def test_fp4_rows_per_workgroup_keep_bits(gpu, dsv4, monkeypatch, rows, cols, blk_r, blk_c):
+    """Rows per workgroup (DSV4_GPU_FP4_RPW; 4 by default) only reshape the
+    grid: a wave owns whole rows, so every setting gives the default's bits,
+    including ragged last workgroups."""
+    rng = np.random.default_rng(rows * 5 + cols)
+    W, S = fp4_matrix(rng, rows, cols, blk_r, blk_c)
+    x = rng.standard_normal(cols).astype(np.float32)
+    m = resident(dsv4, W, S, rows, cols, blk_r, blk_c)
+    y0 = dsv4.mmq(m, x)
+    assert common.vec_rel_err(y0, oracle.matmul_fp4(x, W, S, cols, blk_r, blk_c)) < TOL
+    for rpw in (1, 3, 16, 32):
+        monkeypatch.setenv("DSV4_GPU_FP4_RPW", str(rpw))
+        print("fp4 %dx%d rows per workgroup %d" % (rows, cols, rpw), flush=True)
+        assert common.bits_equal(dsv4.mmq(m, x), y0), rpw
+
+
 def test_mmq_fp4_golden(gpu, dsv4):
     """The compiled reference's dsv4_matmul_fp4 output, committed as a vector."""
     G = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",

@@ -145,7 +145,7 @@ struct B16Plan {
     size_t lds = 0;
 };
 
-inline B16Plan b16_plan(const B16Geom &g, int rows, int nlist)
+inline B16Plan b16_plan(const B16Geom &g, int rows, int nlist, int max_grid = 0)
 {
     static int cus = 0;
     if (!cus) {
@@ -165,6 +165,12 @@ inline B16Plan b16_plan(const B16Geom &g, int rows, int nlist)
     const int want = (2 * cus + nm - 1) / nm;       /* two workgroups per CU */
     const int wpr = g.tc > 64 ? g.tc / 64 : 1;
     int spw = ((rows + step_rows - 1) / step_rows + want - 1) / want;
+    /* at most max_grid workgroups along x (a launch that shares its grid) */
+    if (max_grid > 0) {
+        const int nsteps = (rows + step_rows - 1) / step_rows;
+        const int spw_min = (nsteps + max_grid - 1) / max_grid;
+        if (spw < spw_min) spw = spw_min;
+    }
     const int max_spw = B16_PART_MAX / wpr / step_rows;
     if (spw > max_spw) spw = max_spw;
     if (spw < 1) spw = 1;

@@ -1502,7 +1502,9 @@ int dsv4_xproj_launch(const float *x, int cols, int sfmt, int blk_r, int blk_c, 
     if (!ok) return two();
     const Fp8Valu v = fp8_valu(rmf, cols, blk_r, sfmt, false);
     const Fp8Plan pf = fp8_plan(g, v.R, rmf, cols, v.wpc, nf);
-    const B16Plan pb = b16_plan(gb, rmb, nb);
+    /* the BF16 part within the FP8 part's grid (DSV4_GPU_XPROJ_CAP=0: its own
+     * plan): a wider x grid only adds workgroups of one step each */
+    const B16Plan pb = b16_plan(gb, rmb, nb, env_int("DSV4_GPU_XPROJ_CAP", 1) ? pf.grid : 0);
     /* the one combination built: FP8 with 4 chunks per thread, 2 rows per
      * step, prefetch, x in registers; BF16 with 8 chunks per thread, 1 row
      * (hidden 4096 and 7168, the Flash and full shapes) */

@@ -124,7 +124,9 @@ def test_x_projections_in_one_launch_keep_bits(gpu, dsv4, monkeypatch, ratio):
     """The block's x projections -- FP8 wq_a and wkv, BF16 compressor wkv and
     wgate and (ratio 4) the indexer's weights_proj -- run in one launch: each
     row has the bits of its own listed GEMV launch (DSV4_GPU_XPROJ=0: an FP8
-    and a BF16 listed launch), so every step's output is bit-identical."""
+    and a BF16 listed launch), so every step's output is bit-identical; the
+    same with the BF16 part on its own grid (DSV4_GPU_XPROJ_CAP=0) rather
+    than within the FP8 part's."""
     L, D = gpu, dsv4
     rng = np.random.default_rng(11 + ratio)
     layer = LAYER + 500 + ratio
@@ -134,6 +136,13 @@ def test_x_projections_in_one_launch_keep_bits(gpu, dsv4, monkeypatch, ratio):
     one = _host_steps(L, layer, X)
     assert np.isfinite(one).all() and np.abs(one).max() > 0.0
     assert L.dsv4_gpu_attn_reset(layer) == 0
+    monkeypatch.setenv("DSV4_GPU_XPROJ_CAP", "0")
+    print("attn x projections: ratio %d, one launch, BF16 on its own grid" % ratio, flush=True)
+    own = _host_steps(L, layer, X)
+    assert L.dsv4_gpu_attn_reset(layer) == 0
+    bad = np.nonzero((one.view(np.uint32) != own.view(np.uint32)).any(axis=1))[0]
+    assert bad.size == 0, "positions %s differ with the BF16 grid capped" % bad[:8].tolist()
+    monkeypatch.delenv("DSV4_GPU_XPROJ_CAP")
     monkeypatch.setenv("DSV4_GPU_XPROJ", "0")
     print("attn x projections: ratio %d, two launches" % ratio, flush=True)
     two = _host_steps(L, layer, X)

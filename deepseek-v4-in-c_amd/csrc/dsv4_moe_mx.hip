@@ -570,6 +570,12 @@ __device__ __forceinline__ bool mc2_gate_up_body(uint16_t *__restrict__ ht,
     extern __shared__ __attribute__((aligned(16))) unsigned char m2lds[];
     uint16_t *xl = (uint16_t *)m2lds;                      /* [MC_NT][pitch] */
     __shared__ float red[TILES][2][16];
+    /* hidden = 512 NU: NL 16-byte pieces of x per thread of 2 TILES waves,
+     * requested before the expert lookup (x does not depend on it, and it is
+     * the last input to arrive before the first product) */
+    constexpr int NL = NU > 0 ? (NU * 512 + 4 * 128 * TILES - 1) / (4 * 128 * TILES) : 1;
+    f32x4 xv[NL];
+    if constexpr (NU > 0) m2_x_load<NL>(xv, x, hidden, 0);
     const Dsv4ExpertDev E = mc_expert(table, n_table, idx, k);
     if (!E.w1) return false;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -585,10 +591,6 @@ __device__ __forceinline__ bool mc2_gate_up_body(uint16_t *__restrict__ ht,
 
     M2Unit P[D];
     if constexpr (NU > 0) {
-        /* hidden = 512 NU: NL 16-byte pieces per thread of 2 TILES waves */
-        constexpr int NL = (NU * 512 + 4 * 128 * TILES - 1) / (4 * 128 * TILES);
-        f32x4 xv[NL];
-        m2_x_load<NL>(xv, x, hidden, 0);
         __builtin_amdgcn_sched_barrier(0);
         m2_prologue<D>(P, base, rowb, sb, nsb, NU, lane);
         __builtin_amdgcn_sched_barrier(0);
@@ -695,7 +697,10 @@ k_mc2_down(float *__restrict__ out, const uint16_t *__restrict__ ht,
     extern __shared__ __attribute__((aligned(16))) unsigned char m2lds[];
     __shared__ float accl[MC_KMAX][32];
     const int r0 = blockIdx.x * 32;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    /* the wave index uniform, so that the slot's expert lookup is scalar
+     * loads, counted apart from the h loads in flight before it */
+    const int tid = threadIdx.x, lane = tid & 63,
+              w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nw = blockDim.x >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int nsb = inter >> 5;
@@ -708,23 +713,36 @@ k_mc2_down(float *__restrict__ out, const uint16_t *__restrict__ ht,
     const uint16_t *bl = hl + min(r, MC_NT - 1) * pitch;
 
     for (int k = w; k < topk; k += nw) {
+        /* slot k's planes are contiguous in ht: MC_NT * inter elements; with
+         * NU known they are requested before the expert lookup, which they
+         * do not depend on */
+        const uint16_t *hk = ht + (size_t)k * MC_NT * inter;
+        constexpr int IN = 512 * (NU > 0 ? NU : 1);        /* inter */
+        constexpr int NH = MC_NT * IN / 512;               /* 1 KB pieces per wave */
+        u32x4 hv[NH];
+        if constexpr (NU > 0) {
+#pragma unroll
+            for (int j = 0; j < NH; j++)
+                hv[j] = *(const DSV4_GLOBAL u32x4 *)(hk + 512 * j + 8 * lane);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         const Dsv4ExpertDev E = mc_expert(table, n_table, idx, k);
-        if (!E.w1) {
+        /* (a registered expert has all six pointers, a missing one none: the
+         * pass tests the pointer it reads, so one load serves both) */
+        if (!E.w2) {
+            /* (an empty use of the planes on this path too, so that their
+             * loads stay ahead of the lookup's branch) */
+            if constexpr (NU > 0) {
+#pragma unroll
+                for (int j = 0; j < NH; j++) asm volatile("" ::"v"(hv[j]));
+            }
             if (lane < 32) accl[k][lane] = __builtin_nanf("");
             continue;
         }
-        /* slot k's planes are contiguous in ht: MC_NT * inter elements */
-        const uint16_t *hk = ht + (size_t)k * MC_NT * inter;
         const uint8_t *base = E.w2 + (size_t)r0 * rowb;
         const uint8_t *sb = E.s2 + (size_t)r0 * nsb;
         v4f res[2];
         if constexpr (NU > 0) {
-            constexpr int IN = 512 * NU;                   /* inter */
-            constexpr int NH = MC_NT * IN / 512;           /* 1 KB pieces per wave */
-            u32x4 hv[NH];
-#pragma unroll
-            for (int j = 0; j < NH; j++)
-                hv[j] = *(const DSV4_GLOBAL u32x4 *)(hk + 512 * j + 8 * lane);
             __builtin_amdgcn_sched_barrier(0);
             M2Unit P[D];
             m2_prologue<D>(P, base, rowb, sb, nsb, NU, lane);

@@ -47,6 +47,8 @@
  * first (x, then the weights in K order) and keeps every load outside
  * branches; register arrays are indexed by compile-time constants only.
  */
+#include <type_traits>
+
 #include "dsv4_dev.h"
 #include "dsv4_internal.h"
 
@@ -663,6 +665,262 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
     }
 }
 
+/* The batched kernel with its operands staged by direct-to-LDS loads
+ * (k_fp8_mxd; uniform scales, pre-split x terms). A workgroup of 8 waves
+ * owns 128 rows (8 tiles) and a group of up to 20 tokens (4 column tiles of
+ * five); wave w takes RT row tiles and CT column tiles (RT x CT = 4; the
+ * launcher uses 2 x 2, so each A fragment feeds two column tiles and each B
+ * fragment two row tiles: 1 x 4 and 2 x 1 measured 57-76 against 54.5 us at
+ * 64 tokens). The K axis runs in stages of 128 columns (half a unit): the
+ * workgroup's 128 weight rows x 128 bytes and its 60 term rows x 128 bf16,
+ * copied by global_load_lds_dwordx4 (each lane's 16 bytes land at the
+ * instruction's LDS base + 16 lane, so nothing in flight holds a register)
+ * into a ring of XD_NS stages, XD_NS - 1 of them in flight while one is
+ * read. Each lane fetches the piece that the swizzled layout puts in its
+ * slot: weight piece c of row R sits at piece c ^ (R & 7) of its 128-byte
+ * row, term piece c of term row j at c ^ (j & 15) of its 256-byte row, so
+ * the fragment reads are free of bank conflicts (an in-bounds LDS probe on
+ * MI355X: 437-495 GB/s per CU for these patterns against 146 and 76 with
+ * the rows unswizzled). A wave reads stage s's fragments into one register
+ * set while the set read at stage s - 1 runs through the matrix core, so
+ * the reads' latency hides behind a stage of MFMAs. Per (row, term column)
+ * the chain is k_fp8_mxn's: the same K steps (whole units, zero operands
+ * past cols), the same fragments, one accumulator per segment from zero,
+ * the segments joined in order and y = (hi + mid) + lo, so the bits are the
+ * same. */
+constexpr int XD_K = 128;                        /* K (weight bytes) per stage */
+constexpr int XD_R = 128;                        /* rows per workgroup         */
+constexpr int XD_TR = XTOK * 4 * XNT;            /* term rows per stage (60)   */
+constexpr int XD_WB = XD_R * XD_K;               /* weight bytes per stage     */
+constexpr int XD_SB = XD_WB + XD_TR * XD_K * 2;  /* bytes per stage            */
+constexpr int XD_NS = 5;                         /* stages in the ring         */
+constexpr int XD_LDS = XD_NS * XD_SB;            /* 158,720 bytes              */
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+/* this wave's loads older than its newest `ahead` stages (4 loads each) are
+ * complete (the loop's only memory requests are the stage loads) */
+__device__ __forceinline__ void xd_wait(int ahead)
+{
+    if (ahead >= 3) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    else if (ahead == 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+template <int RT, int CT>
+__global__ void __launch_bounds__(512)
+k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *__restrict__ S,
+          int rows, int cols, int sc, int blk_r, uint32_t bc_m, int nt, int tpg,
+          const uint16_t *__restrict__ xt, int cpad)
+{
+    extern __shared__ __attribute__((aligned(16))) unsigned char xdlds[];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    static_assert(RT * CT == 4, "8 waves x RT x CT = 8 row tiles x 4 column tiles");
+    const int rp = w % (8 / RT), ch = w / (8 / RT);
+    const int row0 = blockIdx.x * XD_R;
+    const int t0 = blockIdx.y * tpg;
+    const int ntok = min(tpg, nt - t0);
+    if (ntok <= 0) return;                           /* the whole workgroup */
+    const int g = lane >> 4, col = lane & 15;
+    const int nst = 2 * ((cols + XU - 1) / XU);      /* whole units, as k_fp8_mxn */
+
+    /* the loads: weight instructions 2w, 2w + 1 (rows 8 i .. 8 i + 7 of the
+     * workgroup, lane -> row 8 i + lane / 8, slot lane % 8) and term
+     * instructions 2w, min(2w + 1, 14) (term rows 4 i .. 4 i + 3, lane ->
+     * row 4 i + lane / 16, slot lane % 16); rows past the matrix read its
+     * last row, term rows past the group's tokens its first (never used) */
+    constexpr int DH = 2;                            /* loads of each kind    */
+    const uint8_t *wsrc[DH];
+    int wcol[DH], xoff[DH];
+    const uint16_t *xsrc[DH];
+#pragma unroll
+    for (int i = 0; i < DH; i++) {
+        const int R = 8 * (DH * w + i) + (lane >> 3);
+        wcol[i] = 16 * ((lane & 7) ^ (R & 7));
+        wsrc[i] = W + (size_t)min(row0 + R, rows - 1) * cols;
+        const int xi = min(DH * w + i, XD_TR / 4 - 1);
+        const int j = 4 * xi + (lane >> 4);
+        const int jj = j / XNT < ntok ? j : 0;
+        xsrc[i] = xt + ((size_t)t0 * XNT + jj) * cpad + 8 * ((lane & 15) ^ (j & 15));
+        xoff[i] = XD_WB + 1024 * xi;
+    }
+    auto issue = [&](int s) {
+        unsigned char *st = xdlds + (size_t)(s % XD_NS) * XD_SB;
+        const int k0 = XD_K * s;
+#pragma unroll
+        for (int i = 0; i < DH; i++) {
+            const int k = k0 + wcol[i];
+            __builtin_amdgcn_global_load_lds((const void *)(wsrc[i] + (k < cols ? k : 0)),
+                                             (lds_void *)(st + 1024 * (DH * w + i)), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < DH; i++)
+            __builtin_amdgcn_global_load_lds((const void *)(xsrc[i] + k0),
+                                             (lds_void *)(st + xoff[i]), 16, 0, 0);
+    };
+
+    /* the fragment reads: A row 16 a + col of tile a = 2 rp + i; B term row
+     * 15 n + min(col, 14) of column tile n = 2 ch + jn (column 15 repeats
+     * column 14; its result is never used) */
+    int aoff[RT], asw[RT], boff[CT], bsw[CT];
+    bool live[RT];
+    int srow[RT];
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+        const int R = 16 * (RT * rp + i) + col;
+        aoff[i] = R * XD_K;
+        asw[i] = R & 7;
+        const int tr0 = row0 + 16 * (RT * rp + i);
+        live[i] = tr0 < rows;
+        srow[i] = ((live[i] ? tr0 : 0) / blk_r) * sc;
+    }
+#pragma unroll
+    for (int n = 0; n < CT; n++) {
+        const int j = 15 * (CT * ch + n) + min(col, 14);
+        boff[n] = XD_WB + j * (2 * XD_K);
+        bsw[n] = j & 15;
+    }
+    v4f acc[RT][CT], tot[RT][CT];
+#pragma unroll
+    for (int i = 0; i < RT; i++)
+#pragma unroll
+        for (int n = 0; n < CT; n++) {
+            acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
+            tot[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < XD_NS - 1; s++)
+        if (s < nst) issue(s);
+    __builtin_amdgcn_sched_barrier(0);
+    /* every segment's scales for the wave's row tiles, requested once behind
+     * the first stages (the loop then issues no memory request the compiler
+     * waits for, so its only waits on the memory counter are the stage
+     * waits): segment z, quarter m is byte z / 4 of sr[i] in lane 16 (z % 4)
+     * + m */
+    uint32_t sr[RT];
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+        sr[i] = 0u;
+#pragma unroll
+        for (int b = 0; b < XSEG_MAX / 4; b++)
+            sr[i] |= xs_seg(S, srow[i], bc_m, XSEG * (4 * b + (lane >> 4)), cols, lane) << (8 * b);
+    }
+
+    /* Stage s: wait for its loads, one barrier (every wave's loads of s are
+     * in LDS, and every wave's reads of s - 1 are complete, so s - 1's slot
+     * takes stage s + XD_NS - 1), then read s's fragments into one register
+     * set while the other set, read one stage earlier, runs through the
+     * matrix core: the fragment reads' latency hides behind a stage of
+     * MFMAs. */
+    struct Ops {
+        u32x4 a[RT][2];                          /* [row tile][quarter]        */
+        u32x4 b[2][2][CT];                       /* [quarter][step][col tile]  */
+    };
+    auto sync = [&](int s) {
+        xd_wait(min(XD_NS - 2, nst - 1 - s));
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (s + XD_NS - 1 < nst) issue(s + XD_NS - 1);
+    };
+    auto fetch = [&](Ops &o, int s) {
+        const unsigned char *st = xdlds + (size_t)(s % XD_NS) * XD_SB;
+#pragma unroll
+        for (int i = 0; i < RT; i++)
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++)
+                o.a[i][qq] = *reinterpret_cast<const u32x4 *>(
+                    st + aoff[i] + 16 * ((4 * qq + g) ^ asw[i]));
+#pragma unroll
+        for (int qq = 0; qq < 2; qq++)
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int n = 0; n < CT; n++)
+                    o.b[qq][h][n] = *reinterpret_cast<const u32x4 *>(
+                        st + boff[n] + 16 * ((8 * qq + 2 * g + h) ^ bsw[n]));
+    };
+    /* one stage through the matrix core; FULL: every column of the stage
+     * is inside the row (no piece to zero) */
+    auto mma = [&](const Ops &o, int s, auto full) {
+        constexpr bool FULL = decltype(full)::value;
+        const int sl = s & 7;                    /* stage within its segment */
+        const int z = s >> 3;
+#pragma unroll
+        for (int qq = 0; qq < 2; qq++) {
+            const bool in = FULL || XD_K * s + 64 * qq + 16 * g < cols;
+            v8bf af[RT][2];
+#pragma unroll
+            for (int i = 0; i < RT; i++) {
+                const u32x4 zv = in ? o.a[i][qq] : u32x4{0u, 0u, 0u, 0u};
+                const float sx = dec_e8m0(
+                    (xs_get(sr[i], 16 * (z & 3) + 2 * sl + qq) >> (8 * (z >> 2))) & 0xffu);
+                const float sv = in ? sx : 0.0f;
+                af[i][0] = fp8x8_bf16(zv.x, zv.y, sv);
+                af[i][1] = fp8x8_bf16(zv.z, zv.w, sv);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int i = 0; i < RT; i++)
+#pragma unroll
+                    for (int n = 0; n < CT; n++)
+                        acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            af[i][h], __builtin_bit_cast(v8bf, o.b[qq][h][n]), acc[i][n], 0, 0,
+                            0);
+        }
+    };
+    auto run = [&](const Ops &o, int s) {
+        if (XD_K * (s + 1) <= cols)
+            mma(o, s, std::true_type{});
+        else
+            mma(o, s, std::false_type{});
+        if ((s & 7) == 7 || s == nst - 1) {      /* a segment ends */
+            asm volatile("" ::: "memory");       /* a branch, not selects on every stage */
+#pragma unroll
+            for (int i = 0; i < RT; i++)
+#pragma unroll
+                for (int n = 0; n < CT; n++) {
+                    tot[i][n] = s < 8 ? acc[i][n] : tot[i][n] + acc[i][n];
+                    acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
+                }
+        }
+    };
+    /* nst is even: stages 1, 2 | 3, 4 | ... pair up, and the last is odd */
+    Ops o0, o1;
+    sync(0);
+    fetch(o0, 0);
+    int s = 1;
+    for (; s + 1 < nst; s += 2) {
+        sync(s);
+        fetch(o1, s);
+        run(o0, s - 1);
+        sync(s + 1);
+        fetch(o0, s + 1);
+        run(o1, s);
+    }
+    sync(s);
+    fetch(o1, s);
+    run(o0, s - 1);
+    run(o1, s);
+    /* y = (hi + mid) + lo per (row, token), as k_fp8_mxn */
+#pragma unroll
+    for (int i = 0; i < RT; i++)
+#pragma unroll
+        for (int n = 0; n < CT; n++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float c0 = tot[i][n][j];
+                const float c1 = __shfl(tot[i][n][j], min(lane + 1, 63), 64);
+                const float c2 = __shfl(tot[i][n][j], min(lane + 2, 63), 64);
+                const int tk = XTOK * (CT * ch + n) + col / XNT;
+                const int rr = row0 + 16 * (RT * rp + i) + 4 * g + j;
+                if (live[i] && col % XNT == 0 && col < XNT * XTOK && tk < ntok && rr < rows)
+                    y[(size_t)(t0 + tk) * rows + rr] = (c0 + c1) + c2;
+            }
+}
+
 /* The batched kernel for one column tile (at most five tokens) with each
  * tile's segments split over KP waves, as the single-token kernel splits
  * them: a workgroup of 4 waves holds 4 / KP tiles, and wave p of a tile takes
@@ -1106,6 +1364,30 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
 #undef XKF
 #undef XK
             HIP_OK(hipGetLastError(), "fp8 mxk launch");
+            return 0;
+        }
+    }
+    /* the DMA-staged kernel: uniform scales and pre-split terms, groups of
+     * at most 20 tokens (as many groups as 20-token groups need, the tokens
+     * spread evenly over them) */
+    /* the DMA-staged kernel (uniform scales, pre-split terms) from three
+     * groups of 20 tokens: 7168 x 7168 at 64 tokens 54.5-58.4 against
+     * 63.4-64.3 us; with one or two groups its 56 or 112 workgroups leave
+     * most CUs idle and the register-staged kernel, with twice the
+     * workgroups, is faster (32 tokens 45 against 52 us, 16 tokens 34
+     * against 51). DSV4_GPU_MXD = 0 / 1 forces it off / on where it applies. */
+    const int gd = (nt + XTOK * 4 - 1) / (XTOK * 4);
+    const int dme = mx_env("DSV4_GPU_MXD", -1);
+    if ((dme < 0 ? gd >= 3 : dme > 0) && uni && xt && (size_t)XD_LDS <= dsv4_lds_limit()) {
+        static int opted_d = 0;                    /* 1 granted, -1 refused */
+        if (!opted_d) opted_d = optin(k_fp8_mxd<2, 2>, "fp8 mxd") ? 1 : -1;
+        if (opted_d > 0) {
+            const int td = (nt + gd - 1) / gd;      /* tokens spread evenly */
+            HIP_OK(xsplit(), "fp8 mxn x split launch");
+            hipLaunchKernelGGL((k_fp8_mxd<2, 2>), dim3((rows + XD_R - 1) / XD_R, gd), dim3(512),
+                               (size_t)XD_LDS, st, y, W, S, rows, cols, sc, blk_r, bc_m, nt, td,
+                               xt, cpad);
+            HIP_OK(hipGetLastError(), "fp8 mxd launch");
             return 0;
         }
     }

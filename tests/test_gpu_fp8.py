@@ -295,6 +295,7 @@ def test_batched_token_tiles_keep_bits(gpu, dsv4, monkeypatch, ntmax):
     passes over the weights a batch takes) only reshapes the batched launch:
     every setting gives each token the single-token GEMV's bits."""
     monkeypatch.setenv("DSV4_GPU_FP8_MX", "1")
+    monkeypatch.setenv("DSV4_GPU_MXD", "0")          # the register-staged kernel
     monkeypatch.setenv("DSV4_GPU_MXN_NT", ntmax)
     for rows, cols, nt in ((300, 1536, 64), (129, 7168, 37), (70, 2096, 11)):
         W, Sf, Se, _ = common.fp8_problem(23, rows, cols)
@@ -335,6 +336,33 @@ def test_batched_segment_split_keeps_bits(gpu, dsv4, monkeypatch, kp, xf):
         yn = dsv4.mmq_n(m, x)
         for t in range(nt):
             assert common.bits_equal(yn[t], dsv4.mmq(m, x[t])), (kp, rows, cols, t)
+        assert common.vec_rel_err(yn, oracle.matmul_fp8(x, W, S, blk_r, blk_c)) < TOL
+
+
+@pytest.mark.parametrize("mxd", ["0", "1"])
+def test_batched_dma_staging_keeps_bits(gpu, dsv4, monkeypatch, mxd):
+    """DSV4_GPU_MXD: the batched matrix-core kernel whose weight and x-term
+    stages are copied into LDS by direct-to-LDS loads (uniform scales, groups
+    of up to 20 tokens) against the register-staged one. Both give each token
+    the single-token GEMV's bits: row counts that leave part of a 128-row
+    workgroup or a 16-row tile empty, a last unit past the row's end, one
+    unit, a single segment and sixteen, groups of 1 to 20 tokens."""
+    monkeypatch.setenv("DSV4_GPU_FP8_MX", "1")
+    monkeypatch.setenv("DSV4_GPU_MXD", mxd)
+    cases = ((7168, 7168, 64, 128, 128), (300, 1536, 64, 128, 128), (129, 7168, 37, 128, 128),
+             (33, 16384, 21, 16, 64), (70, 2096, 41, 32, 64), (16, 512, 20, 128, 128),
+             (40, 64, 3, 128, 128), (257, 1024, 7, 16, 128), (136, 3072, 61, 64, 192))
+    for rows, cols, nt, blk_r, blk_c in cases:
+        rng = np.random.default_rng(rows + cols + nt + 7)
+        W = common.fp8_codes(rng, (rows, cols))
+        S = (127 + rng.integers(-8, -3, size=((rows + blk_r - 1) // blk_r,
+                                              (cols + blk_c - 1) // blk_c))).astype(np.uint8)
+        x = rng.standard_normal((nt, cols), dtype=np.float32)
+        say("fp8 mxd %dx%d nt %d blk %dx%d MXD %s" % (rows, cols, nt, blk_r, blk_c, mxd))
+        _, m = _run(dsv4, W, S, x[0], blk_r=blk_r, blk_c=blk_c)
+        yn = dsv4.mmq_n(m, x)
+        for t in range(nt):
+            assert common.bits_equal(yn[t], dsv4.mmq(m, x[t])), (mxd, rows, cols, t)
         assert common.vec_rel_err(yn, oracle.matmul_fp8(x, W, S, blk_r, blk_c)) < TOL
 
 

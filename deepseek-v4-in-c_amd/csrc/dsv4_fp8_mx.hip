@@ -666,16 +666,17 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
 }
 
 /* The batched kernel with its operands staged by direct-to-LDS loads
- * (k_fp8_mxd; uniform scales, pre-split x terms). A workgroup of 8 waves
- * owns 128 rows (8 tiles) and a group of up to 20 tokens (4 column tiles of
- * five); wave w takes RT row tiles and CT column tiles (RT x CT = 4; the
- * launcher uses 2 x 2, so each A fragment feeds two column tiles and each B
- * fragment two row tiles: 1 x 4 and 2 x 1 measured 57-76 against 54.5 us at
- * 64 tokens). The K axis runs in stages of 128 columns (half a unit): the
- * workgroup's 128 weight rows x 128 bytes and its 60 term rows x 128 bf16,
+ * (k_fp8_mxd; uniform scales, pre-split x terms). A workgroup of MW waves
+ * (the launcher: 8) owns 16 MW rows (MW tiles) and a group of up to 20
+ * tokens (4 column tiles of five); wave w takes RT row tiles and CT column
+ * tiles (RT x CT = 4; the launcher uses 2 x 2, so each A fragment feeds two
+ * column tiles and each B fragment two row tiles: 1 x 4 and 2 x 1 measured
+ * 57-76 against 54.5 us at 64 tokens). The K axis runs in stages of 128
+ * columns (half a unit): the workgroup's weight rows x 128 bytes and its 60
+ * term rows x 128 bf16,
  * copied by global_load_lds_dwordx4 (each lane's 16 bytes land at the
  * instruction's LDS base + 16 lane, so nothing in flight holds a register)
- * into a ring of XD_NS stages, XD_NS - 1 of them in flight while one is
+ * into a ring of NS stages, NS - 1 of them in flight while one is
  * read. Each lane fetches the piece that the swizzled layout puts in its
  * slot: weight piece c of row R sits at piece c ^ (R & 7) of its 128-byte
  * row, term piece c of term row j at c ^ (j & 15) of its 256-byte row, so
@@ -687,29 +688,45 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
  * the chain is k_fp8_mxn's: the same K steps (whole units, zero operands
  * past cols), the same fragments, one accumulator per segment from zero,
  * the segments joined in order and y = (hi + mid) + lo, so the bits are the
- * same. */
+ * same. MW = 4 with a 3-stage ring (two workgroups per CU) measured slower
+ * at 64 tokens (59.6-60.6 against 55.8-56.3 us). */
 constexpr int XD_K = 128;                        /* K (weight bytes) per stage */
-constexpr int XD_R = 128;                        /* rows per workgroup         */
 constexpr int XD_TR = XTOK * 4 * XNT;            /* term rows per stage (60)   */
-constexpr int XD_WB = XD_R * XD_K;               /* weight bytes per stage     */
-constexpr int XD_SB = XD_WB + XD_TR * XD_K * 2;  /* bytes per stage            */
-constexpr int XD_NS = 5;                         /* stages in the ring         */
-constexpr int XD_LDS = XD_NS * XD_SB;            /* 158,720 bytes              */
+
+/* MW waves own 16 MW rows; a stage is their weights and the group's terms;
+ * NS stages in the ring */
+template <int MW>
+struct XdDim {
+    static constexpr int R = 16 * MW;                    /* rows per workgroup   */
+    static constexpr int WB = R * XD_K;                  /* weight bytes / stage */
+    static constexpr int SB = WB + XD_TR * XD_K * 2;     /* bytes per stage      */
+    static constexpr int DX = (XD_TR / 4 + MW - 1) / MW; /* term loads per wave  */
+    static constexpr int DPW = 2 + DX;                   /* loads per wave/stage */
+};
+template <int MW, int NS>
+constexpr size_t xd_lds() { return (size_t)NS * XdDim<MW>::SB; }
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-/* this wave's loads older than its newest `ahead` stages (4 loads each) are
- * complete (the loop's only memory requests are the stage loads) */
-__device__ __forceinline__ void xd_wait(int ahead)
+template <int N>
+__device__ __forceinline__ void xd_vm()
 {
-    if (ahead >= 3) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-    else if (ahead == 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int RT, int CT>
-__global__ void __launch_bounds__(512)
+/* this wave's loads older than its newest `ahead` stages (DPW loads each)
+ * are complete (the loop's only memory requests are the stage loads) */
+template <int DPW>
+__device__ __forceinline__ void xd_wait(int ahead)
+{
+    if (ahead >= 3) xd_vm<3 * DPW>();
+    else if (ahead == 2) xd_vm<2 * DPW>();
+    else if (ahead == 1) xd_vm<DPW>();
+    else xd_vm<0>();
+}
+
+template <int RT, int CT, int MW, int NS>
+__global__ void __launch_bounds__(64 * MW)
 k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *__restrict__ S,
           int rows, int cols, int sc, int blk_r, uint32_t bc_m, int nt, int tpg,
           const uint16_t *__restrict__ xt, int cpad)
@@ -717,9 +734,11 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
     extern __shared__ __attribute__((aligned(16))) unsigned char xdlds[];
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    static_assert(RT * CT == 4, "8 waves x RT x CT = 8 row tiles x 4 column tiles");
-    const int rp = w % (8 / RT), ch = w / (8 / RT);
-    const int row0 = blockIdx.x * XD_R;
+    static_assert(RT * CT == 4, "MW waves x RT x CT = MW row tiles x 4 column tiles");
+    static_assert(NS >= 2 && NS <= 5, "stage waits for up to 3 stages ahead");
+    using D = XdDim<MW>;
+    const int rp = w % (MW / RT), ch = w / (MW / RT);
+    const int row0 = blockIdx.x * D::R;
     const int t0 = blockIdx.y * tpg;
     const int ntok = min(tpg, nt - t0);
     if (ntok <= 0) return;                           /* the whole workgroup */
@@ -731,23 +750,26 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
      * instructions 2w, min(2w + 1, 14) (term rows 4 i .. 4 i + 3, lane ->
      * row 4 i + lane / 16, slot lane % 16); rows past the matrix read its
      * last row, term rows past the group's tokens its first (never used) */
-    constexpr int DH = 2;                            /* loads of each kind    */
+    constexpr int DH = 2, DX = D::DX;                /* loads of each kind    */
     const uint8_t *wsrc[DH];
-    int wcol[DH], xoff[DH];
-    const uint16_t *xsrc[DH];
+    int wcol[DH], xoff[DX];
+    const uint16_t *xsrc[DX];
 #pragma unroll
     for (int i = 0; i < DH; i++) {
         const int R = 8 * (DH * w + i) + (lane >> 3);
         wcol[i] = 16 * ((lane & 7) ^ (R & 7));
         wsrc[i] = W + (size_t)min(row0 + R, rows - 1) * cols;
-        const int xi = min(DH * w + i, XD_TR / 4 - 1);
+    }
+#pragma unroll
+    for (int i = 0; i < DX; i++) {
+        const int xi = min(DX * w + i, XD_TR / 4 - 1);
         const int j = 4 * xi + (lane >> 4);
         const int jj = j / XNT < ntok ? j : 0;
         xsrc[i] = xt + ((size_t)t0 * XNT + jj) * cpad + 8 * ((lane & 15) ^ (j & 15));
-        xoff[i] = XD_WB + 1024 * xi;
+        xoff[i] = D::WB + 1024 * xi;
     }
     auto issue = [&](int s) {
-        unsigned char *st = xdlds + (size_t)(s % XD_NS) * XD_SB;
+        unsigned char *st = xdlds + (size_t)(s % NS) * D::SB;
         const int k0 = XD_K * s;
 #pragma unroll
         for (int i = 0; i < DH; i++) {
@@ -756,7 +778,7 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
                                              (lds_void *)(st + 1024 * (DH * w + i)), 16, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < DH; i++)
+        for (int i = 0; i < DX; i++)
             __builtin_amdgcn_global_load_lds((const void *)(xsrc[i] + k0),
                                              (lds_void *)(st + xoff[i]), 16, 0, 0);
     };
@@ -779,7 +801,7 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
 #pragma unroll
     for (int n = 0; n < CT; n++) {
         const int j = 15 * (CT * ch + n) + min(col, 14);
-        boff[n] = XD_WB + j * (2 * XD_K);
+        boff[n] = D::WB + j * (2 * XD_K);
         bsw[n] = j & 15;
     }
     v4f acc[RT][CT], tot[RT][CT];
@@ -792,7 +814,7 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
         }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int s = 0; s < XD_NS - 1; s++)
+    for (int s = 0; s < NS - 1; s++)
         if (s < nst) issue(s);
     __builtin_amdgcn_sched_barrier(0);
     /* every segment's scales for the wave's row tiles, requested once behind
@@ -811,7 +833,7 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
 
     /* Stage s: wait for its loads, one barrier (every wave's loads of s are
      * in LDS, and every wave's reads of s - 1 are complete, so s - 1's slot
-     * takes stage s + XD_NS - 1), then read s's fragments into one register
+     * takes stage s + NS - 1), then read s's fragments into one register
      * set while the other set, read one stage earlier, runs through the
      * matrix core: the fragment reads' latency hides behind a stage of
      * MFMAs. */
@@ -820,12 +842,12 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
         u32x4 b[2][2][CT];                       /* [quarter][step][col tile]  */
     };
     auto sync = [&](int s) {
-        xd_wait(min(XD_NS - 2, nst - 1 - s));
+        xd_wait<D::DPW>(min(NS - 2, nst - 1 - s));
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (s + XD_NS - 1 < nst) issue(s + XD_NS - 1);
+        if (s + NS - 1 < nst) issue(s + NS - 1);
     };
     auto fetch = [&](Ops &o, int s) {
-        const unsigned char *st = xdlds + (size_t)(s % XD_NS) * XD_SB;
+        const unsigned char *st = xdlds + (size_t)(s % NS) * D::SB;
 #pragma unroll
         for (int i = 0; i < RT; i++)
 #pragma unroll
@@ -1378,15 +1400,15 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
      * against 51). DSV4_GPU_MXD = 0 / 1 forces it off / on where it applies. */
     const int gd = (nt + XTOK * 4 - 1) / (XTOK * 4);
     const int dme = mx_env("DSV4_GPU_MXD", -1);
-    if ((dme < 0 ? gd >= 3 : dme > 0) && uni && xt && (size_t)XD_LDS <= dsv4_lds_limit()) {
+    constexpr size_t lds_d = xd_lds<8, 5>();        /* 158,720 bytes */
+    if ((dme < 0 ? gd >= 3 : dme > 0) && uni && xt && lds_d <= dsv4_lds_limit()) {
         static int opted_d = 0;                    /* 1 granted, -1 refused */
-        if (!opted_d) opted_d = optin(k_fp8_mxd<2, 2>, "fp8 mxd") ? 1 : -1;
+        if (!opted_d) opted_d = optin(k_fp8_mxd<2, 2, 8, 5>, "fp8 mxd") ? 1 : -1;
         if (opted_d > 0) {
             const int td = (nt + gd - 1) / gd;      /* tokens spread evenly */
             HIP_OK(xsplit(), "fp8 mxn x split launch");
-            hipLaunchKernelGGL((k_fp8_mxd<2, 2>), dim3((rows + XD_R - 1) / XD_R, gd), dim3(512),
-                               (size_t)XD_LDS, st, y, W, S, rows, cols, sc, blk_r, bc_m, nt, td,
-                               xt, cpad);
+            hipLaunchKernelGGL((k_fp8_mxd<2, 2, 8, 5>), dim3((rows + 127) / 128, gd), dim3(512),
+                               lds_d, st, y, W, S, rows, cols, sc, blk_r, bc_m, nt, td, xt, cpad);
             HIP_OK(hipGetLastError(), "fp8 mxd launch");
             return 0;
         }

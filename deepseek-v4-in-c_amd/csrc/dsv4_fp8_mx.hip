@@ -467,20 +467,31 @@ __global__ void __launch_bounds__(256)
 k_fp8_xsplit(uint16_t *__restrict__ xt, const float *__restrict__ x, int nt, int cols,
              int cpad)
 {
-    const int i = blockIdx.x * 256 + threadIdx.x;           /* 4 columns per thread */
-    const int per = cpad >> 2;
+    /* 8 columns per thread: two 16-byte loads (x is 16-byte aligned and cols
+     * a multiple of 16 wherever this form runs), three 16-byte stores */
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int per = cpad >> 3;
     if (i >= nt * per) return;
-    const int t = i / per, c = 4 * (i - t * per);
-    float e[4];
+    const int t = i / per, c = 8 * (i - t * per);
+    float e[8];
 #pragma unroll
-    for (int j = 0; j < 4; j++) e[j] = c + j < cols ? x[(size_t)t * cols + c + j] : 0.0f;
-    uint32_t tt[4][XNT];
+    for (int h = 0; h < 2; h++) {
+        const f32x4 v = c + 4 * h < cols
+                            ? *(const DSV4_GLOBAL f32x4 *)(x + (size_t)t * cols + c + 4 * h)
+                            : f32x4{0.f, 0.f, 0.f, 0.f};
+        e[4 * h] = v.x;
+        e[4 * h + 1] = v.y;
+        e[4 * h + 2] = v.z;
+        e[4 * h + 3] = v.w;
+    }
+    uint32_t tt[8][XNT];
 #pragma unroll
-    for (int j = 0; j < 4; j++) terms3(e[j], tt[j]);
+    for (int j = 0; j < 8; j++) terms3(e[j], tt[j]);
 #pragma unroll
     for (int p = 0; p < XNT; p++)
-        *reinterpret_cast<uint2 *>(xt + ((size_t)t * XNT + p) * cpad + c) =
-            uint2{tt[0][p] | (tt[1][p] << 16), tt[2][p] | (tt[3][p] << 16)};
+        *reinterpret_cast<u32x4 *>(xt + ((size_t)t * XNT + p) * cpad + c) =
+            u32x4{tt[0][p] | (tt[1][p] << 16), tt[2][p] | (tt[3][p] << 16),
+                  tt[4][p] | (tt[5][p] << 16), tt[6][p] | (tt[7][p] << 16)};
 }
 
 /* 16-byte pieces of the term planes per thread per unit: a group's tpg
@@ -1331,8 +1342,8 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
     const int cpad = ((cols + XU - 1) / XU) * XU;
     const uint16_t *xt = (const uint16_t *)xscratch;
     auto xsplit = [&]() {
-        const int n4 = nt * (cpad / 4);
-        hipLaunchKernelGGL(k_fp8_xsplit, dim3((n4 + 255) / 256), dim3(256), 0, st,
+        const int n8 = nt * (cpad / 8);
+        hipLaunchKernelGGL(k_fp8_xsplit, dim3((n8 + 255) / 256), dim3(256), 0, st,
                            (uint16_t *)xscratch, x, nt, cols, cpad);
         return hipGetLastError();
     };

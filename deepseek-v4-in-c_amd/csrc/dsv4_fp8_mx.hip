@@ -779,14 +779,23 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
         xsrc[i] = xt + ((size_t)t0 * XNT + jj) * cpad + 8 * ((lane & 15) ^ (j & 15));
         xoff[i] = D::WB + 1024 * xi;
     }
-    auto issue = [&](int s) {
-        unsigned char *st = xdlds + (size_t)(s % NS) * D::SB;
+    auto issue = [&](int s, int slot) {
+        unsigned char *st = xdlds + (size_t)slot * D::SB;
         const int k0 = XD_K * s;
+        if (k0 + XD_K <= cols) {                 /* the whole stage inside the rows */
 #pragma unroll
-        for (int i = 0; i < DH; i++) {
-            const int k = k0 + wcol[i];
-            __builtin_amdgcn_global_load_lds((const void *)(wsrc[i] + (k < cols ? k : 0)),
-                                             (lds_void *)(st + 1024 * (DH * w + i)), 16, 0, 0);
+            for (int i = 0; i < DH; i++)
+                __builtin_amdgcn_global_load_lds((const void *)(wsrc[i] + k0 + wcol[i]),
+                                                 (lds_void *)(st + 1024 * (DH * w + i)), 16, 0,
+                                                 0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < DH; i++) {
+                const int k = k0 + wcol[i];
+                __builtin_amdgcn_global_load_lds((const void *)(wsrc[i] + (k < cols ? k : 0)),
+                                                 (lds_void *)(st + 1024 * (DH * w + i)), 16, 0,
+                                                 0);
+            }
         }
 #pragma unroll
         for (int i = 0; i < DX; i++)
@@ -826,7 +835,7 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < NS - 1; s++)
-        if (s < nst) issue(s);
+        if (s < nst) issue(s, s);
     __builtin_amdgcn_sched_barrier(0);
     /* every segment's scales for the wave's row tiles, requested once behind
      * the first stages (the loop then issues no memory request the compiler
@@ -852,13 +861,14 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
         u32x4 a[RT][2];                          /* [row tile][quarter]        */
         u32x4 b[2][2][CT];                       /* [quarter][step][col tile]  */
     };
-    auto sync = [&](int s) {
+    /* the slot of stage s (s % NS), kept as a running count */
+    auto sync = [&](int s, int slot) {
         xd_wait<D::DPW>(min(NS - 2, nst - 1 - s));
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (s + NS - 1 < nst) issue(s + NS - 1);
+        if (s + NS - 1 < nst) issue(s + NS - 1, slot == 0 ? NS - 1 : slot - 1);
     };
-    auto fetch = [&](Ops &o, int s) {
-        const unsigned char *st = xdlds + (size_t)(s % NS) * D::SB;
+    auto fetch = [&](Ops &o, int slot) {
+        const unsigned char *st = xdlds + (size_t)slot * D::SB;
 #pragma unroll
         for (int i = 0; i < RT; i++)
 #pragma unroll
@@ -876,6 +886,11 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
     };
     /* one stage through the matrix core; FULL: every column of the stage
      * is inside the row (no piece to zero) */
+    /* the current segment's 16 quarter scales per row tile, decoded: lane 16
+     * (z % 4) + m holds quarter m's (set as each segment starts) */
+    float sf[RT];
+#pragma unroll
+    for (int i = 0; i < RT; i++) sf[i] = 0.0f;
     auto mma = [&](const Ops &o, int s, auto full) {
         constexpr bool FULL = decltype(full)::value;
         const int sl = s & 7;                    /* stage within its segment */
@@ -887,8 +902,9 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
 #pragma unroll
             for (int i = 0; i < RT; i++) {
                 const u32x4 zv = in ? o.a[i][qq] : u32x4{0u, 0u, 0u, 0u};
-                const float sx = dec_e8m0(
-                    (xs_get(sr[i], 16 * (z & 3) + 2 * sl + qq) >> (8 * (z >> 2))) & 0xffu);
+                const float sx = __builtin_bit_cast(
+                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sf[i]),
+                                                     16 * (z & 3) + 2 * sl + qq));
                 const float sv = in ? sx : 0.0f;
                 af[i][0] = fp8x8_bf16(zv.x, zv.y, sv);
                 af[i][1] = fp8x8_bf16(zv.z, zv.w, sv);
@@ -905,6 +921,12 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
         }
     };
     auto run = [&](const Ops &o, int s) {
+        if ((s & 7) == 0) {                      /* a segment starts: its scales */
+            asm volatile("" ::: "memory");
+            const int z = s >> 3;
+#pragma unroll
+            for (int i = 0; i < RT; i++) sf[i] = dec_e8m0((sr[i] >> (8 * (z >> 2))) & 0xffu);
+        }
         if (XD_K * (s + 1) <= cols)
             mma(o, s, std::true_type{});
         else
@@ -922,19 +944,22 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
     };
     /* nst is even: stages 1, 2 | 3, 4 | ... pair up, and the last is odd */
     Ops o0, o1;
-    sync(0);
+    sync(0, 0);
     fetch(o0, 0);
-    int s = 1;
+    int s = 1, slot = 1;
+    auto next = [&](int q) { return q + 1 == NS ? 0 : q + 1; };
     for (; s + 1 < nst; s += 2) {
-        sync(s);
-        fetch(o1, s);
+        sync(s, slot);
+        fetch(o1, slot);
         run(o0, s - 1);
-        sync(s + 1);
-        fetch(o0, s + 1);
+        slot = next(slot);
+        sync(s + 1, slot);
+        fetch(o0, slot);
         run(o1, s);
+        slot = next(slot);
     }
-    sync(s);
-    fetch(o1, s);
+    sync(s, slot);
+    fetch(o1, slot);
     run(o0, s - 1);
     run(o1, s);
     /* y = (hi + mid) + lo per (row, token), as k_fp8_mxn */

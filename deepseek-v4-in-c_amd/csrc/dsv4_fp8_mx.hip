@@ -762,14 +762,15 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
      * row 4 i + lane / 16, slot lane % 16); rows past the matrix read its
      * last row, term rows past the group's tokens its first (never used) */
     constexpr int DH = 2, DX = D::DX;                /* loads of each kind    */
-    const uint8_t *wsrc[DH];
+    const uint8_t *wsrc[DH], *wrow[DH];
     int wcol[DH], xoff[DX];
     const uint16_t *xsrc[DX];
 #pragma unroll
     for (int i = 0; i < DH; i++) {
         const int R = 8 * (DH * w + i) + (lane >> 3);
         wcol[i] = 16 * ((lane & 7) ^ (R & 7));
-        wsrc[i] = W + (size_t)min(row0 + R, rows - 1) * cols;
+        wrow[i] = W + (size_t)min(row0 + R, rows - 1) * cols;
+        wsrc[i] = wrow[i] + wcol[i];
     }
 #pragma unroll
     for (int i = 0; i < DX; i++) {
@@ -785,14 +786,14 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
         if (k0 + XD_K <= cols) {                 /* the whole stage inside the rows */
 #pragma unroll
             for (int i = 0; i < DH; i++)
-                __builtin_amdgcn_global_load_lds((const void *)(wsrc[i] + k0 + wcol[i]),
+                __builtin_amdgcn_global_load_lds((const void *)(wsrc[i] + k0),
                                                  (lds_void *)(st + 1024 * (DH * w + i)), 16, 0,
                                                  0);
         } else {
 #pragma unroll
             for (int i = 0; i < DH; i++) {
                 const int k = k0 + wcol[i];
-                __builtin_amdgcn_global_load_lds((const void *)(wsrc[i] + (k < cols ? k : 0)),
+                __builtin_amdgcn_global_load_lds((const void *)(wrow[i] + (k < cols ? k : 0)),
                                                  (lds_void *)(st + 1024 * (DH * w + i)), 16, 0,
                                                  0);
             }
@@ -867,22 +868,33 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (s + NS - 1 < nst) issue(s + NS - 1, slot == 0 ? NS - 1 : slot - 1);
     };
+    /* each read's lane offset within a stage, formed once */
+    int fa[RT][2], fb[2][2][CT];
+#pragma unroll
+    for (int i = 0; i < RT; i++)
+#pragma unroll
+        for (int qq = 0; qq < 2; qq++) fa[i][qq] = aoff[i] + 16 * ((4 * qq + g) ^ asw[i]);
+#pragma unroll
+    for (int qq = 0; qq < 2; qq++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int n = 0; n < CT; n++)
+                fb[qq][h][n] = boff[n] + 16 * ((8 * qq + 2 * g + h) ^ bsw[n]);
     auto fetch = [&](Ops &o, int slot) {
         const unsigned char *st = xdlds + (size_t)slot * D::SB;
 #pragma unroll
         for (int i = 0; i < RT; i++)
 #pragma unroll
             for (int qq = 0; qq < 2; qq++)
-                o.a[i][qq] = *reinterpret_cast<const u32x4 *>(
-                    st + aoff[i] + 16 * ((4 * qq + g) ^ asw[i]));
+                o.a[i][qq] = *reinterpret_cast<const u32x4 *>(st + fa[i][qq]);
 #pragma unroll
         for (int qq = 0; qq < 2; qq++)
 #pragma unroll
             for (int h = 0; h < 2; h++)
 #pragma unroll
                 for (int n = 0; n < CT; n++)
-                    o.b[qq][h][n] = *reinterpret_cast<const u32x4 *>(
-                        st + boff[n] + 16 * ((8 * qq + 2 * g + h) ^ bsw[n]));
+                    o.b[qq][h][n] = *reinterpret_cast<const u32x4 *>(st + fb[qq][h][n]);
     };
     /* one stage through the matrix core; FULL: every column of the stage
      * is inside the row (no piece to zero) */

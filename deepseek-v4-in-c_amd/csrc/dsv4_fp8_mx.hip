@@ -954,12 +954,52 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
                 }
         }
     };
-    /* nst is even: stages 1, 2 | 3, 4 | ... pair up, and the last is odd */
     Ops o0, o1;
     sync(0, 0);
     fetch(o0, 0);
-    int s = 1, slot = 1;
+    int slot = 1;
     auto next = [&](int q) { return q + 1 == NS ? 0 : q + 1; };
+    /* Whole segments first: group z runs stages 8z .. 8z + 7 (every column
+     * inside the rows) while stages 8z + 1 .. 8z + 8 are waited for and
+     * read, so each step's place in its segment is a compile-time constant
+     * and the segment's start and end need no test per stage. */
+    auto seg_step = [&](int z, auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const int r = 8 * z + j;                 /* the stage run; r + 1 is read */
+        Ops &of = (j & 1) ? o0 : o1;
+        const Ops &orun = (j & 1) ? o1 : o0;
+        sync(r + 1, slot);
+        fetch(of, slot);
+        if constexpr (j == 0) {
+#pragma unroll
+            for (int i = 0; i < RT; i++) sf[i] = dec_e8m0((sr[i] >> (8 * (z >> 2))) & 0xffu);
+        }
+        mma(orun, r, std::true_type{});
+        if constexpr (j == 7) {
+#pragma unroll
+            for (int i = 0; i < RT; i++)
+#pragma unroll
+                for (int n = 0; n < CT; n++) {
+                    tot[i][n] = z == 0 ? acc[i][n] : tot[i][n] + acc[i][n];
+                    acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
+                }
+        }
+        slot = next(slot);
+    };
+    int z = 0;
+    for (; 8 * z + 8 < nst && (8 * z + 8) * XD_K <= cols; z++) {
+        seg_step(z, std::integral_constant<int, 0>{});
+        seg_step(z, std::integral_constant<int, 1>{});
+        seg_step(z, std::integral_constant<int, 2>{});
+        seg_step(z, std::integral_constant<int, 3>{});
+        seg_step(z, std::integral_constant<int, 4>{});
+        seg_step(z, std::integral_constant<int, 5>{});
+        seg_step(z, std::integral_constant<int, 6>{});
+        seg_step(z, std::integral_constant<int, 7>{});
+    }
+    /* the rest stage by stage (nst is even: stages 1, 2 | 3, 4 | ... pair up,
+     * and the last is odd) */
+    int s = 8 * z + 1;
     for (; s + 1 < nst; s += 2) {
         sync(s, slot);
         fetch(o1, slot);

@@ -780,10 +780,11 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
         xsrc[i] = xt + ((size_t)t0 * XNT + jj) * cpad + 8 * ((lane & 15) ^ (j & 15));
         xoff[i] = D::WB + 1024 * xi;
     }
-    auto issue = [&](int s, int slot) {
+    /* FULL: the caller knows the whole stage lies inside the rows */
+    auto issue = [&](int s, int slot, auto full) {
         unsigned char *st = xdlds + (size_t)slot * D::SB;
         const int k0 = XD_K * s;
-        if (k0 + XD_K <= cols) {                 /* the whole stage inside the rows */
+        if (decltype(full)::value || k0 + XD_K <= cols) {
 #pragma unroll
             for (int i = 0; i < DH; i++)
                 __builtin_amdgcn_global_load_lds((const void *)(wsrc[i] + k0),
@@ -836,7 +837,7 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < NS - 1; s++)
-        if (s < nst) issue(s, s);
+        if (s < nst) issue(s, s, std::false_type{});
     __builtin_amdgcn_sched_barrier(0);
     /* every segment's scales for the wave's row tiles, requested once behind
      * the first stages (the loop then issues no memory request the compiler
@@ -866,7 +867,13 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
     auto sync = [&](int s, int slot) {
         xd_wait<D::DPW>(min(NS - 2, nst - 1 - s));
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (s + NS - 1 < nst) issue(s + NS - 1, slot == 0 ? NS - 1 : slot - 1);
+        if (s + NS - 1 < nst) issue(s + NS - 1, slot == 0 ? NS - 1 : slot - 1, std::false_type{});
+    };
+    /* the same where stage s + NS - 1 exists and lies inside the rows */
+    auto sync_deep = [&](int s, int slot) {
+        xd_vm<(NS - 2) * D::DPW>();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        issue(s + NS - 1, slot == 0 ? NS - 1 : slot - 1, std::true_type{});
     };
     /* each read's lane offset within a stage, formed once */
     int fa[RT][2], fb[2][2][CT];
@@ -963,12 +970,15 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
      * inside the rows) while stages 8z + 1 .. 8z + 8 are waited for and
      * read, so each step's place in its segment is a compile-time constant
      * and the segment's start and end need no test per stage. */
-    auto seg_step = [&](int z, auto jc) {
+    auto seg_step = [&](int z, auto jc, auto deep) {
         constexpr int j = decltype(jc)::value;
         const int r = 8 * z + j;                 /* the stage run; r + 1 is read */
         Ops &of = (j & 1) ? o0 : o1;
         const Ops &orun = (j & 1) ? o1 : o0;
-        sync(r + 1, slot);
+        if constexpr (decltype(deep)::value)
+            sync_deep(r + 1, slot);
+        else
+            sync(r + 1, slot);
         fetch(of, slot);
         if constexpr (j == 0) {
 #pragma unroll
@@ -986,17 +996,23 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
         }
         slot = next(slot);
     };
+    auto segment = [&](int z, auto deep) {
+        seg_step(z, std::integral_constant<int, 0>{}, deep);
+        seg_step(z, std::integral_constant<int, 1>{}, deep);
+        seg_step(z, std::integral_constant<int, 2>{}, deep);
+        seg_step(z, std::integral_constant<int, 3>{}, deep);
+        seg_step(z, std::integral_constant<int, 4>{}, deep);
+        seg_step(z, std::integral_constant<int, 5>{}, deep);
+        seg_step(z, std::integral_constant<int, 6>{}, deep);
+        seg_step(z, std::integral_constant<int, 7>{}, deep);
+    };
+    /* deep: every stage the group requests (up to 8z + 8 + NS - 1) exists and
+     * lies inside the rows, so its waits and loads need no test */
     int z = 0;
-    for (; 8 * z + 8 < nst && (8 * z + 8) * XD_K <= cols; z++) {
-        seg_step(z, std::integral_constant<int, 0>{});
-        seg_step(z, std::integral_constant<int, 1>{});
-        seg_step(z, std::integral_constant<int, 2>{});
-        seg_step(z, std::integral_constant<int, 3>{});
-        seg_step(z, std::integral_constant<int, 4>{});
-        seg_step(z, std::integral_constant<int, 5>{});
-        seg_step(z, std::integral_constant<int, 6>{});
-        seg_step(z, std::integral_constant<int, 7>{});
-    }
+    for (; 8 * z + 8 + NS - 1 < nst && (8 * z + 8 + NS) * XD_K <= cols; z++)
+        segment(z, std::true_type{});
+    for (; 8 * z + 8 < nst && (8 * z + 8) * XD_K <= cols; z++)
+        segment(z, std::false_type{});
     /* the rest stage by stage (nst is even: stages 1, 2 | 3, 4 | ... pair up,
      * and the last is odd) */
     int s = 8 * z + 1;

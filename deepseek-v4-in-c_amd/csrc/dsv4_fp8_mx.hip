@@ -1496,16 +1496,17 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
     /* the DMA-staged kernel: uniform scales and pre-split terms, groups of
      * at most 20 tokens (as many groups as 20-token groups need, the tokens
      * spread evenly over them) */
-    /* the DMA-staged kernel (uniform scales, pre-split terms) from three
-     * groups of 20 tokens: 7168 x 7168 at 64 tokens 54.5-58.4 against
-     * 63.4-64.3 us; with one or two groups its 56 or 112 workgroups leave
-     * most CUs idle and the register-staged kernel, with twice the
-     * workgroups, is faster (32 tokens 45 against 52 us, 16 tokens 34
-     * against 51). DSV4_GPU_MXD = 0 / 1 forces it off / on where it applies. */
+    /* the DMA-staged kernel (uniform scales, pre-split terms) from two
+     * groups of 20 tokens (7168 x 7168, us, against the register-staged
+     * kernel: 64 tokens 43.7-44.8 / 62.4-64.3, 40 tokens 39.4-39.8 /
+     * 45.7-46.1, 21 tokens 38.6-38.8 / 42.7); with one group its 56
+     * workgroups leave most CUs idle and the register-staged kernel, with
+     * twice the workgroups, is faster (16 tokens 37.2-37.7 / 33.5).
+     * DSV4_GPU_MXD = 0 / 1 forces it off / on where it applies. */
     const int gd = (nt + XTOK * 4 - 1) / (XTOK * 4);
     const int dme = mx_env("DSV4_GPU_MXD", -1);
     constexpr size_t lds_d = xd_lds<8, 5>();        /* 158,720 bytes */
-    if ((dme < 0 ? gd >= 3 : dme > 0) && uni && xt && lds_d <= dsv4_lds_limit()) {
+    if ((dme < 0 ? gd >= 2 : dme > 0) && uni && xt && lds_d <= dsv4_lds_limit()) {
         static int opted_d = 0;                    /* 1 granted, -1 refused */
         if (!opted_d) opted_d = optin(k_fp8_mxd<2, 2, 8, 5>, "fp8 mxd") ? 1 : -1;
         if (opted_d > 0) {

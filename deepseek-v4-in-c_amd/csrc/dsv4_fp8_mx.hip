@@ -681,26 +681,32 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
  * (the launcher: 8) owns 16 MW rows (MW tiles) and a group of up to 20
  * tokens (4 column tiles of five); wave w takes RT row tiles and CT column
  * tiles (RT x CT = 4; the launcher uses 2 x 2, so each A fragment feeds two
- * column tiles and each B fragment two row tiles: 1 x 4 and 2 x 1 measured
- * 57-76 against 54.5 us at 64 tokens). The K axis runs in stages of 128
- * columns (half a unit): the workgroup's weight rows x 128 bytes and its 60
- * term rows x 128 bf16,
- * copied by global_load_lds_dwordx4 (each lane's 16 bytes land at the
- * instruction's LDS base + 16 lane, so nothing in flight holds a register)
- * into a ring of NS stages, NS - 1 of them in flight while one is
- * read. Each lane fetches the piece that the swizzled layout puts in its
- * slot: weight piece c of row R sits at piece c ^ (R & 7) of its 128-byte
- * row, term piece c of term row j at c ^ (j & 15) of its 256-byte row, so
- * the fragment reads are free of bank conflicts (an in-bounds LDS probe on
- * MI355X: 437-495 GB/s per CU for these patterns against 146 and 76 with
- * the rows unswizzled). A wave reads stage s's fragments into one register
- * set while the set read at stage s - 1 runs through the matrix core, so
- * the reads' latency hides behind a stage of MFMAs. Per (row, term column)
- * the chain is k_fp8_mxn's: the same K steps (whole units, zero operands
- * past cols), the same fragments, one accumulator per segment from zero,
- * the segments joined in order and y = (hi + mid) + lo, so the bits are the
- * same. MW = 4 with a 3-stage ring (two workgroups per CU) measured slower
- * at 64 tokens (59.6-60.6 against 55.8-56.3 us). */
+ * column tiles and each B fragment two row tiles).
+ *
+ * The K axis runs in stages of 128 columns (half a unit): the workgroup's
+ * weight rows x 128 bytes and its 60 term rows x 128 bf16, copied by
+ * global_load_lds_dwordx4 (each lane's 16 bytes land at the instruction's
+ * LDS base + 16 lane, so nothing in flight holds a register) into a ring of
+ * NS stages, NS - 1 of them in flight while one is read. Each lane fetches
+ * the piece that the swizzled layout puts in its slot: weight piece c of
+ * row R sits at piece c ^ (R & 7) of its 128-byte row, term piece c of term
+ * row j at c ^ (j & 15) of its 256-byte row, so the fragment reads are free
+ * of bank conflicts (an in-bounds LDS probe on MI355X: 437-495 GB/s per CU
+ * for these patterns against 146 and 76 with the rows unswizzled). A wave
+ * reads stage s's fragments into one register set while the set read at
+ * stage s - 1 runs through the matrix core, so the reads' latency hides
+ * behind a stage of MFMAs.
+ *
+ * On a SIMD the VALU and the scalar unit's work adds to the matrix core's
+ * time, so the per-stage path is kept short: the segment's scales are
+ * decoded once per segment, each lane's read offsets and load pointers are
+ * formed once, and whole segments are unrolled so that a stage's place in
+ * its segment is a compile-time constant.
+ *
+ * Per (row, term column) the chain is k_fp8_mxn's: the same K steps (whole
+ * units, zero operands past cols), the same fragments, one accumulator per
+ * segment from zero, the segments joined in order and y = (hi + mid) + lo,
+ * so the bits are the same. */
 constexpr int XD_K = 128;                        /* K (weight bytes) per stage */
 constexpr int XD_TR = XTOK * 4 * XNT;            /* term rows per stage (60)   */
 

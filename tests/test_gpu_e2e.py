@@ -89,3 +89,28 @@ def test_gpu_trunk_argmax_identical(tmp_path):
     assert int(s45.group(5)) == int(s45.group(6)) == 4 * 46
     # moe_n once per layer and chunk of every chunking: 46 + 23 + 16 + 1 chunks
     assert int(s45.group(7)) == 4 * (46 + 23 + 16 + 1)
+
+
+def test_gpu_trunk_matrix_core_form(tmp_path, monkeypatch):
+    """The same run with DSV4_GPU_FP8_MX=1: the FP8 trunk takes the bf16
+    matrix-core form, one token at a time (k_fp8_mx1) in passes 2 and 3 and
+    batched in passes 4 and 5 (chunks of 2 and 3 on the register-staged
+    kernel, 23 and 46 tokens on the DMA-staged one; a kernel trace of this
+    run lists k_fp8_mx1, k_fp8_mxn and k_fp8_mxd). The reference's prefill
+    protocol must still give every position the per-token pass's bits, and
+    the argmax must still match the CPU reference at every position."""
+    monkeypatch.setenv("DSV4_GPU_FP8_MX", "1")
+    ckpt, tf = e2e_common.prepare(tmp_path)
+    print("e2e: checkpoint %s, matrix-core FP8 form" % ckpt, flush=True)
+    p, rows, summ = e2e_common.run(ckpt, tf)
+    print(p.stdout[-3000:], flush=True)
+    sys.stdout.flush()
+    assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-2000:]
+    assert summ, p.stdout[-2000:]
+    assert int(summ.group(1)) == 46 and int(summ.group(2)) == 46
+    assert float(summ.group(3)) < 2e-3
+    s45 = p.summary45
+    assert s45, p.stdout[-2000:]
+    assert s45.group(1) == "1,2,3,46" and int(s45.group(2)) == 4 * 46
+    assert int(s45.group(3)) == int(s45.group(4)) == 4 * 46
+    assert int(s45.group(5)) == int(s45.group(6)) == 4 * 46

@@ -164,16 +164,20 @@ __device__ __forceinline__ void xu_load(XUnit<UNI> &U, const uint8_t *W, const u
 
 /* Uniform scales: the E8M0 bytes of the 16 quarters of the segment at k0
  * (quarter m = 4 unit + q in lane m % 16; srow is the tile's scale row
- * offset). xs_get reads quarter m's byte back from its lane. */
+ * offset). Decoded once per segment, xs_getf reads quarter m's scale back
+ * from its lane. */
 __device__ __forceinline__ uint32_t xs_seg(const uint8_t *S, int srow, uint32_t bc_m, int k0,
                                            int cols, int lane)
 {
     return ldg8(S + srow + div_bc(min(k0 + 64 * (lane & 15), cols - 1), bc_m));
 }
 
-__device__ __forceinline__ uint32_t xs_get(uint32_t ssb, int m)
+/* Quarter m's scale from a register of decoded scales (lane m holds
+ * quarter m's 2^(e - 127), decoded once per segment): one readlane per
+ * fragment instead of a readlane and a scalar decode. */
+__device__ __forceinline__ float xs_getf(float sf, int m)
 {
-    return (uint32_t)__builtin_amdgcn_readlane((int)ssb, m);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sf), m));
 }
 
 template <bool UNI>
@@ -198,6 +202,18 @@ __device__ __forceinline__ void xu_frags(v8bf *a, const unsigned char *buf, int 
     a[1] = fp8x8_bf16(z.z, z.w, s);
 }
 
+/* The same with the quarter's scale already decoded (uniform scales). */
+__device__ __forceinline__ void xu_frags_f(v8bf *a, const unsigned char *buf, int q, float sq,
+                                           bool live, int lane)
+{
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(buf + (lane & 15) * XWP + 64 * q +
+                                                      16 * (lane >> 4));
+    const u32x4 z = live ? v : u32x4{0u, 0u, 0u, 0u};
+    const float s = live ? sq : 0.0f;
+    a[0] = fp8x8_bf16(z.x, z.y, s);
+    a[1] = fp8x8_bf16(z.z, z.w, s);
+}
+
 /* ------------------------------------------------------ single token */
 
 /* One segment of a tile for a single token: units j = 0..nu-1 of the
@@ -210,7 +226,7 @@ template <bool UNI, bool PF>
 __device__ __forceinline__ v4f mx1_seg(XUnit<UNI> (&P4)[XSEG_U], unsigned char *buf,
                                        const uint16_t *pl, int bplane, const uint8_t *W,
                                        const uint8_t *S, int rows, int cols, uint32_t bc_m,
-                                       int k0, int nu, uint32_t ssb, int row0n, int srown,
+                                       int k0, int nu, float sfb, int row0n, int srown,
                                        int k0n, int nun, int lane)
 {
     const int g = lane >> 4;
@@ -236,7 +252,10 @@ __device__ __forceinline__ v4f mx1_seg(XUnit<UNI> (&P4)[XSEG_U], unsigned char *
             for (int q = 0; q < 4; q++) {
                 const int k = k0 + XU * j + 64 * q + 16 * g;
                 v8bf af[2];
-                xu_frags(af, buf, q, UNI ? xs_get(ssb, 4 * j + q) : sbj[q], k < cols, lane);
+                if (UNI)
+                    xu_frags_f(af, buf, q, xs_getf(sfb, 4 * j + q), k < cols, lane);
+                else
+                    xu_frags(af, buf, q, sbj[q], k < cols, lane);
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
                     const u32x4 bw = *reinterpret_cast<const u32x4 *>(
@@ -392,13 +411,14 @@ k_fp8_mx1(Dsv4Fp8Mx a)
         const int k0n = sn * XSEG, nun = min(XSEG_U, nu_all - sn * XSEG_U);
         const uint32_t ssn = UNI ? xs_seg(S, srown, a.bc_m, k0n, cols, lane) : 0u;
         const v4f acc = mx1_seg<UNI, true>(P4, buf, pl, bplane, W, S, rows, cols, a.bc_m,
-                                           s * XSEG, min(XSEG_U, nu_all - s * XSEG_U), ssb,
+                                           s * XSEG, min(XSEG_U, nu_all - s * XSEG_U),
+                                           UNI ? dec_e8m0(ssb) : 0.0f,
                                            row0n, srown, k0n, nun, lane);
         finish(acc, sn == sa);
         it = itn; s = sn; row0 = row0n; ssb = ssn;
     }
     const v4f acc = mx1_seg<UNI, false>(P4, buf, pl, bplane, W, S, rows, cols, a.bc_m, s * XSEG,
-                                        min(XSEG_U, nu_all - s * XSEG_U), ssb, 0, 0, 0, 1, lane);
+                                        min(XSEG_U, nu_all - s * XSEG_U), UNI ? dec_e8m0(ssb) : 0.0f, 0, 0, 0, 1, lane);
     finish(acc, true);
 }
 
@@ -606,6 +626,7 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
     xu_load<UNI, false>(P[1], W, S, srow, bc_m, wrow0, rows, cols, XU * min(1, nu - 1), lane);
     __builtin_amdgcn_sched_barrier(0);
     for (int s0 = 0; s0 < nu; s0 += XSEG_U) {
+        const float sfb = UNI ? dec_e8m0(ssb) : 0.0f;   /* this segment's scales */
 #pragma unroll
         for (int j = 0; j < XSEG_U; j++) {
             const int u = s0 + j;
@@ -636,7 +657,10 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
                 for (int q = 0; q < 4; q++) {
                     const int k = XU * u + 64 * q + 16 * g;
                     v8bf af[2];
-                    xu_frags(af, buf, q, UNI ? xs_get(ssb, 4 * j + q) : sb[q], k < cols, lane);
+                    if (UNI)
+                        xu_frags_f(af, buf, q, xs_getf(sfb, 4 * j + q), k < cols, lane);
+                    else
+                        xu_frags(af, buf, q, sb[q], k < cols, lane);
 #pragma unroll
                     for (int h = 0; h < 2; h++) {
 #pragma unroll
@@ -1177,6 +1201,11 @@ k_fp8_mxk(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
     xu_load<UNI, false>(P[1], W, S, srow, bc_m, wrow0, rows, cols, XU * min(ub + 1, nu - 1), lane);
     __builtin_amdgcn_sched_barrier(0);
     for (int s0 = 0; s0 < up; s0 += XSEG_U) {
+        /* this segment's scales, decoded once where that measured faster
+         * (4 parts: 2 tokens 15.4 -> 14.9 us, 4 tokens 18.2 -> 17.8; with 2
+         * parts, 8 tokens, the scalar decode per quarter stays: 24.0 against
+         * 24.5) */
+        const float sfb = UNI && KP == 4 ? dec_e8m0(ssb) : 0.0f;
 #pragma unroll
         for (int j = 0; j < XSEG_U; j++) {
             const int i = s0 + j, u = ub + i;
@@ -1201,7 +1230,13 @@ k_fp8_mxk(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
                 for (int q = 0; q < 4; q++) {
                     const int k = XU * u + 64 * q + 16 * g;
                     v8bf af[2];
-                    xu_frags(af, buf, q, UNI ? xs_get(ssb, 4 * j + q) : sb[q], k < cols, lane);
+                    if (UNI && KP == 4)
+                        xu_frags_f(af, buf, q, xs_getf(sfb, 4 * j + q), k < cols, lane);
+                    else
+                        xu_frags(af, buf, q,
+                                 UNI ? (uint32_t)__builtin_amdgcn_readlane((int)ssb, 4 * j + q)
+                                     : sb[q],
+                                 k < cols, lane);
 #pragma unroll
                     for (int h = 0; h < 2; h++) {
                         const u32x4 bw = *reinterpret_cast<const u32x4 *>(

@@ -1537,24 +1537,39 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
     /* the DMA-staged kernel: uniform scales and pre-split terms, groups of
      * at most 20 tokens (as many groups as 20-token groups need, the tokens
      * spread evenly over them) */
-    /* the DMA-staged kernel (uniform scales, pre-split terms) from two
-     * groups of 20 tokens (7168 x 7168, us, against the register-staged
-     * kernel: 64 tokens 43.7-44.8 / 62.4-64.3, 40 tokens 39.4-39.8 /
-     * 45.7-46.1, 21 tokens 38.6-38.8 / 42.7); with one group its 56
-     * workgroups leave most CUs idle and the register-staged kernel, with
-     * twice the workgroups, is faster (16 tokens 37.2-37.7 / 33.5).
-     * DSV4_GPU_MXD = 0 / 1 forces it off / on where it applies. */
+    /* the DMA-staged kernel (uniform scales, pre-split terms) wherever the
+     * segment split above did not take the batch. 7168 x 7168, us, against
+     * the register-staged kernel: 64 tokens 43.1-43.5 / 62.4-64.3, 41
+     * tokens 40.8-41.2 / 54.5-54.9, 32 tokens 30.4 / 45.2-45.5, 16 tokens
+     * 28.0-28.1 / 33.4-33.6, 11 tokens 27.7-27.9 / 32.0. Its workgroups
+     * are 8 waves over 128 rows from three groups of 20 tokens on (64
+     * tokens: 43.1-43.5 against 45.7 with 4 waves), else 4 waves over 64
+     * rows, so that one or two groups still cover the CUs (32 tokens 30.4
+     * against 39.1-39.5 with 8 waves, 16 tokens 28.0 against 37.6).
+     * DSV4_GPU_MXD = 0 / 1 forces it off / on where it applies,
+     * DSV4_GPU_MXD_MW = 4 / 8 the workgroup size. */
     const int gd = (nt + XTOK * 4 - 1) / (XTOK * 4);
     const int dme = mx_env("DSV4_GPU_MXD", -1);
-    constexpr size_t lds_d = xd_lds<8, 5>();        /* 158,720 bytes */
-    if ((dme < 0 ? gd >= 2 : dme > 0) && uni && xt && lds_d <= dsv4_lds_limit()) {
+    const int dmw = mx_env("DSV4_GPU_MXD_MW", gd >= 3 ? 8 : 4);
+    const size_t lds_d = dmw == 4 ? xd_lds<4, 3>() : xd_lds<8, 5>();
+    if (dme != 0 && uni && xt && lds_d <= dsv4_lds_limit()) {
         static int opted_d = 0;                    /* 1 granted, -1 refused */
-        if (!opted_d) opted_d = optin(k_fp8_mxd<2, 2, 8, 5>, "fp8 mxd") ? 1 : -1;
+        if (!opted_d)
+            opted_d = optin(k_fp8_mxd<2, 2, 8, 5>, "fp8 mxd") &&
+                              optin(k_fp8_mxd<2, 2, 4, 3>, "fp8 mxd")
+                          ? 1
+                          : -1;
         if (opted_d > 0) {
             const int td = (nt + gd - 1) / gd;      /* tokens spread evenly */
             HIP_OK(xsplit(), "fp8 mxn x split launch");
-            hipLaunchKernelGGL((k_fp8_mxd<2, 2, 8, 5>), dim3((rows + 127) / 128, gd), dim3(512),
-                               lds_d, st, y, W, S, rows, cols, sc, blk_r, bc_m, nt, td, xt, cpad);
+            if (dmw == 4)
+                hipLaunchKernelGGL((k_fp8_mxd<2, 2, 4, 3>), dim3((rows + 63) / 64, gd), dim3(256),
+                                   lds_d, st, y, W, S, rows, cols, sc, blk_r, bc_m, nt, td, xt,
+                                   cpad);
+            else
+                hipLaunchKernelGGL((k_fp8_mxd<2, 2, 8, 5>), dim3((rows + 127) / 128, gd),
+                                   dim3(512), lds_d, st, y, W, S, rows, cols, sc, blk_r, bc_m, nt,
+                                   td, xt, cpad);
             HIP_OK(hipGetLastError(), "fp8 mxd launch");
             return 0;
         }

@@ -702,13 +702,18 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
 
 /* The batched kernel with its operands staged by direct-to-LDS loads
  * (k_fp8_mxd; uniform scales, pre-split x terms). A workgroup of MW waves
- * (the launcher: 8) owns 16 MW rows (MW tiles) and a group of up to 20
- * tokens (4 column tiles of five); wave w takes RT row tiles and CT column
- * tiles (RT x CT = 4; the launcher uses 2 x 2, so each A fragment feeds two
- * column tiles and each B fragment two row tiles).
+ * owns 16 MW rows (MW tiles) and a group of tokens in one of two layouts:
+ *  - up to 20 tokens in 4 column tiles of five (token j in columns 3 j ..
+ *    3 j + 2, column 15 unused); wave w takes RT x CT = 2 x 2 tiles, so
+ *    each A fragment feeds two column tiles and each B fragment two row
+ *    tiles;
+ *  - planar (CT = 3): up to 16 tokens, column tile n holding term n of
+ *    every token (token = column), so every column is used; wave w takes
+ *    its row tile and all three, and a token's terms meet in one lane.
  *
  * The K axis runs in stages of 128 columns (half a unit): the workgroup's
- * weight rows x 128 bytes and its 60 term rows x 128 bf16, copied by
+ * weight rows x 128 bytes and its group's term rows (60 or 48) x 128 bf16,
+ * copied by
  * global_load_lds_dwordx4 (each lane's 16 bytes land at the instruction's
  * LDS base + 16 lane, so nothing in flight holds a register) into a ring of
  * NS stages, NS - 1 of them in flight while one is read. Each lane fetches
@@ -733,19 +738,21 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
  * so the bits are the same. */
 constexpr int XD_K = 128;                        /* K (weight bytes) per stage */
 constexpr int XD_TR = XTOK * 4 * XNT;            /* term rows per stage (60)   */
+constexpr int XP_TOK = 16;                       /* tokens per planar group    */
+constexpr int XP_TR = XP_TOK * XNT;              /* its term rows (48)         */
 
-/* MW waves own 16 MW rows; a stage is their weights and the group's terms;
- * NS stages in the ring */
-template <int MW>
+/* MW waves own 16 MW rows; a stage is their weights and the group's TR term
+ * rows; NS stages in the ring */
+template <int MW, int TR = XD_TR>
 struct XdDim {
     static constexpr int R = 16 * MW;                    /* rows per workgroup   */
     static constexpr int WB = R * XD_K;                  /* weight bytes / stage */
-    static constexpr int SB = WB + XD_TR * XD_K * 2;     /* bytes per stage      */
-    static constexpr int DX = (XD_TR / 4 + MW - 1) / MW; /* term loads per wave  */
+    static constexpr int SB = WB + TR * XD_K * 2;        /* bytes per stage      */
+    static constexpr int DX = (TR / 4 + MW - 1) / MW;    /* term loads per wave  */
     static constexpr int DPW = 2 + DX;                   /* loads per wave/stage */
 };
-template <int MW, int NS>
-constexpr size_t xd_lds() { return (size_t)NS * XdDim<MW>::SB; }
+template <int MW, int NS, int TR = XD_TR>
+constexpr size_t xd_lds() { return (size_t)NS * XdDim<MW, TR>::SB; }
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -775,9 +782,15 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
     extern __shared__ __attribute__((aligned(16))) unsigned char xdlds[];
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    static_assert(RT * CT == 4, "MW waves x RT x CT = MW row tiles x 4 column tiles");
+    /* PL: the planar group (XP_TOK tokens, column tile n = term n of every
+     * token, token = column); else groups of 20 tokens in 4 column tiles of
+     * five (token j in columns 3 j .. 3 j + 2) */
+    constexpr bool PL = CT == XNT;
+    constexpr int TR = PL ? XP_TR : XD_TR;
+    static_assert(PL ? RT == 1 : RT * CT == 4,
+                  "MW waves x RT x CT = MW row tiles x 4 column tiles (or x 3 terms, one each)");
     static_assert(NS >= 2 && NS <= 5, "stage waits for up to 3 stages ahead");
-    using D = XdDim<MW>;
+    using D = XdDim<MW, TR>;
     const int rp = w % (MW / RT), ch = w / (MW / RT);
     const int row0 = blockIdx.x * D::R;
     const int t0 = blockIdx.y * tpg;
@@ -788,7 +801,7 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
 
     /* the loads: weight instructions 2w, 2w + 1 (rows 8 i .. 8 i + 7 of the
      * workgroup, lane -> row 8 i + lane / 8, slot lane % 8) and term
-     * instructions 2w, min(2w + 1, 14) (term rows 4 i .. 4 i + 3, lane ->
+     * instructions DX w + i, at most TR / 4 - 1 (term rows 4 i .. 4 i + 3, lane ->
      * row 4 i + lane / 16, slot lane % 16); rows past the matrix read its
      * last row, term rows past the group's tokens its first (never used) */
     constexpr int DH = 2, DX = D::DX;                /* loads of each kind    */
@@ -804,7 +817,7 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
     }
 #pragma unroll
     for (int i = 0; i < DX; i++) {
-        const int xi = min(DX * w + i, XD_TR / 4 - 1);
+        const int xi = min(DX * w + i, TR / 4 - 1);
         const int j = 4 * xi + (lane >> 4);
         const int jj = j / XNT < ntok ? j : 0;
         xsrc[i] = xt + ((size_t)t0 * XNT + jj) * cpad + 8 * ((lane & 15) ^ (j & 15));
@@ -835,9 +848,10 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
                                              (lds_void *)(st + xoff[i]), 16, 0, 0);
     };
 
-    /* the fragment reads: A row 16 a + col of tile a = 2 rp + i; B term row
-     * 15 n + min(col, 14) of column tile n = 2 ch + jn (column 15 repeats
-     * column 14; its result is never used) */
+    /* the fragment reads: A row 16 a + col of tile a = RT rp + i; B term row
+     * 15 n + min(col, 14) of column tile n = CT ch + jn (column 15 repeats
+     * column 14; its result is never used), or in the planar group term row
+     * 3 col + n (token col, term n) */
     int aoff[RT], asw[RT], boff[CT], bsw[CT];
     bool live[RT];
     int srow[RT];
@@ -852,7 +866,7 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
     }
 #pragma unroll
     for (int n = 0; n < CT; n++) {
-        const int j = 15 * (CT * ch + n) + min(col, 14);
+        const int j = PL ? XNT * col + n : 15 * (CT * ch + n) + min(col, 14);
         boff[n] = D::WB + j * (2 * XD_K);
         bsw[n] = j & 15;
     }
@@ -1061,6 +1075,17 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
     run(o0, s - 1);
     run(o1, s);
     /* y = (hi + mid) + lo per (row, token), as k_fp8_mxn */
+    if constexpr (PL) {
+#pragma unroll
+        for (int i = 0; i < RT; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int rr = row0 + 16 * (RT * rp + i) + 4 * g + j;
+                if (live[i] && col < ntok && rr < rows)
+                    y[(size_t)(t0 + col) * rows + rr] = (tot[i][0][j] + tot[i][1][j]) + tot[i][2][j];
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < RT; i++)
 #pragma unroll
@@ -1534,42 +1559,67 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
             return 0;
         }
     }
-    /* the DMA-staged kernel: uniform scales and pre-split terms, groups of
-     * at most 20 tokens (as many groups as 20-token groups need, the tokens
-     * spread evenly over them) */
     /* the DMA-staged kernel (uniform scales, pre-split terms) wherever the
      * segment split above did not take the batch. 7168 x 7168, us, against
      * the register-staged kernel: 64 tokens 43.1-43.5 / 62.4-64.3, 41
      * tokens 40.8-41.2 / 54.5-54.9, 32 tokens 30.4 / 45.2-45.5, 16 tokens
-     * 28.0-28.1 / 33.4-33.6, 11 tokens 27.7-27.9 / 32.0. Its workgroups
-     * are 8 waves over 128 rows from three groups of 20 tokens on (64
-     * tokens: 43.1-43.5 against 45.7 with 4 waves), else 4 waves over 64
-     * rows, so that one or two groups still cover the CUs (32 tokens 30.4
+     * 28.0-28.1 / 33.4-33.6, 11 tokens 27.7-27.9 / 32.0 (groups of 20).
+     * Planar groups of 16 tokens (3 column tiles, all used) against groups
+     * of 20 (4 tiles; 16 tokens fill 48 of their 64 columns): 64 tokens
+     * 40.6-40.8 / 42.9-43.4, 60 tokens 40.4-40.9 / 41.6-41.8, 41 tokens
+     * 37.4-37.6 / 40.7, 24 tokens 27.8-28.1 / 29.9-30.0, 17 tokens 27.1-27.2
+     * / 28.0-28.1, 11 tokens 24.5-24.7 / 27.8-28.0; but 40 tokens 37.5 /
+     * 30.2-30.4, where two groups of 20 (8 tiles) beat three of 16 (9), so
+     * the groups of 20 run where they take two or more groups and fewer
+     * tiles. Workgroups: planar, 4 waves over 64 rows (64 tokens 40.3-40.9
+     * against 42.6-43.5 with 8 waves over 128; 16 tokens 26.2 against 37.9),
+     * 2 waves over 32 when there is one group, so that it still covers the
+     * CUs (16 tokens 24.8-25.0 against 26.1-26.2); a ring of 3 stages (4:
+     * 64 tokens 40.5-40.6, 32 tokens 29.5 against 28.3-28.4). Groups of 20,
+     * 8 waves over 128 rows from three groups on (64 tokens: 43.1-43.5
+     * against 45.7 with 4 waves), else 4 waves over 64 rows (32 tokens 30.4
      * against 39.1-39.5 with 8 waves, 16 tokens 28.0 against 37.6).
-     * DSV4_GPU_MXD = 0 / 1 forces it off / on where it applies,
-     * DSV4_GPU_MXD_MW = 4 / 8 the workgroup size. */
-    const int gd = (nt + XTOK * 4 - 1) / (XTOK * 4);
+     * DSV4_GPU_MXD = 0 / 1 forces the kernel off / on where it applies,
+     * DSV4_GPU_MXD_PL = 0 / 1 the groups, DSV4_GPU_MXD_MW = 2 (planar only)
+     * / 4 / 8 the workgroup size. */
+    const int g20 = (nt + XTOK * 4 - 1) / (XTOK * 4), g16 = (nt + XP_TOK - 1) / XP_TOK;
+    const int dpl = mx_env("DSV4_GPU_MXD_PL", g20 >= 2 && 4 * g20 < XNT * g16 ? 0 : 1);
+    const int gtok = dpl ? XP_TOK : XTOK * 4;      /* tokens per group */
+    const int gd = (nt + gtok - 1) / gtok;
     const int dme = mx_env("DSV4_GPU_MXD", -1);
-    const int dmw = mx_env("DSV4_GPU_MXD_MW", gd >= 3 ? 8 : 4);
-    const size_t lds_d = dmw == 4 ? xd_lds<4, 3>() : xd_lds<8, 5>();
+    int dmw = mx_env("DSV4_GPU_MXD_MW", dpl ? (gd == 1 ? 2 : 4) : (gd >= 3 ? 8 : 4));
+    if (dmw != 2 && dmw != 8) dmw = 4;
+    if (!dpl && dmw == 2) dmw = 4;
+    const size_t lds_d = dpl ? (dmw == 2   ? xd_lds<2, 3, XP_TR>()
+                                : dmw == 4 ? xd_lds<4, 3, XP_TR>()
+                                           : xd_lds<8, 5, XP_TR>())
+                             : (dmw == 4 ? xd_lds<4, 3>() : xd_lds<8, 5>());
     if (dme != 0 && uni && xt && lds_d <= dsv4_lds_limit()) {
         static int opted_d = 0;                    /* 1 granted, -1 refused */
         if (!opted_d)
             opted_d = optin(k_fp8_mxd<2, 2, 8, 5>, "fp8 mxd") &&
-                              optin(k_fp8_mxd<2, 2, 4, 3>, "fp8 mxd")
+                              optin(k_fp8_mxd<2, 2, 4, 3>, "fp8 mxd") &&
+                              optin(k_fp8_mxd<1, 3, 8, 5>, "fp8 mxd") &&
+                              optin(k_fp8_mxd<1, 3, 4, 3>, "fp8 mxd") &&
+                              optin(k_fp8_mxd<1, 3, 2, 3>, "fp8 mxd")
                           ? 1
                           : -1;
         if (opted_d > 0) {
             const int td = (nt + gd - 1) / gd;      /* tokens spread evenly */
             HIP_OK(xsplit(), "fp8 mxn x split launch");
-            if (dmw == 4)
-                hipLaunchKernelGGL((k_fp8_mxd<2, 2, 4, 3>), dim3((rows + 63) / 64, gd), dim3(256),
-                                   lds_d, st, y, W, S, rows, cols, sc, blk_r, bc_m, nt, td, xt,
-                                   cpad);
-            else
-                hipLaunchKernelGGL((k_fp8_mxd<2, 2, 8, 5>), dim3((rows + 127) / 128, gd),
-                                   dim3(512), lds_d, st, y, W, S, rows, cols, sc, blk_r, bc_m, nt,
-                                   td, xt, cpad);
+#define XD(RT, CT, MWV, NSV) hipLaunchKernelGGL((k_fp8_mxd<RT, CT, MWV, NSV>),                 \
+                                                dim3((rows + 16 * MWV - 1) / (16 * MWV), gd),   \
+                                                dim3(64 * MWV), lds_d, st, y, W, S, rows, cols,  \
+                                                sc, blk_r, bc_m, nt, td, xt, cpad)
+            if (dpl) {
+                if (dmw == 2) XD(1, 3, 2, 3);
+                else if (dmw == 4) XD(1, 3, 4, 3);
+                else XD(1, 3, 8, 5);
+            } else {
+                if (dmw == 4) XD(2, 2, 4, 3);
+                else XD(2, 2, 8, 5);
+            }
+#undef XD
             HIP_OK(hipGetLastError(), "fp8 mxd launch");
             return 0;
         }

@@ -339,28 +339,34 @@ def test_batched_segment_split_keeps_bits(gpu, dsv4, monkeypatch, kp, xf):
         assert common.vec_rel_err(yn, oracle.matmul_fp8(x, W, S, blk_r, blk_c)) < TOL
 
 
-@pytest.mark.parametrize("mxd,mw", [("0", "8"), ("1", "8"), ("1", "4")])
-def test_batched_dma_staging_keeps_bits(gpu, dsv4, monkeypatch, mxd, mw):
+@pytest.mark.parametrize("mxd,mw,pl", [("0", "8", "0"), ("1", "8", "0"), ("1", "4", "0"),
+                                        ("1", "8", "1"), ("1", "4", "1"), ("1", "2", "1")])
+def test_batched_dma_staging_keeps_bits(gpu, dsv4, monkeypatch, mxd, mw, pl):
     """DSV4_GPU_MXD: the batched matrix-core kernel whose weight and x-term
     stages are copied into LDS by direct-to-LDS loads (uniform scales, groups
-    of up to 20 tokens; DSV4_GPU_MXD_MW: workgroups of 8 waves over 128 rows
-    or 4 over 64) against the register-staged one. Each gives each token
-    the single-token GEMV's bits: row counts that leave part of a workgroup
-    or a 16-row tile empty, a last unit past the row's end, one unit, a
-    single segment and sixteen, groups of 1 to 20 tokens."""
+    of up to 20 tokens with DSV4_GPU_MXD_PL=0, else planar groups of up to
+    16, one column tile per term; DSV4_GPU_MXD_MW: workgroups of 8 waves over
+    128 rows, 4 over 64 or, planar, 2 over 32) against the register-staged
+    one. Each gives each
+    token the single-token GEMV's bits: row counts that leave part of a
+    workgroup or a 16-row tile empty, a last unit past the row's end, one
+    unit, a single segment and sixteen, groups of 1 to 20 tokens."""
     monkeypatch.setenv("DSV4_GPU_FP8_MX", "1")
     monkeypatch.setenv("DSV4_GPU_MXD", mxd)
     monkeypatch.setenv("DSV4_GPU_MXD_MW", mw)
+    monkeypatch.setenv("DSV4_GPU_MXD_PL", pl)
     cases = ((7168, 7168, 64, 128, 128), (300, 1536, 64, 128, 128), (129, 7168, 37, 128, 128),
              (33, 16384, 21, 16, 64), (70, 2096, 41, 32, 64), (16, 512, 20, 128, 128),
-             (40, 64, 3, 128, 128), (257, 1024, 7, 16, 128), (136, 3072, 61, 64, 192))
+             (40, 64, 3, 128, 128), (257, 1024, 7, 16, 128), (136, 3072, 61, 64, 192),
+             (200, 2048, 16, 128, 128), (96, 4096, 48, 128, 128), (81, 1280, 17, 32, 128))
     for rows, cols, nt, blk_r, blk_c in cases:
         rng = np.random.default_rng(rows + cols + nt + 7)
         W = common.fp8_codes(rng, (rows, cols))
         S = (127 + rng.integers(-8, -3, size=((rows + blk_r - 1) // blk_r,
                                               (cols + blk_c - 1) // blk_c))).astype(np.uint8)
         x = rng.standard_normal((nt, cols), dtype=np.float32)
-        say("fp8 mxd %dx%d nt %d blk %dx%d MXD %s MW %s" % (rows, cols, nt, blk_r, blk_c, mxd, mw))
+        say("fp8 mxd %dx%d nt %d blk %dx%d MXD %s MW %s PL %s"
+            % (rows, cols, nt, blk_r, blk_c, mxd, mw, pl))
         _, m = _run(dsv4, W, S, x[0], blk_r=blk_r, blk_c=blk_c)
         yn = dsv4.mmq_n(m, x)
         for t in range(nt):

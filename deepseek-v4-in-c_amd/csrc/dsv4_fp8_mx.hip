@@ -718,10 +718,17 @@ k_fp8_mxn(float *__restrict__ y, const float *__restrict__ x, const uint8_t *__r
  * LDS base + 16 lane, so nothing in flight holds a register) into a ring of
  * NS stages, NS - 1 of them in flight while one is read. Each lane fetches
  * the piece that the swizzled layout puts in its slot: weight piece c of
- * row R sits at piece c ^ (R & 7) of its 128-byte row, term piece c of term
- * row j at c ^ (j & 15) of its 256-byte row, so the fragment reads are free
- * of bank conflicts (an in-bounds LDS probe on MI355X: 437-495 GB/s per CU
- * for these patterns against 146 and 76 with the rows unswizzled). A wave
+ * row R sits at piece c ^ (R & 7) of its 128-byte row (an in-bounds LDS
+ * probe on MI355X: 437-495 GB/s per CU against 146 and 76 with the rows
+ * unswizzled; SQ_LDS_BANK_CONFLICT counts none on these reads). Groups of
+ * 20 keep term piece c of term row j at c ^ (j & 15) of its 256-byte row,
+ * which still costs about 3 conflict cycles per term read. The planar
+ * groups keep each term row as two 128-byte half rows, ordered (term, K
+ * half, token), with the piece a lane group g reads for MFMA h at slot
+ * (4 h + g) ^ (token & 7): a fragment read then takes 16 consecutive half
+ * rows and, across its four lane groups, four consecutive slots, as the
+ * weight reads do, and counts no conflicts (it counted 4 cycles per read
+ * with whole 256-byte rows: 64 tokens 40.6 -> 36.7 us). A wave
  * reads stage s's fragments into one register set while the set read at
  * stage s - 1 runs through the matrix core, so the reads' latency hides
  * behind a stage of MFMAs.
@@ -818,9 +825,22 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
 #pragma unroll
     for (int i = 0; i < DX; i++) {
         const int xi = min(DX * w + i, TR / 4 - 1);
-        const int j = 4 * xi + (lane >> 4);
-        const int jj = j / XNT < ntok ? j : 0;
-        xsrc[i] = xt + ((size_t)t0 * XNT + jj) * cpad + 8 * ((lane & 15) ^ (j & 15));
+        if constexpr (PL) {
+            /* planar: 128-byte half rows r = 16 (2 n + qq) + t (term n, K half
+             * qq, token t); piece 2 g + h of a half row (lane group g's piece
+             * for MFMA h) at slot (4 h + g) ^ (r & 7), so each fragment read
+             * takes four consecutive slots across its lane groups; lane ->
+             * half row 8 i + lane / 8, slot lane % 8 */
+            const int r = 8 * xi + (lane >> 3);
+            const int n = r >> 5, qq = (r >> 4) & 1, t = r & 15;
+            const int jj = t < ntok ? XNT * t + n : 0;
+            const int q = (lane & 7) ^ (t & 7);
+            xsrc[i] = xt + ((size_t)t0 * XNT + jj) * cpad + 8 * (8 * qq + 2 * (q & 3) + (q >> 2));
+        } else {
+            const int j = 4 * xi + (lane >> 4);
+            const int jj = j / XNT < ntok ? j : 0;
+            xsrc[i] = xt + ((size_t)t0 * XNT + jj) * cpad + 8 * ((lane & 15) ^ (j & 15));
+        }
         xoff[i] = D::WB + 1024 * xi;
     }
     /* FULL: the caller knows the whole stage lies inside the rows */
@@ -850,8 +870,8 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
 
     /* the fragment reads: A row 16 a + col of tile a = RT rp + i; B term row
      * 15 n + min(col, 14) of column tile n = CT ch + jn (column 15 repeats
-     * column 14; its result is never used), or in the planar group term row
-     * 3 col + n (token col, term n) */
+     * column 14; its result is never used), or in the planar group half row
+     * 16 (2 n + qq) + col (token col, term n) */
     int aoff[RT], asw[RT], boff[CT], bsw[CT];
     bool live[RT];
     int srow[RT];
@@ -931,7 +951,9 @@ k_fp8_mxd(float *__restrict__ y, const uint8_t *__restrict__ W, const uint8_t *_
         for (int h = 0; h < 2; h++)
 #pragma unroll
             for (int n = 0; n < CT; n++)
-                fb[qq][h][n] = boff[n] + 16 * ((8 * qq + 2 * g + h) ^ bsw[n]);
+                fb[qq][h][n] = PL ? D::WB + (16 * (2 * n + qq) + col) * 128 +
+                                        16 * ((4 * h + g) ^ (col & 7))
+                                  : boff[n] + 16 * ((8 * qq + 2 * g + h) ^ bsw[n]);
     auto fetch = [&](Ops &o, int slot) {
         const unsigned char *st = xdlds + (size_t)slot * D::SB;
 #pragma unroll

@@ -1593,7 +1593,10 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
      * / 28.0-28.1, 11 tokens 24.5-24.7 / 27.8-28.0; but 40 tokens 37.5 /
      * 30.2-30.4, where two groups of 20 (8 tiles) beat three of 16 (9), so
      * the groups of 20 run where they take two or more groups and fewer
-     * tiles. Workgroups: planar, 4 waves over 64 rows (64 tokens 40.3-40.9
+     * tiles (with the planar term reads free of bank conflicts: 64 tokens
+     * 36.5-37.1, 20 tokens 25.7-25.8 / 28.1-28.2, 40 tokens 32.7 /
+     * 30.6-30.7, 33 tokens 32.3-32.6 / 30.2-30.5). Workgroups: planar, 4
+     * waves over 64 rows (64 tokens 40.3-40.9
      * against 42.6-43.5 with 8 waves over 128; 16 tokens 26.2 against 37.9),
      * 2 waves over 32 when there is one group, so that it still covers the
      * CUs (16 tokens 24.8-25.0 against 26.1-26.2); a ring of 3 stages (4:

@@ -1599,8 +1599,12 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
      * waves over 64 rows (64 tokens 40.3-40.9
      * against 42.6-43.5 with 8 waves over 128; 16 tokens 26.2 against 37.9),
      * 2 waves over 32 when there is one group, so that it still covers the
-     * CUs (16 tokens 24.8-25.0 against 26.1-26.2); a ring of 3 stages (4:
-     * 64 tokens 40.5-40.6, 32 tokens 29.5 against 28.3-28.4). Groups of 20,
+     * CUs (16 tokens 24.8-25.0 against 26.1-26.2); the 4-wave form with a
+     * ring of 4 stages (80 KB, two still fit a CU), which the conflict-free
+     * term reads made the faster (64 tokens 36.4-36.8 against 36.8-37.0
+     * with 3, 48 tokens 32.4-32.7 / 33.2-33.5, 32 tokens 25.7-25.9 /
+     * 26.6-26.7; with conflicting reads 4 stages measured no better, 40.5 /
+     * 40.3-40.9 and 29.5 / 28.3-28.4). Groups of 20,
      * 8 waves over 128 rows from three groups on (64 tokens: 43.1-43.5
      * against 45.7 with 4 waves), else 4 waves over 64 rows (32 tokens 30.4
      * against 39.1-39.5 with 8 waves, 16 tokens 28.0 against 37.6).
@@ -1616,7 +1620,7 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
     if (dmw != 2 && dmw != 8) dmw = 4;
     if (!dpl && dmw == 2) dmw = 4;
     const size_t lds_d = dpl ? (dmw == 2   ? xd_lds<2, 3, XP_TR>()
-                                : dmw == 4 ? xd_lds<4, 3, XP_TR>()
+                                : dmw == 4 ? xd_lds<4, 4, XP_TR>()
                                            : xd_lds<8, 5, XP_TR>())
                              : (dmw == 4 ? xd_lds<4, 3>() : xd_lds<8, 5>());
     if (dme != 0 && uni && xt && lds_d <= dsv4_lds_limit()) {
@@ -1625,7 +1629,7 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
             opted_d = optin(k_fp8_mxd<2, 2, 8, 5>, "fp8 mxd") &&
                               optin(k_fp8_mxd<2, 2, 4, 3>, "fp8 mxd") &&
                               optin(k_fp8_mxd<1, 3, 8, 5>, "fp8 mxd") &&
-                              optin(k_fp8_mxd<1, 3, 4, 3>, "fp8 mxd") &&
+                              optin(k_fp8_mxd<1, 3, 4, 4>, "fp8 mxd") &&
                               optin(k_fp8_mxd<1, 3, 2, 3>, "fp8 mxd")
                           ? 1
                           : -1;
@@ -1638,7 +1642,7 @@ int dsv4_fp8_mxn_launch(float *y, const float *x, const uint8_t *W, const uint8_
                                                 sc, blk_r, bc_m, nt, td, xt, cpad)
             if (dpl) {
                 if (dmw == 2) XD(1, 3, 2, 3);
-                else if (dmw == 4) XD(1, 3, 4, 3);
+                else if (dmw == 4) XD(1, 3, 4, 4);
                 else XD(1, 3, 8, 5);
             } else {
                 if (dmw == 4) XD(2, 2, 4, 3);
